@@ -1,0 +1,180 @@
+"""ctypes binding of the C oracle (libzkh_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker or the timed CPU baseline.  Field elements are passed
+as numpy uint32 arrays of shape (n, 8) (the reference's Fr_t layout).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "libzkh_oracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError("oracle not built: run `make -C oracle`")
+        _LIB = ctypes.CDLL(path)
+    return _LIB
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def frs(n):
+    return np.zeros((n, 8), dtype=np.uint32)
+
+
+def ints_to_fr(vals):
+    """Python ints (any sign) -> (n,8) uint32, reduced mod r."""
+    from .pyref import R, to_limbs
+    out = frs(len(vals))
+    for i, v in enumerate(vals):
+        out[i] = to_limbs(int(v) % R)
+    return out
+
+
+def fr_to_ints(a):
+    a = np.asarray(a, dtype=np.uint64).reshape(-1, 8)
+    return [sum(int(row[i]) << (32 * i) for i in range(8)) for row in a]
+
+
+def tr_init(seed):
+    st = np.zeros(32, dtype=np.uint8)
+    b = seed.encode()
+    lib().or_tr_init(_p(st), b, ctypes.c_size_t(len(b)))
+    return st
+
+
+def tr_absorb(st, label, data):
+    lb = label.encode()
+    buf = np.frombuffer(bytes(data), dtype=np.uint8).copy()
+    lib().or_tr_absorb(_p(st), lb, ctypes.c_size_t(len(lb)), _p(buf), ctypes.c_size_t(len(buf)))
+
+
+def tr_challenge_fr(st):
+    out = np.zeros(8, dtype=np.uint32)
+    lib().or_tr_challenge_fr(_p(st), _p(out))
+    return out
+
+
+def sha256(data):
+    buf = np.frombuffer(bytes(data), dtype=np.uint8).copy()
+    out = np.zeros(32, dtype=np.uint8)
+    lib().or_sha256(_p(buf), ctypes.c_size_t(len(buf)), _p(out))
+    return bytes(out)
+
+
+def fr_op(name, a, b=None):
+    out = np.zeros(8, dtype=np.uint32)
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    if b is None:
+        getattr(lib(), "or_fr_" + name)(_p(a), _p(out))
+    else:
+        b = np.ascontiguousarray(b, dtype=np.uint32)
+        getattr(lib(), "or_fr_" + name)(_p(a), _p(b), _p(out))
+    return out
+
+
+def me(t, u):
+    t = np.ascontiguousarray(t, dtype=np.uint32)
+    u = np.ascontiguousarray(u, dtype=np.uint32).reshape(-1, 8)
+    out = np.zeros(8, dtype=np.uint32)
+    rc = lib().or_me(_p(t), ctypes.c_uint32(len(t)), _p(u), ctypes.c_uint32(len(u)), _p(out))
+    return rc, out
+
+
+def partial_me(t, u, cur_dim, window):
+    t = np.ascontiguousarray(t, dtype=np.uint32)
+    u = np.ascontiguousarray(u, dtype=np.uint32).reshape(-1, 8)
+    out = frs(len(t))
+    on = ctypes.c_uint32(0)
+    rc = lib().or_partial_me(_p(t), ctypes.c_uint32(len(t)), _p(u), ctypes.c_uint32(len(u)),
+                             ctypes.c_uint32(cur_dim), ctypes.c_uint32(window), _p(out),
+                             ctypes.byref(on))
+    return rc, out[:on.value]
+
+
+def multi_dim_me(t, us, shape):
+    t = np.ascontiguousarray(t, dtype=np.uint32)
+    ks = np.array([len(u) for u in us], dtype=np.uint32)
+    cat = np.concatenate([np.asarray(u, dtype=np.uint32).reshape(-1, 8) for u in us] +
+                         [frs(0)]) if us else frs(1)
+    cat = np.ascontiguousarray(cat)
+    shp = np.array(shape, dtype=np.uint32)
+    out = np.zeros(8, dtype=np.uint32)
+    rc = lib().or_multi_dim_me(_p(t), ctypes.c_uint32(len(t)), _p(cat), _p(ks), _p(shp),
+                               ctypes.c_uint32(len(shape)), _p(out))
+    return rc, out
+
+
+def build_eq(u):
+    u = np.ascontiguousarray(u, dtype=np.uint32).reshape(-1, 8)
+    out = frs(1 << len(u))
+    lib().or_build_eq(_p(u), ctypes.c_uint32(len(u)), _p(out))
+    return out
+
+
+def mm_prove(st, X, W, Y, B, IN, OUT):
+    """Returns (rc, dict) for the zkob_fc.cu:259-440 segment on int inputs."""
+    from .pyref import ceil_log2
+    X = np.ascontiguousarray(X, dtype=np.int32)
+    W = np.ascontiguousarray(W, dtype=np.int32)
+    Y = np.ascontiguousarray(Y, dtype=np.int64)
+    L, lb, lo = ceil_log2(IN), ceil_log2(B), ceil_log2(OUT)
+    ev, cl = frs(3 * L + 1), frs(3)
+    ub, uo, ui = frs(lb + 1), frs(lo + 1), frs(L + 1)
+    rc = lib().or_mm_prove(_p(st), _p(X), _p(W), _p(Y), ctypes.c_uint32(B), ctypes.c_uint32(IN),
+                           ctypes.c_uint32(OUT), _p(ev), _p(cl), _p(ub), _p(uo), _p(ui))
+    return rc, dict(ev=ev[:3 * L], claims=cl, u_batch=ub[:lb], u_output=uo[:lo], u_input=ui[:L])
+
+
+def range_table(low, length, size):
+    T = frs(size)
+    lib().or_range_table(ctypes.c_int32(low), ctypes.c_uint32(length), ctypes.c_uint32(size), _p(T))
+    return T
+
+
+def lu_prep(S, low, N):
+    S = np.ascontiguousarray(S, dtype=np.uint32)
+    m = frs(N)
+    rc = lib().or_lu_prep(_p(S), ctypes.c_uint32(len(S)), ctypes.c_int32(low), ctypes.c_uint32(N),
+                          _p(m))
+    return rc, m
+
+
+def lu_inverse(S, beta):
+    S = np.ascontiguousarray(S, dtype=np.uint32)
+    beta = np.ascontiguousarray(beta, dtype=np.uint32)
+    A = frs(len(S))
+    lib().or_lu_inverse(_p(S), ctypes.c_uint32(len(S)), _p(beta), _p(A))
+    return A
+
+
+def lu_prove(st, A, S, T, m, alpha, beta, u, strict=True):
+    from .pyref import ceil_log2
+    D, N = len(A), len(T)
+    logD = ceil_log2(D)
+    arrs = [np.ascontiguousarray(x, dtype=np.uint32) for x in (A, S, T, m, alpha, beta, u)]
+    ev, term, ws = frs(4 * logD + 1), frs(5), frs(logD + 1)
+    rc = lib().or_lu_prove(_p(st), *[_p(x) for x in arrs[:4]], ctypes.c_uint32(D),
+                           ctypes.c_uint32(N), _p(arrs[4]), _p(arrs[5]), _p(arrs[6]),
+                           ctypes.c_int(1 if strict else 0), _p(ev), _p(term), _p(ws))
+    return rc, dict(ev=ev[:4 * logD], term=term, ws=ws[:logD])
+
+
+def hp_prove(st, claim, E, S, U, strict=True):
+    n = len(E)
+    k = n.bit_length() - 1
+    arrs = [np.ascontiguousarray(x, dtype=np.uint32) for x in (claim, E, S, U)]
+    ev, term, ws = frs(4 * k + 1), frs(3), frs(k + 1)
+    rc = lib().or_hp_prove(_p(st), _p(arrs[0]), _p(arrs[1]), _p(arrs[2]), _p(arrs[3]),
+                           ctypes.c_uint32(n), ctypes.c_int(1 if strict else 0), _p(ev),
+                           _p(term), _p(ws))
+    return rc, dict(ev=ev[:4 * k], term=term, ws=ws[:k])

@@ -1,0 +1,115 @@
+/*
+ * zkh_oracle.h -- CPU restatement of zk-hillclimb's BLS12-381 Fr prover hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker (or as the
+ * timed CPU baseline).  The product path (zk-hillclimb_amd/, libzkh.so) never
+ * links, loads or calls it.
+ *
+ * Every function follows the reference's algorithmic schedule (geometric
+ * partial_me / multi_dim_me passes, per-round MLE re-evaluation in logUp,
+ * per-element Fermat inverses) so that it doubles as the scalar CPU baseline.
+ * Field elements cross this interface in the reference's Fr_t byte layout:
+ * 8 little-endian uint32 limbs, canonical residue in [0, r), plain (integer
+ * view, not Montgomery form) -- zkllm-src/fr-tensor.cuh:15, bls12-381.cuh:116-120.
+ *
+ * Return codes follow the product library: 0 ok, 1 bad dims/args,
+ * 2 round inconsistency (prover-side p(0)+p(1) != claim or terminal mismatch).
+ */
+#ifndef ZKH_ORACLE_H
+#define ZKH_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- field (bls12-381.cu:245-300, :499-539, :585-623; polynomial.cu:74-143) ---- */
+void or_fr_add(const uint32_t a[8], const uint32_t b[8], uint32_t out[8]);
+void or_fr_sub(const uint32_t a[8], const uint32_t b[8], uint32_t out[8]);
+/* raw Montgomery product a*b*2^-256 mod r (blstrs__scalar__Scalar_mul) */
+void or_fr_montmul(const uint32_t a[8], const uint32_t b[8], uint32_t out[8]);
+/* plain product a*b mod r (= mont(mul(a,b)), vrf_common.cuh k_scalar_op op 2) */
+void or_fr_mul(const uint32_t a[8], const uint32_t b[8], uint32_t out[8]);
+/* plain inverse by Fermat, inverse(0) = 0 (polynomial.cu:127-131, tlookup.cu:50-62) */
+void or_fr_inv(const uint32_t a[8], uint32_t out[8]);
+/* int64 -> Fr: v>=0 -> v, v<0 -> r-|v| (fr-tensor.cu:707-725) */
+void or_fr_from_i64(int64_t v, uint32_t out[8]);
+
+/* ---- SHA-256 transcript (fs_transcript.hpp:121-165; vrf_common.cuh:219-250) ---- */
+void or_sha256(const uint8_t* data, size_t n, uint8_t out[32]);
+void or_tr_init(uint8_t st[32], const char* seed, size_t seed_len);
+void or_tr_absorb(uint8_t st[32], const char* label, size_t label_len,
+                  const void* data, size_t len);
+void or_tr_challenge_bytes(uint8_t st[32], uint8_t out[32]);
+void or_tr_challenge_fr(uint8_t st[32], uint32_t out[8]);
+
+/* ---- tensors (fr-tensor.cu) ---- */
+/* sum (fr-tensor.cu:382-434) */
+void or_sum(const uint32_t* t, uint32_t n, uint32_t out[8]);
+/* FrTensor::operator()(u): LSB-first MLE evaluation (fr-tensor.cu:437-442, :588-609) */
+int or_me(const uint32_t* t, uint32_t n, const uint32_t* u, uint32_t k, uint32_t out[8]);
+/* FrTensor::partial_me(u, cur_dim, window) (fr-tensor.cu:518-560); out holds n/cur_dim*window
+ * entries after all binds ((cur_dim rounded up per bind); *out_n receives the count */
+int or_partial_me(const uint32_t* t, uint32_t n, const uint32_t* u, uint32_t k,
+                  uint32_t cur_dim, uint32_t window, uint32_t* out, uint32_t* out_n);
+/* FrTensor::partial_me(u, window) (fr-tensor.cu:612-641) */
+int or_partial_me_window(const uint32_t* t, uint32_t n, const uint32_t* u, uint32_t k,
+                         uint32_t window, uint32_t* out, uint32_t* out_n);
+/* FrTensor::multi_dim_me(us, shape) (fr-tensor.cu:643-652); us concatenated, ks[i] = |us[i]| */
+int or_multi_dim_me(const uint32_t* t, uint32_t n, const uint32_t* us, const uint32_t* ks,
+                    const uint32_t* shape, uint32_t ndim, uint32_t out[8]);
+/* FrTensor::pad(shape) with zero pad value (fr-tensor.cu:800-828) */
+int or_pad(const uint32_t* t, const uint32_t* shape, uint32_t ndim, uint32_t* out,
+           uint32_t* out_n);
+/* eq table E[b] = prod_i (b>>i&1 ? u_i : 1-u_i) (zkob_lookup.cuh:202-209, :245-265) */
+void or_build_eq(const uint32_t* u, uint32_t k, uint32_t* out);
+
+/* ---- matmul (zkip) sumcheck: zkob_fc.cu:259-440 ----
+ * Starts at the u_batch/u_output draws (the caller has absorbed B, IN, OUT and the
+ * commitments) and ends after absorbing claim_X and claim_W.
+ * ev_out: 3*L Fr (p0,p1,p2 per round, L = ceilLog2(IN)); claims_out: claim, claim_X,
+ * claim_W; u_batch_out (ceilLog2 B), u_output_out (ceilLog2 OUT), u_input_out (L). */
+int or_mm_prove(uint8_t st[32], const int32_t* X, const int32_t* W, const int64_t* Y,
+                uint32_t B, uint32_t IN, uint32_t OUT,
+                uint32_t* ev_out, uint32_t* claims_out,
+                uint32_t* u_batch_out, uint32_t* u_output_out, uint32_t* u_input_out);
+
+/* ---- logUp / tLookup ---- */
+/* tLookupRange table: T[i] = low+i (i<len), else low+len-1 (tlookup.cu:372-391) */
+void or_range_table(int32_t low, uint32_t len, uint32_t table_size, uint32_t* T);
+/* multiplicities: idx = (S - low).limb0, m[idx] += 1 (tlookup.cu:10-48, :414-433).
+ * Returns 1 if an index falls outside [0, N) (the reference's atomicAdd would write out
+ * of bounds there; this restatement reports it). */
+int or_lu_prep(const uint32_t* S, uint32_t D, int32_t low, uint32_t N, uint32_t* m);
+/* A[i] = 1/(S[i]+beta), per-element Fermat (tlookup.cu:50-62) */
+void or_lu_inverse(const uint32_t* S, uint32_t n, const uint32_t beta[8], uint32_t* A);
+/* FS lookup recursion: zkob_rescale.cu:132-146 + zkob_lookup.cuh:143-198.
+ * Inputs are the witness S (D), its inverse table A (D), the table T (N) and m (N),
+ * alpha, beta and u (logD challenges, already drawn by the caller).  Computes
+ * Bv = 1/(T+beta), C = alpha^2 - sum(Bv*m), claim = alpha + alpha^2, runs the rounds
+ * (absorbing "p0".."p3" per round) and absorbs "A_f","S_f","m_f".
+ * ev_out: 4*logD Fr; term_out: A_f,S_f,B_f,T_f,m_f; ws_out: logD round challenges. */
+int or_lu_prove(uint8_t st[32], const uint32_t* A, const uint32_t* S, const uint32_t* T,
+                const uint32_t* m, uint32_t D, uint32_t N, const uint32_t alpha[8],
+                const uint32_t beta[8], const uint32_t* u, int strict,
+                uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+
+/* ---- eq-weighted Hadamard sumcheck: zkob_lookup.cuh:212-233, :267-315 ----
+ * E, S, U: n = 2^k entries.  Per round absorbs "hp0".."hp3"; the caller absorbs the
+ * claim before and S_f2/U_f2 after (as zkob_glu.cu:242-247 does).
+ * ev_out: 4*k Fr; term_out: S_f2, U_f2, E_f; ws_out: k challenges. */
+int or_hp_prove(uint8_t st[32], const uint32_t claim[8], const uint32_t* E,
+                const uint32_t* S, const uint32_t* U, uint32_t n, int strict,
+                uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+
+/* Lagrange interpolation through p(0..2) / p(0..3) (vrf_common.cuh:130-140,
+ * zkob_lookup.cuh:62-73) */
+void or_lagrange3(const uint32_t p[24], const uint32_t x[8], uint32_t out[8]);
+void or_lagrange4(const uint32_t p[32], const uint32_t x[8], uint32_t out[8]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
