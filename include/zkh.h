@@ -1,0 +1,154 @@
+/*
+ * zkh.h -- C ABI of the MI355X (gfx950) prover hot path for zk-hillclimb's BLS12-381
+ * Fr sumchecks: MLE fold/bind, the matmul (zkip) sumcheck, the logUp (tLookup)
+ * lookup sumcheck and the eq-weighted Hadamard sumcheck.
+ *
+ * Conventions (shared by every entry point):
+ *  - A field element crosses the ABI as the reference's Fr_t: 8 little-endian uint32
+ *    limbs, canonical residue in [0, r), plain integer view (zkllm-src/fr-tensor.cuh:15,
+ *    bls12-381.cuh:116-120).  "Fr array" below means n*8 uint32.
+ *  - Return codes: ZKH_OK 0, ZKH_EARG 1 (bad dims/args, as the reference's
+ *    std::runtime_error on dimension mismatch), ZKH_EROUND 2 (prover-side round or
+ *    terminal inconsistency: "witness bug" in the reference), ZKH_EDEV 3 (HIP error).
+ *    zkh_last_error() gives the message of the last failure on that context.
+ *  - A context owns one HIP stream (default priority) on one device, its scratch
+ *    memory and its pinned host staging.  Calls on one context are serialised by the
+ *    caller; independent contexts may be driven from different host threads, which is
+ *    how independent sumchecks (e.g. the 7 matmuls of a layer) overlap.
+ *  - Transcripts are the reference's SHA-256 Fiat-Shamir transcript
+ *    (fs_transcript.hpp:115-166): a 32-byte state owned by the caller.
+ */
+#ifndef ZKH_H
+#define ZKH_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZKH_OK 0
+#define ZKH_EARG 1
+#define ZKH_EROUND 2
+#define ZKH_EDEV 3
+
+typedef struct zkh_ctx zkh_ctx;
+typedef struct zkh_tensor zkh_tensor;
+
+/* element kinds held by a tensor */
+#define ZKH_KIND_FR 0  /* full field elements (device: two uint4 limb planes) */
+#define ZKH_KIND_I32 1 /* small signed integers, int_to_scalar view (fr-tensor.cu:713-717) */
+#define ZKH_KIND_I64 2 /* signed 64-bit integers, long_to_scalar view (fr-tensor.cu:701-705) */
+
+/* ---------------- context ---------------- */
+int zkh_ctx_create(int device, zkh_ctx** out);
+int zkh_ctx_destroy(zkh_ctx* ctx);
+const char* zkh_last_error(const zkh_ctx* ctx);
+/* wait for all work queued on the context's stream */
+int zkh_ctx_sync(zkh_ctx* ctx);
+
+/* ---------------- tensors (replace FrTensor ctors/save/load: fr-tensor.cu:158-248,
+ * zkob_fc.cu:178-185 load_int_tensor, zkob_lookup.cuh:103-110 load_long_tensor) ------- */
+/* host Fr array (AoS, reference byte layout) -> device tensor */
+int zkh_tensor_from_fr(zkh_ctx* ctx, const uint32_t* fr_aos, uint32_t n, zkh_tensor** out);
+/* host int32 / int64 -> device tensor holding the same field values (v<0 -> r-|v|) */
+int zkh_tensor_from_i32(zkh_ctx* ctx, const int32_t* v, uint32_t n, zkh_tensor** out);
+int zkh_tensor_from_i64(zkh_ctx* ctx, const int64_t* v, uint32_t n, zkh_tensor** out);
+/* the same from device pointers (data already resident in HBM; copied, not adopted) */
+int zkh_tensor_from_i32_device(zkh_ctx* ctx, const int32_t* dptr, uint32_t n, zkh_tensor** out);
+int zkh_tensor_from_i64_device(zkh_ctx* ctx, const int64_t* dptr, uint32_t n, zkh_tensor** out);
+/* matmul weight registration: W is IN x OUT row-major int32 (zkob_fc.cu:178 layout); the
+ * device copy is laid out OUT-major so the eq-weighted row reduction streams it
+ * coalesced.  The tensor's logical content is still W (to_fr returns W row-major). */
+int zkh_tensor_weights_i32(zkh_ctx* ctx, const int32_t* W, uint32_t in_dim, uint32_t out_dim,
+                           zkh_tensor** out);
+int zkh_tensor_free(zkh_tensor* t);
+uint32_t zkh_tensor_size(const zkh_tensor* t);
+int zkh_tensor_kind(const zkh_tensor* t);
+/* device tensor -> host Fr array (n*8 uint32) */
+int zkh_tensor_to_fr(zkh_ctx* ctx, const zkh_tensor* t, uint32_t* fr_aos_out);
+
+/* ---------------- MLE primitives (fr-tensor.cu) ---------------- */
+/* sum of all entries (FrTensor::sum, fr-tensor.cu:407-434) */
+int zkh_sum(zkh_ctx* ctx, const zkh_tensor* t, uint32_t out[8]);
+/* FrTensor::operator()(u): LSB-first MLE evaluation, u[0] binds bit 0 (fr-tensor.cu:437-442,
+ * :588-609); requires 2^(k-1) < n <= 2^k */
+int zkh_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k, uint32_t out[8]);
+/* FrTensor::partial_me(u, cur_dim, window) (fr-tensor.cu:518-560): binds the middle
+ * dimension of a row-major [other, cur_dim, window] view; returns a new FR tensor of
+ * other*window entries */
+int zkh_partial_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k,
+                   uint32_t cur_dim, uint32_t window, zkh_tensor** out);
+/* FrTensor::multi_dim_me(us, shape) (fr-tensor.cu:643-652); us concatenated, ks[i] = |us[i]| */
+int zkh_multi_dim_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* us, const uint32_t* ks,
+                     const uint32_t* shape, uint32_t ndim, uint32_t out[8]);
+/* build_eq_tensor(u) (zkob_lookup.cuh:245-265): E[b] = prod_i (b>>i&1 ? u_i : 1-u_i) */
+int zkh_eq_table(zkh_ctx* ctx, const uint32_t* u, uint32_t k, zkh_tensor** out);
+/* FrTensor::pad(shape) with zero fill (fr-tensor.cu:800-828) */
+int zkh_pad(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* shape, uint32_t ndim,
+            zkh_tensor** out);
+/* k_fr_fold (zkob_lookup.cuh:35-41): in-place MSB fold t[i] += v*(t[i+h]-t[i]), n -> n/2 */
+int zkh_fold(zkh_ctx* ctx, zkh_tensor* t, const uint32_t v[8]);
+/* elementwise: out = a + c*b (FrTensor operator+ / operator* by scalar, e.g. the SwiGLU
+ * combiner comb = G + r*S, zkob_glu.cu:155-156) and out = a (.) b (Hadamard product) */
+int zkh_axpy(zkh_ctx* ctx, const zkh_tensor* a, const uint32_t c[8], const zkh_tensor* b,
+             zkh_tensor** out);
+int zkh_hadamard(zkh_ctx* ctx, const zkh_tensor* a, const zkh_tensor* b, zkh_tensor** out);
+
+/* ---------------- Fiat-Shamir transcript (fs_transcript.hpp; vrf_common.cuh:219-250) ----- */
+int zkh_transcript_init(uint8_t state[32], const char* seed, size_t seed_len);
+int zkh_transcript_absorb(uint8_t state[32], const char* label, size_t label_len,
+                          const void* data, size_t len);
+int zkh_transcript_challenge_fr(uint8_t state[32], uint32_t out[8]);
+
+/* ---------------- matmul sumcheck: zkob_fc.cu:259-440 ----------------
+ * X: B x IN (I32), W: IN x OUT (I32, preferably from zkh_tensor_weights_i32), Y: B x OUT
+ * (I64 or I32), Y = X*W.  The caller has absorbed B, IN, OUT and the commitments; this
+ * draws u_batch, u_output, evaluates claim = Y~(u_batch,u_output), absorbs "claim", runs
+ * the ceilLog2(IN) rounds (absorbing "p0","p1","p2" each) and absorbs "claim_X","claim_W".
+ * ev_out: 3L Fr (p(0),p(1),p(2) per round: the sumcheck.bin evals, zkob_fc.cu:101-123);
+ * claims_out: claim, claim_X, claim_W; u_batch_out, u_output_out, u_input_out (any may be
+ * NULL). */
+int zkh_mm_prove(zkh_ctx* ctx, uint8_t transcript[32], const zkh_tensor* X,
+                 const zkh_tensor* W, const zkh_tensor* Y, uint32_t B, uint32_t IN, uint32_t OUT,
+                 uint32_t* ev_out, uint32_t* claims_out, uint32_t* u_batch_out,
+                 uint32_t* u_output_out, uint32_t* u_input_out);
+
+/* ---------------- logUp lookup (tlookup.cu, zkob_lookup.cuh, zkob_rescale.cu) ---------- */
+/* tLookupRange table (tlookup.cu:372-391): T[i] = low+i (i<len) else low+len-1, size N */
+int zkh_lu_range_table(zkh_ctx* ctx, int32_t low, uint32_t len, uint32_t N, zkh_tensor** out);
+/* multiplicities m (tlookup.cu:10-48, :414-433): idx = (S-low).limb0, m[idx] += 1.
+ * Fails with ZKH_EARG if an index falls outside [0, N) (out-of-range witness). */
+int zkh_lu_prep(zkh_ctx* ctx, const zkh_tensor* S, int32_t low, uint32_t N, zkh_tensor** m_out);
+/* tLookupRangeMapping::operator() (tlookup.cu:469-482): S_out[i] = mapped[idx_i] and m */
+int zkh_lu_mapping(zkh_ctx* ctx, const zkh_tensor* S_in, int32_t low, const zkh_tensor* mapped,
+                   zkh_tensor** S_out, zkh_tensor** m_out);
+/* tlookup_inv_kernel (tlookup.cu:50-62): A[i] = 1/(S[i]+beta), inverse(0) = 0; batched
+ * (Montgomery's trick) */
+int zkh_lu_inverse(zkh_ctx* ctx, const zkh_tensor* S, const uint32_t beta[8], zkh_tensor** A_out);
+/* FS lookup recursion, zkob_rescale.cu:132-146 with fs_phase1/fs_phase2
+ * (zkob_lookup.cuh:143-198): from Bv = 1/(T+beta) through the rounds (absorbing
+ * "p0".."p3" each) to absorbing "A_f","S_f","m_f".  A, S: D entries; T, m: N entries;
+ * u: logD challenges drawn by the caller.  ev_out: 4*logD Fr (lookup.bin evals);
+ * term_out: A_f, S_f, B_f, T_f, m_f; ws_out: logD round challenges (may be NULL). */
+int zkh_lu_prove(zkh_ctx* ctx, uint8_t transcript[32], const zkh_tensor* A,
+                 const zkh_tensor* S, const zkh_tensor* T, const zkh_tensor* m,
+                 const uint32_t alpha[8], const uint32_t beta[8], const uint32_t* u,
+                 uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+
+/* ---------------- eq-weighted Hadamard sumcheck (zkob_lookup.cuh:212-315) -------------- */
+/* fs_hadamard over E, S, U (2^k entries each).  The caller absorbs the claim before and
+ * S_f2/U_f2 after, as the drivers do (zkob_glu.cu:242-247, zkob_rope.cu:234-240).
+ * ev_out: 4k Fr; term_out: S_f2, U_f2, E_f; ws_out: k challenges (may be NULL). */
+int zkh_hp_prove(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
+                 const zkh_tensor* E, const zkh_tensor* S, const zkh_tensor* U,
+                 uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+/* the same with E = build_eq_tensor(u) (zkob_glu.cu:243), never materialised */
+int zkh_hp_prove_eq(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
+                    const uint32_t* u, uint32_t k, const zkh_tensor* S, const zkh_tensor* U,
+                    uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,250 @@
+"""GPU parity: libzkh.so (HIP, gfx950) against the C oracle on the same seeded inputs.
+
+Bar: bit-exact field elements, identical transcript states.  Shapes are the reference's
+own test shapes (vrf_toy_matmul.cu:249-260, vrf_toy_lookup.cu:323-335,
+zkob_fc.cu:1246-1248, zkob_rescale.cu:539-541, zkob_glu.cu:711-713) plus BASELINE.json
+config 1 and medium sizes that exercise multi-block reductions, odd/non-pow2 dimensions
+and the eq split (>= 2^11 pairs).
+"""
+import numpy as np
+import pytest
+
+from oracle import coracle as C
+from oracle import pyref as P
+
+pytestmark = pytest.mark.gpu
+
+
+def rand_fr(rng, n):
+    return C.ints_to_fr([int(x) for x in rng.integers(0, 2**63, size=n)] if n else [])
+
+
+def rand_fr_full(rng, n):
+    vals = [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(n)]
+    return C.ints_to_fr(vals)
+
+
+def fr_eq(a, b):
+    return np.array_equal(np.asarray(a, np.uint32).reshape(-1, 8), np.asarray(b, np.uint32).reshape(-1, 8))
+
+
+def seed_transcript(zkh, label):
+    st_g = zkh.transcript(label)
+    st_o = C.tr_init(label)
+    assert bytes(st_g) == bytes(st_o)
+    return st_g, st_o
+
+
+# ---------------------------------------------------------------- MLE primitives
+@pytest.mark.parametrize("n,k", [(1, 0), (5, 3), (8, 3), (1000, 10), (1024, 10), (3000, 12), (70000, 17)])
+def test_me(zkh, ctx, n, k):
+    rng = np.random.default_rng(n * 31 + k)
+    t = rand_fr_full(rng, n)
+    u = rand_fr_full(rng, k) if k else np.zeros((0, 8), np.uint32)
+    rc, want = C.me(t, u)
+    assert rc == 0
+    got = ctx.me(ctx.from_fr(t), u)
+    assert fr_eq(got, want)
+
+
+@pytest.mark.parametrize("shape", [(6, 5, 3), (4, 8, 1), (1, 7, 2), (3, 64, 5)])
+def test_partial_me(zkh, ctx, shape):
+    O, Cd, Wd = shape
+    rng = np.random.default_rng(sum(shape))
+    t = rand_fr_full(rng, O * Cd * Wd)
+    k = P.ceil_log2(Cd)
+    u = rand_fr_full(rng, k)
+    rc, want = C.partial_me(t, u, Cd, Wd)
+    assert rc == 0
+    got = ctx.partial_me(ctx.from_fr(t), u, Cd, Wd).to_fr()
+    assert fr_eq(got, want)
+
+
+@pytest.mark.parametrize("shape", [(4, 8), (3, 5), (16, 12), (64, 128)])
+def test_multi_dim_me_int(zkh, ctx, shape):
+    rng = np.random.default_rng(7 + shape[0])
+    vals = rng.integers(-2**20, 2**20, size=shape[0] * shape[1])
+    us = [rand_fr_full(rng, P.ceil_log2(s)) for s in shape]
+    rc, want = C.multi_dim_me(C.ints_to_fr(vals), us, list(shape))
+    assert rc == 0
+    got = ctx.multi_dim_me(ctx.from_i32(vals), us, list(shape))
+    assert fr_eq(got, want)
+    got64 = ctx.multi_dim_me(ctx.from_i64(vals.astype(np.int64) * (1 << 20)), us, list(shape))
+    rc, want64 = C.multi_dim_me(C.ints_to_fr([int(v) << 20 for v in vals]), us, list(shape))
+    assert fr_eq(got64, want64)
+
+
+def test_eq_table_sum_pad_fold(zkh, ctx):
+    rng = np.random.default_rng(11)
+    u = rand_fr_full(rng, 6)
+    assert fr_eq(ctx.eq_table(u).to_fr(), C.build_eq(u))
+    t = rand_fr_full(rng, 777)
+    want = np.zeros(8, np.uint32)
+    C.lib().or_sum(C._p(np.ascontiguousarray(t)), 777, C._p(want))
+    assert fr_eq(ctx.sum(ctx.from_fr(t)), want)
+    # pad (3,5,6) -> (4,8,8)
+    x = rand_fr_full(rng, 90)
+    out = C.frs(256)
+    on = C.ctypes.c_uint32(0)
+    shp = np.array([3, 5, 6], np.uint32)
+    C.lib().or_pad(C._p(np.ascontiguousarray(x)), C._p(shp), 3, C._p(out), C.ctypes.byref(on))
+    assert on.value == 256
+    assert fr_eq(ctx.pad(ctx.from_fr(x), [3, 5, 6]).to_fr(), out)
+    # fold: MSB halving with v
+    f = rand_fr_full(rng, 64)
+    v = rand_fr_full(rng, 1)
+    tf = ctx.from_fr(f)
+    ctx.fold(tf, v)
+    fi, vi = C.fr_to_ints(f), C.fr_to_ints(v)[0]
+    assert C.fr_to_ints(tf.to_fr()) == [(fi[i] + vi * (fi[i + 32] - fi[i])) % P.R for i in range(32)]
+
+
+# ---------------------------------------------------------------- matmul sumcheck
+MM_SHAPES = [(4, 8, 4), (4, 6, 3), (2, 8, 3), (8, 16, 16),  # vrf_toy_matmul.cu:249-260
+             (8, 8, 8), (16, 12, 5),                          # zkob_fc.cu:1246-1248
+             (1, 4, 2), (3, 5, 7), (1, 1, 1), (5, 1, 3),     # edge: B=1, IN=1
+             (64, 128, 64),
+             (33, 700, 129), (128, 3000, 64)]                 # multi-block, non-pow2
+
+
+def _mm_inputs(shape, seed):
+    from zkh_synth import fp8_e4m3_ints, gaussian_int16, matmul_exact
+    B, IN, OUT = shape
+    rng = np.random.default_rng(seed)
+    X = fp8_e4m3_ints(rng, (B, IN)) if seed % 2 else gaussian_int16(rng, (B, IN))
+    W = fp8_e4m3_ints(rng, (IN, OUT))
+    return X, W, matmul_exact(X, W)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _synth_alias():
+    import importlib.util
+    import os
+    import sys
+    if "zkh_synth" not in sys.modules:
+        path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                            "zk-hillclimb_amd", "synth.py")
+        spec = importlib.util.spec_from_file_location("zkh_synth", path)
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules["zkh_synth"] = mod
+        spec.loader.exec_module(mod)
+    yield
+
+
+@pytest.mark.parametrize("shape", MM_SHAPES)
+@pytest.mark.parametrize("weights", [True, False])
+def test_mm_prove(zkh, ctx, shape, weights):
+    B, IN, OUT = shape
+    X, W, Y = _mm_inputs(shape, B * 1000 + IN + OUT)
+    st_g, st_o = seed_transcript(zkh, "mm:%d:%d:%d" % shape)
+    rc, want = C.mm_prove(st_o, X, W, Y, B, IN, OUT)
+    assert rc == 0
+    Wt = ctx.weights_i32(W, IN, OUT) if weights else ctx.from_i32(W)
+    got = ctx.mm_prove(st_g, ctx.from_i32(X), Wt, ctx.from_i64(Y), B, IN, OUT)
+    for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
+def test_mm_wrong_witness_rejected(zkh, ctx):
+    X, W, Y = _mm_inputs((8, 16, 4), 5)
+    Y = Y.copy()
+    Y[3, 2] += 1
+    st = zkh.transcript("bad")
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.mm_prove(st, ctx.from_i32(X), ctx.from_i32(W), ctx.from_i64(Y), 8, 16, 4)
+    assert e.value.code == zkh.EROUND
+
+
+# ---------------------------------------------------------------- logUp
+LU_SHAPES = [(32, 8, -3, 5), (16, 16, 0, 16), (64, 4, -2, 3),  # vrf_toy_lookup.cu:323-335
+             (32, 4, -2, 4), (64, 16, -8, 16), (48 * 0 + 64, 64, -32, 64),
+             (1 << 12, 1 << 8, -128, 256), (1 << 14, 1 << 14, -(1 << 13), 1 << 14)]
+
+
+@pytest.mark.parametrize("shape", LU_SHAPES)
+def test_lu_prove(zkh, ctx, shape):
+    D, N, low, ln = shape
+    rng = np.random.default_rng(D + N)
+    vals = rng.integers(low, low + ln, size=D).astype(np.int32)
+    S = C.ints_to_fr(vals)
+    T = C.range_table(low, ln, N)
+    st_g, st_o = seed_transcript(zkh, "lu:%d:%d" % (D, N))
+    rc, m = C.lu_prep(S, low, N)
+    assert rc == 0
+    Sg = ctx.from_i32(vals)
+    mg = ctx.lu_prep(Sg, low, N)
+    assert fr_eq(mg.to_fr(), m)
+    Tg = ctx.range_table(low, ln, N)
+    assert fr_eq(Tg.to_fr(), T)
+    beta = C.tr_challenge_fr(st_o)
+    assert fr_eq(zkh.challenge(st_g), beta)
+    A = C.lu_inverse(S, beta)
+    Ag = ctx.lu_inverse(Sg, beta)
+    assert fr_eq(Ag.to_fr(), A)
+    alpha = C.tr_challenge_fr(st_o)
+    assert fr_eq(zkh.challenge(st_g), alpha)
+    logD = P.ceil_log2(D)
+    u = np.array([C.tr_challenge_fr(st_o) for _ in range(logD)])
+    ug = np.array([zkh.challenge(st_g) for _ in range(logD)])
+    assert fr_eq(u, ug)
+    rc, want = C.lu_prove(st_o, A, S, T, m, alpha, beta, u)
+    assert rc == 0
+    # FR-kind witness (not the int view) must give the same proof
+    got = ctx.lu_prove(st_g, Ag, ctx.from_fr(S), Tg, mg, alpha, beta, u)
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
+def test_lu_out_of_range_rejected(zkh, ctx):
+    S = ctx.from_i32(np.array([0, 1, 2, 40], np.int32))
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.lu_prep(S, 0, 16)
+    assert e.value.code == zkh.EARG
+
+
+def test_lu_inverse_zero(zkh, ctx):
+    rng = np.random.default_rng(3)
+    S = rand_fr_full(rng, 5000)
+    beta = C.fr_op("sub", np.zeros(8, np.uint32), S[1234])  # S[1234] + beta = 0
+    want = C.lu_inverse(S, beta)
+    assert not want[1234].any()
+    got = ctx.lu_inverse(ctx.from_fr(S), beta).to_fr()
+    assert fr_eq(got, want)
+
+
+def test_lu_mapping(zkh, ctx):
+    rng = np.random.default_rng(9)
+    low, N = -16, 32
+    mapped_vals = rng.integers(-1000, 1000, size=N)
+    vals = rng.integers(low, low + N, size=256).astype(np.int32)
+    Sout, m = ctx.lu_mapping(ctx.from_i32(vals), low, ctx.from_fr(C.ints_to_fr(mapped_vals)))
+    want = C.ints_to_fr([int(mapped_vals[v - low]) for v in vals])
+    assert fr_eq(Sout.to_fr(), want)
+    rc, mw = C.lu_prep(C.ints_to_fr(vals), low, N)
+    assert fr_eq(m.to_fr(), mw)
+
+
+# ---------------------------------------------------------------- Hadamard
+@pytest.mark.parametrize("k", [1, 2, 5, 11, 14])
+def test_hp_prove(zkh, ctx, k):
+    n = 1 << k
+    rng = np.random.default_rng(k)
+    u = rand_fr_full(rng, k)
+    E = C.build_eq(u)
+    S = C.ints_to_fr(rng.integers(-2**20, 2**20, size=n))
+    U = rand_fr_full(rng, n)
+    Ei, Si, Ui = C.fr_to_ints(E), C.fr_to_ints(S), C.fr_to_ints(U)
+    claim = C.ints_to_fr([sum(a * b % P.R * c for a, b, c in zip(Ei, Si, Ui)) % P.R])[0]
+    for eqform in (False, True):
+        st_g, st_o = seed_transcript(zkh, "hp:%d" % k)
+        rc, want = C.hp_prove(st_o, claim, E, S, U)
+        assert rc == 0
+        if eqform:
+            got = ctx.hp_prove_eq(st_g, claim, u, ctx.from_fr(S), ctx.from_fr(U))
+        else:
+            got = ctx.hp_prove(st_g, claim, ctx.from_fr(E), ctx.from_fr(S), ctx.from_fr(U))
+        for key in ("ev", "term", "ws"):
+            assert fr_eq(got[key], want[key]), (key, eqform)
+        assert bytes(st_g) == bytes(st_o)

@@ -1,0 +1,291 @@
+"""Python binding of libzkh.so, the C-ABI MI355X prover hot path (include/zkh.h).
+
+This is a thin ctypes layer for tests, the smoke check and bench.py; the product is the
+shared library.  Field elements are numpy uint32 arrays of shape (n, 8) in the reference's
+Fr_t layout (8 little-endian limbs, canonical, plain).  Every call raises ZkhError on a
+non-zero return code; there is no CPU fallback: without the built library or a GPU the
+calls fail.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libzkh.so")
+
+OK, EARG, EROUND, EDEV = 0, 1, 2, 3
+KIND_FR, KIND_I32, KIND_I64 = 0, 1, 2
+
+_lib = None
+
+
+class ZkhError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("zkh error %d: %s" % (code, msg))
+        self.code = code
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("libzkh.so is not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, u32, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int32
+        L.zkh_last_error.restype = ctypes.c_char_p
+        L.zkh_last_error.argtypes = [vp]
+        L.zkh_tensor_size.restype = u32
+        L.zkh_tensor_size.argtypes = [vp]
+        L.zkh_tensor_kind.argtypes = [vp]
+        for name in ["zkh_ctx_destroy", "zkh_ctx_sync", "zkh_tensor_free"]:
+            getattr(L, name).argtypes = [vp]
+        L.zkh_ctx_create.argtypes = [ctypes.c_int, ctypes.POINTER(vp)]
+        L.zkh_tensor_from_fr.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_tensor_from_i32.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_tensor_from_i64.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_tensor_from_i32_device.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_tensor_from_i64_device.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_tensor_weights_i32.argtypes = [vp, vp, u32, u32, ctypes.POINTER(vp)]
+        L.zkh_tensor_to_fr.argtypes = [vp, vp, vp]
+        L.zkh_sum.argtypes = [vp, vp, vp]
+        L.zkh_me.argtypes = [vp, vp, vp, u32, vp]
+        L.zkh_partial_me.argtypes = [vp, vp, vp, u32, u32, u32, ctypes.POINTER(vp)]
+        L.zkh_multi_dim_me.argtypes = [vp, vp, vp, vp, vp, u32, vp]
+        L.zkh_eq_table.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_pad.argtypes = [vp, vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_fold.argtypes = [vp, vp, vp]
+        L.zkh_axpy.argtypes = [vp, vp, vp, vp, ctypes.POINTER(vp)]
+        L.zkh_hadamard.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
+        L.zkh_transcript_init.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
+        L.zkh_transcript_absorb.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, vp, ctypes.c_size_t]
+        L.zkh_transcript_challenge_fr.argtypes = [vp, vp]
+        L.zkh_mm_prove.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, vp, vp, vp, vp, vp]
+        L.zkh_lu_range_table.argtypes = [vp, i32, u32, u32, ctypes.POINTER(vp)]
+        L.zkh_lu_prep.argtypes = [vp, vp, i32, u32, ctypes.POINTER(vp)]
+        L.zkh_lu_mapping.argtypes = [vp, vp, i32, vp, ctypes.POINTER(vp), ctypes.POINTER(vp)]
+        L.zkh_lu_inverse.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
+        L.zkh_lu_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.zkh_hp_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.zkh_hp_prove_eq.argtypes = [vp, vp, vp, vp, u32, vp, vp, vp, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _frs(a, n=None):
+    a = np.ascontiguousarray(a, dtype=np.uint32).reshape(-1, 8)
+    if n is not None:
+        assert a.shape[0] == n
+    return a
+
+
+def ceil_log2(n):
+    return 0 if n <= 1 else (int(n) - 1).bit_length()
+
+
+# ---------------- transcript ----------------
+def transcript(seed):
+    st = np.zeros(32, dtype=np.uint8)
+    b = seed.encode()
+    lib().zkh_transcript_init(_p(st), b, len(b))
+    return st
+
+
+def absorb(st, label, data):
+    lb = label.encode()
+    buf = np.frombuffer(bytes(data), dtype=np.uint8).copy()
+    lib().zkh_transcript_absorb(_p(st), lb, len(lb), _p(buf), len(buf))
+
+
+def challenge(st):
+    out = np.zeros(8, dtype=np.uint32)
+    lib().zkh_transcript_challenge_fr(_p(st), _p(out))
+    return out
+
+
+class Tensor:
+    def __init__(self, ctx, handle):
+        self.ctx, self.h = ctx, handle
+
+    def __del__(self):
+        if getattr(self, "h", None) and lib is not None:
+            try:
+                lib().zkh_tensor_free(self.h)
+            except Exception:
+                pass
+            self.h = None
+
+    @property
+    def n(self):
+        return lib().zkh_tensor_size(self.h)
+
+    @property
+    def kind(self):
+        return lib().zkh_tensor_kind(self.h)
+
+    def to_fr(self):
+        out = np.zeros((self.n, 8), dtype=np.uint32)
+        self.ctx._chk(lib().zkh_tensor_to_fr(self.ctx.h, self.h, _p(out)))
+        return out
+
+
+class Context:
+    """One device context (one HIP stream).  Use one per host thread."""
+
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        rc = lib().zkh_ctx_create(device, ctypes.byref(h))
+        if rc:
+            raise ZkhError(rc, "zkh_ctx_create(%d) failed" % device)
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().zkh_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _chk(self, rc):
+        if rc:
+            raise ZkhError(rc, lib().zkh_last_error(self.h).decode(errors="replace"))
+
+    def _new(self, fn, *args):
+        h = ctypes.c_void_p()
+        self._chk(fn(self.h, *args, ctypes.byref(h)))
+        return Tensor(self, h)
+
+    def sync(self):
+        self._chk(lib().zkh_ctx_sync(self.h))
+
+    # tensors
+    def from_fr(self, a):
+        a = _frs(a)
+        return self._new(lib().zkh_tensor_from_fr, _p(a), a.shape[0])
+
+    def from_i32(self, v):
+        v = np.ascontiguousarray(v, dtype=np.int32).reshape(-1)
+        return self._new(lib().zkh_tensor_from_i32, _p(v), v.size)
+
+    def from_i64(self, v):
+        v = np.ascontiguousarray(v, dtype=np.int64).reshape(-1)
+        return self._new(lib().zkh_tensor_from_i64, _p(v), v.size)
+
+    def from_i32_device(self, ptr, n):
+        return self._new(lib().zkh_tensor_from_i32_device, ctypes.c_void_p(ptr), n)
+
+    def from_i64_device(self, ptr, n):
+        return self._new(lib().zkh_tensor_from_i64_device, ctypes.c_void_p(ptr), n)
+
+    def weights_i32(self, W, IN, OUT):
+        W = np.ascontiguousarray(W, dtype=np.int32).reshape(-1)
+        assert W.size == IN * OUT
+        return self._new(lib().zkh_tensor_weights_i32, _p(W), IN, OUT)
+
+    # MLE primitives
+    def sum(self, t):
+        out = np.zeros(8, dtype=np.uint32)
+        self._chk(lib().zkh_sum(self.h, t.h, _p(out)))
+        return out
+
+    def me(self, t, u):
+        u = _frs(u)
+        out = np.zeros(8, dtype=np.uint32)
+        self._chk(lib().zkh_me(self.h, t.h, _p(u), u.shape[0], _p(out)))
+        return out
+
+    def partial_me(self, t, u, cur_dim, window):
+        u = _frs(u)
+        return self._new(lib().zkh_partial_me, t.h, _p(u), u.shape[0], cur_dim, window)
+
+    def multi_dim_me(self, t, us, shape):
+        ks = np.array([len(u) for u in us], dtype=np.uint32)
+        cat = np.concatenate([_frs(u) for u in us] + [np.zeros((1, 8), np.uint32)])
+        shp = np.array(shape, dtype=np.uint32)
+        out = np.zeros(8, dtype=np.uint32)
+        self._chk(lib().zkh_multi_dim_me(self.h, t.h, _p(cat), _p(ks), _p(shp), len(shape), _p(out)))
+        return out
+
+    def eq_table(self, u):
+        u = _frs(u)
+        return self._new(lib().zkh_eq_table, _p(u), u.shape[0])
+
+    def pad(self, t, shape):
+        shp = np.array(shape, dtype=np.uint32)
+        return self._new(lib().zkh_pad, t.h, _p(shp), len(shape))
+
+    def fold(self, t, v):
+        v = _frs(v, 1)
+        self._chk(lib().zkh_fold(self.h, t.h, _p(v)))
+
+    def axpy(self, a, c, b):
+        c = _frs(c, 1)
+        return self._new(lib().zkh_axpy, a.h, _p(c), b.h)
+
+    def hadamard(self, a, b):
+        return self._new(lib().zkh_hadamard, a.h, b.h)
+
+    # provers
+    def mm_prove(self, st, X, W, Y, B, IN, OUT):
+        L, lb, lo = ceil_log2(IN), ceil_log2(B), ceil_log2(OUT)
+        ev = np.zeros((3 * L + 1, 8), np.uint32)
+        cl = np.zeros((3, 8), np.uint32)
+        ub, uo, ui = (np.zeros((x + 1, 8), np.uint32) for x in (lb, lo, L))
+        self._chk(lib().zkh_mm_prove(self.h, _p(st), X.h, W.h, Y.h, B, IN, OUT, _p(ev), _p(cl),
+                                     _p(ub), _p(uo), _p(ui)))
+        return dict(ev=ev[:3 * L], claims=cl, u_batch=ub[:lb], u_output=uo[:lo], u_input=ui[:L])
+
+    def range_table(self, low, length, N):
+        return self._new(lib().zkh_lu_range_table, low, length, N)
+
+    def lu_prep(self, S, low, N):
+        return self._new(lib().zkh_lu_prep, S.h, low, N)
+
+    def lu_mapping(self, S, low, mapped):
+        so, m = ctypes.c_void_p(), ctypes.c_void_p()
+        self._chk(lib().zkh_lu_mapping(self.h, S.h, low, mapped.h, ctypes.byref(so), ctypes.byref(m)))
+        return Tensor(self, so), Tensor(self, m)
+
+    def lu_inverse(self, S, beta):
+        beta = _frs(beta, 1)
+        return self._new(lib().zkh_lu_inverse, S.h, _p(beta))
+
+    def lu_prove(self, st, A, S, T, m, alpha, beta, u):
+        D = A.n
+        logD = ceil_log2(D)
+        alpha, beta = _frs(alpha, 1), _frs(beta, 1)
+        u = _frs(u) if logD else np.zeros((1, 8), np.uint32)
+        ev = np.zeros((4 * logD + 1, 8), np.uint32)
+        term = np.zeros((5, 8), np.uint32)
+        ws = np.zeros((logD + 1, 8), np.uint32)
+        self._chk(lib().zkh_lu_prove(self.h, _p(st), A.h, S.h, T.h, m.h, _p(alpha), _p(beta), _p(u),
+                                     _p(ev), _p(term), _p(ws)))
+        return dict(ev=ev[:4 * logD], term=term, ws=ws[:logD])
+
+    def hp_prove(self, st, claim, E, S, U):
+        k = ceil_log2(S.n)
+        claim = _frs(claim, 1)
+        ev = np.zeros((4 * k + 1, 8), np.uint32)
+        term = np.zeros((3, 8), np.uint32)
+        ws = np.zeros((k + 1, 8), np.uint32)
+        self._chk(lib().zkh_hp_prove(self.h, _p(st), _p(claim), E.h, S.h, U.h, _p(ev), _p(term), _p(ws)))
+        return dict(ev=ev[:4 * k], term=term, ws=ws[:k])
+
+    def hp_prove_eq(self, st, claim, u, S, U):
+        u = _frs(u)
+        k = u.shape[0]
+        claim = _frs(claim, 1)
+        ev = np.zeros((4 * k + 1, 8), np.uint32)
+        term = np.zeros((3, 8), np.uint32)
+        ws = np.zeros((k + 1, 8), np.uint32)
+        self._chk(lib().zkh_hp_prove_eq(self.h, _p(st), _p(claim), _p(u), k, S.h, U.h, _p(ev),
+                                        _p(term), _p(ws)))
+        return dict(ev=ev[:4 * k], term=term, ws=ws[:k])

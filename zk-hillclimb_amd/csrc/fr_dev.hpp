@@ -1,0 +1,239 @@
+// fr_dev.hpp -- BLS12-381 scalar-field arithmetic for gfx950 (CDNA4) integer VALU.
+//
+// Elements are 8 x 32-bit limbs, little-endian, canonical in [0, r).  The Montgomery
+// product uses the CIOS method (Koc, Acar, Kaliski, "Analyzing and comparing Montgomery
+// multiplication algorithms", 1996) with R = 2^256, so mont_mul(a, b) = a*b*2^-256 mod r,
+// the same value as the reference's blstrs__scalar__Scalar_mul (bls12-381.cu:462-531).
+// Each 32x32+64 step is one v_mad_u64_u32; carries travel in the upper half of the 64-bit
+// accumulator.  Since -r^-1 mod 2^32 = 0xffffffff, the reduction multiplier is -t0.
+//
+// Tables in HBM use a structure-of-limb-quads layout: limbs 0-3 of element i in plane 0
+// at lo[i] (uint4), limbs 4-7 in plane 1 at hi[i], so every wave load reads 1 KiB
+// contiguous per plane.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define ZDEV __device__ __forceinline__
+
+struct fr_t {
+    uint32_t v[8];
+};
+
+// r (bls12-381.cu:4)
+#define ZKH_P0 0x00000001u
+#define ZKH_P1 0xffffffffu
+#define ZKH_P2 0xfffe5bfeu
+#define ZKH_P3 0x53bda402u
+#define ZKH_P4 0x09a1d805u
+#define ZKH_P5 0x3339d808u
+#define ZKH_P6 0x299d7d48u
+#define ZKH_P7 0x73eda753u
+
+ZDEV uint32_t fr_p(int i) {
+    switch (i) {
+        case 0: return ZKH_P0;
+        case 1: return ZKH_P1;
+        case 2: return ZKH_P2;
+        case 3: return ZKH_P3;
+        case 4: return ZKH_P4;
+        case 5: return ZKH_P5;
+        case 6: return ZKH_P6;
+        default: return ZKH_P7;
+    }
+}
+
+ZDEV fr_t fr_zero() {
+    fr_t r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.v[i] = 0;
+    return r;
+}
+
+// r if x >= r else x, for x < 2r (single correction, as bls12-381.cu:295-300)
+ZDEV fr_t fr_reduce_once(const fr_t& x, uint32_t carry_in) {
+    fr_t d;
+    uint64_t br = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint64_t t = (uint64_t)x.v[i] - fr_p(i) - br;
+        d.v[i] = (uint32_t)t;
+        br = (t >> 63);
+    }
+    // keep x when it borrowed (x < r) and there was no carry out of limb 7
+    bool keep = (br != 0) && (carry_in == 0);
+    fr_t r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.v[i] = keep ? x.v[i] : d.v[i];
+    return r;
+}
+
+ZDEV fr_t fr_add(const fr_t& a, const fr_t& b) {
+    fr_t s;
+    uint64_t c = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        c = (uint64_t)a.v[i] + b.v[i] + (c >> 32);
+        s.v[i] = (uint32_t)c;
+    }
+    return fr_reduce_once(s, (uint32_t)(c >> 32));
+}
+
+ZDEV fr_t fr_sub(const fr_t& a, const fr_t& b) {
+    fr_t d;
+    uint64_t br = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint64_t t = (uint64_t)a.v[i] - b.v[i] - br;
+        d.v[i] = (uint32_t)t;
+        br = t >> 63;
+    }
+    // on borrow add r back
+    uint32_t mask = br ? 0xffffffffu : 0u;
+    uint64_t c = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        c = (uint64_t)d.v[i] + (fr_p(i) & mask) + (c >> 32);
+        d.v[i] = (uint32_t)c;
+    }
+    return d;
+}
+
+// CIOS Montgomery product a*b*2^-256 mod r, canonical output for canonical inputs.
+ZDEV fr_t mont_mul(const fr_t& a, const fr_t& b) {
+    uint32_t t[9];
+#pragma unroll
+    for (int j = 0; j < 9; j++) t[j] = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint64_t c = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            c = (uint64_t)a.v[j] * b.v[i] + t[j] + (c >> 32);
+            t[j] = (uint32_t)c;
+        }
+        uint64_t s = (uint64_t)t[8] + (c >> 32);
+        t[8] = (uint32_t)s;
+        uint32_t t9 = (uint32_t)(s >> 32);
+        uint32_t m = 0u - t[0];
+        c = (uint64_t)m * ZKH_P0 + t[0];
+#pragma unroll
+        for (int j = 1; j < 8; j++) {
+            c = (uint64_t)m * fr_p(j) + t[j] + (c >> 32);
+            t[j - 1] = (uint32_t)c;
+        }
+        s = (uint64_t)t[8] + (c >> 32);
+        t[7] = (uint32_t)s;
+        t[8] = t9 + (uint32_t)(s >> 32);
+    }
+    fr_t r;
+#pragma unroll
+    for (int j = 0; j < 8; j++) r.v[j] = t[j];
+    return fr_reduce_once(r, t[8]);
+}
+
+// Montgomery reduction of a wide non-negative integer T (nl <= 16 limbs, T < r*2^256):
+// returns T*2^-256 mod r.  Used to fold wide integer accumulators into the field.
+template <int NL>
+ZDEV fr_t redc_wide(const uint32_t* in) {
+    uint32_t t[17];
+#pragma unroll
+    for (int j = 0; j < 17; j++) t[j] = j < NL ? in[j] : 0u;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint32_t m = 0u - t[i];
+        uint64_t c = (uint64_t)m * ZKH_P0 + t[i];
+#pragma unroll
+        for (int j = 1; j < 8; j++) {
+            c = (uint64_t)m * fr_p(j) + t[i + j] + (c >> 32);
+            t[i + j] = (uint32_t)c;
+        }
+#pragma unroll
+        for (int j = i + 8; j < 17; j++) {
+            c = (uint64_t)t[j] + (c >> 32);
+            t[j] = (uint32_t)c;
+        }
+    }
+    fr_t r;
+#pragma unroll
+    for (int j = 0; j < 8; j++) r.v[j] = t[8 + j];
+    return fr_reduce_once(r, t[16]);
+}
+
+// ---- 64-bit column accumulators for small-integer x field products ----
+// acc[j] += w * e[j] with w < 2^20: each product < 2^52, so 2^11 additions stay < 2^63.
+ZDEV void cols_mac(uint64_t acc[8], uint32_t w, const fr_t& e) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] += (uint64_t)w * e.v[j];
+}
+// sum_j acc[j] * 2^(32j) as a 10-limb integer (each acc[j] < 2^63)
+ZDEV void cols_normalize(const uint64_t acc[8], uint32_t out[10]) {
+    uint64_t c = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint64_t s = acc[j] + c;  // < 2^63 + 2^33
+        out[j] = (uint32_t)s;
+        c = s >> 32;
+    }
+    out[8] = (uint32_t)c;
+    out[9] = (uint32_t)(c >> 32);
+}
+
+// ---- loads / stores in the limb-quad layout ----
+struct FrPlanes {
+    uint4* lo;
+    uint4* hi;
+};
+ZDEV fr_t ld_fr(const uint4* lo, const uint4* hi, uint32_t i) {
+    uint4 a = lo[i], b = hi[i];
+    fr_t r;
+    r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+    r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    return r;
+}
+ZDEV void st_fr(uint4* lo, uint4* hi, uint32_t i, const fr_t& x) {
+    lo[i] = make_uint4(x.v[0], x.v[1], x.v[2], x.v[3]);
+    hi[i] = make_uint4(x.v[4], x.v[5], x.v[6], x.v[7]);
+}
+// AoS (reference Fr_t layout) loads/stores, used for small vectors
+ZDEV fr_t ld_aos(const uint32_t* p, uint32_t i) {
+    const uint4* q = reinterpret_cast<const uint4*>(p + 8 * (size_t)i);
+    uint4 a = q[0], b = q[1];
+    fr_t r;
+    r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+    r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    return r;
+}
+ZDEV void st_aos(uint32_t* p, uint32_t i, const fr_t& x) {
+    uint4* q = reinterpret_cast<uint4*>(p + 8 * (size_t)i);
+    q[0] = make_uint4(x.v[0], x.v[1], x.v[2], x.v[3]);
+    q[1] = make_uint4(x.v[4], x.v[5], x.v[6], x.v[7]);
+}
+
+// int -> field (int_to_scalar / long_to_scalar, fr-tensor.cu:701-717)
+ZDEV fr_t fr_from_i64(int64_t v) {
+    fr_t r = fr_zero();
+    if (v >= 0) {
+        r.v[0] = (uint32_t)v;
+        r.v[1] = (uint32_t)((uint64_t)v >> 32);
+        return r;
+    }
+    uint64_t mag = (uint64_t)(-(v + 1)) + 1;
+    fr_t m = fr_zero();
+    m.v[0] = (uint32_t)mag;
+    m.v[1] = (uint32_t)(mag >> 32);
+    return fr_sub(r, m);
+}
+
+// ---- wave / block reductions of field elements (DPP/swizzle via shuffles, then LDS) ----
+ZDEV fr_t fr_shfl_xor(const fr_t& x, int mask) {
+    fr_t r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.v[i] = __shfl_xor(x.v[i], mask, 64);
+    return r;
+}
+ZDEV fr_t fr_wave_sum(fr_t x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x = fr_add(x, fr_shfl_xor(x, m));
+    return x;
+}

@@ -1,0 +1,836 @@
+// kernels.hip -- gfx950 kernels for the Fr sumcheck / fold / logUp hot path.
+//
+// Every kernel is integer VALU work on 255-bit field elements (fr_dev.hpp); nothing here
+// uses MFMA.  Reductions go lane -> wave (cross-lane shuffles) -> block (LDS) -> one AoS
+// partial per block; the host adds the few hundred block partials.  Round kernels fuse the
+// previous round's fold (bind) with the current round's evaluation so each table is read
+// once per round and halved in place.
+//
+// Sum conventions: a sum built from mont_mul(x, y) of plain x, y carries a factor 2^-256
+// per Montgomery product; each wrapper's comment states the power, and the host multiplies
+// it back out (fr_rpow) once per round instead of once per element.
+#include "fr_dev.hpp"
+#include "kernels.hpp"
+
+namespace zkh {
+
+#define NT 256  // threads per block for the streaming kernels (4 waves of 64)
+
+ZDEV fr_t mk(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t a4, uint32_t a5,
+             uint32_t a6, uint32_t a7) {
+    fr_t r;
+    r.v[0] = a0; r.v[1] = a1; r.v[2] = a2; r.v[3] = a3;
+    r.v[4] = a4; r.v[5] = a5; r.v[6] = a6; r.v[7] = a7;
+    return r;
+}
+// 2^256 mod r (Montgomery one)
+ZDEV fr_t one_m() {
+    return mk(0xfffffffeu, 0x00000001u, 0x00034802u, 0x5884b7fau, 0xecbc4ff5u, 0x998c4fefu,
+              0xacc5056fu, 0x1824b159u);
+}
+// 2^512 mod r
+ZDEV fr_t r2_m() {
+    return mk(0xf3f29c6du, 0xc999e990u, 0x87925c23u, 0x2b6cedcbu, 0x7254398fu, 0x05d31496u,
+              0x9f59ff11u, 0x0748d9d9u);
+}
+ZDEV fr_t plain_one() { return mk(1, 0, 0, 0, 0, 0, 0, 0); }
+// 2^(20p) * 2^256 mod r, p = 1..3: recombine 20-bit integer pieces
+ZDEV fr_t piece_scale(int p) {
+    if (p == 1)
+        return mk(0xffdcaaf7u, 0x00235508u, 0xf7a61909u, 0xaa773d1eu, 0x63db3014u, 0x75236b64u,
+                  0x1dfe9e8bu, 0x23b7d0bau);
+    if (p == 2)
+        return mk(0xaf6b1202u, 0x5094ebc8u, 0xa709a833u, 0x9ae3f86fu, 0x3da414adu, 0xf5c24e47u,
+                  0xdc58603fu, 0x64a13769u);
+    return mk(0x20121c89u, 0xbc98da28u, 0x4c7228c5u, 0x1d3d8a4cu, 0x55cc49e3u, 0xd198d0c2u,
+              0xa9088038u, 0x588d22f7u);
+}
+ZDEV bool fr_is_zero(const fr_t& x) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) o |= x.v[i];
+    return o == 0;
+}
+static inline __host__ __device__ fr_t to_fr(const uint32_t* h) {
+    fr_t r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.v[i] = h[i];
+    return r;
+}
+
+#define PL_LO(p) reinterpret_cast<uint4*>((p).lo())
+#define PL_HI(p) reinterpret_cast<uint4*>((p).hi())
+
+uint32_t grid_for(uint32_t work_items, uint32_t per_block, uint32_t max_blocks) {
+    uint32_t g = (work_items + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > max_blocks) g = max_blocks;
+    return g;
+}
+
+// K field accumulators per thread -> one AoS partial per block (partial[blockIdx*K + k])
+template <int K>
+ZDEV void block_reduce_store(fr_t* acc, uint32_t* partial) {
+    __shared__ fr_t red[NT / 64][K];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < K; k++) acc[k] = fr_wave_sum(acc[k]);
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < K; k++) red[wid][k] = acc[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < K) {
+        const int k = threadIdx.x;
+        fr_t s = red[0][k];
+#pragma unroll
+        for (int w = 1; w < NT / 64; w++) s = fr_add(s, red[w][k]);
+        st_aos(partial, blockIdx.x * K + k, s);
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// conversions and layout
+// ------------------------------------------------------------------------------------
+__global__ void k_i32_to_planes(const int32_t* __restrict__ in, uint32_t n, uint4* lo, uint4* hi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        st_fr(lo, hi, i, fr_from_i64(in[i]));
+}
+__global__ void k_i64_to_planes(const int64_t* __restrict__ in, uint32_t n, uint4* lo, uint4* hi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        st_fr(lo, hi, i, fr_from_i64(in[i]));
+}
+__global__ void k_aos_to_planes(const uint32_t* __restrict__ aos, uint32_t n, uint4* lo, uint4* hi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        st_fr(lo, hi, i, ld_aos(aos, i));
+}
+__global__ void k_planes_to_aos(const uint4* lo, const uint4* hi, uint32_t n, uint32_t* aos) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        st_aos(aos, i, ld_fr(lo, hi, i));
+}
+__global__ void k_zero_planes(uint4* lo, uint4* hi, uint32_t from, uint32_t to) {
+    for (uint32_t i = from + blockIdx.x * blockDim.x + threadIdx.x; i < to;
+         i += gridDim.x * blockDim.x)
+        st_fr(lo, hi, i, fr_zero());
+}
+__global__ void k_absmax_i32(const int32_t* __restrict__ in, uint32_t n, uint32_t* out) {
+    uint32_t m = 0;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        int64_t v = in[i];
+        uint32_t a = (uint32_t)(v < 0 ? -v : v);
+        m = a > m ? a : m;
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        uint32_t o = __shfl_xor(m, s, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+}
+__global__ void k_absmax_i64(const int64_t* __restrict__ in, uint32_t n, unsigned long long* out) {
+    unsigned long long m = 0;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        int64_t v = in[i];
+        unsigned long long a = v < 0 ? (unsigned long long)(-(v + 1)) + 1 : (unsigned long long)v;
+        m = a > m ? a : m;
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        unsigned long long o = __shfl_xor(m, s, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+}
+// 32x32 LDS tile transpose: out[c*rows + r] = in[r*cols + c]
+__global__ void k_transpose_i32(const int32_t* __restrict__ in, uint32_t rows, uint32_t cols,
+                                int32_t* __restrict__ out) {
+    __shared__ int32_t tile[32][33];
+    uint32_t c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    uint32_t tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: ty 0..7
+    for (uint32_t j = ty; j < 32; j += 8) {
+        uint32_t r = r0 + j, c = c0 + tx;
+        if (r < rows && c < cols) tile[j][tx] = in[(size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (uint32_t j = ty; j < 32; j += 8) {
+        uint32_t c = c0 + j, r = r0 + tx;
+        if (r < rows && c < cols) out[(size_t)c * rows + r] = tile[tx][j];
+    }
+}
+
+void launch_i32_to_planes(hipStream_t s, const int32_t* in, uint32_t n, DevPlanes out) {
+    if (!n) return;
+    k_i32_to_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(in, n, PL_LO(out), PL_HI(out));
+}
+void launch_i64_to_planes(hipStream_t s, const int64_t* in, uint32_t n, DevPlanes out) {
+    if (!n) return;
+    k_i64_to_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(in, n, PL_LO(out), PL_HI(out));
+}
+void launch_aos_to_planes(hipStream_t s, const uint32_t* aos, uint32_t n, DevPlanes out) {
+    if (!n) return;
+    k_aos_to_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(aos, n, PL_LO(out), PL_HI(out));
+}
+void launch_planes_to_aos(hipStream_t s, DevPlanes in, uint32_t n, uint32_t* aos) {
+    if (!n) return;
+    k_planes_to_aos<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(in), PL_HI(in), n, aos);
+}
+void launch_zero_planes(hipStream_t s, DevPlanes t, uint32_t from, uint32_t to) {
+    if (to <= from) return;
+    k_zero_planes<<<grid_for(to - from, NT, 8192), NT, 0, s>>>(PL_LO(t), PL_HI(t), from, to);
+}
+void launch_absmax_i32(hipStream_t s, const int32_t* in, uint32_t n, uint32_t* out) {
+    if (!n) return;
+    k_absmax_i32<<<grid_for(n, NT * 8, 2048), NT, 0, s>>>(in, n, out);
+}
+void launch_absmax_i64(hipStream_t s, const int64_t* in, uint32_t n, unsigned long long* out) {
+    if (!n) return;
+    k_absmax_i64<<<grid_for(n, NT * 8, 2048), NT, 0, s>>>(in, n, out);
+}
+void launch_transpose_i32(hipStream_t s, const int32_t* in, uint32_t rows, uint32_t cols,
+                          int32_t* out) {
+    dim3 g((cols + 31) / 32, (rows + 31) / 32);
+    k_transpose_i32<<<g, NT, 0, s>>>(in, rows, cols, out);
+}
+
+// ------------------------------------------------------------------------------------
+// eq tables
+// ------------------------------------------------------------------------------------
+ZDEV fr_t eq_prod(const uint32_t* __restrict__ fac, uint32_t K, uint32_t b) {
+    fr_t e = one_m();
+    for (uint32_t t = 0; t < K; t++) e = mont_mul(e, ld_aos(fac, 2 * t + ((b >> t) & 1)));
+    return e;
+}
+__global__ void k_eq_mont(const uint32_t* __restrict__ fac, uint32_t K, uint32_t n, uint32_t* out) {
+    for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < n; b += gridDim.x * blockDim.x)
+        st_aos(out, b, eq_prod(fac, K, b));
+}
+__global__ void k_eq_planes(const uint32_t* __restrict__ fac, uint32_t K, uint32_t n, uint4* lo,
+                            uint4* hi) {
+    for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < n; b += gridDim.x * blockDim.x)
+        st_fr(lo, hi, b, mont_mul(eq_prod(fac, K, b), plain_one()));
+}
+void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, uint32_t* out) {
+    k_eq_mont<<<grid_for(n, NT, 4096), NT, 0, s>>>(fac, K, n, out);
+}
+void launch_eq_planes(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, DevPlanes out) {
+    k_eq_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(fac, K, n, PL_LO(out), PL_HI(out));
+}
+
+// ------------------------------------------------------------------------------------
+// eq-weighted reductions of small-integer matrices.
+// Lane i owns output column i and walks rows k of its chunk; the eq weight e_k is the same
+// for every lane (uniform load).  Each integer (offset by 2^bits so it is non-negative) is
+// cut into 20-bit pieces; piece x limb products (< 2^52) accumulate in 64-bit columns
+// without carries for up to 2^11 rows, then one wide Montgomery reduction per piece folds
+// the column sums into the field.  E is in Montgomery form, so the reduction leaves the
+// plain sum.
+// ------------------------------------------------------------------------------------
+template <typename T, int NP>
+__global__ __launch_bounds__(NT) void k_eqdot(const T* __restrict__ M, uint32_t K, uint32_t N,
+                                              const uint32_t* __restrict__ E, uint32_t kchunk,
+                                              uint32_t bits, uint32_t* __restrict__ partial) {
+    const uint32_t i = blockIdx.x * NT + threadIdx.x;
+    const uint32_t c = blockIdx.y;
+    const uint32_t k0 = c * kchunk;
+    const uint32_t k1 = min(K, k0 + kchunk);
+    uint64_t acc[NP][8];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[p][j] = 0;
+    const int64_t off = (int64_t)1 << bits;
+    if (i < N) {
+        const T* col = M + i;
+        for (uint32_t k = k0; k < k1; k++) {
+            const fr_t e = ld_aos(E, k);
+            const uint64_t w = (uint64_t)((int64_t)col[(size_t)k * N] + off);
+#pragma unroll
+            for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (20 * p)) & 0xFFFFFu, e);
+        }
+    }
+    fr_t r = fr_zero();
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        uint32_t t[10];
+        cols_normalize(acc[p], t);
+        fr_t f = redc_wide<10>(t);
+        if (p > 0) f = mont_mul(f, piece_scale(p));
+        r = fr_add(r, f);
+    }
+    if (i < N) st_aos(partial, (size_t)c * N + i, r);
+}
+template <typename T>
+static void eqdot_dispatch(hipStream_t s, const T* M, uint32_t K, uint32_t N, const uint32_t* E,
+                           uint32_t kchunk, uint32_t bits, uint32_t* partial) {
+    dim3 g((N + NT - 1) / NT, (K + kchunk - 1) / kchunk);
+    uint32_t np = (bits + 1 + 19) / 20;
+    if (np <= 1) k_eqdot<T, 1><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
+    else if (np == 2) k_eqdot<T, 2><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
+    else if (np == 3) k_eqdot<T, 3><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
+    else k_eqdot<T, 4><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
+}
+void launch_eqdot_i32(hipStream_t s, const int32_t* M, uint32_t K, uint32_t N, const uint32_t* E,
+                      uint32_t kchunk, uint32_t bits, uint32_t* partial) {
+    eqdot_dispatch<int32_t>(s, M, K, N, E, kchunk, bits, partial);
+}
+void launch_eqdot_i64(hipStream_t s, const int64_t* M, uint32_t K, uint32_t N, const uint32_t* E,
+                      uint32_t kchunk, uint32_t bits, uint32_t* partial) {
+    eqdot_dispatch<int64_t>(s, M, K, N, E, kchunk, bits, partial);
+}
+__global__ void k_sum_chunks(const uint32_t* __restrict__ partial, uint32_t nch, uint32_t N,
+                             uint32_t Npad, fr_t corr, uint4* lo, uint4* hi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < Npad; i += gridDim.x * blockDim.x) {
+        fr_t s = fr_zero();
+        if (i < N) {
+            for (uint32_t c = 0; c < nch; c++) s = fr_add(s, ld_aos(partial, (size_t)c * N + i));
+            s = fr_sub(s, corr);
+        }
+        st_fr(lo, hi, i, s);
+    }
+}
+void launch_sum_chunks(hipStream_t s, const uint32_t* partial, uint32_t nch, uint32_t N,
+                       uint32_t Npad, const uint32_t* corr, DevPlanes out) {
+    k_sum_chunks<<<grid_for(Npad, NT, 4096), NT, 0, s>>>(partial, nch, N, Npad, to_fr(corr),
+                                                       PL_LO(out), PL_HI(out));
+}
+
+// ------------------------------------------------------------------------------------
+// dot products and sums (block partials)
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(NT) void k_dot_planes(const uint4* alo, const uint4* ahi,
+                                                   const uint4* blo, const uint4* bhi, uint32_t n,
+                                                   uint32_t* partial) {
+    fr_t acc[1] = {fr_zero()};
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT)
+        acc[0] = fr_add(acc[0], mont_mul(ld_fr(alo, ahi, i), ld_fr(blo, bhi, i)));
+    block_reduce_store<1>(acc, partial);
+}
+__global__ __launch_bounds__(NT) void k_dot_aos_planes(const uint32_t* __restrict__ a,
+                                                       const uint4* blo, const uint4* bhi,
+                                                       uint32_t n, uint32_t* partial) {
+    fr_t acc[1] = {fr_zero()};
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT)
+        acc[0] = fr_add(acc[0], mont_mul(ld_aos(a, i), ld_fr(blo, bhi, i)));
+    block_reduce_store<1>(acc, partial);
+}
+__global__ __launch_bounds__(NT) void k_sum_planes(const uint4* alo, const uint4* ahi, uint32_t n,
+                                                   uint32_t* partial) {
+    fr_t acc[1] = {fr_zero()};
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT)
+        acc[0] = fr_add(acc[0], ld_fr(alo, ahi, i));
+    block_reduce_store<1>(acc, partial);
+}
+uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, uint32_t* partial) {
+    uint32_t g = grid_for(n, NT * 4, 1024);
+    k_dot_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n, partial);
+    return g;
+}
+uint32_t launch_dot_aos_planes(hipStream_t s, const uint32_t* a, DevPlanes b, uint32_t n,
+                               uint32_t* partial) {
+    uint32_t g = grid_for(n, NT * 4, 1024);
+    k_dot_aos_planes<<<g, NT, 0, s>>>(a, PL_LO(b), PL_HI(b), n, partial);
+    return g;
+}
+uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, uint32_t* partial) {
+    uint32_t g = grid_for(n, NT * 8, 1024);
+    k_sum_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), n, partial);
+    return g;
+}
+
+// ------------------------------------------------------------------------------------
+// generic MLE pieces
+// ------------------------------------------------------------------------------------
+template <typename Ld>
+__global__ void k_partial_me(Ld ld, uint32_t O, uint32_t C, uint32_t W,
+                             const uint32_t* __restrict__ E, uint4* olo, uint4* ohi) {
+    const uint32_t total = O * W;
+    for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < total; g += gridDim.x * blockDim.x) {
+        uint32_t o = g / W, w = g % W;
+        fr_t acc = fr_zero();
+        for (uint32_t c = 0; c < C; c++)
+            acc = fr_add(acc, mont_mul(ld_aos(E, c), ld(((size_t)o * C + c) * W + w)));
+        st_fr(olo, ohi, g, acc);
+    }
+}
+struct LdPlanes {
+    const uint4* lo;
+    const uint4* hi;
+    ZDEV fr_t operator()(size_t i) const { return ld_fr(lo, hi, (uint32_t)i); }
+};
+struct LdI32 {
+    const int32_t* p;
+    ZDEV fr_t operator()(size_t i) const { return fr_from_i64(p[i]); }
+};
+struct LdI64 {
+    const int64_t* p;
+    ZDEV fr_t operator()(size_t i) const { return fr_from_i64(p[i]); }
+};
+void launch_partial_me_planes(hipStream_t s, DevPlanes t, uint32_t O, uint32_t C, uint32_t W,
+                              const uint32_t* E, DevPlanes out) {
+    LdPlanes ld{PL_LO(t), PL_HI(t)};
+    k_partial_me<<<grid_for(O * W, NT, 8192), NT, 0, s>>>(ld, O, C, W, E, PL_LO(out), PL_HI(out));
+}
+void launch_partial_me_i32(hipStream_t s, const int32_t* t, uint32_t O, uint32_t C, uint32_t W,
+                           const uint32_t* E, DevPlanes out) {
+    LdI32 ld{t};
+    k_partial_me<<<grid_for(O * W, NT, 8192), NT, 0, s>>>(ld, O, C, W, E, PL_LO(out), PL_HI(out));
+}
+void launch_partial_me_i64(hipStream_t s, const int64_t* t, uint32_t O, uint32_t C, uint32_t W,
+                           const uint32_t* E, DevPlanes out) {
+    LdI64 ld{t};
+    k_partial_me<<<grid_for(O * W, NT, 8192), NT, 0, s>>>(ld, O, C, W, E, PL_LO(out), PL_HI(out));
+}
+
+ZDEV fr_t fold_at(const uint4* lo, const uint4* hi, uint32_t j, uint32_t n, const fr_t& vm) {
+    fr_t x = ld_fr(lo, hi, j), y = ld_fr(lo, hi, j + n);
+    return fr_add(x, mont_mul(vm, fr_sub(y, x)));
+}
+// A table taking part in a fused round: read from (slo, shi); when the round folds, the
+// folded entries go to (dlo, dhi), which may alias the source (in-place halving).
+struct TabDev {
+    const uint4* slo;
+    const uint4* shi;
+    uint4* dlo;
+    uint4* dhi;
+};
+static inline TabDev tab_dev(const Tab& t) {
+    return TabDev{reinterpret_cast<const uint4*>(t.src.lo()), reinterpret_cast<const uint4*>(t.src.hi()),
+                  reinterpret_cast<uint4*>(t.dst.lo()), reinterpret_cast<uint4*>(t.dst.hi())};
+}
+// entries i and i+h of this round's table (folding the previous round's table of size 2n
+// when fold is set, and storing the folded pair)
+ZDEV void load_pair(const TabDev& t, uint32_t i, uint32_t h, uint32_t n, int fold, const fr_t& vm,
+                    fr_t& x0, fr_t& x1) {
+    if (fold) {
+        x0 = fold_at(t.slo, t.shi, i, n, vm);
+        x1 = fold_at(t.slo, t.shi, i + h, n, vm);
+        st_fr(t.dlo, t.dhi, i, x0);
+        st_fr(t.dlo, t.dhi, i + h, x1);
+    } else {
+        x0 = ld_fr(t.slo, t.shi, i);
+        x1 = ld_fr(t.slo, t.shi, i + h);
+    }
+}
+__global__ void k_fold(TabDev t, uint32_t h, fr_t vm) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < h; i += gridDim.x * blockDim.x)
+        st_fr(t.dlo, t.dhi, i, fold_at(t.slo, t.shi, i, h, vm));
+}
+void launch_fold(hipStream_t s, Tab t, uint32_t h, const uint32_t* v_m_host) {
+    k_fold<<<grid_for(h, NT, 8192), NT, 0, s>>>(tab_dev(t), h, to_fr(v_m_host));
+}
+__global__ void k_axpy(const uint4* alo, const uint4* ahi, fr_t cm, const uint4* blo,
+                       const uint4* bhi, uint32_t n, uint4* olo, uint4* ohi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        st_fr(olo, ohi, i, fr_add(ld_fr(alo, ahi, i), mont_mul(cm, ld_fr(blo, bhi, i))));
+}
+void launch_axpy(hipStream_t s, DevPlanes a, const uint32_t* c_m_host, DevPlanes b, uint32_t n,
+                 DevPlanes out) {
+    k_axpy<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(a), PL_HI(a), to_fr(c_m_host), PL_LO(b),
+                                                PL_HI(b), n, PL_LO(out), PL_HI(out));
+}
+__global__ void k_hadamard(const uint4* alo, const uint4* ahi, const uint4* blo, const uint4* bhi,
+                           uint32_t n, uint4* olo, uint4* ohi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        st_fr(olo, ohi, i,
+              mont_mul(mont_mul(ld_fr(alo, ahi, i), ld_fr(blo, bhi, i)), r2_m()));
+}
+void launch_hadamard(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, DevPlanes out) {
+    k_hadamard<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n,
+                                                    PL_LO(out), PL_HI(out));
+}
+
+// ------------------------------------------------------------------------------------
+// matmul (zkip) sumcheck round (zkfc.cu:94-127 poly + reduce, fused)
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(NT) void k_zkip_round(TabDev a, TabDev b, uint32_t n, int fold,
+                                                   fr_t vm, uint32_t* partial) {
+    const uint32_t h = n >> 1;
+    fr_t acc[3] = {fr_zero(), fr_zero(), fr_zero()};
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        fr_t a0, a1, b0, b1;
+        load_pair(a, i, h, n, fold, vm, a0, a1);
+        load_pair(b, i, h, n, fold, vm, b0, b1);
+        acc[0] = fr_add(acc[0], mont_mul(a0, b0));
+        acc[1] = fr_add(acc[1], mont_mul(a1, b1));
+        acc[2] = fr_add(acc[2], mont_mul(fr_sub(a1, a0), fr_sub(b1, b0)));
+    }
+    block_reduce_store<3>(acc, partial);
+}
+uint32_t launch_zkip_round(hipStream_t s, Tab a, Tab b, uint32_t n, int fold,
+                           const uint32_t* v_m_host, uint32_t* partial) {
+    uint32_t g = grid_for(n >> 1, NT * 2, 512);
+    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
+    k_zkip_round<<<g, NT, 0, s>>>(tab_dev(a), tab_dev(b), n, fold, vm, partial);
+    return g;
+}
+
+// ------------------------------------------------------------------------------------
+// logUp: multiplicities, mapping, batched inversion
+// ------------------------------------------------------------------------------------
+__global__ void k_lu_count_planes(const uint4* lo, const uint4* hi, uint32_t n, fr_t low,
+                                  uint32_t N, uint32_t* counts, uint32_t* bad) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        uint32_t idx = fr_sub(ld_fr(lo, hi, i), low).v[0];  // limb 0 (tlookup.cu:419)
+        if (idx < N) atomicAdd(&counts[idx], 1u);
+        else atomicOr(bad, 1u);
+    }
+}
+// limb 0 of the field element (v - low) for int32 v, low
+ZDEV uint32_t lu_index_i32(int32_t v, int32_t low) {
+    int64_t d = (int64_t)v - low;
+    return d >= 0 ? (uint32_t)d : (uint32_t)(1u - (uint32_t)(-d));
+}
+__global__ void k_lu_count_i32(const int32_t* __restrict__ S, uint32_t n, int32_t low, uint32_t N,
+                               uint32_t* counts, uint32_t* bad) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        uint32_t idx = lu_index_i32(S[i], low);
+        if (idx < N) atomicAdd(&counts[idx], 1u);
+        else atomicOr(bad, 1u);
+    }
+}
+__global__ void k_counts_to_planes(const uint32_t* __restrict__ counts, uint32_t N, uint4* lo,
+                                   uint4* hi) {
+    for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < N; j += gridDim.x * blockDim.x) {
+        fr_t m = fr_zero();
+        m.v[0] = counts[j];
+        st_fr(lo, hi, j, m);
+    }
+}
+void launch_lu_count_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
+                            uint32_t N, uint32_t* counts, uint32_t* bad) {
+    k_lu_count_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(low_host),
+                                                         N, counts, bad);
+}
+void launch_lu_count_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low, uint32_t N,
+                         uint32_t* counts, uint32_t* bad) {
+    k_lu_count_i32<<<grid_for(n, NT, 8192), NT, 0, s>>>(S, n, low, N, counts, bad);
+}
+void launch_counts_to_planes(hipStream_t s, const uint32_t* counts, uint32_t N, DevPlanes m) {
+    k_counts_to_planes<<<grid_for(N, NT, 8192), NT, 0, s>>>(counts, N, PL_LO(m), PL_HI(m));
+}
+__global__ void k_lu_map_planes(const uint4* lo, const uint4* hi, uint32_t n, fr_t low,
+                                const uint4* mlo, const uint4* mhi, uint32_t N, uint4* olo,
+                                uint4* ohi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        uint32_t idx = fr_sub(ld_fr(lo, hi, i), low).v[0];
+        st_fr(olo, ohi, i, idx < N ? ld_fr(mlo, mhi, idx) : fr_zero());
+    }
+}
+__global__ void k_lu_map_i32(const int32_t* __restrict__ S, uint32_t n, int32_t low,
+                             const uint4* mlo, const uint4* mhi, uint32_t N, uint4* olo,
+                             uint4* ohi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        uint32_t idx = lu_index_i32(S[i], low);
+        st_fr(olo, ohi, i, idx < N ? ld_fr(mlo, mhi, idx) : fr_zero());
+    }
+}
+void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
+                          DevPlanes mapped, DevPlanes out) {
+    k_lu_map_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(low_host),
+                                                       PL_LO(mapped), PL_HI(mapped), mapped.cap,
+                                                       PL_LO(out), PL_HI(out));
+}
+void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
+                       DevPlanes mapped, DevPlanes out) {
+    k_lu_map_i32<<<grid_for(n, NT, 8192), NT, 0, s>>>(S, n, low, PL_LO(mapped), PL_HI(mapped),
+                                                    mapped.cap, PL_LO(out), PL_HI(out));
+}
+
+// Batched inversion (Montgomery's trick).  Block b covers INV_CHK*NT entries; thread t
+// owns entries base + j*NT + t.  Pass 1 stores running products (Montgomery domain) in A
+// and a block-wide inclusive prefix/suffix scan of the thread totals gives each thread
+// the product of all OTHER threads' totals.  The block total goes to blockprod; the host
+// inverts all block totals with one more Montgomery trick and a single exponentiation.
+// Pass 2 walks each thread's entries backwards.  Zero entries (x+beta = 0) take 1 in the
+// products and produce 0, the reference's Fermat convention.
+#define INV_CHK 16
+__global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4* shi, uint32_t n,
+                                                  fr_t beta, uint4* alo, uint4* ahi,
+                                                  uint32_t* others, uint32_t* blockprod) {
+    __shared__ fr_t pre[NT], suf[NT];
+    const uint32_t t = threadIdx.x;
+    const uint32_t base = blockIdx.x * NT * INV_CHK;
+    fr_t run = one_m();
+    for (uint32_t j = 0; j < INV_CHK; j++) {
+        uint32_t idx = base + j * NT + t;
+        if (idx < n) {
+            fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
+            fr_t xm = fr_is_zero(x) ? one_m() : mont_mul(x, r2_m());
+            run = mont_mul(run, xm);
+            st_fr(alo, ahi, idx, run);
+        }
+    }
+    pre[t] = run;
+    suf[t] = run;
+    __syncthreads();
+    for (uint32_t off = 1; off < NT; off <<= 1) {
+        fr_t p = pre[t], q = suf[t];
+        fr_t pp = t >= off ? pre[t - off] : one_m();
+        fr_t qq = t + off < NT ? suf[t + off] : one_m();
+        __syncthreads();
+        pre[t] = mont_mul(p, pp);
+        suf[t] = mont_mul(q, qq);
+        __syncthreads();
+    }
+    fr_t ex_pre = t > 0 ? pre[t - 1] : one_m();
+    fr_t ex_suf = t + 1 < NT ? suf[t + 1] : one_m();
+    st_aos(others, blockIdx.x * NT + t, mont_mul(ex_pre, ex_suf));
+    if (t == NT - 1) st_aos(blockprod, blockIdx.x, pre[NT - 1]);
+}
+__global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4* shi, uint32_t n,
+                                                  fr_t beta, uint4* alo, uint4* ahi,
+                                                  const uint32_t* __restrict__ others,
+                                                  const uint32_t* __restrict__ blockinv) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t base = blockIdx.x * NT * INV_CHK;
+    // 1/run_t = 1/blockprod * prod(other threads' runs)
+    fr_t y = mont_mul(ld_aos(blockinv, blockIdx.x), ld_aos(others, blockIdx.x * NT + t));
+    for (int j = INV_CHK - 1; j >= 0; j--) {
+        uint32_t idx = base + (uint32_t)j * NT + t;
+        if (idx >= n) continue;
+        fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
+        bool z = fr_is_zero(x);
+        fr_t xm = z ? one_m() : mont_mul(x, r2_m());
+        fr_t prev = j > 0 ? ld_fr(alo, ahi, idx - NT) : one_m();
+        fr_t inv_m = mont_mul(y, prev);
+        y = mont_mul(y, xm);
+        st_fr(alo, ahi, idx, z ? fr_zero() : mont_mul(inv_m, plain_one()));
+    }
+}
+uint32_t inv_blocks(uint32_t n) { return (n + NT * INV_CHK - 1) / (NT * INV_CHK); }
+void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
+                      DevPlanes A, uint32_t* others, uint32_t* blockprod) {
+    k_inv_pass1<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
+                                             PL_HI(A), others, blockprod);
+}
+void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
+                      DevPlanes A, const uint32_t* others, const uint32_t* blockinv) {
+    k_inv_pass2<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
+                                             PL_HI(A), others, blockinv);
+}
+
+// ------------------------------------------------------------------------------------
+// eq weighting for pair sums: eq(i, u[0..K)) = elo[i & 1023] * ehi(i >> 10)
+// ------------------------------------------------------------------------------------
+struct EqDev {
+    const uint32_t* elo;
+    const uint32_t* fac;
+    uint32_t K;
+};
+ZDEV fr_t eq_hi(const EqDev& eq, uint32_t row) {
+    fr_t e = one_m();
+    for (uint32_t t = 10; t < eq.K; t++) e = mont_mul(e, ld_aos(eq.fac, 2 * t + ((row >> (t - 10)) & 1)));
+    return e;
+}
+
+// phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
+// acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
+__global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, int fold, fr_t vm,
+                                                  fr_t beta, EqDev eq, uint32_t* partial) {
+    const uint32_t h = n >> 1;
+    fr_t acc[5];
+#pragma unroll
+    for (int k = 0; k < 5; k++) acc[k] = fr_zero();
+    const uint32_t rows = (h + 1023) >> 10;
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const fr_t ehi = eq_hi(eq, row);
+        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
+            const uint32_t i = (row << 10) + lo;
+            if (i >= h) break;
+            fr_t a0, a1, s0, s1;
+            load_pair(A, i, h, n, fold, vm, a0, a1);
+            load_pair(S, i, h, n, fold, vm, s0, s1);
+            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+            s0 = fr_add(s0, beta);
+            s1 = fr_add(s1, beta);
+            const fr_t wa0 = mont_mul(w, a0);
+            const fr_t wda = mont_mul(w, fr_sub(a1, a0));
+            const fr_t wa1 = fr_add(wa0, wda);
+            acc[0] = fr_add(acc[0], mont_mul(wa0, s0));
+            acc[1] = fr_add(acc[1], mont_mul(wa1, s1));
+            acc[2] = fr_add(acc[2], mont_mul(wda, fr_sub(s1, s0)));
+            acc[3] = fr_add(acc[3], a0);
+            acc[4] = fr_add(acc[4], a1);
+        }
+    }
+    block_reduce_store<5>(acc, partial);
+}
+uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
+                          const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
+                          uint32_t* partial) {
+    uint32_t rows = ((n >> 1) + 1023) >> 10;
+    uint32_t g = rows < 1024 ? rows : 1024;
+    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
+    EqDev e{eq.elo, eq.fac, eq.K};
+    k_lu_phase1<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, fold, vm, to_fr(beta_host), e, partial);
+    return g;
+}
+
+// phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused):
+// acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds; 3..5: sum w*b0*t0, w*b1*t1, w*db*dt (x 2^-256);
+// 6, 7: sum a0, sum a1; 8..10: sum m0*b0, m1*b1, dm*db (x 2^-256)
+__global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m,
+                                                  uint32_t n, int fold_as, int fold_btm, fr_t vm,
+                                                  fr_t beta, EqDev eq, uint32_t* partial) {
+    const uint32_t h = n >> 1;
+    fr_t acc[11];
+#pragma unroll
+    for (int k = 0; k < 11; k++) acc[k] = fr_zero();
+    const uint32_t rows = (h + 1023) >> 10;
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const fr_t ehi = eq_hi(eq, row);
+        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
+            const uint32_t i = (row << 10) + lo;
+            if (i >= h) break;
+            fr_t a0, a1, s0, s1, b0, b1, t0, t1, m0, m1;
+            load_pair(A, i, h, n, fold_as, vm, a0, a1);
+            load_pair(S, i, h, n, fold_as, vm, s0, s1);
+            load_pair(B, i, h, n, fold_btm, vm, b0, b1);
+            load_pair(T, i, h, n, fold_btm, vm, t0, t1);
+            load_pair(m, i, h, n, fold_btm, vm, m0, m1);
+            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+            s0 = fr_add(s0, beta);
+            s1 = fr_add(s1, beta);
+            t0 = fr_add(t0, beta);
+            t1 = fr_add(t1, beta);
+            {
+                const fr_t wa0 = mont_mul(w, a0);
+                const fr_t wda = mont_mul(w, fr_sub(a1, a0));
+                const fr_t wa1 = fr_add(wa0, wda);
+                acc[0] = fr_add(acc[0], mont_mul(wa0, s0));
+                acc[1] = fr_add(acc[1], mont_mul(wa1, s1));
+                acc[2] = fr_add(acc[2], mont_mul(wda, fr_sub(s1, s0)));
+            }
+            const fr_t db = fr_sub(b1, b0);
+            {
+                const fr_t wb0 = mont_mul(w, b0);
+                const fr_t wdb = mont_mul(w, db);
+                const fr_t wb1 = fr_add(wb0, wdb);
+                acc[3] = fr_add(acc[3], mont_mul(wb0, t0));
+                acc[4] = fr_add(acc[4], mont_mul(wb1, t1));
+                acc[5] = fr_add(acc[5], mont_mul(wdb, fr_sub(t1, t0)));
+            }
+            acc[6] = fr_add(acc[6], a0);
+            acc[7] = fr_add(acc[7], a1);
+            acc[8] = fr_add(acc[8], mont_mul(m0, b0));
+            acc[9] = fr_add(acc[9], mont_mul(m1, b1));
+            acc[10] = fr_add(acc[10], mont_mul(fr_sub(m1, m0), db));
+        }
+    }
+    block_reduce_store<11>(acc, partial);
+}
+uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
+                          int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
+                          EqW eq, uint32_t* partial) {
+    uint32_t rows = ((n >> 1) + 1023) >> 10;
+    uint32_t g = rows < 1024 ? rows : 1024;
+    fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
+    EqDev e{eq.elo, eq.fac, eq.K};
+    k_lu_phase2<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), tab_dev(m), n,
+                                 fold_as, fold_btm, vm, to_fr(beta_host), e, partial);
+    return g;
+}
+
+// ------------------------------------------------------------------------------------
+// Hadamard sumcheck rounds (zkob_lookup.cuh:212-233 k_hp3_step + k_fr_fold, fused)
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, uint32_t n, int fold,
+                                                 fr_t vm, uint32_t* partial) {
+    const uint32_t h = n >> 1;
+    fr_t acc[4] = {fr_zero(), fr_zero(), fr_zero(), fr_zero()};
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        fr_t e0, e1, s0, s1, u0, u1;
+        load_pair(E, i, h, n, fold, vm, e0, e1);
+        load_pair(S, i, h, n, fold, vm, s0, s1);
+        load_pair(U, i, h, n, fold, vm, u0, u1);
+        const fr_t de = fr_sub(e1, e0), ds = fr_sub(s1, s0), du = fr_sub(u1, u0);
+        fr_t e = e0, s_ = s0, u = u0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            acc[t] = fr_add(acc[t], mont_mul(mont_mul(e, s_), u));
+            if (t < 3) {
+                e = fr_add(e, de);
+                s_ = fr_add(s_, ds);
+                u = fr_add(u, du);
+            }
+        }
+    }
+    block_reduce_store<4>(acc, partial);
+}
+uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fold,
+                         const uint32_t* v_m_host, uint32_t* partial) {
+    uint32_t g = grid_for(n >> 1, NT * 2, 1024);
+    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
+    k_hp_round<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, partial);
+    return g;
+}
+// eq-specialised: sums_t = sum_i eq(i, u[0..K)) S_t[i] U_t[i]  (x 2^-256)
+__global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
+                                                    EqDev eq, uint32_t* partial) {
+    const uint32_t h = n >> 1;
+    fr_t acc[4] = {fr_zero(), fr_zero(), fr_zero(), fr_zero()};
+    const uint32_t rows = (h + 1023) >> 10;
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const fr_t ehi = eq_hi(eq, row);
+        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
+            const uint32_t i = (row << 10) + lo;
+            if (i >= h) break;
+            fr_t s0, s1, u0, u1;
+            load_pair(S, i, h, n, fold, vm, s0, s1);
+            load_pair(U, i, h, n, fold, vm, u0, u1);
+            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+            const fr_t ws0 = mont_mul(w, s0);
+            const fr_t wds = mont_mul(w, fr_sub(s1, s0));
+            const fr_t du = fr_sub(u1, u0);
+            fr_t ws = ws0, u = u0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                acc[t] = fr_add(acc[t], mont_mul(ws, u));
+                if (t < 3) {
+                    ws = fr_add(ws, wds);
+                    u = fr_add(u, du);
+                }
+            }
+        }
+    }
+    block_reduce_store<4>(acc, partial);
+}
+uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
+                            const uint32_t* v_m_host, EqW eq, uint32_t* partial) {
+    uint32_t rows = ((n >> 1) + 1023) >> 10;
+    uint32_t g = rows < 1024 ? rows : 1024;
+    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
+    EqDev e{eq.elo, eq.fac, eq.K};
+    k_hp_eq_round<<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, e, partial);
+    return g;
+}
+// sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n
+__global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* shi, const uint4* ulo,
+                                               const uint4* uhi, int has_u, uint32_t n, EqDev eq,
+                                               uint32_t* partial) {
+    fr_t acc[1] = {fr_zero()};
+    const uint32_t rows = (n + 1023) >> 10;
+    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const fr_t ehi = eq_hi(eq, row);
+        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
+            const uint32_t i = (row << 10) + lo;
+            if (i >= n) break;
+            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+            fr_t ws = mont_mul(w, ld_fr(slo, shi, i));
+            if (has_u) ws = mont_mul(ws, ld_fr(ulo, uhi, i));
+            acc[0] = fr_add(acc[0], ws);
+        }
+    }
+    block_reduce_store<1>(acc, partial);
+}
+uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
+                       uint32_t* partial) {
+    uint32_t rows = (n + 1023) >> 10;
+    uint32_t g = rows < 1024 ? rows : 1024;
+    EqDev e{eq.elo, eq.fac, eq.K};
+    k_eq_sum<<<g, NT, 0, s>>>(PL_LO(S), PL_HI(S), U ? PL_LO(*U) : nullptr, U ? PL_HI(*U) : nullptr,
+                              U ? 1 : 0, n, e, partial);
+    return g;
+}
+
+}  // namespace zkh

@@ -1,0 +1,135 @@
+// kernels.hpp -- launch wrappers for the gfx950 kernels in kernels.hip.
+//
+// All wrappers enqueue on the given stream and return immediately.  Device tables of
+// full field elements use the limb-quad layout (FrPlanes: lo/hi uint4 planes of `cap`
+// entries); small vectors (eq factor tables, partial sums) use the reference's AoS Fr_t
+// layout (8 consecutive uint32 per element).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zkh {
+
+struct DevPlanes {
+    uint32_t* base;  // lo plane at base, hi plane at base + 4*cap uint32
+    uint32_t cap;
+    uint32_t* lo() const { return base; }
+    uint32_t* hi() const { return base + 4 * (size_t)cap; }
+};
+
+// A table in a fused fold+evaluate round: read from src; folded entries go to dst (which
+// may be src itself).  The first fold of a caller-owned table targets a scratch copy.
+struct Tab {
+    DevPlanes src;
+    DevPlanes dst;
+};
+
+// One eq weighting: eq(i, u[0..K)) = Elo[i & 1023] * Ehi(i >> 10) with Elo built over
+// u[0..10) and Ehi over u[10..K) from the Montgomery factor table fac (fac[2t] = mont(1-u_t),
+// fac[2t+1] = mont(u_t)).  When K < 10 the caller supplies the correction factor on the host.
+struct EqW {
+    const uint32_t* elo;  // AoS, 1024 entries, Montgomery form
+    const uint32_t* fac;  // AoS, 2 per variable, Montgomery form
+    uint32_t K;           // number of variables of this weighting
+};
+
+// ---- conversions / layout ----
+void launch_i32_to_planes(hipStream_t s, const int32_t* in, uint32_t n, DevPlanes out);
+void launch_i64_to_planes(hipStream_t s, const int64_t* in, uint32_t n, DevPlanes out);
+void launch_aos_to_planes(hipStream_t s, const uint32_t* aos, uint32_t n, DevPlanes out);
+void launch_planes_to_aos(hipStream_t s, DevPlanes in, uint32_t n, uint32_t* aos);
+void launch_zero_planes(hipStream_t s, DevPlanes t, uint32_t from, uint32_t to);
+void launch_absmax_i32(hipStream_t s, const int32_t* in, uint32_t n, uint32_t* out);
+void launch_absmax_i64(hipStream_t s, const int64_t* in, uint32_t n, unsigned long long* out);
+void launch_transpose_i32(hipStream_t s, const int32_t* in, uint32_t rows, uint32_t cols,
+                          int32_t* out);
+
+// ---- eq tables ----
+// out[b] = prod_t fac[2t + bit_t(b)] (Montgomery form) for b < n, AoS; K = #factors
+void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, uint32_t* out);
+// plain eq table into planes
+void launch_eq_planes(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, DevPlanes out);
+
+// ---- eq-weighted reductions of integer matrices ----
+// partial[c*N + i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) * e_k   (plain, AoS)
+// E: Montgomery-form AoS eq table over k.  Chunks of kchunk <= 2048 rows.
+void launch_eqdot_i32(hipStream_t s, const int32_t* M, uint32_t K, uint32_t N, const uint32_t* E,
+                      uint32_t kchunk, uint32_t bits, uint32_t* partial);
+void launch_eqdot_i64(hipStream_t s, const int64_t* M, uint32_t K, uint32_t N, const uint32_t* E,
+                      uint32_t kchunk, uint32_t bits, uint32_t* partial);
+// out[i] = sum_c partial[c*N+i] - corr for i < N, 0 for N <= i < Npad
+void launch_sum_chunks(hipStream_t s, const uint32_t* partial, uint32_t nch, uint32_t N,
+                       uint32_t Npad, const uint32_t* corr, DevPlanes out);
+
+// ---- dot products / sums (block partials, AoS, summed on the host) ----
+// partial[b] = sum montmul(a_i, b_i) over the block's range (carries 2^-256)
+uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, uint32_t* partial);
+// partial[b] = sum montmul(Eaos_i, b_i)
+uint32_t launch_dot_aos_planes(hipStream_t s, const uint32_t* a, DevPlanes b, uint32_t n,
+                               uint32_t* partial);
+uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, uint32_t* partial);
+
+// ---- generic MLE pieces ----
+// out[o*W + w] = sum_{c < C} montmul(E_m[c], t[(o*C + c)*W + w])  (t as FR planes)
+void launch_partial_me_planes(hipStream_t s, DevPlanes t, uint32_t O, uint32_t C, uint32_t W,
+                              const uint32_t* E, DevPlanes out);
+void launch_partial_me_i32(hipStream_t s, const int32_t* t, uint32_t O, uint32_t C, uint32_t W,
+                           const uint32_t* E, DevPlanes out);
+void launch_partial_me_i64(hipStream_t s, const int64_t* t, uint32_t O, uint32_t C, uint32_t W,
+                           const uint32_t* E, DevPlanes out);
+// MSB fold dst[i] = src[i] + v*(src[i+h]-src[i]), i < h (v in Montgomery form)
+void launch_fold(hipStream_t s, Tab t, uint32_t h, const uint32_t* v_m_host);
+void launch_axpy(hipStream_t s, DevPlanes a, const uint32_t* c_m_host, DevPlanes b, uint32_t n,
+                 DevPlanes out);
+void launch_hadamard(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, DevPlanes out);
+
+// ---- matmul sumcheck round: pairs (i, i+n/2) of tables a, b of size n ----
+// fold != 0: the buffers hold the previous round's tables (size 2n) and are folded in
+// place with v first.  partial per block: sum a0b0, sum a1b1, sum da*db (2^-256 each).
+uint32_t launch_zkip_round(hipStream_t s, Tab a, Tab b, uint32_t n, int fold,
+                           const uint32_t* v_m_host, uint32_t* partial);
+
+// ---- logUp ----
+void launch_lu_count_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
+                            uint32_t N, uint32_t* counts, uint32_t* bad);
+void launch_lu_count_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low, uint32_t N,
+                         uint32_t* counts, uint32_t* bad);
+void launch_counts_to_planes(hipStream_t s, const uint32_t* counts, uint32_t N, DevPlanes m);
+void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
+                          DevPlanes mapped, DevPlanes out);
+void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
+                       DevPlanes mapped, DevPlanes out);
+// A[i] = 1/(S[i]+beta) (0 -> 0), Montgomery's batched inversion in two passes around a
+// host step: pass 1 writes running products to A, per-thread "other threads" products to
+// `others` (inv_blocks(n)*256 AoS) and block totals to blockprod (inv_blocks(n) AoS, in
+// Montgomery form); the host writes blockinv[b] = 1/blockprod[b] (Montgomery form);
+// pass 2 writes the plain inverses into A.
+uint32_t inv_blocks(uint32_t n);
+void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
+                      DevPlanes A, uint32_t* others, uint32_t* blockprod);
+void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
+                      DevPlanes A, const uint32_t* others, const uint32_t* blockinv);
+// phase-1 round over A, S (size n): sums e*a0*s0, e*a1*s1, e*da*ds (x 2^-256), a0, a1
+uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
+                          const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
+                          uint32_t* partial);
+// phase-2 round over A, S, B, T, m: 11 sums (see kernels.hip)
+uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
+                          int fold_as, int fold_btm,
+                          const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
+                          uint32_t* partial);
+
+// ---- Hadamard ----
+// generic: sums_t = sum E_t*S_t*U_t, t = 0..3 (x 2^-512)
+uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
+                         int fold, const uint32_t* v_m_host, uint32_t* partial);
+// eq-specialised: sums_t = sum eq(i,u_)*S_t*U_t, t = 0..3 (x 2^-256)
+uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
+                            const uint32_t* v_m_host, EqW eq, uint32_t* partial);
+// sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)
+uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
+                       uint32_t* partial);
+
+uint32_t grid_for(uint32_t work_items, uint32_t per_block, uint32_t max_blocks);
+
+}  // namespace zkh

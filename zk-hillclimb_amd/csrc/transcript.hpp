@@ -1,0 +1,160 @@
+// transcript.hpp -- the reference's SHA-256 Fiat-Shamir transcript (fs_transcript.hpp:115-166)
+// and Fr challenge derivation (vrf_common.cuh:219-250), host side.
+//
+//   state_0 = SHA256(seed)
+//   absorb(label, data): state = SHA256(state || le32(|label|) || label || le64(|data|) || data)
+//   challenge_bytes():   out = SHA256(state || "chal"); state = SHA256(state || "rtch")
+//   challenge_fr():      8 LE u32 limbs of out, limb 7 %= 1944954707, redraw while zero
+//
+// SHA-256 itself follows FIPS 180-4.
+#pragma once
+#include <stdint.h>
+#include <string.h>
+
+#include "fr_host.hpp"
+
+namespace zkh {
+
+struct Sha256 {
+    uint32_t h[8];
+    uint64_t len;
+    uint8_t buf[64];
+    uint32_t blen;
+
+    static uint32_t rotr(uint32_t x, int n) { return (x >> n) | (x << (32 - n)); }
+    void init() {
+        static const uint32_t iv[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a,
+                                       0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
+        memcpy(h, iv, sizeof(iv));
+        len = 0;
+        blen = 0;
+    }
+    void block(const uint8_t* p) {
+        static const uint32_t K[64] = {
+            0x428a2f98, 0x71374491, 0xb5c0fbcf, 0xe9b5dba5, 0x3956c25b, 0x59f111f1, 0x923f82a4,
+            0xab1c5ed5, 0xd807aa98, 0x12835b01, 0x243185be, 0x550c7dc3, 0x72be5d74, 0x80deb1fe,
+            0x9bdc06a7, 0xc19bf174, 0xe49b69c1, 0xefbe4786, 0x0fc19dc6, 0x240ca1cc, 0x2de92c6f,
+            0x4a7484aa, 0x5cb0a9dc, 0x76f988da, 0x983e5152, 0xa831c66d, 0xb00327c8, 0xbf597fc7,
+            0xc6e00bf3, 0xd5a79147, 0x06ca6351, 0x14292967, 0x27b70a85, 0x2e1b2138, 0x4d2c6dfc,
+            0x53380d13, 0x650a7354, 0x766a0abb, 0x81c2c92e, 0x92722c85, 0xa2bfe8a1, 0xa81a664b,
+            0xc24b8b70, 0xc76c51a3, 0xd192e819, 0xd6990624, 0xf40e3585, 0x106aa070, 0x19a4c116,
+            0x1e376c08, 0x2748774c, 0x34b0bcb5, 0x391c0cb3, 0x4ed8aa4a, 0x5b9cca4f, 0x682e6ff3,
+            0x748f82ee, 0x78a5636f, 0x84c87814, 0x8cc70208, 0x90befffa, 0xa4506ceb, 0xbef9a3f7,
+            0xc67178f2};
+        uint32_t w[64];
+        for (int i = 0; i < 16; i++)
+            w[i] = ((uint32_t)p[4 * i] << 24) | ((uint32_t)p[4 * i + 1] << 16) |
+                   ((uint32_t)p[4 * i + 2] << 8) | (uint32_t)p[4 * i + 3];
+        for (int i = 16; i < 64; i++) {
+            uint32_t s0 = rotr(w[i - 15], 7) ^ rotr(w[i - 15], 18) ^ (w[i - 15] >> 3);
+            uint32_t s1 = rotr(w[i - 2], 17) ^ rotr(w[i - 2], 19) ^ (w[i - 2] >> 10);
+            w[i] = w[i - 16] + s0 + w[i - 7] + s1;
+        }
+        uint32_t a = h[0], b = h[1], c = h[2], d = h[3], e = h[4], f = h[5], g = h[6],
+                 hh = h[7];
+        for (int i = 0; i < 64; i++) {
+            uint32_t t1 = hh + (rotr(e, 6) ^ rotr(e, 11) ^ rotr(e, 25)) + ((e & f) ^ (~e & g)) +
+                          K[i] + w[i];
+            uint32_t t2 = (rotr(a, 2) ^ rotr(a, 13) ^ rotr(a, 22)) + ((a & b) ^ (a & c) ^ (b & c));
+            hh = g;
+            g = f;
+            f = e;
+            e = d + t1;
+            d = c;
+            c = b;
+            b = a;
+            a = t1 + t2;
+        }
+        h[0] += a; h[1] += b; h[2] += c; h[3] += d;
+        h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
+    }
+    void update(const void* data, size_t n) {
+        const uint8_t* p = (const uint8_t*)data;
+        len += n;
+        while (n) {
+            size_t take = 64 - blen;
+            if (take > n) take = n;
+            memcpy(buf + blen, p, take);
+            blen += (uint32_t)take;
+            p += take;
+            n -= take;
+            if (blen == 64) {
+                block(buf);
+                blen = 0;
+            }
+        }
+    }
+    void final(uint8_t out[32]) {
+        uint64_t bits = len * 8;
+        uint8_t pad = 0x80, z = 0;
+        update(&pad, 1);
+        while (blen != 56) update(&z, 1);
+        uint8_t lb[8];
+        for (int i = 0; i < 8; i++) lb[i] = (uint8_t)(bits >> (56 - 8 * i));
+        update(lb, 8);
+        for (int i = 0; i < 8; i++) {
+            out[4 * i] = (uint8_t)(h[i] >> 24);
+            out[4 * i + 1] = (uint8_t)(h[i] >> 16);
+            out[4 * i + 2] = (uint8_t)(h[i] >> 8);
+            out[4 * i + 3] = (uint8_t)h[i];
+        }
+    }
+};
+
+inline void tr_init(uint8_t st[32], const char* seed, size_t n) {
+    Sha256 c;
+    c.init();
+    c.update(seed, n);
+    c.final(st);
+}
+inline void tr_absorb(uint8_t st[32], const char* label, size_t llen, const void* data,
+                      size_t len) {
+    Sha256 c;
+    c.init();
+    c.update(st, 32);
+    uint8_t ll[4], dl[8];
+    for (int i = 0; i < 4; i++) ll[i] = (uint8_t)((uint32_t)llen >> (8 * i));
+    for (int i = 0; i < 8; i++) dl[i] = (uint8_t)((uint64_t)len >> (8 * i));
+    c.update(ll, 4);
+    c.update(label, llen);
+    c.update(dl, 8);
+    c.update(data, len);
+    c.final(st);
+}
+inline void tr_challenge_bytes(uint8_t st[32], uint8_t out[32]) {
+    Sha256 c;
+    c.init();
+    c.update(st, 32);
+    c.update("chal", 4);
+    c.final(out);
+    uint8_t nx[32];
+    c.init();
+    c.update(st, 32);
+    c.update("rtch", 4);
+    c.final(nx);
+    memcpy(st, nx, 32);
+}
+inline void tr_challenge_limbs(uint8_t st[32], uint32_t out[8]) {
+    for (;;) {
+        uint8_t b[32];
+        tr_challenge_bytes(st, b);
+        for (int i = 0; i < 8; i++)
+            out[i] = (uint32_t)b[4 * i] | ((uint32_t)b[4 * i + 1] << 8) |
+                     ((uint32_t)b[4 * i + 2] << 16) | ((uint32_t)b[4 * i + 3] << 24);
+        out[7] %= 1944954707u;
+        for (int i = 0; i < 8; i++)
+            if (out[i]) return;
+    }
+}
+inline Fr tr_challenge(uint8_t st[32]) {
+    uint32_t l[8];
+    tr_challenge_limbs(st, l);
+    return fr_load(l);
+}
+inline void tr_absorb_fr(uint8_t st[32], const char* label, const Fr& x) {
+    uint32_t b[8];
+    fr_store(x, b);
+    tr_absorb(st, label, strlen(label), b, 32);
+}
+
+}  // namespace zkh

@@ -1,0 +1,1316 @@
+// zkh.hip -- host side of the C ABI (include/zkh.h): device tensors, the SHA-256
+// Fiat-Shamir round loops of the matmul, logUp and Hadamard sumchecks, and the MLE
+// primitives, all driving the gfx950 kernels of kernels.hip on one HIP stream per context.
+//
+// Per round the host receives a few hundred block partials (AoS Fr), adds them, turns the
+// sums into the round polynomial, absorbs it, draws the challenge and launches the next
+// fused fold+evaluate kernel.  Only 32-byte scalars cross PCIe per round.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/zkh.h"
+#include "fr_host.hpp"
+#include "kernels.hpp"
+#include "transcript.hpp"
+
+using namespace zkh;
+
+struct zkh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    uint32_t* pinned = nullptr;  // host staging for partials and small vectors
+    size_t pinned_bytes = 0;
+    struct Slot {
+        void* p = nullptr;
+        size_t bytes = 0;
+    };
+    std::vector<Slot> slots;
+};
+
+struct zkh_tensor {
+    zkh_ctx* ctx = nullptr;
+    int kind = ZKH_KIND_FR;
+    uint32_t n = 0;
+    void* d = nullptr;  // FR: planes (cap entries each); I32/I64: n ints
+    uint32_t cap = 0;
+    uint32_t bits = 0;  // integer kinds: |v| < 2^bits
+    int weights = 0;    // I32 matmul weights stored OUT-major (transposed)
+    uint32_t w_in = 0, w_out = 0;
+    DevPlanes planes() const { return DevPlanes{(uint32_t*)d, cap}; }
+};
+
+// ---------------------------------------------------------------------------------------
+// errors and scratch
+// ---------------------------------------------------------------------------------------
+static int fail(zkh_ctx* c, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (c) c->err = buf;
+    return code;
+}
+#define HIPCHK(ctx, x)                                                                  \
+    do {                                                                                \
+        hipError_t e_ = (x);                                                            \
+        if (e_ != hipSuccess)                                                           \
+            return fail((ctx), ZKH_EDEV, "%s failed: %s", #x, hipGetErrorString(e_)); \
+    } while (0)
+
+// named scratch slots, grown on demand (freed with the context)
+enum {
+    SL_PARTIAL = 0,
+    SL_SMALL,
+    SL_FAC,
+    SL_ELO,
+    SL_EB,
+    SL_EO,
+    SL_TMP0,
+    SL_TMP1,
+    SL_TMP2,
+    SL_TMP3,
+    SL_TMP4,
+    SL_TMP5,
+    SL_TMP6,
+    SL_COUNT
+};
+static void* scratch(zkh_ctx* c, int slot, size_t bytes, int* rc) {
+    if ((int)c->slots.size() < SL_COUNT) c->slots.resize(SL_COUNT);
+    zkh_ctx::Slot& s = c->slots[slot];
+    if (s.bytes >= bytes && s.p) return s.p;
+    if (s.p) {
+        hipStreamSynchronize(c->stream);
+        hipFree(s.p);
+        s.p = nullptr;
+        s.bytes = 0;
+    }
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    if (hipMalloc(&s.p, want) != hipSuccess) {
+        *rc = fail(c, ZKH_EDEV, "hipMalloc(%zu) failed", want);
+        return nullptr;
+    }
+    s.bytes = want;
+    return s.p;
+}
+static DevPlanes scratch_planes(zkh_ctx* c, int slot, uint32_t n, int* rc) {
+    uint32_t cap = n ? n : 1;
+    void* p = scratch(c, slot, (size_t)cap * 32, rc);
+    return DevPlanes{(uint32_t*)p, cap};
+}
+static int ensure_pinned(zkh_ctx* c, size_t bytes) {
+    if (c->pinned_bytes >= bytes) return 0;
+    if (c->pinned) hipHostFree(c->pinned);
+    c->pinned = nullptr;
+    size_t want = std::max(bytes, (size_t)1 << 20);
+    if (hipHostMalloc((void**)&c->pinned, want, hipHostMallocDefault) != hipSuccess)
+        return fail(c, ZKH_EDEV, "hipHostMalloc(%zu) failed", want);
+    c->pinned_bytes = want;
+    return 0;
+}
+// copy K*nb AoS partials back and return the K column sums
+static int fetch_sums(zkh_ctx* c, const uint32_t* dpart, uint32_t nb, int K, Fr* out) {
+    size_t bytes = (size_t)nb * K * 32;
+    int rc = ensure_pinned(c, bytes);
+    if (rc) return rc;
+    HIPCHK(c, hipMemcpyAsync(c->pinned, dpart, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    for (int k = 0; k < K; k++) out[k] = kZero;
+    for (uint32_t b = 0; b < nb; b++)
+        for (int k = 0; k < K; k++) out[k] = fr_add(out[k], fr_load(c->pinned + ((size_t)b * K + k) * 8));
+    return 0;
+}
+// host AoS -> device (through the pinned buffer)
+static int upload(zkh_ctx* c, void* dst, const void* src, size_t bytes) {
+    int rc = ensure_pinned(c, bytes);
+    if (rc) return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));  // pinned buffer may still feed a copy
+    memcpy(c->pinned, src, bytes);
+    HIPCHK(c, hipMemcpyAsync(dst, c->pinned, bytes, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return 0;
+}
+static uint32_t ceil_log2(uint32_t n) {
+    uint32_t r = 0;
+    if (n <= 1) return 0;
+    n--;
+    while (n) {
+        n >>= 1;
+        r++;
+    }
+    return r;
+}
+static uint32_t bits_for(uint64_t absmax) {
+    uint32_t b = 0;
+    while (b < 63 && ((uint64_t)1 << b) <= absmax) b++;
+    return b;  // absmax < 2^b
+}
+static const Fr& R2() { return kR2; }                 // mont_mul(x, R2) = x * 2^256
+static Fr fix1(const Fr& x) { return fr_mont_mul(x, kR2); }  // undo one 2^-256
+static Fr fix2(const Fr& x) {
+    static const Fr r3 = fr_rpow(3);
+    return fr_mont_mul(x, r3);
+}
+
+// Montgomery factor table of u: fac[2t] = mont(1-u_t), fac[2t+1] = mont(u_t), for
+// t < nvars; positions t >= len(u) (up to pad) are (mont(1), 0)
+static void make_fac(const std::vector<Fr>& u, uint32_t pad, std::vector<uint32_t>& out) {
+    uint32_t nv = std::max<uint32_t>((uint32_t)u.size(), pad);
+    out.assign((size_t)nv * 16, 0);
+    for (uint32_t t = 0; t < nv; t++) {
+        Fr a, b;
+        if (t < u.size()) {
+            a = fr_to_mont(fr_sub(kOne, u[t]));
+            b = fr_to_mont(u[t]);
+        } else {
+            a = fr_to_mont(kOne);
+            b = kZero;
+        }
+        fr_store(a, &out[(size_t)t * 16]);
+        fr_store(b, &out[(size_t)t * 16 + 8]);
+    }
+}
+// sum_{b < K} eq(b, u) for K <= 2^|u|
+static Fr eq_prefix_sum(const std::vector<Fr>& u, uint64_t K) {
+    uint32_t k = (uint32_t)u.size();
+    if (K >= ((uint64_t)1 << k)) return kOne;
+    Fr sum = kZero, prod = kOne;
+    for (int j = (int)k - 1; j >= 0; j--) {
+        Fr om = fr_sub(kOne, u[j]);
+        if ((K >> j) & 1) {
+            sum = fr_add(sum, fr_mul(prod, om));
+            prod = fr_mul(prod, u[j]);
+        } else {
+            prod = fr_mul(prod, om);
+        }
+    }
+    return sum;
+}
+
+// eq weighting state for the Elo/Ehi kernels: Elo over u[0..10) (padded) and the full
+// factor table; corr[K] undoes the padded factors when K < 10
+struct EqState {
+    uint32_t* fac_d = nullptr;
+    uint32_t* elo_d = nullptr;
+    std::vector<Fr> corr;  // corr[K] for K = 0..10
+    uint32_t nvars = 0;
+};
+static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, int slot_fac, int slot_elo) {
+    int rc = 0;
+    std::vector<uint32_t> fac;
+    make_fac(u, 10, fac);
+    st.nvars = (uint32_t)u.size();
+    st.fac_d = (uint32_t*)scratch(c, slot_fac, fac.size() * 4, &rc);
+    if (rc) return rc;
+    st.elo_d = (uint32_t*)scratch(c, slot_elo, 1024 * 32, &rc);
+    if (rc) return rc;
+    if ((rc = upload(c, st.fac_d, fac.data(), fac.size() * 4))) return rc;
+    launch_eq_mont(c->stream, st.fac_d, 10, 1024, st.elo_d);
+    // Z_K = prod_{t=K}^{9} (1 - u_t) (padded u_t = 0); corr[K] = 1/Z_K
+    Fr z[11];
+    z[10] = kOne;
+    for (int t = 9; t >= 0; t--) {
+        Fr om = t < (int)u.size() ? fr_sub(kOne, u[t]) : kOne;
+        z[t] = fr_mul(z[t + 1], om);
+    }
+    if (fr_eq(z[0], kZero)) return fail(c, ZKH_EARG, "degenerate eq challenge (u_t = 1)");
+    Fr iz0 = fr_inv(z[0]);
+    st.corr.assign(11, kOne);
+    Fr pre = kOne;  // prod_{t<K} (1-u_t)
+    for (int K = 0; K <= 10; K++) {
+        st.corr[K] = fr_mul(iz0, pre);  // 1/Z_K = prod_{t<K}(1-u_t) / Z_0
+        if (K < 10) pre = fr_mul(pre, K < (int)u.size() ? fr_sub(kOne, u[K]) : kOne);
+    }
+    return 0;
+}
+static Fr eq_corr(const EqState& st, uint32_t K) { return K >= 10 ? kOne : st.corr[K]; }
+
+static std::vector<Fr> load_frs(const uint32_t* p, uint32_t n) {
+    std::vector<Fr> v(n);
+    for (uint32_t i = 0; i < n; i++) v[i] = fr_load(p + 8 * (size_t)i);
+    return v;
+}
+static bool all_canonical(const uint32_t* p, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++)
+        if (!fr_is_canonical(p + 8 * (size_t)i)) return false;
+    return true;
+}
+
+// ---------------------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------------------
+extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
+    if (!out) return ZKH_EARG;
+    *out = nullptr;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return ZKH_EDEV;
+    if (device < 0 || device >= ndev) return ZKH_EARG;
+    zkh_ctx* c = new zkh_ctx();
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return ZKH_EDEV;
+    }
+    c->slots.resize(SL_COUNT);
+    if (ensure_pinned(c, (size_t)1 << 20)) {
+        hipStreamDestroy(c->stream);
+        delete c;
+        return ZKH_EDEV;
+    }
+    *out = c;
+    return ZKH_OK;
+}
+extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
+    if (!c) return ZKH_EARG;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    for (auto& s : c->slots)
+        if (s.p) hipFree(s.p);
+    if (c->pinned) hipHostFree(c->pinned);
+    hipStreamDestroy(c->stream);
+    delete c;
+    return ZKH_OK;
+}
+extern "C" const char* zkh_last_error(const zkh_ctx* c) { return c ? c->err.c_str() : "null context"; }
+extern "C" int zkh_ctx_sync(zkh_ctx* c) {
+    if (!c) return ZKH_EARG;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// tensors
+// ---------------------------------------------------------------------------------------
+static int tensor_alloc(zkh_ctx* c, int kind, uint32_t n, zkh_tensor** out) {
+    zkh_tensor* t = new zkh_tensor();
+    t->ctx = c;
+    t->kind = kind;
+    t->n = n;
+    size_t bytes;
+    if (kind == ZKH_KIND_FR) {
+        t->cap = n ? n : 1;
+        bytes = (size_t)t->cap * 32;
+    } else {
+        bytes = (size_t)(n ? n : 1) * (kind == ZKH_KIND_I32 ? 4 : 8);
+    }
+    if (hipMalloc(&t->d, bytes) != hipSuccess) {
+        delete t;
+        return fail(c, ZKH_EDEV, "hipMalloc(%zu) failed", bytes);
+    }
+    *out = t;
+    return ZKH_OK;
+}
+static int int_bits_i32(zkh_ctx* c, const int32_t* d, uint32_t n, uint32_t* bits) {
+    int rc = 0;
+    uint32_t* m = (uint32_t*)scratch(c, SL_SMALL, 64, &rc);
+    if (rc) return rc;
+    HIPCHK(c, hipMemsetAsync(m, 0, 4, c->stream));
+    launch_absmax_i32(c->stream, d, n, m);
+    uint32_t h = 0;
+    HIPCHK(c, hipMemcpyAsync(&h, m, 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *bits = bits_for(h);
+    return 0;
+}
+static int int_bits_i64(zkh_ctx* c, const int64_t* d, uint32_t n, uint32_t* bits) {
+    int rc = 0;
+    unsigned long long* m = (unsigned long long*)scratch(c, SL_SMALL, 64, &rc);
+    if (rc) return rc;
+    HIPCHK(c, hipMemsetAsync(m, 0, 8, c->stream));
+    launch_absmax_i64(c->stream, d, n, m);
+    unsigned long long h = 0;
+    HIPCHK(c, hipMemcpyAsync(&h, m, 8, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *bits = bits_for(h);
+    return 0;
+}
+static int make_int_tensor(zkh_ctx* c, const void* src, uint32_t n, int kind, hipMemcpyKind dir,
+                           zkh_tensor** out) {
+    if (!c || !out || (!src && n)) return fail(c, ZKH_EARG, "null argument");
+    *out = nullptr;
+    HIPCHK(c, hipSetDevice(c->device));
+    zkh_tensor* t;
+    int rc = tensor_alloc(c, kind, n, &t);
+    if (rc) return rc;
+    size_t es = kind == ZKH_KIND_I32 ? 4 : 8;
+    if (n) {
+        hipError_t e = hipMemcpyAsync(t->d, src, (size_t)n * es, dir, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            hipFree(t->d);
+            delete t;
+            return fail(c, ZKH_EDEV, "tensor upload failed: %s", hipGetErrorString(e));
+        }
+        rc = kind == ZKH_KIND_I32 ? int_bits_i32(c, (const int32_t*)t->d, n, &t->bits)
+                                  : int_bits_i64(c, (const int64_t*)t->d, n, &t->bits);
+        if (rc) {
+            hipFree(t->d);
+            delete t;
+            return rc;
+        }
+    }
+    *out = t;
+    return ZKH_OK;
+}
+extern "C" int zkh_tensor_from_i32(zkh_ctx* c, const int32_t* v, uint32_t n, zkh_tensor** out) {
+    return make_int_tensor(c, v, n, ZKH_KIND_I32, hipMemcpyHostToDevice, out);
+}
+extern "C" int zkh_tensor_from_i64(zkh_ctx* c, const int64_t* v, uint32_t n, zkh_tensor** out) {
+    return make_int_tensor(c, v, n, ZKH_KIND_I64, hipMemcpyHostToDevice, out);
+}
+extern "C" int zkh_tensor_from_i32_device(zkh_ctx* c, const int32_t* d, uint32_t n, zkh_tensor** out) {
+    return make_int_tensor(c, d, n, ZKH_KIND_I32, hipMemcpyDeviceToDevice, out);
+}
+extern "C" int zkh_tensor_from_i64_device(zkh_ctx* c, const int64_t* d, uint32_t n, zkh_tensor** out) {
+    return make_int_tensor(c, d, n, ZKH_KIND_I64, hipMemcpyDeviceToDevice, out);
+}
+extern "C" int zkh_tensor_weights_i32(zkh_ctx* c, const int32_t* W, uint32_t in_dim,
+                                      uint32_t out_dim, zkh_tensor** out) {
+    if (!c || !out || !W || !in_dim || !out_dim) return fail(c, ZKH_EARG, "bad weights arguments");
+    uint64_t n64 = (uint64_t)in_dim * out_dim;
+    if (n64 >= (1ull << 32)) return fail(c, ZKH_EARG, "weights too large");
+    zkh_tensor* rm;
+    int rc = zkh_tensor_from_i32(c, W, (uint32_t)n64, &rm);
+    if (rc) return rc;
+    zkh_tensor* t;
+    rc = tensor_alloc(c, ZKH_KIND_I32, (uint32_t)n64, &t);
+    if (rc) {
+        zkh_tensor_free(rm);
+        return rc;
+    }
+    launch_transpose_i32(c->stream, (const int32_t*)rm->d, in_dim, out_dim, (int32_t*)t->d);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    t->bits = rm->bits;
+    t->weights = 1;
+    t->w_in = in_dim;
+    t->w_out = out_dim;
+    zkh_tensor_free(rm);
+    if (e != hipSuccess) {
+        zkh_tensor_free(t);
+        return fail(c, ZKH_EDEV, "transpose failed: %s", hipGetErrorString(e));
+    }
+    *out = t;
+    return ZKH_OK;
+}
+extern "C" int zkh_tensor_from_fr(zkh_ctx* c, const uint32_t* aos, uint32_t n, zkh_tensor** out) {
+    if (!c || !out || (!aos && n)) return fail(c, ZKH_EARG, "null argument");
+    *out = nullptr;
+    if (!all_canonical(aos, n)) return fail(c, ZKH_EARG, "non-canonical field element");
+    HIPCHK(c, hipSetDevice(c->device));
+    zkh_tensor* t;
+    int rc = tensor_alloc(c, ZKH_KIND_FR, n, &t);
+    if (rc) return rc;
+    if (n) {
+        uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)n * 32, &rc);
+        hipError_t e = hipSuccess;
+        if (!rc) e = hipMemcpyAsync(stage, aos, (size_t)n * 32, hipMemcpyHostToDevice, c->stream);
+        if (!rc && e == hipSuccess) {
+            launch_aos_to_planes(c->stream, stage, n, t->planes());
+            e = hipStreamSynchronize(c->stream);
+        }
+        if (rc || e != hipSuccess) {
+            hipFree(t->d);
+            delete t;
+            return rc ? rc : fail(c, ZKH_EDEV, "upload failed: %s", hipGetErrorString(e));
+        }
+    }
+    *out = t;
+    return ZKH_OK;
+}
+extern "C" int zkh_tensor_free(zkh_tensor* t) {
+    if (!t) return ZKH_EARG;
+    if (t->d) hipFree(t->d);
+    delete t;
+    return ZKH_OK;
+}
+extern "C" uint32_t zkh_tensor_size(const zkh_tensor* t) { return t ? t->n : 0; }
+extern "C" int zkh_tensor_kind(const zkh_tensor* t) { return t ? t->kind : -1; }
+
+// FR planes view of any tensor (integer tensors are converted into the given scratch slot)
+static int as_planes(zkh_ctx* c, const zkh_tensor* t, int slot, DevPlanes* out) {
+    int rc = 0;
+    if (t->kind == ZKH_KIND_FR) {
+        *out = t->planes();
+        return 0;
+    }
+    DevPlanes p = scratch_planes(c, slot, t->n, &rc);
+    if (rc) return rc;
+    if (t->kind == ZKH_KIND_I32) {
+        if (t->weights) {
+            // logical W (IN x OUT) from the OUT-major copy
+            int32_t* rm = (int32_t*)scratch(c, SL_TMP5, (size_t)t->n * 4, &rc);
+            if (rc) return rc;
+            launch_transpose_i32(c->stream, (const int32_t*)t->d, t->w_out, t->w_in, rm);
+            launch_i32_to_planes(c->stream, rm, t->n, p);
+        } else {
+            launch_i32_to_planes(c->stream, (const int32_t*)t->d, t->n, p);
+        }
+    } else {
+        launch_i64_to_planes(c->stream, (const int64_t*)t->d, t->n, p);
+    }
+    *out = p;
+    return 0;
+}
+extern "C" int zkh_tensor_to_fr(zkh_ctx* c, const zkh_tensor* t, uint32_t* aos) {
+    if (!c || !t || (!aos && t->n)) return fail(c, ZKH_EARG, "null argument");
+    if (!t->n) return ZKH_OK;
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    DevPlanes p;
+    if ((rc = as_planes(c, t, SL_TMP4, &p))) return rc;
+    uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)t->n * 32, &rc);
+    if (rc) return rc;
+    launch_planes_to_aos(c->stream, p, t->n, stage);
+    HIPCHK(c, hipMemcpyAsync(aos, stage, (size_t)t->n * 32, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// transcript
+// ---------------------------------------------------------------------------------------
+extern "C" int zkh_transcript_init(uint8_t st[32], const char* seed, size_t n) {
+    if (!st || (!seed && n)) return ZKH_EARG;
+    tr_init(st, seed, n);
+    return ZKH_OK;
+}
+extern "C" int zkh_transcript_absorb(uint8_t st[32], const char* label, size_t llen,
+                                     const void* data, size_t len) {
+    if (!st || (!label && llen) || (!data && len)) return ZKH_EARG;
+    tr_absorb(st, label, llen, data, len);
+    return ZKH_OK;
+}
+extern "C" int zkh_transcript_challenge_fr(uint8_t st[32], uint32_t out[8]) {
+    if (!st || !out) return ZKH_EARG;
+    tr_challenge_limbs(st, out);
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// MLE primitives
+// ---------------------------------------------------------------------------------------
+// sum_i eq(i,u) * S[i] (* U[i]) over i < n, with n <= 2^|u|
+static int eq_weighted_sum(zkh_ctx* c, DevPlanes S, const DevPlanes* U, uint32_t n,
+                           const std::vector<Fr>& u, Fr* out) {
+    int rc = 0;
+    EqState st;
+    if ((rc = eq_setup(c, u, st, SL_FAC, SL_ELO))) return rc;
+    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 32, &rc);
+    if (rc) return rc;
+    uint32_t K = (uint32_t)u.size();
+    uint32_t nb = launch_eq_sum(c->stream, S, U, n, EqW{st.elo_d, st.fac_d, K}, part);
+    Fr s;
+    if ((rc = fetch_sums(c, part, nb, 1, &s))) return rc;
+    s = fr_mul(s, eq_corr(st, K));
+    if (U) s = fix1(s);
+    *out = s;
+    return 0;
+}
+extern "C" int zkh_sum(zkh_ctx* c, const zkh_tensor* t, uint32_t out[8]) {
+    if (!c || !t || !out) return fail(c, ZKH_EARG, "null argument");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    DevPlanes p;
+    if ((rc = as_planes(c, t, SL_TMP0, &p))) return rc;
+    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 32, &rc);
+    if (rc) return rc;
+    Fr s = kZero;
+    if (t->n) {
+        uint32_t nb = launch_sum_planes(c->stream, p, t->n, part);
+        if ((rc = fetch_sums(c, part, nb, 1, &s))) return rc;
+    }
+    fr_store(s, out);
+    return ZKH_OK;
+}
+extern "C" int zkh_me(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u, uint32_t k,
+                      uint32_t out[8]) {
+    if (!c || !t || !out || (!u && k)) return fail(c, ZKH_EARG, "null argument");
+    // FrTensor::operator()(u) (fr-tensor.cu:437-442)
+    if (k >= 32 || t->n <= ((1u << k) / 2) || t->n > (1u << k))
+        return fail(c, ZKH_EARG, "Incompatible dimensions");
+    if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    DevPlanes p;
+    if ((rc = as_planes(c, t, SL_TMP0, &p))) return rc;
+    Fr s;
+    if ((rc = eq_weighted_sum(c, p, nullptr, t->n, load_frs(u, k), &s))) return rc;
+    fr_store(s, out);
+    return ZKH_OK;
+}
+// eq table (Montgomery AoS) of u over n entries into a scratch slot
+static int eq_table_mont(zkh_ctx* c, const std::vector<Fr>& u, uint32_t n, int slot, uint32_t** out) {
+    int rc = 0;
+    std::vector<uint32_t> fac;
+    make_fac(u, 0, fac);
+    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
+    if (rc) return rc;
+    if (!fac.empty() && (rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
+    uint32_t* e = (uint32_t*)scratch(c, slot, (size_t)std::max<uint32_t>(n, 1) * 32, &rc);
+    if (rc) return rc;
+    launch_eq_mont(c->stream, fac_d, (uint32_t)u.size(), n, e);
+    *out = e;
+    return 0;
+}
+static int partial_me_impl(zkh_ctx* c, const zkh_tensor* t, const std::vector<Fr>& u,
+                           uint32_t cur_dim, uint32_t window, zkh_tensor** out) {
+    uint32_t k = (uint32_t)u.size();
+    // FrTensor::partial_me(u, cur_dim, window) checks (fr-tensor.cu:554-560)
+    if (k >= 32 || cur_dim <= ((1u << k) >> 1) || cur_dim > (1u << k))
+        return fail(c, ZKH_EARG, "partial_me: incompatible dimensions");
+    if (!window || t->n % ((uint64_t)cur_dim * window) != 0)
+        return fail(c, ZKH_EARG, "t.size %% (cur_dim * window) != 0");
+    uint32_t O = t->n / (cur_dim * window);
+    int rc = 0;
+    uint32_t* E;
+    if ((rc = eq_table_mont(c, u, cur_dim, SL_EB, &E))) return rc;
+    zkh_tensor* o;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, O * window, &o))) return rc;
+    if (t->kind == ZKH_KIND_FR) launch_partial_me_planes(c->stream, t->planes(), O, cur_dim, window, E, o->planes());
+    else if (t->kind == ZKH_KIND_I64)
+        launch_partial_me_i64(c->stream, (const int64_t*)t->d, O, cur_dim, window, E, o->planes());
+    else {
+        DevPlanes p;
+        if (t->weights) {
+            if ((rc = as_planes(c, t, SL_TMP0, &p))) {
+                zkh_tensor_free(o);
+                return rc;
+            }
+            launch_partial_me_planes(c->stream, p, O, cur_dim, window, E, o->planes());
+        } else {
+            launch_partial_me_i32(c->stream, (const int32_t*)t->d, O, cur_dim, window, E, o->planes());
+        }
+    }
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        zkh_tensor_free(o);
+        return fail(c, ZKH_EDEV, "partial_me: %s", hipGetErrorString(e));
+    }
+    *out = o;
+    return 0;
+}
+extern "C" int zkh_partial_me(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u, uint32_t k,
+                              uint32_t cur_dim, uint32_t window, zkh_tensor** out) {
+    if (!c || !t || !out || (!u && k)) return fail(c, ZKH_EARG, "null argument");
+    if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    return partial_me_impl(c, t, load_frs(u, k), cur_dim, window, out);
+}
+extern "C" int zkh_multi_dim_me(zkh_ctx* c, const zkh_tensor* t, const uint32_t* us,
+                                const uint32_t* ks, const uint32_t* shape, uint32_t ndim,
+                                uint32_t out[8]) {
+    if (!c || !t || !out || (ndim && (!ks || !shape))) return fail(c, ZKH_EARG, "null argument");
+    HIPCHK(c, hipSetDevice(c->device));
+    if (ndim == 0) {  // (*this)(0) in the reference is element 0
+        if (!t->n) return fail(c, ZKH_EARG, "empty tensor");
+        return zkh_me(c, t, nullptr, 0, out);
+    }
+    size_t off = 0;
+    std::vector<std::vector<Fr>> uv(ndim);
+    for (uint32_t d = 0; d < ndim; d++) {
+        if (ks[d] && !us) return fail(c, ZKH_EARG, "null challenges");
+        if (ks[d] && !all_canonical(us + 8 * off, ks[d])) return fail(c, ZKH_EARG, "non-canonical challenge");
+        uv[d] = load_frs(us + 8 * off, ks[d]);
+        off += ks[d];
+    }
+    // bind the last dimension first (fr-tensor.cu:643-652)
+    const zkh_tensor* cur = t;
+    zkh_tensor* owned = nullptr;
+    int rc = 0;
+    for (uint32_t d = ndim - 1; d >= 1; d--) {
+        zkh_tensor* nxt;
+        rc = partial_me_impl(c, cur, uv[d], shape[d], 1, &nxt);
+        if (owned) zkh_tensor_free(owned);
+        if (rc) return rc;
+        owned = nxt;
+        cur = nxt;
+    }
+    uint32_t k0 = ks[0];
+    std::vector<uint32_t> u0(8 * (size_t)k0);
+    for (uint32_t i = 0; i < k0; i++) fr_store(uv[0][i], &u0[8 * (size_t)i]);
+    rc = zkh_me(c, cur, u0.data(), k0, out);
+    if (owned) zkh_tensor_free(owned);
+    return rc;
+}
+extern "C" int zkh_eq_table(zkh_ctx* c, const uint32_t* u, uint32_t k, zkh_tensor** out) {
+    if (!c || !out || (!u && k) || k > 30) return fail(c, ZKH_EARG, "bad arguments");
+    if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    std::vector<uint32_t> fac;
+    make_fac(load_frs(u, k), 0, fac);
+    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
+    if (rc) return rc;
+    if (k && (rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
+    zkh_tensor* t;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, 1u << k, &t))) return rc;
+    launch_eq_planes(c->stream, fac_d, k, 1u << k, t->planes());
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *out = t;
+    return ZKH_OK;
+}
+extern "C" int zkh_fold(zkh_ctx* c, zkh_tensor* t, const uint32_t v[8]) {
+    if (!c || !t || !v) return fail(c, ZKH_EARG, "null argument");
+    if (t->kind != ZKH_KIND_FR || t->n < 2 || (t->n & 1)) return fail(c, ZKH_EARG, "fold needs an even FR tensor");
+    if (!fr_is_canonical(v)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    uint32_t vm[8];
+    fr_store(fr_to_mont(fr_load(v)), vm);
+    launch_fold(c->stream, Tab{t->planes(), t->planes()}, t->n / 2, vm);
+    t->n /= 2;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return ZKH_OK;
+}
+extern "C" int zkh_axpy(zkh_ctx* c, const zkh_tensor* a, const uint32_t cc[8], const zkh_tensor* b,
+                        zkh_tensor** out) {
+    if (!c || !a || !b || !cc || !out) return fail(c, ZKH_EARG, "null argument");
+    if (a->n != b->n) return fail(c, ZKH_EARG, "size mismatch");
+    if (!fr_is_canonical(cc)) return fail(c, ZKH_EARG, "non-canonical scalar");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    DevPlanes pa, pb;
+    if ((rc = as_planes(c, a, SL_TMP0, &pa)) || (rc = as_planes(c, b, SL_TMP1, &pb))) return rc;
+    zkh_tensor* o;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, a->n, &o))) return rc;
+    uint32_t cm[8];
+    fr_store(fr_to_mont(fr_load(cc)), cm);
+    if (a->n) launch_axpy(c->stream, pa, cm, pb, a->n, o->planes());
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *out = o;
+    return ZKH_OK;
+}
+extern "C" int zkh_hadamard(zkh_ctx* c, const zkh_tensor* a, const zkh_tensor* b, zkh_tensor** out) {
+    if (!c || !a || !b || !out) return fail(c, ZKH_EARG, "null argument");
+    if (a->n != b->n) return fail(c, ZKH_EARG, "size mismatch");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    DevPlanes pa, pb;
+    if ((rc = as_planes(c, a, SL_TMP0, &pa)) || (rc = as_planes(c, b, SL_TMP1, &pb))) return rc;
+    zkh_tensor* o;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, a->n, &o))) return rc;
+    if (a->n) launch_hadamard(c->stream, pa, pb, a->n, o->planes());
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *out = o;
+    return ZKH_OK;
+}
+extern "C" int zkh_pad(zkh_ctx* c, const zkh_tensor* t, const uint32_t* shape, uint32_t ndim,
+                       zkh_tensor** out) {
+    if (!c || !t || !shape || !out || ndim == 0 || ndim > 8) return fail(c, ZKH_EARG, "bad arguments");
+    uint64_t total = 1, ptotal = 1;
+    for (uint32_t d = 0; d < ndim; d++) {
+        total *= shape[d];
+        ptotal *= (uint64_t)1 << ceil_log2(shape[d]);
+    }
+    if (total != t->n) return fail(c, ZKH_EARG, "pad: cum_shape != size");
+    if (ptotal >= (1ull << 32)) return fail(c, ZKH_EARG, "pad: too large");
+    HIPCHK(c, hipSetDevice(c->device));
+    // host-side index map, then a gather on the device (zero where any index is padding)
+    int rc = 0;
+    DevPlanes p;
+    if ((rc = as_planes(c, t, SL_TMP0, &p))) return rc;
+    std::vector<uint32_t> src(t->n ? t->n * 8 : 8);
+    if (t->n) {
+        uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)t->n * 32, &rc);
+        if (rc) return rc;
+        launch_planes_to_aos(c->stream, p, t->n, stage);
+        HIPCHK(c, hipMemcpyAsync(src.data(), stage, (size_t)t->n * 32, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+    }
+    std::vector<uint32_t> dst((size_t)ptotal * 8, 0);
+    std::vector<uint32_t> pd(ndim);
+    for (uint32_t d = 0; d < ndim; d++) pd[d] = 1u << ceil_log2(shape[d]);
+    for (uint64_t g = 0; g < ptotal; g++) {
+        uint64_t rem = g, sidx = 0, mul = 1;
+        bool in = true;
+        for (int d = (int)ndim - 1; d >= 0; d--) {
+            uint64_t i = rem % pd[d];
+            rem /= pd[d];
+            if (i >= shape[d]) in = false;
+            sidx += i * mul;
+            mul *= shape[d];
+        }
+        if (in) memcpy(&dst[g * 8], &src[sidx * 8], 32);
+    }
+    return zkh_tensor_from_fr(c, dst.data(), (uint32_t)ptotal, out);
+}
+
+// ---------------------------------------------------------------------------------------
+// matmul sumcheck (zkob_fc.cu:259-440)
+// ---------------------------------------------------------------------------------------
+// out[i] (i < N) = sum_k e_k * M[k*N + i] for an integer matrix M (K x N), e = eq table E
+// (Montgomery AoS, K entries) with prefix sum SE; out zero-padded to Npad entries.
+static int eq_reduce_int(zkh_ctx* c, const void* M, int kind, uint32_t bits, uint32_t K, uint32_t N,
+                         const uint32_t* E, const Fr& SE, uint32_t Npad, DevPlanes out) {
+    int rc = 0;
+    uint32_t nch = std::max<uint32_t>(1, (131072 + N - 1) / N);
+    uint32_t kchunk = (K + nch - 1) / nch;
+    kchunk = std::min<uint32_t>(std::max<uint32_t>(kchunk, 16), 2048);
+    nch = (K + kchunk - 1) / kchunk;
+    uint32_t* part = (uint32_t*)scratch(c, SL_TMP6, (size_t)nch * N * 32, &rc);
+    if (rc) return rc;
+    if (kind == ZKH_KIND_I32) launch_eqdot_i32(c->stream, (const int32_t*)M, K, N, E, kchunk, bits, part);
+    else launch_eqdot_i64(c->stream, (const int64_t*)M, K, N, E, kchunk, bits, part);
+    // correction 2^bits * sum_{k<K} e_k
+    Fr corr = fr_mul(fr_from_i64(0), kZero);
+    {
+        Fr two_b = kOne;
+        for (uint32_t b = 0; b < bits; b++) two_b = fr_add(two_b, two_b);
+        corr = fr_mul(two_b, SE);
+    }
+    uint32_t corr_l[8];
+    fr_store(corr, corr_l);
+    launch_sum_chunks(c->stream, part, nch, N, Npad, corr_l, out);
+    return 0;
+}
+
+extern "C" int zkh_mm_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* X, const zkh_tensor* W,
+                            const zkh_tensor* Y, uint32_t B, uint32_t IN, uint32_t OUT,
+                            uint32_t* ev_out, uint32_t* claims_out, uint32_t* ub_out,
+                            uint32_t* uo_out, uint32_t* ui_out) {
+    if (!c || !tr || !X || !W || !Y) return fail(c, ZKH_EARG, "null argument");
+    if (!B || !IN || !OUT) return fail(c, ZKH_EARG, "zero dimension");
+    if (X->kind != ZKH_KIND_I32 || W->kind != ZKH_KIND_I32 || Y->kind == ZKH_KIND_FR)
+        return fail(c, ZKH_EARG, "mm_prove takes int32 X, W and int32/int64 Y");
+    if ((uint64_t)X->n != (uint64_t)B * IN || (uint64_t)W->n != (uint64_t)IN * OUT ||
+        (uint64_t)Y->n != (uint64_t)B * OUT)
+        return fail(c, ZKH_EARG, "input dims");
+    if (W->weights && (W->w_in != IN || W->w_out != OUT)) return fail(c, ZKH_EARG, "weights dims");
+    if (X->bits > 40 || W->bits > 40 || Y->bits > 62) return fail(c, ZKH_EARG, "integer range");
+    HIPCHK(c, hipSetDevice(c->device));
+    const uint32_t lb = ceil_log2(B), lo = ceil_log2(OUT), L = ceil_log2(IN);
+    const uint32_t INp = 1u << L;
+    int rc = 0;
+    std::vector<Fr> ub(lb), uo(lo);
+    for (auto& x : ub) x = tr_challenge(tr);
+    for (auto& x : uo) x = tr_challenge(tr);
+
+    uint32_t *Eb, *Eo;
+    if ((rc = eq_table_mont(c, ub, B, SL_EB, &Eb))) return rc;
+    if ((rc = eq_table_mont(c, uo, OUT, SL_EO, &Eo))) return rc;
+    Fr SEb = eq_prefix_sum(ub, B), SEo = eq_prefix_sum(uo, OUT);
+
+    // Yred[o] = sum_b eb[b] Y[b,o]; claim = sum_o eo[o] Yred[o]
+    DevPlanes yred = scratch_planes(c, SL_TMP2, OUT, &rc);
+    if (rc) return rc;
+    if ((rc = eq_reduce_int(c, Y->d, Y->kind, Y->bits, B, OUT, Eb, SEb, OUT, yred))) return rc;
+    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 11 * 32, &rc);
+    if (rc) return rc;
+    uint32_t nbc = launch_dot_aos_planes(c->stream, Eo, yred, OUT, part);
+    Fr claim;
+    if ((rc = fetch_sums(c, part, nbc, 1, &claim))) return rc;
+    tr_absorb_fr(tr, "claim", claim);
+
+    // a = X_red (IN, padded to INp), b = W_red
+    DevPlanes a = scratch_planes(c, SL_TMP0, INp, &rc);
+    if (rc) return rc;
+    DevPlanes b = scratch_planes(c, SL_TMP1, INp, &rc);
+    if (rc) return rc;
+    if ((rc = eq_reduce_int(c, X->d, ZKH_KIND_I32, X->bits, B, IN, Eb, SEb, INp, a))) return rc;
+    const int32_t* WT = (const int32_t*)W->d;
+    if (!W->weights) {
+        int32_t* t = (int32_t*)scratch(c, SL_TMP5, (size_t)W->n * 4, &rc);
+        if (rc) return rc;
+        launch_transpose_i32(c->stream, (const int32_t*)W->d, IN, OUT, t);
+        WT = t;
+    }
+    if ((rc = eq_reduce_int(c, WT, ZKH_KIND_I32, W->bits, OUT, IN, Eo, SEo, INp, b))) return rc;
+
+    // rounds (zkob_fc.cu:294-332)
+    Fr cur = claim, two = fr_u64(2), four = fr_u64(4);
+    std::vector<Fr> xs(L);
+    uint32_t vm[8] = {0};
+    for (uint32_t r = 0; r < L; r++) {
+        uint32_t n = INp >> r;
+        uint32_t nb = launch_zkip_round(c->stream, Tab{a, a}, Tab{b, b}, n, r > 0, vm, part);
+        Fr s[3];
+        if ((rc = fetch_sums(c, part, nb, 3, s))) return rc;
+        Fr c0 = fix1(s[0]), q1 = fix1(s[1]), c2 = fix1(s[2]);
+        Fr c1 = fr_sub(fr_sub(q1, c0), c2);
+        Fr p[3] = {c0, q1, fr_add(fr_add(c0, fr_mul(two, c1)), fr_mul(four, c2))};
+        if (!fr_eq(cur, fr_add(p[0], p[1])))
+            return fail(c, ZKH_EROUND, "prover sumcheck round inconsistency (witness bug) at round %u", r);
+        tr_absorb_fr(tr, "p0", p[0]);
+        tr_absorb_fr(tr, "p1", p[1]);
+        tr_absorb_fr(tr, "p2", p[2]);
+        Fr x = tr_challenge(tr);
+        xs[r] = x;
+        if (ev_out)
+            for (int j = 0; j < 3; j++) fr_store(p[j], ev_out + 8 * (3 * r + j));
+        cur = fr_lagrange3(p, x);
+        fr_store(fr_to_mont(x), vm);
+    }
+    if (L > 0) {
+        launch_fold(c->stream, Tab{a, a}, 1, vm);
+        launch_fold(c->stream, Tab{b, b}, 1, vm);
+    }
+    uint32_t fin[2][8];
+    HIPCHK(c, hipMemcpyAsync(fin[0], a.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(fin[0] + 4, a.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(fin[1], b.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(fin[1] + 4, b.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    Fr cx = fr_load(fin[0]), cw = fr_load(fin[1]);
+    if (!fr_eq(cur, fr_mul(cx, cw))) return fail(c, ZKH_EROUND, "terminal product mismatch (witness bug)");
+    tr_absorb_fr(tr, "claim_X", cx);
+    tr_absorb_fr(tr, "claim_W", cw);
+    if (claims_out) {
+        fr_store(claim, claims_out);
+        fr_store(cx, claims_out + 8);
+        fr_store(cw, claims_out + 16);
+    }
+    if (ub_out)
+        for (uint32_t i = 0; i < lb; i++) fr_store(ub[i], ub_out + 8 * i);
+    if (uo_out)
+        for (uint32_t i = 0; i < lo; i++) fr_store(uo[i], uo_out + 8 * i);
+    if (ui_out)
+        for (uint32_t i = 0; i < L; i++) fr_store(xs[L - 1 - i], ui_out + 8 * i);
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// logUp
+// ---------------------------------------------------------------------------------------
+extern "C" int zkh_lu_range_table(zkh_ctx* c, int32_t low, uint32_t len, uint32_t N, zkh_tensor** out) {
+    if (!c || !out || !len || N < len) return fail(c, ZKH_EARG, "bad range table arguments");
+    std::vector<int32_t> v(N);
+    for (uint32_t i = 0; i < N; i++)
+        v[i] = i < len ? (int32_t)((int64_t)low + i) : (int32_t)((int64_t)low + len - 1);
+    zkh_tensor* ti;
+    int rc = zkh_tensor_from_i32(c, v.data(), N, &ti);
+    if (rc) return rc;
+    zkh_tensor* t;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &t))) {
+        zkh_tensor_free(ti);
+        return rc;
+    }
+    launch_i32_to_planes(c->stream, (const int32_t*)ti->d, N, t->planes());
+    hipError_t e = hipStreamSynchronize(c->stream);
+    zkh_tensor_free(ti);
+    if (e != hipSuccess) {
+        zkh_tensor_free(t);
+        return fail(c, ZKH_EDEV, "range table: %s", hipGetErrorString(e));
+    }
+    *out = t;
+    return ZKH_OK;
+}
+static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, uint32_t** counts_out) {
+    int rc = 0;
+    uint32_t* counts = (uint32_t*)scratch(c, SL_TMP5, (size_t)(N + 1) * 4, &rc);
+    if (rc) return rc;
+    uint32_t* bad = counts + N;
+    HIPCHK(c, hipMemsetAsync(counts, 0, (size_t)(N + 1) * 4, c->stream));
+    if (S->kind == ZKH_KIND_I32) {
+        launch_lu_count_i32(c->stream, (const int32_t*)S->d, S->n, low, N, counts, bad);
+    } else {
+        DevPlanes p;
+        if ((rc = as_planes(c, S, SL_TMP0, &p))) return rc;
+        uint32_t lowl[8];
+        fr_store(fr_from_i64(low), lowl);
+        launch_lu_count_planes(c->stream, p, S->n, lowl, N, counts, bad);
+    }
+    uint32_t hb = 0;
+    HIPCHK(c, hipMemcpyAsync(&hb, bad, 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (hb) return fail(c, ZKH_EARG, "lookup witness outside the table");
+    *counts_out = counts;
+    return 0;
+}
+extern "C" int zkh_lu_prep(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, zkh_tensor** m_out) {
+    if (!c || !S || !m_out || !N) return fail(c, ZKH_EARG, "bad arguments");
+    HIPCHK(c, hipSetDevice(c->device));
+    uint32_t* counts;
+    int rc = lu_counts(c, S, low, N, &counts);
+    if (rc) return rc;
+    zkh_tensor* m;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
+    launch_counts_to_planes(c->stream, counts, N, m->planes());
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *m_out = m;
+    return ZKH_OK;
+}
+extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, const zkh_tensor* mapped,
+                              zkh_tensor** S_out, zkh_tensor** m_out) {
+    if (!c || !S_in || !mapped || !S_out || !m_out || mapped->kind != ZKH_KIND_FR || !mapped->n)
+        return fail(c, ZKH_EARG, "bad arguments");
+    HIPCHK(c, hipSetDevice(c->device));
+    uint32_t N = mapped->n;
+    uint32_t* counts;
+    int rc = lu_counts(c, S_in, low, N, &counts);
+    if (rc) return rc;
+    zkh_tensor *m, *so;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, S_in->n, &so))) {
+        zkh_tensor_free(m);
+        return rc;
+    }
+    launch_counts_to_planes(c->stream, counts, N, m->planes());
+    DevPlanes mp = mapped->planes();
+    mp.cap = mapped->cap;
+    if (S_in->kind == ZKH_KIND_I32) {
+        launch_lu_map_i32(c->stream, (const int32_t*)S_in->d, S_in->n, low, DevPlanes{mp.base, N}, so->planes());
+    } else {
+        DevPlanes p;
+        if ((rc = as_planes(c, S_in, SL_TMP0, &p))) return rc;
+        uint32_t lowl[8];
+        fr_store(fr_from_i64(low), lowl);
+        launch_lu_map_planes(c->stream, p, S_in->n, lowl, DevPlanes{mp.base, N}, so->planes());
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *S_out = so;
+    *m_out = m;
+    return ZKH_OK;
+}
+// A = 1/(S + beta) into planes A (n entries)
+static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, DevPlanes A) {
+    int rc = 0;
+    uint32_t nb = inv_blocks(n);
+    uint32_t* others = (uint32_t*)scratch(c, SL_TMP4, (size_t)nb * 256 * 32, &rc);
+    if (rc) return rc;
+    uint32_t* bp = (uint32_t*)scratch(c, SL_SMALL, (size_t)nb * 64 + 64, &rc);
+    if (rc) return rc;
+    uint32_t bl[8];
+    fr_store(beta, bl);
+    launch_inv_pass1(c->stream, S, n, bl, A, others, bp);
+    if ((rc = ensure_pinned(c, (size_t)nb * 32))) return rc;
+    HIPCHK(c, hipMemcpyAsync(c->pinned, bp, (size_t)nb * 32, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    // invert the block totals (Montgomery form) with one exponentiation
+    std::vector<Fr> x(nb), pre(nb);
+    for (uint32_t b = 0; b < nb; b++) x[b] = fr_from_mont(fr_load(c->pinned + 8 * (size_t)b));
+    Fr run = kOne;
+    for (uint32_t b = 0; b < nb; b++) {
+        pre[b] = run;
+        run = fr_mul(run, x[b]);
+    }
+    Fr y = fr_inv(run);
+    std::vector<uint32_t> inv_m((size_t)nb * 8);
+    for (int b = (int)nb - 1; b >= 0; b--) {
+        Fr ib = fr_mul(y, pre[b]);
+        y = fr_mul(y, x[b]);
+        fr_store(fr_to_mont(ib), &inv_m[8 * (size_t)b]);
+    }
+    uint32_t* binv = bp + 8 * (size_t)nb;
+    if ((rc = upload(c, binv, inv_m.data(), inv_m.size() * 4))) return rc;
+    launch_inv_pass2(c->stream, S, n, bl, A, others, binv);
+    return 0;
+}
+extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t beta[8], zkh_tensor** A_out) {
+    if (!c || !S || !beta || !A_out) return fail(c, ZKH_EARG, "null argument");
+    if (!fr_is_canonical(beta)) return fail(c, ZKH_EARG, "non-canonical beta");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    DevPlanes p;
+    if ((rc = as_planes(c, S, SL_TMP0, &p))) return rc;
+    zkh_tensor* A;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, S->n, &A))) return rc;
+    if (S->n && (rc = batch_inverse(c, p, S->n, fr_load(beta), A->planes()))) {
+        zkh_tensor_free(A);
+        return rc;
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *A_out = A;
+    return ZKH_OK;
+}
+
+extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const zkh_tensor* S,
+                            const zkh_tensor* T, const zkh_tensor* m, const uint32_t alpha_l[8],
+                            const uint32_t beta_l[8], const uint32_t* u_l, uint32_t* ev_out,
+                            uint32_t* term_out, uint32_t* ws_out) {
+    if (!c || !tr || !A || !S || !T || !m || !alpha_l || !beta_l) return fail(c, ZKH_EARG, "null argument");
+    const uint32_t D = A->n, N = T->n;
+    // tLookup::prove shape rules (tlookup.cu:330-336)
+    if (S->n != D || m->n != N || !D || !N || (D & (D - 1)) || (N & (N - 1)) || D % N)
+        return fail(c, ZKH_EARG, "D or N is not power of 2, or D is not divisible by N");
+    const uint32_t logD = ceil_log2(D);
+    if (logD && !u_l) return fail(c, ZKH_EARG, "null u");
+    if (!fr_is_canonical(alpha_l) || !fr_is_canonical(beta_l) || !all_canonical(u_l, logD))
+        return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    Fr alpha = fr_load(alpha_l), beta = fr_load(beta_l);
+    std::vector<Fr> u = load_frs(u_l, logD);
+
+    // working tables: caller tensors are read in place until their first fold
+    DevPlanes Ac, Sc, Tc, mc;
+    if ((rc = as_planes(c, A, SL_TMP0, &Ac)) || (rc = as_planes(c, S, SL_TMP1, &Sc)) ||
+        (rc = as_planes(c, T, SL_TMP2, &Tc)) || (rc = as_planes(c, m, SL_TMP3, &mc)))
+        return rc;
+    DevPlanes Aw = A->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP0, D / 2, &rc) : Ac;
+    if (rc) return rc;
+    DevPlanes Sw = S->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP1, D / 2, &rc) : Sc;
+    if (rc) return rc;
+    DevPlanes Tw = T->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP2, N / 2, &rc) : Tc;
+    if (rc) return rc;
+    DevPlanes mw = m->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP3, N / 2, &rc) : mc;
+    if (rc) return rc;
+    DevPlanes Bw = scratch_planes(c, SL_TMP4 + 0, N, &rc);  // Bv = 1/(T+beta), owned
+    if (rc) return rc;
+    // SL_TMP4 is also batch_inverse's scratch: give Bv its own slot
+    Bw = scratch_planes(c, SL_EO, N, &rc);
+    if (rc) return rc;
+    if ((rc = batch_inverse(c, Tc, N, beta, Bw))) return rc;
+
+    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 11 * 32, &rc);
+    if (rc) return rc;
+    // C = alpha^2 - sum Bv*m (zkob_rescale.cu:136)
+    Fr bm;
+    {
+        uint32_t nb = launch_dot_planes(c->stream, Bw, mc, N, part);
+        if ((rc = fetch_sums(c, part, nb, 1, &bm))) return rc;
+        bm = fix1(bm);
+    }
+    Fr alpha_sq = fr_mul(alpha, alpha);
+    Fr Cc = fr_sub(alpha_sq, bm);
+    Fr claim = fr_add(alpha, alpha_sq);
+    Fr inv_ratio = fr_mul(fr_u64(N), fr_inv(fr_u64(D)));
+    Fr inv2 = fr_inv2();
+
+    EqState eq;
+    if ((rc = eq_setup(c, u, eq, SL_FAC, SL_ELO))) return rc;
+
+    // table handles: source = current data, dst = working buffer
+    DevPlanes a_src = Ac, s_src = Sc, b_src = Bw, t_src = Tc, m_src = mc;
+    bool as_pending = false, btm_pending = false;  // a fold with vm is owed
+    uint32_t vm[8] = {0};
+    Fr three = fr_u64(3);
+    for (uint32_t r = 0; r < logD; r++) {
+        const uint32_t n = D >> r;
+        const uint32_t k = logD - r;  // remaining variables
+        const uint32_t K = k - 1;     // eq variables of the pairs
+        const Fr ul = u[k - 1];
+        const Fr corr = eq_corr(eq, K);
+        Fr coef[4];
+        if (n > N) {  // phase 1
+            Tab ta{a_src, Aw}, ts{s_src, Sw};
+            uint32_t nb = launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l,
+                                           EqW{eq.elo_d, eq.fac_d, K}, part);
+            if (as_pending) {
+                a_src = Aw;
+                s_src = Sw;
+            }
+            Fr s[5];
+            if ((rc = fetch_sums(c, part, nb, 5, s))) return rc;
+            Fr q0 = fr_mul(fix1(s[0]), corr), q1 = fr_mul(fix1(s[1]), corr), q2 = fr_mul(fix1(s[2]), corr);
+            Fr qc1 = fr_sub(fr_sub(q1, q0), q2);
+            Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
+            Fr aq0 = fr_mul(alpha, q0), aq1 = fr_mul(alpha, qc1), aq2 = fr_mul(alpha, q2);
+            coef[0] = fr_add(fr_add(fr_mul(e0, aq0), s[3]), fr_mul(Cc, inv2));
+            coef[1] = fr_add(fr_add(fr_mul(e0, aq1), fr_mul(e1, aq0)), fr_sub(s[4], s[3]));
+            coef[2] = fr_add(fr_mul(e0, aq2), fr_mul(e1, aq1));
+            coef[3] = fr_mul(e1, aq2);
+            as_pending = true;
+        } else {  // phase 2
+            Tab ta{a_src, Aw}, ts{s_src, Sw}, tb{b_src, Bw}, tt{t_src, Tw}, tm{m_src, mw};
+            uint32_t nb = launch_lu_phase2(c->stream, ta, ts, tb, tt, tm, n, as_pending, btm_pending,
+                                           vm, beta_l, EqW{eq.elo_d, eq.fac_d, K}, part);
+            if (as_pending) {
+                a_src = Aw;
+                s_src = Sw;
+            }
+            if (btm_pending) {
+                b_src = Bw;
+                t_src = Tw;
+                m_src = mw;
+            }
+            Fr s[11];
+            if ((rc = fetch_sums(c, part, nb, 11, s))) return rc;
+            Fr qa0 = fr_mul(fix1(s[0]), corr), qa1 = fr_mul(fix1(s[1]), corr), qa2 = fr_mul(fix1(s[2]), corr);
+            Fr qb0 = fr_mul(fix1(s[3]), corr), qb1 = fr_mul(fix1(s[4]), corr), qb2 = fr_mul(fix1(s[5]), corr);
+            Fr coefBT = fr_mul(inv_ratio, alpha_sq);
+            Fr Q0 = fr_add(fr_mul(alpha, qa0), fr_mul(coefBT, qb0));
+            Fr Q1 = fr_add(fr_mul(alpha, fr_sub(fr_sub(qa1, qa0), qa2)),
+                           fr_mul(coefBT, fr_sub(fr_sub(qb1, qb0), qb2)));
+            Fr Q2 = fr_add(fr_mul(alpha, qa2), fr_mul(coefBT, qb2));
+            Fr M0 = fix1(s[8]), M1 = fix1(s[9]), M2 = fix1(s[10]);
+            Fr Mc1 = fr_sub(fr_sub(M1, M0), M2);
+            Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
+            coef[0] = fr_sub(fr_add(fr_mul(e0, Q0), s[6]), fr_mul(inv_ratio, M0));
+            coef[1] = fr_sub(fr_add(fr_add(fr_mul(e0, Q1), fr_mul(e1, Q0)), fr_sub(s[7], s[6])),
+                             fr_mul(inv_ratio, Mc1));
+            coef[2] = fr_sub(fr_add(fr_mul(e0, Q2), fr_mul(e1, Q1)), fr_mul(inv_ratio, M2));
+            coef[3] = fr_mul(e1, Q2);
+            as_pending = true;
+            btm_pending = true;
+        }
+        Fr e[4] = {coef[0], fr_poly_eval(coef, 3, kOne), fr_poly_eval(coef, 3, fr_u64(2)),
+                   fr_poly_eval(coef, 3, three)};
+        if (!fr_eq(claim, fr_add(e[0], e[1])))
+            return fail(c, ZKH_EROUND, "phase%d round inconsistency (witness bug) at round %u",
+                        n > N ? 1 : 2, r);
+        static const char* lab[4] = {"p0", "p1", "p2", "p3"};
+        for (int t = 0; t < 4; t++) {
+            tr_absorb_fr(tr, lab[t], e[t]);
+            if (ev_out) fr_store(e[t], ev_out + 8 * (4 * r + t));
+        }
+        Fr v = tr_challenge(tr);
+        if (ws_out) fr_store(v, ws_out + 8 * r);
+        claim = fr_poly_eval(coef, 3, v);
+        Fr eqv = fr_eq2(ul, v);
+        alpha = fr_mul(alpha, eqv);
+        if (n > N) Cc = fr_mul(Cc, inv2);
+        else alpha_sq = fr_mul(alpha_sq, eqv);
+        fr_store(fr_to_mont(v), vm);
+    }
+    // owed folds produce the terminals (size 2 -> 1)
+    if (as_pending) {
+        launch_fold(c->stream, Tab{a_src, Aw}, 1, vm);
+        launch_fold(c->stream, Tab{s_src, Sw}, 1, vm);
+        a_src = Aw;
+        s_src = Sw;
+    }
+    if (btm_pending) {
+        launch_fold(c->stream, Tab{b_src, Bw}, 1, vm);
+        launch_fold(c->stream, Tab{t_src, Tw}, 1, vm);
+        launch_fold(c->stream, Tab{m_src, mw}, 1, vm);
+        b_src = Bw;
+        t_src = Tw;
+        m_src = mw;
+    }
+    DevPlanes fin[5] = {a_src, s_src, b_src, t_src, m_src};
+    uint32_t tv[5][8];
+    for (int i = 0; i < 5; i++) {
+        HIPCHK(c, hipMemcpyAsync(tv[i], fin[i].lo(), 16, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(tv[i] + 4, fin[i].hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (term_out)
+        for (int i = 0; i < 5; i++) memcpy(term_out + 8 * i, tv[i], 32);
+    tr_absorb_fr(tr, "A_f", fr_load(tv[0]));
+    tr_absorb_fr(tr, "S_f", fr_load(tv[1]));
+    tr_absorb_fr(tr, "m_f", fr_load(tv[4]));
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// Hadamard sumcheck (zkob_lookup.cuh:267-315)
+// ---------------------------------------------------------------------------------------
+static Fr lagrange4(const Fr e[4], const Fr& v) {
+    // coefficients through (0..3, e) by Newton differences, then Horner
+    Fr inv2 = fr_inv2(), inv6 = fr_inv(fr_u64(6));
+    Fr d1 = fr_sub(e[1], e[0]), d2 = fr_sub(e[2], e[1]), d3 = fr_sub(e[3], e[2]);
+    Fr dd1 = fr_sub(d2, d1), dd2 = fr_sub(d3, d2);
+    Fr ddd = fr_sub(dd2, dd1);
+    // p(v) = e0 + v d1 + v(v-1)/2 dd1 + v(v-1)(v-2)/6 ddd
+    Fr vm1 = fr_sub(v, kOne), vm2 = fr_sub(v, fr_u64(2));
+    Fr t1 = fr_mul(v, d1);
+    Fr t2 = fr_mul(fr_mul(fr_mul(v, vm1), inv2), dd1);
+    Fr t3 = fr_mul(fr_mul(fr_mul(fr_mul(v, vm1), vm2), inv6), ddd);
+    return fr_add(fr_add(fr_add(e[0], t1), t2), t3);
+}
+static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], const zkh_tensor* E,
+                     const std::vector<Fr>* ueq, const zkh_tensor* S, const zkh_tensor* U,
+                     uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out) {
+    const uint32_t n = S->n;
+    if (!n || (n & (n - 1)) || U->n != n || (E && E->n != n))
+        return fail(c, ZKH_EARG, "hadamard tables must share a power-of-two size");
+    if (ueq && ((uint64_t)1 << ueq->size()) != n) return fail(c, ZKH_EARG, "eq size mismatch");
+    if (!fr_is_canonical(claim_l)) return fail(c, ZKH_EARG, "non-canonical claim");
+    HIPCHK(c, hipSetDevice(c->device));
+    const uint32_t k = ceil_log2(n);
+    int rc = 0;
+    DevPlanes Ec{}, Sc, Uc;
+    if (E && (rc = as_planes(c, E, SL_TMP0, &Ec))) return rc;
+    if ((rc = as_planes(c, S, SL_TMP1, &Sc)) || (rc = as_planes(c, U, SL_TMP2, &Uc))) return rc;
+    DevPlanes Ew{}, Sw, Uw;
+    if (E) {
+        Ew = E->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP0, n / 2 + 1, &rc) : Ec;
+        if (rc) return rc;
+    }
+    Sw = S->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP1, n / 2 + 1, &rc) : Sc;
+    if (rc) return rc;
+    Uw = U->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP2, n / 2 + 1, &rc) : Uc;
+    if (rc) return rc;
+    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 11 * 32, &rc);
+    if (rc) return rc;
+    EqState eq;
+    if (ueq && (rc = eq_setup(c, *ueq, eq, SL_FAC, SL_ELO))) return rc;
+    Fr claim = fr_load(claim_l), cE = kOne;
+    DevPlanes e_src = Ec, s_src = Sc, u_src = Uc;
+    uint32_t vm[8] = {0};
+    static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
+    for (uint32_t r = 0; r < k; r++) {
+        const uint32_t sz = n >> r;
+        const int fold = r > 0;
+        Fr e[4];
+        if (!ueq) {
+            uint32_t nb = launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz,
+                                          fold, vm, part);
+            Fr s[4];
+            if ((rc = fetch_sums(c, part, nb, 4, s))) return rc;
+            for (int t = 0; t < 4; t++) e[t] = fix2(s[t]);
+        } else {
+            const uint32_t K = k - r - 1;
+            const Fr ul = (*ueq)[k - r - 1];
+            uint32_t nb = launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm,
+                                             EqW{eq.elo_d, eq.fac_d, K}, part);
+            Fr s[4];
+            if ((rc = fetch_sums(c, part, nb, 4, s))) return rc;
+            Fr f = fr_mul(cE, eq_corr(eq, K));
+            for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(fix1(s[t]), f), fr_eq2(ul, fr_u64(t)));
+        }
+        if (fold) {
+            e_src = Ew;
+            s_src = Sw;
+            u_src = Uw;
+        }
+        if (!fr_eq(claim, fr_add(e[0], e[1])))
+            return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r);
+        for (int t = 0; t < 4; t++) {
+            tr_absorb_fr(tr, lab[t], e[t]);
+            if (ev_out) fr_store(e[t], ev_out + 8 * (4 * r + t));
+        }
+        Fr w = tr_challenge(tr);
+        if (ws_out) fr_store(w, ws_out + 8 * r);
+        claim = lagrange4(e, w);
+        if (ueq) cE = fr_mul(cE, fr_eq2((*ueq)[k - r - 1], w));
+        fr_store(fr_to_mont(w), vm);
+    }
+    if (k > 0) {
+        if (!ueq) launch_fold(c->stream, Tab{e_src, Ew}, 1, vm);
+        launch_fold(c->stream, Tab{s_src, Sw}, 1, vm);
+        launch_fold(c->stream, Tab{u_src, Uw}, 1, vm);
+        e_src = Ew;
+        s_src = Sw;
+        u_src = Uw;
+    }
+    uint32_t tv[3][8];
+    HIPCHK(c, hipMemcpyAsync(tv[0], s_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(tv[0] + 4, s_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(tv[1], u_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(tv[1] + 4, u_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    if (!ueq) {
+        HIPCHK(c, hipMemcpyAsync(tv[2], e_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(tv[2] + 4, e_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    } else {
+        fr_store(cE, tv[2]);
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    // terminal: cur = E_f * S_f2 * U_f2 (zkob_rope.cu:29)
+    if (!fr_eq(claim, fr_mul(fr_mul(fr_load(tv[2]), fr_load(tv[0])), fr_load(tv[1]))))
+        return fail(c, ZKH_EROUND, "hadamard terminal mismatch (witness bug)");
+    if (term_out) memcpy(term_out, tv, sizeof(tv));
+    return ZKH_OK;
+}
+extern "C" int zkh_hp_prove(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const zkh_tensor* E,
+                            const zkh_tensor* S, const zkh_tensor* U, uint32_t* ev_out,
+                            uint32_t* term_out, uint32_t* ws_out) {
+    if (!c || !tr || !claim || !E || !S || !U) return fail(c, ZKH_EARG, "null argument");
+    return hp_common(c, tr, claim, E, nullptr, S, U, ev_out, term_out, ws_out);
+}
+extern "C" int zkh_hp_prove_eq(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const uint32_t* u,
+                               uint32_t k, const zkh_tensor* S, const zkh_tensor* U, uint32_t* ev_out,
+                               uint32_t* term_out, uint32_t* ws_out) {
+    if (!c || !tr || !claim || !S || !U || (!u && k)) return fail(c, ZKH_EARG, "null argument");
+    if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    std::vector<Fr> uv = load_frs(u, k);
+    return hp_common(c, tr, claim, nullptr, &uv, S, U, ev_out, term_out, ws_out);
+}
