@@ -47,6 +47,15 @@ const char* zkh_last_error(const zkh_ctx* ctx);
 /* wait for all work queued on the context's stream */
 int zkh_ctx_sync(zkh_ctx* ctx);
 
+/* kernel timing, a tracing aid (the reference's BoTimer laps, zkob_claims.cuh:68-75):
+ * when enabled, each kernel class launched on the context is bracketed by HIP events on
+ * its stream; zkh_prof_get returns the summed device time, launch count and algorithmic
+ * bytes (bytes the algorithm must move, not measured traffic) for one class name;
+ * zkh_prof_names lists the recorded names, comma-separated.  Enabling clears the records. */
+int zkh_prof_enable(zkh_ctx* ctx, int on);
+int zkh_prof_get(zkh_ctx* ctx, const char* name, double* ms, uint64_t* launches, double* bytes);
+int zkh_prof_names(zkh_ctx* ctx, char* buf, size_t len);
+
 /* ---------------- tensors (replace FrTensor ctors/save/load: fr-tensor.cu:158-248,
  * zkob_fc.cu:178-185 load_int_tensor, zkob_lookup.cuh:103-110 load_long_tensor) ------- */
 /* host Fr array (AoS, reference byte layout) -> device tensor */

@@ -68,6 +68,9 @@ def lib():
         L.zkh_lu_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove_eq.argtypes = [vp, vp, vp, vp, u32, vp, vp, vp, vp, vp]
+        L.zkh_prof_enable.argtypes = [vp, ctypes.c_int]
+        L.zkh_prof_get.argtypes = [vp, ctypes.c_char_p, vp, vp, vp]
+        L.zkh_prof_names.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
         _lib = L
     return _lib
 

@@ -34,7 +34,71 @@ struct zkh_ctx {
         size_t bytes = 0;
     };
     std::vector<Slot> slots;
+    // pinned ring for small host->device uploads: a region is reused only after a later
+    // stream synchronisation, which every API call performs before returning
+    uint8_t* ring = nullptr;
+    size_t ring_bytes = 0, ring_off = 0;
+    // per-kernel-class timing (zkh_prof_*): events around launches on this stream
+    bool prof = false;
+    struct ProfRec {
+        std::string name;
+        double ms = 0, bytes = 0;
+        uint64_t launches = 0;
+    };
+    struct Pending {
+        int rec;
+        hipEvent_t a, b;
+        double bytes;
+    };
+    std::vector<ProfRec> recs;
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> pool;
 };
+
+// Times the launches issued during its lifetime under `name` when profiling is on.
+struct ProfScope {
+    zkh_ctx* c;
+    int rec = -1;
+    hipEvent_t a = nullptr, b = nullptr;
+    double bytes;
+    ProfScope(zkh_ctx* c_, const char* name, double bytes_) : c(c_), bytes(bytes_) {
+        if (!c->prof) return;
+        for (size_t i = 0; i < c->recs.size(); i++)
+            if (c->recs[i].name == name) rec = (int)i;
+        if (rec < 0) {
+            c->recs.push_back(zkh_ctx::ProfRec{name});
+            rec = (int)c->recs.size() - 1;
+        }
+        for (hipEvent_t* e : {&a, &b}) {
+            if (!c->pool.empty()) {
+                *e = c->pool.back();
+                c->pool.pop_back();
+            } else if (hipEventCreate(e) != hipSuccess) {
+                *e = nullptr;
+            }
+        }
+        if (a) (void)hipEventRecord(a, c->stream);
+    }
+    ~ProfScope() {
+        if (rec < 0 || !a || !b) return;
+        (void)hipEventRecord(b, c->stream);
+        c->pending.push_back(zkh_ctx::Pending{rec, a, b, bytes});
+    }
+};
+// fold finished event pairs into the records (call after a stream synchronisation)
+static void prof_resolve(zkh_ctx* c) {
+    for (auto& p : c->pending) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            c->recs[p.rec].ms += ms;
+            c->recs[p.rec].bytes += p.bytes;
+            c->recs[p.rec].launches++;
+        }
+        c->pool.push_back(p.a);
+        c->pool.push_back(p.b);
+    }
+    c->pending.clear();
+}
 
 struct zkh_tensor {
     zkh_ctx* ctx = nullptr;
@@ -89,8 +153,8 @@ static void* scratch(zkh_ctx* c, int slot, size_t bytes, int* rc) {
     zkh_ctx::Slot& s = c->slots[slot];
     if (s.bytes >= bytes && s.p) return s.p;
     if (s.p) {
-        hipStreamSynchronize(c->stream);
-        hipFree(s.p);
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(s.p);
         s.p = nullptr;
         s.bytes = 0;
     }
@@ -109,7 +173,7 @@ static DevPlanes scratch_planes(zkh_ctx* c, int slot, uint32_t n, int* rc) {
 }
 static int ensure_pinned(zkh_ctx* c, size_t bytes) {
     if (c->pinned_bytes >= bytes) return 0;
-    if (c->pinned) hipHostFree(c->pinned);
+    if (c->pinned) (void)hipHostFree(c->pinned);
     c->pinned = nullptr;
     size_t want = std::max(bytes, (size_t)1 << 20);
     if (hipHostMalloc((void**)&c->pinned, want, hipHostMallocDefault) != hipSuccess)
@@ -124,19 +188,35 @@ static int fetch_sums(zkh_ctx* c, const uint32_t* dpart, uint32_t nb, int K, Fr*
     if (rc) return rc;
     HIPCHK(c, hipMemcpyAsync(c->pinned, dpart, bytes, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    c->ring_off = 0;
+    if (c->prof) prof_resolve(c);
     for (int k = 0; k < K; k++) out[k] = kZero;
     for (uint32_t b = 0; b < nb; b++)
         for (int k = 0; k < K; k++) out[k] = fr_add(out[k], fr_load(c->pinned + ((size_t)b * K + k) * 8));
     return 0;
 }
-// host AoS -> device (through the pinned buffer)
+// small host -> device upload through the pinned ring (asynchronous; ordered on the stream)
 static int upload(zkh_ctx* c, void* dst, const void* src, size_t bytes) {
-    int rc = ensure_pinned(c, bytes);
-    if (rc) return rc;
-    HIPCHK(c, hipStreamSynchronize(c->stream));  // pinned buffer may still feed a copy
-    memcpy(c->pinned, src, bytes);
-    HIPCHK(c, hipMemcpyAsync(dst, c->pinned, bytes, hipMemcpyHostToDevice, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
+    size_t need = (bytes + 255) & ~(size_t)255;
+    if (need > c->ring_bytes) {
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        if (c->ring) (void)hipHostFree(c->ring);
+        c->ring = nullptr;
+        c->ring_bytes = std::max(need, (size_t)1 << 20);
+        if (hipHostMalloc((void**)&c->ring, c->ring_bytes, hipHostMallocDefault) != hipSuccess) {
+            c->ring_bytes = 0;
+            return fail(c, ZKH_EDEV, "hipHostMalloc(ring) failed");
+        }
+        c->ring_off = 0;
+    }
+    if (c->ring_off + need > c->ring_bytes) {  // wrap: earlier regions must have been consumed
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        c->ring_off = 0;
+    }
+    uint8_t* h = c->ring + c->ring_off;
+    c->ring_off += need;
+    memcpy(h, src, bytes);
+    HIPCHK(c, hipMemcpyAsync(dst, h, bytes, hipMemcpyHostToDevice, c->stream));
     return 0;
 }
 static uint32_t ceil_log2(uint32_t n) {
@@ -154,7 +234,6 @@ static uint32_t bits_for(uint64_t absmax) {
     while (b < 63 && ((uint64_t)1 << b) <= absmax) b++;
     return b;  // absmax < 2^b
 }
-static const Fr& R2() { return kR2; }                 // mont_mul(x, R2) = x * 2^256
 static Fr fix1(const Fr& x) { return fr_mont_mul(x, kR2); }  // undo one 2^-256
 static Fr fix2(const Fr& x) {
     static const Fr r3 = fr_rpow(3);
@@ -262,7 +341,7 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
     }
     c->slots.resize(SL_COUNT);
     if (ensure_pinned(c, (size_t)1 << 20)) {
-        hipStreamDestroy(c->stream);
+        (void)hipStreamDestroy(c->stream);
         delete c;
         return ZKH_EDEV;
     }
@@ -271,13 +350,58 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
 }
 extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
     if (!c) return ZKH_EARG;
-    hipSetDevice(c->device);
-    hipStreamSynchronize(c->stream);
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
     for (auto& s : c->slots)
-        if (s.p) hipFree(s.p);
-    if (c->pinned) hipHostFree(c->pinned);
-    hipStreamDestroy(c->stream);
+        if (s.p) (void)hipFree(s.p);
+    if (c->pinned) (void)hipHostFree(c->pinned);
+    if (c->ring) (void)hipHostFree(c->ring);
+    for (auto& p : c->pending) {
+        c->pool.push_back(p.a);
+        c->pool.push_back(p.b);
+    }
+    for (hipEvent_t e : c->pool) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(c->stream);
     delete c;
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// kernel timing (tracing aid; the reference's BoTimer laps, zkob_claims.cuh:68-75)
+// ---------------------------------------------------------------------------------------
+extern "C" int zkh_prof_enable(zkh_ctx* c, int on) {
+    if (!c) return ZKH_EARG;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    prof_resolve(c);
+    c->recs.clear();
+    c->prof = on != 0;
+    return ZKH_OK;
+}
+extern "C" int zkh_prof_get(zkh_ctx* c, const char* name, double* ms, uint64_t* launches,
+                            double* bytes) {
+    if (!c || !name) return ZKH_EARG;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    prof_resolve(c);
+    for (auto& r : c->recs)
+        if (r.name == name) {
+            if (ms) *ms = r.ms;
+            if (launches) *launches = r.launches;
+            if (bytes) *bytes = r.bytes;
+            return ZKH_OK;
+        }
+    if (ms) *ms = 0;
+    if (launches) *launches = 0;
+    if (bytes) *bytes = 0;
+    return ZKH_OK;
+}
+extern "C" int zkh_prof_names(zkh_ctx* c, char* buf, size_t len) {
+    if (!c || !buf || !len) return ZKH_EARG;
+    std::string all;
+    for (auto& r : c->recs) {
+        if (!all.empty()) all += ",";
+        all += r.name;
+    }
+    snprintf(buf, len, "%s", all.c_str());
     return ZKH_OK;
 }
 extern "C" const char* zkh_last_error(const zkh_ctx* c) { return c ? c->err.c_str() : "null context"; }
@@ -346,14 +470,14 @@ static int make_int_tensor(zkh_ctx* c, const void* src, uint32_t n, int kind, hi
         hipError_t e = hipMemcpyAsync(t->d, src, (size_t)n * es, dir, c->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
         if (e != hipSuccess) {
-            hipFree(t->d);
+            (void)hipFree(t->d);
             delete t;
             return fail(c, ZKH_EDEV, "tensor upload failed: %s", hipGetErrorString(e));
         }
         rc = kind == ZKH_KIND_I32 ? int_bits_i32(c, (const int32_t*)t->d, n, &t->bits)
                                   : int_bits_i64(c, (const int64_t*)t->d, n, &t->bits);
         if (rc) {
-            hipFree(t->d);
+            (void)hipFree(t->d);
             delete t;
             return rc;
         }
@@ -418,7 +542,7 @@ extern "C" int zkh_tensor_from_fr(zkh_ctx* c, const uint32_t* aos, uint32_t n, z
             e = hipStreamSynchronize(c->stream);
         }
         if (rc || e != hipSuccess) {
-            hipFree(t->d);
+            (void)hipFree(t->d);
             delete t;
             return rc ? rc : fail(c, ZKH_EDEV, "upload failed: %s", hipGetErrorString(e));
         }
@@ -428,7 +552,7 @@ extern "C" int zkh_tensor_from_fr(zkh_ctx* c, const uint32_t* aos, uint32_t n, z
 }
 extern "C" int zkh_tensor_free(zkh_tensor* t) {
     if (!t) return ZKH_EARG;
-    if (t->d) hipFree(t->d);
+    if (t->d) (void)hipFree(t->d);
     delete t;
     return ZKH_OK;
 }
@@ -507,7 +631,11 @@ static int eq_weighted_sum(zkh_ctx* c, DevPlanes S, const DevPlanes* U, uint32_t
     uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 32, &rc);
     if (rc) return rc;
     uint32_t K = (uint32_t)u.size();
-    uint32_t nb = launch_eq_sum(c->stream, S, U, n, EqW{st.elo_d, st.fac_d, K}, part);
+    uint32_t nb;
+    {
+        ProfScope ps(c, "eq_sum", (double)n * (U ? 64 : 32));
+        nb = launch_eq_sum(c->stream, S, U, n, EqW{st.elo_d, st.fac_d, K}, part);
+    }
     Fr s;
     if ((rc = fetch_sums(c, part, nb, 1, &s))) return rc;
     s = fr_mul(s, eq_corr(st, K));
@@ -757,17 +885,18 @@ static int eq_reduce_int(zkh_ctx* c, const void* M, int kind, uint32_t bits, uin
     nch = (K + kchunk - 1) / kchunk;
     uint32_t* part = (uint32_t*)scratch(c, SL_TMP6, (size_t)nch * N * 32, &rc);
     if (rc) return rc;
-    if (kind == ZKH_KIND_I32) launch_eqdot_i32(c->stream, (const int32_t*)M, K, N, E, kchunk, bits, part);
-    else launch_eqdot_i64(c->stream, (const int64_t*)M, K, N, E, kchunk, bits, part);
-    // correction 2^bits * sum_{k<K} e_k
-    Fr corr = fr_mul(fr_from_i64(0), kZero);
     {
-        Fr two_b = kOne;
-        for (uint32_t b = 0; b < bits; b++) two_b = fr_add(two_b, two_b);
-        corr = fr_mul(two_b, SE);
+        ProfScope ps(c, "eqdot", (double)K * N * (kind == ZKH_KIND_I32 ? 4 : 8) + (double)nch * N * 32);
+        if (kind == ZKH_KIND_I32) launch_eqdot_i32(c->stream, (const int32_t*)M, K, N, E, kchunk, bits, part);
+        else launch_eqdot_i64(c->stream, (const int64_t*)M, K, N, E, kchunk, bits, part);
     }
+    // correction 2^bits * sum_{k<K} e_k
+    Fr two_b = kOne;
+    for (uint32_t b = 0; b < bits; b++) two_b = fr_add(two_b, two_b);
+    Fr corr = fr_mul(two_b, SE);
     uint32_t corr_l[8];
     fr_store(corr, corr_l);
+    ProfScope ps(c, "sum_chunks", (double)nch * N * 32 + (double)Npad * 32);
     launch_sum_chunks(c->stream, part, nch, N, Npad, corr_l, out);
     return 0;
 }
@@ -830,7 +959,11 @@ extern "C" int zkh_mm_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* X, con
     uint32_t vm[8] = {0};
     for (uint32_t r = 0; r < L; r++) {
         uint32_t n = INp >> r;
-        uint32_t nb = launch_zkip_round(c->stream, Tab{a, a}, Tab{b, b}, n, r > 0, vm, part);
+        uint32_t nb;
+        {
+            ProfScope ps(c, "zkip_round", (r > 0 ? 2.0 * n + n : (double)n) * 2 * 32);
+            nb = launch_zkip_round(c->stream, Tab{a, a}, Tab{b, b}, n, r > 0, vm, part);
+        }
         Fr s[3];
         if ((rc = fetch_sums(c, part, nb, 3, s))) return rc;
         Fr c0 = fix1(s[0]), q1 = fix1(s[1]), c2 = fix1(s[2]);
@@ -939,13 +1072,15 @@ extern "C" int zkh_lu_prep(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_
 }
 extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, const zkh_tensor* mapped,
                               zkh_tensor** S_out, zkh_tensor** m_out) {
-    if (!c || !S_in || !mapped || !S_out || !m_out || mapped->kind != ZKH_KIND_FR || !mapped->n)
+    if (!c || !S_in || !mapped || !S_out || !m_out || !mapped->n)
         return fail(c, ZKH_EARG, "bad arguments");
     HIPCHK(c, hipSetDevice(c->device));
     uint32_t N = mapped->n;
     uint32_t* counts;
     int rc = lu_counts(c, S_in, low, N, &counts);
     if (rc) return rc;
+    DevPlanes mp;
+    if ((rc = as_planes(c, mapped, SL_TMP1, &mp))) return rc;
     zkh_tensor *m, *so;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, S_in->n, &so))) {
@@ -953,16 +1088,14 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
         return rc;
     }
     launch_counts_to_planes(c->stream, counts, N, m->planes());
-    DevPlanes mp = mapped->planes();
-    mp.cap = mapped->cap;
     if (S_in->kind == ZKH_KIND_I32) {
-        launch_lu_map_i32(c->stream, (const int32_t*)S_in->d, S_in->n, low, DevPlanes{mp.base, N}, so->planes());
+        launch_lu_map_i32(c->stream, (const int32_t*)S_in->d, S_in->n, low, mp, so->planes());
     } else {
         DevPlanes p;
         if ((rc = as_planes(c, S_in, SL_TMP0, &p))) return rc;
         uint32_t lowl[8];
         fr_store(fr_from_i64(low), lowl);
-        launch_lu_map_planes(c->stream, p, S_in->n, lowl, DevPlanes{mp.base, N}, so->planes());
+        launch_lu_map_planes(c->stream, p, S_in->n, lowl, mp, so->planes());
     }
     HIPCHK(c, hipStreamSynchronize(c->stream));
     *S_out = so;
@@ -979,7 +1112,10 @@ static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, De
     if (rc) return rc;
     uint32_t bl[8];
     fr_store(beta, bl);
-    launch_inv_pass1(c->stream, S, n, bl, A, others, bp);
+    {
+        ProfScope ps(c, "inv_pass1", (double)n * 64 + (double)nb * 256 * 32);
+        launch_inv_pass1(c->stream, S, n, bl, A, others, bp);
+    }
     if ((rc = ensure_pinned(c, (size_t)nb * 32))) return rc;
     HIPCHK(c, hipMemcpyAsync(c->pinned, bp, (size_t)nb * 32, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -1000,6 +1136,7 @@ static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, De
     }
     uint32_t* binv = bp + 8 * (size_t)nb;
     if ((rc = upload(c, binv, inv_m.data(), inv_m.size() * 4))) return rc;
+    ProfScope ps(c, "inv_pass2", (double)n * 96 + (double)nb * 256 * 32);
     launch_inv_pass2(c->stream, S, n, bl, A, others, binv);
     return 0;
 }
@@ -1052,10 +1189,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
     if (rc) return rc;
     DevPlanes mw = m->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP3, N / 2, &rc) : mc;
     if (rc) return rc;
-    DevPlanes Bw = scratch_planes(c, SL_TMP4 + 0, N, &rc);  // Bv = 1/(T+beta), owned
-    if (rc) return rc;
-    // SL_TMP4 is also batch_inverse's scratch: give Bv its own slot
-    Bw = scratch_planes(c, SL_EO, N, &rc);
+    DevPlanes Bw = scratch_planes(c, SL_EO, N, &rc);  // Bv = 1/(T+beta), owned
     if (rc) return rc;
     if ((rc = batch_inverse(c, Tc, N, beta, Bw))) return rc;
 
@@ -1091,8 +1225,12 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
         Fr coef[4];
         if (n > N) {  // phase 1
             Tab ta{a_src, Aw}, ts{s_src, Sw};
-            uint32_t nb = launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l,
-                                           EqW{eq.elo_d, eq.fac_d, K}, part);
+            uint32_t nb;
+            {
+                ProfScope ps(c, "lu_phase1", (as_pending ? 3.0 * n : (double)n) * 2 * 32);
+                nb = launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l,
+                                      EqW{eq.elo_d, eq.fac_d, K}, part);
+            }
             if (as_pending) {
                 a_src = Aw;
                 s_src = Sw;
@@ -1110,8 +1248,13 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
             as_pending = true;
         } else {  // phase 2
             Tab ta{a_src, Aw}, ts{s_src, Sw}, tb{b_src, Bw}, tt{t_src, Tw}, tm{m_src, mw};
-            uint32_t nb = launch_lu_phase2(c->stream, ta, ts, tb, tt, tm, n, as_pending, btm_pending,
-                                           vm, beta_l, EqW{eq.elo_d, eq.fac_d, K}, part);
+            uint32_t nb;
+            {
+                ProfScope ps(c, "lu_phase2",
+                             ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
+                nb = launch_lu_phase2(c->stream, ta, ts, tb, tt, tm, n, as_pending, btm_pending,
+                                      vm, beta_l, EqW{eq.elo_d, eq.fac_d, K}, part);
+            }
             if (as_pending) {
                 a_src = Aw;
                 s_src = Sw;
@@ -1242,16 +1385,24 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         const int fold = r > 0;
         Fr e[4];
         if (!ueq) {
-            uint32_t nb = launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz,
-                                          fold, vm, part);
+            uint32_t nb;
+            {
+                ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
+                nb = launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz,
+                                     fold, vm, part);
+            }
             Fr s[4];
             if ((rc = fetch_sums(c, part, nb, 4, s))) return rc;
             for (int t = 0; t < 4; t++) e[t] = fix2(s[t]);
         } else {
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
-            uint32_t nb = launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm,
-                                             EqW{eq.elo_d, eq.fac_d, K}, part);
+            uint32_t nb;
+            {
+                ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
+                nb = launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm,
+                                        EqW{eq.elo_d, eq.fac_d, K}, part);
+            }
             Fr s[4];
             if ((rc = fetch_sums(c, part, nb, 4, s))) return rc;
             Fr f = fr_mul(cE, eq_corr(eq, K));
