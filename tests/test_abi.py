@@ -1,0 +1,65 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point include/zkh.h
+declares, its host-side transcript matches the reference framing, and without a GPU the
+context constructor fails cleanly (no CPU fallback)."""
+import ctypes
+import hashlib
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    src = open(os.path.join(ROOT, "include", "zkh.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(zkh_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    for s in ["zkh_ctx_create", "zkh_mm_prove", "zkh_lu_prove", "zkh_hp_prove", "zkh_me",
+              "zkh_partial_me", "zkh_multi_dim_me", "zkh_lu_inverse", "zkh_lu_prep"]:
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(zkh):
+    lib = zkh.lib()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_transcript_matches_reference_framing(zkh):
+    st = zkh.transcript("run:ob1")
+    ref = hashlib.sha256(b"run:ob1").digest()
+    assert bytes(st) == ref
+    zkh.absorb(st, "B", struct.pack("<I", 512))
+    ref = hashlib.sha256(ref + struct.pack("<I", 1) + b"B" + struct.pack("<Q", 4) + struct.pack("<I", 512)).digest()
+    assert bytes(st) == ref
+    x = zkh.challenge(st)
+    limbs = list(struct.unpack("<8I", hashlib.sha256(ref + b"chal").digest()))
+    limbs[7] %= 1944954707
+    assert list(x) == limbs
+
+
+def test_transcript_matches_oracle(zkh):
+    from oracle import coracle as C
+    a, b = zkh.transcript("s"), C.tr_init("s")
+    for i in range(20):
+        data = bytes(range(i * 3 % 64))
+        zkh.absorb(a, "p%d" % i, data)
+        C.tr_absorb(b, "p%d" % i, data)
+        assert np.array_equal(zkh.challenge(a), C.tr_challenge_fr(b))
+    assert bytes(a) == bytes(b)
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is present")
+def test_no_gpu_fails_loudly(zkh):
+    h = ctypes.c_void_p()
+    rc = zkh.lib().zkh_ctx_create(0, ctypes.byref(h))
+    assert rc == zkh.EDEV and not h.value
+    with pytest.raises(zkh.ZkhError):
+        zkh.Context(0)
