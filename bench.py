@@ -6,9 +6,10 @@ TinyLlama-1.1B".
 
 - A *step* is the 7 matmul (zkip) sumchecks of one layer -- Q, K, V, O (d=2048, 4 KV heads
   x 64 = 256), gate/up (2048 -> 5632), down (5632 -> 2048) at B = 512 -- each the
-  zkob_fc.cu:259-440 segment, run concurrently from 7 host threads on 7 contexts
-  (independent transcripts).  value = elements bound per second, with elements bound
-  E = B*IN + IN*OUT + B*OUT + 2*IN per matmul (every input table entry bound once).
+  zkob_fc.cu:259-440 segment with its own transcript, proven in one batched call
+  (zkh_mm_prove_batch: one launch and one host synchronisation per round for all 7).
+  value = elements bound per second, with elements bound E = B*IN + IN*OUT + B*OUT + 2*IN
+  per matmul (every input table entry bound once).
 - prove_s_per_layer additionally runs the layer's other hot-path segments concurrently:
   the SwiGLU mapping lookup (logUp, D = N = 2^22) with its Hadamard sumcheck (2^22), and
   the RoPE eq-weighted Hadamard sumchecks (q: 2 x 2^20, k: 2 x 2^17).
@@ -24,6 +25,7 @@ TinyLlama-1.1B".
 """
 import argparse
 import concurrent.futures
+import gc
 import hashlib
 import importlib.util
 import json
@@ -229,6 +231,9 @@ def main():
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
+    ap.add_argument("--no-prof", action="store_true", help="time without the kernel-timing events")
+    ap.add_argument("--segment", choices=["glu", "rope"], default=None,
+                    help="only run one non-matmul segment repeatedly (for profiling), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -239,26 +244,54 @@ def main():
     zkh, synth = load_pkg()
     rng = synth.rng_for(4)
     L = LAYER
+    if args.segment:
+        job = GluJob(zkh, synth, rng, L["B"], L["ffn"]) if args.segment == "glu" else \
+            RopeJob(zkh, rng, "q", L["B"], L["d"])
+        ref = job.run()
+        gc.collect()
+        gc.disable()
+        times = []
+        for _ in range(args.steps):
+            t = time.perf_counter()
+            assert job.run() == ref
+            times.append((time.perf_counter() - t) * 1000.0)
+        print(json.dumps({"segment": args.segment, "ms": times}))
+        return
     t_setup = time.perf_counter()
     jobs = [MatmulJob(zkh, synth, rng, n, L["B"], i, o) for n, i, o in MATMULS]
     E_total = sum(j.elements for j in jobs)
     pool = concurrent.futures.ThreadPoolExecutor(max_workers=16)
 
+    mctx = zkh.Context(0)
+
     def mm_step():
-        return list(pool.map(lambda j: j.run(), jobs))
+        items = []
+        for j in jobs:
+            j.st = j.st0.copy()
+            items.append((j.st, j.X, j.W, j.Y, j.B, j.IN, j.OUT))
+        outs, _ = mctx.mm_prove_batch(items)
+        return [o["claims"].tobytes() + j.st.tobytes() for o, j in zip(outs, jobs)]
 
     ref = None
     for _ in range(args.warmup):
         ref = mm_step()
     print("setup %.1fs; matmul step warm" % (time.perf_counter() - t_setup), file=sys.stderr, flush=True)
-    for j in jobs:
-        zkh.lib().zkh_prof_enable(j.ctx.h, 1)
+    zkh.lib().zkh_prof_enable(mctx.h, 0 if args.no_prof else 1)
+    # the interpreter's cyclic GC (millions of objects once torch is imported) would stall
+    # a step for tens of ms at fixed allocation counts; it stays off while timing
+    gc.collect()
+    gc.disable()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    step_ms = []
     for _ in range(args.steps):
+        ts = time.perf_counter()
         out = mm_step()
+        step_ms.append((time.perf_counter() - ts) * 1000.0)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    print("per-step ms: " + " ".join("%.2f" % x for x in step_ms), file=sys.stderr, flush=True)
+    gc.enable()
     assert ref is None or out == ref, "non-deterministic proof output"
     ms_step = (t1 - t0) * 1000.0 / args.steps
     value = E_total / (ms_step / 1000.0)
@@ -267,19 +300,15 @@ def main():
     # per-kernel device time over the timed steps (all contexts)
     import ctypes
     kern = {}
-    for j in jobs:
-        buf = ctypes.create_string_buffer(4096)
-        zkh.lib().zkh_prof_names(j.ctx.h, buf, 4096)
-        for name in filter(None, buf.value.decode().split(",")):
-            ms, la, by = ctypes.c_double(), ctypes.c_uint64(), ctypes.c_double()
-            zkh.lib().zkh_prof_get(j.ctx.h, name.encode(), ctypes.byref(ms), ctypes.byref(la), ctypes.byref(by))
-            k = kern.setdefault(name, [0.0, 0, 0.0])
-            k[0] += ms.value
-            k[1] += la.value
-            k[2] += by.value
-        zkh.lib().zkh_prof_enable(j.ctx.h, 0)
-    dom = max(kern, key=lambda n: kern[n][0])
-    dms, dla, dby = kern[dom]
+    buf = ctypes.create_string_buffer(4096)
+    zkh.lib().zkh_prof_names(mctx.h, buf, 4096)
+    for name in filter(None, buf.value.decode().split(",")):
+        ms, la, by = ctypes.c_double(), ctypes.c_uint64(), ctypes.c_double()
+        zkh.lib().zkh_prof_get(mctx.h, name.encode(), ctypes.byref(ms), ctypes.byref(la), ctypes.byref(by))
+        kern[name] = [ms.value, la.value, by.value]
+    zkh.lib().zkh_prof_enable(mctx.h, 0)
+    dom = max(kern, key=lambda n: kern[n][0]) if kern else None
+    dms, dla, dby = kern[dom] if kern else (1.0, 1, 0.0)
     achieved = dby / (dms / 1000.0) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
@@ -296,7 +325,8 @@ def main():
         others = [glu] + ropes
 
         def layer_step():
-            return list(pool.map(lambda j: j.run(), jobs + others))
+            futs = [pool.submit(j.run) for j in others]
+            return [mm_step()] + [f.result() for f in futs]
 
         lref = layer_step()
         seg = {}
@@ -305,12 +335,15 @@ def main():
             j.run()
             seg[type(j).__name__ + ("" if not hasattr(j, "logD") else ":2^%d" % j.logD)] = \
                 round((time.perf_counter() - t) * 1000.0, 2)
+        gc.collect()
+        gc.disable()
         torch.cuda.synchronize()
         ta = time.perf_counter()
         for _ in range(args.layer_steps):
             lout = layer_step()
         torch.cuda.synchronize()
         tb = time.perf_counter()
+        gc.enable()
         assert lout == lref, "non-deterministic layer output"
         layer = {"prove_s_per_layer": (tb - ta) / args.layer_steps,
                  "segments_isolated_ms": seg,

@@ -123,6 +123,27 @@ int zkh_mm_prove(zkh_ctx* ctx, uint8_t transcript[32], const zkh_tensor* X,
                  uint32_t* ev_out, uint32_t* claims_out, uint32_t* u_batch_out,
                  uint32_t* u_output_out, uint32_t* u_input_out);
 
+/* Several independent matmul sumchecks (e.g. the Q,K,V,O,gate,up,down matmuls of a layer,
+ * each with its own transcript) proven together: every device step is one launch for
+ * all jobs and each round costs one host synchronisation for the whole batch.  Each job
+ * has exactly the inputs, transcript effects and outputs of zkh_mm_prove; status holds
+ * its own return code, and the call returns the first non-zero one.  No counterpart in
+ * the reference, which runs one zkob_fc process per matmul. */
+typedef struct zkh_mm_job {
+    const zkh_tensor* X;
+    const zkh_tensor* W;
+    const zkh_tensor* Y;
+    uint32_t B, IN, OUT;
+    uint8_t* transcript; /* 32-byte state, updated in place */
+    uint32_t* ev_out;
+    uint32_t* claims_out;
+    uint32_t* u_batch_out;
+    uint32_t* u_output_out;
+    uint32_t* u_input_out;
+    int status;
+} zkh_mm_job;
+int zkh_mm_prove_batch(zkh_ctx* ctx, zkh_mm_job* jobs, uint32_t njobs);
+
 /* ---------------- logUp lookup (tlookup.cu, zkob_lookup.cuh, zkob_rescale.cu) ---------- */
 /* tLookupRange table (tlookup.cu:372-391): T[i] = low+i (i<len) else low+len-1, size N */
 int zkh_lu_range_table(zkh_ctx* ctx, int32_t low, uint32_t len, uint32_t N, zkh_tensor** out);

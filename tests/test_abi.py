@@ -56,6 +56,18 @@ def test_transcript_matches_oracle(zkh):
     assert bytes(a) == bytes(b)
 
 
+def test_transcript_long_absorbs(zkh):
+    """Many-block absorbs (the SHA-NI path where the CPU has it) against hashlib."""
+    rng = np.random.default_rng(5)
+    st = zkh.transcript("long")
+    ref = hashlib.sha256(b"long").digest()
+    for n in [0, 1, 55, 56, 63, 64, 65, 119, 120, 128, 1000, 4096 * 3 + 17]:
+        data = rng.integers(0, 256, size=n, dtype=np.uint8).tobytes()
+        zkh.absorb(st, "x" * (n % 7), data)
+        ref = hashlib.sha256(ref + struct.pack("<I", n % 7) + b"x" * (n % 7) + struct.pack("<Q", n) + data).digest()
+        assert bytes(st) == ref, n
+
+
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is present")
 def test_no_gpu_fails_loudly(zkh):
     h = ctypes.c_void_p()

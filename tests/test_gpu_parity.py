@@ -146,6 +146,45 @@ def test_mm_prove(zkh, ctx, shape, weights):
     assert bytes(st_g) == bytes(st_o)
 
 
+def test_mm_prove_batch(zkh, ctx):
+    """All MM_SHAPES proven in one batched call; each job equals its own oracle run."""
+    items, wants, sts = [], [], []
+    keep = []
+    for idx, shape in enumerate(MM_SHAPES):
+        B, IN, OUT = shape
+        X, W, Y = _mm_inputs(shape, 77 + idx)
+        st_g, st_o = seed_transcript(zkh, "batch:%d" % idx)
+        rc, want = C.mm_prove(st_o, X, W, Y, B, IN, OUT)
+        assert rc == 0
+        t = (ctx.from_i32(X), ctx.weights_i32(W, IN, OUT) if idx % 2 else ctx.from_i32(W), ctx.from_i64(Y))
+        keep.append(t)
+        items.append((st_g, t[0], t[1], t[2], B, IN, OUT))
+        wants.append(want)
+        sts.append((st_g, st_o))
+    outs, status = ctx.mm_prove_batch(items)
+    assert status == [0] * len(items)
+    for got, want, (st_g, st_o) in zip(outs, wants, sts):
+        for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+            assert fr_eq(got[key], want[key]), key
+        assert bytes(st_g) == bytes(st_o)
+
+
+def test_mm_batch_isolates_a_bad_job(zkh, ctx):
+    good = _mm_inputs((8, 16, 4), 5)
+    X, W, Y = _mm_inputs((8, 16, 4), 6)
+    Y = Y.copy()
+    Y[0, 0] += 1
+    ta = [ctx.from_i32(good[0]), ctx.from_i32(good[1]), ctx.from_i64(good[2])]
+    tb = [ctx.from_i32(X), ctx.from_i32(W), ctx.from_i64(Y)]
+    st_a, st_o = seed_transcript(zkh, "iso")
+    st_b = zkh.transcript("iso2")
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.mm_prove_batch([(st_a, *ta, 8, 16, 4), (st_b, *tb, 8, 16, 4)])
+    assert e.value.code == zkh.EROUND
+    rc, _ = C.mm_prove(st_o, *good, 8, 16, 4)
+    assert bytes(st_a) == bytes(st_o)  # the good job completed normally
+
+
 def test_mm_wrong_witness_rejected(zkh, ctx):
     X, W, Y = _mm_inputs((8, 16, 4), 5)
     Y = Y.copy()

@@ -20,6 +20,15 @@ KIND_FR, KIND_I32, KIND_I64 = 0, 1, 2
 _lib = None
 
 
+class MmJob(ctypes.Structure):
+    _fields_ = [("X", ctypes.c_void_p), ("W", ctypes.c_void_p), ("Y", ctypes.c_void_p),
+                ("B", ctypes.c_uint32), ("IN", ctypes.c_uint32), ("OUT", ctypes.c_uint32),
+                ("transcript", ctypes.c_void_p), ("ev_out", ctypes.c_void_p),
+                ("claims_out", ctypes.c_void_p), ("u_batch_out", ctypes.c_void_p),
+                ("u_output_out", ctypes.c_void_p), ("u_input_out", ctypes.c_void_p),
+                ("status", ctypes.c_int)]
+
+
 class ZkhError(RuntimeError):
     def __init__(self, code, msg):
         super().__init__("zkh error %d: %s" % (code, msg))
@@ -68,6 +77,7 @@ def lib():
         L.zkh_lu_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove_eq.argtypes = [vp, vp, vp, vp, u32, vp, vp, vp, vp, vp]
+        L.zkh_mm_prove_batch.argtypes = [vp, vp, u32]
         L.zkh_prof_enable.argtypes = [vp, ctypes.c_int]
         L.zkh_prof_get.argtypes = [vp, ctypes.c_char_p, vp, vp, vp]
         L.zkh_prof_names.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
@@ -245,6 +255,30 @@ class Context:
         self._chk(lib().zkh_mm_prove(self.h, _p(st), X.h, W.h, Y.h, B, IN, OUT, _p(ev), _p(cl),
                                      _p(ub), _p(uo), _p(ui)))
         return dict(ev=ev[:3 * L], claims=cl, u_batch=ub[:lb], u_output=uo[:lo], u_input=ui[:L])
+
+    def mm_prove_batch(self, items):
+        """items: list of (transcript, X, W, Y, B, IN, OUT); returns (outputs, statuses);
+        raises on any failing job (statuses still filled)."""
+        n = len(items)
+        arr = (MmJob * n)()
+        outs = []
+        for k, (st, X, W, Y, B, IN, OUT) in enumerate(items):
+            L, lb, lo = ceil_log2(IN), ceil_log2(B), ceil_log2(OUT)
+            o = dict(ev=np.zeros((3 * L + 1, 8), np.uint32), claims=np.zeros((3, 8), np.uint32),
+                     u_batch=np.zeros((lb + 1, 8), np.uint32), u_output=np.zeros((lo + 1, 8), np.uint32),
+                     u_input=np.zeros((L + 1, 8), np.uint32))
+            arr[k] = MmJob(X.h, W.h, Y.h, B, IN, OUT, st.ctypes.data, _p(o["ev"]), _p(o["claims"]),
+                           _p(o["u_batch"]), _p(o["u_output"]), _p(o["u_input"]), 0)
+            o["_sizes"] = (L, lb, lo)
+            outs.append(o)
+        rc = lib().zkh_mm_prove_batch(self.h, ctypes.cast(arr, ctypes.c_void_p), n)
+        status = [arr[k].status for k in range(n)]
+        for o in outs:
+            L, lb, lo = o.pop("_sizes")
+            o["ev"], o["u_batch"], o["u_output"], o["u_input"] = (o["ev"][:3 * L], o["u_batch"][:lb],
+                                                                  o["u_output"][:lo], o["u_input"][:L])
+        self._chk(rc)
+        return outs, status
 
     def range_table(self, low, length, N):
         return self._new(lib().zkh_lu_range_table, low, length, N)

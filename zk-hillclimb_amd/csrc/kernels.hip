@@ -70,7 +70,7 @@ uint32_t grid_for(uint32_t work_items, uint32_t per_block, uint32_t max_blocks) 
 
 // K field accumulators per thread -> one AoS partial per block (partial[blockIdx*K + k])
 template <int K>
-ZDEV void block_reduce_store(fr_t* acc, uint32_t* partial) {
+ZDEV void block_reduce_store_at(fr_t* acc, uint32_t* partial, uint32_t slot) {
     __shared__ fr_t red[NT / 64][K];
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
@@ -85,7 +85,45 @@ ZDEV void block_reduce_store(fr_t* acc, uint32_t* partial) {
         fr_t s = red[0][k];
 #pragma unroll
         for (int w = 1; w < NT / 64; w++) s = fr_add(s, red[w][k]);
-        st_aos(partial, blockIdx.x * K + k, s);
+        st_aos(partial, slot * K + k, s);
+    }
+}
+template <int K>
+ZDEV void block_reduce_store(fr_t* acc, uint32_t* partial) {
+    block_reduce_store_at<K>(acc, partial, blockIdx.x);
+}
+
+// Block partials -> job sums in pinned host memory -> completion flag (see Publish).
+// Every thread of the block must call it.  first/nblk: the job's block range.
+template <int K>
+ZDEV void reduce_publish(fr_t* acc, const Publish& P, uint32_t job, uint32_t first, uint32_t nblk,
+                         uint32_t local) {
+    __shared__ int is_last;
+    block_reduce_store_at<K>(acc, P.part, first + local);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        is_last = atomicAdd(&P.counter[job], 1u) == nblk - 1;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    fr_t s[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) s[k] = fr_zero();
+    for (uint32_t b = threadIdx.x; b < nblk; b += NT)
+#pragma unroll
+        for (int k = 0; k < K; k++) s[k] = fr_add(s[k], ld_aos(P.part, (first + b) * K + k));
+    block_reduce_store_at<K>(s, P.host_out, job);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence_system();
+        P.counter[job] = 0;
+        if (atomicAdd(&P.counter[P.njobs], 1u) == P.njobs - 1) {
+            P.counter[P.njobs] = 0;
+            __threadfence_system();
+            __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 
@@ -299,11 +337,11 @@ void launch_sum_chunks(hipStream_t s, const uint32_t* partial, uint32_t nch, uin
 // ------------------------------------------------------------------------------------
 __global__ __launch_bounds__(NT) void k_dot_planes(const uint4* alo, const uint4* ahi,
                                                    const uint4* blo, const uint4* bhi, uint32_t n,
-                                                   uint32_t* partial) {
+                                                   Publish pub) {
     fr_t acc[1] = {fr_zero()};
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT)
         acc[0] = fr_add(acc[0], mont_mul(ld_fr(alo, ahi, i), ld_fr(blo, bhi, i)));
-    block_reduce_store<1>(acc, partial);
+    reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 __global__ __launch_bounds__(NT) void k_dot_aos_planes(const uint32_t* __restrict__ a,
                                                        const uint4* blo, const uint4* bhi,
@@ -314,15 +352,15 @@ __global__ __launch_bounds__(NT) void k_dot_aos_planes(const uint32_t* __restric
     block_reduce_store<1>(acc, partial);
 }
 __global__ __launch_bounds__(NT) void k_sum_planes(const uint4* alo, const uint4* ahi, uint32_t n,
-                                                   uint32_t* partial) {
+                                                   Publish pub) {
     fr_t acc[1] = {fr_zero()};
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT)
         acc[0] = fr_add(acc[0], ld_fr(alo, ahi, i));
-    block_reduce_store<1>(acc, partial);
+    reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
-uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, uint32_t* partial) {
+uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub) {
     uint32_t g = grid_for(n, NT * 4, 1024);
-    k_dot_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n, partial);
+    k_dot_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n, pub);
     return g;
 }
 uint32_t launch_dot_aos_planes(hipStream_t s, const uint32_t* a, DevPlanes b, uint32_t n,
@@ -331,9 +369,9 @@ uint32_t launch_dot_aos_planes(hipStream_t s, const uint32_t* a, DevPlanes b, ui
     k_dot_aos_planes<<<g, NT, 0, s>>>(a, PL_LO(b), PL_HI(b), n, partial);
     return g;
 }
-uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, uint32_t* partial) {
+uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, Publish pub) {
     uint32_t g = grid_for(n, NT * 8, 1024);
-    k_sum_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), n, partial);
+    k_sum_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), n, pub);
     return g;
 }
 
@@ -467,12 +505,22 @@ uint32_t launch_zkip_round(hipStream_t s, Tab a, Tab b, uint32_t n, int fold,
 // ------------------------------------------------------------------------------------
 // logUp: multiplicities, mapping, batched inversion
 // ------------------------------------------------------------------------------------
-__global__ void k_lu_count_planes(const uint4* lo, const uint4* hi, uint32_t n, fr_t low,
-                                  uint32_t N, uint32_t* counts, uint32_t* bad) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        uint32_t idx = fr_sub(ld_fr(lo, hi, i), low).v[0];  // limb 0 (tlookup.cu:419)
-        if (idx < N) atomicAdd(&counts[idx], 1u);
-        else atomicOr(bad, 1u);
+// Histogram update with wave aggregation: the lanes holding the same index as the first
+// active lane add their count with one atomic (zero padding makes long runs of one index);
+// the others add individually.  Indices >= N raise *bad.  All lanes of the wave call it.
+ZDEV void hist_add(uint32_t idx, bool valid, uint32_t N, uint32_t* counts, uint32_t* bad) {
+    const bool in = valid && idx < N;
+    if (valid && idx >= N) atomicOr(bad, 1u);
+    const uint64_t act = __ballot(in);
+    if (!act) return;
+    const int leader = __ffsll((unsigned long long)act) - 1;
+    const uint32_t lidx = __shfl(idx, leader, 64);
+    const bool same = in && idx == lidx;
+    const uint64_t sm = __ballot(same);
+    if (same) {
+        if ((int)(threadIdx.x & 63) == leader) atomicAdd(&counts[lidx], (uint32_t)__popcll(sm));
+    } else if (in) {
+        atomicAdd(&counts[idx], 1u);
     }
 }
 // limb 0 of the field element (v - low) for int32 v, low
@@ -480,12 +528,21 @@ ZDEV uint32_t lu_index_i32(int32_t v, int32_t low) {
     int64_t d = (int64_t)v - low;
     return d >= 0 ? (uint32_t)d : (uint32_t)(1u - (uint32_t)(-d));
 }
+__global__ void k_lu_count_planes(const uint4* lo, const uint4* hi, uint32_t n, fr_t low,
+                                  uint32_t N, uint32_t* counts, uint32_t* bad) {
+    for (uint32_t base = blockIdx.x * blockDim.x; base < n; base += gridDim.x * blockDim.x) {
+        const uint32_t i = base + threadIdx.x;
+        uint32_t idx = 0;
+        if (i < n) idx = fr_sub(ld_fr(lo, hi, i), low).v[0];  // limb 0 (tlookup.cu:419)
+        hist_add(idx, i < n, N, counts, bad);
+    }
+}
 __global__ void k_lu_count_i32(const int32_t* __restrict__ S, uint32_t n, int32_t low, uint32_t N,
                                uint32_t* counts, uint32_t* bad) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        uint32_t idx = lu_index_i32(S[i], low);
-        if (idx < N) atomicAdd(&counts[idx], 1u);
-        else atomicOr(bad, 1u);
+    for (uint32_t base = blockIdx.x * blockDim.x; base < n; base += gridDim.x * blockDim.x) {
+        const uint32_t i = base + threadIdx.x;
+        const uint32_t idx = i < n ? lu_index_i32(S[i], low) : 0u;
+        hist_add(idx, i < n, N, counts, bad);
     }
 }
 __global__ void k_counts_to_planes(const uint32_t* __restrict__ counts, uint32_t N, uint4* lo,
@@ -626,7 +683,7 @@ ZDEV fr_t eq_hi(const EqDev& eq, uint32_t row) {
 // phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
 // acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
 __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, int fold, fr_t vm,
-                                                  fr_t beta, EqDev eq, uint32_t* partial) {
+                                                  fr_t beta, EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
     fr_t acc[5];
 #pragma unroll
@@ -653,11 +710,11 @@ __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n
             acc[4] = fr_add(acc[4], a1);
         }
     }
-    block_reduce_store<5>(acc, partial);
+    reduce_publish<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
-                          uint32_t* partial) {
+                          Publish partial) {
     uint32_t rows = ((n >> 1) + 1023) >> 10;
     uint32_t g = rows < 1024 ? rows : 1024;
     fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
@@ -671,7 +728,7 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
 // 6, 7: sum a0, sum a1; 8..10: sum m0*b0, m1*b1, dm*db (x 2^-256)
 __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m,
                                                   uint32_t n, int fold_as, int fold_btm, fr_t vm,
-                                                  fr_t beta, EqDev eq, uint32_t* partial) {
+                                                  fr_t beta, EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
     fr_t acc[11];
 #pragma unroll
@@ -717,11 +774,11 @@ __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, 
             acc[10] = fr_add(acc[10], mont_mul(fr_sub(m1, m0), db));
         }
     }
-    block_reduce_store<11>(acc, partial);
+    reduce_publish<11>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
-                          EqW eq, uint32_t* partial) {
+                          EqW eq, Publish partial) {
     uint32_t rows = ((n >> 1) + 1023) >> 10;
     uint32_t g = rows < 1024 ? rows : 1024;
     fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
@@ -735,7 +792,7 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
 // Hadamard sumcheck rounds (zkob_lookup.cuh:212-233 k_hp3_step + k_fr_fold, fused)
 // ------------------------------------------------------------------------------------
 __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, uint32_t n, int fold,
-                                                 fr_t vm, uint32_t* partial) {
+                                                 fr_t vm, Publish pub) {
     const uint32_t h = n >> 1;
     fr_t acc[4] = {fr_zero(), fr_zero(), fr_zero(), fr_zero()};
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
@@ -755,10 +812,10 @@ __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, u
             }
         }
     }
-    block_reduce_store<4>(acc, partial);
+    reduce_publish<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fold,
-                         const uint32_t* v_m_host, uint32_t* partial) {
+                         const uint32_t* v_m_host, Publish partial) {
     uint32_t g = grid_for(n >> 1, NT * 2, 1024);
     fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
     k_hp_round<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, partial);
@@ -766,7 +823,7 @@ uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fol
 }
 // eq-specialised: sums_t = sum_i eq(i, u[0..K)) S_t[i] U_t[i]  (x 2^-256)
 __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
-                                                    EqDev eq, uint32_t* partial) {
+                                                    EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
     fr_t acc[4] = {fr_zero(), fr_zero(), fr_zero(), fr_zero()};
     const uint32_t rows = (h + 1023) >> 10;
@@ -793,10 +850,10 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             }
         }
     }
-    block_reduce_store<4>(acc, partial);
+    reduce_publish<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, EqW eq, uint32_t* partial) {
+                            const uint32_t* v_m_host, EqW eq, Publish partial) {
     uint32_t rows = ((n >> 1) + 1023) >> 10;
     uint32_t g = rows < 1024 ? rows : 1024;
     fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
@@ -807,7 +864,7 @@ uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
 // sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n
 __global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* shi, const uint4* ulo,
                                                const uint4* uhi, int has_u, uint32_t n, EqDev eq,
-                                               uint32_t* partial) {
+                                               Publish pub) {
     fr_t acc[1] = {fr_zero()};
     const uint32_t rows = (n + 1023) >> 10;
     for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
@@ -821,16 +878,203 @@ __global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* sh
             acc[0] = fr_add(acc[0], ws);
         }
     }
-    block_reduce_store<1>(acc, partial);
+    reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
-                       uint32_t* partial) {
+                       Publish partial) {
     uint32_t rows = (n + 1023) >> 10;
     uint32_t g = rows < 1024 ? rows : 1024;
     EqDev e{eq.elo, eq.fac, eq.K};
     k_eq_sum<<<g, NT, 0, s>>>(PL_LO(S), PL_HI(S), U ? PL_LO(*U) : nullptr, U ? PL_HI(*U) : nullptr,
                               U ? 1 : 0, n, e, partial);
     return g;
+}
+
+
+// ------------------------------------------------------------------------------------
+// Batched (multi-job) kernels: one launch serves every independent sumcheck of a batch
+// (e.g. the 7 matmuls of a layer).  Blocks are assigned to jobs contiguously; each job's
+// descriptor holds its first block index.  Thread 0 locates the descriptor.
+// ------------------------------------------------------------------------------------
+template <typename D>
+ZDEV void find_desc(const D* __restrict__ d, uint32_t nd, D& out) {
+    __shared__ uint32_t sj;
+    if (threadIdx.x == 0) {
+        uint32_t j = 0;
+        while (j + 1 < nd && d[j + 1].blk_begin <= blockIdx.x) j++;
+        sj = j;
+    }
+    __syncthreads();
+    out = d[sj];
+}
+
+// eq tables in Montgomery form: E[b] = Tlo[b mod 2^klo] * Thi[b >> klo], the two small
+// factor-product tables built in LDS by separate threads (latency of ~8 products).
+__global__ __launch_bounds__(NT) void k_eq_mont_multi(const EqTabDesc* __restrict__ d, uint32_t nd) {
+    EqTabDesc q;
+    find_desc(d, nd, q);
+    __shared__ fr_t tlo[128], thi[128];
+    const uint32_t K = q.K;
+    const uint32_t klo = K < 7 ? K : 7, khi = K - klo;
+    const uint32_t t = threadIdx.x;
+    if (khi <= 7) {
+        if (t < (1u << klo)) {
+            fr_t e = one_m();
+            for (uint32_t i = 0; i < klo; i++) e = mont_mul(e, ld_aos(q.fac, 2 * i + ((t >> i) & 1)));
+            tlo[t] = e;
+        } else if (t >= 128 && t - 128 < (1u << khi)) {
+            fr_t e = one_m();
+            for (uint32_t i = 0; i < khi; i++)
+                e = mont_mul(e, ld_aos(q.fac, 2 * (klo + i) + (((t - 128) >> i) & 1)));
+            thi[t - 128] = e;
+        }
+    }
+    __syncthreads();
+    const uint32_t b = (blockIdx.x - q.blk_begin) * NT + t;
+    if (b >= q.n) return;
+    fr_t e;
+    if (khi <= 7) {
+        e = khi ? mont_mul(tlo[b & ((1u << klo) - 1)], thi[b >> klo]) : tlo[b];
+    } else {
+        e = eq_prod(q.fac, K, b);
+    }
+    if (q.plain) e = mont_mul(e, plain_one());
+    st_aos(q.out, b, e);
+}
+// out[b] = Tlo_m[b mod 2^klo] * Thi_p[b >> klo] (plain result), into planes
+__global__ void k_eq_outer(const uint32_t* __restrict__ tlo, const uint32_t* __restrict__ thi,
+                           uint32_t klo, uint32_t n, uint4* olo, uint4* ohi) {
+    for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < n; b += gridDim.x * blockDim.x)
+        st_fr(olo, ohi, b, mont_mul(ld_aos(tlo, b & ((1u << klo) - 1)), ld_aos(thi, b >> klo)));
+}
+void launch_eq_outer(hipStream_t s, const uint32_t* tlo_m, const uint32_t* thi_p, uint32_t klo,
+                     uint32_t n, DevPlanes out) {
+    k_eq_outer<<<grid_for(n, NT, 8192), NT, 0, s>>>(tlo_m, thi_p, klo, n, PL_LO(out), PL_HI(out));
+}
+void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, uint32_t nblocks) {
+    k_eq_mont_multi<<<nblocks, NT, 0, s>>>(d_dev, nd);
+}
+
+template <typename T, int NP>
+__global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict__ d, uint32_t nd) {
+    EqDotDesc q;
+    find_desc(d, nd, q);
+    const uint32_t ncb = (q.N + NT - 1) / NT;
+    const uint32_t local = blockIdx.x - q.blk_begin;
+    const uint32_t i = (local % ncb) * NT + threadIdx.x;
+    const uint32_t c = local / ncb;
+    const uint32_t k0 = c * q.kchunk;
+    const uint32_t k1 = min(q.K, k0 + q.kchunk);
+    uint64_t acc[NP][8];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[p][j] = 0;
+    const int64_t off = (int64_t)1 << q.bits;
+    const T* M = reinterpret_cast<const T*>(q.M);
+    if (i < q.N) {
+        const T* col = M + i;
+        for (uint32_t k = k0; k < k1; k++) {
+            const fr_t e = ld_aos(q.E, k);
+            const uint64_t w = (uint64_t)((int64_t)col[(size_t)k * q.N] + off);
+#pragma unroll
+            for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (20 * p)) & 0xFFFFFu, e);
+        }
+    }
+    fr_t r = fr_zero();
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        uint32_t tt[10];
+        cols_normalize(acc[p], tt);
+        fr_t f = redc_wide<10>(tt);
+        if (p > 0) f = mont_mul(f, piece_scale(p));
+        r = fr_add(r, f);
+    }
+    if (i < q.N) st_aos(q.partial, (size_t)c * q.N + i, r);
+}
+void launch_eqdot_multi(hipStream_t s, int is64, uint32_t np, const EqDotDesc* d_dev, uint32_t nd,
+                        uint32_t nblocks) {
+    if (!is64) {
+        if (np <= 1) k_eqdot_multi<int32_t, 1><<<nblocks, NT, 0, s>>>(d_dev, nd);
+        else k_eqdot_multi<int32_t, 2><<<nblocks, NT, 0, s>>>(d_dev, nd);
+    } else {
+        if (np <= 3) k_eqdot_multi<int64_t, 3><<<nblocks, NT, 0, s>>>(d_dev, nd);
+        else k_eqdot_multi<int64_t, 4><<<nblocks, NT, 0, s>>>(d_dev, nd);
+    }
+}
+
+// out[i] = sum_c partial[c*N+i] - corr (i < N; zero up to Npad), or, when E is set, the
+// block partial of sum_i E_m[i] * (sum_c partial[c*N+i] - corr) into dot[slot]
+__global__ __launch_bounds__(NT) void k_sum_chunks_multi(const SumChunksDesc* __restrict__ d, uint32_t nd) {
+    SumChunksDesc q;
+    find_desc(d, nd, q);
+    const uint32_t local = blockIdx.x - q.blk_begin;
+    const uint32_t i = local * NT + threadIdx.x;
+    fr_t s = fr_zero();
+    if (i < q.N) {
+        for (uint32_t c = 0; c < q.nch; c++) s = fr_add(s, ld_aos(q.partial, (size_t)c * q.N + i));
+        s = fr_sub(s, to_fr(q.corr.v));
+    }
+    if (q.E) {
+        fr_t acc[1] = {i < q.N ? mont_mul(ld_aos(q.E, i), s) : fr_zero()};
+        block_reduce_store_at<1>(acc, q.dot, local);
+    } else if (i < q.Npad) {
+        st_fr(reinterpret_cast<uint4*>(q.out_lo), reinterpret_cast<uint4*>(q.out_hi), i, s);
+    }
+}
+void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks) {
+    k_sum_chunks_multi<<<nblocks, NT, 0, s>>>(d_dev, nd);
+}
+
+// zkip rounds of several jobs in one launch: one pair per thread; fold of the previous
+// round fused in (in place); per job: sum a0b0, a1b1, da*db (x 2^-256) published.
+__global__ __launch_bounds__(NT) void k_zkip_round_multi(ZkipBatch bt, Publish pub) {
+    __shared__ uint32_t sj;
+    if (threadIdx.x == 0) {
+        uint32_t j = 0;
+        while (j + 1 < bt.nd && bt.d[j + 1].blk_begin <= blockIdx.x) j++;
+        sj = j;
+    }
+    __syncthreads();
+    const uint32_t job = sj;
+    const ZkipDesc& q = bt.d[job];
+    const uint32_t local = blockIdx.x - q.blk_begin;
+    const uint32_t h = q.n >> 1;
+    const uint32_t nblk = (h + NT - 1) / NT;
+    const uint32_t i = local * NT + threadIdx.x;
+    fr_t acc[3] = {fr_zero(), fr_zero(), fr_zero()};
+    if (i < h) {
+        const TabDev a{reinterpret_cast<const uint4*>(q.a_lo), reinterpret_cast<const uint4*>(q.a_hi),
+                       reinterpret_cast<uint4*>(q.a_lo), reinterpret_cast<uint4*>(q.a_hi)};
+        const TabDev b{reinterpret_cast<const uint4*>(q.b_lo), reinterpret_cast<const uint4*>(q.b_hi),
+                       reinterpret_cast<uint4*>(q.b_lo), reinterpret_cast<uint4*>(q.b_hi)};
+        fr_t a0, a1, b0, b1;
+        const fr_t vm = to_fr(q.vm.v);
+        load_pair(a, i, h, q.n, q.fold, vm, a0, a1);
+        load_pair(b, i, h, q.n, q.fold, vm, b0, b1);
+        acc[0] = mont_mul(a0, b0);
+        acc[1] = mont_mul(a1, b1);
+        acc[2] = mont_mul(fr_sub(a1, a0), fr_sub(b1, b0));
+    }
+    reduce_publish<3>(acc, pub, job, q.blk_begin, nblk, local);
+}
+void launch_zkip_round_multi(hipStream_t s, const ZkipBatch& b, uint32_t nblocks, Publish pub) {
+    k_zkip_round_multi<<<nblocks, NT, 0, s>>>(b, pub);
+}
+// final binds of several 2-entry tables (t[0] += v*(t[1]-t[0]) when fold is set) and the
+// terminal values a[0], b[0] written to partial[0..1] (AoS)
+__global__ void k_fold_last_multi(ZkipBatch bt) {
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= 2 * bt.nd) return;
+    const ZkipDesc& q = bt.d[j >> 1];
+    uint4* lo = reinterpret_cast<uint4*>((j & 1) ? q.b_lo : q.a_lo);
+    uint4* hi = reinterpret_cast<uint4*>((j & 1) ? q.b_hi : q.a_hi);
+    const fr_t x = q.fold ? fold_at(lo, hi, 0, 1, to_fr(q.vm.v)) : ld_fr(lo, hi, 0);
+    st_fr(lo, hi, 0, x);
+    st_aos(q.partial, j & 1, x);
+}
+void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b) {
+    k_fold_last_multi<<<1, 64, 0, s>>>(b);
 }
 
 }  // namespace zkh

@@ -17,6 +17,18 @@ struct DevPlanes {
     uint32_t* hi() const { return base + 4 * (size_t)cap; }
 };
 
+// Round completion without a host synchronisation: every block writes its K partial
+// sums to `part` (device); the last block of a job (device-scope counter) reduces them and
+// writes the job's K sums to host_out (coherent pinned host memory); the last job to finish
+// stores `seq` into *host_flag (system-scope release), which the host spins on.
+struct Publish {
+    uint32_t* part;       // device, [total blocks][K] AoS
+    uint32_t* counter;    // device, njobs + 1 words, zero between launches
+    uint32_t* host_out;   // pinned, [njobs][K] AoS
+    uint32_t* host_flag;  // pinned
+    uint32_t seq, njobs;
+};
+
 // A table in a fused fold+evaluate round: read from src; folded entries go to dst (which
 // may be src itself).  The first fold of a caller-owned table targets a scratch copy.
 struct Tab {
@@ -63,11 +75,11 @@ void launch_sum_chunks(hipStream_t s, const uint32_t* partial, uint32_t nch, uin
 
 // ---- dot products / sums (block partials, AoS, summed on the host) ----
 // partial[b] = sum montmul(a_i, b_i) over the block's range (carries 2^-256)
-uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, uint32_t* partial);
+uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub);
 // partial[b] = sum montmul(Eaos_i, b_i)
 uint32_t launch_dot_aos_planes(hipStream_t s, const uint32_t* a, DevPlanes b, uint32_t n,
                                uint32_t* partial);
-uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, uint32_t* partial);
+uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, Publish pub);
 
 // ---- generic MLE pieces ----
 // out[o*W + w] = sum_{c < C} montmul(E_m[c], t[(o*C + c)*W + w])  (t as FR planes)
@@ -112,24 +124,73 @@ void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 // phase-1 round over A, S (size n): sums e*a0*s0, e*a1*s1, e*da*ds (x 2^-256), a0, a1
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
-                          uint32_t* partial);
+                          Publish pub);
 // phase-2 round over A, S, B, T, m: 11 sums (see kernels.hip)
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
                           int fold_as, int fold_btm,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
-                          uint32_t* partial);
+                          Publish pub);
 
 // ---- Hadamard ----
 // generic: sums_t = sum E_t*S_t*U_t, t = 0..3 (x 2^-512)
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
-                         int fold, const uint32_t* v_m_host, uint32_t* partial);
+                         int fold, const uint32_t* v_m_host, Publish pub);
 // eq-specialised: sums_t = sum eq(i,u_)*S_t*U_t, t = 0..3 (x 2^-256)
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, EqW eq, uint32_t* partial);
+                            const uint32_t* v_m_host, EqW eq, Publish pub);
 // sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
-                       uint32_t* partial);
+                       Publish pub);
 
 uint32_t grid_for(uint32_t work_items, uint32_t per_block, uint32_t max_blocks);
 
+
+// ---- batched (multi-job) launches: descriptors live in device memory; each job's
+// blocks are contiguous from blk_begin ----
+struct fr_arg {
+    uint32_t v[8];
+};
+struct EqTabDesc {  // eq table over K variables, n entries, AoS out (Montgomery unless plain)
+    const uint32_t* fac;
+    uint32_t* out;
+    uint32_t K, n, blk_begin, plain;
+};
+// out[b] = tlo_m[b mod 2^klo] * thi_p[b >> klo]: the plain eq table from two small ones
+void launch_eq_outer(hipStream_t s, const uint32_t* tlo_m, const uint32_t* thi_p, uint32_t klo,
+                     uint32_t n, DevPlanes out);
+struct EqDotDesc {  // partial[c*N+i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) e_k
+    const void* M;
+    const uint32_t* E;
+    uint32_t* partial;
+    uint32_t K, N, kchunk, bits, blk_begin, pad_;
+};
+struct SumChunksDesc {
+    const uint32_t* partial;
+    uint32_t* out_lo;  // planes output (when E == null)
+    uint32_t* out_hi;
+    const uint32_t* E;  // Montgomery eq table: dot mode (block partials into dot)
+    uint32_t* dot;
+    uint32_t nch, N, Npad, blk_begin;
+    fr_arg corr;
+};
+struct ZkipDesc {
+    uint32_t* a_lo;
+    uint32_t* a_hi;
+    uint32_t* b_lo;
+    uint32_t* b_hi;
+    uint32_t* partial;  // 3 Fr per block
+    uint32_t n, fold, blk_begin, pad_;
+    fr_arg vm;  // challenge of the fold, Montgomery form
+};
+void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, uint32_t nblocks);
+void launch_eqdot_multi(hipStream_t s, int is64, uint32_t np, const EqDotDesc* d_dev, uint32_t nd,
+                        uint32_t nblocks);
+void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks);
+#define ZKH_MAX_BATCH 32
+struct ZkipBatch {  // passed by value as the kernel argument (<= 2.1 KB)
+    ZkipDesc d[ZKH_MAX_BATCH];
+    uint32_t nd;
+};
+void launch_zkip_round_multi(hipStream_t s, const ZkipBatch& b, uint32_t nblocks, Publish pub);
+void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
 }  // namespace zkh

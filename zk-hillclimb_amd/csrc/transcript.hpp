@@ -10,6 +10,10 @@
 #pragma once
 #include <stdint.h>
 #include <string.h>
+#if defined(__x86_64__) && !defined(__HIP_DEVICE_COMPILE__)
+#include <cpuid.h>
+#include <immintrin.h>
+#endif
 
 #include "fr_host.hpp"
 
@@ -68,6 +72,7 @@ struct Sha256 {
         h[0] += a; h[1] += b; h[2] += c; h[3] += d;
         h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
     }
+    void compress(const uint8_t* p);
     void update(const void* data, size_t n) {
         const uint8_t* p = (const uint8_t*)data;
         len += n;
@@ -79,7 +84,7 @@ struct Sha256 {
             p += take;
             n -= take;
             if (blen == 64) {
-                block(buf);
+                compress(buf);
                 blen = 0;
             }
         }
@@ -100,6 +105,70 @@ struct Sha256 {
         }
     }
 };
+
+#if defined(__x86_64__) && !defined(__HIP_DEVICE_COMPILE__)
+// SHA-256 compression with the x86 SHA extensions (Intel, "Intel SHA Extensions", 2013):
+// sha256rnds2 performs two rounds on the (ABEF, CDGH) state halves; sha256msg1/msg2 form the
+// message schedule four words at a time.  Used when CPUID reports SHA; same digest as block().
+__attribute__((target("sha,sse4.1,ssse3"))) inline void sha256_block_ni(uint32_t h[8], const uint8_t* p) {
+    alignas(16) static const uint32_t K[64] = {
+        0x428a2f98, 0x71374491, 0xb5c0fbcf, 0xe9b5dba5, 0x3956c25b, 0x59f111f1, 0x923f82a4, 0xab1c5ed5,
+        0xd807aa98, 0x12835b01, 0x243185be, 0x550c7dc3, 0x72be5d74, 0x80deb1fe, 0x9bdc06a7, 0xc19bf174,
+        0xe49b69c1, 0xefbe4786, 0x0fc19dc6, 0x240ca1cc, 0x2de92c6f, 0x4a7484aa, 0x5cb0a9dc, 0x76f988da,
+        0x983e5152, 0xa831c66d, 0xb00327c8, 0xbf597fc7, 0xc6e00bf3, 0xd5a79147, 0x06ca6351, 0x14292967,
+        0x27b70a85, 0x2e1b2138, 0x4d2c6dfc, 0x53380d13, 0x650a7354, 0x766a0abb, 0x81c2c92e, 0x92722c85,
+        0xa2bfe8a1, 0xa81a664b, 0xc24b8b70, 0xc76c51a3, 0xd192e819, 0xd6990624, 0xf40e3585, 0x106aa070,
+        0x19a4c116, 0x1e376c08, 0x2748774c, 0x34b0bcb5, 0x391c0cb3, 0x4ed8aa4a, 0x5b9cca4f, 0x682e6ff3,
+        0x748f82ee, 0x78a5636f, 0x84c87814, 0x8cc70208, 0x90befffa, 0xa4506ceb, 0xbef9a3f7, 0xc67178f2};
+    const __m128i bswap = _mm_set_epi64x(0x0c0d0e0f08090a0bULL, 0x0405060700010203ULL);
+    __m128i tmp = _mm_loadu_si128((const __m128i*)&h[0]);  // A B C D (low to high)
+    __m128i s1 = _mm_loadu_si128((const __m128i*)&h[4]);   // E F G H
+    tmp = _mm_shuffle_epi32(tmp, 0xB1);                     // B A D C
+    s1 = _mm_shuffle_epi32(s1, 0x1B);                       // H G F E
+    __m128i s0 = _mm_alignr_epi8(tmp, s1, 8);               // F E B A = ABEF (high to low)
+    s1 = _mm_blend_epi16(s1, tmp, 0xF0);                    // D C G H = CDGH
+    const __m128i abef = s0, cdgh = s1;
+    __m128i w[4];
+    for (int i = 0; i < 4; i++) w[i] = _mm_shuffle_epi8(_mm_loadu_si128((const __m128i*)(p + 16 * i)), bswap);
+    for (int g = 0; g < 16; g++) {
+        __m128i wg;
+        if (g < 4) {
+            wg = w[g];
+        } else {
+            // W[t..t+3] from W[t-16..t-13], W[t-12..t-9], W[t-7..t-4] and W[t-4..t-1]
+            __m128i x = _mm_sha256msg1_epu32(w[g & 3], w[(g + 1) & 3]);
+            x = _mm_add_epi32(x, _mm_alignr_epi8(w[(g + 3) & 3], w[(g + 2) & 3], 4));
+            wg = _mm_sha256msg2_epu32(x, w[(g + 3) & 3]);
+            w[g & 3] = wg;
+        }
+        __m128i m = _mm_add_epi32(wg, _mm_load_si128((const __m128i*)&K[4 * g]));
+        s1 = _mm_sha256rnds2_epu32(s1, s0, m);
+        s0 = _mm_sha256rnds2_epu32(s0, s1, _mm_shuffle_epi32(m, 0x0E));
+    }
+    s0 = _mm_add_epi32(s0, abef);
+    s1 = _mm_add_epi32(s1, cdgh);
+    tmp = _mm_shuffle_epi32(s0, 0x1B);
+    s1 = _mm_shuffle_epi32(s1, 0xB1);
+    s0 = _mm_blend_epi16(tmp, s1, 0xF0);  // A B C D (low to high)
+    s1 = _mm_alignr_epi8(s1, tmp, 8);     // E F G H
+    _mm_storeu_si128((__m128i*)&h[0], s0);
+    _mm_storeu_si128((__m128i*)&h[4], s1);
+}
+inline bool cpu_has_sha() {
+    static const bool has = [] {
+        unsigned a, b, c, d;
+        if (!__get_cpuid_count(7, 0, &a, &b, &c, &d)) return false;
+        return ((b >> 29) & 1) != 0;
+    }();
+    return has;
+}
+inline void Sha256::compress(const uint8_t* p) {
+    if (cpu_has_sha()) sha256_block_ni(h, p);
+    else block(p);
+}
+#else
+inline void Sha256::compress(const uint8_t* p) { block(p); }
+#endif
 
 inline void tr_init(uint8_t st[32], const char* seed, size_t n) {
     Sha256 c;

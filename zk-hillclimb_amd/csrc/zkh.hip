@@ -13,6 +13,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <string>
 #include <vector>
 
@@ -34,6 +35,12 @@ struct zkh_ctx {
         size_t bytes = 0;
     };
     std::vector<Slot> slots;
+    // round completion (Publish): coherent pinned job sums + flag, device partials/counters
+    uint32_t* pub_host = nullptr;  // [ZKH_MAX_BATCH][11] Fr sums, then the flag word
+    uint32_t* pub_part = nullptr;  // device partial sums (pub_part_cap Fr)
+    size_t pub_part_cap = (size_t)4096 * 11;
+    uint32_t* pub_cnt = nullptr;   // device [ZKH_MAX_BATCH + 1]
+    uint32_t pub_seq = 0;
     // pinned ring for small host->device uploads: a region is reused only after a later
     // stream synchronisation, which every API call performs before returning
     uint8_t* ring = nullptr;
@@ -85,6 +92,24 @@ struct ProfScope {
         c->pending.push_back(zkh_ctx::Pending{rec, a, b, bytes});
     }
 };
+// fold finished event pairs into the records, leaving unfinished ones pending
+static void prof_resolve_ready(zkh_ctx* c) {
+    size_t keep = 0;
+    for (size_t i = 0; i < c->pending.size(); i++) {
+        auto& p = c->pending[i];
+        float ms = 0;
+        if (hipEventQuery(p.b) == hipSuccess && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            c->recs[p.rec].ms += ms;
+            c->recs[p.rec].bytes += p.bytes;
+            c->recs[p.rec].launches++;
+            c->pool.push_back(p.a);
+            c->pool.push_back(p.b);
+        } else {
+            c->pending[keep++] = p;
+        }
+    }
+    c->pending.resize(keep);
+}
 // fold finished event pairs into the records (call after a stream synchronisation)
 static void prof_resolve(zkh_ctx* c) {
     for (auto& p : c->pending) {
@@ -146,6 +171,7 @@ enum {
     SL_TMP4,
     SL_TMP5,
     SL_TMP6,
+    SL_DESC,
     SL_COUNT
 };
 static void* scratch(zkh_ctx* c, int slot, size_t bytes, int* rc) {
@@ -181,20 +207,52 @@ static int ensure_pinned(zkh_ctx* c, size_t bytes) {
     c->pinned_bytes = want;
     return 0;
 }
-// copy K*nb AoS partials back and return the K column sums
-static int fetch_sums(zkh_ctx* c, const uint32_t* dpart, uint32_t nb, int K, Fr* out) {
-    size_t bytes = (size_t)nb * K * 32;
-    int rc = ensure_pinned(c, bytes);
-    if (rc) return rc;
-    HIPCHK(c, hipMemcpyAsync(c->pinned, dpart, bytes, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    c->ring_off = 0;
-    if (c->prof) prof_resolve(c);
-    for (int k = 0; k < K; k++) out[k] = kZero;
-    for (uint32_t b = 0; b < nb; b++)
-        for (int k = 0; k < K; k++) out[k] = fr_add(out[k], fr_load(c->pinned + ((size_t)b * K + k) * 8));
+// ---- host-side round trace (ZKH_TRACE=1): per-round launch / wait / host times ----
+static bool trace_on() {
+    static const bool on = getenv("ZKH_TRACE") && atoi(getenv("ZKH_TRACE")) > 0;
+    return on;
+}
+static double now_us() {
+    return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// ---- round completion without stream synchronisation ----
+static uint32_t* pub_flag(zkh_ctx* c) { return c->pub_host + ZKH_MAX_BATCH * 11 * 8; }
+static Publish make_pub(zkh_ctx* c, uint32_t njobs) {
+    Publish p;
+    p.part = c->pub_part;
+    p.counter = c->pub_cnt;
+    p.host_out = c->pub_host;
+    p.host_flag = pub_flag(c);
+    p.seq = ++c->pub_seq;
+    p.njobs = njobs;
+    return p;
+}
+// spin until the launch carrying `seq` has published (the kernel never waits on the host,
+// so this cannot hang the GPU; a stream error or a finished stream without the flag fails)
+static int wait_pub(zkh_ctx* c, uint32_t seq) {
+    uint32_t* f = pub_flag(c);
+    for (uint64_t spins = 1;; spins++) {
+        if (__atomic_load_n(f, __ATOMIC_ACQUIRE) == seq) break;
+        if ((spins & 0x3FFF) == 0) {
+            hipError_t e = hipStreamQuery(c->stream);
+            if (e == hipSuccess) {
+                if (__atomic_load_n(f, __ATOMIC_ACQUIRE) == seq) break;
+                return fail(c, ZKH_EDEV, "round kernel finished without publishing its sums");
+            }
+            if (e != hipErrorNotReady) return fail(c, ZKH_EDEV, "round kernel: %s", hipGetErrorString(e));
+        }
+        __builtin_ia32_pause();
+    }
+    c->ring_off = 0;  // everything queued before the publishing kernel has completed
+    if (c->prof) prof_resolve_ready(c);
     return 0;
 }
+// the K published sums of job j
+static void pub_read(zkh_ctx* c, uint32_t j, int K, Fr* out) {
+    for (int k = 0; k < K; k++) out[k] = fr_load(c->pub_host + ((size_t)j * K + k) * 8);
+}
+
 // small host -> device upload through the pinned ring (asynchronous; ordered on the stream)
 static int upload(zkh_ctx* c, void* dst, const void* src, size_t bytes) {
     size_t need = (bytes + 255) & ~(size_t)255;
@@ -340,6 +398,15 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
         return ZKH_EDEV;
     }
     c->slots.resize(SL_COUNT);
+    if (hipHostMalloc((void**)&c->pub_host, (ZKH_MAX_BATCH * 11 * 8 + 64) * 4, hipHostMallocCoherent) != hipSuccess ||
+        hipMalloc((void**)&c->pub_part, (size_t)4096 * 11 * 32) != hipSuccess ||
+        hipMalloc((void**)&c->pub_cnt, (ZKH_MAX_BATCH + 1) * 4) != hipSuccess ||
+        hipMemset(c->pub_cnt, 0, (ZKH_MAX_BATCH + 1) * 4) != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return ZKH_EDEV;
+    }
+    memset(c->pub_host, 0, (ZKH_MAX_BATCH * 11 * 8 + 64) * 4);
     if (ensure_pinned(c, (size_t)1 << 20)) {
         (void)hipStreamDestroy(c->stream);
         delete c;
@@ -356,6 +423,9 @@ extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
         if (s.p) (void)hipFree(s.p);
     if (c->pinned) (void)hipHostFree(c->pinned);
     if (c->ring) (void)hipHostFree(c->ring);
+    if (c->pub_host) (void)hipHostFree(c->pub_host);
+    if (c->pub_part) (void)hipFree(c->pub_part);
+    if (c->pub_cnt) (void)hipFree(c->pub_cnt);
     for (auto& p : c->pending) {
         c->pool.push_back(p.a);
         c->pool.push_back(p.b);
@@ -628,16 +698,17 @@ static int eq_weighted_sum(zkh_ctx* c, DevPlanes S, const DevPlanes* U, uint32_t
     int rc = 0;
     EqState st;
     if ((rc = eq_setup(c, u, st, SL_FAC, SL_ELO))) return rc;
-    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 32, &rc);
-    if (rc) return rc;
     uint32_t K = (uint32_t)u.size();
     uint32_t nb;
     {
         ProfScope ps(c, "eq_sum", (double)n * (U ? 64 : 32));
-        nb = launch_eq_sum(c->stream, S, U, n, EqW{st.elo_d, st.fac_d, K}, part);
+        Publish pb = make_pub(c, 1);
+        nb = launch_eq_sum(c->stream, S, U, n, EqW{st.elo_d, st.fac_d, K}, pb);
+        (void)nb;
+        if ((rc = wait_pub(c, pb.seq))) return rc;
     }
     Fr s;
-    if ((rc = fetch_sums(c, part, nb, 1, &s))) return rc;
+    pub_read(c, 0, 1, &s);
     s = fr_mul(s, eq_corr(st, K));
     if (U) s = fix1(s);
     *out = s;
@@ -649,12 +720,12 @@ extern "C" int zkh_sum(zkh_ctx* c, const zkh_tensor* t, uint32_t out[8]) {
     int rc = 0;
     DevPlanes p;
     if ((rc = as_planes(c, t, SL_TMP0, &p))) return rc;
-    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 32, &rc);
-    if (rc) return rc;
     Fr s = kZero;
     if (t->n) {
-        uint32_t nb = launch_sum_planes(c->stream, p, t->n, part);
-        if ((rc = fetch_sums(c, part, nb, 1, &s))) return rc;
+        Publish pb = make_pub(c, 1);
+        launch_sum_planes(c->stream, p, t->n, pb);
+        if ((rc = wait_pub(c, pb.seq))) return rc;
+        pub_read(c, 0, 1, &s);
     }
     fr_store(s, out);
     return ZKH_OK;
@@ -779,9 +850,31 @@ extern "C" int zkh_eq_table(zkh_ctx* c, const uint32_t* u, uint32_t k, zkh_tenso
     uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
     if (rc) return rc;
     if (k && (rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
+    // E = Tlo (first min(k,10) variables, Montgomery) (x) Thi (the rest, plain)
+    const uint32_t klo = k < 10 ? k : 10, khi = k - klo;
+    uint32_t* tlo = (uint32_t*)scratch(c, SL_EB, ((size_t)1 << klo) * 32, &rc);
+    if (rc) return rc;
+    uint32_t* thi = (uint32_t*)scratch(c, SL_EO, ((size_t)1 << khi) * 32, &rc);
+    if (rc) return rc;
+    EqTabDesc d[2] = {};
+    d[0].fac = fac_d;
+    d[0].out = tlo;
+    d[0].K = klo;
+    d[0].n = 1u << klo;
+    d[0].blk_begin = 0;
+    d[1].fac = fac_d + 16 * (size_t)klo;
+    d[1].out = thi;
+    d[1].K = khi;
+    d[1].n = 1u << khi;
+    d[1].blk_begin = (d[0].n + 255) / 256;
+    d[1].plain = 1;
+    EqTabDesc* d_dev = (EqTabDesc*)scratch(c, SL_DESC, sizeof(d), &rc);
+    if (rc) return rc;
+    if ((rc = upload(c, d_dev, d, sizeof(d)))) return rc;
     zkh_tensor* t;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, 1u << k, &t))) return rc;
-    launch_eq_planes(c->stream, fac_d, k, 1u << k, t->planes());
+    launch_eq_mont_multi(c->stream, d_dev, 2, d[1].blk_begin + (d[1].n + 255) / 256);
+    launch_eq_outer(c->stream, tlo, thi, klo, 1u << k, t->planes());
     HIPCHK(c, hipStreamSynchronize(c->stream));
     *out = t;
     return ZKH_OK;
@@ -874,139 +967,405 @@ extern "C" int zkh_pad(zkh_ctx* c, const zkh_tensor* t, const uint32_t* shape, u
 // ---------------------------------------------------------------------------------------
 // matmul sumcheck (zkob_fc.cu:259-440)
 // ---------------------------------------------------------------------------------------
-// out[i] (i < N) = sum_k e_k * M[k*N + i] for an integer matrix M (K x N), e = eq table E
-// (Montgomery AoS, K entries) with prefix sum SE; out zero-padded to Npad entries.
-static int eq_reduce_int(zkh_ctx* c, const void* M, int kind, uint32_t bits, uint32_t K, uint32_t N,
-                         const uint32_t* E, const Fr& SE, uint32_t Npad, DevPlanes out) {
+// Batched matmul sumchecks: all jobs share each launch (eq tables, eq-weighted
+// reductions, every round) and one host synchronisation per round; transcripts stay
+// independent, one per job.
+static uint32_t np_for(uint32_t bits) { return (bits + 1 + 19) / 20; }
+
+static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj);
+extern "C" int zkh_mm_prove_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
+    if (!c || (!jobs && nj)) return fail(c, ZKH_EARG, "null argument");
     int rc = 0;
-    uint32_t nch = std::max<uint32_t>(1, (131072 + N - 1) / N);
-    uint32_t kchunk = (K + nch - 1) / nch;
-    kchunk = std::min<uint32_t>(std::max<uint32_t>(kchunk, 16), 2048);
-    nch = (K + kchunk - 1) / kchunk;
-    uint32_t* part = (uint32_t*)scratch(c, SL_TMP6, (size_t)nch * N * 32, &rc);
-    if (rc) return rc;
-    {
-        ProfScope ps(c, "eqdot", (double)K * N * (kind == ZKH_KIND_I32 ? 4 : 8) + (double)nch * N * 32);
-        if (kind == ZKH_KIND_I32) launch_eqdot_i32(c->stream, (const int32_t*)M, K, N, E, kchunk, bits, part);
-        else launch_eqdot_i64(c->stream, (const int64_t*)M, K, N, E, kchunk, bits, part);
+    for (uint32_t at = 0; at < nj; at += ZKH_MAX_BATCH) {
+        int r = mm_batch(c, jobs + at, std::min<uint32_t>(ZKH_MAX_BATCH, nj - at));
+        if (r && !rc) rc = r;
     }
-    // correction 2^bits * sum_{k<K} e_k
-    Fr two_b = kOne;
-    for (uint32_t b = 0; b < bits; b++) two_b = fr_add(two_b, two_b);
-    Fr corr = fr_mul(two_b, SE);
-    uint32_t corr_l[8];
-    fr_store(corr, corr_l);
-    ProfScope ps(c, "sum_chunks", (double)nch * N * 32 + (double)Npad * 32);
-    launch_sum_chunks(c->stream, part, nch, N, Npad, corr_l, out);
-    return 0;
+    return rc;
+}
+static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
+    int first_rc = 0;
+    for (uint32_t j = 0; j < nj; j++) {
+        zkh_mm_job& J = jobs[j];
+        J.status = ZKH_OK;
+        const zkh_tensor *X = J.X, *W = J.W, *Y = J.Y;
+        const char* why = nullptr;
+        if (!J.transcript || !X || !W || !Y) why = "null argument";
+        else if (!J.B || !J.IN || !J.OUT) why = "zero dimension";
+        else if (X->kind != ZKH_KIND_I32 || W->kind != ZKH_KIND_I32 || Y->kind == ZKH_KIND_FR)
+            why = "mm_prove takes int32 X, W and int32/int64 Y";
+        else if ((uint64_t)X->n != (uint64_t)J.B * J.IN || (uint64_t)W->n != (uint64_t)J.IN * J.OUT ||
+                 (uint64_t)Y->n != (uint64_t)J.B * J.OUT)
+            why = "input dims";
+        else if (W->weights && (W->w_in != J.IN || W->w_out != J.OUT)) why = "weights dims";
+        else if (Y->bits > 62 || J.IN > (1u << 24) || J.B > (1u << 24) || J.OUT > (1u << 24))
+            why = "integer range / size";
+        if (why) {
+            J.status = ZKH_EARG;
+            if (!first_rc) first_rc = fail(c, ZKH_EARG, "job %u: %s", j, why);
+        }
+    }
+    if (first_rc || !nj) return first_rc;
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    struct Job {
+        uint32_t lb, lo, L, INp;
+        std::vector<Fr> ub, uo, xs;
+        Fr claim, cur;
+        size_t eb_off, eo_off, fac_b, fac_o;  // element offsets
+        size_t red_off;                       // planes offset (entries) of a; b follows
+        uint32_t dot_blocks, dot_slot;        // claim partials in pinned memory
+        bool live;
+    };
+    std::vector<Job> J(nj);
+    size_t eq_total = 0, fac_total = 0, red_total = 0, wt_total = 0;
+    for (uint32_t j = 0; j < nj; j++) {
+        Job& q = J[j];
+        const zkh_mm_job& in = jobs[j];
+        q.lb = ceil_log2(in.B);
+        q.lo = ceil_log2(in.OUT);
+        q.L = ceil_log2(in.IN);
+        q.INp = 1u << q.L;
+        q.ub.resize(q.lb);
+        q.uo.resize(q.lo);
+        for (auto& x : q.ub) x = tr_challenge(in.transcript);
+        for (auto& x : q.uo) x = tr_challenge(in.transcript);
+        q.fac_b = fac_total;
+        fac_total += 2 * (size_t)q.lb;
+        q.fac_o = fac_total;
+        fac_total += 2 * (size_t)q.lo;
+        q.eb_off = eq_total;
+        eq_total += in.B;
+        q.eo_off = eq_total;
+        eq_total += in.OUT;
+        q.red_off = red_total;
+        red_total += 2 * (size_t)q.INp;
+        if (!in.W->weights) wt_total += in.W->n;
+        q.live = true;
+    }
+    // device areas
+    std::vector<uint32_t> fac(std::max<size_t>(fac_total, 1) * 8, 0);
+    for (uint32_t j = 0; j < nj; j++) {
+        std::vector<uint32_t> fb, fo;
+        make_fac(J[j].ub, 0, fb);
+        make_fac(J[j].uo, 0, fo);
+        std::copy(fb.begin(), fb.end(), fac.begin() + J[j].fac_b * 8);
+        std::copy(fo.begin(), fo.end(), fac.begin() + J[j].fac_o * 8);
+    }
+    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, fac.size() * 4, &rc);
+    if (rc) return rc;
+    uint32_t* eq_d = (uint32_t*)scratch(c, SL_EB, eq_total * 32, &rc);
+    if (rc) return rc;
+    DevPlanes red = scratch_planes(c, SL_TMP0, (uint32_t)red_total, &rc);
+    if (rc) return rc;
+    int32_t* wt_d = wt_total ? (int32_t*)scratch(c, SL_TMP5, wt_total * 4, &rc) : nullptr;
+    if (rc) return rc;
+    if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
+
+    // 1) eq tables (Montgomery AoS)
+    std::vector<EqTabDesc> eqd;
+    uint32_t eq_blocks = 0;
+    for (uint32_t j = 0; j < nj; j++) {
+        const Job& q = J[j];
+        for (int t = 0; t < 2; t++) {
+            EqTabDesc d{};
+            d.fac = fac_d + 8 * (t ? q.fac_o : q.fac_b);
+            d.out = eq_d + 8 * (t ? q.eo_off : q.eb_off);
+            d.K = t ? q.lo : q.lb;
+            d.n = t ? jobs[j].OUT : jobs[j].B;
+            d.blk_begin = eq_blocks;
+            eq_blocks += (d.n + 255) / 256;
+            eqd.push_back(d);
+        }
+    }
+    // 2) eq-weighted reductions: Y by eb (then dotted with eo -> claim), X by eb, W^T by eo
+    struct Red {
+        EqDotDesc d;
+        int is64;
+        uint32_t np, nch, Npad, job, what;  // what: 0 Y, 1 X, 2 W
+        Fr corr;
+    };
+    std::vector<Red> reds;
+    size_t part_total = 0;
+    size_t wt_off = 0;
+    for (uint32_t j = 0; j < nj; j++) {
+        const zkh_mm_job& in = jobs[j];
+        const Job& q = J[j];
+        Fr SEb = eq_prefix_sum(q.ub, in.B), SEo = eq_prefix_sum(q.uo, in.OUT);
+        const int32_t* WT = (const int32_t*)in.W->d;
+        if (!in.W->weights) {
+            launch_transpose_i32(c->stream, (const int32_t*)in.W->d, in.IN, in.OUT, wt_d + wt_off);
+            WT = wt_d + wt_off;
+            wt_off += in.W->n;
+        }
+        for (uint32_t what = 0; what < 3; what++) {
+            Red r{};
+            const void* M = what == 0 ? in.Y->d : what == 1 ? in.X->d : (const void*)WT;
+            uint32_t K = what == 2 ? in.OUT : in.B;
+            uint32_t N = what == 0 ? in.OUT : in.IN;
+            uint32_t bits = what == 0 ? in.Y->bits : what == 1 ? in.X->bits : in.W->bits;
+            uint32_t nch = std::max<uint32_t>(1, (131072 + N - 1) / N);
+            uint32_t kchunk = std::min<uint32_t>(std::max<uint32_t>((K + nch - 1) / nch, 16), 2048);
+            nch = (K + kchunk - 1) / kchunk;
+            r.d.M = M;
+            r.d.E = eq_d + 8 * (what == 2 ? q.eo_off : q.eb_off);
+            r.d.K = K;
+            r.d.N = N;
+            r.d.kchunk = kchunk;
+            r.d.bits = bits;
+            r.is64 = what == 0 && in.Y->kind == ZKH_KIND_I64;
+            r.np = np_for(bits);
+            r.nch = nch;
+            r.Npad = what == 0 ? N : q.INp;
+            r.job = j;
+            r.what = what;
+            Fr two_b = kOne;
+            for (uint32_t b = 0; b < bits; b++) two_b = fr_add(two_b, two_b);
+            r.corr = fr_mul(two_b, what == 2 ? SEo : SEb);
+            r.d.partial = (uint32_t*)(uintptr_t)(part_total * 32);  // offset, fixed below
+            part_total += (size_t)nch * N;
+            reds.push_back(r);
+        }
+    }
+    uint32_t* part_d = (uint32_t*)scratch(c, SL_TMP6, part_total * 32, &rc);
+    if (rc) return rc;
+    for (auto& r : reds) r.d.partial = part_d + (uintptr_t)r.d.partial / 4;
+    // group the reductions by (int width, pieces) -> one launch per group
+    std::vector<EqDotDesc> dots;
+    struct Grp {
+        int is64;
+        uint32_t np, first, count, blocks;
+    };
+    std::vector<Grp> groups;
+    for (int is64 = 0; is64 < 2; is64++)
+        for (uint32_t np = 1; np <= 4; np++) {
+            Grp g{is64, np, (uint32_t)dots.size(), 0, 0};
+            for (auto& r : reds) {
+                uint32_t gnp = r.is64 ? (r.np <= 3 ? 3 : 4) : (r.np <= 1 ? 1 : 2);
+                if (r.is64 != is64 || gnp != np) continue;
+                EqDotDesc d = r.d;
+                d.blk_begin = g.blocks;
+                g.blocks += ((r.d.N + 255) / 256) * r.nch;
+                dots.push_back(d);
+                g.count++;
+            }
+            if (g.count) groups.push_back(g);
+        }
+    // 3) chunk sums (X, W -> planes; Y -> dot with eo into pinned claim partials)
+    std::vector<SumChunksDesc> sums;
+    uint32_t sum_blocks = 0, claim_slots = 0;
+    for (auto& r : reds) {
+        SumChunksDesc d{};
+        const Job& q = J[r.job];
+        d.partial = r.d.partial;
+        d.nch = r.nch;
+        d.N = r.d.N;
+        d.Npad = r.Npad;
+        d.blk_begin = sum_blocks;
+        fr_store(r.corr, d.corr.v);
+        uint32_t nb = (r.Npad + 255) / 256;
+        if (r.what == 0) {
+            d.E = eq_d + 8 * q.eo_off;
+            d.dot = (uint32_t*)(uintptr_t)claim_slots;  // slot index, fixed below
+            J[r.job].dot_slot = claim_slots;
+            J[r.job].dot_blocks = nb;
+            claim_slots += nb;
+        } else {
+            size_t off = q.red_off + (r.what == 1 ? 0 : q.INp);
+            d.out_lo = red.lo() + 4 * off;
+            d.out_hi = red.hi() + 4 * off;
+        }
+        sum_blocks += nb;
+        sums.push_back(d);
+    }
+    // pinned host layout: claim partials | round partials (per job, max blocks) | terminals
+    uint32_t max_rb = 0;
+    for (auto& q : J) max_rb = std::max(max_rb, (q.INp / 2 + 255) / 256);
+    size_t pin_claim = 0, pin_round = (size_t)claim_slots * 8,
+           pin_term = pin_round + (size_t)nj * std::max<uint32_t>(max_rb, 1) * 24;
+    if ((rc = ensure_pinned(c, (pin_term + (size_t)nj * 16) * 4))) return rc;
+    uint32_t* pin = c->pinned;
+    for (auto& d : sums)
+        if (d.E) d.dot = pin + pin_claim + 8 * (uintptr_t)d.dot;
+    // descriptors -> device (one area, one upload)
+    size_t desc_bytes = eqd.size() * sizeof(EqTabDesc) + dots.size() * sizeof(EqDotDesc) +
+                        sums.size() * sizeof(SumChunksDesc) + 256;
+    uint8_t* desc_d = (uint8_t*)scratch(c, SL_DESC, desc_bytes * 2, &rc);
+    if (rc) return rc;
+    std::vector<uint8_t> blob(desc_bytes, 0);
+    size_t o_eq = 0, o_dot = o_eq + eqd.size() * sizeof(EqTabDesc);
+    size_t o_sum = o_dot + dots.size() * sizeof(EqDotDesc);
+    size_t o_zk = (o_sum + sums.size() * sizeof(SumChunksDesc) + 63) & ~(size_t)63;
+    memcpy(blob.data() + o_eq, eqd.data(), eqd.size() * sizeof(EqTabDesc));
+    memcpy(blob.data() + o_dot, dots.data(), dots.size() * sizeof(EqDotDesc));
+    memcpy(blob.data() + o_sum, sums.data(), sums.size() * sizeof(SumChunksDesc));
+    if ((rc = upload(c, desc_d, blob.data(), o_zk))) return rc;
+    {
+        ProfScope ps(c, "eq_tables", (double)eq_total * 32);
+        launch_eq_mont_multi(c->stream, (const EqTabDesc*)(desc_d + o_eq), (uint32_t)eqd.size(), eq_blocks);
+    }
+    double red_bytes = 0;
+    for (auto& r : reds)
+        red_bytes += (double)r.d.K * r.d.N * (r.is64 ? 8 : 4) + (double)r.nch * r.d.N * 32;
+    {
+        ProfScope ps(c, "eqdot", red_bytes);
+        for (auto& g : groups)
+            launch_eqdot_multi(c->stream, g.is64, g.np, (const EqDotDesc*)(desc_d + o_dot) + g.first, g.count,
+                               g.blocks);
+    }
+    {
+        double b = 0;
+        for (auto& r : reds) b += (double)r.nch * r.d.N * 32 + (double)r.Npad * 32;
+        ProfScope ps(c, "sum_chunks", b);
+        launch_sum_chunks_multi(c->stream, (const SumChunksDesc*)(desc_d + o_sum), (uint32_t)sums.size(),
+                                sum_blocks);
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    c->ring_off = 0;
+    if (c->prof) prof_resolve(c);
+    for (uint32_t j = 0; j < nj; j++) {
+        Job& q = J[j];
+        Fr s = kZero;
+        for (uint32_t b = 0; b < q.dot_blocks; b++) s = fr_add(s, fr_load(pin + pin_claim + 8 * (size_t)(q.dot_slot + b)));
+        q.claim = q.cur = s;
+        tr_absorb_fr(jobs[j].transcript, "claim", s);
+        q.xs.resize(q.L);
+    }
+    // 4) rounds (zkob_fc.cu:294-332): one launch and one synchronisation per round for all jobs
+    const Fr two = fr_u64(2), four = fr_u64(4);
+    uint32_t maxL = 0;
+    for (auto& q : J) maxL = std::max(maxL, q.L);
+    std::vector<ZkipDesc> zk(nj);
+    for (uint32_t j = 0; j < nj; j++) {
+        zk[j] = ZkipDesc{};
+        zk[j].a_lo = red.lo() + 4 * J[j].red_off;
+        zk[j].a_hi = red.hi() + 4 * J[j].red_off;
+        zk[j].b_lo = red.lo() + 4 * (J[j].red_off + J[j].INp);
+        zk[j].b_hi = red.hi() + 4 * (J[j].red_off + J[j].INp);
+    }
+    double tr_t0 = now_us();
+    for (uint32_t r = 0; r < maxL; r++) {
+        double t_a = now_us();
+        std::vector<ZkipDesc> act;
+        std::vector<uint32_t> who;
+        uint32_t blocks = 0;
+        double bytes = 0;
+        for (uint32_t j = 0; j < nj; j++) {
+            Job& q = J[j];
+            if (!q.live || r >= q.L) continue;
+            ZkipDesc d = zk[j];
+            d.n = q.INp >> r;
+            d.fold = r > 0;
+            d.blk_begin = blocks;
+            blocks += (d.n / 2 + 255) / 256;
+            bytes += (r > 0 ? 3.0 * d.n : (double)d.n) * 64;
+            act.push_back(d);
+            who.push_back(j);
+        }
+        if (act.empty()) break;
+        if ((size_t)blocks * 3 > c->pub_part_cap) {
+            HIPCHK(c, hipStreamSynchronize(c->stream));
+            (void)hipFree(c->pub_part);
+            c->pub_part = nullptr;
+            HIPCHK(c, hipMalloc((void**)&c->pub_part, (size_t)blocks * 3 * 32));
+            c->pub_part_cap = (size_t)blocks * 3;
+        }
+        ZkipBatch bt;
+        memset(&bt, 0, sizeof(bt));
+        for (size_t a = 0; a < act.size(); a++) bt.d[a] = act[a];
+        bt.nd = (uint32_t)act.size();
+        Publish pb = make_pub(c, bt.nd);
+        double t_b = now_us();
+        {
+            ProfScope ps(c, "zkip_round", bytes);
+            launch_zkip_round_multi(c->stream, bt, blocks, pb);
+        }
+        double t_c = now_us();
+        if ((rc = wait_pub(c, pb.seq))) return rc;
+        double t_d = now_us();
+        if (trace_on())
+            fprintf(stderr, "[zkh] mm round %u: prep %.1f launch %.1f wait %.1f us (since start %.1f)\n", r,
+                    t_b - t_a, t_c - t_b, t_d - t_c, t_d - tr_t0);
+        for (size_t a = 0; a < act.size(); a++) {
+            uint32_t j = who[a];
+            Job& q = J[j];
+            Fr s3[3];
+            pub_read(c, (uint32_t)a, 3, s3);
+            Fr c0 = fix1(s3[0]), q1 = fix1(s3[1]), c2 = fix1(s3[2]);
+            Fr c1 = fr_sub(fr_sub(q1, c0), c2);
+            Fr p[3] = {c0, q1, fr_add(fr_add(c0, fr_mul(two, c1)), fr_mul(four, c2))};
+            if (!fr_eq(q.cur, fr_add(p[0], p[1]))) {
+                q.live = false;
+                jobs[j].status = ZKH_EROUND;
+                if (!first_rc)
+                    first_rc = fail(c, ZKH_EROUND,
+                                    "job %u: prover sumcheck round inconsistency (witness bug) at round %u", j, r);
+                continue;
+            }
+            uint8_t* tr = jobs[j].transcript;
+            tr_absorb_fr(tr, "p0", p[0]);
+            tr_absorb_fr(tr, "p1", p[1]);
+            tr_absorb_fr(tr, "p2", p[2]);
+            Fr x = tr_challenge(tr);
+            q.xs[r] = x;
+            if (jobs[j].ev_out)
+                for (int k = 0; k < 3; k++) fr_store(p[k], jobs[j].ev_out + 8 * (3 * r + k));
+            q.cur = fr_lagrange3(p, x);
+            fr_store(fr_to_mont(x), zk[j].vm.v);
+        }
+    }
+    // 5) final binds and terminals (written to pinned memory by the kernel)
+    std::vector<ZkipDesc> fin;
+    std::vector<uint32_t> fwho;
+    for (uint32_t j = 0; j < nj; j++) {
+        if (!J[j].live) continue;
+        ZkipDesc d = zk[j];
+        d.fold = J[j].L > 0;
+        d.partial = pin + pin_term + (size_t)j * 16;
+        fin.push_back(d);
+        fwho.push_back(j);
+    }
+    if (!fin.empty()) {
+        ZkipBatch bt;
+        memset(&bt, 0, sizeof(bt));
+        for (size_t a = 0; a < fin.size(); a++) bt.d[a] = fin[a];
+        bt.nd = (uint32_t)fin.size();
+        launch_fold_last_multi(c->stream, bt);
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        c->ring_off = 0;
+        if (c->prof) prof_resolve(c);
+    }
+    for (uint32_t j : fwho) {
+        Job& q = J[j];
+        zkh_mm_job& in = jobs[j];
+        Fr cx = fr_load(pin + pin_term + (size_t)j * 16), cw = fr_load(pin + pin_term + (size_t)j * 16 + 8);
+        if (!fr_eq(q.cur, fr_mul(cx, cw))) {
+            in.status = ZKH_EROUND;
+            if (!first_rc) first_rc = fail(c, ZKH_EROUND, "job %u: terminal product mismatch (witness bug)", j);
+            continue;
+        }
+        tr_absorb_fr(in.transcript, "claim_X", cx);
+        tr_absorb_fr(in.transcript, "claim_W", cw);
+        if (in.claims_out) {
+            fr_store(q.claim, in.claims_out);
+            fr_store(cx, in.claims_out + 8);
+            fr_store(cw, in.claims_out + 16);
+        }
+        if (in.u_batch_out)
+            for (uint32_t i = 0; i < q.lb; i++) fr_store(q.ub[i], in.u_batch_out + 8 * i);
+        if (in.u_output_out)
+            for (uint32_t i = 0; i < q.lo; i++) fr_store(q.uo[i], in.u_output_out + 8 * i);
+        if (in.u_input_out)
+            for (uint32_t i = 0; i < q.L; i++) fr_store(q.xs[q.L - 1 - i], in.u_input_out + 8 * i);
+    }
+    return first_rc;
 }
 
 extern "C" int zkh_mm_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* X, const zkh_tensor* W,
                             const zkh_tensor* Y, uint32_t B, uint32_t IN, uint32_t OUT,
                             uint32_t* ev_out, uint32_t* claims_out, uint32_t* ub_out,
                             uint32_t* uo_out, uint32_t* ui_out) {
-    if (!c || !tr || !X || !W || !Y) return fail(c, ZKH_EARG, "null argument");
-    if (!B || !IN || !OUT) return fail(c, ZKH_EARG, "zero dimension");
-    if (X->kind != ZKH_KIND_I32 || W->kind != ZKH_KIND_I32 || Y->kind == ZKH_KIND_FR)
-        return fail(c, ZKH_EARG, "mm_prove takes int32 X, W and int32/int64 Y");
-    if ((uint64_t)X->n != (uint64_t)B * IN || (uint64_t)W->n != (uint64_t)IN * OUT ||
-        (uint64_t)Y->n != (uint64_t)B * OUT)
-        return fail(c, ZKH_EARG, "input dims");
-    if (W->weights && (W->w_in != IN || W->w_out != OUT)) return fail(c, ZKH_EARG, "weights dims");
-    if (X->bits > 40 || W->bits > 40 || Y->bits > 62) return fail(c, ZKH_EARG, "integer range");
-    HIPCHK(c, hipSetDevice(c->device));
-    const uint32_t lb = ceil_log2(B), lo = ceil_log2(OUT), L = ceil_log2(IN);
-    const uint32_t INp = 1u << L;
-    int rc = 0;
-    std::vector<Fr> ub(lb), uo(lo);
-    for (auto& x : ub) x = tr_challenge(tr);
-    for (auto& x : uo) x = tr_challenge(tr);
-
-    uint32_t *Eb, *Eo;
-    if ((rc = eq_table_mont(c, ub, B, SL_EB, &Eb))) return rc;
-    if ((rc = eq_table_mont(c, uo, OUT, SL_EO, &Eo))) return rc;
-    Fr SEb = eq_prefix_sum(ub, B), SEo = eq_prefix_sum(uo, OUT);
-
-    // Yred[o] = sum_b eb[b] Y[b,o]; claim = sum_o eo[o] Yred[o]
-    DevPlanes yred = scratch_planes(c, SL_TMP2, OUT, &rc);
-    if (rc) return rc;
-    if ((rc = eq_reduce_int(c, Y->d, Y->kind, Y->bits, B, OUT, Eb, SEb, OUT, yred))) return rc;
-    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 11 * 32, &rc);
-    if (rc) return rc;
-    uint32_t nbc = launch_dot_aos_planes(c->stream, Eo, yred, OUT, part);
-    Fr claim;
-    if ((rc = fetch_sums(c, part, nbc, 1, &claim))) return rc;
-    tr_absorb_fr(tr, "claim", claim);
-
-    // a = X_red (IN, padded to INp), b = W_red
-    DevPlanes a = scratch_planes(c, SL_TMP0, INp, &rc);
-    if (rc) return rc;
-    DevPlanes b = scratch_planes(c, SL_TMP1, INp, &rc);
-    if (rc) return rc;
-    if ((rc = eq_reduce_int(c, X->d, ZKH_KIND_I32, X->bits, B, IN, Eb, SEb, INp, a))) return rc;
-    const int32_t* WT = (const int32_t*)W->d;
-    if (!W->weights) {
-        int32_t* t = (int32_t*)scratch(c, SL_TMP5, (size_t)W->n * 4, &rc);
-        if (rc) return rc;
-        launch_transpose_i32(c->stream, (const int32_t*)W->d, IN, OUT, t);
-        WT = t;
-    }
-    if ((rc = eq_reduce_int(c, WT, ZKH_KIND_I32, W->bits, OUT, IN, Eo, SEo, INp, b))) return rc;
-
-    // rounds (zkob_fc.cu:294-332)
-    Fr cur = claim, two = fr_u64(2), four = fr_u64(4);
-    std::vector<Fr> xs(L);
-    uint32_t vm[8] = {0};
-    for (uint32_t r = 0; r < L; r++) {
-        uint32_t n = INp >> r;
-        uint32_t nb;
-        {
-            ProfScope ps(c, "zkip_round", (r > 0 ? 2.0 * n + n : (double)n) * 2 * 32);
-            nb = launch_zkip_round(c->stream, Tab{a, a}, Tab{b, b}, n, r > 0, vm, part);
-        }
-        Fr s[3];
-        if ((rc = fetch_sums(c, part, nb, 3, s))) return rc;
-        Fr c0 = fix1(s[0]), q1 = fix1(s[1]), c2 = fix1(s[2]);
-        Fr c1 = fr_sub(fr_sub(q1, c0), c2);
-        Fr p[3] = {c0, q1, fr_add(fr_add(c0, fr_mul(two, c1)), fr_mul(four, c2))};
-        if (!fr_eq(cur, fr_add(p[0], p[1])))
-            return fail(c, ZKH_EROUND, "prover sumcheck round inconsistency (witness bug) at round %u", r);
-        tr_absorb_fr(tr, "p0", p[0]);
-        tr_absorb_fr(tr, "p1", p[1]);
-        tr_absorb_fr(tr, "p2", p[2]);
-        Fr x = tr_challenge(tr);
-        xs[r] = x;
-        if (ev_out)
-            for (int j = 0; j < 3; j++) fr_store(p[j], ev_out + 8 * (3 * r + j));
-        cur = fr_lagrange3(p, x);
-        fr_store(fr_to_mont(x), vm);
-    }
-    if (L > 0) {
-        launch_fold(c->stream, Tab{a, a}, 1, vm);
-        launch_fold(c->stream, Tab{b, b}, 1, vm);
-    }
-    uint32_t fin[2][8];
-    HIPCHK(c, hipMemcpyAsync(fin[0], a.lo(), 16, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipMemcpyAsync(fin[0] + 4, a.hi(), 16, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipMemcpyAsync(fin[1], b.lo(), 16, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipMemcpyAsync(fin[1] + 4, b.hi(), 16, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    Fr cx = fr_load(fin[0]), cw = fr_load(fin[1]);
-    if (!fr_eq(cur, fr_mul(cx, cw))) return fail(c, ZKH_EROUND, "terminal product mismatch (witness bug)");
-    tr_absorb_fr(tr, "claim_X", cx);
-    tr_absorb_fr(tr, "claim_W", cw);
-    if (claims_out) {
-        fr_store(claim, claims_out);
-        fr_store(cx, claims_out + 8);
-        fr_store(cw, claims_out + 16);
-    }
-    if (ub_out)
-        for (uint32_t i = 0; i < lb; i++) fr_store(ub[i], ub_out + 8 * i);
-    if (uo_out)
-        for (uint32_t i = 0; i < lo; i++) fr_store(uo[i], uo_out + 8 * i);
-    if (ui_out)
-        for (uint32_t i = 0; i < L; i++) fr_store(xs[L - 1 - i], ui_out + 8 * i);
-    return ZKH_OK;
+    zkh_mm_job j{X, W, Y, B, IN, OUT, tr, ev_out, claims_out, ub_out, uo_out, ui_out, 0};
+    return zkh_mm_prove_batch(c, &j, 1);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1193,13 +1552,13 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
     if (rc) return rc;
     if ((rc = batch_inverse(c, Tc, N, beta, Bw))) return rc;
 
-    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 11 * 32, &rc);
-    if (rc) return rc;
     // C = alpha^2 - sum Bv*m (zkob_rescale.cu:136)
     Fr bm;
     {
-        uint32_t nb = launch_dot_planes(c->stream, Bw, mc, N, part);
-        if ((rc = fetch_sums(c, part, nb, 1, &bm))) return rc;
+        Publish pb = make_pub(c, 1);
+        launch_dot_planes(c->stream, Bw, mc, N, pb);
+        if ((rc = wait_pub(c, pb.seq))) return rc;
+        pub_read(c, 0, 1, &bm);
         bm = fix1(bm);
     }
     Fr alpha_sq = fr_mul(alpha, alpha);
@@ -1225,18 +1584,18 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
         Fr coef[4];
         if (n > N) {  // phase 1
             Tab ta{a_src, Aw}, ts{s_src, Sw};
-            uint32_t nb;
+            Publish pb = make_pub(c, 1);
             {
                 ProfScope ps(c, "lu_phase1", (as_pending ? 3.0 * n : (double)n) * 2 * 32);
-                nb = launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l,
-                                      EqW{eq.elo_d, eq.fac_d, K}, part);
+                launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l, EqW{eq.elo_d, eq.fac_d, K}, pb);
             }
             if (as_pending) {
                 a_src = Aw;
                 s_src = Sw;
             }
             Fr s[5];
-            if ((rc = fetch_sums(c, part, nb, 5, s))) return rc;
+            if ((rc = wait_pub(c, pb.seq))) return rc;
+            pub_read(c, 0, 5, s);
             Fr q0 = fr_mul(fix1(s[0]), corr), q1 = fr_mul(fix1(s[1]), corr), q2 = fr_mul(fix1(s[2]), corr);
             Fr qc1 = fr_sub(fr_sub(q1, q0), q2);
             Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
@@ -1248,12 +1607,12 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
             as_pending = true;
         } else {  // phase 2
             Tab ta{a_src, Aw}, ts{s_src, Sw}, tb{b_src, Bw}, tt{t_src, Tw}, tm{m_src, mw};
-            uint32_t nb;
+            Publish pb = make_pub(c, 1);
             {
                 ProfScope ps(c, "lu_phase2",
                              ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
-                nb = launch_lu_phase2(c->stream, ta, ts, tb, tt, tm, n, as_pending, btm_pending,
-                                      vm, beta_l, EqW{eq.elo_d, eq.fac_d, K}, part);
+                launch_lu_phase2(c->stream, ta, ts, tb, tt, tm, n, as_pending, btm_pending, vm, beta_l,
+                                 EqW{eq.elo_d, eq.fac_d, K}, pb);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -1265,7 +1624,8 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
                 m_src = mw;
             }
             Fr s[11];
-            if ((rc = fetch_sums(c, part, nb, 11, s))) return rc;
+            if ((rc = wait_pub(c, pb.seq))) return rc;
+            pub_read(c, 0, 11, s);
             Fr qa0 = fr_mul(fix1(s[0]), corr), qa1 = fr_mul(fix1(s[1]), corr), qa2 = fr_mul(fix1(s[2]), corr);
             Fr qb0 = fr_mul(fix1(s[3]), corr), qb1 = fr_mul(fix1(s[4]), corr), qb2 = fr_mul(fix1(s[5]), corr);
             Fr coefBT = fr_mul(inv_ratio, alpha_sq);
@@ -1372,8 +1732,6 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     if (rc) return rc;
     Uw = U->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP2, n / 2 + 1, &rc) : Uc;
     if (rc) return rc;
-    uint32_t* part = (uint32_t*)scratch(c, SL_PARTIAL, 1024 * 11 * 32, &rc);
-    if (rc) return rc;
     EqState eq;
     if (ueq && (rc = eq_setup(c, *ueq, eq, SL_FAC, SL_ELO))) return rc;
     Fr claim = fr_load(claim_l), cE = kOne;
@@ -1385,26 +1743,27 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         const int fold = r > 0;
         Fr e[4];
         if (!ueq) {
-            uint32_t nb;
+            Publish pb = make_pub(c, 1);
             {
                 ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
-                nb = launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz,
-                                     fold, vm, part);
+                launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, pb);
             }
             Fr s[4];
-            if ((rc = fetch_sums(c, part, nb, 4, s))) return rc;
+            if ((rc = wait_pub(c, pb.seq))) return rc;
+            pub_read(c, 0, 4, s);
             for (int t = 0; t < 4; t++) e[t] = fix2(s[t]);
         } else {
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
-            uint32_t nb;
+            Publish pb = make_pub(c, 1);
             {
                 ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
-                nb = launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm,
-                                        EqW{eq.elo_d, eq.fac_d, K}, part);
+                launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm,
+                                   EqW{eq.elo_d, eq.fac_d, K}, pb);
             }
             Fr s[4];
-            if ((rc = fetch_sums(c, part, nb, 4, s))) return rc;
+            if ((rc = wait_pub(c, pb.seq))) return rc;
+            pub_read(c, 0, 4, s);
             Fr f = fr_mul(cE, eq_corr(eq, K));
             for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(fix1(s[t]), f), fr_eq2(ul, fr_u64(t)));
         }
