@@ -1,11 +1,12 @@
 // fr_dev.hpp -- BLS12-381 scalar-field arithmetic for gfx950 (CDNA4) integer VALU.
 //
 // Elements are 8 x 32-bit limbs, little-endian, canonical in [0, r).  The Montgomery
-// product uses the CIOS method (Koc, Acar, Kaliski, "Analyzing and comparing Montgomery
-// multiplication algorithms", 1996) with R = 2^256, so mont_mul(a, b) = a*b*2^-256 mod r,
-// the same value as the reference's blstrs__scalar__Scalar_mul (bls12-381.cu:462-531).
-// Each 32x32+64 step is one v_mad_u64_u32; carries travel in the upper half of the 64-bit
-// accumulator.  Since -r^-1 mod 2^32 = 0xffffffff, the reduction multiplier is -t0.
+// product (R = 2^256, so mont_mul(a, b) = a*b*2^-256 mod r) is product scanning with the
+// reduction interleaved per column (Koc, Acar, Kaliski, "Analyzing and comparing Montgomery
+// multiplication algorithms", 1996), generated straight-line by gen_mont_mul.py: each of
+// the 120 32x32 products is one v_mad_u64_u32 whose carry-out feeds a v_addc_co_u32 into
+// a 96-bit column sum.  Since -r^-1 mod 2^32 = 0xffffffff, the reduction multiplier of a
+// column is minus its low word.
 //
 // Tables in HBM use a structure-of-limb-quads layout: limbs 0-3 of element i in plane 0
 // at lo[i] (uint4), limbs 4-7 in plane 1 at hi[i], so every wave load reads 1 KiB
@@ -99,38 +100,38 @@ ZDEV fr_t fr_sub(const fr_t& a, const fr_t& b) {
     return d;
 }
 
-// CIOS Montgomery product a*b*2^-256 mod r, canonical output for canonical inputs.
-ZDEV fr_t mont_mul(const fr_t& a, const fr_t& b) {
-    uint32_t t[9];
-#pragma unroll
-    for (int j = 0; j < 9; j++) t[j] = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        uint64_t c = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            c = (uint64_t)a.v[j] * b.v[i] + t[j] + (c >> 32);
-            t[j] = (uint32_t)c;
-        }
-        uint64_t s = (uint64_t)t[8] + (c >> 32);
-        t[8] = (uint32_t)s;
-        uint32_t t9 = (uint32_t)(s >> 32);
-        uint32_t m = 0u - t[0];
-        c = (uint64_t)m * ZKH_P0 + t[0];
-#pragma unroll
-        for (int j = 1; j < 8; j++) {
-            c = (uint64_t)m * fr_p(j) + t[j] + (c >> 32);
-            t[j - 1] = (uint32_t)c;
-        }
-        s = (uint64_t)t[8] + (c >> 32);
-        t[7] = (uint32_t)s;
-        t[8] = t9 + (uint32_t)(s >> 32);
-    }
-    fr_t r;
-#pragma unroll
-    for (int j = 0; j < 8; j++) r.v[j] = t[j];
-    return fr_reduce_once(r, t[8]);
+// 96-bit column accumulation: (lo64, top) += x*y with v_mad_u64_u32's carry-out feeding
+// v_addc_co_u32.  A VALU-written SGPR needs one wait state before a VALU reads it as a
+// carry, so paired forms interleave two independent chains and single forms use s_nop.
+ZDEV void mac1_v(uint64_t& lo, uint32_t& top, uint32_t x, uint32_t y) {
+    uint64_t c;
+    asm("v_mad_u64_u32 %0, %2, %3, %4, %0\n\ts_nop 0\n\tv_addc_co_u32 %1, %2, 0, %1, %2"
+        : "+v"(lo), "+v"(top), "=&s"(c) : "v"(x), "v"(y));
 }
+ZDEV void mac1_s(uint64_t& lo, uint32_t& top, uint32_t x, uint32_t y) {
+    uint64_t c;
+    asm("v_mad_u64_u32 %0, %2, %3, %4, %0\n\ts_nop 0\n\tv_addc_co_u32 %1, %2, 0, %1, %2"
+        : "+v"(lo), "+v"(top), "=&s"(c) : "v"(x), "s"(y));
+}
+#define ZKH_MAC2(NAME, C1, C2)                                                                  \
+    ZDEV void NAME(uint64_t& lo0, uint32_t& top0, uint32_t x0, uint32_t y0, uint64_t& lo1,       \
+                   uint32_t& top1, uint32_t x1, uint32_t y1) {                                  \
+        uint64_t c0, c1;                                                                        \
+        asm("v_mad_u64_u32 %0, %2, %6, %7, %0\n\t"                                              \
+            "v_mad_u64_u32 %3, %5, %8, %9, %3\n\t"                                              \
+            "v_addc_co_u32 %1, %2, 0, %1, %2\n\t"                                               \
+            "v_addc_co_u32 %4, %5, 0, %4, %5"                                                   \
+            : "+v"(lo0), "+v"(top0), "=&s"(c0), "+v"(lo1), "+v"(top1), "=&s"(c1)                \
+            : "v"(x0), C1(y0), "v"(x1), C2(y1));                                                \
+    }
+ZKH_MAC2(mac2_vv, "v", "v")
+ZKH_MAC2(mac2_vs, "v", "s")
+ZKH_MAC2(mac2_sv, "s", "v")
+ZKH_MAC2(mac2_ss, "s", "s")
+
+// Montgomery product a*b*2^-256 mod r, canonical output for canonical inputs
+// (the same value as the reference's blstrs__scalar__Scalar_mul, bls12-381.cu:462-531).
+#include "mont_mul_ps.inc"
 
 // Montgomery reduction of a wide non-negative integer T (nl <= 16 limbs, T < r*2^256):
 // returns T*2^-256 mod r.  Used to fold wide integer accumulators into the field.
