@@ -195,6 +195,44 @@ def test_mm_wrong_witness_rejected(zkh, ctx):
     assert e.value.code == zkh.EROUND
 
 
+def _mm_check_batch(zkh, ctx, shapes, tag):
+    items, wants, sts, keep = [], [], [], []
+    for idx, shape in enumerate(shapes):
+        B, IN, OUT = shape
+        X, W, Y = _mm_inputs(shape, 300 + idx)
+        st_g, st_o = seed_transcript(zkh, "%s:%d" % (tag, idx))
+        rc, want = C.mm_prove(st_o, X, W, Y, B, IN, OUT)
+        assert rc == 0
+        t = (ctx.from_i32(X), ctx.from_i32(W), ctx.from_i64(Y))
+        keep.append(t)
+        items.append((st_g, t[0], t[1], t[2], B, IN, OUT))
+        wants.append(want)
+        sts.append((st_g, st_o))
+    outs, status = ctx.mm_prove_batch(items)
+    assert status == [0] * len(items)
+    for got, want, (st_g, st_o) in zip(outs, wants, sts):
+        for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+            assert fr_eq(got[key], want[key]), key
+        assert bytes(st_g) == bytes(st_o)
+
+
+@pytest.mark.parametrize("shape", [(2, 40000, 3),   # 2^16 entries: 128 blocks in LDS
+                                   (2, 70000, 2)])  # 2^17: beyond LDS, one launch per round
+def test_mm_prove_large_in(zkh, ctx, shape):
+    _mm_check_batch(zkh, ctx, [shape], "large")
+
+
+def test_mm_prove_batch_several_launch_groups(zkh, ctx):
+    """3 x 128 + 4 blocks exceed one 256-block launch: the jobs run in two groups."""
+    _mm_check_batch(zkh, ctx, [(2, 40000, 2), (3, 2048, 4), (2, 33000, 2), (1, 60000, 1)], "groups")
+
+
+def test_mm_prove_per_round_launch_path(zkh, ctx, monkeypatch):
+    """The one-launch-per-round path (used beyond the LDS sizes), forced for small shapes."""
+    monkeypatch.setenv("ZKH_NO_PERSIST", "1")
+    _mm_check_batch(zkh, ctx, [(4, 8, 4), (1, 1, 1), (33, 700, 129), (8, 2048, 8)], "perround")
+
+
 # ---------------------------------------------------------------- logUp
 LU_SHAPES = [(32, 8, -3, 5), (16, 16, 0, 16), (64, 4, -2, 3),  # vrf_toy_lookup.cu:323-335
              (32, 4, -2, 4), (64, 16, -8, 16), (48 * 0 + 64, 64, -32, 64),

@@ -259,25 +259,10 @@ class Context:
     def mm_prove_batch(self, items):
         """items: list of (transcript, X, W, Y, B, IN, OUT); returns (outputs, statuses);
         raises on any failing job (statuses still filled)."""
-        n = len(items)
-        arr = (MmJob * n)()
-        outs = []
-        for k, (st, X, W, Y, B, IN, OUT) in enumerate(items):
-            L, lb, lo = ceil_log2(IN), ceil_log2(B), ceil_log2(OUT)
-            o = dict(ev=np.zeros((3 * L + 1, 8), np.uint32), claims=np.zeros((3, 8), np.uint32),
-                     u_batch=np.zeros((lb + 1, 8), np.uint32), u_output=np.zeros((lo + 1, 8), np.uint32),
-                     u_input=np.zeros((L + 1, 8), np.uint32))
-            arr[k] = MmJob(X.h, W.h, Y.h, B, IN, OUT, st.ctypes.data, _p(o["ev"]), _p(o["claims"]),
-                           _p(o["u_batch"]), _p(o["u_output"]), _p(o["u_input"]), 0)
-            o["_sizes"] = (L, lb, lo)
-            outs.append(o)
-        rc = lib().zkh_mm_prove_batch(self.h, ctypes.cast(arr, ctypes.c_void_p), n)
-        status = [arr[k].status for k in range(n)]
-        for o in outs:
-            L, lb, lo = o.pop("_sizes")
-            o["ev"], o["u_batch"], o["u_output"], o["u_input"] = (o["ev"][:3 * L], o["u_batch"][:lb],
-                                                                  o["u_output"][:lo], o["u_input"][:L])
-        self._chk(rc)
+        b = MmBatch(self, items)
+        status = b.run(check=False)
+        outs = [dict(o) for o in b.outs]
+        self._chk(b.rc)
         return outs, status
 
     def range_table(self, low, length, N):
@@ -326,3 +311,33 @@ class Context:
         self._chk(lib().zkh_hp_prove_eq(self.h, _p(st), _p(claim), _p(u), k, S.h, U.h, _p(ev),
                                         _p(term), _p(ws)))
         return dict(ev=ev[:4 * k], term=term, ws=ws[:k])
+
+
+class MmBatch:
+    """A prepared zkh_mm_prove_batch call (the zkob_fc prove runs of several matmuls): the
+    zkh_mm_job array and the output buffers are built once, so run() is one C call that
+    proves every job again from the transcripts' current states."""
+
+    def __init__(self, ctx, items):
+        self.ctx = ctx
+        n = len(items)
+        self.arr = (MmJob * n)()
+        self.outs = []
+        self._keep = items
+        for k, (st, X, W, Y, B, IN, OUT) in enumerate(items):
+            L, lb, lo = ceil_log2(IN), ceil_log2(B), ceil_log2(OUT)
+            full = dict(ev=np.zeros((3 * L + 1, 8), np.uint32), claims=np.zeros((3, 8), np.uint32),
+                        u_batch=np.zeros((lb + 1, 8), np.uint32), u_output=np.zeros((lo + 1, 8), np.uint32),
+                        u_input=np.zeros((L + 1, 8), np.uint32))
+            self.arr[k] = MmJob(X.h, W.h, Y.h, B, IN, OUT, st.ctypes.data, _p(full["ev"]), _p(full["claims"]),
+                                _p(full["u_batch"]), _p(full["u_output"]), _p(full["u_input"]), 0)
+            self.outs.append(dict(ev=full["ev"][:3 * L], claims=full["claims"], u_batch=full["u_batch"][:lb],
+                                  u_output=full["u_output"][:lo], u_input=full["u_input"][:L]))
+        self._ptr = ctypes.cast(self.arr, ctypes.c_void_p)
+        self.rc = 0
+
+    def run(self, check=True):
+        self.rc = lib().zkh_mm_prove_batch(self.ctx.h, self._ptr, len(self.arr))
+        if check:
+            self.ctx._chk(self.rc)
+        return [self.arr[k].status for k in range(len(self.arr))]

@@ -955,16 +955,47 @@ void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, ui
     k_eq_mont_multi<<<nblocks, NT, 0, s>>>(d_dev, nd);
 }
 
+// uniform descriptor search: the last d[j] with d[j].blk_begin <= blockIdx.x (binary search
+// over scalar loads, so every field of the result stays in scalar registers)
+template <typename D>
+ZDEV uint32_t find_desc_uniform(const D* __restrict__ d, uint32_t nd) {
+    uint32_t lo = 0, hi = nd;  // d[lo].blk_begin <= blockIdx.x < d[hi].blk_begin
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (d[mid].blk_begin <= blockIdx.x) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+typedef __attribute__((address_space(4))) const uint32_t* const_u32p;
+// wave-uniform AoS load through the scalar cache (the table is read-only in the kernel)
+ZDEV fr_t ld_aos_uniform(const uint32_t* p, uint32_t i) {
+    const_u32p c = (const_u32p)(p + 8 * (size_t)i);
+    fr_t r;
+#pragma unroll
+    for (int j = 0; j < 8; j++) r.v[j] = c[j];
+    return r;
+}
+// streaming (read-once) global load
+template <typename T>
+ZDEV T ld_stream(const T* p) {
+    return __builtin_nontemporal_load((__attribute__((address_space(1))) const T*)p);
+}
+
+// partial[c*N + i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) e_k: one column per thread,
+// rows unrolled by 8 with all eight loads issued before the multiply-adds so each wave
+// keeps 8 rows of its column block in flight; e_k comes through scalar loads.
 template <typename T, int NP>
 __global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict__ d, uint32_t nd) {
-    EqDotDesc q;
-    find_desc(d, nd, q);
-    const uint32_t ncb = (q.N + NT - 1) / NT;
+    const EqDotDesc& q = d[find_desc_uniform(d, nd)];
+    const uint32_t N = q.N;
+    const uint32_t ncb = (N + NT - 1) / NT;
     const uint32_t local = blockIdx.x - q.blk_begin;
     const uint32_t i = (local % ncb) * NT + threadIdx.x;
     const uint32_t c = local / ncb;
     const uint32_t k0 = c * q.kchunk;
     const uint32_t k1 = min(q.K, k0 + q.kchunk);
+    const uint32_t* E = q.E;
     uint64_t acc[NP][8];
 #pragma unroll
     for (int p = 0; p < NP; p++)
@@ -972,11 +1003,24 @@ __global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict_
         for (int j = 0; j < 8; j++) acc[p][j] = 0;
     const int64_t off = (int64_t)1 << q.bits;
     const T* M = reinterpret_cast<const T*>(q.M);
-    if (i < q.N) {
+    if (i < N) {
         const T* col = M + i;
-        for (uint32_t k = k0; k < k1; k++) {
-            const fr_t e = ld_aos(q.E, k);
-            const uint64_t w = (uint64_t)((int64_t)col[(size_t)k * q.N] + off);
+        uint32_t k = k0;
+        for (; k + 8 <= k1; k += 8) {
+            T v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = ld_stream(col + (size_t)(k + u) * N);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const fr_t e = ld_aos_uniform(E, k + u);
+                const uint64_t w = (uint64_t)((int64_t)v[u] + off);
+#pragma unroll
+                for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (20 * p)) & 0xFFFFFu, e);
+            }
+        }
+        for (; k < k1; k++) {
+            const fr_t e = ld_aos_uniform(E, k);
+            const uint64_t w = (uint64_t)((int64_t)ld_stream(col + (size_t)k * N) + off);
 #pragma unroll
             for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (20 * p)) & 0xFFFFFu, e);
         }
@@ -990,7 +1034,7 @@ __global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict_
         if (p > 0) f = mont_mul(f, piece_scale(p));
         r = fr_add(r, f);
     }
-    if (i < q.N) st_aos(q.partial, (size_t)c * q.N + i, r);
+    if (i < N) st_aos(q.partial, (size_t)c * N + i, r);
 }
 void launch_eqdot_multi(hipStream_t s, int is64, uint32_t np, const EqDotDesc* d_dev, uint32_t nd,
                         uint32_t nblocks) {
@@ -1075,6 +1119,141 @@ __global__ void k_fold_last_multi(ZkipBatch bt) {
 }
 void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b) {
     k_fold_last_multi<<<1, 64, 0, s>>>(b);
+}
+
+
+// ------------------------------------------------------------------------------------
+// persistent matmul round loop (see ZkipPersist): tables in LDS, one host round trip per
+// round, no device-side reduction or barrier across blocks
+// ------------------------------------------------------------------------------------
+// thread 0 only: wait until the job's command word equals want; false on ZKH_QUIT or when
+// the deadline passes (then *err is set)
+ZDEV bool persist_wait(uint32_t* cmd, uint32_t want, uint32_t* err, uint64_t deadline) {
+    const uint64_t t0 = wall_clock64();
+    for (;;) {
+        const uint32_t v = __hip_atomic_load(cmd, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (v == want) return true;
+        if (v == ZKH_QUIT) return false;
+        if (wall_clock64() - t0 > deadline) {
+            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+#define NTP 1024  // threads of a persistent round block (16 waves)
+#define NPG 320   // threads per product group: waves 0-4, 5-9, 10-14 (wave 15 idle)
+
+// block clock -> slot words 56..59 (publication time, receipt of the previous challenge)
+ZDEV void persist_stamp(uint32_t* slot, uint64_t t_cmd) {
+    const uint64_t now = wall_clock64();
+    slot[56] = (uint32_t)now;
+    slot[57] = (uint32_t)(now >> 32);
+    slot[58] = (uint32_t)t_cmd;
+    slot[59] = (uint32_t)(t_cmd >> 32);
+}
+// Round loop of one block over its LDS slice (see ZkipPersist).  Per round, each group of
+// five waves accumulates one product over the pairs (k, k + h): group 0 a0*b0, group 1
+// a1*b1, group 2 (a1-a0)*(b1-b0); the fold spreads one entry per thread.  With at most 512
+// entries per block, every thread does at most one dependent Montgomery multiplication per
+// phase from the first fold on.
+__global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
+    extern __shared__ uint4 zl[];  // a.lo | a.hi | b.lo | b.hi, ls entries each
+    __shared__ uint32_t sj, sok;
+    __shared__ fr_t sx, red[15];
+    if (threadIdx.x == 0) {
+        uint32_t j = 0;
+        while (j + 1 < P.nd && P.d[j + 1].blk_begin <= blockIdx.x) j++;
+        sj = j;
+    }
+    __syncthreads();
+    const ZkipPJob& q = P.d[sj];
+    const uint32_t lb = blockIdx.x - q.blk_begin;
+    const uint32_t ls = q.n >> q.lgnb;
+    uint4* alo = zl;
+    uint4* ahi = zl + ls;
+    uint4* blo = zl + 2 * ls;
+    uint4* bhi = zl + 3 * ls;
+    {
+        const uint4* ga_lo = reinterpret_cast<const uint4*>(q.a_lo);
+        const uint4* ga_hi = reinterpret_cast<const uint4*>(q.a_hi);
+        const uint4* gb_lo = reinterpret_cast<const uint4*>(q.b_lo);
+        const uint4* gb_hi = reinterpret_cast<const uint4*>(q.b_hi);
+        for (uint32_t k = threadIdx.x; k < ls; k += NTP) {
+            const uint32_t g = lb + (k << q.lgnb);
+            alo[k] = ga_lo[g];
+            ahi[k] = ga_hi[g];
+            blo[k] = gb_lo[g];
+            bhi[k] = gb_hi[g];
+        }
+    }
+    __syncthreads();
+    uint32_t* slot = q.out + (size_t)lb * ZKH_PSLOT;
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t w = wv / 5, gt = threadIdx.x - w * NPG;  // product group, index in it
+    uint32_t m = ls, r = 0;
+    uint64_t t_cmd = 0;
+    for (; m > 1; r++) {
+        const uint32_t h = m >> 1;
+        fr_t acc = fr_zero();
+        for (uint32_t k = gt; w < 3 && k < h; k += NPG) {
+            fr_t x, y;
+            if (w == 0) {
+                x = ld_fr(alo, ahi, k);
+                y = ld_fr(blo, bhi, k);
+            } else if (w == 1) {
+                x = ld_fr(alo, ahi, k + h);
+                y = ld_fr(blo, bhi, k + h);
+            } else {
+                x = fr_sub(ld_fr(alo, ahi, k + h), ld_fr(alo, ahi, k));
+                y = fr_sub(ld_fr(blo, bhi, k + h), ld_fr(blo, bhi, k));
+            }
+            acc = fr_add(acc, mont_mul(x, y));
+        }
+        acc = fr_wave_sum(acc);
+        if (lane == 0 && wv < 15) red[wv] = acc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll 1
+            for (int g = 0; g < 3; g++) {
+                fr_t t = red[5 * g];
+#pragma unroll 1
+                for (int i = 1; i < 5; i++) t = fr_add(t, red[5 * g + i]);
+                st_aos(slot, g, t);
+            }
+            persist_stamp(slot, t_cmd);
+            __hip_atomic_store(slot + 63, r + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            sok = persist_wait(q.cmd, r + 1, P.err, P.deadline);
+            if (sok) sx = ld_aos(q.cmd + 8, 0);
+            t_cmd = wall_clock64();
+        }
+        __syncthreads();
+        if (!sok) return;
+        const fr_t x = sx;
+        for (uint32_t t = threadIdx.x; t < 2 * h; t += NTP) {  // a for t < h, b for t >= h
+            const bool tb = t >= h;
+            const uint32_t k = tb ? t - h : t;
+            uint4* lo = tb ? blo : alo;
+            uint4* hi = tb ? bhi : ahi;
+            const fr_t v0 = ld_fr(lo, hi, k), v1 = ld_fr(lo, hi, k + h);
+            st_fr(lo, hi, k, fr_add(v0, mont_mul(x, fr_sub(v1, v0))));
+        }
+        __syncthreads();
+        m = h;
+    }
+    if (threadIdx.x == 0) {
+        st_aos(slot, 0, ld_fr(alo, ahi, 0));
+        st_aos(slot, 1, ld_fr(blo, bhi, 0));
+        persist_stamp(slot, t_cmd);
+        __hip_atomic_store(slot + 63, r + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+// An ordinary launch on the stream: the blocks never wait for each other, only for the
+// host, and a launch has at most 256 blocks (one per CU at most 32 KiB LDS and 16 waves),
+// so all of them are resident once earlier kernels drain.
+hipError_t launch_zkip_persist(hipStream_t s, const ZkipPersist& p, uint32_t nblocks) {
+    k_zkip_persist<<<nblocks, NTP, (size_t)p.ls_max * 64, s>>>(p);
+    return hipGetLastError();
 }
 
 }  // namespace zkh

@@ -193,4 +193,36 @@ struct ZkipBatch {  // passed by value as the kernel argument (<= 2.1 KB)
 };
 void launch_zkip_round_multi(hipStream_t s, const ZkipBatch& b, uint32_t nblocks, Publish pub);
 void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
+
+// ---- persistent matmul round loop ----
+// Each job's tables a, b (n = 2^L entries) are spread cyclically over nb = 2^lgnb blocks
+// (block l holds entries l + nb*k in LDS), so the pairs (i, i + m/2) of every round with
+// m >= 2*nb stay inside one block.  Round r: every block writes its sums (sum a0b0,
+// sum a1b1, sum da*db, each x 2^-256; AoS words 0..23) to its host slot and stores r + 1
+// into slot word 63 (system-scope release); it then waits for the host to store r + 1 into
+// cmd[0] with the challenge (Montgomery form) in cmd[8..16), and folds.  After the last
+// local round each block stores its single folded entries of a and b (slot words 0..15)
+// with sequence number rounds + 1 and exits.  cmd[0] == ZKH_QUIT makes the job's blocks
+// exit; a block that waits longer than `deadline` ticks of the 100 MHz clock sets *err and
+// exits.
+#define ZKH_QUIT 0xffffffffu
+#define ZKH_PSLOT 64  // words per block slot and per job command area
+#define ZKH_PLS_MAX 512u  // entries per block and table (32 KiB of LDS for both tables)
+struct ZkipPJob {
+    const uint32_t* a_lo;
+    const uint32_t* a_hi;
+    const uint32_t* b_lo;
+    const uint32_t* b_hi;
+    uint32_t* out;  // pinned host, nb slots
+    uint32_t* cmd;  // pinned host, one command area
+    uint32_t n, lgnb, blk_begin, pad_;
+};
+struct ZkipPersist {  // passed by value as the kernel argument
+    ZkipPJob d[ZKH_MAX_BATCH];
+    uint32_t* err;
+    unsigned long long deadline;
+    uint32_t nd, ls_max;
+};
+// at most 256 blocks; returns the HIP status of the launch
+hipError_t launch_zkip_persist(hipStream_t s, const ZkipPersist& p, uint32_t nblocks);
 }  // namespace zkh

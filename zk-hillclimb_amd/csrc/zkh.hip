@@ -13,8 +13,13 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/zkh.h"
@@ -23,6 +28,86 @@
 #include "transcript.hpp"
 
 using namespace zkh;
+
+// Host worker threads for the per-job work of a batch (every job has its own transcript,
+// so jobs advance independently).  After a task a worker polls for the next one for about
+// a millisecond, then sleeps on a condition variable; run() returns when every participant
+// has finished.
+struct HostPool {
+    std::vector<std::thread> th;
+    std::mutex mu;
+    std::condition_variable cv;
+    std::function<void(int)> task;
+    std::atomic<uint64_t> gen{0};
+    int active = 0;  // workers 1..active take part in the current task
+    std::atomic<int> left{0};
+    bool stop = false;
+    void ensure(int n) {
+        while ((int)th.size() < n) {
+            const int id = (int)th.size() + 1;
+            th.emplace_back([this, id] {
+                uint64_t seen = 0;
+                for (;;) {
+                    const auto t0 = std::chrono::steady_clock::now();
+                    for (uint32_t k = 1; gen.load(std::memory_order_acquire) == seen; k++) {
+                        __builtin_ia32_pause();
+                        if ((k & 1023) == 0 &&
+                            std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(1000))
+                            break;
+                    }
+                    std::function<void(int)> f;
+                    {
+                        std::unique_lock<std::mutex> lk(mu);
+                        cv.wait(lk, [&] { return stop || gen.load(std::memory_order_acquire) != seen; });
+                        if (stop) return;
+                        seen = gen.load(std::memory_order_acquire);
+                        if (id > active) continue;
+                        f = task;
+                    }
+                    f(id);
+                    left.fetch_sub(1, std::memory_order_acq_rel);
+                }
+            });
+        }
+    }
+    // f(0) .. f(n-1), f(0) on the calling thread
+    void run(int n, const std::function<void(int)>& f) {
+        if (n <= 1) {
+            f(0);
+            return;
+        }
+        ensure(n - 1);
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            task = f;
+            active = n - 1;
+            left.store(n - 1, std::memory_order_release);
+            gen.fetch_add(1, std::memory_order_acq_rel);
+        }
+        cv.notify_all();
+        f(0);
+        while (left.load(std::memory_order_acquire)) __builtin_ia32_pause();
+    }
+    ~HostPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            stop = true;
+        }
+        cv.notify_all();
+        for (auto& t : th) t.join();
+    }
+};
+// host threads for the per-job work of a batch (ZKH_HOST_THREADS, default 1: extra
+// threads save ~5% of a TinyLlama matmul step but every spinning thread is exposed to
+// preemption on a shared host, which showed as multi-millisecond stalls)
+static int host_threads() {
+    static const int n = [] {
+        const char* e = getenv("ZKH_HOST_THREADS");
+        int v = e ? atoi(e) : 1;
+        return v < 1 ? 1 : v > 16 ? 16 : v;
+    }();
+    return n;
+}
 
 struct zkh_ctx {
     int device = 0;
@@ -41,6 +126,12 @@ struct zkh_ctx {
     size_t pub_part_cap = (size_t)4096 * 11;
     uint32_t* pub_cnt = nullptr;   // device [ZKH_MAX_BATCH + 1]
     uint32_t pub_seq = 0;
+    // persistent round loops: coherent pinned block slots / command areas, clock rate
+    uint32_t* ps_host = nullptr;
+    size_t ps_words = 0;
+    uint64_t clock_khz = 100000;
+    HostPool workers;
+    std::mutex err_mu;  // error reporting from worker threads
     // pinned ring for small host->device uploads: a region is reused only after a later
     // stream synchronisation, which every API call performs before returning
     uint8_t* ring = nullptr;
@@ -205,6 +296,21 @@ static int ensure_pinned(zkh_ctx* c, size_t bytes) {
     if (hipHostMalloc((void**)&c->pinned, want, hipHostMallocDefault) != hipSuccess)
         return fail(c, ZKH_EDEV, "hipHostMalloc(%zu) failed", want);
     c->pinned_bytes = want;
+    return 0;
+}
+// coherent pinned words for the persistent loops' block slots and command areas; the
+// stream is drained before a regrow so no running kernel still points at the old area
+static int ensure_ps(zkh_ctx* c, size_t words) {
+    if (c->ps_words >= words) return 0;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (c->ps_host) (void)hipHostFree(c->ps_host);
+    c->ps_host = nullptr;
+    c->ps_words = 0;
+    const size_t want = std::max(words, (size_t)1 << 16);
+    if (hipHostMalloc((void**)&c->ps_host, want * 4, hipHostMallocCoherent) != hipSuccess)
+        return fail(c, ZKH_EDEV, "hipHostMalloc(coherent, %zu) failed", want * 4);
+    memset(c->ps_host, 0, want * 4);
+    c->ps_words = want;
     return 0;
 }
 // ---- host-side round trace (ZKH_TRACE=1): per-round launch / wait / host times ----
@@ -407,6 +513,9 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
         return ZKH_EDEV;
     }
     memset(c->pub_host, 0, (ZKH_MAX_BATCH * 11 * 8 + 64) * 4);
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device) == hipSuccess && khz > 0)
+        c->clock_khz = (uint64_t)khz;
     if (ensure_pinned(c, (size_t)1 << 20)) {
         (void)hipStreamDestroy(c->stream);
         delete c;
@@ -424,6 +533,7 @@ extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
     if (c->pinned) (void)hipHostFree(c->pinned);
     if (c->ring) (void)hipHostFree(c->ring);
     if (c->pub_host) (void)hipHostFree(c->pub_host);
+    if (c->ps_host) (void)hipHostFree(c->ps_host);
     if (c->pub_part) (void)hipFree(c->pub_part);
     if (c->pub_cnt) (void)hipFree(c->pub_cnt);
     for (auto& p : c->pending) {
@@ -984,6 +1094,10 @@ extern "C" int zkh_mm_prove_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
 }
 static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     int first_rc = 0;
+    const double t_in = now_us();
+    auto stamp = [&](const char* what) {
+        if (trace_on()) fprintf(stderr, "[zkh] mm %-28s %8.1f us\n", what, now_us() - t_in);
+    };
     for (uint32_t j = 0; j < nj; j++) {
         zkh_mm_job& J = jobs[j];
         J.status = ZKH_OK;
@@ -1010,7 +1124,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     struct Job {
         uint32_t lb, lo, L, INp;
         std::vector<Fr> ub, uo, xs;
-        Fr claim, cur;
+        Fr claim, cur, xm;  // xm: the last challenge in Montgomery form
+        Fr SEb, SEo;        // sum of the eq table entries over the first B / OUT indices
         size_t eb_off, eo_off, fac_b, fac_o;  // element offsets
         size_t red_off;                       // planes offset (entries) of a; b follows
         uint32_t dot_blocks, dot_slot;        // claim partials in pinned memory
@@ -1027,8 +1142,6 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         q.INp = 1u << q.L;
         q.ub.resize(q.lb);
         q.uo.resize(q.lo);
-        for (auto& x : q.ub) x = tr_challenge(in.transcript);
-        for (auto& x : q.uo) x = tr_challenge(in.transcript);
         q.fac_b = fac_total;
         fac_total += 2 * (size_t)q.lb;
         q.fac_o = fac_total;
@@ -1043,14 +1156,24 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         q.live = true;
     }
     // device areas
+    // u_batch, u_output draws (zkob_fc.cu:259-262), eq factors and eq prefix sums, per job
+    // on the host workers
     std::vector<uint32_t> fac(std::max<size_t>(fac_total, 1) * 8, 0);
-    for (uint32_t j = 0; j < nj; j++) {
-        std::vector<uint32_t> fb, fo;
-        make_fac(J[j].ub, 0, fb);
-        make_fac(J[j].uo, 0, fo);
-        std::copy(fb.begin(), fb.end(), fac.begin() + J[j].fac_b * 8);
-        std::copy(fo.begin(), fo.end(), fac.begin() + J[j].fac_o * 8);
-    }
+    const int Ts = (int)std::min<uint32_t>(nj, (uint32_t)host_threads());
+    c->workers.run(Ts, [&](int t) {
+        for (uint32_t j = (uint32_t)t; j < nj; j += (uint32_t)Ts) {
+            Job& q = J[j];
+            for (auto& x : q.ub) x = tr_challenge(jobs[j].transcript);
+            for (auto& x : q.uo) x = tr_challenge(jobs[j].transcript);
+            std::vector<uint32_t> fb, fo;
+            make_fac(q.ub, 0, fb);
+            make_fac(q.uo, 0, fo);
+            std::copy(fb.begin(), fb.end(), fac.begin() + q.fac_b * 8);
+            std::copy(fo.begin(), fo.end(), fac.begin() + q.fac_o * 8);
+            q.SEb = eq_prefix_sum(q.ub, jobs[j].B);
+            q.SEo = eq_prefix_sum(q.uo, jobs[j].OUT);
+        }
+    });
     uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, fac.size() * 4, &rc);
     if (rc) return rc;
     uint32_t* eq_d = (uint32_t*)scratch(c, SL_EB, eq_total * 32, &rc);
@@ -1061,6 +1184,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     if (rc) return rc;
     if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
 
+    stamp("challenges + factor upload");
     // 1) eq tables (Montgomery AoS)
     std::vector<EqTabDesc> eqd;
     uint32_t eq_blocks = 0;
@@ -1090,7 +1214,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     for (uint32_t j = 0; j < nj; j++) {
         const zkh_mm_job& in = jobs[j];
         const Job& q = J[j];
-        Fr SEb = eq_prefix_sum(q.ub, in.B), SEo = eq_prefix_sum(q.uo, in.OUT);
+        const Fr SEb = q.SEb, SEo = q.SEo;
         const int32_t* WT = (const int32_t*)in.W->d;
         if (!in.W->weights) {
             launch_transpose_i32(c->stream, (const int32_t*)in.W->d, in.IN, in.OUT, wt_d + wt_off);
@@ -1199,6 +1323,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     memcpy(blob.data() + o_dot, dots.data(), dots.size() * sizeof(EqDotDesc));
     memcpy(blob.data() + o_sum, sums.data(), sums.size() * sizeof(SumChunksDesc));
     if ((rc = upload(c, desc_d, blob.data(), o_zk))) return rc;
+    stamp("descriptors uploaded");
     {
         ProfScope ps(c, "eq_tables", (double)eq_total * 32);
         launch_eq_mont_multi(c->stream, (const EqTabDesc*)(desc_d + o_eq), (uint32_t)eqd.size(), eq_blocks);
@@ -1219,19 +1344,286 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         launch_sum_chunks_multi(c->stream, (const SumChunksDesc*)(desc_d + o_sum), (uint32_t)sums.size(),
                                 sum_blocks);
     }
+    for (auto& q : J) q.xs.resize(q.L);
+    // claim = <Y(u_batch, .), eq(u_output, .)> from the pinned block partials
+    auto absorb_claim = [&](uint32_t j) {
+        Job& q = J[j];
+        Fr s = kZero;
+        for (uint32_t b = 0; b < q.dot_blocks; b++)
+            s = fr_add(s, fr_load(pin + pin_claim + 8 * (size_t)(q.dot_slot + b)));
+        q.claim = q.cur = s;
+        tr_absorb_fr(jobs[j].transcript, "claim", s);
+    };
+    // one round from its three sums c0 = sum a0b0, q1 = sum a1b1, c2 = sum da*db
+    // (zkob_fc.cu:294-332): p(0) = c0, p(1) = q1, p(2) = c0 + 2c1 + 4c2
+    // The running claim becomes p(x) = c0 + x(c1 + x c2), with x in Montgomery form so each
+    // product is one Montgomery multiplication; q.xm keeps it for the device folds.
+    auto round_step = [&](uint32_t j, uint32_t r, const Fr& c0, const Fr& q1, const Fr& c2) -> bool {
+        Job& q = J[j];
+        const Fr c1 = fr_sub(fr_sub(q1, c0), c2);
+        const Fr c1x2 = fr_add(c1, c1), c2x2 = fr_add(c2, c2);
+        Fr p[3] = {c0, q1, fr_add(fr_add(c0, c1x2), fr_add(c2x2, c2x2))};
+        if (!fr_eq(q.cur, fr_add(p[0], p[1]))) {
+            q.live = false;
+            jobs[j].status = ZKH_EROUND;
+            std::lock_guard<std::mutex> lk(c->err_mu);
+            if (!first_rc)
+                first_rc = fail(c, ZKH_EROUND, "job %u: prover sumcheck round inconsistency (witness bug) at round %u",
+                                j, r);
+            return false;
+        }
+        uint8_t* tr = jobs[j].transcript;
+        tr_absorb_fr(tr, "p0", p[0]);
+        tr_absorb_fr(tr, "p1", p[1]);
+        tr_absorb_fr(tr, "p2", p[2]);
+        const Fr x = tr_challenge(tr);
+        q.xs[r] = x;
+        q.xm = fr_to_mont(x);
+        if (jobs[j].ev_out)
+            for (int k = 0; k < 3; k++) fr_store(p[k], jobs[j].ev_out + 8 * (3 * r + k));
+        q.cur = fr_add(c0, fr_mont_mul(q.xm, fr_add(c1, fr_mont_mul(q.xm, c2))));
+        return true;
+    };
+    // terminal check claim == X(u_batch, u_input) * W(u_input, u_output), outputs
+    auto finish = [&](uint32_t j, const Fr& cx, const Fr& cw) {
+        Job& q = J[j];
+        zkh_mm_job& in = jobs[j];
+        if (!fr_eq(q.cur, fr_mul(cx, cw))) {
+            q.live = false;
+            in.status = ZKH_EROUND;
+            std::lock_guard<std::mutex> lk(c->err_mu);
+            if (!first_rc) first_rc = fail(c, ZKH_EROUND, "job %u: terminal product mismatch (witness bug)", j);
+            return;
+        }
+        tr_absorb_fr(in.transcript, "claim_X", cx);
+        tr_absorb_fr(in.transcript, "claim_W", cw);
+        if (in.claims_out) {
+            fr_store(q.claim, in.claims_out);
+            fr_store(cx, in.claims_out + 8);
+            fr_store(cw, in.claims_out + 16);
+        }
+        if (in.u_batch_out)
+            for (uint32_t i = 0; i < q.lb; i++) fr_store(q.ub[i], in.u_batch_out + 8 * i);
+        if (in.u_output_out)
+            for (uint32_t i = 0; i < q.lo; i++) fr_store(q.uo[i], in.u_output_out + 8 * i);
+        if (in.u_input_out)
+            for (uint32_t i = 0; i < q.L; i++) fr_store(q.xs[q.L - 1 - i], in.u_input_out + 8 * i);
+    };
+
+    // 4) rounds.  Tables of up to ZKH_PLS_MAX * 128 entries: one persistent launch per group
+    // of jobs (<= 256 blocks), tables in LDS, one host round trip per round and job.
+    uint32_t max_inp = 0;
+    for (auto& q : J) max_inp = std::max(max_inp, q.INp);
+    if (max_inp <= ZKH_PLS_MAX * 128 && !getenv("ZKH_NO_PERSIST")) {
+        std::vector<uint32_t> lgnb(nj), slot_off(nj), cmd_off(nj), grp_of(nj);
+        std::vector<ZkipPersist> groups_p;
+        std::vector<uint32_t> grp_blocks;
+        size_t words = ZKH_PSLOT;  // word 0: error flag
+        for (uint32_t j = 0; j < nj; j++) {
+            const uint32_t INp = J[j].INp;
+            // ZKH_PLS_MAX entries per block (up to 128 blocks)
+            lgnb[j] = INp > ZKH_PLS_MAX ? ceil_log2(INp / ZKH_PLS_MAX) : 0;
+            const uint32_t nb = 1u << lgnb[j];
+            slot_off[j] = (uint32_t)words;
+            words += (size_t)nb * ZKH_PSLOT;
+            cmd_off[j] = (uint32_t)words;
+            words += ZKH_PSLOT;
+            if (groups_p.empty() || grp_blocks.back() + nb > 256 || groups_p.back().nd == ZKH_MAX_BATCH) {
+                groups_p.emplace_back();
+                memset(&groups_p.back(), 0, sizeof(ZkipPersist));
+                grp_blocks.push_back(0);
+            }
+            grp_of[j] = (uint32_t)groups_p.size() - 1;
+        }
+        if ((rc = ensure_ps(c, words))) return rc;
+        uint32_t* ps = c->ps_host;
+        for (uint32_t j = 0; j < nj; j++) {
+            const uint32_t nb = 1u << lgnb[j];
+            for (uint32_t b = 0; b < nb; b++) ps[slot_off[j] + b * ZKH_PSLOT + 63] = 0;
+            ps[cmd_off[j]] = 0;
+        }
+        ps[0] = 0;
+        const uint64_t deadline_ticks = c->clock_khz * 1000 * 20;  // 20 s without a command
+        for (uint32_t j = 0; j < nj; j++) {
+            ZkipPersist& P = groups_p[grp_of[j]];
+            ZkipPJob& d = P.d[P.nd++];
+            d.a_lo = red.lo() + 4 * J[j].red_off;
+            d.a_hi = red.hi() + 4 * J[j].red_off;
+            d.b_lo = red.lo() + 4 * (J[j].red_off + J[j].INp);
+            d.b_hi = red.hi() + 4 * (J[j].red_off + J[j].INp);
+            d.out = ps + slot_off[j];
+            d.cmd = ps + cmd_off[j];
+            d.n = J[j].INp;
+            d.lgnb = lgnb[j];
+            d.blk_begin = grp_blocks[grp_of[j]];
+            grp_blocks[grp_of[j]] += 1u << lgnb[j];
+            P.err = ps;
+            P.deadline = deadline_ticks;
+            P.ls_max = std::max(P.ls_max, J[j].INp >> lgnb[j]);
+        }
+        auto quit_all = [&]() {
+            for (uint32_t j = 0; j < nj; j++) __atomic_store_n(ps + cmd_off[j], ZKH_QUIT, __ATOMIC_RELEASE);
+            (void)hipStreamSynchronize(c->stream);
+        };
+        double pbytes = 0;
+        for (auto& q : J) pbytes += 2.0 * q.INp * 32;
+        {
+            ProfScope psc(c, "zkip_rounds", pbytes);
+            for (size_t g = 0; g < groups_p.size(); g++) {
+                hipError_t e = launch_zkip_persist(c->stream, groups_p[g], grp_blocks[g]);
+                if (e != hipSuccess) {
+                    quit_all();
+                    return fail(c, ZKH_EDEV, "persistent round launch: %s", hipGetErrorString(e));
+                }
+            }
+        }
+        stamp("all launched");
+        // host side: each worker thread advances its jobs (j = t mod T) whenever all of a
+        // job's blocks have published
+        std::vector<uint32_t> R(nj);
+        for (uint32_t j = 0; j < nj; j++) R[j] = J[j].L - lgnb[j];
+        std::atomic<int> abort_why{0};  // 1 device error, 2 kernel ended early, 3 no progress
+        std::atomic<int> dev_err{0};
+        const double t_start = now_us();
+        auto ready = [&](uint32_t j, uint32_t seq) {
+            const uint32_t nb = 1u << lgnb[j];
+            for (uint32_t b = 0; b < nb; b++)
+                if (__atomic_load_n(ps + slot_off[j] + b * ZKH_PSLOT + 63, __ATOMIC_ACQUIRE) != seq) return false;
+            return true;
+        };
+        const int T = (int)std::min<uint32_t>(nj, (uint32_t)host_threads());
+        const bool tracing = trace_on();
+        std::vector<std::vector<uint64_t>> tr_gpu(tracing ? nj : 0);
+        std::vector<std::vector<double>> tr_host(tracing ? nj : 0);
+        auto worker = [&](int t) {
+            std::vector<uint32_t> mine;
+            for (uint32_t j = (uint32_t)t; j < nj; j += (uint32_t)T) mine.push_back(j);
+            std::vector<uint32_t> rnd(mine.size(), 0);
+            std::vector<uint8_t> done(mine.size(), 0);
+            size_t left = mine.size();
+            std::vector<Fr> ta, tb;
+            double t_prog = now_us();
+            for (uint64_t spins = 1; left; spins++) {
+                bool prog = false;
+                for (size_t a = 0; a < mine.size(); a++) {
+                    if (done[a]) continue;
+                    const uint32_t j = mine[a];
+                    const uint32_t nb = 1u << lgnb[j];
+                    const uint32_t* sl = ps + slot_off[j];
+                    if (!ready(j, rnd[a] + 1)) continue;
+                    prog = true;
+                    if (tracing) {  // block 0's clock: publication, and receipt of the last challenge
+                        const uint32_t* s0 = sl;
+                        tr_gpu[j].push_back(((uint64_t)s0[57] << 32) | s0[56]);
+                        tr_gpu[j].push_back(((uint64_t)s0[59] << 32) | s0[58]);
+                        tr_host[j].push_back(now_us());
+                    }
+                    // a block has run, so every earlier launch (the claim partials) has completed
+                    if (rnd[a] == 0) absorb_claim(j);
+                    if (rnd[a] < R[j]) {
+                        Fr s3[3] = {kZero, kZero, kZero};
+                        for (uint32_t b = 0; b < nb; b++)
+                            for (int k = 0; k < 3; k++) s3[k] = fr_add(s3[k], fr_load(sl + b * ZKH_PSLOT + 8 * k));
+                        if (!round_step(j, rnd[a], fix1(s3[0]), fix1(s3[1]), fix1(s3[2]))) {
+                            __atomic_store_n(ps + cmd_off[j], ZKH_QUIT, __ATOMIC_RELEASE);
+                            done[a] = 1;
+                            left--;
+                            continue;
+                        }
+                        fr_store(J[j].xm, ps + cmd_off[j] + 8);
+                        rnd[a]++;
+                        __atomic_store_n(ps + cmd_off[j], rnd[a], __ATOMIC_RELEASE);
+                        continue;
+                    }
+                    // the blocks' folded entries: the remaining lgnb rounds on the host
+                    ta.resize(nb);
+                    tb.resize(nb);
+                    for (uint32_t b = 0; b < nb; b++) {
+                        ta[b] = fr_load(sl + b * ZKH_PSLOT);
+                        tb[b] = fr_load(sl + b * ZKH_PSLOT + 8);
+                    }
+                    done[a] = 1;
+                    left--;
+                    bool ok = true;
+                    for (uint32_t r = R[j], m = nb; m > 1 && ok; r++, m >>= 1) {
+                        const uint32_t h = m >> 1;
+                        Fr c0 = kZero, q1 = kZero, c2 = kZero;  // each x 2^-256
+                        for (uint32_t i = 0; i < h; i++) {
+                            c0 = fr_add(c0, fr_mont_mul(ta[i], tb[i]));
+                            q1 = fr_add(q1, fr_mont_mul(ta[i + h], tb[i + h]));
+                            c2 = fr_add(c2, fr_mont_mul(fr_sub(ta[i + h], ta[i]), fr_sub(tb[i + h], tb[i])));
+                        }
+                        ok = round_step(j, r, fix1(c0), fix1(q1), fix1(c2));
+                        const Fr xm = J[j].xm;
+                        for (uint32_t i = 0; ok && i < h; i++) {
+                            ta[i] = fr_add(ta[i], fr_mont_mul(xm, fr_sub(ta[i + h], ta[i])));
+                            tb[i] = fr_add(tb[i], fr_mont_mul(xm, fr_sub(tb[i + h], tb[i])));
+                        }
+                    }
+                    if (ok) finish(j, ta[0], tb[0]);
+                }
+                if (prog) {
+                    t_prog = now_us();
+                    continue;
+                }
+                __builtin_ia32_pause();
+                if ((spins & 0x3FFF) == 0) {
+                    if (abort_why.load(std::memory_order_relaxed)) return;
+                    hipError_t e = hipStreamQuery(c->stream);
+                    int why = 0;
+                    if (e != hipSuccess && e != hipErrorNotReady) {
+                        dev_err.store((int)e);
+                        why = 1;
+                    } else if (__atomic_load_n(ps, __ATOMIC_ACQUIRE)) {
+                        why = 2;
+                    } else if (e == hipSuccess) {  // the kernel has ended: whatever is missing never comes
+                        bool all = true;
+                        for (size_t a = 0; a < mine.size(); a++)
+                            all = all && (done[a] || ready(mine[a], rnd[a] + 1));
+                        if (!all) why = 4;
+                    } else if (now_us() - t_prog > 30e6) {
+                        why = 3;
+                    }
+                    if (why) {
+                        int z = 0;
+                        abort_why.compare_exchange_strong(z, why);
+                        return;
+                    }
+                }
+            }
+        };
+        c->workers.run(T, worker);
+        if (int why = abort_why.load()) {
+            quit_all();
+            if (why == 1)
+                return fail(c, ZKH_EDEV, "persistent round loop: %s", hipGetErrorString((hipError_t)dev_err.load()));
+            return fail(c, ZKH_EDEV, "persistent round loop stopped (%s; clock %llu kHz)",
+                        why == 2 ? "a block timed out" : why == 4 ? "stream idle before the last round" : "no progress",
+                        (unsigned long long)c->clock_khz);
+        }
+        c->ring_off = 0;  // every launch before the round loop has completed
+        stamp("round loops done");
+        if (tracing) {
+            fprintf(stderr, "[zkh] mm persistent rounds: %.1f us (%d host threads)\n", now_us() - t_start, T);
+            const double tick_us = 1000.0 / (double)c->clock_khz;
+            for (uint32_t j = 0; j < nj; j++) {  // per round: block compute, then publish -> next challenge
+                const auto& g = tr_gpu[j];
+                fprintf(stderr, "[zkh]   job %u (n=%u, %u blocks): gpu round us", j, J[j].INp, 1u << lgnb[j]);
+                for (size_t r = 1; r + 1 < g.size() / 2 + 1 && 2 * r + 1 < g.size(); r++)
+                    fprintf(stderr, " %.1f/%.1f", (g[2 * r] - g[2 * r + 1]) * tick_us,
+                            (g[2 * r + 1] - g[2 * r - 2]) * tick_us);
+                fprintf(stderr, "\n");
+            }
+        }
+        if (c->prof) prof_resolve_ready(c);
+        return first_rc;
+    }
+
+    // tables beyond the LDS loop: one launch and one synchronisation per round for all jobs
     HIPCHK(c, hipStreamSynchronize(c->stream));
     c->ring_off = 0;
     if (c->prof) prof_resolve(c);
-    for (uint32_t j = 0; j < nj; j++) {
-        Job& q = J[j];
-        Fr s = kZero;
-        for (uint32_t b = 0; b < q.dot_blocks; b++) s = fr_add(s, fr_load(pin + pin_claim + 8 * (size_t)(q.dot_slot + b)));
-        q.claim = q.cur = s;
-        tr_absorb_fr(jobs[j].transcript, "claim", s);
-        q.xs.resize(q.L);
-    }
-    // 4) rounds (zkob_fc.cu:294-332): one launch and one synchronisation per round for all jobs
-    const Fr two = fr_u64(2), four = fr_u64(4);
+    for (uint32_t j = 0; j < nj; j++) absorb_claim(j);
     uint32_t maxL = 0;
     for (auto& q : J) maxL = std::max(maxL, q.L);
     std::vector<ZkipDesc> zk(nj);
@@ -1242,9 +1634,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         zk[j].b_lo = red.lo() + 4 * (J[j].red_off + J[j].INp);
         zk[j].b_hi = red.hi() + 4 * (J[j].red_off + J[j].INp);
     }
-    double tr_t0 = now_us();
     for (uint32_t r = 0; r < maxL; r++) {
-        double t_a = now_us();
         std::vector<ZkipDesc> act;
         std::vector<uint32_t> who;
         uint32_t blocks = 0;
@@ -1274,43 +1664,16 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         for (size_t a = 0; a < act.size(); a++) bt.d[a] = act[a];
         bt.nd = (uint32_t)act.size();
         Publish pb = make_pub(c, bt.nd);
-        double t_b = now_us();
         {
             ProfScope ps(c, "zkip_round", bytes);
             launch_zkip_round_multi(c->stream, bt, blocks, pb);
         }
-        double t_c = now_us();
         if ((rc = wait_pub(c, pb.seq))) return rc;
-        double t_d = now_us();
-        if (trace_on())
-            fprintf(stderr, "[zkh] mm round %u: prep %.1f launch %.1f wait %.1f us (since start %.1f)\n", r,
-                    t_b - t_a, t_c - t_b, t_d - t_c, t_d - tr_t0);
         for (size_t a = 0; a < act.size(); a++) {
             uint32_t j = who[a];
-            Job& q = J[j];
             Fr s3[3];
             pub_read(c, (uint32_t)a, 3, s3);
-            Fr c0 = fix1(s3[0]), q1 = fix1(s3[1]), c2 = fix1(s3[2]);
-            Fr c1 = fr_sub(fr_sub(q1, c0), c2);
-            Fr p[3] = {c0, q1, fr_add(fr_add(c0, fr_mul(two, c1)), fr_mul(four, c2))};
-            if (!fr_eq(q.cur, fr_add(p[0], p[1]))) {
-                q.live = false;
-                jobs[j].status = ZKH_EROUND;
-                if (!first_rc)
-                    first_rc = fail(c, ZKH_EROUND,
-                                    "job %u: prover sumcheck round inconsistency (witness bug) at round %u", j, r);
-                continue;
-            }
-            uint8_t* tr = jobs[j].transcript;
-            tr_absorb_fr(tr, "p0", p[0]);
-            tr_absorb_fr(tr, "p1", p[1]);
-            tr_absorb_fr(tr, "p2", p[2]);
-            Fr x = tr_challenge(tr);
-            q.xs[r] = x;
-            if (jobs[j].ev_out)
-                for (int k = 0; k < 3; k++) fr_store(p[k], jobs[j].ev_out + 8 * (3 * r + k));
-            q.cur = fr_lagrange3(p, x);
-            fr_store(fr_to_mont(x), zk[j].vm.v);
+            if (round_step(j, r, fix1(s3[0]), fix1(s3[1]), fix1(s3[2]))) fr_store(J[j].xm, zk[j].vm.v);
         }
     }
     // 5) final binds and terminals (written to pinned memory by the kernel)
@@ -1334,29 +1697,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         c->ring_off = 0;
         if (c->prof) prof_resolve(c);
     }
-    for (uint32_t j : fwho) {
-        Job& q = J[j];
-        zkh_mm_job& in = jobs[j];
-        Fr cx = fr_load(pin + pin_term + (size_t)j * 16), cw = fr_load(pin + pin_term + (size_t)j * 16 + 8);
-        if (!fr_eq(q.cur, fr_mul(cx, cw))) {
-            in.status = ZKH_EROUND;
-            if (!first_rc) first_rc = fail(c, ZKH_EROUND, "job %u: terminal product mismatch (witness bug)", j);
-            continue;
-        }
-        tr_absorb_fr(in.transcript, "claim_X", cx);
-        tr_absorb_fr(in.transcript, "claim_W", cw);
-        if (in.claims_out) {
-            fr_store(q.claim, in.claims_out);
-            fr_store(cx, in.claims_out + 8);
-            fr_store(cw, in.claims_out + 16);
-        }
-        if (in.u_batch_out)
-            for (uint32_t i = 0; i < q.lb; i++) fr_store(q.ub[i], in.u_batch_out + 8 * i);
-        if (in.u_output_out)
-            for (uint32_t i = 0; i < q.lo; i++) fr_store(q.uo[i], in.u_output_out + 8 * i);
-        if (in.u_input_out)
-            for (uint32_t i = 0; i < q.L; i++) fr_store(q.xs[q.L - 1 - i], in.u_input_out + 8 * i);
-    }
+    for (uint32_t j : fwho)
+        finish(j, fr_load(pin + pin_term + (size_t)j * 16), fr_load(pin + pin_term + (size_t)j * 16 + 8));
     return first_rc;
 }
 
