@@ -146,11 +146,6 @@ __global__ void k_planes_to_aos(const uint4* lo, const uint4* hi, uint32_t n, ui
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
         st_aos(aos, i, ld_fr(lo, hi, i));
 }
-__global__ void k_zero_planes(uint4* lo, uint4* hi, uint32_t from, uint32_t to) {
-    for (uint32_t i = from + blockIdx.x * blockDim.x + threadIdx.x; i < to;
-         i += gridDim.x * blockDim.x)
-        st_fr(lo, hi, i, fr_zero());
-}
 __global__ void k_absmax_i32(const int32_t* __restrict__ in, uint32_t n, uint32_t* out) {
     uint32_t m = 0;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
@@ -212,10 +207,6 @@ void launch_planes_to_aos(hipStream_t s, DevPlanes in, uint32_t n, uint32_t* aos
     if (!n) return;
     k_planes_to_aos<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(in), PL_HI(in), n, aos);
 }
-void launch_zero_planes(hipStream_t s, DevPlanes t, uint32_t from, uint32_t to) {
-    if (to <= from) return;
-    k_zero_planes<<<grid_for(to - from, NT, 8192), NT, 0, s>>>(PL_LO(t), PL_HI(t), from, to);
-}
 void launch_absmax_i32(hipStream_t s, const int32_t* in, uint32_t n, uint32_t* out) {
     if (!n) return;
     k_absmax_i32<<<grid_for(n, NT * 8, 2048), NT, 0, s>>>(in, n, out);
@@ -242,94 +233,8 @@ __global__ void k_eq_mont(const uint32_t* __restrict__ fac, uint32_t K, uint32_t
     for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < n; b += gridDim.x * blockDim.x)
         st_aos(out, b, eq_prod(fac, K, b));
 }
-__global__ void k_eq_planes(const uint32_t* __restrict__ fac, uint32_t K, uint32_t n, uint4* lo,
-                            uint4* hi) {
-    for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < n; b += gridDim.x * blockDim.x)
-        st_fr(lo, hi, b, mont_mul(eq_prod(fac, K, b), plain_one()));
-}
 void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, uint32_t* out) {
     k_eq_mont<<<grid_for(n, NT, 4096), NT, 0, s>>>(fac, K, n, out);
-}
-void launch_eq_planes(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, DevPlanes out) {
-    k_eq_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(fac, K, n, PL_LO(out), PL_HI(out));
-}
-
-// ------------------------------------------------------------------------------------
-// eq-weighted reductions of small-integer matrices.
-// Lane i owns output column i and walks rows k of its chunk; the eq weight e_k is the same
-// for every lane (uniform load).  Each integer (offset by 2^bits so it is non-negative) is
-// cut into 20-bit pieces; piece x limb products (< 2^52) accumulate in 64-bit columns
-// without carries for up to 2^11 rows, then one wide Montgomery reduction per piece folds
-// the column sums into the field.  E is in Montgomery form, so the reduction leaves the
-// plain sum.
-// ------------------------------------------------------------------------------------
-template <typename T, int NP>
-__global__ __launch_bounds__(NT) void k_eqdot(const T* __restrict__ M, uint32_t K, uint32_t N,
-                                              const uint32_t* __restrict__ E, uint32_t kchunk,
-                                              uint32_t bits, uint32_t* __restrict__ partial) {
-    const uint32_t i = blockIdx.x * NT + threadIdx.x;
-    const uint32_t c = blockIdx.y;
-    const uint32_t k0 = c * kchunk;
-    const uint32_t k1 = min(K, k0 + kchunk);
-    uint64_t acc[NP][8];
-#pragma unroll
-    for (int p = 0; p < NP; p++)
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc[p][j] = 0;
-    const int64_t off = (int64_t)1 << bits;
-    if (i < N) {
-        const T* col = M + i;
-        for (uint32_t k = k0; k < k1; k++) {
-            const fr_t e = ld_aos(E, k);
-            const uint64_t w = (uint64_t)((int64_t)col[(size_t)k * N] + off);
-#pragma unroll
-            for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (20 * p)) & 0xFFFFFu, e);
-        }
-    }
-    fr_t r = fr_zero();
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-        uint32_t t[10];
-        cols_normalize(acc[p], t);
-        fr_t f = redc_wide<10>(t);
-        if (p > 0) f = mont_mul(f, piece_scale(p));
-        r = fr_add(r, f);
-    }
-    if (i < N) st_aos(partial, (size_t)c * N + i, r);
-}
-template <typename T>
-static void eqdot_dispatch(hipStream_t s, const T* M, uint32_t K, uint32_t N, const uint32_t* E,
-                           uint32_t kchunk, uint32_t bits, uint32_t* partial) {
-    dim3 g((N + NT - 1) / NT, (K + kchunk - 1) / kchunk);
-    uint32_t np = (bits + 1 + 19) / 20;
-    if (np <= 1) k_eqdot<T, 1><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
-    else if (np == 2) k_eqdot<T, 2><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
-    else if (np == 3) k_eqdot<T, 3><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
-    else k_eqdot<T, 4><<<g, NT, 0, s>>>(M, K, N, E, kchunk, bits, partial);
-}
-void launch_eqdot_i32(hipStream_t s, const int32_t* M, uint32_t K, uint32_t N, const uint32_t* E,
-                      uint32_t kchunk, uint32_t bits, uint32_t* partial) {
-    eqdot_dispatch<int32_t>(s, M, K, N, E, kchunk, bits, partial);
-}
-void launch_eqdot_i64(hipStream_t s, const int64_t* M, uint32_t K, uint32_t N, const uint32_t* E,
-                      uint32_t kchunk, uint32_t bits, uint32_t* partial) {
-    eqdot_dispatch<int64_t>(s, M, K, N, E, kchunk, bits, partial);
-}
-__global__ void k_sum_chunks(const uint32_t* __restrict__ partial, uint32_t nch, uint32_t N,
-                             uint32_t Npad, fr_t corr, uint4* lo, uint4* hi) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < Npad; i += gridDim.x * blockDim.x) {
-        fr_t s = fr_zero();
-        if (i < N) {
-            for (uint32_t c = 0; c < nch; c++) s = fr_add(s, ld_aos(partial, (size_t)c * N + i));
-            s = fr_sub(s, corr);
-        }
-        st_fr(lo, hi, i, s);
-    }
-}
-void launch_sum_chunks(hipStream_t s, const uint32_t* partial, uint32_t nch, uint32_t N,
-                       uint32_t Npad, const uint32_t* corr, DevPlanes out) {
-    k_sum_chunks<<<grid_for(Npad, NT, 4096), NT, 0, s>>>(partial, nch, N, Npad, to_fr(corr),
-                                                       PL_LO(out), PL_HI(out));
 }
 
 // ------------------------------------------------------------------------------------
@@ -343,14 +248,6 @@ __global__ __launch_bounds__(NT) void k_dot_planes(const uint4* alo, const uint4
         acc[0] = fr_add(acc[0], mont_mul(ld_fr(alo, ahi, i), ld_fr(blo, bhi, i)));
     reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
-__global__ __launch_bounds__(NT) void k_dot_aos_planes(const uint32_t* __restrict__ a,
-                                                       const uint4* blo, const uint4* bhi,
-                                                       uint32_t n, uint32_t* partial) {
-    fr_t acc[1] = {fr_zero()};
-    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT)
-        acc[0] = fr_add(acc[0], mont_mul(ld_aos(a, i), ld_fr(blo, bhi, i)));
-    block_reduce_store<1>(acc, partial);
-}
 __global__ __launch_bounds__(NT) void k_sum_planes(const uint4* alo, const uint4* ahi, uint32_t n,
                                                    Publish pub) {
     fr_t acc[1] = {fr_zero()};
@@ -361,12 +258,6 @@ __global__ __launch_bounds__(NT) void k_sum_planes(const uint4* alo, const uint4
 uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub) {
     uint32_t g = grid_for(n, NT * 4, 1024);
     k_dot_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n, pub);
-    return g;
-}
-uint32_t launch_dot_aos_planes(hipStream_t s, const uint32_t* a, DevPlanes b, uint32_t n,
-                               uint32_t* partial) {
-    uint32_t g = grid_for(n, NT * 4, 1024);
-    k_dot_aos_planes<<<g, NT, 0, s>>>(a, PL_LO(b), PL_HI(b), n, partial);
     return g;
 }
 uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, Publish pub) {
@@ -475,31 +366,6 @@ __global__ void k_hadamard(const uint4* alo, const uint4* ahi, const uint4* blo,
 void launch_hadamard(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, DevPlanes out) {
     k_hadamard<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n,
                                                     PL_LO(out), PL_HI(out));
-}
-
-// ------------------------------------------------------------------------------------
-// matmul (zkip) sumcheck round (zkfc.cu:94-127 poly + reduce, fused)
-// ------------------------------------------------------------------------------------
-__global__ __launch_bounds__(NT) void k_zkip_round(TabDev a, TabDev b, uint32_t n, int fold,
-                                                   fr_t vm, uint32_t* partial) {
-    const uint32_t h = n >> 1;
-    fr_t acc[3] = {fr_zero(), fr_zero(), fr_zero()};
-    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
-        fr_t a0, a1, b0, b1;
-        load_pair(a, i, h, n, fold, vm, a0, a1);
-        load_pair(b, i, h, n, fold, vm, b0, b1);
-        acc[0] = fr_add(acc[0], mont_mul(a0, b0));
-        acc[1] = fr_add(acc[1], mont_mul(a1, b1));
-        acc[2] = fr_add(acc[2], mont_mul(fr_sub(a1, a0), fr_sub(b1, b0)));
-    }
-    block_reduce_store<3>(acc, partial);
-}
-uint32_t launch_zkip_round(hipStream_t s, Tab a, Tab b, uint32_t n, int fold,
-                           const uint32_t* v_m_host, uint32_t* partial) {
-    uint32_t g = grid_for(n >> 1, NT * 2, 512);
-    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
-    k_zkip_round<<<g, NT, 0, s>>>(tab_dev(a), tab_dev(b), n, fold, vm, partial);
-    return g;
 }
 
 // ------------------------------------------------------------------------------------
@@ -955,6 +821,15 @@ void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, ui
     k_eq_mont_multi<<<nblocks, NT, 0, s>>>(d_dev, nd);
 }
 
+// ------------------------------------------------------------------------------------
+// eq-weighted reductions of small-integer matrices.
+// Lane i owns output column i and walks rows k of its chunk; the eq weight e_k is the same
+// for every lane (uniform load).  Each integer (offset by 2^bits so it is non-negative) is
+// cut into 20-bit pieces; piece x limb products (< 2^52) accumulate in 64-bit columns
+// without carries for up to 2^11 rows, then one wide Montgomery reduction per piece folds
+// the column sums into the field.  E is in Montgomery form, so the reduction leaves the
+// plain sum.
+// ------------------------------------------------------------------------------------
 // uniform descriptor search: the last d[j] with d[j].blk_begin <= blockIdx.x (binary search
 // over scalar loads, so every field of the result stays in scalar registers)
 template <typename D>
@@ -1050,13 +925,20 @@ void launch_eqdot_multi(hipStream_t s, int is64, uint32_t np, const EqDotDesc* d
 // out[i] = sum_c partial[c*N+i] - corr (i < N; zero up to Npad), or, when E is set, the
 // block partial of sum_i E_m[i] * (sum_c partial[c*N+i] - corr) into dot[slot]
 __global__ __launch_bounds__(NT) void k_sum_chunks_multi(const SumChunksDesc* __restrict__ d, uint32_t nd) {
-    SumChunksDesc q;
-    find_desc(d, nd, q);
+    const SumChunksDesc& q = d[find_desc_uniform(d, nd)];
     const uint32_t local = blockIdx.x - q.blk_begin;
     const uint32_t i = local * NT + threadIdx.x;
     fr_t s = fr_zero();
     if (i < q.N) {
-        for (uint32_t c = 0; c < q.nch; c++) s = fr_add(s, ld_aos(q.partial, (size_t)c * q.N + i));
+        uint32_t c = 0;
+        for (; c + 4 <= q.nch; c += 4) {  // four chunk loads in flight
+            fr_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = ld_aos(q.partial, (size_t)(c + u) * q.N + i);
+#pragma unroll
+            for (int u = 0; u < 4; u++) s = fr_add(s, v[u]);
+        }
+        for (; c < q.nch; c++) s = fr_add(s, ld_aos(q.partial, (size_t)c * q.N + i));
         s = fr_sub(s, to_fr(q.corr.v));
     }
     if (q.E) {
@@ -1195,32 +1077,34 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
     uint64_t t_cmd = 0;
     for (; m > 1; r++) {
         const uint32_t h = m >> 1;
-        fr_t acc = fr_zero();
-        for (uint32_t k = gt; w < 3 && k < h; k += NPG) {
-            fr_t x, y;
-            if (w == 0) {
-                x = ld_fr(alo, ahi, k);
-                y = ld_fr(blo, bhi, k);
-            } else if (w == 1) {
-                x = ld_fr(alo, ahi, k + h);
-                y = ld_fr(blo, bhi, k + h);
-            } else {
-                x = fr_sub(ld_fr(alo, ahi, k + h), ld_fr(alo, ahi, k));
-                y = fr_sub(ld_fr(blo, bhi, k + h), ld_fr(blo, bhi, k));
+        // waves without pairs this round skip the products and the wave reduction
+        if (w < 3 && (wv - 5 * w) * 64 < h) {
+            fr_t acc = fr_zero();
+            for (uint32_t k = gt; k < h; k += NPG) {
+                fr_t x, y;
+                if (w == 0) {
+                    x = ld_fr(alo, ahi, k);
+                    y = ld_fr(blo, bhi, k);
+                } else if (w == 1) {
+                    x = ld_fr(alo, ahi, k + h);
+                    y = ld_fr(blo, bhi, k + h);
+                } else {
+                    x = fr_sub(ld_fr(alo, ahi, k + h), ld_fr(alo, ahi, k));
+                    y = fr_sub(ld_fr(blo, bhi, k + h), ld_fr(blo, bhi, k));
+                }
+                acc = fr_add(acc, mont_mul(x, y));
             }
-            acc = fr_add(acc, mont_mul(x, y));
+            acc = fr_wave_sum(acc);
+            if (lane == 0) red[wv] = acc;
         }
-        acc = fr_wave_sum(acc);
-        if (lane == 0 && wv < 15) red[wv] = acc;
         __syncthreads();
-        if (threadIdx.x == 0) {
-#pragma unroll 1
-            for (int g = 0; g < 3; g++) {
-                fr_t t = red[5 * g];
-#pragma unroll 1
-                for (int i = 1; i < 5; i++) t = fr_add(t, red[5 * g + i]);
-                st_aos(slot, g, t);
-            }
+        if (wv == 0 && lane < 3) {  // lane g adds group g's active waves
+            const uint32_t na = min(5u, (h + 63) >> 6);
+            fr_t t = red[5 * lane];
+            for (uint32_t i = 1; i < na; i++) t = fr_add(t, red[5 * lane + i]);
+            st_aos(slot, lane, t);
+        }
+        if (threadIdx.x == 0) {  // same wave as the stores above: the release covers them
             persist_stamp(slot, t_cmd);
             __hip_atomic_store(slot + 63, r + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             sok = persist_wait(q.cmd, r + 1, P.err, P.deadline);

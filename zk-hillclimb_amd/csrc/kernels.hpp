@@ -50,7 +50,6 @@ void launch_i32_to_planes(hipStream_t s, const int32_t* in, uint32_t n, DevPlane
 void launch_i64_to_planes(hipStream_t s, const int64_t* in, uint32_t n, DevPlanes out);
 void launch_aos_to_planes(hipStream_t s, const uint32_t* aos, uint32_t n, DevPlanes out);
 void launch_planes_to_aos(hipStream_t s, DevPlanes in, uint32_t n, uint32_t* aos);
-void launch_zero_planes(hipStream_t s, DevPlanes t, uint32_t from, uint32_t to);
 void launch_absmax_i32(hipStream_t s, const int32_t* in, uint32_t n, uint32_t* out);
 void launch_absmax_i64(hipStream_t s, const int64_t* in, uint32_t n, unsigned long long* out);
 void launch_transpose_i32(hipStream_t s, const int32_t* in, uint32_t rows, uint32_t cols,
@@ -59,26 +58,10 @@ void launch_transpose_i32(hipStream_t s, const int32_t* in, uint32_t rows, uint3
 // ---- eq tables ----
 // out[b] = prod_t fac[2t + bit_t(b)] (Montgomery form) for b < n, AoS; K = #factors
 void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, uint32_t* out);
-// plain eq table into planes
-void launch_eq_planes(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, DevPlanes out);
-
-// ---- eq-weighted reductions of integer matrices ----
-// partial[c*N + i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) * e_k   (plain, AoS)
-// E: Montgomery-form AoS eq table over k.  Chunks of kchunk <= 2048 rows.
-void launch_eqdot_i32(hipStream_t s, const int32_t* M, uint32_t K, uint32_t N, const uint32_t* E,
-                      uint32_t kchunk, uint32_t bits, uint32_t* partial);
-void launch_eqdot_i64(hipStream_t s, const int64_t* M, uint32_t K, uint32_t N, const uint32_t* E,
-                      uint32_t kchunk, uint32_t bits, uint32_t* partial);
-// out[i] = sum_c partial[c*N+i] - corr for i < N, 0 for N <= i < Npad
-void launch_sum_chunks(hipStream_t s, const uint32_t* partial, uint32_t nch, uint32_t N,
-                       uint32_t Npad, const uint32_t* corr, DevPlanes out);
 
 // ---- dot products / sums (block partials, AoS, summed on the host) ----
 // partial[b] = sum montmul(a_i, b_i) over the block's range (carries 2^-256)
 uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub);
-// partial[b] = sum montmul(Eaos_i, b_i)
-uint32_t launch_dot_aos_planes(hipStream_t s, const uint32_t* a, DevPlanes b, uint32_t n,
-                               uint32_t* partial);
 uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, Publish pub);
 
 // ---- generic MLE pieces ----
@@ -94,12 +77,6 @@ void launch_fold(hipStream_t s, Tab t, uint32_t h, const uint32_t* v_m_host);
 void launch_axpy(hipStream_t s, DevPlanes a, const uint32_t* c_m_host, DevPlanes b, uint32_t n,
                  DevPlanes out);
 void launch_hadamard(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, DevPlanes out);
-
-// ---- matmul sumcheck round: pairs (i, i+n/2) of tables a, b of size n ----
-// fold != 0: the buffers hold the previous round's tables (size 2n) and are folded in
-// place with v first.  partial per block: sum a0b0, sum a1b1, sum da*db (2^-256 each).
-uint32_t launch_zkip_round(hipStream_t s, Tab a, Tab b, uint32_t n, int fold,
-                           const uint32_t* v_m_host, uint32_t* partial);
 
 // ---- logUp ----
 void launch_lu_count_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
@@ -158,7 +135,7 @@ struct EqTabDesc {  // eq table over K variables, n entries, AoS out (Montgomery
 // out[b] = tlo_m[b mod 2^klo] * thi_p[b >> klo]: the plain eq table from two small ones
 void launch_eq_outer(hipStream_t s, const uint32_t* tlo_m, const uint32_t* thi_p, uint32_t klo,
                      uint32_t n, DevPlanes out);
-struct EqDotDesc {  // partial[c*N+i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) e_k
+struct EqDotDesc {  // partial[c*N+i] = sum_{k in rows [c*kchunk, (c+1)*kchunk)} (M[k*N+i] + 2^bits) e_k
     const void* M;
     const uint32_t* E;
     uint32_t* partial;

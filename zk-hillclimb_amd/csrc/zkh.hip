@@ -1227,9 +1227,12 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             uint32_t K = what == 2 ? in.OUT : in.B;
             uint32_t N = what == 0 ? in.OUT : in.IN;
             uint32_t bits = what == 0 ? in.Y->bits : what == 1 ? in.X->bits : in.W->bits;
-            uint32_t nch = std::max<uint32_t>(1, (131072 + N - 1) / N);
-            uint32_t kchunk = std::min<uint32_t>(std::max<uint32_t>((K + nch - 1) / nch, 16), 2048);
-            nch = (K + kchunk - 1) / kchunk;
+            // row chunks of 128..2048 rows: up to 2^17 (column, chunk) cells per reduction
+            // spread it over the CUs, and at least 128 rows per chunk keep the per-cell field
+            // reduction (and the partials' traffic) small next to the streamed rows
+            const uint32_t ncell = std::max<uint32_t>(1, (131072 + N - 1) / N);
+            const uint32_t kchunk = std::min<uint32_t>(std::max<uint32_t>((K + ncell - 1) / ncell, 128), 2048);
+            const uint32_t nch = (K + kchunk - 1) / kchunk;
             r.d.M = M;
             r.d.E = eq_d + 8 * (what == 2 ? q.eo_off : q.eb_off);
             r.d.K = K;
