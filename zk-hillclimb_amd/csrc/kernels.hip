@@ -537,14 +537,11 @@ void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 // ------------------------------------------------------------------------------------
 struct EqDev {
     const uint32_t* elo;
-    const uint32_t* fac;
+    const uint32_t* ehi;
     uint32_t K;
 };
-ZDEV fr_t eq_hi(const EqDev& eq, uint32_t row) {
-    fr_t e = one_m();
-    for (uint32_t t = 10; t < eq.K; t++) e = mont_mul(e, ld_aos(eq.fac, 2 * t + ((row >> (t - 10)) & 1)));
-    return e;
-}
+// device weight of index i (see EqW)
+ZDEV fr_t eq_w(const EqDev& eq, uint32_t i) { return mont_mul(ld_aos(eq.elo, i & 1023), ld_aos(eq.ehi, i >> 10)); }
 
 // phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
 // acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
@@ -554,16 +551,12 @@ __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n
     fr_t acc[5];
 #pragma unroll
     for (int k = 0; k < 5; k++) acc[k] = fr_zero();
-    const uint32_t rows = (h + 1023) >> 10;
-    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        const fr_t ehi = eq_hi(eq, row);
-        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
-            const uint32_t i = (row << 10) + lo;
-            if (i >= h) break;
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        {
             fr_t a0, a1, s0, s1;
             load_pair(A, i, h, n, fold, vm, a0, a1);
             load_pair(S, i, h, n, fold, vm, s0, s1);
-            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+            const fr_t w = eq_w(eq, i);
             s0 = fr_add(s0, beta);
             s1 = fr_add(s1, beta);
             const fr_t wa0 = mont_mul(w, a0);
@@ -581,10 +574,9 @@ __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
                           Publish partial) {
-    uint32_t rows = ((n >> 1) + 1023) >> 10;
-    uint32_t g = rows < 1024 ? rows : 1024;
+    const uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
-    EqDev e{eq.elo, eq.fac, eq.K};
+    EqDev e{eq.elo, eq.ehi, eq.K};
     k_lu_phase1<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, fold, vm, to_fr(beta_host), e, partial);
     return g;
 }
@@ -599,19 +591,15 @@ __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, 
     fr_t acc[11];
 #pragma unroll
     for (int k = 0; k < 11; k++) acc[k] = fr_zero();
-    const uint32_t rows = (h + 1023) >> 10;
-    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        const fr_t ehi = eq_hi(eq, row);
-        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
-            const uint32_t i = (row << 10) + lo;
-            if (i >= h) break;
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        {
             fr_t a0, a1, s0, s1, b0, b1, t0, t1, m0, m1;
             load_pair(A, i, h, n, fold_as, vm, a0, a1);
             load_pair(S, i, h, n, fold_as, vm, s0, s1);
             load_pair(B, i, h, n, fold_btm, vm, b0, b1);
             load_pair(T, i, h, n, fold_btm, vm, t0, t1);
             load_pair(m, i, h, n, fold_btm, vm, m0, m1);
-            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+            const fr_t w = eq_w(eq, i);
             s0 = fr_add(s0, beta);
             s1 = fr_add(s1, beta);
             t0 = fr_add(t0, beta);
@@ -645,10 +633,9 @@ __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, 
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
                           EqW eq, Publish partial) {
-    uint32_t rows = ((n >> 1) + 1023) >> 10;
-    uint32_t g = rows < 1024 ? rows : 1024;
+    const uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
-    EqDev e{eq.elo, eq.fac, eq.K};
+    EqDev e{eq.elo, eq.ehi, eq.K};
     k_lu_phase2<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), tab_dev(m), n,
                                  fold_as, fold_btm, vm, to_fr(beta_host), e, partial);
     return g;
@@ -692,16 +679,12 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
                                                     EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
     fr_t acc[4] = {fr_zero(), fr_zero(), fr_zero(), fr_zero()};
-    const uint32_t rows = (h + 1023) >> 10;
-    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        const fr_t ehi = eq_hi(eq, row);
-        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
-            const uint32_t i = (row << 10) + lo;
-            if (i >= h) break;
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        {
             fr_t s0, s1, u0, u1;
             load_pair(S, i, h, n, fold, vm, s0, s1);
             load_pair(U, i, h, n, fold, vm, u0, u1);
-            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+            const fr_t w = eq_w(eq, i);
             const fr_t ws0 = mont_mul(w, s0);
             const fr_t wds = mont_mul(w, fr_sub(s1, s0));
             const fr_t du = fr_sub(u1, u0);
@@ -720,10 +703,9 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, EqW eq, Publish partial) {
-    uint32_t rows = ((n >> 1) + 1023) >> 10;
-    uint32_t g = rows < 1024 ? rows : 1024;
+    const uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
-    EqDev e{eq.elo, eq.fac, eq.K};
+    EqDev e{eq.elo, eq.ehi, eq.K};
     k_hp_eq_round<<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, e, partial);
     return g;
 }
@@ -732,13 +714,9 @@ __global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* sh
                                                const uint4* uhi, int has_u, uint32_t n, EqDev eq,
                                                Publish pub) {
     fr_t acc[1] = {fr_zero()};
-    const uint32_t rows = (n + 1023) >> 10;
-    for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        const fr_t ehi = eq_hi(eq, row);
-        for (uint32_t lo = threadIdx.x; lo < 1024; lo += NT) {
-            const uint32_t i = (row << 10) + lo;
-            if (i >= n) break;
-            const fr_t w = mont_mul(ld_aos(eq.elo, lo), ehi);
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
+        {
+            const fr_t w = eq_w(eq, i);
             fr_t ws = mont_mul(w, ld_fr(slo, shi, i));
             if (has_u) ws = mont_mul(ws, ld_fr(ulo, uhi, i));
             acc[0] = fr_add(acc[0], ws);
@@ -748,9 +726,8 @@ __global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* sh
 }
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish partial) {
-    uint32_t rows = (n + 1023) >> 10;
-    uint32_t g = rows < 1024 ? rows : 1024;
-    EqDev e{eq.elo, eq.fac, eq.K};
+    const uint32_t g = grid_for(n, NT, 1024);
+    EqDev e{eq.elo, eq.ehi, eq.K};
     k_eq_sum<<<g, NT, 0, s>>>(PL_LO(S), PL_HI(S), U ? PL_LO(*U) : nullptr, U ? PL_HI(*U) : nullptr,
                               U ? 1 : 0, n, e, partial);
     return g;

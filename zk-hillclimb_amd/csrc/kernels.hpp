@@ -36,13 +36,15 @@ struct Tab {
     DevPlanes dst;
 };
 
-// One eq weighting: eq(i, u[0..K)) = Elo[i & 1023] * Ehi(i >> 10) with Elo built over
-// u[0..10) and Ehi over u[10..K) from the Montgomery factor table fac (fac[2t] = mont(1-u_t),
-// fac[2t+1] = mont(u_t)).  When K < 10 the caller supplies the correction factor on the host.
+// One eq weighting over the first 2^K indices: the device weight of index i is
+// Elo[i & 1023] * Ehi[i >> 10], with Elo the eq table of u[0..10) and Ehi that of
+// u[10..kmax) (both Montgomery form, built once per proof; missing variables count as
+// u_t = 0).  For i < 2^K this is eq(i, u[0..K)) * prod_{t=K}^{kmax-1} (1 - u_t); the host
+// multiplies each round's sums by the inverse of that product.
 struct EqW {
-    const uint32_t* elo;  // AoS, 1024 entries, Montgomery form
-    const uint32_t* fac;  // AoS, 2 per variable, Montgomery form
-    uint32_t K;           // number of variables of this weighting
+    const uint32_t* elo;  // AoS, 1024 entries
+    const uint32_t* ehi;  // AoS, 2^(kmax-10) entries (one entry when kmax <= 10)
+    uint32_t K;           // variables of this round's weighting
 };
 
 // ---- conversions / layout ----

@@ -253,6 +253,7 @@ enum {
     SL_SMALL,
     SL_FAC,
     SL_ELO,
+    SL_EHI,
     SL_EB,
     SL_EO,
     SL_TMP0,
@@ -439,43 +440,42 @@ static Fr eq_prefix_sum(const std::vector<Fr>& u, uint64_t K) {
     return sum;
 }
 
-// eq weighting state for the Elo/Ehi kernels: Elo over u[0..10) (padded) and the full
-// factor table; corr[K] undoes the padded factors when K < 10
+// eq weighting state for the Elo/Ehi kernels (EqW): Elo over u[0..10), Ehi over
+// u[10..kmax), kmax = max(|u|, 10); corr[K] = 1/prod_{t=K}^{kmax-1}(1 - u_t) turns the
+// device weights of the first 2^K indices into eq(i, u[0..K)).
 struct EqState {
-    uint32_t* fac_d = nullptr;
     uint32_t* elo_d = nullptr;
-    std::vector<Fr> corr;  // corr[K] for K = 0..10
+    uint32_t* ehi_d = nullptr;
+    std::vector<Fr> corr;  // corr[K] for K = 0..kmax
     uint32_t nvars = 0;
 };
-static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, int slot_fac, int slot_elo) {
+static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st) {
     int rc = 0;
     std::vector<uint32_t> fac;
     make_fac(u, 10, fac);
     st.nvars = (uint32_t)u.size();
-    st.fac_d = (uint32_t*)scratch(c, slot_fac, fac.size() * 4, &rc);
+    const uint32_t kmax = std::max<uint32_t>(st.nvars, 10), khi = kmax - 10;
+    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, fac.size() * 4, &rc);
     if (rc) return rc;
-    st.elo_d = (uint32_t*)scratch(c, slot_elo, 1024 * 32, &rc);
+    st.elo_d = (uint32_t*)scratch(c, SL_ELO, 1024 * 32, &rc);
     if (rc) return rc;
-    if ((rc = upload(c, st.fac_d, fac.data(), fac.size() * 4))) return rc;
-    launch_eq_mont(c->stream, st.fac_d, 10, 1024, st.elo_d);
-    // Z_K = prod_{t=K}^{9} (1 - u_t) (padded u_t = 0); corr[K] = 1/Z_K
-    Fr z[11];
-    z[10] = kOne;
-    for (int t = 9; t >= 0; t--) {
-        Fr om = t < (int)u.size() ? fr_sub(kOne, u[t]) : kOne;
-        z[t] = fr_mul(z[t + 1], om);
-    }
-    if (fr_eq(z[0], kZero)) return fail(c, ZKH_EARG, "degenerate eq challenge (u_t = 1)");
-    Fr iz0 = fr_inv(z[0]);
-    st.corr.assign(11, kOne);
-    Fr pre = kOne;  // prod_{t<K} (1-u_t)
-    for (int K = 0; K <= 10; K++) {
-        st.corr[K] = fr_mul(iz0, pre);  // 1/Z_K = prod_{t<K}(1-u_t) / Z_0
-        if (K < 10) pre = fr_mul(pre, K < (int)u.size() ? fr_sub(kOne, u[K]) : kOne);
-    }
+    st.ehi_d = (uint32_t*)scratch(c, SL_EHI, ((size_t)32 << khi), &rc);
+    if (rc) return rc;
+    if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
+    launch_eq_mont(c->stream, fac_d, 10, 1024, st.elo_d);
+    launch_eq_mont(c->stream, fac_d + 2 * 10 * 8, khi, 1u << khi, st.ehi_d);
+    // prefix[K] = prod_{t<K} (1 - u_t); corr[K] = prefix[K] / prefix[kmax]
+    std::vector<Fr> prefix(kmax + 1);
+    prefix[0] = kOne;
+    for (uint32_t t = 0; t < kmax; t++)
+        prefix[t + 1] = fr_mul(prefix[t], t < st.nvars ? fr_sub(kOne, u[t]) : kOne);
+    if (fr_eq(prefix[kmax], kZero)) return fail(c, ZKH_EARG, "degenerate eq challenge (u_t = 1)");
+    const Fr inv = fr_inv(prefix[kmax]);
+    st.corr.resize(kmax + 1);
+    for (uint32_t K = 0; K <= kmax; K++) st.corr[K] = fr_mul(prefix[K], inv);
     return 0;
 }
-static Fr eq_corr(const EqState& st, uint32_t K) { return K >= 10 ? kOne : st.corr[K]; }
+static Fr eq_corr(const EqState& st, uint32_t K) { return st.corr[K]; }
 
 static std::vector<Fr> load_frs(const uint32_t* p, uint32_t n) {
     std::vector<Fr> v(n);
@@ -807,13 +807,13 @@ static int eq_weighted_sum(zkh_ctx* c, DevPlanes S, const DevPlanes* U, uint32_t
                            const std::vector<Fr>& u, Fr* out) {
     int rc = 0;
     EqState st;
-    if ((rc = eq_setup(c, u, st, SL_FAC, SL_ELO))) return rc;
+    if ((rc = eq_setup(c, u, st))) return rc;
     uint32_t K = (uint32_t)u.size();
     uint32_t nb;
     {
         ProfScope ps(c, "eq_sum", (double)n * (U ? 64 : 32));
         Publish pb = make_pub(c, 1);
-        nb = launch_eq_sum(c->stream, S, U, n, EqW{st.elo_d, st.fac_d, K}, pb);
+        nb = launch_eq_sum(c->stream, S, U, n, EqW{st.elo_d, st.ehi_d, K}, pb);
         (void)nb;
         if ((rc = wait_pub(c, pb.seq))) return rc;
     }
@@ -1331,9 +1331,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         ProfScope ps(c, "eq_tables", (double)eq_total * 32);
         launch_eq_mont_multi(c->stream, (const EqTabDesc*)(desc_d + o_eq), (uint32_t)eqd.size(), eq_blocks);
     }
-    double red_bytes = 0;
-    for (auto& r : reds)
-        red_bytes += (double)r.d.K * r.d.N * (r.is64 ? 8 : 4) + (double)r.nch * r.d.N * 32;
+    double red_bytes = 0;  // algorithmic: every stored integer of X, W and Y read once
+    for (auto& r : reds) red_bytes += (double)r.d.K * r.d.N * (r.is64 ? 8 : 4);
     {
         ProfScope ps(c, "eqdot", red_bytes);
         for (auto& g : groups)
@@ -1913,7 +1912,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
     Fr inv2 = fr_inv2();
 
     EqState eq;
-    if ((rc = eq_setup(c, u, eq, SL_FAC, SL_ELO))) return rc;
+    if ((rc = eq_setup(c, u, eq))) return rc;
 
     // table handles: source = current data, dst = working buffer
     DevPlanes a_src = Ac, s_src = Sc, b_src = Bw, t_src = Tc, m_src = mc;
@@ -1932,7 +1931,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
             Publish pb = make_pub(c, 1);
             {
                 ProfScope ps(c, "lu_phase1", (as_pending ? 3.0 * n : (double)n) * 2 * 32);
-                launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l, EqW{eq.elo_d, eq.fac_d, K}, pb);
+                launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l, EqW{eq.elo_d, eq.ehi_d, K}, pb);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -1957,7 +1956,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
                 ProfScope ps(c, "lu_phase2",
                              ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
                 launch_lu_phase2(c->stream, ta, ts, tb, tt, tm, n, as_pending, btm_pending, vm, beta_l,
-                                 EqW{eq.elo_d, eq.fac_d, K}, pb);
+                                 EqW{eq.elo_d, eq.ehi_d, K}, pb);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -2078,7 +2077,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     Uw = U->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP2, n / 2 + 1, &rc) : Uc;
     if (rc) return rc;
     EqState eq;
-    if (ueq && (rc = eq_setup(c, *ueq, eq, SL_FAC, SL_ELO))) return rc;
+    if (ueq && (rc = eq_setup(c, *ueq, eq))) return rc;
     Fr claim = fr_load(claim_l), cE = kOne;
     DevPlanes e_src = Ec, s_src = Sc, u_src = Uc;
     uint32_t vm[8] = {0};
@@ -2104,7 +2103,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             {
                 ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
                 launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm,
-                                   EqW{eq.elo_d, eq.fac_d, K}, pb);
+                                   EqW{eq.elo_d, eq.ehi_d, K}, pb);
             }
             Fr s[4];
             if ((rc = wait_pub(c, pb.seq))) return rc;
