@@ -581,63 +581,77 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
     return g;
 }
 
-// phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused):
-// acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds; 3..5: sum w*b0*t0, w*b1*t1, w*db*dt (x 2^-256);
-// 6, 7: sum a0, sum a1; 8..10: sum m0*b0, m1*b1, dm*db (x 2^-256)
-__global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m,
-                                                  uint32_t n, int fold_as, int fold_btm, fr_t vm,
-                                                  fr_t beta, EqDev eq, Publish pub) {
+// phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused), split by table
+// group into two kernels that publish as jobs 0 and 1 of one round (each keeps its fold,
+// weights and sums in registers at a fraction of the single kernel's pressure):
+// job 0 (A, S): sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256), sum a0, sum a1  (s + beta)
+// job 1 (B, T, m): sum w*b0*t0, w*b1*t1, w*db*dt, m0*b0, m1*b1, dm*db (x 2^-256)  (t + beta)
+template <int fold>
+__global__ __launch_bounds__(NT) void k_lu_phase2_as(TabDev A, TabDev S, uint32_t n, fr_t vm, fr_t beta,
+                                                     EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
-    fr_t acc[11];
+    fr_t acc[5];
 #pragma unroll
-    for (int k = 0; k < 11; k++) acc[k] = fr_zero();
+    for (int k = 0; k < 5; k++) acc[k] = fr_zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
-        {
-            fr_t a0, a1, s0, s1, b0, b1, t0, t1, m0, m1;
-            load_pair(A, i, h, n, fold_as, vm, a0, a1);
-            load_pair(S, i, h, n, fold_as, vm, s0, s1);
-            load_pair(B, i, h, n, fold_btm, vm, b0, b1);
-            load_pair(T, i, h, n, fold_btm, vm, t0, t1);
-            load_pair(m, i, h, n, fold_btm, vm, m0, m1);
-            const fr_t w = eq_w(eq, i);
-            s0 = fr_add(s0, beta);
-            s1 = fr_add(s1, beta);
-            t0 = fr_add(t0, beta);
-            t1 = fr_add(t1, beta);
-            {
-                const fr_t wa0 = mont_mul(w, a0);
-                const fr_t wda = mont_mul(w, fr_sub(a1, a0));
-                const fr_t wa1 = fr_add(wa0, wda);
-                acc[0] = fr_add(acc[0], mont_mul(wa0, s0));
-                acc[1] = fr_add(acc[1], mont_mul(wa1, s1));
-                acc[2] = fr_add(acc[2], mont_mul(wda, fr_sub(s1, s0)));
-            }
-            const fr_t db = fr_sub(b1, b0);
-            {
-                const fr_t wb0 = mont_mul(w, b0);
-                const fr_t wdb = mont_mul(w, db);
-                const fr_t wb1 = fr_add(wb0, wdb);
-                acc[3] = fr_add(acc[3], mont_mul(wb0, t0));
-                acc[4] = fr_add(acc[4], mont_mul(wb1, t1));
-                acc[5] = fr_add(acc[5], mont_mul(wdb, fr_sub(t1, t0)));
-            }
-            acc[6] = fr_add(acc[6], a0);
-            acc[7] = fr_add(acc[7], a1);
-            acc[8] = fr_add(acc[8], mont_mul(m0, b0));
-            acc[9] = fr_add(acc[9], mont_mul(m1, b1));
-            acc[10] = fr_add(acc[10], mont_mul(fr_sub(m1, m0), db));
-        }
+        fr_t a0, a1, s0, s1;
+        load_pair(A, i, h, n, fold, vm, a0, a1);
+        load_pair(S, i, h, n, fold, vm, s0, s1);
+        const fr_t w = eq_w(eq, i);
+        __builtin_amdgcn_sched_barrier(0);
+        const fr_t wa0 = mont_mul(w, a0);
+        __builtin_amdgcn_sched_barrier(0);
+        const fr_t wda = mont_mul(w, fr_sub(a1, a0));
+        __builtin_amdgcn_sched_barrier(0);
+        acc[0] = fr_add(acc[0], mont_mul(wa0, fr_add(s0, beta)));
+        __builtin_amdgcn_sched_barrier(0);
+        acc[1] = fr_add(acc[1], mont_mul(fr_add(wa0, wda), fr_add(s1, beta)));
+        __builtin_amdgcn_sched_barrier(0);
+        acc[2] = fr_add(acc[2], mont_mul(wda, fr_sub(s1, s0)));
+        acc[3] = fr_add(acc[3], a0);
+        acc[4] = fr_add(acc[4], a1);
     }
-    reduce_publish<11>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+}
+template <int fold>
+__global__ __launch_bounds__(NT) void k_lu_phase2_btm(TabDev B, TabDev T, TabDev m, uint32_t n, fr_t vm,
+                                                      fr_t beta, EqDev eq, Publish pub) {
+    const uint32_t h = n >> 1;
+    fr_t acc[6];
+#pragma unroll
+    for (int k = 0; k < 6; k++) acc[k] = fr_zero();
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        fr_t b0, b1, t0, t1;
+        load_pair(B, i, h, n, fold, vm, b0, b1);
+        load_pair(T, i, h, n, fold, vm, t0, t1);
+        const fr_t db = fr_sub(b1, b0);
+        {
+            const fr_t w = eq_w(eq, i);
+            const fr_t wb0 = mont_mul(w, b0);
+            const fr_t wdb = mont_mul(w, db);
+            acc[0] = fr_add(acc[0], mont_mul(wb0, fr_add(t0, beta)));
+            acc[1] = fr_add(acc[1], mont_mul(fr_add(wb0, wdb), fr_add(t1, beta)));
+            acc[2] = fr_add(acc[2], mont_mul(wdb, fr_sub(t1, t0)));
+        }
+        fr_t m0, m1;
+        load_pair(m, i, h, n, fold, vm, m0, m1);
+        acc[3] = fr_add(acc[3], mont_mul(m0, b0));
+        acc[4] = fr_add(acc[4], mont_mul(m1, b1));
+        acc[5] = fr_add(acc[5], mont_mul(fr_sub(m1, m0), db));
+    }
+    reduce_publish<6>(acc, pub, 1, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
                           EqW eq, Publish partial) {
     const uint32_t g = grid_for(n >> 1, NT, 1024);
-    fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
+    const fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
-    k_lu_phase2<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), tab_dev(m), n,
-                                 fold_as, fold_btm, vm, to_fr(beta_host), e, partial);
+    const fr_t beta = to_fr(beta_host);
+    if (fold_as) k_lu_phase2_as<1><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, beta, e, partial);
+    else k_lu_phase2_as<0><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, beta, e, partial);
+    if (fold_btm) k_lu_phase2_btm<1><<<g, NT, 0, s>>>(tab_dev(B), tab_dev(T), tab_dev(m), n, vm, beta, e, partial);
+    else k_lu_phase2_btm<0><<<g, NT, 0, s>>>(tab_dev(B), tab_dev(T), tab_dev(m), n, vm, beta, e, partial);
     return g;
 }
 

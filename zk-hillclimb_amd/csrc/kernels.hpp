@@ -104,7 +104,8 @@ void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
                           Publish pub);
-// phase-2 round over A, S, B, T, m: 11 sums (see kernels.hip)
+// phase-2 round over A, S, B, T, m as two launches publishing jobs 0 (A, S: 5 sums) and
+// 1 (B, T, m: 6 sums) of `pub` (made for 2 jobs; see kernels.hip)
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
                           int fold_as, int fold_btm,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,

@@ -1951,7 +1951,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
             as_pending = true;
         } else {  // phase 2
             Tab ta{a_src, Aw}, ts{s_src, Sw}, tb{b_src, Bw}, tt{t_src, Tw}, tm{m_src, mw};
-            Publish pb = make_pub(c, 1);
+            Publish pb = make_pub(c, 2);
             {
                 ProfScope ps(c, "lu_phase2",
                              ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
@@ -1967,9 +1967,18 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
                 t_src = Tw;
                 m_src = mw;
             }
-            Fr s[11];
+            Fr s[11], sa[5], sb[6];
             if ((rc = wait_pub(c, pb.seq))) return rc;
-            pub_read(c, 0, 11, s);
+            pub_read(c, 0, 5, sa);
+            pub_read(c, 1, 6, sb);
+            // s: w*a*s sums 0..2, w*b*t sums 3..5, sum a0 / a1 6..7, m*b sums 8..10
+            for (int k = 0; k < 3; k++) {
+                s[k] = sa[k];
+                s[3 + k] = sb[k];
+                s[8 + k] = sb[3 + k];
+            }
+            s[6] = sa[3];
+            s[7] = sa[4];
             Fr qa0 = fr_mul(fix1(s[0]), corr), qa1 = fr_mul(fix1(s[1]), corr), qa2 = fr_mul(fix1(s[2]), corr);
             Fr qb0 = fr_mul(fix1(s[3]), corr), qb1 = fr_mul(fix1(s[4]), corr), qb2 = fr_mul(fix1(s[5]), corr);
             Fr coefBT = fr_mul(inv_ratio, alpha_sq);
