@@ -93,9 +93,15 @@ int zkh_multi_dim_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* us, cons
                      const uint32_t* shape, uint32_t ndim, uint32_t out[8]);
 /* build_eq_tensor(u) (zkob_lookup.cuh:245-265): E[b] = prod_i (b>>i&1 ? u_i : 1-u_i) */
 int zkh_eq_table(zkh_ctx* ctx, const uint32_t* u, uint32_t k, zkh_tensor** out);
-/* FrTensor::pad(shape) with zero fill (fr-tensor.cu:800-828) */
+/* FrTensor::partial_me(u, window) (fr-tensor.cu:512-516, :612-641): k LSB-first binds of
+ * the row index of a [rows, window] view (a partial last row reads as zero-filled);
+ * requires size > window * 2^(k-1); returns ceil(rows / 2^k) * window entries */
+int zkh_partial_me_window(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k,
+                          uint32_t window, zkh_tensor** out);
+/* FrTensor::pad(shape, pad_val) (fr-tensor.cu:800-828; fr-tensor.cuh:150): every
+ * dimension padded to a power of two, padding entries = pad_val (NULL: zero) */
 int zkh_pad(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* shape, uint32_t ndim,
-            zkh_tensor** out);
+            const uint32_t pad_val[8], zkh_tensor** out);
 /* k_fr_fold (zkob_lookup.cuh:35-41): in-place MSB fold t[i] += v*(t[i+h]-t[i]), n -> n/2 */
 int zkh_fold(zkh_ctx* ctx, zkh_tensor* t, const uint32_t v[8]);
 /* elementwise: out = a + c*b (FrTensor operator+ / operator* by scalar, e.g. the SwiGLU
@@ -143,6 +149,39 @@ typedef struct zkh_mm_job {
     int status;
 } zkh_mm_job;
 int zkh_mm_prove_batch(zkh_ctx* ctx, zkh_mm_job* jobs, uint32_t njobs);
+
+/* ---------------- inner-product sumchecks without a transcript (zkfc.cu) ----------------
+ * proof_out receives 3 Fr per round: the coefficients c0, c1, c2 of the round polynomial
+ * p(X) = c0 + c1 X + c2 X^2 (the reference's Polynomial, zkfc.cu:94-137); final_out the
+ * last claim.  ZKH_EROUND when a round's check fails (the reference's runtime_error). */
+/* zkip(claim, a, b, u, proof) (zkfc.cu:139-151): k = |u| <= ceilLog2(n) MSB-first rounds,
+ * u[k-1] binding first; tables of n entries, zero-filled to the next power of two */
+int zkh_zkip(zkh_ctx* ctx, const uint32_t claim[8], const zkh_tensor* a, const zkh_tensor* b,
+             const uint32_t* u, uint32_t k, uint32_t* proof_out, uint32_t final_out[8]);
+/* zkip_stacked(claim, A, B, uN, uD, vN, N, D, proof) (zkfc.cu:153-246): A, B are [N, D]
+ * row-major; kN = ceilLog2(N) eq(uN)-weighted rounds over the rows (checked against
+ * eq(uN.back(), X) * p), binding vN.back() first, then zkip over D with uD (kD entries) */
+int zkh_zkip_stacked(zkh_ctx* ctx, const uint32_t claim[8], const zkh_tensor* A, const zkh_tensor* B,
+                     const uint32_t* uN, uint32_t kN, const uint32_t* uD, uint32_t kD,
+                     const uint32_t* vN, uint32_t N, uint32_t D, uint32_t* proof_out,
+                     uint32_t final_out[8]);
+/* zkFCStacked::prove(u_num, v_num, u_batch, u_input, u_output, proof) (zkfc.cu:288-307):
+ * X num x B x IN, W num x IN x OUT (row-major, not from zkh_tensor_weights_i32), Y num x B x
+ * OUT, optional bias num x OUT (NULL: none).  Challenge counts are ceilLog2 of num, num, B,
+ * IN, OUT.  proof_out: 3*(ceilLog2 num + ceilLog2 IN) Fr; claims_out: claim, final claim.
+ * ZKH_EROUND when the final claim differs from X(v_num,u_batch,u_input)*W(v_num,u_input,u_output). */
+int zkh_fc_stacked_prove(zkh_ctx* ctx, const zkh_tensor* X, const zkh_tensor* W, const zkh_tensor* Y,
+                         const zkh_tensor* bias, uint32_t num, uint32_t B, uint32_t IN, uint32_t OUT,
+                         const uint32_t* u_num, const uint32_t* v_num, const uint32_t* u_batch,
+                         const uint32_t* u_input, const uint32_t* u_output, uint32_t* proof_out,
+                         uint32_t claims_out[16]);
+
+/* ---------------- rescaling witness (rescaling.cu:8-34, zkob_rescale.cu:83-86) ----------- */
+/* x = sf * q + rem with rem = ((x + sf/2) mod sf) - sf/2 (C remainder, made non-negative),
+ * q = (x - rem) / sf; x read through scalar_to_long for FR tensors (fr-tensor.cu:941-945).
+ * q_out, rem_out: new int64 tensors. */
+int zkh_rescale(zkh_ctx* ctx, const zkh_tensor* X, uint32_t sf, zkh_tensor** q_out,
+                zkh_tensor** rem_out);
 
 /* ---------------- logUp lookup (tlookup.cu, zkob_lookup.cuh, zkob_rescale.cu) ---------- */
 /* tLookupRange table (tlookup.cu:372-391): T[i] = low+i (i<len) else low+len-1, size N */

@@ -178,3 +178,82 @@ def hp_prove(st, claim, E, S, U, strict=True):
                            ctypes.c_uint32(n), ctypes.c_int(1 if strict else 0), _p(ev),
                            _p(term), _p(ws))
     return rc, dict(ev=ev[:4 * k], term=term, ws=ws[:k])
+
+
+def pad_val(t, shape, pad):
+    t = np.ascontiguousarray(t, dtype=np.uint32)
+    shp = np.array(shape, dtype=np.uint32)
+    total = 1
+    for s in shape:
+        total *= 1 << (int(s) - 1).bit_length() if s > 1 else 1
+    out = frs(total)
+    on = ctypes.c_uint32(0)
+    pv = np.ascontiguousarray(pad, dtype=np.uint32)
+    rc = lib().or_pad_val(_p(t), _p(shp), ctypes.c_uint32(len(shape)), _p(pv), _p(out), ctypes.byref(on))
+    return rc, out[:on.value]
+
+
+def partial_me_window(t, u, window):
+    t = np.ascontiguousarray(t, dtype=np.uint32)
+    u = np.ascontiguousarray(u, dtype=np.uint32).reshape(-1, 8)
+    out = frs(len(t) + window)
+    on = ctypes.c_uint32(0)
+    rc = lib().or_partial_me_window(_p(t), ctypes.c_uint32(len(t)), _p(u), ctypes.c_uint32(len(u)),
+                                    ctypes.c_uint32(window), _p(out), ctypes.byref(on))
+    return rc, out[:on.value]
+
+
+def _u(u):
+    u = np.ascontiguousarray(u, dtype=np.uint32).reshape(-1, 8)
+    return u if len(u) else frs(1)
+
+
+def zkip(claim, a, b, u):
+    k = len(u)
+    a, b = (np.ascontiguousarray(x, dtype=np.uint32) for x in (a, b))
+    proof, fin = frs(3 * k + 1), np.zeros(8, np.uint32)
+    rc = lib().or_zkip(_p(np.ascontiguousarray(claim, dtype=np.uint32)), _p(a), _p(b),
+                       ctypes.c_uint32(len(a)), _p(_u(u)), ctypes.c_uint32(k), _p(proof), _p(fin))
+    return rc, proof[:3 * k], fin
+
+
+def zkip_stacked(claim, A, B, uN, uD, vN, N, D):
+    kN, kD = len(uN), len(uD)
+    A, B = (np.ascontiguousarray(x, dtype=np.uint32) for x in (A, B))
+    proof, fin = frs(3 * (kN + kD) + 1), np.zeros(8, np.uint32)
+    rc = lib().or_zkip_stacked(_p(np.ascontiguousarray(claim, dtype=np.uint32)), _p(A), _p(B),
+                               _p(_u(uN)), ctypes.c_uint32(kN), _p(_u(uD)), ctypes.c_uint32(kD),
+                               _p(_u(vN)), ctypes.c_uint32(N), ctypes.c_uint32(D), _p(proof), _p(fin))
+    return rc, proof[:3 * (kN + kD)], fin
+
+
+def fc_stacked_prove(X, W, Y, bias, num, B, IN, OUT, u_num, v_num, u_batch, u_input, u_output):
+    X, W, Y = (np.ascontiguousarray(x, dtype=np.uint32) for x in (X, W, Y))
+    bp = None if bias is None else _p(np.ascontiguousarray(bias, dtype=np.uint32))
+    nr = len(u_num) + len(u_input)
+    proof, claims = frs(3 * nr + 1), frs(2)
+    rc = lib().or_fc_stacked_prove(_p(X), _p(W), _p(Y), bp, ctypes.c_uint32(num), ctypes.c_uint32(B),
+                                   ctypes.c_uint32(IN), ctypes.c_uint32(OUT),
+                                   *[_p(_u(x)) for x in (u_num, v_num, u_batch, u_input, u_output)],
+                                   _p(proof), _p(claims))
+    return rc, proof[:3 * nr], claims
+
+
+def scalar_to_long(x):
+    lib().or_scalar_to_long.restype = ctypes.c_int64
+    return lib().or_scalar_to_long(_p(np.ascontiguousarray(x, dtype=np.uint32)))
+
+
+def rescale(x, sf):
+    """x: int64 array or (n, 8) Fr array -> (rc, q, rem) as int64 arrays."""
+    x = np.asarray(x)
+    if x.dtype == np.uint32 and x.ndim == 2:
+        n = len(x)
+        q, r = np.zeros(n, np.int64), np.zeros(n, np.int64)
+        rc = lib().or_rescale_fr(_p(np.ascontiguousarray(x)), ctypes.c_uint32(n), ctypes.c_uint32(sf), _p(q), _p(r))
+    else:
+        x = np.ascontiguousarray(x, dtype=np.int64).reshape(-1)
+        n = len(x)
+        q, r = np.zeros(n, np.int64), np.zeros(n, np.int64)
+        rc = lib().or_rescale_i64(_p(x), ctypes.c_uint32(n), ctypes.c_uint32(sf), _p(q), _p(r))
+    return rc, q, r

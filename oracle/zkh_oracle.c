@@ -445,8 +445,8 @@ int or_multi_dim_me(const uint32_t* t, uint32_t n, const uint32_t* us, const uin
     return rc;
 }
 /* pad: last dimension to pow2 first, then recurse with it merged (fr-tensor.cu:809-828) */
-int or_pad(const uint32_t* t, const uint32_t* shape, uint32_t ndim, uint32_t* out,
-           uint32_t* out_n) {
+int or_pad_val(const uint32_t* t, const uint32_t* shape, uint32_t ndim, const uint32_t pad[8],
+               uint32_t* out, uint32_t* out_n) {
     if (ndim == 0 || ndim > 16) return 1;
     uint64_t total = 1;
     for (uint32_t d = 0; d < ndim; d++) total *= shape[d];
@@ -462,7 +462,7 @@ int or_pad(const uint32_t* t, const uint32_t* shape, uint32_t ndim, uint32_t* ou
         uint32_t* nxt = (uint32_t*)malloc(osz * 32 + 32);
         for (uint64_t g = 0; g < osz; g++) {
             uint64_t g0 = g / lastp, g1 = g % lastp;
-            if (g1 >= last) memset(nxt + 8 * g, 0, 32);
+            if (g1 >= last) memcpy(nxt + 8 * g, pad, 32); /* FrTensor_pad_kernel pad_val */
             else memcpy(nxt + 8 * g, cur + 8 * (g0 * last + g1), 32);
         }
         free(cur);
@@ -476,6 +476,11 @@ int or_pad(const uint32_t* t, const uint32_t* shape, uint32_t ndim, uint32_t* ou
     *out_n = (uint32_t)sz;
     free(cur);
     return 0;
+}
+int or_pad(const uint32_t* t, const uint32_t* shape, uint32_t ndim, uint32_t* out,
+           uint32_t* out_n) {
+    static const uint32_t zero[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    return or_pad_val(t, shape, ndim, zero, out, out_n);
 }
 /* eq table by doubling; bit i becomes the new top bit (zkob_lookup.cuh:202-209) */
 static fr* build_eq_fr(const fr* u, uint32_t k) {
@@ -883,4 +888,211 @@ int or_hp_prove(uint8_t s[32], const uint32_t claim_in[8], const uint32_t* Ein,
     }
     free(E); free(S); free(U);
     return rc;
+}
+
+/* ------------------------------------------------------------------------------ */
+/* zkip and zkip_stacked without a transcript: zkfc.cu:94-246, :288-307              */
+/* ------------------------------------------------------------------------------ */
+/* one round of zkip_stacked_poly_kernel / zkip_poly_kernel over [N, D] (rows n, n+no
+ * paired, rows >= N zero) followed by partial_me(u_, no, D).sum() of each output: the
+ * reference's two-step schedule (products into three tensors, then MLE reductions) */
+static void stk_poly(const fr* a, const fr* b, uint32_t N, uint32_t D, const fr* u_, uint32_t ku,
+                     fr p[3]) {
+    uint32_t no = (1u << ceil_log2(N)) >> 1;
+    size_t so = (size_t)no * D;
+    fr* o[3] = {falloc(so), falloc(so), falloc(so)};
+    for (size_t g = 0; g < so; g++) {
+        fr a0 = a[g], b0 = b[g];
+        fr a1 = g + so < (size_t)N * D ? sub(a[g + so], a0) : sub(ZERO, a0);
+        fr b1 = g + so < (size_t)N * D ? sub(b[g + so], b0) : sub(ZERO, b0);
+        o[0][g] = mul(a0, b0);
+        o[1][g] = add(mul(a0, b1), mul(a1, b0));
+        o[2][g] = mul(a1, b1);
+    }
+    for (int k = 0; k < 3; k++) {
+        if (ku) {
+            uint32_t on;
+            fr* r = partial_me_fr(o[k], (uint32_t)so, u_, ku, no, D, &on);
+            p[k] = sum_fr(r, on);
+            free(r);
+        } else {
+            p[k] = sum_fr(o[k], so);
+        }
+        free(o[k]);
+    }
+}
+/* zkip_stacked_reduce_kernel / zkip_reduce_kernel: a[g] = a0 + v (a1 - a0), g < no*D */
+static void stk_reduce(fr* a, fr* b, uint32_t N, uint32_t D, fr v) {
+    uint32_t no = (1u << ceil_log2(N)) >> 1;
+    size_t so = (size_t)no * D;
+    fr vm = mont(v);
+    for (size_t g = 0; g < so; g++) {
+        fr a1 = g + so < (size_t)N * D ? a[g + so] : ZERO;
+        fr b1 = g + so < (size_t)N * D ? b[g + so] : ZERO;
+        a[g] = add(a[g], mmul(vm, sub(a1, a[g])));
+        b[g] = add(b[g], mmul(vm, sub(b1, b[g])));
+    }
+}
+/* zkip (zkfc.cu:139-151): u.back() binds first; claim != p(0)+p(1) -> 2 */
+static int zkip_fr(fr* claim, fr* a, fr* b, uint32_t n, const fr* u, uint32_t k, fr* proof) {
+    uint32_t sz = n;
+    for (uint32_t r = 0; r < k; r++) {
+        fr p[3];
+        stk_poly(a, b, sz, 1, NULL, 0, p);
+        proof[3 * r] = p[0];
+        proof[3 * r + 1] = p[1];
+        proof[3 * r + 2] = p[2];
+        if (!feq(*claim, add(poly_eval(p, 2, ZERO), poly_eval(p, 2, ONE)))) return 2;
+        fr x = u[k - 1 - r];
+        *claim = poly_eval(p, 2, x);
+        stk_reduce(a, b, sz, 1, x);
+        sz = (1u << ceil_log2(sz)) >> 1;
+    }
+    return 0;
+}
+int or_zkip(const uint32_t claim[8], const uint32_t* a, const uint32_t* b, uint32_t n,
+            const uint32_t* u, uint32_t k, uint32_t* proof_out, uint32_t final_out[8]) {
+    if (!n || k > ceil_log2(n)) return 1;
+    fr* A = from_aos(a, n);
+    fr* B = from_aos(b, n);
+    fr* U = from_aos(u, k);
+    fr* pr = falloc(3 * (size_t)k);
+    fr c = ld(claim);
+    int rc = zkip_fr(&c, A, B, n, U, k, pr);
+    for (uint32_t i = 0; i < 3 * k; i++) st(proof_out + 8 * i, pr[i]);
+    if (!rc) st(final_out, c);
+    free(A); free(B); free(U); free(pr);
+    return rc;
+}
+/* zkip_stacked (zkfc.cu:230-246): q = eq(uN.back(), X) * p must satisfy claim = q(0)+q(1)
+ * (Polynomial::eq: 1 - u + (2u - 1) X, polynomial.cu:342-353); next claim p(vN.back()) */
+static int zkip_stacked_fr(fr* claim, fr* a, fr* b, uint32_t N, uint32_t D, const fr* uN,
+                           uint32_t kN, const fr* uD, uint32_t kD, const fr* vN, fr* proof) {
+    uint32_t n = N;
+    for (uint32_t r = 0; r < kN; r++) {
+        uint32_t ku = kN - 1 - r;
+        fr p[3];
+        stk_poly(a, b, n, D, uN, ku, p);
+        proof[3 * r] = p[0];
+        proof[3 * r + 1] = p[1];
+        proof[3 * r + 2] = p[2];
+        fr ul = uN[ku];
+        fr e[2] = {sub(ONE, ul), sub(add(ul, ul), ONE)};
+        fr q0 = mul(poly_eval(e, 1, ZERO), poly_eval(p, 2, ZERO));
+        fr q1 = mul(poly_eval(e, 1, ONE), poly_eval(p, 2, ONE));
+        if (!feq(*claim, add(q0, q1))) return 2;
+        fr v = vN[ku];
+        *claim = poly_eval(p, 2, v);
+        stk_reduce(a, b, n, D, v);
+        n = (1u << ceil_log2(n)) >> 1;
+    }
+    return zkip_fr(claim, a, b, D, uD, kD, proof + 3 * kN);
+}
+int or_zkip_stacked(const uint32_t claim[8], const uint32_t* a, const uint32_t* b,
+                    const uint32_t* uN, uint32_t kN, const uint32_t* uD, uint32_t kD,
+                    const uint32_t* vN, uint32_t N, uint32_t D, uint32_t* proof_out,
+                    uint32_t final_out[8]) {
+    if (!N || !D || kN != ceil_log2(N) || kD > ceil_log2(D)) return 1;
+    size_t n = (size_t)N * D;
+    fr* A = from_aos(a, n);
+    fr* B = from_aos(b, n);
+    fr* UN = from_aos(uN, kN);
+    fr* VN = from_aos(vN, kN);
+    fr* UD = from_aos(uD, kD);
+    fr* pr = falloc(3 * (size_t)(kN + kD));
+    fr c = ld(claim);
+    int rc = zkip_stacked_fr(&c, A, B, N, D, UN, kN, UD, kD, VN, pr);
+    for (uint32_t i = 0; i < 3 * (kN + kD); i++) st(proof_out + 8 * i, pr[i]);
+    if (!rc) st(final_out, c);
+    free(A); free(B); free(UN); free(VN); free(UD); free(pr);
+    return rc;
+}
+/* zkFCStacked::prove (zkfc.cu:288-307) on field inputs */
+int or_fc_stacked_prove(const uint32_t* X, const uint32_t* W, const uint32_t* Y, const uint32_t* bias,
+                        uint32_t num, uint32_t B, uint32_t IN, uint32_t OUT, const uint32_t* u_num,
+                        const uint32_t* v_num, const uint32_t* u_batch, const uint32_t* u_input,
+                        const uint32_t* u_output, uint32_t* proof_out, uint32_t* claims_out) {
+    if (!num || !B || !IN || !OUT) return 1;
+    uint32_t kn = ceil_log2(num), kb = ceil_log2(B), ki = ceil_log2(IN), ko = ceil_log2(OUT);
+    fr* Xf = from_aos(X, (size_t)num * B * IN);
+    fr* Wf = from_aos(W, (size_t)num * IN * OUT);
+    fr* Yf = from_aos(Y, (size_t)num * B * OUT);
+    fr *un = from_aos(u_num, kn), *vn = from_aos(v_num, kn), *ub = from_aos(u_batch, kb);
+    fr *ui = from_aos(u_input, ki), *uo = from_aos(u_output, ko);
+    int rc = 0;
+    fr claim, fin, ox, ow;
+    fr *xr = NULL, *wr = NULL, *pr = falloc(3 * (size_t)(kn + ki));
+    {
+        const fr* us[3] = {un, ub, uo};
+        uint32_t ks[3] = {kn, kb, ko}, sh[3] = {num, B, OUT};
+        if (multi_dim_me_fr(Yf, num * B * OUT, us, ks, sh, 3, &claim)) { rc = 1; goto done; }
+    }
+    if (bias) {
+        /* broadcasting_ones(u_batch) * b.multi_dim_me({u_num, u_output}, {num, OUT}) */
+        fr* ones = falloc(B);
+        for (uint32_t i = 0; i < B; i++) ones[i] = ONE;
+        fr* bf = from_aos(bias, (size_t)num * OUT);
+        const fr* us[2] = {un, uo};
+        uint32_t ks[2] = {kn, ko}, sh[2] = {num, OUT};
+        fr bb, ob = me_fr(ones, B, ub, kb);
+        rc = multi_dim_me_fr(bf, num * OUT, us, ks, sh, 2, &bb);
+        free(ones); free(bf);
+        if (rc) { rc = 1; goto done; }
+        claim = sub(claim, mul(ob, bb));
+    }
+    {
+        uint32_t nx, nw;
+        xr = partial_me_fr(Xf, num * B * IN, ub, kb, B, IN, &nx);
+        wr = partial_me_fr(Wf, num * IN * OUT, uo, ko, OUT, 1, &nw);
+    }
+    fin = claim;
+    rc = zkip_stacked_fr(&fin, xr, wr, num, IN, un, kn, ui, ki, vn, pr);
+    for (uint32_t i = 0; i < 3 * (kn + ki); i++) st(proof_out + 8 * i, pr[i]);
+    if (rc) goto done;
+    {
+        const fr* usx[3] = {vn, ub, ui};
+        uint32_t ksx[3] = {kn, kb, ki}, shx[3] = {num, B, IN};
+        const fr* usw[3] = {vn, ui, uo};
+        uint32_t ksw[3] = {kn, ki, ko}, shw[3] = {num, IN, OUT};
+        if (multi_dim_me_fr(Xf, num * B * IN, usx, ksx, shx, 3, &ox) ||
+            multi_dim_me_fr(Wf, num * IN * OUT, usw, ksw, shw, 3, &ow)) { rc = 1; goto done; }
+    }
+    st(claims_out, claim);
+    st(claims_out + 8, fin);
+    if (!feq(fin, mul(ox, ow))) rc = 2; /* zkfc.cu:306 */
+done:
+    free(Xf); free(Wf); free(Yf); free(un); free(vn); free(ub); free(ui); free(uo);
+    free(xr); free(wr); free(pr);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------------ */
+/* rescaling witness: rescaling.cu:8-21 with scalar_to_long (fr-tensor.cu:935-945)   */
+/* ------------------------------------------------------------------------------ */
+/* 64-bit limbs here: the reference's limbs 0,1 are v[0]; limbs 2..7 are v[1..3] */
+static uint64_t scalar_to_ulong(fr x) {
+    if (x.v[1] || x.v[2] || x.v[3]) return 0;
+    return x.v[0];
+}
+int64_t or_scalar_to_long(const uint32_t x[8]) {
+    fr v = ld(x);
+    if (!v.v[1] && !v.v[2] && !v.v[3] && !(v.v[0] >> 63)) return (int64_t)v.v[0];
+    return (int64_t)(0 - scalar_to_ulong(sub(ZERO, v)));
+}
+static void rescale1(int64_t x, int64_t sf, int64_t* q, int64_t* rem) {
+    int64_t hsf = sf >> 1;
+    int64_t temp = (int64_t)((uint64_t)x + (uint64_t)hsf) % sf;
+    int64_t r = (temp < 0 ? temp + sf : temp) - hsf;
+    *q = (int64_t)((uint64_t)x - (uint64_t)r) / sf;
+    *rem = r;
+}
+int or_rescale_i64(const int64_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_t* rem) {
+    if (!sf) return 1;
+    for (uint32_t i = 0; i < n; i++) rescale1(x[i], sf, q + i, rem + i);
+    return 0;
+}
+int or_rescale_fr(const uint32_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_t* rem) {
+    if (!sf) return 1;
+    for (uint32_t i = 0; i < n; i++) rescale1(or_scalar_to_long(x + 8 * i), sf, q + i, rem + i);
+    return 0;
 }

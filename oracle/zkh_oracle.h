@@ -63,6 +63,9 @@ int or_multi_dim_me(const uint32_t* t, uint32_t n, const uint32_t* us, const uin
 /* FrTensor::pad(shape) with zero pad value (fr-tensor.cu:800-828) */
 int or_pad(const uint32_t* t, const uint32_t* shape, uint32_t ndim, uint32_t* out,
            uint32_t* out_n);
+/* FrTensor::pad(shape, pad_val) (fr-tensor.cu:800-828, fr-tensor.cuh:150) */
+int or_pad_val(const uint32_t* t, const uint32_t* shape, uint32_t ndim, const uint32_t pad[8],
+               uint32_t* out, uint32_t* out_n);
 /* eq table E[b] = prod_i (b>>i&1 ? u_i : 1-u_i) (zkob_lookup.cuh:202-209, :245-265) */
 void or_build_eq(const uint32_t* u, uint32_t k, uint32_t* out);
 
@@ -103,6 +106,31 @@ int or_lu_prove(uint8_t st[32], const uint32_t* A, const uint32_t* S, const uint
 int or_hp_prove(uint8_t st[32], const uint32_t claim[8], const uint32_t* E,
                 const uint32_t* S, const uint32_t* U, uint32_t n, int strict,
                 uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+
+/* ---- inner-product sumchecks without a transcript (zkfc.cu) ----
+ * proof_out: 3 Fr per round, the coefficients c0, c1, c2 of p(X); final_out: last claim.
+ * Return 2 when a round check fails (the reference's runtime_error). */
+/* zkip (zkfc.cu:94-151): k <= ceilLog2(n) rounds, u[k-1] binds first */
+int or_zkip(const uint32_t claim[8], const uint32_t* a, const uint32_t* b, uint32_t n,
+            const uint32_t* u, uint32_t k, uint32_t* proof_out, uint32_t final_out[8]);
+/* zkip_stacked (zkfc.cu:153-246) over [N, D] tables; kN = ceilLog2(N), kD <= ceilLog2(D) */
+int or_zkip_stacked(const uint32_t claim[8], const uint32_t* a, const uint32_t* b,
+                    const uint32_t* uN, uint32_t kN, const uint32_t* uD, uint32_t kD,
+                    const uint32_t* vN, uint32_t N, uint32_t D, uint32_t* proof_out,
+                    uint32_t final_out[8]);
+/* zkFCStacked::prove(u_num, v_num, u_batch, u_input, u_output) (zkfc.cu:288-307); bias may
+ * be NULL; claims_out: claim, final claim; 2 when final != opening */
+int or_fc_stacked_prove(const uint32_t* X, const uint32_t* W, const uint32_t* Y, const uint32_t* bias,
+                        uint32_t num, uint32_t B, uint32_t IN, uint32_t OUT, const uint32_t* u_num,
+                        const uint32_t* v_num, const uint32_t* u_batch, const uint32_t* u_input,
+                        const uint32_t* u_output, uint32_t* proof_out, uint32_t* claims_out);
+
+/* ---- rescaling witness (rescaling.cu:8-21) ---- */
+/* scalar_to_long (fr-tensor.cu:935-945) */
+int64_t or_scalar_to_long(const uint32_t x[8]);
+/* q = (x - rem)/sf, rem = ((x + sf/2) % sf, made non-negative) - sf/2 */
+int or_rescale_i64(const int64_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_t* rem);
+int or_rescale_fr(const uint32_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_t* rem);
 
 /* Lagrange interpolation through p(0..2) / p(0..3) (vrf_common.cuh:130-140,
  * zkob_lookup.cuh:62-73) */

@@ -62,7 +62,13 @@ def lib():
         L.zkh_partial_me.argtypes = [vp, vp, vp, u32, u32, u32, ctypes.POINTER(vp)]
         L.zkh_multi_dim_me.argtypes = [vp, vp, vp, vp, vp, u32, vp]
         L.zkh_eq_table.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
-        L.zkh_pad.argtypes = [vp, vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_pad.argtypes = [vp, vp, vp, u32, vp, ctypes.POINTER(vp)]
+        L.zkh_partial_me_window.argtypes = [vp, vp, vp, u32, u32, ctypes.POINTER(vp)]
+        L.zkh_zkip.argtypes = [vp, vp, vp, vp, vp, u32, vp, vp]
+        L.zkh_zkip_stacked.argtypes = [vp, vp, vp, vp, vp, u32, vp, u32, vp, u32, u32, vp, vp]
+        L.zkh_fc_stacked_prove.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, vp, vp, vp,
+                                           vp, vp]
+        L.zkh_rescale.argtypes = [vp, vp, u32, ctypes.POINTER(vp), ctypes.POINTER(vp)]
         L.zkh_fold.argtypes = [vp, vp, vp]
         L.zkh_axpy.argtypes = [vp, vp, vp, vp, ctypes.POINTER(vp)]
         L.zkh_hadamard.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
@@ -231,9 +237,49 @@ class Context:
         u = _frs(u)
         return self._new(lib().zkh_eq_table, _p(u), u.shape[0])
 
-    def pad(self, t, shape):
+    def pad(self, t, shape, pad_val=None):
         shp = np.array(shape, dtype=np.uint32)
-        return self._new(lib().zkh_pad, t.h, _p(shp), len(shape))
+        pv = None if pad_val is None else _frs(pad_val, 1)
+        return self._new(lib().zkh_pad, t.h, _p(shp), len(shape), _p(pv))
+
+    def partial_me_window(self, t, u, window):
+        u = _frs(u)
+        return self._new(lib().zkh_partial_me_window, t.h, _p(u), u.shape[0], window)
+
+    # inner-product sumchecks without a transcript (zkfc.cu)
+    def zkip(self, claim, a, b, u):
+        k = len(u)
+        u = _frs(u) if k else np.zeros((1, 8), np.uint32)
+        proof = np.zeros((3 * k + 1, 8), np.uint32)
+        fin = np.zeros(8, np.uint32)
+        self._chk(lib().zkh_zkip(self.h, _p(_frs(claim, 1)), a.h, b.h, _p(u), k, _p(proof), _p(fin)))
+        return proof[:3 * k], fin
+
+    def zkip_stacked(self, claim, A, B, uN, uD, vN, N, D):
+        kN, kD = len(uN), len(uD)
+        z = np.zeros((1, 8), np.uint32)
+        uN, vN = (_frs(x) if kN else z for x in (uN, vN))
+        uD = _frs(uD) if kD else z
+        proof = np.zeros((3 * (kN + kD) + 1, 8), np.uint32)
+        fin = np.zeros(8, np.uint32)
+        self._chk(lib().zkh_zkip_stacked(self.h, _p(_frs(claim, 1)), A.h, B.h, _p(uN), kN, _p(uD), kD,
+                                         _p(vN), N, D, _p(proof), _p(fin)))
+        return proof[:3 * (kN + kD)], fin
+
+    def fc_stacked_prove(self, X, W, Y, bias, num, B, IN, OUT, u_num, v_num, u_batch, u_input, u_output):
+        z = np.zeros((1, 8), np.uint32)
+        us = [_frs(x) if len(x) else z for x in (u_num, v_num, u_batch, u_input, u_output)]
+        nr = len(u_num) + len(u_input)
+        proof = np.zeros((3 * nr + 1, 8), np.uint32)
+        claims = np.zeros((2, 8), np.uint32)
+        self._chk(lib().zkh_fc_stacked_prove(self.h, X.h, W.h, Y.h, None if bias is None else bias.h, num, B,
+                                             IN, OUT, *[_p(x) for x in us], _p(proof), _p(claims)))
+        return proof[:3 * nr], claims
+
+    def rescale(self, X, sf):
+        q, r = ctypes.c_void_p(), ctypes.c_void_p()
+        self._chk(lib().zkh_rescale(self.h, X.h, sf, ctypes.byref(q), ctypes.byref(r)))
+        return Tensor(self, q), Tensor(self, r)
 
     def fold(self, t, v):
         v = _frs(v, 1)

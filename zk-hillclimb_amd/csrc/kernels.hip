@@ -146,33 +146,42 @@ __global__ void k_planes_to_aos(const uint4* lo, const uint4* hi, uint32_t n, ui
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
         st_aos(aos, i, ld_fr(lo, hi, i));
 }
-__global__ void k_absmax_i32(const int32_t* __restrict__ in, uint32_t n, uint32_t* out) {
+// |v| maximum: lane -> wave (shuffles) -> block (LDS) -> one atomic per block
+template <typename U>
+ZDEV U absmax_block(U m) {
+    __shared__ U red[NT / 64];
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        U o = __shfl_xor(m, s, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) m = red[w] > m ? red[w] : m;
+    return m;
+}
+__global__ __launch_bounds__(NT) void k_absmax_i32(const int32_t* __restrict__ in, uint32_t n, uint32_t* out) {
     uint32_t m = 0;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
         int64_t v = in[i];
         uint32_t a = (uint32_t)(v < 0 ? -v : v);
         m = a > m ? a : m;
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-        uint32_t o = __shfl_xor(m, s, 64);
-        m = o > m ? o : m;
-    }
-    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+    m = absmax_block<uint32_t>(m);
+    if (threadIdx.x == 0) atomicMax(out, m);
 }
-__global__ void k_absmax_i64(const int64_t* __restrict__ in, uint32_t n, unsigned long long* out) {
+__global__ __launch_bounds__(NT) void k_absmax_i64(const int64_t* __restrict__ in, uint32_t n,
+                                                   unsigned long long* out) {
     unsigned long long m = 0;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
         int64_t v = in[i];
         unsigned long long a = v < 0 ? (unsigned long long)(-(v + 1)) + 1 : (unsigned long long)v;
         m = a > m ? a : m;
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-        unsigned long long o = __shfl_xor(m, s, 64);
-        m = o > m ? o : m;
-    }
-    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+    m = absmax_block<unsigned long long>(m);
+    if (threadIdx.x == 0) atomicMax(out, m);
 }
 // 32x32 LDS tile transpose: out[c*rows + r] = in[r*cols + c]
 __global__ void k_transpose_i32(const int32_t* __restrict__ in, uint32_t rows, uint32_t cols,
@@ -209,11 +218,11 @@ void launch_planes_to_aos(hipStream_t s, DevPlanes in, uint32_t n, uint32_t* aos
 }
 void launch_absmax_i32(hipStream_t s, const int32_t* in, uint32_t n, uint32_t* out) {
     if (!n) return;
-    k_absmax_i32<<<grid_for(n, NT * 8, 2048), NT, 0, s>>>(in, n, out);
+    k_absmax_i32<<<grid_for(n, NT * 8, 512), NT, 0, s>>>(in, n, out);
 }
 void launch_absmax_i64(hipStream_t s, const int64_t* in, uint32_t n, unsigned long long* out) {
     if (!n) return;
-    k_absmax_i64<<<grid_for(n, NT * 8, 2048), NT, 0, s>>>(in, n, out);
+    k_absmax_i64<<<grid_for(n, NT * 8, 512), NT, 0, s>>>(in, n, out);
 }
 void launch_transpose_i32(hipStream_t s, const int32_t* in, uint32_t rows, uint32_t cols,
                           int32_t* out) {
@@ -308,6 +317,168 @@ void launch_partial_me_i64(hipStream_t s, const int64_t* t, uint32_t O, uint32_t
                            const uint32_t* E, DevPlanes out) {
     LdI64 ld{t};
     k_partial_me<<<grid_for(O * W, NT, 8192), NT, 0, s>>>(ld, O, C, W, E, PL_LO(out), PL_HI(out));
+}
+// the same loaders with entries at index >= n reading as zero (a [rows, W] view whose
+// last rows are partial or missing)
+template <typename Ld>
+struct LdBounded {
+    Ld ld;
+    size_t n;
+    ZDEV fr_t operator()(size_t i) const { return i < n ? ld(i) : fr_zero(); }
+};
+template <typename Ld>
+static void partial_me_bounded(hipStream_t s, Ld ld, size_t n, uint32_t O, uint32_t C, uint32_t W,
+                               const uint32_t* E, DevPlanes out) {
+    LdBounded<Ld> b{ld, n};
+    k_partial_me<<<grid_for(O * W, NT, 8192), NT, 0, s>>>(b, O, C, W, E, PL_LO(out), PL_HI(out));
+}
+void launch_partial_me_window(hipStream_t s, int kind, const void* t, uint32_t cap, uint32_t n,
+                              uint32_t O, uint32_t C, uint32_t W, const uint32_t* E, DevPlanes out) {
+    if (kind == 0) {
+        DevPlanes p{(uint32_t*)t, cap};
+        partial_me_bounded(s, LdPlanes{PL_LO(p), PL_HI(p)}, n, O, C, W, E, out);
+    } else if (kind == 1) {
+        partial_me_bounded(s, LdI32{(const int32_t*)t}, n, O, C, W, E, out);
+    } else {
+        partial_me_bounded(s, LdI64{(const int64_t*)t}, n, O, C, W, E, out);
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// padding and table initialisation
+// ------------------------------------------------------------------------------------
+// out[g] over the padded shape (every dimension 2^lg[d]) = src at the unpadded index, or
+// the pad value where any coordinate lies in a dimension's padding
+__global__ void k_pad(const uint4* slo, const uint4* shi, PadDims pd, uint32_t total, fr_t pv,
+                      uint4* olo, uint4* ohi) {
+    for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < total; g += gridDim.x * blockDim.x) {
+        uint32_t rem = g;
+        size_t sidx = 0, mul = 1;
+        bool in = true;
+        for (int d = (int)pd.nd - 1; d >= 0; d--) {
+            const uint32_t i = rem & ((1u << pd.lg[d]) - 1);
+            rem >>= pd.lg[d];
+            in = in && i < pd.shape[d];
+            sidx += (size_t)i * mul;
+            mul *= pd.shape[d];
+        }
+        st_fr(olo, ohi, g, in ? ld_fr(slo, shi, (uint32_t)sidx) : pv);
+    }
+}
+void launch_pad(hipStream_t s, DevPlanes src, const PadDims& pd, uint32_t total, const uint32_t* pad_host,
+                DevPlanes out) {
+    k_pad<<<grid_for(total, NT, 8192), NT, 0, s>>>(PL_LO(src), PL_HI(src), pd, total, to_fr(pad_host),
+                                                  PL_LO(out), PL_HI(out));
+}
+// tLookupRange table: T[i] = low + i for i < len, low + len - 1 beyond (int arithmetic)
+__global__ void k_range_table(int32_t low, uint32_t len, uint32_t N, uint4* olo, uint4* ohi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < N; i += gridDim.x * blockDim.x) {
+        const uint32_t off = i < len ? i : len - 1;
+        st_fr(olo, ohi, i, fr_from_i64((int32_t)((uint32_t)low + off)));
+    }
+}
+void launch_range_table(hipStream_t s, int32_t low, uint32_t len, uint32_t N, DevPlanes out) {
+    k_range_table<<<grid_for(N, NT, 8192), NT, 0, s>>>(low, len, N, PL_LO(out), PL_HI(out));
+}
+
+// ------------------------------------------------------------------------------------
+// plain and stacked inner-product sumcheck rounds over a [N, D] row layout: row n < Nh
+// pairs with row n + Nh (Nh = 2^ceil(log2 N) / 2; rows >= N read as zero) and carries the
+// weight E[n] (Montgomery form, AoS) or 1 when E is null.  Sums, each x 2^-256:
+// c0 = sum w a0 b0, c1 = sum w (a0 db + b0 da), c2 = sum w da db.
+// ------------------------------------------------------------------------------------
+__global__ __launch_bounds__(NT) void k_stk_round(const uint4* alo, const uint4* ahi, const uint4* blo,
+                                                  const uint4* bhi, uint32_t N, uint32_t D, uint32_t Nh,
+                                                  const uint32_t* __restrict__ E, Publish pub) {
+    fr_t acc[3] = {fr_zero(), fr_zero(), fr_zero()};
+    const uint32_t tot = Nh * D, hiD = Nh * D, full = N * D;
+    for (uint32_t idx = blockIdx.x * NT + threadIdx.x; idx < tot; idx += gridDim.x * NT) {
+        fr_t a0 = ld_fr(alo, ahi, idx), b0 = ld_fr(blo, bhi, idx);
+        const bool up = idx + hiD < full;
+        fr_t da = fr_sub(up ? ld_fr(alo, ahi, idx + hiD) : fr_zero(), a0);
+        fr_t db = fr_sub(up ? ld_fr(blo, bhi, idx + hiD) : fr_zero(), b0);
+        if (E) {
+            const fr_t wm = ld_aos(E, idx / D);
+            a0 = mont_mul(wm, a0);  // w * a0 (plain)
+            da = mont_mul(wm, da);
+        }
+        acc[0] = fr_add(acc[0], mont_mul(a0, b0));
+        acc[1] = fr_add(acc[1], fr_add(mont_mul(a0, db), mont_mul(da, b0)));
+        acc[2] = fr_add(acc[2], mont_mul(da, db));
+    }
+    reduce_publish<3>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+}
+// in-place bind of the top row bit: t[idx] = t0 + v (t1 - t0) for idx < Nh*D (t1 = 0 past N)
+__global__ void k_stk_fold(uint4* alo, uint4* ahi, uint4* blo, uint4* bhi, uint32_t N, uint32_t D,
+                           uint32_t Nh, fr_t vm) {
+    const uint32_t tot = Nh * D, hiD = Nh * D, full = N * D;
+    for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < tot; idx += gridDim.x * blockDim.x) {
+        const bool up = idx + hiD < full;
+        const fr_t a0 = ld_fr(alo, ahi, idx), b0 = ld_fr(blo, bhi, idx);
+        const fr_t a1 = up ? ld_fr(alo, ahi, idx + hiD) : fr_zero();
+        const fr_t b1 = up ? ld_fr(blo, bhi, idx + hiD) : fr_zero();
+        st_fr(alo, ahi, idx, fr_add(a0, mont_mul(vm, fr_sub(a1, a0))));
+        st_fr(blo, bhi, idx, fr_add(b0, mont_mul(vm, fr_sub(b1, b0))));
+    }
+}
+uint32_t launch_stk_round(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t N, uint32_t D, uint32_t Nh,
+                          const uint32_t* E, Publish pub) {
+    const uint32_t g = grid_for(Nh * D, NT, 1024);
+    k_stk_round<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), N, D, Nh, E, pub);
+    return g;
+}
+void launch_stk_fold(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t N, uint32_t D, uint32_t Nh,
+                     const uint32_t* v_m_host) {
+    k_stk_fold<<<grid_for(Nh * D, NT, 8192), NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), N, D, Nh,
+                                                        to_fr(v_m_host));
+}
+
+// ------------------------------------------------------------------------------------
+// rescaling witness (rescaling.cu:8-21): x = sf * q + rem with rem in [-sf/2, sf - sf/2)
+// ------------------------------------------------------------------------------------
+// scalar_to_long (fr-tensor.cu:935-945): small non-negative values as they are, otherwise
+// minus the low 64 bits of r - x (0 when r - x has any limb above the second set)
+ZDEV int64_t fr_to_long(const fr_t& x) {
+    if (!(x.v[7] | x.v[6] | x.v[5] | x.v[4] | x.v[3] | x.v[2]) && !(x.v[1] >> 31))
+        return (int64_t)(((uint64_t)x.v[1] << 32) | x.v[0]);
+    const fr_t y = fr_sub(fr_zero(), x);
+    const uint64_t u = (y.v[7] | y.v[6] | y.v[5] | y.v[4] | y.v[3] | y.v[2])
+                           ? 0
+                           : (((uint64_t)y.v[1] << 32) | y.v[0]);
+    return (int64_t)(0 - u);
+}
+template <typename T>
+struct LdInt {
+    const T* p;
+    ZDEV int64_t operator()(uint32_t i) const { return (int64_t)p[i]; }
+};
+struct LdLong {
+    const uint4* lo;
+    const uint4* hi;
+    ZDEV int64_t operator()(uint32_t i) const { return fr_to_long(ld_fr(lo, hi, i)); }
+};
+template <typename Ld>
+__global__ void k_rescale(Ld ld, uint32_t n, int64_t sf, int64_t* __restrict__ q, int64_t* __restrict__ rem) {
+    const int64_t hsf = sf >> 1;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const int64_t x = ld(i);
+        const int64_t t = (int64_t)((uint64_t)x + (uint64_t)hsf) % sf;  // C remainder: sign of the dividend
+        const int64_t r = (t < 0 ? t + sf : t) - hsf;
+        q[i] = (int64_t)((uint64_t)x - (uint64_t)r) / sf;
+        rem[i] = r;
+    }
+}
+void launch_rescale(hipStream_t s, int kind, const void* x, uint32_t cap, uint32_t n, int64_t sf,
+                    int64_t* q, int64_t* rem) {
+    const uint32_t g = grid_for(n, NT, 8192);
+    if (kind == 0) {
+        DevPlanes p{(uint32_t*)x, cap};
+        k_rescale<<<g, NT, 0, s>>>(LdLong{PL_LO(p), PL_HI(p)}, n, sf, q, rem);
+    } else if (kind == 1) {
+        k_rescale<<<g, NT, 0, s>>>(LdInt<int32_t>{(const int32_t*)x}, n, sf, q, rem);
+    } else {
+        k_rescale<<<g, NT, 0, s>>>(LdInt<int64_t>{(const int64_t*)x}, n, sf, q, rem);
+    }
 }
 
 ZDEV fr_t fold_at(const uint4* lo, const uint4* hi, uint32_t j, uint32_t n, const fr_t& vm) {

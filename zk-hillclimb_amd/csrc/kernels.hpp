@@ -74,6 +74,31 @@ void launch_partial_me_i32(hipStream_t s, const int32_t* t, uint32_t O, uint32_t
                            const uint32_t* E, DevPlanes out);
 void launch_partial_me_i64(hipStream_t s, const int64_t* t, uint32_t O, uint32_t C, uint32_t W,
                            const uint32_t* E, DevPlanes out);
+// the same over a [O, C, W] view of a tensor with only n stored entries (entries at index
+// >= n read as zero); kind 0: FR planes (t, cap), 1: int32, 2: int64
+void launch_partial_me_window(hipStream_t s, int kind, const void* t, uint32_t cap, uint32_t n,
+                              uint32_t O, uint32_t C, uint32_t W, const uint32_t* E, DevPlanes out);
+// padding (FrTensor::pad): dimension d of shape[d] entries padded to 2^lg[d]
+struct PadDims {
+    uint32_t nd;
+    uint32_t shape[8];
+    uint32_t lg[8];
+};
+void launch_pad(hipStream_t s, DevPlanes src, const PadDims& pd, uint32_t total, const uint32_t* pad_host,
+                DevPlanes out);
+// tLookupRange table of N entries: low + min(i, len - 1)
+void launch_range_table(hipStream_t s, int32_t low, uint32_t len, uint32_t N, DevPlanes out);
+// zkip / zkip_stacked round over a [N, D] layout (rows n, n + Nh paired, rows >= N zero,
+// weights E[n] Montgomery AoS of Nh entries, or 1 when E is null): publishes c0, c1, c2
+// (x 2^-256) as job 0 of pub; the fold binds the top row bit in place with v (Montgomery)
+uint32_t launch_stk_round(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t N, uint32_t D, uint32_t Nh,
+                          const uint32_t* E, Publish pub);
+void launch_stk_fold(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t N, uint32_t D, uint32_t Nh,
+                     const uint32_t* v_m_host);
+// rescaling witness: q = (x - rem) / sf, rem = ((x + sf/2) mod sf) - sf/2 for x of the given
+// kind (0: FR planes read through scalar_to_long, 1: int32, 2: int64)
+void launch_rescale(hipStream_t s, int kind, const void* x, uint32_t cap, uint32_t n, int64_t sf,
+                    int64_t* q, int64_t* rem);
 // MSB fold dst[i] = src[i] + v*(src[i+h]-src[i]), i < h (v in Montgomery form)
 void launch_fold(hipStream_t s, Tab t, uint32_t h, const uint32_t* v_m_host);
 void launch_axpy(hipStream_t s, DevPlanes a, const uint32_t* c_m_host, DevPlanes b, uint32_t n,

@@ -1034,44 +1034,38 @@ extern "C" int zkh_hadamard(zkh_ctx* c, const zkh_tensor* a, const zkh_tensor* b
     return ZKH_OK;
 }
 extern "C" int zkh_pad(zkh_ctx* c, const zkh_tensor* t, const uint32_t* shape, uint32_t ndim,
-                       zkh_tensor** out) {
+                       const uint32_t pad_val[8], zkh_tensor** out) {
     if (!c || !t || !shape || !out || ndim == 0 || ndim > 8) return fail(c, ZKH_EARG, "bad arguments");
-    uint64_t total = 1, ptotal = 1;
+    if (pad_val && !fr_is_canonical(pad_val)) return fail(c, ZKH_EARG, "non-canonical pad value");
+    uint64_t total = 1;
+    uint32_t lgsum = 0;
+    PadDims pd{};
+    pd.nd = ndim;
     for (uint32_t d = 0; d < ndim; d++) {
-        total *= shape[d];
-        ptotal *= (uint64_t)1 << ceil_log2(shape[d]);
+        total = std::min<uint64_t>(total * shape[d], 1ull << 33);
+        pd.shape[d] = shape[d];
+        pd.lg[d] = ceil_log2(shape[d]);
+        lgsum += pd.lg[d];
     }
+    // FrTensor::pad checks (fr-tensor.cu:809-813)
     if (total != t->n) return fail(c, ZKH_EARG, "pad: cum_shape != size");
-    if (ptotal >= (1ull << 32)) return fail(c, ZKH_EARG, "pad: too large");
+    if (lgsum >= 32) return fail(c, ZKH_EARG, "pad: too large");
+    const uint64_t ptotal = 1ull << lgsum;
     HIPCHK(c, hipSetDevice(c->device));
-    // host-side index map, then a gather on the device (zero where any index is padding)
     int rc = 0;
     DevPlanes p;
     if ((rc = as_planes(c, t, SL_TMP0, &p))) return rc;
-    std::vector<uint32_t> src(t->n ? t->n * 8 : 8);
-    if (t->n) {
-        uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)t->n * 32, &rc);
-        if (rc) return rc;
-        launch_planes_to_aos(c->stream, p, t->n, stage);
-        HIPCHK(c, hipMemcpyAsync(src.data(), stage, (size_t)t->n * 32, hipMemcpyDeviceToHost, c->stream));
-        HIPCHK(c, hipStreamSynchronize(c->stream));
+    zkh_tensor* o;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, (uint32_t)ptotal, &o))) return rc;
+    static const uint32_t zero[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    launch_pad(c->stream, p, pd, (uint32_t)ptotal, pad_val ? pad_val : zero, o->planes());
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        zkh_tensor_free(o);
+        return fail(c, ZKH_EDEV, "pad: %s", hipGetErrorString(e));
     }
-    std::vector<uint32_t> dst((size_t)ptotal * 8, 0);
-    std::vector<uint32_t> pd(ndim);
-    for (uint32_t d = 0; d < ndim; d++) pd[d] = 1u << ceil_log2(shape[d]);
-    for (uint64_t g = 0; g < ptotal; g++) {
-        uint64_t rem = g, sidx = 0, mul = 1;
-        bool in = true;
-        for (int d = (int)ndim - 1; d >= 0; d--) {
-            uint64_t i = rem % pd[d];
-            rem /= pd[d];
-            if (i >= shape[d]) in = false;
-            sidx += i * mul;
-            mul *= shape[d];
-        }
-        if (in) memcpy(&dst[g * 8], &src[sidx * 8], 32);
-    }
-    return zkh_tensor_from_fr(c, dst.data(), (uint32_t)ptotal, out);
+    *out = o;
+    return ZKH_OK;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1717,20 +1711,12 @@ extern "C" int zkh_mm_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* X, con
 // ---------------------------------------------------------------------------------------
 extern "C" int zkh_lu_range_table(zkh_ctx* c, int32_t low, uint32_t len, uint32_t N, zkh_tensor** out) {
     if (!c || !out || !len || N < len) return fail(c, ZKH_EARG, "bad range table arguments");
-    std::vector<int32_t> v(N);
-    for (uint32_t i = 0; i < N; i++)
-        v[i] = i < len ? (int32_t)((int64_t)low + i) : (int32_t)((int64_t)low + len - 1);
-    zkh_tensor* ti;
-    int rc = zkh_tensor_from_i32(c, v.data(), N, &ti);
-    if (rc) return rc;
+    HIPCHK(c, hipSetDevice(c->device));
     zkh_tensor* t;
-    if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &t))) {
-        zkh_tensor_free(ti);
-        return rc;
-    }
-    launch_i32_to_planes(c->stream, (const int32_t*)ti->d, N, t->planes());
+    int rc = tensor_alloc(c, ZKH_KIND_FR, N, &t);
+    if (rc) return rc;
+    launch_range_table(c->stream, low, len, N, t->planes());
     hipError_t e = hipStreamSynchronize(c->stream);
-    zkh_tensor_free(ti);
     if (e != hipSuccess) {
         zkh_tensor_free(t);
         return fail(c, ZKH_EDEV, "range table: %s", hipGetErrorString(e));
@@ -2176,4 +2162,305 @@ extern "C" int zkh_hp_prove_eq(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[
     if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
     std::vector<Fr> uv = load_frs(u, k);
     return hp_common(c, tr, claim, nullptr, &uv, S, U, ev_out, term_out, ws_out);
+}
+
+// ---------------------------------------------------------------------------------------
+// window partial_me (fr-tensor.cu:512-516, :612-641)
+// ---------------------------------------------------------------------------------------
+// k LSB-first binds of the row index of a [rows, window] view (the last row may be
+// partial; missing entries are zero): out[w*window + j] = sum_{b < 2^k} eq(b, u) *
+// t[(w*2^k + b)*window + j], w < ceil(rows / 2^k) -- the k halving steps of the reference
+// in one pass
+extern "C" int zkh_partial_me_window(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u, uint32_t k,
+                                     uint32_t window, zkh_tensor** out) {
+    if (!c || !t || !out || !u || !k || !window) return fail(c, ZKH_EARG, "bad arguments");
+    if (k >= 32 || (uint64_t)t->n <= (uint64_t)window * (1ull << (k - 1)))
+        return fail(c, ZKH_EARG, "partial_me: Incompatible dimensions");
+    if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    const uint64_t rows = ((uint64_t)t->n + window - 1) / window;
+    uint64_t orows = rows;
+    for (uint32_t r = 0; r < k; r++) orows = (orows + 1) / 2;  // ceil per step, as the reference
+    const uint64_t C = 1ull << k;
+    if (orows * window >= (1ull << 32) || orows * C * window > (1ull << 40))
+        return fail(c, ZKH_EARG, "partial_me: too large");
+    int rc = 0;
+    uint32_t* E;
+    if ((rc = eq_table_mont(c, load_frs(u, k), (uint32_t)C, SL_EB, &E))) return rc;
+    zkh_tensor* o;
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, (uint32_t)(orows * window), &o))) return rc;
+    const void* src = t->d;
+    int kind = t->kind == ZKH_KIND_FR ? 0 : t->kind == ZKH_KIND_I32 ? 1 : 2;
+    DevPlanes p{(uint32_t*)t->d, t->cap};
+    if (t->weights) {  // logical (row-major) W from the OUT-major copy
+        if ((rc = as_planes(c, t, SL_TMP0, &p))) {
+            zkh_tensor_free(o);
+            return rc;
+        }
+        src = p.base;
+        kind = 0;
+    }
+    launch_partial_me_window(c->stream, kind, src, p.cap, t->n, (uint32_t)orows, (uint32_t)C, window, E,
+                             o->planes());
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        zkh_tensor_free(o);
+        return fail(c, ZKH_EDEV, "partial_me: %s", hipGetErrorString(e));
+    }
+    *out = o;
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// zkip and zkip_stacked (zkfc.cu:94-246) and zkFCStacked::prove (zkfc.cu:288-307)
+// ---------------------------------------------------------------------------------------
+// one round over the [N, D] working tables: p = (c0, c1, c2) with the weights of E
+static int stk_round(zkh_ctx* c, DevPlanes a, DevPlanes b, uint32_t N, uint32_t D, uint32_t Nh,
+                     const uint32_t* E, Fr p[3]) {
+    Publish pb = make_pub(c, 1);
+    {
+        ProfScope ps(c, "stk_round", (double)N * D * 64);
+        launch_stk_round(c->stream, a, b, N, D, Nh, E, pb);
+    }
+    int rc = wait_pub(c, pb.seq);
+    if (rc) return rc;
+    pub_read(c, 0, 3, p);
+    for (int i = 0; i < 3; i++) p[i] = fix1(p[i]);
+    return 0;
+}
+// working copies of two tensors of n entries (read by the rounds, folded in place)
+static int stk_copies(zkh_ctx* c, const zkh_tensor* A, const zkh_tensor* B, DevPlanes* a, DevPlanes* b) {
+    int rc = 0;
+    DevPlanes sa, sb;
+    if ((rc = as_planes(c, A, SL_TMP0, &sa)) || (rc = as_planes(c, B, SL_TMP1, &sb))) return rc;
+    *a = scratch_planes(c, SL_TMP2, A->n, &rc);
+    if (rc) return rc;
+    *b = scratch_planes(c, SL_TMP3, B->n, &rc);
+    if (rc) return rc;
+    const size_t q = (size_t)A->n * 16;
+    HIPCHK(c, hipMemcpyAsync(a->lo(), sa.lo(), q, hipMemcpyDeviceToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(a->hi(), sa.hi(), q, hipMemcpyDeviceToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(b->lo(), sb.lo(), q, hipMemcpyDeviceToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(b->hi(), sb.hi(), q, hipMemcpyDeviceToDevice, c->stream));
+    return 0;
+}
+// zkip (zkfc.cu:129-151) over the working tables of n entries: |u| rounds, u.back() first
+static int zkip_rounds(zkh_ctx* c, Fr& claim, DevPlanes a, DevPlanes b, uint32_t n,
+                       const std::vector<Fr>& u, std::vector<Fr>& proof) {
+    uint32_t N = n;
+    for (size_t r = 0; r < u.size(); r++) {
+        const uint32_t Nh = (1u << ceil_log2(N)) >> 1;
+        Fr p[3];
+        int rc = stk_round(c, a, b, N, 1, Nh, nullptr, p);
+        if (rc) return rc;
+        proof.insert(proof.end(), p, p + 3);
+        // claim != p(0) + p(1) (zkfc.cu:145)
+        if (!fr_eq(claim, fr_add(p[0], fr_add(p[0], fr_add(p[1], p[2])))))
+            return fail(c, ZKH_EROUND, "zkip: claim != p(0) + p(1) at round %zu", r);
+        const Fr x = u[u.size() - 1 - r];
+        claim = fr_poly_eval(p, 2, x);
+        uint32_t xm[8];
+        fr_store(fr_to_mont(x), xm);
+        launch_stk_fold(c->stream, a, b, N, 1, Nh, xm);
+        N = Nh;
+    }
+    return 0;
+}
+// zkip_stacked (zkfc.cu:230-246): |uN| rounds over the N rows of [N, D] tables, each
+// weighted by eq(u_, row) of the remaining uN prefix, then zkip over D with uD
+static int zkip_stacked_rounds(zkh_ctx* c, Fr& claim, DevPlanes a, DevPlanes b, uint32_t N, uint32_t D,
+                               const std::vector<Fr>& uN, const std::vector<Fr>& uD,
+                               const std::vector<Fr>& vN, std::vector<Fr>& proof) {
+    int rc = 0;
+    std::vector<Fr> u_ = uN;
+    for (size_t r = 0; r < uN.size(); r++) {
+        const uint32_t Nh = (1u << ceil_log2(N)) >> 1;
+        const Fr ul = u_.back();
+        u_.pop_back();
+        uint32_t* E = nullptr;
+        if (!u_.empty() && (rc = eq_table_mont(c, u_, Nh, SL_EB, &E))) return rc;
+        Fr p[3];
+        if ((rc = stk_round(c, a, b, N, D, Nh, E, p))) return rc;
+        proof.insert(proof.end(), p, p + 3);
+        // q = eq(u_last, X) * p: claim != q(0) + q(1) (zkfc.cu:236-237)
+        const Fr p1 = fr_add(p[0], fr_add(p[1], p[2]));
+        if (!fr_eq(claim, fr_add(fr_mul(fr_sub(kOne, ul), p[0]), fr_mul(ul, p1))))
+            return fail(c, ZKH_EROUND, "zkip_stacked: claim != q(0) + q(1) at round %zu", r);
+        const Fr v = vN[vN.size() - 1 - r];
+        claim = fr_poly_eval(p, 2, v);
+        uint32_t vm[8];
+        fr_store(fr_to_mont(v), vm);
+        launch_stk_fold(c->stream, a, b, N, D, Nh, vm);
+        N = Nh;
+    }
+    return zkip_rounds(c, claim, a, b, D, uD, proof);
+}
+extern "C" int zkh_zkip(zkh_ctx* c, const uint32_t claim_l[8], const zkh_tensor* A, const zkh_tensor* B,
+                        const uint32_t* u, uint32_t k, uint32_t* proof_out, uint32_t final_out[8]) {
+    if (!c || !claim_l || !A || !B || !final_out || (!u && k)) return fail(c, ZKH_EARG, "null argument");
+    if (A->n != B->n) return fail(c, ZKH_EARG, "a.size != b.size");
+    if (!A->n || k > ceil_log2(A->n)) return fail(c, ZKH_EARG, "zkip: more challenges than variables");
+    if (!fr_is_canonical(claim_l) || !all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical input");
+    HIPCHK(c, hipSetDevice(c->device));
+    DevPlanes a, b;
+    int rc = stk_copies(c, A, B, &a, &b);
+    if (rc) return rc;
+    Fr claim = fr_load(claim_l);
+    std::vector<Fr> proof;
+    rc = zkip_rounds(c, claim, a, b, A->n, load_frs(u, k), proof);
+    if (proof_out)
+        for (size_t i = 0; i < proof.size(); i++) fr_store(proof[i], proof_out + 8 * i);
+    if (rc) return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    fr_store(claim, final_out);
+    return ZKH_OK;
+}
+static int stacked_args(zkh_ctx* c, const zkh_tensor* A, const zkh_tensor* B, uint32_t N, uint32_t D,
+                        uint32_t kN, uint32_t kD) {
+    if ((uint64_t)A->n != (uint64_t)N * D || (uint64_t)B->n != (uint64_t)N * D)
+        return fail(c, ZKH_EARG, "a.size != N * D");
+    if (!N || !D || kN != ceil_log2(N) || kD > ceil_log2(D))
+        return fail(c, ZKH_EARG, "zkip_stacked: challenge counts do not match N, D");
+    return 0;
+}
+extern "C" int zkh_zkip_stacked(zkh_ctx* c, const uint32_t claim_l[8], const zkh_tensor* A,
+                                const zkh_tensor* B, const uint32_t* uN, uint32_t kN, const uint32_t* uD,
+                                uint32_t kD, const uint32_t* vN, uint32_t N, uint32_t D,
+                                uint32_t* proof_out, uint32_t final_out[8]) {
+    if (!c || !claim_l || !A || !B || !final_out || (kN && (!uN || !vN)) || (kD && !uD))
+        return fail(c, ZKH_EARG, "null argument");
+    int rc = stacked_args(c, A, B, N, D, kN, kD);
+    if (rc) return rc;
+    if (!fr_is_canonical(claim_l) || !all_canonical(uN, kN) || !all_canonical(vN, kN) || !all_canonical(uD, kD))
+        return fail(c, ZKH_EARG, "non-canonical input");
+    HIPCHK(c, hipSetDevice(c->device));
+    DevPlanes a, b;
+    if ((rc = stk_copies(c, A, B, &a, &b))) return rc;
+    Fr claim = fr_load(claim_l);
+    std::vector<Fr> proof;
+    rc = zkip_stacked_rounds(c, claim, a, b, N, D, load_frs(uN, kN), load_frs(uD, kD), load_frs(vN, kN), proof);
+    if (proof_out)
+        for (size_t i = 0; i < proof.size(); i++) fr_store(proof[i], proof_out + 8 * i);
+    if (rc) return rc;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    fr_store(claim, final_out);
+    return ZKH_OK;
+}
+static int mdm(zkh_ctx* c, const zkh_tensor* t, std::initializer_list<const std::vector<Fr>*> us,
+               std::initializer_list<uint32_t> shape, Fr* out) {
+    std::vector<uint32_t> cat, ks;
+    for (auto* u : us) {
+        ks.push_back((uint32_t)u->size());
+        for (const Fr& x : *u) {
+            uint32_t l[8];
+            fr_store(x, l);
+            cat.insert(cat.end(), l, l + 8);
+        }
+    }
+    cat.resize(cat.size() + 8);
+    std::vector<uint32_t> shp(shape);
+    uint32_t o[8];
+    int rc = zkh_multi_dim_me(c, t, cat.data(), ks.data(), shp.data(), (uint32_t)shp.size(), o);
+    if (!rc) *out = fr_load(o);
+    return rc;
+}
+extern "C" int zkh_fc_stacked_prove(zkh_ctx* c, const zkh_tensor* X, const zkh_tensor* W,
+                                    const zkh_tensor* Y, const zkh_tensor* bias, uint32_t num,
+                                    uint32_t B, uint32_t IN, uint32_t OUT, const uint32_t* u_num,
+                                    const uint32_t* v_num, const uint32_t* u_batch, const uint32_t* u_input,
+                                    const uint32_t* u_output, uint32_t* proof_out, uint32_t claims_out[16]) {
+    if (!c || !X || !W || !Y || !claims_out) return fail(c, ZKH_EARG, "null argument");
+    if (!num || !B || !IN || !OUT) return fail(c, ZKH_EARG, "zero dimension");
+    // zkFCStacked constructor checks (zkfc.cu:266-269)
+    if ((uint64_t)X->n != (uint64_t)num * B * IN) return fail(c, ZKH_EARG, "X size does not match");
+    if ((uint64_t)Y->n != (uint64_t)num * B * OUT) return fail(c, ZKH_EARG, "Y size does not match");
+    if ((uint64_t)W->n != (uint64_t)num * IN * OUT || W->weights)
+        return fail(c, ZKH_EARG, "W size does not match");
+    if (bias && (uint64_t)bias->n != (uint64_t)num * OUT) return fail(c, ZKH_EARG, "b size does not match");
+    const uint32_t kn = ceil_log2(num), kb = ceil_log2(B), ki = ceil_log2(IN), ko = ceil_log2(OUT);
+    if ((kn && (!u_num || !v_num)) || (kb && !u_batch) || (ki && !u_input) || (ko && !u_output))
+        return fail(c, ZKH_EARG, "null challenges");
+    if (!all_canonical(u_num, kn) || !all_canonical(v_num, kn) || !all_canonical(u_batch, kb) ||
+        !all_canonical(u_input, ki) || !all_canonical(u_output, ko))
+        return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    const std::vector<Fr> un = load_frs(u_num, kn), vn = load_frs(v_num, kn), ub = load_frs(u_batch, kb),
+                          ui = load_frs(u_input, ki), uo = load_frs(u_output, ko);
+    int rc = 0;
+    // claim = Y(u_num, u_batch, u_output) - ones_B(u_batch) * b(u_num, u_output) (zkfc.cu:292-302)
+    Fr claim;
+    if ((rc = mdm(c, Y, {&un, &ub, &uo}, {num, B, OUT}, &claim))) return rc;
+    if (bias) {
+        Fr bb;
+        if ((rc = mdm(c, bias, {&un, &uo}, {num, OUT}, &bb))) return rc;
+        claim = fr_sub(claim, fr_mul(eq_prefix_sum(ub, B), bb));
+    }
+    // X_reduced = X.partial_me(u_batch, B, IN), W_reduced = W.partial_me(u_output, OUT, 1)
+    zkh_tensor *Xr = nullptr, *Wr = nullptr;
+    if ((rc = partial_me_impl(c, X, ub, B, IN, &Xr))) return rc;
+    if ((rc = partial_me_impl(c, W, uo, OUT, 1, &Wr))) {
+        zkh_tensor_free(Xr);
+        return rc;
+    }
+    DevPlanes a, b;
+    Fr cur = claim;
+    std::vector<Fr> proof;
+    rc = stacked_args(c, Xr, Wr, num, IN, kn, ki);
+    if (!rc) rc = stk_copies(c, Xr, Wr, &a, &b);
+    if (!rc) rc = zkip_stacked_rounds(c, cur, a, b, num, IN, un, ui, vn, proof);
+    if (!rc) rc = hipStreamSynchronize(c->stream) == hipSuccess ? 0 : fail(c, ZKH_EDEV, "zkip_stacked sync");
+    zkh_tensor_free(Xr);
+    zkh_tensor_free(Wr);
+    if (proof_out)
+        for (size_t i = 0; i < proof.size(); i++) fr_store(proof[i], proof_out + 8 * i);
+    if (rc) return rc;
+    // opening = X(v_num, u_batch, u_input) * W(v_num, u_input, u_output) (zkfc.cu:305-306)
+    Fr ox, ow;
+    if ((rc = mdm(c, X, {&vn, &ub, &ui}, {num, B, IN}, &ox))) return rc;
+    if ((rc = mdm(c, W, {&vn, &ui, &uo}, {num, IN, OUT}, &ow))) return rc;
+    fr_store(claim, claims_out);
+    fr_store(cur, claims_out + 8);
+    if (!fr_eq(cur, fr_mul(ox, ow))) return fail(c, ZKH_EROUND, "final claim != opening");
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// rescaling witness (rescaling.cu:8-34; zkob_rescale.cu:83-86)
+// ---------------------------------------------------------------------------------------
+extern "C" int zkh_rescale(zkh_ctx* c, const zkh_tensor* X, uint32_t sf, zkh_tensor** q_out,
+                           zkh_tensor** rem_out) {
+    if (!c || !X || !q_out || !rem_out || !sf) return fail(c, ZKH_EARG, "bad arguments");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    zkh_tensor *q, *r;
+    if ((rc = tensor_alloc(c, ZKH_KIND_I64, X->n, &q))) return rc;
+    if ((rc = tensor_alloc(c, ZKH_KIND_I64, X->n, &r))) {
+        zkh_tensor_free(q);
+        return rc;
+    }
+    const void* src = X->d;
+    int kind = X->kind == ZKH_KIND_FR ? 0 : X->kind == ZKH_KIND_I32 ? 1 : 2;
+    uint32_t cap = X->cap;
+    if (X->weights) {
+        DevPlanes p;
+        if ((rc = as_planes(c, X, SL_TMP0, &p))) {
+            zkh_tensor_free(q);
+            zkh_tensor_free(r);
+            return rc;
+        }
+        src = p.base;
+        cap = p.cap;
+        kind = 0;
+    }
+    if (X->n) launch_rescale(c->stream, kind, src, cap, X->n, (int64_t)sf, (int64_t*)q->d, (int64_t*)r->d);
+    if (X->n && !rc) rc = int_bits_i64(c, (const int64_t*)q->d, X->n, &q->bits);
+    if (X->n && !rc) rc = int_bits_i64(c, (const int64_t*)r->d, X->n, &r->bits);
+    if (rc) {
+        zkh_tensor_free(q);
+        zkh_tensor_free(r);
+        return rc;
+    }
+    *q_out = q;
+    *rem_out = r;
+    return ZKH_OK;
 }
