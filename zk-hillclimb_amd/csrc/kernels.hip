@@ -1019,15 +1019,37 @@ ZDEV T ld_stream(const T* p) {
     return __builtin_nontemporal_load((__attribute__((address_space(1))) const T*)p);
 }
 
-// partial[c*N + i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) e_k: one column per thread,
-// rows unrolled by 8 with all eight loads issued before the multiply-adds so each wave
-// keeps 8 rows of its column block in flight; e_k comes through scalar loads.
-template <typename T, int NP>
-__global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict__ d, uint32_t nd) {
-    const EqDotDesc& q = d[find_desc_uniform(d, nd)];
+// 2^(22p) * 2^256 mod r, p = 1..2: recombine 22-bit integer pieces
+ZDEV fr_t piece_scale22(int p) {
+    if (p == 1)
+        return mk(0xff72abdbu, 0x008d5424u, 0xde9a0825u, 0x561f5078u, 0x85cae84du, 0xa153d589u,
+                  0x4e5cfce5u, 0x1af19b95u);
+    return mk(0xf6b12013u, 0x094ebc97u, 0x70afd742u, 0x6d9e32d3u, 0x5d095294u, 0xc234ec0bu,
+              0xa886a754u, 0x6701f764u);
+}
+// Reduction variants: element type, pieces per element, piece width (bits).  A piece
+// times a 32-bit eq limb is < 2^(32+PB), so a 64-bit column sum takes 2^(31-PB) rows
+// without overflow (2048 rows at PB = 20, 512 at PB = 22); the host sizes chunks to that.
+template <typename T_, int NP_, int PB_>
+struct EqdotV {
+    typedef T_ T;
+    static constexpr int NP = NP_, PB = PB_;
+};
+typedef EqdotV<int32_t, 1, 20> EqdotI32x1;
+typedef EqdotV<int32_t, 2, 22> EqdotI32x2;
+typedef EqdotV<int64_t, 2, 22> EqdotI64x2;
+typedef EqdotV<int64_t, 3, 22> EqdotI64x3;
+
+// partial[c*N+i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) e_k: one column per thread, rows
+// in groups of 8 with the next group's loads issued before the current group's products
+// (16 rows of the column in flight per wave); e_k comes through scalar loads.
+template <typename V>
+ZDEV void eqdot_body(const EqDotDesc& q, uint32_t local) {
+    typedef typename V::T T;
+    constexpr int NP = V::NP, PB = V::PB;
+    constexpr uint32_t PMASK = (1u << PB) - 1;
     const uint32_t N = q.N;
     const uint32_t ncb = (N + NT - 1) / NT;
-    const uint32_t local = blockIdx.x - q.blk_begin;
     const uint32_t i = (local % ncb) * NT + threadIdx.x;
     const uint32_t c = local / ncb;
     const uint32_t k0 = c * q.kchunk;
@@ -1038,29 +1060,40 @@ __global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict_
     for (int p = 0; p < NP; p++)
 #pragma unroll
         for (int j = 0; j < 8; j++) acc[p][j] = 0;
-    const int64_t off = (int64_t)1 << q.bits;
+    const uint64_t off = (uint64_t)1 << q.bits;
     const T* M = reinterpret_cast<const T*>(q.M);
+    const uint32_t off32 = (uint32_t)off;
+    auto mac = [&](T x, uint32_t k) {
+        const fr_t e = ld_aos_uniform(E, k);
+        if (sizeof(T) == 4 && NP == 1) {  // |x| < 2^19: x + 2^bits < 2^20 in one 32-bit add
+            cols_mac(acc[0], (uint32_t)x + off32, e);
+        } else {
+            const uint64_t w = (uint64_t)(int64_t)x + off;
+#pragma unroll
+            for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (PB * p)) & PMASK, e);
+        }
+    };
     if (i < N) {
         const T* col = M + i;
         uint32_t k = k0;
-        for (; k + 8 <= k1; k += 8) {
+        if (k + 8 <= k1) {
             T v[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) v[u] = ld_stream(col + (size_t)(k + u) * N);
+            for (; k + 16 <= k1; k += 8) {
+                T nx[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const fr_t e = ld_aos_uniform(E, k + u);
-                const uint64_t w = (uint64_t)((int64_t)v[u] + off);
+                for (int u = 0; u < 8; u++) nx[u] = ld_stream(col + (size_t)(k + 8 + u) * N);
 #pragma unroll
-                for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (20 * p)) & 0xFFFFFu, e);
+                for (int u = 0; u < 8; u++) mac(v[u], k + u);
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = nx[u];
             }
-        }
-        for (; k < k1; k++) {
-            const fr_t e = ld_aos_uniform(E, k);
-            const uint64_t w = (uint64_t)((int64_t)ld_stream(col + (size_t)k * N) + off);
 #pragma unroll
-            for (int p = 0; p < NP; p++) cols_mac(acc[p], (uint32_t)(w >> (20 * p)) & 0xFFFFFu, e);
+            for (int u = 0; u < 8; u++) mac(v[u], k + u);
+            k += 8;
         }
+        for (; k < k1; k++) mac(ld_stream(col + (size_t)k * N), k);
     }
     fr_t r = fr_zero();
 #pragma unroll
@@ -1068,44 +1101,57 @@ __global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict_
         uint32_t tt[10];
         cols_normalize(acc[p], tt);
         fr_t f = redc_wide<10>(tt);
-        if (p > 0) f = mont_mul(f, piece_scale(p));
+        if (p > 0) f = mont_mul(f, PB == 20 ? piece_scale(p) : piece_scale22(p));
         r = fr_add(r, f);
     }
     if (i < N) st_aos(q.partial, (size_t)c * N + i, r);
 }
-void launch_eqdot_multi(hipStream_t s, int is64, uint32_t np, const EqDotDesc* d_dev, uint32_t nd,
-                        uint32_t nblocks) {
-    if (!is64) {
-        if (np <= 1) k_eqdot_multi<int32_t, 1><<<nblocks, NT, 0, s>>>(d_dev, nd);
-        else k_eqdot_multi<int32_t, 2><<<nblocks, NT, 0, s>>>(d_dev, nd);
-    } else {
-        if (np <= 3) k_eqdot_multi<int64_t, 3><<<nblocks, NT, 0, s>>>(d_dev, nd);
-        else k_eqdot_multi<int64_t, 4><<<nblocks, NT, 0, s>>>(d_dev, nd);
-    }
+// one launch for two variants: each descriptor's `variant` selects V0 or V1 (uniform per
+// block), so the int32 (X, W) and int64 (Y) reductions of a batch share one grid
+template <typename V0, typename V1>
+__global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict__ d, uint32_t nd) {
+    const EqDotDesc& q = d[find_desc_uniform(d, nd)];
+    const uint32_t local = blockIdx.x - q.blk_begin;
+    if (q.variant) eqdot_body<V1>(q, local);
+    else eqdot_body<V0>(q, local);
+}
+void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_t nd, uint32_t nblocks) {
+    if (!wide) k_eqdot_multi<EqdotI32x1, EqdotI64x2><<<nblocks, NT, 0, s>>>(d_dev, nd);
+    else k_eqdot_multi<EqdotI32x2, EqdotI64x3><<<nblocks, NT, 0, s>>>(d_dev, nd);
 }
 
 // out[i] = sum_c partial[c*N+i] - corr (i < N; zero up to Npad), or, when E is set, the
-// block partial of sum_i E_m[i] * (sum_c partial[c*N+i] - corr) into dot[slot]
+// block partial of sum_i E_m[i] * (sum_c partial[c*N+i] - corr) into dot[slot].  A block
+// covers 64 columns; wave w adds the chunks c = w (mod 4) with four loads in flight, and
+// the four wave sums meet in LDS.
 __global__ __launch_bounds__(NT) void k_sum_chunks_multi(const SumChunksDesc* __restrict__ d, uint32_t nd) {
     const SumChunksDesc& q = d[find_desc_uniform(d, nd)];
     const uint32_t local = blockIdx.x - q.blk_begin;
-    const uint32_t i = local * NT + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t i = local * 64 + lane;
+    __shared__ fr_t part[NT / 64][64];
     fr_t s = fr_zero();
     if (i < q.N) {
-        uint32_t c = 0;
-        for (; c + 4 <= q.nch; c += 4) {  // four chunk loads in flight
+        uint32_t c = w;
+        for (; c + 12 < q.nch; c += 16) {
             fr_t v[4];
 #pragma unroll
-            for (int u = 0; u < 4; u++) v[u] = ld_aos(q.partial, (size_t)(c + u) * q.N + i);
+            for (int u = 0; u < 4; u++) v[u] = ld_aos(q.partial, (size_t)(c + 4 * u) * q.N + i);
 #pragma unroll
             for (int u = 0; u < 4; u++) s = fr_add(s, v[u]);
         }
-        for (; c < q.nch; c++) s = fr_add(s, ld_aos(q.partial, (size_t)c * q.N + i));
-        s = fr_sub(s, to_fr(q.corr.v));
+        for (; c < q.nch; c += 4) s = fr_add(s, ld_aos(q.partial, (size_t)c * q.N + i));
     }
+    part[w][lane] = s;
+    __syncthreads();
+    if (w) return;
+#pragma unroll
+    for (int u = 1; u < NT / 64; u++) s = fr_add(s, part[u][lane]);
+    s = i < q.N ? fr_sub(s, to_fr(q.corr.v)) : fr_zero();
     if (q.E) {
-        fr_t acc[1] = {i < q.N ? mont_mul(ld_aos(q.E, i), s) : fr_zero()};
-        block_reduce_store_at<1>(acc, q.dot, local);
+        fr_t t = i < q.N ? mont_mul(ld_aos(q.E, i), s) : fr_zero();
+        t = fr_wave_sum(t);
+        if (lane == 0) st_aos(q.dot, local, t);
     } else if (i < q.Npad) {
         st_fr(reinterpret_cast<uint4*>(q.out_lo), reinterpret_cast<uint4*>(q.out_hi), i, s);
     }
@@ -1170,19 +1216,46 @@ void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b) {
 // persistent matmul round loop (see ZkipPersist): tables in LDS, one host round trip per
 // round, no device-side reduction or barrier across blocks
 // ------------------------------------------------------------------------------------
-// thread 0 only: wait until the job's command word equals want; false on ZKH_QUIT or when
-// the deadline passes (then *err is set)
-ZDEV bool persist_wait(uint32_t* cmd, uint32_t want, uint32_t* err, uint64_t deadline) {
+// Host <-> device words travel as 16-byte quads [seq, w0, w1, w2], each written and read
+// with one 16-byte access (system coherent); a reader takes the data words of a message
+// only when every quad of it shows the expected seq, so no fence orders data and flag and
+// the challenge arrives with the poll itself.
+typedef uint32_t zkh_v4u __attribute__((ext_vector_type(4)));
+ZDEV uint4 ld_quad_sys(const uint32_t* p) {
+    zkh_v4u r;
+    asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1\n\ts_waitcnt vmcnt(0)" : "=v"(r) : "v"((uint64_t)p) : "memory");
+    return make_uint4(r.x, r.y, r.z, r.w);
+}
+ZDEV void st_quad_sys(uint32_t* p, uint4 v) {
+    const zkh_v4u x = {v.x, v.y, v.z, v.w};
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" : : "v"((uint64_t)p), "v"(x) : "memory");
+}
+// wave 0: wait until the three command quads show want; lanes 0..2 then hold challenge
+// words 3*lane .. 3*lane+2 in (y, z, w).  False on ZKH_QUIT or when the deadline passes
+// (then *err is set).  Every lane of wave 0 calls it and gets the same result.
+ZDEV bool persist_wait(const uint32_t* cmd, uint32_t want, uint32_t* err, uint64_t deadline, uint4& quad) {
+    const uint32_t lane = threadIdx.x & 63;
     const uint64_t t0 = wall_clock64();
     for (;;) {
-        const uint32_t v = __hip_atomic_load(cmd, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (v == want) return true;
-        if (v == ZKH_QUIT) return false;
+        const uint4 qd = lane < 3 ? ld_quad_sys(cmd + 4 * lane) : make_uint4(want, 0, 0, 0);
+        if (__ballot(qd.x == ZKH_QUIT)) return false;
+        if (!__ballot(qd.x != want)) {
+            quad = qd;
+            return true;
+        }
         if (wall_clock64() - t0 > deadline) {
-            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (lane == 0) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             return false;
         }
         __builtin_amdgcn_s_sleep(1);
+    }
+}
+// wave 0: words[0 .. nw) of pub (LDS) as quads with seq into slot (lanes < ceil(nw/3))
+ZDEV void persist_publish(uint32_t* slot, const uint32_t* pub, uint32_t nw, uint32_t seq) {
+    const uint32_t lane = threadIdx.x & 63;
+    if (lane * 3 < nw) {
+        const uint32_t b = 3 * lane;
+        st_quad_sys(slot + 4 * lane, make_uint4(seq, pub[b], b + 1 < nw ? pub[b + 1] : 0u, b + 2 < nw ? pub[b + 2] : 0u));
     }
 }
 #define NTP 1024  // threads of a persistent round block (16 waves)
@@ -1203,8 +1276,8 @@ ZDEV void persist_stamp(uint32_t* slot, uint64_t t_cmd) {
 // phase from the first fold on.
 __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
     extern __shared__ uint4 zl[];  // a.lo | a.hi | b.lo | b.hi, ls entries each
-    __shared__ uint32_t sj, sok;
-    __shared__ fr_t sx, red[15];
+    __shared__ uint32_t sj, sok, pubw[24], sxw[9];
+    __shared__ fr_t red[15];
     if (threadIdx.x == 0) {
         uint32_t j = 0;
         while (j + 1 < P.nd && P.d[j + 1].blk_begin <= blockIdx.x) j++;
@@ -1260,22 +1333,32 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
             if (lane == 0) red[wv] = acc;
         }
         __syncthreads();
-        if (wv == 0 && lane < 3) {  // lane g adds group g's active waves
-            const uint32_t na = min(5u, (h + 63) >> 6);
-            fr_t t = red[5 * lane];
-            for (uint32_t i = 1; i < na; i++) t = fr_add(t, red[5 * lane + i]);
-            st_aos(slot, lane, t);
-        }
-        if (threadIdx.x == 0) {  // same wave as the stores above: the release covers them
-            persist_stamp(slot, t_cmd);
-            __hip_atomic_store(slot + 63, r + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-            sok = persist_wait(q.cmd, r + 1, P.err, P.deadline);
-            if (sok) sx = ld_aos(q.cmd + 8, 0);
+        if (wv == 0) {
+            if (lane < 3) {  // lane g adds group g's active waves
+                const uint32_t na = min(5u, (h + 63) >> 6);
+                fr_t t = red[5 * lane];
+                for (uint32_t i = 1; i < na; i++) t = fr_add(t, red[5 * lane + i]);
+#pragma unroll
+                for (int j = 0; j < 8; j++) pubw[8 * lane + j] = t.v[j];
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) persist_stamp(slot, t_cmd);
+            persist_publish(slot, pubw, 24, r + 1);
+            uint4 qd;
+            const bool ok = persist_wait(q.cmd, r + 1, P.err, P.deadline, qd);
+            if (lane < 3) {
+                sxw[3 * lane] = qd.y;
+                sxw[3 * lane + 1] = qd.z;
+                sxw[3 * lane + 2] = qd.w;
+            }
+            if (lane == 0) sok = ok;
             t_cmd = wall_clock64();
         }
         __syncthreads();
         if (!sok) return;
-        const fr_t x = sx;
+        fr_t x;
+#pragma unroll
+        for (int j = 0; j < 8; j++) x.v[j] = sxw[j];
         for (uint32_t t = threadIdx.x; t < 2 * h; t += NTP) {  // a for t < h, b for t >= h
             const bool tb = t >= h;
             const uint32_t k = tb ? t - h : t;
@@ -1287,11 +1370,15 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
         __syncthreads();
         m = h;
     }
-    if (threadIdx.x == 0) {
-        st_aos(slot, 0, ld_fr(alo, ahi, 0));
-        st_aos(slot, 1, ld_fr(blo, bhi, 0));
-        persist_stamp(slot, t_cmd);
-        __hip_atomic_store(slot + 63, r + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (wv == 0) {  // the block's folded entries a[0], b[0]
+        if (lane < 2) {
+            const fr_t t = lane ? ld_fr(blo, bhi, 0) : ld_fr(alo, ahi, 0);
+#pragma unroll
+            for (int j = 0; j < 8; j++) pubw[8 * lane + j] = t.v[j];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) persist_stamp(slot, t_cmd);
+        persist_publish(slot, pubw, 16, r + 1);
     }
 }
 // An ordinary launch on the stream: the blocks never wait for each other, only for the

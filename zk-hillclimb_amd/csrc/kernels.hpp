@@ -167,7 +167,8 @@ struct EqDotDesc {  // partial[c*N+i] = sum_{k in rows [c*kchunk, (c+1)*kchunk)}
     const void* M;
     const uint32_t* E;
     uint32_t* partial;
-    uint32_t K, N, kchunk, bits, blk_begin, pad_;
+    uint32_t K, N, kchunk, bits, blk_begin;
+    uint32_t variant;  // 0: int32 elements, 1: int64 elements (pieces fixed by the launch)
 };
 struct SumChunksDesc {
     const uint32_t* partial;
@@ -188,8 +189,10 @@ struct ZkipDesc {
     fr_arg vm;  // challenge of the fold, Montgomery form
 };
 void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, uint32_t nblocks);
-void launch_eqdot_multi(hipStream_t s, int is64, uint32_t np, const EqDotDesc* d_dev, uint32_t nd,
-                        uint32_t nblocks);
+// eq-weighted integer reductions; wide = 0: int32 with |v| < 2^19 (one 20-bit piece, chunks
+// <= 2048 rows) and int64 with |v| < 2^43 (two 22-bit pieces); wide = 1: any int32 (two
+// 22-bit pieces) and any int64 (three); chunks <= 512 rows for 22-bit pieces
+void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_t nd, uint32_t nblocks);
 void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks);
 #define ZKH_MAX_BATCH 32
 struct ZkipBatch {  // passed by value as the kernel argument (<= 2.1 KB)
@@ -202,16 +205,21 @@ void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
 // ---- persistent matmul round loop ----
 // Each job's tables a, b (n = 2^L entries) are spread cyclically over nb = 2^lgnb blocks
 // (block l holds entries l + nb*k in LDS), so the pairs (i, i + m/2) of every round with
-// m >= 2*nb stay inside one block.  Round r: every block writes its sums (sum a0b0,
-// sum a1b1, sum da*db, each x 2^-256; AoS words 0..23) to its host slot and stores r + 1
-// into slot word 63 (system-scope release); it then waits for the host to store r + 1 into
-// cmd[0] with the challenge (Montgomery form) in cmd[8..16), and folds.  After the last
-// local round each block stores its single folded entries of a and b (slot words 0..15)
-// with sequence number rounds + 1 and exits.  cmd[0] == ZKH_QUIT makes the job's blocks
-// exit; a block that waits longer than `deadline` ticks of the 100 MHz clock sets *err and
-// exits.
+// m >= 2*nb stay inside one block.  Messages between host and device are 16-byte quads
+// [seq, w, w, w] (zkh_quad_* below), each written with one 16-byte store: a message is
+// complete when all its quads show the expected seq.  Round r: every block publishes its
+// sums (sum a0b0, sum a1b1, sum da*db, each x 2^-256: 24 words, 8 quads) with seq r + 1;
+// it then waits for the job's command (3 quads, seq r + 1) carrying the challenge
+// (Montgomery form, 8 words) and folds.  After the last local round each block publishes
+// its single folded entries of a and b (16 words, 6 quads) with seq rounds + 1 and exits.
+// A command quad with seq ZKH_QUIT makes the job's blocks exit; a block that waits longer
+// than `deadline` ticks of the 100 MHz clock sets *err and exits.  Slot words 56..59 hold
+// the block's clock stamps (tracing only).
 #define ZKH_QUIT 0xffffffffu
 #define ZKH_PSLOT 64  // words per block slot and per job command area
+// quad messages: data word i lives at 4*(i/3) + 1 + i%3, quad q's seq at 4*q
+inline uint32_t zkh_quad_word(uint32_t i) { return 4 * (i / 3) + 1 + i % 3; }
+inline uint32_t zkh_quad_count(uint32_t nwords) { return (nwords + 2) / 3; }
 #define ZKH_PLS_MAX 512u  // entries per block and table (32 KiB of LDS for both tables)
 struct ZkipPJob {
     const uint32_t* a_lo;

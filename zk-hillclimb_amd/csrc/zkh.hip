@@ -1074,7 +1074,6 @@ extern "C" int zkh_pad(zkh_ctx* c, const zkh_tensor* t, const uint32_t* shape, u
 // Batched matmul sumchecks: all jobs share each launch (eq tables, eq-weighted
 // reductions, every round) and one host synchronisation per round; transcripts stay
 // independent, one per job.
-static uint32_t np_for(uint32_t bits) { return (bits + 1 + 19) / 20; }
 
 static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj);
 extern "C" int zkh_mm_prove_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
@@ -1198,8 +1197,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     // 2) eq-weighted reductions: Y by eb (then dotted with eo -> claim), X by eb, W^T by eo
     struct Red {
         EqDotDesc d;
-        int is64;
-        uint32_t np, nch, Npad, job, what;  // what: 0 Y, 1 X, 2 W
+        int is64, wide;
+        uint32_t nch, Npad, job, what;  // what: 0 Y, 1 X, 2 W
         Fr corr;
     };
     std::vector<Red> reds;
@@ -1221,11 +1220,17 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             uint32_t K = what == 2 ? in.OUT : in.B;
             uint32_t N = what == 0 ? in.OUT : in.IN;
             uint32_t bits = what == 0 ? in.Y->bits : what == 1 ? in.X->bits : in.W->bits;
-            // row chunks of 128..2048 rows: up to 2^17 (column, chunk) cells per reduction
-            // spread it over the CUs, and at least 128 rows per chunk keep the per-cell field
-            // reduction (and the partials' traffic) small next to the streamed rows
+            r.is64 = what == 0 && in.Y->kind == ZKH_KIND_I64;
+            // piece layout (see launch_eqdot_multi): narrow = one 20-bit piece for int32 /
+            // two 22-bit pieces for int64; chunks hold at most 2048 / 512 rows accordingly
+            r.wide = r.is64 ? bits + 1 > 44 : bits + 1 > 20;
+            const uint32_t maxrows = (!r.is64 && !r.wide) ? 2048 : 512;
+            // row chunks: up to 2^17 (column, chunk) cells per reduction spread it over the
+            // CUs; at least 128 rows (64 for 8-byte elements) per chunk keep the per-cell
+            // field reduction and the partials' traffic small next to the streamed rows
             const uint32_t ncell = std::max<uint32_t>(1, (131072 + N - 1) / N);
-            const uint32_t kchunk = std::min<uint32_t>(std::max<uint32_t>((K + ncell - 1) / ncell, 128), 2048);
+            const uint32_t minrows = r.is64 ? 64 : 128;
+            const uint32_t kchunk = std::min<uint32_t>(std::max<uint32_t>((K + ncell - 1) / ncell, minrows), maxrows);
             const uint32_t nch = (K + kchunk - 1) / kchunk;
             r.d.M = M;
             r.d.E = eq_d + 8 * (what == 2 ? q.eo_off : q.eb_off);
@@ -1233,8 +1238,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             r.d.N = N;
             r.d.kchunk = kchunk;
             r.d.bits = bits;
-            r.is64 = what == 0 && in.Y->kind == ZKH_KIND_I64;
-            r.np = np_for(bits);
+            r.d.variant = r.is64 ? 1 : 0;
             r.nch = nch;
             r.Npad = what == 0 ? N : q.INp;
             r.job = j;
@@ -1250,27 +1254,25 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     uint32_t* part_d = (uint32_t*)scratch(c, SL_TMP6, part_total * 32, &rc);
     if (rc) return rc;
     for (auto& r : reds) r.d.partial = part_d + (uintptr_t)r.d.partial / 4;
-    // group the reductions by (int width, pieces) -> one launch per group
+    // group the reductions by piece layout -> one launch per group (normally one)
     std::vector<EqDotDesc> dots;
     struct Grp {
-        int is64;
-        uint32_t np, first, count, blocks;
+        int wide;
+        uint32_t first, count, blocks;
     };
     std::vector<Grp> groups;
-    for (int is64 = 0; is64 < 2; is64++)
-        for (uint32_t np = 1; np <= 4; np++) {
-            Grp g{is64, np, (uint32_t)dots.size(), 0, 0};
-            for (auto& r : reds) {
-                uint32_t gnp = r.is64 ? (r.np <= 3 ? 3 : 4) : (r.np <= 1 ? 1 : 2);
-                if (r.is64 != is64 || gnp != np) continue;
-                EqDotDesc d = r.d;
-                d.blk_begin = g.blocks;
-                g.blocks += ((r.d.N + 255) / 256) * r.nch;
-                dots.push_back(d);
-                g.count++;
-            }
-            if (g.count) groups.push_back(g);
+    for (int wide = 0; wide < 2; wide++) {
+        Grp g{wide, (uint32_t)dots.size(), 0, 0};
+        for (auto& r : reds) {
+            if (r.wide != wide) continue;
+            EqDotDesc d = r.d;
+            d.blk_begin = g.blocks;
+            g.blocks += ((r.d.N + 255) / 256) * r.nch;
+            dots.push_back(d);
+            g.count++;
         }
+        if (g.count) groups.push_back(g);
+    }
     // 3) chunk sums (X, W -> planes; Y -> dot with eo into pinned claim partials)
     std::vector<SumChunksDesc> sums;
     uint32_t sum_blocks = 0, claim_slots = 0;
@@ -1283,7 +1285,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         d.Npad = r.Npad;
         d.blk_begin = sum_blocks;
         fr_store(r.corr, d.corr.v);
-        uint32_t nb = (r.Npad + 255) / 256;
+        uint32_t nb = (r.Npad + 63) / 64;  // k_sum_chunks_multi: 64 columns per block
         if (r.what == 0) {
             d.E = eq_d + 8 * q.eo_off;
             d.dot = (uint32_t*)(uintptr_t)claim_slots;  // slot index, fixed below
@@ -1330,8 +1332,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     {
         ProfScope ps(c, "eqdot", red_bytes);
         for (auto& g : groups)
-            launch_eqdot_multi(c->stream, g.is64, g.np, (const EqDotDesc*)(desc_d + o_dot) + g.first, g.count,
-                               g.blocks);
+            launch_eqdot_multi(c->stream, g.wide, (const EqDotDesc*)(desc_d + o_dot) + g.first, g.count, g.blocks);
     }
     {
         double b = 0;
@@ -1435,8 +1436,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         uint32_t* ps = c->ps_host;
         for (uint32_t j = 0; j < nj; j++) {
             const uint32_t nb = 1u << lgnb[j];
-            for (uint32_t b = 0; b < nb; b++) ps[slot_off[j] + b * ZKH_PSLOT + 63] = 0;
-            ps[cmd_off[j]] = 0;
+            for (uint32_t b = 0; b < nb; b++) memset(ps + slot_off[j] + b * ZKH_PSLOT, 0, 32 * 4);
+            memset(ps + cmd_off[j], 0, 12 * 4);
         }
         ps[0] = 0;
         const uint64_t deadline_ticks = c->clock_khz * 1000 * 20;  // 20 s without a command
@@ -1457,8 +1458,15 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             P.deadline = deadline_ticks;
             P.ls_max = std::max(P.ls_max, J[j].INp >> lgnb[j]);
         }
+        // a job's command: the challenge (Montgomery form) in three quads, seqs written last
+        auto send_cmd = [&](uint32_t j, uint32_t seq, const uint32_t* xm) {
+            uint32_t* cmd = ps + cmd_off[j];
+            if (xm)
+                for (uint32_t i = 0; i < 8; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
+            for (uint32_t qd = 0; qd < 3; qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
+        };
         auto quit_all = [&]() {
-            for (uint32_t j = 0; j < nj; j++) __atomic_store_n(ps + cmd_off[j], ZKH_QUIT, __ATOMIC_RELEASE);
+            for (uint32_t j = 0; j < nj; j++) send_cmd(j, ZKH_QUIT, nullptr);
             (void)hipStreamSynchronize(c->stream);
         };
         double pbytes = 0;
@@ -1481,11 +1489,21 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         std::atomic<int> abort_why{0};  // 1 device error, 2 kernel ended early, 3 no progress
         std::atomic<int> dev_err{0};
         const double t_start = now_us();
+        // all blocks of job j have published message seq (round sums: 24 words; the final
+        // folded entries after the last local round: 16 words)
         auto ready = [&](uint32_t j, uint32_t seq) {
             const uint32_t nb = 1u << lgnb[j];
+            const uint32_t nq = zkh_quad_count(seq <= R[j] ? 24 : 16);
             for (uint32_t b = 0; b < nb; b++)
-                if (__atomic_load_n(ps + slot_off[j] + b * ZKH_PSLOT + 63, __ATOMIC_ACQUIRE) != seq) return false;
+                for (uint32_t qd = 0; qd < nq; qd++)
+                    if (__atomic_load_n(ps + slot_off[j] + b * ZKH_PSLOT + 4 * qd, __ATOMIC_ACQUIRE) != seq)
+                        return false;
             return true;
+        };
+        auto slot_fr = [&](const uint32_t* sl, uint32_t k) {  // Fr k of a block's message
+            uint32_t v[8];
+            for (uint32_t i = 0; i < 8; i++) v[i] = sl[zkh_quad_word(8 * k + i)];
+            return fr_load(v);
         };
         const int T = (int)std::min<uint32_t>(nj, (uint32_t)host_threads());
         const bool tracing = trace_on();
@@ -1519,24 +1537,25 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                     if (rnd[a] < R[j]) {
                         Fr s3[3] = {kZero, kZero, kZero};
                         for (uint32_t b = 0; b < nb; b++)
-                            for (int k = 0; k < 3; k++) s3[k] = fr_add(s3[k], fr_load(sl + b * ZKH_PSLOT + 8 * k));
+                            for (int k = 0; k < 3; k++) s3[k] = fr_add(s3[k], slot_fr(sl + b * ZKH_PSLOT, k));
                         if (!round_step(j, rnd[a], fix1(s3[0]), fix1(s3[1]), fix1(s3[2]))) {
-                            __atomic_store_n(ps + cmd_off[j], ZKH_QUIT, __ATOMIC_RELEASE);
+                            send_cmd(j, ZKH_QUIT, nullptr);
                             done[a] = 1;
                             left--;
                             continue;
                         }
-                        fr_store(J[j].xm, ps + cmd_off[j] + 8);
+                        uint32_t xm[8];
+                        fr_store(J[j].xm, xm);
                         rnd[a]++;
-                        __atomic_store_n(ps + cmd_off[j], rnd[a], __ATOMIC_RELEASE);
+                        send_cmd(j, rnd[a], xm);
                         continue;
                     }
                     // the blocks' folded entries: the remaining lgnb rounds on the host
                     ta.resize(nb);
                     tb.resize(nb);
                     for (uint32_t b = 0; b < nb; b++) {
-                        ta[b] = fr_load(sl + b * ZKH_PSLOT);
-                        tb[b] = fr_load(sl + b * ZKH_PSLOT + 8);
+                        ta[b] = slot_fr(sl + b * ZKH_PSLOT, 0);
+                        tb[b] = slot_fr(sl + b * ZKH_PSLOT, 1);
                     }
                     done[a] = 1;
                     left--;
