@@ -518,25 +518,42 @@ __global__ void k_fold(TabDev t, uint32_t h, fr_t vm) {
 void launch_fold(hipStream_t s, Tab t, uint32_t h, const uint32_t* v_m_host) {
     k_fold<<<grid_for(h, NT, 8192), NT, 0, s>>>(tab_dev(t), h, to_fr(v_m_host));
 }
-__global__ void k_axpy(const uint4* alo, const uint4* ahi, fr_t cm, const uint4* blo,
-                       const uint4* bhi, uint32_t n, uint4* olo, uint4* ohi) {
+// calls f with the loader of an in-place operand
+template <typename F>
+static void with_loader(const Src& x, F&& f) {
+    if (x.kind == 0) {
+        DevPlanes p{(uint32_t*)x.p, x.cap};
+        f(LdPlanes{PL_LO(p), PL_HI(p)});
+    } else if (x.kind == 1) {
+        f(LdI32{(const int32_t*)x.p});
+    } else {
+        f(LdI64{(const int64_t*)x.p});
+    }
+}
+template <typename LA, typename LB>
+__global__ void k_axpy(LA a, fr_t cm, LB b, uint32_t n, uint4* olo, uint4* ohi) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        st_fr(olo, ohi, i, fr_add(ld_fr(alo, ahi, i), mont_mul(cm, ld_fr(blo, bhi, i))));
+        st_fr(olo, ohi, i, fr_add(a(i), mont_mul(cm, b(i))));
 }
-void launch_axpy(hipStream_t s, DevPlanes a, const uint32_t* c_m_host, DevPlanes b, uint32_t n,
-                 DevPlanes out) {
-    k_axpy<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(a), PL_HI(a), to_fr(c_m_host), PL_LO(b),
-                                                PL_HI(b), n, PL_LO(out), PL_HI(out));
+void launch_axpy(hipStream_t s, Src a, const uint32_t* c_m_host, Src b, uint32_t n, DevPlanes out) {
+    const fr_t cm = to_fr(c_m_host);
+    with_loader(a, [&](auto la) {
+        with_loader(b, [&](auto lb) {
+            k_axpy<<<grid_for(n, NT, 8192), NT, 0, s>>>(la, cm, lb, n, PL_LO(out), PL_HI(out));
+        });
+    });
 }
-__global__ void k_hadamard(const uint4* alo, const uint4* ahi, const uint4* blo, const uint4* bhi,
-                           uint32_t n, uint4* olo, uint4* ohi) {
+template <typename LA, typename LB>
+__global__ void k_hadamard(LA a, LB b, uint32_t n, uint4* olo, uint4* ohi) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        st_fr(olo, ohi, i,
-              mont_mul(mont_mul(ld_fr(alo, ahi, i), ld_fr(blo, bhi, i)), r2_m()));
+        st_fr(olo, ohi, i, mont_mul(mont_mul(a(i), b(i)), r2_m()));
 }
-void launch_hadamard(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, DevPlanes out) {
-    k_hadamard<<<grid_for(n, NT, 8192), NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n,
-                                                    PL_LO(out), PL_HI(out));
+void launch_hadamard(hipStream_t s, Src a, Src b, uint32_t n, DevPlanes out) {
+    with_loader(a, [&](auto la) {
+        with_loader(b, [&](auto lb) {
+            k_hadamard<<<grid_for(n, NT, 8192), NT, 0, s>>>(la, lb, n, PL_LO(out), PL_HI(out));
+        });
+    });
 }
 
 // ------------------------------------------------------------------------------------
@@ -610,12 +627,12 @@ __global__ void k_lu_map_planes(const uint4* lo, const uint4* hi, uint32_t n, fr
         st_fr(olo, ohi, i, idx < N ? ld_fr(mlo, mhi, idx) : fr_zero());
     }
 }
-__global__ void k_lu_map_i32(const int32_t* __restrict__ S, uint32_t n, int32_t low,
-                             const uint4* mlo, const uint4* mhi, uint32_t N, uint4* olo,
-                             uint4* ohi) {
+template <typename LM>
+__global__ void k_lu_map_i32(const int32_t* __restrict__ S, uint32_t n, int32_t low, LM mapped, uint32_t N,
+                             uint4* olo, uint4* ohi) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         uint32_t idx = lu_index_i32(S[i], low);
-        st_fr(olo, ohi, i, idx < N ? ld_fr(mlo, mhi, idx) : fr_zero());
+        st_fr(olo, ohi, i, idx < N ? mapped(idx) : fr_zero());
     }
 }
 void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
@@ -624,19 +641,21 @@ void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t
                                                        PL_LO(mapped), PL_HI(mapped), mapped.cap,
                                                        PL_LO(out), PL_HI(out));
 }
-void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
-                       DevPlanes mapped, DevPlanes out) {
-    k_lu_map_i32<<<grid_for(n, NT, 8192), NT, 0, s>>>(S, n, low, PL_LO(mapped), PL_HI(mapped),
-                                                    mapped.cap, PL_LO(out), PL_HI(out));
+void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low, Src mapped, uint32_t N,
+                       DevPlanes out) {
+    with_loader(mapped, [&](auto lm) {
+        k_lu_map_i32<<<grid_for(n, NT, 8192), NT, 0, s>>>(S, n, low, lm, N, PL_LO(out), PL_HI(out));
+    });
 }
 
 // Batched inversion (Montgomery's trick).  Block b covers INV_CHK*NT entries; thread t
 // owns entries base + j*NT + t.  Pass 1 stores running products (Montgomery domain) in A
 // and a block-wide inclusive prefix/suffix scan of the thread totals gives each thread
-// the product of all OTHER threads' totals.  The block total goes to blockprod; the host
-// inverts all block totals with one more Montgomery trick and a single exponentiation.
+// the product of all OTHER threads' totals.  The block total goes to blockprod.
 // Pass 2 walks each thread's entries backwards.  Zero entries (x+beta = 0) take 1 in the
-// products and produce 0, the reference's Fermat convention.
+// products and produce 0, the reference's Fermat convention.  Between the passes,
+// k_inv_blocks turns the block totals into "all other blocks" products and publishes the
+// grand product, which the host inverts once.
 #define INV_CHK 16
 __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
@@ -671,14 +690,61 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
     st_aos(others, blockIdx.x * NT + t, mont_mul(ex_pre, ex_suf));
     if (t == NT - 1) st_aos(blockprod, blockIdx.x, pre[NT - 1]);
 }
+// One block over the nb block products (Montgomery form): others[b] = product of all the
+// other blocks' products, and the grand product P published (pub.host_out[0], then the
+// flag) for the host to invert.  Thread t owns products [t*per, (t+1)*per).
+#define NTI 1024
+__global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__ bp, uint32_t nb,
+                                                    uint32_t* others, Publish pub) {
+    __shared__ fr_t pre[NTI], suf[NTI];
+    const uint32_t t = threadIdx.x;
+    const uint32_t per = (nb + NTI - 1) / NTI;
+    const uint32_t b0 = t * per, b1 = min(nb, b0 + per);
+    fr_t loc = one_m();
+    for (uint32_t b = b0; b < b1; b++) {  // local exclusive prefixes into others[]
+        st_aos(others, b, loc);
+        loc = mont_mul(loc, ld_aos(bp, b));
+    }
+    pre[t] = loc;
+    suf[t] = loc;
+    __syncthreads();
+    for (uint32_t off = 1; off < NTI; off <<= 1) {
+        const fr_t p = pre[t], q = suf[t];
+        const fr_t pp = t >= off ? pre[t - off] : one_m();
+        const fr_t qq = t + off < NTI ? suf[t + off] : one_m();
+        __syncthreads();
+        pre[t] = mont_mul(p, pp);
+        suf[t] = mont_mul(q, qq);
+        __syncthreads();
+    }
+    const fr_t ex_pre = t > 0 ? pre[t - 1] : one_m();
+    const fr_t ex_suf = t + 1 < NTI ? suf[t + 1] : one_m();
+    fr_t rs = mont_mul(ex_pre, ex_suf);  // the other threads' products
+    for (int b = (int)b1 - 1; b >= (int)b0; b--) {  // times the local suffix
+        st_aos(others, b, mont_mul(ld_aos(others, b), rs));
+        rs = mont_mul(rs, ld_aos(bp, b));
+    }
+    if (t == NTI - 1) {
+        st_aos(pub.host_out, 0, pre[NTI - 1]);
+        __threadfence_system();
+        __hip_atomic_store(pub.host_flag, pub.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, uint32_t* others_blk,
+                       Publish pub) {
+    k_inv_blocks<<<1, NTI, 0, s>>>(blockprod, nb, others_blk, pub);
+}
+// 1/blockprod[b] = invP * others_blk[b] (Montgomery form); then each thread walks its
+// entries backwards
 __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
                                                   const uint32_t* __restrict__ others,
-                                                  const uint32_t* __restrict__ blockinv) {
+                                                  const uint32_t* __restrict__ others_blk, fr_t inv_total_m) {
     const uint32_t t = threadIdx.x;
     const uint32_t base = blockIdx.x * NT * INV_CHK;
     // 1/run_t = 1/blockprod * prod(other threads' runs)
-    fr_t y = mont_mul(ld_aos(blockinv, blockIdx.x), ld_aos(others, blockIdx.x * NT + t));
+    const fr_t binv = mont_mul(inv_total_m, ld_aos(others_blk, blockIdx.x));
+    fr_t y = mont_mul(binv, ld_aos(others, blockIdx.x * NT + t));
     for (int j = INV_CHK - 1; j >= 0; j--) {
         uint32_t idx = base + (uint32_t)j * NT + t;
         if (idx >= n) continue;
@@ -698,9 +764,10 @@ void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
                                              PL_HI(A), others, blockprod);
 }
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
-                      DevPlanes A, const uint32_t* others, const uint32_t* blockinv) {
+                      DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
+                      const uint32_t* inv_total_m_host) {
     k_inv_pass2<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
-                                             PL_HI(A), others, blockinv);
+                                             PL_HI(A), others, others_blk, to_fr(inv_total_m_host));
 }
 
 // ------------------------------------------------------------------------------------

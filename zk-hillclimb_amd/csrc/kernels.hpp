@@ -101,9 +101,14 @@ void launch_rescale(hipStream_t s, int kind, const void* x, uint32_t cap, uint32
                     int64_t* q, int64_t* rem);
 // MSB fold dst[i] = src[i] + v*(src[i+h]-src[i]), i < h (v in Montgomery form)
 void launch_fold(hipStream_t s, Tab t, uint32_t h, const uint32_t* v_m_host);
-void launch_axpy(hipStream_t s, DevPlanes a, const uint32_t* c_m_host, DevPlanes b, uint32_t n,
-                 DevPlanes out);
-void launch_hadamard(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, DevPlanes out);
+// an operand read in place: kind 0 FR planes (p, cap), 1 int32, 2 int64 (field view)
+struct Src {
+    int kind;
+    const void* p;
+    uint32_t cap;
+};
+void launch_axpy(hipStream_t s, Src a, const uint32_t* c_m_host, Src b, uint32_t n, DevPlanes out);
+void launch_hadamard(hipStream_t s, Src a, Src b, uint32_t n, DevPlanes out);
 
 // ---- logUp ----
 void launch_lu_count_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
@@ -114,17 +119,21 @@ void launch_counts_to_planes(hipStream_t s, const uint32_t* counts, uint32_t N, 
 void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
                           DevPlanes mapped, DevPlanes out);
 void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
-                       DevPlanes mapped, DevPlanes out);
-// A[i] = 1/(S[i]+beta) (0 -> 0), Montgomery's batched inversion in two passes around a
-// host step: pass 1 writes running products to A, per-thread "other threads" products to
-// `others` (inv_blocks(n)*256 AoS) and block totals to blockprod (inv_blocks(n) AoS, in
-// Montgomery form); the host writes blockinv[b] = 1/blockprod[b] (Montgomery form);
-// pass 2 writes the plain inverses into A.
+                       Src mapped, uint32_t N, DevPlanes out);
+// A[i] = 1/(S[i]+beta) (0 -> 0), Montgomery's batched inversion: pass 1 writes running
+// products to A, per-thread "other threads" products to `others` (inv_blocks(n)*256 AoS)
+// and block totals to blockprod (inv_blocks(n) AoS, Montgomery form); k_inv_blocks writes
+// others_blk[b] = product of the other blocks' totals and publishes the grand product P
+// (Montgomery form, job 0 of pub); the host inverts P once; pass 2 writes the plain
+// inverses into A given inv_total_m = 1/P (Montgomery form).
 uint32_t inv_blocks(uint32_t n);
 void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, uint32_t* others, uint32_t* blockprod);
+void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, uint32_t* others_blk,
+                       Publish pub);
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
-                      DevPlanes A, const uint32_t* others, const uint32_t* blockinv);
+                      DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
+                      const uint32_t* inv_total_m_host);
 // phase-1 round over A, S (size n): sums e*a0*s0, e*a1*s1, e*da*ds (x 2^-256), a0, a1
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
