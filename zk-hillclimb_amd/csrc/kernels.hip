@@ -693,7 +693,7 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
 // One block over the nb block products (Montgomery form): others[b] = product of all the
 // other blocks' products, and the grand product P published (pub.host_out[0], then the
 // flag) for the host to invert.  Thread t owns products [t*per, (t+1)*per).
-#define NTI 1024
+#define NTI 256
 __global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__ bp, uint32_t nb,
                                                     uint32_t* others, Publish pub) {
     __shared__ fr_t pre[NTI], suf[NTI];

@@ -2127,7 +2127,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
 // ---------------------------------------------------------------------------------------
 static Fr lagrange4(const Fr e[4], const Fr& v) {
     // coefficients through (0..3, e) by Newton differences, then Horner
-    Fr inv2 = fr_inv2(), inv6 = fr_inv(fr_u64(6));
+    static const Fr inv2 = fr_inv2(), inv6 = fr_inv(fr_u64(6));
     Fr d1 = fr_sub(e[1], e[0]), d2 = fr_sub(e[2], e[1]), d3 = fr_sub(e[3], e[2]);
     Fr dd1 = fr_sub(d2, d1), dd2 = fr_sub(d3, d2);
     Fr ddd = fr_sub(dd2, dd1);
