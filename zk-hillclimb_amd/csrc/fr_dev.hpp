@@ -51,18 +51,18 @@ ZDEV fr_t fr_zero() {
     return r;
 }
 
+// Multi-limb carries go through __builtin_addc / __builtin_subc, which lower to
+// v_add_co_u32 / v_addc_co_u32 (v_sub_co / v_subb) chains on VCC: about a third of the
+// instructions of the same arithmetic written with 64-bit intermediates.
+
 // r if x >= r else x, for x < 2r (single correction, as bls12-381.cu:295-300)
 ZDEV fr_t fr_reduce_once(const fr_t& x, uint32_t carry_in) {
     fr_t d;
-    uint64_t br = 0;
+    unsigned br = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        uint64_t t = (uint64_t)x.v[i] - fr_p(i) - br;
-        d.v[i] = (uint32_t)t;
-        br = (t >> 63);
-    }
+    for (int i = 0; i < 8; i++) d.v[i] = __builtin_subc(x.v[i], fr_p(i), br, &br);
     // keep x when it borrowed (x < r) and there was no carry out of limb 7
-    bool keep = (br != 0) && (carry_in == 0);
+    const bool keep = (br != 0) && (carry_in == 0);
     fr_t r;
 #pragma unroll
     for (int i = 0; i < 8; i++) r.v[i] = keep ? x.v[i] : d.v[i];
@@ -71,32 +71,21 @@ ZDEV fr_t fr_reduce_once(const fr_t& x, uint32_t carry_in) {
 
 ZDEV fr_t fr_add(const fr_t& a, const fr_t& b) {
     fr_t s;
-    uint64_t c = 0;
+    unsigned c = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        c = (uint64_t)a.v[i] + b.v[i] + (c >> 32);
-        s.v[i] = (uint32_t)c;
-    }
-    return fr_reduce_once(s, (uint32_t)(c >> 32));
+    for (int i = 0; i < 8; i++) s.v[i] = __builtin_addc(a.v[i], b.v[i], c, &c);
+    return fr_reduce_once(s, c);
 }
 
 ZDEV fr_t fr_sub(const fr_t& a, const fr_t& b) {
     fr_t d;
-    uint64_t br = 0;
+    unsigned br = 0, c = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        uint64_t t = (uint64_t)a.v[i] - b.v[i] - br;
-        d.v[i] = (uint32_t)t;
-        br = t >> 63;
-    }
+    for (int i = 0; i < 8; i++) d.v[i] = __builtin_subc(a.v[i], b.v[i], br, &br);
     // on borrow add r back
-    uint32_t mask = br ? 0xffffffffu : 0u;
-    uint64_t c = 0;
+    const unsigned mask = 0u - br;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        c = (uint64_t)d.v[i] + (fr_p(i) & mask) + (c >> 32);
-        d.v[i] = (uint32_t)c;
-    }
+    for (int i = 0; i < 8; i++) d.v[i] = __builtin_addc(d.v[i], fr_p(i) & mask, c, &c);
     return d;
 }
 

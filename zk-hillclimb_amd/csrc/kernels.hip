@@ -14,6 +14,8 @@
 
 namespace zkh {
 
+__device__ __attribute__((noinline)) fr_t mont_mul_ol(fr_t x, fr_t y) { return mont_mul(x, y); }
+
 #define NT 256  // threads per block for the streaming kernels (4 waves of 64)
 
 ZDEV fr_t mk(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t a4, uint32_t a5,
@@ -73,12 +75,15 @@ template <int K>
 ZDEV void block_reduce_store_at(fr_t* acc, uint32_t* partial, uint32_t slot) {
     __shared__ fr_t red[NT / 64][K];
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    // one accumulator at a time: interleaved wave sums of K accumulators would hold all
+    // their shuffle temporaries at once and set the kernel's register budget (occupancy)
 #pragma unroll
-    for (int k = 0; k < K; k++) acc[k] = fr_wave_sum(acc[k]);
-    if (lane == 0) {
-#pragma unroll
-        for (int k = 0; k < K; k++) red[wid][k] = acc[k];
+    for (int k = 0; k < K; k++) {
+        __builtin_amdgcn_sched_barrier(0);
+        const fr_t w = fr_wave_sum(acc[k]);
+        if (lane == 0) red[wid][k] = w;
     }
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     if (threadIdx.x < K) {
         const int k = threadIdx.x;
@@ -110,10 +115,11 @@ ZDEV void reduce_publish(fr_t* acc, const Publish& P, uint32_t job, uint32_t fir
     __threadfence();
     fr_t s[K];
 #pragma unroll
-    for (int k = 0; k < K; k++) s[k] = fr_zero();
-    for (uint32_t b = threadIdx.x; b < nblk; b += NT)
-#pragma unroll
-        for (int k = 0; k < K; k++) s[k] = fr_add(s[k], ld_aos(P.part, (first + b) * K + k));
+    for (int k = 0; k < K; k++) {  // one sum at a time (register budget, see above)
+        __builtin_amdgcn_sched_barrier(0);
+        s[k] = fr_zero();
+        for (uint32_t b = threadIdx.x; b < nblk; b += NT) s[k] = fr_add(s[k], ld_aos(P.part, (first + b) * K + k));
+    }
     block_reduce_store_at<K>(s, P.host_out, job);
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -483,7 +489,7 @@ void launch_rescale(hipStream_t s, int kind, const void* x, uint32_t cap, uint32
 
 ZDEV fr_t fold_at(const uint4* lo, const uint4* hi, uint32_t j, uint32_t n, const fr_t& vm) {
     fr_t x = ld_fr(lo, hi, j), y = ld_fr(lo, hi, j + n);
-    return fr_add(x, mont_mul(vm, fr_sub(y, x)));
+    return fr_add(x, mont_mul_ol(vm, fr_sub(y, x)));
 }
 // A table taking part in a fused round: read from (slo, shi); when the round folds, the
 // folded entries go to (dlo, dhi), which may alias the source (in-place halving).
@@ -503,8 +509,9 @@ ZDEV void load_pair(const TabDev& t, uint32_t i, uint32_t h, uint32_t n, int fol
                     fr_t& x0, fr_t& x1) {
     if (fold) {
         x0 = fold_at(t.slo, t.shi, i, n, vm);
-        x1 = fold_at(t.slo, t.shi, i + h, n, vm);
         st_fr(t.dlo, t.dhi, i, x0);
+        __builtin_amdgcn_sched_barrier(0);  // one fold's temporaries at a time
+        x1 = fold_at(t.slo, t.shi, i + h, n, vm);
         st_fr(t.dlo, t.dhi, i + h, x1);
     } else {
         x0 = ld_fr(t.slo, t.shi, i);
@@ -779,35 +786,67 @@ struct EqDev {
     uint32_t K;
 };
 // device weight of index i (see EqW)
-ZDEV fr_t eq_w(const EqDev& eq, uint32_t i) { return mont_mul(ld_aos(eq.elo, i & 1023), ld_aos(eq.ehi, i >> 10)); }
+ZDEV fr_t eq_w(const EqDev& eq, uint32_t i) { return mont_mul_ol(ld_aos(eq.elo, i & 1023), ld_aos(eq.ehi, i >> 10)); }
 
+#define SB() __builtin_amdgcn_sched_barrier(0)
+// Per-thread field accumulators kept in LDS (limb-quad planes, 16-byte lanes): registers
+// then hold only the current stage's operands, which lifts the round kernels' occupancy.
+template <int K>
+struct LdsAcc {
+    uint4* lo;  // [K][NT]
+    uint4* hi;
+    ZDEV void zero() {
+#pragma unroll
+        for (int k = 0; k < K; k++) st_fr(lo + k * NT, hi + k * NT, threadIdx.x, fr_zero());
+    }
+    ZDEV void add(int k, const fr_t& x) {
+        const fr_t c = ld_fr(lo + k * NT, hi + k * NT, threadIdx.x);
+        st_fr(lo + k * NT, hi + k * NT, threadIdx.x, fr_add(c, x));
+    }
+    ZDEV void get(fr_t* out) const {
+#pragma unroll
+        for (int k = 0; k < K; k++) out[k] = ld_fr(lo + k * NT, hi + k * NT, threadIdx.x);
+    }
+};
 // phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
 // acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
 __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, int fold, fr_t vm,
                                                   fr_t beta, EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
-    fr_t acc[5];
-#pragma unroll
-    for (int k = 0; k < 5; k++) acc[k] = fr_zero();
+    __shared__ uint4 accl[5 * NT], acch[5 * NT];
+    LdsAcc<5> acc{accl, acch};
+    acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        fr_t wa0, wda;
         {
-            fr_t a0, a1, s0, s1;
+            fr_t a0, a1;
             load_pair(A, i, h, n, fold, vm, a0, a1);
-            load_pair(S, i, h, n, fold, vm, s0, s1);
+            SB();
+            acc.add(3, a0);
+            acc.add(4, a1);
+            SB();
             const fr_t w = eq_w(eq, i);
-            s0 = fr_add(s0, beta);
-            s1 = fr_add(s1, beta);
-            const fr_t wa0 = mont_mul(w, a0);
-            const fr_t wda = mont_mul(w, fr_sub(a1, a0));
-            const fr_t wa1 = fr_add(wa0, wda);
-            acc[0] = fr_add(acc[0], mont_mul(wa0, s0));
-            acc[1] = fr_add(acc[1], mont_mul(wa1, s1));
-            acc[2] = fr_add(acc[2], mont_mul(wda, fr_sub(s1, s0)));
-            acc[3] = fr_add(acc[3], a0);
-            acc[4] = fr_add(acc[4], a1);
+            SB();
+            wa0 = mont_mul_ol(w, a0);
+            SB();
+            wda = mont_mul_ol(w, fr_sub(a1, a0));
         }
+        SB();
+        fr_t s0, s1;
+        load_pair(S, i, h, n, fold, vm, s0, s1);
+        SB();
+        s0 = fr_add(s0, beta);
+        s1 = fr_add(s1, beta);
+        acc.add(0, mont_mul_ol(wa0, s0));
+        SB();
+        acc.add(1, mont_mul_ol(fr_add(wa0, wda), s1));
+        SB();
+        acc.add(2, mont_mul_ol(wda, fr_sub(s1, s0)));
+        SB();
     }
-    reduce_publish<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    fr_t r[5];
+    acc.get(r);
+    reduce_publish<5>(r, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
@@ -828,56 +867,83 @@ template <int fold>
 __global__ __launch_bounds__(NT) void k_lu_phase2_as(TabDev A, TabDev S, uint32_t n, fr_t vm, fr_t beta,
                                                      EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
-    fr_t acc[5];
-#pragma unroll
-    for (int k = 0; k < 5; k++) acc[k] = fr_zero();
+    __shared__ uint4 accl[5 * NT], acch[5 * NT];
+    LdsAcc<5> acc{accl, acch};
+    acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
-        fr_t a0, a1, s0, s1;
-        load_pair(A, i, h, n, fold, vm, a0, a1);
+        fr_t wa0, wda;
+        {
+            fr_t a0, a1;
+            load_pair(A, i, h, n, fold, vm, a0, a1);
+            SB();
+            acc.add(3, a0);
+            acc.add(4, a1);
+            SB();
+            const fr_t w = eq_w(eq, i);
+            SB();
+            wa0 = mont_mul_ol(w, a0);
+            SB();
+            wda = mont_mul_ol(w, fr_sub(a1, a0));
+        }
+        SB();
+        fr_t s0, s1;
         load_pair(S, i, h, n, fold, vm, s0, s1);
-        const fr_t w = eq_w(eq, i);
-        __builtin_amdgcn_sched_barrier(0);
-        const fr_t wa0 = mont_mul(w, a0);
-        __builtin_amdgcn_sched_barrier(0);
-        const fr_t wda = mont_mul(w, fr_sub(a1, a0));
-        __builtin_amdgcn_sched_barrier(0);
-        acc[0] = fr_add(acc[0], mont_mul(wa0, fr_add(s0, beta)));
-        __builtin_amdgcn_sched_barrier(0);
-        acc[1] = fr_add(acc[1], mont_mul(fr_add(wa0, wda), fr_add(s1, beta)));
-        __builtin_amdgcn_sched_barrier(0);
-        acc[2] = fr_add(acc[2], mont_mul(wda, fr_sub(s1, s0)));
-        acc[3] = fr_add(acc[3], a0);
-        acc[4] = fr_add(acc[4], a1);
+        SB();
+        acc.add(0, mont_mul_ol(wa0, fr_add(s0, beta)));
+        SB();
+        acc.add(1, mont_mul_ol(fr_add(wa0, wda), fr_add(s1, beta)));
+        SB();
+        acc.add(2, mont_mul_ol(wda, fr_sub(s1, s0)));
+        SB();
     }
-    reduce_publish<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    fr_t r[5];
+    acc.get(r);
+    reduce_publish<5>(r, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 template <int fold>
 __global__ __launch_bounds__(NT) void k_lu_phase2_btm(TabDev B, TabDev T, TabDev m, uint32_t n, fr_t vm,
                                                       fr_t beta, EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
-    fr_t acc[6];
-#pragma unroll
-    for (int k = 0; k < 6; k++) acc[k] = fr_zero();
+    __shared__ uint4 accl[6 * NT], acch[6 * NT];
+    LdsAcc<6> acc{accl, acch};
+    acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
-        fr_t b0, b1, t0, t1;
+        fr_t b0, b1;
         load_pair(B, i, h, n, fold, vm, b0, b1);
-        load_pair(T, i, h, n, fold, vm, t0, t1);
-        const fr_t db = fr_sub(b1, b0);
+        SB();
+        {
+            fr_t m0, m1;
+            load_pair(m, i, h, n, fold, vm, m0, m1);
+            SB();
+            acc.add(3, mont_mul_ol(m0, b0));
+            SB();
+            acc.add(4, mont_mul_ol(m1, b1));
+            SB();
+            acc.add(5, mont_mul_ol(fr_sub(m1, m0), fr_sub(b1, b0)));
+        }
+        SB();
+        fr_t wb0, wdb;
         {
             const fr_t w = eq_w(eq, i);
-            const fr_t wb0 = mont_mul(w, b0);
-            const fr_t wdb = mont_mul(w, db);
-            acc[0] = fr_add(acc[0], mont_mul(wb0, fr_add(t0, beta)));
-            acc[1] = fr_add(acc[1], mont_mul(fr_add(wb0, wdb), fr_add(t1, beta)));
-            acc[2] = fr_add(acc[2], mont_mul(wdb, fr_sub(t1, t0)));
+            SB();
+            wb0 = mont_mul_ol(w, b0);
+            SB();
+            wdb = mont_mul_ol(w, fr_sub(b1, b0));
         }
-        fr_t m0, m1;
-        load_pair(m, i, h, n, fold, vm, m0, m1);
-        acc[3] = fr_add(acc[3], mont_mul(m0, b0));
-        acc[4] = fr_add(acc[4], mont_mul(m1, b1));
-        acc[5] = fr_add(acc[5], mont_mul(fr_sub(m1, m0), db));
+        SB();
+        fr_t t0, t1;
+        load_pair(T, i, h, n, fold, vm, t0, t1);
+        SB();
+        acc.add(0, mont_mul_ol(wb0, fr_add(t0, beta)));
+        SB();
+        acc.add(1, mont_mul_ol(fr_add(wb0, wdb), fr_add(t1, beta)));
+        SB();
+        acc.add(2, mont_mul_ol(wdb, fr_sub(t1, t0)));
+        SB();
     }
-    reduce_publish<6>(acc, pub, 1, 0, gridDim.x, blockIdx.x);
+    fr_t r[6];
+    acc.get(r);
+    reduce_publish<6>(r, pub, 1, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
@@ -899,25 +965,41 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
 __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, uint32_t n, int fold,
                                                  fr_t vm, Publish pub) {
     const uint32_t h = n >> 1;
-    fr_t acc[4] = {fr_zero(), fr_zero(), fr_zero(), fr_zero()};
+    __shared__ uint4 accl[4 * NT], acch[4 * NT];
+    LdsAcc<4> acc{accl, acch};
+    acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
-        fr_t e0, e1, s0, s1, u0, u1;
+        fr_t e0, e1, s0, s1;
         load_pair(E, i, h, n, fold, vm, e0, e1);
+        SB();
         load_pair(S, i, h, n, fold, vm, s0, s1);
-        load_pair(U, i, h, n, fold, vm, u0, u1);
-        const fr_t de = fr_sub(e1, e0), ds = fr_sub(s1, s0), du = fr_sub(u1, u0);
-        fr_t e = e0, s_ = s0, u = u0;
+        SB();
+        const fr_t de = fr_sub(e1, e0), ds = fr_sub(s1, s0);
+        // es_t = E_t * S_t (x 2^-256) for t = 0..3
+        fr_t es[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            acc[t] = fr_add(acc[t], mont_mul(mont_mul(e, s_), u));
+            es[t] = mont_mul_ol(e0, s0);
+            SB();
             if (t < 3) {
-                e = fr_add(e, de);
-                s_ = fr_add(s_, ds);
-                u = fr_add(u, du);
+                e0 = fr_add(e0, de);
+                s0 = fr_add(s0, ds);
             }
         }
+        fr_t u0, u1;
+        load_pair(U, i, h, n, fold, vm, u0, u1);
+        SB();
+        const fr_t du = fr_sub(u1, u0);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            acc.add(t, mont_mul_ol(es[t], u0));
+            SB();
+            if (t < 3) u0 = fr_add(u0, du);
+        }
     }
-    reduce_publish<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    fr_t r[4];
+    acc.get(r);
+    reduce_publish<4>(r, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fold,
                          const uint32_t* v_m_host, Publish partial) {
@@ -927,31 +1009,54 @@ uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fol
     return g;
 }
 // eq-specialised: sums_t = sum_i eq(i, u[0..K)) S_t[i] U_t[i]  (x 2^-256)
+// Montgomery products issue in independent pairs between scheduling barriers: two
+// chains per wave at <= 128 registers (four waves per SIMD) keep the VALU busy.
 __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
                                                     EqDev eq, Publish pub) {
     const uint32_t h = n >> 1;
-    fr_t acc[4] = {fr_zero(), fr_zero(), fr_zero(), fr_zero()};
+    __shared__ uint4 accl[4 * NT], acch[4 * NT];
+    LdsAcc<4> acc{accl, acch};
+    acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
-        {
-            fr_t s0, s1, u0, u1;
-            load_pair(S, i, h, n, fold, vm, s0, s1);
-            load_pair(U, i, h, n, fold, vm, u0, u1);
-            const fr_t w = eq_w(eq, i);
-            const fr_t ws0 = mont_mul(w, s0);
-            const fr_t wds = mont_mul(w, fr_sub(s1, s0));
-            const fr_t du = fr_sub(u1, u0);
-            fr_t ws = ws0, u = u0;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                acc[t] = fr_add(acc[t], mont_mul(ws, u));
-                if (t < 3) {
-                    ws = fr_add(ws, wds);
-                    u = fr_add(u, du);
-                }
-            }
+        fr_t s0, s1, u0, u1, w;
+        if (fold) {
+            s0 = fold_at(S.slo, S.shi, i, n, vm);
+            s1 = fold_at(S.slo, S.shi, i + h, n, vm);
+            st_fr(S.dlo, S.dhi, i, s0);
+            st_fr(S.dlo, S.dhi, i + h, s1);
+            SB();
+            u0 = fold_at(U.slo, U.shi, i, n, vm);
+            w = eq_w(eq, i);
+            st_fr(U.dlo, U.dhi, i, u0);
+            SB();
+            u1 = fold_at(U.slo, U.shi, i + h, n, vm);
+        } else {
+            s0 = ld_fr(S.slo, S.shi, i);
+            s1 = ld_fr(S.slo, S.shi, i + h);
+            u0 = ld_fr(U.slo, U.shi, i);
+            w = eq_w(eq, i);
+            SB();
+            u1 = ld_fr(U.slo, U.shi, i + h);
         }
+        fr_t ws = mont_mul_ol(w, s0);
+        if (fold) st_fr(U.dlo, U.dhi, i + h, u1);
+        SB();
+        const fr_t wds = mont_mul_ol(w, fr_sub(s1, s0));
+        acc.add(0, mont_mul_ol(ws, u0));
+        SB();
+        const fr_t du = fr_sub(u1, u0);
+        ws = fr_add(ws, wds);
+        u0 = fr_add(u0, du);
+        const fr_t ws2 = fr_add(ws, wds), u2 = fr_add(u0, du);
+        acc.add(1, mont_mul_ol(ws, u0));
+        acc.add(2, mont_mul_ol(ws2, u2));
+        SB();
+        acc.add(3, mont_mul_ol(fr_add(ws2, wds), fr_add(u2, du)));
+        SB();
     }
-    reduce_publish<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    fr_t r[4];
+    acc.get(r);
+    reduce_publish<4>(r, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, EqW eq, Publish partial) {
@@ -969,8 +1074,8 @@ __global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* sh
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
         {
             const fr_t w = eq_w(eq, i);
-            fr_t ws = mont_mul(w, ld_fr(slo, shi, i));
-            if (has_u) ws = mont_mul(ws, ld_fr(ulo, uhi, i));
+            fr_t ws = mont_mul_ol(w, ld_fr(slo, shi, i));
+            if (has_u) ws = mont_mul_ol(ws, ld_fr(ulo, uhi, i));
             acc[0] = fr_add(acc[0], ws);
         }
     }
