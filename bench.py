@@ -18,10 +18,11 @@ TinyLlama-1.1B".
   in setup), process init.
 - Inputs are seeded synthetic tensors (fp8-e4m3 weights as scaled ints, Gaussian int16
   activations), resident in HBM before the timed region.
-- roofline: the dominant kernel's algorithmic bytes over its HIP-event-timed duration
-  (events on the stream it runs on, via the library's zkh_prof_* hooks) during the timed
-  steps; cpu_baseline: the C oracle (scalar port of the reference schedule) on the Q, K,
-  V and O matmuls, one thread.
+- roofline: the dominant kernel's algorithmic bytes over its duration during the timed
+  steps, from HIP events that the launch itself stamps at its start and end
+  (hipExtLaunchKernel on the library's stream, read through the zkh_prof_* hooks), so the
+  figure is the kernel's execution time as a kernel trace reports it; cpu_baseline: the C
+  oracle (scalar port of the reference schedule) on the Q, K, V and O matmuls, one thread.
 """
 import argparse
 import concurrent.futures

@@ -1151,8 +1151,9 @@ void launch_eq_outer(hipStream_t s, const uint32_t* tlo_m, const uint32_t* thi_p
                      uint32_t n, DevPlanes out) {
     k_eq_outer<<<grid_for(n, NT, 8192), NT, 0, s>>>(tlo_m, thi_p, klo, n, PL_LO(out), PL_HI(out));
 }
-void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, uint32_t nblocks) {
-    k_eq_mont_multi<<<nblocks, NT, 0, s>>>(d_dev, nd);
+void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, uint32_t nblocks, hipEvent_t t0,
+                          hipEvent_t t1) {
+    hipExtLaunchKernelGGL(k_eq_mont_multi, dim3(nblocks), dim3(NT), 0, s, t0, t1, 0, d_dev, nd);
 }
 
 // ------------------------------------------------------------------------------------
@@ -1287,9 +1288,12 @@ __global__ __launch_bounds__(NT) void k_eqdot_multi(const EqDotDesc* __restrict_
     if (q.variant) eqdot_body<V1>(q, local);
     else eqdot_body<V0>(q, local);
 }
-void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_t nd, uint32_t nblocks) {
-    if (!wide) k_eqdot_multi<EqdotI32x1, EqdotI64x2><<<nblocks, NT, 0, s>>>(d_dev, nd);
-    else k_eqdot_multi<EqdotI32x2, EqdotI64x3><<<nblocks, NT, 0, s>>>(d_dev, nd);
+void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_t nd, uint32_t nblocks,
+                        hipEvent_t t0, hipEvent_t t1) {
+    if (!wide)
+        hipExtLaunchKernelGGL(k_eqdot_multi<EqdotI32x1, EqdotI64x2>, dim3(nblocks), dim3(NT), 0, s, t0, t1, 0, d_dev, nd);
+    else
+        hipExtLaunchKernelGGL(k_eqdot_multi<EqdotI32x2, EqdotI64x3>, dim3(nblocks), dim3(NT), 0, s, t0, t1, 0, d_dev, nd);
 }
 
 // out[i] = sum_c partial[c*N+i] - corr (i < N; zero up to Npad), or, when E is set, the
@@ -1328,8 +1332,9 @@ __global__ __launch_bounds__(NT) void k_sum_chunks_multi(const SumChunksDesc* __
         st_fr(reinterpret_cast<uint4*>(q.out_lo), reinterpret_cast<uint4*>(q.out_hi), i, s);
     }
 }
-void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks) {
-    k_sum_chunks_multi<<<nblocks, NT, 0, s>>>(d_dev, nd);
+void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks,
+                             hipEvent_t t0, hipEvent_t t1) {
+    hipExtLaunchKernelGGL(k_sum_chunks_multi, dim3(nblocks), dim3(NT), 0, s, t0, t1, 0, d_dev, nd);
 }
 
 // zkip rounds of several jobs in one launch: one pair per thread; fold of the previous

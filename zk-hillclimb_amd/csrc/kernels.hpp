@@ -5,6 +5,7 @@
 // entries); small vectors (eq factor tables, partial sums) use the reference's AoS Fr_t
 // layout (8 consecutive uint32 per element).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -197,12 +198,16 @@ struct ZkipDesc {
     uint32_t n, fold, blk_begin, pad_;
     fr_arg vm;  // challenge of the fold, Montgomery form
 };
-void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, uint32_t nblocks);
+// t0 / t1: optional events stamped at the start / end of the launch (hipExtLaunchKernel)
+void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, uint32_t nblocks,
+                          hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 // eq-weighted integer reductions; wide = 0: int32 with |v| < 2^19 (one 20-bit piece, chunks
 // <= 2048 rows) and int64 with |v| < 2^43 (two 22-bit pieces); wide = 1: any int32 (two
 // 22-bit pieces) and any int64 (three); chunks <= 512 rows for 22-bit pieces
-void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_t nd, uint32_t nblocks);
-void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks);
+void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_t nd, uint32_t nblocks,
+                        hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
+void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks,
+                             hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 #define ZKH_MAX_BATCH 32
 struct ZkipBatch {  // passed by value as the kernel argument (<= 2.1 KB)
     ZkipDesc d[ZKH_MAX_BATCH];

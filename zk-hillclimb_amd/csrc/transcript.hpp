@@ -90,13 +90,17 @@ struct Sha256 {
         }
     }
     void final(uint8_t out[32]) {
-        uint64_t bits = len * 8;
-        uint8_t pad = 0x80, z = 0;
-        update(&pad, 1);
-        while (blen != 56) update(&z, 1);
-        uint8_t lb[8];
-        for (int i = 0; i < 8; i++) lb[i] = (uint8_t)(bits >> (56 - 8 * i));
-        update(lb, 8);
+        const uint64_t bits = len * 8;
+        buf[blen++] = 0x80;
+        if (blen > 56) {  // no room for the length: pad out this block
+            memset(buf + blen, 0, 64 - blen);
+            compress(buf);
+            blen = 0;
+        }
+        memset(buf + blen, 0, 56 - blen);
+        for (int i = 0; i < 8; i++) buf[56 + i] = (uint8_t)(bits >> (56 - 8 * i));
+        compress(buf);
+        blen = 0;
         for (int i = 0; i < 8; i++) {
             out[4 * i] = (uint8_t)(h[i] >> 24);
             out[4 * i + 1] = (uint8_t)(h[i] >> 16);
@@ -170,6 +174,28 @@ inline void Sha256::compress(const uint8_t* p) {
 inline void Sha256::compress(const uint8_t* p) { block(p); }
 #endif
 
+// SHA-256 of a message of at most 119 bytes: the padded message is built in place and
+// compressed as one or two blocks
+inline void sha256_short(const uint8_t* msg, size_t n, uint8_t out[32]) {
+    uint8_t b[128];
+    memcpy(b, msg, n);
+    b[n] = 0x80;
+    const size_t nb = n + 9 <= 64 ? 64 : 128;
+    memset(b + n + 1, 0, nb - n - 1);
+    const uint64_t bits = (uint64_t)n * 8;
+    for (int i = 0; i < 8; i++) b[nb - 8 + i] = (uint8_t)(bits >> (56 - 8 * i));
+    Sha256 c;
+    c.init();
+    c.compress(b);
+    if (nb == 128) c.compress(b + 64);
+    for (int i = 0; i < 8; i++) {
+        out[4 * i] = (uint8_t)(c.h[i] >> 24);
+        out[4 * i + 1] = (uint8_t)(c.h[i] >> 16);
+        out[4 * i + 2] = (uint8_t)(c.h[i] >> 8);
+        out[4 * i + 3] = (uint8_t)c.h[i];
+    }
+}
+
 inline void tr_init(uint8_t st[32], const char* seed, size_t n) {
     Sha256 c;
     c.init();
@@ -178,6 +204,20 @@ inline void tr_init(uint8_t st[32], const char* seed, size_t n) {
 }
 inline void tr_absorb(uint8_t st[32], const char* label, size_t llen, const void* data,
                       size_t len) {
+    if (32 + 4 + llen + 8 + len <= 119) {  // the per-round absorbs: one short message
+        uint8_t m[119];
+        size_t o = 0;
+        memcpy(m, st, 32);
+        o = 32;
+        for (int i = 0; i < 4; i++) m[o++] = (uint8_t)((uint32_t)llen >> (8 * i));
+        memcpy(m + o, label, llen);
+        o += llen;
+        for (int i = 0; i < 8; i++) m[o++] = (uint8_t)((uint64_t)len >> (8 * i));
+        memcpy(m + o, data, len);
+        o += len;
+        sha256_short(m, o, st);
+        return;
+    }
     Sha256 c;
     c.init();
     c.update(st, 32);
@@ -191,17 +231,12 @@ inline void tr_absorb(uint8_t st[32], const char* label, size_t llen, const void
     c.final(st);
 }
 inline void tr_challenge_bytes(uint8_t st[32], uint8_t out[32]) {
-    Sha256 c;
-    c.init();
-    c.update(st, 32);
-    c.update("chal", 4);
-    c.final(out);
-    uint8_t nx[32];
-    c.init();
-    c.update(st, 32);
-    c.update("rtch", 4);
-    c.final(nx);
-    memcpy(st, nx, 32);
+    uint8_t m[36];
+    memcpy(m, st, 32);
+    memcpy(m + 32, "chal", 4);
+    sha256_short(m, 36, out);
+    memcpy(m + 32, "rtch", 4);
+    sha256_short(m, 36, st);
 }
 inline void tr_challenge_limbs(uint8_t st[32], uint32_t out[8]) {
     for (;;) {

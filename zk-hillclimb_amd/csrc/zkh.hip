@@ -206,13 +206,20 @@ struct zkh_ctx {
     std::vector<hipEvent_t> pool;
 };
 
-// Times the launches issued during its lifetime under `name` when profiling is on.
+// Times the launches issued during its lifetime under `name` when profiling is on.  With
+// kernel_events the scope records no markers of its own: the caller hands start() to the
+// first launch and stop() to the last (hipExtLaunchKernel stamps them at the dispatch's own
+// start and end), so the time is the kernels' execution without marker-packet overhead.
 struct ProfScope {
     zkh_ctx* c;
     int rec = -1;
     hipEvent_t a = nullptr, b = nullptr;
     double bytes;
-    ProfScope(zkh_ctx* c_, const char* name, double bytes_) : c(c_), bytes(bytes_) {
+    bool kev;
+    hipEvent_t start() const { return rec >= 0 && a && b ? a : nullptr; }
+    hipEvent_t stop() const { return rec >= 0 && a && b ? b : nullptr; }
+    ProfScope(zkh_ctx* c_, const char* name, double bytes_, bool kernel_events = false)
+        : c(c_), bytes(bytes_), kev(kernel_events) {
         if (!c->prof) return;
         for (size_t i = 0; i < c->recs.size(); i++)
             if (c->recs[i].name == name) rec = (int)i;
@@ -228,11 +235,11 @@ struct ProfScope {
                 *e = nullptr;
             }
         }
-        if (a) (void)hipEventRecord(a, c->stream);
+        if (a && !kev) (void)hipEventRecord(a, c->stream);
     }
     ~ProfScope() {
         if (rec < 0 || !a || !b) return;
-        (void)hipEventRecord(b, c->stream);
+        if (!kev) (void)hipEventRecord(b, c->stream);
         c->pending.push_back(zkh_ctx::Pending{rec, a, b, bytes});
     }
 };
@@ -1400,22 +1407,26 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     if ((rc = upload(c, desc_d, blob.data(), o_zk))) return rc;
     stamp("descriptors uploaded");
     {
-        ProfScope ps(c, "eq_tables", (double)eq_total * 32);
-        launch_eq_mont_multi(c->stream, (const EqTabDesc*)(desc_d + o_eq), (uint32_t)eqd.size(), eq_blocks);
+        ProfScope ps(c, "eq_tables", (double)eq_total * 32, true);
+        launch_eq_mont_multi(c->stream, (const EqTabDesc*)(desc_d + o_eq), (uint32_t)eqd.size(), eq_blocks,
+                             ps.start(), ps.stop());
     }
     double red_bytes = 0;  // algorithmic: every stored integer of X, W and Y read once
     for (auto& r : reds) red_bytes += (double)r.d.K * r.d.N * (r.is64 ? 8 : 4);
     {
-        ProfScope ps(c, "eqdot", red_bytes);
-        for (auto& g : groups)
-            launch_eqdot_multi(c->stream, g.wide, (const EqDotDesc*)(desc_d + o_dot) + g.first, g.count, g.blocks);
+        ProfScope ps(c, "eqdot", red_bytes, true);
+        for (size_t gi = 0; gi < groups.size(); gi++) {
+            const Grp& g = groups[gi];
+            launch_eqdot_multi(c->stream, g.wide, (const EqDotDesc*)(desc_d + o_dot) + g.first, g.count, g.blocks,
+                               gi == 0 ? ps.start() : nullptr, gi + 1 == groups.size() ? ps.stop() : nullptr);
+        }
     }
     {
         double b = 0;
         for (auto& r : reds) b += (double)r.nch * r.d.N * 32 + (double)r.Npad * 32;
-        ProfScope ps(c, "sum_chunks", b);
+        ProfScope ps(c, "sum_chunks", b, true);
         launch_sum_chunks_multi(c->stream, (const SumChunksDesc*)(desc_d + o_sum), (uint32_t)sums.size(),
-                                sum_blocks);
+                                sum_blocks, ps.start(), ps.stop());
     }
     for (auto& q : J) q.xs.resize(q.L);
     // claim = <Y(u_batch, .), eq(u_output, .)> from the pinned block partials
@@ -1624,6 +1635,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                         fr_store(J[j].xm, xm);
                         rnd[a]++;
                         send_cmd(j, rnd[a], xm);
+                        if (tracing) tr_host[j].push_back(now_us());
                         continue;
                     }
                     // the blocks' folded entries: the remaining lgnb rounds on the host
@@ -1697,12 +1709,16 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         if (tracing) {
             fprintf(stderr, "[zkh] mm persistent rounds: %.1f us (%d host threads)\n", now_us() - t_start, T);
             const double tick_us = 1000.0 / (double)c->clock_khz;
-            for (uint32_t j = 0; j < nj; j++) {  // per round: block compute, then publish -> next challenge
+            // per round: block compute (device clock: challenge received -> sums published),
+            // host work (sums seen -> challenge sent) and the round trip the host observes
+            // (challenge sent -> next sums seen)
+            for (uint32_t j = 0; j < nj; j++) {
                 const auto& g = tr_gpu[j];
-                fprintf(stderr, "[zkh]   job %u (n=%u, %u blocks): gpu round us", j, J[j].INp, 1u << lgnb[j]);
-                for (size_t r = 1; r + 1 < g.size() / 2 + 1 && 2 * r + 1 < g.size(); r++)
-                    fprintf(stderr, " %.1f/%.1f", (g[2 * r] - g[2 * r + 1]) * tick_us,
-                            (g[2 * r + 1] - g[2 * r - 2]) * tick_us);
+                const auto& h = tr_host[j];
+                fprintf(stderr, "[zkh]   job %u (n=%u, %u blocks): gpu/host/trip us", j, J[j].INp, 1u << lgnb[j]);
+                for (size_t r = 1; 2 * r + 1 < g.size() && 2 * r < h.size(); r++)
+                    fprintf(stderr, " %.1f/%.1f/%.1f", (double)(g[2 * r] - g[2 * r + 1]) * tick_us,
+                            h[2 * r - 1] - h[2 * r - 2], h[2 * r] - h[2 * r - 1]);
                 fprintf(stderr, "\n");
             }
         }
