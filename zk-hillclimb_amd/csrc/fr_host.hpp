@@ -95,6 +95,10 @@ inline Fr fr_mont_mul(const Fr& a, const Fr& b) {
     return r;
 }
 inline Fr fr_to_mont(const Fr& a) { return fr_mont_mul(a, kR2); }
+inline const Fr& fr_one_m() {  // 1 in Montgomery form (2^256 mod r)
+    static const Fr v = fr_to_mont(kOne);
+    return v;
+}
 inline Fr fr_from_mont(const Fr& a) { return fr_mont_mul(a, kOne); }
 inline Fr fr_mul(const Fr& a, const Fr& b) { return fr_mont_mul(fr_to_mont(a), b); }
 // a^e for a plain a and a 256-bit exponent

@@ -1407,14 +1407,15 @@ ZDEV void st_quad_sys(uint32_t* p, uint4 v) {
     const zkh_v4u x = {v.x, v.y, v.z, v.w};
     asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" : : "v"((uint64_t)p), "v"(x) : "memory");
 }
-// wave 0: wait until the three command quads show want; lanes 0..2 then hold challenge
-// words 3*lane .. 3*lane+2 in (y, z, w).  False on ZKH_QUIT or when the deadline passes
+// wave 0: wait until the first nq (<= 11) command quads show want; lane i < nq then holds
+// command words 3i .. 3i+2 in (y, z, w).  False on ZKH_QUIT or when the deadline passes
 // (then *err is set).  Every lane of wave 0 calls it and gets the same result.
-ZDEV bool persist_wait(const uint32_t* cmd, uint32_t want, uint32_t* err, uint64_t deadline, uint4& quad) {
+ZDEV bool persist_wait(const uint32_t* cmd, uint32_t nq, uint32_t want, uint32_t* err, uint64_t deadline,
+                       uint4& quad) {
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t t0 = wall_clock64();
     for (;;) {
-        const uint4 qd = lane < 3 ? ld_quad_sys(cmd + 4 * lane) : make_uint4(want, 0, 0, 0);
+        const uint4 qd = lane < nq ? ld_quad_sys(cmd + 4 * lane) : make_uint4(want, 0, 0, 0);
         if (__ballot(qd.x == ZKH_QUIT)) return false;
         if (!__ballot(qd.x != want)) {
             quad = qd;
@@ -1436,25 +1437,58 @@ ZDEV void persist_publish(uint32_t* slot, const uint32_t* pub, uint32_t nw, uint
     }
 }
 #define NTP 1024  // threads of a persistent round block (16 waves)
-#define NPG 320   // threads per product group: waves 0-4, 5-9, 10-14 (wave 15 idle)
+static_assert(2 * ZKH_PLS_MAX <= NTP, "the double fold takes one product per thread");
 
-// block clock -> slot words 56..59 (publication time, receipt of the previous challenge)
-ZDEV void persist_stamp(uint32_t* slot, uint64_t t_cmd) {
+// block clock -> slot words 96..99 (publication time, receipt of the previous command),
+// and the low words of both per message s < 14 into words 100 + 2s (publication of message
+// s) and 101 + 2(s - 1) (receipt of command s - 1); the host reads the per-message words
+// after the kernel has ended
+ZDEV void persist_stamp(uint32_t* slot, uint32_t s, uint64_t t_cmd) {
     const uint64_t now = wall_clock64();
-    slot[56] = (uint32_t)now;
-    slot[57] = (uint32_t)(now >> 32);
-    slot[58] = (uint32_t)t_cmd;
-    slot[59] = (uint32_t)(t_cmd >> 32);
+    slot[96] = (uint32_t)now;
+    slot[97] = (uint32_t)(now >> 32);
+    slot[98] = (uint32_t)t_cmd;
+    slot[99] = (uint32_t)(t_cmd >> 32);
+    if (s < 14) slot[100 + 2 * s] = (uint32_t)now;
+    if (s >= 1 && s <= 14) slot[101 + 2 * (s - 1)] = (uint32_t)t_cmd;
 }
-// Round loop of one block over its LDS slice (see ZkipPersist).  Per round, each group of
-// five waves accumulates one product over the pairs (k, k + h): group 0 a0*b0, group 1
-// a1*b1, group 2 (a1-a0)*(b1-b0); the fold spreads one entry per thread.  With at most 512
-// entries per block, every thread does at most one dependent Montgomery multiplication per
-// phase from the first fold on.
+// operand sel of a table at position p of the halves (L = T[p], H = T[p + h], D = H - L)
+ZDEV fr_t half_opnd(const uint4* lo, const uint4* hi, uint32_t sel, uint32_t p, uint32_t h) {
+    if (sel == 0) return ld_fr(lo, hi, p);
+    if (sel == 1) return ld_fr(lo, hi, p + h);
+    return fr_sub(ld_fr(lo, hi, p + h), ld_fr(lo, hi, p));
+}
+// Two-round products by operand class, so that the lanes of a wave run the same code:
+// class X (types 0, 3, 1, 4): T[p]; class D (types 2, 5, 6, 7): T[p + d] - T[p]; class E
+// (type 8): (T[j'+h] - T[j']) - (T[j+h] - T[j]).  kPairType lists the types in wave order.
+__constant__ uint32_t kPairType[9] = {0, 3, 1, 4, 2, 5, 6, 7, 8};
+// offsets of type t's operand at quarter index j (j' = j + q4): p and, for class D, d
+ZDEV void pair_pos(uint32_t t, uint32_t j, uint32_t q4, uint32_t h, uint32_t& p, uint32_t& d) {
+    const uint32_t jq = j + q4;
+    switch (t) {
+        case 0: p = j; d = 0; break;
+        case 1: p = j + h; d = 0; break;
+        case 3: p = jq; d = 0; break;
+        case 4: p = jq + h; d = 0; break;
+        case 2: p = j; d = h; break;
+        case 5: p = jq; d = h; break;
+        case 6: p = j; d = q4; break;
+        default: p = j + h; d = q4; break;  // 7
+    }
+}
+ZDEV fr_t pair_opnd_e(const uint4* lo, const uint4* hi, uint32_t j, uint32_t q4, uint32_t h) {
+    return fr_sub(fr_sub(ld_fr(lo, hi, j + q4 + h), ld_fr(lo, hi, j + q4)),
+                  fr_sub(ld_fr(lo, hi, j + h), ld_fr(lo, hi, j)));
+}
+// Round loop of one block over its LDS slice (see ZkipPersist).  A two-round message: a
+// group of min(m/4, 64) lanes accumulates product type t over j < m/4; the double fold
+// computes the four products of an output entry on a quad of lanes and adds them with two
+// lane swaps.  A one-round message (m = 2): lanes 0..2 of wave 0 form a0b0, a1b1,
+// (a1-a0)(b1-b0).
 __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
     extern __shared__ uint4 zl[];  // a.lo | a.hi | b.lo | b.hi, ls entries each
-    __shared__ uint32_t sj, sok, pubw[24], sxw[9];
-    __shared__ fr_t red[15];
+    __shared__ uint32_t sj, sok, pubw[ZKH_MSG_PAIR], sxw[33];
+    __shared__ fr_t red[9];
     if (threadIdx.x == 0) {
         uint32_t j = 0;
         while (j + 1 < P.nd && P.d[j + 1].blk_begin <= blockIdx.x) j++;
@@ -1484,46 +1518,81 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
     __syncthreads();
     uint32_t* slot = q.out + (size_t)lb * ZKH_PSLOT;
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const uint32_t w = wv / 5, gt = threadIdx.x - w * NPG;  // product group, index in it
-    uint32_t m = ls, r = 0;
+    uint32_t m = ls;
     uint64_t t_cmd = 0;
-    for (; m > 1; r++) {
-        const uint32_t h = m >> 1;
-        // waves without pairs this round skip the products and the wave reduction
-        if (w < 3 && (wv - 5 * w) * 64 < h) {
-            fr_t acc = fr_zero();
-            for (uint32_t k = gt; k < h; k += NPG) {
-                fr_t x, y;
-                if (w == 0) {
-                    x = ld_fr(alo, ahi, k);
-                    y = ld_fr(blo, bhi, k);
-                } else if (w == 1) {
-                    x = ld_fr(alo, ahi, k + h);
-                    y = ld_fr(blo, bhi, k + h);
-                } else {
-                    x = fr_sub(ld_fr(alo, ahi, k + h), ld_fr(alo, ahi, k));
-                    y = fr_sub(ld_fr(blo, bhi, k + h), ld_fr(blo, bhi, k));
+    for (uint32_t seq = 1;; seq++) {
+        uint32_t nw;
+        if (m >= 4) {
+            const uint32_t q4 = m >> 2, h = m >> 1;
+            // S = min(q4, 64) lanes per type and k = min(4, 64 / S) types per wave, the
+            // waves of a class (X: 4 types, D: 4, E: 1) next to each other: 8/k + 1 waves
+            // (3 for q4 <= 16), each running one class's code, so a wave's SIMD does one
+            // multiply per lane per 64 / (k S) products (a wave's Montgomery products
+            // nearly fill its SIMD: fewer waves per SIMD finish sooner)
+            const uint32_t S = q4 < 64 ? q4 : 64;
+            const uint32_t k = S <= 16 ? 4 : 64 / S;
+            const uint32_t nwx = 4 / k;  // waves per class X and D
+            if (wv < 2 * nwx + 1) {
+                const uint32_t cls = wv < nwx ? 0 : wv < 2 * nwx ? 1 : 2;
+                const uint32_t slot = lane / S, sub = lane % S;
+                const bool live = cls < 2 ? slot < k : slot == 0;
+                const uint32_t t = cls == 2 ? 8 : kPairType[(wv - cls * nwx) * k + (live ? slot : 0) + 4 * cls];
+                fr_t acc = fr_zero();
+                if (live) {
+                    for (uint32_t j = sub; j < q4; j += S) {
+                        fr_t x, y;
+                        if (cls == 2) {
+                            x = pair_opnd_e(alo, ahi, j, q4, h);
+                            y = pair_opnd_e(blo, bhi, j, q4, h);
+                        } else {
+                            uint32_t pp, d;
+                            pair_pos(t, j, q4, h, pp, d);
+                            x = ld_fr(alo, ahi, pp + d);
+                            y = ld_fr(blo, bhi, pp + d);
+                            if (cls == 1) {
+                                x = fr_sub(x, ld_fr(alo, ahi, pp));
+                                y = fr_sub(y, ld_fr(blo, bhi, pp));
+                            }
+                        }
+                        acc = fr_add(acc, mont_mul_ol(x, y));
+                    }
                 }
-                acc = fr_add(acc, mont_mul(x, y));
+                for (uint32_t z = S >> 1; z >= 1; z >>= 1) acc = fr_add(acc, fr_shfl_xor(acc, z));
+                if (live && sub == 0) red[t] = acc;
             }
-            acc = fr_wave_sum(acc);
-            if (lane == 0) red[wv] = acc;
-        }
-        __syncthreads();
-        if (wv == 0) {
-            if (lane < 3) {  // lane g adds group g's active waves
-                const uint32_t na = min(5u, (h + 63) >> 6);
-                fr_t t = red[5 * lane];
-                for (uint32_t i = 1; i < na; i++) t = fr_add(t, red[5 * lane + i]);
+            __syncthreads();
+            nw = ZKH_MSG_PAIR;
+            if (wv == 0 && lane < 9) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) pubw[8 * lane + j] = t.v[j];
+                for (int i = 0; i < 8; i++) pubw[8 * lane + i] = red[lane].v[i];
             }
+        } else if (m == 2) {
+            nw = ZKH_MSG_ONE;
+            if (wv == 0 && lane < 3) {
+                const fr_t x = half_opnd(alo, ahi, lane, 0, 1), y = half_opnd(blo, bhi, lane, 0, 1);
+                const fr_t t = mont_mul_ol(x, y);
+#pragma unroll
+                for (int i = 0; i < 8; i++) pubw[8 * lane + i] = t.v[i];
+            }
+        } else {  // the block's folded entries a[0], b[0]
+            nw = ZKH_MSG_FINAL;
+            if (wv == 0 && lane < 2) {
+                const fr_t t = lane ? ld_fr(blo, bhi, 0) : ld_fr(alo, ahi, 0);
+#pragma unroll
+                for (int i = 0; i < 8; i++) pubw[8 * lane + i] = t.v[i];
+            }
+        }
+        if (wv == 0) {
             __builtin_amdgcn_wave_barrier();
-            if (lane == 0) persist_stamp(slot, t_cmd);
-            persist_publish(slot, pubw, 24, r + 1);
+            if (lane == 0) persist_stamp(slot, seq, t_cmd);
+            persist_publish(slot, pubw, nw, seq);
+        }
+        if (m == 1) return;
+        if (wv == 0) {
             uint4 qd;
-            const bool ok = persist_wait(q.cmd, r + 1, P.err, P.deadline, qd);
-            if (lane < 3) {
+            const uint32_t nq = zkh_quad_count(m >= 4 ? 32 : 8);
+            const bool ok = persist_wait(q.cmd, nq, seq, P.err, P.deadline, qd);
+            if (lane < nq) {
                 sxw[3 * lane] = qd.y;
                 sxw[3 * lane + 1] = qd.z;
                 sxw[3 * lane + 2] = qd.w;
@@ -1533,29 +1602,37 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
         }
         __syncthreads();
         if (!sok) return;
-        fr_t x;
+        if (m >= 4) {  // double fold: m -> m/4; the four products of an output on four lanes
+            const uint32_t q4 = m >> 2, h = m >> 1;
+            const uint32_t t = threadIdx.x;  // 8*q4 <= 8*ZKH_PLS_MAX/4 = NTP products, one per thread
+            if (t < 8 * q4) {                // whole lane quads (8*q4 is a multiple of 8)
+                const uint32_t o = t >> 2, term = t & 3;  // output o (a for o < q4, b after), term
+                const bool tb = o >= q4;
+                const uint32_t k = tb ? o - q4 : o;
+                uint4* lo = tb ? blo : alo;
+                uint4* hi = tb ? bhi : ahi;
+                fr_t w;
 #pragma unroll
-        for (int j = 0; j < 8; j++) x.v[j] = sxw[j];
-        for (uint32_t t = threadIdx.x; t < 2 * h; t += NTP) {  // a for t < h, b for t >= h
-            const bool tb = t >= h;
-            const uint32_t k = tb ? t - h : t;
-            uint4* lo = tb ? blo : alo;
-            uint4* hi = tb ? bhi : ahi;
-            const fr_t v0 = ld_fr(lo, hi, k), v1 = ld_fr(lo, hi, k + h);
-            st_fr(lo, hi, k, fr_add(v0, mont_mul(x, fr_sub(v1, v0))));
+                for (int i = 0; i < 8; i++) w.v[i] = sxw[8 * term + i];
+                fr_t r = mont_mul_ol(w, ld_fr(lo, hi, k + (term & 1 ? h : 0) + (term & 2 ? q4 : 0)));
+                r = fr_add(r, fr_shfl_xor(r, 1));
+                r = fr_add(r, fr_shfl_xor(r, 2));
+                if (term == 0) st_fr(lo, hi, k, r);  // T[k] is read only by this quad
+            }
+            m = q4;
+        } else {  // m == 2: T[0] <- T[0] + x (T[1] - T[0])
+            fr_t x;
+#pragma unroll
+            for (int i = 0; i < 8; i++) x.v[i] = sxw[i];
+            if (threadIdx.x < 2) {
+                uint4* lo = threadIdx.x ? blo : alo;
+                uint4* hi = threadIdx.x ? bhi : ahi;
+                const fr_t v0 = ld_fr(lo, hi, 0), v1 = ld_fr(lo, hi, 1);
+                st_fr(lo, hi, 0, fr_add(v0, mont_mul(x, fr_sub(v1, v0))));
+            }
+            m = 1;
         }
         __syncthreads();
-        m = h;
-    }
-    if (wv == 0) {  // the block's folded entries a[0], b[0]
-        if (lane < 2) {
-            const fr_t t = lane ? ld_fr(blo, bhi, 0) : ld_fr(alo, ahi, 0);
-#pragma unroll
-            for (int j = 0; j < 8; j++) pubw[8 * lane + j] = t.v[j];
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (lane == 0) persist_stamp(slot, t_cmd);
-        persist_publish(slot, pubw, 16, r + 1);
     }
 }
 // An ordinary launch on the stream: the blocks never wait for each other, only for the

@@ -221,19 +221,31 @@ void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
 // (block l holds entries l + nb*k in LDS), so the pairs (i, i + m/2) of every round with
 // m >= 2*nb stay inside one block.  Messages between host and device are 16-byte quads
 // [seq, w, w, w] (zkh_quad_* below), each written with one 16-byte store: a message is
-// complete when all its quads show the expected seq.  Round r: every block publishes its
-// sums (sum a0b0, sum a1b1, sum da*db, each x 2^-256: 24 words, 8 quads) with seq r + 1;
-// it then waits for the job's command (3 quads, seq r + 1) carrying the challenge
-// (Montgomery form, 8 words) and folds.  After the last local round each block publishes
-// its single folded entries of a and b (16 words, 6 quads) with seq rounds + 1 and exits.
-// A command quad with seq ZKH_QUIT makes the job's blocks exit; a block that waits longer
-// than `deadline` ticks of the 100 MHz clock sets *err and exits.  Slot words 56..59 hold
-// the block's clock stamps (tracing only).
+// complete when all its quads show the expected seq.  A block with m >= 4 local entries
+// serves two rounds per message: over the halves L = T[0, m/2), H = T[m/2, m), D = H - L
+// and the quarter index j < m/4 (j' = j + m/4) it publishes nine sums (each x 2^-256,
+// ZKH_MSG_PAIR words): L_j.L_j, H_j.H_j, D_j.D_j, the same three at j', and
+// (L_j' - L_j).(L_j' - L_j), (H_j' - H_j).(H_j' - H_j), (D_j' - D_j).(D_j' - D_j), where
+// u.v means u_a * u_b over the two tables.  They give this round's sums and, as quadratics
+// in its challenge x, the next round's sums over the table folded by x; the host derives
+// both challenges and answers with the four weights (1-x)(1-y), x(1-y), (1-x)y, xy
+// (Montgomery form, 32 words) of the double fold T[k] <- w00 T[k] + w01 T[k + m/2] +
+// w10 T[k + m/4] + w11 T[k + 3m/4].  With m = 2 the block publishes one round's sums
+// (a0b0, a1b1, da*db: ZKH_MSG_ONE words) and receives the challenge (8 words); with m = 1
+// its folded entries a[0], b[0] (ZKH_MSG_FINAL words), then exits.  Message s carries seq
+// s (1, 2, ...) both ways.  A command quad with seq ZKH_QUIT makes the job's blocks exit;
+// a block that waits longer than `deadline` ticks of the 100 MHz clock sets *err and
+// exits.  Slot words 96..99 hold the block's clock at its last message (publication, and
+// receipt of the previous command) and words 100 + 2s, 101 + 2s (s < 14) the same per
+// message s (tracing only).
 #define ZKH_QUIT 0xffffffffu
-#define ZKH_PSLOT 64  // words per block slot and per job command area
+#define ZKH_PSLOT 128  // words per block slot and per job command area
+#define ZKH_MSG_PAIR 72
+#define ZKH_MSG_ONE 24
+#define ZKH_MSG_FINAL 16
 // quad messages: data word i lives at 4*(i/3) + 1 + i%3, quad q's seq at 4*q
-inline uint32_t zkh_quad_word(uint32_t i) { return 4 * (i / 3) + 1 + i % 3; }
-inline uint32_t zkh_quad_count(uint32_t nwords) { return (nwords + 2) / 3; }
+__host__ __device__ inline uint32_t zkh_quad_word(uint32_t i) { return 4 * (i / 3) + 1 + i % 3; }
+__host__ __device__ inline uint32_t zkh_quad_count(uint32_t nwords) { return (nwords + 2) / 3; }
 #define ZKH_PLS_MAX 512u  // entries per block and table (32 KiB of LDS for both tables)
 struct ZkipPJob {
     const uint32_t* a_lo;

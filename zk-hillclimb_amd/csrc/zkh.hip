@@ -1523,8 +1523,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         uint32_t* ps = c->ps_host;
         for (uint32_t j = 0; j < nj; j++) {
             const uint32_t nb = 1u << lgnb[j];
-            for (uint32_t b = 0; b < nb; b++) memset(ps + slot_off[j] + b * ZKH_PSLOT, 0, 32 * 4);
-            memset(ps + cmd_off[j], 0, 12 * 4);
+            for (uint32_t b = 0; b < nb; b++) memset(ps + slot_off[j] + b * ZKH_PSLOT, 0, ZKH_PSLOT * 4);
+            memset(ps + cmd_off[j], 0, ZKH_PSLOT * 4);
         }
         ps[0] = 0;
         const uint64_t deadline_ticks = c->clock_khz * 1000 * 20;  // 20 s without a command
@@ -1545,15 +1545,17 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             P.deadline = deadline_ticks;
             P.ls_max = std::max(P.ls_max, J[j].INp >> lgnb[j]);
         }
-        // a job's command: the challenge (Montgomery form) in three quads, seqs written last
-        auto send_cmd = [&](uint32_t j, uint32_t seq, const uint32_t* xm) {
+        // a job's command: nw data words (the challenge or the four fold weights, Montgomery
+        // form), then the seqs of its quads; without data, seq (ZKH_QUIT) goes to every quad
+        // a block may poll
+        auto send_cmd = [&](uint32_t j, uint32_t seq, const uint32_t* w, uint32_t nw) {
             uint32_t* cmd = ps + cmd_off[j];
-            if (xm)
-                for (uint32_t i = 0; i < 8; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
-            for (uint32_t qd = 0; qd < 3; qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
+            for (uint32_t i = 0; i < nw; i++) __atomic_store_n(cmd + zkh_quad_word(i), w[i], __ATOMIC_RELAXED);
+            const uint32_t nq = zkh_quad_count(w ? nw : 32);
+            for (uint32_t qd = 0; qd < nq; qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
         };
         auto quit_all = [&]() {
-            for (uint32_t j = 0; j < nj; j++) send_cmd(j, ZKH_QUIT, nullptr);
+            for (uint32_t j = 0; j < nj; j++) send_cmd(j, ZKH_QUIT, nullptr, 0);
             (void)hipStreamSynchronize(c->stream);
         };
         double pbytes = 0;
@@ -1576,11 +1578,16 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         std::atomic<int> abort_why{0};  // 1 device error, 2 kernel ended early, 3 no progress
         std::atomic<int> dev_err{0};
         const double t_start = now_us();
-        // all blocks of job j have published message seq (round sums: 24 words; the final
-        // folded entries after the last local round: 16 words)
-        auto ready = [&](uint32_t j, uint32_t seq) {
+        // words of the message that follows `done` local rounds: two rounds' sums, one
+        // round's sums, or the folded entries after the last local round
+        auto msg_words = [&](uint32_t j, uint32_t done) {
+            const uint32_t rem = R[j] - done;
+            return rem >= 2 ? (uint32_t)ZKH_MSG_PAIR : rem == 1 ? (uint32_t)ZKH_MSG_ONE : (uint32_t)ZKH_MSG_FINAL;
+        };
+        // all blocks of job j have published message seq of nw words
+        auto ready = [&](uint32_t j, uint32_t seq, uint32_t nw) {
             const uint32_t nb = 1u << lgnb[j];
-            const uint32_t nq = zkh_quad_count(seq <= R[j] ? 24 : 16);
+            const uint32_t nq = zkh_quad_count(nw);
             for (uint32_t b = 0; b < nb; b++)
                 for (uint32_t qd = 0; qd < nq; qd++)
                     if (__atomic_load_n(ps + slot_off[j] + b * ZKH_PSLOT + 4 * qd, __ATOMIC_ACQUIRE) != seq)
@@ -1599,7 +1606,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         auto worker = [&](int t) {
             std::vector<uint32_t> mine;
             for (uint32_t j = (uint32_t)t; j < nj; j += (uint32_t)T) mine.push_back(j);
-            std::vector<uint32_t> rnd(mine.size(), 0);
+            std::vector<uint32_t> rnd(mine.size(), 0), msg(mine.size(), 0);  // local rounds, messages
             std::vector<uint8_t> done(mine.size(), 0);
             size_t left = mine.size();
             std::vector<Fr> ta, tb;
@@ -1611,22 +1618,58 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                     const uint32_t j = mine[a];
                     const uint32_t nb = 1u << lgnb[j];
                     const uint32_t* sl = ps + slot_off[j];
-                    if (!ready(j, rnd[a] + 1)) continue;
+                    const uint32_t nw = msg_words(j, rnd[a]);
+                    if (!ready(j, msg[a] + 1, nw)) continue;
                     prog = true;
-                    if (tracing) {  // block 0's clock: publication, and receipt of the last challenge
-                        const uint32_t* s0 = sl;
-                        tr_gpu[j].push_back(((uint64_t)s0[57] << 32) | s0[56]);
-                        tr_gpu[j].push_back(((uint64_t)s0[59] << 32) | s0[58]);
-                        tr_host[j].push_back(now_us());
-                    }
+                    if (tracing) tr_host[j].push_back(now_us());
                     // a block has run, so every earlier launch (the claim partials) has completed
-                    if (rnd[a] == 0) absorb_claim(j);
-                    if (rnd[a] < R[j]) {
+                    if (msg[a] == 0) absorb_claim(j);
+                    const uint32_t r = rnd[a];
+                    if (nw == ZKH_MSG_PAIR) {  // rounds r and r + 1
+                        Fr sm[9];
+                        for (int k = 0; k < 9; k++) sm[k] = kZero;
+                        for (uint32_t b = 0; b < nb; b++)
+                            for (int k = 0; k < 9; k++) sm[k] = fr_add(sm[k], slot_fr(sl + b * ZKH_PSLOT, k));
+                        // (the sums carry 2^-256; fix1 removes it from the combinations)
+                        bool ok = round_step(j, r, fix1(fr_add(sm[0], sm[3])), fix1(fr_add(sm[1], sm[4])),
+                                             fix1(fr_add(sm[2], sm[5])));
+                        const Fr x0m = J[j].xm;
+                        if (ok) {
+                            // round r + 1's sum k at x: A + x (B + x C) with A = sm[3k],
+                            // C = sm[3k + 2] and B = sm[3k + 1] - A - C
+                            Fr nx[3];
+                            for (int k = 0; k < 3; k++) {
+                                const Fr A = sm[3 * k], C = sm[3 * k + 2];
+                                const Fr Bc = fr_sub(fr_sub(sm[3 * k + 1], A), C);
+                                nx[k] = fix1(fr_add(A, fr_mont_mul(x0m, fr_add(Bc, fr_mont_mul(x0m, C)))));
+                            }
+                            ok = round_step(j, r + 1, nx[0], nx[1], nx[2]);
+                        }
+                        if (!ok) {
+                            send_cmd(j, ZKH_QUIT, nullptr, 0);
+                            done[a] = 1;
+                            left--;
+                            continue;
+                        }
+                        // fold weights in Montgomery form from x0 R, x1 R: (1 - x) R = R - x R
+                        const Fr x1m = J[j].xm;
+                        const Fr u0m = fr_sub(fr_one_m(), x0m), u1m = fr_sub(fr_one_m(), x1m);
+                        const Fr w[4] = {fr_mont_mul(u0m, u1m), fr_mont_mul(x0m, u1m), fr_mont_mul(u0m, x1m),
+                                         fr_mont_mul(x0m, x1m)};
+                        uint32_t cw[32];
+                        for (int k = 0; k < 4; k++) fr_store(w[k], cw + 8 * k);
+                        rnd[a] += 2;
+                        msg[a]++;
+                        send_cmd(j, msg[a], cw, 32);
+                        if (tracing) tr_host[j].push_back(now_us());
+                        continue;
+                    }
+                    if (nw == ZKH_MSG_ONE) {
                         Fr s3[3] = {kZero, kZero, kZero};
                         for (uint32_t b = 0; b < nb; b++)
                             for (int k = 0; k < 3; k++) s3[k] = fr_add(s3[k], slot_fr(sl + b * ZKH_PSLOT, k));
-                        if (!round_step(j, rnd[a], fix1(s3[0]), fix1(s3[1]), fix1(s3[2]))) {
-                            send_cmd(j, ZKH_QUIT, nullptr);
+                        if (!round_step(j, r, fix1(s3[0]), fix1(s3[1]), fix1(s3[2]))) {
+                            send_cmd(j, ZKH_QUIT, nullptr, 0);
                             done[a] = 1;
                             left--;
                             continue;
@@ -1634,9 +1677,16 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                         uint32_t xm[8];
                         fr_store(J[j].xm, xm);
                         rnd[a]++;
-                        send_cmd(j, rnd[a], xm);
+                        msg[a]++;
+                        send_cmd(j, msg[a], xm, 8);
                         if (tracing) tr_host[j].push_back(now_us());
                         continue;
+                    }
+                    if (tracing) {  // block 0's per-message clock stamps are complete once it has exited
+                        for (uint32_t m2 = 1; m2 <= msg[a] + 1 && m2 < 14; m2++) {
+                            tr_gpu[j].push_back(sl[100 + 2 * m2] - sl[99 + 2 * m2]);
+                            tr_gpu[j].push_back(m2 <= msg[a] ? sl[101 + 2 * m2] - sl[100 + 2 * m2] : 0);
+                        }
                     }
                     // the blocks' folded entries: the remaining lgnb rounds on the host
                     ta.resize(nb);
@@ -1682,7 +1732,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                     } else if (e == hipSuccess) {  // the kernel has ended: whatever is missing never comes
                         bool all = true;
                         for (size_t a = 0; a < mine.size(); a++)
-                            all = all && (done[a] || ready(mine[a], rnd[a] + 1));
+                            all = all && (done[a] || ready(mine[a], msg[a] + 1, msg_words(mine[a], rnd[a])));
                         if (!all) why = 4;
                     } else if (now_us() - t_prog > 30e6) {
                         why = 3;
@@ -1709,16 +1759,17 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         if (tracing) {
             fprintf(stderr, "[zkh] mm persistent rounds: %.1f us (%d host threads)\n", now_us() - t_start, T);
             const double tick_us = 1000.0 / (double)c->clock_khz;
-            // per round: block compute (device clock: challenge received -> sums published),
-            // host work (sums seen -> challenge sent) and the round trip the host observes
-            // (challenge sent -> next sums seen)
+            // per message: block 0's compute (device clock: previous command received -> sums
+            // published) and round trip (sums published -> command received), and the host's
+            // work (sums seen -> command sent)
             for (uint32_t j = 0; j < nj; j++) {
                 const auto& g = tr_gpu[j];
                 const auto& h = tr_host[j];
-                fprintf(stderr, "[zkh]   job %u (n=%u, %u blocks): gpu/host/trip us", j, J[j].INp, 1u << lgnb[j]);
-                for (size_t r = 1; 2 * r + 1 < g.size() && 2 * r < h.size(); r++)
-                    fprintf(stderr, " %.1f/%.1f/%.1f", (double)(g[2 * r] - g[2 * r + 1]) * tick_us,
-                            h[2 * r - 1] - h[2 * r - 2], h[2 * r] - h[2 * r - 1]);
+                fprintf(stderr, "[zkh]   job %u (n=%u, %u blocks, %u local rounds): compute/trip/host us", j, J[j].INp,
+                        1u << lgnb[j], R[j]);
+                for (size_t m2 = 0; 2 * m2 + 1 < g.size(); m2++)
+                    fprintf(stderr, " %.1f/%.1f/%.1f", m2 ? (double)(uint32_t)g[2 * m2] * tick_us : 0.0,
+                            (double)(uint32_t)g[2 * m2 + 1] * tick_us, 2 * m2 + 1 < h.size() ? h[2 * m2 + 1] - h[2 * m2] : 0.0);
                 fprintf(stderr, "\n");
             }
         }
