@@ -43,7 +43,7 @@ LATENCY_BOUND = {"zkip_rounds"}
 # HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs
 # (profiles/eqdot_hbm_traffic_tinyllama.txt): the counters of a 256 MiB device copy read
 # 0.500x (FETCH) and 1.000x (WRITE) of its bytes, so FETCH is scaled by 2.
-TRAFFIC = {"eqdot": 314.6e6}
+TRAFFIC = {"eqdot": 315.4e6}
 
 
 def load_pkg():
