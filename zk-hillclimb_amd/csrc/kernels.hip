@@ -858,19 +858,20 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
     return g;
 }
 
-// phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused), split by table
-// group into two kernels that publish as jobs 0 and 1 of one round (each keeps its fold,
-// weights and sums in registers at a fraction of the single kernel's pressure):
+// phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused), one launch whose
+// blocks [0, g) take the (A, S) group and blocks [g, 2g) the (B, T, m) group, publishing as
+// jobs 0 and 1 of one round (each group keeps its fold, weights and sums in registers at a
+// fraction of a single fused body's pressure; one launch instead of two halves the fixed
+// cost of a small round):
 // job 0 (A, S): sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256), sum a0, sum a1  (s + beta)
 // job 1 (B, T, m): sum w*b0*t0, w*b1*t1, w*db*dt, m0*b0, m1*b1, dm*db (x 2^-256)  (t + beta)
 template <int fold>
-__global__ __launch_bounds__(NT) void k_lu_phase2_as(TabDev A, TabDev S, uint32_t n, fr_t vm, fr_t beta,
-                                                     EqDev eq, Publish pub) {
+ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t& vm, const fr_t& beta,
+                       const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint4* accl, uint4* acch) {
     const uint32_t h = n >> 1;
-    __shared__ uint4 accl[5 * NT], acch[5 * NT];
     LdsAcc<5> acc{accl, acch};
     acc.zero();
-    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+    for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
         fr_t wa0, wda;
         {
             fr_t a0, a1;
@@ -898,16 +899,16 @@ __global__ __launch_bounds__(NT) void k_lu_phase2_as(TabDev A, TabDev S, uint32_
     }
     fr_t r[5];
     acc.get(r);
-    reduce_publish<5>(r, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish<5>(r, pub, 0, 0, g, lb);
 }
 template <int fold>
-__global__ __launch_bounds__(NT) void k_lu_phase2_btm(TabDev B, TabDev T, TabDev m, uint32_t n, fr_t vm,
-                                                      fr_t beta, EqDev eq, Publish pub) {
+ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const fr_t& vm,
+                        const fr_t& beta, const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint4* accl,
+                        uint4* acch) {
     const uint32_t h = n >> 1;
-    __shared__ uint4 accl[6 * NT], acch[6 * NT];
     LdsAcc<6> acc{accl, acch};
     acc.zero();
-    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+    for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
         fr_t b0, b1;
         load_pair(B, i, h, n, fold, vm, b0, b1);
         SB();
@@ -943,7 +944,15 @@ __global__ __launch_bounds__(NT) void k_lu_phase2_btm(TabDev B, TabDev T, TabDev
     }
     fr_t r[6];
     acc.get(r);
-    reduce_publish<6>(r, pub, 1, 0, gridDim.x, blockIdx.x);
+    // partials after the (A, S) group's 5g entries: indices (g + lb) * 6 + k >= 6g
+    reduce_publish<6>(r, pub, 1, g, g, lb);
+}
+template <int fold_as, int fold_btm>
+__global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m, uint32_t n,
+                                                  fr_t vm, fr_t beta, EqDev eq, Publish pub, uint32_t g) {
+    __shared__ uint4 accl[6 * NT], acch[6 * NT];
+    if (blockIdx.x < g) lu_phase2_as<fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, g, accl, acch);
+    else lu_phase2_btm<fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - g, g, accl, acch);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
@@ -952,10 +961,11 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
     const fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
     const fr_t beta = to_fr(beta_host);
-    if (fold_as) k_lu_phase2_as<1><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, beta, e, partial);
-    else k_lu_phase2_as<0><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, beta, e, partial);
-    if (fold_btm) k_lu_phase2_btm<1><<<g, NT, 0, s>>>(tab_dev(B), tab_dev(T), tab_dev(m), n, vm, beta, e, partial);
-    else k_lu_phase2_btm<0><<<g, NT, 0, s>>>(tab_dev(B), tab_dev(T), tab_dev(m), n, vm, beta, e, partial);
+    const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T), md = tab_dev(m);
+    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
+    else if (fold_as) k_lu_phase2<1, 0><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
+    else if (fold_btm) k_lu_phase2<0, 1><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
+    else k_lu_phase2<0, 0><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
     return g;
 }
 

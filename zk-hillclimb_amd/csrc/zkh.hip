@@ -2062,8 +2062,11 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
     bool as_pending = false, btm_pending = false;  // a fold with vm is owed
     uint32_t vm[8] = {0};
     Fr three = fr_u64(3);
+    const bool tracing = trace_on();
+    std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
     for (uint32_t r = 0; r < logD; r++) {
         const uint32_t n = D >> r;
+        if (tracing) tr_t.push_back(now_us());
         const uint32_t k = logD - r;  // remaining variables
         const uint32_t K = k - 1;     // eq variables of the pairs
         const Fr ul = u[k - 1];
@@ -2082,6 +2085,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
             }
             Fr s[5];
             if ((rc = wait_pub(c, pb.seq))) return rc;
+            if (tracing) tr_t.push_back(now_us());
             pub_read(c, 0, 5, s);
             Fr q0 = fr_mul(fix1(s[0]), corr), q1 = fr_mul(fix1(s[1]), corr), q2 = fr_mul(fix1(s[2]), corr);
             Fr qc1 = fr_sub(fr_sub(q1, q0), q2);
@@ -2112,6 +2116,7 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
             }
             Fr s[11], sa[5], sb[6];
             if ((rc = wait_pub(c, pb.seq))) return rc;
+            if (tracing) tr_t.push_back(now_us());
             pub_read(c, 0, 5, sa);
             pub_read(c, 1, 6, sb);
             // s: w*a*s sums 0..2, w*b*t sums 3..5, sum a0 / a1 6..7, m*b sums 8..10
@@ -2158,6 +2163,13 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
         if (n > N) Cc = fr_mul(Cc, inv2);
         else alpha_sq = fr_mul(alpha_sq, eqv);
         fr_store(fr_to_mont(v), vm);
+        if (tracing) tr_t.push_back(now_us());
+    }
+    if (tracing) {  // per round: table size, launch -> sums seen, host work (us)
+        fprintf(stderr, "[zkh] lu rounds (n: device/host us):");
+        for (uint32_t r = 0; r < logD; r++)
+            fprintf(stderr, " %u:%.1f/%.1f", D >> r, tr_t[3 * r + 1] - tr_t[3 * r], tr_t[3 * r + 2] - tr_t[3 * r + 1]);
+        fprintf(stderr, "\n");
     }
     // owed folds produce the terminals (size 2 -> 1)
     if (as_pending) {
@@ -2234,8 +2246,11 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     DevPlanes e_src = Ec, s_src = Sc, u_src = Uc;
     uint32_t vm[8] = {0};
     static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
+    const bool tracing = trace_on();
+    std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
     for (uint32_t r = 0; r < k; r++) {
         const uint32_t sz = n >> r;
+        if (tracing) tr_t.push_back(now_us());
         const int fold = r > 0;
         Fr e[4];
         if (!ueq) {
@@ -2246,6 +2261,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             }
             Fr s[4];
             if ((rc = wait_pub(c, pb.seq))) return rc;
+            if (tracing) tr_t.push_back(now_us());
             pub_read(c, 0, 4, s);
             for (int t = 0; t < 4; t++) e[t] = fix2(s[t]);
         } else {
@@ -2259,6 +2275,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             }
             Fr s[4];
             if ((rc = wait_pub(c, pb.seq))) return rc;
+            if (tracing) tr_t.push_back(now_us());
             pub_read(c, 0, 4, s);
             Fr f = fr_mul(cE, eq_corr(eq, K));
             for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(fix1(s[t]), f), fr_eq2(ul, fr_u64(t)));
@@ -2279,6 +2296,13 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         claim = lagrange4(e, w);
         if (ueq) cE = fr_mul(cE, fr_eq2((*ueq)[k - r - 1], w));
         fr_store(fr_to_mont(w), vm);
+        if (tracing) tr_t.push_back(now_us());
+    }
+    if (tracing) {  // per round: table size, launch -> sums seen, host work (us)
+        fprintf(stderr, "[zkh] hp rounds (n: device/host us):");
+        for (uint32_t r = 0; r < k; r++)
+            fprintf(stderr, " %u:%.1f/%.1f", n >> r, tr_t[3 * r + 1] - tr_t[3 * r], tr_t[3 * r + 2] - tr_t[3 * r + 1]);
+        fprintf(stderr, "\n");
     }
     if (k > 0) {
         if (!ueq) launch_fold(c->stream, Tab{e_src, Ew}, 1, vm);
