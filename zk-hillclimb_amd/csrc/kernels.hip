@@ -808,6 +808,61 @@ struct LdsAcc {
         for (int k = 0; k < K; k++) out[k] = ld_fr(lo + k * NT, hi + k * NT, threadIdx.x);
     }
 };
+// Tree over the block's LDS accumulators: level s adds entry t + s into entry t (t < s) of
+// every plane, all threads sharing the K*s additions; afterwards entry 0 of plane k holds
+// the block's sum k.  Cheaper than K 64-lane shuffle trees (one after the other) when the
+// block's work is small.
+template <int K>
+ZDEV void lds_tree(const LdsAcc<K>& acc) {
+    for (uint32_t s = NT / 2; s >= 1; s >>= 1) {
+        __syncthreads();
+        for (uint32_t q = threadIdx.x; q < K * s; q += NT) {
+            const uint32_t k = q / s, t = q - k * s;
+            uint4* lo = acc.lo + k * NT;
+            uint4* hi = acc.hi + k * NT;
+            st_fr(lo, hi, t, fr_add(ld_fr(lo, hi, t), ld_fr(lo, hi, t + s)));
+        }
+    }
+    __syncthreads();
+}
+// reduce_publish over LDS accumulators: the block's sums by an LDS tree; a job of one block
+// writes them to the host directly, otherwise the last block of the job adds the partials
+// (thread t takes blocks t, t + NT, ...) with the same tree.  Same completion protocol.
+template <int K>
+ZDEV void reduce_publish_lds(const LdsAcc<K>& acc, const Publish& P, uint32_t job, uint32_t first, uint32_t nblk,
+                             uint32_t local) {
+    __shared__ int is_last;
+    lds_tree<K>(acc);
+    if (nblk > 1) {
+        if (threadIdx.x < K) st_aos(P.part, (first + local) * K + threadIdx.x, ld_fr(acc.lo + threadIdx.x * NT, acc.hi + threadIdx.x * NT, 0));
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __threadfence();
+            is_last = atomicAdd(&P.counter[job], 1u) == nblk - 1;
+        }
+        __syncthreads();
+        if (!is_last) return;
+        __threadfence();
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            fr_t t = fr_zero();
+            for (uint32_t b = threadIdx.x; b < nblk; b += NT) t = fr_add(t, ld_aos(P.part, (first + b) * K + k));
+            st_fr(acc.lo + k * NT, acc.hi + k * NT, threadIdx.x, t);
+        }
+        lds_tree<K>(acc);
+    }
+    if (threadIdx.x < K) st_aos(P.host_out, job * K + threadIdx.x, ld_fr(acc.lo + threadIdx.x * NT, acc.hi + threadIdx.x * NT, 0));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence_system();
+        P.counter[job] = 0;
+        if (atomicAdd(&P.counter[P.njobs], 1u) == P.njobs - 1) {
+            P.counter[P.njobs] = 0;
+            __threadfence_system();
+            __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
 // phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
 // acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
 __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, int fold, fr_t vm,
@@ -844,9 +899,7 @@ __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n
         acc.add(2, mont_mul_ol(wda, fr_sub(s1, s0)));
         SB();
     }
-    fr_t r[5];
-    acc.get(r);
-    reduce_publish<5>(r, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish_lds<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
@@ -897,9 +950,7 @@ ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t&
         acc.add(2, mont_mul_ol(wda, fr_sub(s1, s0)));
         SB();
     }
-    fr_t r[5];
-    acc.get(r);
-    reduce_publish<5>(r, pub, 0, 0, g, lb);
+    reduce_publish_lds<5>(acc, pub, 0, 0, g, lb);
 }
 template <int fold>
 ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const fr_t& vm,
@@ -942,10 +993,8 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
         acc.add(2, mont_mul_ol(wdb, fr_sub(t1, t0)));
         SB();
     }
-    fr_t r[6];
-    acc.get(r);
     // partials after the (A, S) group's 5g entries: indices (g + lb) * 6 + k >= 6g
-    reduce_publish<6>(r, pub, 1, g, g, lb);
+    reduce_publish_lds<6>(acc, pub, 1, g, g, lb);
 }
 template <int fold_as, int fold_btm>
 __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m, uint32_t n,
@@ -1007,9 +1056,7 @@ __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, u
             if (t < 3) u0 = fr_add(u0, du);
         }
     }
-    fr_t r[4];
-    acc.get(r);
-    reduce_publish<4>(r, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish_lds<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fold,
                          const uint32_t* v_m_host, Publish partial) {
@@ -1064,9 +1111,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
         acc.add(3, mont_mul_ol(fr_add(ws2, wds), fr_add(u2, du)));
         SB();
     }
-    fr_t r[4];
-    acc.get(r);
-    reduce_publish<4>(r, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish_lds<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, EqW eq, Publish partial) {
