@@ -304,7 +304,7 @@ def test_lu_mapping(zkh, ctx):
 
 
 # ---------------------------------------------------------------- Hadamard
-@pytest.mark.parametrize("k", [1, 2, 5, 11, 14])
+@pytest.mark.parametrize("k", [1, 2, 5, 11, 13, 14])
 def test_hp_prove(zkh, ctx, k):
     n = 1 << k
     rng = np.random.default_rng(k)
@@ -325,3 +325,34 @@ def test_hp_prove(zkh, ctx, k):
         for key in ("ev", "term", "ws"):
             assert fr_eq(got[key], want[key]), (key, eqform)
         assert bytes(st_g) == bytes(st_o)
+
+
+@pytest.mark.parametrize("k", [3, 11])
+def test_hp_prove_eq_wrong_claim_stops(zkh, ctx, k):
+    """A claim off by one fails the first round inside the persistent round loop (eq and
+    explicit-E forms): the call returns ZKH_EROUND (2), the blocks exit on the quit command,
+    and the context stays usable (the next proof is bit-exact against the oracle)."""
+    n = 1 << k
+    rng = np.random.default_rng(100 + k)
+    u = rand_fr_full(rng, k)
+    S = C.ints_to_fr(rng.integers(-2**20, 2**20, size=n))
+    U = rand_fr_full(rng, n)
+    E = C.build_eq(u)
+    Ei, Si, Ui = C.fr_to_ints(E), C.fr_to_ints(S), C.fr_to_ints(U)
+    good = sum(a * b % P.R * c for a, b, c in zip(Ei, Si, Ui)) % P.R
+    bad = C.ints_to_fr([(good + 1) % P.R])[0]
+    for eqform in (True, False):
+        st_g, _ = seed_transcript(zkh, "hpbad:%d" % k)
+        with pytest.raises(zkh.ZkhError) as e:
+            if eqform:
+                ctx.hp_prove_eq(st_g, bad, u, ctx.from_fr(S), ctx.from_fr(U))
+            else:
+                ctx.hp_prove(st_g, bad, ctx.from_fr(E), ctx.from_fr(S), ctx.from_fr(U))
+        assert e.value.code == 2
+    st_g, st_o = seed_transcript(zkh, "hpgood:%d" % k)
+    claim = C.ints_to_fr([good])[0]
+    rc, want = C.hp_prove(st_o, claim, E, S, U)
+    got = ctx.hp_prove_eq(st_g, claim, u, ctx.from_fr(S), ctx.from_fr(U))
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)

@@ -1690,6 +1690,155 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
         __syncthreads();
     }
 }
+// Persistent Hadamard rounds (see HpPersist).  Eq mode: the eq weight of a local pair k is
+// the same in every round (g = block + nb*k; only the host's correction changes), so
+// W[k] = eq_w(g) is formed once while the tables load.  Per round, with h = m/2 pairs, two
+// levels of one Montgomery product per thread, each spread over as many waves as it has
+// products:
+//   eq mode   level 1: WS[k] = W[k] s0[k], WD[k] = W[k] (s1[k] - s0[k]);
+//             level 2: P[t][k] = (WS[k] + t WD[k]) (u0[k] + t du[k]), t < 4;
+//   E mode    level 1: Q[t][k] = E_t[k] S_t[k];  level 2: P[t][k] = Q[t][k] U_t[k];
+// then wave t < 4 adds row t.  After the challenge one thread per entry folds the tables.
+// LDS: the tables (ls entries each, lo plane then hi plane) and 8 rows of ls/2 entries
+// (eq mode: W, WS, WD, -, P[0..3]; E mode: Q[0..3], P[0..3]).
+__global__ __launch_bounds__(NTP) void k_hp_persist(HpPersist P) {
+    extern __shared__ uint4 zl[];
+    __shared__ uint32_t sok, pubw[ZKH_HP_MSG], sxw[9];
+    const uint32_t lb = blockIdx.x;
+    const uint32_t ls = P.n >> P.lgnb, hs = ls >> 1;
+    const bool em = P.e_lo != nullptr;
+    const uint32_t ntab = em ? 3 : 2;  // S, U (, E)
+    uint4* tlo[3];
+    uint4* thi[3];
+    for (uint32_t i = 0; i < 3; i++) {
+        tlo[i] = zl + 2 * i * ls;
+        thi[i] = tlo[i] + ls;
+    }
+    uint4* rlo = zl + 2 * ntab * ls;  // 8 rows of hs: lo planes, then hi planes
+    uint4* rhi = rlo + 8 * hs;
+    const EqDev eq{P.elo, P.ehi, 0};
+    {
+        const uint4* glo_[3] = {reinterpret_cast<const uint4*>(P.s_lo), reinterpret_cast<const uint4*>(P.u_lo),
+                                reinterpret_cast<const uint4*>(P.e_lo)};
+        const uint4* ghi_[3] = {reinterpret_cast<const uint4*>(P.s_hi), reinterpret_cast<const uint4*>(P.u_hi),
+                                reinterpret_cast<const uint4*>(P.e_hi)};
+        const fr_t vm = to_fr(P.vm.v);
+        const uint32_t nload = ntab * ls + (em ? 0 : hs);
+        for (uint32_t t = threadIdx.x; t < nload; t += NTP) {  // tables, then (eq mode) W
+            if (t < ntab * ls) {
+                const uint32_t i = t / ls, k = t - i * ls;
+                const uint32_t g = lb + (k << P.lgnb);
+                const fr_t v = P.fold ? fold_at(glo_[i], ghi_[i], g, P.n, vm) : ld_fr(glo_[i], ghi_[i], g);
+                st_fr(tlo[i], thi[i], k, v);
+            } else {
+                const uint32_t k = t - ntab * ls;
+                st_fr(rlo, rhi, k, eq_w(eq, lb + (k << P.lgnb)));
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t* slot = P.out + (size_t)lb * ZKH_PSLOT;
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint32_t m = ls;
+    uint64_t t_cmd = 0;
+    for (uint32_t seq = 1;; seq++) {
+        uint32_t nw;
+        if (m >= 2) {
+            const uint32_t h = m >> 1;
+            if (!em) {
+                for (uint32_t t = threadIdx.x; t < 2 * h; t += NTP) {  // level 1
+                    const bool d = t >= h;
+                    const uint32_t k = d ? t - h : t;
+                    const fr_t s0 = ld_fr(tlo[0], thi[0], k);
+                    const fr_t x = d ? fr_sub(ld_fr(tlo[0], thi[0], k + h), s0) : s0;
+                    st_fr(rlo + (1 + d) * hs, rhi + (1 + d) * hs, k, mont_mul_ol(ld_fr(rlo, rhi, k), x));
+                }
+            } else {
+                for (uint32_t q = threadIdx.x; q < 4 * h; q += NTP) {  // level 1: q = t * h + k
+                    const uint32_t t = q / h, k = q - t * h;
+                    fr_t e = ld_fr(tlo[2], thi[2], k), sv = ld_fr(tlo[0], thi[0], k);
+                    const fr_t de = fr_sub(ld_fr(tlo[2], thi[2], k + h), e), ds = fr_sub(ld_fr(tlo[0], thi[0], k + h), sv);
+                    for (uint32_t i = 0; i < t; i++) {
+                        e = fr_add(e, de);
+                        sv = fr_add(sv, ds);
+                    }
+                    st_fr(rlo + t * hs, rhi + t * hs, k, mont_mul_ol(e, sv));
+                }
+            }
+            __syncthreads();
+            for (uint32_t q = threadIdx.x; q < 4 * h; q += NTP) {  // level 2: q = t * h + k
+                const uint32_t t = q / h, k = q - t * h;
+                const fr_t u0 = ld_fr(tlo[1], thi[1], k), du = fr_sub(ld_fr(tlo[1], thi[1], k + h), u0);
+                fr_t a, c = u0;
+                if (!em) {
+                    a = ld_fr(rlo + hs, rhi + hs, k);
+                    const fr_t wd = ld_fr(rlo + 2 * hs, rhi + 2 * hs, k);
+                    for (uint32_t i = 0; i < t; i++) a = fr_add(a, wd);
+                } else {
+                    a = ld_fr(rlo + t * hs, rhi + t * hs, k);
+                }
+                for (uint32_t i = 0; i < t; i++) c = fr_add(c, du);
+                st_fr(rlo + (4 + t) * hs, rhi + (4 + t) * hs, k, mont_mul_ol(a, c));
+            }
+            __syncthreads();
+            if (wv < 4) {  // wave t adds row 4 + t
+                fr_t acc = fr_zero();
+                for (uint32_t k = lane; k < h; k += 64)
+                    acc = fr_add(acc, ld_fr(rlo + (4 + wv) * hs, rhi + (4 + wv) * hs, k));
+                acc = fr_wave_sum(acc);
+                if (lane == 0)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) pubw[8 * wv + i] = acc.v[i];
+            }
+            nw = ZKH_HP_MSG;
+        } else {  // the block's folded entries S[0], U[0] (, E[0])
+            nw = 8 * ntab;
+            if (wv == 0 && lane < ntab) {
+                const fr_t t = ld_fr(tlo[lane], thi[lane], 0);
+#pragma unroll
+                for (int i = 0; i < 8; i++) pubw[8 * lane + i] = t.v[i];
+            }
+        }
+        __syncthreads();
+        if (wv == 0) {
+            if (lane == 0) persist_stamp(slot, seq, t_cmd);
+            persist_publish(slot, pubw, nw, seq);
+        }
+        if (m == 1) return;
+        if (wv == 0) {
+            uint4 qd;
+            const bool ok = persist_wait(P.cmd, 3, seq, P.err, P.deadline, qd);
+            if (lane < 3) {
+                sxw[3 * lane] = qd.y;
+                sxw[3 * lane + 1] = qd.z;
+                sxw[3 * lane + 2] = qd.w;
+            }
+            if (lane == 0) sok = ok;
+            t_cmd = wall_clock64();
+        }
+        __syncthreads();
+        if (!sok) return;
+        {  // fold the tables: T[k] <- T[k] + x (T[k + m/2] - T[k])
+            fr_t x;
+#pragma unroll
+            for (int i = 0; i < 8; i++) x.v[i] = sxw[i];
+            const uint32_t h = m >> 1;
+            for (uint32_t t = threadIdx.x; t < ntab * h; t += NTP) {
+                const uint32_t i = t / h, k = t - i * h;
+                const fr_t v0 = ld_fr(tlo[i], thi[i], k), v1 = ld_fr(tlo[i], thi[i], k + h);
+                st_fr(tlo[i], thi[i], k, fr_add(v0, mont_mul_ol(x, fr_sub(v1, v0))));
+            }
+        }
+        m >>= 1;
+        __syncthreads();
+    }
+}
+hipError_t launch_hp_persist(hipStream_t s, const HpPersist& p) {
+    const uint32_t ls = p.n >> p.lgnb;  // LDS: 2 or 3 tables of ls + 8 rows of ls/2 entries, 32 B each
+    const size_t lds = (size_t)ls * 32 * (p.e_lo ? 3 : 2) + (size_t)(ls >> 1) * 8 * 32;
+    k_hp_persist<<<1u << p.lgnb, NTP, lds, s>>>(p);
+    return hipGetLastError();
+}
 // An ordinary launch on the stream: the blocks never wait for each other, only for the
 // host, and a launch has at most 256 blocks (one per CU at most 32 KiB LDS and 16 waves),
 // so all of them are resident once earlier kernels drain.

@@ -247,6 +247,37 @@ void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
 __host__ __device__ inline uint32_t zkh_quad_word(uint32_t i) { return 4 * (i / 3) + 1 + i % 3; }
 __host__ __device__ inline uint32_t zkh_quad_count(uint32_t nwords) { return (nwords + 2) / 3; }
 #define ZKH_PLS_MAX 512u  // entries per block and table (32 KiB of LDS for both tables)
+
+// ---- persistent Hadamard rounds (the small rounds of zkh_hp_prove / zkh_hp_prove_eq) ----
+// Tables S, U (and E) of n entries (after the fold owed by the last launched round, applied
+// while they load into LDS) spread cyclically over nb = 2^lgnb blocks as in the matmul
+// loop.  Per local round with m entries per block each block publishes, over its pairs
+// (k, k + m/2), sum_k eq_w(g) S_t[k] U_t[k] for t = 0..3 (g = block + nb*k the global pair
+// index, eq_w the device eq weight of the per-round kernels; x 2^-256) or, with E,
+// sum_k E_t[k] S_t[k] U_t[k] (x 2^-512): 32 words, 11 quads.  It then waits for the
+// challenge (Montgomery form, 3 quads) and folds the tables; with m = 1 it publishes S[0],
+// U[0] (and E[0]) (16 or 24 words) and exits.  Message s carries seq s.  Slot layout,
+// ZKH_QUIT and the deadline as in ZkipPersist.
+struct HpPersist {
+    const uint32_t* s_lo;
+    const uint32_t* s_hi;
+    const uint32_t* u_lo;
+    const uint32_t* u_hi;
+    const uint32_t* e_lo;  // an explicit E table (zkh_hp_prove), or null: the eq weights
+    const uint32_t* e_hi;
+    const uint32_t* elo;  // eq factor tables (EqW)
+    const uint32_t* ehi;
+    uint32_t* out;  // pinned host, nb slots
+    uint32_t* cmd;  // pinned host, one command area
+    uint32_t* err;
+    unsigned long long deadline;
+    fr_arg vm;        // the owed fold's challenge (Montgomery form) when fold != 0
+    uint32_t n, lgnb, fold, pad_;  // fold: entries g and g + n of the sources fold into g
+};
+#define ZKH_HP_MSG 32
+// at most 16 blocks of ZKH_PLS_MAX entries; returns the HIP status of the launch
+hipError_t launch_hp_persist(hipStream_t s, const HpPersist& p);
+
 struct ZkipPJob {
     const uint32_t* a_lo;
     const uint32_t* a_hi;

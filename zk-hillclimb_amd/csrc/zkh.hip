@@ -2217,6 +2217,176 @@ static Fr lagrange4(const Fr e[4], const Fr& v) {
     Fr t3 = fr_mul(fr_mul(fr_mul(fr_mul(v, vm1), vm2), inv6), ddd);
     return fr_add(fr_add(fr_add(e[0], t1), t2), t3);
 }
+// Rounds r0 .. k-1 of a Hadamard sumcheck in one persistent launch (see HpPersist) once the
+// tables have sz <= ZKH_HP_PERSIST_MAX entries: one host round trip per round instead of a
+// launch; the block-count rounds at the end run on the host.  The per-round host logic is
+// hp_common's: e[t] = sums_t * cE * corr(K) * eq(u_last, t) with the eq weights (u given),
+// e[t] = sums_t with an explicit E table (e_src given, u null); then the claim check, the
+// absorbs "hp0".."hp3" and the challenge.
+#define ZKH_HP_PERSIST_MAX 8192u
+static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* u, const EqState& eq, uint32_t k,
+                             uint32_t r0, uint32_t sz, int fold, DevPlanes e_src, DevPlanes s_src, DevPlanes u_src,
+                             const uint32_t vm[8], Fr& claim, Fr& cE, uint32_t* ev_out, uint32_t* ws_out, Fr& e_fin,
+                             Fr& s_fin, Fr& u_fin) {
+    const bool em = u == nullptr;  // explicit E table
+    static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
+    const uint32_t lgnb = sz > ZKH_PLS_MAX ? ceil_log2(sz / ZKH_PLS_MAX) : 0, nb = 1u << lgnb;
+    const uint32_t R = ceil_log2(sz) - lgnb;  // local rounds
+    int rc;
+    if ((rc = ensure_ps(c, (size_t)ZKH_PSLOT * (nb + 2)))) return rc;
+    uint32_t* ps = c->ps_host;
+    uint32_t* slots = ps + ZKH_PSLOT;
+    uint32_t* cmd = ps + (size_t)ZKH_PSLOT * (nb + 1);
+    memset(ps, 0, (size_t)ZKH_PSLOT * (nb + 2) * 4);
+    HpPersist P{};
+    P.s_lo = s_src.lo();
+    P.s_hi = s_src.hi();
+    P.u_lo = u_src.lo();
+    P.u_hi = u_src.hi();
+    P.e_lo = em ? e_src.lo() : nullptr;
+    P.e_hi = em ? e_src.hi() : nullptr;
+    P.elo = eq.elo_d;
+    P.ehi = eq.ehi_d;
+    P.out = slots;
+    P.cmd = cmd;
+    P.err = ps;
+    P.deadline = c->clock_khz * 1000 * 20;  // 20 s without a command
+    memcpy(P.vm.v, vm, 32);
+    P.n = sz;
+    P.lgnb = lgnb;
+    P.fold = fold ? 1 : 0;
+    auto send = [&](uint32_t seq, const uint32_t* xm) {
+        for (uint32_t i = 0; i < 8 && xm; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
+        for (uint32_t qd = 0; qd < 3; qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
+    };
+    auto quit = [&]() {
+        send(ZKH_QUIT, nullptr);
+        (void)hipStreamSynchronize(c->stream);
+    };
+    {
+        ProfScope ps_(c, "hp_persist", (double)sz * (em ? 3 : 2) * 32 * (fold ? 3 : 1));
+        hipError_t e = launch_hp_persist(c->stream, P);
+        if (e != hipSuccess) {
+            quit();
+            return fail(c, ZKH_EDEV, "persistent hadamard launch: %s", hipGetErrorString(e));
+        }
+    }
+    const double t_launch = now_us();
+    auto slot_fr = [&](uint32_t b, uint32_t i) {
+        uint32_t v[8];
+        for (uint32_t j = 0; j < 8; j++) v[j] = slots[(size_t)b * ZKH_PSLOT + zkh_quad_word(8 * i + j)];
+        return fr_load(v);
+    };
+    // every block has published message seq (nw words); device errors, a block's
+    // deadline and an ended kernel stop the wait
+    auto wait_msg = [&](uint32_t seq, uint32_t nw) -> int {
+        const uint32_t nq = zkh_quad_count(nw);
+        const double t0 = now_us();
+        for (uint64_t spins = 1;; spins++) {
+            bool all = true;
+            for (uint32_t b = 0; b < nb && all; b++)
+                for (uint32_t qd = 0; qd < nq; qd++)
+                    if (__atomic_load_n(slots + (size_t)b * ZKH_PSLOT + 4 * qd, __ATOMIC_ACQUIRE) != seq) {
+                        all = false;
+                        break;
+                    }
+            if (all) return 0;
+            __builtin_ia32_pause();
+            if ((spins & 0x3FFF) == 0) {
+                hipError_t e = hipStreamQuery(c->stream);
+                if (e != hipSuccess && e != hipErrorNotReady) {
+                    quit();
+                    return fail(c, ZKH_EDEV, "persistent hadamard rounds: %s", hipGetErrorString(e));
+                }
+                if (__atomic_load_n(ps, __ATOMIC_ACQUIRE) || e == hipSuccess || now_us() - t0 > 30e6) {
+                    quit();
+                    return fail(c, ZKH_EDEV, "persistent hadamard rounds stopped (%s)",
+                                ps[0] ? "a block timed out" : e == hipSuccess ? "kernel ended early" : "no progress");
+                }
+            }
+        }
+    };
+    auto host_round = [&](uint32_t r, const Fr sums[4], bool device, Fr& w) -> bool {
+        const uint32_t K = k - r - 1;
+        const Fr ul = em ? kZero : (*u)[k - r - 1];
+        Fr e[4];
+        if (em) {
+            for (int t = 0; t < 4; t++) e[t] = device ? fix2(sums[t]) : sums[t];
+        } else {
+            const Fr f = device ? fr_mul(cE, eq_corr(eq, K)) : cE;
+            for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(device ? fix1(sums[t]) : sums[t], f), fr_eq2(ul, fr_u64(t)));
+        }
+        if (!fr_eq(claim, fr_add(e[0], e[1]))) return false;
+        for (int t = 0; t < 4; t++) {
+            tr_absorb_fr(tr, lab[t], e[t]);
+            if (ev_out) fr_store(e[t], ev_out + 8 * (4 * r + t));
+        }
+        w = tr_challenge(tr);
+        if (ws_out) fr_store(w, ws_out + 8 * r);
+        claim = lagrange4(e, w);
+        if (!em) cE = fr_mul(cE, fr_eq2(ul, w));
+        return true;
+    };
+    for (uint32_t lr = 0; lr < R; lr++) {
+        if ((rc = wait_msg(lr + 1, ZKH_HP_MSG))) return rc;
+        Fr sums[4] = {kZero, kZero, kZero, kZero};
+        for (uint32_t b = 0; b < nb; b++)
+            for (int t = 0; t < 4; t++) sums[t] = fr_add(sums[t], slot_fr(b, t));
+        Fr w;
+        if (!host_round(r0 + lr, sums, true, w)) {
+            quit();
+            return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r0 + lr);
+        }
+        uint32_t xm[8];
+        fr_store(fr_to_mont(w), xm);
+        send(lr + 1, xm);
+    }
+    if ((rc = wait_msg(R + 1, em ? 24 : 16))) return rc;
+    std::vector<Fr> ta(nb), tb(nb), te(em ? nb : 0);
+    for (uint32_t b = 0; b < nb; b++) {
+        ta[b] = slot_fr(b, 0);
+        tb[b] = slot_fr(b, 1);
+        if (em) te[b] = slot_fr(b, 2);
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));  // the blocks have exited
+    // the last lgnb rounds over the blocks' entries (entry b is global index b)
+    for (uint32_t r = r0 + R, m = nb; m > 1; r++, m >>= 1) {
+        const uint32_t h = m >> 1, K = k - r - 1;
+        Fr sums[4] = {kZero, kZero, kZero, kZero};
+        for (uint32_t i = 0; i < h; i++) {
+            Fr w = kOne, de = kZero;
+            if (em) {
+                w = te[i];
+                de = fr_sub(te[i + h], te[i]);
+            } else {
+                for (uint32_t j = 0; j < K; j++) w = fr_mul(w, ((i >> j) & 1) ? (*u)[j] : fr_sub(kOne, (*u)[j]));
+            }
+            const Fr ds = fr_sub(ta[i + h], ta[i]), du = fr_sub(tb[i + h], tb[i]);
+            Fr st = ta[i], ut = tb[i];
+            for (int t = 0; t < 4; t++) {
+                sums[t] = fr_add(sums[t], fr_mul(w, fr_mul(st, ut)));
+                st = fr_add(st, ds);
+                ut = fr_add(ut, du);
+                w = fr_add(w, de);
+            }
+        }
+        Fr w;
+        if (!host_round(r, sums, false, w))
+            return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r);
+        for (uint32_t i = 0; i < h; i++) {
+            ta[i] = fr_add(ta[i], fr_mul(w, fr_sub(ta[i + h], ta[i])));
+            tb[i] = fr_add(tb[i], fr_mul(w, fr_sub(tb[i + h], tb[i])));
+            if (em) te[i] = fr_add(te[i], fr_mul(w, fr_sub(te[i + h], te[i])));
+        }
+    }
+    s_fin = ta[0];
+    u_fin = tb[0];
+    e_fin = em ? te[0] : cE;
+    if (trace_on())
+        fprintf(stderr, "[zkh] hp persistent loop: n=%u, %u blocks, %u device + %u host rounds in %.1f us\n", sz, nb, R,
+                lgnb, now_us() - t_launch);
+    return 0;
+}
 static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], const zkh_tensor* E,
                      const std::vector<Fr>* ueq, const zkh_tensor* S, const zkh_tensor* U,
                      uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out) {
@@ -2248,10 +2418,19 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
     const bool tracing = trace_on();
     std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
+    bool persisted = false;    // the last rounds ran in hp_persist_rounds
+    Fr e_fin = kZero, s_fin = kZero, u_fin = kZero;
     for (uint32_t r = 0; r < k; r++) {
         const uint32_t sz = n >> r;
-        if (tracing) tr_t.push_back(now_us());
         const int fold = r > 0;
+        if (sz <= ZKH_HP_PERSIST_MAX && !getenv("ZKH_NO_PERSIST")) {  // the rest in one launch
+            if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, vm, claim, cE, ev_out,
+                                        ws_out, e_fin, s_fin, u_fin)))
+                return rc;
+            persisted = true;
+            break;
+        }
+        if (tracing) tr_t.push_back(now_us());
         Fr e[4];
         if (!ueq) {
             Publish pb = make_pub(c, 1);
@@ -2299,31 +2478,37 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         if (tracing) tr_t.push_back(now_us());
     }
     if (tracing) {  // per round: table size, launch -> sums seen, host work (us)
-        fprintf(stderr, "[zkh] hp rounds (n: device/host us):");
-        for (uint32_t r = 0; r < k; r++)
+        fprintf(stderr, "[zkh] hp rounds (n: device/host us)%s:", persisted ? ", then the persistent loop" : "");
+        for (uint32_t r = 0; r < tr_t.size() / 3; r++)
             fprintf(stderr, " %u:%.1f/%.1f", n >> r, tr_t[3 * r + 1] - tr_t[3 * r], tr_t[3 * r + 2] - tr_t[3 * r + 1]);
         fprintf(stderr, "\n");
     }
-    if (k > 0) {
-        if (!ueq) launch_fold(c->stream, Tab{e_src, Ew}, 1, vm);
-        launch_fold(c->stream, Tab{s_src, Sw}, 1, vm);
-        launch_fold(c->stream, Tab{u_src, Uw}, 1, vm);
-        e_src = Ew;
-        s_src = Sw;
-        u_src = Uw;
-    }
     uint32_t tv[3][8];
-    HIPCHK(c, hipMemcpyAsync(tv[0], s_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipMemcpyAsync(tv[0] + 4, s_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipMemcpyAsync(tv[1], u_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipMemcpyAsync(tv[1] + 4, u_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
-    if (!ueq) {
-        HIPCHK(c, hipMemcpyAsync(tv[2], e_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
-        HIPCHK(c, hipMemcpyAsync(tv[2] + 4, e_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    if (persisted) {
+        fr_store(s_fin, tv[0]);
+        fr_store(u_fin, tv[1]);
+        fr_store(e_fin, tv[2]);
     } else {
-        fr_store(cE, tv[2]);
+        if (k > 0) {
+            if (!ueq) launch_fold(c->stream, Tab{e_src, Ew}, 1, vm);
+            launch_fold(c->stream, Tab{s_src, Sw}, 1, vm);
+            launch_fold(c->stream, Tab{u_src, Uw}, 1, vm);
+            e_src = Ew;
+            s_src = Sw;
+            u_src = Uw;
+        }
+        HIPCHK(c, hipMemcpyAsync(tv[0], s_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(tv[0] + 4, s_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(tv[1], u_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(tv[1] + 4, u_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+        if (!ueq) {
+            HIPCHK(c, hipMemcpyAsync(tv[2], e_src.lo(), 16, hipMemcpyDeviceToHost, c->stream));
+            HIPCHK(c, hipMemcpyAsync(tv[2] + 4, e_src.hi(), 16, hipMemcpyDeviceToHost, c->stream));
+        } else {
+            fr_store(cE, tv[2]);
+        }
+        HIPCHK(c, hipStreamSynchronize(c->stream));
     }
-    HIPCHK(c, hipStreamSynchronize(c->stream));
     // terminal: cur = E_f * S_f2 * U_f2 (zkob_rope.cu:29)
     if (!fr_eq(claim, fr_mul(fr_mul(fr_load(tv[2]), fr_load(tv[0])), fr_load(tv[1]))))
         return fail(c, ZKH_EROUND, "hadamard terminal mismatch (witness bug)");
