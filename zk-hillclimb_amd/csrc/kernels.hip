@@ -1494,18 +1494,19 @@ ZDEV void persist_publish(uint32_t* slot, const uint32_t* pub, uint32_t nw, uint
 #define NTP 1024  // threads of a persistent round block (16 waves)
 static_assert(2 * ZKH_PLS_MAX <= NTP, "the double fold takes one product per thread");
 
-// block clock -> slot words 96..99 (publication time, receipt of the previous command),
-// and the low words of both per message s < 14 into words 100 + 2s (publication of message
-// s) and 101 + 2(s - 1) (receipt of command s - 1); the host reads the per-message words
-// after the kernel has ended
+// block clock -> slot words ZKH_PSTAMP + 0..3 (publication time, receipt of the previous
+// command), and the low words of both per message s < 14 into words ZKH_PSTAMP + 4 + 2s
+// (publication of message s) and ZKH_PSTAMP + 5 + 2(s - 1) (receipt of command s - 1); the
+// host reads the per-message words after the kernel has ended
 ZDEV void persist_stamp(uint32_t* slot, uint32_t s, uint64_t t_cmd) {
     const uint64_t now = wall_clock64();
-    slot[96] = (uint32_t)now;
-    slot[97] = (uint32_t)(now >> 32);
-    slot[98] = (uint32_t)t_cmd;
-    slot[99] = (uint32_t)(t_cmd >> 32);
-    if (s < 14) slot[100 + 2 * s] = (uint32_t)now;
-    if (s >= 1 && s <= 14) slot[101 + 2 * (s - 1)] = (uint32_t)t_cmd;
+    uint32_t* st = slot + ZKH_PSTAMP;
+    st[0] = (uint32_t)now;
+    st[1] = (uint32_t)(now >> 32);
+    st[2] = (uint32_t)t_cmd;
+    st[3] = (uint32_t)(t_cmd >> 32);
+    if (s < 14) st[4 + 2 * s] = (uint32_t)now;
+    if (s >= 1 && s <= 14) st[5 + 2 * (s - 1)] = (uint32_t)t_cmd;
 }
 // operand sel of a table at position p of the halves (L = T[p], H = T[p + h], D = H - L)
 ZDEV fr_t half_opnd(const uint4* lo, const uint4* hi, uint32_t sel, uint32_t p, uint32_t h) {
@@ -1837,6 +1838,148 @@ hipError_t launch_hp_persist(hipStream_t s, const HpPersist& p) {
     const uint32_t ls = p.n >> p.lgnb;  // LDS: 2 or 3 tables of ls + 8 rows of ls/2 entries, 32 B each
     const size_t lds = (size_t)ls * 32 * (p.e_lo ? 3 : 2) + (size_t)(ls >> 1) * 8 * 32;
     k_hp_persist<<<1u << p.lgnb, NTP, lds, s>>>(p);
+    return hipGetLastError();
+}
+// Persistent logUp phase-2 rounds (see LuPersist).  W[k] = eq_w(g) is formed once while the
+// tables load.  Per round, with h = m/2 pairs: level 1, one product per thread, rows
+// WA0 = W a0, WDA = W (a1 - a0), WB0 = W b0, WDB = W (b1 - b0); level 2, wave j < 11
+// accumulates sum type kLuType[j] over the pairs (one product per pair, none for sum a0 /
+// sum a1) and adds its lanes.  The type order puts 3, 2, 2, 2 product waves on the four
+// SIMDs.  After the challenge one thread per entry folds the five tables.
+// LDS: 5 tables (ls entries each, lo plane then hi plane) and 5 rows of ls/2 (W, WA0, WDA,
+// WB0, WDB).
+__constant__ uint32_t kLuType[11] = {0, 1, 2, 5, 6, 3, 4, 7, 8, 9, 10};
+__global__ __launch_bounds__(NTP) void k_lu_persist(LuPersist P) {
+    extern __shared__ uint4 zl[];
+    __shared__ uint32_t sok, pubw[ZKH_LU_MSG], sxw[9];
+    const uint32_t lb = blockIdx.x;
+    const uint32_t ls = P.n >> P.lgnb, hs = ls >> 1;
+    uint4* tlo[5];
+    uint4* thi[5];
+    for (uint32_t i = 0; i < 5; i++) {
+        tlo[i] = zl + 2 * i * ls;
+        thi[i] = tlo[i] + ls;
+    }
+    uint4* rlo = zl + 10 * ls;  // 5 rows of hs: lo planes, then hi planes
+    uint4* rhi = rlo + 5 * hs;
+    const EqDev eq{P.elo, P.ehi, 0};
+    const fr_t beta = to_fr(P.beta.v);
+    {
+        const fr_t vm = to_fr(P.vm.v);
+        for (uint32_t t = threadIdx.x; t < 5 * ls + hs; t += NTP) {  // tables, then W
+            if (t < 5 * ls) {
+                const uint32_t i = t / ls, k = t - i * ls;
+                const uint32_t g = lb + (k << P.lgnb);
+                const uint4* glo = reinterpret_cast<const uint4*>(P.lo[i]);
+                const uint4* ghi = reinterpret_cast<const uint4*>(P.hi[i]);
+                const bool f = i < 2 ? P.fold_as : P.fold_btm;
+                st_fr(tlo[i], thi[i], k, f ? fold_at(glo, ghi, g, P.n, vm) : ld_fr(glo, ghi, g));
+            } else {
+                const uint32_t k = t - 5 * ls;
+                st_fr(rlo, rhi, k, eq_w(eq, lb + (k << P.lgnb)));
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t* slot = P.out + (size_t)lb * ZKH_PSLOT;
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    uint32_t m = ls;
+    uint64_t t_cmd = 0;
+    for (uint32_t seq = 1;; seq++) {
+        uint32_t nw;
+        if (m >= 2) {
+            const uint32_t h = m >> 1;
+            for (uint32_t q = threadIdx.x; q < 4 * h; q += NTP) {  // level 1: row 1 + j, j = q / h
+                const uint32_t j = q / h, k = q - j * h;
+                const uint32_t ti = j < 2 ? 0 : 2;  // A or B
+                const fr_t x0 = ld_fr(tlo[ti], thi[ti], k);
+                const fr_t x = (j & 1) ? fr_sub(ld_fr(tlo[ti], thi[ti], k + h), x0) : x0;
+                st_fr(rlo + (1 + j) * hs, rhi + (1 + j) * hs, k, mont_mul_ol(ld_fr(rlo, rhi, k), x));
+            }
+            __syncthreads();
+            if (wv < 11) {  // level 2: wave wv, sum type ty
+                const uint32_t ty = kLuType[wv];
+                fr_t acc = fr_zero();
+                for (uint32_t k = lane; k < h; k += 64) {
+                    if (ty == 3 || ty == 4) {  // sum a0 / sum a1
+                        acc = fr_add(acc, ld_fr(tlo[0], thi[0], ty == 3 ? k : k + h));
+                        continue;
+                    }
+                    fr_t x, y;
+                    if (ty < 8) {  // (A, S) or (B, T) with the level-1 rows
+                        const uint32_t g0 = ty < 3 ? 0 : 1;   // group
+                        const uint32_t r0 = 1 + 2 * g0;       // WA0 / WB0 row
+                        const uint32_t tt = g0 ? 3 : 1;       // S or T
+                        const uint32_t sel = ty < 3 ? ty : ty - 5;
+                        const fr_t w0 = ld_fr(rlo + r0 * hs, rhi + r0 * hs, k);
+                        const fr_t wd = ld_fr(rlo + (r0 + 1) * hs, rhi + (r0 + 1) * hs, k);
+                        const fr_t v0 = ld_fr(tlo[tt], thi[tt], k), v1 = ld_fr(tlo[tt], thi[tt], k + h);
+                        x = sel == 0 ? w0 : sel == 1 ? fr_add(w0, wd) : wd;
+                        y = sel == 0 ? fr_add(v0, beta) : sel == 1 ? fr_add(v1, beta) : fr_sub(v1, v0);
+                    } else {  // m . b
+                        const fr_t m0 = ld_fr(tlo[4], thi[4], k), b0 = ld_fr(tlo[2], thi[2], k);
+                        if (ty == 8) {
+                            x = m0;
+                            y = b0;
+                        } else {
+                            const fr_t m1 = ld_fr(tlo[4], thi[4], k + h), b1 = ld_fr(tlo[2], thi[2], k + h);
+                            x = ty == 9 ? m1 : fr_sub(m1, m0);
+                            y = ty == 9 ? b1 : fr_sub(b1, b0);
+                        }
+                    }
+                    acc = fr_add(acc, mont_mul_ol(x, y));
+                }
+                acc = fr_wave_sum(acc);
+                if (lane == 0)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) pubw[8 * ty + i] = acc.v[i];
+            }
+            nw = ZKH_LU_MSG;
+        } else {  // the block's folded entries A[0], S[0], B[0], T[0], m[0]
+            nw = 40;
+            if (wv == 0 && lane < 5) {
+                const fr_t t = ld_fr(tlo[lane], thi[lane], 0);
+#pragma unroll
+                for (int i = 0; i < 8; i++) pubw[8 * lane + i] = t.v[i];
+            }
+        }
+        __syncthreads();
+        if (wv == 0) {
+            if (lane == 0) persist_stamp(slot, seq, t_cmd);
+            persist_publish(slot, pubw, nw, seq);
+        }
+        if (m == 1) return;
+        if (wv == 0) {
+            uint4 qd;
+            const bool ok = persist_wait(P.cmd, 3, seq, P.err, P.deadline, qd);
+            if (lane < 3) {
+                sxw[3 * lane] = qd.y;
+                sxw[3 * lane + 1] = qd.z;
+                sxw[3 * lane + 2] = qd.w;
+            }
+            if (lane == 0) sok = ok;
+            t_cmd = wall_clock64();
+        }
+        __syncthreads();
+        if (!sok) return;
+        {  // fold the five tables: T[k] <- T[k] + x (T[k + m/2] - T[k])
+            fr_t x;
+#pragma unroll
+            for (int i = 0; i < 8; i++) x.v[i] = sxw[i];
+            const uint32_t h = m >> 1;
+            for (uint32_t t = threadIdx.x; t < 5 * h; t += NTP) {
+                const uint32_t i = t / h, k = t - i * h;
+                const fr_t v0 = ld_fr(tlo[i], thi[i], k), v1 = ld_fr(tlo[i], thi[i], k + h);
+                st_fr(tlo[i], thi[i], k, fr_add(v0, mont_mul_ol(x, fr_sub(v1, v0))));
+            }
+        }
+        m >>= 1;
+        __syncthreads();
+    }
+}
+hipError_t launch_lu_persist(hipStream_t s, const LuPersist& p) {
+    const uint32_t ls = p.n >> p.lgnb;  // LDS: 5 tables of ls + 5 rows of ls/2 entries, 32 B each
+    k_lu_persist<<<1u << p.lgnb, NTP, (size_t)ls * 32 * 5 + (size_t)(ls >> 1) * 5 * 32, s>>>(p);
     return hipGetLastError();
 }
 // An ordinary launch on the stream: the blocks never wait for each other, only for the

@@ -235,11 +235,12 @@ void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
 // its folded entries a[0], b[0] (ZKH_MSG_FINAL words), then exits.  Message s carries seq
 // s (1, 2, ...) both ways.  A command quad with seq ZKH_QUIT makes the job's blocks exit;
 // a block that waits longer than `deadline` ticks of the 100 MHz clock sets *err and
-// exits.  Slot words 96..99 hold the block's clock at its last message (publication, and
-// receipt of the previous command) and words 100 + 2s, 101 + 2s (s < 14) the same per
-// message s (tracing only).
+// exits.  Slot words 128..131 hold the block's clock at its last message (publication, and
+// receipt of the previous command) and words 132 + 2s, 133 + 2s (s < 14) the same per
+// message s (tracing only); words 0..127 carry messages of up to 32 quads.
 #define ZKH_QUIT 0xffffffffu
-#define ZKH_PSLOT 128  // words per block slot and per job command area
+#define ZKH_PSLOT 160  // words per block slot and per job command area
+#define ZKH_PSTAMP 128  // first clock-stamp word of a slot
 #define ZKH_MSG_PAIR 72
 #define ZKH_MSG_ONE 24
 #define ZKH_MSG_FINAL 16
@@ -275,6 +276,32 @@ struct HpPersist {
     uint32_t n, lgnb, fold, pad_;  // fold: entries g and g + n of the sources fold into g
 };
 #define ZKH_HP_MSG 32
+
+// ---- persistent logUp phase-2 rounds (the small rounds of zkh_lu_prove) ----
+// Tables A, S, B, T, m of n entries (n <= N: phase 2), each group (A, S) / (B, T, m) after
+// the fold it owes, spread cyclically over nb = 2^lgnb blocks as in the matmul loop.  Per
+// local round with m entries per block each block publishes its 11 sums over the pairs
+// (k, k + m/2), in the order of the per-round kernels' jobs 0 and 1: sum w a0 (s0 + beta),
+// w a1 (s1 + beta), w da ds, sum a0, sum a1, sum w b0 (t0 + beta), w b1 (t1 + beta),
+// w db dt, m0 b0, m1 b1, dm db (products x 2^-256; w = eq_w(g) of the global pair index;
+// 88 words, 30 quads), waits for the challenge (3 quads) and folds all five tables; with
+// m = 1 it publishes A[0], S[0], B[0], T[0], m[0] (40 words) and exits.  Slot layout,
+// ZKH_QUIT and the deadline as in ZkipPersist.
+struct LuPersist {
+    const uint32_t* lo[5];  // A, S, B, T, m: sources (limb-quad planes)
+    const uint32_t* hi[5];
+    const uint32_t* elo;  // eq factor tables (EqW)
+    const uint32_t* ehi;
+    uint32_t* out;  // pinned host, nb slots
+    uint32_t* cmd;  // pinned host, one command area
+    uint32_t* err;
+    unsigned long long deadline;
+    fr_arg vm;    // the owed folds' challenge (Montgomery form)
+    fr_arg beta;  // plain
+    uint32_t n, lgnb, fold_as, fold_btm;  // fold_*: that group's sources hold 2n entries
+};
+#define ZKH_LU_MSG 88
+hipError_t launch_lu_persist(hipStream_t s, const LuPersist& p);
 // at most 16 blocks of ZKH_PLS_MAX entries; returns the HIP status of the launch
 hipError_t launch_hp_persist(hipStream_t s, const HpPersist& p);
 

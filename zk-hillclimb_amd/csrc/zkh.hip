@@ -1684,8 +1684,9 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                     }
                     if (tracing) {  // block 0's per-message clock stamps are complete once it has exited
                         for (uint32_t m2 = 1; m2 <= msg[a] + 1 && m2 < 14; m2++) {
-                            tr_gpu[j].push_back(sl[100 + 2 * m2] - sl[99 + 2 * m2]);
-                            tr_gpu[j].push_back(m2 <= msg[a] ? sl[101 + 2 * m2] - sl[100 + 2 * m2] : 0);
+                            const uint32_t* st = sl + ZKH_PSTAMP;
+                            tr_gpu[j].push_back(st[4 + 2 * m2] - st[3 + 2 * m2]);
+                            tr_gpu[j].push_back(m2 <= msg[a] ? st[5 + 2 * m2] - st[4 + 2 * m2] : 0);
                         }
                     }
                     // the blocks' folded entries: the remaining lgnb rounds on the host
@@ -2004,6 +2005,189 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
     return ZKH_OK;
 }
 
+// logUp phase-2 state carried across rounds (zkob_lookup.cuh:143-198): the running claim,
+// alpha and alpha^2 eq accumulators, N/D, the eq point u and its device tables
+struct LuState {
+    Fr claim, alpha, alpha_sq, inv_ratio;
+    const std::vector<Fr>* u;
+    const EqState* eq;
+    uint32_t logD;
+};
+// One phase-2 round from its 11 sums (device order: w a s sums 0..2, sum a0, sum a1, w b t
+// sums 0..2, m b sums 0..2).  dev: sums from the device (products x 2^-256, eq weights with
+// the padded factors that corr(K) removes); otherwise exact host sums.  Absorbs "p0".."p3",
+// draws the challenge v, updates the state; false on a round inconsistency.
+static bool lu_phase2_round(uint8_t tr[32], LuState& L, uint32_t r, const Fr sm[11], bool dev, Fr& v,
+                            uint32_t* ev_out, uint32_t* ws_out) {
+    const uint32_t k = L.logD - r, K = k - 1;
+    const Fr ul = (*L.u)[k - 1];
+    const Fr corr = dev ? eq_corr(*L.eq, K) : kOne;
+    auto pr = [&](const Fr& x) { return dev ? fr_mul(fix1(x), corr) : x; };  // w-weighted product sums
+    auto mb = [&](const Fr& x) { return dev ? fix1(x) : x; };                 // m b product sums
+    const Fr qa0 = pr(sm[0]), qa1 = pr(sm[1]), qa2 = pr(sm[2]);
+    const Fr qb0 = pr(sm[5]), qb1 = pr(sm[6]), qb2 = pr(sm[7]);
+    const Fr coefBT = fr_mul(L.inv_ratio, L.alpha_sq);
+    const Fr Q0 = fr_add(fr_mul(L.alpha, qa0), fr_mul(coefBT, qb0));
+    const Fr Q1 = fr_add(fr_mul(L.alpha, fr_sub(fr_sub(qa1, qa0), qa2)), fr_mul(coefBT, fr_sub(fr_sub(qb1, qb0), qb2)));
+    const Fr Q2 = fr_add(fr_mul(L.alpha, qa2), fr_mul(coefBT, qb2));
+    const Fr M0 = mb(sm[8]), M1 = mb(sm[9]), M2 = mb(sm[10]);
+    const Fr Mc1 = fr_sub(fr_sub(M1, M0), M2);
+    const Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
+    Fr coef[4];
+    coef[0] = fr_sub(fr_add(fr_mul(e0, Q0), sm[3]), fr_mul(L.inv_ratio, M0));
+    coef[1] = fr_sub(fr_add(fr_add(fr_mul(e0, Q1), fr_mul(e1, Q0)), fr_sub(sm[4], sm[3])), fr_mul(L.inv_ratio, Mc1));
+    coef[2] = fr_sub(fr_add(fr_mul(e0, Q2), fr_mul(e1, Q1)), fr_mul(L.inv_ratio, M2));
+    coef[3] = fr_mul(e1, Q2);
+    const Fr e[4] = {coef[0], fr_poly_eval(coef, 3, kOne), fr_poly_eval(coef, 3, fr_u64(2)),
+                     fr_poly_eval(coef, 3, fr_u64(3))};
+    if (!fr_eq(L.claim, fr_add(e[0], e[1]))) return false;
+    static const char* lab[4] = {"p0", "p1", "p2", "p3"};
+    for (int t = 0; t < 4; t++) {
+        tr_absorb_fr(tr, lab[t], e[t]);
+        if (ev_out) fr_store(e[t], ev_out + 8 * (4 * r + t));
+    }
+    v = tr_challenge(tr);
+    if (ws_out) fr_store(v, ws_out + 8 * r);
+    L.claim = fr_poly_eval(coef, 3, v);
+    const Fr eqv = fr_eq2(ul, v);
+    L.alpha = fr_mul(L.alpha, eqv);
+    L.alpha_sq = fr_mul(L.alpha_sq, eqv);
+    return true;
+}
+// Phase-2 rounds r0 .. logD-1 in one persistent launch (see LuPersist) once the tables have
+// n <= ZKH_LU_PERSIST_MAX entries; the block-count rounds at the end run on the host with
+// the exact eq weights.  fin receives the terminals A_f, S_f, B_f, T_f, m_f.
+#define ZKH_LU_PERSIST_MAX 8192u
+static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0, uint32_t n, const DevPlanes src[5],
+                             bool fold_as, bool fold_btm, const uint32_t vm[8], const uint32_t beta_l[8],
+                             uint32_t* ev_out, uint32_t* ws_out, Fr fin[5]) {
+    const uint32_t lgnb = n > ZKH_PLS_MAX ? ceil_log2(n / ZKH_PLS_MAX) : 0, nb = 1u << lgnb;
+    const uint32_t R = ceil_log2(n) - lgnb;  // local rounds
+    int rc;
+    if ((rc = ensure_ps(c, (size_t)ZKH_PSLOT * (nb + 2)))) return rc;
+    uint32_t* ps = c->ps_host;
+    uint32_t* slots = ps + ZKH_PSLOT;
+    uint32_t* cmd = ps + (size_t)ZKH_PSLOT * (nb + 1);
+    memset(ps, 0, (size_t)ZKH_PSLOT * (nb + 2) * 4);
+    LuPersist P{};
+    for (int i = 0; i < 5; i++) {
+        P.lo[i] = src[i].lo();
+        P.hi[i] = src[i].hi();
+    }
+    P.elo = L.eq->elo_d;
+    P.ehi = L.eq->ehi_d;
+    P.out = slots;
+    P.cmd = cmd;
+    P.err = ps;
+    P.deadline = c->clock_khz * 1000 * 20;  // 20 s without a command
+    memcpy(P.vm.v, vm, 32);
+    memcpy(P.beta.v, beta_l, 32);
+    P.n = n;
+    P.lgnb = lgnb;
+    P.fold_as = fold_as;
+    P.fold_btm = fold_btm;
+    auto send = [&](uint32_t seq, const uint32_t* xm) {
+        for (uint32_t i = 0; i < 8 && xm; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
+        for (uint32_t qd = 0; qd < 3; qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
+    };
+    auto quit = [&]() {
+        send(ZKH_QUIT, nullptr);
+        (void)hipStreamSynchronize(c->stream);
+    };
+    {
+        ProfScope ps_(c, "lu_persist", (double)n * 5 * 32 * 2);
+        hipError_t e = launch_lu_persist(c->stream, P);
+        if (e != hipSuccess) {
+            quit();
+            return fail(c, ZKH_EDEV, "persistent logUp launch: %s", hipGetErrorString(e));
+        }
+    }
+    const double t_launch = now_us();
+    auto slot_fr = [&](uint32_t b, uint32_t i) {
+        uint32_t v[8];
+        for (uint32_t j = 0; j < 8; j++) v[j] = slots[(size_t)b * ZKH_PSLOT + zkh_quad_word(8 * i + j)];
+        return fr_load(v);
+    };
+    auto wait_msg = [&](uint32_t seq, uint32_t nw) -> int {
+        const uint32_t nq = zkh_quad_count(nw);
+        const double t0 = now_us();
+        for (uint64_t spins = 1;; spins++) {
+            bool all = true;
+            for (uint32_t b = 0; b < nb && all; b++)
+                for (uint32_t qd = 0; qd < nq; qd++)
+                    if (__atomic_load_n(slots + (size_t)b * ZKH_PSLOT + 4 * qd, __ATOMIC_ACQUIRE) != seq) {
+                        all = false;
+                        break;
+                    }
+            if (all) return 0;
+            __builtin_ia32_pause();
+            if ((spins & 0x3FFF) == 0) {
+                hipError_t e = hipStreamQuery(c->stream);
+                if (e != hipSuccess && e != hipErrorNotReady) {
+                    quit();
+                    return fail(c, ZKH_EDEV, "persistent logUp rounds: %s", hipGetErrorString(e));
+                }
+                if (__atomic_load_n(ps, __ATOMIC_ACQUIRE) || e == hipSuccess || now_us() - t0 > 30e6) {
+                    quit();
+                    return fail(c, ZKH_EDEV, "persistent logUp rounds stopped (%s)",
+                                ps[0] ? "a block timed out" : e == hipSuccess ? "kernel ended early" : "no progress");
+                }
+            }
+        }
+    };
+    for (uint32_t lr = 0; lr < R; lr++) {
+        if ((rc = wait_msg(lr + 1, ZKH_LU_MSG))) return rc;
+        Fr sm[11];
+        for (int t = 0; t < 11; t++) sm[t] = kZero;
+        for (uint32_t b = 0; b < nb; b++)
+            for (int t = 0; t < 11; t++) sm[t] = fr_add(sm[t], slot_fr(b, t));
+        Fr v;
+        if (!lu_phase2_round(tr, L, r0 + lr, sm, true, v, ev_out, ws_out)) {
+            quit();
+            return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r0 + lr);
+        }
+        uint32_t xm[8];
+        fr_store(fr_to_mont(v), xm);
+        send(lr + 1, xm);
+    }
+    if ((rc = wait_msg(R + 1, 40))) return rc;
+    std::vector<Fr> t[5];
+    for (int i = 0; i < 5; i++) {
+        t[i].resize(nb);
+        for (uint32_t b = 0; b < nb; b++) t[i][b] = slot_fr(b, i);
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));  // the blocks have exited
+    const Fr beta = fr_load(beta_l);
+    // the last lgnb rounds over the blocks' entries (entry b is global index b)
+    for (uint32_t r = r0 + R, m = nb; m > 1; r++, m >>= 1) {
+        const uint32_t h = m >> 1, K = L.logD - r - 1;
+        Fr sm[11];
+        for (int q = 0; q < 11; q++) sm[q] = kZero;
+        const std::vector<Fr>& A = t[0], &S = t[1], &B = t[2], &T = t[3], &M = t[4];
+        for (uint32_t i = 0; i < h; i++) {
+            Fr w = kOne;
+            for (uint32_t j = 0; j < K; j++) w = fr_mul(w, ((i >> j) & 1) ? (*L.u)[j] : fr_sub(kOne, (*L.u)[j]));
+            const Fr wa0 = fr_mul(w, A[i]), wda = fr_mul(w, fr_sub(A[i + h], A[i]));
+            const Fr wb0 = fr_mul(w, B[i]), wdb = fr_mul(w, fr_sub(B[i + h], B[i]));
+            const Fr add[11] = {fr_mul(wa0, fr_add(S[i], beta)), fr_mul(fr_add(wa0, wda), fr_add(S[i + h], beta)),
+                                fr_mul(wda, fr_sub(S[i + h], S[i])), A[i], A[i + h],
+                                fr_mul(wb0, fr_add(T[i], beta)), fr_mul(fr_add(wb0, wdb), fr_add(T[i + h], beta)),
+                                fr_mul(wdb, fr_sub(T[i + h], T[i])), fr_mul(M[i], B[i]), fr_mul(M[i + h], B[i + h]),
+                                fr_mul(fr_sub(M[i + h], M[i]), fr_sub(B[i + h], B[i]))};
+            for (int q = 0; q < 11; q++) sm[q] = fr_add(sm[q], add[q]);
+        }
+        Fr v;
+        if (!lu_phase2_round(tr, L, r, sm, false, v, ev_out, ws_out))
+            return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r);
+        for (int q = 0; q < 5; q++)
+            for (uint32_t i = 0; i < h; i++) t[q][i] = fr_add(t[q][i], fr_mul(v, fr_sub(t[q][i + h], t[q][i])));
+    }
+    for (int i = 0; i < 5; i++) fin[i] = t[i][0];
+    if (trace_on())
+        fprintf(stderr, "[zkh] lu persistent loop: n=%u, %u blocks, %u device + %u host rounds in %.1f us\n", n, nb, R,
+                lgnb, now_us() - t_launch);
+    return 0;
+}
 extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const zkh_tensor* S,
                             const zkh_tensor* T, const zkh_tensor* m, const uint32_t alpha_l[8],
                             const uint32_t beta_l[8], const uint32_t* u_l, uint32_t* ev_out,
@@ -2064,8 +2248,18 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
     Fr three = fr_u64(3);
     const bool tracing = trace_on();
     std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
+    bool persisted = false;    // the last rounds ran in lu_persist_rounds
+    Fr fin[5];
     for (uint32_t r = 0; r < logD; r++) {
         const uint32_t n = D >> r;
+        if (n <= N && n <= ZKH_LU_PERSIST_MAX && !getenv("ZKH_NO_PERSIST")) {  // phase 2: the rest in one launch
+            LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD};
+            const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
+            if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, beta_l, ev_out, ws_out, fin)))
+                return rc;
+            persisted = true;
+            break;
+        }
         if (tracing) tr_t.push_back(now_us());
         const uint32_t k = logD - r;  // remaining variables
         const uint32_t K = k - 1;     // eq variables of the pairs
@@ -2166,33 +2360,37 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
         if (tracing) tr_t.push_back(now_us());
     }
     if (tracing) {  // per round: table size, launch -> sums seen, host work (us)
-        fprintf(stderr, "[zkh] lu rounds (n: device/host us):");
-        for (uint32_t r = 0; r < logD; r++)
+        fprintf(stderr, "[zkh] lu rounds (n: device/host us)%s:", persisted ? ", then the persistent loop" : "");
+        for (uint32_t r = 0; r < tr_t.size() / 3; r++)
             fprintf(stderr, " %u:%.1f/%.1f", D >> r, tr_t[3 * r + 1] - tr_t[3 * r], tr_t[3 * r + 2] - tr_t[3 * r + 1]);
         fprintf(stderr, "\n");
     }
-    // owed folds produce the terminals (size 2 -> 1)
-    if (as_pending) {
-        launch_fold(c->stream, Tab{a_src, Aw}, 1, vm);
-        launch_fold(c->stream, Tab{s_src, Sw}, 1, vm);
-        a_src = Aw;
-        s_src = Sw;
-    }
-    if (btm_pending) {
-        launch_fold(c->stream, Tab{b_src, Bw}, 1, vm);
-        launch_fold(c->stream, Tab{t_src, Tw}, 1, vm);
-        launch_fold(c->stream, Tab{m_src, mw}, 1, vm);
-        b_src = Bw;
-        t_src = Tw;
-        m_src = mw;
-    }
-    DevPlanes fin[5] = {a_src, s_src, b_src, t_src, m_src};
     uint32_t tv[5][8];
-    for (int i = 0; i < 5; i++) {
-        HIPCHK(c, hipMemcpyAsync(tv[i], fin[i].lo(), 16, hipMemcpyDeviceToHost, c->stream));
-        HIPCHK(c, hipMemcpyAsync(tv[i] + 4, fin[i].hi(), 16, hipMemcpyDeviceToHost, c->stream));
+    if (persisted) {
+        for (int i = 0; i < 5; i++) fr_store(fin[i], tv[i]);
+    } else {
+        // owed folds produce the terminals (size 2 -> 1)
+        if (as_pending) {
+            launch_fold(c->stream, Tab{a_src, Aw}, 1, vm);
+            launch_fold(c->stream, Tab{s_src, Sw}, 1, vm);
+            a_src = Aw;
+            s_src = Sw;
+        }
+        if (btm_pending) {
+            launch_fold(c->stream, Tab{b_src, Bw}, 1, vm);
+            launch_fold(c->stream, Tab{t_src, Tw}, 1, vm);
+            launch_fold(c->stream, Tab{m_src, mw}, 1, vm);
+            b_src = Bw;
+            t_src = Tw;
+            m_src = mw;
+        }
+        const DevPlanes dfin[5] = {a_src, s_src, b_src, t_src, m_src};
+        for (int i = 0; i < 5; i++) {
+            HIPCHK(c, hipMemcpyAsync(tv[i], dfin[i].lo(), 16, hipMemcpyDeviceToHost, c->stream));
+            HIPCHK(c, hipMemcpyAsync(tv[i] + 4, dfin[i].hi(), 16, hipMemcpyDeviceToHost, c->stream));
+        }
+        HIPCHK(c, hipStreamSynchronize(c->stream));
     }
-    HIPCHK(c, hipStreamSynchronize(c->stream));
     if (term_out)
         for (int i = 0; i < 5; i++) memcpy(term_out + 8 * i, tv[i], 32);
     tr_absorb_fr(tr, "A_f", fr_load(tv[0]));
