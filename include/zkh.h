@@ -183,6 +183,15 @@ int zkh_fc_stacked_prove(zkh_ctx* ctx, const zkh_tensor* X, const zkh_tensor* W,
 int zkh_rescale(zkh_ctx* ctx, const zkh_tensor* X, uint32_t sf, zkh_tensor** q_out,
                 zkh_tensor** rem_out);
 
+/* ---------------- witness GEMM (zkob_fc.cu:211-214, zkfc.cu:44-58, fr-tensor.cu:831-878) ------ */
+/* Y = X W (+ bias) over the integers: X int32 [B][IN], W int32 [IN][OUT] (row-major, or
+ * registered with zkh_tensor_weights_i32), bias NULL or an int32/int64 tensor of OUT
+ * entries; Y_out: a new int64 tensor [B][OUT], exact.  Replaces zkFC::operator() / Y = fc(X)
+ * for integer witnesses: the reference's field product equals this integer product
+ * reduced mod r.  ZKH_EARG when the operands' magnitude bounds allow a sum beyond 63 bits. */
+int zkh_matmul_i32(zkh_ctx* ctx, const zkh_tensor* X, const zkh_tensor* W, const zkh_tensor* bias,
+                   uint32_t B, uint32_t IN, uint32_t OUT, zkh_tensor** Y_out);
+
 /* ---------------- logUp lookup (tlookup.cu, zkob_lookup.cuh, zkob_rescale.cu) ---------- */
 /* tLookupRange table (tlookup.cu:372-391): T[i] = low+i (i<len) else low+len-1, size N */
 int zkh_lu_range_table(zkh_ctx* ctx, int32_t low, uint32_t len, uint32_t N, zkh_tensor** out);

@@ -257,3 +257,13 @@ def rescale(x, sf):
         q, r = np.zeros(n, np.int64), np.zeros(n, np.int64)
         rc = lib().or_rescale_i64(_p(x), ctypes.c_uint32(n), ctypes.c_uint32(sf), _p(q), _p(r))
     return rc, q, r
+
+
+def matmul_fr(A, B, M, N, Pc, bias=None):
+    """FrTensor::matmul (+ zkFC bias): A (M*N, 8), B (N*Pc, 8) Fr arrays -> (rc, C (M*Pc, 8))."""
+    A = np.ascontiguousarray(A, dtype=np.uint32)
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    C = np.zeros((M * Pc, 8), np.uint32)
+    bp = _p(np.ascontiguousarray(bias, dtype=np.uint32)) if bias is not None else None
+    rc = lib().or_matmul_fr(_p(A), _p(B), bp, ctypes.c_uint32(M), ctypes.c_uint32(N), ctypes.c_uint32(Pc), _p(C))
+    return rc, C

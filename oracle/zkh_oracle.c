@@ -1096,3 +1096,23 @@ int or_rescale_fr(const uint32_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_
     for (uint32_t i = 0; i < n; i++) rescale1(or_scalar_to_long(x + 8 * i), sf, q + i, rem + i);
     return 0;
 }
+
+/* ------------------------------------------------------------------------------ */
+/* witness GEMM: matrixMultiplyOptimized / FrTensor::matmul (fr-tensor.cu:831-878)   */
+/* ------------------------------------------------------------------------------ */
+/* C[i][j] = mont(sum_k mmul(A[i][k], B[k][j])) (the reference accumulates Montgomery
+ * products and converts once, fr-tensor.cu:862-872), plus bias[j] when given (zkFC adds it
+ * per column, zkfc.cu:38-40, :53-56) */
+int or_matmul_fr(const uint32_t* A, const uint32_t* B, const uint32_t* bias, uint32_t M, uint32_t N, uint32_t Pc,
+                 uint32_t* C) {
+    if (!M || !N || !Pc) return 1;
+    for (uint32_t i = 0; i < M; i++)
+        for (uint32_t j = 0; j < Pc; j++) {
+            fr sum = ZERO;
+            for (uint32_t k = 0; k < N; k++) sum = add(sum, mmul(ld(A + 8 * ((size_t)i * N + k)), ld(B + 8 * ((size_t)k * Pc + j))));
+            fr c = mont(sum);
+            if (bias) c = add(c, ld(bias + 8 * j));
+            st(C + 8 * ((size_t)i * Pc + j), c);
+        }
+    return 0;
+}

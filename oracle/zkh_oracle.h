@@ -132,6 +132,11 @@ int64_t or_scalar_to_long(const uint32_t x[8]);
 int or_rescale_i64(const int64_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_t* rem);
 int or_rescale_fr(const uint32_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_t* rem);
 
+/* ---- witness GEMM (fr-tensor.cu:831-878, zkfc.cu:38-58) ----
+ * C = A B (+ bias per column) in the field: A [M][N], B [N][Pc], bias [Pc] or NULL */
+int or_matmul_fr(const uint32_t* A, const uint32_t* B, const uint32_t* bias, uint32_t M, uint32_t N, uint32_t Pc,
+                 uint32_t* C);
+
 /* Lagrange interpolation through p(0..2) / p(0..3) (vrf_common.cuh:130-140,
  * zkob_lookup.cuh:62-73) */
 void or_lagrange3(const uint32_t p[24], const uint32_t x[8], uint32_t out[8]);

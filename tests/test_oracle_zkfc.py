@@ -210,3 +210,23 @@ def test_rescale_identity(sf):
         for x, qq, rr in zip(xs, q.tolist(), r.tolist()):
             assert qq * sf + rr == x and -hsf <= rr < sf - hsf, (x, sf, qq, rr)
     assert C.rescale(np.array([5], np.int64), 0)[0] == 1
+
+
+# ------------------------------------------------------------------ witness GEMM
+@pytest.mark.parametrize("M,N,Pc", [(1, 1, 1), (3, 5, 4), (7, 2, 9)])
+def test_matmul_fr_definition(M, N, Pc):
+    """The oracle's field matmul (Montgomery accumulation, fr-tensor.cu:862-872) against
+    sum_k A[i][k] B[k][j] mod r on full-size field elements and on small signed integers
+    (where it is the integer product reduced mod r), with and without a bias."""
+    rng = random.Random(M * 100 + N * 10 + Pc)
+    for full in (True, False):
+        A = rnd(rng, M * N) if full else [rng.randrange(-2**20, 2**20) for _ in range(M * N)]
+        B = rnd(rng, N * Pc) if full else [rng.randrange(-2**20, 2**20) for _ in range(N * Pc)]
+        bias = rnd(rng, Pc)
+        for bv in (None, bias):
+            rc, got = C.matmul_fr(C.ints_to_fr(A), C.ints_to_fr(B), M, N, Pc, C.ints_to_fr(bv) if bv else None)
+            assert rc == 0
+            want = [(sum(A[i * N + k] * B[k * Pc + j] for k in range(N)) + (bv[j] if bv else 0)) % R
+                    for i in range(M) for j in range(Pc)]
+            assert [I(x) for x in got] == want
+    assert C.matmul_fr(C.ints_to_fr([1]), C.ints_to_fr([1]), 0, 1, 1)[0] == 1

@@ -69,6 +69,7 @@ def lib():
         L.zkh_fc_stacked_prove.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, vp, vp, vp,
                                            vp, vp]
         L.zkh_rescale.argtypes = [vp, vp, u32, ctypes.POINTER(vp), ctypes.POINTER(vp)]
+        L.zkh_matmul_i32.argtypes = [vp, vp, vp, vp, u32, u32, u32, ctypes.POINTER(vp)]
         L.zkh_fold.argtypes = [vp, vp, vp]
         L.zkh_axpy.argtypes = [vp, vp, vp, vp, ctypes.POINTER(vp)]
         L.zkh_hadamard.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
@@ -280,6 +281,14 @@ class Context:
         q, r = ctypes.c_void_p(), ctypes.c_void_p()
         self._chk(lib().zkh_rescale(self.h, X.h, sf, ctypes.byref(q), ctypes.byref(r)))
         return Tensor(self, q), Tensor(self, r)
+
+    def matmul_i32(self, X, W, B, IN, OUT, bias=None):
+        """Y = X W (+ bias), exact int64 (zkh_matmul_i32); X, W int32 tensors (W row-major or
+        registered weights), bias None or an int tensor of OUT entries."""
+        y = ctypes.c_void_p()
+        self._chk(lib().zkh_matmul_i32(self.h, X.h, W.h, bias.h if bias is not None else None, B, IN, OUT,
+                                       ctypes.byref(y)))
+        return Tensor(self, y)
 
     def fold(self, t, v):
         v = _frs(v, 1)

@@ -1445,6 +1445,114 @@ void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b) {
 
 
 // ------------------------------------------------------------------------------------
+// witness GEMM (zkfc.cu:44-58, fr-tensor.cu:831-878 for integer operands): Y = X W exactly
+// ------------------------------------------------------------------------------------
+typedef double zkh_d4 __attribute__((ext_vector_type(4)));
+typedef int32_t zkh_i4 __attribute__((ext_vector_type(4)));
+// four consecutive int32 of a row from column k (zero past the row's end or for a row
+// outside the matrix)
+ZDEV zkh_i4 ld_row4(const int32_t* row, uint32_t k, uint32_t len, bool ok, bool vec) {
+    if (ok && vec && k + 3 < len) return *reinterpret_cast<const zkh_i4*>(row + k);
+    zkh_i4 v = {0, 0, 0, 0};
+    if (ok)
+        for (int i = 0; i < 4; i++)
+            if (k + i < len) v[i] = row[k + i];
+    return v;
+}
+// fp64 matrix cores (v_mfma_f64_16x16x4f64: lane l holds A[l%16][l/16], B[l/16][l%16]; result
+// register r of lane l is D[l/16 + 4r][l%16]).  A wave computes a 32 x 32 tile of Y as 2 x 2
+// fragments; a block of 4 waves a 64 x 64 tile.  Per 16 values of k a lane loads four
+// consecutive k of one X row and of one WT row per fragment and feeds them to four
+// products; A and B use the same order of k, so each product sums a permutation of k.
+// Integers below 2^53 are exact doubles and every partial sum stays below 2^53 (checked by
+// the caller from the operands' magnitude bounds), so the result is exact.
+__global__ __launch_bounds__(256) void k_matmul_f64(const int32_t* __restrict__ X, const int32_t* __restrict__ WT,
+                                                    const int64_t* __restrict__ bias, uint32_t B, uint32_t IN,
+                                                    uint32_t OUT, int64_t* __restrict__ Y) {
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.y * 64 + (wv >> 1) * 32, col0 = blockIdx.x * 64 + (wv & 1) * 32;
+    const uint32_t li = lane & 15, lk = lane >> 4;
+    const bool vec = (IN & 3) == 0;
+    zkh_d4 acc[2][2];
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int g = 0; g < 2; g++) acc[f][g] = zkh_d4{0.0, 0.0, 0.0, 0.0};
+    const uint32_t r0 = row0 + li, r1 = row0 + 16 + li, c0 = col0 + li, c1 = col0 + 16 + li;
+    const int32_t* xr0 = X + (size_t)(r0 < B ? r0 : 0) * IN;
+    const int32_t* xr1 = X + (size_t)(r1 < B ? r1 : 0) * IN;
+    const int32_t* wr0 = WT + (size_t)(c0 < OUT ? c0 : 0) * IN;
+    const int32_t* wr1 = WT + (size_t)(c1 < OUT ? c1 : 0) * IN;
+    // the next 16 values of k load while this step's products issue
+    zkh_i4 nx0 = ld_row4(xr0, 4 * lk, IN, r0 < B, vec), nx1 = ld_row4(xr1, 4 * lk, IN, r1 < B, vec);
+    zkh_i4 nw0 = ld_row4(wr0, 4 * lk, IN, c0 < OUT, vec), nw1 = ld_row4(wr1, 4 * lk, IN, c1 < OUT, vec);
+    for (uint32_t k0 = 0; k0 < IN; k0 += 16) {
+        const zkh_i4 xa0 = nx0, xa1 = nx1, wb0 = nw0, wb1 = nw1;
+        if (k0 + 16 < IN) {
+            const uint32_t k = k0 + 16 + 4 * lk;
+            nx0 = ld_row4(xr0, k, IN, r0 < B, vec);
+            nx1 = ld_row4(xr1, k, IN, r1 < B, vec);
+            nw0 = ld_row4(wr0, k, IN, c0 < OUT, vec);
+            nw1 = ld_row4(wr1, k, IN, c1 < OUT, vec);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const double a0 = (double)xa0[t], a1 = (double)xa1[t], b0 = (double)wb0[t], b1 = (double)wb1[t];
+            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const uint32_t col = col0 + 16 * g + li;
+            if (col >= OUT) continue;
+            const int64_t bv = bias ? bias[col] : 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t row = row0 + 16 * f + lk + 4 * r;
+                if (row < B) Y[(size_t)row * OUT + col] = (int64_t)acc[f][g][r] + bv;
+            }
+        }
+}
+// int64 VALU (operands whose partial sums may exceed 2^53): 16 x 16 output tile per block,
+// 16-wide k tiles of X and WT through LDS
+__global__ __launch_bounds__(256) void k_matmul_i64(const int32_t* __restrict__ X, const int32_t* __restrict__ WT,
+                                                    const int64_t* __restrict__ bias, uint32_t B, uint32_t IN,
+                                                    uint32_t OUT, int64_t* __restrict__ Y) {
+    __shared__ int32_t xs[16][17], ws[16][17];
+    const uint32_t tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const uint32_t row = blockIdx.y * 16 + ty, col = blockIdx.x * 16 + tx;
+    const uint32_t wrow = blockIdx.x * 16 + ty;  // WT row loaded by this thread
+    int64_t acc = 0;
+    for (uint32_t k0 = 0; k0 < IN; k0 += 16) {
+        xs[ty][tx] = (row < B && k0 + tx < IN) ? X[(size_t)row * IN + k0 + tx] : 0;
+        ws[ty][tx] = (wrow < OUT && k0 + tx < IN) ? WT[(size_t)wrow * IN + k0 + tx] : 0;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 16; k++) acc += (int64_t)xs[ty][k] * (int64_t)ws[tx][k];
+        __syncthreads();
+    }
+    if (row < B && col < OUT) Y[(size_t)row * OUT + col] = acc + (bias ? bias[col] : 0);
+}
+void launch_matmul_i32(hipStream_t s, const int32_t* X, const int32_t* WT, const int64_t* bias, uint32_t B,
+                       uint32_t IN, uint32_t OUT, int64_t* Y, int f64) {
+    if (f64)
+        k_matmul_f64<<<dim3((OUT + 63) / 64, (B + 63) / 64), 256, 0, s>>>(X, WT, bias, B, IN, OUT, Y);
+    else
+        k_matmul_i64<<<dim3((OUT + 15) / 16, (B + 15) / 16), 256, 0, s>>>(X, WT, bias, B, IN, OUT, Y);
+}
+__global__ void k_widen_i32(const int32_t* __restrict__ in, uint32_t n, int64_t* __restrict__ out) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = in[i];
+}
+void launch_widen_i32(hipStream_t s, const int32_t* in, uint32_t n, int64_t* out) {
+    k_widen_i32<<<grid_for(n, NT, 1024), NT, 0, s>>>(in, n, out);
+}
+
+// ------------------------------------------------------------------------------------
 // persistent matmul round loop (see ZkipPersist): tables in LDS, one host round trip per
 // round, no device-side reduction or barrier across blocks
 // ------------------------------------------------------------------------------------

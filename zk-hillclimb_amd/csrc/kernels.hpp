@@ -216,6 +216,14 @@ struct ZkipBatch {  // passed by value as the kernel argument (<= 2.1 KB)
 void launch_zkip_round_multi(hipStream_t s, const ZkipBatch& b, uint32_t nblocks, Publish pub);
 void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
 
+// ---- witness GEMM: Y = X W (+ bias) over the integers, exact ----
+// X [B][IN] int32, WT [OUT][IN] int32 (W transposed, the registered-weights layout), bias
+// [OUT] int64 or null, Y [B][OUT] int64.  f64: fp64 matrix cores, exact while every partial
+// sum stays below 2^53 (the caller checks the magnitude bounds); otherwise int64 VALU.
+void launch_matmul_i32(hipStream_t s, const int32_t* X, const int32_t* WT, const int64_t* bias, uint32_t B,
+                       uint32_t IN, uint32_t OUT, int64_t* Y, int f64);
+void launch_widen_i32(hipStream_t s, const int32_t* in, uint32_t n, int64_t* out);
+
 // ---- persistent matmul round loop ----
 // Each job's tables a, b (n = 2^L entries) are spread cyclically over nb = 2^lgnb blocks
 // (block l holds entries l + nb*k in LDS), so the pairs (i, i + m/2) of every round with

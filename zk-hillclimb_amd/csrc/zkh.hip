@@ -2400,6 +2400,71 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
 }
 
 // ---------------------------------------------------------------------------------------
+// witness GEMM: Y = X W (+ bias) over the integers (zkob_fc.cu:212 Y = fc(X); zkFC::operator()
+// zkfc.cu:44-58; FrTensor::matmul fr-tensor.cu:831-878).  The reference multiplies in the
+// field; for integer operands its result is the integer product reduced mod r, which is
+// what an exact int64 product represents (zkh_tensor_from_i64 semantics), and what its
+// driver writes with save_long (zkob_fc.cu:214).
+// ---------------------------------------------------------------------------------------
+extern "C" int zkh_matmul_i32(zkh_ctx* c, const zkh_tensor* X, const zkh_tensor* W, const zkh_tensor* bias,
+                              uint32_t B, uint32_t IN, uint32_t OUT, zkh_tensor** Y_out) {
+    if (!c || !X || !W || !Y_out) return fail(c, ZKH_EARG, "null argument");
+    *Y_out = nullptr;
+    if (!B || !IN || !OUT) return fail(c, ZKH_EARG, "matmul dimensions must be positive");
+    if (X->kind != ZKH_KIND_I32 || W->kind != ZKH_KIND_I32)
+        return fail(c, ZKH_EARG, "matmul operands must be int32 tensors");
+    if ((uint64_t)X->n != (uint64_t)B * IN || (uint64_t)W->n != (uint64_t)IN * OUT)
+        return fail(c, ZKH_EARG, "matmul: incompatible dimensions");  // fr-tensor.cu:873
+    if (W->weights && (W->w_in != IN || W->w_out != OUT)) return fail(c, ZKH_EARG, "weights registered as another shape");
+    if ((uint64_t)B * OUT >= (1ull << 32)) return fail(c, ZKH_EARG, "output too large");
+    if (bias && ((bias->kind != ZKH_KIND_I32 && bias->kind != ZKH_KIND_I64) || bias->n != OUT))
+        return fail(c, ZKH_EARG, "bias must be an integer tensor of OUT entries");
+    // |partial sums| < 2^(bits X + bits W + ceil log2 IN); the bias adds at most one bit
+    const uint32_t span = X->bits + W->bits + ceil_log2(IN);
+    const uint32_t bb = bias ? bias->bits : 0;
+    if (std::max(span, bb) + 1 > 63) return fail(c, ZKH_EARG, "matmul result may exceed 63 bits");
+    const int f64 = span <= 53;
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    const int32_t* WT = (const int32_t*)W->d;
+    if (!W->weights) {  // row-major IN x OUT: transpose once into scratch
+        int32_t* wt = (int32_t*)scratch(c, SL_TMP5, (size_t)W->n * 4, &rc);
+        if (rc) return rc;
+        launch_transpose_i32(c->stream, (const int32_t*)W->d, IN, OUT, wt);
+        WT = wt;
+    }
+    const int64_t* bd = nullptr;
+    if (bias) {
+        if (bias->kind == ZKH_KIND_I32) {
+            int64_t* b64 = (int64_t*)scratch(c, SL_TMP4, (size_t)OUT * 8, &rc);
+            if (rc) return rc;
+            launch_widen_i32(c->stream, (const int32_t*)bias->d, OUT, b64);
+            bd = b64;
+        } else {
+            bd = (const int64_t*)bias->d;
+        }
+    }
+    zkh_tensor* Y;
+    if ((rc = tensor_alloc(c, ZKH_KIND_I64, B * OUT, &Y))) return rc;
+    {
+        ProfScope ps(c, f64 ? "matmul_f64" : "matmul_i64", (double)B * IN * 4 + (double)IN * OUT * 4 + (double)B * OUT * 8);
+        launch_matmul_i32(c->stream, (const int32_t*)X->d, WT, bd, B, IN, OUT, (int64_t*)Y->d, f64);
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        zkh_tensor_free(Y);
+        return fail(c, ZKH_EDEV, "matmul: %s", hipGetErrorString(e));
+    }
+    if ((rc = int_bits_i64(c, (const int64_t*)Y->d, Y->n, &Y->bits))) {
+        zkh_tensor_free(Y);
+        return rc;
+    }
+    *Y_out = Y;
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
 // Hadamard sumcheck (zkob_lookup.cuh:267-315)
 // ---------------------------------------------------------------------------------------
 static Fr lagrange4(const Fr e[4], const Fr& v) {
