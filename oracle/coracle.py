@@ -267,3 +267,41 @@ def matmul_fr(A, B, M, N, Pc, bias=None):
     bp = _p(np.ascontiguousarray(bias, dtype=np.uint32)) if bias is not None else None
     rc = lib().or_matmul_fr(_p(A), _p(B), bp, ctypes.c_uint32(M), ctypes.c_uint32(N), ctypes.c_uint32(Pc), _p(C))
     return rc, C
+
+
+# ---- G1 over Fp (zkh_g1_oracle.c): Fp as (12,) uint32, points as (36,) uint32 ----
+def fp_op(name, a, b):
+    out = np.zeros(12, dtype=np.uint32)
+    getattr(lib(), "or_fp_" + name)(_p(np.ascontiguousarray(a, np.uint32)),
+                                     _p(np.ascontiguousarray(b, np.uint32)), _p(out))
+    return out
+
+
+def g1_dbl(p):
+    out = np.zeros(36, dtype=np.uint32)
+    lib().or_g1_dbl(_p(np.ascontiguousarray(p, np.uint32)), _p(out))
+    return out
+
+
+def g1_add(a, b):
+    out = np.zeros(36, dtype=np.uint32)
+    lib().or_g1_add(_p(np.ascontiguousarray(a, np.uint32)), _p(np.ascontiguousarray(b, np.uint32)),
+                    _p(out))
+    return out
+
+
+def g1_mul(a, s):
+    out = np.zeros(36, dtype=np.uint32)
+    lib().or_g1_mul(_p(np.ascontiguousarray(a, np.uint32)), _p(np.ascontiguousarray(s, np.uint32)),
+                    _p(out))
+    return out
+
+
+def g1_commit(gens, scalars, n):
+    """gens (n, 36) uint32; scalars (m*n, 8) plain Fr -> (m, 36) points."""
+    gens = np.ascontiguousarray(gens, np.uint32).reshape(n, 36)
+    sc = np.ascontiguousarray(scalars, np.uint32).reshape(-1, 8)
+    m = sc.shape[0] // n
+    out = np.zeros((m, 36), dtype=np.uint32)
+    rc = lib().or_g1_commit(_p(gens), ctypes.c_uint32(n), _p(sc), ctypes.c_uint32(m), _p(out))
+    return rc, out

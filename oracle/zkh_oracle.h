@@ -142,6 +142,22 @@ int or_matmul_fr(const uint32_t* A, const uint32_t* B, const uint32_t* bias, uin
 void or_lagrange3(const uint32_t p[24], const uint32_t x[8], uint32_t out[8]);
 void or_lagrange4(const uint32_t p[32], const uint32_t x[8], uint32_t out[8]);
 
+/* ---- G1 over the base field Fp (zkh_g1_oracle.c) ----
+ * Fp: 12 LE uint32 limbs, canonical, Montgomery form R = 2^384.  G1 point: 36 limbs
+ * {x, y, z} Jacobian, the reference's G1Jacobian_t (g1-tensor.cuh:63). */
+void or_fp_mul(const uint32_t a[12], const uint32_t b[12], uint32_t out[12]);
+void or_fp_add(const uint32_t a[12], const uint32_t b[12], uint32_t out[12]);
+void or_fp_sub(const uint32_t a[12], const uint32_t b[12], uint32_t out[12]);
+/* dbl-2009-l (bls12-381.cu:1360-1386) and add-2007-bl (bls12-381.cu:1429-1465) */
+void or_g1_dbl(const uint32_t p[36], uint32_t out[36]);
+void or_g1_add(const uint32_t a[36], const uint32_t b[36], uint32_t out[36]);
+/* G1Jacobian_mul: double-and-add over the scalar's raw 256 bits (g1-tensor.cu:445-454) */
+void or_g1_mul(const uint32_t a[36], const uint32_t s[8], uint32_t out[36]);
+/* Commitment::commit = commit_pippenger (commitment.cu:47-103): scalars [m][n] plain Fr,
+ * gens [n] points, out [m] points */
+int or_g1_commit(const uint32_t* gens, uint32_t n, const uint32_t* scalars, uint32_t m,
+                 uint32_t* out);
+
 #ifdef __cplusplus
 }
 #endif
