@@ -34,6 +34,7 @@ extern "C" {
 
 typedef struct zkh_ctx zkh_ctx;
 typedef struct zkh_tensor zkh_tensor;
+typedef struct zkh_g1 zkh_g1; /* device array of G1 points (G1TensorJacobian) */
 
 /* element kinds held by a tensor */
 #define ZKH_KIND_FR 0  /* full field elements (device: two uint4 limb planes) */
@@ -225,6 +226,24 @@ int zkh_hp_prove(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
 int zkh_hp_prove_eq(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
                     const uint32_t* u, uint32_t k, const zkh_tensor* S, const zkh_tensor* U,
                     uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+
+/* ---------------- Pedersen commitments over BLS12-381 G1 (commitment.cu, g1-tensor.cu) -------
+ * A point is the reference's 144-byte G1Jacobian_t (g1-tensor.cuh:63): x, y, z, each 12
+ * little-endian uint32 limbs of a canonical Fp residue in Montgomery form (R = 2^384);
+ * {0, R mod p, 0} is the point at infinity.  Point arrays have their own handle type, so
+ * they cannot reach an Fr entry point. */
+/* host points -> device (G1TensorJacobian(filename) / loadbin, g1-tensor.cu:179-183) */
+int zkh_g1_from_host(zkh_ctx* ctx, const uint32_t* pts, uint32_t n, zkh_g1** out);
+/* device points -> host, n*36 uint32 (G1TensorJacobian::save, g1-tensor.cu:174-177) */
+int zkh_g1_to_host(zkh_ctx* ctx, const zkh_g1* g, uint32_t* pts);
+int zkh_g1_free(zkh_g1* g);
+uint32_t zkh_g1_size(const zkh_g1* g);
+/* Commitment::commit (commitment.cu:105-108 -> commit_pippenger :85-103): t holds m rows of
+ * n = size(gens) scalars (row-major, any tensor kind); out[row] = sum_i t[row][i] gens[i],
+ * byte-identical to the reference's bucket method (4-bit windows over the raw scalar
+ * limbs, buckets in generator order, running sum, Horner).  ZKH_EARG when size(t) is not a
+ * multiple of n (the reference's "Incompatible dimensions") or n > 65536. */
+int zkh_commit(zkh_ctx* ctx, const zkh_g1* gens, const zkh_tensor* t, zkh_g1** out);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,129 @@
+"""GPU parity for the Pedersen commitment (zkh_commit): Commitment::commit = commit_pippenger
+(commitment.cu:47-108).  Every output point is compared byte for byte with the C oracle,
+whose G1 arithmetic and schedule tests/test_oracle_g1.py pins: the Jacobian bytes are what
+the reference's transcript absorbs (zkob_fc.cu:256-258), so equal group elements are not
+enough.  Generators are G1Jacobian_mul(G, random) as Commitment::random makes them
+(commitment.cu:3-8), with Z != 1.  Covered: every tensor kind (FR, int32, int64, registered
+weights), rows that are not a multiple of the 64-row wave, zero rows and zero columns,
+repeated and opposite generators (the doubling and P + (-P) branches of the addition),
+a generator at infinity, and the dimension errors; at a matmul's real shape (X of a
+TinyLlama projection, 512 x 2048) sampled rows are checked against the oracle."""
+import numpy as np
+import pytest
+
+from oracle import coracle as C
+from oracle import pyg1 as G
+from oracle import pyref as P
+
+pytestmark = pytest.mark.gpu
+
+_BASE = G.aff_to_jac((G.GX, G.GY))
+
+
+def gens_for(seed, n):
+    rng = np.random.default_rng(seed)
+    out = np.zeros((n, 36), np.uint32)
+    for i in range(n):
+        k = int.from_bytes(rng.bytes(32), "little") % P.R
+        out[i] = C.g1_mul(_BASE, np.array(P.to_limbs(k), np.uint32))
+    return out
+
+
+def scalars_mixed(rng, count):
+    """small signed ints (the witness tables) mixed with full-width field elements."""
+    small = rng.integers(-229376, 229377, size=count)
+    full = [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(count)]
+    pick = rng.random(count) < 0.25
+    return [full[i] if pick[i] else int(small[i]) for i in range(count)]
+
+
+def check(ctx, gens, t, sc_fr, n, rows=None):
+    g = ctx.g1_from_host(gens)
+    got = ctx.commit(g, t).to_host()
+    m = sc_fr.shape[0] // n
+    assert got.shape == (m, 36)
+    rows = range(m) if rows is None else rows
+    for r in rows:
+        rc, want = C.g1_commit(gens, sc_fr[r * n:(r + 1) * n], n)
+        assert rc == 0
+        assert np.array_equal(got[r], want[0]), "row %d" % r
+
+
+@pytest.mark.parametrize("m,n", [(1, 1), (3, 5), (2, 64), (70, 16), (5, 257)])
+def test_commit_fr_vs_oracle(ctx, m, n):
+    rng = np.random.default_rng(m * 1000 + n)
+    gens = gens_for(n, n)
+    sc = C.ints_to_fr(scalars_mixed(rng, m * n))
+    check(ctx, gens, ctx.from_fr(sc), sc, n)
+
+
+@pytest.mark.parametrize("kind", ["i32", "i64", "weights"])
+def test_commit_int_kinds(ctx, kind):
+    rng = np.random.default_rng(11)
+    m, n = 9, 24
+    gens = gens_for(3, n)
+    if kind == "i64":
+        v = rng.integers(-2**40, 2**40, size=m * n).astype(np.int64)
+        t = ctx.from_i64(v)
+    else:
+        v = rng.integers(-2**17, 2**17, size=m * n).astype(np.int32)
+        t = ctx.weights_i32(v, m, n) if kind == "weights" else ctx.from_i32(v)
+    check(ctx, gens, t, C.ints_to_fr(v), n)
+
+
+def test_commit_zero_rows_and_columns(ctx):
+    rng = np.random.default_rng(12)
+    m, n = 6, 8
+    v = rng.integers(-1000, 1000, size=(m, n)).astype(np.int32)
+    v[2] = 0
+    v[:, 5] = 0
+    gens = gens_for(4, n)
+    check(ctx, gens, ctx.from_i32(v.reshape(-1)), C.ints_to_fr(v.reshape(-1)), n)
+    got = ctx.commit(ctx.g1_from_host(gens), ctx.from_i32(v.reshape(-1))).to_host()
+    assert np.array_equal(got[2], G.g1_zero())
+
+
+def test_commit_special_generators(ctx):
+    """equal generators (U1 = U2, S1 = S2: doubling), a generator and its negation
+    (P + (-P) = a Z = 0 point that later additions skip) and a generator at infinity."""
+    n = 6
+    gens = gens_for(5, n)
+    gens[1] = gens[0]
+    neg = gens[0].copy()
+    y = G.from_limbs12(neg[12:24])
+    neg[12:24] = G.limbs12((G.P - y) % G.P)
+    gens[2] = neg
+    gens[4] = G.jac_point(0, 1, 0)
+    rng = np.random.default_rng(13)
+    v = rng.integers(-50, 50, size=(40, n)).astype(np.int32)
+    v[0] = [3, 3, 3, 0, 7, 1]      # same digits for 0, 1 and 2 in window 0
+    v[1] = [-5, -5, -5, 2, 2, -5]  # negatives: every high window sees all three
+    check(ctx, gens, ctx.from_i32(v.reshape(-1)), C.ints_to_fr(v.reshape(-1)), n)
+
+
+def test_commit_dimension_errors(zkh, ctx):
+    gens = ctx.g1_from_host(gens_for(6, 4))
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.commit(gens, ctx.from_i32(np.arange(10, dtype=np.int32)))
+    assert e.value.code == zkh.EARG
+    many = ctx.g1_from_host(np.tile(G.g1_zero(), (65537, 1)))
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.commit(many, ctx.from_i32(np.zeros(65537, np.int32)))
+    assert e.value.code == zkh.EARG
+
+
+def test_commit_real_shape_sampled_rows(ctx):
+    """X of a TinyLlama projection: 512 rows of 2048 (int16-range activations)."""
+    rng = np.random.default_rng(14)
+    m, n = 512, 2048
+    gens = gens_for(7, n)
+    v = rng.integers(-2**15, 2**15, size=m * n).astype(np.int32)
+    sc = C.ints_to_fr(v[:3 * n])
+    g = ctx.g1_from_host(gens)
+    got = ctx.commit(g, ctx.from_i32(v)).to_host()
+    for r in (0, 1, 2):
+        rc, want = C.g1_commit(gens, sc[r * n:(r + 1) * n], n)
+        assert np.array_equal(got[r], want[0]), "row %d" % r
+    for r in (200, 511):
+        rc, want = C.g1_commit(gens, C.ints_to_fr(v[r * n:(r + 1) * n]), n)
+        assert np.array_equal(got[r], want[0]), "row %d" % r

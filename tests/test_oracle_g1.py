@@ -1,7 +1,7 @@
 """Pins the oracle's G1 routines (oracle/zkh_g1_oracle.c) -- Fp Montgomery arithmetic,
 doubling, addition, scalar multiplication and the Pippenger commitment -- against:
 
-- the reference's own constants (tests/golden/g1_constants.json: the generator and one in
+- the reference's own constants (tests/golden/g1/constants.json: the generator and one in
   Montgomery form, -p^-1 mod 2^32), which fix p, R and the Montgomery layout;
 - Python big-integer arithmetic (a*b*2^-384 mod p) for Fp;
 - textbook affine group arithmetic (oracle/pyg1.py) for every group element produced;
@@ -26,7 +26,7 @@ from oracle import pyg1 as G
 from oracle import pyref
 
 P = G.P
-GOLD = os.path.join(os.path.dirname(__file__), "golden", "g1_constants.json")
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "g1", "constants.json")
 
 
 def rand_point(rng, k=None, z=None):

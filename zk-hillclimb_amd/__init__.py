@@ -88,6 +88,12 @@ def lib():
         L.zkh_prof_enable.argtypes = [vp, ctypes.c_int]
         L.zkh_prof_get.argtypes = [vp, ctypes.c_char_p, vp, vp, vp]
         L.zkh_prof_names.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
+        L.zkh_g1_from_host.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
+        L.zkh_g1_to_host.argtypes = [vp, vp, vp]
+        L.zkh_g1_free.argtypes = [vp]
+        L.zkh_g1_size.restype = u32
+        L.zkh_g1_size.argtypes = [vp]
+        L.zkh_commit.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
         _lib = L
     return _lib
 
@@ -150,6 +156,30 @@ class Tensor:
     def to_fr(self):
         out = np.zeros((self.n, 8), dtype=np.uint32)
         self.ctx._chk(lib().zkh_tensor_to_fr(self.ctx.h, self.h, _p(out)))
+        return out
+
+
+class G1:
+    """Device array of G1 points (the reference's 144-byte G1Jacobian_t)."""
+
+    def __init__(self, ctx, handle):
+        self.ctx, self.h = ctx, handle
+
+    def __del__(self):
+        if getattr(self, "h", None) and lib is not None:
+            try:
+                lib().zkh_g1_free(self.h)
+            except Exception:
+                pass
+            self.h = None
+
+    @property
+    def n(self):
+        return lib().zkh_g1_size(self.h)
+
+    def to_host(self):
+        out = np.zeros((self.n, 36), dtype=np.uint32)
+        self.ctx._chk(lib().zkh_g1_to_host(self.ctx.h, self.h, _p(out)))
         return out
 
 
@@ -289,6 +319,19 @@ class Context:
         self._chk(lib().zkh_matmul_i32(self.h, X.h, W.h, bias.h if bias is not None else None, B, IN, OUT,
                                        ctypes.byref(y)))
         return Tensor(self, y)
+
+    def g1_from_host(self, pts):
+        """(n, 36) uint32 points -> device G1 array."""
+        pts = np.ascontiguousarray(pts, dtype=np.uint32).reshape(-1, 36)
+        h = ctypes.c_void_p()
+        self._chk(lib().zkh_g1_from_host(self.h, _p(pts), pts.shape[0], ctypes.byref(h)))
+        return G1(self, h)
+
+    def commit(self, gens, t):
+        """Commitment::commit: rows of n = gens.n scalars of tensor t -> one point per row."""
+        h = ctypes.c_void_p()
+        self._chk(lib().zkh_commit(self.h, gens.h, t.h, ctypes.byref(h)))
+        return G1(self, h)
 
     def fold(self, t, v):
         v = _frs(v, 1)

@@ -16,7 +16,7 @@ LIB = os.path.join(HERE, "libzkh.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-SOURCES = ["kernels.hip", "zkh.hip"]
+SOURCES = ["kernels.hip", "g1.hip", "zkh.hip"]
 
 
 def _compile(src):

@@ -1,0 +1,31 @@
+// g1.hpp -- host launchers of the G1 commitment kernels (g1.hip).
+//
+// Pedersen commitment by the bucket method, producing the reference's commit_pippenger
+// result byte for byte (commitment.cu:47-103): for every row of a [m][n] scalar table,
+// out[row] = sum_i s[row][i] * gens[i] over 4-bit windows of the scalar's raw limbs.
+// Points are 144-byte G1Jacobian_t in Montgomery form, array-of-structures.
+//
+// The reference runs one thread per (row, window) that walks all n generators adding
+// each into one of 16 buckets.  Here the work is split where the Jacobian result allows
+// it -- each bucket's additions form an independent chain (its generators in ascending
+// index order), so one lane runs one (row, window, digit) chain with its bucket in
+// registers, after a sort pass has listed each chain's generator indices:
+//   pip_sort    one wave per row, lane w = window w: per-digit counts, then the index
+//               lists (uint16, generators in ascending order) and their offsets;
+//   pip_bucket  one lane per (row, window, digit) chain; a wave holds 64 rows of one
+//               (window, digit), so its lanes' chains have similar lengths;
+//   pip_window  one lane per (row, window): the running sum over digits 15..1;
+//   pip_combine one lane per row: Horner over windows 63..0 (four doublings, one add).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define ZKH_PIP_MAX_GENS 65536u  // generator indices are stored as uint16
+
+// scalars: FR limb planes (lo: limbs 0-3, hi: limbs 4-7 as uint4 per element), m*n entries
+void launch_pip_sort(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t m, uint32_t n,
+                     uint16_t* lists, uint32_t* offs);
+void launch_pip_bucket(hipStream_t s, const uint32_t* gens, const uint16_t* lists, const uint32_t* offs,
+                       uint32_t m, uint32_t n, uint32_t* buckets);
+void launch_pip_window(hipStream_t s, const uint32_t* buckets, uint32_t m, uint32_t* partials);
+void launch_pip_combine(hipStream_t s, const uint32_t* partials, uint32_t m, uint32_t* out);

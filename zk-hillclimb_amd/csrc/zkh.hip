@@ -26,6 +26,7 @@
 
 #include "../../include/zkh.h"
 #include "fr_host.hpp"
+#include "g1.hpp"
 #include "kernels.hpp"
 #include "transcript.hpp"
 
@@ -2461,6 +2462,112 @@ extern "C" int zkh_matmul_i32(zkh_ctx* c, const zkh_tensor* X, const zkh_tensor*
         return rc;
     }
     *Y_out = Y;
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// Pedersen commitments (commitment.cu:85-108).  Points are 144-byte G1Jacobian_t, AoS.
+// ---------------------------------------------------------------------------------------
+struct zkh_g1 {
+    zkh_ctx* ctx = nullptr;
+    uint32_t n = 0;
+    void* d = nullptr;
+    std::shared_ptr<MemPool> pool;
+    size_t cls = 0;
+};
+static int g1_alloc(zkh_ctx* c, uint32_t n, zkh_g1** out) {
+    zkh_g1* g = new zkh_g1();
+    g->ctx = c;
+    g->n = n;
+    g->pool = c->mem;
+    g->cls = MemPool::size_class((size_t)(n ? n : 1) * 144);
+    g->d = c->mem->get(g->cls);
+    if (!g->d && hipMalloc(&g->d, g->cls) != hipSuccess) {
+        delete g;
+        return fail(c, ZKH_EDEV, "hipMalloc(%zu) failed", (size_t)(n ? n : 1) * 144);
+    }
+    *out = g;
+    return ZKH_OK;
+}
+extern "C" int zkh_g1_free(zkh_g1* g) {
+    if (!g) return ZKH_EARG;
+    if (g->d) g->pool->put(g->d, g->cls);
+    delete g;
+    return ZKH_OK;
+}
+extern "C" uint32_t zkh_g1_size(const zkh_g1* g) { return g ? g->n : 0; }
+extern "C" int zkh_g1_from_host(zkh_ctx* c, const uint32_t* pts, uint32_t n, zkh_g1** out) {
+    if (!c || !out || (!pts && n)) return fail(c, ZKH_EARG, "null argument");
+    *out = nullptr;
+    HIPCHK(c, hipSetDevice(c->device));
+    zkh_g1* g;
+    int rc = g1_alloc(c, n, &g);
+    if (rc) return rc;
+    if (n) {
+        hipError_t e = hipMemcpyAsync(g->d, pts, (size_t)n * 144, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            zkh_g1_free(g);
+            return fail(c, ZKH_EDEV, "point upload failed: %s", hipGetErrorString(e));
+        }
+    }
+    *out = g;
+    return ZKH_OK;
+}
+extern "C" int zkh_g1_to_host(zkh_ctx* c, const zkh_g1* g, uint32_t* pts) {
+    if (!c || !g || (!pts && g->n)) return fail(c, ZKH_EARG, "null argument");
+    if (!g->n) return ZKH_OK;
+    HIPCHK(c, hipMemcpyAsync(pts, g->d, (size_t)g->n * 144, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return ZKH_OK;
+}
+extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, zkh_g1** out) {
+    if (!c || !gens || !t || !out) return fail(c, ZKH_EARG, "null argument");
+    *out = nullptr;
+    const uint32_t n = gens->n;
+    if (!n || t->n % n) return fail(c, ZKH_EARG, "commit: incompatible dimensions");  // commitment.cu:87
+    if (n > ZKH_PIP_MAX_GENS) return fail(c, ZKH_EARG, "commit: more than %u generators", ZKH_PIP_MAX_GENS);
+    const uint32_t m = t->n / n;
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    zkh_g1* o;
+    if ((rc = g1_alloc(c, m, &o))) return rc;
+    if (m) {
+        DevPlanes p;
+        uint16_t* lists = nullptr;
+        uint32_t *offs = nullptr, *buckets = nullptr, *partials = nullptr;
+        if (!(rc = as_planes(c, t, SL_TMP0, &p))) lists = (uint16_t*)scratch(c, SL_TMP1, (size_t)m * 64 * n * 2, &rc);
+        if (!rc) offs = (uint32_t*)scratch(c, SL_TMP2, (size_t)m * 64 * 16 * 4, &rc);
+        if (!rc) buckets = (uint32_t*)scratch(c, SL_TMP3, (size_t)m * 64 * 16 * 144, &rc);
+        if (!rc) partials = (uint32_t*)scratch(c, SL_TMP6, (size_t)m * 64 * 144, &rc);
+        if (rc) {
+            zkh_g1_free(o);
+            return rc;
+        }
+        {
+            ProfScope ps(c, "pip_sort", (double)m * n * 32);
+            launch_pip_sort(c->stream, p.lo(), p.hi(), m, n, lists, offs);
+        }
+        {
+            ProfScope ps(c, "pip_bucket", (double)m * n * 32 + (double)n * 144);
+            launch_pip_bucket(c->stream, (const uint32_t*)gens->d, lists, offs, m, n, buckets);
+        }
+        {
+            ProfScope ps(c, "pip_window", (double)m * 64 * 144);
+            launch_pip_window(c->stream, buckets, m, partials);
+        }
+        {
+            ProfScope ps(c, "pip_combine", (double)m * 144);
+            launch_pip_combine(c->stream, partials, m, (uint32_t*)o->d);
+        }
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            zkh_g1_free(o);
+            return fail(c, ZKH_EDEV, "commit: %s", hipGetErrorString(e));
+        }
+    }
+    *out = o;
     return ZKH_OK;
 }
 
