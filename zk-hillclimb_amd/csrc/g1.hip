@@ -39,23 +39,36 @@ __global__ __launch_bounds__(64) void k_pip_sort(const uint32_t* __restrict__ lo
     }
 }
 
-// block b -> digit d = b % 15 + 1, window (b / 15) % 64, rows 64 (b / 960) + lane.  The
-// chain starts from the point at infinity, so its first addition returns the generator
-// itself (bls12-381.cu:1432), as the reference's bucket does.
+// block b -> row block b % RB (rows 64 (b % RB) + lane), digit (b / RB) % 15 + 1, window
+// b / (15 RB).  The row block varies fastest: blocks go round-robin to the 8 XCDs, and for
+// small-integer scalars nearly all the work of a window sits in one digit (the digit of
+// r - |v| for negative v), so any other order puts a window's long chains on one XCD.
+// The chain starts from the point at infinity, so its first addition returns the
+// generator itself (bls12-381.cu:1432), as the reference's bucket does.
 __global__ __launch_bounds__(64) void k_pip_bucket(const uint32_t* __restrict__ gens,
                                                    const uint16_t* __restrict__ lists,
                                                    const uint32_t* __restrict__ offs, uint32_t m, uint32_t n,
                                                    uint32_t* __restrict__ buckets) {
-    const uint32_t b = blockIdx.x;
-    const uint32_t d = b % 15 + 1, w = (b / 15) % 64;
-    const uint32_t row = (b / 960) * 64 + threadIdx.x;
+    const uint32_t b = blockIdx.x, RB = (m + 63) / 64;
+    const uint32_t d = (b / RB) % 15 + 1, w = b / (15 * RB);
+    const uint32_t row = (b % RB) * 64 + threadIdx.x;
     if (row >= m) return;
     const size_t rw = (size_t)row * 64 + w;
     const uint32_t* o = offs + rw * 16;
     const uint32_t beg = o[d], end = d == 15 ? o[0] : o[d + 1];
     const uint16_t* L = lists + rw * n;
     g1_t acc = g1_zero();
-    for (uint32_t k = beg; k < end; k++) acc = g1_add(acc, g1_load(gens + 36 * (size_t)L[k]));
+    if (beg < end) {
+        // the next generator (and the index after it) are loaded one addition ahead
+        g1_t nxt = g1_load(gens + 36 * (size_t)L[beg]);
+        uint32_t idx = beg + 1 < end ? L[beg + 1] : 0;
+        for (uint32_t k = beg; k < end; k++) {
+            const g1_t g = nxt;
+            if (k + 1 < end) nxt = g1_load(gens + 36 * (size_t)idx);
+            if (k + 2 < end) idx = L[k + 2];
+            acc = g1_add(acc, g);
+        }
+    }
     g1_store(buckets + (rw * 16 + d) * 36, acc);
 }
 
