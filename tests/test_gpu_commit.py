@@ -127,3 +127,24 @@ def test_commit_real_shape_sampled_rows(ctx):
     for r in (200, 511):
         rc, want = C.g1_commit(gens, C.ints_to_fr(v[r * n:(r + 1) * n]), n)
         assert np.array_equal(got[r], want[0]), "row %d" % r
+
+
+def test_commit_shared_chain_edges(ctx):
+    """values whose high digits break the shared-list pattern in some windows only: -1
+    (digits of r itself), -2 and 2 (one above / below), magnitudes at window boundaries
+    (2^k - 1, 2^k), int32 extremes; rows mixing them with ordinary small negatives, so
+    that equal fingerprints must be confirmed and near-equal lists must stay apart."""
+    rng = np.random.default_rng(15)
+    edge = [-1, -2, 2, 1, 0, -(2**20), 2**20, -(2**20) + 1, 2**31 - 1, -(2**31), 15, -15, 16, -16]
+    m, n = 66, 40
+    v = rng.integers(-300, 300, size=(m, n)).astype(np.int64)
+    for r in range(m):
+        k = rng.integers(0, 4)
+        v[r, rng.integers(0, n, size=k)] = rng.choice(edge, size=k)
+    v[0] = -1
+    v[1] = -5
+    v[2, ::2] = -1
+    v[3] = np.where(np.arange(n) % 3 == 0, -(2**20), -7)
+    v = v.astype(np.int32)
+    gens = gens_for(8, n)
+    check(ctx, gens, ctx.from_i32(v.reshape(-1)), C.ints_to_fr(v.reshape(-1)), n)

@@ -12,8 +12,12 @@
 // registers, after a sort pass has listed each chain's generator indices:
 //   pip_sort    one wave per row, lane w = window w: per-digit counts, then the index
 //               lists (uint16, generators in ascending order) and their offsets;
-//   pip_bucket  one lane per (row, window, digit) chain; a wave holds 64 rows of one
-//               (window, digit), so its lanes' chains have similar lengths;
+//   pip_alias   one wave per row: chains whose index lists are equal (the usual case for
+//               small signed scalars, where every window above the witness width holds
+//               the list of negative entries) are computed once; lists are matched by a
+//               fingerprint and confirmed entry by entry;
+//   pip_bucket  one lane per distinct nonempty (row, window, digit) chain; a wave holds 64
+//               rows of one (window, digit), so its lanes' chains have similar lengths;
 //   pip_window  one lane per (row, window): the running sum over digits 15..1;
 //   pip_combine one lane per row: Horner over windows 63..0 (four doublings, one add).
 #pragma once
@@ -25,7 +29,10 @@
 // scalars: FR limb planes (lo: limbs 0-3, hi: limbs 4-7 as uint4 per element), m*n entries
 void launch_pip_sort(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t m, uint32_t n,
                      uint16_t* lists, uint32_t* offs);
+void launch_pip_alias(hipStream_t s, const uint16_t* lists, const uint32_t* offs, uint32_t m, uint32_t n,
+                      uint16_t* alias);
 void launch_pip_bucket(hipStream_t s, const uint32_t* gens, const uint16_t* lists, const uint32_t* offs,
-                       uint32_t m, uint32_t n, uint32_t* buckets);
-void launch_pip_window(hipStream_t s, const uint32_t* buckets, uint32_t m, uint32_t* partials);
+                       const uint16_t* alias, uint32_t m, uint32_t n, uint32_t* buckets);
+void launch_pip_window(hipStream_t s, const uint32_t* buckets, const uint32_t* offs, const uint16_t* alias,
+                       uint32_t m, uint32_t* partials);
 void launch_pip_combine(hipStream_t s, const uint32_t* partials, uint32_t m, uint32_t* out);

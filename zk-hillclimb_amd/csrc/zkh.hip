@@ -2540,6 +2540,8 @@ extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, z
         if (!rc) offs = (uint32_t*)scratch(c, SL_TMP2, (size_t)m * 64 * 16 * 4, &rc);
         if (!rc) buckets = (uint32_t*)scratch(c, SL_TMP3, (size_t)m * 64 * 16 * 144, &rc);
         if (!rc) partials = (uint32_t*)scratch(c, SL_TMP6, (size_t)m * 64 * 144, &rc);
+        uint16_t* alias = nullptr;
+        if (!rc) alias = (uint16_t*)scratch(c, SL_TMP4, (size_t)m * 64 * 16 * 2, &rc);
         if (rc) {
             zkh_g1_free(o);
             return rc;
@@ -2549,12 +2551,16 @@ extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, z
             launch_pip_sort(c->stream, p.lo(), p.hi(), m, n, lists, offs);
         }
         {
+            ProfScope ps(c, "pip_alias", (double)m * 64 * 64);
+            launch_pip_alias(c->stream, lists, offs, m, n, alias);
+        }
+        {
             ProfScope ps(c, "pip_bucket", (double)m * n * 32 + (double)n * 144);
-            launch_pip_bucket(c->stream, (const uint32_t*)gens->d, lists, offs, m, n, buckets);
+            launch_pip_bucket(c->stream, (const uint32_t*)gens->d, lists, offs, alias, m, n, buckets);
         }
         {
             ProfScope ps(c, "pip_window", (double)m * 64 * 144);
-            launch_pip_window(c->stream, buckets, m, partials);
+            launch_pip_window(c->stream, buckets, offs, alias, m, partials);
         }
         {
             ProfScope ps(c, "pip_combine", (double)m * 144);
