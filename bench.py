@@ -16,6 +16,9 @@ TinyLlama-1.1B".
   Excluded, as in the reference's accounting: Pedersen commitments (their transcript
   absorbs use fixed synthetic blobs), IPA openings, the witness GEMM Y = X*W (computed
   in setup), process init.
+- commitments: the layer's com_X, com_W, com_Y (zkob_fc.cu:215-230) with zkh_commit,
+  byte-identical to the reference's commit_pippenger, reported beside the metric (not part
+  of it) with their own CPU baseline (the C oracle on one row each of X, W, Y).
 - Inputs are seeded synthetic tensors (fp8-e4m3 weights as scaled ints, Gaussian int16
   activations), resident in HBM before the timed region.
 - The throughput steps carry no timing events (stamping them costs the host ~20 us per
@@ -238,6 +241,99 @@ def witness_gemm(zkh, jobs, reps=5):
             "scope": "Y = X W for the 7 matmuls (exact int64), not part of prove_s_per_layer"}
 
 
+def commit_setup(zkh, jobs, seed=0x5EED0004):
+    """Commitment keys and padded tensors for the layer's matmuls (zkob_fc.cu:215-230):
+    gen_in (IN_pad points) and gen_out (OUT_pad points) as Commitment::random makes them
+    (the generator times random field elements, commitment.cu:3-8, here zkh_g1_mul), and
+    X, W, Y padded per dimension to powers of two."""
+    rng = np.random.default_rng(seed)
+    G = zkh.g1_generator()[None, :]
+    for j in jobs:
+        c = j.ctx
+        base = c.g1_from_host(G)
+
+        def rand_fr(n):
+            a = rng.integers(0, 2**32, size=(n, 8), dtype=np.uint64).astype(np.uint32)
+            a[:, 7] %= 0x73EDA753  # below r's top limb: canonical
+            return c.from_fr(a)
+
+        j.gen_in = c.g1_mul(base, rand_fr(pow2(j.IN)))
+        j.gen_out = c.g1_mul(base, rand_fr(pow2(j.OUT)))
+        j.Xp = c.pad(j.X, (j.B, j.IN))
+        j.Wp = c.pad(j.W, (j.IN, j.OUT))
+        j.Yp = c.pad(j.Y, (j.B, j.OUT))
+        j.commit_scalars = j.Xp.n + j.Wp.n + j.Yp.n
+
+
+def commit_job(j):
+    """com_X, com_W, com_Y of one matmul (zkob_fc.cu:219-230), as digests of the points."""
+    c = j.ctx
+    outs = [c.commit(j.gen_in, j.Xp), c.commit(j.gen_out, j.Wp), c.commit(j.gen_out, j.Yp)]
+    return b"".join(hashlib.sha256(o.to_host().tobytes()).digest() for o in outs)
+
+
+PIP_KERNELS = ("pip_sort", "pip_alias", "pip_bucket", "pip_window", "pip_combine")
+
+
+def commitments(zkh, jobs, pool, reps=3, cpu=True):
+    """Pedersen commitments of the layer's 7 matmuls: com_X, com_W, com_Y each (the reference
+    recomputes com_W on every proof, zkob_fc.cu:220), byte-identical to commit_pippenger.
+    Timed with the 7 matmuls' commitments issued concurrently (one context and stream per
+    matmul), and sequentially; kernel times from the launch-stamped events."""
+    import ctypes
+    commit_setup(zkh, jobs)
+    ref = [commit_job(j) for j in jobs]
+    for j in jobs:
+        zkh.lib().zkh_prof_enable(j.ctx.h, 1)
+    t = time.perf_counter()
+    for j in jobs:
+        assert commit_job(j) == ref[jobs.index(j)]
+    seq = time.perf_counter() - t
+    kern = {}
+    for j in jobs:
+        for name in PIP_KERNELS:
+            ms, la, by = ctypes.c_double(), ctypes.c_uint64(), ctypes.c_double()
+            zkh.lib().zkh_prof_get(j.ctx.h, name.encode(), ctypes.byref(ms), ctypes.byref(la), ctypes.byref(by))
+            kern[name] = kern.get(name, 0.0) + ms.value
+        zkh.lib().zkh_prof_enable(j.ctx.h, 0)
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        futs = [pool.submit(commit_job, j) for j in jobs]
+        assert [f.result() for f in futs] == ref, "non-deterministic commitments"
+        times.append(time.perf_counter() - t)
+    scalars = sum(j.commit_scalars for j in jobs)
+    best = min(times)
+    res = {"commit_s_per_layer": round(best, 4), "commit_s_per_layer_sequential": round(seq, 4),
+           "scalars_committed": scalars, "scalars_per_s": round(scalars / best),
+           "kernel_ms_sequential": {k: round(v, 3) for k, v in kern.items()},
+           "scope": "com_X, com_W, com_Y of Q,K,V,O,gate,up,down (padded tensors, zkob_fc.cu:215-230), "
+                    "7 matmuls concurrent on 7 streams; byte-identical to commit_pippenger"}
+    if cpu:
+        res["cpu_baseline"] = commit_cpu_baseline(jobs[0])
+    return res
+
+
+def commit_cpu_baseline(j, rows=1):
+    """The C oracle's commit_pippenger (scalar, one thread) on one row each of the Q
+    projection's X, W and Y (the same generators and padded values as the GPU run)."""
+    sys.path.insert(0, ROOT)
+    from oracle import coracle
+    total, secs = 0, 0.0
+    for t, g in ((j.Xp, j.gen_in), (j.Wp, j.gen_out), (j.Yp, j.gen_out)):
+        gens = g.to_host()
+        n = g.n
+        sc = t.to_fr()[: rows * n]
+        t0 = time.perf_counter()
+        rc, _ = coracle.g1_commit(gens, sc, n)
+        secs += time.perf_counter() - t0
+        assert rc == 0
+        total += rows * n
+    return {"value": round(total / secs, 1), "unit": "scalars committed/s", "cores": 1, "kind": "port",
+            "sample": "C oracle commit_pippenger on %d row(s) each of the Q projection's padded X, W, Y "
+                      "(%d scalars, %.1f s, 1 thread)" % (rows, total, secs)}
+
+
 def cpu_baseline(jobs, budget_names=("q", "k", "v", "o")):
     """The C oracle (reference algorithmic schedule, scalar, one thread) on a bounded
     sample: the four attention projections of the same layer."""
@@ -268,11 +364,12 @@ def main():
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
+    ap.add_argument("--no-commit", action="store_true", help="skip the Pedersen commitments")
     ap.add_argument("--no-prof", action="store_true", help="skip the profiled pass (no kernel times)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--segment", choices=["glu", "rope"], default=None,
+    ap.add_argument("--segment", choices=["glu", "rope", "commit"], default=None,
                     help="only run one non-matmul segment repeatedly (for profiling), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -290,6 +387,12 @@ def main():
         del src, dst
     rng = synth.rng_for(4)
     L = LAYER
+    if args.segment == "commit":
+        jobs = [MatmulJob(zkh, synth, rng, n, L["B"], i, o) for n, i, o in MATMULS]
+        pool = concurrent.futures.ThreadPoolExecutor(max_workers=16)
+        print(json.dumps({"segment": "commit", **commitments(zkh, jobs, pool, reps=args.steps, cpu=False)}))
+        pool.shutdown()
+        return
     if args.segment:
         job = GluJob(zkh, synth, rng, L["B"], L["ffn"]) if args.segment == "glu" else \
             RopeJob(zkh, rng, "q", L["B"], L["d"])
@@ -429,6 +532,9 @@ def main():
         print("layer %.3f s" % layer["prove_s_per_layer"], file=sys.stderr, flush=True)
 
     wg = None if args.no_layer else witness_gemm(zkh, jobs)
+    com = None if args.no_commit else commitments(zkh, jobs, pool, cpu=not args.no_cpu)
+    if com:
+        print("commitments %.3f s per layer" % com["commit_s_per_layer"], file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(jobs)
     res = {
         "metric": "Fr elements bound/sec in matmul sumcheck; prove s/layer at TinyLlama-1.1B",
@@ -445,6 +551,8 @@ def main():
         res["layer"] = layer
     if wg:
         res["witness_gemm"] = wg
+    if com:
+        res["commitments"] = com
     print(json.dumps(res))
     pool.shutdown()
 

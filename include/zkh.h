@@ -238,6 +238,13 @@ int zkh_g1_from_host(zkh_ctx* ctx, const uint32_t* pts, uint32_t n, zkh_g1** out
 int zkh_g1_to_host(zkh_ctx* ctx, const zkh_g1* g, uint32_t* pts);
 int zkh_g1_free(zkh_g1* g);
 uint32_t zkh_g1_size(const zkh_g1* g);
+/* the reference's G1Jacobian_generator (g1-tensor.cuh:63): 36 uint32 */
+void zkh_g1_generator(uint32_t* out);
+/* out[i] = base[i % size(base)] * t[i], G1Jacobian_mul (g1-tensor.cu:445-454) elementwise
+ * with a broadcast base (G1_jacobian_elementwise_mul_broadcast, :463-468): double-and-add
+ * over the scalar's raw bits.  With the generator as base and random scalars this is
+ * Commitment::random (commitment.cu:3-8), the public generators of a commitment key. */
+int zkh_g1_mul(zkh_ctx* ctx, const zkh_g1* base, const zkh_tensor* t, zkh_g1** out);
 /* Commitment::commit (commitment.cu:105-108 -> commit_pippenger :85-103): t holds m rows of
  * n = size(gens) scalars (row-major, any tensor kind); out[row] = sum_i t[row][i] gens[i],
  * byte-identical to the reference's bucket method (4-bit windows over the raw scalar

@@ -148,3 +148,29 @@ def test_commit_shared_chain_edges(ctx):
     v = v.astype(np.int32)
     gens = gens_for(8, n)
     check(ctx, gens, ctx.from_i32(v.reshape(-1)), C.ints_to_fr(v.reshape(-1)), n)
+
+
+def test_g1_generator_matches_reference_constant(zkh):
+    assert np.array_equal(zkh.g1_generator(), G.aff_to_jac((G.GX, G.GY)))
+
+
+def test_g1_mul_vs_oracle(zkh, ctx):
+    """G1Jacobian_mul elementwise with a broadcast base (Commitment::random's step)."""
+    rng = np.random.default_rng(16)
+    n = 70
+    ks = [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(n - 6)] + [0, 1, 2, P.R - 1, 2**255 - 1, 2**128]
+    sc = np.zeros((n, 8), np.uint32)
+    for i, k in enumerate(ks):
+        sc[i] = P.to_limbs(k)   # raw bits, as G1Jacobian_mul reads them (2^255 - 1 is not reduced)
+    bases = gens_for(9, 3)
+    # from_fr takes canonical values only
+    canon = [i for i, k in enumerate(ks) if k < P.R]
+    g = ctx.g1_mul(ctx.g1_from_host(bases), ctx.from_fr(sc[canon])).to_host()
+    for j, i in enumerate(canon):
+        want = C.g1_mul(bases[j % 3], sc[i])
+        assert np.array_equal(g[j], want), i
+    one = ctx.g1_mul(ctx.g1_from_host(zkh.g1_generator()[None, :]), ctx.from_i32(np.array([3, -1, 0], np.int32))).to_host()
+    base = zkh.g1_generator()
+    assert np.array_equal(one[0], C.g1_mul(base, np.array(P.to_limbs(3), np.uint32)))
+    assert np.array_equal(one[1], C.g1_mul(base, np.array(P.to_limbs(P.R - 1), np.uint32)))
+    assert np.array_equal(one[2], G.g1_zero())

@@ -94,6 +94,9 @@ def lib():
         L.zkh_g1_size.restype = u32
         L.zkh_g1_size.argtypes = [vp]
         L.zkh_commit.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
+        L.zkh_g1_generator.restype = None
+        L.zkh_g1_generator.argtypes = [vp]
+        L.zkh_g1_mul.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
         _lib = L
     return _lib
 
@@ -157,6 +160,13 @@ class Tensor:
         out = np.zeros((self.n, 8), dtype=np.uint32)
         self.ctx._chk(lib().zkh_tensor_to_fr(self.ctx.h, self.h, _p(out)))
         return out
+
+
+def g1_generator():
+    """the standard G1 generator as the reference stores it (36 uint32, Montgomery form)."""
+    out = np.zeros(36, dtype=np.uint32)
+    lib().zkh_g1_generator(_p(out))
+    return out
 
 
 class G1:
@@ -325,6 +335,12 @@ class Context:
         pts = np.ascontiguousarray(pts, dtype=np.uint32).reshape(-1, 36)
         h = ctypes.c_void_p()
         self._chk(lib().zkh_g1_from_host(self.h, _p(pts), pts.shape[0], ctypes.byref(h)))
+        return G1(self, h)
+
+    def g1_mul(self, base, t):
+        """out[i] = base[i % base.n] * t[i] (G1Jacobian_mul)."""
+        h = ctypes.c_void_p()
+        self._chk(lib().zkh_g1_mul(self.h, base.h, t.h, ctypes.byref(h)))
         return G1(self, h)
 
     def commit(self, gens, t):

@@ -52,85 +52,128 @@ __device__ __forceinline__ uint64_t pip_mix(uint64_t z) {
 // (window, digit) chains of a row with the same list produce the same bytes.  For small
 // signed scalars this is the common case: a negative v is r - |v|, whose digits above
 // |v|'s top window are those of r - 2^k for every such element, so the windows above
-// the witness width all hold the list of negative entries under one digit each.  Lane w
-// fingerprints its 15 lists (count, sum of mixed indices), then looks for the first
-// earlier window with an equal fingerprint and confirms the match entry by entry; alias
-// holds the (window * 16 + digit) whose bucket stands in, itself when there is none.
+// the witness width all hold the list of negative entries under one digit each.  One
+// wave per row works through the row's chains together (coalesced list reads): it
+// fingerprints each nonempty list (count, sum of mixed indices), then, in window order,
+// looks for the first earlier chain with an equal fingerprint and confirms the match
+// entry by entry.  alias holds the (window * 16 + digit) whose bucket stands in, itself
+// when there is none; representatives are always first occurrences.
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
 __global__ __launch_bounds__(64) void k_pip_alias(const uint16_t* __restrict__ lists,
                                                   const uint32_t* __restrict__ offs, uint32_t n,
                                                   uint16_t* __restrict__ alias) {
-    __shared__ uint32_t beg_s[64 * 16], cnt_s[64 * 16];
-    __shared__ uint64_t fp_s[64 * 16];
-    const uint32_t row = blockIdx.x, w = threadIdx.x;
-    const size_t rw = (size_t)row * 64 + w;
-    const uint32_t* o = offs + rw * 16;
-    const uint16_t* L = lists + rw * n;
-    for (int d = 1; d < 16; d++) {
-        const uint32_t b = o[d], e = d == 15 ? o[0] : o[d + 1];
-        uint64_t h = 0;
-        for (uint32_t k = b; k < e; k++) h += pip_mix(L[k]);
-        beg_s[w * 16 + d] = b;
-        cnt_s[w * 16 + d] = e - b;
-        fp_s[w * 16 + d] = h;
+    __shared__ uint32_t beg_s[1024], cnt_s[1024];
+    __shared__ uint64_t fp_s[1024];
+    __shared__ uint16_t tgt_s[1024];
+    const uint32_t row = blockIdx.x, lane = threadIdx.x;
+    const uint16_t* Lrow = lists + (size_t)row * 64 * n;
+    {
+        const uint32_t* o = offs + ((size_t)row * 64 + lane) * 16;
+        for (int d = 1; d < 16; d++) {
+            const uint32_t b = o[d], e = d == 15 ? o[0] : o[d + 1];
+            beg_s[lane * 16 + d] = b;
+            cnt_s[lane * 16 + d] = e - b;
+        }
     }
     __syncthreads();
-    const uint16_t* Lrow = lists + (size_t)row * 64 * n;
-    for (int d = 1; d < 16; d++) {
-        const uint32_t c = cnt_s[w * 16 + d], b = beg_s[w * 16 + d];
-        const uint64_t h = fp_s[w * 16 + d];
-        uint32_t target = w * 16 + d;
-        for (uint32_t w2 = 0; c && w2 < w && target == w * 16 + d; w2++) {
-            for (int d2 = 1; d2 < 16; d2++) {
-                if (cnt_s[w2 * 16 + d2] != c || fp_s[w2 * 16 + d2] != h) continue;
-                const uint16_t* A = L + b;
-                const uint16_t* B = Lrow + (size_t)w2 * n + beg_s[w2 * 16 + d2];
-                uint32_t k = 0;
-                while (k < c && A[k] == B[k]) k++;
-                if (k == c) {
-                    target = w2 * 16 + d2;
-                    break;
+    for (uint32_t c = 0; c < 1024; c++) {
+        if ((c & 15) == 0) continue;
+        const uint32_t cnt = cnt_s[c];
+        uint64_t h = 0;
+        if (cnt) {
+            const uint16_t* L = Lrow + (size_t)(c >> 4) * n + beg_s[c];
+            for (uint32_t k = lane; k < cnt; k += 64) h += pip_mix(L[k]);
+            h = wave_sum_u64(h);
+        }
+        if (lane == 0) fp_s[c] = h;
+    }
+    __syncthreads();
+    for (uint32_t c = 0; c < 1024; c++) {
+        if ((c & 15) == 0) continue;
+        const uint32_t cnt = cnt_s[c];
+        uint32_t target = c;
+        if (cnt && c >= 16) {
+            const uint64_t h = fp_s[c];
+            const uint16_t* A = Lrow + (size_t)(c >> 4) * n + beg_s[c];
+            // candidates in earlier windows, 64 at a time, lowest first
+            for (uint32_t base = 0; base < (c & ~15u) && target == c; base += 64) {
+                const uint32_t cc = base + lane;
+                const bool hit = cc < (c & ~15u) && (cc & 15) && cnt_s[cc] == cnt && fp_s[cc] == h;
+                uint64_t hits = __ballot(hit);
+                while (hits && target == c) {
+                    const uint32_t cand = base + __builtin_ctzll(hits);
+                    hits &= hits - 1;
+                    const uint16_t* B = Lrow + (size_t)(cand >> 4) * n + beg_s[cand];
+                    bool diff = false;
+                    for (uint32_t k = lane; k < cnt; k += 64) diff |= A[k] != B[k];
+                    if (!__any(diff)) target = cand;
                 }
             }
         }
-        alias[rw * 16 + d] = (uint16_t)target;
+        if (lane == 0) tgt_s[c] = (uint16_t)target;
     }
+    __syncthreads();
+    uint16_t* out = alias + (size_t)row * 1024;
+    for (uint32_t c = lane; c < 1024; c += 64) out[c] = tgt_s[c];
 }
 
-// block b -> row block b % RB (rows 64 (b % RB) + lane), digit (b / RB) % 15 + 1, window
-// b / (15 RB).  The row block varies fastest: blocks go round-robin to the 8 XCDs, and for
-// small-integer scalars nearly all the work of a window sits in one digit (the digit of
-// r - |v| for negative v), so any other order puts a window's long chains on one XCD.
-// The chain starts from the point at infinity, so its first addition returns the
-// generator itself (bls12-381.cu:1432), as the reference's bucket does.
+// Bucket chains, two ways in one launch.  A long chain (at least long_min additions: with
+// small signed scalars, the shared list of negative entries) is latency-bound, so one
+// quad (4 lanes) shares each addition (g1_add_quad: 5 multiply rounds instead of 16); a
+// short chain runs on one lane (g1_add), which costs fewer instructions in total.  Blocks
+// [0, nq) are quad blocks: a wave holds 16 rows of one (window, digit); the rest are lane
+// blocks of 64 rows.  In both, block b -> row block b % RB, digit (b / RB) % 15 + 1,
+// window b / (15 RB): the row block varies fastest because blocks go round-robin to the 8
+// XCDs and nearly all of a window's work sits in one digit, so any other order puts a
+// window's long chains on one XCD.  A chain starts from the point at infinity, so its
+// first addition returns the generator itself (bls12-381.cu:1432), as the reference's
+// bucket does; the next generator is loaded one addition ahead.
+template <bool QUAD>
+__device__ __forceinline__ void pip_chain(const uint32_t* __restrict__ gens, const uint16_t* __restrict__ L,
+                                          uint32_t beg, uint32_t end, int q, uint32_t* out) {
+    g1_t acc = g1_load(gens + 36 * (size_t)L[beg]);
+    g1_t nxt = acc;
+    uint32_t idx = beg + 1 < end ? L[beg + 1] : 0;
+    if (beg + 1 < end) nxt = g1_load(gens + 36 * (size_t)idx);
+    if (beg + 2 < end) idx = L[beg + 2];
+    for (uint32_t k = beg + 1; k < end; k++) {
+        const g1_t g = nxt;
+        if (k + 1 < end) nxt = g1_load(gens + 36 * (size_t)idx);
+        if (k + 2 < end) idx = L[k + 2];
+        acc = QUAD ? g1_add_quad(acc, g, q) : g1_add(acc, g);
+    }
+    if (!QUAD || q == 0) g1_store(out, acc);
+}
 __global__ __launch_bounds__(64) void k_pip_bucket(const uint32_t* __restrict__ gens,
                                                    const uint16_t* __restrict__ lists,
                                                    const uint32_t* __restrict__ offs,
                                                    const uint16_t* __restrict__ alias, uint32_t m, uint32_t n,
+                                                   uint32_t long_min, uint32_t nq,
                                                    uint32_t* __restrict__ buckets) {
-    const uint32_t b = blockIdx.x, RB = (m + 63) / 64;
+    const bool quad = blockIdx.x < nq;
+    const uint32_t b = quad ? blockIdx.x : blockIdx.x - nq;
+    const uint32_t RB = quad ? (m + 15) / 16 : (m + 63) / 64;
     const uint32_t d = (b / RB) % 15 + 1, w = b / (15 * RB);
-    const uint32_t row = (b % RB) * 64 + threadIdx.x;
+    const uint32_t row = (b % RB) * (quad ? 16 : 64) + (quad ? threadIdx.x / 4 : threadIdx.x);
     if (row >= m) return;
     const size_t rw = (size_t)row * 64 + w;
     const uint32_t* o = offs + rw * 16;
     const uint32_t beg = o[d], end = d == 15 ? o[0] : o[d + 1];
     // empty chains are the point at infinity and aliased ones are another chain's bucket:
     // k_pip_window reads neither from here
-    if (beg == end || alias[rw * 16 + d] != w * 16 + d) return;
+    if (beg == end || alias[rw * 16 + d] != w * 16 + d || (end - beg >= long_min) != quad) return;
     const uint16_t* L = lists + rw * n;
-    g1_t acc = g1_zero();
-    {
-        // the next generator (and the index after it) are loaded one addition ahead
-        g1_t nxt = g1_load(gens + 36 * (size_t)L[beg]);
-        uint32_t idx = beg + 1 < end ? L[beg + 1] : 0;
-        for (uint32_t k = beg; k < end; k++) {
-            const g1_t g = nxt;
-            if (k + 1 < end) nxt = g1_load(gens + 36 * (size_t)idx);
-            if (k + 2 < end) idx = L[k + 2];
-            acc = g1_add(acc, g);
-        }
+    uint32_t* out = buckets + (rw * 16 + d) * 36;
+    if (quad) {
+        // the long chains set the kernel's length: their waves issue first on a shared SIMD
+        __builtin_amdgcn_s_setprio(3);
+        pip_chain<true>(gens, L, beg, end, threadIdx.x & 3, out);
     }
-    g1_store(buckets + (rw * 16 + d) * 36, acc);
+    else pip_chain<false>(gens, L, beg, end, 0, out);
 }
 
 // sum_b b * bucket[b] by the running sum acc += bucket[b]; run += acc, b = 15..1
@@ -166,6 +209,32 @@ __global__ __launch_bounds__(64) void k_pip_combine(const uint32_t* __restrict__
     g1_store(out + (size_t)row * 36, acc);
 }
 
+// G1Jacobian_mul (g1-tensor.cu:445-454), elementwise with a broadcast base
+// (G1_jacobian_elementwise_mul_broadcast, :463-468): double-and-add over the scalar's 256
+// raw bits, low bit first; out[i] = base[i % nb] * s[i]
+__global__ __launch_bounds__(64) void k_g1_mul(const uint32_t* __restrict__ base, uint32_t nb,
+                                               const uint32_t* __restrict__ lo, const uint32_t* __restrict__ hi,
+                                               uint32_t n, uint32_t* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 64 + threadIdx.x;
+    if (i >= n) return;
+    g1_t a = g1_load(base + 36 * (size_t)(i % nb));
+    g1_t acc = g1_zero();
+    const uint4 s0 = ((const uint4*)lo)[i], s1 = ((const uint4*)hi)[i];
+    const uint32_t limb[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    for (int l = 0; l < 8; l++) {
+        const uint32_t x = limb[l];
+        for (int bit = 0; bit < 32; bit++) {
+            if ((x >> bit) & 1u) acc = g1_add(acc, a);
+            a = g1_dbl(a);
+        }
+    }
+    g1_store(out + 36 * (size_t)i, acc);
+}
+
+void launch_g1_mul(hipStream_t s, const uint32_t* base, uint32_t nb, const uint32_t* lo, const uint32_t* hi,
+                   uint32_t n, uint32_t* out) {
+    hipLaunchKernelGGL(k_g1_mul, dim3((n + 63) / 64), dim3(64), 0, s, base, nb, lo, hi, n, out);
+}
 void launch_pip_sort(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t m, uint32_t n,
                      uint16_t* lists, uint32_t* offs) {
     hipLaunchKernelGGL(k_pip_sort, dim3(m), dim3(64), 0, s, lo, hi, n, lists, offs);
@@ -176,8 +245,12 @@ void launch_pip_alias(hipStream_t s, const uint16_t* lists, const uint32_t* offs
 }
 void launch_pip_bucket(hipStream_t s, const uint32_t* gens, const uint16_t* lists, const uint32_t* offs,
                        const uint16_t* alias, uint32_t m, uint32_t n, uint32_t* buckets) {
-    const uint32_t rb = (m + 63) / 64;
-    hipLaunchKernelGGL(k_pip_bucket, dim3(rb * 960), dim3(64), 0, s, gens, lists, offs, alias, m, n, buckets);
+    // a chain is long from n/8 additions on: twice the mean of a window whose digits are
+    // spread evenly, so evenly spread scalars never take the quad path
+    const uint32_t long_min = n / 8 > 32 ? n / 8 : 32;
+    const uint32_t nq = (m + 15) / 16 * 960, ns = (m + 63) / 64 * 960;
+    hipLaunchKernelGGL(k_pip_bucket, dim3(nq + ns), dim3(64), 0, s, gens, lists, offs, alias, m, n, long_min, nq,
+                       buckets);
 }
 void launch_pip_window(hipStream_t s, const uint32_t* buckets, const uint32_t* offs, const uint16_t* alias,
                        uint32_t m, uint32_t* partials) {

@@ -16,8 +16,9 @@
 //               small signed scalars, where every window above the witness width holds
 //               the list of negative entries) are computed once; lists are matched by a
 //               fingerprint and confirmed entry by entry;
-//   pip_bucket  one lane per distinct nonempty (row, window, digit) chain; a wave holds 64
-//               rows of one (window, digit), so its lanes' chains have similar lengths;
+//   pip_bucket  each distinct nonempty (row, window, digit) chain once: a long chain on a
+//               quad of lanes that share every point addition (latency-bound), a short
+//               one on one lane (throughput-bound);
 //   pip_window  one lane per (row, window): the running sum over digits 15..1;
 //   pip_combine one lane per row: Horner over windows 63..0 (four doublings, one add).
 #pragma once
@@ -36,3 +37,6 @@ void launch_pip_bucket(hipStream_t s, const uint32_t* gens, const uint16_t* list
 void launch_pip_window(hipStream_t s, const uint32_t* buckets, const uint32_t* offs, const uint16_t* alias,
                        uint32_t m, uint32_t* partials);
 void launch_pip_combine(hipStream_t s, const uint32_t* partials, uint32_t m, uint32_t* out);
+// out[i] = base[i % nb] * s[i] (G1Jacobian_mul, raw scalar bits)
+void launch_g1_mul(hipStream_t s, const uint32_t* base, uint32_t nb, const uint32_t* lo, const uint32_t* hi,
+                   uint32_t n, uint32_t* out);

@@ -2521,6 +2521,43 @@ extern "C" int zkh_g1_to_host(zkh_ctx* c, const zkh_g1* g, uint32_t* pts) {
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return ZKH_OK;
 }
+// the reference's G1Jacobian_generator {G1_generator_x_mont, G1_generator_y_mont, G1_ONE}
+// (g1-tensor.cuh:26-63): the standard BLS12-381 G1 generator in Montgomery form, Z = R mod p
+extern "C" void zkh_g1_generator(uint32_t* out) {
+    static const uint32_t g[36] = {
+        4250078230u, 1555269520u, 2574712821u, 2014837863u, 339452353u, 357537223u, 4090554183u,
+        4037962445u, 568063040u, 3989728972u, 2651585397u, 302085953u,
+        216474225u, 3131872213u, 2031680910u, 2351063834u, 1460086222u, 3713621779u, 1346392468u,
+        1370249257u, 2902481344u, 236751935u, 1342743146u, 196886268u,
+        196605u, 1980301312u, 3289120770u, 3958636555u, 1405573306u, 1598593111u, 1884444485u,
+        2010011731u, 2723605613u, 1543969431u, 4202751123u, 368467651u};
+    if (out) memcpy(out, g, sizeof(g));
+}
+extern "C" int zkh_g1_mul(zkh_ctx* c, const zkh_g1* base, const zkh_tensor* t, zkh_g1** out) {
+    if (!c || !base || !t || !out) return fail(c, ZKH_EARG, "null argument");
+    *out = nullptr;
+    if (!base->n) return fail(c, ZKH_EARG, "g1_mul: empty base");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc;
+    zkh_g1* o;
+    if ((rc = g1_alloc(c, t->n, &o))) return rc;
+    if (t->n) {
+        DevPlanes p;
+        if ((rc = as_planes(c, t, SL_TMP0, &p))) {
+            zkh_g1_free(o);
+            return rc;
+        }
+        launch_g1_mul(c->stream, (const uint32_t*)base->d, base->n, p.lo(), p.hi(), t->n, (uint32_t*)o->d);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            zkh_g1_free(o);
+            return fail(c, ZKH_EDEV, "g1_mul: %s", hipGetErrorString(e));
+        }
+    }
+    *out = o;
+    return ZKH_OK;
+}
 extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, zkh_g1** out) {
     if (!c || !gens || !t || !out) return fail(c, ZKH_EARG, "null argument");
     *out = nullptr;
