@@ -177,12 +177,13 @@ __global__ __launch_bounds__(64) void k_pip_bucket(const uint32_t* __restrict__ 
 }
 
 // sum_b b * bucket[b] by the running sum acc += bucket[b]; run += acc, b = 15..1
-// (commitment.cu:73-77)
+// (commitment.cu:73-77); one quad per (row, window) shares each addition
 __global__ __launch_bounds__(64) void k_pip_window(const uint32_t* __restrict__ buckets,
                                                    const uint32_t* __restrict__ offs,
                                                    const uint16_t* __restrict__ alias, uint32_t m,
                                                    uint32_t* __restrict__ partials) {
-    const size_t t = (size_t)blockIdx.x * 64 + threadIdx.x;
+    const size_t t = (size_t)blockIdx.x * 16 + threadIdx.x / 4;
+    const int q = threadIdx.x & 3;
     if (t >= (size_t)m * 64) return;
     const uint32_t* o = offs + t * 16;
     const size_t row0 = t / 64 * 64;
@@ -190,23 +191,24 @@ __global__ __launch_bounds__(64) void k_pip_window(const uint32_t* __restrict__ 
     for (int b = 15; b >= 1; b--) {
         const uint32_t e = b == 15 ? o[0] : o[b + 1];
         const g1_t bk = e == o[b] ? g1_zero() : g1_load(buckets + ((row0 * 16 + alias[t * 16 + b])) * 36);
-        acc = g1_add(acc, bk);
-        run = g1_add(run, acc);
+        acc = g1_add_quad(acc, bk, q);
+        run = g1_add_quad(run, acc, q);
     }
-    g1_store(partials + t * 36, run);
+    if (q == 0) g1_store(partials + t * 36, run);
 }
 
-// Horner over the windows, most significant first (commitment.cu:81-89)
+// Horner over the windows, most significant first (commitment.cu:81-89); one quad per row
 __global__ __launch_bounds__(64) void k_pip_combine(const uint32_t* __restrict__ partials, uint32_t m,
                                                     uint32_t* __restrict__ out) {
-    const uint32_t row = blockIdx.x * 64 + threadIdx.x;
+    const uint32_t row = blockIdx.x * 16 + threadIdx.x / 4;
+    const int q = threadIdx.x & 3;
     if (row >= m) return;
     g1_t acc = g1_zero();
     for (int w = 63; w >= 0; w--) {
-        for (int k = 0; k < 4; k++) acc = g1_dbl(acc);
-        acc = g1_add(acc, g1_load(partials + ((size_t)row * 64 + w) * 36));
+        for (int k = 0; k < 4; k++) acc = g1_dbl_quad(acc, q);
+        acc = g1_add_quad(acc, g1_load(partials + ((size_t)row * 64 + w) * 36), q);
     }
-    g1_store(out + (size_t)row * 36, acc);
+    if (q == 0) g1_store(out + (size_t)row * 36, acc);
 }
 
 // G1Jacobian_mul (g1-tensor.cu:445-454), elementwise with a broadcast base
@@ -254,8 +256,8 @@ void launch_pip_bucket(hipStream_t s, const uint32_t* gens, const uint16_t* list
 }
 void launch_pip_window(hipStream_t s, const uint32_t* buckets, const uint32_t* offs, const uint16_t* alias,
                        uint32_t m, uint32_t* partials) {
-    hipLaunchKernelGGL(k_pip_window, dim3(m), dim3(64), 0, s, buckets, offs, alias, m, partials);
+    hipLaunchKernelGGL(k_pip_window, dim3(4 * m), dim3(64), 0, s, buckets, offs, alias, m, partials);
 }
 void launch_pip_combine(hipStream_t s, const uint32_t* partials, uint32_t m, uint32_t* out) {
-    hipLaunchKernelGGL(k_pip_combine, dim3((m + 63) / 64), dim3(64), 0, s, partials, m, out);
+    hipLaunchKernelGGL(k_pip_combine, dim3((m + 15) / 16), dim3(64), 0, s, partials, m, out);
 }

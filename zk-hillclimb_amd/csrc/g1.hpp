@@ -19,8 +19,10 @@
 //   pip_bucket  each distinct nonempty (row, window, digit) chain once: a long chain on a
 //               quad of lanes that share every point addition (latency-bound), a short
 //               one on one lane (throughput-bound);
-//   pip_window  one lane per (row, window): the running sum over digits 15..1;
-//   pip_combine one lane per row: Horner over windows 63..0 (four doublings, one add).
+//   pip_window  one quad per (row, window): the running sum over digits 15..1;
+//   pip_combine one quad per row: Horner over windows 63..0 (four doublings, one add).
+// Quads share each point operation (g1_add_quad, g1_dbl_quad): the window and Horner
+// chains are short in total work but sequential, so their latency is what counts.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
