@@ -242,23 +242,22 @@ def witness_gemm(zkh, jobs, reps=5):
 
 
 def commit_setup(zkh, jobs, seed=0x5EED0004):
-    """Commitment keys and padded tensors for the layer's matmuls (zkob_fc.cu:215-230):
-    gen_in (IN_pad points) and gen_out (OUT_pad points) as Commitment::random makes them
-    (the generator times random field elements, commitment.cu:3-8, here zkh_g1_mul), and
-    X, W, Y padded per dimension to powers of two."""
+    """Commitment keys and padded tensors for the layer's matmuls (zkob_fc.cu:215-230): one
+    pool of random generators made as Commitment::random makes them (the generator times
+    random field elements, commitment.cu:3-8, here zkh_g1_mul), of which gen_in takes the
+    first IN_pad points and gen_out the first OUT_pad; X, W, Y padded per dimension to
+    powers of two."""
     rng = np.random.default_rng(seed)
     G = zkh.g1_generator()[None, :]
+    c0 = jobs[0].ctx
+    npool = max(max(pow2(j.IN), pow2(j.OUT)) for j in jobs)
+    a = rng.integers(0, 2**32, size=(npool, 8), dtype=np.uint64).astype(np.uint32)
+    a[:, 7] %= 0x73EDA753  # below r's top limb: canonical
+    pool = c0.g1_mul(c0.g1_from_host(G), c0.from_fr(a)).to_host()
     for j in jobs:
         c = j.ctx
-        base = c.g1_from_host(G)
-
-        def rand_fr(n):
-            a = rng.integers(0, 2**32, size=(n, 8), dtype=np.uint64).astype(np.uint32)
-            a[:, 7] %= 0x73EDA753  # below r's top limb: canonical
-            return c.from_fr(a)
-
-        j.gen_in = c.g1_mul(base, rand_fr(pow2(j.IN)))
-        j.gen_out = c.g1_mul(base, rand_fr(pow2(j.OUT)))
+        j.gen_in = c.g1_from_host(pool[:pow2(j.IN)])
+        j.gen_out = c.g1_from_host(pool[:pow2(j.OUT)])
         j.Xp = c.pad(j.X, (j.B, j.IN))
         j.Wp = c.pad(j.W, (j.IN, j.OUT))
         j.Yp = c.pad(j.Y, (j.B, j.OUT))

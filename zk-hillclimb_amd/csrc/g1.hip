@@ -213,11 +213,13 @@ __global__ __launch_bounds__(64) void k_pip_combine(const uint32_t* __restrict__
 
 // G1Jacobian_mul (g1-tensor.cu:445-454), elementwise with a broadcast base
 // (G1_jacobian_elementwise_mul_broadcast, :463-468): double-and-add over the scalar's 256
-// raw bits, low bit first; out[i] = base[i % nb] * s[i]
+// raw bits, low bit first; out[i] = base[i % nb] * s[i].  One quad per element shares
+// each point operation (the 256-step chain is latency-bound).
 __global__ __launch_bounds__(64) void k_g1_mul(const uint32_t* __restrict__ base, uint32_t nb,
                                                const uint32_t* __restrict__ lo, const uint32_t* __restrict__ hi,
                                                uint32_t n, uint32_t* __restrict__ out) {
-    const uint32_t i = blockIdx.x * 64 + threadIdx.x;
+    const uint32_t i = blockIdx.x * 16 + threadIdx.x / 4;
+    const int q = threadIdx.x & 3;
     if (i >= n) return;
     g1_t a = g1_load(base + 36 * (size_t)(i % nb));
     g1_t acc = g1_zero();
@@ -226,16 +228,16 @@ __global__ __launch_bounds__(64) void k_g1_mul(const uint32_t* __restrict__ base
     for (int l = 0; l < 8; l++) {
         const uint32_t x = limb[l];
         for (int bit = 0; bit < 32; bit++) {
-            if ((x >> bit) & 1u) acc = g1_add(acc, a);
-            a = g1_dbl(a);
+            if ((x >> bit) & 1u) acc = g1_add_quad(acc, a, q);
+            a = g1_dbl_quad(a, q);
         }
     }
-    g1_store(out + 36 * (size_t)i, acc);
+    if (q == 0) g1_store(out + 36 * (size_t)i, acc);
 }
 
 void launch_g1_mul(hipStream_t s, const uint32_t* base, uint32_t nb, const uint32_t* lo, const uint32_t* hi,
                    uint32_t n, uint32_t* out) {
-    hipLaunchKernelGGL(k_g1_mul, dim3((n + 63) / 64), dim3(64), 0, s, base, nb, lo, hi, n, out);
+    hipLaunchKernelGGL(k_g1_mul, dim3((n + 15) / 16), dim3(64), 0, s, base, nb, lo, hi, n, out);
 }
 void launch_pip_sort(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t m, uint32_t n,
                      uint16_t* lists, uint32_t* offs) {
