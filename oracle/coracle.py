@@ -305,3 +305,15 @@ def g1_commit(gens, scalars, n):
     out = np.zeros((m, 36), dtype=np.uint32)
     rc = lib().or_g1_commit(_p(gens), ctypes.c_uint32(n), _p(sc), ctypes.c_uint32(m), _p(out))
     return rc, out
+
+
+def ipa_prove(st, a, b, g, Q, n):
+    """ipa_prove: a, b (n, 8) plain Fr; g (n, 36); Q (36,).  Returns (rc, L, R, a_final)."""
+    rounds = max(n.bit_length() - 1, 0)
+    L = np.zeros((rounds, 36), np.uint32)
+    R = np.zeros((rounds, 36), np.uint32)
+    af = np.zeros(8, np.uint32)
+    rc = lib().or_ipa_prove(_p(st), _p(np.ascontiguousarray(a, np.uint32)), _p(np.ascontiguousarray(b, np.uint32)),
+                            _p(np.ascontiguousarray(g, np.uint32)), _p(np.ascontiguousarray(Q, np.uint32)),
+                            ctypes.c_uint32(n), _p(L), _p(R), _p(af))
+    return rc, L, R, af

@@ -235,3 +235,87 @@ int or_g1_commit(const uint32_t* gens, uint32_t n, const uint32_t* scalars, uint
     }
     return 0;
 }
+
+/* ---- inner-product argument (ipa_prove, vrf_common.cuh:302-336) ----
+ * Fr values cross as plain canonical 8-limb arrays; the Fr arithmetic is zkh_oracle.c's. */
+#include <stdlib.h>
+
+static void fr_plain_mul(const uint32_t* a, const uint32_t* b, uint32_t* out) { or_fr_mul(a, b, out); }
+
+/* dev_msm (vrf_common.cuh:166-183): elementwise G1Jacobian_mul, then the pairwise tree
+   x[i] = x[i] + x[i + half] down to one point */
+static g1 msm_tree(const uint32_t* g, const uint32_t* a, uint32_t n, g1* tmp) {
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t p[36];
+        or_g1_mul(g + (size_t)i * 36, a + (size_t)i * 8, p);
+        tmp[i] = g1_load(p);
+    }
+    for (uint32_t sz = n; sz > 1; sz /= 2)
+        for (uint32_t i = 0; i < sz / 2; i++) tmp[i] = g1_add(tmp[i], tmp[i + sz / 2]);
+    return tmp[0];
+}
+/* dev_ip (vrf_common.cuh:185-203): sum of plain products */
+static void inner(const uint32_t* a, const uint32_t* b, uint32_t n, uint32_t out[8]) {
+    uint32_t acc[8] = {0}, t[8];
+    for (uint32_t i = 0; i < n; i++) {
+        fr_plain_mul(a + (size_t)i * 8, b + (size_t)i * 8, t);
+        or_fr_add(acc, t, acc);
+    }
+    memcpy(out, acc, 32);
+}
+
+int or_ipa_prove(uint8_t st[32], const uint32_t* a_in, const uint32_t* b_in, const uint32_t* g_in,
+                 const uint32_t Q[36], uint32_t n, uint32_t* L_out, uint32_t* R_out, uint32_t a_final[8]) {
+    if (!n || (n & (n - 1))) return 1;
+    uint32_t* a = malloc((size_t)n * 32);
+    uint32_t* b = malloc((size_t)n * 32);
+    uint32_t* g = malloc((size_t)n * 144);
+    g1* tmp = malloc((size_t)n * sizeof(g1));
+    memcpy(a, a_in, (size_t)n * 32);
+    memcpy(b, b_in, (size_t)n * 32);
+    memcpy(g, g_in, (size_t)n * 144);
+    uint32_t r = 0;
+    for (uint32_t sz = n; sz > 1; sz /= 2, r++) {
+        const uint32_t h = sz / 2;
+        uint32_t ip[8], qp[36], Lp[36], Rp[36];
+        g1 m = msm_tree(g + (size_t)h * 36, a, h, tmp);
+        inner(a, b + (size_t)h * 8, h, ip);
+        or_g1_mul(Q, ip, qp);
+        g1 t = g1_add(m, g1_load(qp));
+        g1_store(Lp, &t);
+        m = msm_tree(g, a + (size_t)h * 8, h, tmp);
+        inner(a + (size_t)h * 8, b, h, ip);
+        or_g1_mul(Q, ip, qp);
+        t = g1_add(m, g1_load(qp));
+        g1_store(Rp, &t);
+        or_tr_absorb(st, "L", 1, Lp, 144);
+        or_tr_absorb(st, "R", 1, Rp, 144);
+        uint32_t x[8], xi[8];
+        or_tr_challenge_fr(st, x);
+        or_fr_inv(x, xi);
+        /* k_fr_fold2 (vrf_common.cuh:63-69): a' = x a_lo + xi a_hi, b' = xi b_lo + x b_hi;
+           k_g1_fold2 (:71-76): g' = xi g_lo + x g_hi, added in that order */
+        for (uint32_t i = 0; i < h; i++) {
+            uint32_t u[8], v[8];
+            fr_plain_mul(x, a + (size_t)i * 8, u);
+            fr_plain_mul(xi, a + (size_t)(i + h) * 8, v);
+            or_fr_add(u, v, a + (size_t)i * 8);
+            fr_plain_mul(xi, b + (size_t)i * 8, u);
+            fr_plain_mul(x, b + (size_t)(i + h) * 8, v);
+            or_fr_add(u, v, b + (size_t)i * 8);
+            uint32_t p1[36], p2[36];
+            or_g1_mul(g + (size_t)i * 36, xi, p1);
+            or_g1_mul(g + (size_t)(i + h) * 36, x, p2);
+            g1 s = g1_add(g1_load(p1), g1_load(p2));
+            g1_store(g + (size_t)i * 36, &s);
+        }
+        memcpy(L_out + (size_t)r * 36, Lp, 144);
+        memcpy(R_out + (size_t)r * 36, Rp, 144);
+    }
+    memcpy(a_final, a, 32);
+    free(a);
+    free(b);
+    free(g);
+    free(tmp);
+    return 0;
+}

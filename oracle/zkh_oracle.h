@@ -157,6 +157,10 @@ void or_g1_mul(const uint32_t a[36], const uint32_t s[8], uint32_t out[36]);
  * gens [n] points, out [m] points */
 int or_g1_commit(const uint32_t* gens, uint32_t n, const uint32_t* scalars, uint32_t m,
                  uint32_t* out);
+/* ipa_prove (vrf_common.cuh:302-336): a, b n plain Fr, g n points, Q one point, n a power of
+ * two; continues the transcript st; L_out, R_out log2(n) points each, a_final one Fr */
+int or_ipa_prove(uint8_t st[32], const uint32_t* a, const uint32_t* b, const uint32_t* g,
+                 const uint32_t Q[36], uint32_t n, uint32_t* L_out, uint32_t* R_out, uint32_t a_final[8]);
 
 #ifdef __cplusplus
 }

@@ -187,3 +187,85 @@ def test_commit_bucket_order():
     for _ in range(4 * w):
         want = C.g1_dbl(want)
     assert np.array_equal(out[0], want)
+
+
+# ---- inner-product argument (ipa_prove, vrf_common.cuh:302-336) ----
+def ipa_verify(state, g_aff, Q_aff, a, b, L, R, a_final):
+    """Witness-free IPA check written from the argument's algebra (the reference's
+    ipa_verify, vrf_common.cuh:338-371): P0 = <a, g> + <a, b> Q; per round P <- x^2 L + P +
+    x^-2 R and b folds to x^-1 b_lo + x b_hi; the final generator is sum_i s_i g_i with
+    s_i = prod_r (bit (rounds-1-r) of i ? x_r : x_r^-1); accept iff P = a_f g_f + a_f b_f Q.
+    Affine big-integer arithmetic; returns (accepted, final transcript state)."""
+    RR = pyref.R
+    n = len(g_aff)
+    P = None
+    for i in range(n):
+        P = G.aff_add(P, G.aff_mul(g_aff[i], a[i]))
+    P = G.aff_add(P, G.aff_mul(Q_aff, sum(x * y for x, y in zip(a, b)) % RR))
+    tr = pyref.Transcript(state=bytes(state))
+    xs = []
+    bb = list(b)
+    for r in range(len(L)):
+        tr.absorb("L", bytes(np.asarray(L[r], np.uint32).tobytes()))
+        tr.absorb("R", bytes(np.asarray(R[r], np.uint32).tobytes()))
+        x = tr.challenge_fr()
+        xi = pow(x, RR - 2, RR)
+        xs.append((x, xi))
+        P = G.aff_add(G.aff_add(G.aff_mul(G.to_affine(L[r]), x * x % RR), P),
+                      G.aff_mul(G.to_affine(R[r]), xi * xi % RR))
+        h = len(bb) // 2
+        bb = [(xi * bb[k] + x * bb[k + h]) % RR for k in range(h)]
+    rounds = len(L)
+    gf = None
+    for i in range(n):
+        s = 1
+        for r in range(rounds):
+            s = s * (xs[r][0] if (i >> (rounds - 1 - r)) & 1 else xs[r][1]) % RR
+        gf = G.aff_add(gf, G.aff_mul(g_aff[i], s))
+    want = G.aff_add(G.aff_mul(gf, a_final), G.aff_mul(Q_aff, a_final * bb[0] % RR))
+    return P == want, tr.state
+
+
+@pytest.mark.parametrize("n", [1, 2, 8])
+def test_ipa_oracle_accepted_by_verifier(n):
+    rng = random.Random(200 + n)
+    pts = [rand_point(rng) for _ in range(n + 1)]
+    g_aff = [p[0] for p in pts[:n]]
+    g = np.stack([p[1] for p in pts[:n]])
+    Q_aff, Q = pts[n]
+    a = [rng.randrange(pyref.R) for _ in range(n)]
+    u = [rng.randrange(pyref.R) for _ in range(max(n.bit_length() - 1, 0))]
+    b = [pyref.eq_weight(k, u) if u else 1 for k in range(n)]
+    st = C.tr_init("ipa-test")
+    st0 = st.copy()
+    rc, L, R, af = C.ipa_prove(st, C.ints_to_fr(a), C.ints_to_fr(b), g, Q, n)
+    assert rc == 0 and len(L) == n.bit_length() - 1
+    ok, st_v = ipa_verify(st0, g_aff, Q_aff, a, b, L, R, pyref.from_limbs(af))
+    assert ok
+    assert bytes(st_v) == bytes(st)
+    if n > 1:
+        # a wrong final scalar and a swapped L/R pair must both fail
+        bad, _ = ipa_verify(st0, g_aff, Q_aff, a, b, L, R, (pyref.from_limbs(af) + 1) % pyref.R)
+        assert not bad
+        bad, _ = ipa_verify(st0, g_aff, Q_aff, a, b, R, L, pyref.from_limbs(af))
+        assert not bad
+
+
+def test_ipa_round_points_by_definition():
+    """L and R of the first round are, as group elements, <g_hi, a_lo> + <a_lo, b_hi> Q and
+    <g_lo, a_hi> + <a_hi, b_lo> Q."""
+    rng = random.Random(210)
+    n = 4
+    pts = [rand_point(rng) for _ in range(n + 1)]
+    g = np.stack([p[1] for p in pts[:n]])
+    Q_aff, Q = pts[n]
+    a = [rng.randrange(pyref.R) for _ in range(n)]
+    b = [rng.randrange(pyref.R) for _ in range(n)]
+    rc, L, R, af = C.ipa_prove(C.tr_init("ipa-def"), C.ints_to_fr(a), C.ints_to_fr(b), g, Q, n)
+    h = n // 2
+    wantL = G.aff_mul(Q_aff, sum(a[i] * b[h + i] for i in range(h)) % pyref.R)
+    wantR = G.aff_mul(Q_aff, sum(a[h + i] * b[i] for i in range(h)) % pyref.R)
+    for i in range(h):
+        wantL = G.aff_add(wantL, G.aff_mul(pts[h + i][0], a[i]))
+        wantR = G.aff_add(wantR, G.aff_mul(pts[i][0], a[h + i]))
+    assert G.to_affine(L[0]) == wantL and G.to_affine(R[0]) == wantR
