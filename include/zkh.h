@@ -251,6 +251,14 @@ int zkh_g1_mul(zkh_ctx* ctx, const zkh_g1* base, const zkh_tensor* t, zkh_g1** o
  * limbs, buckets in generator order, running sum, Horner).  ZKH_EARG when size(t) is not a
  * multiple of n (the reference's "Incompatible dimensions") or n > 65536. */
 int zkh_commit(zkh_ctx* ctx, const zkh_g1* gens, const zkh_tensor* t, zkh_g1** out);
+/* ipa_prove (vrf_common.cuh:302-336), continuing the caller's transcript: a and b n field
+ * elements (b: me_weights(u) in the drivers, i.e. zkh_eq_table), g n generators, Q one point,
+ * n a power of two.  Per round it absorbs "L" and "R" (144 raw bytes each, as absorb_g1) and
+ * draws x; L_out, R_out receive log2(n) points each (36 uint32) and a_final the folded a --
+ * the IpaProof fields write_ipa saves (vrf_common.cuh:280-289), byte-identical. */
+int zkh_ipa_prove(zkh_ctx* ctx, uint8_t transcript[32], const zkh_tensor* a, const zkh_tensor* b,
+                  const zkh_g1* g, const uint32_t Q[36], uint32_t* L_out, uint32_t* R_out,
+                  uint32_t a_final[8]);
 
 #ifdef __cplusplus
 }

@@ -174,3 +174,44 @@ def test_g1_mul_vs_oracle(zkh, ctx):
     assert np.array_equal(one[0], C.g1_mul(base, np.array(P.to_limbs(3), np.uint32)))
     assert np.array_equal(one[1], C.g1_mul(base, np.array(P.to_limbs(P.R - 1), np.uint32)))
     assert np.array_equal(one[2], G.g1_zero())
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 32, 256])
+def test_ipa_prove_vs_oracle(zkh, ctx, n):
+    """ipa_prove (vrf_common.cuh:302-336): L, R (absorbed, so byte-exact), a_final and the
+    transcript state equal the oracle's, with b = me_weights(u) as the drivers pass it."""
+    rng = np.random.default_rng(300 + n)
+    gens = gens_for(20 + n, n + 1)
+    g, Q = gens[:n], gens[n]
+    a = [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(n)]
+    u = [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(max(n.bit_length() - 1, 0))]
+    b = [P.eq_weight(k, u) if u else 1 for k in range(n)]
+    st_g = zkh.transcript("ipa-%d" % n)
+    st_o = C.tr_init("ipa-%d" % n)
+    got = ctx.ipa_prove(st_g, ctx.from_fr(C.ints_to_fr(a)), ctx.from_fr(C.ints_to_fr(b)), ctx.g1_from_host(g), Q)
+    rc, L, R, af = C.ipa_prove(st_o, C.ints_to_fr(a), C.ints_to_fr(b), g, Q, n)
+    assert rc == 0
+    assert np.array_equal(got["L"], L) and np.array_equal(got["R"], R)
+    assert np.array_equal(got["a_final"], af)
+    assert bytes(st_g) == bytes(st_o)
+
+
+def test_ipa_prove_int_witness_and_errors(zkh, ctx):
+    """a from an int32 tensor (a folded weight row is small until it is folded); sizes that
+    are not a power of two or disagree are ZKH_EARG."""
+    n = 16
+    rng = np.random.default_rng(310)
+    v = rng.integers(-229376, 229377, size=n).astype(np.int32)
+    gens = gens_for(40, n + 1)
+    u = [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(4)]
+    b = C.ints_to_fr([P.eq_weight(k, u) for k in range(n)])
+    st_g, st_o = zkh.transcript("ipa-int"), C.tr_init("ipa-int")
+    got = ctx.ipa_prove(st_g, ctx.from_i32(v), ctx.from_fr(b), ctx.g1_from_host(gens[:n]), gens[n])
+    rc, L, R, af = C.ipa_prove(st_o, C.ints_to_fr(v), b, gens[:n], gens[n], n)
+    assert np.array_equal(got["L"], L) and np.array_equal(got["R"], R) and np.array_equal(got["a_final"], af)
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.ipa_prove(zkh.transcript("x"), ctx.from_i32(v[:12]), ctx.from_fr(b[:12]), ctx.g1_from_host(gens[:12]), gens[n])
+    assert e.value.code == zkh.EARG
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.ipa_prove(zkh.transcript("x"), ctx.from_i32(v[:8]), ctx.from_fr(b), ctx.g1_from_host(gens[:n]), gens[n])
+    assert e.value.code == zkh.EARG

@@ -97,6 +97,7 @@ def lib():
         L.zkh_g1_generator.restype = None
         L.zkh_g1_generator.argtypes = [vp]
         L.zkh_g1_mul.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
+        L.zkh_ipa_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
         _lib = L
     return _lib
 
@@ -342,6 +343,18 @@ class Context:
         h = ctypes.c_void_p()
         self._chk(lib().zkh_g1_mul(self.h, base.h, t.h, ctypes.byref(h)))
         return G1(self, h)
+
+    def ipa_prove(self, st, a, b, g, Q):
+        """ipa_prove over n = g.n: returns {"L": (log n, 36), "R": (log n, 36), "a_final": (8,)};
+        st (32 uint8) is advanced in place."""
+        n = g.n
+        rounds = max(n.bit_length() - 1, 0)
+        L = np.zeros((max(rounds, 1), 36), np.uint32)
+        R = np.zeros((max(rounds, 1), 36), np.uint32)
+        af = np.zeros(8, np.uint32)
+        Q = np.ascontiguousarray(Q, np.uint32)
+        self._chk(lib().zkh_ipa_prove(self.h, _p(st), a.h, b.h, g.h, _p(Q), _p(L), _p(R), _p(af)))
+        return {"L": L[:rounds], "R": R[:rounds], "a_final": af}
 
     def commit(self, gens, t):
         """Commitment::commit: rows of n = gens.n scalars of tensor t -> one point per row."""

@@ -1,5 +1,6 @@
 // g1.hip -- G1 Pedersen commitment kernels (bucket method, commitment.cu:47-103).
 #include "fp_dev.hpp"
+#include "fr_dev.hpp"
 #include "g1.hpp"
 
 // Lane w of the row's wave owns window w (bits 4w..4w+3 of the raw scalar, commitment.cu:
@@ -211,30 +212,161 @@ __global__ __launch_bounds__(64) void k_pip_combine(const uint32_t* __restrict__
     if (q == 0) g1_store(out + (size_t)row * 36, acc);
 }
 
-// G1Jacobian_mul (g1-tensor.cu:445-454), elementwise with a broadcast base
-// (G1_jacobian_elementwise_mul_broadcast, :463-468): double-and-add over the scalar's 256
-// raw bits, low bit first; out[i] = base[i % nb] * s[i].  One quad per element shares
-// each point operation (the 256-step chain is latency-bound).
+// G1Jacobian_mul (g1-tensor.cu:445-454) on a quad: double-and-add over the scalar's raw
+// bits, low bit first.  The doublings after the highest set bit do not reach the result
+// and are skipped.
+__device__ __forceinline__ uint32_t limb8(const uint32_t s[8], uint32_t l) {
+    return l == 0 ? s[0] : l == 1 ? s[1] : l == 2 ? s[2] : l == 3 ? s[3]
+         : l == 4 ? s[4] : l == 5 ? s[5] : l == 6 ? s[6] : s[7];
+}
+__device__ __forceinline__ g1_t g1_mul_quad(g1_t a, const uint32_t s[8], int q) {
+    int top = -1;
+    for (int l = 7; l >= 0 && top < 0; l--)
+        if (s[l]) top = 32 * l + 31 - __builtin_clz(s[l]);
+    g1_t acc = g1_zero();
+    uint32_t w = 0;
+    for (int i = 0; i <= top; i++) {
+        if ((i & 31) == 0) w = limb8(s, (uint32_t)i >> 5);
+        if ((w >> (i & 31)) & 1u) acc = g1_add_quad(acc, a, q);
+        if (i < top) a = g1_dbl_quad(a, q);
+    }
+    return acc;
+}
+
+// elementwise with a broadcast base (G1_jacobian_elementwise_mul_broadcast,
+// g1-tensor.cu:463-468): out[i] = base[i % nb] * s[i], one quad per element
 __global__ __launch_bounds__(64) void k_g1_mul(const uint32_t* __restrict__ base, uint32_t nb,
                                                const uint32_t* __restrict__ lo, const uint32_t* __restrict__ hi,
                                                uint32_t n, uint32_t* __restrict__ out) {
     const uint32_t i = blockIdx.x * 16 + threadIdx.x / 4;
     const int q = threadIdx.x & 3;
     if (i >= n) return;
-    g1_t a = g1_load(base + 36 * (size_t)(i % nb));
-    g1_t acc = g1_zero();
     const uint4 s0 = ((const uint4*)lo)[i], s1 = ((const uint4*)hi)[i];
-    const uint32_t limb[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-    for (int l = 0; l < 8; l++) {
-        const uint32_t x = limb[l];
-        for (int bit = 0; bit < 32; bit++) {
-            if ((x >> bit) & 1u) acc = g1_add_quad(acc, a, q);
-            a = g1_dbl_quad(a, q);
-        }
-    }
-    if (q == 0) g1_store(out + 36 * (size_t)i, acc);
+    const uint32_t sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const g1_t r = g1_mul_quad(g1_load(base + 36 * (size_t)(i % nb)), sc, q);
+    if (q == 0) g1_store(out + 36 * (size_t)i, r);
 }
 
+// ---- inner-product argument rounds (ipa_prove, vrf_common.cuh:302-336) ----
+// a, b: plain Fr, 8 words per entry; g, P: points.  Round of size 2h:
+//   ip = (<a_lo, b_hi>, <a_hi, b_lo>)                       (dev_ip, one block)
+//   P[j] = g_hi[j] a_lo[j], P[h + j] = g_lo[j] a_hi[j], P[2h] = Q ip_L, P[2h+1] = Q ip_R
+//   pairwise trees over P[0, h) and P[h, 2h)                  (dev_msm's order)
+//   L = P[0] + P[2h], R = P[h] + P[2h+1]
+//   fold: a' = x a_lo + x^-1 a_hi, b' = x^-1 b_lo + x b_hi, g' = x^-1 g_lo + x g_hi
+__global__ __launch_bounds__(256) void k_ipa_ip(const uint32_t* __restrict__ a, const uint32_t* __restrict__ b,
+                                                uint32_t h, fr_t r2, uint32_t* __restrict__ ip) {
+    __shared__ fr_t red[2][256];
+    fr_t sl = fr_zero(), sr = fr_zero();
+    for (uint32_t i = threadIdx.x; i < h; i += 256) {
+        sl = fr_add(sl, mont_mul(ld_aos(a, i), ld_aos(b, h + i)));
+        sr = fr_add(sr, mont_mul(ld_aos(a, h + i), ld_aos(b, i)));
+    }
+    red[0][threadIdx.x] = sl;
+    red[1][threadIdx.x] = sr;
+    __syncthreads();
+    for (uint32_t o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            red[0][threadIdx.x] = fr_add(red[0][threadIdx.x], red[0][threadIdx.x + o]);
+            red[1][threadIdx.x] = fr_add(red[1][threadIdx.x], red[1][threadIdx.x + o]);
+        }
+        __syncthreads();
+    }
+    // sums of a b 2^-256; times R^2 2^-256 gives the plain sums
+    if (threadIdx.x < 2) st_aos(ip, threadIdx.x, mont_mul(red[threadIdx.x][0], r2));
+}
+__global__ __launch_bounds__(64) void k_ipa_scale(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
+                                                  const uint32_t* __restrict__ Q, const uint32_t* __restrict__ ip,
+                                                  uint32_t h, uint32_t* __restrict__ P) {
+    const uint32_t j = blockIdx.x * 16 + threadIdx.x / 4;
+    const int q = threadIdx.x & 3;
+    if (j >= 2 * h + 2) return;
+    const uint32_t* base = j < h ? g + 36 * (size_t)(h + j) : j < 2 * h ? g + 36 * (size_t)(j - h) : Q;
+    const uint32_t* sp = j < 2 * h ? a + 8 * (size_t)j : ip + 8 * (j - 2 * h);
+    uint32_t sc[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) sc[k] = sp[k];
+    const g1_t r = g1_mul_quad(g1_load(base), sc, q);
+    if (q == 0) g1_store(P + 36 * (size_t)j, r);
+}
+__global__ __launch_bounds__(64) void k_ipa_tree(uint32_t* __restrict__ P, uint32_t h, uint32_t half) {
+    const uint32_t i = blockIdx.x * 16 + threadIdx.x / 4;
+    const int q = threadIdx.x & 3;
+    if (i >= 2 * half) return;
+    const size_t k = (size_t)(i / half) * h + i % half;
+    const g1_t r = g1_add_quad(g1_load(P + 36 * k), g1_load(P + 36 * (k + half)), q);
+    if (q == 0) g1_store(P + 36 * k, r);
+}
+__global__ __launch_bounds__(64) void k_ipa_lr(const uint32_t* __restrict__ P, uint32_t h, uint32_t* __restrict__ LR) {
+    const uint32_t side = threadIdx.x / 4;
+    const int q = threadIdx.x & 3;
+    if (side >= 2) return;
+    const g1_t r = g1_add_quad(g1_load(P + 36 * (size_t)(side * h)), g1_load(P + 36 * (size_t)(2 * h + side)), q);
+    if (q == 0) g1_store(LR + 36 * side, r);
+}
+// eight lanes per element: quad 0 computes x^-1 g_lo[i], quad 1 x g_hi[i] (k_g1_fold2's
+// two products, vrf_common.cuh:71-76), then quad 0 adds them in that order
+__global__ __launch_bounds__(64) void k_ipa_fold(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
+                                                 const uint32_t* __restrict__ b, uint32_t h, fr_t x, fr_t xi,
+                                                 fr_t xm, fr_t xim, uint32_t* __restrict__ g2,
+                                                 uint32_t* __restrict__ a2, uint32_t* __restrict__ b2) {
+    __shared__ uint32_t hi_pt[8][36];
+    const uint32_t e = threadIdx.x / 8, i = blockIdx.x * 8 + e;
+    const int q = threadIdx.x & 3, half_sel = (threadIdx.x >> 2) & 1;
+    g1_t r = g1_zero();
+    if (i < h) {
+        r = g1_mul_quad(g1_load(g + 36 * (size_t)(i + half_sel * h)), half_sel ? x.v : xi.v, q);
+        if (half_sel && q == 0) g1_store(hi_pt[e], r);
+    }
+    __syncthreads();
+    if (i < h && !half_sel) {
+        r = g1_add_quad(r, g1_load(hi_pt[e]), q);
+        if (q == 0) {
+            g1_store(g2 + 36 * (size_t)i, r);
+            st_aos(a2, i, fr_add(mont_mul(xm, ld_aos(a, i)), mont_mul(xim, ld_aos(a, i + h))));
+            st_aos(b2, i, fr_add(mont_mul(xim, ld_aos(b, i)), mont_mul(xm, ld_aos(b, i + h))));
+        }
+    }
+}
+// planes -> 8-word entries
+__global__ __launch_bounds__(256) void k_planes_to_aos(const uint32_t* __restrict__ lo, const uint32_t* __restrict__ hi,
+                                                       uint32_t n, uint32_t* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    st_aos(out, i, ld_fr((const uint4*)lo, (const uint4*)hi, i));
+}
+
+void launch_ipa_ip(hipStream_t s, const uint32_t* a, const uint32_t* b, uint32_t h, const uint32_t r2[8],
+                   uint32_t* ip) {
+    fr_t R2;
+    for (int k = 0; k < 8; k++) R2.v[k] = r2[k];
+    hipLaunchKernelGGL(k_ipa_ip, dim3(1), dim3(256), 0, s, a, b, h, R2, ip);
+}
+void launch_ipa_scale(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* Q, const uint32_t* ip,
+                      uint32_t h, uint32_t* P) {
+    hipLaunchKernelGGL(k_ipa_scale, dim3((2 * h + 2 + 15) / 16), dim3(64), 0, s, g, a, Q, ip, h, P);
+}
+void launch_ipa_tree(hipStream_t s, uint32_t* P, uint32_t h, uint32_t half) {
+    hipLaunchKernelGGL(k_ipa_tree, dim3((2 * half + 15) / 16), dim3(64), 0, s, P, h, half);
+}
+void launch_ipa_lr(hipStream_t s, const uint32_t* P, uint32_t h, uint32_t* LR) {
+    hipLaunchKernelGGL(k_ipa_lr, dim3(1), dim3(64), 0, s, P, h, LR);
+}
+void launch_ipa_fold(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* b, uint32_t h,
+                     const uint32_t x[8], const uint32_t xi[8], const uint32_t xm[8], const uint32_t xim[8],
+                     uint32_t* g2, uint32_t* a2, uint32_t* b2) {
+    fr_t X, XI, XM, XIM;
+    for (int k = 0; k < 8; k++) {
+        X.v[k] = x[k];
+        XI.v[k] = xi[k];
+        XM.v[k] = xm[k];
+        XIM.v[k] = xim[k];
+    }
+    hipLaunchKernelGGL(k_ipa_fold, dim3((h + 7) / 8), dim3(64), 0, s, g, a, b, h, X, XI, XM, XIM, g2, a2, b2);
+}
+void launch_planes_to_aos(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t n, uint32_t* out) {
+    hipLaunchKernelGGL(k_planes_to_aos, dim3((n + 255) / 256), dim3(256), 0, s, lo, hi, n, out);
+}
 void launch_g1_mul(hipStream_t s, const uint32_t* base, uint32_t nb, const uint32_t* lo, const uint32_t* hi,
                    uint32_t n, uint32_t* out) {
     hipLaunchKernelGGL(k_g1_mul, dim3((n + 15) / 16), dim3(64), 0, s, base, nb, lo, hi, n, out);

@@ -39,6 +39,17 @@ void launch_pip_bucket(hipStream_t s, const uint32_t* gens, const uint16_t* list
 void launch_pip_window(hipStream_t s, const uint32_t* buckets, const uint32_t* offs, const uint16_t* alias,
                        uint32_t m, uint32_t* partials);
 void launch_pip_combine(hipStream_t s, const uint32_t* partials, uint32_t m, uint32_t* out);
+// inner-product argument rounds (ipa_prove); a, b plain Fr 8 words per entry, g/P points
+void launch_ipa_ip(hipStream_t s, const uint32_t* a, const uint32_t* b, uint32_t h, const uint32_t r2[8],
+                   uint32_t* ip);
+void launch_ipa_scale(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* Q, const uint32_t* ip,
+                      uint32_t h, uint32_t* P);
+void launch_ipa_tree(hipStream_t s, uint32_t* P, uint32_t h, uint32_t half);
+void launch_ipa_lr(hipStream_t s, const uint32_t* P, uint32_t h, uint32_t* LR);
+void launch_ipa_fold(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* b, uint32_t h,
+                     const uint32_t x[8], const uint32_t xi[8], const uint32_t xm[8], const uint32_t xim[8],
+                     uint32_t* g2, uint32_t* a2, uint32_t* b2);
+void launch_planes_to_aos(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t n, uint32_t* out);
 // out[i] = base[i % nb] * s[i] (G1Jacobian_mul, raw scalar bits)
 void launch_g1_mul(hipStream_t s, const uint32_t* base, uint32_t nb, const uint32_t* lo, const uint32_t* hi,
                    uint32_t n, uint32_t* out);

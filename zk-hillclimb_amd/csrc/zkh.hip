@@ -2615,6 +2615,77 @@ extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, z
 }
 
 // ---------------------------------------------------------------------------------------
+// inner-product argument (ipa_prove, vrf_common.cuh:302-336), continuing the caller's
+// transcript; the round points are byte-identical to the reference's (they are absorbed)
+// ---------------------------------------------------------------------------------------
+extern "C" int zkh_ipa_prove(zkh_ctx* c, uint8_t* transcript, const zkh_tensor* a, const zkh_tensor* b,
+                             const zkh_g1* g, const uint32_t* Q, uint32_t* L_out, uint32_t* R_out,
+                             uint32_t* a_final) {
+    if (!c || !transcript || !a || !b || !g || !Q || !a_final) return fail(c, ZKH_EARG, "null argument");
+    const uint32_t n = g->n;
+    if (!n || (n & (n - 1))) return fail(c, ZKH_EARG, "ipa_prove: n not a power of two");  // vrf_common.cuh:305
+    if (a->n != n || b->n != n) return fail(c, ZKH_EARG, "ipa_prove: a, b and g sizes differ");
+    if (n > 1 && (!L_out || !R_out)) return fail(c, ZKH_EARG, "null argument");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    // a, b, g working copies (two of each, the fold writes the other), round products P,
+    // inner products, L and R
+    uint32_t* fr_w = (uint32_t*)scratch(c, SL_TMP1, (size_t)n * 32 * 4, &rc);
+    uint32_t* g_w = rc ? nullptr : (uint32_t*)scratch(c, SL_TMP2, (size_t)n * 144 * 2, &rc);
+    uint32_t* P = rc ? nullptr : (uint32_t*)scratch(c, SL_TMP3, (size_t)(n + 2) * 144 + 1024, &rc);
+    if (rc) return rc;
+    uint32_t* ip = P + 36 * (size_t)(n + 2);
+    uint32_t* LR = ip + 16;
+    uint32_t* Qd = LR + 72;
+    uint32_t *a0 = fr_w, *a1 = fr_w + 8 * (size_t)n, *b0 = fr_w + 16 * (size_t)n, *b1 = fr_w + 24 * (size_t)n;
+    uint32_t *g0 = g_w, *g1 = g_w + 36 * (size_t)n;
+    DevPlanes pa, pb;
+    if ((rc = as_planes(c, a, SL_TMP0, &pa))) return rc;
+    launch_planes_to_aos(c->stream, pa.lo(), pa.hi(), n, a0);
+    if ((rc = as_planes(c, b, SL_TMP0, &pb))) return rc;
+    launch_planes_to_aos(c->stream, pb.lo(), pb.hi(), n, b0);
+    HIPCHK(c, hipMemcpyAsync(g0, g->d, (size_t)n * 144, hipMemcpyDeviceToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(Qd, Q, 144, hipMemcpyHostToDevice, c->stream));
+    uint32_t r2[8];
+    fr_store(kR2, r2);
+    uint32_t lr[72];
+    uint32_t round = 0;
+    for (uint32_t sz = n; sz > 1; sz /= 2, round++) {
+        const uint32_t h = sz / 2;
+        {
+            ProfScope ps(c, "ipa_msm", (double)sz * (144 + 32));
+            launch_ipa_ip(c->stream, a0, b0, h, r2, ip);
+            launch_ipa_scale(c->stream, g0, a0, Qd, ip, h, P);
+            for (uint32_t half = h / 2; half >= 1; half /= 2) launch_ipa_tree(c->stream, P, h, half);
+            launch_ipa_lr(c->stream, P, h, LR);
+        }
+        HIPCHK(c, hipMemcpyAsync(lr, LR, sizeof(lr), hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        tr_absorb(transcript, "L", 1, lr, 144);
+        tr_absorb(transcript, "R", 1, lr + 36, 144);
+        const Fr x = tr_challenge(transcript), xi = fr_inv(x);
+        uint32_t xv[8], xiv[8], xm[8], xim[8];
+        fr_store(x, xv);
+        fr_store(xi, xiv);
+        fr_store(fr_to_mont(x), xm);
+        fr_store(fr_to_mont(xi), xim);
+        {
+            ProfScope ps(c, "ipa_fold", (double)sz * (144 + 64));
+            launch_ipa_fold(c->stream, g0, a0, b0, h, xv, xiv, xm, xim, g1, a1, b1);
+        }
+        std::swap(g0, g1);
+        std::swap(a0, a1);
+        std::swap(b0, b1);
+        memcpy(L_out + 36 * (size_t)round, lr, 144);
+        memcpy(R_out + 36 * (size_t)round, lr + 36, 144);
+    }
+    HIPCHK(c, hipMemcpyAsync(a_final, a0, 32, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipGetLastError());
+    return ZKH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
 // Hadamard sumcheck (zkob_lookup.cuh:267-315)
 // ---------------------------------------------------------------------------------------
 static Fr lagrange4(const Fr e[4], const Fr& v) {
