@@ -77,6 +77,9 @@ uint32_t zkh_tensor_size(const zkh_tensor* t);
 int zkh_tensor_kind(const zkh_tensor* t);
 /* device tensor -> host Fr array (n*8 uint32) */
 int zkh_tensor_to_fr(zkh_ctx* ctx, const zkh_tensor* t, uint32_t* fr_aos_out);
+/* device tensor -> host int64 by scalar_to_long per entry (FrTensor::save_long,
+ * fr-tensor.cu:210-218; scalar_to_long :935-945): exact for integer tensors */
+int zkh_tensor_to_i64(zkh_ctx* ctx, const zkh_tensor* t, int64_t* out);
 
 /* ---------------- MLE primitives (fr-tensor.cu) ---------------- */
 /* sum of all entries (FrTensor::sum, fr-tensor.cu:407-434) */

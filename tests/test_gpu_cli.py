@@ -1,0 +1,165 @@
+"""The zkob_fc-compatible driver zk-hillclimb_amd/zkh_fc (zkob_fc.cu:1207-1330,
+zkob_serve.cuh): `prove` in the reference's plain mode must write the same obligation files
+as the reference, byte for byte -- com_X.bin, com_Y.bin, dims.bin, sumcheck.bin, ipa_W.bin,
+ipa_X.bin, ipa_Y.bin and the int64 Y -- which this test restates from the C oracle: the
+commitments (commit_pippenger), the transcript absorbs (zkob_fc.cu:254-258), the matmul
+sumcheck (:259-440), write_sumcheck (:105-112), the IPA openings in the order W, X, Y
+(:473-483) and write_ipa (vrf_common.cuh:284-289).  Shapes: the reference's own selftest
+cases (zkob_fc.cu:1246-1248) and a non-power-of-two B.  `commit` (weight registration) and
+`serve` (ZKW-READY / ZKW-RC) are covered too."""
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import coracle as C
+from oracle import pyg1 as G
+from oracle import pyref as P
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CLI = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_fc")
+BASE = G.aff_to_jac((G.GX, G.GY))
+
+
+def points(seed, n):
+    rng = np.random.default_rng(seed)
+    out = np.zeros((n, 36), np.uint32)
+    for i in range(n):
+        k = int.from_bytes(rng.bytes(32), "little") % P.R
+        out[i] = C.g1_mul(BASE, np.array(P.to_limbs(k), np.uint32))
+    return out
+
+
+def pow2(n):
+    return 1 << max(n - 1, 0).bit_length()
+
+
+def padded(M):
+    r, c = M.shape
+    out = np.zeros((pow2(r), pow2(c)), np.int64)
+    out[:r, :c] = M
+    return out
+
+
+def pod(arr, words):
+    a = np.ascontiguousarray(arr, np.uint32).reshape(-1, words)
+    return struct.pack("<I", a.shape[0]) + a.tobytes()
+
+
+def expected(seed, X, W, gin, gout, Q):
+    """the obligation directory's files, restated from the oracle"""
+    B, IN = X.shape
+    OUT = W.shape[1]
+    Y = X.astype(np.int64) @ W.astype(np.int64)
+    Xp, Wp, Yp = padded(X), padded(W), padded(Y)
+    files = {}
+    coms = {}
+    for name, T, g in (("X", Xp, gin), ("W", Wp, gout), ("Y", Yp, gout)):
+        rc, c = C.g1_commit(g, C.ints_to_fr(T.reshape(-1)), T.shape[1])
+        assert rc == 0
+        coms[name] = c
+    files["com_X.bin"] = coms["X"].tobytes()
+    files["com_Y.bin"] = coms["Y"].tobytes()
+    files["dims.bin"] = struct.pack("<III", B, IN, OUT)
+    st = C.tr_init(seed)
+    for lab, v in (("B", B), ("IN", IN), ("OUT", OUT)):
+        C.tr_absorb(st, lab, struct.pack("<I", v))
+    for lab in ("X", "W", "Y"):
+        C.tr_absorb(st, "com_" + lab, coms[lab].tobytes())
+    rc, mm = C.mm_prove(st, X, W, Y, B, IN, OUT)
+    assert rc == 0
+    files["sumcheck.bin"] = pod(mm["ev"], 8) + mm["claims"].tobytes()
+    bW = C.build_eq(mm["u_output"])
+    for name, T, u, b, g, win in (("W", Wp, mm["u_input"], bW, gout, Wp.shape[1]),
+                                  ("X", Xp, mm["u_batch"], C.build_eq(mm["u_input"]), gin, Xp.shape[1]),
+                                  ("Y", Yp, mm["u_batch"], bW, gout, Yp.shape[1])):
+        rc, a = C.partial_me_window(C.ints_to_fr(T.reshape(-1)), u, win)
+        assert rc == 0 and len(a) == win
+        rc, L, R, af = C.ipa_prove(st, a, b, g, Q, win)
+        assert rc == 0
+        files["ipa_%s.bin" % name] = pod(L, 36) + pod(R, 36) + af.tobytes()
+    return files, Y
+
+
+def write_inputs(d, X, W, gin, gout, q):
+    paths = {}
+    for name, arr in (("X.bin", X.astype(np.int32)), ("W.bin", W.astype(np.int32)), ("gen_in.bin", gin),
+                      ("gen_out.bin", gout), ("q.bin", q)):
+        paths[name] = os.path.join(d, name)
+        np.ascontiguousarray(arr).tofile(paths[name])
+    return paths
+
+
+@pytest.mark.parametrize("B,IN,OUT", [(4, 6, 3), (8, 8, 8), (16, 12, 5), (3, 16, 2)])
+def test_prove_files_match_reference_format(tmp_path, B, IN, OUT):
+    rng = np.random.default_rng(B * 100 + IN * 10 + OUT)
+    X = rng.integers(-2**15, 2**15, size=(B, IN)).astype(np.int32)
+    W = rng.integers(-229376, 229377, size=(IN, OUT)).astype(np.int32)
+    gin, gout, q = points(1, pow2(IN)), points(2, pow2(OUT)), points(3, 2)
+    p = write_inputs(str(tmp_path), X, W, gin, gout, q)
+    ob = tmp_path / "ob"
+    ob.mkdir()
+    yout = str(tmp_path / "Y.i64")
+    seed = "run7:layer0.q_proj.matmul"
+    r = subprocess.run([CLI, "prove", str(ob), seed, p["X.bin"], p["W.bin"], str(B), str(IN), str(OUT),
+                        p["gen_in.bin"], p["gen_out.bin"], p["q.bin"], yout], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "PROVED matmul obligation" in r.stdout
+    want, Y = expected(seed, X, W, gin, gout, q[0])
+    for name, data in want.items():
+        assert (ob / name).read_bytes() == data, name
+    assert open(yout, "rb").read() == Y.astype(np.int64).tobytes()
+
+
+def test_commit_registration_and_errors(tmp_path):
+    rng = np.random.default_rng(5)
+    IN, OUT = 6, 5
+    W = rng.integers(-1000, 1000, size=(IN, OUT)).astype(np.int32)
+    gout = points(4, pow2(OUT))
+    p = write_inputs(str(tmp_path), W[:1], W, gout, gout, gout[:1])
+    out = str(tmp_path / "com_W.bin")
+    r = subprocess.run([CLI, "commit", p["W.bin"], str(IN), str(OUT), p["gen_out.bin"], out],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    rc, want = C.g1_commit(gout, C.ints_to_fr(padded(W).reshape(-1)), pow2(OUT))
+    assert open(out, "rb").read() == want.tobytes()
+    # a generator file of the wrong size, a short input file, an unsupported mode flag
+    r = subprocess.run([CLI, "commit", p["W.bin"], str(IN), str(OUT * 2), p["gen_out.bin"], out],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1
+    r = subprocess.run([CLI, "commit", p["X.bin"], str(IN), str(OUT), p["gen_out.bin"], out],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1 and "short read" in r.stderr
+    r = subprocess.run([CLI, "prove", "x", "y", "--claims", "a", "b", "c"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+
+
+def test_serve_mode(tmp_path):
+    rng = np.random.default_rng(6)
+    B, IN, OUT = 4, 6, 3
+    X = rng.integers(-100, 100, size=(B, IN)).astype(np.int32)
+    W = rng.integers(-100, 100, size=(IN, OUT)).astype(np.int32)
+    gin, gout, q = points(7, pow2(IN)), points(8, pow2(OUT)), points(9, 1)
+    p = write_inputs(str(tmp_path), X, W, gin, gout, q)
+    obs = [tmp_path / "a", tmp_path / "b"]
+    for o in obs:
+        o.mkdir()
+    lines = ["prove %s s%d %s %s %d %d %d %s %s %s" % (o, i, p["X.bin"], p["W.bin"], B, IN, OUT, p["gen_in.bin"],
+                                                       p["gen_out.bin"], p["q.bin"]) for i, o in enumerate(obs)]
+    lines.append("prove %s s --wpriv a b" % obs[0])
+    r = subprocess.run([CLI, "serve"], input="\n".join(lines) + "\n", capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0
+    out = r.stdout.splitlines()
+    assert out[0] == "ZKW-READY"
+    rcs = [l for l in out if l.startswith("ZKW-RC ")]
+    assert rcs == ["ZKW-RC 0", "ZKW-RC 0", "ZKW-RC 3"]
+    for i, o in enumerate(obs):
+        want, _ = expected("s%d" % i, X, W, gin, gout, q[0])
+        for name, data in want.items():
+            assert (o / name).read_bytes() == data, (i, name)

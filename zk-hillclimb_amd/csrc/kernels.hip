@@ -1548,6 +1548,14 @@ void launch_matmul_i32(hipStream_t s, const int32_t* X, const int32_t* WT, const
 __global__ void k_widen_i32(const int32_t* __restrict__ in, uint32_t n, int64_t* __restrict__ out) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = in[i];
 }
+__global__ void k_to_long(const uint4* __restrict__ lo, const uint4* __restrict__ hi, uint32_t n,
+                          int64_t* __restrict__ out) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = fr_to_long(ld_fr(lo, hi, i));
+}
+void launch_to_long(hipStream_t s, DevPlanes p, uint32_t n, int64_t* out) {
+    k_to_long<<<grid_for(n, NT, 1024), NT, 0, s>>>((const uint4*)p.lo(), (const uint4*)p.hi(), n, out);
+}
 void launch_widen_i32(hipStream_t s, const int32_t* in, uint32_t n, int64_t* out) {
     k_widen_i32<<<grid_for(n, NT, 1024), NT, 0, s>>>(in, n, out);
 }

@@ -223,6 +223,8 @@ void launch_fold_last_multi(hipStream_t s, const ZkipBatch& b);
 void launch_matmul_i32(hipStream_t s, const int32_t* X, const int32_t* WT, const int64_t* bias, uint32_t B,
                        uint32_t IN, uint32_t OUT, int64_t* Y, int f64);
 void launch_widen_i32(hipStream_t s, const int32_t* in, uint32_t n, int64_t* out);
+// scalar_to_long of every entry (FrTensor::save_long, fr-tensor.cu:210-218)
+void launch_to_long(hipStream_t s, DevPlanes p, uint32_t n, int64_t* out);
 
 // ---- persistent matmul round loop ----
 // Each job's tables a, b (n = 2^L entries) are spread cyclically over nb = 2^lgnb blocks

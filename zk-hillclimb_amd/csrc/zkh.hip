@@ -831,6 +831,20 @@ static int as_planes(zkh_ctx* c, const zkh_tensor* t, int slot, DevPlanes* out) 
     *out = p;
     return 0;
 }
+extern "C" int zkh_tensor_to_i64(zkh_ctx* c, const zkh_tensor* t, int64_t* out) {
+    if (!c || !t || (!out && t->n)) return fail(c, ZKH_EARG, "null argument");
+    if (!t->n) return ZKH_OK;
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc;
+    DevPlanes p;
+    if ((rc = as_planes(c, t, SL_TMP4, &p))) return rc;
+    int64_t* d = (int64_t*)scratch(c, SL_TMP6, (size_t)t->n * 8, &rc);
+    if (rc) return rc;
+    launch_to_long(c->stream, p, t->n, d);
+    HIPCHK(c, hipMemcpyAsync(out, d, (size_t)t->n * 8, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return ZKH_OK;
+}
 extern "C" int zkh_tensor_to_fr(zkh_ctx* c, const zkh_tensor* t, uint32_t* aos) {
     if (!c || !t || (!aos && t->n)) return fail(c, ZKH_EARG, "null argument");
     if (!t->n) return ZKH_OK;
