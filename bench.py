@@ -18,7 +18,9 @@ TinyLlama-1.1B".
   in setup), process init.
 - commitments: the layer's com_X, com_W, com_Y (zkob_fc.cu:215-230) with zkh_commit,
   byte-identical to the reference's commit_pippenger, reported beside the metric (not part
-  of it) with their own CPU baseline (the C oracle on one row each of X, W, Y).
+  of it) with their own CPU baseline (the C oracle on one row each of X, W, Y); openings:
+  the layer's 21 IPA openings (zkob_fc.cu:473-483, zkh_ipa_prove) after the sumchecks, with
+  the oracle's time for one of them as CPU baseline.
 - Inputs are seeded synthetic tensors (fp8-e4m3 weights as scaled ints, Gaussian int16
   activations), resident in HBM before the timed region.
 - The throughput steps carry no timing events (stamping them costs the host ~20 us per
@@ -251,11 +253,12 @@ def commit_setup(zkh, jobs, seed=0x5EED0004):
     G = zkh.g1_generator()[None, :]
     c0 = jobs[0].ctx
     npool = max(max(pow2(j.IN), pow2(j.OUT)) for j in jobs)
-    a = rng.integers(0, 2**32, size=(npool, 8), dtype=np.uint64).astype(np.uint32)
+    a = rng.integers(0, 2**32, size=(npool + 1, 8), dtype=np.uint64).astype(np.uint32)
     a[:, 7] %= 0x73EDA753  # below r's top limb: canonical
     pool = c0.g1_mul(c0.g1_from_host(G), c0.from_fr(a)).to_host()
     for j in jobs:
         c = j.ctx
+        j.Q = pool[npool]  # the IPA's Q (the first point of the reference's q.bin)
         j.gen_in = c.g1_from_host(pool[:pow2(j.IN)])
         j.gen_out = c.g1_from_host(pool[:pow2(j.OUT)])
         j.Xp = c.pad(j.X, (j.B, j.IN))
@@ -310,6 +313,48 @@ def commitments(zkh, jobs, pool, reps=3, cpu=True):
                     "7 matmuls concurrent on 7 streams; byte-identical to commit_pippenger"}
     if cpu:
         res["cpu_baseline"] = commit_cpu_baseline(jobs[0])
+    return res
+
+
+def open_job(j, out):
+    """The IPA openings that end zkob_fc's prove (zkob_fc.cu:473-483), order W, X, Y, each
+    continuing the matmul's transcript after its sumcheck: a = the padded tensor folded over
+    its rows by the proof's challenges (partial_me), b = me_weights of the other point."""
+    c = j.ctx
+    st = j.st.copy()
+    ub, uo, ui = out["u_batch"], out["u_output"], out["u_input"]
+    bW = c.eq_table(uo)
+    r = [c.ipa_prove(st, c.partial_me_window(j.Wp, ui, pow2(j.OUT)), bW, j.gen_out, j.Q),
+         c.ipa_prove(st, c.partial_me_window(j.Xp, ub, pow2(j.IN)), c.eq_table(ui), j.gen_in, j.Q),
+         c.ipa_prove(st, c.partial_me_window(j.Yp, ub, pow2(j.OUT)), bW, j.gen_out, j.Q)]
+    return b"".join(x["L"].tobytes() + x["R"].tobytes() + x["a_final"].tobytes() for x in r) + st.tobytes()
+
+
+def openings(zkh, jobs, outs, pool, reps=2, cpu=True):
+    """The layer's 21 IPA openings (3 per matmul), the 7 matmuls concurrent on their own
+    contexts; every pass must reproduce the first pass's proofs."""
+    ref = [open_job(j, o) for j, o in zip(jobs, outs)]
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        futs = [pool.submit(open_job, j, o) for j, o in zip(jobs, outs)]
+        assert [f.result() for f in futs] == ref, "non-deterministic openings"
+        times.append(time.perf_counter() - t)
+    res = {"ipa_s_per_layer": round(min(times), 4), "ipas": 3 * len(jobs),
+           "scope": "ipa_W, ipa_X, ipa_Y of the 7 matmuls (vrf_common.cuh:302-336), byte-identical round points"}
+    if cpu:
+        sys.path.insert(0, ROOT)
+        from oracle import coracle
+        j, o = jobs[0], outs[0]
+        st = coracle.tr_init("cpu-ipa")
+        a = j.ctx.partial_me_window(j.Xp, o["u_batch"], pow2(j.IN)).to_fr()
+        b = j.ctx.eq_table(o["u_input"]).to_fr()
+        t0 = time.perf_counter()
+        rc, _, _, _ = coracle.ipa_prove(st, a, b, j.gen_in.to_host(), j.Q, pow2(j.IN))
+        secs = time.perf_counter() - t0
+        assert rc == 0
+        res["cpu_baseline"] = {"value": round(secs, 3), "unit": "s per IPA (n = %d)" % pow2(j.IN), "cores": 1,
+                               "kind": "port", "sample": "C oracle ipa_prove of the Q projection's X opening"}
     return res
 
 
@@ -532,8 +577,11 @@ def main():
 
     wg = None if args.no_layer else witness_gemm(zkh, jobs)
     com = None if args.no_commit else commitments(zkh, jobs, pool, cpu=not args.no_cpu)
+    ope = None
     if com:
         print("commitments %.3f s per layer" % com["commit_s_per_layer"], file=sys.stderr, flush=True)
+        ope = openings(zkh, jobs, mbatch.outs, pool, cpu=not args.no_cpu)
+        print("openings %.3f s per layer" % ope["ipa_s_per_layer"], file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(jobs)
     res = {
         "metric": "Fr elements bound/sec in matmul sumcheck; prove s/layer at TinyLlama-1.1B",
@@ -552,6 +600,8 @@ def main():
         res["witness_gemm"] = wg
     if com:
         res["commitments"] = com
+    if ope:
+        res["openings"] = ope
     print(json.dumps(res))
     pool.shutdown()
 
