@@ -6,7 +6,10 @@ commitments (commit_pippenger), the transcript absorbs (zkob_fc.cu:254-258), the
 sumcheck (:259-440), write_sumcheck (:105-112), the IPA openings in the order W, X, Y
 (:473-483) and write_ipa (vrf_common.cuh:284-289).  Shapes: the reference's own selftest
 cases (zkob_fc.cu:1246-1248) and a non-power-of-two B.  `commit` (weight registration) and
-`serve` (ZKW-READY / ZKW-RC) are covered too."""
+`serve` (ZKW-READY / ZKW-RC) are covered too.  zkh_rescale (zkob_rescale.cu:70-197) is
+checked the same way: rescaling witness, multiplicities, five commitments, the logUp proof
+(write_lookup, zkob_lookup.cuh:80-87) and the openings of A, rem and m (open_prove,
+zkob_lookup.cuh:116-127), on the reference's rescale selftest shapes (zkob_rescale.cu:539-541)."""
 import os
 import struct
 import subprocess
@@ -22,6 +25,7 @@ pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CLI = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_fc")
+RESCALE = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_rescale")
 BASE = G.aff_to_jac((G.GX, G.GY))
 
 
@@ -163,3 +167,76 @@ def test_serve_mode(tmp_path):
         want, _ = expected("s%d" % i, X, W, gin, gout, q[0])
         for name, data in want.items():
             assert (o / name).read_bytes() == data, (i, name)
+
+
+def log2(n):
+    return n.bit_length() - 1
+
+
+def expected_rescale(seed, X, B, Cc, log_sf, gen, Q):
+    sf = 1 << log_sf
+    Bp, Cp = pow2(B), pow2(Cc)
+    D, N = Bp * Cp, sf
+    logD, n1, logG = log2(D), log2(D // N), log2(Cp)
+    rc, q, rem = C.rescale(X.reshape(-1), sf)
+    assert rc == 0
+    Xp, Xrp, remp = padded(X.reshape(B, Cc)), padded(q.reshape(B, Cc)), padded(rem.reshape(B, Cc))
+    low = -(sf >> 1)
+    T = C.range_table(low, sf, N)
+    S = C.ints_to_fr(remp.reshape(-1))
+    rc, m = C.lu_prep(S, low, N)
+    assert rc == 0
+    files, coms = {}, {}
+    for name, t in (("X", C.ints_to_fr(Xp.reshape(-1))), ("Xr", C.ints_to_fr(Xrp.reshape(-1))), ("rem", S), ("m", m)):
+        rc, coms[name] = C.g1_commit(gen, t, Cp)
+        files["com_%s.bin" % name] = coms[name].tobytes()
+    files["dims.bin"] = struct.pack("<III", B, Cc, log_sf)
+    st = C.tr_init(seed)
+    for lab, v in (("B", B), ("C", Cc), ("LOG_SF", log_sf)):
+        C.tr_absorb(st, lab, struct.pack("<I", v))
+    for name in ("X", "Xr", "rem", "m"):
+        C.tr_absorb(st, "com_" + name, coms[name].tobytes())
+    beta = C.tr_challenge_fr(st)
+    A = C.lu_inverse(S, beta)
+    rc, comA = C.g1_commit(gen, A, Cp)
+    files["com_A.bin"] = comA.tobytes()
+    C.tr_absorb(st, "com_A", comA.tobytes())
+    alpha = C.tr_challenge_fr(st)
+    u = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, lk = C.lu_prove(st, A, S, T, m, alpha, beta, u)
+    assert rc == 0
+    files["lookup.bin"] = pod(lk["ev"], 8) + lk["term"][0].tobytes() + lk["term"][1].tobytes() + lk["term"][4].tobytes()
+    u_pt = lk["ws"][::-1]
+    for name, t, pt in (("A", A, u_pt), ("rem", S, u_pt), ("m", m, u_pt[:logD - n1])):
+        a = t if len(pt) == logG else C.partial_me_window(t, pt[logG:], Cp)[1]
+        rc, L, R, af = C.ipa_prove(st, a, C.build_eq(pt[:logG]), gen, Q, Cp)
+        assert rc == 0
+        files["ipa_%s.bin" % name] = pod(L, 36) + pod(R, 36) + af.tobytes()
+    return files, q
+
+
+@pytest.mark.parametrize("B,Cc,log_sf", [(8, 4, 4), (4, 16, 4), (8, 6, 6)])
+def test_rescale_prove_files_match_reference_format(tmp_path, B, Cc, log_sf):
+    rng = np.random.default_rng(B * 100 + Cc * 10 + log_sf)
+    X = rng.integers(-(1 << 12), 1 << 12, size=(B, Cc)).astype(np.int64) * 37
+    gen, q = points(11, pow2(Cc)), points(12, 1)
+    xp, gp, qp = (str(tmp_path / n) for n in ("X.i64", "gen.bin", "q.bin"))
+    X.tofile(xp)
+    gen.tofile(gp)
+    q.tofile(qp)
+    ob = tmp_path / "ob"
+    ob.mkdir()
+    xr = str(tmp_path / "Xr.i32")
+    seed = "selftest:rescale"
+    r = subprocess.run([RESCALE, "prove", str(ob), seed, xp, str(B), str(Cc), str(log_sf), gp, qp, xr],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "PROVED rescaling obligation" in r.stdout
+    want, Xr = expected_rescale(seed, X, B, Cc, log_sf, gen, q[0])
+    for name, data in want.items():
+        assert (ob / name).read_bytes() == data, name
+    assert open(xr, "rb").read() == Xr.astype(np.int32).tobytes()
+    # a layout the reference rejects (N > D) and a generator of the wrong size
+    r = subprocess.run([RESCALE, "prove", str(ob), seed, xp, str(B), str(Cc), str(10), gp, qp],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1

@@ -1,7 +1,8 @@
 """Build libzkh.so (the C-ABI library) for gfx950 with hipcc, in-tree.
 
 Compiles csrc/*.hip to objects in parallel and links one shared library next to this
-file, then the zkob_fc-compatible driver `zkh_fc` (cli/zkh_fc.cpp, host C++ against it).  Flags: -O3, C++17, gfx950 only, packed FP32 disabled (the field arithmetic is
+file, then the zkob_*-compatible drivers `zkh_fc` and `zkh_rescale` (cli/*.cpp, host C++
+against it).  Flags: -O3, C++17, gfx950 only, packed FP32 disabled (the field arithmetic is
 integer-only; the flag keeps hipcc from forming packed fp32 ops anywhere).
 """
 import concurrent.futures
@@ -13,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libzkh.so")
-CLI = os.path.join(HERE, "zkh_fc")
+CLIS = ("zkh_fc", "zkh_rescale")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -44,14 +45,15 @@ def build(verbose=True):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
-    # the zkob_fc-compatible driver (host C++ over the C ABI)
-    tmp = CLI + ".tmp"
-    cmd = ["g++", "-O2", "-std=c++17", "-Wall", os.path.join(HERE, "cli", "zkh_fc.cpp"), "-o", tmp,
-           "-L" + HERE, "-lzkh", "-Wl,-rpath,$ORIGIN"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("zkh_fc build failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, CLI)
+    # the zkob_*-compatible drivers (host C++ over the C ABI)
+    for name in CLIS:
+        out = os.path.join(HERE, name)
+        cmd = ["g++", "-O2", "-std=c++17", "-Wall", os.path.join(HERE, "cli", name + ".cpp"), "-o", out + ".tmp",
+               "-L" + HERE, "-lzkh", "-Wl,-rpath,$ORIGIN"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError("%s build failed:\n%s%s" % (name, r.stdout, r.stderr))
+        os.replace(out + ".tmp", out)
     return LIB
 
 
