@@ -240,3 +240,105 @@ def test_rescale_prove_files_match_reference_format(tmp_path, B, Cc, log_sf):
     r = subprocess.run([RESCALE, "prove", str(ob), seed, xp, str(B), str(Cc), str(10), gp, qp],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 1
+
+
+GLU = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_glu")
+
+
+def fr_of(vals):
+    return C.ints_to_fr([int(v) % P.R for v in np.asarray(vals, dtype=object).reshape(-1)])
+
+
+def open_ipa(st, t, pt, Cp, gen, Q):
+    logG = log2(Cp)
+    a = t if len(pt) == logG else C.partial_me_window(t, pt[logG:], Cp)[1]
+    rc, L, R, af = C.ipa_prove(st, a, C.build_eq(pt[:logG]), gen, Q, Cp)
+    assert rc == 0
+    return pod(L, 36) + pod(R, 36) + af.tobytes()
+
+
+def expected_glu(seed, Gm, Um, low, ln, mapped, gen, Q):
+    """zkob_glu.cu:86-247 (plain mode) restated from the oracle and the definitions of the
+    mapping lookup (S = mapped[G - low], m = counts)"""
+    B, Cc = Gm.shape
+    Bp, Cp = pow2(B), pow2(Cc)
+    D, N = Bp * Cp, ln
+    logD, n1 = log2(D), log2(D // N)
+    Gp, Up = padded(Gm), padded(Um)
+    idx = (Gp - low).reshape(-1)
+    S = np.asarray(mapped, np.int64)[idx].reshape(Gp.shape)
+    m = np.bincount(idx, minlength=N).astype(np.int64)
+    H = S * Up
+    files, coms = {}, {}
+    for name, t in (("G", Gp), ("S", S), ("U", Up), ("H", H), ("m", m)):
+        rc, coms[name] = C.g1_commit(gen, fr_of(t), Cp)
+        files["com_%s.bin" % name] = coms[name].tobytes()
+    files["dims.bin"] = struct.pack("<iiii", B, Cc, low, ln)
+    st = C.tr_init(seed)
+    for lab, v in (("B", B), ("C", Cc), ("LOW", low & 0xFFFFFFFF), ("LEN", ln)):
+        C.tr_absorb(st, lab, struct.pack("<I", v))
+    for name in ("G", "S", "U", "H", "m"):
+        C.tr_absorb(st, "com_" + name, coms[name].tobytes())
+    r = P.from_limbs(C.tr_challenge_fr(st))
+    beta = C.tr_challenge_fr(st)
+    comb = fr_of([(int(g) + r * int(s)) % P.R for g, s in zip(Gp.reshape(-1), S.reshape(-1))])
+    Tcomb = fr_of([(low + i + r * int(mapped[i])) % P.R for i in range(N)])
+    A = C.lu_inverse(comb, beta)
+    rc, comA = C.g1_commit(gen, A, Cp)
+    files["com_A.bin"] = comA.tobytes()
+    C.tr_absorb(st, "com_A", comA.tobytes())
+    alpha = C.tr_challenge_fr(st)
+    u = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, lk = C.lu_prove(st, A, comb, Tcomb, fr_of(m), alpha, beta, u)
+    assert rc == 0
+    files["lookup.bin"] = pod(lk["ev"], 8) + lk["term"][0].tobytes() + lk["term"][1].tobytes() + lk["term"][4].tobytes()
+    u_pt = lk["ws"][::-1]
+    files["ipa_A.bin"] = open_ipa(st, A, u_pt, Cp, gen, Q)
+    files["ipa_comb.bin"] = open_ipa(st, comb, u_pt, Cp, gen, Q)
+    files["ipa_m.bin"] = open_ipa(st, fr_of(m), u_pt[:logD - n1], Cp, gen, Q)
+    uh = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, claimH = C.me(fr_of(H), uh)
+    assert rc == 0
+    C.tr_absorb(st, "claim_H", claimH.tobytes())
+    rc, hp = C.hp_prove(st, claimH, C.build_eq(uh), fr_of(S), fr_of(Up))
+    assert rc == 0
+    C.tr_absorb(st, "S_f2", hp["term"][0].tobytes())
+    C.tr_absorb(st, "U_f2", hp["term"][1].tobytes())
+    files["hp.bin"] = claimH.tobytes() + pod(hp["ev"], 8) + hp["term"][0].tobytes() + hp["term"][1].tobytes()
+    u_pt2 = hp["ws"][::-1]
+    files["ipa_H.bin"] = open_ipa(st, fr_of(H), uh, Cp, gen, Q)
+    files["ipa_S.bin"] = open_ipa(st, fr_of(S), u_pt2, Cp, gen, Q)
+    files["ipa_U.bin"] = open_ipa(st, fr_of(Up), u_pt2, Cp, gen, Q)
+    return files, H[:B, :Cc]
+
+
+@pytest.mark.parametrize("B,Cc,low,ln", [(8, 4, -8, 16), (4, 4, -8, 16), (8, 6, -16, 32)])
+def test_glu_prove_files_match_reference_format(tmp_path, B, Cc, low, ln):
+    rng = np.random.default_rng(B * 1000 + Cc * 10 + ln)
+    mapped = np.array([(i + low) ** 2 for i in range(ln)], np.int32)  # the reference selftest's table
+    Gm = rng.integers(low, low + ln, size=(B, Cc)).astype(np.int32)
+    Um = rng.integers(-300, 300, size=(B, Cc)).astype(np.int32)
+    gen, q = points(21, pow2(Cc)), points(22, 1)
+    paths = {}
+    for name, arr in (("G", Gm), ("U", Um), ("map", mapped), ("gen", gen), ("q", q)):
+        paths[name] = str(tmp_path / (name + ".bin"))
+        np.ascontiguousarray(arr).tofile(paths[name])
+    ob = tmp_path / "ob"
+    ob.mkdir()
+    hout = str(tmp_path / "H.i64")
+    seed = "selftest:glu"
+    r = subprocess.run([GLU, "prove", str(ob), seed, paths["G"], paths["U"], str(B), str(Cc), str(low), str(ln),
+                        paths["map"], paths["gen"], paths["q"], hout], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "PROVED swiglu obligation" in r.stdout
+    want, H = expected_glu(seed, Gm, Um, low, ln, mapped, gen, q[0])
+    for name, data in want.items():
+        assert (ob / name).read_bytes() == data, name
+    assert open(hout, "rb").read() == H.astype(np.int64).tobytes()
+    # a table without (0, 0) is refused, as load_mapped refuses it
+    bad = mapped.copy()
+    bad[-low] = 5
+    bad.tofile(paths["map"])
+    r = subprocess.run([GLU, "prove", str(ob), seed, paths["G"], paths["U"], str(B), str(Cc), str(low), str(ln),
+                        paths["map"], paths["gen"], paths["q"]], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1 and "mapped(0)" in r.stderr
