@@ -342,3 +342,91 @@ def test_glu_prove_files_match_reference_format(tmp_path, B, Cc, low, ln):
     r = subprocess.run([GLU, "prove", str(ob), seed, paths["G"], paths["U"], str(B), str(Cc), str(low), str(ln),
                         paths["map"], paths["gen"], paths["q"]], capture_output=True, text=True, timeout=120)
     assert r.returncode == 1 and "mapped(0)" in r.stderr
+
+
+ROPE = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_rope")
+
+
+def ints_of(fr):
+    return [P.from_limbs(x) for x in np.asarray(fr, np.uint32).reshape(-1, 8)]
+
+
+def expected_rope(seed, Th, HD, cosT, sinT, gen, Q):
+    """zkob_rope.cu prove (plain mode) restated: weights and the flipped T by their
+    definitions, then the oracle for commitments, MLEs, both Hadamard sumchecks and IPAs"""
+    B, Cc = Th.shape
+    Cp = pow2(Cc)
+    logCp, logD = log2(Cp), log2(B) + log2(Cp)
+    flipv, fb = HD // 2, log2(HD) - 1
+    W1 = np.zeros((B, Cp), np.int64)
+    W2 = np.zeros((B, Cp), np.int64)
+    Tg = np.zeros((B, Cp), np.int64)
+    for t in range(B):
+        for e in range(Cc):
+            W1[t, e] = cosT[t, e % HD]
+            W2[t, e] = (1 if e & flipv else -1) * sinT[t, e % HD]
+            Tg[t, e] = Th[t, e]
+    Txg = Tg[:, [e ^ flipv for e in range(Cp)]]
+    Y = Tg * W1 + Txg * W2
+    T_fr, Tx_fr, Y_fr, ones = fr_of(Tg), fr_of(Txg), fr_of(Y), fr_of(np.ones(B * Cp, np.int64))
+    files = {}
+    rc, comT = C.g1_commit(gen, T_fr, Cp)
+    rc, comY = C.g1_commit(gen, Y_fr, Cp)
+    files["com_T.bin"], files["com_Y64.bin"] = comT.tobytes(), comY.tobytes()
+    files["dims.bin"] = struct.pack("<IIII", B, Cc, HD, 16)
+    st = C.tr_init(seed)
+    for lab, v in (("B", B), ("C", Cc), ("HD", HD), ("SCALE_R", 16)):
+        C.tr_absorb(st, lab, struct.pack("<I", v))
+    C.tr_absorb(st, "com_T", comT.tobytes())
+    C.tr_absorb(st, "com_Y64", comY.tobytes())
+    u = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, ev = C.me(Y_fr, u)
+    C.tr_absorb(st, "ev", ev.tobytes())
+    files["ev.bin"] = ev.tobytes()
+    Eu = ints_of(C.build_eq(u))
+    for k, (W, S_fr, S_int) in enumerate(((W1, T_fr, Tg), (W2, Tx_fr, Txg)), start=1):
+        E = [e * int(w) % P.R for e, w in zip(Eu, W.reshape(-1))]
+        c = sum(e * int(s) for e, s in zip(E, S_int.reshape(-1))) % P.R
+        cl = np.array(P.to_limbs(c), np.uint32)
+        C.tr_absorb(st, "c%d" % k, cl.tobytes())
+        rc, hp = C.hp_prove(st, cl, fr_of(E), S_fr, ones)
+        assert rc == 0
+        C.tr_absorb(st, "S_f2", hp["term"][0].tobytes())
+        C.tr_absorb(st, "U_f2", hp["term"][1].tobytes())
+        files["hp%d.bin" % k] = cl.tobytes() + pod(hp["ev"], 8) + hp["term"][0].tobytes() + hp["term"][1].tobytes()
+        pt = hp["ws"][::-1].copy()
+        if k == 2:
+            pt[fb] = P.to_limbs((1 - P.from_limbs(pt[fb])) % P.R)
+        files["ipa_T%d.bin" % k] = open_ipa(st, T_fr, pt, Cp, gen, Q)
+    files["ipa_Y.bin"] = open_ipa(st, Y_fr, u, Cp, gen, Q)
+    return files, Y[:, :Cc]
+
+
+@pytest.mark.parametrize("B,Cc,HD", [(8, 6, 2), (4, 8, 4), (16, 12, 4)])
+def test_rope_prove_files_match_reference_format(tmp_path, B, Cc, HD):
+    rng = np.random.default_rng(2026 + B * 100 + Cc * 10 + HD)
+    cosT = rng.integers(-128, 129, size=(B, HD)).astype(np.int32)
+    sinT = rng.integers(-128, 129, size=(B, HD)).astype(np.int32)
+    Th = rng.integers(-128, 129, size=(B, Cc)).astype(np.int32)
+    gen, q = points(31, pow2(Cc)), points(32, 1)
+    paths = {}
+    for name, arr in (("T", Th), ("cos", cosT), ("sin", sinT), ("gen", gen), ("q", q)):
+        paths[name] = str(tmp_path / (name + ".bin"))
+        np.ascontiguousarray(arr).tofile(paths[name])
+    ob = tmp_path / "ob"
+    ob.mkdir()
+    yout = str(tmp_path / "Y64.i64")
+    seed = "selftest:rope"
+    r = subprocess.run([ROPE, "prove", str(ob), seed, paths["T"], str(B), str(Cc), str(HD), paths["cos"],
+                        paths["sin"], paths["gen"], paths["q"], yout], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "PROVED rope obligation" in r.stdout
+    want, Y = expected_rope(seed, Th, HD, cosT, sinT, gen, q[0])
+    for name, data in want.items():
+        assert (ob / name).read_bytes() == data, name
+    assert open(yout, "rb").read() == Y.astype(np.int64).tobytes()
+    # a layout the reference refuses: HD not dividing C
+    r = subprocess.run([ROPE, "prove", str(ob), seed, paths["T"], str(B), str(Cc), str(8 if Cc % 8 else 16),
+                        paths["cos"], paths["sin"], paths["gen"], paths["q"]], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 1

@@ -1,7 +1,7 @@
 """Build libzkh.so (the C-ABI library) for gfx950 with hipcc, in-tree.
 
 Compiles csrc/*.hip to objects in parallel and links one shared library next to this
-file, then the zkob_*-compatible drivers `zkh_fc`, `zkh_rescale` and `zkh_glu` (cli/*.cpp, host C++
+file, then the zkob_*-compatible drivers `zkh_fc`, `zkh_rescale`, `zkh_glu` and `zkh_rope` (cli/*.cpp, host C++
 against it).  Flags: -O3, C++17, gfx950 only, packed FP32 disabled (the field arithmetic is
 integer-only; the flag keeps hipcc from forming packed fp32 ops anywhere).
 """
@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libzkh.so")
-CLIS = ("zkh_fc", "zkh_rescale", "zkh_glu")
+CLIS = ("zkh_fc", "zkh_rescale", "zkh_glu", "zkh_rope")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
