@@ -87,6 +87,16 @@ int zkh_sum(zkh_ctx* ctx, const zkh_tensor* t, uint32_t out[8]);
 /* FrTensor::operator()(u): LSB-first MLE evaluation, u[0] binds bit 0 (fr-tensor.cu:437-442,
  * :588-609); requires 2^(k-1) < n <= 2^k */
 int zkh_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k, uint32_t out[8]);
+/* one degree-2 product round over MSB pairs (k_bo_hp2 + bo_dev_sum, zkob_claims.cuh:367-383,
+ * :577-592): out[t] = sum_{i < n/2} a_t[i] b_t[i] for t = 0, 1, 2, with
+ * X_t[i] = X[i] + t (X[i + n/2] - X[i]); a, b FR tensors of one even size n.  With zkh_fold
+ * this runs the batch-evaluation sumcheck of the claims accumulator. */
+int zkh_prod_round(zkh_ctx* ctx, const zkh_tensor* a, const zkh_tensor* b, uint32_t out[24]);
+/* host scalar arithmetic on canonical Fr, the reference's h_scalar / k_scalar_op
+ * (vrf_common.cuh:30-38, :100-104): op 0 a+b, 1 a-b, 2 a*b, 3 a^-1 (0 -> 0); no device */
+int zkh_fr_scalar(const uint32_t a[8], const uint32_t b[8], int op, uint32_t out[8]);
+/* SHA-256 of a byte string (bo_file_sha256's digest, zkob_claims.cuh:310-318); no device */
+int zkh_sha256(const void* data, size_t n, uint8_t out[32]);
 /* FrTensor::partial_me(u, cur_dim, window) (fr-tensor.cu:518-560): binds the middle
  * dimension of a row-major [other, cur_dim, window] view; returns a new FR tensor of
  * other*window entries */

@@ -68,6 +68,17 @@ def test_transcript_long_absorbs(zkh):
         assert bytes(st) == ref, n
 
 
+def test_sha256_matches_hashlib(zkh):
+    """zkh_sha256 (bo_file_sha256, zkob_claims.cuh:311-318) on a fresh state per call, host
+    only: block-boundary lengths and two calls in a row agree with hashlib."""
+    rng = np.random.default_rng(9)
+    for n in [0, 1, 55, 56, 63, 64, 65, 144, 1000, 65537, 3]:
+        data = rng.integers(0, 256, size=n, dtype=np.uint8).tobytes()
+        out = (ctypes.c_uint8 * 32)()
+        assert zkh.lib().zkh_sha256(data, ctypes.c_size_t(n), out) == 0
+        assert bytes(out) == hashlib.sha256(data).digest(), n
+
+
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="a GPU is present")
 def test_no_gpu_fails_loudly(zkh):
     h = ctypes.c_void_p()

@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libzkh.so")
-CLIS = ("zkh_fc", "zkh_rescale", "zkh_glu", "zkh_rope")
+CLIS = ("zkh_fc", "zkh_rescale", "zkh_glu", "zkh_rope", "zkh_batchopen")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -186,4 +186,194 @@ inline void reject_flags(const std::vector<std::string>& rest, const char* drv) 
         if (s.rfind("--", 0) == 0) throw Err(2, std::string(drv) + ": " + s + " (claim and privacy modes) is not provided");
 }
 
+// ---- field scalars on the host (h_scalar) ----
+struct Fr8 {
+    uint32_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+};
+inline Fr8 fr_u32(uint32_t x) {
+    Fr8 r;
+    r.v[0] = x;
+    return r;
+}
+inline Fr8 fr_of(const uint32_t* p) {
+    Fr8 r;
+    memcpy(r.v, p, 32);
+    return r;
+}
+inline Fr8 fop(const Fr8& a, const Fr8& b, int op) {
+    Fr8 r;
+    if (zkh_fr_scalar(a.v, b.v, op, r.v)) throw Err(1, "non-canonical field element");
+    return r;
+}
+inline Fr8 fadd(const Fr8& a, const Fr8& b) { return fop(a, b, 0); }
+inline Fr8 fsub(const Fr8& a, const Fr8& b) { return fop(a, b, 1); }
+inline Fr8 fmul(const Fr8& a, const Fr8& b) { return fop(a, b, 2); }
+inline Fr8 finv(const Fr8& a) { return fop(a, a, 3); }
+inline bool feq(const Fr8& a, const Fr8& b) { return memcmp(a.v, b.v, 32) == 0; }
+// lagrange3 (vrf_common.cuh:130-140): p(u) through p(0), p(1), p(2)
+inline Fr8 lagrange3(const Fr8& p0, const Fr8& p1, const Fr8& p2, const Fr8& u) {
+    const Fr8 one = fr_u32(1), two = fr_u32(2), inv2 = finv(two);
+    const Fr8 um1 = fsub(u, one), um2 = fsub(u, two);
+    const Fr8 l0 = fmul(fmul(um1, um2), inv2), l1 = fmul(u, fsub(two, u)), l2 = fmul(fmul(u, um1), inv2);
+    return fadd(fadd(fmul(p0, l0), fmul(p1, l1)), fmul(p2, l2));
+}
+
+// ---- claims accumulator files (zkob_claims.cuh:82-270) ----
+inline void put_u32(std::vector<uint8_t>& b, uint32_t v) {
+    for (int i = 0; i < 4; i++) b.push_back(uint8_t(v >> (8 * i)));
+}
+inline void put_bytes(std::vector<uint8_t>& b, const void* p, size_t n) {
+    const uint8_t* q = (const uint8_t*)p;
+    b.insert(b.end(), q, q + n);
+}
+struct Claim {
+    std::string id, comref;
+    uint32_t domain = 0, n_rows = 0;
+    std::vector<uint32_t> point;  // 8 words per coordinate: u_col ++ u_row
+    uint8_t tag = 0;              // 0: plain evaluation
+    uint32_t eval[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t nvars() const { return (uint32_t)(point.size() / 8); }
+};
+// claim_blob (zkob_claims.cuh:104-116): length-prefixed id, comref and point, tag, eval
+inline std::vector<uint8_t> claim_blob(const Claim& c) {
+    std::vector<uint8_t> b;
+    put_u32(b, (uint32_t)c.id.size());
+    put_bytes(b, c.id.data(), c.id.size());
+    put_u32(b, (uint32_t)c.comref.size());
+    put_bytes(b, c.comref.data(), c.comref.size());
+    put_u32(b, c.domain);
+    put_u32(b, c.n_rows);
+    put_u32(b, c.nvars());
+    put_bytes(b, c.point.data(), c.point.size() * 4);
+    b.push_back(c.tag);
+    put_bytes(b, c.eval, 32);
+    return b;
+}
+struct Reader {
+    const std::vector<uint8_t>& b;
+    size_t off = 0;
+    explicit Reader(const std::vector<uint8_t>& bytes) : b(bytes) {}
+    void bytes(void* p, size_t n) {
+        if (off + n > b.size()) throw Err(1, "truncated file");
+        memcpy(p, b.data() + off, n);
+        off += n;
+    }
+    uint32_t u32() {
+        uint32_t v;
+        bytes(&v, 4);
+        return v;
+    }
+    std::string str(uint32_t n) {
+        std::string s(n, '\0');
+        bytes(&s[0], n);
+        return s;
+    }
+};
+inline bool file_exists(const std::string& path) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (f) fclose(f);
+    return f != nullptr;
+}
+// claims_parse (zkob_claims.cuh:171-194); committed (tag 1) claims are not provided
+inline std::vector<Claim> claims_load(const std::string& path) {
+    std::vector<uint8_t> bytes = read_all(path);
+    Reader r(bytes);
+    char magic[4];
+    r.bytes(magic, 4);
+    if (memcmp(magic, "ZKCL", 4)) throw Err(1, "claims: bad magic");
+    if (r.u32() != 1) throw Err(1, "claims: bad version");
+    std::vector<Claim> cs(r.u32());
+    for (auto& c : cs) {
+        c.id = r.str(r.u32());
+        c.comref = r.str(r.u32());
+        c.domain = r.u32();
+        c.n_rows = r.u32();
+        const uint32_t np = r.u32();
+        if (np > 64) throw Err(1, "claims: point too long");
+        c.point.resize((size_t)np * 8);
+        r.bytes(c.point.data(), (size_t)np * 32);
+        r.bytes(&c.tag, 1);
+        if (c.tag == 1) throw Err(2, "claims: committed evaluations are not provided");
+        if (c.tag != 0) throw Err(1, "claims: unknown EvalVar tag");
+        r.bytes(c.eval, 32);
+    }
+    if (r.off != bytes.size()) throw Err(1, "claims: trailing bytes");
+    return cs;
+}
+inline void claims_save(const std::string& path, const std::vector<Claim>& cs) {
+    std::vector<uint8_t> b;
+    put_bytes(b, "ZKCL", 4);
+    put_u32(b, 1);
+    put_u32(b, (uint32_t)cs.size());
+    for (const auto& c : cs) {
+        std::vector<uint8_t> cb = claim_blob(c);
+        put_bytes(b, cb.data(), cb.size());
+    }
+    write_all(path, b.data(), b.size());
+}
+// claim_emit (zkob_claims.cuh:225-231): append to <accdir>/claims.bin
+inline void claim_emit(const std::string& accdir, const Claim& c) {
+    const std::string path = accdir + "/claims.bin";
+    std::vector<Claim> cs;
+    if (file_exists(path)) cs = claims_load(path);
+    cs.push_back(c);
+    claims_save(path, cs);
+}
+// witref_emit (zkob_claims.cuh:233-244): one "comref\twitpath" line per distinct tensor
+inline void witref_emit(const std::string& accdir, const std::string& comref, const std::string& witpath) {
+    const std::string path = accdir + "/witrefs.txt";
+    if (file_exists(path)) {
+        std::vector<uint8_t> b = read_all(path);
+        if (std::string((const char*)b.data(), b.size()).find(comref + "\t") != std::string::npos) return;
+    }
+    FILE* f = fopen(path.c_str(), "ab");
+    if (!f) throw Err(1, "cannot open " + path);
+    fprintf(f, "%s\t%s\n", comref.c_str(), witpath.c_str());
+    fclose(f);
+}
+struct DrvState {
+    std::string id;
+    uint8_t state[32];
+};
+inline std::vector<DrvState> drvstates_load(const std::string& path) {
+    std::vector<uint8_t> bytes = read_all(path);
+    Reader r(bytes);
+    char magic[4];
+    r.bytes(magic, 4);
+    if (memcmp(magic, "ZKDS", 4)) throw Err(1, "drvstates: bad magic");
+    if (r.u32() != 1) throw Err(1, "drvstates: bad version");
+    std::vector<DrvState> ds(r.u32());
+    for (auto& d : ds) {
+        d.id = r.str(r.u32());
+        r.bytes(d.state, 32);
+    }
+    return ds;
+}
+// drvstate_emit (zkob_claims.cuh:259-270): append (id, transcript state) to drvstates.bin
+inline void drvstate_emit(const std::string& accdir, const std::string& id, const uint8_t st[32]) {
+    const std::string path = accdir + "/drvstates.bin";
+    std::vector<DrvState> ds;
+    if (file_exists(path)) ds = drvstates_load(path);
+    DrvState d;
+    d.id = id;
+    memcpy(d.state, st, 32);
+    ds.push_back(d);
+    std::vector<uint8_t> b;
+    put_bytes(b, "ZKDS", 4);
+    put_u32(b, 1);
+    put_u32(b, (uint32_t)ds.size());
+    for (const auto& e : ds) {
+        put_u32(b, (uint32_t)e.id.size());
+        put_bytes(b, e.id.data(), e.id.size());
+        put_bytes(b, e.state, 32);
+    }
+    write_all(path, b.data(), b.size());
+}
+// FrTensor::save of a device tensor: raw 8-word entries
+inline void save_fr(const std::string& path, const zkh_tensor* t) {
+    std::vector<uint32_t> v((size_t)zkh_tensor_size(t) * 8);
+    chk(zkh_tensor_to_fr(g_ctx, t, v.data()), "to_fr");
+    write_all(path, v.data(), v.size() * 4);
+}
+
 }  // namespace zkhcli

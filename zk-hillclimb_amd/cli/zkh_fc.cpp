@@ -13,15 +13,26 @@
 // a_final: write_ipa, vrf_common.cuh:284-289), and the optional int64 Y (save_long).
 // Input files: int32 arrays (load_int_tensor, zkob_fc.cu:178-185) and raw point arrays
 // (Commitment(filename), g1-tensor.cu:179-183); Q is the first point of q.bin.
-// The claim, weight-privacy and activation-privacy modes, `verify` and `selftest` are not
-// provided: such a request fails with exit status 2 and a message.
+// `--claims <accdir> <obid> <com_W>` is the claim mode (zkob_fc.cu:449-470): the IPAs are
+// replaced by three claims appended to <accdir>/claims.bin (ids <obid>:W, :X, :Y; comrefs
+// <com_W>, <obdir>/com_X.bin, <obdir>/com_Y.bin), the padded witnesses saved as
+// <accdir>/wit_<obid>_{W,X,Y}.fr with their witrefs.txt lines, and the transcript state in
+// drvstates.bin; zkh_batchopen later opens them all in one batch.  The weight-privacy and
+// activation-privacy modes, `verify` and `selftest` are not provided: such a request fails
+// with exit status 2 and a message.
 #include "common.hpp"
 
 using namespace zkhcli;
 
 namespace {
 
-int do_prove(const std::vector<std::string>& a) {
+// --claims <accdir> <obid> <registered-com_W-path> (zkob_fc.cu:1224-1228)
+struct ClaimMode {
+    std::string accdir, obid, comW;
+    bool on() const { return !accdir.empty(); }
+};
+
+int do_prove(const std::vector<std::string>& a, const ClaimMode& cm) {
     const std::string obdir = a[0], seed = a[1];
     const uint32_t B = parse_u32(a[4].c_str()), IN = parse_u32(a[5].c_str()), OUT = parse_u32(a[6].c_str());
     const uint32_t INp = 1u << ceil_log2(IN), OUTp = 1u << ceil_log2(OUT);
@@ -76,6 +87,37 @@ int do_prove(const std::vector<std::string>& a) {
     sc.insert(sc.end(), (uint8_t*)claims.data(), (uint8_t*)claims.data() + 96);
     write_all(obdir + "/sumcheck.bin", sc.data(), sc.size());
 
+    if (cm.on()) {  // claim emission in place of the IPAs, order W, X, Y (zkob_fc.cu:449-470)
+        const std::string witW = cm.accdir + "/wit_" + cm.obid + "_W.fr", witX = cm.accdir + "/wit_" + cm.obid + "_X.fr",
+                          witY = cm.accdir + "/wit_" + cm.obid + "_Y.fr";
+        save_fr(witW, Wp.t);
+        save_fr(witX, Xp.t);
+        save_fr(witY, Yp.t);
+        auto mk = [&](const char* tensor, const std::string& comref, uint32_t domain, uint32_t n_rows,
+                      const std::vector<uint32_t>& ucol, uint32_t ncol, const std::vector<uint32_t>& urow,
+                      uint32_t nrow, const uint32_t* eval) {
+            Claim c;
+            c.id = cm.obid + ":" + tensor;
+            c.comref = comref;
+            c.domain = domain;
+            c.n_rows = n_rows;
+            c.point.assign(ucol.begin(), ucol.begin() + 8 * (size_t)ncol);
+            c.point.insert(c.point.end(), urow.begin(), urow.begin() + 8 * (size_t)nrow);
+            memcpy(c.eval, eval, 32);
+            claim_emit(cm.accdir, c);
+        };
+        const uint32_t Bp = 1u << lb;
+        mk("W", cm.comW, OUTp, INp, uo, lo, ui, L, claims.data() + 16);
+        witref_emit(cm.accdir, cm.comW, witW);
+        mk("X", obdir + "/com_X.bin", INp, Bp, ui, L, ub, lb, claims.data() + 8);
+        witref_emit(cm.accdir, obdir + "/com_X.bin", witX);
+        mk("Y", obdir + "/com_Y.bin", OUTp, Bp, uo, lo, ub, lb, claims.data());
+        witref_emit(cm.accdir, obdir + "/com_Y.bin", witY);
+        drvstate_emit(cm.accdir, cm.obid, st);
+        printf("PROVED matmul obligation (claim mode, 3 claims emitted) -> %s\n", obdir.c_str());
+        return 0;
+    }
+
     // IPA openings, order W, X, Y (zkob_fc.cu:473-483)
     Tensor aW, bW, aX, bX, aY;
     chk(zkh_partial_me_window(g_ctx, Wp.t, ui.data(), L, OUTp, &aW.t), "W.partial_me");
@@ -111,15 +153,27 @@ int do_commit(const std::vector<std::string>& a) {
 int run1(const std::vector<std::string>& args) {
     const std::string mode = args.empty() ? "" : args[0];
     std::vector<std::string> rest(args.begin() + (args.empty() ? 0 : 1), args.end());
+    ClaimMode cm;
+    for (size_t i = 0; i < rest.size(); i++) {
+        if (rest[i] != "--claims") continue;
+        if (i + 4 > rest.size()) throw Err(1, "--claims needs <accdir> <obid> <com_W>");
+        cm.accdir = rest[i + 1];
+        cm.obid = rest[i + 2];
+        cm.comW = rest[i + 3];
+        rest.erase(rest.begin() + i, rest.begin() + i + 4);
+        break;
+    }
+    if (cm.on() && mode != "prove") throw Err(1, "--claims applies to prove only");
     reject_flags(rest, "zkh_fc");
     const bool prove = mode == "prove" && (rest.size() == 10 || rest.size() == 11);
     const bool commit = mode == "commit" && rest.size() == 5;
     if (prove || commit) {
         need_ctx();
-        return prove ? do_prove(rest) : do_commit(rest);
+        return prove ? do_prove(rest, cm) : do_commit(rest);
     }
     fprintf(stderr,
-            "usage: zkh_fc prove <obdir> <seed> <X> <W> <B> <IN> <OUT> <gen_in> <gen_out> <q> [Y-out] | "
+            "usage: zkh_fc prove <obdir> <seed> <X> <W> <B> <IN> <OUT> <gen_in> <gen_out> <q> [Y-out] "
+            "[--claims <accdir> <obid> <com_W>] | "
             "commit <W> <IN> <OUT> <gen_out> <com_out> | serve\n");
     return 2;
 }

@@ -270,6 +270,25 @@ __global__ __launch_bounds__(NT) void k_sum_planes(const uint4* alo, const uint4
         acc[0] = fr_add(acc[0], ld_fr(alo, ahi, i));
     reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
+// degree-2 product round over MSB pairs (k_bo_hp2 + bo_dev_sum, zkob_claims.cuh:367-383,
+// :577-592): sums of a_t[i] b_t[i] for t = 0, 1, 2, X_t = X[i] + t (X[i+h] - X[i])
+__global__ __launch_bounds__(NT) void k_prod_round(const uint4* alo, const uint4* ahi, const uint4* blo,
+                                                   const uint4* bhi, uint32_t h, Publish pub) {
+    fr_t acc[3] = {fr_zero(), fr_zero(), fr_zero()};
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        const fr_t a0 = ld_fr(alo, ahi, i), a1 = ld_fr(alo, ahi, i + h);
+        const fr_t b0 = ld_fr(blo, bhi, i), b1 = ld_fr(blo, bhi, i + h);
+        acc[0] = fr_add(acc[0], mont_mul(a0, b0));
+        acc[1] = fr_add(acc[1], mont_mul(a1, b1));
+        acc[2] = fr_add(acc[2], mont_mul(fr_sub(fr_add(a1, a1), a0), fr_sub(fr_add(b1, b1), b0)));
+    }
+    reduce_publish<3>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+}
+uint32_t launch_prod_round(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t h, Publish pub) {
+    uint32_t g = grid_for(h, NT * 4, 1024);
+    k_prod_round<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), h, pub);
+    return g;
+}
 uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub) {
     uint32_t g = grid_for(n, NT * 4, 1024);
     k_dot_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n, pub);

@@ -65,6 +65,8 @@ void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, 
 // ---- dot products / sums (block partials, AoS, summed on the host) ----
 // partial[b] = sum montmul(a_i, b_i) over the block's range (carries 2^-256)
 uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub);
+// sums of a_t b_t over MSB pairs for t = 0, 1, 2 (three published sums)
+uint32_t launch_prod_round(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t h, Publish pub);
 uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, Publish pub);
 
 // ---- generic MLE pieces ----

@@ -921,6 +921,43 @@ extern "C" int zkh_sum(zkh_ctx* c, const zkh_tensor* t, uint32_t out[8]) {
     fr_store(s, out);
     return ZKH_OK;
 }
+extern "C" int zkh_prod_round(zkh_ctx* c, const zkh_tensor* a, const zkh_tensor* b, uint32_t out[24]) {
+    if (!c || !a || !b || !out) return fail(c, ZKH_EARG, "null argument");
+    if (a->kind != ZKH_KIND_FR || b->kind != ZKH_KIND_FR || a->n != b->n || a->n < 2 || (a->n & 1))
+        return fail(c, ZKH_EARG, "prod_round needs two FR tensors of one even size");
+    HIPCHK(c, hipSetDevice(c->device));
+    Publish pb = make_pub(c, 1);
+    launch_prod_round(c->stream, a->planes(), b->planes(), a->n / 2, pb);
+    int rc;
+    if ((rc = wait_pub(c, pb.seq))) return rc;
+    Fr s[3];
+    pub_read(c, 0, 3, s);
+    // each sum carries 2^-256 (Montgomery products of plain values)
+    for (int t = 0; t < 3; t++) fr_store(fr_mont_mul(s[t], kR2), out + 8 * t);
+    return ZKH_OK;
+}
+extern "C" int zkh_fr_scalar(const uint32_t a[8], const uint32_t b[8], int op, uint32_t out[8]) {
+    if (!a || !out || (op != 3 && !b) || op < 0 || op > 3) return ZKH_EARG;
+    if (!fr_is_canonical(a) || (op != 3 && !fr_is_canonical(b))) return ZKH_EARG;
+    const Fr x = fr_load(a);
+    Fr r;
+    switch (op) {
+        case 0: r = fr_add(x, fr_load(b)); break;
+        case 1: r = fr_sub(x, fr_load(b)); break;
+        case 2: r = fr_mul(x, fr_load(b)); break;
+        default: r = fr_inv(x); break;
+    }
+    fr_store(r, out);
+    return ZKH_OK;
+}
+extern "C" int zkh_sha256(const void* data, size_t n, uint8_t out[32]) {
+    if ((!data && n) || !out) return ZKH_EARG;
+    Sha256 h;
+    h.init();
+    h.update(data, n);
+    h.final(out);
+    return ZKH_OK;
+}
 extern "C" int zkh_me(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u, uint32_t k,
                       uint32_t out[8]) {
     if (!c || !t || !out || (!u && k)) return fail(c, ZKH_EARG, "null argument");
