@@ -256,10 +256,11 @@ def setup_dirs(tmp):
     return acc
 
 
-def accumulate(tmp, obligations):
+def accumulate(tmp, obligations, acc=None, cs=None, ds=None, wit=None, comfiles=None):
     """run zkh_fc --claims for each (obid, X, W, comW-name) and restate what it must emit"""
-    acc = setup_dirs(tmp)
-    cs, ds, wit, comfiles = [], [], {}, {}
+    if acc is None:
+        acc = setup_dirs(tmp)
+        cs, ds, wit, comfiles = [], [], {}, {}
     for obid, X, W, wname in obligations:
         comW = os.path.join(tmp, wname)
         obdir = os.path.join(tmp, obid)
@@ -280,7 +281,7 @@ def check_accumulator(acc, cs, ds, wit, obligations):
     assert open(os.path.join(acc, "claims.bin"), "rb").read() == claims_file(cs)
     assert open(os.path.join(acc, "drvstates.bin"), "rb").read() == drvstates_file(ds)
     lines, seen = [], set()
-    for obid, _, _, _ in obligations:
+    for obid in [o[0] for o in obligations]:
         for c in cs:
             if c["id"].startswith(obid + ":") and c["comref"] not in seen:
                 seen.add(c["comref"])
@@ -359,3 +360,83 @@ def test_batch_open_errors(tmp_path):
     assert r.returncode == 1 and "no witref" in r.stderr
     r = subprocess.run([FC, "prove", "--claims", acc], capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "--claims needs" in r.stderr
+
+
+RESCALE = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_rescale")
+
+
+def rescale_claims(seed, obid, obdir, X, log_sf, gen):
+    """zkob_rescale claim mode restated (zkob_rescale.cu:70-190): the claims on A, rem and m
+    at the logUp proof's terminal points, their witnesses and commitments, the final state."""
+    B, Cc = X.shape
+    sf = 1 << log_sf
+    Bp, Cp = pow2(B), pow2(Cc)
+    D, N = Bp * Cp, sf
+    logD, n1 = P.ceil_log2(D), P.ceil_log2(D // N)
+    rc, q, rem = C.rescale(X.reshape(-1), sf)
+    assert rc == 0
+    Xp, Xrp, remp = padded(X), padded(q.reshape(B, Cc)), padded(rem.reshape(B, Cc))
+    low = -(sf >> 1)
+    S = C.ints_to_fr(remp.reshape(-1))
+    rc, m = C.lu_prep(S, low, N)
+    assert rc == 0
+    coms = {}
+    for name, t in (("X", C.ints_to_fr(Xp.reshape(-1))), ("Xr", C.ints_to_fr(Xrp.reshape(-1))), ("rem", S),
+                    ("m", m)):
+        rc, c = C.g1_commit(gen, t, Cp)
+        coms[name] = c.tobytes()
+    st = C.tr_init(seed)
+    for lab, v in (("B", B), ("C", Cc), ("LOG_SF", log_sf)):
+        C.tr_absorb(st, lab, struct.pack("<I", v))
+    for name in ("X", "Xr", "rem", "m"):
+        C.tr_absorb(st, "com_" + name, coms[name])
+    beta = C.tr_challenge_fr(st)
+    A = C.lu_inverse(S, beta)
+    rc, c = C.g1_commit(gen, A, Cp)
+    coms["A"] = c.tobytes()
+    C.tr_absorb(st, "com_A", coms["A"])
+    alpha = C.tr_challenge_fr(st)
+    u = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, lk = C.lu_prove(st, A, S, C.range_table(low, sf, N), m, alpha, beta, u)
+    assert rc == 0
+    u_pt = ints(lk["ws"][::-1])
+    A_f, S_f, _, _, m_f = ints(lk["term"])
+    ref = {t: os.path.join(obdir, "com_%s.bin" % t) for t in ("A", "rem", "m")}
+    cs = [dict(id=obid + ":A", comref=ref["A"], domain=Cp, n_rows=Bp, point=u_pt, eval=A_f),
+          dict(id=obid + ":rem", comref=ref["rem"], domain=Cp, n_rows=Bp, point=u_pt, eval=S_f),
+          dict(id=obid + ":m", comref=ref["m"], domain=Cp, n_rows=N // Cp, point=u_pt[:logD - n1], eval=m_f)]
+    wit = {ref["A"]: ints(A), ref["rem"]: ints(S), ref["m"]: ints(m)}
+    return cs, wit, {ref[t]: coms[t] for t in ref}, bytes(st)
+
+
+@pytest.mark.parametrize("B,Cc,log_sf", [(8, 4, 4), (4, 8, 5)])
+def test_rescale_and_fc_claims_in_one_batch(tmp_path, B, Cc, log_sf):
+    """lookup-derived claims (A, rem, m of a rescaling, zkob_rescale.cu:165-190) and a
+    matmul's claims accumulated together, then opened in one batch"""
+    tmp = str(tmp_path)
+    acc = setup_dirs(tmp)
+    rng = np.random.default_rng(B + Cc + log_sf)
+    X = rng.integers(-(1 << 12), 1 << 12, size=(B, Cc)).astype(np.int64) * 37
+    obid, obdir = "L3.rescale", os.path.join(tmp, "L3.rescale")
+    os.makedirs(obdir)
+    xp = os.path.join(obdir, "X.i64")
+    X.tofile(xp)
+    seed = "run5:" + obid
+    r = subprocess.run([RESCALE, "prove", obdir, seed, xp, str(B), str(Cc), str(log_sf),
+                        os.path.join(tmp, "gen_%d.bin" % pow2(Cc)), os.path.join(tmp, "q.bin"), "--claims", acc, obid],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "claim mode, 3 claims emitted" in r.stdout
+    assert not os.path.exists(os.path.join(obdir, "ipa_A.bin"))
+    cs, wit, comfiles, state = rescale_claims(seed, obid, obdir, X, log_sf, GENS[pow2(Cc)])
+    ds = [(obid, state)]
+    X1, W1 = rng_mats(6, 4, 8, 4)
+    obs = [("L3.fc", X1, W1, "comW.bin")]
+    acc, cs, ds, wit, comfiles = accumulate(tmp, obs, acc, cs, ds, wit, comfiles)
+    check_accumulator(acc, cs, ds, wit, [(obid,)] + obs)
+    r = run_bo(acc, tmp, "run5", (4, 8))
+    assert r.returncode == 0, r.stderr
+    assert "(6 claims, 6 tensors, 2 domains)" in r.stdout
+    want = batch_expected(cs, ds, wit, comfiles, "run5", GENS, Q2[0])
+    for name, data in want.items():
+        assert open(os.path.join(acc, name), "rb").read() == data, name

@@ -181,6 +181,17 @@ inline int driver_main(int argc, char** argv, int (*run1)(const std::vector<std:
 inline void need_ctx() {
     if (!g_ctx && zkh_ctx_create(0, &g_ctx) != ZKH_OK) throw Err(1, "no GPU context");
 }
+// removes "--claims" and the nargs arguments after it from rest; returns them (empty: absent)
+inline std::vector<std::string> take_claims(std::vector<std::string>& rest, size_t nargs) {
+    for (size_t i = 0; i < rest.size(); i++) {
+        if (rest[i] != "--claims") continue;
+        if (i + 1 + nargs > rest.size()) throw Err(1, "--claims needs " + std::to_string(nargs) + " arguments");
+        std::vector<std::string> out(rest.begin() + i + 1, rest.begin() + i + 1 + nargs);
+        rest.erase(rest.begin() + i, rest.begin() + i + 1 + nargs);
+        return out;
+    }
+    return {};
+}
 inline void reject_flags(const std::vector<std::string>& rest, const char* drv) {
     for (const auto& s : rest)
         if (s.rfind("--", 0) == 0) throw Err(2, std::string(drv) + ": " + s + " (claim and privacy modes) is not provided");

@@ -10,15 +10,18 @@
 // their first log N), writing dims.bin (B, C, LOG_SF), com_X.bin, com_Xr.bin, com_rem.bin,
 // com_m.bin, com_A.bin, lookup.bin (count-prefixed evals, then A_f, S_f, m_f: write_lookup,
 // zkob_lookup.cuh:80-87), ipa_A.bin, ipa_rem.bin, ipa_m.bin and the optional int32 Xr
-// (save_int), byte-identical to the reference's.  The claim mode, `verify` and `selftest`
-// answer exit status 2.
+// (save_int), byte-identical to the reference's.  With `--claims <accdir> <obid>` (claim
+// mode, zkob_rescale.cu:165-190) the three openings become claims <obid>:A, :rem, :m in
+// <accdir>/claims.bin, with their witness files, witrefs.txt lines and the transcript state
+// in drvstates.bin, for zkh_batchopen.  `verify` and `selftest` answer exit status 2.
 #include "common.hpp"
 
 using namespace zkhcli;
 
 namespace {
 
-int do_prove(const std::vector<std::string>& a) {
+// claim_args: empty, or {accdir, obid} of the claim mode
+int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& claim_args) {
     const std::string obdir = a[0], seed = a[1];
     const uint32_t B = parse_u32(a[3].c_str()), C = parse_u32(a[4].c_str());
     const uint32_t log_sf = (uint32_t)strtoul(a[5].c_str(), nullptr, 10);
@@ -96,6 +99,33 @@ int do_prove(const std::vector<std::string>& a) {
     std::vector<uint32_t> u_pt((size_t)logD * 8);
     for (uint32_t i = 0; i < logD; i++) memcpy(u_pt.data() + 8 * i, ws.data() + 8 * (logD - 1 - i), 32);
     std::vector<uint32_t> u_m(u_pt.begin(), u_pt.begin() + 8 * (size_t)(logD - n1));
+    if (!claim_args.empty()) {  // claim emission in place of the IPAs, order A, rem, m (zkob_rescale.cu:165-190)
+        const std::string &accdir = claim_args[0], &obid = claim_args[1];
+        const std::string witA = accdir + "/wit_" + obid + "_A.fr", witR = accdir + "/wit_" + obid + "_rem.fr",
+                          witM = accdir + "/wit_" + obid + "_m.fr";
+        save_fr(witA, A.t);
+        save_fr(witR, remp.t);
+        save_fr(witM, m.t);
+        auto mk = [&](const char* tensor, uint32_t n_rows, const std::vector<uint32_t>& pt, const uint32_t* eval) {
+            Claim c;
+            c.id = obid + ":" + tensor;
+            c.comref = obdir + "/com_" + tensor + ".bin";
+            c.domain = Cp;
+            c.n_rows = n_rows;
+            c.point = pt;
+            memcpy(c.eval, eval, 32);
+            claim_emit(accdir, c);
+        };
+        mk("A", Bp, u_pt, term.data());
+        witref_emit(accdir, obdir + "/com_A.bin", witA);
+        mk("rem", Bp, u_pt, term.data() + 8);
+        witref_emit(accdir, obdir + "/com_rem.bin", witR);
+        mk("m", N / Cp, u_m, term.data() + 32);
+        witref_emit(accdir, obdir + "/com_m.bin", witM);
+        drvstate_emit(accdir, obid, st);
+        printf("PROVED rescaling obligation (claim mode, 3 claims emitted) -> %s\n", obdir.c_str());
+        return 0;
+    }
     open_prove(A.t, Cp, g.g, q.data(), u_pt, obdir + "/ipa_A.bin", st);
     open_prove(remp.t, Cp, g.g, q.data(), u_pt, obdir + "/ipa_rem.bin", st);
     open_prove(m.t, Cp, g.g, q.data(), u_m, obdir + "/ipa_m.bin", st);
@@ -106,12 +136,15 @@ int do_prove(const std::vector<std::string>& a) {
 int run1(const std::vector<std::string>& args) {
     const std::string mode = args.empty() ? "" : args[0];
     std::vector<std::string> rest(args.begin() + (args.empty() ? 0 : 1), args.end());
+    const std::vector<std::string> cm = take_claims(rest, 2);  // --claims <accdir> <obid> (zkob_rescale.cu:528-532)
     reject_flags(rest, "zkh_rescale");
     if (mode == "prove" && (rest.size() == 8 || rest.size() == 9)) {
         need_ctx();
-        return do_prove(rest);
+        return do_prove(rest, cm);
     }
-    fprintf(stderr, "usage: zkh_rescale prove <obdir> <seed> <X-int64> <B> <C> <LOG_SF> <gen> <q> [Xr-out] | serve\n");
+    fprintf(stderr,
+            "usage: zkh_rescale prove <obdir> <seed> <X-int64> <B> <C> <LOG_SF> <gen> <q> [Xr-out] "
+            "[--claims <accdir> <obid>] | serve\n");
     return 2;
 }
 
