@@ -440,3 +440,96 @@ def test_rescale_and_fc_claims_in_one_batch(tmp_path, B, Cc, log_sf):
     want = batch_expected(cs, ds, wit, comfiles, "run5", GENS, Q2[0])
     for name, data in want.items():
         assert open(os.path.join(acc, name), "rb").read() == data, name
+
+
+ROPE = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_rope")
+
+
+def rope_claims(seed, obid, obdir, Th, HD, cosT, sinT, gen):
+    """zkob_rope claim mode restated (zkob_rope.cu:102-304): the weights and the flipped T by
+    their definitions, the two Hadamard sumchecks from the oracle, and the claims T1 (at the
+    first terminal point), T2 (at the second, its coordinate log2(HD)-1 complemented) and Y
+    (at u), both T claims on the one tensor com_T.bin."""
+    B, Cc = Th.shape
+    Cp = pow2(Cc)
+    logD = P.ceil_log2(B) + P.ceil_log2(Cp)
+    flipv, fb = HD // 2, P.ceil_log2(HD) - 1
+    W1, W2, Tg = (np.zeros((B, Cp), np.int64) for _ in range(3))
+    for t in range(B):
+        for e in range(Cc):
+            W1[t, e] = cosT[t, e % HD]
+            W2[t, e] = (1 if e & flipv else -1) * sinT[t, e % HD]
+            Tg[t, e] = Th[t, e]
+    Txg = Tg[:, [e ^ flipv for e in range(Cp)]]
+    Y = Tg * W1 + Txg * W2
+    T_fr, Tx_fr, Y_fr = (C.ints_to_fr(M.reshape(-1)) for M in (Tg, Txg, Y))
+    ones = C.ints_to_fr([1] * (B * Cp))
+    comT, comY = (C.g1_commit(gen, t, Cp)[1].tobytes() for t in (T_fr, Y_fr))
+    st = C.tr_init(seed)
+    for lab, v in (("B", B), ("C", Cc), ("HD", HD), ("SCALE_R", 16)):
+        C.tr_absorb(st, lab, struct.pack("<I", v))
+    C.tr_absorb(st, "com_T", comT)
+    C.tr_absorb(st, "com_Y64", comY)
+    u = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, ev = C.me(Y_fr, u)
+    C.tr_absorb(st, "ev", ev.tobytes())
+    Eu = ints(C.build_eq(u))
+    refT, refY = os.path.join(obdir, "com_T.bin"), os.path.join(obdir, "com_Y64.bin")
+    cs = []
+    for k, (W, S_fr, S_int) in enumerate(((W1, T_fr, Tg), (W2, Tx_fr, Txg)), start=1):
+        E = [e * int(w) % R for e, w in zip(Eu, W.reshape(-1))]
+        c = sum(e * int(s) for e, s in zip(E, S_int.reshape(-1))) % R
+        C.tr_absorb(st, "c%d" % k, fr_bytes(c))
+        rc, hp = C.hp_prove(st, np.array(P.to_limbs(c), np.uint32), C.ints_to_fr(E), S_fr, ones)
+        assert rc == 0
+        C.tr_absorb(st, "S_f2", hp["term"][0].tobytes())
+        C.tr_absorb(st, "U_f2", hp["term"][1].tobytes())
+        pt = ints(hp["ws"][::-1])
+        if k == 2:
+            pt[fb] = (1 - pt[fb]) % R
+        cs.append(dict(id="%s:T%d" % (obid, k), comref=refT, domain=Cp, n_rows=B, point=pt,
+                       eval=ints(hp["term"][0])[0]))
+    cs.append(dict(id=obid + ":Y", comref=refY, domain=Cp, n_rows=B, point=ints(u), eval=ints(ev)[0]))
+    wit = {refT: Tg.reshape(-1), refY: Y.reshape(-1)}
+    return cs, wit, {refT: comT, refY: comY}, bytes(st)
+
+
+@pytest.mark.parametrize("B,Cc,HD", [(8, 6, 2), (4, 8, 4)])
+def test_rope_and_fc_claims_in_one_batch(tmp_path, B, Cc, HD):
+    """a RoPE obligation's three claims (two on one tensor, zkob_rope.cu:250-304) and a
+    matmul's accumulated together, then opened in one batch"""
+    tmp = str(tmp_path)
+    acc = setup_dirs(tmp)
+    rng = np.random.default_rng(2027 + B * 100 + Cc * 10 + HD)
+    cosT = rng.integers(-128, 129, size=(B, HD)).astype(np.int32)
+    sinT = rng.integers(-128, 129, size=(B, HD)).astype(np.int32)
+    Th = rng.integers(-128, 129, size=(B, Cc)).astype(np.int32)
+    obid, obdir = "L4.rope_q", os.path.join(tmp, "L4.rope_q")
+    os.makedirs(obdir)
+    paths = {}
+    for name, arr in (("T", Th), ("cos", cosT), ("sin", sinT)):
+        paths[name] = os.path.join(obdir, name + ".in")
+        np.ascontiguousarray(arr).tofile(paths[name])
+    seed = "run6:" + obid
+    r = subprocess.run([ROPE, "prove", obdir, seed, paths["T"], str(B), str(Cc), str(HD), paths["cos"], paths["sin"],
+                        os.path.join(tmp, "gen_%d.bin" % pow2(Cc)), os.path.join(tmp, "q.bin"), "--claims", acc, obid],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "claim mode, 3 claims emitted" in r.stdout
+    assert not os.path.exists(os.path.join(obdir, "ipa_T1.bin"))
+    cs, wit, comfiles, state = rope_claims(seed, obid, obdir, Th, HD, cosT, sinT, GENS[pow2(Cc)])
+    ds = [(obid, state)]
+    X1, W1 = rng_mats(7, 2, 4, 8)
+    obs = [("L4.fc", X1, W1, "comW.bin")]
+    acc, cs, ds, wit, comfiles = accumulate(tmp, obs, acc, cs, ds, wit, comfiles)
+    assert open(os.path.join(acc, "claims.bin"), "rb").read() == claims_file(cs)
+    assert open(os.path.join(acc, "drvstates.bin"), "rb").read() == drvstates_file(ds)
+    for t, ref in (("T", cs[0]["comref"]), ("Y", cs[2]["comref"])):
+        wpath = os.path.join(acc, "wit_%s_%s.fr" % (obid, t))
+        assert open(wpath, "rb").read() == C.ints_to_fr(wit[ref]).tobytes()
+    r = run_bo(acc, tmp, "run6", (4, 8))
+    assert r.returncode == 0, r.stderr
+    assert "(6 claims, 5 tensors, 2 domains)" in r.stdout
+    want = batch_expected(cs, ds, wit, comfiles, "run6", GENS, Q2[0])
+    for name, data in want.items():
+        assert open(os.path.join(acc, name), "rb").read() == data, name

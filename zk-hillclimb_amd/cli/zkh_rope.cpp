@@ -11,7 +11,10 @@
 // with coordinate log2(HD)-1 replaced by its complement) and of Y64 at u.  Files,
 // byte-identical to the reference's: dims.bin (B, C, HD, 16), com_T.bin, com_Y64.bin,
 // ev.bin, hp1.bin, hp2.bin, ipa_T1.bin, ipa_T2.bin, ipa_Y.bin and the optional unpadded
-// int64 Y64.  The claim mode, `verify` and `selftest` answer exit status 2.
+// int64 Y64.  With `--claims <accdir> <obid>` (claim mode, zkob_rope.cu:250-304) the openings
+// become claims <obid>:T1, :T2 (both on com_T.bin) and :Y in <accdir>/claims.bin, with the
+// witness files, witrefs.txt lines and the transcript state, for zkh_batchopen.  `verify` and
+// `selftest` answer exit status 2.
 #include <stdlib.h>
 
 #include "common.hpp"
@@ -72,7 +75,8 @@ void hp_file(const std::string& path, const uint32_t claim[8], const std::vector
     write_all(path, out.data(), out.size());
 }
 
-int do_prove(const std::vector<std::string>& a) {
+// claim_args: empty, or {accdir, obid} of the claim mode
+int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& claim_args) {
     const std::string obdir = a[0], seed = a[1];
     const uint32_t B = parse_u32(a[3].c_str()), C = parse_u32(a[4].c_str()), HD = parse_u32(a[5].c_str());
     const uint32_t Cp = 1u << ceil_log2(C);
@@ -162,7 +166,27 @@ int do_prove(const std::vector<std::string>& a) {
     hp_file(obdir + "/hp1.bin", c1, hev, logD, hterm.data());
     std::vector<uint32_t> pt((size_t)logD * 8);
     for (uint32_t i = 0; i < logD; i++) memcpy(pt.data() + 8 * i, hws.data() + 8 * (logD - 1 - i), 32);
-    open_prove(tT.t, Cp, g.g, q.data(), pt, obdir + "/ipa_T1.bin", st);
+    // claim mode (zkob_rope.cu:250-268, :296-304): claims T1 (here), T2 and Y replace the IPAs
+    const bool claim_mode = !claim_args.empty();
+    auto mk_claim = [&](const char* tensor, const char* com, const std::vector<uint32_t>& point,
+                        const uint32_t* eval) {
+        Claim c;
+        c.id = claim_args[1] + ":" + tensor;
+        c.comref = obdir + "/" + com;
+        c.domain = Cp;
+        c.n_rows = B;
+        c.point = point;
+        memcpy(c.eval, eval, 32);
+        claim_emit(claim_args[0], c);
+    };
+    if (claim_mode) {
+        const std::string witT = claim_args[0] + "/wit_" + claim_args[1] + "_T.fr";
+        save_fr(witT, tT.t);
+        mk_claim("T1", "com_T.bin", pt, hterm.data());
+        witref_emit(claim_args[0], obdir + "/com_T.bin", witT);
+    } else {
+        open_prove(tT.t, Cp, g.g, q.data(), pt, obdir + "/ipa_T1.bin", st);
+    }
 
     // hadamard 2: E = eq(u).W2, S = column-flipped T, U = 1
     chk(zkh_hadamard(g_ctx, Eu.t, tW2.t, &E2.t), "E2");
@@ -177,6 +201,16 @@ int do_prove(const std::vector<std::string>& a) {
     hp_file(obdir + "/hp2.bin", c2, hev, logD, hterm.data());
     for (uint32_t i = 0; i < logD; i++) memcpy(pt.data() + 8 * i, hws.data() + 8 * (logD - 1 - i), 32);
     one_minus(pt.data() + 8 * fb, pt.data() + 8 * fb);  // rotate_half: T~(pt2') = Tx~(pt2)
+    if (claim_mode) {
+        mk_claim("T2", "com_T.bin", pt, hterm.data());
+        const std::string witY = claim_args[0] + "/wit_" + claim_args[1] + "_Y.fr";
+        save_fr(witY, tY.t);
+        mk_claim("Y", "com_Y64.bin", u, ev);
+        witref_emit(claim_args[0], obdir + "/com_Y64.bin", witY);
+        drvstate_emit(claim_args[0], claim_args[1], st);
+        printf("PROVED rope obligation (claim mode, 3 claims emitted) -> %s\n", obdir.c_str());
+        return 0;
+    }
     open_prove(tT.t, Cp, g.g, q.data(), pt, obdir + "/ipa_T2.bin", st);
     open_prove(tY.t, Cp, g.g, q.data(), u, obdir + "/ipa_Y.bin", st);
     printf("PROVED rope obligation -> %s\n", obdir.c_str());
@@ -186,12 +220,15 @@ int do_prove(const std::vector<std::string>& a) {
 int run1(const std::vector<std::string>& args) {
     const std::string mode = args.empty() ? "" : args[0];
     std::vector<std::string> rest(args.begin() + (args.empty() ? 0 : 1), args.end());
+    const std::vector<std::string> claim_args = take_claims(rest, 2);  // --claims <accdir> <obid>
     reject_flags(rest, "zkh_rope");
     if (mode == "prove" && (rest.size() == 10 || rest.size() == 11)) {
         need_ctx();
-        return do_prove(rest);
+        return do_prove(rest, claim_args);
     }
-    fprintf(stderr, "usage: zkh_rope prove <obdir> <seed> <T> <B> <C> <HD> <cos> <sin> <gen> <q> [Y64-out] | serve\n");
+    fprintf(stderr,
+            "usage: zkh_rope prove <obdir> <seed> <T> <B> <C> <HD> <cos> <sin> <gen> <q> [Y64-out] "
+            "[--claims <accdir> <obid>] | serve\n");
     return 2;
 }
 
