@@ -16,7 +16,15 @@
 //       r[logG..vars_j)), b = me_weights(r[0..logG)), an IPA over the domain's generators.
 // Files, byte-identical to the reference's: batch_sumcheck.bin ("ZKBS", n_claims, m_max,
 // count-prefixed evals), batch_vfin.bin ("ZKBV", count-prefixed terminals),
-// ipa_batch_<G>.bin.  `verify`, `genq` and `selftest` answer exit status 2.
+// ipa_batch_<G>.bin.  With ZKOB_PROF set it prints the reference's lap lines
+// ("PROF batch_prove.{setup,rounds,terminal,ipa} <s> s").  `verify`, `genq` and `selftest`
+// answer exit status 2.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <chrono>
 #include <map>
 #include <set>
 
@@ -65,6 +73,24 @@ std::vector<TensorInfo> derive_tensors(const std::vector<Claim>& cs) {
     return out;
 }
 
+// witnesses kept on the device between the rounds and G5 up to this many bytes in total
+constexpr uint64_t kResidentMax = 32ull << 30;
+
+// BoTimer (zkob_claims.cuh:62-75): with ZKOB_PROF set, "PROF batch_prove.<lap> <s> s" per lap,
+// after the device has finished the lap's work
+struct Laps {
+    const bool on = getenv("ZKOB_PROF") != nullptr;
+    std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+    void lap(const char* what) {
+        if (on) {
+            zkh_ctx_sync(g_ctx);
+            printf("PROF batch_prove.%s %.4f s\n", what,
+                   std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
+        }
+        t0 = std::chrono::steady_clock::now();
+    }
+};
+
 std::map<std::string, std::string> witrefs_load(const std::string& accdir) {
     std::map<std::string, std::string> m;
     std::vector<uint8_t> b = read_all(accdir + "/witrefs.txt");
@@ -91,10 +117,21 @@ Fr8 kappa(uint32_t vars, const std::vector<Fr8>& r) {  // prod_{v >= vars} (1 - 
     return k;
 }
 
+// FrTensor(witpath) (fr-tensor.cu:190-197): the raw 32-byte entries, mapped rather than copied
 void load_witness(const std::string& path, uint64_t n, Tensor& t) {
-    std::vector<uint8_t> b = read_all(path);
-    if (b.size() != n * 32) throw Err(1, "batch_prove: witness size mismatch for " + path);
-    chk(zkh_tensor_from_fr(g_ctx, (const uint32_t*)b.data(), (uint32_t)n, &t.t), "witness");
+    const int fd = open(path.c_str(), O_RDONLY);
+    if (fd < 0) throw Err(1, "cannot open " + path);
+    struct stat sb;
+    if (fstat(fd, &sb) != 0 || (uint64_t)sb.st_size != n * 32 || n == 0) {
+        close(fd);
+        throw Err(1, "batch_prove: witness size mismatch for " + path);
+    }
+    void* p = mmap(nullptr, n * 32, PROT_READ, MAP_PRIVATE | MAP_POPULATE, fd, 0);
+    close(fd);
+    if (p == MAP_FAILED) throw Err(1, "cannot map " + path);
+    const int rc = zkh_tensor_from_fr(g_ctx, (const uint32_t*)p, (uint32_t)n, &t.t);
+    munmap(p, n * 32);
+    chk(rc, "witness");
 }
 void absorb_fr(uint8_t st[32], const char* label, const Fr8& x) { absorb(st, label, x.v, 32); }
 Fr8 draw(uint8_t st[32]) {
@@ -104,6 +141,7 @@ Fr8 draw(uint8_t st[32]) {
 }
 
 int do_prove(const std::vector<std::string>& a) {
+    Laps T;
     const std::string accdir = a[0], run_seed = a[1];
     std::vector<uint32_t> q = load_points(a[2]);
     if (q.empty()) throw Err(1, "q.bin holds no point");
@@ -163,11 +201,19 @@ int do_prove(const std::vector<std::string>& a) {
     for (uint32_t i = 1; i < ncl; i++) rho_pows[i] = fmul(rho_pows[i - 1], rho);
 
     // per tensor: M_j = sum_i rho^i eq(point_i), P_j = witness, S_j = <M_j, P_j> if short
-    std::vector<Tensor> M(nT), Pt(nT);
+    uint64_t wit_bytes = 0;
+    for (const auto& t : ts) wit_bytes += 32ull << t.vars;
+    const bool resident = wit_bytes <= kResidentMax;
+    std::vector<Tensor> M(nT), Pt(nT), Wt(nT);
     std::vector<Fr8> c2(nT, fr_u32(1)), S(nT);
     for (uint32_t j = 0; j < nT; j++) {
         const uint64_t n = 1ull << ts[j].vars;
-        load_witness(witpath[j], (uint64_t)ts[j].n_rows * ts[j].domain, Pt[j]);
+        // the witness stays on the device for G5 when the layer's witnesses fit the budget
+        // (the reference reloads it there); P_j is a copy that the rounds fold in place
+        Tensor w;
+        load_witness(witpath[j], n, w);
+        chk(zkh_axpy(g_ctx, w.t, fr_u32(0).v, w.t, &Pt[j].t), "P");
+        if (resident) std::swap(Wt[j].t, w.t);
         for (uint32_t k = 0; k < ts[j].idx.size(); k++) {
             const Claim& c = cs[ts[j].idx[k]];
             Tensor e, acc;
@@ -186,6 +232,7 @@ int do_prove(const std::vector<std::string>& a) {
             chk(zkh_sum(g_ctx, h.t, S[j].v), "S_j");
         }
     }
+    T.lap("setup");
     Fr8 cur;
     for (uint32_t i = 0; i < ncl; i++) cur = fadd(cur, fmul(rho_pows[i], fr_of(cs[i].eval)));
 
@@ -233,6 +280,7 @@ int do_prove(const std::vector<std::string>& a) {
         put_pod(b, ev.data(), 3 * m_max, 8);
         write_all(accdir + "/batch_sumcheck.bin", b.data(), b.size());
     }
+    T.lap("rounds");
 
     // G3 terminals
     std::vector<Fr8> vfin(nT);
@@ -271,6 +319,8 @@ int do_prove(const std::vector<std::string>& a) {
         t.t = nullptr;
     }
 
+    T.lap("terminal");
+
     // G4 + G5: one IPA per generator domain, ascending
     const Fr8 rhop = draw(st);
     std::vector<Fr8> rhop_pows(nT);
@@ -285,7 +335,11 @@ int do_prove(const std::vector<std::string>& a) {
             if (ts[j].domain != G) continue;
             const Fr8 coef = fmul(rhop_pows[j], kappa(ts[j].vars, r));
             Tensor w, rf, nxt;
-            load_witness(witpath[j], (uint64_t)ts[j].n_rows * G, w);
+            if (resident) {
+                std::swap(w.t, Wt[j].t);
+            } else {
+                load_witness(witpath[j], (uint64_t)ts[j].n_rows * G, w);
+            }
             const zkh_tensor* row = w.t;
             if (ts[j].vars > logG) {
                 std::vector<uint32_t> urow;
@@ -312,6 +366,7 @@ int do_prove(const std::vector<std::string>& a) {
         chk(zkh_eq_table(g_ctx, ucol.data(), logG, &b.t), "me_weights");
         ipa_file(accdir + "/ipa_batch_" + std::to_string(G) + ".bin", st, acc.t, b.t, g.g, q.data());
     }
+    T.lap("ipa");
     printf("PROVED opening_batch (%u claims, %u tensors, %zu domains) -> %s\n", ncl, nT, domains.size(),
            accdir.c_str());
     return 0;
