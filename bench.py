@@ -478,6 +478,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--no-commit", action="store_true", help="skip the Pedersen commitments")
+    ap.add_argument("--no-batchopen", action="store_true", help="skip the claim-mode batch opening")
     ap.add_argument("--no-prof", action="store_true", help="skip the profiled pass (no kernel times)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (the known-size kernel that "
@@ -655,6 +656,10 @@ def main():
         print("commitments %.3f s per layer" % com["commit_s_per_layer"], file=sys.stderr, flush=True)
         ope = openings(zkh, jobs, mbatch.outs, pool, cpu=not args.no_cpu)
         print("openings %.3f s per layer" % ope["ipa_s_per_layer"], file=sys.stderr, flush=True)
+    bo = None
+    if com and not args.no_batchopen:
+        bo = batch_open(zkh, jobs, reps=2)
+        print("batch opening %.3f s per layer" % bo["batch_open_s_per_layer"], file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(jobs)
     res = {
         "metric": "Fr elements bound/sec in matmul sumcheck; prove s/layer at TinyLlama-1.1B",
@@ -675,6 +680,8 @@ def main():
         res["commitments"] = com
     if ope:
         res["openings"] = ope
+    if bo:
+        res["batch_opening"] = bo
     print(json.dumps(res))
     pool.shutdown()
 
