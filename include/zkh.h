@@ -258,6 +258,11 @@ void zkh_g1_generator(uint32_t* out);
  * over the scalar's raw bits.  With the generator as base and random scalars this is
  * Commitment::random (commitment.cu:3-8), the public generators of a commitment key. */
 int zkh_g1_mul(zkh_ctx* ctx, const zkh_g1* base, const zkh_tensor* t, zkh_g1** out);
+/* out[i] = b[i] + a[i] * s for point arrays a, b of one size and one plain scalar s: the
+ * reference's hb_addmul with mul_first = false (zkob_fastg1.cuh:56-88; G1Jacobian_mul, then
+ * the addition with b[i] as first operand), e.g. the SwiGLU claim mode's com_comb =
+ * com_G + r com_S row by row (zkob_glu.cu:207-215), byte-identical */
+int zkh_g1_addmul(zkh_ctx* ctx, const zkh_g1* a, const uint32_t s[8], const zkh_g1* b, zkh_g1** out);
 /* Commitment::commit (commitment.cu:105-108 -> commit_pippenger :85-103): t holds m rows of
  * n = size(gens) scalars (row-major, any tensor kind); out[row] = sum_i t[row][i] gens[i],
  * byte-identical to the reference's bucket method (4-bit windows over the raw scalar

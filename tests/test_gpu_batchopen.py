@@ -533,3 +533,104 @@ def test_rope_and_fc_claims_in_one_batch(tmp_path, B, Cc, HD):
     want = batch_expected(cs, ds, wit, comfiles, "run6", GENS, Q2[0])
     for name, data in want.items():
         assert open(os.path.join(acc, name), "rb").read() == data, name
+
+
+GLU = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_glu")
+
+
+def glu_claims(seed, obid, obdir, Gm, Um, low, ln, mapped, gen):
+    """zkob_glu claim mode restated (zkob_glu.cu:86-275): the mapping lookup by its
+    definition, com_comb = com_G + r com_S row by row (hb_addmul, zkob_fastg1.cuh:56-88), and
+    the six claims A, comb, m (lookup terminals) and H, S, U (Hadamard)."""
+    B, Cc = Gm.shape
+    Bp, Cp = pow2(B), pow2(Cc)
+    D, N = Bp * Cp, ln
+    logD, n1 = P.ceil_log2(D), P.ceil_log2(D // N)
+    Gp, Up = padded(Gm), padded(Um)
+    idx = (Gp - low).reshape(-1)
+    S = np.asarray(mapped, np.int64)[idx].reshape(Gp.shape)
+    m = np.bincount(idx, minlength=N).astype(np.int64)
+    H = S * Up
+    coms = {}
+    for name, t in (("G", Gp), ("S", S), ("U", Up), ("H", H), ("m", m)):
+        coms[name] = C.g1_commit(gen, C.ints_to_fr(t.reshape(-1)), Cp)[1]
+    st = C.tr_init(seed)
+    for lab, v in (("B", B), ("C", Cc), ("LOW", low & 0xFFFFFFFF), ("LEN", ln)):
+        C.tr_absorb(st, lab, struct.pack("<I", v))
+    for name in ("G", "S", "U", "H", "m"):
+        C.tr_absorb(st, "com_" + name, coms[name].tobytes())
+    r = challenge(st)
+    beta = C.tr_challenge_fr(st)
+    comb = [(int(g) + r * int(s)) % R for g, s in zip(Gp.reshape(-1), S.reshape(-1))]
+    Tcomb = C.ints_to_fr([(low + i + r * int(mapped[i])) % R for i in range(N)])
+    A = C.lu_inverse(C.ints_to_fr(comb), beta)
+    coms["A"] = C.g1_commit(gen, A, Cp)[1]
+    C.tr_absorb(st, "com_A", coms["A"].tobytes())
+    alpha = C.tr_challenge_fr(st)
+    u = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, lk = C.lu_prove(st, A, C.ints_to_fr(comb), Tcomb, C.ints_to_fr(m), alpha, beta, u)
+    assert rc == 0
+    rl = np.array(P.to_limbs(r), np.uint32)
+    coms["comb"] = np.array([C.g1_add(coms["G"][j], C.g1_mul(coms["S"][j], rl)) for j in range(Bp)])
+    # pin: com_comb row j is the commitment of comb row j as a group element
+    for j in (0, Bp - 1):
+        want = C.g1_commit(gen, C.ints_to_fr(comb[j * Cp:(j + 1) * Cp]), Cp)[1][0]
+        assert G.to_affine(coms["comb"][j]) == G.to_affine(want)
+    u_pt = ints(lk["ws"][::-1])
+    A_f, S_f, _, _, m_f = ints(lk["term"])
+    uh = np.array([C.tr_challenge_fr(st) for _ in range(logD)])
+    rc, claimH = C.me(C.ints_to_fr(H.reshape(-1)), uh)
+    C.tr_absorb(st, "claim_H", claimH.tobytes())
+    rc, hp = C.hp_prove(st, claimH, C.build_eq(uh), C.ints_to_fr(S.reshape(-1)), C.ints_to_fr(Up.reshape(-1)))
+    assert rc == 0
+    C.tr_absorb(st, "S_f2", hp["term"][0].tobytes())
+    C.tr_absorb(st, "U_f2", hp["term"][1].tobytes())
+    u_pt2 = ints(hp["ws"][::-1])
+    S_f2, U_f2 = ints(hp["term"][:2])
+    ref = {t: os.path.join(obdir, "com_%s.bin" % t) for t in ("A", "comb", "m", "H", "S", "U")}
+    rows = dict(A=Bp, comb=Bp, m=N // Cp, H=Bp, S=Bp, U=Bp)
+    pts = dict(A=u_pt, comb=u_pt, m=u_pt[:logD - n1], H=ints(uh), S=u_pt2, U=u_pt2)
+    evs = dict(A=A_f, comb=S_f, m=m_f, H=ints(claimH)[0], S=S_f2, U=U_f2)
+    cs = [dict(id="%s:%s" % (obid, t), comref=ref[t], domain=Cp, n_rows=rows[t], point=pts[t], eval=evs[t])
+          for t in ("A", "comb", "m", "H", "S", "U")]
+    wit = {ref["A"]: ints(A), ref["comb"]: comb, ref["m"]: m.reshape(-1), ref["H"]: H.reshape(-1),
+           ref["S"]: S.reshape(-1), ref["U"]: Up.reshape(-1)}
+    return cs, wit, {ref[t]: coms[t].tobytes() for t in ref}, bytes(st)
+
+
+@pytest.mark.parametrize("B,Cc,low,ln", [(8, 4, -8, 16), (8, 6, -16, 32)])
+def test_glu_and_fc_claims_in_one_batch(tmp_path, B, Cc, low, ln):
+    """a SwiGLU obligation's six claims (zkob_glu.cu:204-275, com_comb.bin included) and a
+    matmul's accumulated together, then opened in one batch"""
+    tmp = str(tmp_path)
+    acc = setup_dirs(tmp)
+    rng = np.random.default_rng(B * 1000 + Cc * 10 + ln + 1)
+    mapped = np.array([(i + low) ** 2 for i in range(ln)], np.int32)
+    Gm = rng.integers(low, low + ln, size=(B, Cc)).astype(np.int32)
+    Um = rng.integers(-300, 300, size=(B, Cc)).astype(np.int32)
+    obid, obdir = "L5.glu", os.path.join(tmp, "L5.glu")
+    os.makedirs(obdir)
+    paths = {}
+    for name, arr in (("G", Gm), ("U", Um), ("mapped", mapped)):
+        paths[name] = os.path.join(obdir, name + ".in")
+        np.ascontiguousarray(arr).tofile(paths[name])
+    seed = "run8:" + obid
+    r = subprocess.run([GLU, "prove", obdir, seed, paths["G"], paths["U"], str(B), str(Cc), str(low), str(ln),
+                        paths["mapped"], os.path.join(tmp, "gen_%d.bin" % pow2(Cc)), os.path.join(tmp, "q.bin"),
+                        "--claims", acc, obid], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "claim mode, 6 claims emitted" in r.stdout
+    assert not os.path.exists(os.path.join(obdir, "ipa_A.bin"))
+    cs, wit, comfiles, state = glu_claims(seed, obid, obdir, Gm, Um, low, ln, mapped, GENS[pow2(Cc)])
+    assert open(os.path.join(obdir, "com_comb.bin"), "rb").read() == comfiles[cs[1]["comref"]]
+    ds = [(obid, state)]
+    X1, W1 = rng_mats(8, 4, 8, 4)
+    obs = [("L5.fc", X1, W1, "comW.bin")]
+    acc, cs, ds, wit, comfiles = accumulate(tmp, obs, acc, cs, ds, wit, comfiles)
+    check_accumulator(acc, cs, ds, wit, [(obid,)] + obs)
+    r = run_bo(acc, tmp, "run8", (4, 8))
+    assert r.returncode == 0, r.stderr
+    assert "(9 claims, 9 tensors, 2 domains)" in r.stdout
+    want = batch_expected(cs, ds, wit, comfiles, "run8", GENS, Q2[0])
+    for name, data in want.items():
+        assert open(os.path.join(acc, name), "rb").read() == data, name

@@ -176,6 +176,30 @@ def test_g1_mul_vs_oracle(zkh, ctx):
     assert np.array_equal(one[2], G.g1_zero())
 
 
+def test_g1_addmul_vs_oracle(zkh, ctx):
+    """hb_addmul, mul_first false (zkob_fastg1.cuh:56-88): out[i] = b[i] + a[i] * s, row by
+    row, with the addition's special cases: b[i] the point at infinity, b[i] equal to a[i] s
+    (the doubling branch), b[i] its negative (infinity), and s = 0."""
+    rng = np.random.default_rng(23)
+    n = 40
+    a = gens_for(31, n)
+    for s in [int.from_bytes(rng.bytes(32), "little") % P.R, 0, 1, P.R - 1]:
+        sl = np.array(P.to_limbs(s), np.uint32)
+        b = gens_for(32, n)
+        b[0] = G.g1_zero()
+        b[1] = C.g1_mul(a[1], sl)
+        b[2] = C.g1_mul(a[2], np.array(P.to_limbs((P.R - s) % P.R), np.uint32))
+        got = ctx.g1_addmul(ctx.g1_from_host(a), sl, ctx.g1_from_host(b)).to_host()
+        for i in range(n):
+            assert np.array_equal(got[i], C.g1_add(b[i], C.g1_mul(a[i], sl))), (s, i)
+        # the group element: b + s a, by affine arithmetic
+        assert G.to_affine(got[3]) == G.aff_add(G.to_affine(b[3]), G.aff_mul(G.to_affine(a[3]), s))
+        assert G.to_affine(got[2]) is None and G.to_affine(got[0]) == G.aff_mul(G.to_affine(a[0]), s)
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.g1_addmul(ctx.g1_from_host(a), np.zeros(8, np.uint32), ctx.g1_from_host(a[:3]))
+    assert e.value.code == zkh.EARG
+
+
 @pytest.mark.parametrize("n", [1, 2, 4, 32, 256])
 def test_ipa_prove_vs_oracle(zkh, ctx, n):
     """ipa_prove (vrf_common.cuh:302-336): L, R (absorbed, so byte-exact), a_final and the

@@ -97,6 +97,7 @@ def lib():
         L.zkh_g1_generator.restype = None
         L.zkh_g1_generator.argtypes = [vp]
         L.zkh_g1_mul.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
+        L.zkh_g1_addmul.argtypes = [vp, vp, vp, vp, ctypes.POINTER(vp)]
         L.zkh_ipa_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
         _lib = L
     return _lib
@@ -342,6 +343,13 @@ class Context:
         """out[i] = base[i % base.n] * t[i] (G1Jacobian_mul)."""
         h = ctypes.c_void_p()
         self._chk(lib().zkh_g1_mul(self.h, base.h, t.h, ctypes.byref(h)))
+        return G1(self, h)
+
+    def g1_addmul(self, a, s, b):
+        """out[i] = b[i] + a[i] * s, s one plain scalar (8 uint32): hb_addmul, mul_first false."""
+        sc = np.ascontiguousarray(s, dtype=np.uint32).reshape(8)
+        h = ctypes.c_void_p()
+        self._chk(lib().zkh_g1_addmul(self.h, a.h, _p(sc), b.h, ctypes.byref(h)))
         return G1(self, h)
 
     def ipa_prove(self, st, a, b, g, Q):

@@ -11,15 +11,19 @@
 // Hadamard challenges).  Files, byte-identical to the reference's: dims.bin (B, C, low, len
 // as int32), com_G/S/U/H/m/A.bin, lookup.bin, hp.bin (claim_H, count-prefixed evals,
 // S_f2, U_f2: write_hp, zkob_lookup.cuh:272-279), ipa_A/comb/m/H/S/U.bin and the optional
-// int64 H (save_long, padding rows and columns stripped).  The claim mode, `verify` and
-// `selftest` answer exit status 2.
+// int64 H (save_long, padding rows and columns stripped).  With `--claims <accdir> <obid>`
+// (claim mode, zkob_glu.cu:204-275) it also writes com_comb.bin (com_G + r com_S row by row)
+// and the six openings become claims <obid>:A, :comb, :m, :H, :S, :U in <accdir>/claims.bin,
+// with their witness files, witrefs.txt lines and the transcript state, for zkh_batchopen.
+// `verify` and `selftest` answer exit status 2.
 #include "common.hpp"
 
 using namespace zkhcli;
 
 namespace {
 
-int do_prove(const std::vector<std::string>& a) {
+// claim_args: empty, or {accdir, obid} of the claim mode
+int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& claim_args) {
     const std::string obdir = a[0], seed = a[1];
     const uint32_t B = parse_u32(a[4].c_str()), C = parse_u32(a[5].c_str());
     const int32_t low = (int32_t)strtol(a[6].c_str(), nullptr, 10);
@@ -108,9 +112,38 @@ int do_prove(const std::vector<std::string>& a) {
     std::vector<uint32_t> u_pt((size_t)logD * 8);
     for (uint32_t i = 0; i < logD; i++) memcpy(u_pt.data() + 8 * i, ws.data() + 8 * (logD - 1 - i), 32);
     std::vector<uint32_t> u_m(u_pt.begin(), u_pt.begin() + 8 * (size_t)(logD - n1));
-    open_prove(A.t, Cp, g.g, q.data(), u_pt, obdir + "/ipa_A.bin", st);
-    open_prove(comb.t, Cp, g.g, q.data(), u_pt, obdir + "/ipa_comb.bin", st);
-    open_prove(m.t, Cp, g.g, q.data(), u_m, obdir + "/ipa_m.bin", st);
+    const bool claim_mode = !claim_args.empty();
+    auto mk_claim = [&](const char* tensor, uint32_t n_rows, const std::vector<uint32_t>& point,
+                        const uint32_t* eval) {
+        const std::string &accdir = claim_args[0], &obid = claim_args[1];
+        const std::string witp = accdir + "/wit_" + obid + "_" + tensor + ".fr";
+        Claim c;
+        c.id = obid + ":" + tensor;
+        c.comref = obdir + "/com_" + tensor + ".bin";
+        c.domain = Cp;
+        c.n_rows = n_rows;
+        c.point = point;
+        memcpy(c.eval, eval, 32);
+        claim_emit(accdir, c);
+        witref_emit(accdir, c.comref, witp);
+    };
+    if (claim_mode) {  // claims A, comb, m in place of the three IPAs (zkob_glu.cu:204-227)
+        Points cC;  // com_comb = com_G + r com_S row by row (hb_addmul, mul_first = false)
+        chk(zkh_g1_addmul(g_ctx, cS.g, r.data(), cG.g, &cC.g), "com_comb");
+        const std::vector<uint32_t> hC = to_host(cC.g);
+        write_all(obdir + "/com_comb.bin", hC.data(), hC.size() * 4);
+        const std::string &accdir = claim_args[0], &obid = claim_args[1];
+        save_fr(accdir + "/wit_" + obid + "_A.fr", A.t);
+        save_fr(accdir + "/wit_" + obid + "_comb.fr", comb.t);
+        save_fr(accdir + "/wit_" + obid + "_m.fr", m.t);
+        mk_claim("A", Bp, u_pt, term.data());
+        mk_claim("comb", Bp, u_pt, term.data() + 8);
+        mk_claim("m", N / Cp, u_m, term.data() + 32);
+    } else {
+        open_prove(A.t, Cp, g.g, q.data(), u_pt, obdir + "/ipa_A.bin", st);
+        open_prove(comb.t, Cp, g.g, q.data(), u_pt, obdir + "/ipa_comb.bin", st);
+        open_prove(m.t, Cp, g.g, q.data(), u_m, obdir + "/ipa_m.bin", st);
+    }
 
     // Hadamard part (zkob_glu.cu:242-247): u_h, claim_H = H~(u_h) (columns on the low bits)
     std::vector<uint32_t> uh((size_t)logD * 8 + 8);
@@ -131,6 +164,18 @@ int do_prove(const std::vector<std::string>& a) {
     std::vector<uint32_t> u_pt2((size_t)logD * 8);
     for (uint32_t i = 0; i < logD; i++) memcpy(u_pt2.data() + 8 * i, hws.data() + 8 * (logD - 1 - i), 32);
     std::vector<uint32_t> uhv(uh.begin(), uh.begin() + 8 * (size_t)logD);
+    if (claim_mode) {  // claims H, S, U in place of the three IPAs (zkob_glu.cu:259-275)
+        const std::string &accdir = claim_args[0], &obid = claim_args[1];
+        save_fr(accdir + "/wit_" + obid + "_H.fr", Hp.t);
+        save_fr(accdir + "/wit_" + obid + "_S.fr", Sp.t);
+        save_fr(accdir + "/wit_" + obid + "_U.fr", Up.t);
+        mk_claim("H", Bp, uhv, claimH);
+        mk_claim("S", Bp, u_pt2, hterm.data());
+        mk_claim("U", Bp, u_pt2, hterm.data() + 8);
+        drvstate_emit(accdir, obid, st);
+        printf("PROVED swiglu obligation (claim mode, 6 claims emitted) -> %s\n", obdir.c_str());
+        return 0;
+    }
     open_prove(Hp.t, Cp, g.g, q.data(), uhv, obdir + "/ipa_H.bin", st);
     open_prove(Sp.t, Cp, g.g, q.data(), u_pt2, obdir + "/ipa_S.bin", st);
     open_prove(Up.t, Cp, g.g, q.data(), u_pt2, obdir + "/ipa_U.bin", st);
@@ -141,13 +186,15 @@ int do_prove(const std::vector<std::string>& a) {
 int run1(const std::vector<std::string>& args) {
     const std::string mode = args.empty() ? "" : args[0];
     std::vector<std::string> rest(args.begin() + (args.empty() ? 0 : 1), args.end());
+    const std::vector<std::string> claim_args = take_claims(rest, 2);  // --claims <accdir> <obid>
     reject_flags(rest, "zkh_glu");
     if (mode == "prove" && (rest.size() == 11 || rest.size() == 12)) {
         need_ctx();
-        return do_prove(rest);
+        return do_prove(rest, claim_args);
     }
     fprintf(stderr,
-            "usage: zkh_glu prove <obdir> <seed> <G> <U> <B> <C> <low> <len> <mapped> <gen> <q> [H-out] | serve\n");
+            "usage: zkh_glu prove <obdir> <seed> <G> <U> <B> <C> <low> <len> <mapped> <gen> <q> [H-out] "
+            "[--claims <accdir> <obid>] | serve\n");
     return 2;
 }
 

@@ -247,6 +247,19 @@ __global__ __launch_bounds__(64) void k_g1_mul(const uint32_t* __restrict__ base
     if (q == 0) g1_store(out + 36 * (size_t)i, r);
 }
 
+// out[i] = b[i] + a[i] * s: one scalar for every row, the sum with b[i] as first operand
+// (hb_addmul with mul_first = false, zkob_fastg1.cuh:56-88: k_g1_mul then k_g1_addsub)
+__global__ __launch_bounds__(64) void k_g1_addmul(const uint32_t* __restrict__ a, G1Scalar sc,
+                                                  const uint32_t* __restrict__ b, uint32_t n,
+                                                  uint32_t* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 16 + threadIdx.x / 4;
+    const int q = threadIdx.x & 3;
+    if (i >= n) return;
+    const g1_t m = g1_mul_quad(g1_load(a + 36 * (size_t)i), sc.v, q);
+    const g1_t r = g1_add_quad(g1_load(b + 36 * (size_t)i), m, q);
+    if (q == 0) g1_store(out + 36 * (size_t)i, r);
+}
+
 // ---- inner-product argument rounds (ipa_prove, vrf_common.cuh:302-336) ----
 // a, b: plain Fr, 8 words per entry; g, P: points.  Round of size 2h:
 //   ip = (<a_lo, b_hi>, <a_hi, b_lo>)                       (dev_ip, one block)
@@ -366,6 +379,10 @@ void launch_ipa_fold(hipStream_t s, const uint32_t* g, const uint32_t* a, const 
 }
 void launch_planes_to_aos(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t n, uint32_t* out) {
     hipLaunchKernelGGL(k_planes_to_aos, dim3((n + 255) / 256), dim3(256), 0, s, lo, hi, n, out);
+}
+void launch_g1_addmul(hipStream_t s, const uint32_t* a, const G1Scalar& sc, const uint32_t* b, uint32_t n,
+                      uint32_t* out) {
+    hipLaunchKernelGGL(k_g1_addmul, dim3((n + 15) / 16), dim3(64), 0, s, a, sc, b, n, out);
 }
 void launch_g1_mul(hipStream_t s, const uint32_t* base, uint32_t nb, const uint32_t* lo, const uint32_t* hi,
                    uint32_t n, uint32_t* out) {

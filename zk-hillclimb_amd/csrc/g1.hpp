@@ -51,5 +51,12 @@ void launch_ipa_fold(hipStream_t s, const uint32_t* g, const uint32_t* a, const 
                      uint32_t* g2, uint32_t* a2, uint32_t* b2);
 void launch_planes_to_aos(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t n, uint32_t* out);
 // out[i] = base[i % nb] * s[i] (G1Jacobian_mul, raw scalar bits)
+// a scalar passed by value to a kernel: 8 plain little-endian words
+struct G1Scalar {
+    uint32_t v[8];
+};
+// out[i] = b[i] + a[i] * sc (hb_addmul, mul_first = false)
+void launch_g1_addmul(hipStream_t s, const uint32_t* a, const G1Scalar& sc, const uint32_t* b, uint32_t n,
+                      uint32_t* out);
 void launch_g1_mul(hipStream_t s, const uint32_t* base, uint32_t nb, const uint32_t* lo, const uint32_t* hi,
                    uint32_t n, uint32_t* out);

@@ -2609,6 +2609,28 @@ extern "C" int zkh_g1_mul(zkh_ctx* c, const zkh_g1* base, const zkh_tensor* t, z
     *out = o;
     return ZKH_OK;
 }
+extern "C" int zkh_g1_addmul(zkh_ctx* c, const zkh_g1* a, const uint32_t sc[8], const zkh_g1* b, zkh_g1** out) {
+    if (!c || !a || !sc || !b || !out) return fail(c, ZKH_EARG, "null argument");
+    *out = nullptr;
+    if (a->n != b->n) return fail(c, ZKH_EARG, "g1_addmul: %u and %u points", a->n, b->n);
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc;
+    zkh_g1* o;
+    if ((rc = g1_alloc(c, a->n, &o))) return rc;
+    if (a->n) {
+        G1Scalar s;
+        memcpy(s.v, sc, 32);
+        launch_g1_addmul(c->stream, (const uint32_t*)a->d, s, (const uint32_t*)b->d, a->n, (uint32_t*)o->d);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            zkh_g1_free(o);
+            return fail(c, ZKH_EDEV, "g1_addmul: %s", hipGetErrorString(e));
+        }
+    }
+    *out = o;
+    return ZKH_OK;
+}
 extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, zkh_g1** out) {
     if (!c || !gens || !t || !out) return fail(c, ZKH_EARG, "null argument");
     *out = nullptr;
