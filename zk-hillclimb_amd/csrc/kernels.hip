@@ -1288,8 +1288,12 @@ typedef EqdotV<int64_t, 2, 22> EqdotI64x2;
 typedef EqdotV<int64_t, 3, 22> EqdotI64x3;
 
 // partial[c*N+i] = sum_{k in chunk c} (M[k*N+i] + 2^bits) e_k: one column per thread, rows
-// in groups of 8 with the next group's loads issued before the current group's products
-// (16 rows of the column in flight per wave); e_k comes through scalar loads.
+// in groups of EQDOT_GROUP with the next group's loads issued before the current group's
+// products (2 * EQDOT_GROUP rows of the column in flight per wave); e_k comes through
+// scalar loads.
+#ifndef EQDOT_GROUP
+#define EQDOT_GROUP 8
+#endif
 template <typename V>
 ZDEV void eqdot_body(const EqDotDesc& q, uint32_t local) {
     typedef typename V::T T;
@@ -1323,22 +1327,23 @@ ZDEV void eqdot_body(const EqDotDesc& q, uint32_t local) {
     if (i < N) {
         const T* col = M + i;
         uint32_t k = k0;
-        if (k + 8 <= k1) {
-            T v[8];
+        constexpr uint32_t G = EQDOT_GROUP;
+        if (k + G <= k1) {
+            T v[G];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = ld_stream(col + (size_t)(k + u) * N);
-            for (; k + 16 <= k1; k += 8) {
-                T nx[8];
+            for (uint32_t u = 0; u < G; u++) v[u] = ld_stream(col + (size_t)(k + u) * N);
+            for (; k + 2 * G <= k1; k += G) {
+                T nx[G];
 #pragma unroll
-                for (int u = 0; u < 8; u++) nx[u] = ld_stream(col + (size_t)(k + 8 + u) * N);
+                for (uint32_t u = 0; u < G; u++) nx[u] = ld_stream(col + (size_t)(k + G + u) * N);
 #pragma unroll
-                for (int u = 0; u < 8; u++) mac(v[u], k + u);
+                for (uint32_t u = 0; u < G; u++) mac(v[u], k + u);
 #pragma unroll
-                for (int u = 0; u < 8; u++) v[u] = nx[u];
+                for (uint32_t u = 0; u < G; u++) v[u] = nx[u];
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) mac(v[u], k + u);
-            k += 8;
+            for (uint32_t u = 0; u < G; u++) mac(v[u], k + u);
+            k += G;
         }
         for (; k < k1; k++) mac(ld_stream(col + (size_t)k * N), k);
     }
