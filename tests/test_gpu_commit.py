@@ -239,3 +239,19 @@ def test_ipa_prove_int_witness_and_errors(zkh, ctx):
     with pytest.raises(zkh.ZkhError) as e:
         ctx.ipa_prove(zkh.transcript("x"), ctx.from_i32(v[:8]), ctx.from_fr(b), ctx.g1_from_host(gens[:n]), gens[n])
     assert e.value.code == zkh.EARG
+
+
+def test_from_fr_rejects_non_canonical(zkh, ctx):
+    """zkh_tensor_from_fr checks canonical form on the device: r itself, r + 1 and 2^256 - 1
+    anywhere in the array are rejected; r - 1 and 0 round-trip."""
+    rng = np.random.default_rng(41)
+    n = 5000
+    good = np.array([P.to_limbs(int.from_bytes(rng.bytes(32), "little") % P.R) for _ in range(n)], np.uint32)
+    good[0], good[n - 1] = P.to_limbs(P.R - 1), P.to_limbs(0)
+    assert np.array_equal(ctx.from_fr(good).to_fr(), good)
+    for pos, v in ((0, P.R), (n // 2, P.R + 1), (n - 1, 2**256 - 1)):
+        bad = good.copy()
+        bad[pos] = P.to_limbs(v)
+        with pytest.raises(zkh.ZkhError) as e:
+            ctx.from_fr(bad)
+        assert e.value.code == zkh.EARG, (pos, v)

@@ -214,6 +214,24 @@ void launch_i64_to_planes(hipStream_t s, const int64_t* in, uint32_t n, DevPlane
     if (!n) return;
     k_i64_to_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(in, n, PL_LO(out), PL_HI(out));
 }
+// *bad += number of 8-word entries >= r (an upload's canonical-form check, on the device so
+// that multi-GB witness files are not scanned by one host thread)
+__global__ void k_count_noncanonical(const uint32_t* __restrict__ aos, uint32_t n, uint32_t* bad) {
+    uint32_t cnt = 0;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const uint4 a = ((const uint4*)aos)[2 * (size_t)i], b = ((const uint4*)aos)[2 * (size_t)i + 1];
+        const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t br = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) (void)__builtin_subc(v[k], fr_p(k), br, &br);
+        cnt += br ? 0u : 1u;  // no borrow from v - r: v >= r
+    }
+    if (cnt) atomicAdd(bad, cnt);
+}
+void launch_count_noncanonical(hipStream_t s, const uint32_t* aos, uint32_t n, uint32_t* bad) {
+    if (!n) return;
+    k_count_noncanonical<<<grid_for(n, NT, 8192), NT, 0, s>>>(aos, n, bad);
+}
 void launch_aos_to_planes(hipStream_t s, const uint32_t* aos, uint32_t n, DevPlanes out) {
     if (!n) return;
     k_aos_to_planes<<<grid_for(n, NT, 8192), NT, 0, s>>>(aos, n, PL_LO(out), PL_HI(out));

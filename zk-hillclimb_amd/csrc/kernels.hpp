@@ -52,6 +52,8 @@ struct EqW {
 void launch_i32_to_planes(hipStream_t s, const int32_t* in, uint32_t n, DevPlanes out);
 void launch_i64_to_planes(hipStream_t s, const int64_t* in, uint32_t n, DevPlanes out);
 void launch_aos_to_planes(hipStream_t s, const uint32_t* aos, uint32_t n, DevPlanes out);
+// *bad (zeroed by the caller) += entries of aos that are not below r
+void launch_count_noncanonical(hipStream_t s, const uint32_t* aos, uint32_t n, uint32_t* bad);
 void launch_planes_to_aos(hipStream_t s, DevPlanes in, uint32_t n, uint32_t* aos);
 void launch_absmax_i32(hipStream_t s, const int32_t* in, uint32_t n, uint32_t* out);
 void launch_absmax_i64(hipStream_t s, const int64_t* in, uint32_t n, unsigned long long* out);

@@ -773,22 +773,31 @@ extern "C" int zkh_tensor_weights_i32(zkh_ctx* c, const int32_t* W, uint32_t in_
 extern "C" int zkh_tensor_from_fr(zkh_ctx* c, const uint32_t* aos, uint32_t n, zkh_tensor** out) {
     if (!c || !out || (!aos && n)) return fail(c, ZKH_EARG, "null argument");
     *out = nullptr;
-    if (!all_canonical(aos, n)) return fail(c, ZKH_EARG, "non-canonical field element");
     HIPCHK(c, hipSetDevice(c->device));
     zkh_tensor* t;
     int rc = tensor_alloc(c, ZKH_KIND_FR, n, &t);
     if (rc) return rc;
     if (n) {
-        uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)n * 32, &rc);
+        // the entries, then one word counting non-canonical entries (checked on the device)
+        uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)n * 32 + 256, &rc);
+        uint32_t* bad = stage + 8 * (size_t)n;
+        uint32_t nbad = 0;
         hipError_t e = hipSuccess;
         if (!rc) e = hipMemcpyAsync(stage, aos, (size_t)n * 32, hipMemcpyHostToDevice, c->stream);
+        if (!rc && e == hipSuccess) e = hipMemsetAsync(bad, 0, 4, c->stream);
         if (!rc && e == hipSuccess) {
+            launch_count_noncanonical(c->stream, stage, n, bad);
             launch_aos_to_planes(c->stream, stage, n, t->planes());
-            e = hipStreamSynchronize(c->stream);
+            e = hipMemcpyAsync(&nbad, bad, 4, hipMemcpyDeviceToHost, c->stream);
         }
+        if (!rc && e == hipSuccess) e = hipStreamSynchronize(c->stream);
         if (rc || e != hipSuccess) {
             zkh_tensor_free(t);
             return rc ? rc : fail(c, ZKH_EDEV, "upload failed: %s", hipGetErrorString(e));
+        }
+        if (nbad) {
+            zkh_tensor_free(t);
+            return fail(c, ZKH_EARG, "non-canonical field element");
         }
     }
     *out = t;
