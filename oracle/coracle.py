@@ -31,8 +31,23 @@ def frs(n):
     return np.zeros((n, 8), dtype=np.uint32)
 
 
+def set_threads(n):
+    """OpenMP threads of the oracle's table loops (1: the scalar CPU baseline)."""
+    lib().or_set_threads(ctypes.c_int(int(n)))
+
+
+def get_threads():
+    return int(lib().or_get_threads())
+
+
 def ints_to_fr(vals):
-    """Python ints (any sign) -> (n,8) uint32, reduced mod r."""
+    """Integers (any sign) -> (n,8) uint32, reduced mod r."""
+    arr = np.asarray(vals)
+    if arr.dtype.kind in "iu" and (arr.dtype.itemsize < 8 or arr.dtype.kind == "i"):
+        v = np.ascontiguousarray(arr.reshape(-1), dtype=np.int64)
+        out = frs(len(v))
+        lib().or_ints_to_fr(_p(v), ctypes.c_size_t(len(v)), _p(out))
+        return out
     from .pyref import R, to_limbs
     out = frs(len(vals))
     for i, v in enumerate(vals):
@@ -133,6 +148,40 @@ def mm_prove(st, X, W, Y, B, IN, OUT):
     rc = lib().or_mm_prove(_p(st), _p(X), _p(W), _p(Y), ctypes.c_uint32(B), ctypes.c_uint32(IN),
                            ctypes.c_uint32(OUT), _p(ev), _p(cl), _p(ub), _p(uo), _p(ui))
     return rc, dict(ev=ev[:3 * L], claims=cl, u_batch=ub[:lb], u_output=uo[:lo], u_input=ui[:L])
+
+
+def mm_prove_fr(st, X, W, Y, B, IN, OUT):
+    """The same segment on field-element tables: X (B*IN, 8), W (IN*OUT, 8), Y (B*OUT, 8)."""
+    from .pyref import ceil_log2
+    X, W, Y = (np.ascontiguousarray(a, dtype=np.uint32) for a in (X, W, Y))
+    L, lb, lo = ceil_log2(IN), ceil_log2(B), ceil_log2(OUT)
+    ev, cl = frs(3 * L + 1), frs(3)
+    ub, uo, ui = frs(lb + 1), frs(lo + 1), frs(L + 1)
+    rc = lib().or_mm_prove_fr(_p(st), _p(X), _p(W), _p(Y), ctypes.c_uint32(B), ctypes.c_uint32(IN),
+                              ctypes.c_uint32(OUT), _p(ev), _p(cl), _p(ub), _p(uo), _p(ui))
+    return rc, dict(ev=ev[:3 * L], claims=cl, u_batch=ub[:lb], u_output=uo[:lo], u_input=ui[:L])
+
+
+def axpy(a, c, b):
+    a, b = (np.ascontiguousarray(x, dtype=np.uint32).reshape(-1, 8) for x in (a, b))
+    out = frs(len(a))
+    lib().or_axpy(_p(a), _p(np.ascontiguousarray(c, dtype=np.uint32)), _p(b), ctypes.c_size_t(len(a)), _p(out))
+    return out
+
+
+def hadamard(a, b):
+    a, b = (np.ascontiguousarray(x, dtype=np.uint32).reshape(-1, 8) for x in (a, b))
+    out = frs(len(a))
+    lib().or_hadamard(_p(a), _p(b), ctypes.c_size_t(len(a)), _p(out))
+    return out
+
+
+def check_inverse(S, A, beta):
+    """Entries of A that are not 1/(S + beta) (0 where S + beta = 0)."""
+    S, A = (np.ascontiguousarray(x, dtype=np.uint32).reshape(-1, 8) for x in (S, A))
+    lib().or_check_inverse.restype = ctypes.c_size_t
+    return int(lib().or_check_inverse(_p(S), _p(A), ctypes.c_size_t(len(S)),
+                                      _p(np.ascontiguousarray(beta, dtype=np.uint32))))
 
 
 def range_table(low, length, size):

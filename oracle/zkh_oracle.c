@@ -9,11 +9,19 @@
  * Montgomery multiplication by CIOS (Koc, Acar, Kaliski 1996) on 4x64-bit limbs with
  * unsigned __int128; R = 2^256 as in the reference's 8x32-bit limbs, so the raw
  * Montgomery product a*b*2^-256 is the same value.
+ *
+ * Loops over table entries run under OpenMP (or_set_threads; 1 thread gives the scalar
+ * baseline).  Every parallel loop either writes disjoint entries or adds field elements,
+ * and addition mod r is exact, so results do not depend on the thread count.
  */
 #include "zkh_oracle.h"
 
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* loops shorter than this stay on one thread */
+#define PAR_MIN 8192
 
 typedef unsigned __int128 u128;
 typedef struct { uint64_t v[4]; } fr;
@@ -292,19 +300,35 @@ static uint32_t ceil_log2(uint32_t n) { /* fr-tensor.cu:26-41 */
 static fr* falloc(size_t n) { return (fr*)calloc(n ? n : 1, sizeof(fr)); }
 static fr* from_aos(const uint32_t* t, size_t n) {
     fr* o = falloc(n);
+#pragma omp parallel for if (n >= PAR_MIN)
     for (size_t i = 0; i < n; i++) o[i] = ld(t + 8 * i);
     return o;
 }
 
+void or_set_threads(int n) { omp_set_num_threads(n < 1 ? 1 : n); }
+int or_get_threads(void) { return omp_get_max_threads(); }
+
 static fr sum_fr(const fr* t, size_t n) {
-    fr s = ZERO;
-    for (size_t i = 0; i < n; i++) s = add(s, t[i]);
-    return s;
+    fr total = ZERO;
+#pragma omp parallel if (n >= PAR_MIN)
+    {
+        fr s = ZERO;
+#pragma omp for nowait
+        for (size_t i = 0; i < n; i++) s = add(s, t[i]);
+#pragma omp critical
+        total = add(total, s);
+    }
+    return total;
 }
 void or_sum(const uint32_t* t, uint32_t n, uint32_t out[8]) {
-    fr s = ZERO;
-    for (uint32_t i = 0; i < n; i++) s = add(s, ld(t + 8 * i));
-    st(out, s);
+    fr* a = from_aos(t, n);
+    st(out, sum_fr(a, n));
+    free(a);
+}
+/* int64 values -> Fr array (int_to_scalar / long_to_scalar per entry, fr-tensor.cu:701-717) */
+void or_ints_to_fr(const int64_t* v, size_t n, uint32_t* out) {
+#pragma omp parallel for if (n >= PAR_MIN)
+    for (size_t i = 0; i < n; i++) st(out + 8 * i, from_i64(v[i]));
 }
 
 /* Fr_me: pairs (2i, 2i+1), u[0] binds the LSB; odd tail a0 - x*a0 (fr-tensor.cu:588-609) */
@@ -314,11 +338,16 @@ static fr me_fr(const fr* t, uint32_t n, const fr* u, uint32_t k) {
     uint32_t sz = n;
     for (uint32_t r = 0; r < k; r++) {
         uint32_t out = (sz + 1) / 2;
+        const fr x = mont(u[r]);
+        fr* nxt = falloc(out);
+#pragma omp parallel for if (out >= PAR_MIN)
         for (uint32_t i = 0; i < out; i++) {
             uint32_t g0 = 2 * i, g1 = 2 * i + 1;
-            if (g1 < sz) cur[i] = add(cur[g0], mmul(mont(u[r]), sub(cur[g1], cur[g0])));
-            else cur[i] = sub(cur[g0], mmul(mont(u[r]), cur[g0]));
+            if (g1 < sz) nxt[i] = add(cur[g0], mmul(x, sub(cur[g1], cur[g0])));
+            else nxt[i] = sub(cur[g0], mmul(x, cur[g0]));
         }
+        free(cur);
+        cur = nxt;
         sz = out;
     }
     fr res = cur[0];
@@ -348,6 +377,7 @@ static fr* partial_me_fr(const fr* t, uint32_t n, const fr* u, uint32_t k, uint3
         uint32_t osz = other * cdo * window;
         fr* nxt = falloc(osz);
         fr x = mont(u[r]);
+#pragma omp parallel for if (osz >= PAR_MIN)
         for (uint32_t g = 0; g < osz; g++) {
             uint32_t i0 = g / (cdo * window), i1 = (g / window) % cdo, i2 = g % window;
             uint32_t g0 = i0 * cd * window + (2 * i1) * window + i2;
@@ -392,6 +422,7 @@ int or_partial_me_window(const uint32_t* t, uint32_t n, const uint32_t* u, uint3
         uint32_t nw = (sz + 2 * window - 1) / (2 * window);
         uint32_t osz = window * nw;
         fr* nxt = falloc(osz);
+#pragma omp parallel for if (osz >= PAR_MIN)
         for (uint32_t g = 0; g < osz; g++) {
             uint32_t w = g / window, j = g % window;
             uint32_t g0 = 2 * w * window + j, g1 = (2 * w + 1) * window + j;
@@ -489,6 +520,7 @@ static fr* build_eq_fr(const fr* u, uint32_t k) {
     uint32_t n = 1;
     for (uint32_t i = 0; i < k; i++) {
         fr om = sub(ONE, u[i]);
+#pragma omp parallel for if (n >= PAR_MIN)
         for (uint32_t g = 0; g < n; g++) {
             fr v = e[g];
             e[g] = mul(om, v);
@@ -551,18 +583,13 @@ static fr poly_eval(const fr* c, int deg, fr x) {
 /* ------------------------------------------------------------------------------ */
 /* matmul sumcheck: zkob_fc.cu:259-440 with zkfc.cu:94-127 kernels                  */
 /* ------------------------------------------------------------------------------ */
-int or_mm_prove(uint8_t s[32], const int32_t* X, const int32_t* W, const int64_t* Y,
-                uint32_t B, uint32_t IN, uint32_t OUT, uint32_t* ev_out,
-                uint32_t* claims_out, uint32_t* u_batch_out, uint32_t* u_output_out,
-                uint32_t* u_input_out) {
-    if (!B || !IN || !OUT) return 1;
+/* the segment over field tables X (B x IN), W (IN x OUT), Y (B x OUT): the FrTensors that
+ * zkob_fc binds (zkob_fc.cu:276-277, :337-338) */
+static int mm_prove_core(uint8_t s[32], const fr* Xf, const fr* Wf, const fr* Yf,
+                         uint32_t B, uint32_t IN, uint32_t OUT, uint32_t* ev_out,
+                         uint32_t* claims_out, uint32_t* u_batch_out, uint32_t* u_output_out,
+                         uint32_t* u_input_out) {
     uint32_t lb = ceil_log2(B), lo = ceil_log2(OUT), L = ceil_log2(IN);
-    fr* Xf = falloc((size_t)B * IN);
-    fr* Wf = falloc((size_t)IN * OUT);
-    fr* Yf = falloc((size_t)B * OUT);
-    for (size_t i = 0; i < (size_t)B * IN; i++) Xf[i] = from_i64(X[i]);
-    for (size_t i = 0; i < (size_t)IN * OUT; i++) Wf[i] = from_i64(W[i]);
-    for (size_t i = 0; i < (size_t)B * OUT; i++) Yf[i] = from_i64(Y[i]);
     fr* ub = falloc(lb);
     fr* uo = falloc(lo);
     for (uint32_t i = 0; i < lb; i++) ub[i] = challenge(s);
@@ -584,12 +611,23 @@ int or_mm_prove(uint8_t s[32], const int32_t* X, const int32_t* W, const int64_t
     for (uint32_t r = 0; r < L; r++) {
         uint32_t no = (1u << ceil_log2(sz)) >> 1;
         fr c0 = ZERO, c1 = ZERO, c2 = ZERO;
-        for (uint32_t i = 0; i < no; i++) { /* zkip_poly_kernel, zero-fill */
-            fr a0 = i < sz ? a[i] : ZERO, b0 = i < sz ? b[i] : ZERO;
-            fr a1 = i + no < sz ? a[i + no] : ZERO, b1 = i + no < sz ? b[i + no] : ZERO;
-            c0 = add(c0, mul(a0, b0));
-            c1 = add(c1, mont(add(mmul(a0, sub(b1, b0)), mmul(b0, sub(a1, a0)))));
-            c2 = add(c2, mul(sub(a1, a0), sub(b1, b0)));
+#pragma omp parallel if (no >= PAR_MIN)
+        {
+            fr l0 = ZERO, l1 = ZERO, l2 = ZERO;
+#pragma omp for nowait
+            for (uint32_t i = 0; i < no; i++) { /* zkip_poly_kernel, zero-fill */
+                fr a0 = i < sz ? a[i] : ZERO, b0 = i < sz ? b[i] : ZERO;
+                fr a1 = i + no < sz ? a[i + no] : ZERO, b1 = i + no < sz ? b[i + no] : ZERO;
+                l0 = add(l0, mul(a0, b0));
+                l1 = add(l1, mont(add(mmul(a0, sub(b1, b0)), mmul(b0, sub(a1, a0)))));
+                l2 = add(l2, mul(sub(a1, a0), sub(b1, b0)));
+            }
+#pragma omp critical
+            {
+                c0 = add(c0, l0);
+                c1 = add(c1, l1);
+                c2 = add(c2, l2);
+            }
         }
         fr p0 = c0, p1 = add(add(c0, c1), c2);
         fr two = from_u32(2);
@@ -605,6 +643,7 @@ int or_mm_prove(uint8_t s[32], const int32_t* X, const int32_t* W, const int64_t
         st(ev_out + 24 * r + 16, p2);
         cur = lagrange3(p0, p1, p2, x);
         fr xm = mont(x);
+#pragma omp parallel for if (no >= PAR_MIN)
         for (uint32_t i = 0; i < no; i++) { /* zkip_reduce_kernel */
             fr a0 = i < sz ? a[i] : ZERO, b0 = i < sz ? b[i] : ZERO;
             fr a1 = i + no < sz ? a[i + no] : ZERO, b1 = i + no < sz ? b[i + no] : ZERO;
@@ -641,7 +680,42 @@ int or_mm_prove(uint8_t s[32], const int32_t* X, const int32_t* W, const int64_t
     for (uint32_t i = 0; i < lo; i++) st(u_output_out + 8 * i, uo[i]);
     free(a); free(b); free(xs);
 done0:
-    free(Xf); free(Wf); free(Yf); free(ub); free(uo);
+    free(ub); free(uo);
+    return rc;
+}
+/* zkob_fc's segment on its int32 input files (load_int_tensor, zkob_fc.cu:178-185) and
+ * the int64 product */
+int or_mm_prove(uint8_t s[32], const int32_t* X, const int32_t* W, const int64_t* Y,
+                uint32_t B, uint32_t IN, uint32_t OUT, uint32_t* ev_out,
+                uint32_t* claims_out, uint32_t* u_batch_out, uint32_t* u_output_out,
+                uint32_t* u_input_out) {
+    if (!B || !IN || !OUT) return 1;
+    fr* Xf = falloc((size_t)B * IN);
+    fr* Wf = falloc((size_t)IN * OUT);
+    fr* Yf = falloc((size_t)B * OUT);
+#pragma omp parallel for
+    for (size_t i = 0; i < (size_t)B * IN; i++) Xf[i] = from_i64(X[i]);
+#pragma omp parallel for
+    for (size_t i = 0; i < (size_t)IN * OUT; i++) Wf[i] = from_i64(W[i]);
+#pragma omp parallel for
+    for (size_t i = 0; i < (size_t)B * OUT; i++) Yf[i] = from_i64(Y[i]);
+    int rc = mm_prove_core(s, Xf, Wf, Yf, B, IN, OUT, ev_out, claims_out, u_batch_out, u_output_out,
+                           u_input_out);
+    free(Xf); free(Wf); free(Yf);
+    return rc;
+}
+/* the same on field-element tables (Fr arrays, canonical) */
+int or_mm_prove_fr(uint8_t s[32], const uint32_t* X, const uint32_t* W, const uint32_t* Y,
+                   uint32_t B, uint32_t IN, uint32_t OUT, uint32_t* ev_out,
+                   uint32_t* claims_out, uint32_t* u_batch_out, uint32_t* u_output_out,
+                   uint32_t* u_input_out) {
+    if (!B || !IN || !OUT) return 1;
+    fr* Xf = from_aos(X, (size_t)B * IN);
+    fr* Wf = from_aos(W, (size_t)IN * OUT);
+    fr* Yf = from_aos(Y, (size_t)B * OUT);
+    int rc = mm_prove_core(s, Xf, Wf, Yf, B, IN, OUT, ev_out, claims_out, u_batch_out, u_output_out,
+                           u_input_out);
+    free(Xf); free(Wf); free(Yf);
     return rc;
 }
 
@@ -669,11 +743,38 @@ int or_lu_prep(const uint32_t* S, uint32_t D, int32_t low, uint32_t N, uint32_t*
     return rc;
 }
 static void inv_table(const fr* in, uint32_t n, fr beta, fr* out) {
+#pragma omp parallel for if (n >= 256)
     for (uint32_t i = 0; i < n; i++) out[i] = inv(add(in[i], beta));
 }
 void or_lu_inverse(const uint32_t* S, uint32_t n, const uint32_t beta[8], uint32_t* A) {
     fr b = ld(beta);
+#pragma omp parallel for if (n >= 256)
     for (uint32_t i = 0; i < n; i++) st(A + 8 * i, inv(add(ld(S + 8 * i), b)));
+}
+
+/* out = a + c*b (FrTensor operator+ with a scalar multiple, e.g. comb = G + r*S,
+ * zkob_glu.cu:155-156) and out = a (.) b (FrTensor operator*, fr-tensor.cu elementwise) */
+void or_axpy(const uint32_t* a, const uint32_t c[8], const uint32_t* b, size_t n, uint32_t* out) {
+    const fr cm = mont(ld(c));
+#pragma omp parallel for if (n >= PAR_MIN)
+    for (size_t i = 0; i < n; i++) st(out + 8 * i, add(ld(a + 8 * i), mmul(cm, ld(b + 8 * i))));
+}
+void or_hadamard(const uint32_t* a, const uint32_t* b, size_t n, uint32_t* out) {
+#pragma omp parallel for if (n >= PAR_MIN)
+    for (size_t i = 0; i < n; i++) st(out + 8 * i, mul(ld(a + 8 * i), ld(b + 8 * i)));
+}
+/* entries violating A[i] (S[i] + beta) = 1, with A[i] = 0 required where S[i] + beta = 0
+ * (the Fermat convention of tlookup.cu:50-62): the identity that fixes 1/(S + beta) */
+size_t or_check_inverse(const uint32_t* S, const uint32_t* A, size_t n, const uint32_t beta[8]) {
+    const fr b = ld(beta);
+    size_t bad = 0;
+#pragma omp parallel for reduction(+ : bad) if (n >= PAR_MIN)
+    for (size_t i = 0; i < n; i++) {
+        const fr d = add(ld(S + 8 * i), b), a = ld(A + 8 * i);
+        const int ok = feq(d, ZERO) ? feq(a, ZERO) : feq(mul(a, d), ONE);
+        bad += !ok;
+    }
+    return bad;
 }
 
 /* Polynomial::eq(u) * {q0,q1,q2} -> degree-3 coefficients */
@@ -702,6 +803,7 @@ int or_lu_prove(uint8_t s[32], const uint32_t* Ain, const uint32_t* Sin, const u
     inv_table(T, N, beta, Bv); /* zkob_rescale.cu:132-135 */
     fr alpha_sq = mul(alpha, alpha);
     fr* bm = falloc(N);
+#pragma omp parallel for if (N >= PAR_MIN)
     for (uint32_t i = 0; i < N; i++) bm[i] = mul(Bv[i], m[i]);
     fr Cc = sub(alpha_sq, sum_fr(bm, N));
     free(bm);
@@ -716,15 +818,25 @@ int or_lu_prove(uint8_t s[32], const uint32_t* Ain, const uint32_t* Sin, const u
     while (sz != N) {
         uint32_t h = sz >> 1;
         fr sA0 = ZERO, sA1 = ZERO;
-        for (uint32_t i = 0; i < h; i++) {
-            fr c00 = A[i], c01 = sub(A[i + h], A[i]);
-            fr c10 = add(S[i], beta), c11 = sub(S[i + h], S[i]);
-            fr am = mont(alpha);
-            t0[i] = mmul(am, mul(c00, c10));
-            t1[i] = mmul(am, mont(add(mmul(c01, c10), mmul(c00, c11))));
-            t2[i] = mmul(am, mul(c01, c11));
-            sA0 = add(sA0, c00);
-            sA1 = add(sA1, c01);
+        const fr am = mont(alpha);
+#pragma omp parallel if (h >= PAR_MIN)
+        {
+            fr l0 = ZERO, l1 = ZERO;
+#pragma omp for nowait
+            for (uint32_t i = 0; i < h; i++) {
+                fr c00 = A[i], c01 = sub(A[i + h], A[i]);
+                fr c10 = add(S[i], beta), c11 = sub(S[i + h], S[i]);
+                t0[i] = mmul(am, mul(c00, c10));
+                t1[i] = mmul(am, mont(add(mmul(c01, c10), mmul(c00, c11))));
+                t2[i] = mmul(am, mul(c01, c11));
+                l0 = add(l0, c00);
+                l1 = add(l1, c01);
+            }
+#pragma omp critical
+            {
+                sA0 = add(sA0, l0);
+                sA1 = add(sA1, l1);
+            }
         }
         fr q[3] = {me_fr(t0, h, u, ulen - 1), me_fr(t1, h, u, ulen - 1),
                    me_fr(t2, h, u, ulen - 1)};
@@ -742,6 +854,7 @@ int or_lu_prove(uint8_t s[32], const uint32_t* Ain, const uint32_t* Sin, const u
         fr v = challenge(s);
         st(ws_out + 8 * r, v);
         fr vm = mont(v);
+#pragma omp parallel for if (h >= PAR_MIN)
         for (uint32_t i = 0; i < h; i++) {
             A[i] = add(A[i], mmul(vm, sub(A[i + h], A[i])));
             S[i] = add(S[i], mmul(vm, sub(S[i + h], S[i])));
@@ -762,6 +875,7 @@ int or_lu_prove(uint8_t s[32], const uint32_t* Ain, const uint32_t* Sin, const u
         fr am = mont(alpha), cm = mont(mul(inv_ratio, alpha_sq));
         fr q[3];
         /* A,S with alpha_ */
+#pragma omp parallel for if (h >= PAR_MIN)
         for (uint32_t i = 0; i < h; i++) {
             fr c00 = A[i], c01 = sub(A[i + h], A[i]);
             fr c10 = add(S[i], beta), c11 = sub(S[i + h], S[i]);
@@ -772,6 +886,7 @@ int or_lu_prove(uint8_t s[32], const uint32_t* Ain, const uint32_t* Sin, const u
         for (int j = 0; j < 3; j++)
             q[j] = me_fr(j == 0 ? t0 : j == 1 ? t1 : t2, h, u, ulen - 1);
         /* B,T with inv_ratio*alpha_sq */
+#pragma omp parallel for if (h >= PAR_MIN)
         for (uint32_t i = 0; i < h; i++) {
             fr c00 = Bv[i], c01 = sub(Bv[i + h], Bv[i]);
             fr c10 = add(T[i], beta), c11 = sub(T[i + h], T[i]);
@@ -784,10 +899,12 @@ int or_lu_prove(uint8_t s[32], const uint32_t* Ain, const uint32_t* Sin, const u
         fr c[4];
         eq_times(u[ulen - 1], q, c);
         /* + {sum A0, sum A1} (tLookup_phase2_poly_sum_kernel) */
+#pragma omp parallel for if (h >= PAR_MIN)
         for (uint32_t i = 0; i < h; i++) { t3[i] = A[i]; t4[i] = sub(A[i + h], A[i]); }
         c[0] = add(c[0], sum_fr(t3, h));
         c[1] = add(c[1], sum_fr(t4, h));
         /* - inv_ratio * {sum m0B0, sum m1B0+m0B1, sum m1B1} (dotprod kernel) */
+#pragma omp parallel for if (h >= PAR_MIN)
         for (uint32_t i = 0; i < h; i++) {
             fr a0 = m[i], a1 = sub(m[i + h], m[i]);
             fr b0 = Bv[i], b1 = sub(Bv[i + h], Bv[i]);
@@ -807,6 +924,7 @@ int or_lu_prove(uint8_t s[32], const uint32_t* Ain, const uint32_t* Sin, const u
         fr v = challenge(s);
         st(ws_out + 8 * r, v);
         fr vm = mont(v);
+#pragma omp parallel for if (h >= PAR_MIN)
         for (uint32_t i = 0; i < h; i++) {
             A[i] = add(A[i], mmul(vm, sub(A[i + h], A[i])));
             S[i] = add(S[i], mmul(vm, sub(S[i + h], S[i])));
@@ -853,17 +971,24 @@ int or_hp_prove(uint8_t s[32], const uint32_t claim_in[8], const uint32_t* Ein,
     while (sz > 1) {
         uint32_t h = sz >> 1;
         fr e[4] = {ZERO, ZERO, ZERO, ZERO};
-        for (uint32_t i = 0; i < h; i++) {
-            fr ee = E[i], de = sub(E[i + h], E[i]);
-            fr ss = S[i], ds = sub(S[i + h], S[i]);
-            fr uu = U[i], du = sub(U[i + h], U[i]);
-            for (int t = 0; t < 4; t++) {
-                fr es = mmul(mont(ee), mont(ss));
-                e[t] = add(e[t], mmul(es, uu));
-                ee = add(ee, de);
-                ss = add(ss, ds);
-                uu = add(uu, du);
+#pragma omp parallel if (h >= PAR_MIN)
+        {
+            fr l[4] = {ZERO, ZERO, ZERO, ZERO};
+#pragma omp for nowait
+            for (uint32_t i = 0; i < h; i++) {
+                fr ee = E[i], de = sub(E[i + h], E[i]);
+                fr ss = S[i], ds = sub(S[i + h], S[i]);
+                fr uu = U[i], du = sub(U[i + h], U[i]);
+                for (int t = 0; t < 4; t++) {
+                    fr es = mmul(mont(ee), mont(ss));
+                    l[t] = add(l[t], mmul(es, uu));
+                    ee = add(ee, de);
+                    ss = add(ss, ds);
+                    uu = add(uu, du);
+                }
             }
+#pragma omp critical
+            for (int t = 0; t < 4; t++) e[t] = add(e[t], l[t]);
         }
         if (strict && !feq(claim, add(e[0], e[1]))) { rc = 2; break; }
         for (int t = 0; t < 4; t++) st(ev_out + 32 * r + 8 * t, e[t]);
@@ -872,6 +997,7 @@ int or_hp_prove(uint8_t s[32], const uint32_t claim_in[8], const uint32_t* Ein,
         fr w = challenge(s);
         st(ws_out + 8 * r, w);
         fr wm = mont(w);
+#pragma omp parallel for if (h >= PAR_MIN)
         for (uint32_t i = 0; i < h; i++) { /* k_fr_fold x3 */
             E[i] = add(E[i], mmul(wm, sub(E[i + h], E[i])));
             S[i] = add(S[i], mmul(wm, sub(S[i + h], S[i])));
@@ -1106,6 +1232,7 @@ int or_rescale_fr(const uint32_t* x, uint32_t n, uint32_t sf, int64_t* q, int64_
 int or_matmul_fr(const uint32_t* A, const uint32_t* B, const uint32_t* bias, uint32_t M, uint32_t N, uint32_t Pc,
                  uint32_t* C) {
     if (!M || !N || !Pc) return 1;
+#pragma omp parallel for collapse(2) if ((size_t)M * Pc >= 64)
     for (uint32_t i = 0; i < M; i++)
         for (uint32_t j = 0; j < Pc; j++) {
             fr sum = ZERO;

@@ -37,6 +37,12 @@ void or_fr_inv(const uint32_t a[8], uint32_t out[8]);
 /* int64 -> Fr: v>=0 -> v, v<0 -> r-|v| (fr-tensor.cu:707-725) */
 void or_fr_from_i64(int64_t v, uint32_t out[8]);
 
+/* OpenMP threads of the table loops (1: the scalar CPU baseline); results do not depend on it */
+void or_set_threads(int n);
+int or_get_threads(void);
+/* int64 values -> Fr array (long_to_scalar per entry, fr-tensor.cu:701-717) */
+void or_ints_to_fr(const int64_t* v, size_t n, uint32_t* out);
+
 /* ---- SHA-256 transcript (fs_transcript.hpp:121-165; vrf_common.cuh:219-250) ---- */
 void or_sha256(const uint8_t* data, size_t n, uint8_t out[32]);
 void or_tr_init(uint8_t st[32], const char* seed, size_t seed_len);
@@ -78,6 +84,12 @@ int or_mm_prove(uint8_t st[32], const int32_t* X, const int32_t* W, const int64_
                 uint32_t B, uint32_t IN, uint32_t OUT,
                 uint32_t* ev_out, uint32_t* claims_out,
                 uint32_t* u_batch_out, uint32_t* u_output_out, uint32_t* u_input_out);
+/* the same segment on field-element tables X, W, Y (Fr arrays): the FrTensors zkob_fc binds
+ * (zkob_fc.cu:276-277, :337-338) */
+int or_mm_prove_fr(uint8_t st[32], const uint32_t* X, const uint32_t* W, const uint32_t* Y,
+                uint32_t B, uint32_t IN, uint32_t OUT,
+                uint32_t* ev_out, uint32_t* claims_out,
+                uint32_t* u_batch_out, uint32_t* u_output_out, uint32_t* u_input_out);
 
 /* ---- logUp / tLookup ---- */
 /* tLookupRange table: T[i] = low+i (i<len), else low+len-1 (tlookup.cu:372-391) */
@@ -88,6 +100,11 @@ void or_range_table(int32_t low, uint32_t len, uint32_t table_size, uint32_t* T)
 int or_lu_prep(const uint32_t* S, uint32_t D, int32_t low, uint32_t N, uint32_t* m);
 /* A[i] = 1/(S[i]+beta), per-element Fermat (tlookup.cu:50-62) */
 void or_lu_inverse(const uint32_t* S, uint32_t n, const uint32_t beta[8], uint32_t* A);
+/* out = a + c*b and out = a (.) b over n entries (FrTensor operators; zkob_glu.cu:155-156) */
+void or_axpy(const uint32_t* a, const uint32_t c[8], const uint32_t* b, size_t n, uint32_t* out);
+void or_hadamard(const uint32_t* a, const uint32_t* b, size_t n, uint32_t* out);
+/* number of entries with A[i] (S[i] + beta) != 1 (or A[i] != 0 where S[i] + beta = 0) */
+size_t or_check_inverse(const uint32_t* S, const uint32_t* A, size_t n, const uint32_t beta[8]);
 /* FS lookup recursion: zkob_rescale.cu:132-146 + zkob_lookup.cuh:143-198.
  * Inputs are the witness S (D), its inverse table A (D), the table T (N) and m (N),
  * alpha, beta and u (logD challenges, already drawn by the caller).  Computes
