@@ -233,6 +233,75 @@ def test_mm_prove_per_round_launch_path(zkh, ctx, monkeypatch):
     _mm_check_batch(zkh, ctx, [(4, 8, 4), (1, 1, 1), (33, 700, 129), (8, 2048, 8)], "perround")
 
 
+# Wide integer operands: the eq-weighted reductions switch from one 20-bit piece per int32
+# (|v| < 2^19) and two 22-bit pieces per int64 (|Y| < 2^43) to two / three 22-bit pieces.
+# Each case names which operands take the wide layout.
+def _wide_inputs(case, B, IN, OUT, seed):
+    rng = np.random.default_rng(seed)
+    if case == "all":  # X, W near +-2^24, |Y| ~ 2^54: every reduction wide
+        X = rng.integers(-2**24, 2**24, size=(B, IN), dtype=np.int64)
+        W = rng.integers(-2**24, 2**24, size=(IN, OUT), dtype=np.int64)
+        X[0, :] = 2**24 - 1
+        W[:, 0] = -(2**24 - 1)
+    elif case == "y":  # X, W narrow (|v| < 2^19) but |Y| >= 2^43
+        X = rng.integers(-(2**19 - 1), 2**19, size=(B, IN), dtype=np.int64)
+        W = rng.integers(-(2**19 - 1), 2**19, size=(IN, OUT), dtype=np.int64)
+        X[0, :] = 2**19 - 1
+        W[:, 0] = 2**19 - 1
+    else:  # "x": only X wide (int32 needing 2 pieces), W and Y narrow
+        X = rng.integers(-2**19, 2**19, size=(B, IN), dtype=np.int64)
+        X[1, 2] = -(2**30)
+        W = rng.integers(-2, 3, size=(IN, OUT), dtype=np.int64)
+    Y = X @ W  # exact int64 (|Y| < 2^63)
+    return X.astype(np.int32), W.astype(np.int32), Y
+
+
+WIDE_CASES = [("all", (8, 64, 16)), ("all", (3, 100, 5)), ("y", (4, 64, 8)), ("y", (33, 128, 7)),
+              ("x", (5, 40, 6))]
+
+
+@pytest.mark.parametrize("case,shape", WIDE_CASES)
+@pytest.mark.parametrize("weights", [True, False])
+def test_mm_prove_wide(zkh, ctx, case, shape, weights):
+    B, IN, OUT = shape
+    X, W, Y = _wide_inputs(case, B, IN, OUT, B * 7 + IN + OUT)
+    if case == "y":
+        assert np.abs(Y).max() >= 2**43 and np.abs(X).max() < 2**19 and np.abs(W).max() < 2**19
+    st_g, st_o = seed_transcript(zkh, "wide:%s:%d:%d:%d" % ((case,) + shape))
+    rc, want = C.mm_prove(st_o, X, W, Y, B, IN, OUT)
+    assert rc == 0
+    Wt = ctx.weights_i32(W, IN, OUT) if weights else ctx.from_i32(W)
+    got = ctx.mm_prove(st_g, ctx.from_i32(X), Wt, ctx.from_i64(Y), B, IN, OUT)
+    for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
+def test_mm_prove_batch_mixed_widths(zkh, ctx):
+    """Narrow and wide jobs in one batch: two eqdot launch groups in one call."""
+    items, wants, sts, keep = [], [], [], []
+    for idx, (case, shape) in enumerate(WIDE_CASES + [("narrow", (16, 12, 5)), ("narrow", (64, 128, 64))]):
+        B, IN, OUT = shape
+        if case == "narrow":
+            X, W, Y = _mm_inputs(shape, 900 + idx)
+        else:
+            X, W, Y = _wide_inputs(case, B, IN, OUT, 900 + idx)
+        st_g, st_o = seed_transcript(zkh, "mixed:%d" % idx)
+        rc, want = C.mm_prove(st_o, X, W, Y, B, IN, OUT)
+        assert rc == 0
+        t = (ctx.from_i32(X), ctx.weights_i32(W, IN, OUT) if idx % 2 else ctx.from_i32(W), ctx.from_i64(Y))
+        keep.append(t)
+        items.append((st_g, t[0], t[1], t[2], B, IN, OUT))
+        wants.append(want)
+        sts.append((st_g, st_o))
+    outs, status = ctx.mm_prove_batch(items)
+    assert status == [0] * len(items)
+    for got, want, (st_g, st_o) in zip(outs, wants, sts):
+        for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+            assert fr_eq(got[key], want[key]), key
+        assert bytes(st_g) == bytes(st_o)
+
+
 # ---------------------------------------------------------------- logUp
 LU_SHAPES = [(32, 8, -3, 5), (16, 16, 0, 16), (64, 4, -2, 3),  # vrf_toy_lookup.cu:323-335
              (32, 4, -2, 4), (64, 16, -8, 16), (48 * 0 + 64, 64, -32, 64),
