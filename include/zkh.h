@@ -131,8 +131,11 @@ int zkh_transcript_absorb(uint8_t state[32], const char* label, size_t label_len
 int zkh_transcript_challenge_fr(uint8_t state[32], uint32_t out[8]);
 
 /* ---------------- matmul sumcheck: zkob_fc.cu:259-440 ----------------
- * X: B x IN (I32), W: IN x OUT (I32, preferably from zkh_tensor_weights_i32), Y: B x OUT
- * (I64 or I32), Y = X*W.  The caller has absorbed B, IN, OUT and the commitments; this
+ * X: B x IN, W: IN x OUT, Y: B x OUT with Y = X*W over Fr, each either a field-element
+ * tensor (the FrTensors zkob_fc binds, zkob_fc.cu:276-277, :337-338) or an integer tensor
+ * (X, W: I32, W preferably from zkh_tensor_weights_i32; Y: I32 or I64 -- the int32 input
+ * files of zkob_fc.cu:178-185 and their product); kinds may be mixed.  The caller has
+ * absorbed B, IN, OUT and the commitments; this
  * draws u_batch, u_output, evaluates claim = Y~(u_batch,u_output), absorbs "claim", runs
  * the ceilLog2(IN) rounds (absorbing "p0","p1","p2" each) and absorbs "claim_X","claim_W".
  * ev_out: 3L Fr (p(0),p(1),p(2) per round: the sumcheck.bin evals, zkob_fc.cu:101-123);

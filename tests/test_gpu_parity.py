@@ -302,6 +302,113 @@ def test_mm_prove_batch_mixed_widths(zkh, ctx):
         assert bytes(st_g) == bytes(st_o)
 
 
+# Field-element operands: the FrTensors zkob_fc binds (zkob_fc.cu:276-277, :337-338).
+FR_SHAPES = [(4, 8, 4), (3, 5, 7), (1, 1, 1), (5, 1, 3), (16, 12, 5), (64, 128, 64), (33, 700, 129),
+             (128, 3000, 64), (2, 40000, 3)]
+
+
+def _fr_inputs(shape, seed):
+    B, IN, OUT = shape
+    rng = np.random.default_rng(seed)
+    X = rand_fr_full(rng, B * IN)
+    W = rand_fr_full(rng, IN * OUT)
+    rc, Y = C.matmul_fr(X, W, B, IN, OUT)
+    assert rc == 0
+    return X, W, Y
+
+
+@pytest.mark.parametrize("shape", FR_SHAPES)
+def test_mm_prove_fr(zkh, ctx, shape):
+    B, IN, OUT = shape
+    X, W, Y = _fr_inputs(shape, sum(shape) + 5)
+    st_g, st_o = seed_transcript(zkh, "mmfr:%d:%d:%d" % shape)
+    rc, want = C.mm_prove_fr(st_o, X, W, Y, B, IN, OUT)
+    assert rc == 0
+    got = ctx.mm_prove(st_g, ctx.from_fr(X), ctx.from_fr(W), ctx.from_fr(Y), B, IN, OUT)
+    for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
+@pytest.mark.parametrize("kinds", ["fii", "ifi", "iif", "ffi", "fif", "iff"])
+def test_mm_prove_mixed_kinds(zkh, ctx, kinds):
+    """Each of X, W, Y as an integer tensor (f: field-element tensor of the same values)."""
+    shape = (33, 700, 129)
+    B, IN, OUT = shape
+    X, W, Y = _mm_inputs(shape, 4242)
+    st_g, st_o = seed_transcript(zkh, "mixed-kinds:" + kinds)
+    rc, want = C.mm_prove(st_o, X, W, Y, B, IN, OUT)
+    assert rc == 0
+    tX = ctx.from_fr(C.ints_to_fr(X.ravel())) if kinds[0] == "f" else ctx.from_i32(X)
+    tW = ctx.from_fr(C.ints_to_fr(W.ravel())) if kinds[1] == "f" else ctx.weights_i32(W, IN, OUT)
+    tY = ctx.from_fr(C.ints_to_fr(Y.ravel())) if kinds[2] == "f" else ctx.from_i64(Y)
+    got = ctx.mm_prove(st_g, tX, tW, tY, B, IN, OUT)
+    for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
+def test_mm_prove_fr_batch_with_int_jobs(zkh, ctx):
+    items, wants, sts, keep = [], [], [], []
+    for idx, shape in enumerate(FR_SHAPES[:7]):
+        B, IN, OUT = shape
+        st_g, st_o = seed_transcript(zkh, "frbatch:%d" % idx)
+        if idx % 2:
+            X, W, Y = _mm_inputs(shape, 500 + idx)
+            rc, want = C.mm_prove(st_o, X, W, Y, B, IN, OUT)
+            t = (ctx.from_i32(X), ctx.weights_i32(W, IN, OUT), ctx.from_i64(Y))
+        else:
+            X, W, Y = _fr_inputs(shape, 500 + idx)
+            rc, want = C.mm_prove_fr(st_o, X, W, Y, B, IN, OUT)
+            t = (ctx.from_fr(X), ctx.from_fr(W), ctx.from_fr(Y))
+        assert rc == 0
+        keep.append(t)
+        items.append((st_g, t[0], t[1], t[2], B, IN, OUT))
+        wants.append(want)
+        sts.append((st_g, st_o))
+    outs, status = ctx.mm_prove_batch(items)
+    assert status == [0] * len(items)
+    for got, want, (st_g, st_o) in zip(outs, wants, sts):
+        for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+            assert fr_eq(got[key], want[key]), key
+        assert bytes(st_g) == bytes(st_o)
+
+
+def test_mm_prove_fr_wrong_witness(zkh, ctx):
+    X, W, Y = _fr_inputs((8, 16, 4), 77)
+    Y = Y.copy()
+    Y[5] = C.fr_op("add", Y[5], C.ints_to_fr([1])[0])
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.mm_prove(zkh.transcript("frbad"), ctx.from_fr(X), ctx.from_fr(W), ctx.from_fr(Y), 8, 16, 4)
+    assert e.value.code == zkh.EROUND
+
+
+def test_mm_prove_fr_tinyllama_layer_equals_int_path(zkh, ctx):
+    """The 7 TinyLlama matmuls with X, W, Y bound as field-element tensors: every proof equals
+    the integer-input proof of the same values (which test_gpu_configs checks against the
+    oracle at this size)."""
+    from zkh_synth import CONFIGS, matmul_inputs, rng_for
+    c = CONFIGS["C4"]
+    B = c["B"]
+    rng = rng_for(4)
+    items_i, items_f, keep = [], [], []
+    for name, IN, OUT in c["matmuls"]:
+        X, W, Y = matmul_inputs(rng, B, IN, OUT)
+        ti = (ctx.from_i32(X), ctx.weights_i32(W, IN, OUT), ctx.from_i64(Y))
+        tf = (ctx.from_fr(C.ints_to_fr(X.ravel())), ctx.from_fr(C.ints_to_fr(W.ravel())),
+              ctx.from_fr(C.ints_to_fr(Y.ravel())))
+        keep += [ti, tf]
+        items_i.append((zkh.transcript("frl:" + name), *ti, B, IN, OUT))
+        items_f.append((zkh.transcript("frl:" + name), *tf, B, IN, OUT))
+    outs_i, st_i = ctx.mm_prove_batch(items_i)
+    outs_f, st_f = ctx.mm_prove_batch(items_f)
+    assert st_i == [0] * 7 and st_f == [0] * 7
+    for a, b, ia, ib in zip(outs_i, outs_f, items_i, items_f):
+        for key in ("ev", "claims", "u_batch", "u_output", "u_input"):
+            assert fr_eq(a[key], b[key]), key
+        assert bytes(ia[0]) == bytes(ib[0])
+
+
 # ---------------------------------------------------------------- logUp
 LU_SHAPES = [(32, 8, -3, 5), (16, 16, 0, 16), (64, 4, -2, 3),  # vrf_toy_lookup.cu:323-335
              (32, 4, -2, 4), (64, 16, -8, 16), (48 * 0 + 64, 64, -32, 64),

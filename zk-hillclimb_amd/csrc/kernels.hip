@@ -1393,6 +1393,155 @@ void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_
         hipExtLaunchKernelGGL(k_eqdot_multi<EqdotI32x2, EqdotI64x3>, dim3(nblocks), dim3(NT), 0, s, t0, t1, 0, d_dev, nd);
 }
 
+// ------------------------------------------------------------------------------------
+// eq-weighted reductions of full field-element tables.  A product x e of two 8-limb
+// values is accumulated without reduction: its 64 limb products x_i e_j go into 15 column
+// sums of 96 bits (one v_mad_u64_u32 whose carry-out feeds one v_addc_co_u32 per
+// product), and a (column, chunk) cell is reduced once: two Montgomery reductions take the
+// 527-bit column total T to T 2^-512 mod r, and one multiplication by 2^512 mod r leaves
+// sum x (e 2^256) 2^-256 = sum x e for the Montgomery-form weights e.  Per element that is
+// 128 VALU instructions against ~330 for a reduced Montgomery product and a field add.
+// ------------------------------------------------------------------------------------
+struct Cols15 {
+    uint64_t lo[15];
+    uint32_t top[15];
+};
+ZDEV void cols15_zero(Cols15& a) {
+#pragma unroll
+    for (int p = 0; p < 15; p++) {
+        a.lo[p] = 0;
+        a.top[p] = 0;
+    }
+}
+// a += x e with the weight e in scalar registers (wave-uniform)
+ZDEV void cols15_mac_s(Cols15& a, const fr_t& x, const fr_t& e) {
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j += 2)
+            mac2_ss(a.lo[i + j], a.top[i + j], x.v[i], e.v[j], a.lo[i + j + 1], a.top[i + j + 1], x.v[i], e.v[j + 1]);
+}
+// a += x e with a per-lane weight
+ZDEV void cols15_mac_v(Cols15& a, const fr_t& x, const fr_t& e) {
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j += 2)
+            mac2_vv(a.lo[i + j], a.top[i + j], x.v[i], e.v[j], a.lo[i + j + 1], a.top[i + j + 1], x.v[i], e.v[j + 1]);
+}
+// sum_p (lo_p + top_p 2^64) 2^(32p) mod r, for a total below 2^544
+ZDEV fr_t cols15_reduce(const Cols15& a) {
+    uint32_t t[18];
+    uint64_t c = 0;
+#pragma unroll
+    for (int k = 0; k < 18; k++) {
+        uint64_t s = c;
+        if (k < 15) s += (uint32_t)a.lo[k];
+        if (k >= 1 && k <= 15) s += a.lo[k - 1] >> 32;
+        if (k >= 2 && k <= 16) s += a.top[k - 2];
+        t[k] = (uint32_t)s;
+        c = s >> 32;
+    }
+    // first reduction: t[8..17] = (T + m r) / 2^256 < 2^288 + r
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t m = 0u - t[i];
+        uint64_t cc = (uint64_t)m * ZKH_P0 + t[i];
+#pragma unroll
+        for (int j = 1; j < 8; j++) {
+            cc = (uint64_t)m * fr_p(j) + t[i + j] + (cc >> 32);
+            t[i + j] = (uint32_t)cc;
+        }
+#pragma unroll
+        for (int j = i + 8; j < 18; j++) {
+            cc = (uint64_t)t[j] + (cc >> 32);
+            t[j] = (uint32_t)cc;
+        }
+    }
+    // second reduction (its input is below r 2^256), then undo the remaining 2^-256
+    return mont_mul(redc_wide<10>(t + 8), r2_m());
+}
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+ZDEV fr_t ld_fr_stream(const uint4* lo, const uint4* hi, size_t i) {
+    const u32x4 a = ld_stream(reinterpret_cast<const u32x4*>(lo) + i);
+    const u32x4 b = ld_stream(reinterpret_cast<const u32x4*>(hi) + i);
+    fr_t r;
+    r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+    r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    return r;
+}
+// column mode: lane = output column i, rows of chunk c in groups of 4 with the next group's
+// loads issued before the current group's products
+ZDEV void eqdot_fr_cols(const EqDotFrDesc& q, uint32_t local) {
+    const uint32_t N = q.N;
+    const uint32_t ncb = (N + NT - 1) / NT;
+    const uint32_t i = (local % ncb) * NT + threadIdx.x;
+    const uint32_t c = local / ncb;
+    const uint32_t k0 = c * q.kchunk;
+    const uint32_t k1 = min(q.K, k0 + q.kchunk);
+    Cols15 a;
+    cols15_zero(a);
+    if (i < N) {
+        const uint4* lo = reinterpret_cast<const uint4*>(q.lo) + i;
+        const uint4* hi = reinterpret_cast<const uint4*>(q.hi) + i;
+        constexpr uint32_t G = 4;
+        uint32_t k = k0;
+        if (k + G <= k1) {
+            fr_t v[G];
+#pragma unroll
+            for (uint32_t u = 0; u < G; u++) v[u] = ld_fr_stream(lo, hi, (size_t)(k + u) * N);
+            for (; k + 2 * G <= k1; k += G) {
+                fr_t nx[G];
+#pragma unroll
+                for (uint32_t u = 0; u < G; u++) nx[u] = ld_fr_stream(lo, hi, (size_t)(k + G + u) * N);
+#pragma unroll
+                for (uint32_t u = 0; u < G; u++) cols15_mac_s(a, v[u], ld_aos_uniform(q.E, k + u));
+#pragma unroll
+                for (uint32_t u = 0; u < G; u++) v[u] = nx[u];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < G; u++) cols15_mac_s(a, v[u], ld_aos_uniform(q.E, k + u));
+            k += G;
+        }
+        for (; k < k1; k++) cols15_mac_s(a, ld_fr_stream(lo, hi, (size_t)k * N), ld_aos_uniform(q.E, k));
+    }
+    const fr_t r = cols15_reduce(a);
+    if (i < N) st_aos(q.partial, (size_t)c * N + i, r);
+}
+// row mode: wave w of the block reduces row i = local * 4 + w over its K entries (lane l
+// takes k = l, l + 64, ...), then a wave sum
+ZDEV void eqdot_fr_rows(const EqDotFrDesc& q, uint32_t local) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = local * (NT / 64) + (threadIdx.x >> 6);
+    Cols15 a;
+    cols15_zero(a);
+    if (row < q.N) {
+        const size_t base = (size_t)row * q.K;
+        const uint4* lo = reinterpret_cast<const uint4*>(q.lo) + base;
+        const uint4* hi = reinterpret_cast<const uint4*>(q.hi) + base;
+        uint32_t k = lane;
+        for (; k + 64 < q.K; k += 128) {  // two entries in flight per lane
+            const fr_t x0 = ld_fr_stream(lo, hi, k), x1 = ld_fr_stream(lo, hi, k + 64);
+            const fr_t e0 = ld_aos(q.E, k), e1 = ld_aos(q.E, k + 64);
+            cols15_mac_v(a, x0, e0);
+            cols15_mac_v(a, x1, e1);
+        }
+        if (k < q.K) cols15_mac_v(a, ld_fr_stream(lo, hi, k), ld_aos(q.E, k));
+    }
+    const fr_t r = fr_wave_sum(cols15_reduce(a));
+    if (row < q.N && lane == 0) st_aos(q.partial, row, r);
+}
+__global__ __launch_bounds__(NT) void k_eqdot_fr_multi(const EqDotFrDesc* __restrict__ d, uint32_t nd) {
+    const EqDotFrDesc& q = d[find_desc_uniform(d, nd)];
+    const uint32_t local = blockIdx.x - q.blk_begin;
+    if (q.rowmode) eqdot_fr_rows(q, local);
+    else eqdot_fr_cols(q, local);
+}
+void launch_eqdot_fr_multi(hipStream_t s, const EqDotFrDesc* d_dev, uint32_t nd, uint32_t nblocks, hipEvent_t t0,
+                           hipEvent_t t1) {
+    hipExtLaunchKernelGGL(k_eqdot_fr_multi, dim3(nblocks), dim3(NT), 0, s, t0, t1, 0, d_dev, nd);
+}
+
 // out[i] = sum_c partial[c*N+i] - corr (i < N; zero up to Npad), or, when E is set, the
 // block partial of sum_i E_m[i] * (sum_c partial[c*N+i] - corr) into dot[slot].  A block
 // covers 64 columns; wave w adds the chunks c = w (mod 4) with four loads in flight, and

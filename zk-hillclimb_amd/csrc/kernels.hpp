@@ -210,6 +210,21 @@ void launch_eq_mont_multi(hipStream_t s, const EqTabDesc* d_dev, uint32_t nd, ui
 // 22-bit pieces) and any int64 (three); chunks <= 512 rows for 22-bit pieces
 void launch_eqdot_multi(hipStream_t s, int wide, const EqDotDesc* d_dev, uint32_t nd, uint32_t nblocks,
                         hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
+// eq-weighted reductions of full field-element tables (the FrTensor inputs of zkob_fc,
+// zkob_fc.cu:276-277): column mode (rowmode = 0) partial[c*N+i] = sum_{k in rows
+// [c*kchunk, (c+1)*kchunk) of K} M[k*N+i] e_k, as for the integer reductions; row mode
+// (rowmode = 1) partial[i] = sum_{k < K} M[i*K+k] e_k, one wave per output i (row-major W
+// reduced over OUT).  M: limb-quad planes (lo, hi); E: Montgomery eq table, AoS; partials
+// plain.
+struct EqDotFrDesc {
+    const uint32_t* lo;
+    const uint32_t* hi;
+    const uint32_t* E;
+    uint32_t* partial;
+    uint32_t K, N, kchunk, blk_begin, rowmode, pad_;
+};
+void launch_eqdot_fr_multi(hipStream_t s, const EqDotFrDesc* d_dev, uint32_t nd, uint32_t nblocks,
+                           hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 void launch_sum_chunks_multi(hipStream_t s, const SumChunksDesc* d_dev, uint32_t nd, uint32_t nblocks,
                              hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 #define ZKH_MAX_BATCH 32

@@ -1242,13 +1242,15 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         const char* why = nullptr;
         if (!J.transcript || !X || !W || !Y) why = "null argument";
         else if (!J.B || !J.IN || !J.OUT) why = "zero dimension";
-        else if (X->kind != ZKH_KIND_I32 || W->kind != ZKH_KIND_I32 || Y->kind == ZKH_KIND_FR)
-            why = "mm_prove takes int32 X, W and int32/int64 Y";
+        else if ((X->kind != ZKH_KIND_I32 && X->kind != ZKH_KIND_FR) ||
+                 (W->kind != ZKH_KIND_I32 && W->kind != ZKH_KIND_FR))
+            why = "mm_prove takes int32 or field-element X and W";
         else if ((uint64_t)X->n != (uint64_t)J.B * J.IN || (uint64_t)W->n != (uint64_t)J.IN * J.OUT ||
                  (uint64_t)Y->n != (uint64_t)J.B * J.OUT)
             why = "input dims";
         else if (W->weights && (W->w_in != J.IN || W->w_out != J.OUT)) why = "weights dims";
-        else if (Y->bits > 62 || J.IN > (1u << 24) || J.B > (1u << 24) || J.OUT > (1u << 24))
+        else if ((Y->kind != ZKH_KIND_FR && Y->bits > 62) || J.IN > (1u << 24) || J.B > (1u << 24) ||
+                 J.OUT > (1u << 24))
             why = "integer range / size";
         if (why) {
             J.status = ZKH_EARG;
@@ -1289,7 +1291,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         eq_total += in.OUT;
         q.red_off = red_total;
         red_total += 2 * (size_t)q.INp;
-        if (!in.W->weights) wt_total += in.W->n;
+        if (in.W->kind == ZKH_KIND_I32 && !in.W->weights) wt_total += in.W->n;
         q.live = true;
     }
     // device areas
@@ -1340,8 +1342,9 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     }
     // 2) eq-weighted reductions: Y by eb (then dotted with eo -> claim), X by eb, W^T by eo
     struct Red {
-        EqDotDesc d;
-        int is64, wide;
+        EqDotDesc d;   // integer operands (d.partial, d.N also describe field operands)
+        EqDotFrDesc f;  // field-element operands
+        int is64, wide, fr;
         uint32_t nch, Npad, job, what;  // what: 0 Y, 1 X, 2 W
         Fr corr;
     };
@@ -1353,13 +1356,44 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         const Job& q = J[j];
         const Fr SEb = q.SEb, SEo = q.SEo;
         const int32_t* WT = (const int32_t*)in.W->d;
-        if (!in.W->weights) {
+        if (in.W->kind == ZKH_KIND_I32 && !in.W->weights) {
             launch_transpose_i32(c->stream, (const int32_t*)in.W->d, in.IN, in.OUT, wt_d + wt_off);
             WT = wt_d + wt_off;
             wt_off += in.W->n;
         }
         for (uint32_t what = 0; what < 3; what++) {
             Red r{};
+            const zkh_tensor* T = what == 0 ? in.Y : what == 1 ? in.X : in.W;
+            if (T->kind == ZKH_KIND_FR) {
+                // X (B x IN) and Y (B x OUT) reduce over their rows by eq(u_batch); W (IN x
+                // OUT, row-major) over its columns by eq(u_output), one wave per row
+                r.fr = 1;
+                r.f.lo = T->planes().lo();
+                r.f.hi = T->planes().hi();
+                r.f.E = eq_d + 8 * (what == 2 ? q.eo_off : q.eb_off);
+                r.f.rowmode = what == 2;
+                r.f.K = what == 2 ? in.OUT : in.B;
+                r.f.N = what == 0 ? in.OUT : in.IN;
+                uint32_t nch = 1;
+                if (!r.f.rowmode) {
+                    // about 2^16 (column, chunk) cells, 32..512 rows each: enough blocks for
+                    // the chip while a cell's reduction stays small next to its rows
+                    const uint32_t ncell = std::max<uint32_t>(1, 65536 / r.f.N);
+                    r.f.kchunk = std::min<uint32_t>(std::max<uint32_t>((r.f.K + ncell - 1) / ncell, 32), 512);
+                    nch = (r.f.K + r.f.kchunk - 1) / r.f.kchunk;
+                }
+                r.d.N = r.f.N;
+                r.d.K = r.f.K;
+                r.nch = nch;
+                r.Npad = what == 0 ? r.f.N : q.INp;
+                r.job = j;
+                r.what = what;
+                r.corr = kZero;
+                r.d.partial = (uint32_t*)(uintptr_t)(part_total * 32);  // offset, fixed below
+                part_total += (size_t)nch * r.f.N;
+                reds.push_back(r);
+                continue;
+            }
             const void* M = what == 0 ? in.Y->d : what == 1 ? in.X->d : (const void*)WT;
             uint32_t K = what == 2 ? in.OUT : in.B;
             uint32_t N = what == 0 ? in.OUT : in.IN;
@@ -1397,8 +1431,22 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     }
     uint32_t* part_d = (uint32_t*)scratch(c, SL_TMP6, part_total * 32, &rc);
     if (rc) return rc;
-    for (auto& r : reds) r.d.partial = part_d + (uintptr_t)r.d.partial / 4;
-    // group the reductions by piece layout -> one launch per group (normally one)
+    for (auto& r : reds) {
+        r.d.partial = part_d + (uintptr_t)r.d.partial / 4;
+        r.f.partial = r.d.partial;
+    }
+    // field-element reductions: one launch for all of them
+    std::vector<EqDotFrDesc> frds;
+    uint32_t fr_blocks = 0;
+    for (auto& r : reds) {
+        if (!r.fr) continue;
+        EqDotFrDesc d = r.f;
+        d.blk_begin = fr_blocks;
+        // 256-thread blocks: four rows per block in row mode, 256 columns per block otherwise
+        fr_blocks += r.f.rowmode ? (r.f.N + 3) / 4 : ((r.f.N + 255) / 256) * r.nch;
+        frds.push_back(d);
+    }
+    // group the integer reductions by piece layout -> one launch per group (normally one)
     std::vector<EqDotDesc> dots;
     struct Grp {
         int wide;
@@ -1408,7 +1456,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     for (int wide = 0; wide < 2; wide++) {
         Grp g{wide, (uint32_t)dots.size(), 0, 0};
         for (auto& r : reds) {
-            if (r.wide != wide) continue;
+            if (r.fr || r.wide != wide) continue;
             EqDotDesc d = r.d;
             d.blk_begin = g.blocks;
             g.blocks += ((r.d.N + 255) / 256) * r.nch;
@@ -1455,16 +1503,18 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         if (d.E) d.dot = pin + pin_claim + 8 * (uintptr_t)d.dot;
     // descriptors -> device (one area, one upload)
     size_t desc_bytes = eqd.size() * sizeof(EqTabDesc) + dots.size() * sizeof(EqDotDesc) +
-                        sums.size() * sizeof(SumChunksDesc) + 256;
+                        sums.size() * sizeof(SumChunksDesc) + frds.size() * sizeof(EqDotFrDesc) + 256;
     uint8_t* desc_d = (uint8_t*)scratch(c, SL_DESC, desc_bytes * 2, &rc);
     if (rc) return rc;
     std::vector<uint8_t> blob(desc_bytes, 0);
     size_t o_eq = 0, o_dot = o_eq + eqd.size() * sizeof(EqTabDesc);
     size_t o_sum = o_dot + dots.size() * sizeof(EqDotDesc);
-    size_t o_zk = (o_sum + sums.size() * sizeof(SumChunksDesc) + 63) & ~(size_t)63;
+    size_t o_fr = o_sum + sums.size() * sizeof(SumChunksDesc);
+    size_t o_zk = (o_fr + frds.size() * sizeof(EqDotFrDesc) + 63) & ~(size_t)63;
     memcpy(blob.data() + o_eq, eqd.data(), eqd.size() * sizeof(EqTabDesc));
     memcpy(blob.data() + o_dot, dots.data(), dots.size() * sizeof(EqDotDesc));
     memcpy(blob.data() + o_sum, sums.data(), sums.size() * sizeof(SumChunksDesc));
+    memcpy(blob.data() + o_fr, frds.data(), frds.size() * sizeof(EqDotFrDesc));
     if ((rc = upload(c, desc_d, blob.data(), o_zk))) return rc;
     stamp("descriptors uploaded");
     {
@@ -1472,9 +1522,17 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         launch_eq_mont_multi(c->stream, (const EqTabDesc*)(desc_d + o_eq), (uint32_t)eqd.size(), eq_blocks,
                              ps.start(), ps.stop());
     }
-    double red_bytes = 0;  // algorithmic: every stored integer of X, W and Y read once
-    for (auto& r : reds) red_bytes += (double)r.d.K * r.d.N * (r.is64 ? 8 : 4);
-    {
+    double red_bytes = 0, fr_bytes = 0;  // algorithmic: every stored entry of X, W and Y read once
+    for (auto& r : reds) {
+        if (r.fr) fr_bytes += (double)r.d.K * r.d.N * 32;
+        else red_bytes += (double)r.d.K * r.d.N * (r.is64 ? 8 : 4);
+    }
+    if (!frds.empty()) {
+        ProfScope ps(c, "eqdot_fr", fr_bytes, true);
+        launch_eqdot_fr_multi(c->stream, (const EqDotFrDesc*)(desc_d + o_fr), (uint32_t)frds.size(), fr_blocks,
+                              ps.start(), ps.stop());
+    }
+    if (!groups.empty()) {
         ProfScope ps(c, "eqdot", red_bytes, true);
         for (size_t gi = 0; gi < groups.size(); gi++) {
             const Grp& g = groups[gi];
