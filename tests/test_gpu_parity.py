@@ -47,6 +47,23 @@ def test_me(zkh, ctx, n, k):
     assert fr_eq(got, want)
 
 
+@pytest.mark.parametrize("n,k", [(8, 3), (1000, 10), (70000, 17)])
+def test_me_boolean_and_one_coordinates(zkh, ctx, n, k):
+    """FrTensor::operator()(u) at points with coordinates 0 and 1: at a Boolean point the MLE
+    is the table entry itself; a coordinate 1 among random ones matches the oracle."""
+    rng = np.random.default_rng(n + k)
+    t = rand_fr_full(rng, n)
+    tt = ctx.from_fr(t)
+    for idx in (0, n - 1, n // 3):
+        u = C.ints_to_fr([(idx >> b) & 1 for b in range(k)])
+        assert fr_eq(ctx.me(tt, u), t[idx])
+    u = rand_fr_full(rng, k)
+    u[k // 2] = C.ints_to_fr([1])[0]
+    rc, want = C.me(t, u)
+    assert rc == 0
+    assert fr_eq(ctx.me(tt, u), want)
+
+
 @pytest.mark.parametrize("shape", [(6, 5, 3), (4, 8, 1), (1, 7, 2), (3, 64, 5)])
 def test_partial_me(zkh, ctx, shape):
     O, Cd, Wd = shape

@@ -329,7 +329,7 @@ enum {
     SL_DESC,
     SL_COUNT
 };
-static void* scratch(zkh_ctx* c, int slot, size_t bytes, int* rc) {
+static void* scratch_slot(zkh_ctx* c, int slot, size_t bytes, int* rc) {
     if ((int)c->slots.size() < SL_COUNT) c->slots.resize(SL_COUNT);
     zkh_ctx::Slot& s = c->slots[slot];
     if (s.bytes >= bytes && s.p) return s.p;
@@ -349,7 +349,7 @@ static void* scratch(zkh_ctx* c, int slot, size_t bytes, int* rc) {
 }
 static DevPlanes scratch_planes(zkh_ctx* c, int slot, uint32_t n, int* rc) {
     uint32_t cap = n ? n : 1;
-    void* p = scratch(c, slot, (size_t)cap * 32, rc);
+    void* p = scratch_slot(c, slot, (size_t)cap * 32, rc);
     return DevPlanes{(uint32_t*)p, cap};
 }
 static int ensure_pinned(zkh_ctx* c, size_t bytes) {
@@ -512,17 +512,20 @@ struct EqState {
     std::vector<Fr> corr;  // corr[K] for K = 0..kmax
     uint32_t nvars = 0;
 };
-static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st) {
+// all_rounds: the caller will weight shorter prefixes K < |u| (sumcheck rounds), which
+// needs every 1 - u_t invertible; a single full-length weighting (K = |u|) needs no
+// correction and accepts any point, e.g. a Boolean one.
+static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_rounds = true) {
     int rc = 0;
     std::vector<uint32_t> fac;
     make_fac(u, 10, fac);
     st.nvars = (uint32_t)u.size();
     const uint32_t kmax = std::max<uint32_t>(st.nvars, 10), khi = kmax - 10;
-    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, fac.size() * 4, &rc);
+    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, fac.size() * 4, &rc);
     if (rc) return rc;
-    st.elo_d = (uint32_t*)scratch(c, SL_ELO, 1024 * 32, &rc);
+    st.elo_d = (uint32_t*)scratch_slot(c, SL_ELO, 1024 * 32, &rc);
     if (rc) return rc;
-    st.ehi_d = (uint32_t*)scratch(c, SL_EHI, ((size_t)32 << khi), &rc);
+    st.ehi_d = (uint32_t*)scratch_slot(c, SL_EHI, ((size_t)32 << khi), &rc);
     if (rc) return rc;
     if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
     launch_eq_mont(c->stream, fac_d, 10, 1024, st.elo_d);
@@ -532,7 +535,12 @@ static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st) {
     prefix[0] = kOne;
     for (uint32_t t = 0; t < kmax; t++)
         prefix[t + 1] = fr_mul(prefix[t], t < st.nvars ? fr_sub(kOne, u[t]) : kOne);
-    if (fr_eq(prefix[kmax], kZero)) return fail(c, ZKH_EARG, "degenerate eq challenge (u_t = 1)");
+    if (fr_eq(prefix[kmax], kZero)) {
+        if (all_rounds) return fail(c, ZKH_EARG, "degenerate eq challenge (u_t = 1)");
+        st.corr.assign(kmax + 1, kZero);
+        st.corr[st.nvars] = kOne;  // the factors of positions >= |u| are 1 - 0
+        return 0;
+    }
     const Fr inv = fr_inv(prefix[kmax]);
     st.corr.resize(kmax + 1);
     for (uint32_t K = 0; K <= kmax; K++) st.corr[K] = fr_mul(prefix[K], inv);
@@ -682,7 +690,7 @@ static int tensor_alloc(zkh_ctx* c, int kind, uint32_t n, zkh_tensor** out) {
 }
 static int int_bits_i32(zkh_ctx* c, const int32_t* d, uint32_t n, uint32_t* bits) {
     int rc = 0;
-    uint32_t* m = (uint32_t*)scratch(c, SL_SMALL, 64, &rc);
+    uint32_t* m = (uint32_t*)scratch_slot(c, SL_SMALL, 64, &rc);
     if (rc) return rc;
     HIPCHK(c, hipMemsetAsync(m, 0, 4, c->stream));
     launch_absmax_i32(c->stream, d, n, m);
@@ -694,7 +702,7 @@ static int int_bits_i32(zkh_ctx* c, const int32_t* d, uint32_t n, uint32_t* bits
 }
 static int int_bits_i64(zkh_ctx* c, const int64_t* d, uint32_t n, uint32_t* bits) {
     int rc = 0;
-    unsigned long long* m = (unsigned long long*)scratch(c, SL_SMALL, 64, &rc);
+    unsigned long long* m = (unsigned long long*)scratch_slot(c, SL_SMALL, 64, &rc);
     if (rc) return rc;
     HIPCHK(c, hipMemsetAsync(m, 0, 8, c->stream));
     launch_absmax_i64(c->stream, d, n, m);
@@ -779,7 +787,7 @@ extern "C" int zkh_tensor_from_fr(zkh_ctx* c, const uint32_t* aos, uint32_t n, z
     if (rc) return rc;
     if (n) {
         // the entries, then one word counting non-canonical entries (checked on the device)
-        uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)n * 32 + 256, &rc);
+        uint32_t* stage = (uint32_t*)scratch_slot(c, SL_TMP6, (size_t)n * 32 + 256, &rc);
         uint32_t* bad = stage + 8 * (size_t)n;
         uint32_t nbad = 0;
         hipError_t e = hipSuccess;
@@ -827,7 +835,7 @@ static int as_planes(zkh_ctx* c, const zkh_tensor* t, int slot, DevPlanes* out) 
     if (t->kind == ZKH_KIND_I32) {
         if (t->weights) {
             // logical W (IN x OUT) from the OUT-major copy
-            int32_t* rm = (int32_t*)scratch(c, SL_TMP5, (size_t)t->n * 4, &rc);
+            int32_t* rm = (int32_t*)scratch_slot(c, SL_TMP5, (size_t)t->n * 4, &rc);
             if (rc) return rc;
             launch_transpose_i32(c->stream, (const int32_t*)t->d, t->w_out, t->w_in, rm);
             launch_i32_to_planes(c->stream, rm, t->n, p);
@@ -847,7 +855,7 @@ extern "C" int zkh_tensor_to_i64(zkh_ctx* c, const zkh_tensor* t, int64_t* out) 
     int rc;
     DevPlanes p;
     if ((rc = as_planes(c, t, SL_TMP4, &p))) return rc;
-    int64_t* d = (int64_t*)scratch(c, SL_TMP6, (size_t)t->n * 8, &rc);
+    int64_t* d = (int64_t*)scratch_slot(c, SL_TMP6, (size_t)t->n * 8, &rc);
     if (rc) return rc;
     launch_to_long(c->stream, p, t->n, d);
     HIPCHK(c, hipMemcpyAsync(out, d, (size_t)t->n * 8, hipMemcpyDeviceToHost, c->stream));
@@ -861,7 +869,7 @@ extern "C" int zkh_tensor_to_fr(zkh_ctx* c, const zkh_tensor* t, uint32_t* aos) 
     int rc = 0;
     DevPlanes p;
     if ((rc = as_planes(c, t, SL_TMP4, &p))) return rc;
-    uint32_t* stage = (uint32_t*)scratch(c, SL_TMP6, (size_t)t->n * 32, &rc);
+    uint32_t* stage = (uint32_t*)scratch_slot(c, SL_TMP6, (size_t)t->n * 32, &rc);
     if (rc) return rc;
     launch_planes_to_aos(c->stream, p, t->n, stage);
     HIPCHK(c, hipMemcpyAsync(aos, stage, (size_t)t->n * 32, hipMemcpyDeviceToHost, c->stream));
@@ -897,7 +905,7 @@ static int eq_weighted_sum(zkh_ctx* c, DevPlanes S, const DevPlanes* U, uint32_t
                            const std::vector<Fr>& u, Fr* out) {
     int rc = 0;
     EqState st;
-    if ((rc = eq_setup(c, u, st))) return rc;
+    if ((rc = eq_setup(c, u, st, false))) return rc;
     uint32_t K = (uint32_t)u.size();
     uint32_t nb;
     {
@@ -988,10 +996,10 @@ static int eq_table_mont(zkh_ctx* c, const std::vector<Fr>& u, uint32_t n, int s
     int rc = 0;
     std::vector<uint32_t> fac;
     make_fac(u, 0, fac);
-    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
+    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
     if (rc) return rc;
     if (!fac.empty() && (rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
-    uint32_t* e = (uint32_t*)scratch(c, slot, (size_t)std::max<uint32_t>(n, 1) * 32, &rc);
+    uint32_t* e = (uint32_t*)scratch_slot(c, slot, (size_t)std::max<uint32_t>(n, 1) * 32, &rc);
     if (rc) return rc;
     launch_eq_mont(c->stream, fac_d, (uint32_t)u.size(), n, e);
     *out = e;
@@ -1084,14 +1092,14 @@ extern "C" int zkh_eq_table(zkh_ctx* c, const uint32_t* u, uint32_t k, zkh_tenso
     int rc = 0;
     std::vector<uint32_t> fac;
     make_fac(load_frs(u, k), 0, fac);
-    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
+    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
     if (rc) return rc;
     if (k && (rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
     // E = Tlo (first min(k,10) variables, Montgomery) (x) Thi (the rest, plain)
     const uint32_t klo = k < 10 ? k : 10, khi = k - klo;
-    uint32_t* tlo = (uint32_t*)scratch(c, SL_EB, ((size_t)1 << klo) * 32, &rc);
+    uint32_t* tlo = (uint32_t*)scratch_slot(c, SL_EB, ((size_t)1 << klo) * 32, &rc);
     if (rc) return rc;
-    uint32_t* thi = (uint32_t*)scratch(c, SL_EO, ((size_t)1 << khi) * 32, &rc);
+    uint32_t* thi = (uint32_t*)scratch_slot(c, SL_EO, ((size_t)1 << khi) * 32, &rc);
     if (rc) return rc;
     EqTabDesc d[2] = {};
     d[0].fac = fac_d;
@@ -1105,7 +1113,7 @@ extern "C" int zkh_eq_table(zkh_ctx* c, const uint32_t* u, uint32_t k, zkh_tenso
     d[1].n = 1u << khi;
     d[1].blk_begin = (d[0].n + 255) / 256;
     d[1].plain = 1;
-    EqTabDesc* d_dev = (EqTabDesc*)scratch(c, SL_DESC, sizeof(d), &rc);
+    EqTabDesc* d_dev = (EqTabDesc*)scratch_slot(c, SL_DESC, sizeof(d), &rc);
     if (rc) return rc;
     if ((rc = upload(c, d_dev, d, sizeof(d)))) return rc;
     zkh_tensor* t;
@@ -1313,13 +1321,13 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             q.SEo = eq_prefix_sum(q.uo, jobs[j].OUT);
         }
     });
-    uint32_t* fac_d = (uint32_t*)scratch(c, SL_FAC, fac.size() * 4, &rc);
+    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, fac.size() * 4, &rc);
     if (rc) return rc;
-    uint32_t* eq_d = (uint32_t*)scratch(c, SL_EB, eq_total * 32, &rc);
+    uint32_t* eq_d = (uint32_t*)scratch_slot(c, SL_EB, eq_total * 32, &rc);
     if (rc) return rc;
     DevPlanes red = scratch_planes(c, SL_TMP0, (uint32_t)red_total, &rc);
     if (rc) return rc;
-    int32_t* wt_d = wt_total ? (int32_t*)scratch(c, SL_TMP5, wt_total * 4, &rc) : nullptr;
+    int32_t* wt_d = wt_total ? (int32_t*)scratch_slot(c, SL_TMP5, wt_total * 4, &rc) : nullptr;
     if (rc) return rc;
     if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
 
@@ -1429,7 +1437,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             reds.push_back(r);
         }
     }
-    uint32_t* part_d = (uint32_t*)scratch(c, SL_TMP6, part_total * 32, &rc);
+    uint32_t* part_d = (uint32_t*)scratch_slot(c, SL_TMP6, part_total * 32, &rc);
     if (rc) return rc;
     for (auto& r : reds) {
         r.d.partial = part_d + (uintptr_t)r.d.partial / 4;
@@ -1504,7 +1512,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     // descriptors -> device (one area, one upload)
     size_t desc_bytes = eqd.size() * sizeof(EqTabDesc) + dots.size() * sizeof(EqDotDesc) +
                         sums.size() * sizeof(SumChunksDesc) + frds.size() * sizeof(EqDotFrDesc) + 256;
-    uint8_t* desc_d = (uint8_t*)scratch(c, SL_DESC, desc_bytes * 2, &rc);
+    uint8_t* desc_d = (uint8_t*)scratch_slot(c, SL_DESC, desc_bytes * 2, &rc);
     if (rc) return rc;
     std::vector<uint8_t> blob(desc_bytes, 0);
     size_t o_eq = 0, o_dot = o_eq + eqd.size() * sizeof(EqTabDesc);
@@ -2008,7 +2016,7 @@ extern "C" int zkh_lu_range_table(zkh_ctx* c, int32_t low, uint32_t len, uint32_
 }
 static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, uint32_t** counts_out) {
     int rc = 0;
-    uint32_t* counts = (uint32_t*)scratch(c, SL_TMP5, (size_t)(N + 1) * 4, &rc);
+    uint32_t* counts = (uint32_t*)scratch_slot(c, SL_TMP5, (size_t)(N + 1) * 4, &rc);
     if (rc) return rc;
     uint32_t* bad = counts + N;
     HIPCHK(c, hipMemsetAsync(counts, 0, (size_t)(N + 1) * 4, c->stream));
@@ -2083,9 +2091,9 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
 static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, DevPlanes A) {
     int rc = 0;
     uint32_t nb = inv_blocks(n);
-    uint32_t* others = (uint32_t*)scratch(c, SL_TMP4, (size_t)nb * 256 * 32, &rc);
+    uint32_t* others = (uint32_t*)scratch_slot(c, SL_TMP4, (size_t)nb * 256 * 32, &rc);
     if (rc) return rc;
-    uint32_t* bp = (uint32_t*)scratch(c, SL_SMALL, (size_t)nb * 64 + 64, &rc);
+    uint32_t* bp = (uint32_t*)scratch_slot(c, SL_SMALL, (size_t)nb * 64 + 64, &rc);
     if (rc) return rc;
     uint32_t* others_blk = bp + 8 * (size_t)nb;
     uint32_t bl[8];
@@ -2547,7 +2555,7 @@ extern "C" int zkh_matmul_i32(zkh_ctx* c, const zkh_tensor* X, const zkh_tensor*
     int rc = 0;
     const int32_t* WT = (const int32_t*)W->d;
     if (!W->weights) {  // row-major IN x OUT: transpose once into scratch
-        int32_t* wt = (int32_t*)scratch(c, SL_TMP5, (size_t)W->n * 4, &rc);
+        int32_t* wt = (int32_t*)scratch_slot(c, SL_TMP5, (size_t)W->n * 4, &rc);
         if (rc) return rc;
         launch_transpose_i32(c->stream, (const int32_t*)W->d, IN, OUT, wt);
         WT = wt;
@@ -2555,7 +2563,7 @@ extern "C" int zkh_matmul_i32(zkh_ctx* c, const zkh_tensor* X, const zkh_tensor*
     const int64_t* bd = nullptr;
     if (bias) {
         if (bias->kind == ZKH_KIND_I32) {
-            int64_t* b64 = (int64_t*)scratch(c, SL_TMP4, (size_t)OUT * 8, &rc);
+            int64_t* b64 = (int64_t*)scratch_slot(c, SL_TMP4, (size_t)OUT * 8, &rc);
             if (rc) return rc;
             launch_widen_i32(c->stream, (const int32_t*)bias->d, OUT, b64);
             bd = b64;
@@ -2713,12 +2721,12 @@ extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, z
         DevPlanes p;
         uint16_t* lists = nullptr;
         uint32_t *offs = nullptr, *buckets = nullptr, *partials = nullptr;
-        if (!(rc = as_planes(c, t, SL_TMP0, &p))) lists = (uint16_t*)scratch(c, SL_TMP1, (size_t)m * 64 * n * 2, &rc);
-        if (!rc) offs = (uint32_t*)scratch(c, SL_TMP2, (size_t)m * 64 * 16 * 4, &rc);
-        if (!rc) buckets = (uint32_t*)scratch(c, SL_TMP3, (size_t)m * 64 * 16 * 144, &rc);
-        if (!rc) partials = (uint32_t*)scratch(c, SL_TMP6, (size_t)m * 64 * 144, &rc);
+        if (!(rc = as_planes(c, t, SL_TMP0, &p))) lists = (uint16_t*)scratch_slot(c, SL_TMP1, (size_t)m * 64 * n * 2, &rc);
+        if (!rc) offs = (uint32_t*)scratch_slot(c, SL_TMP2, (size_t)m * 64 * 16 * 4, &rc);
+        if (!rc) buckets = (uint32_t*)scratch_slot(c, SL_TMP3, (size_t)m * 64 * 16 * 144, &rc);
+        if (!rc) partials = (uint32_t*)scratch_slot(c, SL_TMP6, (size_t)m * 64 * 144, &rc);
         uint16_t* alias = nullptr;
-        if (!rc) alias = (uint16_t*)scratch(c, SL_TMP4, (size_t)m * 64 * 16 * 2, &rc);
+        if (!rc) alias = (uint16_t*)scratch_slot(c, SL_TMP4, (size_t)m * 64 * 16 * 2, &rc);
         if (rc) {
             zkh_g1_free(o);
             return rc;
@@ -2770,9 +2778,9 @@ extern "C" int zkh_ipa_prove(zkh_ctx* c, uint8_t* transcript, const zkh_tensor* 
     int rc = 0;
     // a, b, g working copies (two of each, the fold writes the other), round products P,
     // inner products, L and R
-    uint32_t* fr_w = (uint32_t*)scratch(c, SL_TMP1, (size_t)n * 32 * 4, &rc);
-    uint32_t* g_w = rc ? nullptr : (uint32_t*)scratch(c, SL_TMP2, (size_t)n * 144 * 2, &rc);
-    uint32_t* P = rc ? nullptr : (uint32_t*)scratch(c, SL_TMP3, (size_t)(n + 2) * 144 + 1024, &rc);
+    uint32_t* fr_w = (uint32_t*)scratch_slot(c, SL_TMP1, (size_t)n * 32 * 4, &rc);
+    uint32_t* g_w = rc ? nullptr : (uint32_t*)scratch_slot(c, SL_TMP2, (size_t)n * 144 * 2, &rc);
+    uint32_t* P = rc ? nullptr : (uint32_t*)scratch_slot(c, SL_TMP3, (size_t)(n + 2) * 144 + 1024, &rc);
     if (rc) return rc;
     uint32_t* ip = P + 36 * (size_t)(n + 2);
     uint32_t* LR = ip + 16;
