@@ -87,6 +87,13 @@ int zkh_sum(zkh_ctx* ctx, const zkh_tensor* t, uint32_t out[8]);
 /* FrTensor::operator()(u): LSB-first MLE evaluation, u[0] binds bit 0 (fr-tensor.cu:437-442,
  * :588-609); requires 2^(k-1) < n <= 2^k */
 int zkh_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k, uint32_t out[8]);
+/* zkh_me without device allocation.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Its device scratch (eq tables, block partials,
+ * counters: 557,312 bytes) is one static array per device, held until the process ends and
+ * resolved at zkh_ctx_create; the call allocates nothing.  t: a field-element tensor;
+ * k <= 24 (ZKH_EARG beyond).  Calls that overlap on one device share that scratch and race. */
+int zkh_me_static(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k, uint32_t out[8]);
 /* one degree-2 product round over MSB pairs (k_bo_hp2 + bo_dev_sum, zkob_claims.cuh:367-383,
  * :577-592): out[t] = sum_{i < n/2} a_t[i] b_t[i] for t = 0, 1, 2, with
  * X_t[i] = X[i] + t (X[i + n/2] - X[i]); a, b FR tensors of one even size n.  With zkh_fold

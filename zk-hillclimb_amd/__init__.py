@@ -59,6 +59,7 @@ def lib():
         L.zkh_tensor_to_fr.argtypes = [vp, vp, vp]
         L.zkh_sum.argtypes = [vp, vp, vp]
         L.zkh_me.argtypes = [vp, vp, vp, u32, vp]
+        L.zkh_me_static.argtypes = [vp, vp, vp, u32, vp]
         L.zkh_partial_me.argtypes = [vp, vp, vp, u32, u32, u32, ctypes.POINTER(vp)]
         L.zkh_multi_dim_me.argtypes = [vp, vp, vp, vp, vp, u32, vp]
         L.zkh_eq_table.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
@@ -262,6 +263,13 @@ class Context:
         u = _frs(u)
         out = np.zeros(8, dtype=np.uint32)
         self._chk(lib().zkh_me(self.h, t.h, _p(u), u.shape[0], _p(out)))
+        return out
+
+    def me_static(self, t, u):
+        """zkh_me without device allocation (static per-device scratch)."""
+        u = _frs(u)
+        out = np.zeros(8, dtype=np.uint32)
+        self._chk(lib().zkh_me_static(self.h, t.h, _p(u), u.shape[0], _p(out)))
         return out
 
     def partial_me(self, t, u, cur_dim, window):

@@ -1183,6 +1183,15 @@ uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t 
 }
 
 
+__global__ void k_static_setup(StaticFacArg fac, uint32_t words, uint32_t* fac_dst, uint32_t* cnt, uint32_t ncnt) {
+    for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) fac_dst[i] = fac.w[i];
+    for (uint32_t i = threadIdx.x; i < ncnt; i += blockDim.x) cnt[i] = 0;
+}
+void launch_static_setup(hipStream_t s, const StaticFacArg& fac, uint32_t words, uint32_t* fac_dst,
+                         uint32_t* cnt, uint32_t ncnt) {
+    k_static_setup<<<1, NT, 0, s>>>(fac, words, fac_dst, cnt, ncnt);
+}
+
 // ------------------------------------------------------------------------------------
 // Batched (multi-job) kernels: one launch serves every independent sumcheck of a batch
 // (e.g. the 7 matmuls of a layer).  Blocks are assigned to jobs contiguously; each job's

@@ -161,6 +161,15 @@ uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish pub);
 
+// setup of the allocation-free MLE evaluation: copies `words` factor words (passed by value)
+// to fac_dst and zeroes ncnt completion counters, all inside caller-provided device memory
+#define ZKH_STATIC_MAX_VARS 24
+struct StaticFacArg {
+    uint32_t w[ZKH_STATIC_MAX_VARS * 16];  // (1 - u_t, u_t) per variable, Montgomery form
+};
+void launch_static_setup(hipStream_t s, const StaticFacArg& fac, uint32_t words, uint32_t* fac_dst,
+                         uint32_t* cnt, uint32_t ncnt);
+
 uint32_t grid_for(uint32_t work_items, uint32_t per_block, uint32_t max_blocks);
 
 

@@ -347,6 +347,37 @@ static void* scratch_slot(zkh_ctx* c, int slot, size_t bytes, int* rc) {
     s.bytes = want;
     return s.p;
 }
+// Device scratch of the allocation-free entry point zkh_me_static: its eq factor table, the
+// two eq tables (up to ZKH_STATIC_MAX_VARS variables), the block partials and completion
+// counters of its one reduction.  Every device holds its own copy, at its own address, for
+// the life of the process; host code uses only the address that hipGetSymbolAddress gives
+// for the current device (kept per device at context creation), never the array's name.
+// Calls that overlap on one device share the copy and race.
+static constexpr size_t kStFac = 0;                                  // <= 24 x 2 Fr
+static constexpr size_t kStElo = 4096;                               // 1024 Fr
+static constexpr size_t kStEhi = kStElo + 1024 * 32;                 // 2^(24-10) Fr
+static constexpr size_t kStPart = kStEhi + ((size_t)32 << (ZKH_STATIC_MAX_VARS - 10));  // 1024 Fr
+static constexpr size_t kStCnt = kStPart + 1024 * 32;               // 2 words (+ padding)
+static constexpr size_t kStBytes = kStCnt + 256;                     // 557,312 bytes
+static __device__ __align__(256) uint8_t scratch[kStBytes];
+#define ZKH_MAX_DEVICES 64
+static uint8_t* g_static_scratch[ZKH_MAX_DEVICES];
+static std::mutex g_static_mu;
+// resolve this device's copy once (the device must be current)
+static int static_scratch_init(int device) {
+    if (device < 0 || device >= ZKH_MAX_DEVICES) return ZKH_EARG;
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (g_static_scratch[device]) return ZKH_OK;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return ZKH_EDEV;
+    g_static_scratch[device] = (uint8_t*)p;
+    return ZKH_OK;
+}
+static uint8_t* static_scratch(int device) {
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    return device >= 0 && device < ZKH_MAX_DEVICES ? g_static_scratch[device] : nullptr;
+}
+
 static DevPlanes scratch_planes(zkh_ctx* c, int slot, uint32_t n, int* rc) {
     uint32_t cap = n ? n : 1;
     void* p = scratch_slot(c, slot, (size_t)cap * 32, rc);
@@ -570,7 +601,8 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
     if (device < 0 || device >= ndev) return ZKH_EARG;
     zkh_ctx* c = new zkh_ctx();
     c->device = device;
-    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    if (hipSetDevice(device) != hipSuccess || static_scratch_init(device) != ZKH_OK ||
+        hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return ZKH_EDEV;
     }
@@ -988,6 +1020,52 @@ extern "C" int zkh_me(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u, uint32
     if ((rc = as_planes(c, t, SL_TMP0, &p))) return rc;
     Fr s;
     if ((rc = eq_weighted_sum(c, p, nullptr, t->n, load_frs(u, k), &s))) return rc;
+    fr_store(s, out);
+    return ZKH_OK;
+}
+// zkh_me without device allocation: the same eq-weighted sum (eq tables Elo, Ehi from the
+// factors of u, one reduction kernel publishing through the context's pinned words), with
+// every device buffer in the static scratch.  Field-element tensors of up to 2^24 entries.
+extern "C" int zkh_me_static(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u, uint32_t k, uint32_t out[8]) {
+    if (!c || !t || !out || (!u && k)) return fail(c, ZKH_EARG, "null argument");
+    if (k >= 32 || t->n <= ((1u << k) / 2) || t->n > (1u << k))
+        return fail(c, ZKH_EARG, "Incompatible dimensions");
+    if (k > ZKH_STATIC_MAX_VARS)
+        return fail(c, ZKH_EARG, "zkh_me_static: %u variables exceed its static scratch (at most %u)", k,
+                    (unsigned)ZKH_STATIC_MAX_VARS);
+    if (t->kind != ZKH_KIND_FR) return fail(c, ZKH_EARG, "zkh_me_static takes a field-element tensor");
+    if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    HIPCHK(c, hipSetDevice(c->device));
+    uint8_t* base = static_scratch(c->device);
+    if (!base) return fail(c, ZKH_EDEV, "static scratch of device %d not resolved", c->device);
+    // factors (1 - u_t, u_t) in Montgomery form for t < max(k, 10); positions >= k are (1, 0)
+    const uint32_t kmax = std::max<uint32_t>(k, 10), khi = kmax - 10;
+    StaticFacArg fac;
+    for (uint32_t t2 = 0; t2 < kmax; t2++) {
+        Fr a = fr_to_mont(kOne), b = kZero;
+        if (t2 < k) {
+            const Fr ut = fr_load(u + 8 * (size_t)t2);
+            a = fr_to_mont(fr_sub(kOne, ut));
+            b = fr_to_mont(ut);
+        }
+        fr_store(a, fac.w + 16 * t2);
+        fr_store(b, fac.w + 16 * t2 + 8);
+    }
+    uint32_t* fac_d = (uint32_t*)(base + kStFac);
+    uint32_t* elo = (uint32_t*)(base + kStElo);
+    uint32_t* ehi = (uint32_t*)(base + kStEhi);
+    uint32_t* cnt = (uint32_t*)(base + kStCnt);
+    launch_static_setup(c->stream, fac, kmax * 16, fac_d, cnt, 2);
+    launch_eq_mont(c->stream, fac_d, 10, 1024, elo);
+    launch_eq_mont(c->stream, fac_d + 2 * 10 * 8, khi, 1u << khi, ehi);
+    Publish pb = make_pub(c, 1);
+    pb.part = (uint32_t*)(base + kStPart);  // launch_eq_sum uses at most 1024 blocks
+    pb.counter = cnt;
+    launch_eq_sum(c->stream, t->planes(), nullptr, t->n, EqW{elo, ehi, k}, pb);
+    int rc;
+    if ((rc = wait_pub(c, pb.seq))) return rc;
+    Fr s;
+    pub_read(c, 0, 1, &s);  // the full-length weighting needs no correction
     fr_store(s, out);
     return ZKH_OK;
 }
