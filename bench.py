@@ -27,9 +27,15 @@ TinyLlama-1.1B".
   step).  roofline: the dominant kernel's algorithmic bytes over its duration in a second
   live pass of the same steps, from HIP events that the launch itself stamps at its start
   and end (hipExtLaunchKernel on the library's stream, read through the zkh_prof_* hooks),
-  so the figure is the kernel's execution time as a kernel trace reports it; cpu_baseline:
-  the C oracle (scalar port of the reference schedule) on the Q, K, V and O matmuls, one
-  thread.
+  so the figure is the kernel's execution time as a kernel trace reports it.
+- layer_roofline: the same for the dominant kernel class of the SwiGLU segment.
+- fr_inputs: the 7 matmuls with X, W, Y bound as field-element tensors (32 B per entry).
+- configs: BASELINE configs C2 (llama-68m FFN matmuls), C3 (logUp 2^20 vs 2^16) and C5
+  (OpenLLaMA-3B layer at seq 2048: matmuls, SwiGLU lookup 2^25 vs 2^22 + Hadamard).
+- cpu_baseline: the C oracle (scalar port of the reference schedule) on the Q, K, V, O
+  matmuls on one thread and on all cores, on the GPU proofs' own transcripts, each proof
+  asserted byte-identical to the GPU's; layer.cpu_baseline: the whole layer hot path the
+  same way (all cores; one thread estimated from bounded samples); C3 likewise.
 """
 import argparse
 import concurrent.futures
@@ -80,32 +86,39 @@ def pow2(n):
 
 
 LAYER = dict(B=512, d=2048, kv=256, ffn=5632, heads=32, hd=64)
-MATMULS = [("q", 2048, 2048), ("k", 2048, 256), ("v", 2048, 256), ("o", 2048, 2048),
-           ("gate", 2048, 5632), ("up", 2048, 5632), ("down", 5632, 2048)]
 
 
-def mm_elements(B, IN, OUT):
-    return B * IN + IN * OUT + B * OUT + 2 * IN
+def _oracle():
+    """The C oracle, imported only by the CPU-baseline legs (test infrastructure)."""
+    sys.path.insert(0, ROOT)
+    from oracle import coracle
+    return coracle
 
 
 class MatmulJob:
-    def __init__(self, zkh, synth, rng, name, B, IN, OUT):
+    """One zkob_fc sumcheck segment (zkob_fc.cu:254-345) with its own transcript; fr=True binds
+    X, W, Y as field-element tensors (the FrTensors of zkob_fc.cu:276-277) instead of ints."""
+
+    def __init__(self, zkh, synth, rng, name, B, IN, OUT, tag="cfg4:layer0", fr=False, inputs=None):
         self.zkh, self.name, self.B, self.IN, self.OUT = zkh, name, B, IN, OUT
-        X = synth.gaussian_int16(rng, (B, IN))
-        W = synth.fp8_e4m3_ints(rng, (IN, OUT))
-        Y = synth.matmul_exact(X, W)
+        X, W, Y = inputs if inputs is not None else synth.matmul_inputs(rng, B, IN, OUT)
         self.ctx = zkh.Context(0)
-        self.X = self.ctx.from_i32(X)
-        self.W = self.ctx.weights_i32(W, IN, OUT)
-        self.Y = self.ctx.from_i64(Y)
-        st = zkh.transcript("cfg4:layer0.%s" % name)
+        if fr:
+            self.X = self.ctx.from_fr(zkh.ints_to_fr(X))
+            self.W = self.ctx.from_fr(zkh.ints_to_fr(W))
+            self.Y = self.ctx.from_fr(zkh.ints_to_fr(Y))
+        else:
+            self.X = self.ctx.from_i32(X)
+            self.W = self.ctx.weights_i32(W, IN, OUT)
+            self.Y = self.ctx.from_i64(Y)
+        st = zkh.transcript("%s.%s" % (tag, name))
         for lab, v in (("B", B), ("IN", IN), ("OUT", OUT)):
             zkh.absorb(st, lab, struct.pack("<I", v))
         zkh.absorb(st, "com_X", blob(name + "X", pow2(B) * 144))
         zkh.absorb(st, "com_W", blob(name + "W", pow2(IN) * 144))
         zkh.absorb(st, "com_Y", blob(name + "Y", pow2(B) * 144))
         self.st0 = st
-        self.elements = mm_elements(B, IN, OUT)
+        self.elements = synth.mm_elements(B, IN, OUT)
         self.inputs = (X, W, Y)
 
     def run(self):
@@ -113,36 +126,42 @@ class MatmulJob:
         out = self.ctx.mm_prove(st, self.X, self.W, self.Y, self.B, self.IN, self.OUT)
         return out["claims"].tobytes() + st.tobytes()
 
+    @staticmethod
+    def result(out, st):
+        """Bytes that identify a proof: round evaluations, claims, challenges, transcript."""
+        return b"".join(out[k].tobytes() for k in ("ev", "claims", "u_batch", "u_output", "u_input")) + st.tobytes()
+
+    def cpu_run(self):
+        C = _oracle()
+        st = self.st0.copy()
+        rc, out = C.mm_prove(st, *self.inputs, self.B, self.IN, self.OUT)
+        assert rc == 0
+        return self.result(out, st)
+
 
 class GluJob:
-    """SwiGLU obligation hot path (zkob_glu.cu:146-247): mapping lookup + Hadamard."""
+    """SwiGLU obligation hot path (zkob_glu.cu:146-247): mapping lookup of G into the silu
+    table, combiner comb = G + r S against T_comb = T + r silu, the logUp proof, and the
+    eq-weighted Hadamard sumcheck of H = S (.) U."""
 
-    def __init__(self, zkh, synth, rng, B, C, scale_bits=12):
+    def __init__(self, zkh, synth, rng, B, C, N=None, tag="cfg4:layer0", inputs=None):
         self.zkh = zkh
-        Cp, Bp = pow2(C), pow2(B)
-        self.D = D = Bp * Cp
-        self.N = N = D
-        self.low = low = -(N // 2)
+        inp = inputs if inputs is not None else synth.glu_inputs(rng, B, C, N=N)
+        self.inp = inp
+        self.D, self.N, self.low = inp["D"], inp["N"], inp["low"]
         self.ctx = zkh.Context(0)
-        G = np.zeros((Bp, Cp), np.int32)
-        G[:B, :C] = rng.integers(low, low + N, size=(B, C))
-        U = np.zeros((Bp, Cp), np.int32)
-        U[:B, :C] = synth.gaussian_int16(rng, (B, C))
-        x = (np.arange(N, dtype=np.float64) + low) / (1 << scale_bits)
-        silu = np.rint(x / (1.0 + np.exp(-x)) * (1 << scale_bits)).astype(np.int32)
-        assert silu[-low] == 0  # the table holds (0, 0), so zero padding is a valid row
-        self.G = self.ctx.from_i32(G)
-        self.U = self.ctx.from_i32(U)
-        self.mapped = self.ctx.from_i32(silu)
-        self.T = self.ctx.range_table(low, N, N)
-        st = zkh.transcript("cfg4:layer0.swiglu")
-        for lab, v in (("B", B), ("C", C), ("LOW", low & 0xFFFFFFFF), ("LEN", N)):
+        self.G = self.ctx.from_i32(inp["G"].ravel())
+        self.U = self.ctx.from_i32(inp["U"].ravel())
+        self.mapped = self.ctx.from_i32(inp["silu"])
+        self.T = self.ctx.range_table(self.low, self.N, self.N)
+        st = zkh.transcript(tag + ".swiglu")
+        for lab, v in (("B", B), ("C", C), ("LOW", self.low & 0xFFFFFFFF), ("LEN", self.N)):
             zkh.absorb(st, lab, struct.pack("<I", v))
         for lab in ("com_G", "com_S", "com_U", "com_H", "com_m"):
-            zkh.absorb(st, lab, blob("glu" + lab, Bp * 144))
+            zkh.absorb(st, lab, blob("glu" + lab, inp["Bp"] * 144))
         self.st0 = st
-        self.comA = blob("gluA", Bp * 144)
-        self.logD = D.bit_length() - 1
+        self.comA = blob("gluA", inp["Bp"] * 144)
+        self.logD = self.D.bit_length() - 1
 
     def run(self):
         zkh, c = self.zkh, self.ctx
@@ -164,37 +183,58 @@ class GluJob:
         hp = c.hp_prove_eq(st, claim_H, u_h, S, self.U)
         zkh.absorb(st, "S_f2", hp["term"][0].tobytes())
         zkh.absorb(st, "U_f2", hp["term"][1].tobytes())
-        return lu["term"].tobytes() + hp["term"].tobytes() + st.tobytes()
+        return lu["ev"].tobytes() + lu["term"].tobytes() + hp["ev"].tobytes() + hp["term"].tobytes() + st.tobytes()
+
+    def cpu_run(self):
+        """The same segment on the C oracle (the reference's schedule: per-element Fermat
+        inverses, per-round MLE re-evaluation), on the same transcript."""
+        C = _oracle()
+        inp, low, N = self.inp, self.low, self.N
+        G = inp["G"].ravel()
+        st = self.st0.copy()
+        Gf = C.ints_to_fr(G)
+        Sf = C.ints_to_fr(inp["silu"][G.astype(np.int64) - low])
+        Uf = C.ints_to_fr(inp["U"].ravel())
+        rc, m = C.lu_prep(Gf, low, N)
+        assert rc == 0
+        r = C.tr_challenge_fr(st)
+        beta = C.tr_challenge_fr(st)
+        comb = C.axpy(Gf, r, Sf)
+        Tcomb = C.axpy(C.range_table(low, N, N), r, C.ints_to_fr(inp["silu"]))
+        A = C.lu_inverse(comb, beta)
+        C.tr_absorb(st, "com_A", self.comA)
+        alpha = C.tr_challenge_fr(st)
+        u = np.array([C.tr_challenge_fr(st) for _ in range(self.logD)])
+        rc, lu = C.lu_prove(st, A, comb, Tcomb, m, alpha, beta, u)
+        assert rc == 0
+        u_h = np.array([C.tr_challenge_fr(st) for _ in range(self.logD)])
+        rc, claim = C.me(C.hadamard(Sf, Uf), u_h)
+        C.tr_absorb(st, "claim_H", claim.tobytes())
+        rc, hp = C.hp_prove(st, claim, C.build_eq(u_h), Sf, Uf)
+        assert rc == 0
+        C.tr_absorb(st, "S_f2", hp["term"][0].tobytes())
+        C.tr_absorb(st, "U_f2", hp["term"][1].tobytes())
+        return lu["ev"].tobytes() + lu["term"].tobytes() + hp["ev"].tobytes() + hp["term"].tobytes() + st.tobytes()
 
 
 class RopeJob:
     """One RoPE obligation (zkob_rope.cu:215-281): two eq-weighted Hadamard sumchecks
     c1 = sum eq(u,b) W1(b) T(b) and c2 = sum eq(u,b) W2(b) Tx(b), with U = 1."""
 
-    def __init__(self, zkh, rng, name, B, C, HD=64):
+    def __init__(self, zkh, synth, rng, name, B, C, HD=64, tag="cfg4:layer0"):
         self.zkh = zkh
-        Bp, Cp = pow2(B), pow2(C)
-        self.D = Bp * Cp
+        self.inp = inp = synth.rope_inputs(rng, B, C, HD)
+        self.D = inp["D"]
         self.logD = self.D.bit_length() - 1
         self.ctx = c = zkh.Context(0)
-        T = np.zeros((Bp, Cp), np.int32)
-        T[:B, :C] = rng.integers(-(1 << 15), 1 << 15, size=(B, C))
-        e = np.arange(Cp)
-        flip = e ^ (HD // 2)
-        Tx = T[:, np.minimum(flip, Cp - 1)] * (flip < Cp)
-        t = np.arange(Bp)[:, None]
-        ang = t / (10000.0 ** ((2 * ((e % HD) // 2)) / HD))[None, :]
-        sigma = np.where(e & (HD // 2), 1, -1)[None, :]
-        W1 = np.where(e[None, :] < C, np.rint(np.cos(ang) * 65536), 0).astype(np.int32)
-        W2 = np.where(e[None, :] < C, sigma * np.rint(np.sin(ang) * 65536), 0).astype(np.int32)
-        self.T, self.Tx = c.from_i32(T), c.from_i32(Tx.astype(np.int32))
-        self.W1, self.W2 = c.from_i32(W1), c.from_i32(W2)
+        self.T, self.Tx = c.from_i32(inp["T"].ravel()), c.from_i32(inp["Tx"].ravel())
+        self.W1, self.W2 = c.from_i32(inp["W1"].ravel()), c.from_i32(inp["W2"].ravel())
         self.ONE = c.from_i32(np.ones(self.D, np.int32))
-        st = zkh.transcript("cfg4:layer0.rope." + name)
+        st = zkh.transcript(tag + ".rope." + name)
         for lab, v in (("B", B), ("C", C), ("HD", HD), ("SCALE_R", 16)):
             zkh.absorb(st, lab, struct.pack("<I", v))
-        zkh.absorb(st, "com_T", blob("rope" + name + "T", Bp * 144))
-        zkh.absorb(st, "com_Y64", blob("rope" + name + "Y", Bp * 144))
+        zkh.absorb(st, "com_T", blob("rope" + name + "T", inp["Bp"] * 144))
+        zkh.absorb(st, "com_Y64", blob("rope" + name + "Y", inp["Bp"] * 144))
         self.st0 = st
 
     def run(self):
@@ -210,8 +250,73 @@ class RopeJob:
             hp = c.hp_prove(st, claim, E, S, self.ONE)
             zkh.absorb(st, "S_f2", hp["term"][0].tobytes())
             zkh.absorb(st, "U_f2", hp["term"][1].tobytes())
-            outs.append(hp["term"].tobytes())
+            outs.append(hp["ev"].tobytes() + hp["term"].tobytes())
         return b"".join(outs) + st.tobytes()
+
+    def cpu_run(self):
+        C = _oracle()
+        st = self.st0.copy()
+        u = np.array([C.tr_challenge_fr(st) for _ in range(self.logD)])
+        Eu = C.build_eq(u)
+        one = C.ints_to_fr(np.ones(self.D, np.int64))
+        outs = []
+        for lab, Wk, Sk in (("c1", "W1", "T"), ("c2", "W2", "Tx")):
+            Sf = C.ints_to_fr(self.inp[Sk].ravel())
+            E = C.hadamard(Eu, C.ints_to_fr(self.inp[Wk].ravel()))
+            claim = np.zeros(8, np.uint32)
+            C.lib().or_sum(C._p(np.ascontiguousarray(C.hadamard(E, Sf))), self.D, C._p(claim))
+            C.tr_absorb(st, lab, claim.tobytes())
+            rc, hp = C.hp_prove(st, claim, E, Sf, one)
+            assert rc == 0
+            C.tr_absorb(st, "S_f2", hp["term"][0].tobytes())
+            C.tr_absorb(st, "U_f2", hp["term"][1].tobytes())
+            outs.append(hp["ev"].tobytes() + hp["term"].tobytes())
+        return b"".join(outs) + st.tobytes()
+
+
+class LookupJob:
+    """BASELINE config 3 / zkob_rescale's lookup (zkob_rescale.cu:110-150): 2^20 witnesses
+    uniform in [-2^15, 2^15) against tLookupRange(-2^15, 2^16): multiplicities, the batched
+    inverse 1/(S + beta) and the logUp sumcheck."""
+
+    def __init__(self, zkh, rng, D, N, low, tag="cfg3"):
+        self.zkh, self.D, self.N, self.low = zkh, D, N, low
+        self.vals = rng.integers(low, low + N, size=D).astype(np.int32)
+        self.ctx = c = zkh.Context(0)
+        self.S = c.from_i32(self.vals)
+        self.T = c.range_table(low, N, N)
+        st = zkh.transcript(tag + ".rescale")
+        zkh.absorb(st, "com_rem", blob("c3rem", 1024 * 144))
+        self.st0 = st
+        self.logD = D.bit_length() - 1
+
+    def run(self):
+        zkh, c = self.zkh, self.ctx
+        st = self.st0.copy()
+        m = c.lu_prep(self.S, self.low, self.N)
+        beta = zkh.challenge(st)
+        A = c.lu_inverse(self.S, beta)
+        alpha = zkh.challenge(st)
+        u = np.array([zkh.challenge(st) for _ in range(self.logD)])
+        lu = c.lu_prove(st, A, self.S, self.T, m, alpha, beta, u)
+        return lu["ev"].tobytes() + lu["term"].tobytes() + st.tobytes()
+
+    def cpu_run(self, sample=None):
+        """The oracle on the same transcript; sample = D' < D runs the first D' witnesses
+        against the same table instead (a bounded single-thread sample, not compared)."""
+        C = _oracle()
+        vals = self.vals if sample is None else self.vals[:sample]
+        D = len(vals)
+        st = self.st0.copy()
+        Sf = C.ints_to_fr(vals)
+        rc, m = C.lu_prep(Sf, self.low, self.N)
+        beta = C.tr_challenge_fr(st)
+        A = C.lu_inverse(Sf, beta)
+        alpha = C.tr_challenge_fr(st)
+        u = np.array([C.tr_challenge_fr(st) for _ in range(D.bit_length() - 1)])
+        rc, lu = C.lu_prove(st, A, Sf, C.range_table(self.low, self.N, self.N), m, alpha, beta, u)
+        assert rc == 0
+        return lu["ev"].tobytes() + lu["term"].tobytes() + st.tobytes()
 
 
 def witness_gemm(zkh, jobs, reps=5):
@@ -447,26 +552,143 @@ def commit_cpu_baseline(j, rows=1):
                       "(%d scalars, %.1f s, 1 thread)" % (rows, total, secs)}
 
 
-def cpu_baseline(jobs, budget_names=("q", "k", "v", "o")):
-    """The C oracle (reference algorithmic schedule, scalar, one thread) on a bounded
-    sample: the four attention projections of the same layer."""
-    sys.path.insert(0, ROOT)
-    from oracle import coracle
-    total_e, total_t = 0, 0.0
+def host_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "cpu_model": model}
+
+
+def timed(fn):
+    t = time.perf_counter()
+    out = fn()
+    return out, time.perf_counter() - t
+
+
+def cpu_baseline(jobs, outs, names=("q", "k", "v", "o")):
+    """The C oracle (the reference's algorithmic schedule: partial_me + multi_dim_me passes,
+    per-round zkip kernels) on the Q, K, V, O matmuls of the same layer, on the GPU proofs'
+    own transcripts: each CPU proof must equal the GPU's byte for byte.  Timed on one thread
+    and on all the host cores the process may use."""
+    C = _oracle()
+    host = host_info()
+    sel = [(j, o) for j, o in zip(jobs, outs) if j.name in names]
+    E = sum(j.elements for j, _ in sel)
+    res = {}
+    for label, thr in (("single_thread", 1), ("all_cores", host["affinity"])):
+        C.set_threads(thr)
+        t = 0.0
+        for j, (out, st) in sel:
+            got, secs = timed(j.cpu_run)
+            assert got == MatmulJob.result(out, st), "CPU proof differs from the GPU's (%s)" % j.name
+            t += secs
+        res[label] = {"value": E / t, "cores": thr, "s": round(t, 3)}
+    best = res["all_cores"]
+    return {"value": best["value"], "unit": "Fr elements/s", "cores": best["cores"], "kind": "port",
+            "sample": "C oracle (reference schedule: partial_me + multi_dim_me passes, per-round zkip "
+                      "kernels) on the Q,K,V,O matmul sumchecks of the same layer (%d elements) on the GPU "
+                      "proofs' transcripts, every proof byte-identical to the GPU's; %d threads %.2f s, "
+                      "1 thread %.2f s" % (E, best["cores"], best["s"], res["single_thread"]["s"]),
+            "single_thread": {"value": res["single_thread"]["value"], "cores": 1, "s": res["single_thread"]["s"]},
+            **host}
+
+
+def layer_cpu_baseline(jobs, mm_outs, others, others_ref, glu, rope_k, synth):
+    """The whole layer hot path on the C oracle, all cores, on the GPU's transcripts (every
+    segment byte-identical to the GPU's): the 7 matmuls, the SwiGLU lookup + Hadamard and
+    the RoPE Hadamards.  One thread is estimated from bounded samples: the Q,K,V,O matmuls
+    (scaled by elements to the 7), the SwiGLU segment at 2^16 entries (scaled by 2^22 / 2^16)
+    and the RoPE k obligation (2^17, scaled by entries to q + k)."""
+    C = _oracle()
+    host = host_info()
+    C.set_threads(host["affinity"])
+    t_mm = 0.0
+    for j, (out, st) in zip(jobs, mm_outs):
+        got, secs = timed(j.cpu_run)
+        assert got == MatmulJob.result(out, st), "CPU proof differs from the GPU's (%s)" % j.name
+        t_mm += secs
+    seg = {}
+    for j, ref in zip(others, others_ref):
+        got, secs = timed(j.cpu_run)
+        assert got == ref, "CPU segment differs from the GPU's (%s)" % type(j).__name__
+        seg[type(j).__name__ + ":2^%d" % j.logD] = round(secs, 3)
+    all_cores = t_mm + sum(seg.values())
+    # one thread, bounded samples
+    C.set_threads(1)
+    E_all = sum(j.elements for j in jobs)
+    qkvo = [j for j in jobs if j.name in ("q", "k", "v", "o")]
+    t1_qkvo = sum(timed(j.cpu_run)[1] for j in qkvo)
+    small = GluJob(glu.zkh, synth, synth.rng_for(99), 64, 1024)  # D = N = 2^16
+    t1_glu = timed(small.cpu_run)[1] * (glu.D / small.D)
+    t1_rope = timed(rope_k.cpu_run)[1] * (sum(o.D for o in others if isinstance(o, RopeJob)) / rope_k.D)
+    C.set_threads(host["affinity"])
+    one = t1_qkvo * E_all / sum(j.elements for j in qkvo) + t1_glu + t1_rope
+    return {"value": all_cores, "unit": "s per layer", "cores": host["affinity"], "kind": "port",
+            "sample": "the whole TinyLlama layer hot path on the C oracle (reference schedule, per-element "
+                      "Fermat inverses), all cores, every output byte-identical to the GPU's: 7 matmuls %.2f s, "
+                      "segments %s" % (t_mm, seg),
+            "single_thread_estimate_s": round(one, 2),
+            "single_thread_basis": "Q,K,V,O matmuls on 1 thread scaled by elements to the 7 (%.2f s); SwiGLU "
+                                   "segment at D = N = 2^16 on 1 thread scaled to 2^22 (%.2f s); RoPE k on 1 "
+                                   "thread scaled to q + k (%.2f s)" % (t1_qkvo, t1_glu, t1_rope),
+            **host}
+
+
+def prof_kernels(zkh, ctx, reps=1):
+    """Per-kernel-class device time (ms per run), launches and algorithmic bytes of the
+    launch-stamped records on one context."""
+    import ctypes
+    kern = {}
+    buf = ctypes.create_string_buffer(4096)
+    zkh.lib().zkh_prof_names(ctx.h, buf, 4096)
+    for name in filter(None, buf.value.decode().split(",")):
+        ms, la, by = ctypes.c_double(), ctypes.c_uint64(), ctypes.c_double()
+        zkh.lib().zkh_prof_get(ctx.h, name.encode(), ctypes.byref(ms), ctypes.byref(la), ctypes.byref(by))
+        kern[name] = [ms.value / reps, la.value / reps, by.value / reps]
+    return kern
+
+
+def mm_batch_rate(zkh, jobs, steps, warmup):
+    """Elements bound per second of one batched call over the jobs (inputs resident)."""
+    ctx = jobs[0].ctx
     for j in jobs:
-        if j.name not in budget_names:
-            continue
-        X, W, Y = j.inputs
-        st = coracle.tr_init("cpu")
-        t0 = time.perf_counter()
-        rc, _ = coracle.mm_prove(st, X, W, Y, j.B, j.IN, j.OUT)
-        total_t += time.perf_counter() - t0
-        assert rc == 0
-        total_e += j.elements
-    return {"value": total_e / total_t, "unit": "Fr elements/s", "cores": 1, "kind": "port",
-            "sample": "C oracle (reference schedule: partial_me + multi_dim_me passes, per-round "
-                      "zkip kernels) on the Q,K,V,O matmul sumchecks of the same layer "
-                      "(%d elements, %.1f s, 1 thread)" % (total_e, total_t)}
+        j.st = j.st0.copy()
+    mb = zkh.MmBatch(ctx, [(j.st, j.X, j.W, j.Y, j.B, j.IN, j.OUT) for j in jobs])
+
+    def step():
+        for j in jobs:
+            np.copyto(j.st, j.st0)
+        mb.run()
+    for _ in range(warmup):
+        step()
+    ref = [MatmulJob.result(o, j.st) for o, j in zip(mb.outs, jobs)]
+    gc.collect()
+    gc.disable()
+    t = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ms = (time.perf_counter() - t) * 1000.0 / steps
+    gc.enable()
+    assert [MatmulJob.result(o, j.st) for o, j in zip(mb.outs, jobs)] == ref
+    E = sum(j.elements for j in jobs)
+    return {"value": E / (ms / 1000.0), "unit": "Fr elements/s", "ms_per_step": round(ms, 4),
+            "elements_bound_per_step": E}, mb, ref
+
+
+def seg_time(job, reps):
+    ref = job.run()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        assert job.run() == ref
+        times.append((time.perf_counter() - t) * 1000.0)
+    return min(times), ref
 
 
 def main():
@@ -477,14 +699,15 @@ def main():
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C2, C3, C5 and field-input keys")
     ap.add_argument("--no-commit", action="store_true", help="skip the Pedersen commitments")
     ap.add_argument("--no-batchopen", action="store_true", help="skip the claim-mode batch opening")
     ap.add_argument("--no-prof", action="store_true", help="skip the profiled pass (no kernel times)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--segment", choices=["glu", "rope", "commit", "batchopen"], default=None,
-                    help="only run one non-matmul segment repeatedly (for profiling), then exit")
+    ap.add_argument("--segment", choices=["glu", "rope", "commit", "batchopen", "c3", "c5glu", "mmfr"],
+                    default=None, help="only run one segment repeatedly (for profiling), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -501,6 +724,8 @@ def main():
         del src, dst
     rng = synth.rng_for(4)
     L = LAYER
+    C4 = synth.CONFIGS["C4"]
+    MATMULS = C4["matmuls"]
     if args.segment == "commit":
         jobs = [MatmulJob(zkh, synth, rng, n, L["B"], i, o) for n, i, o in MATMULS]
         pool = concurrent.futures.ThreadPoolExecutor(max_workers=16)
@@ -511,9 +736,22 @@ def main():
         jobs = [MatmulJob(zkh, synth, rng, n, L["B"], i, o) for n, i, o in MATMULS]
         print(json.dumps({"segment": "batchopen", **batch_open(zkh, jobs, reps=max(1, min(args.steps, 3)))}))
         return
+    if args.segment == "mmfr":
+        jobs = [MatmulJob(zkh, synth, rng, n, L["B"], i, o, fr=True) for n, i, o in MATMULS]
+        r, _, _ = mm_batch_rate(zkh, jobs, args.steps, args.warmup)
+        print(json.dumps({"segment": "mmfr", **r}))
+        return
     if args.segment:
-        job = GluJob(zkh, synth, rng, L["B"], L["ffn"]) if args.segment == "glu" else \
-            RopeJob(zkh, rng, "q", L["B"], L["d"])
+        if args.segment == "glu":
+            job = GluJob(zkh, synth, rng, L["B"], L["ffn"])
+        elif args.segment == "c5glu":
+            C5 = synth.CONFIGS["C5"]
+            job = GluJob(zkh, synth, synth.rng_for(5), C5["B"], C5["ffn"], N=C5["glu_table"], tag="cfg5:layer0")
+        elif args.segment == "c3":
+            c3 = synth.CONFIGS["C3"]
+            job = LookupJob(zkh, synth.rng_for(3), c3["D"], c3["N"], c3["low"])
+        else:
+            job = RopeJob(zkh, synth, rng, "q", L["B"], L["d"])
         ref = job.run()
         gc.collect()
         gc.disable()
@@ -549,6 +787,7 @@ def main():
     for _ in range(args.warmup):
         mm_step()
         ref = mm_result()
+    mm_outs = [({k: v.copy() for k, v in o.items()}, j.st.copy()) for o, j in zip(mbatch.outs, jobs)]
     print("setup %.1fs; matmul step warm" % (time.perf_counter() - t_setup), file=sys.stderr, flush=True)
     # the interpreter's cyclic GC (millions of objects once torch is imported) would stall
     # a step for tens of ms at fixed allocation counts; it stays off while timing
@@ -583,15 +822,8 @@ def main():
         zkh.lib().zkh_prof_enable(mctx.h, 1)
         prof_ms_step, _ = timed_steps()
 
-    # per-kernel device time over the profiled pass's steps (all contexts)
-    import ctypes
-    kern = {}
-    buf = ctypes.create_string_buffer(4096)
-    zkh.lib().zkh_prof_names(mctx.h, buf, 4096)
-    for name in filter(None, buf.value.decode().split(",")):
-        ms, la, by = ctypes.c_double(), ctypes.c_uint64(), ctypes.c_double()
-        zkh.lib().zkh_prof_get(mctx.h, name.encode(), ctypes.byref(ms), ctypes.byref(la), ctypes.byref(by))
-        kern[name] = [ms.value, la.value, by.value]
+    # per-kernel device time over the profiled pass's steps
+    kern = {k: [v[0] * args.steps, v[1] * args.steps, v[2] * args.steps] for k, v in prof_kernels(zkh, mctx).items()}
     zkh.lib().zkh_prof_enable(mctx.h, 0)
     # The roofline object covers the dominant HBM-bound kernel.  The persistent round loop
     # (zkip_rounds) runs one host round trip per round (Fiat-Shamir challenge) and moves
@@ -615,9 +847,10 @@ def main():
                for n, v in sorted(kern.items(), key=lambda kv: -kv[1][0])}
 
     layer = None
+    glu = ropes = others = lref_others = None
     if not args.no_layer:
         glu = GluJob(zkh, synth, rng, L["B"], L["ffn"])
-        ropes = [RopeJob(zkh, rng, "q", L["B"], L["d"]), RopeJob(zkh, rng, "k", L["B"], L["kv"])]
+        ropes = [RopeJob(zkh, synth, rng, "q", L["B"], L["d"]), RopeJob(zkh, synth, rng, "k", L["B"], L["kv"])]
         others = [glu] + ropes
 
         def layer_step():
@@ -626,12 +859,12 @@ def main():
             return [mm_result()] + [f.result() for f in futs]
 
         lref = layer_step()
+        lref_others = lref[1:]
         seg = {}
         for j in others:  # isolated segment times (sequential, for the breakdown)
             t = time.perf_counter()
             j.run()
-            seg[type(j).__name__ + ("" if not hasattr(j, "logD") else ":2^%d" % j.logD)] = \
-                round((time.perf_counter() - t) * 1000.0, 2)
+            seg[type(j).__name__ + ":2^%d" % j.logD] = round((time.perf_counter() - t) * 1000.0, 2)
         gc.collect()
         gc.disable()
         torch.cuda.synchronize()
@@ -642,12 +875,95 @@ def main():
         tb = time.perf_counter()
         gc.enable()
         assert lout == lref, "non-deterministic layer output"
+        # kernel classes of the SwiGLU segment (the layer's largest) in one profiled run
+        zkh.lib().zkh_prof_enable(glu.ctx.h, 1)
+        assert glu.run() == lref_others[0]
+        gk = prof_kernels(zkh, glu.ctx)
+        zkh.lib().zkh_prof_enable(glu.ctx.h, 0)
+        gdom = max(gk, key=lambda n: gk[n][0])
+        gms, gla, gby = gk[gdom]
         layer = {"prove_s_per_layer": (tb - ta) / args.layer_steps,
                  "segments_isolated_ms": seg,
+                 "swiglu_kernels": {n: {"ms": round(v[0], 4), "launches": int(v[1]),
+                                        "GBps": round(v[2] / (v[0] / 1000.0) / 1e9, 1) if v[0] else None}
+                                    for n, v in sorted(gk.items(), key=lambda kv: -kv[1][0])},
                  "scope": "7 matmul sumchecks + SwiGLU logUp (D=N=2^22) + its Hadamard (2^22) + "
                           "RoPE q/k Hadamards (2x2^20, 2x2^17), concurrent; commitments, IPA "
                           "openings and the witness GEMM excluded"}
+        layer_roofline = {"bound": "hbm", "kernel": gdom, "achieved": round(gby / (gms / 1000.0) / 1e9, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gby / (gms / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+                          "bytes_per_launch": gby / max(gla, 1), "avg_launch_us": gms * 1000.0 / max(gla, 1),
+                          "launches_per_segment": gla,
+                          "scope": "dominant kernel class of the SwiGLU segment (the layer's largest), "
+                                   "algorithmic bytes over launch-stamped time"}
         print("layer %.3f s" % layer["prove_s_per_layer"], file=sys.stderr, flush=True)
+
+    configs = None
+    fr_key = None
+    if not args.no_configs:
+        configs = {}
+        # field-element inputs: the same 7 matmuls with X, W, Y bound as FrTensors
+        fr_jobs = [MatmulJob(zkh, synth, None, j.name, j.B, j.IN, j.OUT, fr=True, inputs=j.inputs) for j in jobs]
+        r, fb, fref = mm_batch_rate(zkh, fr_jobs, args.steps, args.warmup)
+        assert [MatmulJob.result(o, st) for o, st in mm_outs] == fref, "FR-input proofs differ from the int ones"
+        zkh.lib().zkh_prof_enable(fr_jobs[0].ctx.h, 1)
+        fb.run()
+        fk = prof_kernels(zkh, fr_jobs[0].ctx)
+        zkh.lib().zkh_prof_enable(fr_jobs[0].ctx.h, 0)
+        fms, fla, fby = fk.get("eqdot_fr", (1.0, 1, 0.0))
+        fr_key = dict(r, roofline={"bound": "hbm", "kernel": "eqdot_fr",
+                                   "achieved": round(fby / (fms / 1000.0) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                                   "unit": "GB/s", "frac": round(fby / (fms / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+                                   "bytes_per_launch": fby, "avg_launch_us": fms * 1000.0},
+                      kernels_ms={n: round(v[0], 4) for n, v in fk.items()},
+                      scope="the TinyLlama layer's 7 matmuls with X, W, Y as field-element tensors (32 B "
+                            "per entry); proofs byte-identical to the integer-input ones")
+        del fr_jobs, fb
+        print("FR-input matmul step %.3f ms" % fr_key["ms_per_step"], file=sys.stderr, flush=True)
+        # C2: llama-68m FFN matmuls at seq 128
+        c2 = synth.CONFIGS["C2"]
+        c2_jobs = [MatmulJob(zkh, synth, synth.rng_for(2), n, c2["B"], i, o, tag="cfg2") for n, i, o in c2["matmuls"]]
+        r, _, _ = mm_batch_rate(zkh, c2_jobs, args.steps, args.warmup)
+        configs["C2"] = dict(r, workload="llama-68m FFN matmul sumchecks, X 128x768, W_up 768x3072, W_down 3072x768")
+        del c2_jobs
+        # C3: the logUp range proof (zkob_rescale's shape; 2.19 s on an RTX 4090 for the whole
+        # zkob_rescale prove incl. commitments, INT_BASELINE.md:176)
+        c3 = synth.CONFIGS["C3"]
+        lj = LookupJob(zkh, synth.rng_for(3), c3["D"], c3["N"], c3["low"])
+        ms3, ref3 = seg_time(lj, 5)
+        configs["C3"] = {"ms": round(ms3, 3), "witness_per_s": round(lj.D / (ms3 / 1000.0)),
+                         "workload": "logUp: 2^20 witnesses in [-2^15, 2^15) vs the 2^16 range table "
+                                     "(multiplicities, batched inverse, 20 rounds)"}
+        # C5: OpenLLaMA-3B layer at seq 2048: 7 matmuls, SwiGLU 2^25 vs 2^22
+        c5 = synth.CONFIGS["C5"]
+        c5rng = synth.rng_for(5)
+        c5_jobs = [MatmulJob(zkh, synth, c5rng, n, c5["B"], i, o, tag="cfg5:layer0") for n, i, o in c5["matmuls"]]
+        r5, _, _ = mm_batch_rate(zkh, c5_jobs, max(3, args.steps // 4), 1)
+        del c5_jobs
+        g5 = GluJob(zkh, synth, synth.rng_for(5), c5["B"], c5["ffn"], N=c5["glu_table"], tag="cfg5:layer0")
+        ms5, _ = seg_time(g5, 3)
+        del g5
+        configs["C5"] = {"matmuls": r5, "swiglu_ms": round(ms5, 3),
+                         "workload": "OpenLLaMA-3B layer, seq 2048: 7 matmul sumchecks (d 3200, ffn 8640) and the "
+                                     "SwiGLU lookup on the 2048x16384 grid (2^25 witnesses) vs a 2^22 table with its "
+                                     "2^25 Hadamard"}
+        print("configs: C2 %.3f ms, C3 %.2f ms, C5 matmuls %.3f ms, C5 SwiGLU %.1f ms" %
+              (configs["C2"]["ms_per_step"], ms3, r5["ms_per_step"], ms5), file=sys.stderr, flush=True)
+        if not args.no_cpu:
+            C = _oracle()
+            C.set_threads(len(os.sched_getaffinity(0)))
+            got, secs = timed(lj.cpu_run)
+            assert got == ref3, "C3 CPU proof differs from the GPU's"
+            C.set_threads(1)
+            sample = 1 << 16
+            _, secs1 = timed(lambda: lj.cpu_run(sample))
+            C.set_threads(len(os.sched_getaffinity(0)))
+            configs["C3"]["cpu_baseline"] = {
+                "value": round(secs, 3), "unit": "s", "cores": len(os.sched_getaffinity(0)), "kind": "port",
+                "sample": "the C oracle on the same lookup and transcript (byte-identical proof), all cores",
+                "single_thread_estimate_s": round(secs1 * lj.D / sample, 2),
+                "single_thread_basis": "the first 2^16 witnesses against the same table on 1 thread, scaled by 2^4"}
 
     wg = None if args.no_layer else witness_gemm(zkh, jobs)
     com = None if args.no_commit else commitments(zkh, jobs, pool, cpu=not args.no_cpu)
@@ -660,7 +976,15 @@ def main():
     if com and not args.no_batchopen:
         bo = batch_open(zkh, jobs, reps=2)
         print("batch opening %.3f s per layer" % bo["batch_open_s_per_layer"], file=sys.stderr, flush=True)
-    cpu = None if args.no_cpu else cpu_baseline(jobs)
+    cpu = lcpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(jobs, mm_outs)
+        print("cpu baseline (Q,K,V,O): %.3g elements/s on %d threads" % (cpu["value"], cpu["cores"]),
+              file=sys.stderr, flush=True)
+        if layer:
+            lcpu = layer_cpu_baseline(jobs, mm_outs, others, lref_others, glu, ropes[1], synth)
+            print("cpu baseline layer: %.2f s on %d threads" % (lcpu["value"], lcpu["cores"]),
+                  file=sys.stderr, flush=True)
     res = {
         "metric": "Fr elements bound/sec in matmul sumcheck; prove s/layer at TinyLlama-1.1B",
         "value": value, "unit": "Fr elements/s", "n_gpus": 1, "steps": args.steps,
@@ -668,12 +992,21 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "u32", "data": "synthetic",
         "config": {"workload": "TinyLlama-1.1B layer (BASELINE config 4), seq 512: Q,K,V,O,gate,up,down "
                                "matmul sumchecks", "B": L["B"], "d": L["d"], "kv": L["kv"],
-                   "ffn": L["ffn"], "elements_bound_per_step": E_total, "field": "BLS12-381 Fr"},
+                   "ffn": L["ffn"], "elements_bound_per_step": E_total, "field": "BLS12-381 Fr",
+                   "inputs": "X, W int32 and Y int64 tensors (zkob_fc's int input files); the field-element "
+                             "input rate is under fr_inputs"},
         "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
     }
     if layer:
         res["prove_s_per_layer"] = layer["prove_s_per_layer"]
         res["layer"] = layer
+        res["layer_roofline"] = layer_roofline
+        if lcpu:
+            res["layer"]["cpu_baseline"] = lcpu
+    if fr_key:
+        res["fr_inputs"] = fr_key
+    if configs:
+        res["configs"] = configs
     if wg:
         res["witness_gemm"] = wg
     if com:

@@ -119,6 +119,27 @@ def ceil_log2(n):
     return 0 if n <= 1 else (int(n) - 1).bit_length()
 
 
+# r, the BLS12-381 scalar field modulus, as 8 little-endian uint32 limbs (bls12-381.cu:4)
+R_LIMBS = np.array([0x00000001, 0xFFFFFFFF, 0xFFFE5BFE, 0x53BDA402, 0x09A1D805, 0x3339D808,
+                    0x299D7D48, 0x73EDA753], dtype=np.int64)
+
+
+def ints_to_fr(v):
+    """int_to_scalar / long_to_scalar on an integer array (fr-tensor.cu:701-717): v >= 0 -> v,
+    v < 0 -> r - |v|, as an (n, 8) uint32 Fr array."""
+    v = np.ascontiguousarray(v).reshape(-1).astype(np.int64)
+    neg = v < 0
+    mag = np.where(neg, -(v + 1), v).astype(np.uint64) + neg.astype(np.uint64)  # |v|, also for -2^63
+    out = np.zeros((len(v), 8), dtype=np.int64)
+    m = [(mag & np.uint64(0xFFFFFFFF)).astype(np.int64), (mag >> np.uint64(32)).astype(np.int64)]
+    borrow = np.zeros(len(v), dtype=np.int64)
+    for k in range(8):
+        d = R_LIMBS[k] - (m[k] if k < 2 else 0) - borrow
+        borrow = (d < 0).astype(np.int64)
+        out[:, k] = np.where(neg, d + (borrow << 32), m[k] if k < 2 else 0)
+    return out.astype(np.uint32)
+
+
 # ---------------- transcript ----------------
 def transcript(seed):
     st = np.zeros(32, dtype=np.uint8)
