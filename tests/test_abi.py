@@ -86,3 +86,17 @@ def test_no_gpu_fails_loudly(zkh):
     assert rc == zkh.EDEV and not h.value
     with pytest.raises(zkh.ZkhError):
         zkh.Context(0)
+
+
+def test_ints_to_fr_helper_vs_oracle():
+    """The package's numpy int -> Fr conversion (used to bind field-element tensors) against
+    the oracle's long_to_scalar, including the int64 extremes."""
+    import numpy as np
+    from conftest import load_zkh
+    from oracle import coracle as C
+    zkh = load_zkh()
+    rng = np.random.default_rng(12)
+    v = np.concatenate([rng.integers(-2**63, 2**63 - 1, size=5000, dtype=np.int64),
+                        np.array([0, 1, -1, -2**63, 2**63 - 1, -2**31, 2**32], np.int64)])
+    assert np.array_equal(zkh.ints_to_fr(v), C.ints_to_fr(v))
+    assert np.array_equal(zkh.ints_to_fr(v[:100].astype(np.int32)), C.ints_to_fr(v[:100].astype(np.int32)))
