@@ -692,14 +692,19 @@ void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
     });
 }
 
-// Batched inversion (Montgomery's trick).  Block b covers INV_CHK*NT entries; thread t
-// owns entries base + j*NT + t.  Pass 1 stores running products (Montgomery domain) in A
-// and a block-wide inclusive prefix/suffix scan of the thread totals gives each thread
-// the product of all OTHER threads' totals.  The block total goes to blockprod.
-// Pass 2 walks each thread's entries backwards.  Zero entries (x+beta = 0) take 1 in the
-// products and produce 0, the reference's Fermat convention.  Between the passes,
-// k_inv_blocks turns the block totals into "all other blocks" products and publishes the
-// grand product, which the host inverts once.
+// Batched inversion (Montgomery's trick) in three Montgomery products per entry.  With
+// M(a, b) = a b 2^-256, the running products P_0 = 2^256, P_j = M(P_{j-1}, x_j) of the plain
+// values x_j need no conversion into the Montgomery domain, and for Y_j = 1/P_j:
+//   1/x_j = M(P_{j-1}, Y_j)   and   Y_{j-1} = M(x_j, Y_j)
+// (P_j = P_{j-1} x_j / 2^256), so the backward walk yields plain inverses directly.  The
+// same identities combine totals: for Q = M(a, b), 1/a = M(b, 1/Q).  Block b covers
+// INV_CHK*NT entries; thread t owns entries base + j*NT + t.  Pass 1 stores P_j in A, and
+// a block-wide inclusive prefix/suffix scan of the thread totals gives each thread the
+// M-product of all OTHER threads' totals; the block total goes to blockprod.  Between the
+// passes, k_inv_blocks turns the block totals into "all other blocks" products and
+// publishes the grand product G, whose plain inverse the host computes once.  Pass 2 walks
+// each thread's entries backwards.  Zero entries (x + beta = 0) take 2^256, M's identity,
+// in the products and produce 0, the reference's Fermat convention.
 #define INV_CHK 16
 __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
@@ -711,9 +716,8 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
     for (uint32_t j = 0; j < INV_CHK; j++) {
         uint32_t idx = base + j * NT + t;
         if (idx < n) {
-            fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
-            fr_t xm = fr_is_zero(x) ? one_m() : mont_mul(x, r2_m());
-            run = mont_mul(run, xm);
+            const fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
+            run = mont_mul(run, fr_is_zero(x) ? one_m() : x);
             st_fr(alo, ahi, idx, run);
         }
     }
@@ -778,27 +782,25 @@ void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, ui
                        Publish pub) {
     k_inv_blocks<<<1, NTI, 0, s>>>(blockprod, nb, others_blk, pub);
 }
-// 1/blockprod[b] = invP * others_blk[b] (Montgomery form); then each thread walks its
-// entries backwards
+// 1/blockprod[b] = M(others_blk[b], 1/G), 1/(thread total) = M(others[t], 1/blockprod[b]);
+// then each thread walks its entries backwards
 __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
                                                   const uint32_t* __restrict__ others,
-                                                  const uint32_t* __restrict__ others_blk, fr_t inv_total_m) {
+                                                  const uint32_t* __restrict__ others_blk, fr_t inv_total) {
     const uint32_t t = threadIdx.x;
     const uint32_t base = blockIdx.x * NT * INV_CHK;
-    // 1/run_t = 1/blockprod * prod(other threads' runs)
-    const fr_t binv = mont_mul(inv_total_m, ld_aos(others_blk, blockIdx.x));
+    const fr_t binv = mont_mul(inv_total, ld_aos(others_blk, blockIdx.x));
     fr_t y = mont_mul(binv, ld_aos(others, blockIdx.x * NT + t));
     for (int j = INV_CHK - 1; j >= 0; j--) {
         uint32_t idx = base + (uint32_t)j * NT + t;
         if (idx >= n) continue;
-        fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
-        bool z = fr_is_zero(x);
-        fr_t xm = z ? one_m() : mont_mul(x, r2_m());
-        fr_t prev = j > 0 ? ld_fr(alo, ahi, idx - NT) : one_m();
-        fr_t inv_m = mont_mul(y, prev);
-        y = mont_mul(y, xm);
-        st_fr(alo, ahi, idx, z ? fr_zero() : mont_mul(inv_m, plain_one()));
+        const fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
+        const bool z = fr_is_zero(x);
+        const fr_t prev = j > 0 ? ld_fr(alo, ahi, idx - NT) : one_m();
+        const fr_t inv = mont_mul(prev, y);
+        y = mont_mul(z ? one_m() : x, y);
+        st_fr(alo, ahi, idx, z ? fr_zero() : inv);
     }
 }
 uint32_t inv_blocks(uint32_t n) { return (n + NT * INV_CHK - 1) / (NT * INV_CHK); }
@@ -809,9 +811,9 @@ void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 }
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
-                      const uint32_t* inv_total_m_host) {
+                      const uint32_t* inv_total_host) {
     k_inv_pass2<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
-                                             PL_HI(A), others, others_blk, to_fr(inv_total_m_host));
+                                             PL_HI(A), others, others_blk, to_fr(inv_total_host));
 }
 
 // ------------------------------------------------------------------------------------

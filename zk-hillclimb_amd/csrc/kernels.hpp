@@ -125,12 +125,12 @@ void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t
                           DevPlanes mapped, DevPlanes out);
 void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
                        Src mapped, uint32_t N, DevPlanes out);
-// A[i] = 1/(S[i]+beta) (0 -> 0), Montgomery's batched inversion: pass 1 writes running
-// products to A, per-thread "other threads" products to `others` (inv_blocks(n)*256 AoS)
-// and block totals to blockprod (inv_blocks(n) AoS, Montgomery form); k_inv_blocks writes
-// others_blk[b] = product of the other blocks' totals and publishes the grand product P
-// (Montgomery form, job 0 of pub); the host inverts P once; pass 2 writes the plain
-// inverses into A given inv_total_m = 1/P (Montgomery form).
+// A[i] = 1/(S[i]+beta) (0 -> 0), Montgomery's batched inversion with M(a, b) = a b 2^-256
+// products of the plain values: pass 1 writes the running products P_j to A, per-thread
+// "other threads" products to `others` (inv_blocks(n)*256 AoS) and block totals to
+// blockprod (inv_blocks(n) AoS); k_inv_blocks writes others_blk[b] = the M-product of the
+// other blocks' totals and publishes the grand product G (job 0 of pub); the host computes
+// the plain inverse 1/G once; pass 2 writes the plain inverses into A given inv_total = 1/G.
 uint32_t inv_blocks(uint32_t n);
 void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, uint32_t* others, uint32_t* blockprod);
@@ -138,7 +138,7 @@ void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, ui
                        Publish pub);
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
-                      const uint32_t* inv_total_m_host);
+                      const uint32_t* inv_total_host);
 // phase-1 round over A, S (size n): sums e*a0*s0, e*a1*s1, e*da*ds (x 2^-256), a0, a1
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,

@@ -2183,13 +2183,13 @@ static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, De
         launch_inv_blocks(c->stream, bp, nb, others_blk, pb);
     }
     if ((rc = wait_pub(c, pb.seq))) return rc;
-    // the grand product (Montgomery form) -> its inverse, once, on the host
-    Fr P;
-    pub_read(c, 0, 1, &P);
-    uint32_t inv_m[8];
-    fr_store(fr_to_mont(fr_inv(fr_from_mont(P))), inv_m);
+    // the grand product G (never zero) -> its plain inverse, once, on the host
+    Fr G;
+    pub_read(c, 0, 1, &G);
+    uint32_t inv_g[8];
+    fr_store(fr_inv(G), inv_g);
     ProfScope ps(c, "inv_pass2", (double)n * 96 + (double)nb * 256 * 32);
-    launch_inv_pass2(c->stream, S, n, bl, A, others, others_blk, inv_m);
+    launch_inv_pass2(c->stream, S, n, bl, A, others, others_blk, inv_g);
     return 0;
 }
 extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t beta[8], zkh_tensor** A_out) {
