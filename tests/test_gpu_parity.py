@@ -467,6 +467,43 @@ def test_lu_prove(zkh, ctx, shape):
     assert bytes(st_g) == bytes(st_o)
 
 
+@pytest.mark.parametrize("D,N,skew", [(1000, 64, 0), (70000, 16384, 1), (1 << 17, 40000, 1), (1 << 17, 40000, 0),
+                                       (300000, 1 << 16, 1), (1 << 18, 1 << 24, 1)])
+def test_lu_prep_histogram(zkh, ctx, D, N, skew):
+    """Multiplicities against brute-force counting, through the LDS histogram's direct mode
+    (N <= 16384) and its partitioned mode (several buckets, a partial last bucket, up to the
+    1024-bucket maximum), with a skewed witness (a quarter of the entries on one index, as
+    zero padding makes) and FR-kind witnesses."""
+    rng = np.random.default_rng(D + N)
+    low = -(N // 2)
+    vals = rng.integers(low, low + N, size=D).astype(np.int32)
+    if skew:
+        vals[: D // 4] = 0
+    want = np.bincount((vals.astype(np.int64) - low), minlength=N)
+    got = ctx.lu_prep(ctx.from_i32(vals), low, N).to_fr()
+    assert np.array_equal(got[:, 0], want.astype(np.uint32)) and not got[:, 1:].any()
+    if D <= (1 << 17):
+        got_fr = ctx.lu_prep(ctx.from_fr(C.ints_to_fr(vals)), low, N).to_fr()
+        assert fr_eq(got_fr, got)
+
+
+@pytest.mark.parametrize("N", [64, 40000])
+def test_lu_prep_out_of_range_partitioned(zkh, ctx, N):
+    vals = np.zeros(50000, np.int32)
+    vals[4321] = N  # low = 0: index N is one past the table
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.lu_prep(ctx.from_i32(vals), 0, N)
+    assert e.value.code == zkh.EARG
+    # limb 0 of r - 2 (the field image of -2) is 2^32 - 1: outside; -1 (limb 0 of r - 1 is
+    # 0) aliases into bin 0 as the reference's limb-0 index does (tlookup.cu:419)
+    vals[4321] = -2
+    with pytest.raises(zkh.ZkhError):
+        ctx.lu_prep(ctx.from_i32(vals), 0, N)
+    vals[4321] = -1
+    got = ctx.lu_prep(ctx.from_i32(vals), 0, N).to_fr()
+    assert got[0, 0] == 50000 and not got[1:].any()
+
+
 def test_lu_out_of_range_rejected(zkh, ctx):
     S = ctx.from_i32(np.array([0, 1, 2, 40], np.int32))
     with pytest.raises(zkh.ZkhError) as e:

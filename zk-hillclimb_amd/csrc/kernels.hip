@@ -663,6 +663,224 @@ void launch_lu_count_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t lo
 void launch_counts_to_planes(hipStream_t s, const uint32_t* counts, uint32_t N, DevPlanes m) {
     k_counts_to_planes<<<grid_for(N, NT, 8192), NT, 0, s>>>(counts, N, PL_LO(m), PL_HI(m));
 }
+// ---- multiplicities by LDS histograms (see HistArgs) ----
+// index of entry i (limb 0 of S[i] - low), and whether it lies in the table
+ZDEV uint32_t hist_index(const HistArgs& a, uint32_t i) {
+    if (a.S.kind == 1) return lu_index_i32(reinterpret_cast<const int32_t*>(a.S.p)[i], a.low);
+    const uint4* lo = reinterpret_cast<const uint4*>(a.S.p);
+    return fr_sub(ld_fr(lo, lo + a.S.cap, i), to_fr(a.low_fr)).v[0];
+}
+// pass 1: per tile of ZKH_HIST_TILE entries, the count of each bucket
+__global__ __launch_bounds__(NT) void k_hist_tiles(HistArgs a) {
+    __shared__ uint32_t cnt[ZKH_HIST_MAX_BUCKETS];
+    for (uint32_t b = threadIdx.x; b < a.nbuckets; b += NT) cnt[b] = 0;
+    __syncthreads();
+    const uint32_t base = blockIdx.x * ZKH_HIST_TILE;
+    bool bad = false;
+    for (uint32_t k = threadIdx.x; k < ZKH_HIST_TILE; k += NT) {
+        const uint32_t i = base + k;
+        if (i >= a.n) break;
+        const uint32_t idx = hist_index(a, i);
+        if (idx >= a.N) bad = true;
+        else atomicAdd(&cnt[idx >> ZKH_HIST_BITS], 1u);
+    }
+    if (bad) atomicOr(a.bad, 1u);
+    __syncthreads();
+    for (uint32_t b = threadIdx.x; b < a.nbuckets; b += NT) a.tile_cnt[(size_t)b * a.ntiles + blockIdx.x] = cnt[b];
+}
+// pass 2: one block per bucket: exclusive prefix of its tile counts (in place) and its total
+__global__ __launch_bounds__(NT) void k_hist_rows(HistArgs a) {
+    __shared__ uint32_t part[NT];
+    uint32_t* row = a.tile_cnt + (size_t)blockIdx.x * a.ntiles;
+    const uint32_t per = (a.ntiles + NT - 1) / NT;
+    const uint32_t t0 = threadIdx.x * per, t1 = min(a.ntiles, t0 + per);
+    uint32_t loc = 0;
+    for (uint32_t t = t0; t < t1; t++) loc += row[t];
+    part[threadIdx.x] = loc;
+    __syncthreads();
+    for (uint32_t off = 1; off < NT; off <<= 1) {  // inclusive scan of the thread sums
+        const uint32_t v = threadIdx.x >= off ? part[threadIdx.x - off] : 0u;
+        __syncthreads();
+        part[threadIdx.x] += v;
+        __syncthreads();
+    }
+    uint32_t run = threadIdx.x ? part[threadIdx.x - 1] : 0u;
+    for (uint32_t t = t0; t < t1; t++) {
+        const uint32_t c = row[t];
+        row[t] = run;
+        run += c;
+    }
+    if (threadIdx.x == NT - 1) a.bucket_info[4 * blockIdx.x + 1] = part[NT - 1];
+}
+// pass 3 (one block): bucket starts, slots per bucket and the slot work list
+__global__ __launch_bounds__(NT) void k_hist_plan(HistArgs a) {
+    __shared__ uint32_t st[ZKH_HIST_MAX_BUCKETS], sl[ZKH_HIST_MAX_BUCKETS];
+    for (uint32_t b = threadIdx.x; b < a.nbuckets; b += NT) st[b] = a.bucket_info[4 * b + 1];
+    __syncthreads();
+    if (threadIdx.x == 0) {  // serial scans over at most 1,024 buckets, in LDS
+        uint32_t start = 0, slot = 0;
+        for (uint32_t b = 0; b < a.nbuckets; b++) {
+            const uint32_t tot = st[b];
+            st[b] = start;
+            sl[b] = slot;
+            start += tot;
+            slot += (tot + ZKH_HIST_CHUNK - 1) / ZKH_HIST_CHUNK;
+        }
+        *a.nslots = slot;
+    }
+    __syncthreads();
+    for (uint32_t b = threadIdx.x; b < a.nbuckets; b += NT) {
+        const uint32_t tot = a.bucket_info[4 * b + 1], ns = (tot + ZKH_HIST_CHUNK - 1) / ZKH_HIST_CHUNK;
+        a.bucket_info[4 * b + 0] = st[b];
+        a.bucket_info[4 * b + 2] = sl[b];
+        a.bucket_info[4 * b + 3] = ns;
+        for (uint32_t s = 0; s < ns; s++) {
+            uint32_t* w = a.work + 4 * (size_t)(sl[b] + s);
+            w[0] = b;
+            w[1] = st[b] + s * ZKH_HIST_CHUNK;
+            w[2] = min(ZKH_HIST_CHUNK, tot - s * ZKH_HIST_CHUNK);
+        }
+    }
+}
+// pass 4: scatter each tile's low index bits to its bucket's range (LDS cursors)
+__global__ __launch_bounds__(NT) void k_hist_scatter(HistArgs a) {
+    __shared__ uint32_t cur[ZKH_HIST_MAX_BUCKETS];
+    for (uint32_t b = threadIdx.x; b < a.nbuckets; b += NT)
+        cur[b] = a.bucket_info[4 * b] + a.tile_cnt[(size_t)b * a.ntiles + blockIdx.x];
+    __syncthreads();
+    const uint32_t base = blockIdx.x * ZKH_HIST_TILE;
+    for (uint32_t k = threadIdx.x; k < ZKH_HIST_TILE; k += NT) {
+        const uint32_t i = base + k;
+        if (i >= a.n) break;
+        const uint32_t idx = hist_index(a, i);
+        if (idx >= a.N) continue;
+        const uint32_t pos = atomicAdd(&cur[idx >> ZKH_HIST_BITS], 1u);
+        a.part[pos] = (uint16_t)(idx & (ZKH_HIST_BINS - 1));
+    }
+}
+// LDS histogram update aggregated over the lanes of a wave holding the leader's bin
+ZDEV void lds_hist_add(uint32_t* h, uint32_t bin, bool valid) {
+    const uint64_t act = __ballot(valid);
+    if (!act) return;
+    const int leader = __ffsll((unsigned long long)act) - 1;
+    const uint32_t lb = __shfl(bin, leader, 64);
+    const bool same = valid && bin == lb;
+    const uint64_t sm = __ballot(same);
+    if (same) {
+        if ((int)(threadIdx.x & 63) == leader) atomicAdd(&h[lb], (uint32_t)__popcll(sm));
+    } else if (valid) {
+        atomicAdd(&h[bin], 1u);
+    }
+}
+#define NTH 512
+// pass 5: one block per work slot: its indices counted in a 64 KB LDS histogram, stored
+// (direct: one bucket, slot s reads input entries [s CHUNK, (s + 1) CHUNK) itself)
+template <int direct>
+__global__ __launch_bounds__(NTH) void k_hist_slots(HistArgs a) {
+    __shared__ uint32_t h[ZKH_HIST_BINS];
+    const uint32_t slot = blockIdx.x;
+    uint32_t begin, count;
+    if (direct) {
+        begin = slot * ZKH_HIST_CHUNK;
+        count = min(ZKH_HIST_CHUNK, a.n - begin);
+    } else {
+        if (slot >= *a.nslots) return;  // uniform per block
+        begin = a.work[4 * slot + 1];
+        count = a.work[4 * slot + 2];
+    }
+    for (uint32_t j = threadIdx.x; j < ZKH_HIST_BINS; j += NTH) h[j] = 0;
+    __syncthreads();
+    bool bad = false;
+    for (uint32_t k0 = 0; k0 < count; k0 += NTH) {  // every lane takes part in the wave votes
+        const uint32_t k = k0 + threadIdx.x;
+        uint32_t bin = 0;
+        bool valid = k < count;
+        if (valid) {
+            if (direct) {
+                const uint32_t idx = hist_index(a, begin + k);
+                if (idx >= a.N) {
+                    bad = true;
+                    valid = false;
+                }
+                bin = idx;
+            } else {
+                bin = a.part[begin + k];
+            }
+        }
+        lds_hist_add(h, bin, valid);
+    }
+    if (bad) atomicOr(a.bad, 1u);
+    __syncthreads();
+    uint4* out = reinterpret_cast<uint4*>(a.slot_hist + (size_t)slot * ZKH_HIST_BINS);
+    for (uint32_t j = threadIdx.x; j < ZKH_HIST_BINS / 4; j += NTH)
+        out[j] = make_uint4(h[4 * j], h[4 * j + 1], h[4 * j + 2], h[4 * j + 3]);
+}
+// pass 6: m[j] = sum of bin j over its bucket's slots, as a field element (direct: the
+// one bucket's direct_slots slots, possibly none)
+__global__ void k_hist_sum(HistArgs a, int direct, uint32_t direct_slots, uint4* lo, uint4* hi) {
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= a.N) return;
+    uint32_t s0, ns;
+    if (direct) {
+        s0 = 0;
+        ns = direct_slots;
+    } else {
+        const uint32_t b = j >> ZKH_HIST_BITS;
+        s0 = a.bucket_info[4 * b + 2];
+        ns = a.bucket_info[4 * b + 3];
+    }
+    const uint32_t* h = a.slot_hist + (size_t)s0 * ZKH_HIST_BINS + (j & (ZKH_HIST_BINS - 1));
+    uint32_t c = 0, s = 0;
+    for (; s + 8 <= ns; s += 8) {  // eight loads in flight (a skewed bucket has many slots)
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = h[(size_t)(s + u) * ZKH_HIST_BINS];
+#pragma unroll
+        for (int u = 0; u < 8; u++) c += v[u];
+    }
+    for (; s < ns; s++) c += h[(size_t)s * ZKH_HIST_BINS];
+    fr_t m = fr_zero();
+    m.v[0] = c;
+    st_fr(lo, hi, j, m);
+}
+static size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
+size_t hist_scratch_bytes(uint32_t n, uint32_t N) {
+    const uint32_t nb = (N + ZKH_HIST_BINS - 1) / ZKH_HIST_BINS, nt = (n + ZKH_HIST_TILE - 1) / ZKH_HIST_TILE;
+    const uint32_t ms = nb + (n + ZKH_HIST_CHUNK - 1) / ZKH_HIST_CHUNK;
+    return align16((size_t)nb * nt * 4) + align16((size_t)nb * 16) + align16((size_t)ms * 16) + 16 +
+           align16((size_t)n * 2) + (size_t)ms * ZKH_HIST_BINS * 4;
+}
+void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m) {
+    a.nbuckets = (a.N + ZKH_HIST_BINS - 1) / ZKH_HIST_BINS;
+    a.ntiles = (a.n + ZKH_HIST_TILE - 1) / ZKH_HIST_TILE;
+    a.max_slots = a.nbuckets + (a.n + ZKH_HIST_CHUNK - 1) / ZKH_HIST_CHUNK;
+    uint8_t* p = static_cast<uint8_t*>(scratch);
+    a.tile_cnt = reinterpret_cast<uint32_t*>(p);
+    p += align16((size_t)a.nbuckets * a.ntiles * 4);
+    a.bucket_info = reinterpret_cast<uint32_t*>(p);
+    p += align16((size_t)a.nbuckets * 16);
+    a.work = reinterpret_cast<uint32_t*>(p);
+    p += align16((size_t)a.max_slots * 16);
+    a.nslots = reinterpret_cast<uint32_t*>(p);
+    p += 16;
+    a.part = reinterpret_cast<uint16_t*>(p);
+    p += align16((size_t)a.n * 2);
+    a.slot_hist = reinterpret_cast<uint32_t*>(p);
+    const uint32_t gsum = (a.N + NT - 1) / NT;
+    if (a.nbuckets == 1) {  // one LDS histogram covers the table: slots read the input
+        const uint32_t ns = (a.n + ZKH_HIST_CHUNK - 1) / ZKH_HIST_CHUNK;
+        if (ns) k_hist_slots<1><<<ns, NTH, 0, s>>>(a);
+        k_hist_sum<<<gsum, NT, 0, s>>>(a, 1, ns, PL_LO(m), PL_HI(m));
+        return;
+    }
+    k_hist_tiles<<<a.ntiles, NT, 0, s>>>(a);
+    k_hist_rows<<<a.nbuckets, NT, 0, s>>>(a);
+    k_hist_plan<<<1, NT, 0, s>>>(a);
+    k_hist_scatter<<<a.ntiles, NT, 0, s>>>(a);
+    k_hist_slots<0><<<a.max_slots, NTH, 0, s>>>(a);
+    k_hist_sum<<<gsum, NT, 0, s>>>(a, 0, 0, PL_LO(m), PL_HI(m));
+}
+
 __global__ void k_lu_map_planes(const uint4* lo, const uint4* hi, uint32_t n, fr_t low,
                                 const uint4* mlo, const uint4* mhi, uint32_t N, uint4* olo,
                                 uint4* ohi) {

@@ -121,6 +121,39 @@ void launch_lu_count_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32
 void launch_lu_count_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low, uint32_t N,
                          uint32_t* counts, uint32_t* bad);
 void launch_counts_to_planes(hipStream_t s, const uint32_t* counts, uint32_t N, DevPlanes m);
+// Multiplicities without global atomics (tlookup.cu:10-48, :414-433 semantics): every
+// index idx = limb 0 of (S - low) is bucketed by idx >> ZKH_HIST_BITS (16,384 bins per
+// bucket, one 64 KB LDS histogram); the indices are partitioned by bucket (tile counts,
+// per-bucket prefixes, a scatter with LDS cursors); each work slot (at most ZKH_HIST_CHUNK
+// indices of one bucket, so a skewed bucket such as the zero padding spreads over many
+// blocks) counts in LDS and stores its histogram; m[j] is the sum of bin j over its
+// bucket's slots, written as field elements.  With one bucket (N <= 16,384) the slots read
+// the input directly.  An index >= N sets *bad.  N <= 2^24 (1,024 buckets).
+#define ZKH_HIST_BITS 14
+#define ZKH_HIST_BINS (1u << ZKH_HIST_BITS)
+#define ZKH_HIST_CHUNK 16384u
+#define ZKH_HIST_TILE 4096u
+#define ZKH_HIST_MAX_BUCKETS 1024u
+struct HistArgs {
+    Src S;          // int32 or FR planes
+    uint32_t n;     // entries of S
+    int32_t low;    // table offset (int32 inputs)
+    uint32_t low_fr[8];  // the same as a field element (FR inputs)
+    uint32_t N;     // table size
+    uint32_t nbuckets, ntiles, max_slots;
+    uint32_t* tile_cnt;     // [nbuckets][ntiles]: counts, then in-row exclusive prefixes
+    uint32_t* bucket_info;  // [nbuckets][4]: start, total, first slot, slots
+    uint32_t* work;         // [max_slots][4]: bucket, begin, count, -
+    uint32_t* nslots;       // one word
+    uint16_t* part;         // n partitioned low index bits
+    uint32_t* slot_hist;    // [max_slots][ZKH_HIST_BINS]
+    uint32_t* bad;          // zeroed by the caller
+};
+// scratch words needed by launch_hist for these sizes (tile_cnt .. slot_hist, 16-byte aligned parts)
+size_t hist_scratch_bytes(uint32_t n, uint32_t N);
+// lays HistArgs' buffers out in `scratch` (hist_scratch_bytes bytes) and enqueues the passes
+void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m);
+
 void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
                           DevPlanes mapped, DevPlanes out);
 void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,

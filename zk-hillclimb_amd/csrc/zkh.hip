@@ -2114,16 +2114,54 @@ static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, u
     *counts_out = counts;
     return 0;
 }
+// multiplicities m (N field elements) of the witness S against a table of N entries at low:
+// LDS histograms for N <= 2^24 (launch_hist), global atomics beyond
+static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, DevPlanes m) {
+    int rc = 0;
+    if (N > ZKH_HIST_MAX_BUCKETS * ZKH_HIST_BINS) {
+        uint32_t* counts;
+        if ((rc = lu_counts(c, S, low, N, &counts))) return rc;
+        launch_counts_to_planes(c->stream, counts, N, m);
+        return 0;
+    }
+    HistArgs a{};
+    if (S->kind == ZKH_KIND_I32) {
+        a.S = Src{1, S->d, 0};
+    } else {
+        DevPlanes p;
+        if ((rc = as_planes(c, S, SL_TMP0, &p))) return rc;
+        a.S = Src{0, p.base, p.cap};
+    }
+    a.n = S->n;
+    a.low = low;
+    fr_store(fr_from_i64(low), a.low_fr);
+    a.N = N;
+    uint32_t* bad = (uint32_t*)scratch_slot(c, SL_SMALL, 64, &rc);
+    if (rc) return rc;
+    void* hs = scratch_slot(c, SL_TMP5, hist_scratch_bytes(S->n, N), &rc);
+    if (rc) return rc;
+    a.bad = bad;
+    HIPCHK(c, hipMemsetAsync(bad, 0, 4, c->stream));
+    {
+        ProfScope ps(c, "lu_hist", (double)S->n * (S->kind == ZKH_KIND_I32 ? 4 : 32) + (double)N * 32);
+        launch_hist(c->stream, a, hs, m);
+    }
+    uint32_t hb = 0;
+    HIPCHK(c, hipMemcpyAsync(&hb, bad, 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (hb) return fail(c, ZKH_EARG, "lookup witness outside the table");
+    return 0;
+}
 extern "C" int zkh_lu_prep(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, zkh_tensor** m_out) {
     if (!c || !S || !m_out || !N) return fail(c, ZKH_EARG, "bad arguments");
     HIPCHK(c, hipSetDevice(c->device));
-    uint32_t* counts;
-    int rc = lu_counts(c, S, low, N, &counts);
-    if (rc) return rc;
     zkh_tensor* m;
+    int rc;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
-    launch_counts_to_planes(c->stream, counts, N, m->planes());
-    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if ((rc = lu_multiplicities(c, S, low, N, m->planes()))) {
+        zkh_tensor_free(m);
+        return rc;
+    }
     *m_out = m;
     return ZKH_OK;
 }
@@ -2133,16 +2171,17 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
         return fail(c, ZKH_EARG, "bad arguments");
     HIPCHK(c, hipSetDevice(c->device));
     uint32_t N = mapped->n;
-    uint32_t* counts;
-    int rc = lu_counts(c, S_in, low, N, &counts);
-    if (rc) return rc;
     zkh_tensor *m, *so;
+    int rc;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
+    if ((rc = lu_multiplicities(c, S_in, low, N, m->planes()))) {
+        zkh_tensor_free(m);
+        return rc;
+    }
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, S_in->n, &so))) {
         zkh_tensor_free(m);
         return rc;
     }
-    launch_counts_to_planes(c->stream, counts, N, m->planes());
     if (S_in->kind == ZKH_KIND_I32) {
         Src ms;
         rc = src_of(c, mapped, SL_TMP1, &ms);
