@@ -1046,6 +1046,10 @@ struct EqDev {
 ZDEV fr_t eq_w(const EqDev& eq, uint32_t i) { return mont_mul_ol(ld_aos(eq.elo, i & 1023), ld_aos(eq.ehi, i >> 10)); }
 
 #define SB() __builtin_amdgcn_sched_barrier(0)
+// blocks of a logUp phase-2 round (both groups; 256 CUs hold 768 of them at once)
+#ifndef LU2_GRID
+#define LU2_GRID 1536
+#endif
 // Per-thread field accumulators kept in LDS (limb-quad planes, 16-byte lanes): registers
 // then hold only the current stage's operands, which lifts the round kernels' occupancy.
 template <int K>
@@ -1169,10 +1173,11 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
 }
 
 // phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused), one launch whose
-// blocks [0, g) take the (A, S) group and blocks [g, 2g) the (B, T, m) group, publishing as
-// jobs 0 and 1 of one round (each group keeps its fold, weights and sums in registers at a
-// fraction of a single fused body's pressure; one launch instead of two halves the fixed
-// cost of a small round):
+// blocks [0, ga) take the (A, S) group and blocks [ga, ga + gb) the (B, T, m) group,
+// publishing as jobs 0 and 1 of one round (each group keeps its fold, weights and sums in
+// registers at a fraction of a single fused body's pressure; one launch instead of two
+// halves the fixed cost of a small round).  The groups' block counts follow their work per
+// pair (6 / 9 Montgomery products, 10 / 15 with the folds):
 // job 0 (A, S): sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256), sum a0, sum a1  (s + beta)
 // job 1 (B, T, m): sum w*b0*t0, w*b1*t1, w*db*dt, m0*b0, m1*b1, dm*db (x 2^-256)  (t + beta)
 template <int fold>
@@ -1211,8 +1216,8 @@ ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t&
 }
 template <int fold>
 ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const fr_t& vm,
-                        const fr_t& beta, const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint4* accl,
-                        uint4* acch) {
+                        const fr_t& beta, const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint32_t ga,
+                        uint4* accl, uint4* acch) {
     const uint32_t h = n >> 1;
     LdsAcc<6> acc{accl, acch};
     acc.zero();
@@ -1250,28 +1255,29 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
         acc.add(2, mont_mul_ol(wdb, fr_sub(t1, t0)));
         SB();
     }
-    // partials after the (A, S) group's 5g entries: indices (g + lb) * 6 + k >= 6g
-    reduce_publish_lds<6>(acc, pub, 1, g, g, lb);
+    // partials after the (A, S) group's 5 ga entries: indices (ga + lb) * 6 + k >= 6 ga
+    reduce_publish_lds<6>(acc, pub, 1, ga, g, lb);
 }
 template <int fold_as, int fold_btm>
 __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m, uint32_t n,
-                                                  fr_t vm, fr_t beta, EqDev eq, Publish pub, uint32_t g) {
+                                                  fr_t vm, fr_t beta, EqDev eq, Publish pub, uint32_t ga, uint32_t gb) {
     __shared__ uint4 accl[6 * NT], acch[6 * NT];
-    if (blockIdx.x < g) lu_phase2_as<fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, g, accl, acch);
-    else lu_phase2_btm<fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - g, g, accl, acch);
+    if (blockIdx.x < ga) lu_phase2_as<fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, ga, accl, acch);
+    else lu_phase2_btm<fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - ga, gb, ga, accl, acch);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
                           EqW eq, Publish partial) {
-    const uint32_t g = grid_for(n >> 1, NT, 1024);
+    const uint32_t ga = grid_for(n >> 1, NT, LU2_GRID * 2 / 5), gb = grid_for(n >> 1, NT, LU2_GRID * 3 / 5);
     const fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
     const fr_t beta = to_fr(beta_host);
     const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T), md = tab_dev(m);
-    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
-    else if (fold_as) k_lu_phase2<1, 0><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
-    else if (fold_btm) k_lu_phase2<0, 1><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
-    else k_lu_phase2<0, 0><<<2 * g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, g);
+    const uint32_t g = ga + gb;
+    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
+    else if (fold_as) k_lu_phase2<1, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
+    else if (fold_btm) k_lu_phase2<0, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
+    else k_lu_phase2<0, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
     return g;
 }
 
