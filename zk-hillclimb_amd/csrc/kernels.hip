@@ -1384,24 +1384,32 @@ uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
     k_hp_eq_round<<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, e, partial);
     return g;
 }
-// sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n
+// sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n, by chunks of 1024 indices sharing their
+// Ehi factor: sum_c Ehi[c] * sum_{j < 1024} Elo[j] S[1024c + j] (U[...]), one product per
+// entry for the Elo weight and one per chunk and thread for Ehi
 __global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* shi, const uint4* ulo,
                                                const uint4* uhi, int has_u, uint32_t n, EqDev eq,
                                                Publish pub) {
     fr_t acc[1] = {fr_zero()};
-    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
-        {
-            const fr_t w = eq_w(eq, i);
-            fr_t ws = mont_mul_ol(w, ld_fr(slo, shi, i));
-            if (has_u) ws = mont_mul_ol(ws, ld_fr(ulo, uhi, i));
-            acc[0] = fr_add(acc[0], ws);
+    const uint32_t nchunk = (n + 1023) >> 10;
+    for (uint32_t c = blockIdx.x; c < nchunk; c += gridDim.x) {
+        fr_t part = fr_zero();
+#pragma unroll
+        for (uint32_t k = 0; k < 1024 / NT; k++) {
+            const uint32_t j = k * NT + threadIdx.x, i = (c << 10) + j;
+            if (i < n) {
+                fr_t ws = mont_mul_ol(ld_aos(eq.elo, j), ld_fr(slo, shi, i));
+                if (has_u) ws = mont_mul_ol(ws, ld_fr(ulo, uhi, i));
+                part = fr_add(part, ws);
+            }
         }
+        acc[0] = fr_add(acc[0], mont_mul_ol(part, ld_aos(eq.ehi, c)));
     }
     reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish partial) {
-    const uint32_t g = grid_for(n, NT, 1024);
+    const uint32_t g = grid_for((n + 1023) >> 10, 1, 1024);
     EqDev e{eq.elo, eq.ehi, eq.K};
     k_eq_sum<<<g, NT, 0, s>>>(PL_LO(S), PL_HI(S), U ? PL_LO(*U) : nullptr, U ? PL_HI(*U) : nullptr,
                               U ? 1 : 0, n, e, partial);
