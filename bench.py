@@ -174,9 +174,9 @@ class GluJob:
         A = c.lu_inverse(comb, beta)
         zkh.absorb(st, "com_A", self.comA)
         alpha = zkh.challenge(st)
-        u = np.array([zkh.challenge(st) for _ in range(self.logD)])
+        u = zkh.challenges(st, self.logD)
         lu = c.lu_prove(st, A, comb, Tcomb, m, alpha, beta, u)
-        u_h = np.array([zkh.challenge(st) for _ in range(self.logD)])
+        u_h = zkh.challenges(st, self.logD)
         H = c.hadamard(S, self.U)
         claim_H = c.me(H, u_h)
         zkh.absorb(st, "claim_H", claim_H.tobytes())
@@ -240,7 +240,7 @@ class RopeJob:
     def run(self):
         zkh, c = self.zkh, self.ctx
         st = self.st0.copy()
-        u = np.array([zkh.challenge(st) for _ in range(self.logD)])
+        u = zkh.challenges(st, self.logD)
         Eu = c.eq_table(u)
         outs = []
         for lab, W, S in (("c1", self.W1, self.T), ("c2", self.W2, self.Tx)):
@@ -297,7 +297,7 @@ class LookupJob:
         beta = zkh.challenge(st)
         A = c.lu_inverse(self.S, beta)
         alpha = zkh.challenge(st)
-        u = np.array([zkh.challenge(st) for _ in range(self.logD)])
+        u = zkh.challenges(st, self.logD)
         lu = c.lu_prove(st, A, self.S, self.T, m, alpha, beta, u)
         return lu["ev"].tobytes() + lu["term"].tobytes() + st.tobytes()
 

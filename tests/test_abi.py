@@ -100,3 +100,16 @@ def test_ints_to_fr_helper_vs_oracle():
                         np.array([0, 1, -1, -2**63, 2**63 - 1, -2**31, 2**32], np.int64)])
     assert np.array_equal(zkh.ints_to_fr(v), C.ints_to_fr(v))
     assert np.array_equal(zkh.ints_to_fr(v[:100].astype(np.int32)), C.ints_to_fr(v[:100].astype(np.int32)))
+
+
+def test_challenge_vec_is_sequential_draws(zkh):
+    """zkh_transcript_challenge_vec (fs_challenge_vec) equals n single draws in sequence."""
+    from oracle import coracle as C
+    st, so = zkh.transcript("vec"), C.tr_init("vec")
+    zkh.absorb(st, "x", b"abc")
+    C.tr_absorb(so, "x", b"abc")
+    got = zkh.challenges(st, 23)
+    want = [C.tr_challenge_fr(so) for _ in range(23)]
+    assert got.shape == (23, 8) and all((g == w).all() for g, w in zip(got, want))
+    assert bytes(st) == bytes(so)
+    assert zkh.challenges(st, 0).shape == (0, 8)

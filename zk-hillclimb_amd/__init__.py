@@ -77,6 +77,7 @@ def lib():
         L.zkh_transcript_init.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
         L.zkh_transcript_absorb.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, vp, ctypes.c_size_t]
         L.zkh_transcript_challenge_fr.argtypes = [vp, vp]
+        L.zkh_transcript_challenge_vec.argtypes = [vp, u32, vp]
         L.zkh_mm_prove.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, vp, vp, vp, vp, vp]
         L.zkh_lu_range_table.argtypes = [vp, i32, u32, u32, ctypes.POINTER(vp)]
         L.zkh_lu_prep.argtypes = [vp, vp, i32, u32, ctypes.POINTER(vp)]
@@ -158,6 +159,13 @@ def challenge(st):
     out = np.zeros(8, dtype=np.uint32)
     lib().zkh_transcript_challenge_fr(_p(st), _p(out))
     return out
+
+
+def challenges(st, n):
+    """fs_challenge_vec: n challenges in sequence, as an (n, 8) array (one C call)."""
+    out = np.zeros((max(n, 1), 8), dtype=np.uint32)
+    lib().zkh_transcript_challenge_vec(_p(st), n, _p(out))
+    return out[:n]
 
 
 class Tensor:

@@ -928,6 +928,11 @@ extern "C" int zkh_transcript_challenge_fr(uint8_t st[32], uint32_t out[8]) {
     tr_challenge_limbs(st, out);
     return ZKH_OK;
 }
+extern "C" int zkh_transcript_challenge_vec(uint8_t st[32], uint32_t n, uint32_t* out) {
+    if (!st || (!out && n)) return ZKH_EARG;
+    for (uint32_t i = 0; i < n; i++) tr_challenge_limbs(st, out + 8 * (size_t)i);
+    return ZKH_OK;
+}
 
 // ---------------------------------------------------------------------------------------
 // MLE primitives
@@ -2467,9 +2472,9 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
     if (rc) return rc;
     if ((rc = batch_inverse(c, Tc, N, beta, Bw))) return rc;
 
-    // C = alpha^2 - sum Bv*m (zkob_rescale.cu:136)
-    Fr bm;
-    {
+    // C = alpha^2 - sum Bv*m (zkob_rescale.cu:136); only the phase-1 rounds (D > N) use it
+    Fr bm = kZero;
+    if (D > N) {
         Publish pb = make_pub(c, 1);
         launch_dot_planes(c->stream, Bw, mc, N, pb);
         if ((rc = wait_pub(c, pb.seq))) return rc;
