@@ -113,3 +113,34 @@ def test_challenge_vec_is_sequential_draws(zkh):
     assert got.shape == (23, 8) and all((g == w).all() for g, w in zip(got, want))
     assert bytes(st) == bytes(so)
     assert zkh.challenges(st, 0).shape == (0, 8)
+
+
+def test_absorb_trace_matches_reference_format(tmp_path):
+    """P3_ABLOG=path (the reference's absorb trace, fs_transcript.hpp:135-148): one line per
+    absorb with the label, the data length and the first 8 bytes of the new state in hex."""
+    import os
+    import subprocess
+    import sys
+    from oracle import coracle as C
+    log = tmp_path / "ab.log"
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    prog = (
+        "import sys; sys.path.insert(0, %r); sys.path.insert(0, %r)\n"
+        "from conftest import load_zkh\n"
+        "zkh = load_zkh()\n"
+        "st = zkh.transcript('trace')\n"
+        "zkh.absorb(st, 'B', b'\\x04\\x00\\x00\\x00')\n"
+        "zkh.absorb(st, 'com_X', bytes(range(144)) * 3)\n"
+        "zkh.challenge(st)\n"
+        "zkh.absorb(st, 'p0', bytes(32))\n" % (root, os.path.join(root, "tests")))
+    env = dict(os.environ, P3_ABLOG=str(log))
+    subprocess.run([sys.executable, "-c", prog], check=True, env=env, timeout=120)
+    st = C.tr_init("trace")
+    want = []
+    for label, data, chal in (("B", b"\x04\x00\x00\x00", False), ("com_X", bytes(range(144)) * 3, True),
+                              ("p0", bytes(32), False)):
+        C.tr_absorb(st, label, data)
+        want.append("%s %d %s" % (label, len(data), bytes(st[:8]).hex()))
+        if chal:
+            C.tr_challenge_fr(st)
+    assert log.read_text().splitlines() == want

@@ -29,6 +29,13 @@ RESCALE = os.path.join(ROOT, "zk-hillclimb_amd", "zkh_rescale")
 BASE = G.aff_to_jac((G.GX, G.GY))
 
 
+@pytest.fixture(autouse=True)
+def _convention_crosschecks(monkeypatch):
+    """The drivers run with ZKH_XCHECK=1: every proof also checks its folded terminals against
+    multi_dim_me at the opening point, as the reference's drivers do."""
+    monkeypatch.setenv("ZKH_XCHECK", "1")
+
+
 def points(seed, n):
     rng = np.random.default_rng(seed)
     out = np.zeros((n, 36), np.uint32)

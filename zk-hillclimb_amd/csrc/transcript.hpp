@@ -9,7 +9,11 @@
 // SHA-256 itself follows FIPS 180-4.
 #pragma once
 #include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <mutex>
 #if defined(__x86_64__) && !defined(__HIP_DEVICE_COMPILE__)
 #include <cpuid.h>
 #include <immintrin.h>
@@ -202,8 +206,31 @@ inline void tr_init(uint8_t st[32], const char* seed, size_t n) {
     c.update(seed, n);
     c.final(st);
 }
+// Absorb trace, the reference's P3_ABLOG switch (fs_transcript.hpp:135-148): with
+// P3_ABLOG=path set, every absorb appends "label length state[0..8)" (hex) to that file, the
+// reference's own line format, so a run of this library and a run of the reference can be
+// diffed to find the first diverging absorb.  Debug only; no protocol effect.  Lines of
+// transcripts absorbed on several threads interleave as whole lines.
+inline void tr_ablog(const uint8_t st[32], const char* label, size_t llen, size_t len) {
+    static FILE* f = [] {
+        const char* p = getenv("P3_ABLOG");
+        return p ? fopen(p, "w") : nullptr;
+    }();
+    if (!f) return;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lk(mu);
+    fprintf(f, "%.*s %zu %02x%02x%02x%02x%02x%02x%02x%02x\n", (int)llen, label, len, st[0], st[1], st[2], st[3],
+            st[4], st[5], st[6], st[7]);
+    fflush(f);
+}
+inline void tr_absorb_raw(uint8_t st[32], const char* label, size_t llen, const void* data, size_t len);
 inline void tr_absorb(uint8_t st[32], const char* label, size_t llen, const void* data,
                       size_t len) {
+    tr_absorb_raw(st, label, llen, data, len);
+    tr_ablog(st, label, llen, len);
+}
+inline void tr_absorb_raw(uint8_t st[32], const char* label, size_t llen, const void* data,
+                          size_t len) {
     if (32 + 4 + llen + 8 + len <= 119) {  // the per-round absorbs: one short message
         uint8_t m[119];
         size_t o = 0;

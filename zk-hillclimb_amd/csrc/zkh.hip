@@ -408,6 +408,16 @@ static int ensure_ps(zkh_ctx* c, size_t words) {
     c->ps_words = want;
     return 0;
 }
+// ---- convention cross-checks (ZKH_XCHECK=1): the reference's "fold terminals ==
+// multi_dim_me" guards (zkob_fc.cu:337-345, zkob_glu.cu:186-192, :254-260,
+// zkob_rescale.cu:151-165): after a proof, each folded terminal is recomputed as the MLE of
+// its input table at the opening point, and a mismatch fails the call (ZKH_EROUND).  Off by
+// default: the sumcheck algebra already implies the equality, the re-evaluations cost
+// extra passes over the inputs. ----
+static bool xcheck_on() {
+    static const bool on = getenv("ZKH_XCHECK") && atoi(getenv("ZKH_XCHECK")) > 0;
+    return on;
+}
 // ---- host-side round trace (ZKH_TRACE=1): per-round launch / wait / host times ----
 static bool trace_on() {
     static const bool on = getenv("ZKH_TRACE") && atoi(getenv("ZKH_TRACE")) > 0;
@@ -1355,6 +1365,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         uint32_t lb, lo, L, INp;
         std::vector<Fr> ub, uo, xs;
         Fr claim, cur, xm;  // xm: the last challenge in Montgomery form
+        Fr cx, cw;          // the folded terminals (kept for the convention cross-check)
         Fr SEb, SEo;        // sum of the eq table entries over the first B / OUT indices
         size_t eb_off, eo_off, fac_b, fac_o;  // element offsets
         size_t red_off;                       // planes offset (entries) of a; b follows
@@ -1682,6 +1693,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     auto finish = [&](uint32_t j, const Fr& cx, const Fr& cw) {
         Job& q = J[j];
         zkh_mm_job& in = jobs[j];
+        q.cx = cx;
+        q.cw = cw;
         if (!fr_eq(q.cur, fr_mul(cx, cw))) {
             q.live = false;
             in.status = ZKH_EROUND;
@@ -1702,6 +1715,42 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             for (uint32_t i = 0; i < q.lo; i++) fr_store(q.uo[i], in.u_output_out + 8 * i);
         if (in.u_input_out)
             for (uint32_t i = 0; i < q.L; i++) fr_store(q.xs[q.L - 1 - i], in.u_input_out + 8 * i);
+    };
+
+    // zkob_fc.cu:337-345 with ZKH_XCHECK: claim_X = X(u_batch, u_input), claim_W =
+    // W(u_input, u_output) by multi_dim_me against the folded terminals, after every round
+    // (the persistent loop no longer holds the stream)
+    auto xcheck = [&]() -> int {
+        if (!xcheck_on()) return first_rc;
+        for (uint32_t j = 0; j < nj; j++) {
+            Job& q = J[j];
+            if (jobs[j].status != ZKH_OK) continue;
+            std::vector<uint32_t> ux, uw;
+            auto put = [](std::vector<uint32_t>& v, const std::vector<Fr>& a) {
+                for (const Fr& x : a) {
+                    uint32_t w[8];
+                    fr_store(x, w);
+                    v.insert(v.end(), w, w + 8);
+                }
+            };
+            std::vector<Fr> ui(q.xs.rbegin(), q.xs.rend());
+            put(ux, q.ub);
+            put(ux, ui);
+            put(uw, ui);
+            put(uw, q.uo);
+            const uint32_t kx[2] = {q.lb, q.L}, kw[2] = {q.L, q.lo};
+            const uint32_t sx[2] = {jobs[j].B, jobs[j].IN}, sw[2] = {jobs[j].IN, jobs[j].OUT};
+            uint32_t ex[8], ew[8];
+            int r2 = zkh_multi_dim_me(c, jobs[j].X, ux.data(), kx, sx, 2, ex);
+            if (!r2) r2 = zkh_multi_dim_me(c, jobs[j].W, uw.data(), kw, sw, 2, ew);
+            if (!r2 && (!fr_eq(fr_load(ex), q.cx) || !fr_eq(fr_load(ew), q.cw)))
+                r2 = fail(c, ZKH_EROUND, "job %u: folded terminals != multi_dim_me claims (convention bug)", j);
+            if (r2) {
+                jobs[j].status = r2;
+                if (!first_rc) first_rc = r2;
+            }
+        }
+        return first_rc;
     };
 
     // 4) rounds.  Tables of up to ZKH_PLS_MAX * 128 entries: one persistent launch per group
@@ -1985,7 +2034,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             }
         }
         if (c->prof) prof_resolve_ready(c);
-        return first_rc;
+        return xcheck();
     }
 
     // tables beyond the LDS loop: one launch and one synchronisation per round for all jobs
@@ -2068,7 +2117,7 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     }
     for (uint32_t j : fwho)
         finish(j, fr_load(pin + pin_term + (size_t)j * 16), fr_load(pin + pin_term + (size_t)j * 16 + 8));
-    return first_rc;
+    return xcheck();
 }
 
 extern "C" int zkh_mm_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* X, const zkh_tensor* W,
@@ -2437,10 +2486,10 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
                 lgnb, now_us() - t_launch);
     return 0;
 }
-extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const zkh_tensor* S,
-                            const zkh_tensor* T, const zkh_tensor* m, const uint32_t alpha_l[8],
-                            const uint32_t beta_l[8], const uint32_t* u_l, uint32_t* ev_out,
-                            uint32_t* term_out, uint32_t* ws_out) {
+static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const zkh_tensor* S,
+                         const zkh_tensor* T, const zkh_tensor* m, const uint32_t alpha_l[8],
+                         const uint32_t beta_l[8], const uint32_t* u_l, uint32_t* ev_out,
+                         uint32_t* term_out, uint32_t* ws_out) {
     if (!c || !tr || !A || !S || !T || !m || !alpha_l || !beta_l) return fail(c, ZKH_EARG, "null argument");
     const uint32_t D = A->n, N = T->n;
     // tLookup::prove shape rules (tlookup.cu:330-336)
@@ -2645,6 +2694,43 @@ extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, con
     tr_absorb_fr(tr, "A_f", fr_load(tv[0]));
     tr_absorb_fr(tr, "S_f", fr_load(tv[1]));
     tr_absorb_fr(tr, "m_f", fr_load(tv[4]));
+    return ZKH_OK;
+}
+// the opening point of a sumcheck's tables: its round challenges reversed (zkob_fc.cu:334-336,
+// zkob_rescale.cu:148-149), as Fr words
+static std::vector<uint32_t> reversed_point(const uint32_t* ws, uint32_t k) {
+    std::vector<uint32_t> pt(8 * (size_t)std::max<uint32_t>(k, 1));
+    for (uint32_t i = 0; i < k; i++) memcpy(&pt[8 * (size_t)i], ws + 8 * (size_t)(k - 1 - i), 32);
+    return pt;
+}
+// t(pt[0..k)) against a terminal (ZKH_EROUND with the reference's message on mismatch)
+static int xcheck_me(zkh_ctx* c, const zkh_tensor* t, const uint32_t* pt, uint32_t k, const uint32_t* term,
+                     const char* what) {
+    uint32_t e[8];
+    int rc = zkh_me(c, t, pt, k, e);
+    if (rc) return rc;
+    if (memcmp(e, term, 32)) return fail(c, ZKH_EROUND, "%s terminal != multi_dim_me (convention bug)", what);
+    return ZKH_OK;
+}
+extern "C" int zkh_lu_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const zkh_tensor* S,
+                            const zkh_tensor* T, const zkh_tensor* m, const uint32_t alpha_l[8],
+                            const uint32_t beta_l[8], const uint32_t* u_l, uint32_t* ev_out,
+                            uint32_t* term_out, uint32_t* ws_out) {
+    if (!xcheck_on() || !A || !T) return lu_prove_impl(c, tr, A, S, T, m, alpha_l, beta_l, u_l, ev_out, term_out, ws_out);
+    const uint32_t logD = ceil_log2(A->n), logN = ceil_log2(T->n);
+    std::vector<uint32_t> wsb(8 * (size_t)std::max<uint32_t>(logD, 1)), tb(40);
+    uint32_t* ws = ws_out ? ws_out : wsb.data();
+    uint32_t* term = term_out ? term_out : tb.data();
+    int rc = lu_prove_impl(c, tr, A, S, T, m, alpha_l, beta_l, u_l, ev_out, term, ws);
+    if (rc) return rc;
+    // zkob_rescale.cu:151-165, zkob_glu.cu:186-192: A_f, S_f at the point; m_f (and the
+    // public T_f) at its first logN coordinates
+    const std::vector<uint32_t> pt = reversed_point(ws, logD);
+    if ((rc = xcheck_me(c, A, pt.data(), logD, term, "lookup A")) ||
+        (rc = xcheck_me(c, S, pt.data(), logD, term + 8, "lookup S")) ||
+        (rc = xcheck_me(c, T, pt.data(), logN, term + 24, "lookup T")) ||
+        (rc = xcheck_me(c, m, pt.data(), logN, term + 32, "m")))
+        return rc;
     return ZKH_OK;
 }
 
@@ -3269,11 +3355,33 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     if (term_out) memcpy(term_out, tv, sizeof(tv));
     return ZKH_OK;
 }
+// hp_common with the ZKH_XCHECK guards of zkob_glu.cu:254-260 / zkob_rope.cu:240-246: S_f2
+// and U_f2 (and E_f) against the MLEs of S, U (and E, or the eq polynomial) at the point
+static int hp_checked(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const zkh_tensor* E,
+                      const std::vector<Fr>* ueq, const zkh_tensor* S, const zkh_tensor* U, uint32_t* ev_out,
+                      uint32_t* term_out, uint32_t* ws_out) {
+    if (!xcheck_on() || !S) return hp_common(c, tr, claim, E, ueq, S, U, ev_out, term_out, ws_out);
+    const uint32_t k = ceil_log2(S->n);
+    std::vector<uint32_t> wsb(8 * (size_t)std::max<uint32_t>(k, 1)), tb(24);
+    uint32_t* ws = ws_out ? ws_out : wsb.data();
+    uint32_t* term = term_out ? term_out : tb.data();
+    int rc = hp_common(c, tr, claim, E, ueq, S, U, ev_out, term, ws);
+    if (rc) return rc;
+    const std::vector<uint32_t> pt = reversed_point(ws, k);
+    if ((rc = xcheck_me(c, S, pt.data(), k, term, "hadamard S")) ||
+        (rc = xcheck_me(c, U, pt.data(), k, term + 8, "hadamard U")))
+        return rc;
+    if (E) return xcheck_me(c, E, pt.data(), k, term + 16, "hadamard E");
+    Fr e = kOne;  // eq(u, pt) = prod_i eq2(u_i, pt_i)
+    for (uint32_t i = 0; i < k; i++) e = fr_mul(e, fr_eq2((*ueq)[i], fr_load(&pt[8 * (size_t)i])));
+    if (!fr_eq(e, fr_load(term + 16))) return fail(c, ZKH_EROUND, "hadamard E terminal != eq(u, point) (convention bug)");
+    return ZKH_OK;
+}
 extern "C" int zkh_hp_prove(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const zkh_tensor* E,
                             const zkh_tensor* S, const zkh_tensor* U, uint32_t* ev_out,
                             uint32_t* term_out, uint32_t* ws_out) {
     if (!c || !tr || !claim || !E || !S || !U) return fail(c, ZKH_EARG, "null argument");
-    return hp_common(c, tr, claim, E, nullptr, S, U, ev_out, term_out, ws_out);
+    return hp_checked(c, tr, claim, E, nullptr, S, U, ev_out, term_out, ws_out);
 }
 extern "C" int zkh_hp_prove_eq(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const uint32_t* u,
                                uint32_t k, const zkh_tensor* S, const zkh_tensor* U, uint32_t* ev_out,
@@ -3281,7 +3389,7 @@ extern "C" int zkh_hp_prove_eq(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[
     if (!c || !tr || !claim || !S || !U || (!u && k)) return fail(c, ZKH_EARG, "null argument");
     if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
     std::vector<Fr> uv = load_frs(u, k);
-    return hp_common(c, tr, claim, nullptr, &uv, S, U, ev_out, term_out, ws_out);
+    return hp_checked(c, tr, claim, nullptr, &uv, S, U, ev_out, term_out, ws_out);
 }
 
 // ---------------------------------------------------------------------------------------
