@@ -39,3 +39,33 @@ def test_bad_mode_prints_usage(name):
     r = run(name, "selftest")
     assert r.returncode == 2
     assert "usage" in r.stderr
+
+
+@pytest.mark.parametrize("spec,why", [("3=gen.bin", "power of two"), ("1=gen.bin", "power of two"),
+                                      ("4x=gen.bin", "power of two"), ("=gen.bin", "power of two"),
+                                      ("4", "power of two"), ("4=", "power of two"),
+                                      ("99999999999=g", "power of two")])
+def test_batchopen_rejects_bad_generator_spec(spec, why):
+    """A generator spec is <G>=<file> with the whole of G a decimal power of two >= 2; anything
+    else is refused by name before any file is read."""
+    r = run("zkh_batchopen", "prove", "acc", "seed", "q.bin", "2=a.bin", spec)
+    assert r.returncode == 1
+    assert "generator spec '%s'" % spec in r.stderr and why in r.stderr
+
+
+def test_batchopen_rejects_duplicate_domain():
+    r = run("zkh_batchopen", "prove", "acc", "seed", "q.bin", "4=a.bin", "8=b.bin", "4=c.bin")
+    assert r.returncode == 1
+    assert "generator spec '4=c.bin': domain 4 given twice" in r.stderr
+
+
+def test_serve_reads_long_request_lines_whole():
+    """A request line longer than any fixed buffer is one request (zkob_serve.cuh reads lines
+    with std::getline): one ZKW-RC answer, here usage (2) for an unknown mode."""
+    if not os.path.exists(BIN["zkh_batchopen"]):
+        pytest.skip("drivers not built")
+    line = "selftest " + "x" * 200000
+    r = subprocess.run([BIN["zkh_batchopen"], "serve"], input=line + "\n\n", capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 0
+    assert r.stdout.splitlines() == ["ZKW-READY", "ZKW-RC 2"]

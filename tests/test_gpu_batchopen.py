@@ -38,8 +38,10 @@ R = P.R
 @pytest.fixture(autouse=True)
 def _convention_crosschecks(monkeypatch):
     """The drivers run with ZKH_XCHECK=1: every proof also checks its folded terminals against
-    multi_dim_me at the opening point, as the reference's drivers do."""
+    multi_dim_me at the opening point, as the reference's drivers do; the batch opening also
+    runs its commitment-side self-check (ZKOB_BATCH_SELFCHECK, zkob_claims.cuh:1038-1052)."""
     monkeypatch.setenv("ZKH_XCHECK", "1")
+    monkeypatch.setenv("ZKOB_BATCH_SELFCHECK", "1")
 
 
 def points(seed, n):

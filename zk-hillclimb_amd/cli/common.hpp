@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <iostream>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -147,10 +149,11 @@ inline int driver_main(int argc, char** argv, int (*run1)(const std::vector<std:
     if (argc > 1 && std::string(argv[1]) == "serve") {
         printf("ZKW-READY\n");
         fflush(stdout);
-        char line[1 << 16];
-        while (fgets(line, sizeof(line), stdin)) {
+        std::string line;  // one request per line, of any length
+        while (std::getline(std::cin, line)) {
             std::vector<std::string> toks;
-            for (char* t = strtok(line, " \t\r\n"); t; t = strtok(nullptr, " \t\r\n")) toks.push_back(t);
+            std::istringstream words(line);
+            for (std::string t; words >> t;) toks.push_back(t);
             if (toks.empty()) continue;
             int rc;
             try {

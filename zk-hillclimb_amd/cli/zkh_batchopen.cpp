@@ -1,32 +1,45 @@
-// zkh_batchopen -- a zkob_batchopen-compatible driver over libzkh (zkob_batchopen.cu:695-755,
-// batch_prove zkob_claims.cuh:832-1066).
+// zkh_batchopen -- a zkob_batchopen-compatible driver over libzkh (zkob_batchopen.cu:695-755;
+// the proof it writes is batch_prove's, zkob_claims.cuh:832-1066).
 //
 //   zkh_batchopen prove <accdir> <run_seed> <q.bin> <G>=<gen.bin> ...
 //   zkh_batchopen serve
 //
 // `prove` opens every claim the drivers emitted into <accdir> (claims.bin, witrefs.txt,
-// drvstates.bin) with ONE batch-evaluation sumcheck and one IPA per generator domain:
-//   G0  transcript "<run_seed>:opening_batch" absorbs the claim count, every claim blob,
-//       every distinct commitment file (path, SHA-256 of its bytes), every driver state;
-//       rho; M_j = sum over tensor j's claims of rho^i eq(point_i), P_j = its witness;
-//   G2  m_max rounds, round t binding variable m_max-1-t: sum_j c2_j (sum M_j P_j at
-//       0, 1, 2) (a tensor with fewer variables contributes c2_j S_j (1-T)^2); "bp0".."bp2";
-//   G3  terminals vfin_j = P_j(r), absorbed, checked against sum_j M_j(r) kappa_j vfin_j;
-//   G4  rho'; per domain G ascending, a = sum_j rho'^j kappa_j (w_j folded over its rows by
-//       r[logG..vars_j)), b = me_weights(r[0..logG)), an IPA over the domain's generators.
+// drvstates.bin) with one batch-evaluation sumcheck and one IPA per generator domain.
+// Protocol (kept byte for byte; the code below is organised differently):
+//   header   transcript "<run_seed>:opening_batch" absorbs "n_claims", each claim blob
+//            ("claim"), each committed tensor's (path, SHA-256 of its file) ("comref", in
+//            the order the tensors first appear among the claims) and each driver state
+//            ("drvstate"); rho is drawn; claim i carries weight rho^i.
+//   rounds   one round per variable of the largest tensor, from the top variable down:
+//            the round polynomial at 0, 1, 2 is absorbed as "bp0".."bp2" and the challenge
+//            drawn.  A tensor with fewer variables than the round's index contributes
+//            lift * <M_j, P_j> (1 - X)^2, lift being the product of (1 - r)^2 over the
+//            rounds already bound; from its first own round on it is an ordinary product
+//            sumcheck of M_j = sum_i rho^i eq(point_i, .) and its witness P_j, scaled by
+//            the lift at that moment (= kappa_j^2, kappa_j = prod over the variables above
+//            it of (1 - r_v)).
+//   terms    the folded witnesses P_j(r) are absorbed ("vfin") and checked against the
+//            final claim: sum_j kappa_j^2 M_j(r) P_j(r).
+//   ipa      rho' is drawn; per domain G, ascending, a = sum_j rho'^j kappa_j (witness j
+//            with its rows bound by r[logG..vars_j)) and b = eq(r[0..logG), .), proved by
+//            one IPA over the domain's generators.
 // Files, byte-identical to the reference's: batch_sumcheck.bin ("ZKBS", n_claims, m_max,
-// count-prefixed evals), batch_vfin.bin ("ZKBV", count-prefixed terminals),
-// ipa_batch_<G>.bin.  With ZKOB_PROF set it prints the reference's lap lines
-// ("PROF batch_prove.{setup,rounds,terminal,ipa} <s> s").  `verify`, `genq` and `selftest`
-// answer exit status 2.
+// count-prefixed evaluations), batch_vfin.bin ("ZKBV", count-prefixed terminals),
+// ipa_batch_<G>.bin.  ZKOB_PROF prints the reference's lap lines ("PROF
+// batch_prove.{setup,rounds,terminal,ipa} <s> s").  ZKOB_BATCH_SELFCHECK also checks, per
+// domain, that <gen, a> equals the same combination of the tensors' row commitments
+// (the commitment-side identity of zkob_claims.cuh:1038-1052).  `verify`, `genq` and
+// `selftest` answer exit status 2.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <chrono>
 #include <map>
-#include <set>
+#include <unordered_map>
 
 #include "common.hpp"
 
@@ -34,341 +47,387 @@ using namespace zkhcli;
 
 namespace {
 
-struct TensorInfo {
-    std::string comref;
-    uint32_t domain = 0, n_rows = 0, vars = 0, logG = 0;
-    std::vector<uint32_t> idx;
+// witnesses stay on the device from the setup to the openings up to this many bytes in total
+constexpr uint64_t kResidentMax = 32ull << 30;
+
+// one committed tensor and the claims made on it
+struct Opened {
+    std::string comref, witness;
+    uint32_t domain = 0, logG = 0, nv = 0;  // nv: variables of the padded witness
+    std::vector<uint32_t> claims;           // indices into the claim list
+    Tensor M, P, W;                         // weight table, folded witness, resident witness
+    Fr8 inner;                              // <M, P> before the rounds reach the tensor
+    Fr8 kappa = fr_u32(1);                  // prod of (1 - r_v) over v >= nv
+    Fr8 term;                               // P(r) after the rounds
 };
 
-// derive_tensors (zkob_claims.cuh:280-308): distinct comrefs in first-appearance order
-std::vector<TensorInfo> derive_tensors(const std::vector<Claim>& cs) {
-    std::vector<TensorInfo> out;
-    std::map<std::string, uint32_t> key;
+// lap timer with the reference's ZKOB_PROF lines; each lap waits for the device
+struct Stopwatch {
+    bool on = getenv("ZKOB_PROF") != nullptr;
+    std::chrono::steady_clock::time_point since = std::chrono::steady_clock::now();
+    void lap(const char* name) {
+        if (on) {
+            zkh_ctx_sync(g_ctx);
+            const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - since).count();
+            printf("PROF batch_prove.%s %.4f s\n", name, s);
+        }
+        since = std::chrono::steady_clock::now();
+    }
+};
+
+bool is_pow2_at_least_2(uint64_t x) { return x >= 2 && (x & (x - 1)) == 0; }
+
+// The claims grouped by committed tensor, tensors in order of first appearance.  Every claim
+// on a tensor must describe the same geometry: a power-of-two domain of G >= 2 columns, a
+// point of logG column coordinates then row coordinates, and 2^(rows coordinates) rows.
+std::vector<Opened> group_claims(const std::vector<Claim>& cs) {
+    std::vector<Opened> ts;
+    std::unordered_map<std::string, size_t> slot;
     for (uint32_t i = 0; i < cs.size(); i++) {
         const Claim& c = cs[i];
-        if (c.domain < 2 || (c.domain & (c.domain - 1)))
-            throw Err(1, "claim " + c.id + ": domain not a power of two >= 2");
-        const uint32_t logG = ceil_log2(c.domain), vars = c.nvars();
-        if (vars < logG) throw Err(1, "claim " + c.id + ": point shorter than logG");
-        if (vars - logG >= 32 || c.n_rows != (1u << (vars - logG)))
-            throw Err(1, "claim " + c.id + ": n_rows != 2^{vars-logG}");
-        auto it = key.find(c.comref);
-        if (it == key.end()) {
-            TensorInfo t;
-            t.comref = c.comref;
-            t.domain = c.domain;
-            t.n_rows = c.n_rows;
-            t.vars = vars;
-            t.logG = logG;
-            t.idx.push_back(i);
-            key[c.comref] = (uint32_t)out.size();
-            out.push_back(t);
-        } else {
-            TensorInfo& t = out[it->second];
-            if (t.domain != c.domain || t.n_rows != c.n_rows || t.vars != vars)
-                throw Err(1, "claim " + c.id + ": shape disagrees with earlier claim on same tensor");
-            t.idx.push_back(i);
+        const std::string who = "claim '" + c.id + "' on " + c.comref;
+        if (!is_pow2_at_least_2(c.domain))
+            throw Err(1, who + ": generator domain " + std::to_string(c.domain) + " is not a power of two >= 2");
+        const uint32_t logG = ceil_log2(c.domain), nv = c.nvars();
+        if (nv < logG)
+            throw Err(1, who + ": point has " + std::to_string(nv) + " coordinates, fewer than log2(domain)");
+        if (nv - logG >= 32 || c.n_rows != (1u << (nv - logG)))
+            throw Err(1, who + ": " + std::to_string(c.n_rows) + " rows do not match a point of " +
+                             std::to_string(nv - logG) + " row coordinates");
+        auto [it, fresh] = slot.emplace(c.comref, ts.size());
+        if (fresh) {
+            ts.emplace_back();
+            ts.back().comref = c.comref;
+            ts.back().domain = c.domain;
+            ts.back().logG = logG;
+            ts.back().nv = nv;
         }
+        Opened& t = ts[it->second];
+        if (t.domain != c.domain || t.nv != nv)
+            throw Err(1, who + ": geometry differs from an earlier claim on the same tensor");
+        t.claims.push_back(i);
+    }
+    return ts;
+}
+
+// "<G>=<path>" arguments: G a decimal power of two >= 2, each domain named once
+std::map<uint32_t, std::string> parse_generators(const std::vector<std::string>& specs) {
+    std::map<uint32_t, std::string> out;
+    for (const std::string& s : specs) {
+        const size_t eq = s.find('=');
+        const std::string g = s.substr(0, eq == std::string::npos ? 0 : eq);
+        const bool digits = !g.empty() && g.size() <= 10 &&
+                            std::all_of(g.begin(), g.end(), [](char ch) { return ch >= '0' && ch <= '9'; });
+        const uint64_t G = digits ? std::stoull(g) : 0;
+        if (eq == std::string::npos || eq + 1 == s.size() || !digits || !is_pow2_at_least_2(G) || G > (1u << 31))
+            throw Err(1, "generator spec '" + s + "': expected <G>=<file> with G a power of two >= 2");
+        if (!out.emplace((uint32_t)G, s.substr(eq + 1)).second)
+            throw Err(1, "generator spec '" + s + "': domain " + g + " given twice");
     }
     return out;
 }
 
-// witnesses kept on the device between the rounds and G5 up to this many bytes in total
-constexpr uint64_t kResidentMax = 32ull << 30;
-
-// BoTimer (zkob_claims.cuh:62-75): with ZKOB_PROF set, "PROF batch_prove.<lap> <s> s" per lap,
-// after the device has finished the lap's work
-struct Laps {
-    const bool on = getenv("ZKOB_PROF") != nullptr;
-    std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
-    void lap(const char* what) {
-        if (on) {
-            zkh_ctx_sync(g_ctx);
-            printf("PROF batch_prove.%s %.4f s\n", what,
-                   std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
-        }
-        t0 = std::chrono::steady_clock::now();
-    }
-};
-
-std::map<std::string, std::string> witrefs_load(const std::string& accdir) {
-    std::map<std::string, std::string> m;
-    std::vector<uint8_t> b = read_all(accdir + "/witrefs.txt");
-    std::string all((const char*)b.data(), b.size());
-    size_t pos = 0;
-    while (pos < all.size()) {
-        size_t nl = all.find('\n', pos);
-        if (nl == std::string::npos) nl = all.size();
-        const std::string line = all.substr(pos, nl - pos);
-        pos = nl + 1;
+// witrefs.txt: "<comref>\t<witness path>" lines
+std::unordered_map<std::string, std::string> read_witrefs(const std::string& accdir) {
+    const std::vector<uint8_t> raw = read_all(accdir + "/witrefs.txt");
+    std::unordered_map<std::string, std::string> m;
+    size_t at = 0;
+    while (at < raw.size()) {
+        size_t end = at;
+        while (end < raw.size() && raw[end] != '\n') end++;
+        const std::string line((const char*)raw.data() + at, end - at);
         const size_t tab = line.find('\t');
         if (tab != std::string::npos) m[line.substr(0, tab)] = line.substr(tab + 1);
+        at = end + 1;
     }
     return m;
 }
 
-Fr8 eq1(const Fr8& u, const Fr8& v) {  // bo_eq1: 2uv - (u + v) + 1
-    const Fr8 uv = fmul(u, v);
-    return fadd(fsub(fadd(uv, uv), fadd(u, v)), fr_u32(1));
-}
-Fr8 kappa(uint32_t vars, const std::vector<Fr8>& r) {  // prod_{v >= vars} (1 - r[v])
-    Fr8 k = fr_u32(1);
-    for (uint32_t v = vars; v < r.size(); v++) k = fmul(k, fsub(fr_u32(1), r[v]));
-    return k;
-}
-
-// FrTensor(witpath) (fr-tensor.cu:190-197): the raw 32-byte entries, mapped rather than copied
-void load_witness(const std::string& path, uint64_t n, Tensor& t) {
+// the n 32-byte entries of a witness file (FrTensor(path), fr-tensor.cu:190-197), mapped and
+// uploaded without a host copy
+void upload_witness(const std::string& path, uint64_t n, Tensor& t) {
     const int fd = open(path.c_str(), O_RDONLY);
-    if (fd < 0) throw Err(1, "cannot open " + path);
+    if (fd < 0) throw Err(1, "cannot open witness " + path);
     struct stat sb;
-    if (fstat(fd, &sb) != 0 || (uint64_t)sb.st_size != n * 32 || n == 0) {
-        close(fd);
-        throw Err(1, "batch_prove: witness size mismatch for " + path);
-    }
-    void* p = mmap(nullptr, n * 32, PROT_READ, MAP_PRIVATE | MAP_POPULATE, fd, 0);
+    const bool ok = fstat(fd, &sb) == 0 && n > 0 && (uint64_t)sb.st_size == n * 32;
+    void* p = ok ? mmap(nullptr, n * 32, PROT_READ, MAP_PRIVATE | MAP_POPULATE, fd, 0) : MAP_FAILED;
     close(fd);
-    if (p == MAP_FAILED) throw Err(1, "cannot map " + path);
+    if (!ok) throw Err(1, "witness " + path + " does not hold " + std::to_string(n) + " field elements");
+    if (p == MAP_FAILED) throw Err(1, "cannot map witness " + path);
     const int rc = zkh_tensor_from_fr(g_ctx, (const uint32_t*)p, (uint32_t)n, &t.t);
     munmap(p, n * 32);
-    chk(rc, "witness");
+    chk(rc, "witness upload");
 }
-void absorb_fr(uint8_t st[32], const char* label, const Fr8& x) { absorb(st, label, x.v, 32); }
+
 Fr8 draw(uint8_t st[32]) {
     Fr8 x;
     zkh_transcript_challenge_fr(st, x.v);
     return x;
 }
+void absorb_fr(uint8_t st[32], const char* label, const Fr8& x) { absorb(st, label, x.v, 32); }
+std::vector<Fr8> powers(const Fr8& x, size_t n) {
+    std::vector<Fr8> p(n, fr_u32(1));
+    for (size_t i = 1; i < n; i++) p[i] = fmul(p[i - 1], x);
+    return p;
+}
+std::vector<uint32_t> words(const std::vector<Fr8>& r, uint32_t from, uint32_t to) {
+    std::vector<uint32_t> w;
+    for (uint32_t v = from; v < to; v++) w.insert(w.end(), r[v].v, r[v].v + 8);
+    return w;
+}
 
-int do_prove(const std::vector<std::string>& a) {
-    Laps T;
-    const std::string accdir = a[0], run_seed = a[1];
-    std::vector<uint32_t> q = load_points(a[2]);
-    if (q.empty()) throw Err(1, "q.bin holds no point");
-    std::map<uint32_t, std::string> genpaths;  // parse_genspecs: <G>=<path>
-    for (size_t i = 3; i < a.size(); i++) {
-        const size_t eq = a[i].find('=');
-        if (eq == std::string::npos) throw Err(1, "bad generator spec " + a[i]);
-        genpaths[(uint32_t)strtoul(a[i].substr(0, eq).c_str(), nullptr, 10)] = a[i].substr(eq + 1);
+// the batch header: claim count, claims, committed tensors (path + file digest), driver states
+void absorb_header(uint8_t st[32], const std::vector<Claim>& cs, const std::vector<Opened>& ts,
+                   const std::vector<DrvState>& dss) {
+    const uint32_t n = (uint32_t)cs.size();
+    absorb(st, "n_claims", &n, 4);
+    for (const Claim& c : cs) {
+        const std::vector<uint8_t> blob = claim_blob(c);
+        absorb(st, "claim", blob.data(), blob.size());
     }
-    const std::vector<Claim> cs = claims_load(accdir + "/claims.bin");
-    if (cs.empty()) throw Err(1, "batch_prove: zero claims");
-    const std::vector<TensorInfo> ts = derive_tensors(cs);
-    std::vector<DrvState> dss;
-    if (file_exists(accdir + "/drvstates.bin")) dss = drvstates_load(accdir + "/drvstates.bin");
-    const std::map<std::string, std::string> wits = witrefs_load(accdir);
-    uint32_t m_max = 0;
-    for (const auto& t : ts) m_max = std::max(m_max, t.vars);
-    if (m_max < 1) throw Err(1, "batch_prove: m_max < 1");
-    const uint32_t nT = (uint32_t)ts.size();
-    std::vector<std::string> witpath(nT);
-    for (uint32_t j = 0; j < nT; j++) {
-        auto it = wits.find(ts[j].comref);
-        if (it == wits.end()) throw Err(1, "batch_prove: no witref for " + ts[j].comref);
-        witpath[j] = it->second;
-    }
-
-    // G0 (batch_absorb_g0, zkob_claims.cuh:320-346) and rho
-    uint8_t st[32];
-    const std::string seed = run_seed + ":opening_batch";
-    zkh_transcript_init(st, seed.data(), seed.size());
-    const uint32_t ncl = (uint32_t)cs.size();
-    absorb(st, "n_claims", &ncl, 4);
-    for (const auto& c : cs) {
-        const std::vector<uint8_t> b = claim_blob(c);
-        absorb(st, "claim", b.data(), b.size());
-    }
-    for (const auto& t : ts) {
+    auto named = [](const std::string& s, const uint8_t* tail, size_t tn) {
         std::vector<uint8_t> b;
-        put_u32(b, (uint32_t)t.comref.size());
-        put_bytes(b, t.comref.data(), t.comref.size());
-        const std::vector<uint8_t> f = read_all(t.comref);
-        uint8_t h[32];
-        zkh_sha256(f.data(), f.size(), h);
-        put_bytes(b, h, 32);
+        put_u32(b, (uint32_t)s.size());
+        put_bytes(b, s.data(), s.size());
+        put_bytes(b, tail, tn);
+        return b;
+    };
+    for (const Opened& t : ts) {
+        const std::vector<uint8_t> file = read_all(t.comref);
+        uint8_t digest[32];
+        zkh_sha256(file.data(), file.size(), digest);
+        const std::vector<uint8_t> b = named(t.comref, digest, 32);
         absorb(st, "comref", b.data(), b.size());
     }
-    for (const auto& d : dss) {
-        std::vector<uint8_t> b;
-        put_u32(b, (uint32_t)d.id.size());
-        put_bytes(b, d.id.data(), d.id.size());
-        put_bytes(b, d.state, 32);
+    for (const DrvState& d : dss) {
+        const std::vector<uint8_t> b = named(d.id, d.state, 32);
         absorb(st, "drvstate", b.data(), b.size());
     }
-    const Fr8 rho = draw(st);
-    std::vector<Fr8> rho_pows(ncl);
-    rho_pows[0] = fr_u32(1);
-    for (uint32_t i = 1; i < ncl; i++) rho_pows[i] = fmul(rho_pows[i - 1], rho);
+}
 
-    // per tensor: M_j = sum_i rho^i eq(point_i), P_j = witness, S_j = <M_j, P_j> if short
-    uint64_t wit_bytes = 0;
-    for (const auto& t : ts) wit_bytes += 32ull << t.vars;
-    const bool resident = wit_bytes <= kResidentMax;
-    std::vector<Tensor> M(nT), Pt(nT), Wt(nT);
-    std::vector<Fr8> c2(nT, fr_u32(1)), S(nT);
-    for (uint32_t j = 0; j < nT; j++) {
-        const uint64_t n = 1ull << ts[j].vars;
-        // the witness stays on the device for G5 when the layer's witnesses fit the budget
-        // (the reference reloads it there); P_j is a copy that the rounds fold in place
-        Tensor w;
-        load_witness(witpath[j], n, w);
-        chk(zkh_axpy(g_ctx, w.t, fr_u32(0).v, w.t, &Pt[j].t), "P");
-        if (resident) std::swap(Wt[j].t, w.t);
-        for (uint32_t k = 0; k < ts[j].idx.size(); k++) {
-            const Claim& c = cs[ts[j].idx[k]];
-            Tensor e, acc;
-            chk(zkh_eq_table(g_ctx, c.point.data(), c.nvars(), &e.t), "eq(point)");
-            if (k == 0) {  // rho^i eq = eq + (rho^i - 1) eq
-                chk(zkh_axpy(g_ctx, e.t, fsub(rho_pows[ts[j].idx[k]], fr_u32(1)).v, e.t, &acc.t), "M");
-            } else {
-                chk(zkh_axpy(g_ctx, M[j].t, rho_pows[ts[j].idx[k]].v, e.t, &acc.t), "M");
-            }
-            std::swap(M[j].t, acc.t);
+// M = sum over the tensor's claims of rho^i eq(point_i, .); P = a copy of the witness, which
+// the rounds fold in place; the witness itself is kept for the openings when `keep`
+void build_tables(Opened& t, const std::vector<Claim>& cs, const std::vector<Fr8>& weight, bool keep) {
+    Tensor w;
+    upload_witness(t.witness, 1ull << t.nv, w);
+    chk(zkh_axpy(g_ctx, w.t, fr_u32(0).v, w.t, &t.P.t), "witness copy");
+    if (keep) std::swap(t.W.t, w.t);
+    for (uint32_t i : t.claims) {
+        Tensor e, next;
+        chk(zkh_eq_table(g_ctx, cs[i].point.data(), cs[i].nvars(), &e.t), "eq table");
+        if (!t.M.t)  // the first claim: eq + (rho^i - 1) eq
+            chk(zkh_axpy(g_ctx, e.t, fsub(weight[i], fr_u32(1)).v, e.t, &next.t), "weights");
+        else
+            chk(zkh_axpy(g_ctx, t.M.t, weight[i].v, e.t, &next.t), "weights");
+        std::swap(t.M.t, next.t);
+    }
+}
+
+// sum_i rho^i eq(point_i, r) over the tensor's own variables
+Fr8 weight_at(const Opened& t, const std::vector<Claim>& cs, const std::vector<Fr8>& weight,
+              const std::vector<Fr8>& r) {
+    Fr8 s;
+    for (uint32_t i : t.claims) {
+        Fr8 e = weight[i];
+        for (uint32_t v = 0; v < t.nv; v++) {
+            const Fr8 a = fr_of(cs[i].point.data() + 8 * v), ar = fmul(a, r[v]);
+            e = fmul(e, fadd(fsub(fadd(ar, ar), fadd(a, r[v])), fr_u32(1)));  // eq(a, r_v)
         }
-        if (zkh_tensor_size(M[j].t) != n) throw Err(1, "batch_prove: table size");
-        if (ts[j].vars < m_max) {
+        s = fadd(s, e);
+    }
+    return s;
+}
+
+// ZKOB_BATCH_SELFCHECK: <gen, a> - sum_j coef_j (row commitments of j bound by its row
+// challenges) must be the point at infinity (z = 0)
+void selfcheck_domain(const Points& gen, const zkh_tensor* a, const std::vector<const Opened*>& group,
+                      const std::vector<Fr8>& coef, const std::vector<Fr8>& r) {
+    Points acc;
+    chk(zkh_commit(g_ctx, gen.g, a, &acc.g), "selfcheck <gen, a>");
+    for (size_t k = 0; k < group.size(); k++) {
+        const Opened& t = *group[k];
+        const std::vector<uint32_t> rows = load_points(t.comref);
+        Points com, bound, next;
+        chk(zkh_g1_from_host(g_ctx, rows.data(), (uint32_t)(rows.size() / 36), &com.g), "selfcheck com");
+        const zkh_g1* c = com.g;
+        if (t.nv > t.logG) {
+            const std::vector<uint32_t> ur = words(r, t.logG, t.nv);
+            Tensor e;
+            chk(zkh_eq_table(g_ctx, ur.data(), t.nv - t.logG, &e.t), "selfcheck row weights");
+            chk(zkh_commit(g_ctx, com.g, e.t, &bound.g), "selfcheck row fold");
+            c = bound.g;
+        }
+        chk(zkh_g1_addmul(g_ctx, c, fsub(Fr8(), coef[k]).v, acc.g, &next.g), "selfcheck combine");
+        std::swap(acc.g, next.g);
+    }
+    const std::vector<uint32_t> p = to_host(acc.g);
+    for (int i = 24; i < 36; i++)
+        if (p[i]) throw Err(1, "batch_prove: commitment-side self-check failed for domain " + std::to_string(group[0]->domain));
+}
+
+int prove(const std::vector<std::string>& a) {
+    Stopwatch sw;
+    const std::string accdir = a[0], run_seed = a[1];
+    const std::map<uint32_t, std::string> gens = parse_generators({a.begin() + 3, a.end()});
+    const std::vector<uint32_t> Q = load_points(a[2]);
+    if (Q.empty()) throw Err(1, "q.bin holds no point");
+
+    const std::vector<Claim> cs = claims_load(accdir + "/claims.bin");
+    if (cs.empty()) throw Err(1, "batch_prove: claims.bin holds no claim");
+    std::vector<Opened> ts = group_claims(cs);
+    const std::vector<DrvState> dss =
+        file_exists(accdir + "/drvstates.bin") ? drvstates_load(accdir + "/drvstates.bin") : std::vector<DrvState>();
+    const auto refs = read_witrefs(accdir);
+    uint32_t nvars = 0;
+    uint64_t witness_bytes = 0;
+    for (Opened& t : ts) {
+        auto it = refs.find(t.comref);
+        if (it == refs.end()) throw Err(1, "batch_prove: no witref for " + t.comref);
+        t.witness = it->second;
+        nvars = std::max(nvars, t.nv);
+        witness_bytes += 32ull << t.nv;
+    }
+    if (nvars == 0) throw Err(1, "batch_prove: every claim is on a single entry");
+
+    uint8_t st[32];
+    const std::string label = run_seed + ":opening_batch";
+    zkh_transcript_init(st, label.data(), label.size());
+    absorb_header(st, cs, ts, dss);
+    const std::vector<Fr8> weight = powers(draw(st), cs.size());
+
+    need_ctx();
+    const bool keep = witness_bytes <= kResidentMax;
+    for (Opened& t : ts) {
+        build_tables(t, cs, weight, keep);
+        if (zkh_tensor_size(t.M.t) != (1u << t.nv)) throw Err(1, "batch_prove: weight table size");
+        if (t.nv < nvars) {  // needed by the rounds above the tensor's variables
             Tensor h;
-            chk(zkh_hadamard(g_ctx, M[j].t, Pt[j].t, &h.t), "M P");
-            chk(zkh_sum(g_ctx, h.t, S[j].v), "S_j");
+            chk(zkh_hadamard(g_ctx, t.M.t, t.P.t, &h.t), "M P");
+            chk(zkh_sum(g_ctx, h.t, t.inner.v), "<M, P>");
         }
     }
-    T.lap("setup");
-    Fr8 cur;
-    for (uint32_t i = 0; i < ncl; i++) cur = fadd(cur, fmul(rho_pows[i], fr_of(cs[i].eval)));
+    sw.lap("setup");
 
-    // G2 rounds
-    std::vector<Fr8> r(m_max);
-    std::vector<uint32_t> ev;
-    for (uint32_t t = 0; t < m_max; t++) {
-        const uint32_t v = m_max - 1 - t;
-        Fr8 p[3];
-        for (uint32_t j = 0; j < nT; j++) {
-            if (ts[j].vars <= v) {
-                const Fr8 term = fmul(c2[j], S[j]);
-                p[0] = fadd(p[0], term);
-                p[2] = fadd(p[2], term);
-            } else {
-                uint32_t qv[24];
-                chk(zkh_prod_round(g_ctx, M[j].t, Pt[j].t, qv), "round sums");
-                for (int k = 0; k < 3; k++) p[k] = fadd(p[k], fmul(c2[j], fr_of(qv + 8 * k)));
+    Fr8 claim;
+    for (uint32_t i = 0; i < cs.size(); i++) claim = fadd(claim, fmul(weight[i], fr_of(cs[i].eval)));
+
+    // rounds, top variable first.  `lin` = prod (1 - r) over the bound variables; a tensor
+    // whose variables are all below the bound ones has kappa = lin and weight lin^2.
+    std::vector<Fr8> r(nvars);
+    std::vector<uint32_t> evals;
+    Fr8 lin = fr_u32(1);
+    for (uint32_t v = nvars; v-- > 0;) {
+        Fr8 p[3], idle;
+        for (Opened& t : ts) {
+            if (t.nv <= v) {
+                idle = fadd(idle, t.inner);
+                continue;
             }
+            if (t.nv == v + 1) t.kappa = lin;  // the tensor's first own round
+            uint32_t q[24];
+            chk(zkh_prod_round(g_ctx, t.M.t, t.P.t, q), "round sums");
+            const Fr8 c = fmul(t.kappa, t.kappa);
+            for (int k = 0; k < 3; k++) p[k] = fadd(p[k], fmul(c, fr_of(q + 8 * k)));
         }
-        if (!feq(cur, fadd(p[0], p[1])))
-            throw Err(1, "batch_prove: round " + std::to_string(t) + " inconsistency (witness/claims bug)");
+        const Fr8 lifted = fmul(fmul(lin, lin), idle);
+        p[0] = fadd(p[0], lifted);
+        p[2] = fadd(p[2], lifted);
+        if (!feq(fadd(p[0], p[1]), claim))
+            throw Err(1, "batch_prove: round " + std::to_string(nvars - 1 - v) +
+                             " inconsistency: p(0) + p(1) differs from the claim (witness or claims wrong)");
         absorb_fr(st, "bp0", p[0]);
         absorb_fr(st, "bp1", p[1]);
         absorb_fr(st, "bp2", p[2]);
-        const Fr8 x = draw(st);
-        r[v] = x;
-        for (int k = 0; k < 3; k++) ev.insert(ev.end(), p[k].v, p[k].v + 8);
-        cur = lagrange3(p[0], p[1], p[2], x);
-        const Fr8 omx = fsub(fr_u32(1), x), omx2 = fmul(omx, omx);
-        for (uint32_t j = 0; j < nT; j++) {
-            if (ts[j].vars <= v) {
-                c2[j] = fmul(c2[j], omx2);
-            } else {
-                chk(zkh_fold(g_ctx, M[j].t, x.v), "fold M");
-                chk(zkh_fold(g_ctx, Pt[j].t, x.v), "fold P");
-            }
+        for (const Fr8& x : p) evals.insert(evals.end(), x.v, x.v + 8);
+        r[v] = draw(st);
+        claim = lagrange3(p[0], p[1], p[2], r[v]);
+        lin = fmul(lin, fsub(fr_u32(1), r[v]));
+        for (Opened& t : ts) {
+            if (t.nv <= v) continue;
+            chk(zkh_fold(g_ctx, t.M.t, r[v].v), "fold M");
+            chk(zkh_fold(g_ctx, t.P.t, r[v].v), "fold P");
         }
     }
     {
         std::vector<uint8_t> b;
         put_bytes(b, "ZKBS", 4);
-        put_u32(b, ncl);
-        put_u32(b, m_max);
-        put_pod(b, ev.data(), 3 * m_max, 8);
+        put_u32(b, (uint32_t)cs.size());
+        put_u32(b, nvars);
+        put_pod(b, evals.data(), 3 * nvars, 8);
         write_all(accdir + "/batch_sumcheck.bin", b.data(), b.size());
     }
-    T.lap("rounds");
+    sw.lap("rounds");
 
-    // G3 terminals
-    std::vector<Fr8> vfin(nT);
-    for (uint32_t j = 0; j < nT; j++) {
-        chk(zkh_tensor_to_fr(g_ctx, Pt[j].t, vfin[j].v), "vfin");
-        absorb_fr(st, "vfin", vfin[j]);
+    // terminals
+    std::vector<uint32_t> vfin;
+    Fr8 expect;
+    for (Opened& t : ts) {
+        chk(zkh_tensor_to_fr(g_ctx, t.P.t, t.term.v), "terminal");
+        absorb_fr(st, "vfin", t.term);
+        vfin.insert(vfin.end(), t.term.v, t.term.v + 8);
+        const Fr8 k2 = fmul(t.kappa, t.kappa);
+        expect = fadd(expect, fmul(fmul(k2, weight_at(t, cs, weight, r)), t.term));
+        zkh_tensor_free(t.M.t);
+        zkh_tensor_free(t.P.t);
+        t.M.t = t.P.t = nullptr;
     }
     {
-        std::vector<uint32_t> vv;
-        for (const auto& x : vfin) vv.insert(vv.end(), x.v, x.v + 8);
         std::vector<uint8_t> b;
         put_bytes(b, "ZKBV", 4);
-        put_pod(b, vv.data(), nT, 8);
+        put_pod(b, vfin.data(), (uint32_t)ts.size(), 8);
         write_all(accdir + "/batch_vfin.bin", b.data(), b.size());
     }
-    {  // sum_j M_j(r) kappa_j vfin_j == cur (bo_Mj_at_r, bo_kappa)
-        Fr8 chkv;
-        for (uint32_t j = 0; j < nT; j++) {
-            const Fr8 kap = kappa(ts[j].vars, r);
-            Fr8 mj;
-            for (uint32_t i : ts[j].idx) {
-                Fr8 term = rho_pows[i];
-                for (uint32_t v = 0; v < ts[j].vars; v++) term = fmul(term, eq1(fr_of(cs[i].point.data() + 8 * v), r[v]));
-                mj = fadd(mj, fmul(term, kap));
-            }
-            chkv = fadd(chkv, fmul(fmul(mj, kap), vfin[j]));
-        }
-        if (!feq(chkv, cur)) throw Err(1, "batch_prove: G3 terminal self-check failed");
-    }
-    for (auto& t : M) {
-        zkh_tensor_free(t.t);
-        t.t = nullptr;
-    }
-    for (auto& t : Pt) {
-        zkh_tensor_free(t.t);
-        t.t = nullptr;
-    }
+    if (!feq(expect, claim)) throw Err(1, "batch_prove: terminals do not reproduce the final claim");
+    sw.lap("terminal");
 
-    T.lap("terminal");
-
-    // G4 + G5: one IPA per generator domain, ascending
-    const Fr8 rhop = draw(st);
-    std::vector<Fr8> rhop_pows(nT);
-    rhop_pows[0] = fr_u32(1);
-    for (uint32_t j = 1; j < nT; j++) rhop_pows[j] = fmul(rhop_pows[j - 1], rhop);
-    std::set<uint32_t> domains;
-    for (const auto& t : ts) domains.insert(t.domain);
-    for (uint32_t G : domains) {
+    // openings, one per generator domain in ascending order
+    const std::vector<Fr8> mix = powers(draw(st), ts.size());
+    std::map<uint32_t, std::vector<size_t>> by_domain;
+    for (size_t j = 0; j < ts.size(); j++) by_domain[ts[j].domain].push_back(j);
+    const bool selfcheck = getenv("ZKOB_BATCH_SELFCHECK") != nullptr;
+    for (const auto& [G, members] : by_domain) {
         const uint32_t logG = ceil_log2(G);
         Tensor acc;
-        for (uint32_t j = 0; j < nT; j++) {
-            if (ts[j].domain != G) continue;
-            const Fr8 coef = fmul(rhop_pows[j], kappa(ts[j].vars, r));
-            Tensor w, rf, nxt;
-            if (resident) {
-                std::swap(w.t, Wt[j].t);
-            } else {
-                load_witness(witpath[j], (uint64_t)ts[j].n_rows * G, w);
-            }
+        std::vector<const Opened*> group;
+        std::vector<Fr8> coefs;
+        for (size_t j : members) {
+            Opened& t = ts[j];
+            const Fr8 coef = fmul(mix[j], t.kappa);
+            Tensor w, bound, next;
+            if (keep)
+                std::swap(w.t, t.W.t);
+            else
+                upload_witness(t.witness, 1ull << t.nv, w);
             const zkh_tensor* row = w.t;
-            if (ts[j].vars > logG) {
-                std::vector<uint32_t> urow;
-                for (uint32_t v = logG; v < ts[j].vars; v++) urow.insert(urow.end(), r[v].v, r[v].v + 8);
-                chk(zkh_partial_me_window(g_ctx, w.t, urow.data(), ts[j].vars - logG, G, &rf.t), "row fold");
-                row = rf.t;
+            if (t.nv > logG) {  // bind the rows by r[logG..nv)
+                const std::vector<uint32_t> ur = words(r, logG, t.nv);
+                chk(zkh_partial_me_window(g_ctx, w.t, ur.data(), t.nv - logG, G, &bound.t), "row binding");
+                row = bound.t;
             }
-            if (!acc.t) {
-                chk(zkh_axpy(g_ctx, row, fsub(coef, fr_u32(1)).v, row, &nxt.t), "group RLC");
-            } else {
-                chk(zkh_axpy(g_ctx, acc.t, coef.v, row, &nxt.t), "group RLC");
-            }
-            std::swap(acc.t, nxt.t);
+            if (acc.t)
+                chk(zkh_axpy(g_ctx, acc.t, coef.v, row, &next.t), "combination");
+            else
+                chk(zkh_axpy(g_ctx, row, fsub(coef, fr_u32(1)).v, row, &next.t), "combination");
+            std::swap(acc.t, next.t);
+            group.push_back(&t);
+            coefs.push_back(coef);
         }
-        auto git = genpaths.find(G);
-        if (git == genpaths.end()) throw Err(1, "batch_prove: no generator file for domain " + std::to_string(G));
-        std::vector<uint32_t> gen = load_points(git->second);
-        if (gen.size() / 36 != G) throw Err(1, "batch_prove: generator size mismatch for domain " + std::to_string(G));
-        Points g;
+        auto g = gens.find(G);
+        if (g == gens.end()) throw Err(1, "batch_prove: no generator file for domain " + std::to_string(G));
+        const std::vector<uint32_t> pts = load_points(g->second);
+        if (pts.size() != (size_t)G * 36)
+            throw Err(1, "batch_prove: " + g->second + " does not hold " + std::to_string(G) + " generators");
+        Points gen;
+        chk(zkh_g1_from_host(g_ctx, pts.data(), G, &gen.g), "generators");
+        if (selfcheck) selfcheck_domain(gen, acc.t, group, coefs, r);
         Tensor b;
-        chk(zkh_g1_from_host(g_ctx, gen.data(), G, &g.g), "gen");
-        std::vector<uint32_t> ucol;
-        for (uint32_t v = 0; v < logG; v++) ucol.insert(ucol.end(), r[v].v, r[v].v + 8);
-        chk(zkh_eq_table(g_ctx, ucol.data(), logG, &b.t), "me_weights");
-        ipa_file(accdir + "/ipa_batch_" + std::to_string(G) + ".bin", st, acc.t, b.t, g.g, q.data());
+        const std::vector<uint32_t> uc = words(r, 0, logG);
+        chk(zkh_eq_table(g_ctx, uc.data(), logG, &b.t), "column weights");
+        ipa_file(accdir + "/ipa_batch_" + std::to_string(G) + ".bin", st, acc.t, b.t, gen.g, Q.data());
     }
-    T.lap("ipa");
-    printf("PROVED opening_batch (%u claims, %u tensors, %zu domains) -> %s\n", ncl, nT, domains.size(),
-           accdir.c_str());
+    sw.lap("ipa");
+    printf("PROVED opening_batch (%zu claims, %zu tensors, %zu domains) -> %s\n", cs.size(), ts.size(),
+           by_domain.size(), accdir.c_str());
     return 0;
 }
 
@@ -376,10 +435,7 @@ int run1(const std::vector<std::string>& args) {
     const std::string mode = args.empty() ? "" : args[0];
     std::vector<std::string> rest(args.begin() + (args.empty() ? 0 : 1), args.end());
     reject_flags(rest, "zkh_batchopen");
-    if (mode == "prove" && rest.size() >= 3) {
-        need_ctx();
-        return do_prove(rest);
-    }
+    if (mode == "prove" && rest.size() >= 3) return prove(rest);
     fprintf(stderr, "usage: zkh_batchopen prove <accdir> <run_seed> <q.bin> <G>=<gen.bin> ... | serve\n");
     return 2;
 }
