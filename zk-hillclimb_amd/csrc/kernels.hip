@@ -1448,19 +1448,22 @@ ZDEV void find_desc(const D* __restrict__ d, uint32_t nd, D& out) {
 __global__ __launch_bounds__(NT) void k_eq_mont_multi(const EqTabDesc* __restrict__ d, uint32_t nd) {
     EqTabDesc q;
     find_desc(d, nd, q);
-    __shared__ fr_t tlo[128], thi[128];
+    __shared__ fr_t tlo[128], thi[128], fs[28];
     const uint32_t K = q.K;
     const uint32_t klo = K < 7 ? K : 7, khi = K - klo;
     const uint32_t t = threadIdx.x;
     if (khi <= 7) {
+        // the 2K factors into LDS with one load per thread, so that the product chains
+        // below wait on LDS instead of on a dependent global load per factor
+        if (t < 2 * K) fs[t] = ld_aos(q.fac, t);
+        __syncthreads();
         if (t < (1u << klo)) {
             fr_t e = one_m();
-            for (uint32_t i = 0; i < klo; i++) e = mont_mul(e, ld_aos(q.fac, 2 * i + ((t >> i) & 1)));
+            for (uint32_t i = 0; i < klo; i++) e = mont_mul(e, fs[2 * i + ((t >> i) & 1)]);
             tlo[t] = e;
         } else if (t >= 128 && t - 128 < (1u << khi)) {
             fr_t e = one_m();
-            for (uint32_t i = 0; i < khi; i++)
-                e = mont_mul(e, ld_aos(q.fac, 2 * (klo + i) + (((t - 128) >> i) & 1)));
+            for (uint32_t i = 0; i < khi; i++) e = mont_mul(e, fs[2 * (klo + i) + (((t - 128) >> i) & 1)]);
             thi[t - 128] = e;
         }
     }

@@ -100,13 +100,15 @@ struct HostPool {
         for (auto& t : th) t.join();
     }
 };
-// host threads for the per-job work of a batch (ZKH_HOST_THREADS, default 1: extra
-// threads save ~5% of a TinyLlama matmul step but every spinning thread is exposed to
-// preemption on a shared host, which showed as multi-millisecond stalls)
+// host threads for the per-job work of a batch (ZKH_HOST_THREADS, default 4: with one
+// thread the jobs of a TinyLlama layer wait on each other's transcript work at every round
+// trip, 0.204 against 0.181 ms per matmul step with 4).  The persistent round loops hand
+// each ready message to whichever thread is free, so a thread that the OS preempts delays
+// only the message it is serving.
 static int host_threads() {
     static const int n = [] {
         const char* e = getenv("ZKH_HOST_THREADS");
-        int v = e ? atoi(e) : 1;
+        int v = e ? atoi(e) : 4;
         return v < 1 ? 1 : v > 16 ? 16 : v;
     }();
     return n;
@@ -1862,118 +1864,128 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         const bool tracing = trace_on();
         std::vector<std::vector<uint64_t>> tr_gpu(tracing ? nj : 0);
         std::vector<std::vector<double>> tr_host(tracing ? nj : 0);
+        // Any worker serves any job whose message is complete: a job is taken with a
+        // try-lock, so a worker that the OS preempts holds up at most the message it is
+        // serving, and the others keep every other job moving.
+        std::vector<uint32_t> rnd(nj, 0), msg(nj, 0);  // local rounds done, messages answered
+        std::vector<uint8_t> fin(nj, 0);
+        std::unique_ptr<std::atomic<uint8_t>[]> busy(new std::atomic<uint8_t>[nj]);
+        for (uint32_t j = 0; j < nj; j++) busy[j].store(0, std::memory_order_relaxed);
+        std::atomic<uint32_t> open_jobs{nj};
+        // serve job j's pending message if complete (caller holds busy[j]); false if not ready
+        auto serve = [&](uint32_t j, std::vector<Fr>& ta, std::vector<Fr>& tb) -> bool {
+            const uint32_t nb = 1u << lgnb[j];
+            const uint32_t* sl = ps + slot_off[j];
+            const uint32_t nw = msg_words(j, rnd[j]);
+            if (!ready(j, msg[j] + 1, nw)) return false;
+            if (tracing) tr_host[j].push_back(now_us());
+            // a block has run, so every earlier launch (the claim partials) has completed
+            if (msg[j] == 0) absorb_claim(j);
+            const uint32_t r = rnd[j];
+            auto stop_job = [&]() {
+                send_cmd(j, ZKH_QUIT, nullptr, 0);
+                fin[j] = 1;
+                open_jobs.fetch_sub(1, std::memory_order_acq_rel);
+            };
+            if (nw == ZKH_MSG_PAIR) {  // rounds r and r + 1
+                Fr sm[9];
+                for (int k = 0; k < 9; k++) sm[k] = kZero;
+                for (uint32_t b = 0; b < nb; b++)
+                    for (int k = 0; k < 9; k++) sm[k] = fr_add(sm[k], slot_fr(sl + b * ZKH_PSLOT, k));
+                // (the sums carry 2^-256; fix1 removes it from the combinations)
+                bool ok = round_step(j, r, fix1(fr_add(sm[0], sm[3])), fix1(fr_add(sm[1], sm[4])),
+                                     fix1(fr_add(sm[2], sm[5])));
+                const Fr x0m = J[j].xm;
+                if (ok) {
+                    // round r + 1's sum k at x: A + x (B + x C) with A = sm[3k],
+                    // C = sm[3k + 2] and B = sm[3k + 1] - A - C
+                    Fr nx[3];
+                    for (int k = 0; k < 3; k++) {
+                        const Fr A = sm[3 * k], C = sm[3 * k + 2];
+                        const Fr Bc = fr_sub(fr_sub(sm[3 * k + 1], A), C);
+                        nx[k] = fix1(fr_add(A, fr_mont_mul(x0m, fr_add(Bc, fr_mont_mul(x0m, C)))));
+                    }
+                    ok = round_step(j, r + 1, nx[0], nx[1], nx[2]);
+                }
+                if (!ok) {
+                    stop_job();
+                    return true;
+                }
+                // fold weights in Montgomery form from x0 R, x1 R: (1 - x) R = R - x R
+                const Fr x1m = J[j].xm;
+                const Fr u0m = fr_sub(fr_one_m(), x0m), u1m = fr_sub(fr_one_m(), x1m);
+                const Fr w[4] = {fr_mont_mul(u0m, u1m), fr_mont_mul(x0m, u1m), fr_mont_mul(u0m, x1m),
+                                 fr_mont_mul(x0m, x1m)};
+                uint32_t cw[32];
+                for (int k = 0; k < 4; k++) fr_store(w[k], cw + 8 * k);
+                rnd[j] += 2;
+                msg[j]++;
+                send_cmd(j, msg[j], cw, 32);
+                if (tracing) tr_host[j].push_back(now_us());
+                return true;
+            }
+            if (nw == ZKH_MSG_ONE) {
+                Fr s3[3] = {kZero, kZero, kZero};
+                for (uint32_t b = 0; b < nb; b++)
+                    for (int k = 0; k < 3; k++) s3[k] = fr_add(s3[k], slot_fr(sl + b * ZKH_PSLOT, k));
+                if (!round_step(j, r, fix1(s3[0]), fix1(s3[1]), fix1(s3[2]))) {
+                    stop_job();
+                    return true;
+                }
+                uint32_t xm[8];
+                fr_store(J[j].xm, xm);
+                rnd[j]++;
+                msg[j]++;
+                send_cmd(j, msg[j], xm, 8);
+                if (tracing) tr_host[j].push_back(now_us());
+                return true;
+            }
+            if (tracing) {  // block 0's per-message clock stamps are complete once it has exited
+                for (uint32_t m2 = 1; m2 <= msg[j] + 1 && m2 < 14; m2++) {
+                    const uint32_t* st = sl + ZKH_PSTAMP;
+                    tr_gpu[j].push_back(st[4 + 2 * m2] - st[3 + 2 * m2]);
+                    tr_gpu[j].push_back(m2 <= msg[j] ? st[5 + 2 * m2] - st[4 + 2 * m2] : 0);
+                }
+            }
+            // the blocks' folded entries: the remaining lgnb rounds on the host
+            ta.resize(nb);
+            tb.resize(nb);
+            for (uint32_t b = 0; b < nb; b++) {
+                ta[b] = slot_fr(sl + b * ZKH_PSLOT, 0);
+                tb[b] = slot_fr(sl + b * ZKH_PSLOT, 1);
+            }
+            bool ok = true;
+            for (uint32_t rr = R[j], m = nb; m > 1 && ok; rr++, m >>= 1) {
+                const uint32_t h = m >> 1;
+                Fr c0 = kZero, q1 = kZero, c2 = kZero;  // each x 2^-256
+                for (uint32_t i = 0; i < h; i++) {
+                    c0 = fr_add(c0, fr_mont_mul(ta[i], tb[i]));
+                    q1 = fr_add(q1, fr_mont_mul(ta[i + h], tb[i + h]));
+                    c2 = fr_add(c2, fr_mont_mul(fr_sub(ta[i + h], ta[i]), fr_sub(tb[i + h], tb[i])));
+                }
+                ok = round_step(j, rr, fix1(c0), fix1(q1), fix1(c2));
+                const Fr xm = J[j].xm;
+                for (uint32_t i = 0; ok && i < h; i++) {
+                    ta[i] = fr_add(ta[i], fr_mont_mul(xm, fr_sub(ta[i + h], ta[i])));
+                    tb[i] = fr_add(tb[i], fr_mont_mul(xm, fr_sub(tb[i + h], tb[i])));
+                }
+            }
+            if (ok) finish(j, ta[0], tb[0]);
+            fin[j] = 1;
+            open_jobs.fetch_sub(1, std::memory_order_acq_rel);
+            return true;
+        };
         auto worker = [&](int t) {
-            std::vector<uint32_t> mine;
-            for (uint32_t j = (uint32_t)t; j < nj; j += (uint32_t)T) mine.push_back(j);
-            std::vector<uint32_t> rnd(mine.size(), 0), msg(mine.size(), 0);  // local rounds, messages
-            std::vector<uint8_t> done(mine.size(), 0);
-            size_t left = mine.size();
             std::vector<Fr> ta, tb;
             double t_prog = now_us();
-            for (uint64_t spins = 1; left; spins++) {
+            for (uint64_t spins = 1; open_jobs.load(std::memory_order_acquire); spins++) {
                 bool prog = false;
-                for (size_t a = 0; a < mine.size(); a++) {
-                    if (done[a]) continue;
-                    const uint32_t j = mine[a];
-                    const uint32_t nb = 1u << lgnb[j];
-                    const uint32_t* sl = ps + slot_off[j];
-                    const uint32_t nw = msg_words(j, rnd[a]);
-                    if (!ready(j, msg[a] + 1, nw)) continue;
-                    prog = true;
-                    if (tracing) tr_host[j].push_back(now_us());
-                    // a block has run, so every earlier launch (the claim partials) has completed
-                    if (msg[a] == 0) absorb_claim(j);
-                    const uint32_t r = rnd[a];
-                    if (nw == ZKH_MSG_PAIR) {  // rounds r and r + 1
-                        Fr sm[9];
-                        for (int k = 0; k < 9; k++) sm[k] = kZero;
-                        for (uint32_t b = 0; b < nb; b++)
-                            for (int k = 0; k < 9; k++) sm[k] = fr_add(sm[k], slot_fr(sl + b * ZKH_PSLOT, k));
-                        // (the sums carry 2^-256; fix1 removes it from the combinations)
-                        bool ok = round_step(j, r, fix1(fr_add(sm[0], sm[3])), fix1(fr_add(sm[1], sm[4])),
-                                             fix1(fr_add(sm[2], sm[5])));
-                        const Fr x0m = J[j].xm;
-                        if (ok) {
-                            // round r + 1's sum k at x: A + x (B + x C) with A = sm[3k],
-                            // C = sm[3k + 2] and B = sm[3k + 1] - A - C
-                            Fr nx[3];
-                            for (int k = 0; k < 3; k++) {
-                                const Fr A = sm[3 * k], C = sm[3 * k + 2];
-                                const Fr Bc = fr_sub(fr_sub(sm[3 * k + 1], A), C);
-                                nx[k] = fix1(fr_add(A, fr_mont_mul(x0m, fr_add(Bc, fr_mont_mul(x0m, C)))));
-                            }
-                            ok = round_step(j, r + 1, nx[0], nx[1], nx[2]);
-                        }
-                        if (!ok) {
-                            send_cmd(j, ZKH_QUIT, nullptr, 0);
-                            done[a] = 1;
-                            left--;
-                            continue;
-                        }
-                        // fold weights in Montgomery form from x0 R, x1 R: (1 - x) R = R - x R
-                        const Fr x1m = J[j].xm;
-                        const Fr u0m = fr_sub(fr_one_m(), x0m), u1m = fr_sub(fr_one_m(), x1m);
-                        const Fr w[4] = {fr_mont_mul(u0m, u1m), fr_mont_mul(x0m, u1m), fr_mont_mul(u0m, x1m),
-                                         fr_mont_mul(x0m, x1m)};
-                        uint32_t cw[32];
-                        for (int k = 0; k < 4; k++) fr_store(w[k], cw + 8 * k);
-                        rnd[a] += 2;
-                        msg[a]++;
-                        send_cmd(j, msg[a], cw, 32);
-                        if (tracing) tr_host[j].push_back(now_us());
+                for (uint32_t k = 0; k < nj; k++) {
+                    const uint32_t j = (k + (uint32_t)t) % nj;  // each worker starts at its own job
+                    if (busy[j].load(std::memory_order_relaxed) || busy[j].exchange(1, std::memory_order_acquire))
                         continue;
-                    }
-                    if (nw == ZKH_MSG_ONE) {
-                        Fr s3[3] = {kZero, kZero, kZero};
-                        for (uint32_t b = 0; b < nb; b++)
-                            for (int k = 0; k < 3; k++) s3[k] = fr_add(s3[k], slot_fr(sl + b * ZKH_PSLOT, k));
-                        if (!round_step(j, r, fix1(s3[0]), fix1(s3[1]), fix1(s3[2]))) {
-                            send_cmd(j, ZKH_QUIT, nullptr, 0);
-                            done[a] = 1;
-                            left--;
-                            continue;
-                        }
-                        uint32_t xm[8];
-                        fr_store(J[j].xm, xm);
-                        rnd[a]++;
-                        msg[a]++;
-                        send_cmd(j, msg[a], xm, 8);
-                        if (tracing) tr_host[j].push_back(now_us());
-                        continue;
-                    }
-                    if (tracing) {  // block 0's per-message clock stamps are complete once it has exited
-                        for (uint32_t m2 = 1; m2 <= msg[a] + 1 && m2 < 14; m2++) {
-                            const uint32_t* st = sl + ZKH_PSTAMP;
-                            tr_gpu[j].push_back(st[4 + 2 * m2] - st[3 + 2 * m2]);
-                            tr_gpu[j].push_back(m2 <= msg[a] ? st[5 + 2 * m2] - st[4 + 2 * m2] : 0);
-                        }
-                    }
-                    // the blocks' folded entries: the remaining lgnb rounds on the host
-                    ta.resize(nb);
-                    tb.resize(nb);
-                    for (uint32_t b = 0; b < nb; b++) {
-                        ta[b] = slot_fr(sl + b * ZKH_PSLOT, 0);
-                        tb[b] = slot_fr(sl + b * ZKH_PSLOT, 1);
-                    }
-                    done[a] = 1;
-                    left--;
-                    bool ok = true;
-                    for (uint32_t r = R[j], m = nb; m > 1 && ok; r++, m >>= 1) {
-                        const uint32_t h = m >> 1;
-                        Fr c0 = kZero, q1 = kZero, c2 = kZero;  // each x 2^-256
-                        for (uint32_t i = 0; i < h; i++) {
-                            c0 = fr_add(c0, fr_mont_mul(ta[i], tb[i]));
-                            q1 = fr_add(q1, fr_mont_mul(ta[i + h], tb[i + h]));
-                            c2 = fr_add(c2, fr_mont_mul(fr_sub(ta[i + h], ta[i]), fr_sub(tb[i + h], tb[i])));
-                        }
-                        ok = round_step(j, r, fix1(c0), fix1(q1), fix1(c2));
-                        const Fr xm = J[j].xm;
-                        for (uint32_t i = 0; ok && i < h; i++) {
-                            ta[i] = fr_add(ta[i], fr_mont_mul(xm, fr_sub(ta[i + h], ta[i])));
-                            tb[i] = fr_add(tb[i], fr_mont_mul(xm, fr_sub(tb[i + h], tb[i])));
-                        }
-                    }
-                    if (ok) finish(j, ta[0], tb[0]);
+                    if (!fin[j] && serve(j, ta, tb)) prog = true;
+                    busy[j].store(0, std::memory_order_release);
                 }
                 if (prog) {
                     t_prog = now_us();
@@ -1991,8 +2003,11 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                         why = 2;
                     } else if (e == hipSuccess) {  // the kernel has ended: whatever is missing never comes
                         bool all = true;
-                        for (size_t a = 0; a < mine.size(); a++)
-                            all = all && (done[a] || ready(mine[a], msg[a] + 1, msg_words(mine[a], rnd[a])));
+                        for (uint32_t j = 0; j < nj; j++) {
+                            if (busy[j].exchange(1, std::memory_order_acquire)) continue;  // being served
+                            all = all && (fin[j] || ready(j, msg[j] + 1, msg_words(j, rnd[j])));
+                            busy[j].store(0, std::memory_order_release);
+                        }
                         if (!all) why = 4;
                     } else if (now_us() - t_prog > 30e6) {
                         why = 3;
