@@ -1124,10 +1124,19 @@ ZDEV void reduce_publish_lds(const LdsAcc<K>& acc, const Publish& P, uint32_t jo
         }
     }
 }
+// the challenge of a relayed launch: false when the relay says the proof was abandoned
+ZDEV bool relayed_vm(const uint32_t* vmp, fr_t& vm) {
+    if (!vmp) return true;
+    if (vmp[8]) return false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) vm.v[i] = vmp[i];
+    return true;
+}
 // phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
 // acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
 __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, int fold, fr_t vm,
-                                                  fr_t beta, EqDev eq, Publish pub) {
+                                                  const uint32_t* vmp, fr_t beta, EqDev eq, Publish pub) {
+    if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
     __shared__ uint4 accl[5 * NT], acch[5 * NT];
     LdsAcc<5> acc{accl, acch};
@@ -1163,12 +1172,12 @@ __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n
     reduce_publish_lds<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
-                          const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
+                          const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
                           Publish partial) {
     const uint32_t g = grid_for(n >> 1, NT, 1024);
-    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
+    fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
-    k_lu_phase1<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, fold, vm, to_fr(beta_host), e, partial);
+    k_lu_phase1<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, fold, vm, vmp, to_fr(beta_host), e, partial);
     return g;
 }
 
@@ -1260,24 +1269,26 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
 }
 template <int fold_as, int fold_btm>
 __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m, uint32_t n,
-                                                  fr_t vm, fr_t beta, EqDev eq, Publish pub, uint32_t ga, uint32_t gb) {
+                                                  fr_t vm, const uint32_t* vmp, fr_t beta, EqDev eq, Publish pub,
+                                                  uint32_t ga, uint32_t gb) {
+    if (!relayed_vm(vmp, vm)) return;
     __shared__ uint4 accl[6 * NT], acch[6 * NT];
     if (blockIdx.x < ga) lu_phase2_as<fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, ga, accl, acch);
     else lu_phase2_btm<fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - ga, gb, ga, accl, acch);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
-                          int fold_btm, const uint32_t* v_m_host, const uint32_t* beta_host,
+                          int fold_btm, const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host,
                           EqW eq, Publish partial) {
     const uint32_t ga = grid_for(n >> 1, NT, LU2_GRID * 2 / 5), gb = grid_for(n >> 1, NT, LU2_GRID * 3 / 5);
-    const fr_t vm = (fold_as || fold_btm) ? to_fr(v_m_host) : fr_t{};
+    const fr_t vm = (fold_as || fold_btm) && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
     const fr_t beta = to_fr(beta_host);
     const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T), md = tab_dev(m);
     const uint32_t g = ga + gb;
-    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
-    else if (fold_as) k_lu_phase2<1, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
-    else if (fold_btm) k_lu_phase2<0, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
-    else k_lu_phase2<0, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, beta, e, partial, ga, gb);
+    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
+    else if (fold_as) k_lu_phase2<1, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
+    else if (fold_btm) k_lu_phase2<0, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
+    else k_lu_phase2<0, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
     return g;
 }
 
@@ -1285,7 +1296,8 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
 // Hadamard sumcheck rounds (zkob_lookup.cuh:212-233 k_hp3_step + k_fr_fold, fused)
 // ------------------------------------------------------------------------------------
 __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, uint32_t n, int fold,
-                                                 fr_t vm, Publish pub) {
+                                                 fr_t vm, const uint32_t* vmp, Publish pub) {
+    if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
     __shared__ uint4 accl[4 * NT], acch[4 * NT];
     LdsAcc<4> acc{accl, acch};
@@ -1322,17 +1334,18 @@ __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, u
     reduce_publish_lds<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fold,
-                         const uint32_t* v_m_host, Publish partial) {
+                         const uint32_t* v_m_host, const uint32_t* vmp, Publish partial) {
     uint32_t g = grid_for(n >> 1, NT * 2, 1024);
-    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
-    k_hp_round<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, partial);
+    fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
+    k_hp_round<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, vmp, partial);
     return g;
 }
 // eq-specialised: sums_t = sum_i eq(i, u[0..K)) S_t[i] U_t[i]  (x 2^-256)
 // Montgomery products issue in independent pairs between scheduling barriers: two
 // chains per wave at <= 128 registers (four waves per SIMD) keep the VALU busy.
 __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
-                                                    EqDev eq, Publish pub) {
+                                                    const uint32_t* vmp, EqDev eq, Publish pub) {
+    if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
     __shared__ uint4 accl[4 * NT], acch[4 * NT];
     LdsAcc<4> acc{accl, acch};
@@ -1377,11 +1390,11 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
     reduce_publish_lds<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, EqW eq, Publish partial) {
+                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial) {
     const uint32_t g = grid_for(n >> 1, NT, 1024);
-    fr_t vm = fold ? to_fr(v_m_host) : fr_t{};
+    fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
-    k_hp_eq_round<<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, e, partial);
+    k_hp_eq_round<<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, vmp, e, partial);
     return g;
 }
 // sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n, by chunks of 1024 indices sharing their
@@ -2043,6 +2056,26 @@ ZDEV void persist_publish(uint32_t* slot, const uint32_t* pub, uint32_t nw, uint
         const uint32_t b = 3 * lane;
         st_quad_sys(slot + 4 * lane, make_uint4(seq, pub[b], b + 1 < nw ? pub[b + 1] : 0u, b + 2 < nw ? pub[b + 2] : 0u));
     }
+}
+// the relay between two round launches (launch_relay)
+__global__ __launch_bounds__(64) void k_relay(const uint32_t* cmd, uint32_t want, uint32_t* err,
+                                              unsigned long long deadline, uint32_t* vmp) {
+    uint4 qd;
+    const bool ok = persist_wait(cmd, 3, want, err, deadline, qd);
+    __shared__ uint32_t w[9];
+    const uint32_t lane = threadIdx.x;
+    if (lane < 3) {
+        w[3 * lane] = qd.y;
+        w[3 * lane + 1] = qd.z;
+        w[3 * lane + 2] = qd.w;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < 8) vmp[lane] = ok ? w[lane] : 0u;
+    if (lane == 8) vmp[8] = ok ? 0u : 1u;
+}
+void launch_relay(hipStream_t s, const uint32_t* cmd, uint32_t want, uint32_t* err, unsigned long long deadline,
+                  uint32_t* vmp) {
+    k_relay<<<1, 64, 0, s>>>(cmd, want, err, deadline, vmp);
 }
 #define NTP 1024  // threads of a persistent round block (16 waves)
 static_assert(2 * ZKH_PLS_MAX <= NTP, "the double fold takes one product per thread");

@@ -172,24 +172,28 @@ void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, ui
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
                       const uint32_t* inv_total_host);
+// Round kernels take the previous round's challenge (Montgomery form) either from the host
+// at launch (v_m_host) or, when vmp is given, from device words vmp[0..8) written by a relay
+// (launch_relay) that runs between the previous round and this one; vmp[8] != 0 makes the
+// kernel return at once (the host abandoned the proof).
 // phase-1 round over A, S (size n): sums e*a0*s0, e*a1*s1, e*da*ds (x 2^-256), a0, a1
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
-                          const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
+                          const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
                           Publish pub);
 // phase-2 round over A, S, B, T, m as two launches publishing jobs 0 (A, S: 5 sums) and
 // 1 (B, T, m: 6 sums) of `pub` (made for 2 jobs; see kernels.hip)
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
                           int fold_as, int fold_btm,
-                          const uint32_t* v_m_host, const uint32_t* beta_host, EqW eq,
+                          const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
                           Publish pub);
 
 // ---- Hadamard ----
 // generic: sums_t = sum E_t*S_t*U_t, t = 0..3 (x 2^-512)
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
-                         int fold, const uint32_t* v_m_host, Publish pub);
+                         int fold, const uint32_t* v_m_host, const uint32_t* vmp, Publish pub);
 // eq-specialised: sums_t = sum eq(i,u_)*S_t*U_t, t = 0..3 (x 2^-256)
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, EqW eq, Publish pub);
+                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub);
 // sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish pub);
@@ -373,6 +377,11 @@ struct LuPersist {
 };
 #define ZKH_LU_MSG 88
 hipError_t launch_lu_persist(hipStream_t s, const LuPersist& p);
+// One wave that waits (as a persistent block waits for its command) until the three quads
+// at cmd carry seq `want`, then writes their eight data words to vmp[0..8) and 0 to vmp[8];
+// on ZKH_QUIT or past `deadline` (100 MHz ticks; then *err = 1) it writes 1 to vmp[8].
+void launch_relay(hipStream_t s, const uint32_t* cmd, uint32_t want, uint32_t* err, unsigned long long deadline,
+                  uint32_t* vmp);
 // at most 16 blocks of ZKH_PLS_MAX entries; returns the HIP status of the launch
 hipError_t launch_hp_persist(hipStream_t s, const HpPersist& p);
 

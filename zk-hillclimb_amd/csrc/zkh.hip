@@ -182,6 +182,11 @@ struct zkh_ctx {
     size_t pub_part_cap = (size_t)4096 * 11;
     uint32_t* pub_cnt = nullptr;   // device [ZKH_MAX_BATCH + 1]
     uint32_t pub_seq = 0;
+    // relayed round launches: coherent pinned command (three quads; word 16: a relay's
+    // timeout flag) and the device words the relay fills (challenge, abandon flag)
+    uint32_t* relay_host = nullptr;
+    uint32_t* relay_vm = nullptr;
+    uint32_t relay_seq = 0;
     // persistent round loops: coherent pinned block slots / command areas, clock rate
     uint32_t* ps_host = nullptr;
     size_t ps_words = 0;
@@ -466,6 +471,40 @@ static void pub_read(zkh_ctx* c, uint32_t j, int K, Fr* out) {
     for (int k = 0; k < K; k++) out[k] = fr_load(c->pub_host + ((size_t)j * K + k) * 8);
 }
 
+// ---- relayed round launches.  A round kernel can be queued before the host has the
+// previous round's challenge: a relay (one wave, launch_relay) ahead of it on the stream
+// waits for the challenge in the pinned command and copies it to device words that the
+// kernel reads, so the kernel's launch overlaps the previous round and the host's
+// transcript work.  At most one relay is outstanding per context. ----
+static uint32_t relay_enqueue(zkh_ctx* c) {
+    uint32_t seq = ++c->relay_seq;
+    if (seq == 0 || seq == ZKH_QUIT) seq = c->relay_seq = 1;
+    launch_relay(c->stream, c->relay_host, seq, c->relay_host + 16, c->clock_khz * 1000 * 20, c->relay_vm);
+    return seq;
+}
+// hand the challenge (Montgomery form) to the relay waiting for seq
+static void relay_send(zkh_ctx* c, uint32_t seq, const uint32_t vm[8]) {
+    uint32_t* cmd = c->relay_host;
+    for (uint32_t i = 0; i < 8; i++) __atomic_store_n(cmd + zkh_quad_word(i), vm[i], __ATOMIC_RELAXED);
+    for (uint32_t q = 0; q < 3; q++) __atomic_store_n(cmd + 4 * q, seq, __ATOMIC_RELEASE);
+}
+// release a waiting relay without a challenge: it flags its kernel to return at once; the
+// stream drains before the command is cleared for the next relay
+static void relay_quit(zkh_ctx* c) {
+    uint32_t* cmd = c->relay_host;
+    for (uint32_t q = 0; q < 3; q++) __atomic_store_n(cmd + 4 * q, ZKH_QUIT, __ATOMIC_RELEASE);
+    (void)hipStreamSynchronize(c->stream);
+    for (uint32_t q = 0; q < 3; q++) __atomic_store_n(cmd + 4 * q, 0u, __ATOMIC_RELEASE);
+}
+// releases the outstanding relay of a round loop that returns early
+struct RelayGuard {
+    zkh_ctx* c;
+    uint32_t pending = 0;
+    ~RelayGuard() {
+        if (pending) relay_quit(c);
+    }
+};
+
 // small host -> device upload through the pinned ring (asynchronous; ordered on the stream)
 static int upload(zkh_ctx* c, void* dst, const void* src, size_t bytes) {
     size_t need = (bytes + 255) & ~(size_t)255;
@@ -622,12 +661,15 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
     if (hipHostMalloc((void**)&c->pub_host, (ZKH_MAX_BATCH * 11 * 8 + 64) * 4, hipHostMallocCoherent) != hipSuccess ||
         hipMalloc((void**)&c->pub_part, (size_t)4096 * 11 * 32) != hipSuccess ||
         hipMalloc((void**)&c->pub_cnt, (ZKH_MAX_BATCH + 1) * 4) != hipSuccess ||
-        hipMemset(c->pub_cnt, 0, (ZKH_MAX_BATCH + 1) * 4) != hipSuccess) {
+        hipMemset(c->pub_cnt, 0, (ZKH_MAX_BATCH + 1) * 4) != hipSuccess ||
+        hipHostMalloc((void**)&c->relay_host, 64 * 4, hipHostMallocCoherent) != hipSuccess ||
+        hipMalloc((void**)&c->relay_vm, 16 * 4) != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
         delete c;
         return ZKH_EDEV;
     }
     memset(c->pub_host, 0, (ZKH_MAX_BATCH * 11 * 8 + 64) * 4);
+    memset(c->relay_host, 0, 64 * 4);
     int khz = 0;
     if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device) == hipSuccess && khz > 0)
         c->clock_khz = (uint64_t)khz;
@@ -652,6 +694,8 @@ extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
     if (c->ps_host) (void)hipHostFree(c->ps_host);
     if (c->pub_part) (void)hipFree(c->pub_part);
     if (c->pub_cnt) (void)hipFree(c->pub_cnt);
+    if (c->relay_host) (void)hipHostFree(c->relay_host);
+    if (c->relay_vm) (void)hipFree(c->relay_vm);
     for (auto& p : c->pending) {
         c->pool.push_back(p.a);
         c->pool.push_back(p.b);
@@ -2563,53 +2607,35 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
     bool persisted = false;    // the last rounds ran in lu_persist_rounds
     Fr fin[5];
-    for (uint32_t r = 0; r < logD; r++) {
+    const bool no_persist = getenv("ZKH_NO_PERSIST") != nullptr;
+    auto persists = [&](uint32_t r) {  // phase 2 small enough for the persistent loop
         const uint32_t n = D >> r;
-        if (n <= N && n <= ZKH_LU_PERSIST_MAX && !getenv("ZKH_NO_PERSIST")) {  // phase 2: the rest in one launch
-            LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD};
-            const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
-            if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, beta_l, ev_out, ws_out, fin)))
-                return rc;
-            persisted = true;
-            break;
-        }
-        if (tracing) tr_t.push_back(now_us());
-        const uint32_t k = logD - r;  // remaining variables
-        const uint32_t K = k - 1;     // eq variables of the pairs
-        const Fr ul = u[k - 1];
-        const Fr corr = eq_corr(eq, K);
-        Fr coef[4];
+        return n <= N && n <= ZKH_LU_PERSIST_MAX && !no_persist;
+    };
+    // launches round r (reading the previous challenge from vm, or from the relay when vmp
+    // is given) and moves the table handles to the folded copies the launch writes
+    auto launch = [&](uint32_t r, const uint32_t* vmp) {
+        const uint32_t n = D >> r, K = logD - r - 1;
+        Publish pb;
         if (n > N) {  // phase 1
-            Tab ta{a_src, Aw}, ts{s_src, Sw};
-            Publish pb = make_pub(c, 1);
+            pb = make_pub(c, 1);
             {
                 ProfScope ps(c, "lu_phase1", (as_pending ? 3.0 * n : (double)n) * 2 * 32);
-                launch_lu_phase1(c->stream, ta, ts, n, as_pending, vm, beta_l, EqW{eq.elo_d, eq.ehi_d, K}, pb);
+                launch_lu_phase1(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, n, as_pending, vm, vmp, beta_l,
+                                 EqW{eq.elo_d, eq.ehi_d, K}, pb);
             }
             if (as_pending) {
                 a_src = Aw;
                 s_src = Sw;
             }
-            Fr s[5];
-            if ((rc = wait_pub(c, pb.seq))) return rc;
-            if (tracing) tr_t.push_back(now_us());
-            pub_read(c, 0, 5, s);
-            Fr q0 = fr_mul(fix1(s[0]), corr), q1 = fr_mul(fix1(s[1]), corr), q2 = fr_mul(fix1(s[2]), corr);
-            Fr qc1 = fr_sub(fr_sub(q1, q0), q2);
-            Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
-            Fr aq0 = fr_mul(alpha, q0), aq1 = fr_mul(alpha, qc1), aq2 = fr_mul(alpha, q2);
-            coef[0] = fr_add(fr_add(fr_mul(e0, aq0), s[3]), fr_mul(Cc, inv2));
-            coef[1] = fr_add(fr_add(fr_mul(e0, aq1), fr_mul(e1, aq0)), fr_sub(s[4], s[3]));
-            coef[2] = fr_add(fr_mul(e0, aq2), fr_mul(e1, aq1));
-            coef[3] = fr_mul(e1, aq2);
             as_pending = true;
         } else {  // phase 2
-            Tab ta{a_src, Aw}, ts{s_src, Sw}, tb{b_src, Bw}, tt{t_src, Tw}, tm{m_src, mw};
-            Publish pb = make_pub(c, 2);
+            pb = make_pub(c, 2);
             {
                 ProfScope ps(c, "lu_phase2",
                              ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
-                launch_lu_phase2(c->stream, ta, ts, tb, tt, tm, n, as_pending, btm_pending, vm, beta_l,
+                launch_lu_phase2(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
+                                 Tab{m_src, mw}, n, as_pending, btm_pending, vm, vmp, beta_l,
                                  EqW{eq.elo_d, eq.ehi_d, K}, pb);
             }
             if (as_pending) {
@@ -2621,9 +2647,53 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                 t_src = Tw;
                 m_src = mw;
             }
+            as_pending = true;
+            btm_pending = true;
+        }
+        return pb;
+    };
+    RelayGuard relay{c};
+    Publish pb{};
+    bool launched = false;  // round r is already queued
+    for (uint32_t r = 0; r < logD; r++) {
+        const uint32_t n = D >> r;
+        if (persists(r)) {  // phase 2: the rest in one launch
+            LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD};
+            const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
+            if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, beta_l, ev_out, ws_out, fin)))
+                return rc;
+            persisted = true;
+            break;
+        }
+        if (tracing) tr_t.push_back(now_us());
+        if (!launched) pb = launch(r, nullptr);
+        // round r + 1 goes behind a relay now, so that its launch overlaps this round
+        const bool relay_next = r + 1 < logD && !persists(r + 1);
+        Publish pb_next{};
+        if (relay_next) {
+            relay.pending = relay_enqueue(c);
+            pb_next = launch(r + 1, c->relay_vm);
+        }
+        const uint32_t k = logD - r;  // remaining variables
+        const uint32_t K = k - 1;     // eq variables of the pairs
+        const Fr ul = u[k - 1];
+        const Fr corr = eq_corr(eq, K);
+        Fr coef[4];
+        if ((rc = wait_pub(c, pb.seq))) return rc;
+        if (tracing) tr_t.push_back(now_us());
+        if (n > N) {  // phase 1
+            Fr s[5];
+            pub_read(c, 0, 5, s);
+            Fr q0 = fr_mul(fix1(s[0]), corr), q1 = fr_mul(fix1(s[1]), corr), q2 = fr_mul(fix1(s[2]), corr);
+            Fr qc1 = fr_sub(fr_sub(q1, q0), q2);
+            Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
+            Fr aq0 = fr_mul(alpha, q0), aq1 = fr_mul(alpha, qc1), aq2 = fr_mul(alpha, q2);
+            coef[0] = fr_add(fr_add(fr_mul(e0, aq0), s[3]), fr_mul(Cc, inv2));
+            coef[1] = fr_add(fr_add(fr_mul(e0, aq1), fr_mul(e1, aq0)), fr_sub(s[4], s[3]));
+            coef[2] = fr_add(fr_mul(e0, aq2), fr_mul(e1, aq1));
+            coef[3] = fr_mul(e1, aq2);
+        } else {  // phase 2
             Fr s[11], sa[5], sb[6];
-            if ((rc = wait_pub(c, pb.seq))) return rc;
-            if (tracing) tr_t.push_back(now_us());
             pub_read(c, 0, 5, sa);
             pub_read(c, 1, 6, sb);
             // s: w*a*s sums 0..2, w*b*t sums 3..5, sum a0 / a1 6..7, m*b sums 8..10
@@ -2649,8 +2719,6 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                              fr_mul(inv_ratio, Mc1));
             coef[2] = fr_sub(fr_add(fr_mul(e0, Q2), fr_mul(e1, Q1)), fr_mul(inv_ratio, M2));
             coef[3] = fr_mul(e1, Q2);
-            as_pending = true;
-            btm_pending = true;
         }
         Fr e[4] = {coef[0], fr_poly_eval(coef, 3, kOne), fr_poly_eval(coef, 3, fr_u64(2)),
                    fr_poly_eval(coef, 3, three)};
@@ -2670,6 +2738,12 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         if (n > N) Cc = fr_mul(Cc, inv2);
         else alpha_sq = fr_mul(alpha_sq, eqv);
         fr_store(fr_to_mont(v), vm);
+        if (relay_next) {
+            relay_send(c, relay.pending, vm);
+            relay.pending = 0;
+            pb = pb_next;
+        }
+        launched = relay_next;
         if (tracing) tr_t.push_back(now_us());
     }
     if (tracing) {  // per round: table size, launch -> sums seen, host work (us)
@@ -3275,10 +3349,36 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
     bool persisted = false;    // the last rounds ran in hp_persist_rounds
     Fr e_fin = kZero, s_fin = kZero, u_fin = kZero;
+    const bool no_persist = getenv("ZKH_NO_PERSIST") != nullptr;
+    auto persists = [&](uint32_t r) { return (n >> r) <= ZKH_HP_PERSIST_MAX && !no_persist; };
+    // launches round r (previous challenge from vm, or from the relay when vmp is given) and
+    // moves the table handles to the folded copies the launch writes
+    auto launch = [&](uint32_t r, const uint32_t* vmp) {
+        const uint32_t sz = n >> r;
+        const int fold = r > 0;
+        Publish pb = make_pub(c, 1);
+        if (!ueq) {
+            ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
+            launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp, pb);
+        } else {
+            ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
+            launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp,
+                               EqW{eq.elo_d, eq.ehi_d, k - r - 1}, pb);
+        }
+        if (fold) {
+            e_src = Ew;
+            s_src = Sw;
+            u_src = Uw;
+        }
+        return pb;
+    };
+    RelayGuard relay{c};
+    Publish pb{};
+    bool launched = false;  // round r is already queued
     for (uint32_t r = 0; r < k; r++) {
         const uint32_t sz = n >> r;
         const int fold = r > 0;
-        if (sz <= ZKH_HP_PERSIST_MAX && !getenv("ZKH_NO_PERSIST")) {  // the rest in one launch
+        if (persists(r)) {  // the rest in one launch
             if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, vm, claim, cE, ev_out,
                                         ws_out, e_fin, s_fin, u_fin)))
                 return rc;
@@ -3286,38 +3386,25 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             break;
         }
         if (tracing) tr_t.push_back(now_us());
-        Fr e[4];
+        if (!launched) pb = launch(r, nullptr);
+        // round r + 1 goes behind a relay now, so that its launch overlaps this round
+        const bool relay_next = r + 1 < k && !persists(r + 1);
+        Publish pb_next{};
+        if (relay_next) {
+            relay.pending = relay_enqueue(c);
+            pb_next = launch(r + 1, c->relay_vm);
+        }
+        Fr e[4], sums[4];
+        if ((rc = wait_pub(c, pb.seq))) return rc;
+        if (tracing) tr_t.push_back(now_us());
+        pub_read(c, 0, 4, sums);
         if (!ueq) {
-            Publish pb = make_pub(c, 1);
-            {
-                ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
-                launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, pb);
-            }
-            Fr s[4];
-            if ((rc = wait_pub(c, pb.seq))) return rc;
-            if (tracing) tr_t.push_back(now_us());
-            pub_read(c, 0, 4, s);
-            for (int t = 0; t < 4; t++) e[t] = fix2(s[t]);
+            for (int t = 0; t < 4; t++) e[t] = fix2(sums[t]);
         } else {
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
-            Publish pb = make_pub(c, 1);
-            {
-                ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
-                launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm,
-                                   EqW{eq.elo_d, eq.ehi_d, K}, pb);
-            }
-            Fr s[4];
-            if ((rc = wait_pub(c, pb.seq))) return rc;
-            if (tracing) tr_t.push_back(now_us());
-            pub_read(c, 0, 4, s);
             Fr f = fr_mul(cE, eq_corr(eq, K));
-            for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(fix1(s[t]), f), fr_eq2(ul, fr_u64(t)));
-        }
-        if (fold) {
-            e_src = Ew;
-            s_src = Sw;
-            u_src = Uw;
+            for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(fix1(sums[t]), f), fr_eq2(ul, fr_u64(t)));
         }
         if (!fr_eq(claim, fr_add(e[0], e[1])))
             return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r);
@@ -3330,6 +3417,12 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         claim = lagrange4(e, w);
         if (ueq) cE = fr_mul(cE, fr_eq2((*ueq)[k - r - 1], w));
         fr_store(fr_to_mont(w), vm);
+        if (relay_next) {
+            relay_send(c, relay.pending, vm);
+            relay.pending = 0;
+            pb = pb_next;
+        }
+        launched = relay_next;
         if (tracing) tr_t.push_back(now_us());
     }
     if (tracing) {  // per round: table size, launch -> sums seen, host work (us)
