@@ -28,7 +28,9 @@ TinyLlama-1.1B".
   live pass of the same steps, from HIP events that the launch itself stamps at its start
   and end (hipExtLaunchKernel on the library's stream, read through the zkh_prof_* hooks),
   so the figure is the kernel's execution time as a kernel trace reports it.
-- layer_roofline: the same for the dominant kernel class of the SwiGLU segment.
+- layer_roofline: the same for the dominant kernel class of the SwiGLU segment, and (valu)
+  its Montgomery products per second against fr_mul_peak, the device-wide rate of the
+  library's multiply measured by zkh_calib_fr_mul in the same run.
 - fr_inputs: the 7 matmuls with X, W, Y bound as field-element tensors (32 B per entry).
 - configs: BASELINE configs C2 (llama-68m FFN matmuls), C3 (logUp 2^20 vs 2^16) and C5
   (OpenLLaMA-3B layer at seq 2048: matmuls, SwiGLU lookup 2^25 vs 2^22 + Hadamard).
@@ -706,7 +708,7 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--segment", choices=["glu", "rope", "commit", "batchopen", "c3", "c5glu", "mmfr"],
+    ap.add_argument("--segment", choices=["glu", "rope", "commit", "batchopen", "c3", "c5glu", "mmfr", "frmul"],
                     default=None, help="only run one segment repeatedly (for profiling), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -726,6 +728,11 @@ def main():
     L = LAYER
     C4 = synth.CONFIGS["C4"]
     MATMULS = C4["matmuls"]
+    if args.segment == "frmul":  # the Montgomery-multiply rate probe alone (for profiling)
+        ctx = zkh.Context(0)
+        rates = [ctx.calib_fr_mul(256) for _ in range(max(args.steps, 1))]
+        print(json.dumps({"segment": "frmul", "mul_per_s": rates}))
+        return
     if args.segment == "commit":
         jobs = [MatmulJob(zkh, synth, rng, n, L["B"], i, o) for n, i, o in MATMULS]
         pool = concurrent.futures.ThreadPoolExecutor(max_workers=16)
@@ -768,6 +775,8 @@ def main():
     pool = concurrent.futures.ThreadPoolExecutor(max_workers=16)
 
     mctx = zkh.Context(0)
+    # the Montgomery-multiply rate of this build (the VALU roofline of the field kernels)
+    fr_peak = max(mctx.calib_fr_mul(256) for _ in range(3))
 
     # one prepared zkh_mm_prove_batch call (job array and output buffers built once); a
     # step resets each transcript to its pre-proof state and proves all seven matmuls
@@ -783,17 +792,20 @@ def main():
     def mm_result():
         return [o["claims"].tobytes() + j.st.tobytes() for o, j in zip(mbatch.outs, jobs)]
 
-    ref = None
-    for _ in range(args.warmup):
-        mm_step()
-        ref = mm_result()
+    mm_step()  # the reference proofs (every timed step must reproduce them)
+    ref = mm_result()
     mm_outs = [({k: v.copy() for k, v in o.items()}, j.st.copy()) for o, j in zip(mbatch.outs, jobs)]
     print("setup %.1fs; matmul step warm" % (time.perf_counter() - t_setup), file=sys.stderr, flush=True)
     # the interpreter's cyclic GC (millions of objects once torch is imported) would stall
-    # a step for tens of ms at fixed allocation counts; it stays off while timing
+    # a step for tens of ms at fixed allocation counts; it stays off while timing.  The W
+    # warmup steps run right before the timed ones, after the collection: a step that follows
+    # an idle pause (the collection, the device and the host workers going idle) takes
+    # several times as long as the next ones.
     def timed_steps():
         gc.collect()
         gc.disable()
+        for _ in range(args.warmup):
+            mm_step()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         step_ms = []
@@ -805,7 +817,7 @@ def main():
         t1 = time.perf_counter()
         out = mm_result()
         gc.enable()
-        assert ref is None or out == ref, "non-deterministic proof output"
+        assert out == ref, "non-deterministic proof output"
         return (t1 - t0) * 1000.0 / args.steps, step_ms
 
     # Timed steps without kernel-timing events: a launch that stamps HIP events costs the host
@@ -897,6 +909,19 @@ def main():
                           "launches_per_segment": gla,
                           "scope": "dominant kernel class of the SwiGLU segment (the layer's largest), "
                                    "algorithmic bytes over launch-stamped time"}
+        if gdom == "lu_phase2":
+            # the same launches against the Montgomery-multiply peak: per pair 15 products in
+            # the first round (eq weight, 5 (A, S) and 9 (B, T, m) products) and 25 after it
+            # (the owed folds of A, S, B, T, m: 2 per table)
+            pairs = [(glu.D >> r) // 2 for r in range(int(gla))]
+            prods = sum(p * (15 if r == 0 else 25) for r, p in enumerate(pairs))
+            rate = prods / (gms / 1000.0)
+            layer_roofline["valu"] = {
+                "products_per_segment": prods, "achieved_Gmul_s": round(rate / 1e9, 1),
+                "peak_Gmul_s": round(fr_peak / 1e9, 1), "frac": round(rate / fr_peak, 4),
+                "basis": "Montgomery products of the %d lu_phase2 launches (n = 2^%d .. 2^%d) over their "
+                         "launch-stamped time, against zkh_calib_fr_mul's device-wide rate"
+                         % (gla, glu.logD, glu.logD - int(gla) + 1)}
         print("layer %.3f s" % layer["prove_s_per_layer"], file=sys.stderr, flush=True)
 
     configs = None
@@ -996,6 +1021,9 @@ def main():
                    "inputs": "X, W int32 and Y int64 tensors (zkob_fc's int input files); the field-element "
                              "input rate is under fr_inputs"},
         "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
+        "fr_mul_peak": {"value": fr_peak, "unit": "Montgomery products/s",
+                        "probe": "zkh_calib_fr_mul: 2048 blocks x 256 threads, 4 independent chains of 256 "
+                                 "products per thread, device time of the launch (best of 3)"},
     }
     if layer:
         res["prove_s_per_layer"] = layer["prove_s_per_layer"]

@@ -102,6 +102,11 @@ int zkh_prod_round(zkh_ctx* ctx, const zkh_tensor* a, const zkh_tensor* b, uint3
 /* host scalar arithmetic on canonical Fr, the reference's h_scalar / k_scalar_op
  * (vrf_common.cuh:30-38, :100-104): op 0 a+b, 1 a-b, 2 a*b, 3 a^-1 (0 -> 0); no device */
 int zkh_fr_scalar(const uint32_t a[8], const uint32_t b[8], int op, uint32_t out[8]);
+/* Calibration, no counterpart in the reference: the device's rate of this build's Montgomery
+ * multiply (the one every field kernel uses), from a launch of 2048 blocks x 256 threads,
+ * each thread running four independent chains of `iters` products; *mul_per_s receives
+ * products per second over the launch's device time.  ZKH_EARG when iters is 0. */
+int zkh_calib_fr_mul(zkh_ctx* ctx, uint32_t iters, double* mul_per_s);
 /* SHA-256 of a byte string (bo_file_sha256's digest, zkob_claims.cuh:310-318); no device */
 int zkh_sha256(const void* data, size_t n, uint8_t out[32]);
 /* FrTensor::partial_me(u, cur_dim, window) (fr-tensor.cu:518-560): binds the middle

@@ -586,3 +586,12 @@ def test_hp_prove_eq_wrong_claim_stops(zkh, ctx, k):
     for key in ("ev", "term", "ws"):
         assert fr_eq(got[key], want[key]), key
     assert bytes(st_g) == bytes(st_o)
+
+
+def test_calib_fr_mul(zkh, ctx):
+    """The multiply-rate probe runs and reports a plausible device-wide rate; zero
+    iterations are refused."""
+    rate = ctx.calib_fr_mul(64)
+    assert 1e9 < rate < 1e13, rate
+    with pytest.raises(zkh.ZkhError):
+        ctx.calib_fr_mul(0)

@@ -89,6 +89,7 @@ def lib():
         L.zkh_mm_prove_batch.argtypes = [vp, vp, u32]
         L.zkh_prof_enable.argtypes = [vp, ctypes.c_int]
         L.zkh_prof_get.argtypes = [vp, ctypes.c_char_p, vp, vp, vp]
+        L.zkh_calib_fr_mul.argtypes = [vp, u32, ctypes.POINTER(ctypes.c_double)]
         L.zkh_prof_names.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t]
         L.zkh_g1_from_host.argtypes = [vp, vp, u32, ctypes.POINTER(vp)]
         L.zkh_g1_to_host.argtypes = [vp, vp, vp]
@@ -283,6 +284,12 @@ class Context:
         return self._new(lib().zkh_tensor_weights_i32, _p(W), IN, OUT)
 
     # MLE primitives
+    def calib_fr_mul(self, iters=256):
+        """Montgomery products per second of the library's multiply on this device."""
+        r = ctypes.c_double(0)
+        self._chk(lib().zkh_calib_fr_mul(self.h, iters, ctypes.byref(r)))
+        return r.value
+
     def sum(self, t):
         out = np.zeros(8, dtype=np.uint32)
         self._chk(lib().zkh_sum(self.h, t.h, _p(out)))

@@ -1434,6 +1434,30 @@ __global__ void k_static_setup(StaticFacArg fac, uint32_t words, uint32_t* fac_d
     for (uint32_t i = threadIdx.x; i < words; i += blockDim.x) fac_dst[i] = fac.w[i];
     for (uint32_t i = threadIdx.x; i < ncnt; i += blockDim.x) cnt[i] = 0;
 }
+static_assert(NT == kFrMulPeakThreads, "k_fr_mul_peak runs NT threads per block");
+__global__ __launch_bounds__(NT) void k_fr_mul_peak(uint32_t iters, uint32_t* out) {
+    const uint32_t t = blockIdx.x * NT + threadIdx.x;
+    fr_t x[4], y[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {  // canonical: the top limb stays below r's
+            x[c].v[i] = (i == 7 ? 0x0fffffffu : 0xffffffffu) & (t * 0x9e3779b9u + (uint32_t)(c * 8 + i) * 0x85ebca6bu);
+            y[c].v[i] = (i == 7 ? 0x0fffffffu : 0xffffffffu) & ((uint32_t)(c * 8 + i + 1) * 0xc2b2ae35u);
+        }
+    for (uint32_t k = 0; k < iters; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) x[c] = mont_mul(x[c], y[c]);
+    uint32_t d = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) d ^= x[c].v[i];
+    out[t] = d;
+}
+void launch_fr_mul_peak(hipStream_t s, uint32_t blocks, uint32_t iters, uint32_t* out, hipEvent_t t0, hipEvent_t t1) {
+    hipExtLaunchKernelGGL(k_fr_mul_peak, dim3(blocks), dim3(NT), 0, s, t0, t1, 0, iters, out);
+}
 void launch_static_setup(hipStream_t s, const StaticFacArg& fac, uint32_t words, uint32_t* fac_dst,
                          uint32_t* cnt, uint32_t ncnt) {
     k_static_setup<<<1, NT, 0, s>>>(fac, words, fac_dst, cnt, ncnt);

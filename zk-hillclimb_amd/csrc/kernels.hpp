@@ -204,6 +204,10 @@ uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t 
 struct StaticFacArg {
     uint32_t w[ZKH_STATIC_MAX_VARS * 16];  // (1 - u_t, u_t) per variable, Montgomery form
 };
+// the Montgomery-multiply rate probe: `blocks` x kFrMulPeakThreads threads, four independent
+// chains of `iters` products per thread; out[thread] receives a digest of the chains
+constexpr uint32_t kFrMulPeakThreads = 256;
+void launch_fr_mul_peak(hipStream_t s, uint32_t blocks, uint32_t iters, uint32_t* out, hipEvent_t t0, hipEvent_t t1);
 void launch_static_setup(hipStream_t s, const StaticFacArg& fac, uint32_t words, uint32_t* fac_dst,
                          uint32_t* cnt, uint32_t ncnt);
 

@@ -1046,6 +1046,29 @@ extern "C" int zkh_prod_round(zkh_ctx* c, const zkh_tensor* a, const zkh_tensor*
     for (int t = 0; t < 3; t++) fr_store(fr_mont_mul(s[t], kR2), out + 8 * t);
     return ZKH_OK;
 }
+extern "C" int zkh_calib_fr_mul(zkh_ctx* c, uint32_t iters, double* mul_per_s) {
+    if (!c || !mul_per_s || !iters) return fail(c, ZKH_EARG, "calib_fr_mul: null argument or zero iterations");
+    HIPCHK(c, hipSetDevice(c->device));
+    const uint32_t blocks = 2048;
+    int rc = 0;
+    uint32_t* out = (uint32_t*)scratch_slot(c, SL_TMP6, (size_t)blocks * kFrMulPeakThreads * 4, &rc);
+    if (rc) return rc;
+    hipEvent_t a, b;
+    HIPCHK(c, hipEventCreate(&a));
+    if (hipEventCreate(&b) != hipSuccess) {
+        (void)hipEventDestroy(a);
+        return fail(c, ZKH_EDEV, "hipEventCreate failed");
+    }
+    launch_fr_mul_peak(c->stream, blocks, iters, out, a, b);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    float ms = 0;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    if (e != hipSuccess) return fail(c, ZKH_EDEV, "calib_fr_mul: %s", hipGetErrorString(e));
+    *mul_per_s = (double)blocks * kFrMulPeakThreads * 4.0 * iters / (ms * 1e-3);
+    return ZKH_OK;
+}
 extern "C" int zkh_fr_scalar(const uint32_t a[8], const uint32_t b[8], int op, uint32_t out[8]) {
     if (!a || !out || (op != 3 && !b) || op < 0 || op > 3) return ZKH_EARG;
     if (!fr_is_canonical(a) || (op != 3 && !fr_is_canonical(b))) return ZKH_EARG;
