@@ -458,6 +458,7 @@ def test_lu_prove(zkh, ctx, shape):
     u = np.array([C.tr_challenge_fr(st_o) for _ in range(logD)])
     ug = np.array([zkh.challenge(st_g) for _ in range(logD)])
     assert fr_eq(u, ug)
+    st_g2 = st_g.copy()
     rc, want = C.lu_prove(st_o, A, S, T, m, alpha, beta, u)
     assert rc == 0
     # FR-kind witness (not the int view) must give the same proof
@@ -465,6 +466,12 @@ def test_lu_prove(zkh, ctx, shape):
     for key in ("ev", "term", "ws"):
         assert fr_eq(got[key], want[key]), key
     assert bytes(st_g) == bytes(st_o)
+    # with the tensor that zkh_lu_inverse inverted, the first round takes A (S + beta) = 1
+    # (the closed-form sums) and must give the same proof
+    got = ctx.lu_prove(st_g2, Ag, Sg, Tg, mg, alpha, beta, u)
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), ("closed form", key)
+    assert bytes(st_g2) == bytes(st_o)
 
 
 @pytest.mark.parametrize("D,N,skew", [(1000, 64, 0), (70000, 16384, 1), (1 << 17, 40000, 1), (1 << 17, 40000, 0),

@@ -1132,15 +1132,52 @@ ZDEV bool relayed_vm(const uint32_t* vmp, fr_t& vm) {
     for (int i = 0; i < 8; i++) vm.v[i] = vmp[i];
     return true;
 }
+// First-round sums of a table X known to be 1/(Y + beta) entry-wise (inverse(0) = 0), with
+// no fold owed: x (y + beta) is 1 for x != 0 and 0 for x = 0, so the two weighted products
+// reduce to sums of the weight w = e 2^256 over the nonzero entries (the host takes them
+// as sum e, removing the 2^256, where the general path's sums carry 2^-256); the third,
+// w (x1 - x0)(y1 - y0), keeps its two products.  Accumulator slots 0, 1, 2 as the general
+// path's.
+ZDEV bool fr_nonzero(const fr_t& x) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) o |= x.v[i];
+    return o != 0;
+}
+template <int K>
+ZDEV void inverse_pair_sums(const fr_t& x0, const fr_t& x1, const fr_t& y0, const fr_t& y1, const fr_t& w,
+                            LdsAcc<K>& acc) {
+    acc.add(0, fr_nonzero(x0) ? w : fr_zero());
+    acc.add(1, fr_nonzero(x1) ? w : fr_zero());
+    const fr_t wdx = mont_mul_ol(w, fr_sub(x1, x0));
+    SB();
+    acc.add(2, mont_mul_ol(wdx, fr_sub(y1, y0)));
+}
+// the (A, S) group's first round with A = 1/(S + beta): sums 0..2 as above, 3, 4 sum a0, a1
+ZDEV void lu_as_inverse(const TabDev& A, const TabDev& S, uint32_t i, uint32_t h, const EqDev& eq, LdsAcc<5>& acc) {
+    const fr_t a0 = ld_fr(A.slo, A.shi, i), a1 = ld_fr(A.slo, A.shi, i + h);
+    acc.add(3, a0);
+    acc.add(4, a1);
+    const fr_t w = eq_w(eq, i);
+    SB();
+    const fr_t s0 = ld_fr(S.slo, S.shi, i), s1 = ld_fr(S.slo, S.shi, i + h);
+    inverse_pair_sums<5>(a0, a1, s0, s1, w, acc);
+    SB();
+}
 // phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
 // acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
 __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, int fold, fr_t vm,
-                                                  const uint32_t* vmp, fr_t beta, EqDev eq, Publish pub) {
+                                                  const uint32_t* vmp, fr_t beta, EqDev eq, Publish pub, int inv) {
     if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
     __shared__ uint4 accl[5 * NT], acch[5 * NT];
     LdsAcc<5> acc{accl, acch};
     acc.zero();
+    if (inv && !fold) {  // A = 1/(S + beta) unfolded: see lu_as_inverse
+        for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) lu_as_inverse(A, S, i, h, eq, acc);
+        reduce_publish_lds<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+        return;
+    }
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t wa0, wda;
         {
@@ -1173,11 +1210,11 @@ __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n
 }
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
-                          Publish partial) {
+                          Publish partial, int inv) {
     const uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
-    k_lu_phase1<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, fold, vm, vmp, to_fr(beta_host), e, partial);
+    k_lu_phase1<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, fold, vm, vmp, to_fr(beta_host), e, partial, inv);
     return g;
 }
 
@@ -1191,10 +1228,16 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
 // job 1 (B, T, m): sum w*b0*t0, w*b1*t1, w*db*dt, m0*b0, m1*b1, dm*db (x 2^-256)  (t + beta)
 template <int fold>
 ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t& vm, const fr_t& beta,
-                       const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint4* accl, uint4* acch) {
+                       const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint4* accl, uint4* acch,
+                       int inv) {
     const uint32_t h = n >> 1;
     LdsAcc<5> acc{accl, acch};
     acc.zero();
+    if (!fold && inv) {
+        for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) lu_as_inverse(A, S, i, h, eq, acc);
+        reduce_publish_lds<5>(acc, pub, 0, 0, g, lb);
+        return;
+    }
     for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
         fr_t wa0, wda;
         {
@@ -1226,10 +1269,32 @@ ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t&
 template <int fold>
 ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const fr_t& vm,
                         const fr_t& beta, const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint32_t ga,
-                        uint4* accl, uint4* acch) {
+                        uint4* accl, uint4* acch, int inv) {
     const uint32_t h = n >> 1;
     LdsAcc<6> acc{accl, acch};
     acc.zero();
+    if (!fold && inv) {  // B = 1/(T + beta) unfolded (see inverse_pair_sums); 3..5 as below
+        for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
+            const fr_t b0 = ld_fr(B.slo, B.shi, i), b1 = ld_fr(B.slo, B.shi, i + h);
+            {
+                const fr_t m0 = ld_fr(m.slo, m.shi, i), m1 = ld_fr(m.slo, m.shi, i + h);
+                SB();
+                acc.add(3, mont_mul_ol(m0, b0));
+                SB();
+                acc.add(4, mont_mul_ol(m1, b1));
+                SB();
+                acc.add(5, mont_mul_ol(fr_sub(m1, m0), fr_sub(b1, b0)));
+            }
+            SB();
+            const fr_t w = eq_w(eq, i);
+            SB();
+            const fr_t t0 = ld_fr(T.slo, T.shi, i), t1 = ld_fr(T.slo, T.shi, i + h);
+            inverse_pair_sums<6>(b0, b1, t0, t1, w, acc);
+            SB();
+        }
+        reduce_publish_lds<6>(acc, pub, 1, ga, g, lb);
+        return;
+    }
     for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
         fr_t b0, b1;
         load_pair(B, i, h, n, fold, vm, b0, b1);
@@ -1270,25 +1335,25 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
 template <int fold_as, int fold_btm>
 __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m, uint32_t n,
                                                   fr_t vm, const uint32_t* vmp, fr_t beta, EqDev eq, Publish pub,
-                                                  uint32_t ga, uint32_t gb) {
+                                                  uint32_t ga, uint32_t gb, int inv_as, int inv_btm) {
     if (!relayed_vm(vmp, vm)) return;
     __shared__ uint4 accl[6 * NT], acch[6 * NT];
-    if (blockIdx.x < ga) lu_phase2_as<fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, ga, accl, acch);
-    else lu_phase2_btm<fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - ga, gb, ga, accl, acch);
+    if (blockIdx.x < ga) lu_phase2_as<fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, ga, accl, acch, inv_as);
+    else lu_phase2_btm<fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - ga, gb, ga, accl, acch, inv_btm);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host,
-                          EqW eq, Publish partial) {
+                          EqW eq, Publish partial, int inv_as, int inv_btm) {
     const uint32_t ga = grid_for(n >> 1, NT, LU2_GRID * 2 / 5), gb = grid_for(n >> 1, NT, LU2_GRID * 3 / 5);
     const fr_t vm = (fold_as || fold_btm) && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
     const fr_t beta = to_fr(beta_host);
     const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T), md = tab_dev(m);
     const uint32_t g = ga + gb;
-    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
-    else if (fold_as) k_lu_phase2<1, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
-    else if (fold_btm) k_lu_phase2<0, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
-    else k_lu_phase2<0, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb);
+    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
+    else if (fold_as) k_lu_phase2<1, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
+    else if (fold_btm) k_lu_phase2<0, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
+    else k_lu_phase2<0, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
     return g;
 }
 

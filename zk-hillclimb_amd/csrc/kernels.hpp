@@ -177,15 +177,19 @@ void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 // (launch_relay) that runs between the previous round and this one; vmp[8] != 0 makes the
 // kernel return at once (the host abandoned the proof).
 // phase-1 round over A, S (size n): sums e*a0*s0, e*a1*s1, e*da*ds (x 2^-256), a0, a1
+// inv: A is 1/(S + beta) entry-wise and no fold is owed: sums 0 and 1 become sum_{a != 0} w
+// with w = e 2^256 (sum e after one Montgomery reduction), two products per pair fewer
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
-                          Publish pub);
+                          Publish pub, int inv);
 // phase-2 round over A, S, B, T, m as two launches publishing jobs 0 (A, S: 5 sums) and
 // 1 (B, T, m: 6 sums) of `pub` (made for 2 jobs; see kernels.hip)
+// inv_as / inv_btm: A = 1/(S + beta) / B = 1/(T + beta) with that group's fold not owed, as
+// inv of launch_lu_phase1 (sums 0, 1 of the group then carry 2^256 instead of 2^-256)
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
                           int fold_as, int fold_btm,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
-                          Publish pub);
+                          Publish pub, int inv_as, int inv_btm);
 
 // ---- Hadamard ----
 // generic: sums_t = sum E_t*S_t*U_t, t = 0..3 (x 2^-512)

@@ -295,8 +295,18 @@ struct zkh_tensor {
     uint32_t w_in = 0, w_out = 0;
     std::shared_ptr<MemPool> pool;  // owner of d (size class cls)
     size_t cls = 0;
+    // identity of the contents: a fresh number at creation and after every in-place change
+    uint64_t gen = 0;
+    // set by zkh_lu_inverse: this tensor is 1/(S + beta) entry-wise (inverse(0) = 0) for
+    // the tensor S of generation inv_of (0: no such knowledge)
+    uint64_t inv_of = 0;
+    uint32_t inv_beta[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     DevPlanes planes() const { return DevPlanes{(uint32_t*)d, cap}; }
 };
+static uint64_t next_gen() {
+    static std::atomic<uint64_t> g{0};
+    return ++g;
+}
 
 // ---------------------------------------------------------------------------------------
 // errors and scratch
@@ -759,6 +769,7 @@ static int tensor_alloc(zkh_ctx* c, int kind, uint32_t n, zkh_tensor** out) {
     t->ctx = c;
     t->kind = kind;
     t->n = n;
+    t->gen = next_gen();
     size_t bytes;
     if (kind == ZKH_KIND_FR) {
         t->cap = n ? n : 1;
@@ -1295,6 +1306,8 @@ extern "C" int zkh_fold(zkh_ctx* c, zkh_tensor* t, const uint32_t v[8]) {
     fr_store(fr_to_mont(fr_load(v)), vm);
     launch_fold(c->stream, Tab{t->planes(), t->planes()}, t->n / 2, vm);
     t->n /= 2;
+    t->gen = next_gen();
+    t->inv_of = 0;
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return ZKH_OK;
 }
@@ -2381,6 +2394,8 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
         return rc;
     }
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    A->inv_of = S->gen;
+    memcpy(A->inv_beta, beta, 32);
     *A_out = A;
     return ZKH_OK;
 }
@@ -2635,17 +2650,27 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         const uint32_t n = D >> r;
         return n <= N && n <= ZKH_LU_PERSIST_MAX && !no_persist;
     };
+    // A from zkh_lu_inverse(S, beta) is 1/(S + beta) entry-wise, and so is the internal B of
+    // T: a group's first (unfolded) round then needs two products per pair fewer, its sums
+    // 0 and 1 coming as sum e over the nonzero entries (cf: no 2^-256 to undo)
+    const bool a_is_inv = A->kind == ZKH_KIND_FR && A->inv_of && A->inv_of == S->gen && !memcmp(A->inv_beta, beta_l, 32);
+    struct Launched {
+        Publish pb;
+        bool cf_a, cf_b;
+    };
     // launches round r (reading the previous challenge from vm, or from the relay when vmp
     // is given) and moves the table handles to the folded copies the launch writes
     auto launch = [&](uint32_t r, const uint32_t* vmp) {
         const uint32_t n = D >> r, K = logD - r - 1;
-        Publish pb;
+        Launched l{};
+        Publish& pb = l.pb;
         if (n > N) {  // phase 1
             pb = make_pub(c, 1);
+            l.cf_a = a_is_inv && !as_pending;
             {
                 ProfScope ps(c, "lu_phase1", (as_pending ? 3.0 * n : (double)n) * 2 * 32);
                 launch_lu_phase1(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, n, as_pending, vm, vmp, beta_l,
-                                 EqW{eq.elo_d, eq.ehi_d, K}, pb);
+                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -2654,12 +2679,14 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             as_pending = true;
         } else {  // phase 2
             pb = make_pub(c, 2);
+            l.cf_a = a_is_inv && !as_pending;
+            l.cf_b = !btm_pending;
             {
                 ProfScope ps(c, "lu_phase2",
                              ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
                 launch_lu_phase2(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
                                  Tab{m_src, mw}, n, as_pending, btm_pending, vm, vmp, beta_l,
-                                 EqW{eq.elo_d, eq.ehi_d, K}, pb);
+                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -2673,10 +2700,12 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             as_pending = true;
             btm_pending = true;
         }
-        return pb;
+        return l;
     };
+    // a published weighted-product sum as the round polynomial takes it
+    auto q_of = [](const Fr& s, bool cf) { return cf ? fr_from_mont(s) : fix1(s); };
     RelayGuard relay{c};
-    Publish pb{};
+    Launched cur{};
     bool launched = false;  // round r is already queued
     for (uint32_t r = 0; r < logD; r++) {
         const uint32_t n = D >> r;
@@ -2689,25 +2718,26 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             break;
         }
         if (tracing) tr_t.push_back(now_us());
-        if (!launched) pb = launch(r, nullptr);
+        if (!launched) cur = launch(r, nullptr);
         // round r + 1 goes behind a relay now, so that its launch overlaps this round
         const bool relay_next = r + 1 < logD && !persists(r + 1);
-        Publish pb_next{};
+        Launched next{};
         if (relay_next) {
             relay.pending = relay_enqueue(c);
-            pb_next = launch(r + 1, c->relay_vm);
+            next = launch(r + 1, c->relay_vm);
         }
         const uint32_t k = logD - r;  // remaining variables
         const uint32_t K = k - 1;     // eq variables of the pairs
         const Fr ul = u[k - 1];
         const Fr corr = eq_corr(eq, K);
         Fr coef[4];
-        if ((rc = wait_pub(c, pb.seq))) return rc;
+        if ((rc = wait_pub(c, cur.pb.seq))) return rc;
         if (tracing) tr_t.push_back(now_us());
         if (n > N) {  // phase 1
             Fr s[5];
             pub_read(c, 0, 5, s);
-            Fr q0 = fr_mul(fix1(s[0]), corr), q1 = fr_mul(fix1(s[1]), corr), q2 = fr_mul(fix1(s[2]), corr);
+            Fr q0 = fr_mul(q_of(s[0], cur.cf_a), corr), q1 = fr_mul(q_of(s[1], cur.cf_a), corr),
+               q2 = fr_mul(fix1(s[2]), corr);
             Fr qc1 = fr_sub(fr_sub(q1, q0), q2);
             Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
             Fr aq0 = fr_mul(alpha, q0), aq1 = fr_mul(alpha, qc1), aq2 = fr_mul(alpha, q2);
@@ -2727,8 +2757,10 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             }
             s[6] = sa[3];
             s[7] = sa[4];
-            Fr qa0 = fr_mul(fix1(s[0]), corr), qa1 = fr_mul(fix1(s[1]), corr), qa2 = fr_mul(fix1(s[2]), corr);
-            Fr qb0 = fr_mul(fix1(s[3]), corr), qb1 = fr_mul(fix1(s[4]), corr), qb2 = fr_mul(fix1(s[5]), corr);
+            Fr qa0 = fr_mul(q_of(s[0], cur.cf_a), corr), qa1 = fr_mul(q_of(s[1], cur.cf_a), corr),
+               qa2 = fr_mul(fix1(s[2]), corr);
+            Fr qb0 = fr_mul(q_of(s[3], cur.cf_b), corr), qb1 = fr_mul(q_of(s[4], cur.cf_b), corr),
+               qb2 = fr_mul(fix1(s[5]), corr);
             Fr coefBT = fr_mul(inv_ratio, alpha_sq);
             Fr Q0 = fr_add(fr_mul(alpha, qa0), fr_mul(coefBT, qb0));
             Fr Q1 = fr_add(fr_mul(alpha, fr_sub(fr_sub(qa1, qa0), qa2)),
@@ -2764,7 +2796,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         if (relay_next) {
             relay_send(c, relay.pending, vm);
             relay.pending = 0;
-            pb = pb_next;
+            cur = next;
         }
         launched = relay_next;
         if (tracing) tr_t.push_back(now_us());
