@@ -602,3 +602,24 @@ def test_calib_fr_mul(zkh, ctx):
     assert 1e9 < rate < 1e13, rate
     with pytest.raises(zkh.ZkhError):
         ctx.calib_fr_mul(0)
+
+
+@pytest.mark.parametrize("k", [4, 14, 16])
+def test_hp_prove_u_all_ones(zkh, ctx, k):
+    """U = 1 everywhere as an int32 tensor (the RoPE obligations' U, zkob_rope.cu:215-281): the
+    per-round kernels skip U (E_t S_t from three products per pair) and must give the oracle's
+    proof of the generic E, S, U sumcheck."""
+    n = 1 << k
+    rng = np.random.default_rng(100 + k)
+    E = rand_fr_full(rng, n)
+    S = C.ints_to_fr(rng.integers(-2**20, 2**20, size=n))
+    ones = np.ones(n, np.int64)
+    Ei, Si = C.fr_to_ints(E), C.fr_to_ints(S)
+    claim = C.ints_to_fr([sum(a * b for a, b in zip(Ei, Si)) % P.R])[0]
+    st_g, st_o = seed_transcript(zkh, "hp1:%d" % k)
+    rc, want = C.hp_prove(st_o, claim, E, S, C.ints_to_fr(ones))
+    assert rc == 0
+    got = ctx.hp_prove(st_g, claim, ctx.from_fr(E), ctx.from_fr(S), ctx.from_i32(ones.astype(np.int32)))
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)

@@ -169,14 +169,19 @@ ZDEV U absmax_block(U m) {
     return m;
 }
 __global__ __launch_bounds__(NT) void k_absmax_i32(const int32_t* __restrict__ in, uint32_t n, uint32_t* out) {
-    uint32_t m = 0;
+    uint32_t m = 0, not_one = 0;
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < n; i += gridDim.x * NT) {
         int64_t v = in[i];
         uint32_t a = (uint32_t)(v < 0 ? -v : v);
         m = a > m ? a : m;
+        not_one |= v != 1;
     }
     m = absmax_block<uint32_t>(m);
-    if (threadIdx.x == 0) atomicMax(out, m);
+    not_one = absmax_block<uint32_t>(not_one);
+    if (threadIdx.x == 0) {
+        atomicMax(out, m);
+        if (not_one) atomicOr(out + 1, 1u);
+    }
 }
 __global__ __launch_bounds__(NT) void k_absmax_i64(const int64_t* __restrict__ in, uint32_t n,
                                                    unsigned long long* out) {
@@ -1403,6 +1408,38 @@ uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fol
     uint32_t g = grid_for(n >> 1, NT * 2, 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     k_hp_round<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, vmp, partial);
+    return g;
+}
+// U = 1 everywhere (the RoPE obligations' Hadamard): E_t S_t U_t = E_t S_t, a quadratic in t
+// from three products per pair: sums e0 s0, e1 s1, (e1 - e0)(s1 - s0) (x 2^-256).  U is
+// neither read nor folded (every fold of an all-ones table is all ones).
+__global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32_t n, int fold, fr_t vm,
+                                                      const uint32_t* vmp, Publish pub) {
+    if (!relayed_vm(vmp, vm)) return;
+    const uint32_t h = n >> 1;
+    __shared__ uint4 accl[3 * NT], acch[3 * NT];
+    LdsAcc<3> acc{accl, acch};
+    acc.zero();
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        fr_t e0, e1, s0, s1;
+        load_pair(E, i, h, n, fold, vm, e0, e1);
+        SB();
+        load_pair(S, i, h, n, fold, vm, s0, s1);
+        SB();
+        acc.add(0, mont_mul_ol(e0, s0));
+        SB();
+        acc.add(1, mont_mul_ol(e1, s1));
+        SB();
+        acc.add(2, mont_mul_ol(fr_sub(e1, e0), fr_sub(s1, s0)));
+        SB();
+    }
+    reduce_publish_lds<3>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+}
+uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
+                              const uint32_t* vmp, Publish partial) {
+    uint32_t g = grid_for(n >> 1, NT, 1024);
+    fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
+    k_hp_round_ones<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial);
     return g;
 }
 // eq-specialised: sums_t = sum_i eq(i, u[0..K)) S_t[i] U_t[i]  (x 2^-256)

@@ -55,6 +55,7 @@ void launch_aos_to_planes(hipStream_t s, const uint32_t* aos, uint32_t n, DevPla
 // *bad (zeroed by the caller) += entries of aos that are not below r
 void launch_count_noncanonical(hipStream_t s, const uint32_t* aos, uint32_t n, uint32_t* bad);
 void launch_planes_to_aos(hipStream_t s, DevPlanes in, uint32_t n, uint32_t* aos);
+// out[0] = max |in[i]|, out[1] |= 1 when some entry is not 1 (both zeroed by the caller)
 void launch_absmax_i32(hipStream_t s, const int32_t* in, uint32_t n, uint32_t* out);
 void launch_absmax_i64(hipStream_t s, const int64_t* in, uint32_t n, unsigned long long* out);
 void launch_transpose_i32(hipStream_t s, const int32_t* in, uint32_t rows, uint32_t cols,
@@ -195,6 +196,9 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
 // generic: sums_t = sum E_t*S_t*U_t, t = 0..3 (x 2^-512)
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
                          int fold, const uint32_t* v_m_host, const uint32_t* vmp, Publish pub);
+// generic with U = 1 everywhere: sums e0*s0, e1*s1, de*ds (x 2^-256); U is not touched
+uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
+                              const uint32_t* vmp, Publish pub);
 // eq-specialised: sums_t = sum eq(i,u_)*S_t*U_t, t = 0..3 (x 2^-256)
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub);

@@ -295,6 +295,7 @@ struct zkh_tensor {
     uint32_t w_in = 0, w_out = 0;
     std::shared_ptr<MemPool> pool;  // owner of d (size class cls)
     size_t cls = 0;
+    bool ones = false;  // an I32 tensor whose entries are all 1 (measured at ingest)
     // identity of the contents: a fresh number at creation and after every in-place change
     uint64_t gen = 0;
     // set by zkh_lu_inverse: this tensor is 1/(S + beta) entry-wise (inverse(0) = 0) for
@@ -787,16 +788,17 @@ static int tensor_alloc(zkh_ctx* c, int kind, uint32_t n, zkh_tensor** out) {
     *out = t;
     return ZKH_OK;
 }
-static int int_bits_i32(zkh_ctx* c, const int32_t* d, uint32_t n, uint32_t* bits) {
+static int int_bits_i32(zkh_ctx* c, const int32_t* d, uint32_t n, uint32_t* bits, bool* ones) {
     int rc = 0;
     uint32_t* m = (uint32_t*)scratch_slot(c, SL_SMALL, 64, &rc);
     if (rc) return rc;
-    HIPCHK(c, hipMemsetAsync(m, 0, 4, c->stream));
+    HIPCHK(c, hipMemsetAsync(m, 0, 8, c->stream));
     launch_absmax_i32(c->stream, d, n, m);
-    uint32_t h = 0;
-    HIPCHK(c, hipMemcpyAsync(&h, m, 4, hipMemcpyDeviceToHost, c->stream));
+    uint32_t h[2] = {0, 0};
+    HIPCHK(c, hipMemcpyAsync(h, m, 8, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    *bits = bits_for(h);
+    *bits = bits_for(h[0]);
+    *ones = n > 0 && h[1] == 0;
     return 0;
 }
 static int int_bits_i64(zkh_ctx* c, const int64_t* d, uint32_t n, uint32_t* bits) {
@@ -827,7 +829,7 @@ static int make_int_tensor(zkh_ctx* c, const void* src, uint32_t n, int kind, hi
             zkh_tensor_free(t);
             return fail(c, ZKH_EDEV, "tensor upload failed: %s", hipGetErrorString(e));
         }
-        rc = kind == ZKH_KIND_I32 ? int_bits_i32(c, (const int32_t*)t->d, n, &t->bits)
+        rc = kind == ZKH_KIND_I32 ? int_bits_i32(c, (const int32_t*)t->d, n, &t->bits, &t->ones)
                                   : int_bits_i64(c, (const int64_t*)t->d, n, &t->bits);
         if (rc) {
             zkh_tensor_free(t);
@@ -1497,17 +1499,22 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             q.SEo = eq_prefix_sum(q.uo, jobs[j].OUT);
         }
     });
-    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, fac.size() * 4, &rc);
+    // one device area and one upload for the eq factors and every stage's descriptors: the
+    // factors first, the descriptors (at most 2 eq tables and 3 reductions per job) after
+    const size_t fac_bytes = (fac.size() * 4 + 255) & ~(size_t)255;
+    const size_t desc_cap = (size_t)nj * (2 * sizeof(EqTabDesc) + 3 * (sizeof(EqDotDesc) + sizeof(SumChunksDesc) +
+                                                                      sizeof(EqDotFrDesc))) + 256;
+    uint8_t* area_d = (uint8_t*)scratch_slot(c, SL_DESC, fac_bytes + desc_cap, &rc);
     if (rc) return rc;
+    uint32_t* fac_d = (uint32_t*)area_d;
     uint32_t* eq_d = (uint32_t*)scratch_slot(c, SL_EB, eq_total * 32, &rc);
     if (rc) return rc;
     DevPlanes red = scratch_planes(c, SL_TMP0, (uint32_t)red_total, &rc);
     if (rc) return rc;
     int32_t* wt_d = wt_total ? (int32_t*)scratch_slot(c, SL_TMP5, wt_total * 4, &rc) : nullptr;
     if (rc) return rc;
-    if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
 
-    stamp("challenges + factor upload");
+    stamp("challenges");
     // 1) eq tables (Montgomery AoS)
     std::vector<EqTabDesc> eqd;
     uint32_t eq_blocks = 0;
@@ -1685,22 +1692,21 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     uint32_t* pin = c->pinned;
     for (auto& d : sums)
         if (d.E) d.dot = pin + pin_claim + 8 * (uintptr_t)d.dot;
-    // descriptors -> device (one area, one upload)
-    size_t desc_bytes = eqd.size() * sizeof(EqTabDesc) + dots.size() * sizeof(EqDotDesc) +
-                        sums.size() * sizeof(SumChunksDesc) + frds.size() * sizeof(EqDotFrDesc) + 256;
-    uint8_t* desc_d = (uint8_t*)scratch_slot(c, SL_DESC, desc_bytes * 2, &rc);
-    if (rc) return rc;
-    std::vector<uint8_t> blob(desc_bytes, 0);
+    // eq factors and descriptors -> device in one upload
+    uint8_t* desc_d = area_d + fac_bytes;
     size_t o_eq = 0, o_dot = o_eq + eqd.size() * sizeof(EqTabDesc);
     size_t o_sum = o_dot + dots.size() * sizeof(EqDotDesc);
     size_t o_fr = o_sum + sums.size() * sizeof(SumChunksDesc);
-    size_t o_zk = (o_fr + frds.size() * sizeof(EqDotFrDesc) + 63) & ~(size_t)63;
-    memcpy(blob.data() + o_eq, eqd.data(), eqd.size() * sizeof(EqTabDesc));
-    memcpy(blob.data() + o_dot, dots.data(), dots.size() * sizeof(EqDotDesc));
-    memcpy(blob.data() + o_sum, sums.data(), sums.size() * sizeof(SumChunksDesc));
-    memcpy(blob.data() + o_fr, frds.data(), frds.size() * sizeof(EqDotFrDesc));
-    if ((rc = upload(c, desc_d, blob.data(), o_zk))) return rc;
-    stamp("descriptors uploaded");
+    size_t o_end = o_fr + frds.size() * sizeof(EqDotFrDesc);
+    if (o_end > desc_cap) return fail(c, ZKH_EDEV, "descriptor area overflow (%zu > %zu)", o_end, desc_cap);
+    std::vector<uint8_t> blob(fac_bytes + o_end, 0);
+    memcpy(blob.data(), fac.data(), fac.size() * 4);
+    memcpy(blob.data() + fac_bytes + o_eq, eqd.data(), eqd.size() * sizeof(EqTabDesc));
+    memcpy(blob.data() + fac_bytes + o_dot, dots.data(), dots.size() * sizeof(EqDotDesc));
+    memcpy(blob.data() + fac_bytes + o_sum, sums.data(), sums.size() * sizeof(SumChunksDesc));
+    memcpy(blob.data() + fac_bytes + o_fr, frds.data(), frds.size() * sizeof(EqDotFrDesc));
+    if ((rc = upload(c, area_d, blob.data(), blob.size()))) return rc;
+    stamp("factors + descriptors uploaded");
     {
         ProfScope ps(c, "eq_tables", (double)eq_total * 32, true);
         launch_eq_mont_multi(c->stream, (const EqTabDesc*)(desc_d + o_eq), (uint32_t)eqd.size(), eq_blocks,
@@ -3406,13 +3412,19 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     Fr e_fin = kZero, s_fin = kZero, u_fin = kZero;
     const bool no_persist = getenv("ZKH_NO_PERSIST") != nullptr;
     auto persists = [&](uint32_t r) { return (n >> r) <= ZKH_HP_PERSIST_MAX && !no_persist; };
+    // U all ones (an I32 tensor measured so at ingest: the RoPE obligations' U = 1) with an
+    // explicit E: the per-round kernels skip U, whose folds stay all ones in its source
+    const bool u_ones = !ueq && U->kind == ZKH_KIND_I32 && U->ones;
     // launches round r (previous challenge from vm, or from the relay when vmp is given) and
     // moves the table handles to the folded copies the launch writes
     auto launch = [&](uint32_t r, const uint32_t* vmp) {
         const uint32_t sz = n >> r;
         const int fold = r > 0;
         Publish pb = make_pub(c, 1);
-        if (!ueq) {
+        if (u_ones) {
+            ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
+            launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, pb);
+        } else if (!ueq) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
             launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp, pb);
         } else {
@@ -3423,7 +3435,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         if (fold) {
             e_src = Ew;
             s_src = Sw;
-            u_src = Uw;
+            if (!u_ones) u_src = Uw;
         }
         return pb;
     };
@@ -3452,10 +3464,15 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         Fr e[4], sums[4];
         if ((rc = wait_pub(c, pb.seq))) return rc;
         if (tracing) tr_t.push_back(now_us());
-        pub_read(c, 0, 4, sums);
-        if (!ueq) {
+        if (u_ones) {  // E_t S_t = c0 + c1 t + c2 t^2 from sum e0s0, e1s1, de*ds
+            pub_read(c, 0, 3, sums);
+            const Fr c0 = fix1(sums[0]), c2 = fix1(sums[2]), c1 = fr_sub(fr_sub(fix1(sums[1]), c0), c2);
+            for (int t = 0; t < 4; t++) e[t] = fr_add(c0, fr_mul(fr_u64(t), fr_add(c1, fr_mul(fr_u64(t), c2))));
+        } else if (!ueq) {
+            pub_read(c, 0, 4, sums);
             for (int t = 0; t < 4; t++) e[t] = fix2(sums[t]);
         } else {
+            pub_read(c, 0, 4, sums);
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
             Fr f = fr_mul(cE, eq_corr(eq, K));
