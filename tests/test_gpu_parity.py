@@ -623,3 +623,27 @@ def test_hp_prove_u_all_ones(zkh, ctx, k):
     for key in ("ev", "term", "ws"):
         assert fr_eq(got[key], want[key]), key
     assert bytes(st_g) == bytes(st_o)
+
+
+@pytest.mark.parametrize("k,bits", [(15, 20), (16, 29), (15, 31)])
+def test_hp_prove_eq_small_ints(zkh, ctx, k, bits):
+    """Eq-form Hadamard on int32 witnesses (the SwiGLU segment's S and U): the first round forms
+    the products as 64-bit integers while every value is within (-2^30, 2^30) and as field
+    products otherwise (bits = 31 mixes both within one round); proofs equal the oracle's."""
+    n = 1 << k
+    rng = np.random.default_rng(200 + k + bits)
+    u = rand_fr_full(rng, k)
+    Si = rng.integers(-(1 << bits), 1 << bits, size=n)
+    Ui = rng.integers(-(1 << 15), 1 << 15, size=n)
+    Si[:4] = [-(1 << 30), (1 << 30) - 1, -(1 << 31), (1 << 31) - 1]
+    E = C.build_eq(u)
+    S, U = C.ints_to_fr(Si), C.ints_to_fr(Ui)
+    Ei = C.fr_to_ints(E)
+    claim = C.ints_to_fr([sum(a * int(b) % P.R * int(c) for a, b, c in zip(Ei, Si, Ui)) % P.R])[0]
+    st_g, st_o = seed_transcript(zkh, "hpeq:%d:%d" % (k, bits))
+    rc, want = C.hp_prove(st_o, claim, E, S, U)
+    assert rc == 0
+    got = ctx.hp_prove_eq(st_g, claim, u, ctx.from_i32(Si.astype(np.int32)), ctx.from_i32(Ui.astype(np.int32)))
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)

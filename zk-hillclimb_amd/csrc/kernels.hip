@@ -1442,15 +1442,39 @@ uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold,
     k_hp_round_ones<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial);
     return g;
 }
-// eq-specialised: sums_t = sum_i eq(i, u[0..K)) S_t[i] U_t[i]  (x 2^-256)
-// Montgomery products issue in independent pairs between scheduling barriers: two
-// chains per wave at <= 128 registers (four waves per SIMD) keep the VALU busy.
+// x as an integer in (-2^30, 2^30) when it is one (a field element or its negative)
+ZDEV bool small_int(const fr_t& x, int32_t& out) {
+    uint32_t hiw = 0;
+#pragma unroll
+    for (int i = 1; i < 8; i++) hiw |= x.v[i];
+    if (!hiw && x.v[0] < (1u << 30)) {
+        out = (int32_t)x.v[0];
+        return true;
+    }
+    const fr_t d = fr_sub(fr_zero(), x);  // r - x
+    hiw = 0;
+#pragma unroll
+    for (int i = 1; i < 8; i++) hiw |= d.v[i];
+    if (!hiw && d.v[0] < (1u << 30)) {
+        out = -(int32_t)d.v[0];
+        return true;
+    }
+    return false;
+}
+// the product x y as a field element (x 1): a Montgomery product lifted by 2^512
+ZDEV fr_t exact_mul(const fr_t& x, const fr_t& y) { return mont_mul_ol(mont_mul_ol(x, y), r2_m()); }
+// eq-specialised: with w = eq(i, u[0..K)) of the pair, S_t U_t = (s0 + t ds)(u0 + t du) is a
+// quadratic in t, so three sums give the round: sum w s0 u0, sum w s1 u1, sum w ds du.  In a
+// round that folds, w s0 and w ds are formed first and the sums carry 2^-256.  In the first
+// round (no fold) the tables still hold the witness' small integers: the three products are
+// formed exactly as 64-bit integers and weighted once each (sums x 1; a pair whose values are
+// not all in (-2^30, 2^30) forms them as exact field products instead).
 __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
                                                     const uint32_t* vmp, EqDev eq, Publish pub) {
     if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
-    __shared__ uint4 accl[4 * NT], acch[4 * NT];
-    LdsAcc<4> acc{accl, acch};
+    __shared__ uint4 accl[3 * NT], acch[3 * NT];
+    LdsAcc<3> acc{accl, acch};
     acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t s0, s1, u0, u1, w;
@@ -1465,31 +1489,45 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             st_fr(U.dlo, U.dhi, i, u0);
             SB();
             u1 = fold_at(U.slo, U.shi, i + h, n, vm);
-        } else {
-            s0 = ld_fr(S.slo, S.shi, i);
-            s1 = ld_fr(S.slo, S.shi, i + h);
-            u0 = ld_fr(U.slo, U.shi, i);
-            w = eq_w(eq, i);
+            st_fr(U.dlo, U.dhi, i + h, u1);
             SB();
-            u1 = ld_fr(U.slo, U.shi, i + h);
+            const fr_t ws = mont_mul_ol(w, s0);
+            SB();
+            const fr_t wds = mont_mul_ol(w, fr_sub(s1, s0));
+            acc.add(0, mont_mul_ol(ws, u0));
+            SB();
+            acc.add(1, mont_mul_ol(fr_add(ws, wds), u1));
+            SB();
+            acc.add(2, mont_mul_ol(wds, fr_sub(u1, u0)));
+            SB();
+            continue;
         }
-        fr_t ws = mont_mul_ol(w, s0);
-        if (fold) st_fr(U.dlo, U.dhi, i + h, u1);
+        s0 = ld_fr(S.slo, S.shi, i);
+        s1 = ld_fr(S.slo, S.shi, i + h);
+        u0 = ld_fr(U.slo, U.shi, i);
+        u1 = ld_fr(U.slo, U.shi, i + h);
+        w = eq_w(eq, i);
         SB();
-        const fr_t wds = mont_mul_ol(w, fr_sub(s1, s0));
-        acc.add(0, mont_mul_ol(ws, u0));
+        fr_t p0, p1, pd;
+        int32_t a0, a1, b0, b1;
+        if (small_int(s0, a0) && small_int(s1, a1) && small_int(u0, b0) && small_int(u1, b1)) {
+            p0 = fr_from_i64((int64_t)a0 * b0);
+            p1 = fr_from_i64((int64_t)a1 * b1);
+            pd = fr_from_i64((int64_t)(a1 - a0) * (b1 - b0));
+        } else {
+            p0 = exact_mul(s0, u0);
+            p1 = exact_mul(s1, u1);
+            pd = exact_mul(fr_sub(s1, s0), fr_sub(u1, u0));
+        }
         SB();
-        const fr_t du = fr_sub(u1, u0);
-        ws = fr_add(ws, wds);
-        u0 = fr_add(u0, du);
-        const fr_t ws2 = fr_add(ws, wds), u2 = fr_add(u0, du);
-        acc.add(1, mont_mul_ol(ws, u0));
-        acc.add(2, mont_mul_ol(ws2, u2));
+        acc.add(0, mont_mul_ol(w, p0));
         SB();
-        acc.add(3, mont_mul_ol(fr_add(ws2, wds), fr_add(u2, du)));
+        acc.add(1, mont_mul_ol(w, p1));
+        SB();
+        acc.add(2, mont_mul_ol(w, pd));
         SB();
     }
-    reduce_publish_lds<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish_lds<3>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial) {

@@ -199,7 +199,8 @@ uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
 // generic with U = 1 everywhere: sums e0*s0, e1*s1, de*ds (x 2^-256); U is not touched
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
                               const uint32_t* vmp, Publish pub);
-// eq-specialised: sums_t = sum eq(i,u_)*S_t*U_t, t = 0..3 (x 2^-256)
+// eq-specialised: sums w*s0*u0, w*s1*u1, w*ds*du with w = eq(i,u_) (x 2^-256 when folding,
+// x 1 in the first round)
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub);
 // sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)

@@ -3471,12 +3471,17 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         } else if (!ueq) {
             pub_read(c, 0, 4, sums);
             for (int t = 0; t < 4; t++) e[t] = fix2(sums[t]);
-        } else {
-            pub_read(c, 0, 4, sums);
+        } else {  // sum_t = c0 + c1 t + c2 t^2 from sum w s0u0, w s1u1, w ds du (x 1 in round 0)
+            pub_read(c, 0, 3, sums);
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
             Fr f = fr_mul(cE, eq_corr(eq, K));
-            for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(fix1(sums[t]), f), fr_eq2(ul, fr_u64(t)));
+            auto unfix = [&](const Fr& x) { return fold ? fix1(x) : x; };
+            const Fr c0 = unfix(sums[0]), c2 = unfix(sums[2]), c1 = fr_sub(fr_sub(unfix(sums[1]), c0), c2);
+            for (int t = 0; t < 4; t++) {
+                const Fr st = fr_add(c0, fr_mul(fr_u64(t), fr_add(c1, fr_mul(fr_u64(t), c2))));
+                e[t] = fr_mul(fr_mul(st, f), fr_eq2(ul, fr_u64(t)));
+            }
         }
         if (!fr_eq(claim, fr_add(e[0], e[1])))
             return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r);
