@@ -910,11 +910,12 @@ def main():
                           "scope": "dominant kernel class of the SwiGLU segment (the layer's largest), "
                                    "algorithmic bytes over launch-stamped time"}
         if gdom == "lu_phase2":
-            # the same launches against the Montgomery-multiply peak: per pair 15 products in
-            # the first round (eq weight, 5 (A, S) and 9 (B, T, m) products) and 25 after it
-            # (the owed folds of A, S, B, T, m: 2 per table)
+            # the same launches against the Montgomery-multiply peak: per pair 9 products in
+            # the first round (A = 1/(comb + beta) and B = 1/(T_comb + beta) take the closed
+            # form: 3 for (A, S) and 6 for (B, T, m), eq weights included) and 25 after it (the
+            # general round's 6 + 9 and the owed folds of A, S, B, T, m, 2 per table)
             pairs = [(glu.D >> r) // 2 for r in range(int(gla))]
-            prods = sum(p * (15 if r == 0 else 25) for r, p in enumerate(pairs))
+            prods = sum(p * (9 if r == 0 else 25) for r, p in enumerate(pairs))
             rate = prods / (gms / 1000.0)
             layer_roofline["valu"] = {
                 "products_per_segment": prods, "achieved_Gmul_s": round(rate / 1e9, 1),
