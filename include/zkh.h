@@ -141,7 +141,7 @@ int zkh_transcript_init(uint8_t state[32], const char* seed, size_t seed_len);
 int zkh_transcript_absorb(uint8_t state[32], const char* label, size_t label_len,
                           const void* data, size_t len);
 int zkh_transcript_challenge_fr(uint8_t state[32], uint32_t out[8]);
-/* fs_challenge_vec (vrf_common.cuh:247-250): n challenges drawn in sequence, out: n Fr */
+/* fs_challenge_vec (vrf_common.cuh:246-250): n challenges drawn in sequence, out: n Fr */
 int zkh_transcript_challenge_vec(uint8_t state[32], uint32_t n, uint32_t* out);
 
 /* ---------------- matmul sumcheck: zkob_fc.cu:259-440 ----------------
