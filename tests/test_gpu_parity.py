@@ -474,6 +474,36 @@ def test_lu_prove(zkh, ctx, shape):
     assert bytes(st_g2) == bytes(st_o)
 
 
+@pytest.mark.parametrize("D,N,zeros", [(1 << 16, 1 << 16, ()), (1 << 16, 1 << 12, ()),
+                                        (1 << 16, 1 << 16, (14, 13)), (1 << 16, 1 << 12, (15, 11, 3))])
+def test_lu_prove_derived_rounds(zkh, ctx, D, N, zeros):
+    """Tables above the persistent loop's size: the folding rounds leave their sums at 1 to the
+    pieces' claims (phase 1, the phase-1 -> 2 round, phase 2).  Coordinates of u set to 0 make
+    those rounds compute every sum instead.  Proofs and terminals equal the oracle's."""
+    low, ln = -(N // 2), N
+    rng = np.random.default_rng(D + N + len(zeros))
+    vals = rng.integers(low, low + ln, size=D).astype(np.int32)
+    S = C.ints_to_fr(vals)
+    T = C.range_table(low, ln, N)
+    rc, m = C.lu_prep(S, low, N)
+    assert rc == 0
+    beta, alpha = rand_fr_full(rng, 2)
+    logD = P.ceil_log2(D)
+    u = rand_fr_full(rng, logD)
+    for z in zeros:
+        u[z] = 0
+    A = C.lu_inverse(S, beta)
+    st_g, st_o = seed_transcript(zkh, "lud:%d:%d:%d" % (D, N, len(zeros)))
+    rc, want = C.lu_prove(st_o, A, S, T, m, alpha, beta, u)
+    assert rc == 0
+    Sg = ctx.from_i32(vals)
+    got = ctx.lu_prove(st_g, ctx.lu_inverse(Sg, beta), Sg, ctx.range_table(low, ln, N), ctx.from_fr(m),
+                       alpha, beta, u)
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
 @pytest.mark.parametrize("D,N,skew", [(1000, 64, 0), (70000, 16384, 1), (1 << 17, 40000, 1), (1 << 17, 40000, 0),
                                        (300000, 1 << 16, 1), (1 << 18, 1 << 24, 1)])
 def test_lu_prep_histogram(zkh, ctx, D, N, skew):
@@ -553,6 +583,34 @@ def test_hp_prove(zkh, ctx, k):
     claim = C.ints_to_fr([sum(a * b % P.R * c for a, b, c in zip(Ei, Si, Ui)) % P.R])[0]
     for eqform in (False, True):
         st_g, st_o = seed_transcript(zkh, "hp:%d" % k)
+        rc, want = C.hp_prove(st_o, claim, E, S, U)
+        assert rc == 0
+        if eqform:
+            got = ctx.hp_prove_eq(st_g, claim, u, ctx.from_fr(S), ctx.from_fr(U))
+        else:
+            got = ctx.hp_prove(st_g, claim, ctx.from_fr(E), ctx.from_fr(S), ctx.from_fr(U))
+        for key in ("ev", "term", "ws"):
+            assert fr_eq(got[key], want[key]), (key, eqform)
+        assert bytes(st_g) == bytes(st_o)
+
+
+@pytest.mark.parametrize("k,zeros", [(16, ()), (16, (14, 13)), (17, (15,))])
+def test_hp_prove_derived_rounds(zkh, ctx, k, zeros):
+    """Tables above the persistent loop's size (explicit E and eq form): the folding rounds leave
+    their sum at 1 to the host (claim - p(0), or the inner claim of the eq form); a coordinate
+    of u set to 0 makes the eq form's round compute all three sums.  Proofs equal the oracle's."""
+    n = 1 << k
+    rng = np.random.default_rng(300 + k + len(zeros))
+    u = rand_fr_full(rng, k)
+    for z in zeros:
+        u[z] = 0
+    E = C.build_eq(u)
+    S = rand_fr_full(rng, n)
+    U = rand_fr_full(rng, n)
+    Ei, Si, Ui = C.fr_to_ints(E), C.fr_to_ints(S), C.fr_to_ints(U)
+    claim = C.ints_to_fr([sum(a * b % P.R * c for a, b, c in zip(Ei, Si, Ui)) % P.R])[0]
+    for eqform in (False, True):
+        st_g, st_o = seed_transcript(zkh, "hpd:%d:%d" % (k, len(zeros)))
         rc, want = C.hp_prove(st_o, claim, E, S, U)
         assert rc == 0
         if eqform:

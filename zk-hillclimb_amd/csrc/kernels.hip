@@ -1094,19 +1094,23 @@ ZDEV void lds_tree(const LdsAcc<K>& acc) {
 // reduce_publish over LDS accumulators: the block's sums by an LDS tree; a job of one block
 // writes them to the host directly, otherwise the last block of the job adds the partials
 // (thread t takes blocks t, t + NT, ...) with the same tree.  Same completion protocol.
+// The last-block flag travels through entry 1 of plane 0, dead after the tree, so that the
+// block's LDS is exactly its accumulators (K = 4 at 256 threads: 32 KiB, 5 blocks per CU).
 template <int K>
 ZDEV void reduce_publish_lds(const LdsAcc<K>& acc, const Publish& P, uint32_t job, uint32_t first, uint32_t nblk,
                              uint32_t local) {
-    __shared__ int is_last;
+    static_assert(NT >= 2, "the flag needs a second entry");
     lds_tree<K>(acc);
     if (nblk > 1) {
         if (threadIdx.x < K) st_aos(P.part, (first + local) * K + threadIdx.x, ld_fr(acc.lo + threadIdx.x * NT, acc.hi + threadIdx.x * NT, 0));
         __syncthreads();
         if (threadIdx.x == 0) {
             __threadfence();
-            is_last = atomicAdd(&P.counter[job], 1u) == nblk - 1;
+            acc.lo[1].x = atomicAdd(&P.counter[job], 1u) == nblk - 1;
         }
         __syncthreads();
+        const bool is_last = acc.lo[1].x != 0;
+        __syncthreads();  // every thread has the flag before the entries are reused
         if (!is_last) return;
         __threadfence();
 #pragma unroll
@@ -1169,60 +1173,6 @@ ZDEV void lu_as_inverse(const TabDev& A, const TabDev& S, uint32_t i, uint32_t h
     inverse_pair_sums<5>(a0, a1, s0, s1, w, acc);
     SB();
 }
-// phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused):
-// acc 0..2: sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256); acc 3, 4: sum a0, sum a1
-__global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, int fold, fr_t vm,
-                                                  const uint32_t* vmp, fr_t beta, EqDev eq, Publish pub, int inv) {
-    if (!relayed_vm(vmp, vm)) return;
-    const uint32_t h = n >> 1;
-    __shared__ uint4 accl[5 * NT], acch[5 * NT];
-    LdsAcc<5> acc{accl, acch};
-    acc.zero();
-    if (inv && !fold) {  // A = 1/(S + beta) unfolded: see lu_as_inverse
-        for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) lu_as_inverse(A, S, i, h, eq, acc);
-        reduce_publish_lds<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
-        return;
-    }
-    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
-        fr_t wa0, wda;
-        {
-            fr_t a0, a1;
-            load_pair(A, i, h, n, fold, vm, a0, a1);
-            SB();
-            acc.add(3, a0);
-            acc.add(4, a1);
-            SB();
-            const fr_t w = eq_w(eq, i);
-            SB();
-            wa0 = mont_mul_ol(w, a0);
-            SB();
-            wda = mont_mul_ol(w, fr_sub(a1, a0));
-        }
-        SB();
-        fr_t s0, s1;
-        load_pair(S, i, h, n, fold, vm, s0, s1);
-        SB();
-        s0 = fr_add(s0, beta);
-        s1 = fr_add(s1, beta);
-        acc.add(0, mont_mul_ol(wa0, s0));
-        SB();
-        acc.add(1, mont_mul_ol(fr_add(wa0, wda), s1));
-        SB();
-        acc.add(2, mont_mul_ol(wda, fr_sub(s1, s0)));
-        SB();
-    }
-    reduce_publish_lds<5>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
-}
-uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
-                          const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
-                          Publish partial, int inv) {
-    const uint32_t g = grid_for(n >> 1, NT, 1024);
-    fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
-    EqDev e{eq.elo, eq.ehi, eq.K};
-    k_lu_phase1<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, fold, vm, vmp, to_fr(beta_host), e, partial, inv);
-    return g;
-}
-
 // phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused), one launch whose
 // blocks [0, ga) take the (A, S) group and blocks [ga, ga + gb) the (B, T, m) group,
 // publishing as jobs 0 and 1 of one round (each group keeps its fold, weights and sums in
@@ -1231,11 +1181,44 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
 // pair (6 / 9 Montgomery products, 10 / 15 with the folds):
 // job 0 (A, S): sum w*a0*s0, w*a1*s1, w*da*ds (x 2^-256), sum a0, sum a1  (s + beta)
 // job 1 (B, T, m): sum w*b0*t0, w*b1*t1, w*db*dt, m0*b0, m1*b1, dm*db (x 2^-256)  (t + beta)
-template <int fold>
+// derive (folding groups only): the sums at 1 are left out, the host taking them from the
+// previous round's claims of each piece (q(0)(1 - u) + q(1) u = claim for the eq-weighted
+// pieces, q(0) + q(1) = claim for the plain ones):
+// job 0: sum w*a0*s0, w*da*ds, a0;  job 1: sum w*b0*t0, w*db*dt, m0*b0, dm*db
+template <int fold, int derive>
 ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t& vm, const fr_t& beta,
                        const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint4* accl, uint4* acch,
                        int inv) {
     const uint32_t h = n >> 1;
+    if constexpr (derive) {
+        LdsAcc<3> acc{accl, acch};
+        acc.zero();
+        for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
+            fr_t wa0, wda;
+            {
+                fr_t a0, a1;
+                load_pair(A, i, h, n, 1, vm, a0, a1);
+                SB();
+                acc.add(2, a0);
+                SB();
+                const fr_t w = eq_w(eq, i);
+                SB();
+                wa0 = mont_mul_ol(w, a0);
+                SB();
+                wda = mont_mul_ol(w, fr_sub(a1, a0));
+            }
+            SB();
+            fr_t s0, s1;
+            load_pair(S, i, h, n, 1, vm, s0, s1);
+            SB();
+            acc.add(0, mont_mul_ol(wa0, fr_add(s0, beta)));
+            SB();
+            acc.add(1, mont_mul_ol(wda, fr_sub(s1, s0)));
+            SB();
+        }
+        reduce_publish_lds<3>(acc, pub, 0, 0, g, lb);
+        return;
+    }
     LdsAcc<5> acc{accl, acch};
     acc.zero();
     if (!fold && inv) {
@@ -1271,11 +1254,48 @@ ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t&
     }
     reduce_publish_lds<5>(acc, pub, 0, 0, g, lb);
 }
-template <int fold>
+template <int fold, int derive>
 ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const fr_t& vm,
                         const fr_t& beta, const EqDev& eq, const Publish& pub, uint32_t lb, uint32_t g, uint32_t ga,
                         uint4* accl, uint4* acch, int inv) {
     const uint32_t h = n >> 1;
+    // partials after the (A, S) group's ga entries of K_as <= K sums: indices (ga + lb) * K + k
+    if constexpr (derive) {
+        LdsAcc<4> acc{accl, acch};
+        acc.zero();
+        for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
+            fr_t b0, b1;
+            load_pair(B, i, h, n, 1, vm, b0, b1);
+            SB();
+            {
+                fr_t m0, m1;
+                load_pair(m, i, h, n, 1, vm, m0, m1);
+                SB();
+                acc.add(2, mont_mul_ol(m0, b0));
+                SB();
+                acc.add(3, mont_mul_ol(fr_sub(m1, m0), fr_sub(b1, b0)));
+            }
+            SB();
+            fr_t wb0, wdb;
+            {
+                const fr_t w = eq_w(eq, i);
+                SB();
+                wb0 = mont_mul_ol(w, b0);
+                SB();
+                wdb = mont_mul_ol(w, fr_sub(b1, b0));
+            }
+            SB();
+            fr_t t0, t1;
+            load_pair(T, i, h, n, 1, vm, t0, t1);
+            SB();
+            acc.add(0, mont_mul_ol(wb0, fr_add(t0, beta)));
+            SB();
+            acc.add(1, mont_mul_ol(wdb, fr_sub(t1, t0)));
+            SB();
+        }
+        reduce_publish_lds<4>(acc, pub, 1, ga, g, lb);
+        return;
+    }
     LdsAcc<6> acc{accl, acch};
     acc.zero();
     if (!fold && inv) {  // B = 1/(T + beta) unfolded (see inverse_pair_sums); 3..5 as below
@@ -1334,43 +1354,81 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
         acc.add(2, mont_mul_ol(wdb, fr_sub(t1, t0)));
         SB();
     }
-    // partials after the (A, S) group's 5 ga entries: indices (ga + lb) * 6 + k >= 6 ga
     reduce_publish_lds<6>(acc, pub, 1, ga, g, lb);
 }
-template <int fold_as, int fold_btm>
+// phase 1 (tlookup.cu:74-104 poly + reduce kernels, fused): the (A, S) group of phase 2 over
+// the whole grid, same sums (derive as there)
+template <int fold, int derive>
+__global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n, fr_t vm, const uint32_t* vmp,
+                                                  fr_t beta, EqDev eq, Publish pub, int inv) {
+    if (!relayed_vm(vmp, vm)) return;
+    constexpr int K = derive ? 3 : 5;
+    __shared__ uint4 accl[K * NT], acch[K * NT];
+    lu_phase2_as<fold, derive>(A, S, n, vm, beta, eq, pub, blockIdx.x, gridDim.x, accl, acch, inv);
+}
+uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
+                          const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
+                          Publish partial, int inv, int derive) {
+    const uint32_t g = grid_for(n >> 1, NT, 1024);
+    fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
+    EqDev e{eq.elo, eq.ehi, eq.K};
+    const fr_t beta = to_fr(beta_host);
+    if (fold && derive) k_lu_phase1<1, 1><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, vmp, beta, e, partial, inv);
+    else if (fold) k_lu_phase1<1, 0><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, vmp, beta, e, partial, inv);
+    else k_lu_phase1<0, 0><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, vmp, beta, e, partial, inv);
+    return g;
+}
+// per-thread accumulator slots of a phase-2 launch: the larger group's
+template <int fold_as, int fold_btm, int derive>
+constexpr int lu2_slots() {
+    return (derive && fold_btm) ? 4 : 6;
+}
+template <int fold_as, int fold_btm, int derive>
 __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m, uint32_t n,
                                                   fr_t vm, const uint32_t* vmp, fr_t beta, EqDev eq, Publish pub,
                                                   uint32_t ga, uint32_t gb, int inv_as, int inv_btm) {
     if (!relayed_vm(vmp, vm)) return;
-    __shared__ uint4 accl[6 * NT], acch[6 * NT];
-    if (blockIdx.x < ga) lu_phase2_as<fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, ga, accl, acch, inv_as);
-    else lu_phase2_btm<fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - ga, gb, ga, accl, acch, inv_btm);
+    constexpr int K = lu2_slots<fold_as, fold_btm, derive>();
+    __shared__ uint4 accl[K * NT], acch[K * NT];
+    if (blockIdx.x < ga) lu_phase2_as<fold_as, derive && fold_as>(A, S, n, vm, beta, eq, pub, blockIdx.x, ga, accl, acch, inv_as);
+    else lu_phase2_btm<fold_btm, derive && fold_btm>(B, T, m, n, vm, beta, eq, pub, blockIdx.x - ga, gb, ga, accl, acch, inv_btm);
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host,
-                          EqW eq, Publish partial, int inv_as, int inv_btm) {
-    const uint32_t ga = grid_for(n >> 1, NT, LU2_GRID * 2 / 5), gb = grid_for(n >> 1, NT, LU2_GRID * 3 / 5);
+                          EqW eq, Publish partial, int inv_as, int inv_btm, int derive) {
+    // the derived variant holds 5 blocks per CU (32 KiB of accumulators): one resident wave
+    const uint32_t G = derive && fold_as && fold_btm ? 1280 : LU2_GRID;
+    const uint32_t ga = grid_for(n >> 1, NT, G * 2 / 5), gb = grid_for(n >> 1, NT, G * 3 / 5);
     const fr_t vm = (fold_as || fold_btm) && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
     const fr_t beta = to_fr(beta_host);
     const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T), md = tab_dev(m);
     const uint32_t g = ga + gb;
-    if (fold_as && fold_btm) k_lu_phase2<1, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
-    else if (fold_as) k_lu_phase2<1, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
-    else if (fold_btm) k_lu_phase2<0, 1><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
-    else k_lu_phase2<0, 0><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm);
+#define LU2(FA, FB, DV) k_lu_phase2<FA, FB, DV><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm)
+    if (fold_as && fold_btm) {
+        if (derive) LU2(1, 1, 1);
+        else LU2(1, 1, 0);
+    } else if (fold_as) {
+        if (derive) LU2(1, 0, 1);
+        else LU2(1, 0, 0);
+    } else if (fold_btm) LU2(0, 1, 0);
+    else LU2(0, 0, 0);
+#undef LU2
     return g;
 }
 
 // ------------------------------------------------------------------------------------
 // Hadamard sumcheck rounds (zkob_lookup.cuh:212-233 k_hp3_step + k_fr_fold, fused)
 // ------------------------------------------------------------------------------------
+// derive (folding rounds): the sum at t = 1 is left out (the host takes it as claim - sum_0)
+template <int derive>
 __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, uint32_t n, int fold,
                                                  fr_t vm, const uint32_t* vmp, Publish pub) {
     if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
-    __shared__ uint4 accl[4 * NT], acch[4 * NT];
-    LdsAcc<4> acc{accl, acch};
+    constexpr int K = derive ? 3 : 4;
+    __shared__ uint4 accl[K * NT], acch[K * NT];
+    LdsAcc<K> acc{accl, acch};
     acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t e0, e1, s0, s1;
@@ -1379,11 +1437,11 @@ __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, u
         load_pair(S, i, h, n, fold, vm, s0, s1);
         SB();
         const fr_t de = fr_sub(e1, e0), ds = fr_sub(s1, s0);
-        // es_t = E_t * S_t (x 2^-256) for t = 0..3
+        // es_t = E_t * S_t (x 2^-256) for t = 0..3 (t = 1 skipped under derive)
         fr_t es[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            es[t] = mont_mul_ol(e0, s0);
+            if (!derive || t != 1) es[t] = mont_mul_ol(e0, s0);
             SB();
             if (t < 3) {
                 e0 = fr_add(e0, de);
@@ -1396,29 +1454,33 @@ __global__ __launch_bounds__(NT) void k_hp_round(TabDev E, TabDev S, TabDev U, u
         const fr_t du = fr_sub(u1, u0);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            acc.add(t, mont_mul_ol(es[t], u0));
+            if (!derive || t != 1) acc.add(derive && t > 1 ? t - 1 : t, mont_mul_ol(es[t], u0));
             SB();
             if (t < 3) u0 = fr_add(u0, du);
         }
     }
-    reduce_publish_lds<4>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fold,
-                         const uint32_t* v_m_host, const uint32_t* vmp, Publish partial) {
+                         const uint32_t* v_m_host, const uint32_t* vmp, Publish partial, int derive) {
     uint32_t g = grid_for(n >> 1, NT * 2, 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
-    k_hp_round<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, vmp, partial);
+    if (fold && derive) k_hp_round<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, vmp, partial);
+    else k_hp_round<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, vmp, partial);
     return g;
 }
 // U = 1 everywhere (the RoPE obligations' Hadamard): E_t S_t U_t = E_t S_t, a quadratic in t
 // from three products per pair: sums e0 s0, e1 s1, (e1 - e0)(s1 - s0) (x 2^-256).  U is
 // neither read nor folded (every fold of an all-ones table is all ones).
+// derive (folding rounds): sum e1 s1 is left out (the host takes it as claim - sum e0 s0)
+template <int derive>
 __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32_t n, int fold, fr_t vm,
                                                       const uint32_t* vmp, Publish pub) {
     if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
-    __shared__ uint4 accl[3 * NT], acch[3 * NT];
-    LdsAcc<3> acc{accl, acch};
+    constexpr int K = derive ? 2 : 3;
+    __shared__ uint4 accl[K * NT], acch[K * NT];
+    LdsAcc<K> acc{accl, acch};
     acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t e0, e1, s0, s1;
@@ -1428,18 +1490,21 @@ __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32
         SB();
         acc.add(0, mont_mul_ol(e0, s0));
         SB();
-        acc.add(1, mont_mul_ol(e1, s1));
-        SB();
-        acc.add(2, mont_mul_ol(fr_sub(e1, e0), fr_sub(s1, s0)));
+        if constexpr (!derive) {
+            acc.add(1, mont_mul_ol(e1, s1));
+            SB();
+        }
+        acc.add(K - 1, mont_mul_ol(fr_sub(e1, e0), fr_sub(s1, s0)));
         SB();
     }
-    reduce_publish_lds<3>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
-                              const uint32_t* vmp, Publish partial) {
+                              const uint32_t* vmp, Publish partial, int derive) {
     uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
-    k_hp_round_ones<<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial);
+    if (fold && derive) k_hp_round_ones<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial);
+    else k_hp_round_ones<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial);
     return g;
 }
 // x as an integer in (-2^30, 2^30) when it is one (a field element or its negative)
@@ -1469,12 +1534,16 @@ ZDEV fr_t exact_mul(const fr_t& x, const fr_t& y) { return mont_mul_ol(mont_mul_
 // round (no fold) the tables still hold the witness' small integers: the three products are
 // formed exactly as 64-bit integers and weighted once each (sums x 1; a pair whose values are
 // not all in (-2^30, 2^30) forms them as exact field products instead).
+// derive (folding rounds): sum w s1 u1 is left out (the host takes it from the previous
+// round's claim, q(0)(1 - u) + q(1) u)
+template <int derive>
 __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
                                                     const uint32_t* vmp, EqDev eq, Publish pub) {
     if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
-    __shared__ uint4 accl[3 * NT], acch[3 * NT];
-    LdsAcc<3> acc{accl, acch};
+    constexpr int K = derive ? 2 : 3;
+    __shared__ uint4 accl[K * NT], acch[K * NT];
+    LdsAcc<K> acc{accl, acch};
     acc.zero();
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t s0, s1, u0, u1, w;
@@ -1496,45 +1565,50 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             const fr_t wds = mont_mul_ol(w, fr_sub(s1, s0));
             acc.add(0, mont_mul_ol(ws, u0));
             SB();
-            acc.add(1, mont_mul_ol(fr_add(ws, wds), u1));
-            SB();
-            acc.add(2, mont_mul_ol(wds, fr_sub(u1, u0)));
+            if constexpr (!derive) {
+                acc.add(1, mont_mul_ol(fr_add(ws, wds), u1));
+                SB();
+            }
+            acc.add(K - 1, mont_mul_ol(wds, fr_sub(u1, u0)));
             SB();
             continue;
         }
-        s0 = ld_fr(S.slo, S.shi, i);
-        s1 = ld_fr(S.slo, S.shi, i + h);
-        u0 = ld_fr(U.slo, U.shi, i);
-        u1 = ld_fr(U.slo, U.shi, i + h);
-        w = eq_w(eq, i);
-        SB();
-        fr_t p0, p1, pd;
-        int32_t a0, a1, b0, b1;
-        if (small_int(s0, a0) && small_int(s1, a1) && small_int(u0, b0) && small_int(u1, b1)) {
-            p0 = fr_from_i64((int64_t)a0 * b0);
-            p1 = fr_from_i64((int64_t)a1 * b1);
-            pd = fr_from_i64((int64_t)(a1 - a0) * (b1 - b0));
-        } else {
-            p0 = exact_mul(s0, u0);
-            p1 = exact_mul(s1, u1);
-            pd = exact_mul(fr_sub(s1, s0), fr_sub(u1, u0));
+        if constexpr (!derive) {
+            s0 = ld_fr(S.slo, S.shi, i);
+            s1 = ld_fr(S.slo, S.shi, i + h);
+            u0 = ld_fr(U.slo, U.shi, i);
+            u1 = ld_fr(U.slo, U.shi, i + h);
+            w = eq_w(eq, i);
+            SB();
+            fr_t p0, p1, pd;
+            int32_t a0, a1, b0, b1;
+            if (small_int(s0, a0) && small_int(s1, a1) && small_int(u0, b0) && small_int(u1, b1)) {
+                p0 = fr_from_i64((int64_t)a0 * b0);
+                p1 = fr_from_i64((int64_t)a1 * b1);
+                pd = fr_from_i64((int64_t)(a1 - a0) * (b1 - b0));
+            } else {
+                p0 = exact_mul(s0, u0);
+                p1 = exact_mul(s1, u1);
+                pd = exact_mul(fr_sub(s1, s0), fr_sub(u1, u0));
+            }
+            SB();
+            acc.add(0, mont_mul_ol(w, p0));
+            SB();
+            acc.add(1, mont_mul_ol(w, p1));
+            SB();
+            acc.add(2, mont_mul_ol(w, pd));
+            SB();
         }
-        SB();
-        acc.add(0, mont_mul_ol(w, p0));
-        SB();
-        acc.add(1, mont_mul_ol(w, p1));
-        SB();
-        acc.add(2, mont_mul_ol(w, pd));
-        SB();
     }
-    reduce_publish_lds<3>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+    reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial) {
-    const uint32_t g = grid_for(n >> 1, NT, 1024);
+                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial, int derive) {
+    const uint32_t g = grid_for(n >> 1, NT, fold && derive ? 1280 : 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
-    k_hp_eq_round<<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, vmp, e, partial);
+    if (fold && derive) k_hp_eq_round<1><<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, vmp, e, partial);
+    else k_hp_eq_round<0><<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, vmp, e, partial);
     return g;
 }
 // sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n, by chunks of 1024 indices sharing their

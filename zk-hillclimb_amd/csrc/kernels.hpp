@@ -180,29 +180,35 @@ void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 // phase-1 round over A, S (size n): sums e*a0*s0, e*a1*s1, e*da*ds (x 2^-256), a0, a1
 // inv: A is 1/(S + beta) entry-wise and no fold is owed: sums 0 and 1 become sum_{a != 0} w
 // with w = e 2^256 (sum e after one Montgomery reduction), two products per pair fewer
+// derive (with fold): the sums at 1 are left out: e*a0*s0, e*da*ds, a0 (see kernels.hip)
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
-                          Publish pub, int inv);
+                          Publish pub, int inv, int derive);
 // phase-2 round over A, S, B, T, m as two launches publishing jobs 0 (A, S: 5 sums) and
 // 1 (B, T, m: 6 sums) of `pub` (made for 2 jobs; see kernels.hip)
 // inv_as / inv_btm: A = 1/(S + beta) / B = 1/(T + beta) with that group's fold not owed, as
 // inv of launch_lu_phase1 (sums 0, 1 of the group then carry 2^256 instead of 2^-256)
+// derive: the folding groups leave out their sums at 1: job 0 publishes 3 sums (w*a0*s0,
+// w*da*ds, a0), job 1 (when it folds) 4 (w*b0*t0, w*db*dt, m0*b0, dm*db)
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
                           int fold_as, int fold_btm,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
-                          Publish pub, int inv_as, int inv_btm);
+                          Publish pub, int inv_as, int inv_btm, int derive);
 
 // ---- Hadamard ----
-// generic: sums_t = sum E_t*S_t*U_t, t = 0..3 (x 2^-512)
+// With derive (folding rounds only) each Hadamard round kernel leaves out its sum at t = 1,
+// which the host takes from the previous round's claim.
+// generic: sums_t = sum E_t*S_t*U_t, t = 0..3 (x 2^-512); derive: t = 0, 2, 3
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
-                         int fold, const uint32_t* v_m_host, const uint32_t* vmp, Publish pub);
-// generic with U = 1 everywhere: sums e0*s0, e1*s1, de*ds (x 2^-256); U is not touched
+                         int fold, const uint32_t* v_m_host, const uint32_t* vmp, Publish pub, int derive);
+// generic with U = 1 everywhere: sums e0*s0, e1*s1, de*ds (x 2^-256); U is not touched;
+// derive: e0*s0, de*ds
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
-                              const uint32_t* vmp, Publish pub);
+                              const uint32_t* vmp, Publish pub, int derive);
 // eq-specialised: sums w*s0*u0, w*s1*u1, w*ds*du with w = eq(i,u_) (x 2^-256 when folding,
-// x 1 in the first round)
+// x 1 in the first round); derive: w*s0*u0, w*ds*du
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub);
+                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub, int derive);
 // sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish pub);

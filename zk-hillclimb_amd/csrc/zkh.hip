@@ -2406,6 +2406,24 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
     return ZKH_OK;
 }
 
+// The logUp round polynomial is a sum of pieces, each itself a sumcheck over the remaining
+// variables: Ia = sum eq A (S + beta), Sa = sum A, Ib = sum eq B (T + beta), Mb = sum m B
+// (eq over the variables after the round's own, the round's eq factor kept outside).  A
+// round's piece q satisfies (1 - u) q(0) + u q(1) = I (eq-weighted) or q(0) + q(1) = I
+// (plain) and binds to I' = q(v), so a round that folds can leave its sums at 1 to the
+// host.  At the end I equals the piece of the terminals.
+struct LuPieces {
+    Fr Ia = kZero, Sa = kZero, Ib = kZero, Mb = kZero;
+    bool b = false;  // Ib, Mb hold (a phase-2 round has run)
+};
+// q(v) of a quadratic piece from q(0), q(1) and its t^2 coefficient c2
+static Fr quad_at(const Fr& q0, const Fr& q1, const Fr& c2, const Fr& v) {
+    return fr_add(q0, fr_mul(v, fr_add(fr_sub(fr_sub(q1, q0), c2), fr_mul(v, c2))));
+}
+// q(1) of an eq-weighted piece with claim I and eq coordinate ul: (I - (1 - ul) q(0)) / ul
+static Fr eq_piece_q1(const Fr& I, const Fr& q0, const Fr& ul, const Fr& inv_ul) {
+    return fr_mul(fr_sub(I, fr_mul(fr_sub(kOne, ul), q0)), inv_ul);
+}
 // logUp phase-2 state carried across rounds (zkob_lookup.cuh:143-198): the running claim,
 // alpha and alpha^2 eq accumulators, N/D, the eq point u and its device tables
 struct LuState {
@@ -2413,6 +2431,7 @@ struct LuState {
     const std::vector<Fr>* u;
     const EqState* eq;
     uint32_t logD;
+    LuPieces* pc;
 };
 // One phase-2 round from its 11 sums (device order: w a s sums 0..2, sum a0, sum a1, w b t
 // sums 0..2, m b sums 0..2).  dev: sums from the device (products x 2^-256, eq weights with
@@ -2453,6 +2472,11 @@ static bool lu_phase2_round(uint8_t tr[32], LuState& L, uint32_t r, const Fr sm[
     const Fr eqv = fr_eq2(ul, v);
     L.alpha = fr_mul(L.alpha, eqv);
     L.alpha_sq = fr_mul(L.alpha_sq, eqv);
+    L.pc->Ia = quad_at(qa0, qa1, qa2, v);
+    L.pc->Sa = fr_add(sm[3], fr_mul(v, fr_sub(sm[4], sm[3])));
+    L.pc->Ib = quad_at(qb0, qb1, qb2, v);
+    L.pc->Mb = quad_at(M0, M1, M2, v);
+    L.pc->b = true;
     return true;
 }
 // Phase-2 rounds r0 .. logD-1 in one persistent launch (see LuPersist) once the tables have
@@ -2660,9 +2684,15 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     // T: a group's first (unfolded) round then needs two products per pair fewer, its sums
     // 0 and 1 coming as sum e over the nonzero entries (cf: no 2^-256 to undo)
     const bool a_is_inv = A->kind == ZKH_KIND_FR && A->inv_of && A->inv_of == S->gen && !memcmp(A->inv_beta, beta_l, 32);
+    // a folding round leaves its sums at 1 to the pieces (LuPieces) unless its eq coordinate
+    // is 0; inv_u holds 1/u_j, computed while the first round runs
+    LuPieces pc;
+    std::vector<Fr> inv_u;
+    auto derives = [&](uint32_t r) { return !fr_eq(u[logD - r - 1], kZero); };
     struct Launched {
         Publish pb;
         bool cf_a, cf_b;
+        bool dv_a, dv_b;  // the group's sums at 1 are left out
     };
     // launches round r (reading the previous challenge from vm, or from the relay when vmp
     // is given) and moves the table handles to the folded copies the launch writes
@@ -2673,10 +2703,11 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         if (n > N) {  // phase 1
             pb = make_pub(c, 1);
             l.cf_a = a_is_inv && !as_pending;
+            l.dv_a = as_pending && derives(r);
             {
                 ProfScope ps(c, "lu_phase1", (as_pending ? 3.0 * n : (double)n) * 2 * 32);
                 launch_lu_phase1(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, n, as_pending, vm, vmp, beta_l,
-                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a);
+                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.dv_a);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -2687,12 +2718,15 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             pb = make_pub(c, 2);
             l.cf_a = a_is_inv && !as_pending;
             l.cf_b = !btm_pending;
+            const bool dv = as_pending && derives(r);
+            l.dv_a = dv;
+            l.dv_b = dv && btm_pending;
             {
                 ProfScope ps(c, "lu_phase2",
                              ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
                 launch_lu_phase2(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
                                  Tab{m_src, mw}, n, as_pending, btm_pending, vm, vmp, beta_l,
-                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b);
+                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b, dv);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -2716,7 +2750,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     for (uint32_t r = 0; r < logD; r++) {
         const uint32_t n = D >> r;
         if (persists(r)) {  // phase 2: the rest in one launch
-            LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD};
+            LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD, &pc};
             const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
             if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, beta_l, ev_out, ws_out, fin)))
                 return rc;
@@ -2737,48 +2771,78 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         const Fr ul = u[k - 1];
         const Fr corr = eq_corr(eq, K);
         Fr coef[4];
+        if (r == 0 && logD > 1) {  // 1/u_j for the rounds that derive (batch inverse, host)
+            inv_u.assign(logD, kZero);
+            std::vector<Fr> pre(logD + 1, kOne);
+            for (uint32_t j = 0; j < logD; j++) pre[j + 1] = fr_eq(u[j], kZero) ? pre[j] : fr_mul(pre[j], u[j]);
+            Fr t = fr_inv(pre[logD]);
+            for (uint32_t j = logD; j-- > 0;)
+                if (!fr_eq(u[j], kZero)) {
+                    inv_u[j] = fr_mul(t, pre[j]);
+                    t = fr_mul(t, u[j]);
+                }
+        }
         if ((rc = wait_pub(c, cur.pb.seq))) return rc;
         if (tracing) tr_t.push_back(now_us());
-        if (n > N) {  // phase 1
+        // the pieces' values at 0 and 1 and their t^2 coefficients (true sums)
+        Fr qa[3], sa[2], qb[3] = {kZero, kZero, kZero}, M[3] = {kZero, kZero, kZero};
+        {
             Fr s[5];
-            pub_read(c, 0, 5, s);
-            Fr q0 = fr_mul(q_of(s[0], cur.cf_a), corr), q1 = fr_mul(q_of(s[1], cur.cf_a), corr),
-               q2 = fr_mul(fix1(s[2]), corr);
-            Fr qc1 = fr_sub(fr_sub(q1, q0), q2);
-            Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
-            Fr aq0 = fr_mul(alpha, q0), aq1 = fr_mul(alpha, qc1), aq2 = fr_mul(alpha, q2);
-            coef[0] = fr_add(fr_add(fr_mul(e0, aq0), s[3]), fr_mul(Cc, inv2));
-            coef[1] = fr_add(fr_add(fr_mul(e0, aq1), fr_mul(e1, aq0)), fr_sub(s[4], s[3]));
+            if (cur.dv_a) {  // w a0 s0, w da ds, a0
+                pub_read(c, 0, 3, s);
+                qa[0] = fr_mul(fix1(s[0]), corr);
+                qa[2] = fr_mul(fix1(s[1]), corr);
+                qa[1] = eq_piece_q1(pc.Ia, qa[0], ul, inv_u[k - 1]);
+                sa[0] = s[2];
+                sa[1] = fr_sub(pc.Sa, s[2]);
+            } else {
+                pub_read(c, 0, 5, s);
+                qa[0] = fr_mul(q_of(s[0], cur.cf_a), corr);
+                qa[1] = fr_mul(q_of(s[1], cur.cf_a), corr);
+                qa[2] = fr_mul(fix1(s[2]), corr);
+                sa[0] = s[3];
+                sa[1] = s[4];
+            }
+        }
+        if (n <= N) {
+            Fr s[6];
+            if (cur.dv_b) {  // w b0 t0, w db dt, m0 b0, dm db
+                pub_read(c, 1, 4, s);
+                qb[0] = fr_mul(fix1(s[0]), corr);
+                qb[2] = fr_mul(fix1(s[1]), corr);
+                qb[1] = eq_piece_q1(pc.Ib, qb[0], ul, inv_u[k - 1]);
+                M[0] = fix1(s[2]);
+                M[2] = fix1(s[3]);
+                M[1] = fr_sub(pc.Mb, M[0]);
+            } else {
+                pub_read(c, 1, 6, s);
+                qb[0] = fr_mul(q_of(s[0], cur.cf_b), corr);
+                qb[1] = fr_mul(q_of(s[1], cur.cf_b), corr);
+                qb[2] = fr_mul(fix1(s[2]), corr);
+                M[0] = fix1(s[3]);
+                M[1] = fix1(s[4]);
+                M[2] = fix1(s[5]);
+            }
+        }
+        const Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
+        if (n > N) {  // phase 1
+            const Fr qc1 = fr_sub(fr_sub(qa[1], qa[0]), qa[2]);
+            const Fr aq0 = fr_mul(alpha, qa[0]), aq1 = fr_mul(alpha, qc1), aq2 = fr_mul(alpha, qa[2]);
+            coef[0] = fr_add(fr_add(fr_mul(e0, aq0), sa[0]), fr_mul(Cc, inv2));
+            coef[1] = fr_add(fr_add(fr_mul(e0, aq1), fr_mul(e1, aq0)), fr_sub(sa[1], sa[0]));
             coef[2] = fr_add(fr_mul(e0, aq2), fr_mul(e1, aq1));
             coef[3] = fr_mul(e1, aq2);
         } else {  // phase 2
-            Fr s[11], sa[5], sb[6];
-            pub_read(c, 0, 5, sa);
-            pub_read(c, 1, 6, sb);
-            // s: w*a*s sums 0..2, w*b*t sums 3..5, sum a0 / a1 6..7, m*b sums 8..10
-            for (int k = 0; k < 3; k++) {
-                s[k] = sa[k];
-                s[3 + k] = sb[k];
-                s[8 + k] = sb[3 + k];
-            }
-            s[6] = sa[3];
-            s[7] = sa[4];
-            Fr qa0 = fr_mul(q_of(s[0], cur.cf_a), corr), qa1 = fr_mul(q_of(s[1], cur.cf_a), corr),
-               qa2 = fr_mul(fix1(s[2]), corr);
-            Fr qb0 = fr_mul(q_of(s[3], cur.cf_b), corr), qb1 = fr_mul(q_of(s[4], cur.cf_b), corr),
-               qb2 = fr_mul(fix1(s[5]), corr);
-            Fr coefBT = fr_mul(inv_ratio, alpha_sq);
-            Fr Q0 = fr_add(fr_mul(alpha, qa0), fr_mul(coefBT, qb0));
-            Fr Q1 = fr_add(fr_mul(alpha, fr_sub(fr_sub(qa1, qa0), qa2)),
-                           fr_mul(coefBT, fr_sub(fr_sub(qb1, qb0), qb2)));
-            Fr Q2 = fr_add(fr_mul(alpha, qa2), fr_mul(coefBT, qb2));
-            Fr M0 = fix1(s[8]), M1 = fix1(s[9]), M2 = fix1(s[10]);
-            Fr Mc1 = fr_sub(fr_sub(M1, M0), M2);
-            Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
-            coef[0] = fr_sub(fr_add(fr_mul(e0, Q0), s[6]), fr_mul(inv_ratio, M0));
-            coef[1] = fr_sub(fr_add(fr_add(fr_mul(e0, Q1), fr_mul(e1, Q0)), fr_sub(s[7], s[6])),
+            const Fr coefBT = fr_mul(inv_ratio, alpha_sq);
+            const Fr Q0 = fr_add(fr_mul(alpha, qa[0]), fr_mul(coefBT, qb[0]));
+            const Fr Q1 = fr_add(fr_mul(alpha, fr_sub(fr_sub(qa[1], qa[0]), qa[2])),
+                                 fr_mul(coefBT, fr_sub(fr_sub(qb[1], qb[0]), qb[2])));
+            const Fr Q2 = fr_add(fr_mul(alpha, qa[2]), fr_mul(coefBT, qb[2]));
+            const Fr Mc1 = fr_sub(fr_sub(M[1], M[0]), M[2]);
+            coef[0] = fr_sub(fr_add(fr_mul(e0, Q0), sa[0]), fr_mul(inv_ratio, M[0]));
+            coef[1] = fr_sub(fr_add(fr_add(fr_mul(e0, Q1), fr_mul(e1, Q0)), fr_sub(sa[1], sa[0])),
                              fr_mul(inv_ratio, Mc1));
-            coef[2] = fr_sub(fr_add(fr_mul(e0, Q2), fr_mul(e1, Q1)), fr_mul(inv_ratio, M2));
+            coef[2] = fr_sub(fr_add(fr_mul(e0, Q2), fr_mul(e1, Q1)), fr_mul(inv_ratio, M[2]));
             coef[3] = fr_mul(e1, Q2);
         }
         Fr e[4] = {coef[0], fr_poly_eval(coef, 3, kOne), fr_poly_eval(coef, 3, fr_u64(2)),
@@ -2798,6 +2862,13 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         alpha = fr_mul(alpha, eqv);
         if (n > N) Cc = fr_mul(Cc, inv2);
         else alpha_sq = fr_mul(alpha_sq, eqv);
+        pc.Ia = quad_at(qa[0], qa[1], qa[2], v);
+        pc.Sa = fr_add(sa[0], fr_mul(v, fr_sub(sa[1], sa[0])));
+        if (n <= N) {
+            pc.Ib = quad_at(qb[0], qb[1], qb[2], v);
+            pc.Mb = quad_at(M[0], M[1], M[2], v);
+            pc.b = true;
+        }
         fr_store(fr_to_mont(v), vm);
         if (relay_next) {
             relay_send(c, relay.pending, vm);
@@ -2838,6 +2909,12 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             HIPCHK(c, hipMemcpyAsync(tv[i] + 4, dfin[i].hi(), 16, hipMemcpyDeviceToHost, c->stream));
         }
         HIPCHK(c, hipStreamSynchronize(c->stream));
+    }
+    if (logD > 0) {  // every piece's claim is its terminal form (checks the rounds whose sums at 1 were derived)
+        const Fr Af = fr_load(tv[0]), Sf = fr_load(tv[1]), Bf = fr_load(tv[2]), Tf = fr_load(tv[3]), mf = fr_load(tv[4]);
+        bool ok = fr_eq(pc.Ia, fr_mul(Af, fr_add(Sf, beta))) && fr_eq(pc.Sa, Af);
+        if (pc.b) ok = ok && fr_eq(pc.Ib, fr_mul(Bf, fr_add(Tf, beta))) && fr_eq(pc.Mb, fr_mul(mf, Bf));
+        if (!ok) return fail(c, ZKH_EROUND, "logUp terminal mismatch (witness bug)");
     }
     if (term_out)
         for (int i = 0; i < 5; i++) memcpy(term_out + 8 * i, tv[i], 32);
@@ -3415,32 +3492,41 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     // U all ones (an I32 tensor measured so at ingest: the RoPE obligations' U = 1) with an
     // explicit E: the per-round kernels skip U, whose folds stay all ones in its source
     const bool u_ones = !ueq && U->kind == ZKH_KIND_I32 && U->ones;
+    // A folding round leaves its sum at 1 to the host: claim - p(0) for an explicit E; with
+    // the eq form, from the inner claim I = sum eq S U over the remaining variables (the
+    // running claim without the eq factor cE) as (I - (1 - u) q(0)) / u, unless u is 0.
+    Fr I = claim;
+    std::vector<Fr> inv_u;  // 1/u_j, computed while the first round runs
+    struct Launched {
+        Publish pb;
+        bool dv;
+    };
     // launches round r (previous challenge from vm, or from the relay when vmp is given) and
     // moves the table handles to the folded copies the launch writes
     auto launch = [&](uint32_t r, const uint32_t* vmp) {
         const uint32_t sz = n >> r;
         const int fold = r > 0;
-        Publish pb = make_pub(c, 1);
+        Launched l{make_pub(c, 1), fold && (!ueq || !fr_eq((*ueq)[k - r - 1], kZero))};
         if (u_ones) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
-            launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, pb);
+            launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, l.pb, l.dv);
         } else if (!ueq) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
-            launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp, pb);
+            launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp, l.pb, l.dv);
         } else {
             ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
             launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp,
-                               EqW{eq.elo_d, eq.ehi_d, k - r - 1}, pb);
+                               EqW{eq.elo_d, eq.ehi_d, k - r - 1}, l.pb, l.dv);
         }
         if (fold) {
             e_src = Ew;
             s_src = Sw;
             if (!u_ones) u_src = Uw;
         }
-        return pb;
+        return l;
     };
     RelayGuard relay{c};
-    Publish pb{};
+    Launched cur{};
     bool launched = false;  // round r is already queued
     for (uint32_t r = 0; r < k; r++) {
         const uint32_t sz = n >> r;
@@ -3453,34 +3539,75 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             break;
         }
         if (tracing) tr_t.push_back(now_us());
-        if (!launched) pb = launch(r, nullptr);
+        if (!launched) cur = launch(r, nullptr);
         // round r + 1 goes behind a relay now, so that its launch overlaps this round
         const bool relay_next = r + 1 < k && !persists(r + 1);
-        Publish pb_next{};
+        Launched next{};
         if (relay_next) {
             relay.pending = relay_enqueue(c);
-            pb_next = launch(r + 1, c->relay_vm);
+            next = launch(r + 1, c->relay_vm);
+        }
+        if (r == 0 && ueq && k > 1) {  // 1/u_j for the rounds that derive (batch inverse, host)
+            inv_u.assign(k, kZero);
+            std::vector<Fr> pre(k + 1, kOne);
+            for (uint32_t j = 0; j < k; j++) pre[j + 1] = fr_eq((*ueq)[j], kZero) ? pre[j] : fr_mul(pre[j], (*ueq)[j]);
+            Fr t = fr_inv(pre[k]);
+            for (uint32_t j = k; j-- > 0;)
+                if (!fr_eq((*ueq)[j], kZero)) {
+                    inv_u[j] = fr_mul(t, pre[j]);
+                    t = fr_mul(t, (*ueq)[j]);
+                }
         }
         Fr e[4], sums[4];
-        if ((rc = wait_pub(c, pb.seq))) return rc;
+        if ((rc = wait_pub(c, cur.pb.seq))) return rc;
         if (tracing) tr_t.push_back(now_us());
+        Fr st_true[3];  // eq form: the inner sum's q(0), q(1) and t^2 coefficient
         if (u_ones) {  // E_t S_t = c0 + c1 t + c2 t^2 from sum e0s0, e1s1, de*ds
-            pub_read(c, 0, 3, sums);
-            const Fr c0 = fix1(sums[0]), c2 = fix1(sums[2]), c1 = fr_sub(fr_sub(fix1(sums[1]), c0), c2);
+            Fr c0, c2, q1;
+            if (cur.dv) {
+                pub_read(c, 0, 2, sums);
+                c0 = fix1(sums[0]);
+                c2 = fix1(sums[1]);
+                q1 = fr_sub(claim, c0);
+            } else {
+                pub_read(c, 0, 3, sums);
+                c0 = fix1(sums[0]);
+                c2 = fix1(sums[2]);
+                q1 = fix1(sums[1]);
+            }
+            const Fr c1 = fr_sub(fr_sub(q1, c0), c2);
             for (int t = 0; t < 4; t++) e[t] = fr_add(c0, fr_mul(fr_u64(t), fr_add(c1, fr_mul(fr_u64(t), c2))));
         } else if (!ueq) {
-            pub_read(c, 0, 4, sums);
-            for (int t = 0; t < 4; t++) e[t] = fix2(sums[t]);
+            if (cur.dv) {
+                pub_read(c, 0, 3, sums);
+                e[0] = fix2(sums[0]);
+                e[1] = fr_sub(claim, e[0]);
+                e[2] = fix2(sums[1]);
+                e[3] = fix2(sums[2]);
+            } else {
+                pub_read(c, 0, 4, sums);
+                for (int t = 0; t < 4; t++) e[t] = fix2(sums[t]);
+            }
         } else {  // sum_t = c0 + c1 t + c2 t^2 from sum w s0u0, w s1u1, w ds du (x 1 in round 0)
-            pub_read(c, 0, 3, sums);
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
-            Fr f = fr_mul(cE, eq_corr(eq, K));
-            auto unfix = [&](const Fr& x) { return fold ? fix1(x) : x; };
-            const Fr c0 = unfix(sums[0]), c2 = unfix(sums[2]), c1 = fr_sub(fr_sub(unfix(sums[1]), c0), c2);
+            const Fr corr = eq_corr(eq, K);
+            auto unfix = [&](const Fr& x) { return fr_mul(fold ? fix1(x) : x, corr); };
+            if (cur.dv) {
+                pub_read(c, 0, 2, sums);
+                st_true[0] = unfix(sums[0]);
+                st_true[2] = unfix(sums[1]);
+                st_true[1] = eq_piece_q1(I, st_true[0], ul, inv_u[k - r - 1]);
+            } else {
+                pub_read(c, 0, 3, sums);
+                st_true[0] = unfix(sums[0]);
+                st_true[1] = unfix(sums[1]);
+                st_true[2] = unfix(sums[2]);
+            }
+            const Fr c0 = st_true[0], c2 = st_true[2], c1 = fr_sub(fr_sub(st_true[1], c0), c2);
             for (int t = 0; t < 4; t++) {
                 const Fr st = fr_add(c0, fr_mul(fr_u64(t), fr_add(c1, fr_mul(fr_u64(t), c2))));
-                e[t] = fr_mul(fr_mul(st, f), fr_eq2(ul, fr_u64(t)));
+                e[t] = fr_mul(fr_mul(st, cE), fr_eq2(ul, fr_u64(t)));
             }
         }
         if (!fr_eq(claim, fr_add(e[0], e[1])))
@@ -3492,12 +3619,15 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         Fr w = tr_challenge(tr);
         if (ws_out) fr_store(w, ws_out + 8 * r);
         claim = lagrange4(e, w);
-        if (ueq) cE = fr_mul(cE, fr_eq2((*ueq)[k - r - 1], w));
+        if (ueq) {
+            cE = fr_mul(cE, fr_eq2((*ueq)[k - r - 1], w));
+            I = quad_at(st_true[0], st_true[1], st_true[2], w);
+        }
         fr_store(fr_to_mont(w), vm);
         if (relay_next) {
             relay_send(c, relay.pending, vm);
             relay.pending = 0;
-            pb = pb_next;
+            cur = next;
         }
         launched = relay_next;
         if (tracing) tr_t.push_back(now_us());
