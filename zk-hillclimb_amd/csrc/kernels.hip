@@ -2295,6 +2295,15 @@ ZDEV void persist_publish(uint32_t* slot, const uint32_t* pub, uint32_t nw, uint
         st_quad_sys(slot + 4 * lane, make_uint4(seq, pub[b], b + 1 < nw ? pub[b + 1] : 0u, b + 2 < nw ? pub[b + 2] : 0u));
     }
 }
+// completion flag of a stream (the host's settle): the value of *word (when given) to
+// host_word, then seq to the host flag
+__global__ void k_fence(uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t* host_word) {
+    if (word) __hip_atomic_store(host_word, *word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+void launch_fence(hipStream_t s, uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t* host_word) {
+    k_fence<<<1, 1, 0, s>>>(flag, seq, word, host_word);
+}
 // the relay between two round launches (launch_relay)
 __global__ __launch_bounds__(64) void k_relay(const uint32_t* cmd, uint32_t want, uint32_t* err,
                                               unsigned long long deadline, uint32_t* vmp) {

@@ -396,6 +396,9 @@ struct LuPersist {
 };
 #define ZKH_LU_MSG 88
 hipError_t launch_lu_persist(hipStream_t s, const LuPersist& p);
+// one thread: *word (when word is given) to *host_word, then seq to *flag (pinned host
+// memory, system scope): the completion flag of everything queued before it on the stream
+void launch_fence(hipStream_t s, uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t* host_word);
 // One wave that waits (as a persistent block waits for its command) until the three quads
 // at cmd carry seq `want`, then writes their eight data words to vmp[0..8) and 0 to vmp[8];
 // on ZKH_QUIT or past `deadline` (100 MHz ticks; then *err = 1) it writes 1 to vmp[8].

@@ -481,6 +481,18 @@ static int wait_pub(zkh_ctx* c, uint32_t seq) {
 static void pub_read(zkh_ctx* c, uint32_t j, int K, Fr* out) {
     for (int k = 0; k < K; k++) out[k] = fr_load(c->pub_host + ((size_t)j * K + k) * 8);
 }
+// completion of everything queued on the stream so far: a one-thread kernel stores a flag
+// to pinned memory and the host spins on it (wakes sooner than hipStreamSynchronize); when
+// word (device) is given, its value reaches *out on the way.  Only for device-side work:
+// a copy into pageable host memory still needs hipStreamSynchronize.
+static int settle(zkh_ctx* c, const uint32_t* word = nullptr, uint32_t* out = nullptr) {
+    const uint32_t seq = ++c->pub_seq;
+    uint32_t* hw = pub_flag(c) + 1;
+    launch_fence(c->stream, pub_flag(c), seq, word, hw);
+    const int rc = wait_pub(c, seq);
+    if (!rc && out) *out = __atomic_load_n(hw, __ATOMIC_ACQUIRE);
+    return rc;
+}
 
 // ---- relayed round launches.  A round kernel can be queued before the host has the
 // previous round's challenge: a relay (one wave, launch_relay) ahead of it on the stream
@@ -1344,7 +1356,10 @@ extern "C" int zkh_axpy(zkh_ctx* c, const zkh_tensor* a, const uint32_t cc[8], c
     uint32_t cm[8];
     fr_store(fr_to_mont(fr_load(cc)), cm);
     if (a->n) launch_axpy(c->stream, sa, cm, sb, a->n, o->planes());
-    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if ((rc = settle(c))) {
+        zkh_tensor_free(o);
+        return rc;
+    }
     *out = o;
     return ZKH_OK;
 }
@@ -1358,7 +1373,10 @@ extern "C" int zkh_hadamard(zkh_ctx* c, const zkh_tensor* a, const zkh_tensor* b
     zkh_tensor* o;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, a->n, &o))) return rc;
     if (a->n) launch_hadamard(c->stream, sa, sb, a->n, o->planes());
-    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if ((rc = settle(c))) {
+        zkh_tensor_free(o);
+        return rc;
+    }
     *out = o;
     return ZKH_OK;
 }
@@ -2247,7 +2265,8 @@ extern "C" int zkh_lu_range_table(zkh_ctx* c, int32_t low, uint32_t len, uint32_
     *out = t;
     return ZKH_OK;
 }
-static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, uint32_t** counts_out) {
+static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, uint32_t** counts_out,
+                     uint32_t** bad_out) {
     int rc = 0;
     uint32_t* counts = (uint32_t*)scratch_slot(c, SL_TMP5, (size_t)(N + 1) * 4, &rc);
     if (rc) return rc;
@@ -2262,20 +2281,19 @@ static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, u
         fr_store(fr_from_i64(low), lowl);
         launch_lu_count_planes(c->stream, p, S->n, lowl, N, counts, bad);
     }
-    uint32_t hb = 0;
-    HIPCHK(c, hipMemcpyAsync(&hb, bad, 4, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    if (hb) return fail(c, ZKH_EARG, "lookup witness outside the table");
     *counts_out = counts;
+    *bad_out = bad;
     return 0;
 }
 // multiplicities m (N field elements) of the witness S against a table of N entries at low:
-// LDS histograms for N <= 2^24 (launch_hist), global atomics beyond
-static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, DevPlanes m) {
+// LDS histograms for N <= 2^24 (launch_hist), global atomics beyond.  Queues the work only;
+// *bad (device word) becomes nonzero when a witness lies outside the table (check_bad).
+static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, DevPlanes m,
+                             uint32_t** bad_out) {
     int rc = 0;
     if (N > ZKH_HIST_MAX_BUCKETS * ZKH_HIST_BINS) {
         uint32_t* counts;
-        if ((rc = lu_counts(c, S, low, N, &counts))) return rc;
+        if ((rc = lu_counts(c, S, low, N, &counts, bad_out))) return rc;
         launch_counts_to_planes(c->stream, counts, N, m);
         return 0;
     }
@@ -2301,9 +2319,15 @@ static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint3
         ProfScope ps(c, "lu_hist", (double)S->n * (S->kind == ZKH_KIND_I32 ? 4 : 32) + (double)N * 32);
         launch_hist(c->stream, a, hs, m);
     }
+    *bad_out = bad;
+    return 0;
+}
+// waits for the queued work and fails when the multiplicity pass flagged a witness outside
+// the table
+static int check_bad(zkh_ctx* c, const uint32_t* bad) {
     uint32_t hb = 0;
-    HIPCHK(c, hipMemcpyAsync(&hb, bad, 4, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
+    int rc = settle(c, bad, &hb);
+    if (rc) return rc;
     if (hb) return fail(c, ZKH_EARG, "lookup witness outside the table");
     return 0;
 }
@@ -2313,7 +2337,8 @@ extern "C" int zkh_lu_prep(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_
     zkh_tensor* m;
     int rc;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
-    if ((rc = lu_multiplicities(c, S, low, N, m->planes()))) {
+    uint32_t* bad = nullptr;
+    if ((rc = lu_multiplicities(c, S, low, N, m->planes(), &bad)) || (rc = check_bad(c, bad))) {
         zkh_tensor_free(m);
         return rc;
     }
@@ -2329,7 +2354,10 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
     zkh_tensor *m, *so;
     int rc;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
-    if ((rc = lu_multiplicities(c, S_in, low, N, m->planes()))) {
+    // the mapping is queued behind the multiplicities (its kernels bound-check the index) and
+    // one completion wait then checks the witness range
+    uint32_t* bad = nullptr;
+    if ((rc = lu_multiplicities(c, S_in, low, N, m->planes(), &bad))) {
         zkh_tensor_free(m);
         return rc;
     }
@@ -2349,12 +2377,12 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
         fr_store(fr_from_i64(low), lowl);
         if (!rc) launch_lu_map_planes(c->stream, p, S_in->n, lowl, mp, so->planes());
     }
+    if (!rc) rc = check_bad(c, bad);
     if (rc) {
         zkh_tensor_free(m);
         zkh_tensor_free(so);
         return rc;
     }
-    HIPCHK(c, hipStreamSynchronize(c->stream));
     *S_out = so;
     *m_out = m;
     return ZKH_OK;
@@ -2395,11 +2423,10 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
     if ((rc = as_planes(c, S, SL_TMP0, &p))) return rc;
     zkh_tensor* A;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, S->n, &A))) return rc;
-    if (S->n && (rc = batch_inverse(c, p, S->n, fr_load(beta), A->planes()))) {
+    if ((S->n && (rc = batch_inverse(c, p, S->n, fr_load(beta), A->planes()))) || (rc = settle(c))) {
         zkh_tensor_free(A);
         return rc;
     }
-    HIPCHK(c, hipStreamSynchronize(c->stream));
     A->inv_of = S->gen;
     memcpy(A->inv_beta, beta, 32);
     *A_out = A;
