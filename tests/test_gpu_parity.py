@@ -570,6 +570,30 @@ def test_lu_mapping(zkh, ctx):
     assert fr_eq(m.to_fr(), mw)
 
 
+# ---------------------------------------------------------------- elementwise with int32 operands
+def test_hadamard_axpy_int32_edges(zkh, ctx):
+    """Elementwise products and axpy with int32 operands take the 32-bit multiply (quotient
+    estimated in double precision, one correction): every kind pairing against the field
+    definition, with field values 0, 1, r-1, r-2, (r-1)/2 and random ones against int32
+    values 0, +-1, +-2^30, -2^31, 2^31-1 and random ones, plus a long random tail that goes
+    through the grid-stride loops."""
+    rng = np.random.default_rng(7)
+    fv = [0, 1, P.R - 1, P.R - 2, (P.R - 1) // 2] + [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(27)]
+    iv = [0, 1, -1, 2**30, -2**30, -2**31, 2**31 - 1] + [int(x) for x in rng.integers(-2**31, 2**31, size=25)]
+    F = [f for f in fv for _ in iv] + [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(70000)]
+    I = [i for _ in fv for i in iv] + [int(x) for x in rng.integers(-2**31, 2**31, size=70000)]
+    I2 = I[1:] + I[:1]
+    A, B, B2 = ctx.from_fr(C.ints_to_fr(F)), ctx.from_i32(np.array(I, np.int32)), ctx.from_i32(np.array(I2, np.int32))
+    ints = lambda t: C.fr_to_ints(t.to_fr())
+    assert ints(ctx.hadamard(A, B)) == [f * i % P.R for f, i in zip(F, I)]
+    assert ints(ctx.hadamard(B, A)) == [f * i % P.R for f, i in zip(F, I)]
+    assert ints(ctx.hadamard(B2, B)) == [i * j % P.R for i, j in zip(I2, I)]
+    for c in (0, 1, P.R - 1, int.from_bytes(rng.bytes(32), "little") % P.R):
+        cf = C.ints_to_fr([c])[0]
+        assert ints(ctx.axpy(A, cf, B)) == [(f + c * i) % P.R for f, i in zip(F, I)], c
+        assert ints(ctx.axpy(B2, cf, B)) == [(j + c * i) % P.R for j, i in zip(I2, I)], c
+
+
 # ---------------------------------------------------------------- Hadamard
 @pytest.mark.parametrize("k", [1, 2, 5, 11, 13, 14])
 def test_hp_prove(zkh, ctx, k):
@@ -662,22 +686,27 @@ def test_calib_fr_mul(zkh, ctx):
         ctx.calib_fr_mul(0)
 
 
-@pytest.mark.parametrize("k", [4, 14, 16])
-def test_hp_prove_u_all_ones(zkh, ctx, k):
+@pytest.mark.parametrize("k,extreme", [(4, False), (14, False), (16, False), (15, True)])
+def test_hp_prove_u_all_ones(zkh, ctx, k, extreme):
     """U = 1 everywhere as an int32 tensor (the RoPE obligations' U, zkob_rope.cu:215-281): the
     per-round kernels skip U (E_t S_t from three products per pair) and must give the oracle's
-    proof of the generic E, S, U sumcheck."""
+    proof of the generic E, S, U sumcheck.  With an int32 S (extreme) the first round forms its
+    sums exactly with the 32-bit multiply, here at the ends of the int32 range."""
     n = 1 << k
     rng = np.random.default_rng(100 + k)
     E = rand_fr_full(rng, n)
-    S = C.ints_to_fr(rng.integers(-2**20, 2**20, size=n))
+    Sv = rng.integers(-2**31 if extreme else -2**20, 2**31 if extreme else 2**20, size=n)
+    if extreme:  # the first round's 32-bit multiply at the ends of the int32 range
+        Sv[:6] = [-2**31, 2**31 - 1, 0, -1, 2**31 - 1, -2**31]
+    S = C.ints_to_fr(Sv)
     ones = np.ones(n, np.int64)
     Ei, Si = C.fr_to_ints(E), C.fr_to_ints(S)
     claim = C.ints_to_fr([sum(a * b for a, b in zip(Ei, Si)) % P.R])[0]
     st_g, st_o = seed_transcript(zkh, "hp1:%d" % k)
     rc, want = C.hp_prove(st_o, claim, E, S, C.ints_to_fr(ones))
     assert rc == 0
-    got = ctx.hp_prove(st_g, claim, ctx.from_fr(E), ctx.from_fr(S), ctx.from_i32(ones.astype(np.int32)))
+    got = ctx.hp_prove(st_g, claim, ctx.from_fr(E), ctx.from_i32(Sv.astype(np.int32)) if extreme else ctx.from_fr(S),
+                       ctx.from_i32(ones.astype(np.int32)))
     for key in ("ev", "term", "ws"):
         assert fr_eq(got[key], want[key]), key
     assert bytes(st_g) == bytes(st_o)

@@ -215,6 +215,60 @@ ZDEV fr_t fr_from_i64(int64_t v) {
     return fr_sub(r, m);
 }
 
+// a m mod r for canonical a and m < 2^32 (plain in, plain out).  The 288-bit product comes
+// from one multiply-add chain; the quotient q = floor(a m / r) < 2^32 is estimated from the
+// top 64 bits in double precision (2^224 / r as the constant; relative error of the
+// estimate below 2^-50, the ignored low limbs below 2^-31 of a unit) and biased down by 1/2,
+// so it is q or q - 1; after removing it times r one conditional subtraction remains.  About
+// 50 instructions against 332 for a Montgomery product.
+ZDEV fr_t fr_mul_u32(const fr_t& a, uint32_t m) {
+    uint32_t t[9];
+    uint64_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        acc = (uint64_t)a.v[i] * m + (acc >> 32);
+        t[i] = (uint32_t)acc;
+    }
+    t[8] = (uint32_t)(acc >> 32);
+    const double top = (double)t[8] * 4294967296.0 + (double)t[7];  // the product is exact
+    const double qd = top * 0x1.1aa84a76ff6f2p-31 - 0.5;
+    const uint32_t q = qd > 0.0 ? (uint32_t)qd : 0u;
+    uint64_t c = 0;
+    unsigned br = 0;
+    fr_t x;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        c = (uint64_t)fr_p(i) * q + (c >> 32);
+        x.v[i] = __builtin_subc(t[i], (uint32_t)c, br, &br);
+    }
+    return fr_reduce_once(x, 0);  // a m - q r < 2r < 2^256: nothing is left above limb 7
+}
+// a s mod r for canonical a and |s| < 2^32
+ZDEV fr_t fr_mul_i64s(const fr_t& a, int64_t s) {
+    const bool neg = s < 0;
+    const fr_t p = fr_mul_u32(a, (uint32_t)(neg ? -s : s));
+    return neg ? fr_sub(fr_zero(), p) : p;
+}
+// x as an integer in (-2^32, 2^32) when it is one (the field element or its negative)
+ZDEV bool fr_int32ish(const fr_t& x, int64_t& out) {
+    uint32_t hiw = 0;
+#pragma unroll
+    for (int i = 1; i < 8; i++) hiw |= x.v[i];
+    if (!hiw) {
+        out = x.v[0];
+        return true;
+    }
+    const fr_t d = fr_sub(fr_zero(), x);  // r - x
+    hiw = 0;
+#pragma unroll
+    for (int i = 1; i < 8; i++) hiw |= d.v[i];
+    if (!hiw) {
+        out = -(int64_t)d.v[0];
+        return true;
+    }
+    return false;
+}
+
 // ---- wave / block reductions of field elements (DPP/swizzle via shuffles, then LDS) ----
 ZDEV fr_t fr_shfl_xor(const fr_t& x, int mask) {
     fr_t r;

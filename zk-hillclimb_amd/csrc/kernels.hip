@@ -579,23 +579,46 @@ static void with_loader(const Src& x, F&& f) {
         f(LdI64{(const int64_t*)x.p});
     }
 }
-template <typename LA, typename LB>
-__global__ void k_axpy(LA a, fr_t cm, LB b, uint32_t n, uint4* olo, uint4* ohi) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        st_fr(olo, ohi, i, fr_add(a(i), mont_mul(cm, b(i))));
+// c b for the scalar c (Montgomery form cm, plain c): one Montgomery product, or with an
+// int32 b the 32-bit multiply
+template <typename LB>
+ZDEV fr_t scale_of(const fr_t& cm, const fr_t&, const LB& b, uint32_t i) {
+    return mont_mul(cm, b(i));
 }
-void launch_axpy(hipStream_t s, Src a, const uint32_t* c_m_host, Src b, uint32_t n, DevPlanes out) {
-    const fr_t cm = to_fr(c_m_host);
+ZDEV fr_t scale_of(const fr_t&, const fr_t& c, const LdI32& b, uint32_t i) { return fr_mul_i64s(c, b.p[i]); }
+template <typename LA, typename LB>
+__global__ void k_axpy(LA a, fr_t cm, fr_t c, LB b, uint32_t n, uint4* olo, uint4* ohi) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        st_fr(olo, ohi, i, fr_add(a(i), scale_of(cm, c, b, i)));
+}
+void launch_axpy(hipStream_t s, Src a, const uint32_t* c_host, const uint32_t* c_m_host, Src b, uint32_t n,
+                 DevPlanes out) {
+    const fr_t cm = to_fr(c_m_host), c = to_fr(c_host);
     with_loader(a, [&](auto la) {
         with_loader(b, [&](auto lb) {
-            k_axpy<<<grid_for(n, NT, 8192), NT, 0, s>>>(la, cm, lb, n, PL_LO(out), PL_HI(out));
+            k_axpy<<<grid_for(n, NT, 8192), NT, 0, s>>>(la, cm, c, lb, n, PL_LO(out), PL_HI(out));
         });
     });
 }
+// the plain product a b: two Montgomery products (the second by 2^512 mod r), or with an
+// int32 operand the 32-bit multiply, or with two int32 operands the exact 64-bit product
+template <typename LA, typename LB>
+ZDEV fr_t prod_of(const LA& a, const LB& b, uint32_t i) {
+    return mont_mul(mont_mul(a(i), b(i)), r2_m());
+}
+template <typename LA>
+ZDEV fr_t prod_of(const LA& a, const LdI32& b, uint32_t i) {
+    return fr_mul_i64s(a(i), b.p[i]);
+}
+template <typename LB>
+ZDEV fr_t prod_of(const LdI32& a, const LB& b, uint32_t i) {
+    return fr_mul_i64s(b(i), a.p[i]);
+}
+ZDEV fr_t prod_of(const LdI32& a, const LdI32& b, uint32_t i) { return fr_from_i64((int64_t)a.p[i] * b.p[i]); }
 template <typename LA, typename LB>
 __global__ void k_hadamard(LA a, LB b, uint32_t n, uint4* olo, uint4* ohi) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-        st_fr(olo, ohi, i, mont_mul(mont_mul(a(i), b(i)), r2_m()));
+        st_fr(olo, ohi, i, prod_of(a, b, i));
 }
 void launch_hadamard(hipStream_t s, Src a, Src b, uint32_t n, DevPlanes out) {
     with_loader(a, [&](auto la) {
@@ -1051,6 +1074,8 @@ struct EqDev {
 ZDEV fr_t eq_w(const EqDev& eq, uint32_t i) { return mont_mul_ol(ld_aos(eq.elo, i & 1023), ld_aos(eq.ehi, i >> 10)); }
 
 #define SB() __builtin_amdgcn_sched_barrier(0)
+// the product x y as a field element (x 1): a Montgomery product lifted by 2^512
+ZDEV fr_t exact_mul(const fr_t& x, const fr_t& y) { return mont_mul_ol(mont_mul_ol(x, y), r2_m()); }
 // blocks of a logUp phase-2 round (both groups; 256 CUs hold 768 of them at once)
 #ifndef LU2_GRID
 #define LU2_GRID 1536
@@ -1301,14 +1326,22 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
     if (!fold && inv) {  // B = 1/(T + beta) unfolded (see inverse_pair_sums); 3..5 as below
         for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
             const fr_t b0 = ld_fr(B.slo, B.shi, i), b1 = ld_fr(B.slo, B.shi, i + h);
-            {
+            {  // multiplicities are small integers: sums 3..5 exact (x 1) by the 32-bit multiply
                 const fr_t m0 = ld_fr(m.slo, m.shi, i), m1 = ld_fr(m.slo, m.shi, i + h);
                 SB();
-                acc.add(3, mont_mul_ol(m0, b0));
-                SB();
-                acc.add(4, mont_mul_ol(m1, b1));
-                SB();
-                acc.add(5, mont_mul_ol(fr_sub(m1, m0), fr_sub(b1, b0)));
+                int64_t i0, i1;
+                if (fr_int32ish(m0, i0) && fr_int32ish(m1, i1) && i1 - i0 > -(int64_t)0xffffffffll &&
+                    i1 - i0 < (int64_t)0xffffffffll) {
+                    acc.add(3, fr_mul_i64s(b0, i0));
+                    acc.add(4, fr_mul_i64s(b1, i1));
+                    acc.add(5, fr_mul_i64s(fr_sub(b1, b0), i1 - i0));
+                } else {
+                    acc.add(3, exact_mul(m0, b0));
+                    SB();
+                    acc.add(4, exact_mul(m1, b1));
+                    SB();
+                    acc.add(5, exact_mul(fr_sub(m1, m0), fr_sub(b1, b0)));
+                }
             }
             SB();
             const fr_t w = eq_w(eq, i);
@@ -1473,9 +1506,11 @@ uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fol
 // from three products per pair: sums e0 s0, e1 s1, (e1 - e0)(s1 - s0) (x 2^-256).  U is
 // neither read nor folded (every fold of an all-ones table is all ones).
 // derive (folding rounds): sum e1 s1 is left out (the host takes it as claim - sum e0 s0)
+// s_int (first round only): S holds int32 values, and the three sums are formed exactly
+// (x 1) with the 32-bit multiply (a pair outside that range takes two Montgomery products)
 template <int derive>
 __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32_t n, int fold, fr_t vm,
-                                                      const uint32_t* vmp, Publish pub) {
+                                                      const uint32_t* vmp, Publish pub, int s_int) {
     if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
     constexpr int K = derive ? 2 : 3;
@@ -1488,6 +1523,21 @@ __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32
         SB();
         load_pair(S, i, h, n, fold, vm, s0, s1);
         SB();
+        if constexpr (!derive) {
+            int64_t a0, a1;
+            if (!fold && s_int && fr_int32ish(s0, a0) && fr_int32ish(s1, a1)) {
+                acc.add(0, fr_mul_i64s(e0, a0));
+                acc.add(1, fr_mul_i64s(e1, a1));
+                acc.add(2, fr_mul_i64s(fr_sub(e1, e0), a1 - a0));
+                continue;
+            }
+            if (!fold && s_int) {
+                acc.add(0, exact_mul(e0, s0));
+                acc.add(1, exact_mul(e1, s1));
+                acc.add(2, exact_mul(fr_sub(e1, e0), fr_sub(s1, s0)));
+                continue;
+            }
+        }
         acc.add(0, mont_mul_ol(e0, s0));
         SB();
         if constexpr (!derive) {
@@ -1500,11 +1550,11 @@ __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32
     reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
-                              const uint32_t* vmp, Publish partial, int derive) {
+                              const uint32_t* vmp, Publish partial, int derive, int s_int) {
     uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
-    if (fold && derive) k_hp_round_ones<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial);
-    else k_hp_round_ones<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial);
+    if (fold && derive) k_hp_round_ones<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, 0);
+    else k_hp_round_ones<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, s_int);
     return g;
 }
 // x as an integer in (-2^30, 2^30) when it is one (a field element or its negative)
@@ -1526,8 +1576,6 @@ ZDEV bool small_int(const fr_t& x, int32_t& out) {
     }
     return false;
 }
-// the product x y as a field element (x 1): a Montgomery product lifted by 2^512
-ZDEV fr_t exact_mul(const fr_t& x, const fr_t& y) { return mont_mul_ol(mont_mul_ol(x, y), r2_m()); }
 // eq-specialised: with w = eq(i, u[0..K)) of the pair, S_t U_t = (s0 + t ds)(u0 + t du) is a
 // quadratic in t, so three sums give the round: sum w s0 u0, sum w s1 u1, sum w ds du.  In a
 // round that folds, w s0 and w ds are formed first and the sums carry 2^-256.  In the first

@@ -113,7 +113,9 @@ struct Src {
     const void* p;
     uint32_t cap;
 };
-void launch_axpy(hipStream_t s, Src a, const uint32_t* c_m_host, Src b, uint32_t n, DevPlanes out);
+// out = a + c b (c plain and in Montgomery form; an int32 b takes the 32-bit multiply)
+void launch_axpy(hipStream_t s, Src a, const uint32_t* c_host, const uint32_t* c_m_host, Src b, uint32_t n,
+                 DevPlanes out);
 void launch_hadamard(hipStream_t s, Src a, Src b, uint32_t n, DevPlanes out);
 
 // ---- logUp ----
@@ -187,7 +189,8 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
 // phase-2 round over A, S, B, T, m as two launches publishing jobs 0 (A, S: 5 sums) and
 // 1 (B, T, m: 6 sums) of `pub` (made for 2 jobs; see kernels.hip)
 // inv_as / inv_btm: A = 1/(S + beta) / B = 1/(T + beta) with that group's fold not owed, as
-// inv of launch_lu_phase1 (sums 0, 1 of the group then carry 2^256 instead of 2^-256)
+// inv of launch_lu_phase1 (sums 0, 1 of the group then carry 2^256 instead of 2^-256); with
+// inv_btm the m b sums (3..5 of job 1) are exact (x 1)
 // derive: the folding groups leave out their sums at 1: job 0 publishes 3 sums (w*a0*s0,
 // w*da*ds, a0), job 1 (when it folds) 4 (w*b0*t0, w*db*dt, m0*b0, dm*db)
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
@@ -202,9 +205,9 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
                          int fold, const uint32_t* v_m_host, const uint32_t* vmp, Publish pub, int derive);
 // generic with U = 1 everywhere: sums e0*s0, e1*s1, de*ds (x 2^-256); U is not touched;
-// derive: e0*s0, de*ds
+// derive: e0*s0, de*ds; s_int (first round, S of int32 values): the sums exact (x 1)
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
-                              const uint32_t* vmp, Publish pub, int derive);
+                              const uint32_t* vmp, Publish pub, int derive, int s_int);
 // eq-specialised: sums w*s0*u0, w*s1*u1, w*ds*du with w = eq(i,u_) (x 2^-256 when folding,
 // x 1 in the first round); derive: w*s0*u0, w*ds*du
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,

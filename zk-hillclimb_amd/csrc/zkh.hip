@@ -1355,7 +1355,7 @@ extern "C" int zkh_axpy(zkh_ctx* c, const zkh_tensor* a, const uint32_t cc[8], c
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, a->n, &o))) return rc;
     uint32_t cm[8];
     fr_store(fr_to_mont(fr_load(cc)), cm);
-    if (a->n) launch_axpy(c->stream, sa, cm, sb, a->n, o->planes());
+    if (a->n) launch_axpy(c->stream, sa, cc, cm, sb, a->n, o->planes());
     if ((rc = settle(c))) {
         zkh_tensor_free(o);
         return rc;
@@ -2846,9 +2846,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                 qb[0] = fr_mul(q_of(s[0], cur.cf_b), corr);
                 qb[1] = fr_mul(q_of(s[1], cur.cf_b), corr);
                 qb[2] = fr_mul(fix1(s[2]), corr);
-                M[0] = fix1(s[3]);
-                M[1] = fix1(s[4]);
-                M[2] = fix1(s[5]);
+                for (int t = 0; t < 3; t++) M[t] = cur.cf_b ? s[3 + t] : fix1(s[3 + t]);  // exact when cf_b
             }
         }
         const Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
@@ -3519,6 +3517,8 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     // U all ones (an I32 tensor measured so at ingest: the RoPE obligations' U = 1) with an
     // explicit E: the per-round kernels skip U, whose folds stay all ones in its source
     const bool u_ones = !ueq && U->kind == ZKH_KIND_I32 && U->ones;
+    // with U all ones and an int32 S, the first round's sums are exact (x 1): 32-bit multiplies
+    const bool s_int = u_ones && S->kind == ZKH_KIND_I32;
     // A folding round leaves its sum at 1 to the host: claim - p(0) for an explicit E; with
     // the eq form, from the inner claim I = sum eq S U over the remaining variables (the
     // running claim without the eq factor cE) as (I - (1 - u) q(0)) / u, unless u is 0.
@@ -3536,7 +3536,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         Launched l{make_pub(c, 1), fold && (!ueq || !fr_eq((*ueq)[k - r - 1], kZero))};
         if (u_ones) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
-            launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, l.pb, l.dv);
+            launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, l.pb, l.dv, s_int);
         } else if (!ueq) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
             launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp, l.pb, l.dv);
@@ -3598,9 +3598,10 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
                 q1 = fr_sub(claim, c0);
             } else {
                 pub_read(c, 0, 3, sums);
-                c0 = fix1(sums[0]);
-                c2 = fix1(sums[2]);
-                q1 = fix1(sums[1]);
+                auto unfix = [&](const Fr& x) { return !fold && s_int ? x : fix1(x); };
+                c0 = unfix(sums[0]);
+                c2 = unfix(sums[2]);
+                q1 = unfix(sums[1]);
             }
             const Fr c1 = fr_sub(fr_sub(q1, c0), c2);
             for (int t = 0; t < 4; t++) e[t] = fr_add(c0, fr_mul(fr_u64(t), fr_add(c1, fr_mul(fr_u64(t), c2))));
