@@ -215,21 +215,12 @@ ZDEV fr_t fr_from_i64(int64_t v) {
     return fr_sub(r, m);
 }
 
-// a m mod r for canonical a and m < 2^32 (plain in, plain out).  The 288-bit product comes
-// from one multiply-add chain; the quotient q = floor(a m / r) < 2^32 is estimated from the
-// top 64 bits in double precision (2^224 / r as the constant; relative error of the
-// estimate below 2^-50, the ignored low limbs below 2^-31 of a unit) and biased down by 1/2,
-// so it is q or q - 1; after removing it times r one conditional subtraction remains.  About
-// 50 instructions against 332 for a Montgomery product.
-ZDEV fr_t fr_mul_u32(const fr_t& a, uint32_t m) {
-    uint32_t t[9];
-    uint64_t acc = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        acc = (uint64_t)a.v[i] * m + (acc >> 32);
-        t[i] = (uint32_t)acc;
-    }
-    t[8] = (uint32_t)(acc >> 32);
+// t mod r for a 288-bit t < r 2^32 (t[8] the top limb): the quotient q = floor(t / r) <
+// 2^32 estimated from the top 64 bits in double precision (2^224 / r as the constant;
+// relative error of the estimate below 2^-50, the ignored low limbs below 2^-31 of a unit)
+// and biased down by 1/2, so it is q or q - 1; after removing it times r one conditional
+// subtraction remains.
+ZDEV fr_t fr_reduce288(const uint32_t* t) {
     const double top = (double)t[8] * 4294967296.0 + (double)t[7];  // the product is exact
     const double qd = top * 0x1.1aa84a76ff6f2p-31 - 0.5;
     const uint32_t q = qd > 0.0 ? (uint32_t)qd : 0u;
@@ -241,12 +232,46 @@ ZDEV fr_t fr_mul_u32(const fr_t& a, uint32_t m) {
         c = (uint64_t)fr_p(i) * q + (c >> 32);
         x.v[i] = __builtin_subc(t[i], (uint32_t)c, br, &br);
     }
-    return fr_reduce_once(x, 0);  // a m - q r < 2r < 2^256: nothing is left above limb 7
+    return fr_reduce_once(x, 0);  // t - q r < 2r < 2^256: nothing is left above limb 7
+}
+// a m mod r for canonical a and m < 2^32 (plain in, plain out): the 288-bit product from one
+// multiply-add chain, then fr_reduce288.  About 50 instructions against 332 for a Montgomery
+// product.
+ZDEV fr_t fr_mul_u32(const fr_t& a, uint32_t m) {
+    uint32_t t[9];
+    uint64_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        acc = (uint64_t)a.v[i] * m + (acc >> 32);
+        t[i] = (uint32_t)acc;
+    }
+    t[8] = (uint32_t)(acc >> 32);
+    return fr_reduce288(t);
+}
+// a 2^32 mod r: the limbs shifted by one, then fr_reduce288
+ZDEV fr_t fr_shl32(const fr_t& a) {
+    uint32_t t[9];
+    t[0] = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) t[i + 1] = a.v[i];
+    return fr_reduce288(t);
+}
+// a m mod r for a 64-bit m: the two halves (the high one shifted by 2^32), one when m < 2^32
+ZDEV fr_t fr_mul_u64(const fr_t& a, uint64_t m) {
+    const fr_t lo = fr_mul_u32(a, (uint32_t)m);
+    const uint32_t hi = (uint32_t)(m >> 32);
+    return hi ? fr_add(lo, fr_shl32(fr_mul_u32(a, hi))) : lo;
 }
 // a s mod r for canonical a and |s| < 2^32
 ZDEV fr_t fr_mul_i64s(const fr_t& a, int64_t s) {
     const bool neg = s < 0;
     const fr_t p = fr_mul_u32(a, (uint32_t)(neg ? -s : s));
+    return neg ? fr_sub(fr_zero(), p) : p;
+}
+// a s mod r for canonical a and any int64 s
+ZDEV fr_t fr_mul_i64(const fr_t& a, int64_t s) {
+    const bool neg = s < 0;
+    const fr_t p = fr_mul_u64(a, neg ? 0ull - (uint64_t)s : (uint64_t)s);
     return neg ? fr_sub(fr_zero(), p) : p;
 }
 // x as an integer in (-2^32, 2^32) when it is one (the field element or its negative)

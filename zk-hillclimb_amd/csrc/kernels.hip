@@ -1580,8 +1580,9 @@ ZDEV bool small_int(const fr_t& x, int32_t& out) {
 // quadratic in t, so three sums give the round: sum w s0 u0, sum w s1 u1, sum w ds du.  In a
 // round that folds, w s0 and w ds are formed first and the sums carry 2^-256.  In the first
 // round (no fold) the tables still hold the witness' small integers: the three products are
-// formed exactly as 64-bit integers and weighted once each (sums x 1; a pair whose values are
-// not all in (-2^30, 2^30) forms them as exact field products instead).
+// formed exactly as 64-bit integers and the Montgomery-form weight multiplies them with the
+// 64-bit multiply (sums x 2^256; a pair whose values are not all in (-2^30, 2^30) forms them
+// as exact field products weighted to the same factor).
 // derive (folding rounds): sum w s1 u1 is left out (the host takes it from the previous
 // round's claim, q(0)(1 - u) + q(1) u)
 template <int derive>
@@ -1628,23 +1629,20 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             u1 = ld_fr(U.slo, U.shi, i + h);
             w = eq_w(eq, i);
             SB();
-            fr_t p0, p1, pd;
             int32_t a0, a1, b0, b1;
             if (small_int(s0, a0) && small_int(s1, a1) && small_int(u0, b0) && small_int(u1, b1)) {
-                p0 = fr_from_i64((int64_t)a0 * b0);
-                p1 = fr_from_i64((int64_t)a1 * b1);
-                pd = fr_from_i64((int64_t)(a1 - a0) * (b1 - b0));
-            } else {
-                p0 = exact_mul(s0, u0);
-                p1 = exact_mul(s1, u1);
-                pd = exact_mul(fr_sub(s1, s0), fr_sub(u1, u0));
+                // the weight (e 2^256) times the exact 64-bit products: sums e s u 2^256
+                acc.add(0, fr_mul_i64(w, (int64_t)a0 * b0));
+                acc.add(1, fr_mul_i64(w, (int64_t)a1 * b1));
+                acc.add(2, fr_mul_i64(w, (int64_t)(a1 - a0) * (b1 - b0)));
+            } else {  // exact field products, weighted to the same e s u 2^256
+                const fr_t w2 = mont_mul_ol(w, r2_m());
+                acc.add(0, mont_mul_ol(w2, exact_mul(s0, u0)));
+                SB();
+                acc.add(1, mont_mul_ol(w2, exact_mul(s1, u1)));
+                SB();
+                acc.add(2, mont_mul_ol(w2, exact_mul(fr_sub(s1, s0), fr_sub(u1, u0))));
             }
-            SB();
-            acc.add(0, mont_mul_ol(w, p0));
-            SB();
-            acc.add(1, mont_mul_ol(w, p1));
-            SB();
-            acc.add(2, mont_mul_ol(w, pd));
             SB();
         }
     }

@@ -209,7 +209,7 @@ uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
                               const uint32_t* vmp, Publish pub, int derive, int s_int);
 // eq-specialised: sums w*s0*u0, w*s1*u1, w*ds*du with w = eq(i,u_) (x 2^-256 when folding,
-// x 1 in the first round); derive: w*s0*u0, w*ds*du
+// x 2^256 in the first round); derive: w*s0*u0, w*ds*du
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub, int derive);
 // sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)

@@ -3616,11 +3616,11 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
                 pub_read(c, 0, 4, sums);
                 for (int t = 0; t < 4; t++) e[t] = fix2(sums[t]);
             }
-        } else {  // sum_t = c0 + c1 t + c2 t^2 from sum w s0u0, w s1u1, w ds du (x 1 in round 0)
+        } else {  // sum_t = c0 + c1 t + c2 t^2 from sum w s0u0, w s1u1, w ds du (x 2^256 in round 0)
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
             const Fr corr = eq_corr(eq, K);
-            auto unfix = [&](const Fr& x) { return fr_mul(fold ? fix1(x) : x, corr); };
+            auto unfix = [&](const Fr& x) { return fr_mul(fold ? fix1(x) : fr_from_mont(x), corr); };
             if (cur.dv) {
                 pub_read(c, 0, 2, sums);
                 st_true[0] = unfix(sums[0]);
