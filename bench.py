@@ -696,7 +696,7 @@ def seg_time(job, reps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
@@ -910,12 +910,13 @@ def main():
                           "scope": "dominant kernel class of the SwiGLU segment (the layer's largest), "
                                    "algorithmic bytes over launch-stamped time"}
         if gdom == "lu_phase2":
-            # the same launches against the Montgomery-multiply peak: per pair 9 products in
-            # the first round (A = 1/(comb + beta) and B = 1/(T_comb + beta) take the closed
-            # form: 3 for (A, S) and 6 for (B, T, m), eq weights included) and 25 after it (the
-            # general round's 6 + 9 and the owed folds of A, S, B, T, m, 2 per table)
+            # the same launches against the Montgomery-multiply peak: per pair 6 Montgomery
+            # products in the first round (A = 1/(comb + beta) and B = 1/(T_comb + beta) take
+            # the closed form: 3 per group, eq weights included; the three multiplicity
+            # products there are 32-bit multiplies, not counted) and 22 after it (the sums at 1
+            # derived on the host: 5 + 7, and the owed folds of A, S, B, T, m, 2 per table)
             pairs = [(glu.D >> r) // 2 for r in range(int(gla))]
-            prods = sum(p * (9 if r == 0 else 25) for r, p in enumerate(pairs))
+            prods = sum(p * (6 if r == 0 else 22) for r, p in enumerate(pairs))
             rate = prods / (gms / 1000.0)
             layer_roofline["valu"] = {
                 "products_per_segment": prods, "achieved_Gmul_s": round(rate / 1e9, 1),
@@ -965,7 +966,7 @@ def main():
         c5 = synth.CONFIGS["C5"]
         c5rng = synth.rng_for(5)
         c5_jobs = [MatmulJob(zkh, synth, c5rng, n, c5["B"], i, o, tag="cfg5:layer0") for n, i, o in c5["matmuls"]]
-        r5, _, _ = mm_batch_rate(zkh, c5_jobs, max(3, args.steps // 4), 1)
+        r5, _, _ = mm_batch_rate(zkh, c5_jobs, max(5, args.steps // 2), 2)
         del c5_jobs
         g5 = GluJob(zkh, synth, synth.rng_for(5), c5["B"], c5["ffn"], N=c5["glu_table"], tag="cfg5:layer0")
         ms5, _ = seg_time(g5, 3)
