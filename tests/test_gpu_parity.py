@@ -677,6 +677,56 @@ def test_hp_prove_eq_wrong_claim_stops(zkh, ctx, k):
     assert bytes(st_g) == bytes(st_o)
 
 
+def test_lu_hp_per_round_launch_path(zkh, ctx, monkeypatch):
+    """Every round of the lookup and Hadamard sumchecks as its own launch (the persistent loops
+    off): the folding rounds derive their sums at 1 down to 2-entry tables, the terminals come
+    from the folded tables, and the proofs equal the oracle's (phase 1 and 2, explicit E, eq
+    form, U all ones over an int32 S)."""
+    monkeypatch.setenv("ZKH_NO_PERSIST", "1")
+    rng = np.random.default_rng(41)
+    for D, N, low in [(1 << 10, 1 << 10, -512), (1 << 12, 1 << 8, -128)]:
+        vals = rng.integers(low, low + N, size=D).astype(np.int32)
+        S = C.ints_to_fr(vals)
+        T = C.range_table(low, N, N)
+        rc, m = C.lu_prep(S, low, N)
+        assert rc == 0
+        beta, alpha = rand_fr_full(rng, 2)
+        u = rand_fr_full(rng, P.ceil_log2(D))
+        st_g, st_o = seed_transcript(zkh, "lupr:%d:%d" % (D, N))
+        rc, want = C.lu_prove(st_o, C.lu_inverse(S, beta), S, T, m, alpha, beta, u)
+        assert rc == 0
+        Sg = ctx.from_i32(vals)
+        got = ctx.lu_prove(st_g, ctx.lu_inverse(Sg, beta), Sg, ctx.range_table(low, N, N), ctx.from_fr(m),
+                           alpha, beta, u)
+        for key in ("ev", "term", "ws"):
+            assert fr_eq(got[key], want[key]), (D, N, key)
+        assert bytes(st_g) == bytes(st_o)
+    k = 11
+    n = 1 << k
+    u = rand_fr_full(rng, k)
+    E = C.build_eq(u)
+    Sv = rng.integers(-2**31, 2**31, size=n)
+    S, U = C.ints_to_fr(Sv), rand_fr_full(rng, n)
+    Ei, Si, Ui = C.fr_to_ints(E), C.fr_to_ints(S), C.fr_to_ints(U)
+    claim = C.ints_to_fr([sum(a * b % P.R * c for a, b, c in zip(Ei, Si, Ui)) % P.R])[0]
+    ones = np.ones(n, np.int64)
+    claim1 = C.ints_to_fr([sum(a * b for a, b in zip(Ei, Si)) % P.R])[0]
+    for form in ("E", "eq", "ones"):
+        st_g, st_o = seed_transcript(zkh, "hppr:" + form)
+        if form == "ones":
+            rc, want = C.hp_prove(st_o, claim1, E, S, C.ints_to_fr(ones))
+            got = ctx.hp_prove(st_g, claim1, ctx.from_fr(E), ctx.from_i32(Sv.astype(np.int32)),
+                               ctx.from_i32(ones.astype(np.int32)))
+        else:
+            rc, want = C.hp_prove(st_o, claim, E, S, U)
+            got = (ctx.hp_prove_eq(st_g, claim, u, ctx.from_fr(S), ctx.from_fr(U)) if form == "eq"
+                   else ctx.hp_prove(st_g, claim, ctx.from_fr(E), ctx.from_fr(S), ctx.from_fr(U)))
+        assert rc == 0
+        for key in ("ev", "term", "ws"):
+            assert fr_eq(got[key], want[key]), (form, key)
+        assert bytes(st_g) == bytes(st_o)
+
+
 def test_calib_fr_mul(zkh, ctx):
     """The multiply-rate probe runs and reports a plausible device-wide rate; zero
     iterations are refused."""
