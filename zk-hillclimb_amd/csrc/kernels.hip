@@ -1330,11 +1330,10 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
                 const fr_t m0 = ld_fr(m.slo, m.shi, i), m1 = ld_fr(m.slo, m.shi, i + h);
                 SB();
                 int64_t i0, i1;
-                if (fr_int32ish(m0, i0) && fr_int32ish(m1, i1) && i1 - i0 > -(int64_t)0xffffffffll &&
-                    i1 - i0 < (int64_t)0xffffffffll) {
+                if (fr_int32ish(m0, i0) && fr_int32ish(m1, i1)) {
                     acc.add(3, fr_mul_i64s(b0, i0));
                     acc.add(4, fr_mul_i64s(b1, i1));
-                    acc.add(5, fr_mul_i64s(fr_sub(b1, b0), i1 - i0));
+                    acc.add(5, fr_mul_i64(fr_sub(b1, b0), i1 - i0));
                 } else {
                     acc.add(3, exact_mul(m0, b0));
                     SB();
@@ -1528,7 +1527,7 @@ __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32
             if (!fold && s_int && fr_int32ish(s0, a0) && fr_int32ish(s1, a1)) {
                 acc.add(0, fr_mul_i64s(e0, a0));
                 acc.add(1, fr_mul_i64s(e1, a1));
-                acc.add(2, fr_mul_i64s(fr_sub(e1, e0), a1 - a0));
+                acc.add(2, fr_mul_i64(fr_sub(e1, e0), a1 - a0));
                 continue;
             }
             if (!fold && s_int) {
