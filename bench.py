@@ -697,7 +697,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-layer", action="store_true")
@@ -800,12 +800,16 @@ def main():
     # a step for tens of ms at fixed allocation counts; it stays off while timing.  The W
     # warmup steps run right before the timed ones, after the collection: a step that follows
     # an idle pause (the collection, the device and the host workers going idle) takes
-    # several times as long as the next ones.
-    def timed_steps():
+    # several times as long as the next ones, and the first ~200 steps after the jobs' setup
+    # (the large uploads and allocations) run at ~0.205 ms against ~0.18 after them; W
+    # defaults to 300 steps (~60 ms).
+    def timed_steps(prof=False):
         gc.collect()
         gc.disable()
         for _ in range(args.warmup):
             mm_step()
+        if prof:  # launch records of the K timed steps only (enabling clears the records)
+            zkh.lib().zkh_prof_enable(mctx.h, 1)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         step_ms = []
@@ -831,11 +835,10 @@ def main():
     print("matmul step %.3f ms -> %.3g elements/s" % (ms_step, value), file=sys.stderr, flush=True)
     prof_ms_step = None
     if not args.no_prof:
-        zkh.lib().zkh_prof_enable(mctx.h, 1)
-        prof_ms_step, _ = timed_steps()
+        prof_ms_step, _ = timed_steps(prof=True)
 
-    # per-kernel device time over the profiled pass's steps
-    kern = {k: [v[0] * args.steps, v[1] * args.steps, v[2] * args.steps] for k, v in prof_kernels(zkh, mctx).items()}
+    # per-kernel device time, launches and bytes over the profiled pass's K timed steps
+    kern = prof_kernels(zkh, mctx)
     zkh.lib().zkh_prof_enable(mctx.h, 0)
     # The roofline object covers the dominant HBM-bound kernel.  The persistent round loop
     # (zkip_rounds) runs one host round trip per round (Fiat-Shamir challenge) and moves

@@ -7,6 +7,8 @@
 // fused fold+evaluate kernel.  Only 32-byte scalars cross PCIe per round.
 #include <hip/hip_runtime.h>
 
+#include <pthread.h>
+#include <sched.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -32,79 +34,138 @@
 
 using namespace zkh;
 
+// One step of a host spin-wait; step k = 0 mod 256 gives the CPU to any other runnable
+// thread on the same CPU.  The host threads of a batch all spin, and the scheduler may put
+// a woken thread on the CPU of the thread that woke it: two spinning threads on one CPU
+// would take turns at the scheduler's time-slice granularity (a two-job batch lost ~4 ms
+// in about one step of 40 so, with no CPU time stolen by the host).
+static inline void spin_pause(uint64_t k) {
+    if ((k & 255) == 0) sched_yield();
+    else __builtin_ia32_pause();
+}
+
+// Worker `id` of a pool goes on a CPU of its own: the id-th CPU of the process's allowed
+// set after the creating thread's current one (ZKH_PIN_WORKERS=0 leaves placement to the
+// scheduler, which left a worker sharing the caller's CPU for the first ~40 ms of a
+// TinyLlama layer's matmul steps: 0.208 against 0.18 ms per step until it moved).
+static void pin_worker(std::thread& t, int id) {
+    static const bool on = !(getenv("ZKH_PIN_WORKERS") && atoi(getenv("ZKH_PIN_WORKERS")) == 0);
+    if (!on) return;
+    cpu_set_t allowed;
+    if (sched_getaffinity(0, sizeof(allowed), &allowed) != 0 || CPU_COUNT(&allowed) < 2) return;
+    const int here = sched_getcpu();
+    std::vector<int> cpus;
+    for (int k = 1; k < CPU_SETSIZE; k++) {
+        const int cpu = (here + k) % CPU_SETSIZE;
+        if (CPU_ISSET(cpu, &allowed)) cpus.push_back(cpu);
+    }
+    if (cpus.empty()) return;
+    cpu_set_t one;
+    CPU_ZERO(&one);
+    CPU_SET(cpus[(size_t)(id - 1) % cpus.size()], &one);
+    (void)pthread_setaffinity_np(t.native_handle(), sizeof(one), &one);
+}
+
 // Host worker threads for the per-job work of a batch (every job has its own transcript,
-// so jobs advance independently).  After a task a worker polls for the next one for about
-// a millisecond, then sleeps on a condition variable; run() returns when every participant
-// has finished.
+// so jobs advance independently).  run(n, f) calls f(0) on the calling thread, offers
+// f(1) .. f(n-1) to the workers and returns when f(0) returns, without waiting for them:
+// a worker that the scheduler leaves off its CPU for a time slice (milliseconds) would
+// otherwise stall a caller whose task is already done.  A worker may therefore call f(t)
+// late, after run() has returned, or not at all.  A task is written so that the calling thread alone completes it, it touches the
+// caller's frame only while holding a claim that the caller waits for, and otherwise
+// only state that it holds by value.  After a task a worker polls for the next one for
+// about a millisecond, then sleeps on a condition variable.
 struct HostPool {
-    std::vector<std::thread> th;
-    std::mutex mu;
-    std::condition_variable cv;
-    std::function<void(int)> task;
-    std::atomic<uint64_t> gen{0};
-    int active = 0;  // workers 1..active take part in the current task
-    std::atomic<int> left{0};
-    bool stop = false;
+    struct Worker {  // one worker thread and its task slot
+        std::mutex mu;
+        std::condition_variable cv;
+        std::function<void(int)> task;
+        std::atomic<uint64_t> gen{0};  // tasks posted to this worker
+        bool stop = false;
+        std::thread th;
+    };
+    std::vector<std::unique_ptr<Worker>> w;
     void ensure(int n) {
-        while ((int)th.size() < n) {
-            const int id = (int)th.size() + 1;
-            th.emplace_back([this, id] {
+        while ((int)w.size() < n) {
+            w.push_back(std::make_unique<Worker>());
+            Worker* W = w.back().get();
+            const int id = (int)w.size();
+            W->th = std::thread([W, id] {
                 uint64_t seen = 0;
                 for (;;) {
                     const auto t0 = std::chrono::steady_clock::now();
-                    for (uint32_t k = 1; gen.load(std::memory_order_acquire) == seen; k++) {
-                        __builtin_ia32_pause();
+                    for (uint32_t k = 1; W->gen.load(std::memory_order_acquire) == seen; k++) {
+                        spin_pause(k);
                         if ((k & 1023) == 0 &&
                             std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(1000))
                             break;
                     }
                     std::function<void(int)> f;
                     {
-                        std::unique_lock<std::mutex> lk(mu);
-                        cv.wait(lk, [&] { return stop || gen.load(std::memory_order_acquire) != seen; });
-                        if (stop) return;
-                        seen = gen.load(std::memory_order_acquire);
-                        if (id > active) continue;
-                        f = task;
+                        std::unique_lock<std::mutex> lk(W->mu);
+                        W->cv.wait(lk, [&] { return W->stop || W->gen.load(std::memory_order_acquire) != seen; });
+                        if (W->stop) return;
+                        seen = W->gen.load(std::memory_order_acquire);  // a late worker takes the latest task
+                        f = W->task;
                     }
                     f(id);
-                    left.fetch_sub(1, std::memory_order_acq_rel);
                 }
             });
+            pin_worker(W->th, id);
         }
     }
-    // f(0) .. f(n-1), f(0) on the calling thread
+    // wakes workers 1 .. n-1 only: the others stay asleep
     void run(int n, const std::function<void(int)>& f) {
-        if (n <= 1) {
-            f(0);
-            return;
+        if (n > 1) ensure(n - 1);
+        for (int i = 0; i + 1 < n; i++) {
+            Worker& W = *w[i];
+            {
+                std::lock_guard<std::mutex> lk(W.mu);
+                W.task = f;
+                W.gen.fetch_add(1, std::memory_order_acq_rel);
+            }
+            W.cv.notify_one();
         }
-        ensure(n - 1);
-        {
-            std::lock_guard<std::mutex> lk(mu);
-            task = f;
-            active = n - 1;
-            left.store(n - 1, std::memory_order_release);
-            gen.fetch_add(1, std::memory_order_acq_rel);
-        }
-        cv.notify_all();
         f(0);
-        while (left.load(std::memory_order_acquire)) __builtin_ia32_pause();
     }
-    ~HostPool() {
-        {
-            std::lock_guard<std::mutex> lk(mu);
-            stop = true;
+    // stop and join the workers (each finishes the task it is in: a task ends by itself
+    // once the caller's share has ended)
+    void shutdown() {
+        for (auto& W : w) {
+            {
+                std::lock_guard<std::mutex> lk(W->mu);
+                W->stop = true;
+            }
+            W->cv.notify_one();
         }
-        cv.notify_all();
-        for (auto& t : th) t.join();
+        for (auto& W : w)
+            if (W->th.joinable()) W->th.join();
+        w.clear();
     }
+    ~HostPool() { shutdown(); }
 };
-// host threads for the per-job work of a batch (ZKH_HOST_THREADS, default 4: with one
-// thread the jobs of a TinyLlama layer wait on each other's transcript work at every round
-// trip, 0.204 against 0.181 ms per matmul step with 4).  The persistent round loops hand
-// each ready message to whichever thread is free, so a thread that the OS preempts delays
-// only the message it is serving.
+// body(0) .. body(n - 1) on up to T threads, each item taken by claiming; returns when
+// every item has completed.  A worker that starts late finds every item claimed and
+// touches only the claim counters, which it holds by value.
+static void pool_for(HostPool& pool, int T, uint32_t n, const std::function<void(uint32_t)>& body) {
+    struct Claims {
+        std::atomic<uint32_t> next{0}, done{0};
+    };
+    auto cl = std::make_shared<Claims>();
+    const std::function<void(uint32_t)>* bp = &body;  // called only for a claimed item
+    pool.run(T, [cl, bp, n](int) {
+        for (uint32_t i; (i = cl->next.fetch_add(1, std::memory_order_acq_rel)) < n;) {
+            (*bp)(i);
+            cl->done.fetch_add(1, std::memory_order_acq_rel);
+        }
+    });
+    for (uint64_t k = 1; cl->done.load(std::memory_order_acquire) < n; k++) spin_pause(k);
+}
+// host threads for the per-job work of a batch, the caller included (ZKH_HOST_THREADS,
+// default 4: with one thread the jobs of a TinyLlama layer wait on each other's transcript
+// work at every round trip, 0.21 against 0.18 ms per matmul step with 4).  The persistent
+// round loops hand each ready message to whichever thread is free, so a thread that the OS
+// deschedules delays only the message it is serving.
 static int host_threads() {
     static const int n = [] {
         const char* e = getenv("ZKH_HOST_THREADS");
@@ -471,7 +532,7 @@ static int wait_pub(zkh_ctx* c, uint32_t seq) {
             }
             if (e != hipErrorNotReady) return fail(c, ZKH_EDEV, "round kernel: %s", hipGetErrorString(e));
         }
-        __builtin_ia32_pause();
+        spin_pause(spins);
     }
     c->ring_off = 0;  // everything queued before the publishing kernel has completed
     if (c->prof) prof_resolve_ready(c);
@@ -706,6 +767,7 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
 }
 extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
     if (!c) return ZKH_EARG;
+    c->workers.shutdown();  // a worker still in a finished task may poll the stream and pinned areas
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     c->mem->release_all();
@@ -1502,20 +1564,17 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
     // u_batch, u_output draws (zkob_fc.cu:259-262), eq factors and eq prefix sums, per job
     // on the host workers
     std::vector<uint32_t> fac(std::max<size_t>(fac_total, 1) * 8, 0);
-    const int Ts = (int)std::min<uint32_t>(nj, (uint32_t)host_threads());
-    c->workers.run(Ts, [&](int t) {
-        for (uint32_t j = (uint32_t)t; j < nj; j += (uint32_t)Ts) {
-            Job& q = J[j];
-            for (auto& x : q.ub) x = tr_challenge(jobs[j].transcript);
-            for (auto& x : q.uo) x = tr_challenge(jobs[j].transcript);
-            std::vector<uint32_t> fb, fo;
-            make_fac(q.ub, 0, fb);
-            make_fac(q.uo, 0, fo);
-            std::copy(fb.begin(), fb.end(), fac.begin() + q.fac_b * 8);
-            std::copy(fo.begin(), fo.end(), fac.begin() + q.fac_o * 8);
-            q.SEb = eq_prefix_sum(q.ub, jobs[j].B);
-            q.SEo = eq_prefix_sum(q.uo, jobs[j].OUT);
-        }
+    pool_for(c->workers, (int)std::min<uint32_t>(nj, (uint32_t)host_threads()), nj, [&](uint32_t j) {
+        Job& q = J[j];
+        for (auto& x : q.ub) x = tr_challenge(jobs[j].transcript);
+        for (auto& x : q.uo) x = tr_challenge(jobs[j].transcript);
+        std::vector<uint32_t> fb, fo;
+        make_fac(q.ub, 0, fb);
+        make_fac(q.uo, 0, fo);
+        std::copy(fb.begin(), fb.end(), fac.begin() + q.fac_b * 8);
+        std::copy(fo.begin(), fo.end(), fac.begin() + q.fac_o * 8);
+        q.SEb = eq_prefix_sum(q.ub, jobs[j].B);
+        q.SEo = eq_prefix_sum(q.uo, jobs[j].OUT);
     });
     // one device area and one upload for the eq factors and every stage's descriptors: the
     // factors first, the descriptors (at most 2 eq tables and 3 reductions per job) after
@@ -1940,8 +1999,6 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         // job's blocks have published
         std::vector<uint32_t> R(nj);
         for (uint32_t j = 0; j < nj; j++) R[j] = J[j].L - lgnb[j];
-        std::atomic<int> abort_why{0};  // 1 device error, 2 kernel ended early, 3 no progress
-        std::atomic<int> dev_err{0};
         const double t_start = now_us();
         // words of the message that follows `done` local rounds: two rounds' sums, one
         // round's sums, or the folded entries after the last local round
@@ -1972,10 +2029,25 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         // try-lock, so a worker that the OS preempts holds up at most the message it is
         // serving, and the others keep every other job moving.
         std::vector<uint32_t> rnd(nj, 0), msg(nj, 0);  // local rounds done, messages answered
-        std::vector<uint8_t> fin(nj, 0);
-        std::unique_ptr<std::atomic<uint8_t>[]> busy(new std::atomic<uint8_t>[nj]);
-        for (uint32_t j = 0; j < nj; j++) busy[j].store(0, std::memory_order_relaxed);
-        std::atomic<uint32_t> open_jobs{nj};
+        // What a worker touches outside a job's lock lives on the heap, held by each worker
+        // by value: a worker that the OS deschedules may return after this frame has ended.
+        // A worker touches this frame only inside serve() and the stall check, holding
+        // busy[j] for an unfinished job; this frame ends only after every job is finished
+        // or abandoned and it has taken every job's lock.
+        struct Loop {
+            std::unique_ptr<std::atomic<uint8_t>[]> busy;
+            std::vector<uint8_t> fin;  // written and read under busy[j]
+            std::atomic<uint32_t> open_jobs;
+            std::atomic<int> abort_why{0};  // 1 device error, 2 kernel ended early, 3 no progress, 4 stream idle
+            std::atomic<int> dev_err{0};
+            std::atomic<bool> closed{false};
+            std::vector<double> tr_thr;  // each thread's entry / exit / longest stream query (tracing)
+            Loop(uint32_t nj, int T, bool tracing)
+                : busy(new std::atomic<uint8_t>[nj]), fin(nj, 0), open_jobs(nj), tr_thr(tracing ? 3 * T : 0) {
+                for (uint32_t j = 0; j < nj; j++) busy[j].store(0, std::memory_order_relaxed);
+            }
+        };
+        const auto lp = std::make_shared<Loop>(nj, T, tracing);
         // serve job j's pending message if complete (caller holds busy[j]); false if not ready
         auto serve = [&](uint32_t j, std::vector<Fr>& ta, std::vector<Fr>& tb) -> bool {
             const uint32_t nb = 1u << lgnb[j];
@@ -1988,8 +2060,8 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
             const uint32_t r = rnd[j];
             auto stop_job = [&]() {
                 send_cmd(j, ZKH_QUIT, nullptr, 0);
-                fin[j] = 1;
-                open_jobs.fetch_sub(1, std::memory_order_acq_rel);
+                lp->fin[j] = 1;
+                lp->open_jobs.fetch_sub(1, std::memory_order_acq_rel);
             };
             if (nw == ZKH_MSG_PAIR) {  // rounds r and r + 1
                 Fr sm[9];
@@ -2075,42 +2147,54 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                 }
             }
             if (ok) finish(j, ta[0], tb[0]);
-            fin[j] = 1;
-            open_jobs.fetch_sub(1, std::memory_order_acq_rel);
+            lp->fin[j] = 1;
+            lp->open_jobs.fetch_sub(1, std::memory_order_acq_rel);
             return true;
         };
-        auto worker = [&](int t) {
+        // captures by value but for what is used under a job's lock
+        auto worker = [lp, c, ps, nj, tracing, &serve, &ready, &msg_words, &msg, &rnd](int t) {
+            Loop& L = *lp;
+            struct Stamp {
+                double* at;
+                ~Stamp() {
+                    if (at) *at = now_us();
+                }
+            } on_exit{tracing ? &L.tr_thr[3 * t + 1] : nullptr};
+            if (tracing) L.tr_thr[3 * t] = now_us();
             std::vector<Fr> ta, tb;
             double t_prog = now_us();
-            for (uint64_t spins = 1; open_jobs.load(std::memory_order_acquire); spins++) {
+            for (uint64_t spins = 1;
+                 !L.closed.load(std::memory_order_acquire) && L.open_jobs.load(std::memory_order_acquire); spins++) {
                 bool prog = false;
                 for (uint32_t k = 0; k < nj; k++) {
                     const uint32_t j = (k + (uint32_t)t) % nj;  // each worker starts at its own job
-                    if (busy[j].load(std::memory_order_relaxed) || busy[j].exchange(1, std::memory_order_acquire))
+                    if (L.busy[j].load(std::memory_order_relaxed) || L.busy[j].exchange(1, std::memory_order_acquire))
                         continue;
-                    if (!fin[j] && serve(j, ta, tb)) prog = true;
-                    busy[j].store(0, std::memory_order_release);
+                    if (!L.fin[j] && serve(j, ta, tb)) prog = true;
+                    L.busy[j].store(0, std::memory_order_release);
                 }
                 if (prog) {
                     t_prog = now_us();
                     continue;
                 }
-                __builtin_ia32_pause();
+                spin_pause(spins);
                 if ((spins & 0x3FFF) == 0) {
-                    if (abort_why.load(std::memory_order_relaxed)) return;
+                    if (L.abort_why.load(std::memory_order_relaxed) || L.closed.load(std::memory_order_acquire)) return;
+                    const double q0 = tracing ? now_us() : 0.0;
                     hipError_t e = hipStreamQuery(c->stream);
+                    if (tracing) L.tr_thr[3 * t + 2] = std::max(L.tr_thr[3 * t + 2], now_us() - q0);
                     int why = 0;
                     if (e != hipSuccess && e != hipErrorNotReady) {
-                        dev_err.store((int)e);
+                        L.dev_err.store((int)e);
                         why = 1;
                     } else if (__atomic_load_n(ps, __ATOMIC_ACQUIRE)) {
                         why = 2;
                     } else if (e == hipSuccess) {  // the kernel has ended: whatever is missing never comes
                         bool all = true;
                         for (uint32_t j = 0; j < nj; j++) {
-                            if (busy[j].exchange(1, std::memory_order_acquire)) continue;  // being served
-                            all = all && (fin[j] || ready(j, msg[j] + 1, msg_words(j, rnd[j])));
-                            busy[j].store(0, std::memory_order_release);
+                            if (L.busy[j].exchange(1, std::memory_order_acquire)) continue;  // being served
+                            all = all && (L.fin[j] || ready(j, msg[j] + 1, msg_words(j, rnd[j])));
+                            L.busy[j].store(0, std::memory_order_release);
                         }
                         if (!all) why = 4;
                     } else if (now_us() - t_prog > 30e6) {
@@ -2118,17 +2202,22 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
                     }
                     if (why) {
                         int z = 0;
-                        abort_why.compare_exchange_strong(z, why);
+                        L.abort_why.compare_exchange_strong(z, why);
                         return;
                     }
                 }
             }
         };
         c->workers.run(T, worker);
-        if (int why = abort_why.load()) {
+        // the calling thread's share has ended: every job is finished, or the loop is
+        // abandoned; close it and wait out any worker still inside a job's work
+        lp->closed.store(true, std::memory_order_release);
+        for (uint32_t j = 0; j < nj; j++)
+            for (uint64_t k = 1; lp->busy[j].exchange(1, std::memory_order_acquire); k++) spin_pause(k);
+        if (int why = lp->abort_why.load()) {
             quit_all();
             if (why == 1)
-                return fail(c, ZKH_EDEV, "persistent round loop: %s", hipGetErrorString((hipError_t)dev_err.load()));
+                return fail(c, ZKH_EDEV, "persistent round loop: %s", hipGetErrorString((hipError_t)lp->dev_err.load()));
             return fail(c, ZKH_EDEV, "persistent round loop stopped (%s; clock %llu kHz)",
                         why == 2 ? "a block timed out" : why == 4 ? "stream idle before the last round" : "no progress",
                         (unsigned long long)c->clock_khz);
@@ -2136,7 +2225,13 @@ static int mm_batch(zkh_ctx* c, zkh_mm_job* jobs, uint32_t nj) {
         c->ring_off = 0;  // every launch before the round loop has completed
         stamp("round loops done");
         if (tracing) {
-            fprintf(stderr, "[zkh] mm persistent rounds: %.1f us (%d host threads)\n", now_us() - t_start, T);
+            fprintf(stderr, "[zkh] mm persistent rounds: %.1f us (%d host threads; entry/exit us", now_us() - t_start, T);
+            for (int t = 0; t < T; t++) {  // a worker still running (or not started) shows 0
+                const double* th = &lp->tr_thr[3 * t];
+                fprintf(stderr, " %.1f/%.1f (longest stream query %.1f)", th[0] ? th[0] - t_start : 0.0,
+                        th[1] ? th[1] - t_start : 0.0, th[2]);
+            }
+            fprintf(stderr, ")\n");
             const double tick_us = 1000.0 / (double)c->clock_khz;
             // per message: block 0's compute (device clock: previous command received -> sums
             // published) and round trip (sums published -> command received), and the host's
@@ -2572,7 +2667,7 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
                         break;
                     }
             if (all) return 0;
-            __builtin_ia32_pause();
+            spin_pause(spins);
             if ((spins & 0x3FFF) == 0) {
                 hipError_t e = hipStreamQuery(c->stream);
                 if (e != hipSuccess && e != hipErrorNotReady) {
@@ -3383,7 +3478,7 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
                         break;
                     }
             if (all) return 0;
-            __builtin_ia32_pause();
+            spin_pause(spins);
             if ((spins & 0x3FFF) == 0) {
                 hipError_t e = hipStreamQuery(c->stream);
                 if (e != hipSuccess && e != hipErrorNotReady) {
