@@ -171,9 +171,7 @@ class GluJob:
         S, m = c.lu_mapping(self.G, self.low, self.mapped)
         r = zkh.challenge(st)
         beta = zkh.challenge(st)
-        comb = c.axpy(self.G, r, S)
-        Tcomb = c.axpy(self.T, r, self.mapped)
-        A = c.lu_inverse(comb, beta)
+        comb, Tcomb, A = c.lu_tuple_inverse(self.G, self.low, self.T, self.mapped, r, beta)
         zkh.absorb(st, "com_A", self.comA)
         alpha = zkh.challenge(st)
         u = zkh.challenges(st, self.logD)

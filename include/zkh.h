@@ -235,6 +235,18 @@ int zkh_lu_mapping(zkh_ctx* ctx, const zkh_tensor* S_in, int32_t low, const zkh_
 /* tlookup_inv_kernel (tlookup.cu:50-62): A[i] = 1/(S[i]+beta), inverse(0) = 0; batched
  * (Montgomery's trick) */
 int zkh_lu_inverse(zkh_ctx* ctx, const zkh_tensor* S, const uint32_t beta[8], zkh_tensor** A_out);
+/* zkob_glu.cu:155-170 in one call, for int32 G (D entries), T and mapped (N entries):
+ * comb = G + r*S with S[i] = mapped[(G[i]-low).limb0] (zkh_lu_mapping's S), T_comb = T +
+ * r*mapped, A = 1/(comb+beta) (inverse(0) = 0) -- the outputs of zkh_lu_mapping's S with
+ * zkh_axpy twice and zkh_lu_inverse.  No counterpart in the reference, which inverts comb
+ * (D entries) and T_comb (N entries) separately: here A[i] is read off the table inverse
+ * 1/(T_comb+beta) wherever T[j] == G[i] (comb[i] is then T_comb[j]), with a direct inversion
+ * of comb if some entry is not; the table inverse stays with the context, and the next
+ * zkh_lu_prove on this T_comb and beta uses it instead of inverting T_comb again.
+ * ZKH_EARG if an index falls outside [0, N) (as zkh_lu_mapping). */
+int zkh_lu_tuple_inverse(zkh_ctx* ctx, const zkh_tensor* G, int32_t low, const zkh_tensor* T,
+                         const zkh_tensor* mapped, const uint32_t r[8], const uint32_t beta[8],
+                         zkh_tensor** comb_out, zkh_tensor** Tcomb_out, zkh_tensor** A_out);
 /* FS lookup recursion, zkob_rescale.cu:132-146 with fs_phase1/fs_phase2
  * (zkob_lookup.cuh:143-198): from Bv = 1/(T+beta) through the rounds (absorbing
  * "p0".."p3" each) to absorbing "A_f","S_f","m_f".  A, S: D entries; T, m: N entries;

@@ -570,6 +570,86 @@ def test_lu_mapping(zkh, ctx):
     assert fr_eq(m.to_fr(), mw)
 
 
+def tuple_case(D, N, ln, seed):
+    """A SwiGLU-style tuple lookup: witness G in the table's domain with zero padding in its
+    last eighth, a mapped table with int32 extremes, and where the table is padded (ln < N)
+    a few witnesses past ln, whose table entry (low + ln - 1) is not the witness."""
+    rng = np.random.default_rng(seed)
+    low = -(N // 2)
+    mapped = rng.integers(-2**31, 2**31, size=N, dtype=np.int64)
+    mapped[:4] = [2**31 - 1, -2**31, -1, 0]
+    mapped[-low] = 0
+    mapped = mapped.astype(np.int32)
+    G = rng.integers(low, low + min(ln, N), size=D).astype(np.int32)
+    G[-(D // 8):] = 0
+    if ln < N:
+        G[:7] = low + ln + np.arange(7) % (N - ln)
+    r, beta = rand_fr_full(rng, 2)
+    # the reference's steps on the oracle (zkob_glu.cu:155-160, :168-170)
+    S = C.ints_to_fr([int(mapped[g - low]) for g in G])
+    comb = C.axpy(C.ints_to_fr([int(g) for g in G]), r, S)
+    Tcomb = C.axpy(C.range_table(low, ln, N), r, C.ints_to_fr([int(v) for v in mapped]))
+    return dict(low=low, mapped=mapped, G=G, r=r, beta=beta, comb=comb, Tcomb=Tcomb)
+
+
+@pytest.mark.parametrize("D,N,ln,gkind", [(4096, 4096, 4096, "i32"), (1 << 14, 1 << 12, 1 << 12, "fr"),
+                                           (4096, 1024, 1000, "i32"), (4096, 1024, 1000, "fr"),
+                                           (1 << 20, 1 << 18, 1 << 18, "i32")])
+def test_lu_tuple_inverse(zkh, ctx, D, N, ln, gkind):
+    """comb = G + r mapped[G - low], T_comb = T + r mapped and A = 1/(comb + beta) in one call
+    equal the reference's separate steps on the oracle: A read off the table inverse (every
+    G[i] the table's entry at its index), or, with a padded table and witnesses past ln, by
+    the direct inversion of comb; int32- and field-kind witnesses.  A is also checked against
+    the definition (A (comb + beta) = 1)."""
+    t = tuple_case(D, N, ln, D + N + ln)
+    G = ctx.from_i32(t["G"]) if gkind == "i32" else ctx.from_fr(C.ints_to_fr([int(g) for g in t["G"]]))
+    comb, Tcomb, A = ctx.lu_tuple_inverse(G, t["low"], ctx.range_table(t["low"], ln, N), ctx.from_i32(t["mapped"]),
+                                          t["r"], t["beta"])
+    assert fr_eq(comb.to_fr(), t["comb"])
+    assert fr_eq(Tcomb.to_fr(), t["Tcomb"])
+    got = A.to_fr()
+    assert C.check_inverse(t["comb"], got, t["beta"]) == 0
+    if D <= 1 << 14:
+        assert fr_eq(got, C.lu_inverse(t["comb"], t["beta"]))
+
+
+@pytest.mark.parametrize("D,N", [(1 << 16, 1 << 16), (1 << 16, 1 << 14)])
+def test_lu_prove_takes_table_inverse(zkh, ctx, D, N):
+    """The SwiGLU lookup through zkh_lu_tuple_inverse: the proof that takes its table inverse
+    over equals the oracle's from the separate steps; a second proof on the same tensors (the
+    table inverse then folded and gone) inverts T_comb itself and equals it too."""
+    t = tuple_case(D, N, N, D * 3 + N)
+    rng = np.random.default_rng(D + 5 * N)
+    alpha = rand_fr_full(rng, 1)
+    u = rand_fr_full(rng, P.ceil_log2(D))
+    rc, m = C.lu_prep(C.ints_to_fr([int(g) for g in t["G"]]), t["low"], N)
+    assert rc == 0
+    A_o = C.lu_inverse(t["comb"], t["beta"])
+    Gg = ctx.from_i32(t["G"])
+    _, mg = ctx.lu_mapping(Gg, t["low"], ctx.from_i32(t["mapped"]))
+    assert fr_eq(mg.to_fr(), m)
+    comb, Tcomb, A = ctx.lu_tuple_inverse(Gg, t["low"], ctx.range_table(t["low"], N, N), ctx.from_i32(t["mapped"]),
+                                          t["r"], t["beta"])
+    for k in range(2):
+        st_g, st_o = seed_transcript(zkh, "lut:%d:%d:%d" % (D, N, k))
+        rc, want = C.lu_prove(st_o, A_o, t["comb"], t["Tcomb"], m, alpha, t["beta"], u)
+        assert rc == 0
+        got = ctx.lu_prove(st_g, A, comb, Tcomb, mg, alpha, t["beta"], u)
+        for key in ("ev", "term", "ws"):
+            assert fr_eq(got[key], want[key]), (k, key)
+        assert bytes(st_g) == bytes(st_o)
+
+
+def test_lu_tuple_inverse_out_of_range(zkh, ctx):
+    """A witness outside the table's domain fails as zkh_lu_mapping does."""
+    low, N = -8, 16
+    G = np.array([0, 3, low + N, -2], np.int32)
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.lu_tuple_inverse(ctx.from_i32(G), low, ctx.range_table(low, N, N), ctx.from_i32(np.zeros(N, np.int32)),
+                             C.ints_to_fr([5]), C.ints_to_fr([7]))
+    assert e.value.code == zkh.EARG
+
+
 # ---------------------------------------------------------------- elementwise with int32 operands
 def test_hadamard_axpy_int32_edges(zkh, ctx):
     """Elementwise products and axpy with int32 operands take the 32-bit multiply (quotient

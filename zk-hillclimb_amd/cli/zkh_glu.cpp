@@ -89,10 +89,11 @@ int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& 
     absorb(st, "com_H", hH.data(), hH.size() * 4);
     absorb(st, "com_m", hm.data(), hm.size() * 4);
     const std::vector<uint32_t> r = challenge(st), beta = challenge(st);
-    chk(zkh_axpy(g_ctx, Gp.t, r.data(), Sp.t, &comb.t), "comb = G + r S");
+    // comb = G + r S, T_comb = T + r mapped and A = 1/(comb + beta) (zkob_glu.cu:155-160),
+    // A through the table inverse, which zkh_lu_prove then takes over (zkob_glu.cu:168-170)
     chk(zkh_lu_range_table(g_ctx, low, len, N, &T.t), "table");
-    chk(zkh_axpy(g_ctx, T.t, r.data(), tmap.t, &Tcomb.t), "T_comb = T + r mapped");
-    chk(zkh_lu_inverse(g_ctx, comb.t, beta.data(), &A.t), "inverses");
+    chk(zkh_lu_tuple_inverse(g_ctx, Gp.t, low, T.t, tmap.t, r.data(), beta.data(), &comb.t, &Tcomb.t, &A.t),
+        "comb, T_comb and inverses");
     chk(zkh_commit(g_ctx, g.g, A.t, &cA.g), "commit A");
     const std::vector<uint32_t> hA = to_host(cA.g);
     write_all(obdir + "/com_A.bin", hA.data(), hA.size() * 4);

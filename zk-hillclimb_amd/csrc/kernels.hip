@@ -937,6 +937,61 @@ void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
         k_lu_map_i32<<<grid_for(n, NT, 8192), NT, 0, s>>>(S, n, low, lm, N, PL_LO(out), PL_HI(out));
     });
 }
+// The tuple lookup's witness side from the table side: with j = (G[i] - low).limb0 (the
+// reference's index, tlookup.cu:469-482), comb[i] = G[i] + r mapped[j] (the combiner of
+// zkob_glu.cu:155 with S = mapped[j], the product formed as k_axpy forms it) and, where
+// T[j] == G[i] (comb[i] is then T_comb[j]), A[i] = Binv[j] = 1/(T_comb[j] + beta).
+// *flags |= 1 for j outside [0, N) (nothing written at i), |= 2 for T[j] != G[i] (A[i] left
+// for the caller's direct inversion).  tlen > 0: T is the range table low + min(j, tlen - 1),
+// so T[j] == G[i] iff G[i] - low is the integer j < tlen, and T is not read.
+template <typename LG, typename LT, typename LM>
+__global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tlen, LM mapped, uint32_t N, fr_t rm,
+                                  fr_t r,
+                                  const uint4* __restrict__ blo, const uint4* __restrict__ bhi, uint4* clo,
+                                  uint4* chi, uint4* alo, uint4* ahi, uint32_t* flags) {
+    uint32_t f = 0;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const fr_t g = G(i);
+        const fr_t d = fr_sub(g, low);
+        const uint32_t j = d.v[0];
+        if (j >= N) {
+            f |= 1u;
+            continue;
+        }
+        st_fr(clo, chi, i, fr_add(g, scale_of(rm, r, mapped, j)));
+        bool same = true;
+        if (tlen) {
+            same = j < tlen;
+            for (int k = 1; k < 8; k++) same = same && d.v[k] == 0;
+        } else {
+            const fr_t t = T(j);
+            for (int k = 0; k < 8; k++) same = same && t.v[k] == g.v[k];
+        }
+        if (same) {
+            alo[i] = blo[j];
+            ahi[i] = bhi[j];
+        } else {
+            f |= 2u;
+        }
+    }
+    // one atomic per wave that saw a flag
+    const uint64_t any1 = __ballot(f & 1u), any2 = __ballot(f & 2u);
+    if ((any1 | any2) && (threadIdx.x & 63) == 0) atomicOr(flags, (any1 ? 1u : 0u) | (any2 ? 2u : 0u));
+}
+void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
+                            Src mapped, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host, DevPlanes Binv,
+                            DevPlanes comb, DevPlanes A, uint32_t* flags) {
+    const fr_t low = to_fr(low_host), r = to_fr(r_host), rm = to_fr(r_m_host);
+    with_loader(G, [&](auto lg) {
+        with_loader(T, [&](auto lt) {
+            with_loader(mapped, [&](auto lm) {
+                k_lu_tuple_gather<<<grid_for(n, NT, 8192), NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
+                                                                        PL_HI(Binv), PL_LO(comb), PL_HI(comb),
+                                                                        PL_LO(A), PL_HI(A), flags);
+            });
+        });
+    });
+}
 
 // Batched inversion (Montgomery's trick) in three Montgomery products per entry.  With
 // M(a, b) = a b 2^-256, the running products P_0 = 2^256, P_j = M(P_{j-1}, x_j) of the plain

@@ -253,6 +253,11 @@ struct zkh_ctx {
     size_t ps_words = 0;
     uint64_t clock_khz = 100000;
     HostPool workers;
+    // the table inverse 1/(T_comb + beta) of the last zkh_lu_tuple_inverse, for the
+    // zkh_lu_prove on that T_comb (generation lu_tinv_of) and beta, which takes it over
+    zkh_tensor* lu_tinv = nullptr;
+    uint64_t lu_tinv_of = 0;
+    uint32_t lu_tinv_beta[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     std::mutex err_mu;  // error reporting from worker threads
     // pinned ring for small host->device uploads: a region is reused only after a later
     // stream synchronisation, which every API call performs before returning
@@ -363,6 +368,11 @@ struct zkh_tensor {
     // the tensor S of generation inv_of (0: no such knowledge)
     uint64_t inv_of = 0;
     uint32_t inv_beta[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    // set by zkh_lu_range_table: entry j is range_low + min(j, range_len - 1) while gen is
+    // range_gen (0: no such knowledge)
+    uint64_t range_gen = 0;
+    int32_t range_low = 0;
+    uint32_t range_len = 0;
     DevPlanes planes() const { return DevPlanes{(uint32_t*)d, cap}; }
 };
 static uint64_t next_gen() {
@@ -770,6 +780,7 @@ extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
     c->workers.shutdown();  // a worker still in a finished task may poll the stream and pinned areas
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    if (c->lu_tinv) zkh_tensor_free(c->lu_tinv);
     c->mem->release_all();
     for (auto& s : c->slots)
         if (s.p) (void)hipFree(s.p);
@@ -2357,6 +2368,9 @@ extern "C" int zkh_lu_range_table(zkh_ctx* c, int32_t low, uint32_t len, uint32_
         zkh_tensor_free(t);
         return fail(c, ZKH_EDEV, "range table: %s", hipGetErrorString(e));
     }
+    t->range_gen = t->gen;
+    t->range_low = low;
+    t->range_len = len;
     *out = t;
     return ZKH_OK;
 }
@@ -2524,6 +2538,63 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
     }
     A->inv_of = S->gen;
     memcpy(A->inv_beta, beta, 32);
+    *A_out = A;
+    return ZKH_OK;
+}
+extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low, const zkh_tensor* T,
+                                    const zkh_tensor* mapped, const uint32_t r[8], const uint32_t beta[8],
+                                    zkh_tensor** comb_out, zkh_tensor** Tcomb_out, zkh_tensor** A_out) {
+    if (!c || !G || !T || !mapped || !r || !beta || !comb_out || !Tcomb_out || !A_out)
+        return fail(c, ZKH_EARG, "null argument");
+    const uint32_t D = G->n, N = T->n;
+    if (!N || mapped->n != N) return fail(c, ZKH_EARG, "T and mapped differ in size or are empty");
+    if (!fr_is_canonical(r) || !fr_is_canonical(beta)) return fail(c, ZKH_EARG, "non-canonical r or beta");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    Src sg, st, sm;
+    if ((rc = src_of(c, G, SL_TMP0, &sg)) || (rc = src_of(c, T, SL_TMP1, &st)) || (rc = src_of(c, mapped, SL_TMP2, &sm)))
+        return rc;
+    zkh_tensor *comb = nullptr, *Tcomb = nullptr, *A = nullptr, *Binv = nullptr;
+    auto drop = [&](int code) {
+        for (zkh_tensor* t : {comb, Tcomb, A, Binv})
+            if (t) zkh_tensor_free(t);
+        return code;
+    };
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, D, &comb)) || (rc = tensor_alloc(c, ZKH_KIND_FR, N, &Tcomb)) ||
+        (rc = tensor_alloc(c, ZKH_KIND_FR, D, &A)) || (rc = tensor_alloc(c, ZKH_KIND_FR, N, &Binv)))
+        return drop(rc);
+    uint32_t rm[8];
+    fr_store(fr_to_mont(fr_load(r)), rm);
+    // T_comb = T + r mapped (zkob_glu.cu:156) and its inverse (zkob_glu.cu:168-170)
+    launch_axpy(c->stream, st, r, rm, sm, N, Tcomb->planes());
+    if ((rc = batch_inverse(c, Tcomb->planes(), N, fr_load(beta), Binv->planes()))) return drop(rc);
+    uint32_t* flags = (uint32_t*)scratch_slot(c, SL_PARTIAL, 256, &rc);
+    if (rc) return drop(rc);
+    HIPCHK(c, hipMemsetAsync(flags, 0, 4, c->stream));
+    uint32_t hf = 0;
+    if (D) {
+        ProfScope ps(c, "lu_tuple_gather", (double)D * (4 + 4 + 4 + 32 + 32 + 32));
+        uint32_t lowl[8];
+        fr_store(fr_from_i64(low), lowl);
+        // a range table at this low: T[j] == G[i] iff G[i] - low is j < len, read from G alone
+        const uint32_t tlen = T->range_gen == T->gen && T->range_low == low ? T->range_len : 0;
+        launch_lu_tuple_gather(c->stream, sg, D, lowl, st, tlen, sm, N, r, rm, Binv->planes(), comb->planes(),
+                               A->planes(), flags);
+    }
+    if ((rc = settle(c, flags, &hf))) return drop(rc);
+    if (hf & 1u) return drop(fail(c, ZKH_EARG, "lookup witness outside the table"));
+    // an entry whose G is not the table's at its index (comb is then no table entry): A by
+    // the direct batched inversion of comb (zkob_glu.cu:158-160)
+    if ((hf & 2u) && ((rc = batch_inverse(c, comb->planes(), D, fr_load(beta), A->planes())) || (rc = settle(c))))
+        return drop(rc);
+    A->inv_of = comb->gen;
+    memcpy(A->inv_beta, beta, 32);
+    if (c->lu_tinv) zkh_tensor_free(c->lu_tinv);
+    c->lu_tinv = Binv;
+    c->lu_tinv_of = Tcomb->gen;
+    memcpy(c->lu_tinv_beta, beta, 32);
+    *comb_out = comb;
+    *Tcomb_out = Tcomb;
     *A_out = A;
     return ZKH_OK;
 }
@@ -2766,9 +2837,25 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     if (rc) return rc;
     DevPlanes mw = m->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP3, N / 2, &rc) : mc;
     if (rc) return rc;
-    DevPlanes Bw = scratch_planes(c, SL_EO, N, &rc);  // Bv = 1/(T+beta), owned
+    // Bv = 1/(T+beta), owned: zkh_lu_tuple_inverse's table inverse when T is its T_comb and
+    // beta its beta (taken over: the rounds fold it in place), else inverted here
+    struct TakenInverse {
+        zkh_ctx* c;
+        zkh_tensor* t = nullptr;
+        ~TakenInverse() {
+            if (!t) return;
+            (void)hipStreamSynchronize(c->stream);
+            zkh_tensor_free(t);
+        }
+    } taken{c};
+    if (c->lu_tinv && c->lu_tinv_of == T->gen && !memcmp(c->lu_tinv_beta, beta_l, 32) && c->lu_tinv->n == N) {
+        taken.t = c->lu_tinv;
+        c->lu_tinv = nullptr;
+        c->lu_tinv_of = 0;
+    }
+    DevPlanes Bw = taken.t ? taken.t->planes() : scratch_planes(c, SL_EO, N, &rc);
     if (rc) return rc;
-    if ((rc = batch_inverse(c, Tc, N, beta, Bw))) return rc;
+    if (!taken.t && (rc = batch_inverse(c, Tc, N, beta, Bw))) return rc;
 
     // C = alpha^2 - sum Bv*m (zkob_rescale.cu:136); only the phase-1 rounds (D > N) use it
     Fr bm = kZero;
