@@ -295,7 +295,7 @@ class LookupJob:
         st = self.st0.copy()
         m = c.lu_prep(self.S, self.low, self.N)
         beta = zkh.challenge(st)
-        A = c.lu_inverse(self.S, beta)
+        A = c.lu_range_inverse(self.S, self.low, self.T, beta)
         alpha = zkh.challenge(st)
         u = zkh.challenges(st, self.logD)
         lu = c.lu_prove(st, A, self.S, self.T, m, alpha, beta, u)

@@ -235,6 +235,14 @@ int zkh_lu_mapping(zkh_ctx* ctx, const zkh_tensor* S_in, int32_t low, const zkh_
 /* tlookup_inv_kernel (tlookup.cu:50-62): A[i] = 1/(S[i]+beta), inverse(0) = 0; batched
  * (Montgomery's trick) */
 int zkh_lu_inverse(zkh_ctx* ctx, const zkh_tensor* S, const uint32_t beta[8], zkh_tensor** A_out);
+/* zkh_lu_inverse's A = 1/(S+beta) (inverse(0) = 0) for a range lookup against the table T
+ * (N entries): A[i] is read off the table inverse 1/(T+beta) at j = (S[i]-low).limb0 wherever
+ * T[j] == S[i] (one table-sized inversion instead of a witness-sized one), with a direct
+ * inversion of S if some entry is not; the table inverse stays with the context, and the
+ * next zkh_lu_prove on this T and beta uses it instead of inverting T again.  No counterpart
+ * in the reference, which inverts S (zkob_rescale.cu:121-123) and T separately. */
+int zkh_lu_range_inverse(zkh_ctx* ctx, const zkh_tensor* S, int32_t low, const zkh_tensor* T,
+                         const uint32_t beta[8], zkh_tensor** A_out);
 /* zkob_glu.cu:155-170 in one call, for int32 G (D entries), T and mapped (N entries):
  * comb = G + r*S with S[i] = mapped[(G[i]-low).limb0] (zkh_lu_mapping's S), T_comb = T +
  * r*mapped, A = 1/(comb+beta) (inverse(0) = 0) -- the outputs of zkh_lu_mapping's S with

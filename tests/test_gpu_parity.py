@@ -570,6 +570,22 @@ def test_lu_mapping(zkh, ctx):
     assert fr_eq(m.to_fr(), mw)
 
 
+@pytest.mark.parametrize("n", [3 * (1 << 20) + 17, 1 << 21, (1 << 23) + 3])
+def test_lu_inverse_sizes(zkh, ctx, n):
+    """Batched inversion at sizes whose block products take the one-block stage's register
+    path (up to 8 per thread, a partial last group) and its loop path (more than 8):
+    A (S + beta) = 1 on every entry, against the oracle, with one entry S = -beta (inverse
+    of zero is zero)."""
+    rng = np.random.default_rng(n)
+    S = rng.integers(0, 2**32, size=(n, 8), dtype=np.uint64).astype(np.uint32)
+    S[:, 7] %= 0x73EDA753  # below r
+    beta = rand_fr_full(rng, 1)[0]
+    S[5] = C.ints_to_fr([(P.R - C.fr_to_ints(beta.reshape(1, 8))[0]) % P.R])[0]
+    A = ctx.lu_inverse(ctx.from_fr(S), beta).to_fr()
+    assert C.check_inverse(S, A, beta) == 0
+    assert not np.asarray(A).reshape(-1, 8)[5].any()
+
+
 def tuple_case(D, N, ln, seed):
     """A SwiGLU-style tuple lookup: witness G in the table's domain with zero padding in its
     last eighth, a mapped table with int32 extremes, and where the table is padded (ln < N)
@@ -635,6 +651,54 @@ def test_lu_prove_takes_table_inverse(zkh, ctx, D, N):
         rc, want = C.lu_prove(st_o, A_o, t["comb"], t["Tcomb"], m, alpha, t["beta"], u)
         assert rc == 0
         got = ctx.lu_prove(st_g, A, comb, Tcomb, mg, alpha, t["beta"], u)
+        for key in ("ev", "term", "ws"):
+            assert fr_eq(got[key], want[key]), (k, key)
+        assert bytes(st_g) == bytes(st_o)
+
+
+@pytest.mark.parametrize("D,N,ln,skind", [(1 << 16, 1 << 12, 1 << 12, "i32"), (1 << 14, 1 << 12, 3000, "fr"),
+                                           (1 << 14, 1 << 12, 3000, "i32"), (4096, 4096, 4096, "fr")])
+def test_lu_range_inverse(zkh, ctx, D, N, ln, skind):
+    """zkh_lu_range_inverse's A (read off the table inverse) equals zkh_lu_inverse's and the
+    oracle's 1/(S + beta): witnesses in the table's domain with zero padding, and with a padded
+    table (ln < N) witnesses past ln and one outside the domain (the direct inversion);
+    int32- and field-kind witnesses."""
+    rng = np.random.default_rng(D + N + ln)
+    low = -(N // 2)
+    vals = rng.integers(low, low + ln, size=D).astype(np.int64)
+    vals[-(D // 8):] = 0
+    if ln < N:
+        vals[:5] = low + ln + np.arange(5) % (N - ln)
+        vals[5] = low + N + 7
+    ints = [int(v) for v in vals]
+    beta = rand_fr_full(rng, 1)[0]
+    S = ctx.from_i32(vals.astype(np.int32)) if skind == "i32" else ctx.from_fr(C.ints_to_fr(ints))
+    want = C.lu_inverse(C.ints_to_fr(ints), beta)
+    assert fr_eq(ctx.lu_range_inverse(S, low, ctx.range_table(low, ln, N), beta).to_fr(), want)
+    assert fr_eq(ctx.lu_inverse(S, beta).to_fr(), want)
+
+
+@pytest.mark.parametrize("D,N", [(1 << 16, 1 << 12), (1 << 15, 1 << 15)])
+def test_lu_prove_takes_range_table_inverse(zkh, ctx, D, N):
+    """The rescale lookup through zkh_lu_range_inverse (phase 1 and phase 2, and phase 2
+    alone): the proof that takes the table inverse over, and a second proof on the same
+    tensors, equal the oracle's."""
+    low = -(N // 2)
+    rng = np.random.default_rng(7 * D + N)
+    vals = rng.integers(low, low + N, size=D).astype(np.int32)
+    Sf = C.ints_to_fr([int(v) for v in vals])
+    rc, m = C.lu_prep(Sf, low, N)
+    assert rc == 0
+    beta, alpha = rand_fr_full(rng, 2)
+    u = rand_fr_full(rng, P.ceil_log2(D))
+    A_o = C.lu_inverse(Sf, beta)
+    Sg, Tg = ctx.from_i32(vals), ctx.range_table(low, N, N)
+    A, mg = ctx.lu_range_inverse(Sg, low, Tg, beta), ctx.from_fr(m)
+    for k in range(2):
+        st_g, st_o = seed_transcript(zkh, "lur:%d:%d:%d" % (D, N, k))
+        rc, want = C.lu_prove(st_o, A_o, Sf, C.range_table(low, N, N), m, alpha, beta, u)
+        assert rc == 0
+        got = ctx.lu_prove(st_g, A, Sg, Tg, mg, alpha, beta, u)
         for key in ("ev", "term", "ws"):
             assert fr_eq(got[key], want[key]), (k, key)
         assert bytes(st_g) == bytes(st_o)

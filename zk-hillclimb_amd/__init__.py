@@ -83,6 +83,7 @@ def lib():
         L.zkh_lu_prep.argtypes = [vp, vp, i32, u32, ctypes.POINTER(vp)]
         L.zkh_lu_mapping.argtypes = [vp, vp, i32, vp, ctypes.POINTER(vp), ctypes.POINTER(vp)]
         L.zkh_lu_inverse.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
+        L.zkh_lu_range_inverse.argtypes = [vp, vp, i32, vp, vp, ctypes.POINTER(vp)]
         L.zkh_lu_tuple_inverse.argtypes = [vp, vp, i32, vp, vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp),
                                            ctypes.POINTER(vp)]
         L.zkh_lu_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -460,6 +461,12 @@ class Context:
     def lu_inverse(self, S, beta):
         beta = _frs(beta, 1)
         return self._new(lib().zkh_lu_inverse, S.h, _p(beta))
+
+    def lu_range_inverse(self, S, low, T, beta):
+        """1/(S + beta) as lu_inverse, read off the table inverse of T (a range lookup); the
+        table inverse goes on to the lu_prove on T and beta."""
+        beta = _frs(beta, 1)
+        return self._new(lib().zkh_lu_range_inverse, S.h, int(low), T.h, _p(beta))
 
     def lu_tuple_inverse(self, G, low, T, mapped, r, beta):
         """(comb, T_comb, A) = (G + r mapped[G - low], T + r mapped, 1/(comb + beta)) for int32

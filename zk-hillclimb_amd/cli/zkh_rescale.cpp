@@ -77,7 +77,9 @@ int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& 
     absorb(st, "com_rem", hrem.data(), hrem.size() * 4);
     absorb(st, "com_m", hm.data(), hm.size() * 4);
     const std::vector<uint32_t> beta = challenge(st);
-    chk(zkh_lu_inverse(g_ctx, remp.t, beta.data(), &A.t), "inverses");
+    // A = 1/(rem + beta) (zkob_rescale.cu:121-123) through the table inverse, which
+    // zkh_lu_prove then takes over
+    chk(zkh_lu_range_inverse(g_ctx, remp.t, low, T.t, beta.data(), &A.t), "inverses");
     chk(zkh_commit(g_ctx, g.g, A.t, &cA.g), "commit A");
     const std::vector<uint32_t> hA = to_host(cA.g);
     write_all(obdir + "/com_A.bin", hA.data(), hA.size() * 4);

@@ -943,8 +943,9 @@ void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
 // T[j] == G[i] (comb[i] is then T_comb[j]), A[i] = Binv[j] = 1/(T_comb[j] + beta).
 // *flags |= 1 for j outside [0, N) (nothing written at i), |= 2 for T[j] != G[i] (A[i] left
 // for the caller's direct inversion).  tlen > 0: T is the range table low + min(j, tlen - 1),
-// so T[j] == G[i] iff G[i] - low is the integer j < tlen, and T is not read.
-template <typename LG, typename LT, typename LM>
+// so T[j] == G[i] iff G[i] - low is the integer j < tlen, and T is not read.  Without Comb
+// (a plain range lookup: A = 1/(G + beta)) neither mapped nor comb is touched.
+template <bool Comb, typename LG, typename LT, typename LM>
 __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tlen, LM mapped, uint32_t N, fr_t rm,
                                   fr_t r,
                                   const uint4* __restrict__ blo, const uint4* __restrict__ bhi, uint4* clo,
@@ -958,7 +959,7 @@ __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tle
             f |= 1u;
             continue;
         }
-        st_fr(clo, chi, i, fr_add(g, scale_of(rm, r, mapped, j)));
+        if constexpr (Comb) st_fr(clo, chi, i, fr_add(g, scale_of(rm, r, mapped, j)));
         bool same = true;
         if (tlen) {
             same = j < tlen;
@@ -985,10 +986,21 @@ void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* lo
     with_loader(G, [&](auto lg) {
         with_loader(T, [&](auto lt) {
             with_loader(mapped, [&](auto lm) {
-                k_lu_tuple_gather<<<grid_for(n, NT, 8192), NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
+                k_lu_tuple_gather<true><<<grid_for(n, NT, 8192), NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
                                                                         PL_HI(Binv), PL_LO(comb), PL_HI(comb),
                                                                         PL_LO(A), PL_HI(A), flags);
             });
+        });
+    });
+}
+void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
+                            uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags) {
+    const fr_t low = to_fr(low_host);
+    with_loader(S, [&](auto ls) {
+        with_loader(T, [&](auto lt) {
+            k_lu_tuple_gather<false><<<grid_for(n, NT, 8192), NT, 0, s>>>(
+                ls, n, low, lt, tlen, LdI32{nullptr}, N, fr_t{}, fr_t{}, PL_LO(Binv), PL_HI(Binv), nullptr, nullptr,
+                PL_LO(A), PL_HI(A), flags);
         });
     });
 }

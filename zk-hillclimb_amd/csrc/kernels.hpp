@@ -167,6 +167,9 @@ void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
 void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
                             Src mapped, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host, DevPlanes Binv,
                             DevPlanes comb, DevPlanes A, uint32_t* flags);
+// the same for a plain range lookup: A[i] = Binv[j] (j = (S[i] - low).limb0) where T[j] == S[i]
+void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
+                            uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags);
 // A[i] = 1/(S[i]+beta) (0 -> 0), Montgomery's batched inversion with M(a, b) = a b 2^-256
 // products of the plain values: pass 1 writes the running products P_j to A, per-thread
 // "other threads" products to `others` (inv_blocks(n)*256 AoS) and block totals to

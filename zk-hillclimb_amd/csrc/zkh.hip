@@ -2541,6 +2541,56 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
     *A_out = A;
     return ZKH_OK;
 }
+extern "C" int zkh_lu_range_inverse(zkh_ctx* c, const zkh_tensor* S, int32_t low, const zkh_tensor* T,
+                                    const uint32_t beta[8], zkh_tensor** A_out) {
+    if (!c || !S || !T || !beta || !A_out) return fail(c, ZKH_EARG, "null argument");
+    const uint32_t D = S->n, N = T->n;
+    if (!N) return fail(c, ZKH_EARG, "empty table");
+    if (!fr_is_canonical(beta)) return fail(c, ZKH_EARG, "non-canonical beta");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    Src ss, st;
+    DevPlanes Tp;
+    if ((rc = src_of(c, S, SL_TMP0, &ss)) || (rc = src_of(c, T, SL_TMP1, &st)) || (rc = as_planes(c, T, SL_TMP2, &Tp)))
+        return rc;
+    zkh_tensor *A = nullptr, *Binv = nullptr;
+    auto drop = [&](int code) {
+        for (zkh_tensor* t : {A, Binv})
+            if (t) zkh_tensor_free(t);
+        return code;
+    };
+    if ((rc = tensor_alloc(c, ZKH_KIND_FR, D, &A)) || (rc = tensor_alloc(c, ZKH_KIND_FR, N, &Binv))) return drop(rc);
+    // the table's inverse (tlookup.cu:50-62 over T, as zkh_lu_prove takes it), then A read off it
+    if ((rc = batch_inverse(c, Tp, N, fr_load(beta), Binv->planes()))) return drop(rc);
+    uint32_t* flags = (uint32_t*)scratch_slot(c, SL_PARTIAL, 256, &rc);
+    if (rc) return drop(rc);
+    HIPCHK(c, hipMemsetAsync(flags, 0, 4, c->stream));
+    uint32_t hf = 0;
+    if (D) {
+        ProfScope ps(c, "lu_range_gather", (double)D * (32 + 32 + 32));
+        uint32_t lowl[8];
+        fr_store(fr_from_i64(low), lowl);
+        const uint32_t tlen = T->range_gen == T->gen && T->range_low == low ? T->range_len : 0;
+        launch_lu_range_gather(c->stream, ss, D, lowl, st, tlen, N, Binv->planes(), A->planes(), flags);
+    }
+    if ((rc = settle(c, flags, &hf))) return drop(rc);
+    // a witness outside the table or not the table's entry at its index: the direct batched
+    // inversion of S (zkob_rescale.cu:121-123), as zkh_lu_inverse
+    if (hf) {
+        DevPlanes Sp;
+        if ((rc = as_planes(c, S, SL_TMP0, &Sp)) || (rc = batch_inverse(c, Sp, D, fr_load(beta), A->planes())) ||
+            (rc = settle(c)))
+            return drop(rc);
+    }
+    A->inv_of = S->gen;
+    memcpy(A->inv_beta, beta, 32);
+    if (c->lu_tinv) zkh_tensor_free(c->lu_tinv);
+    c->lu_tinv = Binv;
+    c->lu_tinv_of = T->gen;
+    memcpy(c->lu_tinv_beta, beta, 32);
+    *A_out = A;
+    return ZKH_OK;
+}
 extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low, const zkh_tensor* T,
                                     const zkh_tensor* mapped, const uint32_t r[8], const uint32_t beta[8],
                                     zkh_tensor** comb_out, zkh_tensor** Tcomb_out, zkh_tensor** A_out) {
