@@ -77,21 +77,28 @@ struct Sha256 {
         h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
     }
     void compress(const uint8_t* p);
+    void compress_blocks(const uint8_t* p, size_t nb);  // nb consecutive 64-byte blocks
     void update(const void* data, size_t n) {
         const uint8_t* p = (const uint8_t*)data;
         len += n;
-        while (n) {
-            size_t take = 64 - blen;
-            if (take > n) take = n;
+        if (blen) {  // top up the buffered partial block
+            const size_t take = n < 64 - blen ? n : 64 - blen;
             memcpy(buf + blen, p, take);
             blen += (uint32_t)take;
             p += take;
             n -= take;
-            if (blen == 64) {
-                compress(buf);
-                blen = 0;
-            }
+            if (blen < 64) return;
+            compress(buf);
+            blen = 0;
         }
+        if (n >= 64) {  // whole blocks straight from the input
+            const size_t nb = n / 64;
+            compress_blocks(p, nb);
+            p += nb * 64;
+            n -= nb * 64;
+        }
+        memcpy(buf, p, n);
+        blen = (uint32_t)n;
     }
     void final(uint8_t out[32]) {
         const uint64_t bits = len * 8;
@@ -118,7 +125,7 @@ struct Sha256 {
 // SHA-256 compression with the x86 SHA extensions (Intel, "Intel SHA Extensions", 2013):
 // sha256rnds2 performs two rounds on the (ABEF, CDGH) state halves; sha256msg1/msg2 form the
 // message schedule four words at a time.  Used when CPUID reports SHA; same digest as block().
-__attribute__((target("sha,sse4.1,ssse3"))) inline void sha256_block_ni(uint32_t h[8], const uint8_t* p) {
+__attribute__((target("sha,sse4.1,ssse3"))) inline void sha256_blocks_ni(uint32_t h[8], const uint8_t* p, size_t nb) {
     alignas(16) static const uint32_t K[64] = {
         0x428a2f98, 0x71374491, 0xb5c0fbcf, 0xe9b5dba5, 0x3956c25b, 0x59f111f1, 0x923f82a4, 0xab1c5ed5,
         0xd807aa98, 0x12835b01, 0x243185be, 0x550c7dc3, 0x72be5d74, 0x80deb1fe, 0x9bdc06a7, 0xc19bf174,
@@ -135,26 +142,30 @@ __attribute__((target("sha,sse4.1,ssse3"))) inline void sha256_block_ni(uint32_t
     s1 = _mm_shuffle_epi32(s1, 0x1B);                       // H G F E
     __m128i s0 = _mm_alignr_epi8(tmp, s1, 8);               // F E B A = ABEF (high to low)
     s1 = _mm_blend_epi16(s1, tmp, 0xF0);                    // D C G H = CDGH
-    const __m128i abef = s0, cdgh = s1;
-    __m128i w[4];
-    for (int i = 0; i < 4; i++) w[i] = _mm_shuffle_epi8(_mm_loadu_si128((const __m128i*)(p + 16 * i)), bswap);
-    for (int g = 0; g < 16; g++) {
-        __m128i wg;
-        if (g < 4) {
-            wg = w[g];
-        } else {
-            // W[t..t+3] from W[t-16..t-13], W[t-12..t-9], W[t-7..t-4] and W[t-4..t-1]
-            __m128i x = _mm_sha256msg1_epu32(w[g & 3], w[(g + 1) & 3]);
-            x = _mm_add_epi32(x, _mm_alignr_epi8(w[(g + 3) & 3], w[(g + 2) & 3], 4));
-            wg = _mm_sha256msg2_epu32(x, w[(g + 3) & 3]);
-            w[g & 3] = wg;
+    // the state stays in the (ABEF, CDGH) form from block to block
+    for (; nb; nb--, p += 64) {
+        const __m128i abef = s0, cdgh = s1;
+        __m128i w[4];
+        for (int i = 0; i < 4; i++) w[i] = _mm_shuffle_epi8(_mm_loadu_si128((const __m128i*)(p + 16 * i)), bswap);
+#pragma GCC unroll 16
+        for (int g = 0; g < 16; g++) {
+            __m128i wg;
+            if (g < 4) {
+                wg = w[g];
+            } else {
+                // W[t..t+3] from W[t-16..t-13], W[t-12..t-9], W[t-7..t-4] and W[t-4..t-1]
+                __m128i x = _mm_sha256msg1_epu32(w[g & 3], w[(g + 1) & 3]);
+                x = _mm_add_epi32(x, _mm_alignr_epi8(w[(g + 3) & 3], w[(g + 2) & 3], 4));
+                wg = _mm_sha256msg2_epu32(x, w[(g + 3) & 3]);
+                w[g & 3] = wg;
+            }
+            __m128i m = _mm_add_epi32(wg, _mm_load_si128((const __m128i*)&K[4 * g]));
+            s1 = _mm_sha256rnds2_epu32(s1, s0, m);
+            s0 = _mm_sha256rnds2_epu32(s0, s1, _mm_shuffle_epi32(m, 0x0E));
         }
-        __m128i m = _mm_add_epi32(wg, _mm_load_si128((const __m128i*)&K[4 * g]));
-        s1 = _mm_sha256rnds2_epu32(s1, s0, m);
-        s0 = _mm_sha256rnds2_epu32(s0, s1, _mm_shuffle_epi32(m, 0x0E));
+        s0 = _mm_add_epi32(s0, abef);
+        s1 = _mm_add_epi32(s1, cdgh);
     }
-    s0 = _mm_add_epi32(s0, abef);
-    s1 = _mm_add_epi32(s1, cdgh);
     tmp = _mm_shuffle_epi32(s0, 0x1B);
     s1 = _mm_shuffle_epi32(s1, 0xB1);
     s0 = _mm_blend_epi16(tmp, s1, 0xF0);  // A B C D (low to high)
@@ -171,11 +182,19 @@ inline bool cpu_has_sha() {
     return has;
 }
 inline void Sha256::compress(const uint8_t* p) {
-    if (cpu_has_sha()) sha256_block_ni(h, p);
+    if (cpu_has_sha()) sha256_blocks_ni(h, p, 1);
     else block(p);
+}
+inline void Sha256::compress_blocks(const uint8_t* p, size_t nb) {
+    if (cpu_has_sha()) sha256_blocks_ni(h, p, nb);
+    else
+        for (; nb; nb--, p += 64) block(p);
 }
 #else
 inline void Sha256::compress(const uint8_t* p) { block(p); }
+inline void Sha256::compress_blocks(const uint8_t* p, size_t nb) {
+    for (; nb; nb--, p += 64) block(p);
+}
 #endif
 
 // SHA-256 of a message of at most 119 bytes: the padded message is built in place and
