@@ -1808,6 +1808,17 @@ ZDEV void find_desc(const D* __restrict__ d, uint32_t nd, D& out) {
 
 // eq tables in Montgomery form: E[b] = Tlo[b mod 2^klo] * Thi[b >> klo], the two small
 // factor-product tables built in LDS by separate threads (latency of ~8 products).
+// prod_{i < k} fs[2 (i0 + i) + bit i of t] (Montgomery form), k <= 7, as a balanced tree of
+// six products (three levels): the independent products of a level overlap, where a chain of
+// k products waits on each in turn
+ZDEV fr_t eq_lds_tree(const fr_t* fs, uint32_t i0, uint32_t k, uint32_t t) {
+    fr_t p[7];
+#pragma unroll
+    for (uint32_t i = 0; i < 7; i++) p[i] = i < k ? fs[2 * (i0 + i) + ((t >> i) & 1)] : one_m();
+    const fr_t a = mont_mul(p[0], p[1]), b = mont_mul(p[2], p[3]), c = mont_mul(p[4], p[5]);
+    const fr_t ab = mont_mul(a, b), cd = mont_mul(c, p[6]);
+    return mont_mul(ab, cd);
+}
 __global__ __launch_bounds__(NT) void k_eq_mont_multi(const EqTabDesc* __restrict__ d, uint32_t nd) {
     EqTabDesc q;
     find_desc(d, nd, q);
@@ -1820,15 +1831,8 @@ __global__ __launch_bounds__(NT) void k_eq_mont_multi(const EqTabDesc* __restric
         // below wait on LDS instead of on a dependent global load per factor
         if (t < 2 * K) fs[t] = ld_aos(q.fac, t);
         __syncthreads();
-        if (t < (1u << klo)) {
-            fr_t e = one_m();
-            for (uint32_t i = 0; i < klo; i++) e = mont_mul(e, fs[2 * i + ((t >> i) & 1)]);
-            tlo[t] = e;
-        } else if (t >= 128 && t - 128 < (1u << khi)) {
-            fr_t e = one_m();
-            for (uint32_t i = 0; i < khi; i++) e = mont_mul(e, fs[2 * (klo + i) + (((t - 128) >> i) & 1)]);
-            thi[t - 128] = e;
-        }
+        if (t < (1u << klo)) tlo[t] = eq_lds_tree(fs, 0, klo, t);
+        else if (t >= 128 && t - 128 < (1u << khi)) thi[t - 128] = eq_lds_tree(fs, klo, khi, t - 128);
     }
     __syncthreads();
     const uint32_t b = (blockIdx.x - q.blk_begin) * NT + t;
