@@ -533,31 +533,39 @@ ZDEV fr_t fold_at(const uint4* lo, const uint4* hi, uint32_t j, uint32_t n, cons
     fr_t x = ld_fr(lo, hi, j), y = ld_fr(lo, hi, j + n);
     return fr_add(x, mont_mul_ol(vm, fr_sub(y, x)));
 }
-// A table taking part in a fused round: read from (slo, shi); when the round folds, the
-// folded entries go to (dlo, dhi), which may alias the source (in-place halving).
+// A table taking part in a fused round: read from (slo, shi), or from the int32 entries s32
+// when set (an integer table not yet folded); when the round folds, the folded entries go
+// to (dlo, dhi), which may alias the source (in-place halving).
 struct TabDev {
     const uint4* slo;
     const uint4* shi;
     uint4* dlo;
     uint4* dhi;
+    const int32_t* s32;
 };
+ZDEV fr_t tab_ld(const TabDev& t, uint32_t i) { return t.s32 ? fr_from_i64(t.s32[i]) : ld_fr(t.slo, t.shi, i); }
+ZDEV fr_t tab_fold_at(const TabDev& t, uint32_t j, uint32_t n, const fr_t& vm) {
+    if (!t.s32) return fold_at(t.slo, t.shi, j, n, vm);
+    const fr_t x = fr_from_i64(t.s32[j]), y = fr_from_i64(t.s32[j + n]);
+    return fr_add(x, mont_mul_ol(vm, fr_sub(y, x)));
+}
 static inline TabDev tab_dev(const Tab& t) {
     return TabDev{reinterpret_cast<const uint4*>(t.src.lo()), reinterpret_cast<const uint4*>(t.src.hi()),
-                  reinterpret_cast<uint4*>(t.dst.lo()), reinterpret_cast<uint4*>(t.dst.hi())};
+                  reinterpret_cast<uint4*>(t.dst.lo()), reinterpret_cast<uint4*>(t.dst.hi()), nullptr};
 }
 // entries i and i+h of this round's table (folding the previous round's table of size 2n
 // when fold is set, and storing the folded pair)
 ZDEV void load_pair(const TabDev& t, uint32_t i, uint32_t h, uint32_t n, int fold, const fr_t& vm,
                     fr_t& x0, fr_t& x1) {
     if (fold) {
-        x0 = fold_at(t.slo, t.shi, i, n, vm);
+        x0 = tab_fold_at(t, i, n, vm);
         st_fr(t.dlo, t.dhi, i, x0);
         __builtin_amdgcn_sched_barrier(0);  // one fold's temporaries at a time
-        x1 = fold_at(t.slo, t.shi, i + h, n, vm);
+        x1 = tab_fold_at(t, i + h, n, vm);
         st_fr(t.dlo, t.dhi, i + h, x1);
     } else {
-        x0 = ld_fr(t.slo, t.shi, i);
-        x1 = ld_fr(t.slo, t.shi, i + h);
+        x0 = tab_ld(t, i);
+        x1 = tab_ld(t, i + h);
     }
 }
 __global__ void k_fold(TabDev t, uint32_t h, fr_t vm) {
@@ -845,7 +853,7 @@ __global__ __launch_bounds__(NTH) void k_hist_slots(HistArgs a) {
 }
 // pass 6: m[j] = sum of bin j over its bucket's slots, as a field element (direct: the
 // one bucket's direct_slots slots, possibly none)
-__global__ void k_hist_sum(HistArgs a, int direct, uint32_t direct_slots, uint4* lo, uint4* hi) {
+__global__ void k_hist_sum(HistArgs a, int direct, uint32_t direct_slots, uint4* lo, uint4* hi, int32_t* out32) {
     const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= a.N) return;
     uint32_t s0, ns;
@@ -867,6 +875,10 @@ __global__ void k_hist_sum(HistArgs a, int direct, uint32_t direct_slots, uint4*
         for (int u = 0; u < 8; u++) c += v[u];
     }
     for (; s < ns; s++) c += h[(size_t)s * ZKH_HIST_BINS];
+    if (out32) {
+        out32[j] = (int32_t)c;
+        return;
+    }
     fr_t m = fr_zero();
     m.v[0] = c;
     st_fr(lo, hi, j, m);
@@ -878,7 +890,7 @@ size_t hist_scratch_bytes(uint32_t n, uint32_t N) {
     return align16((size_t)nb * nt * 4) + align16((size_t)nb * 16) + align16((size_t)ms * 16) + 16 +
            align16((size_t)n * 2) + (size_t)ms * ZKH_HIST_BINS * 4;
 }
-void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m) {
+void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m, int32_t* m32) {
     a.nbuckets = (a.N + ZKH_HIST_BINS - 1) / ZKH_HIST_BINS;
     a.ntiles = (a.n + ZKH_HIST_TILE - 1) / ZKH_HIST_TILE;
     a.max_slots = a.nbuckets + (a.n + ZKH_HIST_CHUNK - 1) / ZKH_HIST_CHUNK;
@@ -898,7 +910,7 @@ void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m) {
     if (a.nbuckets == 1) {  // one LDS histogram covers the table: slots read the input
         const uint32_t ns = (a.n + ZKH_HIST_CHUNK - 1) / ZKH_HIST_CHUNK;
         if (ns) k_hist_slots<1><<<ns, NTH, 0, s>>>(a);
-        k_hist_sum<<<gsum, NT, 0, s>>>(a, 1, ns, PL_LO(m), PL_HI(m));
+        k_hist_sum<<<gsum, NT, 0, s>>>(a, 1, ns, PL_LO(m), PL_HI(m), m32);
         return;
     }
     k_hist_tiles<<<a.ntiles, NT, 0, s>>>(a);
@@ -906,7 +918,7 @@ void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m) {
     k_hist_plan<<<1, NT, 0, s>>>(a);
     k_hist_scatter<<<a.ntiles, NT, 0, s>>>(a);
     k_hist_slots<0><<<a.max_slots, NTH, 0, s>>>(a);
-    k_hist_sum<<<gsum, NT, 0, s>>>(a, 0, 0, PL_LO(m), PL_HI(m));
+    k_hist_sum<<<gsum, NT, 0, s>>>(a, 0, 0, PL_LO(m), PL_HI(m), m32);
 }
 
 __global__ void k_lu_map_planes(const uint4* lo, const uint4* hi, uint32_t n, fr_t low,
@@ -1394,7 +1406,7 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
         for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
             const fr_t b0 = ld_fr(B.slo, B.shi, i), b1 = ld_fr(B.slo, B.shi, i + h);
             {  // multiplicities are small integers: sums 3..5 exact (x 1) by the 32-bit multiply
-                const fr_t m0 = ld_fr(m.slo, m.shi, i), m1 = ld_fr(m.slo, m.shi, i + h);
+                const fr_t m0 = tab_ld(m, i), m1 = tab_ld(m, i + h);
                 SB();
                 int64_t i0, i1;
                 if (fr_int32ish(m0, i0) && fr_int32ish(m1, i1)) {
@@ -1494,14 +1506,16 @@ __global__ __launch_bounds__(NT) void k_lu_phase2(TabDev A, TabDev S, TabDev B, 
 }
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int fold_as,
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host,
-                          EqW eq, Publish partial, int inv_as, int inv_btm, int derive) {
+                          EqW eq, Publish partial, int inv_as, int inv_btm, int derive, const int32_t* m32) {
     // the derived variant holds 5 blocks per CU (32 KiB of accumulators): one resident wave
     const uint32_t G = derive && fold_as && fold_btm ? 1280 : LU2_GRID;
     const uint32_t ga = grid_for(n >> 1, NT, G * 2 / 5), gb = grid_for(n >> 1, NT, G * 3 / 5);
     const fr_t vm = (fold_as || fold_btm) && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
     const fr_t beta = to_fr(beta_host);
-    const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T), md = tab_dev(m);
+    const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T);
+    TabDev md = tab_dev(m);
+    md.s32 = m32;
     const uint32_t g = ga + gb;
 #define LU2(FA, FB, DV) k_lu_phase2<FA, FB, DV><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm)
     if (fold_as && fold_btm) {

@@ -155,7 +155,8 @@ struct HistArgs {
 // scratch words needed by launch_hist for these sizes (tile_cnt .. slot_hist, 16-byte aligned parts)
 size_t hist_scratch_bytes(uint32_t n, uint32_t N);
 // lays HistArgs' buffers out in `scratch` (hist_scratch_bytes bytes) and enqueues the passes
-void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m);
+// (m32 set: the counts go to m32 as int32 instead of m's planes)
+void launch_hist(hipStream_t s, HistArgs a, void* scratch, DevPlanes m, int32_t* m32);
 
 void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
                           DevPlanes mapped, DevPlanes out);
@@ -202,10 +203,12 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
 // inv_btm the m b sums (3..5 of job 1) are exact (x 1)
 // derive: the folding groups leave out their sums at 1: job 0 publishes 3 sums (w*a0*s0,
 // w*da*ds, a0), job 1 (when it folds) 4 (w*b0*t0, w*db*dt, m0*b0, dm*db)
+// m32: m read as int32 entries (not yet folded) instead of m's source planes
 uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n,
                           int fold_as, int fold_btm,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
-                          Publish pub, int inv_as, int inv_btm, int derive);
+                          Publish pub, int inv_as, int inv_btm, int derive,
+                          const int32_t* m32);
 
 // ---- Hadamard ----
 // With derive (folding rounds only) each Hadamard round kernel leaves out its sum at t = 1,

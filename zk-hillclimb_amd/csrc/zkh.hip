@@ -2394,13 +2394,25 @@ static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, u
     *bad_out = bad;
     return 0;
 }
-// multiplicities m (N field elements) of the witness S against a table of N entries at low:
-// LDS histograms for N <= 2^24 (launch_hist), global atomics beyond.  Queues the work only;
-// *bad (device word) becomes nonzero when a witness lies outside the table (check_bad).
-static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, DevPlanes m,
+// the tensor for the multiplicities of S against N entries: int32 counts (a 4-byte entry
+// where field planes take 32) when the LDS histogram counts them and no count can reach
+// 2^31, field elements otherwise
+static int mult_alloc(zkh_ctx* c, const zkh_tensor* S, uint32_t N, zkh_tensor** m) {
+    const bool i32 = N <= ZKH_HIST_MAX_BUCKETS * ZKH_HIST_BINS && S->n < (1u << 31);
+    int rc = tensor_alloc(c, i32 ? ZKH_KIND_I32 : ZKH_KIND_FR, N, m);
+    if (!rc && i32) (*m)->bits = bits_for(S->n);  // every count is at most |S|
+    return rc;
+}
+// multiplicities m (N entries, from mult_alloc) of the witness S against a table of N entries
+// at low: LDS histograms for N <= 2^24 (launch_hist), global atomics beyond.  Queues the work
+// only; *bad (device word) becomes nonzero when a witness lies outside the table (check_bad).
+static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, zkh_tensor* mt,
                              uint32_t** bad_out) {
     int rc = 0;
+    const DevPlanes m = mt->kind == ZKH_KIND_FR ? mt->planes() : DevPlanes{};
+    int32_t* m32 = mt->kind == ZKH_KIND_I32 ? (int32_t*)mt->d : nullptr;
     if (N > ZKH_HIST_MAX_BUCKETS * ZKH_HIST_BINS) {
+        if (m32) return fail(c, ZKH_EARG, "int32 multiplicities beyond the histogram's table size");
         uint32_t* counts;
         if ((rc = lu_counts(c, S, low, N, &counts, bad_out))) return rc;
         launch_counts_to_planes(c->stream, counts, N, m);
@@ -2426,7 +2438,7 @@ static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint3
     HIPCHK(c, hipMemsetAsync(bad, 0, 4, c->stream));
     {
         ProfScope ps(c, "lu_hist", (double)S->n * (S->kind == ZKH_KIND_I32 ? 4 : 32) + (double)N * 32);
-        launch_hist(c->stream, a, hs, m);
+        launch_hist(c->stream, a, hs, m, m32);
     }
     *bad_out = bad;
     return 0;
@@ -2445,9 +2457,9 @@ extern "C" int zkh_lu_prep(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_
     HIPCHK(c, hipSetDevice(c->device));
     zkh_tensor* m;
     int rc;
-    if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
+    if ((rc = mult_alloc(c, S, N, &m))) return rc;
     uint32_t* bad = nullptr;
-    if ((rc = lu_multiplicities(c, S, low, N, m->planes(), &bad)) || (rc = check_bad(c, bad))) {
+    if ((rc = lu_multiplicities(c, S, low, N, m, &bad)) || (rc = check_bad(c, bad))) {
         zkh_tensor_free(m);
         return rc;
     }
@@ -2462,11 +2474,11 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
     uint32_t N = mapped->n;
     zkh_tensor *m, *so;
     int rc;
-    if ((rc = tensor_alloc(c, ZKH_KIND_FR, N, &m))) return rc;
+    if ((rc = mult_alloc(c, S_in, N, &m))) return rc;
     // the mapping is queued behind the multiplicities (its kernels bound-check the index) and
     // one completion wait then checks the witness range
     uint32_t* bad = nullptr;
-    if ((rc = lu_multiplicities(c, S_in, low, N, m->planes(), &bad))) {
+    if ((rc = lu_multiplicities(c, S_in, low, N, m, &bad))) {
         zkh_tensor_free(m);
         return rc;
     }
@@ -2874,18 +2886,23 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     Fr alpha = fr_load(alpha_l), beta = fr_load(beta_l);
     std::vector<Fr> u = load_frs(u_l, logD);
 
-    // working tables: caller tensors are read in place until their first fold
-    DevPlanes Ac, Sc, Tc, mc;
+    // working tables: caller tensors are read in place until their first fold.  An int32 m
+    // (the counts of zkh_lu_prep / zkh_lu_mapping) is read as int32 by the round kernels up to
+    // its first fold when D == N and the first two rounds (m's first read and first fold) are
+    // round kernels, not the persistent loop; otherwise as planes
+    const bool m_i32 = m->kind == ZKH_KIND_I32 && !m->weights && D == N && N / 2 > ZKH_LU_PERSIST_MAX;
+    DevPlanes Ac, Sc, Tc, mc{};
     if ((rc = as_planes(c, A, SL_TMP0, &Ac)) || (rc = as_planes(c, S, SL_TMP1, &Sc)) ||
-        (rc = as_planes(c, T, SL_TMP2, &Tc)) || (rc = as_planes(c, m, SL_TMP3, &mc)))
+        (rc = as_planes(c, T, SL_TMP2, &Tc)) || (!m_i32 && (rc = as_planes(c, m, SL_TMP3, &mc))))
         return rc;
+    const int32_t* m_src32 = m_i32 ? (const int32_t*)m->d : nullptr;  // m's source while unfolded
     DevPlanes Aw = A->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP0, D / 2, &rc) : Ac;
     if (rc) return rc;
     DevPlanes Sw = S->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP1, D / 2, &rc) : Sc;
     if (rc) return rc;
     DevPlanes Tw = T->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP2, N / 2, &rc) : Tc;
     if (rc) return rc;
-    DevPlanes mw = m->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP3, N / 2, &rc) : mc;
+    DevPlanes mw = m->kind == ZKH_KIND_FR || m_i32 ? scratch_planes(c, SL_TMP3, N / 2, &rc) : mc;
     if (rc) return rc;
     // Bv = 1/(T+beta), owned: zkh_lu_tuple_inverse's table inverse when T is its T_comb and
     // beta its beta (taken over: the rounds fold it in place), else inverted here
@@ -2985,7 +3002,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                              ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
                 launch_lu_phase2(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
                                  Tab{m_src, mw}, n, as_pending, btm_pending, vm, vmp, beta_l,
-                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b, dv);
+                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b, dv, m_src32);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -2995,6 +3012,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                 b_src = Bw;
                 t_src = Tw;
                 m_src = mw;
+                m_src32 = nullptr;
             }
             as_pending = true;
             btm_pending = true;
@@ -3010,6 +3028,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         const uint32_t n = D >> r;
         if (persists(r)) {  // phase 2: the rest in one launch
             LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD, &pc};
+            if (m_src32) return fail(c, ZKH_EDEV, "internal: unfolded int32 m at the persistent loop");
             const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
             if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, beta_l, ev_out, ws_out, fin)))
                 return rc;
@@ -3155,6 +3174,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         if (btm_pending) {
             launch_fold(c->stream, Tab{b_src, Bw}, 1, vm);
             launch_fold(c->stream, Tab{t_src, Tw}, 1, vm);
+            if (m_src32) return fail(c, ZKH_EDEV, "internal: unfolded int32 m at the last fold");
             launch_fold(c->stream, Tab{m_src, mw}, 1, vm);
             b_src = Bw;
             t_src = Tw;
