@@ -943,6 +943,21 @@ void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t
                                                        PL_LO(mapped), PL_HI(mapped), mapped.cap,
                                                        PL_LO(out), PL_HI(out));
 }
+// S_out[i] = mapped[j] as int32, j = (S[i] - low).limb0 (0 outside the table, which the
+// multiplicity pass flags): the mapping of an int32 table keeps its 4-byte entries
+template <typename LS>
+__global__ void k_lu_map_to_i32(LS S, uint32_t n, fr_t low, const int32_t* __restrict__ mapped, uint32_t N,
+                                int32_t* out) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const uint32_t j = fr_sub(S(i), low).v[0];
+        out[i] = j < N ? mapped[j] : 0;
+    }
+}
+void launch_lu_map_to_i32(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, const int32_t* mapped,
+                          uint32_t N, int32_t* out) {
+    const fr_t low = to_fr(low_host);
+    with_loader(S, [&](auto ls) { k_lu_map_to_i32<<<grid_for(n, NT, 8192), NT, 0, s>>>(ls, n, low, mapped, N, out); });
+}
 void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low, Src mapped, uint32_t N,
                        DevPlanes out) {
     with_loader(mapped, [&](auto lm) {
@@ -1677,16 +1692,16 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t s0, s1, u0, u1, w;
         if (fold) {
-            s0 = fold_at(S.slo, S.shi, i, n, vm);
-            s1 = fold_at(S.slo, S.shi, i + h, n, vm);
+            s0 = tab_fold_at(S, i, n, vm);
+            s1 = tab_fold_at(S, i + h, n, vm);
             st_fr(S.dlo, S.dhi, i, s0);
             st_fr(S.dlo, S.dhi, i + h, s1);
             SB();
-            u0 = fold_at(U.slo, U.shi, i, n, vm);
+            u0 = tab_fold_at(U, i, n, vm);
             w = eq_w(eq, i);
             st_fr(U.dlo, U.dhi, i, u0);
             SB();
-            u1 = fold_at(U.slo, U.shi, i + h, n, vm);
+            u1 = tab_fold_at(U, i + h, n, vm);
             st_fr(U.dlo, U.dhi, i + h, u1);
             SB();
             const fr_t ws = mont_mul_ol(w, s0);
@@ -1703,13 +1718,29 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             continue;
         }
         if constexpr (!derive) {
-            s0 = ld_fr(S.slo, S.shi, i);
-            s1 = ld_fr(S.slo, S.shi, i + h);
-            u0 = ld_fr(U.slo, U.shi, i);
-            u1 = ld_fr(U.slo, U.shi, i + h);
+            int32_t a0, a1, b0, b1;
+            if (S.s32 && U.s32) {  // int32 tables: the exact 64-bit products directly
+                a0 = S.s32[i];
+                a1 = S.s32[i + h];
+                b0 = U.s32[i];
+                b1 = U.s32[i + h];
+                // small_int's range (-2^30, 2^30): differences and their product stay exact
+                auto in30 = [](int32_t v) { return v > -(1 << 30) && v < (1 << 30); };
+                if (in30(a0) && in30(a1) && in30(b0) && in30(b1)) {
+                    w = eq_w(eq, i);
+                    acc.add(0, fr_mul_i64(w, (int64_t)a0 * b0));
+                    acc.add(1, fr_mul_i64(w, (int64_t)a1 * b1));
+                    acc.add(2, fr_mul_i64(w, (int64_t)(a1 - a0) * (b1 - b0)));
+                    SB();
+                    continue;
+                }
+            }
+            s0 = tab_ld(S, i);
+            s1 = tab_ld(S, i + h);
+            u0 = tab_ld(U, i);
+            u1 = tab_ld(U, i + h);
             w = eq_w(eq, i);
             SB();
-            int32_t a0, a1, b0, b1;
             if (small_int(s0, a0) && small_int(s1, a1) && small_int(u0, b0) && small_int(u1, b1)) {
                 // the weight (e 2^256) times the exact 64-bit products: sums e s u 2^256
                 acc.add(0, fr_mul_i64(w, (int64_t)a0 * b0));
@@ -1729,12 +1760,16 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
     reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial, int derive) {
+                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial, int derive,
+                            const int32_t* s32, const int32_t* u32) {
     const uint32_t g = grid_for(n >> 1, NT, fold && derive ? 1280 : 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
-    if (fold && derive) k_hp_eq_round<1><<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, vmp, e, partial);
-    else k_hp_eq_round<0><<<g, NT, 0, s>>>(tab_dev(S), tab_dev(U), n, fold, vm, vmp, e, partial);
+    TabDev sd = tab_dev(S), ud = tab_dev(U);
+    sd.s32 = s32;
+    ud.s32 = u32;
+    if (fold && derive) k_hp_eq_round<1><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
+    else k_hp_eq_round<0><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
     return g;
 }
 // sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n, by chunks of 1024 indices sharing their

@@ -162,6 +162,9 @@ void launch_lu_map_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t
                           DevPlanes mapped, DevPlanes out);
 void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
                        Src mapped, uint32_t N, DevPlanes out);
+// the same into int32 entries for an int32 mapped table (out[i] = 0 outside the table)
+void launch_lu_map_to_i32(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, const int32_t* mapped,
+                          uint32_t N, int32_t* out);
 // tuple lookup, j = (G[i] - low).limb0: comb[i] = G[i] + r mapped[j]; A[i] = Binv[j] where
 // T[j] == G[i]; *flags |= 1 (j >= N) / 2 (T[j] != G[i]); r plain and in Montgomery form;
 // tlen > 0: T is the range table low + min(j, tlen - 1) (not read)
@@ -223,7 +226,8 @@ uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold,
 // eq-specialised: sums w*s0*u0, w*s1*u1, w*ds*du with w = eq(i,u_) (x 2^-256 when folding,
 // x 2^256 in the first round); derive: w*s0*u0, w*ds*du
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
-                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub, int derive);
+                            const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub, int derive,
+                            const int32_t* s32, const int32_t* u32);
 // sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish pub);

@@ -2482,11 +2482,21 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
         zkh_tensor_free(m);
         return rc;
     }
-    if ((rc = tensor_alloc(c, ZKH_KIND_FR, S_in->n, &so))) {
+    // an int32 mapped table maps into int32 entries (4 bytes where field planes take 32)
+    const bool out_i32 = mapped->kind == ZKH_KIND_I32 && !mapped->weights;
+    if ((rc = tensor_alloc(c, out_i32 ? ZKH_KIND_I32 : ZKH_KIND_FR, S_in->n, &so))) {
         zkh_tensor_free(m);
         return rc;
     }
-    if (S_in->kind == ZKH_KIND_I32) {
+    if (out_i32) {
+        so->bits = mapped->bits;  // the entries are mapped's
+        Src ss;
+        rc = src_of(c, S_in, SL_TMP0, &ss);
+        uint32_t lowl[8];
+        fr_store(fr_from_i64(low), lowl);
+        if (!rc)
+            launch_lu_map_to_i32(c->stream, ss, S_in->n, lowl, (const int32_t*)mapped->d, N, (int32_t*)so->d);
+    } else if (S_in->kind == ZKH_KIND_I32) {
         Src ms;
         rc = src_of(c, mapped, SL_TMP1, &ms);
         if (!rc) launch_lu_map_i32(c->stream, (const int32_t*)S_in->d, S_in->n, low, ms, N, so->planes());
@@ -3742,17 +3752,26 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     HIPCHK(c, hipSetDevice(c->device));
     const uint32_t k = ceil_log2(n);
     int rc = 0;
-    DevPlanes Ec{}, Sc, Uc;
+    // int32 S and U of the eq form (SwiGLU's mapped S and int16-range U) are read as int32 by
+    // the round kernels up to their first fold when the first two rounds are round kernels,
+    // not the persistent loop; otherwise as planes
+    const bool big = (n >> 1) > ZKH_HP_PERSIST_MAX;
+    const bool s_i32 = ueq && big && S->kind == ZKH_KIND_I32 && !S->weights;
+    const bool u_i32 = ueq && big && U->kind == ZKH_KIND_I32 && !U->weights;
+    DevPlanes Ec{}, Sc{}, Uc{};
     if (E && (rc = as_planes(c, E, SL_TMP0, &Ec))) return rc;
-    if ((rc = as_planes(c, S, SL_TMP1, &Sc)) || (rc = as_planes(c, U, SL_TMP2, &Uc))) return rc;
+    if ((!s_i32 && (rc = as_planes(c, S, SL_TMP1, &Sc))) || (!u_i32 && (rc = as_planes(c, U, SL_TMP2, &Uc))))
+        return rc;
+    const int32_t* s32 = s_i32 ? (const int32_t*)S->d : nullptr;  // the sources while unfolded
+    const int32_t* u32 = u_i32 ? (const int32_t*)U->d : nullptr;
     DevPlanes Ew{}, Sw, Uw;
     if (E) {
         Ew = E->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP0, n / 2 + 1, &rc) : Ec;
         if (rc) return rc;
     }
-    Sw = S->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP1, n / 2 + 1, &rc) : Sc;
+    Sw = S->kind == ZKH_KIND_FR || s_i32 ? scratch_planes(c, SL_TMP1, n / 2 + 1, &rc) : Sc;
     if (rc) return rc;
-    Uw = U->kind == ZKH_KIND_FR ? scratch_planes(c, SL_TMP2, n / 2 + 1, &rc) : Uc;
+    Uw = U->kind == ZKH_KIND_FR || u_i32 ? scratch_planes(c, SL_TMP2, n / 2 + 1, &rc) : Uc;
     if (rc) return rc;
     EqState eq;
     if (ueq && (rc = eq_setup(c, *ueq, eq))) return rc;
@@ -3795,12 +3814,13 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         } else {
             ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
             launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp,
-                               EqW{eq.elo_d, eq.ehi_d, k - r - 1}, l.pb, l.dv);
+                               EqW{eq.elo_d, eq.ehi_d, k - r - 1}, l.pb, l.dv, s32, u32);
         }
         if (fold) {
             e_src = Ew;
             s_src = Sw;
             if (!u_ones) u_src = Uw;
+            s32 = u32 = nullptr;
         }
         return l;
     };
@@ -3811,6 +3831,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         const uint32_t sz = n >> r;
         const int fold = r > 0;
         if (persists(r)) {  // the rest in one launch
+            if (s32 || u32) return fail(c, ZKH_EDEV, "internal: unfolded int32 table at the persistent loop");
             if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, vm, claim, cE, ev_out,
                                         ws_out, e_fin, s_fin, u_fin)))
                 return rc;
@@ -3924,6 +3945,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         fr_store(u_fin, tv[1]);
         fr_store(e_fin, tv[2]);
     } else {
+        if (s32 || u32) return fail(c, ZKH_EDEV, "internal: unfolded int32 table at the last fold");
         if (k > 0) {
             if (!ueq) launch_fold(c->stream, Tab{e_src, Ew}, 1, vm);
             launch_fold(c->stream, Tab{s_src, Sw}, 1, vm);
