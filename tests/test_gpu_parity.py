@@ -47,6 +47,34 @@ def test_me(zkh, ctx, n, k):
     assert fr_eq(got, want)
 
 
+@pytest.mark.parametrize("n,k", [(5, 3), (1000, 10), (70001, 17), (1 << 20, 20)])
+def test_me_integer_tensors(zkh, ctx, n, k):
+    """FrTensor::operator()(u) of int32 and int64 tensors read as integers (the field x int64
+    weighting, its 2^256 removed on the host), with the ends of both ranges and a partial last
+    chunk of 1024; and of H = S (.) U over int32 S and U, which comes back as the exact int64
+    products.  Against the oracle's evaluation of the same field values."""
+    rng = np.random.default_rng(n + k)
+    u = rand_fr_full(rng, k)
+    v32 = rng.integers(-2**31, 2**31, size=n, dtype=np.int64)
+    v32[:4] = [-2**31, 2**31 - 1, -1, 0][: min(4, n)]
+    v64 = rng.integers(-2**63, 2**63, size=n, dtype=np.int64)
+    v64[:4] = [-2**63, 2**63 - 1, -1, 0][: min(4, n)]
+    for vals, t in ((v32, ctx.from_i32(v32.astype(np.int32))), (v64, ctx.from_i64(v64))):
+        rc, want = C.me(C.ints_to_fr([int(x) for x in vals]), u)
+        assert rc == 0
+        assert fr_eq(ctx.me(t, u), want)
+    s = rng.integers(-2**31, 2**31, size=n, dtype=np.int64)
+    s[:2] = [-2**31, 2**31 - 1][: min(2, n)]
+    uu = rng.integers(-2**31, 2**31, size=n, dtype=np.int64)
+    uu[:2] = [-2**31, -2**31][: min(2, n)]
+    H = ctx.hadamard(ctx.from_i32(s.astype(np.int32)), ctx.from_i32(uu.astype(np.int32)))
+    assert zkh.lib().zkh_tensor_kind(H.h) == zkh.KIND_I64
+    prod = [int(a) * int(b) for a, b in zip(s, uu)]
+    assert fr_eq(H.to_fr(), C.ints_to_fr(prod))
+    rc, want = C.me(C.ints_to_fr(prod), u)
+    assert fr_eq(ctx.me(H, u), want)
+
+
 @pytest.mark.parametrize("n,k", [(8, 3), (1000, 10), (70000, 17)])
 def test_me_boolean_and_one_coordinates(zkh, ctx, n, k):
     """FrTensor::operator()(u) at points with coordinates 0 and 1: at a Boolean point the MLE

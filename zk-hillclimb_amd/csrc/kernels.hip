@@ -628,6 +628,14 @@ __global__ void k_hadamard(LA a, LB b, uint32_t n, uint4* olo, uint4* ohi) {
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
         st_fr(olo, ohi, i, prod_of(a, b, i));
 }
+// int32 x int32 -> the exact int64 product
+__global__ void k_hadamard_i64(const int32_t* __restrict__ a, const int32_t* __restrict__ b, uint32_t n, int64_t* out) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+        out[i] = (int64_t)a[i] * b[i];
+}
+void launch_hadamard_i64(hipStream_t s, const int32_t* a, const int32_t* b, uint32_t n, int64_t* out) {
+    k_hadamard_i64<<<grid_for(n, NT, 8192), NT, 0, s>>>(a, b, n, out);
+}
 void launch_hadamard(hipStream_t s, Src a, Src b, uint32_t n, DevPlanes out) {
     with_loader(a, [&](auto la) {
         with_loader(b, [&](auto lb) {
@@ -1794,6 +1802,30 @@ __global__ __launch_bounds__(NT) void k_eq_sum(const uint4* slo, const uint4* sh
         acc[0] = fr_add(acc[0], mont_mul_ol(part, ld_aos(eq.ehi, c)));
     }
     reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+}
+// the same over integer entries: the Elo weight times the entry by the field x int64
+// multiply (its sums carry 2^256 for the host to remove), no field planes read
+template <typename T>
+__global__ __launch_bounds__(NT) void k_eq_sum_int(const T* __restrict__ S, uint32_t n, EqDev eq, Publish pub) {
+    fr_t acc[1] = {fr_zero()};
+    const uint32_t nchunk = (n + 1023) >> 10;
+    for (uint32_t c = blockIdx.x; c < nchunk; c += gridDim.x) {
+        fr_t part = fr_zero();
+#pragma unroll
+        for (uint32_t k = 0; k < 1024 / NT; k++) {
+            const uint32_t j = k * NT + threadIdx.x, i = (c << 10) + j;
+            if (i < n) part = fr_add(part, fr_mul_i64(ld_aos(eq.elo, j), (int64_t)S[i]));
+        }
+        acc[0] = fr_add(acc[0], mont_mul_ol(part, ld_aos(eq.ehi, c)));
+    }
+    reduce_publish<1>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+}
+uint32_t launch_eq_sum_int(hipStream_t s, int kind, const void* S, uint32_t n, EqW eq, Publish partial) {
+    const uint32_t g = grid_for((n + 1023) >> 10, 1, 1024);
+    EqDev e{eq.elo, eq.ehi, eq.K};
+    if (kind == 1) k_eq_sum_int<<<g, NT, 0, s>>>((const int32_t*)S, n, e, partial);
+    else k_eq_sum_int<<<g, NT, 0, s>>>((const int64_t*)S, n, e, partial);
+    return g;
 }
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish partial) {

@@ -117,6 +117,8 @@ struct Src {
 void launch_axpy(hipStream_t s, Src a, const uint32_t* c_host, const uint32_t* c_m_host, Src b, uint32_t n,
                  DevPlanes out);
 void launch_hadamard(hipStream_t s, Src a, Src b, uint32_t n, DevPlanes out);
+// int32 a (.) b into the exact int64 products
+void launch_hadamard_i64(hipStream_t s, const int32_t* a, const int32_t* b, uint32_t n, int64_t* out);
 
 // ---- logUp ----
 void launch_lu_count_planes(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* low_host,
@@ -228,6 +230,8 @@ uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold,
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish pub, int derive,
                             const int32_t* s32, const int32_t* u32);
+// sum_i eq(i, u[0..K)) * S[i] over integer entries (kind 1 int32, 2 int64), x 2^256
+uint32_t launch_eq_sum_int(hipStream_t s, int kind, const void* S, uint32_t n, EqW eq, Publish partial);
 // sum_i eq(i, u[0..K)) * S[i] * U[i] over i < n (x 2^-256); U may be null (then S only, x 1)
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
                        Publish pub);

@@ -1113,6 +1113,23 @@ static int eq_weighted_sum(zkh_ctx* c, DevPlanes S, const DevPlanes* U, uint32_t
     *out = s;
     return 0;
 }
+// the same over an integer tensor's own entries (no conversion to planes)
+static int eq_weighted_sum_int(zkh_ctx* c, const zkh_tensor* t, const std::vector<Fr>& u, Fr* out) {
+    int rc = 0;
+    EqState st;
+    if ((rc = eq_setup(c, u, st, false))) return rc;
+    const uint32_t K = (uint32_t)u.size();
+    {
+        ProfScope ps(c, "eq_sum", (double)t->n * (t->kind == ZKH_KIND_I32 ? 4 : 8));
+        Publish pb = make_pub(c, 1);
+        launch_eq_sum_int(c->stream, t->kind, t->d, t->n, EqW{st.elo_d, st.ehi_d, K}, pb);
+        if ((rc = wait_pub(c, pb.seq))) return rc;
+    }
+    Fr s;
+    pub_read(c, 0, 1, &s);
+    *out = fr_from_mont(fr_mul(s, eq_corr(st, K)));  // the int64 multiply's 2^256 removed
+    return 0;
+}
 extern "C" int zkh_sum(zkh_ctx* c, const zkh_tensor* t, uint32_t out[8]) {
     if (!c || !t || !out) return fail(c, ZKH_EARG, "null argument");
     HIPCHK(c, hipSetDevice(c->device));
@@ -1198,9 +1215,14 @@ extern "C" int zkh_me(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u, uint32
     if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
     HIPCHK(c, hipSetDevice(c->device));
     int rc = 0;
+    Fr s;
+    if (t->kind != ZKH_KIND_FR && !t->weights) {  // integer entries read as such
+        if ((rc = eq_weighted_sum_int(c, t, load_frs(u, k), &s))) return rc;
+        fr_store(s, out);
+        return ZKH_OK;
+    }
     DevPlanes p;
     if ((rc = as_planes(c, t, SL_TMP0, &p))) return rc;
-    Fr s;
     if ((rc = eq_weighted_sum(c, p, nullptr, t->n, load_frs(u, k), &s))) return rc;
     fr_store(s, out);
     return ZKH_OK;
@@ -1441,11 +1463,18 @@ extern "C" int zkh_hadamard(zkh_ctx* c, const zkh_tensor* a, const zkh_tensor* b
     if (a->n != b->n) return fail(c, ZKH_EARG, "size mismatch");
     HIPCHK(c, hipSetDevice(c->device));
     int rc = 0;
-    Src sa, sb;
-    if ((rc = src_of(c, a, SL_TMP0, &sa)) || (rc = src_of(c, b, SL_TMP1, &sb))) return rc;
     zkh_tensor* o;
-    if ((rc = tensor_alloc(c, ZKH_KIND_FR, a->n, &o))) return rc;
-    if (a->n) launch_hadamard(c->stream, sa, sb, a->n, o->planes());
+    if (a->kind == ZKH_KIND_I32 && b->kind == ZKH_KIND_I32 && !a->weights && !b->weights) {
+        // two int32 tensors: the exact int64 products (8 bytes an entry where planes take 32)
+        if ((rc = tensor_alloc(c, ZKH_KIND_I64, a->n, &o))) return rc;
+        o->bits = std::min<uint32_t>(a->bits + b->bits, 63);  // |a b| < 2^(bits_a + bits_b), <= 2^62
+        if (a->n) launch_hadamard_i64(c->stream, (const int32_t*)a->d, (const int32_t*)b->d, a->n, (int64_t*)o->d);
+    } else {
+        Src sa, sb;
+        if ((rc = src_of(c, a, SL_TMP0, &sa)) || (rc = src_of(c, b, SL_TMP1, &sb))) return rc;
+        if ((rc = tensor_alloc(c, ZKH_KIND_FR, a->n, &o))) return rc;
+        if (a->n) launch_hadamard(c->stream, sa, sb, a->n, o->planes());
+    }
     if ((rc = settle(c))) {
         zkh_tensor_free(o);
         return rc;
