@@ -723,8 +723,10 @@ int or_mm_prove_fr(uint8_t s[32], const uint32_t* X, const uint32_t* W, const ui
 /* logUp (tlookup.cu, zkob_lookup.cuh fs_phase1/fs_phase2)                          */
 /* ------------------------------------------------------------------------------ */
 void or_range_table(int32_t low, uint32_t len, uint32_t table_size, uint32_t* T) {
+    /* tlookuprange_init_kernel (tlookup.cu:372-380) adds in C++ int: a 32-bit add on the
+       device, so entries past 2^31 - 1 wrap to negative values */
     for (uint32_t i = 0; i < table_size; i++) {
-        int64_t v = i < len ? (int64_t)i + low : (int64_t)len + low - 1;
+        int32_t v = (int32_t)((uint32_t)low + (i < len ? i : len - 1));
         st(T + 8 * i, from_i64(v));
     }
 }

@@ -58,8 +58,11 @@ def test_pad(zkh, ctx, shape):
         ctx.pad(ctx.from_fr(x), shape + [2])
 
 
-@pytest.mark.parametrize("low,length,N", [(-8, 16, 16), (-32768, 65536, 65536), (5, 3, 8), (-(1 << 21), 1 << 22, 1 << 22)])
+@pytest.mark.parametrize("low,length,N", [(-8, 16, 16), (-32768, 65536, 65536), (5, 3, 8), (-(1 << 21), 1 << 22, 1 << 22),
+                                           (2**31 - 4, 8, 8), (-2**31, 4, 8)])
 def test_range_table(zkh, ctx, low, length, N):
+    """tLookupRange's table (int32 entries, the reference's 32-bit arithmetic wrapping past
+    2^31 - 1) against the oracle, with padding past len."""
     assert fr_eq(ctx.range_table(low, length, N).to_fr(), C.range_table(low, length, N))
 
 

@@ -241,6 +241,14 @@ def test_mm_oracle_rejects_wrong_witness():
 LU = [(32, 8, -3, 5), (16, 16, 0, 16), (64, 4, -2, 3), (32, 4, -2, 4), (8, 4, -2, 4), (64, 16, -8, 16)]
 
 
+@pytest.mark.parametrize("low,ln,N", [(2**31 - 4, 8, 8), (2**31 - 2, 3, 4), (-2**31, 4, 8)])
+def test_range_table_int32_arithmetic(low, ln, N):
+    """tlookuprange_init_kernel adds in C++ int (tlookup.cu:376): past 2^31 - 1 the entries
+    wrap, as numpy's int32 addition does."""
+    want = (np.int32(low) + np.minimum(np.arange(N), ln - 1).astype(np.int32)).astype(np.int64)
+    assert C.fr_to_ints(C.range_table(low, ln, N)) == [int(v) % R for v in want]
+
+
 @pytest.mark.parametrize("shape", LU)
 def test_lu_oracle_pins(shape):
     D, N, low, ln = shape

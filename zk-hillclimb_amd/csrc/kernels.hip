@@ -428,6 +428,14 @@ __global__ void k_range_table(int32_t low, uint32_t len, uint32_t N, uint4* olo,
 void launch_range_table(hipStream_t s, int32_t low, uint32_t len, uint32_t N, DevPlanes out) {
     k_range_table<<<grid_for(N, NT, 8192), NT, 0, s>>>(low, len, N, PL_LO(out), PL_HI(out));
 }
+// the same entries as int32 (the table's own 32-bit arithmetic)
+__global__ void k_range_table_i32(int32_t low, uint32_t len, uint32_t N, int32_t* out) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < N; i += gridDim.x * blockDim.x)
+        out[i] = (int32_t)((uint32_t)low + (i < len ? i : len - 1));
+}
+void launch_range_table_i32(hipStream_t s, int32_t low, uint32_t len, uint32_t N, int32_t* out) {
+    k_range_table_i32<<<grid_for(N, NT, 8192), NT, 0, s>>>(low, len, N, out);
+}
 
 // ------------------------------------------------------------------------------------
 // plain and stacked inner-product sumcheck rounds over a [N, D] row layout: row n < Nh

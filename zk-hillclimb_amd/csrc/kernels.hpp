@@ -94,6 +94,7 @@ void launch_pad(hipStream_t s, DevPlanes src, const PadDims& pd, uint32_t total,
                 DevPlanes out);
 // tLookupRange table of N entries: low + min(i, len - 1)
 void launch_range_table(hipStream_t s, int32_t low, uint32_t len, uint32_t N, DevPlanes out);
+void launch_range_table_i32(hipStream_t s, int32_t low, uint32_t len, uint32_t N, int32_t* out);
 // zkip / zkip_stacked round over a [N, D] layout (rows n, n + Nh paired, rows >= N zero,
 // weights E[n] Montgomery AoS of Nh entries, or 1 when E is null): publishes c0, c1, c2
 // (x 2^-256) as job 0 of pub; the fold binds the top row bit in place with v (Montgomery)

@@ -2388,10 +2388,16 @@ extern "C" int zkh_mm_prove(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* X, con
 extern "C" int zkh_lu_range_table(zkh_ctx* c, int32_t low, uint32_t len, uint32_t N, zkh_tensor** out) {
     if (!c || !out || !len || N < len) return fail(c, ZKH_EARG, "bad range table arguments");
     HIPCHK(c, hipSetDevice(c->device));
+    // int32 entries (4 bytes where field planes take 32): the table's values are 32-bit
     zkh_tensor* t;
-    int rc = tensor_alloc(c, ZKH_KIND_FR, N, &t);
+    int rc = tensor_alloc(c, ZKH_KIND_I32, N, &t);
     if (rc) return rc;
-    launch_range_table(c->stream, low, len, N, t->planes());
+    {
+        const int64_t last = (int64_t)low + (int64_t)len - 1;
+        const uint64_t lo_abs = low < 0 ? (uint64_t)(-(int64_t)low) : (uint64_t)low;
+        t->bits = last > INT32_MAX ? 32 : bits_for(std::max<uint64_t>(lo_abs, last < 0 ? (uint64_t)-last : (uint64_t)last));
+    }
+    launch_range_table_i32(c->stream, low, len, N, (int32_t*)t->d);
     hipError_t e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         zkh_tensor_free(t);
