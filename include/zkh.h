@@ -224,7 +224,8 @@ int zkh_matmul_i32(zkh_ctx* ctx, const zkh_tensor* X, const zkh_tensor* W, const
                    uint32_t B, uint32_t IN, uint32_t OUT, zkh_tensor** Y_out);
 
 /* ---------------- logUp lookup (tlookup.cu, zkob_lookup.cuh, zkob_rescale.cu) ---------- */
-/* tLookupRange table (tlookup.cu:372-391): T[i] = low+i (i<len) else low+len-1, size N */
+/* tLookupRange table (tlookup.cu:372-391): T[i] = low+i (i<len) else low+len-1, size N, as an
+ * int32-kind tensor (the sum in 32-bit int arithmetic, wrapping as the reference's int does) */
 int zkh_lu_range_table(zkh_ctx* ctx, int32_t low, uint32_t len, uint32_t N, zkh_tensor** out);
 /* multiplicities m (tlookup.cu:10-48, :414-433): idx = (S-low).limb0, m[idx] += 1.
  * Fails with ZKH_EARG if an index falls outside [0, N) (out-of-range witness). */
