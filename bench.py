@@ -177,10 +177,10 @@ class GluJob:
         u = zkh.challenges(st, self.logD)
         lu = c.lu_prove(st, A, comb, Tcomb, m, alpha, beta, u)
         u_h = zkh.challenges(st, self.logD)
-        H = c.hadamard(S, self.U)
-        claim_H = c.me(H, u_h)
-        zkh.absorb(st, "claim_H", claim_H.tobytes())
-        hp = c.hp_prove_eq(st, claim_H, u_h, S, self.U)
+        # claim_H = H(u_h) of H = S (.) U, absorbed, then the Hadamard sumcheck: one call that
+        # takes the claim from the first round's sums (same transcript bytes as forming H,
+        # evaluating it and absorbing the claim before zkh_hp_prove_eq)
+        hp = c.hp_prove_eq_claim(st, "claim_H", u_h, S, self.U)
         zkh.absorb(st, "S_f2", hp["term"][0].tobytes())
         zkh.absorb(st, "U_f2", hp["term"][1].tobytes())
         return lu["ev"].tobytes() + lu["term"].tobytes() + hp["ev"].tobytes() + hp["term"].tobytes() + st.tobytes()

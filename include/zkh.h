@@ -277,6 +277,15 @@ int zkh_hp_prove(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
 int zkh_hp_prove_eq(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
                     const uint32_t* u, uint32_t k, const zkh_tensor* S, const zkh_tensor* U,
                     uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+/* No single counterpart in the reference: zkob_glu.cu:231-247's claim_H = H(u) of H = S * U
+ * (multi_dim_me), its absorb under `label`, then fs_hadamard, in one call.  The claim
+ * sum eq(i, u) S[i] U[i] comes from the first round's own sums (q(0) + q(1) of the round
+ * polynomial equals the claim), so H and its evaluation are never formed; claim_out receives
+ * it.  Transcript, ev_out, term_out and ws_out are byte-identical to zkh_me(zkh_hadamard(S,
+ * U), u) + zkh_transcript_absorb(label, claim) + zkh_hp_prove_eq. */
+int zkh_hp_prove_eq_claim(zkh_ctx* ctx, uint8_t transcript[32], const char* label, const uint32_t* u,
+                          uint32_t k, const zkh_tensor* S, const zkh_tensor* U, uint32_t claim_out[8],
+                          uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
 
 /* ---------------- Pedersen commitments over BLS12-381 G1 (commitment.cu, g1-tensor.cu) -------
  * A point is the reference's 144-byte G1Jacobian_t (g1-tensor.cuh:63): x, y, z, each 12

@@ -956,3 +956,42 @@ def test_hp_prove_eq_small_ints(zkh, ctx, k, bits):
     for key in ("ev", "term", "ws"):
         assert fr_eq(got[key], want[key]), key
     assert bytes(st_g) == bytes(st_o)
+
+
+@pytest.mark.parametrize("k,kind", [(6, "i32"), (13, "i32"), (14, "i32"), (14, "fr"), (18, "i32")])
+def test_hp_prove_eq_claim(zkh, ctx, k, kind):
+    """claim_H = H(u) of H = S (.) U, its absorb, then the eq-form Hadamard sumcheck in one call
+    (zkob_glu.cu:231-247): the claim from the first round's sums (k >= 14) or from the
+    eq-weighted sum ahead of the persistent loop (k <= 13).  Claim, proof and transcript equal
+    the separate steps' (me of the hadamard, absorb, hp_prove_eq) and, up to 2^14, the oracle's."""
+    n = 1 << k
+    rng = np.random.default_rng(500 + k + (kind == "fr"))
+    s = rng.integers(-2**15, 2**15, size=n, dtype=np.int64)
+    uu = rng.integers(-2**15, 2**15, size=n, dtype=np.int64)
+    s[:3] = [-2**31, 2**31 - 1, 0]  # beyond the first round's small-integer range
+    uu[:3] = [-2**31, -2**31, 5]
+    Sf, Uf = C.ints_to_fr([int(x) for x in s]), C.ints_to_fr([int(x) for x in uu])
+    if kind == "i32":
+        S, U = ctx.from_i32(s.astype(np.int32)), ctx.from_i32(uu.astype(np.int32))
+    else:
+        S, U = ctx.from_fr(Sf), ctx.from_fr(Uf)
+    u = rand_fr_full(rng, k)
+    st1, st_o = seed_transcript(zkh, "hpclaim%d" % k)
+    st2 = st1.copy()
+    got = ctx.hp_prove_eq_claim(st1, "claim_H", u, S, U)
+    claim = ctx.me(ctx.hadamard(S, U), u)
+    zkh.absorb(st2, "claim_H", claim.tobytes())
+    want = ctx.hp_prove_eq(st2, claim, u, S, U)
+    assert fr_eq(got["claim"], claim)
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st1) == bytes(st2)
+    if k <= 14:
+        rc, oc = C.me(C.hadamard(Sf, Uf), u)
+        assert rc == 0
+        C.tr_absorb(st_o, "claim_H", oc.tobytes())
+        rc, hp = C.hp_prove(st_o, oc, C.build_eq(u), Sf, Uf)
+        assert rc == 0
+        assert fr_eq(got["claim"], oc)
+        assert fr_eq(got["ev"], hp["ev"]) and fr_eq(got["term"], hp["term"])
+        assert bytes(st1) == bytes(st_o)

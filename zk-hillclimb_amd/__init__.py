@@ -89,6 +89,7 @@ def lib():
         L.zkh_lu_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove_eq.argtypes = [vp, vp, vp, vp, u32, vp, vp, vp, vp, vp]
+        L.zkh_hp_prove_eq_claim.argtypes = [vp, vp, ctypes.c_char_p, vp, u32, vp, vp, vp, vp, vp, vp]
         L.zkh_mm_prove_batch.argtypes = [vp, vp, u32]
         L.zkh_prof_enable.argtypes = [vp, ctypes.c_int]
         L.zkh_prof_get.argtypes = [vp, ctypes.c_char_p, vp, vp, vp]
@@ -508,6 +509,19 @@ class Context:
         self._chk(lib().zkh_hp_prove_eq(self.h, _p(st), _p(claim), _p(u), k, S.h, U.h, _p(ev),
                                         _p(term), _p(ws)))
         return dict(ev=ev[:4 * k], term=term, ws=ws[:k])
+
+    def hp_prove_eq_claim(self, st, label, u, S, U):
+        """claim = sum eq(u, i) S[i] U[i] absorbed under label, then hp_prove_eq, in one call
+        (the claim from the first round's sums; zkob_glu.cu:231-247)."""
+        u = _frs(u)
+        k = u.shape[0]
+        claim = np.zeros(8, np.uint32)
+        ev = np.zeros((4 * k + 1, 8), np.uint32)
+        term = np.zeros((3, 8), np.uint32)
+        ws = np.zeros((k + 1, 8), np.uint32)
+        self._chk(lib().zkh_hp_prove_eq_claim(self.h, _p(st), label.encode(), _p(u), k, S.h, U.h, _p(claim),
+                                              _p(ev), _p(term), _p(ws)))
+        return dict(claim=claim, ev=ev[:4 * k], term=term, ws=ws[:k])
 
 
 class MmBatch:

@@ -3776,14 +3776,20 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
                 lgnb, now_us() - t_launch);
     return 0;
 }
+// claim_label (eq form only): the claim is not given but is sum eq(i, u) S[i] U[i], taken
+// from the first round's sums (q(0) + q(1) of the round's polynomial in t, which the check
+// below compares with the claim) and absorbed under that label before the first round's
+// evaluations; claim_out receives it
 static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], const zkh_tensor* E,
                      const std::vector<Fr>* ueq, const zkh_tensor* S, const zkh_tensor* U,
-                     uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out) {
+                     uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out, const char* claim_label = nullptr,
+                     uint32_t* claim_out = nullptr) {
     const uint32_t n = S->n;
     if (!n || (n & (n - 1)) || U->n != n || (E && E->n != n))
         return fail(c, ZKH_EARG, "hadamard tables must share a power-of-two size");
     if (ueq && ((uint64_t)1 << ueq->size()) != n) return fail(c, ZKH_EARG, "eq size mismatch");
-    if (!fr_is_canonical(claim_l)) return fail(c, ZKH_EARG, "non-canonical claim");
+    if (claim_label && (!ueq || !claim_out)) return fail(c, ZKH_EARG, "a derived claim needs the eq form");
+    if (!claim_label && !fr_is_canonical(claim_l)) return fail(c, ZKH_EARG, "non-canonical claim");
     HIPCHK(c, hipSetDevice(c->device));
     const uint32_t k = ceil_log2(n);
     int rc = 0;
@@ -3810,7 +3816,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     if (rc) return rc;
     EqState eq;
     if (ueq && (rc = eq_setup(c, *ueq, eq))) return rc;
-    Fr claim = fr_load(claim_l), cE = kOne;
+    Fr claim = claim_label ? kZero : fr_load(claim_l), cE = kOne;
     DevPlanes e_src = Ec, s_src = Sc, u_src = Uc;
     uint32_t vm[8] = {0};
     static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
@@ -3820,6 +3826,13 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     Fr e_fin = kZero, s_fin = kZero, u_fin = kZero;
     const bool no_persist = getenv("ZKH_NO_PERSIST") != nullptr;
     auto persists = [&](uint32_t r) { return (n >> r) <= ZKH_HP_PERSIST_MAX && !no_persist; };
+    const bool derive_claim = claim_label && !persists(0);  // from the first round kernel's sums
+    if (claim_label && !derive_claim) {  // all rounds in the persistent loop: the sum first
+        // (a table this small is never read as int32, so Sc and Uc hold its planes)
+        if ((rc = eq_weighted_sum(c, Sc, &Uc, n, *ueq, &claim))) return rc;
+        tr_absorb_fr(tr, claim_label, claim);
+    }
+    if (claim_label) fr_store(claim, claim_out);
     // U all ones (an I32 tensor measured so at ingest: the RoPE obligations' U = 1) with an
     // explicit E: the per-round kernels skip U, whose folds stay all ones in its source
     const bool u_ones = !ueq && U->kind == ZKH_KIND_I32 && U->ones;
@@ -3946,6 +3959,11 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
                 e[t] = fr_mul(fr_mul(st, cE), fr_eq2(ul, fr_u64(t)));
             }
         }
+        if (r == 0 && derive_claim) {
+            claim = I = fr_add(e[0], e[1]);
+            tr_absorb_fr(tr, claim_label, claim);
+            fr_store(claim, claim_out);
+        }
         if (!fr_eq(claim, fr_add(e[0], e[1])))
             return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r);
         for (int t = 0; t < 4; t++) {
@@ -4011,13 +4029,15 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
 // and U_f2 (and E_f) against the MLEs of S, U (and E, or the eq polynomial) at the point
 static int hp_checked(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const zkh_tensor* E,
                       const std::vector<Fr>* ueq, const zkh_tensor* S, const zkh_tensor* U, uint32_t* ev_out,
-                      uint32_t* term_out, uint32_t* ws_out) {
-    if (!xcheck_on() || !S) return hp_common(c, tr, claim, E, ueq, S, U, ev_out, term_out, ws_out);
+                      uint32_t* term_out, uint32_t* ws_out, const char* claim_label = nullptr,
+                      uint32_t* claim_out = nullptr) {
+    if (!xcheck_on() || !S)
+        return hp_common(c, tr, claim, E, ueq, S, U, ev_out, term_out, ws_out, claim_label, claim_out);
     const uint32_t k = ceil_log2(S->n);
     std::vector<uint32_t> wsb(8 * (size_t)std::max<uint32_t>(k, 1)), tb(24);
     uint32_t* ws = ws_out ? ws_out : wsb.data();
     uint32_t* term = term_out ? term_out : tb.data();
-    int rc = hp_common(c, tr, claim, E, ueq, S, U, ev_out, term, ws);
+    int rc = hp_common(c, tr, claim, E, ueq, S, U, ev_out, term, ws, claim_label, claim_out);
     if (rc) return rc;
     const std::vector<uint32_t> pt = reversed_point(ws, k);
     if ((rc = xcheck_me(c, S, pt.data(), k, term, "hadamard S")) ||
@@ -4042,6 +4062,14 @@ extern "C" int zkh_hp_prove_eq(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[
     if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
     std::vector<Fr> uv = load_frs(u, k);
     return hp_checked(c, tr, claim, nullptr, &uv, S, U, ev_out, term_out, ws_out);
+}
+extern "C" int zkh_hp_prove_eq_claim(zkh_ctx* c, uint8_t tr[32], const char* label, const uint32_t* u, uint32_t k,
+                                     const zkh_tensor* S, const zkh_tensor* U, uint32_t claim_out[8],
+                                     uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out) {
+    if (!c || !tr || !label || !claim_out || !S || !U || (!u && k)) return fail(c, ZKH_EARG, "null argument");
+    if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
+    std::vector<Fr> uv = load_frs(u, k);
+    return hp_checked(c, tr, nullptr, nullptr, &uv, S, U, ev_out, term_out, ws_out, label, claim_out);
 }
 
 // ---------------------------------------------------------------------------------------
