@@ -88,11 +88,14 @@ int zkh_sum(zkh_ctx* ctx, const zkh_tensor* t, uint32_t out[8]);
  * :588-609); requires 2^(k-1) < n <= 2^k */
 int zkh_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k, uint32_t out[8]);
 /* zkh_me without device allocation.  No counterpart in the reference: it is for callers
- * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  Its device scratch (eq tables, block partials,
- * counters: 557,312 bytes) is one static array per device, held until the process ends and
- * resolved at zkh_ctx_create; the call allocates nothing.  t: a field-element tensor;
- * k <= 24 (ZKH_EARG beyond).  Calls that overlap on one device share that scratch and race. */
+ * that cannot allocate device memory (tight serving loops, harnesses that forbid hipMalloc,
+ * a process between the captures of a HIP graph that must not grow the device heap).  Its
+ * device scratch (eq tables, block partials, counters: 557,312 bytes) is one static array
+ * per device, held until the process ends and resolved at zkh_ctx_create; the call
+ * allocates nothing.  It is synchronous: it runs on the context's stream and waits for its
+ * result there (a host spin with hipStreamQuery), so the call itself cannot be recorded into
+ * a graph.  t: a field-element tensor; k <= 24 (ZKH_EARG beyond).  Calls that overlap on one
+ * device share that scratch and race. */
 int zkh_me_static(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k, uint32_t out[8]);
 /* one degree-2 product round over MSB pairs (k_bo_hp2 + bo_dev_sum, zkob_claims.cuh:367-383,
  * :577-592): out[t] = sum_{i < n/2} a_t[i] b_t[i] for t = 0, 1, 2, with
@@ -240,8 +243,11 @@ int zkh_lu_inverse(zkh_ctx* ctx, const zkh_tensor* S, const uint32_t beta[8], zk
  * (N entries): A[i] is read off the table inverse 1/(T+beta) at j = (S[i]-low).limb0 wherever
  * T[j] == S[i] (one table-sized inversion instead of a witness-sized one), with a direct
  * inversion of S if some entry is not; the table inverse stays with the context, and the
- * next zkh_lu_prove on this T and beta uses it instead of inverting T again.  No counterpart
- * in the reference, which inverts S (zkob_rescale.cu:121-123) and T separately. */
+ * next zkh_lu_prove on this T and beta uses it instead of inverting T again.  Retention: the
+ * context holds that inverse (N field elements, 128 MiB at N = 2^22) until a zkh_lu_prove
+ * takes it over or, on another table or beta, frees it; until the next zkh_lu_range_inverse
+ * or zkh_lu_tuple_inverse replaces it; or until zkh_ctx_destroy.  No counterpart in the
+ * reference, which inverts S (zkob_rescale.cu:121-123) and T separately. */
 int zkh_lu_range_inverse(zkh_ctx* ctx, const zkh_tensor* S, int32_t low, const zkh_tensor* T,
                          const uint32_t beta[8], zkh_tensor** A_out);
 /* zkob_glu.cu:155-170 in one call, for int32 G (D entries), T and mapped (N entries):
@@ -251,8 +257,8 @@ int zkh_lu_range_inverse(zkh_ctx* ctx, const zkh_tensor* S, int32_t low, const z
  * (D entries) and T_comb (N entries) separately: here A[i] is read off the table inverse
  * 1/(T_comb+beta) wherever T[j] == G[i] (comb[i] is then T_comb[j]), with a direct inversion
  * of comb if some entry is not; the table inverse stays with the context, and the next
- * zkh_lu_prove on this T_comb and beta uses it instead of inverting T_comb again.
- * ZKH_EARG if an index falls outside [0, N) (as zkh_lu_mapping). */
+ * zkh_lu_prove on this T_comb and beta uses it instead of inverting T_comb again (retained
+ * as zkh_lu_range_inverse's).  ZKH_EARG if an index falls outside [0, N) (as zkh_lu_mapping). */
 int zkh_lu_tuple_inverse(zkh_ctx* ctx, const zkh_tensor* G, int32_t low, const zkh_tensor* T,
                          const zkh_tensor* mapped, const uint32_t r[8], const uint32_t beta[8],
                          zkh_tensor** comb_out, zkh_tensor** Tcomb_out, zkh_tensor** A_out);
@@ -282,7 +288,10 @@ int zkh_hp_prove_eq(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8
  * sum eq(i, u) S[i] U[i] comes from the first round's own sums (q(0) + q(1) of the round
  * polynomial equals the claim), so H and its evaluation are never formed; claim_out receives
  * it.  Transcript, ev_out, term_out and ws_out are byte-identical to zkh_me(zkh_hadamard(S,
- * U), u) + zkh_transcript_absorb(label, claim) + zkh_hp_prove_eq. */
+ * U), u) + zkh_transcript_absorb(label, claim) + zkh_hp_prove_eq.  The claim equals the
+ * committed H's evaluation only when that H is S * U: a caller whose H is sourced separately
+ * (e.g. a driver testing a forged H) keeps zkh_me on H and calls zkh_hp_prove_eq.  With
+ * ZKH_XCHECK=1 the claim is also recomputed as the eq-weighted sum of S * U and compared. */
 int zkh_hp_prove_eq_claim(zkh_ctx* ctx, uint8_t transcript[32], const char* label, const uint32_t* u,
                           uint32_t k, const zkh_tensor* S, const zkh_tensor* U, uint32_t claim_out[8],
                           uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);

@@ -150,13 +150,49 @@ def test_c3_logup(zkh, ctx):
     assert bytes(st_g) == bytes(st_o)
 
 
+def test_c3_logup_range_inverse(zkh, ctx):
+    """C3 through the entry point the bench times: zkh_lu_range_inverse (A read off the
+    table inverse, which zkh_lu_prove then takes over; zkob_rescale.cu:119-146), the whole
+    proof against the oracle's separate steps (Fermat inverses of S and of T)."""
+    c = S.CONFIGS["C3"]
+    D, N, low = c["D"], c["N"], c["low"]
+    rng = S.rng_for(3)
+    vals = rng.integers(low, low + N, size=D).astype(np.int32)
+    Sf = C.ints_to_fr(vals)
+    T = C.range_table(low, N, N)
+    st_g, st_o = both(zkh, "C3:rescale:fused")
+    rc, m = C.lu_prep(Sf, low, N)
+    assert rc == 0
+    Sg = ctx.from_i32(vals)
+    mg = ctx.lu_prep(Sg, low, N)
+    Tg = ctx.range_table(low, N, N)
+    beta = chal_both(zkh, st_g, st_o)
+    log("C3 fused: oracle inverse (Fermat, 2^20)")
+    A = C.lu_inverse(Sf, beta)
+    Ag = ctx.lu_range_inverse(Sg, low, Tg, beta)
+    assert fr_eq(Ag.to_fr(), A)
+    alpha = chal_both(zkh, st_g, st_o)
+    u = chal_both(zkh, st_g, st_o, P.ceil_log2(D))
+    log("C3 fused: oracle proof")
+    rc, want = C.lu_prove(st_o, A, Sf, T, m, alpha, beta, u)
+    assert rc == 0
+    got = ctx.lu_prove(st_g, Ag, Sg, Tg, mg, alpha, beta, u)
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
 # ------------------------------------------------------------------ SwiGLU (C4, C5)
-def _glu(zkh, ctx, cfg, seed, parts=("lookup", "hadamard")):
+def _glu(zkh, ctx, cfg, seed, parts=("lookup", "hadamard"), fused=False):
     """zkob_glu.cu:146-247: mapping lookup of G into the silu table, combiner
     comb = G + r S against T_comb = T + r silu, logUp proof, then the eq-weighted Hadamard
     sumcheck of H = S (.) U, on the GPU and on the oracle side by side.  With parts =
     ("hadamard",) the lookup runs on the GPU only (its challenges advance both transcripts
-    identically: the oracle replays the same absorbs from the GPU's round polynomials)."""
+    identically: the oracle replays the same absorbs from the GPU's round polynomials).
+    fused: the GPU side runs the entry points the bench times, zkh_lu_tuple_inverse (comb,
+    T_comb and A in one call, A read off the table inverse that zkh_lu_prove takes over) and
+    zkh_hp_prove_eq_claim (claim_H from the Hadamard prover's first round, absorbed inside),
+    against the oracle's separate steps (zkob_glu.cu:155-170, :231-247)."""
     c = S.CONFIGS[cfg]
     inp = S.glu_inputs(S.rng_for(seed), c["B"], c["ffn"], N=c["glu_table"])
     D, N, low = inp["D"], inp["N"], inp["low"]
@@ -182,13 +218,17 @@ def _glu(zkh, ctx, cfg, seed, parts=("lookup", "hadamard")):
     assert fr_eq(mg.to_fr(), m)
     r = chal_both(zkh, st_g, st_o)
     beta = chal_both(zkh, st_g, st_o)
-    comb_g = ctx.axpy(Gg, r, Sg)
-    tcomb_g = ctx.axpy(Tg, r, mapped)
+    if fused:
+        comb_g, tcomb_g, Ag = ctx.lu_tuple_inverse(Gg, low, Tg, mapped, r, beta)
+    else:
+        comb_g = ctx.axpy(Gg, r, Sg)
+        tcomb_g = ctx.axpy(Tg, r, mapped)
     comb = C.axpy(Gf, r, Sf)
     tcomb = C.axpy(C.range_table(low, N, N), r, C.ints_to_fr(silu))
     assert fr_eq(comb_g.to_fr(), comb)
     assert fr_eq(tcomb_g.to_fr(), tcomb)
-    Ag = ctx.lu_inverse(comb_g, beta)
+    if not fused:
+        Ag = ctx.lu_inverse(comb_g, beta)
     A = Ag.to_fr()
     assert C.check_inverse(comb, A, beta) == 0  # fixes A = 1/(comb + beta) entry by entry
     absorb_both(zkh, st_g, st_o, "com_A", bytes(range(144)))
@@ -219,14 +259,22 @@ def _glu(zkh, ctx, cfg, seed, parts=("lookup", "hadamard")):
     rc, claim = C.me(H, u_h)
     assert rc == 0
     del H
-    claim_g = ctx.me(ctx.hadamard(Sg, Ug), u_h)
-    assert fr_eq(claim_g, claim)
-    absorb_both(zkh, st_g, st_o, "claim_H", claim.tobytes())
+    if fused:
+        # the claim absorbed inside the call, before the first round's evaluations
+        C.tr_absorb(st_o, "claim_H", claim.tobytes())
+    else:
+        claim_g = ctx.me(ctx.hadamard(Sg, Ug), u_h)
+        assert fr_eq(claim_g, claim)
+        absorb_both(zkh, st_g, st_o, "claim_H", claim.tobytes())
     log("%s SwiGLU: oracle Hadamard proof" % cfg)
     E = C.build_eq(u_h)
     rc, want = C.hp_prove(st_o, claim, E, Sf, Uf)
     assert rc == 0
-    got = ctx.hp_prove_eq(st_g, claim_g, u_h, Sg, Ug)
+    if fused:
+        got = ctx.hp_prove_eq_claim(st_g, "claim_H", u_h, Sg, Ug)
+        assert fr_eq(got["claim"], claim)
+    else:
+        got = ctx.hp_prove_eq(st_g, claim_g, u_h, Sg, Ug)
     for key in ("ev", "term", "ws"):
         assert fr_eq(got[key], want[key]), key
     assert bytes(st_g) == bytes(st_o)
@@ -242,6 +290,20 @@ def test_c5_swiglu_lookup(zkh, ctx):
 
 def test_c5_swiglu_hadamard(zkh, ctx):
     _glu(zkh, ctx, "C5", 5, parts=("hadamard",))
+
+
+def test_c4_swiglu_fused(zkh, ctx):
+    _glu(zkh, ctx, "C4", 4, fused=True)
+
+
+def test_c5_swiglu_lookup_fused(zkh, ctx):
+    """2^25 witnesses against the 2^22 table: A gathered from the table inverse, which the
+    proof takes over and folds through its three phase-1 rounds into phase 2."""
+    _glu(zkh, ctx, "C5", 5, parts=("lookup",), fused=True)
+
+
+def test_c5_swiglu_hadamard_fused(zkh, ctx):
+    _glu(zkh, ctx, "C5", 5, parts=("hadamard",), fused=True)
 
 
 # ------------------------------------------------------------------ RoPE (C4)

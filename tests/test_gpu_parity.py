@@ -742,6 +742,41 @@ def test_lu_tuple_inverse_out_of_range(zkh, ctx):
     assert e.value.code == zkh.EARG
 
 
+@pytest.mark.parametrize("gkind", ["i32", "fr"])
+def test_range_inverses_table_past_int32_max(zkh, ctx, gkind):
+    """A range table whose entries wrap past 2^31 - 1 (low + j computed in 32-bit int, as
+    tlookup.cu:376 builds it): witnesses low + j are the table's entry only below the wrap.
+    A field-kind witness above 2^31 - 1 is no table entry, so its A must be its own inverse
+    1/(G + beta) (the direct inversion), for both gathers; int32 witnesses cover the entries
+    below the wrap."""
+    N = 64
+    low = 2**31 - 1 - 40  # entries j <= 40 are low + j, j >= 41 wrap to negative values
+    js = np.array(list(range(N)) * 3, np.int64)
+    rng = np.random.default_rng(41)
+    rng.shuffle(js)
+    if gkind == "i32":
+        js = js[js <= 40]
+    vals = [low + int(j) for j in js]  # the true integers, past 2^31 - 1 for j > 40
+    D = len(vals)
+    beta, r = rand_fr_full(rng, 2)
+    mapped = rng.integers(-2**20, 2**20, size=N).astype(np.int32)
+    Gf = C.ints_to_fr(vals)
+    G = ctx.from_i32(np.array(vals, np.int64).astype(np.int32)) if gkind == "i32" else ctx.from_fr(Gf)
+    T = ctx.range_table(low, N, N)
+    T_o = C.range_table(low, N, N)
+    assert fr_eq(T.to_fr(), T_o)
+    # plain range lookup: A = 1/(G + beta)
+    want = C.lu_inverse(Gf, beta)
+    assert fr_eq(ctx.lu_range_inverse(G, low, T, beta).to_fr(), want)
+    # SwiGLU combiner: comb = G + r mapped[(G - low).limb0], A = 1/(comb + beta)
+    S_o = C.ints_to_fr([int(mapped[int(j)]) for j in js])
+    comb_o = C.axpy(Gf, r, S_o)
+    comb, Tcomb, A = ctx.lu_tuple_inverse(G, low, T, ctx.from_i32(mapped), r, beta)
+    assert fr_eq(comb.to_fr(), comb_o)
+    assert fr_eq(Tcomb.to_fr(), C.axpy(T_o, r, C.ints_to_fr(mapped)))
+    assert fr_eq(A.to_fr(), C.lu_inverse(comb_o, beta))
+
+
 # ---------------------------------------------------------------- elementwise with int32 operands
 def test_hadamard_axpy_int32_edges(zkh, ctx):
     """Elementwise products and axpy with int32 operands take the 32-bit multiply (quotient
@@ -958,8 +993,10 @@ def test_hp_prove_eq_small_ints(zkh, ctx, k, bits):
     assert bytes(st_g) == bytes(st_o)
 
 
-@pytest.mark.parametrize("k,kind", [(6, "i32"), (13, "i32"), (14, "i32"), (14, "fr"), (18, "i32")])
-def test_hp_prove_eq_claim(zkh, ctx, k, kind):
+@pytest.mark.parametrize("k,kind,no_persist", [(0, "i32", False), (0, "i32", True), (6, "i32", False),
+                                               (13, "i32", False), (14, "i32", False), (14, "fr", False),
+                                               (18, "i32", False)])
+def test_hp_prove_eq_claim(zkh, ctx, k, kind, no_persist, monkeypatch):
     """claim_H = H(u) of H = S (.) U, its absorb, then the eq-form Hadamard sumcheck in one call
     (zkob_glu.cu:231-247): the claim from the first round's sums (k >= 14) or from the
     eq-weighted sum ahead of the persistent loop (k <= 13).  Claim, proof and transcript equal
@@ -968,8 +1005,10 @@ def test_hp_prove_eq_claim(zkh, ctx, k, kind):
     rng = np.random.default_rng(500 + k + (kind == "fr"))
     s = rng.integers(-2**15, 2**15, size=n, dtype=np.int64)
     uu = rng.integers(-2**15, 2**15, size=n, dtype=np.int64)
-    s[:3] = [-2**31, 2**31 - 1, 0]  # beyond the first round's small-integer range
-    uu[:3] = [-2**31, -2**31, 5]
+    s[:3] = [-2**31, 2**31 - 1, 0][:n]  # beyond the first round's small-integer range
+    uu[:3] = [-2**31, -2**31, 5][:n]
+    if no_persist:  # every round a round kernel (k = 0: none at all, the sum first)
+        monkeypatch.setenv("ZKH_NO_PERSIST", "1")
     Sf, Uf = C.ints_to_fr([int(x) for x in s]), C.ints_to_fr([int(x) for x in uu])
     if kind == "i32":
         S, U = ctx.from_i32(s.astype(np.int32)), ctx.from_i32(uu.astype(np.int32))

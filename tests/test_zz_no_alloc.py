@@ -1,6 +1,9 @@
 """zkh_me_static (the allocation-free MLE evaluation) against zkh_me and the oracle, through
 the C ABI: two calls in a row, the second on a smaller input, then a third larger again,
-Boolean points, and the rejections (too many variables, integer tensor)."""
+Boolean points, the rejections (too many variables, integer tensor), and that the calls
+leave the device's free memory unchanged."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -77,3 +80,33 @@ def test_me_static_rejections(zkh, sctx):
     assert e.value.code == zkh.EARG
     # the context still works afterwards
     _check(zkh, sctx, 100, 7, 8)
+
+
+def _device_free_bytes():
+    """hipMemGetInfo's free bytes of the current device, from the HIP runtime libzkh.so uses."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_me_static_allocates_nothing(zkh):
+    """A fresh context: after its tensors exist and one zkh_me has run the same kernels once
+    (the runtime's first launches may set up the code object), several zkh_me_static calls
+    of different sizes must not change the device's free memory."""
+    ctx = zkh.Context(0)
+    try:
+        rng = np.random.default_rng(9)
+        big = ctx.from_fr(rand_fr_full(rng, 1 << 16))
+        small = ctx.from_fr(rand_fr_full(rng, 300))
+        u16, u9 = rand_fr_full(rng, 16), rand_fr_full(rng, 9)
+        want_big, want_small = ctx.me(big, u16), ctx.me(small, u9)
+        ctx.sync()
+        before = _device_free_bytes()
+        for _ in range(3):
+            assert fr_eq(ctx.me_static(big, u16), want_big)
+            assert fr_eq(ctx.me_static(small, u9), want_small)
+        ctx.sync()
+        assert _device_free_bytes() == before
+    finally:
+        ctx.close()

@@ -1,7 +1,9 @@
 """Runs matmul, logUp and Hadamard proofs through libzkh.so in a process started with
 ZKH_XCHECK=1, so that every proof also re-evaluates its folded terminals as MLEs of its
 input tables at the opening point (the reference's "terminal != multi_dim_me" guards,
-zkob_fc.cu:337-345, zkob_rescale.cu:151-165, zkob_glu.cu:186-192 and :254-260).  A
+zkob_fc.cu:337-345, zkob_rescale.cu:151-165, zkob_glu.cu:186-192 and :254-260), and the
+logUp and Hadamard round kernels compute every round's sums at 1, so that each round's
+p(0) + p(1) = claim is checked on device sums (zkob_lookup.cuh:155, :183, :303).  A
 mismatch fails the call with ZKH_EROUND; the script prints one line per case and exits
 non-zero on the first failure.  Called by tests/test_gpu_xcheck.py; not a test module."""
 import os
@@ -75,6 +77,57 @@ def main():
         ctx.hp_prove(zkh.transcript("xc:hp:%d" % k), claim, ctx.from_fr(E), ctx.from_fr(S), ctx.from_fr(U))
         ctx.hp_prove_eq(zkh.transcript("xc:hp:%d" % k), claim, u, ctx.from_fr(S), ctx.from_fr(U))
         say("hp ok", k)
+
+    # per-round checks: tables large enough for the round kernels (above the persistent
+    # loops' 8192 entries), whose folding rounds then compute their sums at 1 instead of
+    # deriving them; each call checks p(0) + p(1) = claim every round, and the proofs
+    # must equal the oracle's (which checks the same identity per round)
+    D = N = 1 << 16
+    low = -(1 << 15)
+    vals = rng.integers(low, low + N, size=D).astype(np.int32)
+    Sf = C.ints_to_fr(vals)
+    Sg = ctx.from_i32(vals)
+    Tg = ctx.range_table(low, N, N)
+    st, st_o = zkh.transcript("xc:lu:rounds"), C.tr_init("xc:lu:rounds")
+    beta = zkh.challenge(st)
+    assert np.array_equal(C.tr_challenge_fr(st_o), beta)
+    Ag = ctx.lu_range_inverse(Sg, low, Tg, beta)
+    alpha = zkh.challenge(st)
+    C.tr_challenge_fr(st_o)
+    u = np.array([zkh.challenge(st) for _ in range(16)])
+    for _ in range(16):
+        C.tr_challenge_fr(st_o)
+    got = ctx.lu_prove(st, Ag, Sg, Tg, ctx.lu_prep(Sg, low, N), alpha, beta, u)
+    rc, m = C.lu_prep(Sf, low, N)
+    rc, want = C.lu_prove(st_o, C.lu_inverse(Sf, beta), Sf, C.range_table(low, N, N), m, alpha, beta, u)
+    assert rc == 0
+    for key in ("ev", "term", "ws"):
+        assert np.array_equal(got[key], want[key]), key
+    assert bytes(st) == bytes(st_o)
+    say("lu per-round ok", D)
+    k = 16
+    n = 1 << k
+    S_i = rng.integers(-2**15, 2**15, size=n).astype(np.int32)
+    U_i = rng.integers(-2**15, 2**15, size=n).astype(np.int32)
+    Sf, Uf = C.ints_to_fr(S_i), C.ints_to_fr(U_i)
+    st, st_o = zkh.transcript("xc:hp:rounds"), C.tr_init("xc:hp:rounds")
+    u = np.array([zkh.challenge(st) for _ in range(k)])
+    for _ in range(k):
+        C.tr_challenge_fr(st_o)
+    got = ctx.hp_prove_eq_claim(st, "claim_H", u, ctx.from_i32(S_i), ctx.from_i32(U_i))
+    rc, claim = C.me(C.hadamard(Sf, Uf), u)
+    C.tr_absorb(st_o, "claim_H", claim.tobytes())
+    rc, want = C.hp_prove(st_o, claim, C.build_eq(u), Sf, Uf)
+    assert rc == 0 and np.array_equal(got["claim"], claim)
+    for key in ("ev", "term", "ws"):
+        assert np.array_equal(got[key], want[key]), key
+    assert bytes(st) == bytes(st_o)
+    E = C.build_eq(u)
+    got = ctx.hp_prove(zkh.transcript("xc:hpE"), claim, ctx.from_fr(E), ctx.from_fr(Sf), ctx.from_fr(Uf))
+    rc, want = C.hp_prove(C.tr_init("xc:hpE"), claim, E, Sf, Uf)
+    for key in ("ev", "term", "ws"):
+        assert np.array_equal(got[key], want[key]), key
+    say("hp per-round ok", k)
     ctx.close()
     say("xcheck all ok")
 

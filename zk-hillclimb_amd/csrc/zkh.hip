@@ -500,9 +500,11 @@ static int ensure_ps(zkh_ctx* c, size_t words) {
 // ---- convention cross-checks (ZKH_XCHECK=1): the reference's "fold terminals ==
 // multi_dim_me" guards (zkob_fc.cu:337-345, zkob_glu.cu:186-192, :254-260,
 // zkob_rescale.cu:151-165): after a proof, each folded terminal is recomputed as the MLE of
-// its input table at the opening point, and a mismatch fails the call (ZKH_EROUND).  Off by
-// default: the sumcheck algebra already implies the equality, the re-evaluations cost
-// extra passes over the inputs. ----
+// its input table at the opening point, and a mismatch fails the call (ZKH_EROUND).  The
+// logUp and Hadamard round kernels then also compute every round's sums at 1 instead of
+// deriving them from the pieces' claims, so p(0) + p(1) = claim is checked per round on
+// device sums (zkob_lookup.cuh:155, :183, :303).  Off by default: the sumcheck algebra
+// already implies the equalities, the re-evaluations cost extra passes over the inputs. ----
 static bool xcheck_on() {
     static const bool on = getenv("ZKH_XCHECK") && atoi(getenv("ZKH_XCHECK")) > 0;
     return on;
@@ -2598,6 +2600,15 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
     *A_out = A;
     return ZKH_OK;
 }
+// Entries j < the returned length of the range table T are the true integers low + j, so
+// T[j] == G iff G - low is the integer j below it (the gathers then read G alone).  The
+// table's entries are int32 sums that wrap past 2^31 - 1 (tlookup.cu:376), so the length
+// stops at the last entry that does not wrap; 0 when T is not a known range table at low.
+static uint32_t range_shortcut_len(const zkh_tensor* T, int32_t low) {
+    if (T->range_gen != T->gen || T->range_low != low) return 0;
+    const int64_t fit = (int64_t)INT32_MAX - (int64_t)low + 1;  // entries low .. INT32_MAX
+    return (uint32_t)std::min<int64_t>((int64_t)T->range_len, fit);
+}
 extern "C" int zkh_lu_range_inverse(zkh_ctx* c, const zkh_tensor* S, int32_t low, const zkh_tensor* T,
                                     const uint32_t beta[8], zkh_tensor** A_out) {
     if (!c || !S || !T || !beta || !A_out) return fail(c, ZKH_EARG, "null argument");
@@ -2627,7 +2638,7 @@ extern "C" int zkh_lu_range_inverse(zkh_ctx* c, const zkh_tensor* S, int32_t low
         ProfScope ps(c, "lu_range_gather", (double)D * (32 + 32 + 32));
         uint32_t lowl[8];
         fr_store(fr_from_i64(low), lowl);
-        const uint32_t tlen = T->range_gen == T->gen && T->range_low == low ? T->range_len : 0;
+        const uint32_t tlen = range_shortcut_len(T, low);
         launch_lu_range_gather(c->stream, ss, D, lowl, st, tlen, N, Binv->planes(), A->planes(), flags);
     }
     if ((rc = settle(c, flags, &hf))) return drop(rc);
@@ -2684,7 +2695,7 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
         uint32_t lowl[8];
         fr_store(fr_from_i64(low), lowl);
         // a range table at this low: T[j] == G[i] iff G[i] - low is j < len, read from G alone
-        const uint32_t tlen = T->range_gen == T->gen && T->range_low == low ? T->range_len : 0;
+        const uint32_t tlen = range_shortcut_len(T, low);
         launch_lu_tuple_gather(c->stream, sg, D, lowl, st, tlen, sm, N, r, rm, Binv->planes(), comb->planes(),
                                A->planes(), flags);
     }
@@ -2964,6 +2975,10 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         taken.t = c->lu_tinv;
         c->lu_tinv = nullptr;
         c->lu_tinv_of = 0;
+    } else if (c->lu_tinv) {  // kept for another table or beta: this proof ends its use
+        zkh_tensor_free(c->lu_tinv);
+        c->lu_tinv = nullptr;
+        c->lu_tinv_of = 0;
     }
     DevPlanes Bw = taken.t ? taken.t->planes() : scratch_planes(c, SL_EO, N, &rc);
     if (rc) return rc;
@@ -3009,7 +3024,11 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     // is 0; inv_u holds 1/u_j, computed while the first round runs
     LuPieces pc;
     std::vector<Fr> inv_u;
-    auto derives = [&](uint32_t r) { return !fr_eq(u[logD - r - 1], kZero); };
+    // (ZKH_XCHECK=1: no round derives, so every round's p(0) + p(1) = claim is checked on
+    // sums the device computed, and a device error fails at its own round as in the
+    // reference, zkob_lookup.cuh:155, :183)
+    const bool per_round_check = xcheck_on();
+    auto derives = [&](uint32_t r) { return !per_round_check && !fr_eq(u[logD - r - 1], kZero); };
     struct Launched {
         Publish pb;
         bool cf_a, cf_b;
@@ -3043,8 +3062,11 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             l.dv_a = dv;
             l.dv_b = dv && btm_pending;
             {
-                ProfScope ps(c, "lu_phase2",
-                             ((as_pending ? 3.0 * n : (double)n) * 2 + (btm_pending ? 3.0 * n : (double)n) * 3) * 32);
+                // bytes each table moves: read n entries, or fold 2n read into n written; m
+                // is read as int32 counts (4 bytes) until its first fold writes its planes
+                const double per = as_pending ? 3.0 * n : (double)n, pbt = btm_pending ? 3.0 * n : (double)n;
+                const double m_bytes = !m_src32 ? pbt * 32 : btm_pending ? 2.0 * n * 4 + (double)n * 32 : (double)n * 4;
+                ProfScope ps(c, "lu_phase2", per * 2 * 32 + pbt * 2 * 32 + m_bytes);
                 launch_lu_phase2(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
                                  Tab{m_src, mw}, n, as_pending, btm_pending, vm, vmp, beta_l,
                                  EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b, dv, m_src32);
@@ -3826,7 +3848,8 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     Fr e_fin = kZero, s_fin = kZero, u_fin = kZero;
     const bool no_persist = getenv("ZKH_NO_PERSIST") != nullptr;
     auto persists = [&](uint32_t r) { return (n >> r) <= ZKH_HP_PERSIST_MAX && !no_persist; };
-    const bool derive_claim = claim_label && !persists(0);  // from the first round kernel's sums
+    // from the first round kernel's sums (a one-entry table has no round: the sum first)
+    const bool derive_claim = claim_label && k > 0 && !persists(0);
     if (claim_label && !derive_claim) {  // all rounds in the persistent loop: the sum first
         // (a table this small is never read as int32, so Sc and Uc hold its planes)
         if ((rc = eq_weighted_sum(c, Sc, &Uc, n, *ueq, &claim))) return rc;
@@ -3852,7 +3875,9 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     auto launch = [&](uint32_t r, const uint32_t* vmp) {
         const uint32_t sz = n >> r;
         const int fold = r > 0;
-        Launched l{make_pub(c, 1), fold && (!ueq || !fr_eq((*ueq)[k - r - 1], kZero))};
+        // a folding round derives its sum at 1 unless its eq coordinate is 0, or ZKH_XCHECK=1
+        // asks for every round's p(0) + p(1) = claim on device sums (zkob_lookup.cuh:303)
+        Launched l{make_pub(c, 1), fold && !xcheck_on() && (!ueq || !fr_eq((*ueq)[k - r - 1], kZero))};
         if (u_ones) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
             launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, l.pb, l.dv, s_int);
@@ -3860,7 +3885,11 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
             launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp, l.pb, l.dv);
         } else {
-            ProfScope ps(c, "hp_eq_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
+            // S and U read as int32 (4 bytes) until their first fold writes their planes
+            auto tab_bytes = [&](bool i32) {
+                return !i32 ? (fold ? 3.0 * sz : (double)sz) * 32 : fold ? 2.0 * sz * 4 + (double)sz * 32 : (double)sz * 4;
+            };
+            ProfScope ps(c, "hp_eq_round", tab_bytes(s32 != nullptr) + tab_bytes(u32 != nullptr));
             launch_hp_eq_round(c->stream, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp,
                                EqW{eq.elo_d, eq.ehi_d, k - r - 1}, l.pb, l.dv, s32, u32);
         }
@@ -4047,6 +4076,14 @@ static int hp_checked(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const
     Fr e = kOne;  // eq(u, pt) = prod_i eq2(u_i, pt_i)
     for (uint32_t i = 0; i < k; i++) e = fr_mul(e, fr_eq2((*ueq)[i], fr_load(&pt[8 * (size_t)i])));
     if (!fr_eq(e, fr_load(term + 16))) return fail(c, ZKH_EROUND, "hadamard E terminal != eq(u, point) (convention bug)");
+    if (claim_label) {  // the claim taken from the first round against sum eq(u, i) S[i] U[i]
+        DevPlanes Sp, Up;
+        Fr direct;
+        if ((rc = as_planes(c, S, SL_TMP1, &Sp)) || (rc = as_planes(c, U, SL_TMP2, &Up)) ||
+            (rc = eq_weighted_sum(c, Sp, &Up, S->n, *ueq, &direct)))
+            return rc;
+        if (!fr_eq(direct, fr_load(claim_out))) return fail(c, ZKH_EROUND, "hadamard claim != sum eq S U");
+    }
     return ZKH_OK;
 }
 extern "C" int zkh_hp_prove(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const zkh_tensor* E,
