@@ -586,6 +586,50 @@ def test_lu_inverse_zero(zkh, ctx):
     assert fr_eq(got, want)
 
 
+@pytest.mark.parametrize("D,N", [(1 << 15, 1 << 15), (1 << 16, 1 << 14)])
+def test_lu_prove_zero_inverse(zkh, ctx, D, N):
+    """beta = -(a table value v): A and B have zero entries (inverse of zero is zero), so
+    a (s + beta) = 0 where S = v and the first round may not take sum eq a (s + beta) = 1;
+    the logUp relation then fails and, as in the oracle, the proof stops at its first
+    round's consistency check.  With a random beta (no zero) the same tensors prove and
+    equal the oracle's proof (phase 2 alone, and phase 1 first)."""
+    low = -(N // 2)
+    rng = np.random.default_rng(D + 3 * N)
+    vals = rng.integers(low, low + N, size=D).astype(np.int32)
+    v = int(vals[7])
+    S = C.ints_to_fr(vals)
+    T = C.range_table(low, N, N)
+    rc, m = C.lu_prep(S, low, N)
+    assert rc == 0
+    alpha = rand_fr_full(rng, 1)[0]
+    u = rand_fr_full(rng, P.ceil_log2(D))
+    Sg, Tg = ctx.from_i32(vals), ctx.range_table(low, N, N)
+    mg = ctx.lu_prep(Sg, low, N)
+    for shift in (0, 1):
+        beta = C.ints_to_fr([-v % P.R])[0] if not shift else rand_fr_full(rng, 1)[0]
+        A = C.lu_inverse(S, beta)
+        assert A[7].any() == bool(shift)
+        st_g, st_o = seed_transcript(zkh, "luz:%d:%d:%d" % (D, N, shift))
+        rc, want = C.lu_prove(st_o, A, S, T, m, alpha, beta, u)
+        Ag = ctx.lu_inverse(Sg, beta)
+        if not shift:
+            assert rc != 0
+            with pytest.raises(zkh.ZkhError) as e:
+                ctx.lu_prove(st_g, Ag, Sg, Tg, mg, alpha, beta, u)
+            assert e.value.code == zkh.EROUND and "round 0" in str(e.value)
+            # the same through the range gather (A read off the table inverse)
+            Ar = ctx.lu_range_inverse(Sg, low, Tg, beta)
+            with pytest.raises(zkh.ZkhError) as e:
+                ctx.lu_prove(seed_transcript(zkh, "luz")[0], Ar, Sg, Tg, mg, alpha, beta, u)
+            assert e.value.code == zkh.EROUND and "round 0" in str(e.value)
+        else:
+            assert rc == 0
+            got = ctx.lu_prove(st_g, Ag, Sg, Tg, mg, alpha, beta, u)
+            for key in ("ev", "term", "ws"):
+                assert fr_eq(got[key], want[key]), key
+            assert bytes(st_g) == bytes(st_o)
+
+
 def test_lu_mapping(zkh, ctx):
     rng = np.random.default_rng(9)
     low, N = -16, 32

@@ -1060,23 +1060,28 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
 // passes, k_inv_blocks turns the block totals into "all other blocks" products and
 // publishes the grand product G, whose plain inverse the host computes once.  Pass 2 walks
 // each thread's entries backwards.  Zero entries (x + beta = 0) take 2^256, M's identity,
-// in the products and produce 0, the reference's Fermat convention.
+// in the products and produce 0, the reference's Fermat convention; pass 1 sets *zflag when
+// it meets one (the inverse then has a zero entry).
 #define INV_CHK 16
 __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
-                                                  uint32_t* others, uint32_t* blockprod) {
+                                                  uint32_t* others, uint32_t* blockprod, uint32_t* zflag) {
     __shared__ fr_t pre[NT], suf[NT];
     const uint32_t t = threadIdx.x;
     const uint32_t base = blockIdx.x * NT * INV_CHK;
     fr_t run = one_m();
+    bool zero = false;
     for (uint32_t j = 0; j < INV_CHK; j++) {
         uint32_t idx = base + j * NT + t;
         if (idx < n) {
             const fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
-            run = mont_mul(run, fr_is_zero(x) ? one_m() : x);
+            const bool z = fr_is_zero(x);
+            zero = zero || z;
+            run = mont_mul(run, z ? one_m() : x);
             st_fr(alo, ahi, idx, run);
         }
     }
+    if (__ballot(zero) && (t & 63) == 0) atomicOr(zflag, 1u);  // one atomic per wave that met a zero
     pre[t] = run;
     suf[t] = run;
     __syncthreads();
@@ -1099,7 +1104,7 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
 // flag) for the host to invert.  Thread t owns products [t*per, (t+1)*per).
 #define NTI 256
 __global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__ bp, uint32_t nb,
-                                                    uint32_t* others, Publish pub) {
+                                                    uint32_t* others, Publish pub, const uint32_t* zflag) {
     __shared__ fr_t pre[NTI], suf[NTI];
     const uint32_t t = threadIdx.x;
     const uint32_t per = (nb + NTI - 1) / NTI;
@@ -1130,13 +1135,14 @@ __global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__
     }
     if (t == NTI - 1) {
         st_aos(pub.host_out, 0, pre[NTI - 1]);
+        pub.host_out[8] = *zflag;  // pass 1 met a zero entry
         __threadfence_system();
         __hip_atomic_store(pub.host_flag, pub.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, uint32_t* others_blk,
-                       Publish pub) {
-    k_inv_blocks<<<1, NTI, 0, s>>>(blockprod, nb, others_blk, pub);
+                       Publish pub, const uint32_t* zflag) {
+    k_inv_blocks<<<1, NTI, 0, s>>>(blockprod, nb, others_blk, pub, zflag);
 }
 // 1/blockprod[b] = M(others_blk[b], 1/G), 1/(thread total) = M(others[t], 1/blockprod[b]);
 // then each thread walks its entries backwards
@@ -1161,9 +1167,9 @@ __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4*
 }
 uint32_t inv_blocks(uint32_t n) { return (n + NT * INV_CHK - 1) / (NT * INV_CHK); }
 void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
-                      DevPlanes A, uint32_t* others, uint32_t* blockprod) {
+                      DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag) {
     k_inv_pass1<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
-                                             PL_HI(A), others, blockprod);
+                                             PL_HI(A), others, blockprod, zflag);
 }
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
@@ -1307,6 +1313,71 @@ ZDEV void lu_as_inverse(const TabDev& A, const TabDev& S, uint32_t i, uint32_t h
     const fr_t s0 = ld_fr(S.slo, S.shi, i), s1 = ld_fr(S.slo, S.shi, i + h);
     inverse_pair_sums<5>(a0, a1, s0, s1, w, acc);
     SB();
+}
+// First round of a group whose table X is 1/(Y + beta) with no zero entry: x (y + beta) = 1
+// for every pair entry, so the two weighted sums of those products are sum_i eq(i, u) = 1
+// (the host takes them as such) and only w dx dy is formed.  A/S slots: 0 w da ds
+// (x 2^-256), 1 a0, 2 a1.  B/T/m slots: 0 w db dt (x 2^-256), 1..3 m0 b0, m1 b1, dm db
+// (exact, x 1).
+ZDEV void lu_as_first_nz(const TabDev& A, const TabDev& S, uint32_t n, const EqDev& eq, uint32_t lb, uint32_t g,
+                         const Publish& pub, uint4* accl, uint4* acch) {
+    const uint32_t h = n >> 1;
+    LdsAcc<3> acc{accl, acch};
+    acc.zero();
+    for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
+        // every load of the iteration first: one wait for memory per pair
+        const fr_t a0 = ld_fr(A.slo, A.shi, i), a1 = ld_fr(A.slo, A.shi, i + h);
+        const fr_t s0 = ld_fr(S.slo, S.shi, i), s1 = ld_fr(S.slo, S.shi, i + h);
+        const fr_t elo = ld_aos(eq.elo, i & 1023), ehi = ld_aos(eq.ehi, i >> 10);
+        SB();
+        acc.add(1, a0);
+        acc.add(2, a1);
+        const fr_t ds = fr_sub(s1, s0);
+        const fr_t w = mont_mul_ol(elo, ehi);
+        SB();
+        const fr_t wda = mont_mul_ol(w, fr_sub(a1, a0));
+        SB();
+        acc.add(0, mont_mul_ol(wda, ds));
+        SB();
+    }
+    reduce_publish_lds<3>(acc, pub, 0, 0, g, lb);
+}
+ZDEV void lu_btm_first_nz(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const EqDev& eq, uint32_t lb,
+                          uint32_t g, uint32_t ga, const Publish& pub, uint4* accl, uint4* acch) {
+    const uint32_t h = n >> 1;
+    LdsAcc<4> acc{accl, acch};
+    acc.zero();
+    for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
+        // every load of the iteration first: one wait for memory per pair
+        const fr_t b0 = ld_fr(B.slo, B.shi, i), b1 = ld_fr(B.slo, B.shi, i + h);
+        const fr_t t0 = ld_fr(T.slo, T.shi, i), t1 = ld_fr(T.slo, T.shi, i + h);
+        const fr_t elo = ld_aos(eq.elo, i & 1023), ehi = ld_aos(eq.ehi, i >> 10);
+        const fr_t dt = fr_sub(t1, t0);
+        {  // multiplicities are small integers: exact (x 1) by the 32-bit multiply
+            const fr_t m0 = tab_ld(m, i), m1 = tab_ld(m, i + h);
+            SB();
+            int64_t i0, i1;
+            if (fr_int32ish(m0, i0) && fr_int32ish(m1, i1)) {
+                acc.add(1, fr_mul_i64s(b0, i0));
+                acc.add(2, fr_mul_i64s(b1, i1));
+                acc.add(3, fr_mul_i64(fr_sub(b1, b0), i1 - i0));
+            } else {
+                acc.add(1, exact_mul(m0, b0));
+                SB();
+                acc.add(2, exact_mul(m1, b1));
+                SB();
+                acc.add(3, exact_mul(fr_sub(m1, m0), fr_sub(b1, b0)));
+            }
+        }
+        SB();
+        const fr_t w = mont_mul_ol(elo, ehi);
+        SB();
+        const fr_t wdb = mont_mul_ol(w, fr_sub(b1, b0));
+        SB();
+        acc.add(0, mont_mul_ol(wdb, dt));
+        SB();
+    }
+    reduce_publish_lds<4>(acc, pub, 1, ga, g, lb);
 }
 // phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused), one launch whose
 // blocks [0, ga) take the (A, S) group and blocks [ga, ga + gb) the (B, T, m) group,
@@ -1507,6 +1578,34 @@ __global__ __launch_bounds__(NT) void k_lu_phase1(TabDev A, TabDev S, uint32_t n
     constexpr int K = derive ? 3 : 5;
     __shared__ uint4 accl[K * NT], acch[K * NT];
     lu_phase2_as<fold, derive>(A, S, n, vm, beta, eq, pub, blockIdx.x, gridDim.x, accl, acch, inv);
+}
+// the first round of phase 1 when A = 1/(S + beta) has no zero entry (lu_as_first_nz): 24 KiB
+// of accumulators, 6 blocks per CU
+__global__ __launch_bounds__(NT) void k_lu_phase1_first_nz(TabDev A, TabDev S, uint32_t n, EqDev eq, Publish pub) {
+    __shared__ uint4 accl[3 * NT], acch[3 * NT];
+    lu_as_first_nz(A, S, n, eq, blockIdx.x, gridDim.x, pub, accl, acch);
+}
+// the first round of phase 2 when A and B have no zero entry: 32 KiB, 5 blocks per CU
+__global__ __launch_bounds__(NT) void k_lu_phase2_first_nz(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m,
+                                                           uint32_t n, EqDev eq, Publish pub, uint32_t ga,
+                                                           uint32_t gb) {
+    __shared__ uint4 accl[4 * NT], acch[4 * NT];
+    if (blockIdx.x < ga) lu_as_first_nz(A, S, n, eq, blockIdx.x, ga, pub, accl, acch);
+    else lu_btm_first_nz(B, T, m, n, eq, blockIdx.x - ga, gb, ga, pub, accl, acch);
+}
+uint32_t launch_lu_first_nz(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int phase2, EqW eq,
+                            Publish partial, const int32_t* m32) {
+    const EqDev e{eq.elo, eq.ehi, eq.K};
+    if (!phase2) {
+        const uint32_t g = grid_for(n >> 1, NT, 1536);
+        k_lu_phase1_first_nz<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, e, partial);
+        return g;
+    }
+    const uint32_t ga = grid_for(n >> 1, NT, 1280 * 2 / 5), gb = grid_for(n >> 1, NT, 1280 * 3 / 5);
+    TabDev md = tab_dev(m);
+    md.s32 = m32;
+    k_lu_phase2_first_nz<<<ga + gb, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), md, n, e, partial, ga, gb);
+    return ga + gb;
 }
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,

@@ -184,10 +184,12 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
 // other blocks' totals and publishes the grand product G (job 0 of pub); the host computes
 // the plain inverse 1/G once; pass 2 writes the plain inverses into A given inv_total = 1/G.
 uint32_t inv_blocks(uint32_t n);
+// zflag: a device word (zero before pass 1) that pass 1 sets when some S[i] + beta is zero;
+// k_inv_blocks publishes it as word 8 of pub.host_out, after G
 void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
-                      DevPlanes A, uint32_t* others, uint32_t* blockprod);
+                      DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag);
 void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, uint32_t* others_blk,
-                       Publish pub);
+                       Publish pub, const uint32_t* zflag);
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
                       const uint32_t* inv_total_host);
@@ -202,6 +204,12 @@ void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
                           const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host, EqW eq,
                           Publish pub, int inv, int derive);
+// the first (unfolded) round of phase 1 (phase2 = 0: A, S only) or phase 2 when A = 1/(S + beta)
+// and B = 1/(T + beta) have no zero entry: sum w a (s + beta) and sum w b (t + beta) are
+// sum eq = 1 and not formed.  Job 0 (A, S): w da ds (x 2^-256), a0, a1; job 1 (B, T, m):
+// w db dt (x 2^-256), m0 b0, m1 b1, dm db (x 1); m read as int32 when m32 is set.
+uint32_t launch_lu_first_nz(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int phase2, EqW eq,
+                            Publish pub, const int32_t* m32);
 // phase-2 round over A, S, B, T, m as two launches publishing jobs 0 (A, S: 5 sums) and
 // 1 (B, T, m: 6 sums) of `pub` (made for 2 jobs; see kernels.hip)
 // inv_as / inv_btm: A = 1/(S + beta) / B = 1/(T + beta) with that group's fold not owed, as

@@ -368,6 +368,8 @@ struct zkh_tensor {
     // the tensor S of generation inv_of (0: no such knowledge)
     uint64_t inv_of = 0;
     uint32_t inv_beta[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    // an inverse (as inv_of) known to have no zero entry (no S[i] + beta was zero)
+    bool inv_nz = false;
     // set by zkh_lu_range_table: entry j is range_low + min(j, range_len - 1) while gen is
     // range_gen (0: no such knowledge)
     uint64_t range_gen = 0;
@@ -2556,7 +2558,9 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
     return ZKH_OK;
 }
 // A = 1/(S + beta) into planes A (n entries)
-static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, DevPlanes A) {
+// any_zero (when given): whether some S[i] + beta was zero (its inverse entry is 0)
+static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, DevPlanes A,
+                         bool* any_zero = nullptr) {
     int rc = 0;
     uint32_t nb = inv_blocks(n);
     uint32_t* others = (uint32_t*)scratch_slot(c, SL_TMP4, (size_t)nb * 256 * 32, &rc);
@@ -2564,18 +2568,21 @@ static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, De
     uint32_t* bp = (uint32_t*)scratch_slot(c, SL_SMALL, (size_t)nb * 64 + 64, &rc);
     if (rc) return rc;
     uint32_t* others_blk = bp + 8 * (size_t)nb;
+    uint32_t* zflag = bp + 16 * (size_t)nb;  // in the slot's last 64 bytes
     uint32_t bl[8];
     fr_store(beta, bl);
+    HIPCHK(c, hipMemsetAsync(zflag, 0, 4, c->stream));
     Publish pb = make_pub(c, 1);
     {
         ProfScope ps(c, "inv_pass1", (double)n * 64 + (double)nb * 256 * 32);
-        launch_inv_pass1(c->stream, S, n, bl, A, others, bp);
-        launch_inv_blocks(c->stream, bp, nb, others_blk, pb);
+        launch_inv_pass1(c->stream, S, n, bl, A, others, bp, zflag);
+        launch_inv_blocks(c->stream, bp, nb, others_blk, pb, zflag);
     }
     if ((rc = wait_pub(c, pb.seq))) return rc;
     // the grand product G (never zero) -> its plain inverse, once, on the host
     Fr G;
     pub_read(c, 0, 1, &G);
+    if (any_zero) *any_zero = __atomic_load_n(c->pub_host + 8, __ATOMIC_ACQUIRE) != 0;
     uint32_t inv_g[8];
     fr_store(fr_inv(G), inv_g);
     ProfScope ps(c, "inv_pass2", (double)n * 96 + (double)nb * 256 * 32);
@@ -2591,12 +2598,14 @@ extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t be
     if ((rc = as_planes(c, S, SL_TMP0, &p))) return rc;
     zkh_tensor* A;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, S->n, &A))) return rc;
-    if ((S->n && (rc = batch_inverse(c, p, S->n, fr_load(beta), A->planes()))) || (rc = settle(c))) {
+    bool zero = false;
+    if ((S->n && (rc = batch_inverse(c, p, S->n, fr_load(beta), A->planes(), &zero))) || (rc = settle(c))) {
         zkh_tensor_free(A);
         return rc;
     }
     A->inv_of = S->gen;
     memcpy(A->inv_beta, beta, 32);
+    A->inv_nz = !zero;
     *A_out = A;
     return ZKH_OK;
 }
@@ -2629,7 +2638,8 @@ extern "C" int zkh_lu_range_inverse(zkh_ctx* c, const zkh_tensor* S, int32_t low
     };
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, D, &A)) || (rc = tensor_alloc(c, ZKH_KIND_FR, N, &Binv))) return drop(rc);
     // the table's inverse (tlookup.cu:50-62 over T, as zkh_lu_prove takes it), then A read off it
-    if ((rc = batch_inverse(c, Tp, N, fr_load(beta), Binv->planes()))) return drop(rc);
+    bool tzero = false, szero = false;
+    if ((rc = batch_inverse(c, Tp, N, fr_load(beta), Binv->planes(), &tzero))) return drop(rc);
     uint32_t* flags = (uint32_t*)scratch_slot(c, SL_PARTIAL, 256, &rc);
     if (rc) return drop(rc);
     HIPCHK(c, hipMemsetAsync(flags, 0, 4, c->stream));
@@ -2646,12 +2656,15 @@ extern "C" int zkh_lu_range_inverse(zkh_ctx* c, const zkh_tensor* S, int32_t low
     // inversion of S (zkob_rescale.cu:121-123), as zkh_lu_inverse
     if (hf) {
         DevPlanes Sp;
-        if ((rc = as_planes(c, S, SL_TMP0, &Sp)) || (rc = batch_inverse(c, Sp, D, fr_load(beta), A->planes())) ||
-            (rc = settle(c)))
+        if ((rc = as_planes(c, S, SL_TMP0, &Sp)) ||
+            (rc = batch_inverse(c, Sp, D, fr_load(beta), A->planes(), &szero)) || (rc = settle(c)))
             return drop(rc);
     }
     A->inv_of = S->gen;
     memcpy(A->inv_beta, beta, 32);
+    // A is the table inverse's entries (no zero there: none in A) or S's own inverse
+    A->inv_nz = hf ? !szero : !tzero;
+    Binv->inv_nz = !tzero;
     if (c->lu_tinv) zkh_tensor_free(c->lu_tinv);
     c->lu_tinv = Binv;
     c->lu_tinv_of = T->gen;
@@ -2685,7 +2698,8 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
     fr_store(fr_to_mont(fr_load(r)), rm);
     // T_comb = T + r mapped (zkob_glu.cu:156) and its inverse (zkob_glu.cu:168-170)
     launch_axpy(c->stream, st, r, rm, sm, N, Tcomb->planes());
-    if ((rc = batch_inverse(c, Tcomb->planes(), N, fr_load(beta), Binv->planes()))) return drop(rc);
+    bool tzero = false, czero = false;
+    if ((rc = batch_inverse(c, Tcomb->planes(), N, fr_load(beta), Binv->planes(), &tzero))) return drop(rc);
     uint32_t* flags = (uint32_t*)scratch_slot(c, SL_PARTIAL, 256, &rc);
     if (rc) return drop(rc);
     HIPCHK(c, hipMemsetAsync(flags, 0, 4, c->stream));
@@ -2703,10 +2717,13 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
     if (hf & 1u) return drop(fail(c, ZKH_EARG, "lookup witness outside the table"));
     // an entry whose G is not the table's at its index (comb is then no table entry): A by
     // the direct batched inversion of comb (zkob_glu.cu:158-160)
-    if ((hf & 2u) && ((rc = batch_inverse(c, comb->planes(), D, fr_load(beta), A->planes())) || (rc = settle(c))))
+    if ((hf & 2u) && ((rc = batch_inverse(c, comb->planes(), D, fr_load(beta), A->planes(), &czero)) ||
+                      (rc = settle(c))))
         return drop(rc);
     A->inv_of = comb->gen;
     memcpy(A->inv_beta, beta, 32);
+    A->inv_nz = (hf & 2u) ? !czero : !tzero;
+    Binv->inv_nz = !tzero;
     if (c->lu_tinv) zkh_tensor_free(c->lu_tinv);
     c->lu_tinv = Binv;
     c->lu_tinv_of = Tcomb->gen;
@@ -2794,10 +2811,14 @@ static bool lu_phase2_round(uint8_t tr[32], LuState& L, uint32_t r, const Fr sm[
 // n <= ZKH_LU_PERSIST_MAX entries; the block-count rounds at the end run on the host with
 // the exact eq weights.  fin receives the terminals A_f, S_f, B_f, T_f, m_f.
 #define ZKH_LU_PERSIST_MAX 8192u
+// entries per block and table of the logUp and Hadamard persistent loops
+#ifndef ZKH_LH_PLS
+#define ZKH_LH_PLS ZKH_PLS_MAX
+#endif
 static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0, uint32_t n, const DevPlanes src[5],
                              bool fold_as, bool fold_btm, const uint32_t vm[8], const uint32_t beta_l[8],
                              uint32_t* ev_out, uint32_t* ws_out, Fr fin[5]) {
-    const uint32_t lgnb = n > ZKH_PLS_MAX ? ceil_log2(n / ZKH_PLS_MAX) : 0, nb = 1u << lgnb;
+    const uint32_t lgnb = n > ZKH_LH_PLS ? ceil_log2(n / ZKH_LH_PLS) : 0, nb = 1u << lgnb;
     const uint32_t R = ceil_log2(n) - lgnb;  // local rounds
     int rc;
     if ((rc = ensure_ps(c, (size_t)ZKH_PSLOT * (nb + 2)))) return rc;
@@ -2982,7 +3003,8 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     }
     DevPlanes Bw = taken.t ? taken.t->planes() : scratch_planes(c, SL_EO, N, &rc);
     if (rc) return rc;
-    if (!taken.t && (rc = batch_inverse(c, Tc, N, beta, Bw))) return rc;
+    bool b_zero = taken.t && !taken.t->inv_nz;  // B has a zero entry (or may have)
+    if (!taken.t && (rc = batch_inverse(c, Tc, N, beta, Bw, &b_zero))) return rc;
 
     // C = alpha^2 - sum Bv*m (zkob_rescale.cu:136); only the phase-1 rounds (D > N) use it
     Fr bm = kZero;
@@ -3020,6 +3042,9 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     // T: a group's first (unfolded) round then needs two products per pair fewer, its sums
     // 0 and 1 coming as sum e over the nonzero entries (cf: no 2^-256 to undo)
     const bool a_is_inv = A->kind == ZKH_KIND_FR && A->inv_of && A->inv_of == S->gen && !memcmp(A->inv_beta, beta_l, 32);
+    // ... and with no zero entry in A (B) every a (s + beta) (b (t + beta)) is 1: the first
+    // round's weighted sums of those products are sum eq = 1, not formed on the device
+    const bool a_nz = a_is_inv && A->inv_nz, b_nz = !b_zero;
     // a folding round leaves its sums at 1 to the pieces (LuPieces) unless its eq coordinate
     // is 0; inv_u holds 1/u_j, computed while the first round runs
     LuPieces pc;
@@ -3033,6 +3058,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         Publish pb;
         bool cf_a, cf_b;
         bool dv_a, dv_b;  // the group's sums at 1 are left out
+        bool nz;          // first round with no zero in A (and B in phase 2): reduced sums
     };
     // launches round r (reading the previous challenge from vm, or from the relay when vmp
     // is given) and moves the table handles to the folded copies the launch writes
@@ -3044,7 +3070,12 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             pb = make_pub(c, 1);
             l.cf_a = a_is_inv && !as_pending;
             l.dv_a = as_pending && derives(r);
-            {
+            l.nz = l.cf_a && a_nz && !vmp;
+            if (l.nz) {
+                ProfScope ps(c, "lu_phase1", (double)n * 2 * 32);
+                launch_lu_first_nz(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{}, Tab{}, Tab{}, n, 0,
+                                   EqW{eq.elo_d, eq.ehi_d, K}, pb, nullptr);
+            } else {
                 ProfScope ps(c, "lu_phase1", (as_pending ? 3.0 * n : (double)n) * 2 * 32);
                 launch_lu_phase1(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, n, as_pending, vm, vmp, beta_l,
                                  EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.dv_a);
@@ -3061,15 +3092,20 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             const bool dv = as_pending && derives(r);
             l.dv_a = dv;
             l.dv_b = dv && btm_pending;
+            l.nz = l.cf_a && l.cf_b && a_nz && b_nz && !vmp;
             {
                 // bytes each table moves: read n entries, or fold 2n read into n written; m
                 // is read as int32 counts (4 bytes) until its first fold writes its planes
                 const double per = as_pending ? 3.0 * n : (double)n, pbt = btm_pending ? 3.0 * n : (double)n;
                 const double m_bytes = !m_src32 ? pbt * 32 : btm_pending ? 2.0 * n * 4 + (double)n * 32 : (double)n * 4;
                 ProfScope ps(c, "lu_phase2", per * 2 * 32 + pbt * 2 * 32 + m_bytes);
-                launch_lu_phase2(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
-                                 Tab{m_src, mw}, n, as_pending, btm_pending, vm, vmp, beta_l,
-                                 EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b, dv, m_src32);
+                if (l.nz)
+                    launch_lu_first_nz(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
+                                       Tab{m_src, mw}, n, 1, EqW{eq.elo_d, eq.ehi_d, K}, pb, m_src32);
+                else
+                    launch_lu_phase2(c->stream, Tab{a_src, Aw}, Tab{s_src, Sw}, Tab{b_src, Bw}, Tab{t_src, Tw},
+                                     Tab{m_src, mw}, n, as_pending, btm_pending, vm, vmp, beta_l,
+                                     EqW{eq.elo_d, eq.ehi_d, K}, pb, l.cf_a, l.cf_b, dv, m_src32);
             }
             if (as_pending) {
                 a_src = Aw;
@@ -3140,6 +3176,12 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                 qa[1] = eq_piece_q1(pc.Ia, qa[0], ul, inv_u[k - 1]);
                 sa[0] = s[2];
                 sa[1] = fr_sub(pc.Sa, s[2]);
+            } else if (cur.nz) {  // w da ds, a0, a1; sum eq a (s + beta) = sum eq = 1 (no zero in A)
+                pub_read(c, 0, 3, s);
+                qa[0] = qa[1] = kOne;
+                qa[2] = fr_mul(fix1(s[0]), corr);
+                sa[0] = s[1];
+                sa[1] = s[2];
             } else {
                 pub_read(c, 0, 5, s);
                 qa[0] = fr_mul(q_of(s[0], cur.cf_a), corr);
@@ -3159,6 +3201,11 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                 M[0] = fix1(s[2]);
                 M[2] = fix1(s[3]);
                 M[1] = fr_sub(pc.Mb, M[0]);
+            } else if (cur.nz) {  // w db dt, m0 b0, m1 b1, dm db (exact); sum eq b (t + beta) = 1
+                pub_read(c, 1, 4, s);
+                qb[0] = qb[1] = kOne;
+                qb[2] = fr_mul(fix1(s[0]), corr);
+                for (int t = 0; t < 3; t++) M[t] = s[1 + t];
             } else {
                 pub_read(c, 1, 6, s);
                 qb[0] = fr_mul(q_of(s[0], cur.cf_b), corr);
@@ -3641,7 +3688,7 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
                              Fr& s_fin, Fr& u_fin) {
     const bool em = u == nullptr;  // explicit E table
     static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
-    const uint32_t lgnb = sz > ZKH_PLS_MAX ? ceil_log2(sz / ZKH_PLS_MAX) : 0, nb = 1u << lgnb;
+    const uint32_t lgnb = sz > ZKH_LH_PLS ? ceil_log2(sz / ZKH_LH_PLS) : 0, nb = 1u << lgnb;
     const uint32_t R = ceil_log2(sz) - lgnb;  // local rounds
     int rc;
     if ((rc = ensure_ps(c, (size_t)ZKH_PSLOT * (nb + 2)))) return rc;
