@@ -171,7 +171,7 @@ class GluJob:
         S, m = c.lu_mapping(self.G, self.low, self.mapped)
         r = zkh.challenge(st)
         beta = zkh.challenge(st)
-        comb, Tcomb, A = c.lu_tuple_inverse(self.G, self.low, self.T, self.mapped, r, beta)
+        comb, Tcomb, A = c.lu_tuple_inverse(self.G, self.low, self.T, self.mapped, r, beta, S=S)
         zkh.absorb(st, "com_A", self.comA)
         alpha = zkh.challenge(st)
         u = zkh.challenges(st, self.logD)

@@ -258,10 +258,14 @@ int zkh_lu_range_inverse(zkh_ctx* ctx, const zkh_tensor* S, int32_t low, const z
  * 1/(T_comb+beta) wherever T[j] == G[i] (comb[i] is then T_comb[j]), with a direct inversion
  * of comb if some entry is not; the table inverse stays with the context, and the next
  * zkh_lu_prove on this T_comb and beta uses it instead of inverting T_comb again (retained
- * as zkh_lu_range_inverse's).  ZKH_EARG if an index falls outside [0, N) (as zkh_lu_mapping). */
+ * as zkh_lu_range_inverse's).  ZKH_EARG if an index falls outside [0, N) (as zkh_lu_mapping).
+ * S (may be NULL): the S that zkh_lu_mapping returned for this G, low and mapped; comb then
+ * reads S[i] in order instead of mapped[j] at random (the same values); ZKH_EARG for any
+ * other tensor. */
 int zkh_lu_tuple_inverse(zkh_ctx* ctx, const zkh_tensor* G, int32_t low, const zkh_tensor* T,
-                         const zkh_tensor* mapped, const uint32_t r[8], const uint32_t beta[8],
-                         zkh_tensor** comb_out, zkh_tensor** Tcomb_out, zkh_tensor** A_out);
+                         const zkh_tensor* mapped, const zkh_tensor* S, const uint32_t r[8],
+                         const uint32_t beta[8], zkh_tensor** comb_out, zkh_tensor** Tcomb_out,
+                         zkh_tensor** A_out);
 /* FS lookup recursion, zkob_rescale.cu:132-146 with fs_phase1/fs_phase2
  * (zkob_lookup.cuh:143-198): from Bv = 1/(T+beta) through the rounds (absorbing
  * "p0".."p3" each) to absorbing "A_f","S_f","m_f".  A, S: D entries; T, m: N entries;

@@ -219,7 +219,7 @@ def _glu(zkh, ctx, cfg, seed, parts=("lookup", "hadamard"), fused=False):
     r = chal_both(zkh, st_g, st_o)
     beta = chal_both(zkh, st_g, st_o)
     if fused:
-        comb_g, tcomb_g, Ag = ctx.lu_tuple_inverse(Gg, low, Tg, mapped, r, beta)
+        comb_g, tcomb_g, Ag = ctx.lu_tuple_inverse(Gg, low, Tg, mapped, r, beta, S=Sg)
     else:
         comb_g = ctx.axpy(Gg, r, Sg)
         tcomb_g = ctx.axpy(Tg, r, mapped)

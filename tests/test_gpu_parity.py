@@ -691,14 +691,30 @@ def test_lu_tuple_inverse(zkh, ctx, D, N, ln, gkind):
     the definition (A (comb + beta) = 1)."""
     t = tuple_case(D, N, ln, D + N + ln)
     G = ctx.from_i32(t["G"]) if gkind == "i32" else ctx.from_fr(C.ints_to_fr([int(g) for g in t["G"]]))
-    comb, Tcomb, A = ctx.lu_tuple_inverse(G, t["low"], ctx.range_table(t["low"], ln, N), ctx.from_i32(t["mapped"]),
-                                          t["r"], t["beta"])
-    assert fr_eq(comb.to_fr(), t["comb"])
-    assert fr_eq(Tcomb.to_fr(), t["Tcomb"])
-    got = A.to_fr()
-    assert C.check_inverse(t["comb"], got, t["beta"]) == 0
-    if D <= 1 << 14:
-        assert fr_eq(got, C.lu_inverse(t["comb"], t["beta"]))
+    mapped = ctx.from_i32(t["mapped"])
+    S, _ = ctx.lu_mapping(G, t["low"], mapped)
+    for s_in in (None, S):  # comb from mapped[j], or from the mapping's S read in order
+        comb, Tcomb, A = ctx.lu_tuple_inverse(G, t["low"], ctx.range_table(t["low"], ln, N), mapped, t["r"], t["beta"],
+                                              S=s_in)
+        assert fr_eq(comb.to_fr(), t["comb"])
+        assert fr_eq(Tcomb.to_fr(), t["Tcomb"])
+        got = A.to_fr()
+        assert C.check_inverse(t["comb"], got, t["beta"]) == 0
+        if D <= 1 << 14:
+            assert fr_eq(got, C.lu_inverse(t["comb"], t["beta"]))
+
+
+def test_lu_tuple_inverse_rejects_other_s(zkh, ctx):
+    """S must be zkh_lu_mapping's output for the same G, low and mapped."""
+    t = tuple_case(4096, 1024, 1024, 77)
+    G, mapped = ctx.from_i32(t["G"]), ctx.from_i32(t["mapped"])
+    T = ctx.range_table(t["low"], 1024, 1024)
+    S, _ = ctx.lu_mapping(G, t["low"], mapped)
+    G2 = ctx.from_i32(t["G"])  # same values, another tensor
+    for args in ((G2, t["low"], S), (G, t["low"] + 1, S), (G, t["low"], ctx.from_i32(np.zeros(4096, np.int32)))):
+        with pytest.raises(zkh.ZkhError) as e:
+            ctx.lu_tuple_inverse(args[0], args[1], T, mapped, t["r"], t["beta"], S=args[2])
+        assert e.value.code == zkh.EARG
 
 
 @pytest.mark.parametrize("D,N", [(1 << 16, 1 << 16), (1 << 16, 1 << 14)])

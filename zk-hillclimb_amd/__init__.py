@@ -84,7 +84,7 @@ def lib():
         L.zkh_lu_mapping.argtypes = [vp, vp, i32, vp, ctypes.POINTER(vp), ctypes.POINTER(vp)]
         L.zkh_lu_inverse.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
         L.zkh_lu_range_inverse.argtypes = [vp, vp, i32, vp, vp, ctypes.POINTER(vp)]
-        L.zkh_lu_tuple_inverse.argtypes = [vp, vp, i32, vp, vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp),
+        L.zkh_lu_tuple_inverse.argtypes = [vp, vp, i32, vp, vp, vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp),
                                            ctypes.POINTER(vp)]
         L.zkh_lu_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -469,13 +469,14 @@ class Context:
         beta = _frs(beta, 1)
         return self._new(lib().zkh_lu_range_inverse, S.h, int(low), T.h, _p(beta))
 
-    def lu_tuple_inverse(self, G, low, T, mapped, r, beta):
+    def lu_tuple_inverse(self, G, low, T, mapped, r, beta, S=None):
         """(comb, T_comb, A) = (G + r mapped[G - low], T + r mapped, 1/(comb + beta)) for int32
-        G, T, mapped; the table inverse goes on to the lu_prove on T_comb and beta."""
+        G, T, mapped; the table inverse goes on to the lu_prove on T_comb and beta.  S: the
+        lu_mapping output for this G (comb then reads it in order)."""
         r, beta = _frs(r, 1), _frs(beta, 1)
         hs = [ctypes.c_void_p() for _ in range(3)]
-        self._chk(lib().zkh_lu_tuple_inverse(self.h, G.h, int(low), T.h, mapped.h, _p(r), _p(beta),
-                                             *[ctypes.byref(h) for h in hs]))
+        self._chk(lib().zkh_lu_tuple_inverse(self.h, G.h, int(low), T.h, mapped.h, S.h if S is not None else None,
+                                             _p(r), _p(beta), *[ctypes.byref(h) for h in hs]))
         return tuple(Tensor(self, h) for h in hs)
 
     def lu_prove(self, st, A, S, T, m, alpha, beta, u):

@@ -92,7 +92,7 @@ int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& 
     // comb = G + r S, T_comb = T + r mapped and A = 1/(comb + beta) (zkob_glu.cu:155-160),
     // A through the table inverse, which zkh_lu_prove then takes over (zkob_glu.cu:168-170)
     chk(zkh_lu_range_table(g_ctx, low, len, N, &T.t), "table");
-    chk(zkh_lu_tuple_inverse(g_ctx, Gp.t, low, T.t, tmap.t, r.data(), beta.data(), &comb.t, &Tcomb.t, &A.t),
+    chk(zkh_lu_tuple_inverse(g_ctx, Gp.t, low, T.t, tmap.t, Sp.t, r.data(), beta.data(), &comb.t, &Tcomb.t, &A.t),
         "comb, T_comb and inverses");
     chk(zkh_commit(g_ctx, g.g, A.t, &cA.g), "commit A");
     const std::vector<uint32_t> hA = to_host(cA.g);

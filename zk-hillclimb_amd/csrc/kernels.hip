@@ -987,8 +987,10 @@ void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
 // *flags |= 1 for j outside [0, N) (nothing written at i), |= 2 for T[j] != G[i] (A[i] left
 // for the caller's direct inversion).  tlen > 0: T is the range table low + min(j, tlen - 1),
 // so T[j] == G[i] iff G[i] - low is the integer j < tlen, and T is not read.  Without Comb
-// (a plain range lookup: A = 1/(G + beta)) neither mapped nor comb is touched.
-template <bool Comb, typename LG, typename LT, typename LM>
+// (a plain range lookup: A = 1/(G + beta)) neither mapped nor comb is touched.  SeqS: the
+// loader `mapped` is the caller's S = mapped[(G - low).limb0] itself, read at i (sequential)
+// instead of mapped at j (a random 4-byte read per entry).
+template <bool Comb, bool SeqS, typename LG, typename LT, typename LM>
 __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tlen, LM mapped, uint32_t N, fr_t rm,
                                   fr_t r,
                                   const uint4* __restrict__ blo, const uint4* __restrict__ bhi, uint4* clo,
@@ -1002,7 +1004,7 @@ __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tle
             f |= 1u;
             continue;
         }
-        if constexpr (Comb) st_fr(clo, chi, i, fr_add(g, scale_of(rm, r, mapped, j)));
+        if constexpr (Comb) st_fr(clo, chi, i, fr_add(g, scale_of(rm, r, mapped, SeqS ? i : j)));
         bool same = true;
         if (tlen) {
             same = j < tlen;
@@ -1023,15 +1025,21 @@ __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tle
     if ((any1 | any2) && (threadIdx.x & 63) == 0) atomicOr(flags, (any1 ? 1u : 0u) | (any2 ? 2u : 0u));
 }
 void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
-                            Src mapped, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host, DevPlanes Binv,
-                            DevPlanes comb, DevPlanes A, uint32_t* flags) {
+                            Src mapped, int seq_s, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host,
+                            DevPlanes Binv, DevPlanes comb, DevPlanes A, uint32_t* flags) {
     const fr_t low = to_fr(low_host), r = to_fr(r_host), rm = to_fr(r_m_host);
+    const uint32_t g = grid_for(n, NT, 8192);
     with_loader(G, [&](auto lg) {
         with_loader(T, [&](auto lt) {
             with_loader(mapped, [&](auto lm) {
-                k_lu_tuple_gather<true><<<grid_for(n, NT, 8192), NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
-                                                                        PL_HI(Binv), PL_LO(comb), PL_HI(comb),
-                                                                        PL_LO(A), PL_HI(A), flags);
+                if (seq_s)
+                    k_lu_tuple_gather<true, true><<<g, NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
+                                                                    PL_HI(Binv), PL_LO(comb), PL_HI(comb), PL_LO(A),
+                                                                    PL_HI(A), flags);
+                else
+                    k_lu_tuple_gather<true, false><<<g, NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
+                                                                     PL_HI(Binv), PL_LO(comb), PL_HI(comb), PL_LO(A),
+                                                                     PL_HI(A), flags);
             });
         });
     });
@@ -1041,7 +1049,7 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
     const fr_t low = to_fr(low_host);
     with_loader(S, [&](auto ls) {
         with_loader(T, [&](auto lt) {
-            k_lu_tuple_gather<false><<<grid_for(n, NT, 8192), NT, 0, s>>>(
+            k_lu_tuple_gather<false, false><<<grid_for(n, NT, 8192), NT, 0, s>>>(
                 ls, n, low, lt, tlen, LdI32{nullptr}, N, fr_t{}, fr_t{}, PL_LO(Binv), PL_HI(Binv), nullptr, nullptr,
                 PL_LO(A), PL_HI(A), flags);
         });

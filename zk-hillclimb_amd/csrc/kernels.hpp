@@ -170,10 +170,11 @@ void launch_lu_map_to_i32(hipStream_t s, Src S, uint32_t n, const uint32_t* low_
                           uint32_t N, int32_t* out);
 // tuple lookup, j = (G[i] - low).limb0: comb[i] = G[i] + r mapped[j]; A[i] = Binv[j] where
 // T[j] == G[i]; *flags |= 1 (j >= N) / 2 (T[j] != G[i]); r plain and in Montgomery form;
-// tlen > 0: T is the range table low + min(j, tlen - 1) (not read)
+// tlen > 0: T is the range table low + min(j, tlen - 1) (not read); seq_s: `mapped` is
+// S = mapped[(G - low).limb0] (n entries), read at i
 void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
-                            Src mapped, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host, DevPlanes Binv,
-                            DevPlanes comb, DevPlanes A, uint32_t* flags);
+                            Src mapped, int seq_s, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host,
+                            DevPlanes Binv, DevPlanes comb, DevPlanes A, uint32_t* flags);
 // the same for a plain range lookup: A[i] = Binv[j] (j = (S[i] - low).limb0) where T[j] == S[i]
 void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
                             uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags);

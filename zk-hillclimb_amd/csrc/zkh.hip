@@ -370,6 +370,10 @@ struct zkh_tensor {
     uint32_t inv_beta[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     // an inverse (as inv_of) known to have no zero entry (no S[i] + beta was zero)
     bool inv_nz = false;
+    // set by zkh_lu_mapping on its S: S[i] = mapped[(G[i] - low).limb0] for the tensors G and
+    // mapped of generations map_G, map_mapped (0: no such knowledge)
+    uint64_t map_G = 0, map_mapped = 0;
+    int32_t map_low = 0;
     // set by zkh_lu_range_table: entry j is range_low + min(j, range_len - 1) while gen is
     // range_gen (0: no such knowledge)
     uint64_t range_gen = 0;
@@ -2553,6 +2557,9 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
         zkh_tensor_free(so);
         return rc;
     }
+    so->map_G = S_in->gen;
+    so->map_mapped = mapped->gen;
+    so->map_low = low;
     *S_out = so;
     *m_out = m;
     return ZKH_OK;
@@ -2673,17 +2680,21 @@ extern "C" int zkh_lu_range_inverse(zkh_ctx* c, const zkh_tensor* S, int32_t low
     return ZKH_OK;
 }
 extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low, const zkh_tensor* T,
-                                    const zkh_tensor* mapped, const uint32_t r[8], const uint32_t beta[8],
-                                    zkh_tensor** comb_out, zkh_tensor** Tcomb_out, zkh_tensor** A_out) {
+                                    const zkh_tensor* mapped, const zkh_tensor* S, const uint32_t r[8],
+                                    const uint32_t beta[8], zkh_tensor** comb_out, zkh_tensor** Tcomb_out,
+                                    zkh_tensor** A_out) {
     if (!c || !G || !T || !mapped || !r || !beta || !comb_out || !Tcomb_out || !A_out)
         return fail(c, ZKH_EARG, "null argument");
     const uint32_t D = G->n, N = T->n;
     if (!N || mapped->n != N) return fail(c, ZKH_EARG, "T and mapped differ in size or are empty");
+    if (S && (S->n != D || S->map_G != G->gen || S->map_mapped != mapped->gen || S->map_low != low))
+        return fail(c, ZKH_EARG, "S is not zkh_lu_mapping's output for this G, low and mapped");
     if (!fr_is_canonical(r) || !fr_is_canonical(beta)) return fail(c, ZKH_EARG, "non-canonical r or beta");
     HIPCHK(c, hipSetDevice(c->device));
     int rc = 0;
-    Src sg, st, sm;
-    if ((rc = src_of(c, G, SL_TMP0, &sg)) || (rc = src_of(c, T, SL_TMP1, &st)) || (rc = src_of(c, mapped, SL_TMP2, &sm)))
+    Src sg, st, sm, ss{};
+    if ((rc = src_of(c, G, SL_TMP0, &sg)) || (rc = src_of(c, T, SL_TMP1, &st)) || (rc = src_of(c, mapped, SL_TMP2, &sm)) ||
+        (S && (rc = src_of(c, S, SL_TMP3, &ss))))
         return rc;
     zkh_tensor *comb = nullptr, *Tcomb = nullptr, *A = nullptr, *Binv = nullptr;
     auto drop = [&](int code) {
@@ -2706,12 +2717,13 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
     uint32_t hf = 0;
     if (D) {
         ProfScope ps(c, "lu_tuple_gather", (double)D * (4 + 4 + 4 + 32 + 32 + 32));
+        // comb from the mapping's S when the caller has it (read in order), else mapped[j]
         uint32_t lowl[8];
         fr_store(fr_from_i64(low), lowl);
         // a range table at this low: T[j] == G[i] iff G[i] - low is j < len, read from G alone
         const uint32_t tlen = range_shortcut_len(T, low);
-        launch_lu_tuple_gather(c->stream, sg, D, lowl, st, tlen, sm, N, r, rm, Binv->planes(), comb->planes(),
-                               A->planes(), flags);
+        launch_lu_tuple_gather(c->stream, sg, D, lowl, st, tlen, S ? ss : sm, S != nullptr, N, r, rm, Binv->planes(),
+                               comb->planes(), A->planes(), flags);
     }
     if ((rc = settle(c, flags, &hf))) return drop(rc);
     if (hf & 1u) return drop(fail(c, ZKH_EARG, "lookup witness outside the table"));
