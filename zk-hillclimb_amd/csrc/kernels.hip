@@ -1627,6 +1627,208 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
     else k_lu_phase1<0, 0><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, vmp, beta, e, partial, inv);
     return g;
 }
+// ------------------------------------------------------------------------------------
+// Small folding rounds, one pair's products spread over the block's lanes
+// ------------------------------------------------------------------------------------
+// Below about 2^17 pairs a folding round is bound by the chain of dependent Montgomery
+// products each thread runs for its pair (13 in the (B, T, m) group of logUp phase 2, 9 in
+// the eq-form Hadamard), not by the device's product rate.  These kernels give each block
+// a run of P pairs and split the round into levels of independent products that every lane
+// of the block shares: (1) the folds of the tables' pair entries and the eq weight, (2) the
+// weighted differences, (3) the products that are summed.  Each level's results go to LDS
+// rows; one wave per sum adds its row.  The products, their operands and their order are
+// those of k_lu_phase2<1, 1, 1> / k_hp_eq_round<1> / k_hp_round_ones<1> (derive form), so
+// the sums, the folded tables and the Publish layout are the same; the critical path is
+// three or two products instead of a pair's whole chain.
+#define NTW 512  // threads of a wide round block (8 waves)
+// rows of P field elements in LDS, limb-quad planes
+template <uint32_t P>
+struct Rows {
+    uint4* lo;
+    uint4* hi;
+    ZDEV fr_t ld(uint32_t r, uint32_t p) const { return ld_fr(lo + r * P, hi + r * P, p); }
+    ZDEV void st(uint32_t r, uint32_t p, const fr_t& x) const { st_fr(lo + r * P, hi + r * P, p, x); }
+};
+// The block's sums (wave w < nsum holds sum w of the block in lane 0, after fr_wave_sum)
+// go to the partials of their jobs; the last block adds every block's partials and
+// publishes all jobs at once.  Sum w belongs to job jw(w) as its entry kw(w) of K(jw)
+// (K = {k0, k1}, k1 = 0 for one job); job j's block b partial is part[(j g + b) K_j + k],
+// as reduce_publish_lds lays out two jobs of g blocks each.
+ZDEV void wide_publish(const fr_t& bsum, uint32_t nsum, uint32_t k0, const Publish& P, uint32_t* s_last) {
+    const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63, g = gridDim.x, b = blockIdx.x;
+    const uint32_t k1 = nsum - k0;
+    auto slot = [&](uint32_t w, uint32_t blk) { return w < k0 ? blk * k0 + w : (g + blk) * k1 + (w - k0); };
+    if (wv < nsum && lane == 0) st_aos(P.part, slot(wv, b), bsum);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        *s_last = atomicAdd(&P.counter[0], 1u) == g - 1;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    __threadfence();
+    if (wv < nsum) {
+        fr_t t = fr_zero();
+        for (uint32_t q = lane; q < g; q += 64) t = fr_add(t, ld_aos(P.part, slot(wv, q)));
+        t = fr_wave_sum(t);
+        if (lane == 0) st_aos(P.host_out, wv < k0 ? wv : k1 + (wv - k0), t);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence_system();
+        P.counter[0] = 0;
+        __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+// sum of row r over the block's np entries, by wave (lane-strided, then the wave's tree)
+template <uint32_t P>
+ZDEV fr_t wide_row_sum(const Rows<P>& R, uint32_t r, uint32_t np) {
+    fr_t acc = fr_zero();
+    for (uint32_t p = threadIdx.x & 63; p < np; p += 64) acc = fr_add(acc, R.ld(r, p));
+    return fr_wave_sum(acc);
+}
+#ifndef LUW_P
+#define LUW_P 64
+#endif
+// logUp phase 2, both groups folding, derived sums (lu_phase2_as / lu_phase2_btm derive):
+// rows 0..9 the folded a0 a1 s0 s1 b0 b1 t0 t1 m0 m1, 10 W, 11..14 W a0, W da, W b0, W db,
+// 15 m0 b0, 16 dm db, 17..20 W a0 (s0 + beta), W da ds, W b0 (t0 + beta), W db dt.
+// Job 0 sums: rows 17, 18, 0; job 1: rows 19, 20, 15, 16.
+__global__ __launch_bounds__(NTW) void k_lu_phase2_wide(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m, uint32_t n,
+                                                       fr_t vm, const uint32_t* vmp, fr_t beta, EqDev eq,
+                                                       Publish pub) {
+    if (!relayed_vm(vmp, vm)) return;
+    constexpr uint32_t P = LUW_P;
+    __shared__ uint4 rlo[21 * P], rhi[21 * P];
+    __shared__ uint32_t s_last;
+    const Rows<P> R{rlo, rhi};
+    const uint32_t h = n >> 1, np = h < P ? h : P, base = blockIdx.x * P;
+    for (uint32_t q = threadIdx.x; q < 11 * np; q += NTW) {  // level 1
+        const uint32_t k = q / np, p = q - k * np, i = base + p;
+        if (k == 10) {
+            R.st(10, p, eq_w(eq, i));
+            continue;
+        }
+        const uint32_t tt = k >> 1, e = i + (k & 1) * h;
+        const TabDev t = tt == 0 ? A : tt == 1 ? S : tt == 2 ? B : tt == 3 ? T : m;
+        const fr_t v = tab_fold_at(t, e, n, vm);
+        st_fr(t.dlo, t.dhi, e, v);
+        R.st(k, p, v);
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < 6 * np; q += NTW) {  // level 2
+        const uint32_t k = q / np, p = q - k * np;
+        fr_t x, y;
+        if (k < 4) {
+            x = R.ld(10, p);
+            const uint32_t r0 = k < 2 ? 0 : 4;  // a or b
+            y = (k & 1) ? fr_sub(R.ld(r0 + 1, p), R.ld(r0, p)) : R.ld(r0, p);
+        } else if (k == 4) {
+            x = R.ld(8, p);
+            y = R.ld(4, p);
+        } else {
+            x = fr_sub(R.ld(9, p), R.ld(8, p));
+            y = fr_sub(R.ld(5, p), R.ld(4, p));
+        }
+        R.st(11 + k, p, mont_mul_ol(x, y));
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < 4 * np; q += NTW) {  // level 3
+        const uint32_t k = q / np, p = q - k * np;
+        const uint32_t r0 = k < 2 ? 2 : 6;  // s or t
+        const fr_t x = R.ld(11 + k, p);
+        const fr_t y = (k & 1) ? fr_sub(R.ld(r0 + 1, p), R.ld(r0, p)) : fr_add(R.ld(r0, p), beta);
+        R.st(17 + k, p, mont_mul_ol(x, y));
+    }
+    __syncthreads();
+    const uint32_t wv = threadIdx.x >> 6;
+    fr_t bs = fr_zero();
+    if (wv < 7) {
+        const uint32_t row = wv == 0 ? 17 : wv == 1 ? 18 : wv == 2 ? 0 : wv == 3 ? 19 : wv == 4 ? 20 : wv == 5 ? 15 : 16;
+        bs = wide_row_sum<P>(R, row, np);
+    }
+    wide_publish(bs, 7, 3, pub, &s_last);
+}
+#ifndef HPW_P
+#define HPW_P 128
+#endif
+// eq-form Hadamard, folding, derived sums (k_hp_eq_round<1>): rows 0..3 the folded s0 s1 u0
+// u1, 4 W, 5 W s0, 6 W ds, 7 W s0 u0, 8 W ds du; sums rows 7, 8
+__global__ __launch_bounds__(NTW) void k_hp_eq_round_wide(TabDev S, TabDev U, uint32_t n, fr_t vm, const uint32_t* vmp,
+                                                         EqDev eq, Publish pub) {
+    if (!relayed_vm(vmp, vm)) return;
+    constexpr uint32_t P = HPW_P;
+    __shared__ uint4 rlo[9 * P], rhi[9 * P];
+    __shared__ uint32_t s_last;
+    const Rows<P> R{rlo, rhi};
+    const uint32_t h = n >> 1, np = h < P ? h : P, base = blockIdx.x * P;
+    for (uint32_t q = threadIdx.x; q < 5 * np; q += NTW) {
+        const uint32_t k = q / np, p = q - k * np, i = base + p;
+        if (k == 4) {
+            R.st(4, p, eq_w(eq, i));
+            continue;
+        }
+        const TabDev t = k < 2 ? S : U;
+        const uint32_t e = i + (k & 1) * h;
+        const fr_t v = tab_fold_at(t, e, n, vm);
+        st_fr(t.dlo, t.dhi, e, v);
+        R.st(k, p, v);
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < 2 * np; q += NTW) {
+        const uint32_t k = q / np, p = q - k * np;
+        const fr_t y = k ? fr_sub(R.ld(1, p), R.ld(0, p)) : R.ld(0, p);
+        R.st(5 + k, p, mont_mul_ol(R.ld(4, p), y));
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < 2 * np; q += NTW) {
+        const uint32_t k = q / np, p = q - k * np;
+        const fr_t y = k ? fr_sub(R.ld(3, p), R.ld(2, p)) : R.ld(2, p);
+        R.st(7 + k, p, mont_mul_ol(R.ld(5 + k, p), y));
+    }
+    __syncthreads();
+    const uint32_t wv = threadIdx.x >> 6;
+    fr_t bs = fr_zero();
+    if (wv < 2) bs = wide_row_sum<P>(R, 7 + wv, np);
+    wide_publish(bs, 2, 2, pub, &s_last);
+}
+// Hadamard with U = 1, folding, derived sums (k_hp_round_ones<1>): rows 0..3 the folded e0
+// e1 s0 s1, 4 e0 s0, 5 de ds; sums rows 4, 5
+__global__ __launch_bounds__(NTW) void k_hp_ones_wide(TabDev E, TabDev S, uint32_t n, fr_t vm, const uint32_t* vmp,
+                                                     Publish pub) {
+    if (!relayed_vm(vmp, vm)) return;
+    constexpr uint32_t P = HPW_P;
+    __shared__ uint4 rlo[6 * P], rhi[6 * P];
+    __shared__ uint32_t s_last;
+    const Rows<P> R{rlo, rhi};
+    const uint32_t h = n >> 1, np = h < P ? h : P, base = blockIdx.x * P;
+    for (uint32_t q = threadIdx.x; q < 4 * np; q += NTW) {
+        const uint32_t k = q / np, p = q - k * np, i = base + p;
+        const TabDev t = k < 2 ? E : S;
+        const uint32_t e = i + (k & 1) * h;
+        const fr_t v = tab_fold_at(t, e, n, vm);
+        st_fr(t.dlo, t.dhi, e, v);
+        R.st(k, p, v);
+    }
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < 2 * np; q += NTW) {
+        const uint32_t k = q / np, p = q - k * np;
+        const fr_t x = k ? fr_sub(R.ld(1, p), R.ld(0, p)) : R.ld(0, p);
+        const fr_t y = k ? fr_sub(R.ld(3, p), R.ld(2, p)) : R.ld(2, p);
+        R.st(4 + k, p, mont_mul_ol(x, y));
+    }
+    __syncthreads();
+    const uint32_t wv = threadIdx.x >> 6;
+    fr_t bs = fr_zero();
+    if (wv < 2) bs = wide_row_sum<P>(R, 4 + wv, np);
+    wide_publish(bs, 2, 2, pub, &s_last);
+}
+// the wide kernels take rounds of at most 2^ZKH_WIDE_LG pairs
+#ifndef ZKH_WIDE_LG
+#define ZKH_WIDE_LG 15
+#endif
+static bool wide_round(uint32_t n) { return (n >> 1) <= (1u << ZKH_WIDE_LG); }
+
 // per-thread accumulator slots of a phase-2 launch: the larger group's
 template <int fold_as, int fold_btm, int derive>
 constexpr int lu2_slots() {
@@ -1654,6 +1856,11 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
     const TabDev a = tab_dev(A), sd = tab_dev(S), b = tab_dev(B), t = tab_dev(T);
     TabDev md = tab_dev(m);
     md.s32 = m32;
+    if (fold_as && fold_btm && derive && wide_round(n)) {
+        const uint32_t gw = ((n >> 1) + LUW_P - 1) / LUW_P;
+        k_lu_phase2_wide<<<gw, NTW, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial);
+        return gw;
+    }
     const uint32_t g = ga + gb;
 #define LU2(FA, FB, DV) k_lu_phase2<FA, FB, DV><<<g, NT, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial, ga, gb, inv_as, inv_btm)
     if (fold_as && fold_btm) {
@@ -1771,6 +1978,11 @@ uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold,
                               const uint32_t* vmp, Publish partial, int derive, int s_int) {
     uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
+    if (fold && derive && wide_round(n)) {
+        const uint32_t gw = ((n >> 1) + HPW_P - 1) / HPW_P;
+        k_hp_ones_wide<<<gw, NTW, 0, s>>>(tab_dev(E), tab_dev(S), n, vm, vmp, partial);
+        return gw;
+    }
     if (fold && derive) k_hp_round_ones<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, 0);
     else k_hp_round_ones<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, s_int);
     return g;
@@ -1891,6 +2103,11 @@ uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
     TabDev sd = tab_dev(S), ud = tab_dev(U);
     sd.s32 = s32;
     ud.s32 = u32;
+    if (fold && derive && wide_round(n)) {
+        const uint32_t gw = ((n >> 1) + HPW_P - 1) / HPW_P;
+        k_hp_eq_round_wide<<<gw, NTW, 0, s>>>(sd, ud, n, vm, vmp, e, partial);
+        return gw;
+    }
     if (fold && derive) k_hp_eq_round<1><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
     else k_hp_eq_round<0><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
     return g;
@@ -2601,10 +2818,9 @@ ZDEV bool persist_wait(const uint32_t* cmd, uint32_t nq, uint32_t want, uint32_t
 }
 // wave 0: words[0 .. nw) of pub (LDS) as quads with seq into slot (lanes < ceil(nw/3))
 ZDEV void persist_publish(uint32_t* slot, const uint32_t* pub, uint32_t nw, uint32_t seq) {
-    const uint32_t lane = threadIdx.x & 63;
-    if (lane * 3 < nw) {
-        const uint32_t b = 3 * lane;
-        st_quad_sys(slot + 4 * lane, make_uint4(seq, pub[b], b + 1 < nw ? pub[b + 1] : 0u, b + 2 < nw ? pub[b + 2] : 0u));
+    for (uint32_t qd = threadIdx.x & 63; qd * 3 < nw; qd += 64) {
+        const uint32_t b = 3 * qd;
+        st_quad_sys(slot + 4 * qd, make_uint4(seq, pub[b], b + 1 < nw ? pub[b + 1] : 0u, b + 2 < nw ? pub[b + 2] : 0u));
     }
 }
 // completion flag of a stream (the host's settle): the value of *word (when given) to
@@ -2643,9 +2859,9 @@ static_assert(2 * ZKH_PLS_MAX <= NTP, "the double fold takes one product per thr
 // command), and the low words of both per message s < 14 into words ZKH_PSTAMP + 4 + 2s
 // (publication of message s) and ZKH_PSTAMP + 5 + 2(s - 1) (receipt of command s - 1); the
 // host reads the per-message words after the kernel has ended
-ZDEV void persist_stamp(uint32_t* slot, uint32_t s, uint64_t t_cmd) {
+ZDEV void persist_stamp(uint32_t* slot, uint32_t s, uint64_t t_cmd, uint32_t stamp = ZKH_PSTAMP) {
     const uint64_t now = wall_clock64();
-    uint32_t* st = slot + ZKH_PSTAMP;
+    uint32_t* st = slot + stamp;
     st[0] = (uint32_t)now;
     st[1] = (uint32_t)(now >> 32);
     st[2] = (uint32_t)t_cmd;
@@ -2836,6 +3052,19 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
         __syncthreads();
     }
 }
+// Value at point pt = 3 a + b of {0, 1, inf}^2 of the bilinear function of a cell whose
+// corners are X[c + (2 y1 + y2) q] (inf: the difference along that axis)
+ZDEV fr_t pt_val(const uint4* lo, const uint4* hi, uint32_t c, uint32_t q, uint32_t pt) {
+    const uint32_t a = pt / 3, b = pt - 3 * a;
+    auto along2 = [&](uint32_t y1) {
+        const uint32_t o = c + 2 * y1 * q;
+        if (b == 0) return ld_fr(lo, hi, o);
+        if (b == 1) return ld_fr(lo, hi, o + q);
+        return fr_sub(ld_fr(lo, hi, o + q), ld_fr(lo, hi, o));
+    };
+    if (a < 2) return along2(a);
+    return fr_sub(along2(1), along2(0));
+}
 // Persistent Hadamard rounds (see HpPersist).  Eq mode: the eq weight of a local pair k is
 // the same in every round (g = block + nb*k; only the host's correction changes), so
 // W[k] = eq_w(g) is formed once while the tables load.  Per round, with h = m/2 pairs, two
@@ -2849,7 +3078,7 @@ __global__ __launch_bounds__(NTP) void k_zkip_persist(ZkipPersist P) {
 // (eq mode: W, WS, WD, -, P[0..3]; E mode: Q[0..3], P[0..3]).
 __global__ __launch_bounds__(NTP) void k_hp_persist(HpPersist P) {
     extern __shared__ uint4 zl[];
-    __shared__ uint32_t sok, pubw[ZKH_HP_MSG], sxw[9];
+    __shared__ uint32_t sok, pubw[ZKH_HP_MSG2], sxw[33];
     const uint32_t lb = blockIdx.x;
     const uint32_t ls = P.n >> P.lgnb, hs = ls >> 1;
     const bool em = P.e_lo != nullptr;
@@ -2889,7 +3118,30 @@ __global__ __launch_bounds__(NTP) void k_hp_persist(HpPersist P) {
     uint64_t t_cmd = 0;
     for (uint32_t seq = 1;; seq++) {
         uint32_t nw;
-        if (m >= 2) {
+        const bool dbl = P.two && m >= 4;
+        if (dbl) {  // two rounds: the nine point sums over the cells c < q
+            const uint32_t q = m >> 2;
+            uint4* xlo = rlo + (em ? 0 : hs);  // 9 rows of q after the W row (eq mode)
+            uint4* xhi = rhi + (em ? 0 : hs);
+            for (uint32_t t = threadIdx.x; t < 9 * q; t += NTP) {  // W S(y) or E(y) S(y)
+                const uint32_t pt = t / q, cc = t - pt * q;
+                const fr_t x = em ? pt_val(tlo[2], thi[2], cc, q, pt) : ld_fr(rlo, rhi, cc);
+                st_fr(xlo, xhi, t, mont_mul_ol(x, pt_val(tlo[0], thi[0], cc, q, pt)));
+            }
+            __syncthreads();
+            if (wv < 9) {  // wave pt: sum over the cells of W S(y) U(y), or of E(y) S(y)
+                fr_t acc = fr_zero();
+                for (uint32_t cc = lane; cc < q; cc += 64) {
+                    const fr_t x = ld_fr(xlo, xhi, wv * q + cc);
+                    acc = fr_add(acc, em ? x : mont_mul_ol(x, pt_val(tlo[1], thi[1], cc, q, wv)));
+                }
+                acc = fr_wave_sum(acc);
+                if (lane == 0)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) pubw[8 * wv + i] = acc.v[i];
+            }
+            nw = ZKH_HP_MSG2;
+        } else if (m >= 2) {
             const uint32_t h = m >> 1;
             if (!em) {
                 for (uint32_t t = threadIdx.x; t < 2 * h; t += NTP) {  // level 1
@@ -2953,8 +3205,9 @@ __global__ __launch_bounds__(NTP) void k_hp_persist(HpPersist P) {
         if (m == 1) return;
         if (wv == 0) {
             uint4 qd;
-            const bool ok = persist_wait(P.cmd, 3, seq, P.err, P.deadline, qd);
-            if (lane < 3) {
+            const uint32_t nq = dbl ? zkh_quad_count(32) : 3;
+            const bool ok = persist_wait(P.cmd, nq, seq, P.err, P.deadline, qd);
+            if (lane < nq) {
                 sxw[3 * lane] = qd.y;
                 sxw[3 * lane + 1] = qd.z;
                 sxw[3 * lane + 2] = qd.w;
@@ -2964,6 +3217,22 @@ __global__ __launch_bounds__(NTP) void k_hp_persist(HpPersist P) {
         }
         __syncthreads();
         if (!sok) return;
+        if (dbl) {  // double fold m -> m/4: the four products of an output on four lanes
+            const uint32_t q = m >> 2;
+            for (uint32_t t = threadIdx.x; t < ntab * q * 4; t += NTP) {  // whole lane quads
+                const uint32_t o = t >> 2, term = t & 3, i = o / q, cc = o - i * q;
+                fr_t w;
+#pragma unroll
+                for (int j = 0; j < 8; j++) w.v[j] = sxw[8 * term + j];
+                fr_t r = mont_mul_ol(w, ld_fr(tlo[i], thi[i], cc + term * q));
+                r = fr_add(r, fr_shfl_xor(r, 1));
+                r = fr_add(r, fr_shfl_xor(r, 2));
+                if (term == 0) st_fr(tlo[i], thi[i], cc, r);  // T[cc] is read only by this quad
+            }
+            m >>= 2;
+            __syncthreads();
+            continue;
+        }
         {  // fold the tables: T[k] <- T[k] + x (T[k + m/2] - T[k])
             fr_t x;
 #pragma unroll
@@ -2996,7 +3265,7 @@ hipError_t launch_hp_persist(hipStream_t s, const HpPersist& p) {
 __constant__ uint32_t kLuType[11] = {0, 1, 2, 5, 6, 3, 4, 7, 8, 9, 10};
 __global__ __launch_bounds__(NTP) void k_lu_persist(LuPersist P) {
     extern __shared__ uint4 zl[];
-    __shared__ uint32_t sok, pubw[ZKH_LU_MSG], sxw[9];
+    __shared__ uint32_t sok, pubw[ZKH_LU_MSG2], sxw[33];
     const uint32_t lb = blockIdx.x;
     const uint32_t ls = P.n >> P.lgnb, hs = ls >> 1;
     uint4* tlo[5];
@@ -3026,13 +3295,50 @@ __global__ __launch_bounds__(NTP) void k_lu_persist(LuPersist P) {
         }
     }
     __syncthreads();
-    uint32_t* slot = P.out + (size_t)lb * ZKH_PSLOT;
+    uint32_t* slot = P.out + (size_t)lb * ZKH_LU_PSLOT;
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     uint32_t m = ls;
     uint64_t t_cmd = 0;
     for (uint32_t seq = 1;; seq++) {
         uint32_t nw;
-        if (m >= 2) {
+        const bool dbl = P.two && m >= 4;
+        if (dbl) {  // two rounds: the point sums over the cells c < q
+            const uint32_t q = m >> 2;
+            uint4* wlo = rlo + hs;  // W A, then W B, at the corners (2 rows of m after the W row)
+            uint4* whi = rhi + hs;
+            for (uint32_t t = threadIdx.x; t < 2 * m; t += NTP) {
+                const uint32_t g2 = t >= m, r = t - g2 * m;  // A or B; table entry r = cc + j q
+                st_fr(wlo, whi, t, mont_mul_ol(ld_fr(rlo, rhi, r & (q - 1)), ld_fr(tlo[2 * g2], thi[2 * g2], r)));
+            }
+            __syncthreads();
+            // wave wv: sum types wv, wv + 16: 0..8 W A(y) (S(y) + beta'), 9..17 W B(y) (T(y) +
+            // beta'), 18..26 m(y) B(y), 27..30 A at corner j
+            for (uint32_t ty = wv; ty < 31; ty += NTP / 64) {
+                fr_t acc = fr_zero();
+                const uint32_t grp = ty / 9, pt = ty - 9 * grp;
+                for (uint32_t cc = lane; cc < q; cc += 64) {
+                    if (ty >= 27) {
+                        acc = fr_add(acc, ld_fr(tlo[0], thi[0], cc + (ty - 27) * q));
+                        continue;
+                    }
+                    fr_t x, y;
+                    if (grp < 2) {
+                        x = pt_val(wlo + grp * m, whi + grp * m, cc, q, pt);
+                        y = pt_val(tlo[1 + 2 * grp], thi[1 + 2 * grp], cc, q, pt);
+                        if (pt / 3 < 2 && pt % 3 < 2) y = fr_add(y, beta);
+                    } else {
+                        x = pt_val(tlo[4], thi[4], cc, q, pt);
+                        y = pt_val(tlo[2], thi[2], cc, q, pt);
+                    }
+                    acc = fr_add(acc, mont_mul_ol(x, y));
+                }
+                acc = fr_wave_sum(acc);
+                if (lane == 0)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) pubw[8 * ty + i] = acc.v[i];
+            }
+            nw = ZKH_LU_MSG2;
+        } else if (m >= 2) {
             const uint32_t h = m >> 1;
             for (uint32_t q = threadIdx.x; q < 4 * h; q += NTP) {  // level 1: row 1 + j, j = q / h
                 const uint32_t j = q / h, k = q - j * h;
@@ -3090,14 +3396,15 @@ __global__ __launch_bounds__(NTP) void k_lu_persist(LuPersist P) {
         }
         __syncthreads();
         if (wv == 0) {
-            if (lane == 0) persist_stamp(slot, seq, t_cmd);
+            if (lane == 0) persist_stamp(slot, seq, t_cmd, ZKH_LU_PSTAMP);
             persist_publish(slot, pubw, nw, seq);
         }
         if (m == 1) return;
         if (wv == 0) {
             uint4 qd;
-            const bool ok = persist_wait(P.cmd, 3, seq, P.err, P.deadline, qd);
-            if (lane < 3) {
+            const uint32_t nq = dbl ? zkh_quad_count(32) : 3;
+            const bool ok = persist_wait(P.cmd, nq, seq, P.err, P.deadline, qd);
+            if (lane < nq) {
                 sxw[3 * lane] = qd.y;
                 sxw[3 * lane + 1] = qd.z;
                 sxw[3 * lane + 2] = qd.w;
@@ -3107,6 +3414,22 @@ __global__ __launch_bounds__(NTP) void k_lu_persist(LuPersist P) {
         }
         __syncthreads();
         if (!sok) return;
+        if (dbl) {  // double fold m -> m/4 of the five tables: four products per output
+            const uint32_t q = m >> 2;
+            for (uint32_t t = threadIdx.x; t < 5 * q * 4; t += NTP) {  // whole lane quads
+                const uint32_t o = t >> 2, term = t & 3, i = o / q, cc = o - i * q;
+                fr_t w;
+#pragma unroll
+                for (int j = 0; j < 8; j++) w.v[j] = sxw[8 * term + j];
+                fr_t r = mont_mul_ol(w, ld_fr(tlo[i], thi[i], cc + term * q));
+                r = fr_add(r, fr_shfl_xor(r, 1));
+                r = fr_add(r, fr_shfl_xor(r, 2));
+                if (term == 0) st_fr(tlo[i], thi[i], cc, r);  // T[cc] is read only by this quad
+            }
+            m >>= 2;
+            __syncthreads();
+            continue;
+        }
         {  // fold the five tables: T[k] <- T[k] + x (T[k + m/2] - T[k])
             fr_t x;
 #pragma unroll

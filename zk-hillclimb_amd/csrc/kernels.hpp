@@ -386,6 +386,12 @@ __host__ __device__ inline uint32_t zkh_quad_count(uint32_t nwords) { return (nw
 // challenge (Montgomery form, 3 quads) and folds the tables; with m = 1 it publishes S[0],
 // U[0] (and E[0]) (16 or 24 words) and exits.  Message s carries seq s.  Slot layout,
 // ZKH_QUIT and the deadline as in ZkipPersist.
+// With `two` set (eq mode, or an E table with U all ones) a message covers two rounds while
+// m >= 4: over its cells c < m/4 (entries c + j m/4, j = 2 y1 + y2, y1 the first round's
+// variable) each block publishes sum_c eq_w(g_c) S_c(y) U_c(y) (eq mode, x 2^-256) or
+// sum_c E_c(y) S_c(y) (x 2^-256) at the nine points y of {0, 1, inf}^2, point 3 a + b
+// (inf: the difference along that axis), ZKH_HP_MSG2 words, and receives the four weights
+// of the double fold as ZkipPersist does (32 words).
 struct HpPersist {
     const uint32_t* s_lo;
     const uint32_t* s_hi;
@@ -400,9 +406,10 @@ struct HpPersist {
     uint32_t* err;
     unsigned long long deadline;
     fr_arg vm;        // the owed fold's challenge (Montgomery form) when fold != 0
-    uint32_t n, lgnb, fold, pad_;  // fold: entries g and g + n of the sources fold into g
+    uint32_t n, lgnb, fold, two;  // fold: entries g and g + n of the sources fold into g
 };
 #define ZKH_HP_MSG 32
+#define ZKH_HP_MSG2 72
 
 // ---- persistent logUp phase-2 rounds (the small rounds of zkh_lu_prove) ----
 // Tables A, S, B, T, m of n entries (n <= N: phase 2), each group (A, S) / (B, T, m) after
@@ -412,8 +419,16 @@ struct HpPersist {
 // w a1 (s1 + beta), w da ds, sum a0, sum a1, sum w b0 (t0 + beta), w b1 (t1 + beta),
 // w db dt, m0 b0, m1 b1, dm db (products x 2^-256; w = eq_w(g) of the global pair index;
 // 88 words, 30 quads), waits for the challenge (3 quads) and folds all five tables; with
-// m = 1 it publishes A[0], S[0], B[0], T[0], m[0] (40 words) and exits.  Slot layout,
-// ZKH_QUIT and the deadline as in ZkipPersist.
+// m = 1 it publishes A[0], S[0], B[0], T[0], m[0] (40 words) and exits.  Slots of
+// ZKH_LU_PSLOT words (clock stamps from word ZKH_LU_PSTAMP); ZKH_QUIT and the deadline as in
+// ZkipPersist.
+// With `two` set a message covers two rounds while m >= 4: over its cells c < m/4 (entries
+// c + j m/4, j = 2 y1 + y2, y1 the first round's variable) each block publishes, at the
+// nine points y of {0, 1, inf}^2 (point 3 a + b, inf: the difference along that axis),
+// sum_c W_c A(y) (S(y) + beta'), sum_c W_c B(y) (T(y) + beta'), sum_c m(y) B(y) (x 2^-256;
+// W_c = eq_w(g_c), beta' = beta at the points without inf, 0 at the others), then sum_c A
+// at the four corners j (ZKH_LU_MSG2 words), and receives the four weights of the double
+// fold as ZkipPersist does (32 words).
 struct LuPersist {
     const uint32_t* lo[5];  // A, S, B, T, m: sources (limb-quad planes)
     const uint32_t* hi[5];
@@ -426,8 +441,12 @@ struct LuPersist {
     fr_arg vm;    // the owed folds' challenge (Montgomery form)
     fr_arg beta;  // plain
     uint32_t n, lgnb, fold_as, fold_btm;  // fold_*: that group's sources hold 2n entries
+    uint32_t two, pad_[3];
 };
 #define ZKH_LU_MSG 88
+#define ZKH_LU_MSG2 248
+#define ZKH_LU_PSLOT 384   // words per block slot and command area of the logUp loop
+#define ZKH_LU_PSTAMP 352  // first clock-stamp word of its slots
 hipError_t launch_lu_persist(hipStream_t s, const LuPersist& p);
 // one thread: *word (when word is given) to *host_word, then seq to *flag (pinned host
 // memory, system scope): the completion flag of everything queued before it on the stream

@@ -693,7 +693,8 @@ static Fr eq_prefix_sum(const std::vector<Fr>& u, uint64_t K) {
 struct EqState {
     uint32_t* elo_d = nullptr;
     uint32_t* ehi_d = nullptr;
-    std::vector<Fr> corr;  // corr[K] for K = 0..kmax
+    std::vector<Fr> corr;     // corr[K] for K = 0..kmax
+    std::vector<Fr> inv1mu;   // 1 / (1 - u_t) for t < kmax (empty for a degenerate point)
     uint32_t nvars = 0;
 };
 // all_rounds: the caller will weight shorter prefixes K < |u| (sumcheck rounds), which
@@ -728,6 +729,13 @@ static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_
     const Fr inv = fr_inv(prefix[kmax]);
     st.corr.resize(kmax + 1);
     for (uint32_t K = 0; K <= kmax; K++) st.corr[K] = fr_mul(prefix[K], inv);
+    // 1 / (1 - u_t) = prefix[t] / prefix[t + 1], with 1 / prefix[t] = (1 - u_t) / prefix[t + 1]
+    st.inv1mu.resize(kmax);
+    Fr ip = inv;  // 1 / prefix[t + 1]
+    for (uint32_t t = kmax; t-- > 0;) {
+        st.inv1mu[t] = fr_mul(prefix[t], ip);
+        ip = fr_mul(ip, t < st.nvars ? fr_sub(kOne, u[t]) : kOne);
+    }
     return 0;
 }
 static Fr eq_corr(const EqState& st, uint32_t K) { return st.corr[K]; }
@@ -2827,17 +2835,36 @@ static bool lu_phase2_round(uint8_t tr[32], LuState& L, uint32_t r, const Fr sm[
 #ifndef ZKH_LH_PLS
 #define ZKH_LH_PLS ZKH_PLS_MAX
 #endif
+// Per message of a persistent loop (ZKH_TRACE): block 0's compute (command received -> sums
+// published, device clock; the first message's load and round are not bracketed), round
+// trip (sums published -> command received) and the host's work (sums seen -> command
+// sent).  slot0: block 0's slot after the kernel has exited; host: the sums-seen and
+// command-sent times of each message.
+static void trace_persist(zkh_ctx* c, const char* what, const uint32_t* slot0, uint32_t nmsg,
+                          const std::vector<double>& host, uint32_t stamp = ZKH_PSTAMP) {
+    const double tick_us = 1000.0 / (double)c->clock_khz;
+    const uint32_t* st = slot0 + stamp;
+    fprintf(stderr, "[zkh]   %s messages (compute/trip/host us):", what);
+    for (uint32_t m = 1; m <= nmsg && m < 14; m++) {
+        const double comp = m > 1 ? (double)(uint32_t)(st[4 + 2 * m] - st[3 + 2 * m]) * tick_us : 0.0;
+        const double trip = m < nmsg ? (double)(uint32_t)(st[5 + 2 * m] - st[4 + 2 * m]) * tick_us : 0.0;
+        const size_t i = 2 * (size_t)(m - 1);
+        const double hw = i + 1 < host.size() ? host[i + 1] - host[i] : 0.0;
+        fprintf(stderr, " %.1f/%.1f/%.1f", comp, trip, hw);
+    }
+    fprintf(stderr, "\n");
+}
 static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0, uint32_t n, const DevPlanes src[5],
                              bool fold_as, bool fold_btm, const uint32_t vm[8], const uint32_t beta_l[8],
                              uint32_t* ev_out, uint32_t* ws_out, Fr fin[5]) {
     const uint32_t lgnb = n > ZKH_LH_PLS ? ceil_log2(n / ZKH_LH_PLS) : 0, nb = 1u << lgnb;
     const uint32_t R = ceil_log2(n) - lgnb;  // local rounds
     int rc;
-    if ((rc = ensure_ps(c, (size_t)ZKH_PSLOT * (nb + 2)))) return rc;
+    if ((rc = ensure_ps(c, (size_t)ZKH_LU_PSLOT * (nb + 2)))) return rc;
     uint32_t* ps = c->ps_host;
-    uint32_t* slots = ps + ZKH_PSLOT;
-    uint32_t* cmd = ps + (size_t)ZKH_PSLOT * (nb + 1);
-    memset(ps, 0, (size_t)ZKH_PSLOT * (nb + 2) * 4);
+    uint32_t* slots = ps + ZKH_LU_PSLOT;
+    uint32_t* cmd = ps + (size_t)ZKH_LU_PSLOT * (nb + 1);
+    memset(ps, 0, (size_t)ZKH_LU_PSLOT * (nb + 2) * 4);
     LuPersist P{};
     for (int i = 0; i < 5; i++) {
         P.lo[i] = src[i].lo();
@@ -2855,12 +2882,13 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
     P.lgnb = lgnb;
     P.fold_as = fold_as;
     P.fold_btm = fold_btm;
-    auto send = [&](uint32_t seq, const uint32_t* xm) {
-        for (uint32_t i = 0; i < 8 && xm; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
-        for (uint32_t qd = 0; qd < 3; qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
+    P.two = getenv("ZKH_PERSIST_ONE") ? 0 : 1;  // two rounds per message while a block holds >= 4 entries
+    auto send = [&](uint32_t seq, const uint32_t* xm, uint32_t nw) {
+        for (uint32_t i = 0; i < nw && xm; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
+        for (uint32_t qd = 0; qd < zkh_quad_count(nw); qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
     };
     auto quit = [&]() {
-        send(ZKH_QUIT, nullptr);
+        send(ZKH_QUIT, nullptr, 32);
         (void)hipStreamSynchronize(c->stream);
     };
     {
@@ -2874,7 +2902,7 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
     const double t_launch = now_us();
     auto slot_fr = [&](uint32_t b, uint32_t i) {
         uint32_t v[8];
-        for (uint32_t j = 0; j < 8; j++) v[j] = slots[(size_t)b * ZKH_PSLOT + zkh_quad_word(8 * i + j)];
+        for (uint32_t j = 0; j < 8; j++) v[j] = slots[(size_t)b * ZKH_LU_PSLOT + zkh_quad_word(8 * i + j)];
         return fr_load(v);
     };
     auto wait_msg = [&](uint32_t seq, uint32_t nw) -> int {
@@ -2884,7 +2912,7 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
             bool all = true;
             for (uint32_t b = 0; b < nb && all; b++)
                 for (uint32_t qd = 0; qd < nq; qd++)
-                    if (__atomic_load_n(slots + (size_t)b * ZKH_PSLOT + 4 * qd, __ATOMIC_ACQUIRE) != seq) {
+                    if (__atomic_load_n(slots + (size_t)b * ZKH_LU_PSLOT + 4 * qd, __ATOMIC_ACQUIRE) != seq) {
                         all = false;
                         break;
                     }
@@ -2904,22 +2932,76 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
             }
         }
     };
-    for (uint32_t lr = 0; lr < R; lr++) {
-        if ((rc = wait_msg(lr + 1, ZKH_LU_MSG))) return rc;
-        Fr sm[11];
-        for (int t = 0; t < 11; t++) sm[t] = kZero;
-        for (uint32_t b = 0; b < nb; b++)
-            for (int t = 0; t < 11; t++) sm[t] = fr_add(sm[t], slot_fr(b, t));
-        Fr v;
-        if (!lu_phase2_round(tr, L, r0 + lr, sm, true, v, ev_out, ws_out)) {
-            quit();
-            return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r0 + lr);
+    const bool tracing = trace_on();
+    std::vector<double> tr_h;  // per message: sums seen, command sent
+    uint32_t seq = 1;
+    for (uint32_t lr = 0; lr < R; seq++) {
+        const uint32_t r1 = r0 + lr;
+        if (!P.two || R - lr < 2) {  // one round
+            if ((rc = wait_msg(seq, ZKH_LU_MSG))) return rc;
+            if (tracing) tr_h.push_back(now_us());
+            Fr sm[11];
+            for (int t = 0; t < 11; t++) sm[t] = kZero;
+            for (uint32_t b = 0; b < nb; b++)
+                for (int t = 0; t < 11; t++) sm[t] = fr_add(sm[t], slot_fr(b, t));
+            Fr v;
+            if (!lu_phase2_round(tr, L, r1, sm, true, v, ev_out, ws_out)) {
+                quit();
+                return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r1);
+            }
+            uint32_t xm[8];
+            fr_store(fr_to_mont(v), xm);
+            send(seq, xm, 8);
+            if (tracing) tr_h.push_back(now_us());
+            lr++;
+            continue;
         }
-        uint32_t xm[8];
-        fr_store(fr_to_mont(v), xm);
-        send(lr + 1, xm);
+        // two rounds from the point sums (index 3 a + b; a: the first variable y1, b: the
+        // second y2; 0, 1, inf): AS = G[0..9), BT = G[9..18), MB = G[18..27), A at corner
+        // 2 y1 + y2 = G[27 + j].  Round r1's sums over the pairs (c + y2 q, c + y2 q + 2q):
+        // the eq-weighted pieces as X(t, 0) + rho X(t, 1) (rho = u/(1 - u) of y2 relative to
+        // the cell weight), the others X(t, 0) + X(t, 1); round r1 + 1's: X(v1, t)
+        if ((rc = wait_msg(seq, ZKH_LU_MSG2))) return rc;
+        if (tracing) tr_h.push_back(now_us());
+        Fr G[31];
+        for (int p = 0; p < 31; p++) G[p] = kZero;
+        for (uint32_t b = 0; b < nb; b++)
+            for (int p = 0; p < 31; p++) G[p] = fr_add(G[p], slot_fr(b, p));
+        const uint32_t K2 = L.logD - r1 - 2;  // eq coordinate of y2
+        const Fr rho = fr_mul((*L.u)[K2], L.eq->inv1mu[K2]);
+        Fr sm[11], v1, v2;
+        for (int a = 0; a < 3; a++) {
+            sm[a] = fr_add(G[3 * a], fr_mul(rho, G[3 * a + 1]));
+            sm[5 + a] = fr_add(G[9 + 3 * a], fr_mul(rho, G[9 + 3 * a + 1]));
+            sm[8 + a] = fr_add(G[18 + 3 * a], G[18 + 3 * a + 1]);
+        }
+        sm[3] = fr_add(G[27], G[28]);
+        sm[4] = fr_add(G[29], G[30]);
+        if (!lu_phase2_round(tr, L, r1, sm, true, v1, ev_out, ws_out)) {
+            quit();
+            return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r1);
+        }
+        for (int b = 0; b < 3; b++) {
+            sm[b] = quad_at(G[b], G[3 + b], G[6 + b], v1);
+            sm[5 + b] = quad_at(G[9 + b], G[12 + b], G[15 + b], v1);
+            sm[8 + b] = quad_at(G[18 + b], G[21 + b], G[24 + b], v1);
+        }
+        sm[3] = fr_add(G[27], fr_mul(v1, fr_sub(G[29], G[27])));
+        sm[4] = fr_add(G[28], fr_mul(v1, fr_sub(G[30], G[28])));
+        if (!lu_phase2_round(tr, L, r1 + 1, sm, true, v2, ev_out, ws_out)) {
+            quit();
+            return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r1 + 1);
+        }
+        // double fold weights of T[c + (2 y1 + y2) q]
+        const Fr a1 = fr_sub(kOne, v1), a2 = fr_sub(kOne, v2);
+        const Fr Lw[4] = {fr_mul(a1, a2), fr_mul(a1, v2), fr_mul(v1, a2), fr_mul(v1, v2)};
+        uint32_t xm[32];
+        for (int j = 0; j < 4; j++) fr_store(fr_to_mont(Lw[j]), xm + 8 * j);
+        send(seq, xm, 32);
+        if (tracing) tr_h.push_back(now_us());
+        lr += 2;
     }
-    if ((rc = wait_msg(R + 1, 40))) return rc;
+    if ((rc = wait_msg(seq, 40))) return rc;
     std::vector<Fr> t[5];
     for (int i = 0; i < 5; i++) {
         t[i].resize(nb);
@@ -2952,9 +3034,11 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
             for (uint32_t i = 0; i < h; i++) t[q][i] = fr_add(t[q][i], fr_mul(v, fr_sub(t[q][i + h], t[q][i])));
     }
     for (int i = 0; i < 5; i++) fin[i] = t[i][0];
-    if (trace_on())
+    if (tracing) {
         fprintf(stderr, "[zkh] lu persistent loop: n=%u, %u blocks, %u device + %u host rounds in %.1f us\n", n, nb, R,
                 lgnb, now_us() - t_launch);
+        trace_persist(c, "lu", slots, seq, tr_h, ZKH_LU_PSTAMP);
+    }
     return 0;
 }
 static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const zkh_tensor* S,
@@ -3696,8 +3780,8 @@ static Fr lagrange4(const Fr e[4], const Fr& v) {
 #define ZKH_HP_PERSIST_MAX 8192u
 static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* u, const EqState& eq, uint32_t k,
                              uint32_t r0, uint32_t sz, int fold, DevPlanes e_src, DevPlanes s_src, DevPlanes u_src,
-                             const uint32_t vm[8], Fr& claim, Fr& cE, uint32_t* ev_out, uint32_t* ws_out, Fr& e_fin,
-                             Fr& s_fin, Fr& u_fin) {
+                             bool u_ones, const uint32_t vm[8], Fr& claim, Fr& cE, uint32_t* ev_out, uint32_t* ws_out,
+                             Fr& e_fin, Fr& s_fin, Fr& u_fin) {
     const bool em = u == nullptr;  // explicit E table
     static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
     const uint32_t lgnb = sz > ZKH_LH_PLS ? ceil_log2(sz / ZKH_LH_PLS) : 0, nb = 1u << lgnb;
@@ -3725,12 +3809,15 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
     P.n = sz;
     P.lgnb = lgnb;
     P.fold = fold ? 1 : 0;
-    auto send = [&](uint32_t seq, const uint32_t* xm) {
-        for (uint32_t i = 0; i < 8 && xm; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
-        for (uint32_t qd = 0; qd < 3; qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
+    // two rounds per message while a block holds >= 4 entries: the product is then of degree
+    // 2 in each variable (eq mode, or an E table with U all ones)
+    P.two = (!em || u_ones) && !getenv("ZKH_PERSIST_ONE") ? 1 : 0;
+    auto send = [&](uint32_t seq, const uint32_t* xm, uint32_t nw) {
+        for (uint32_t i = 0; i < nw && xm; i++) __atomic_store_n(cmd + zkh_quad_word(i), xm[i], __ATOMIC_RELAXED);
+        for (uint32_t qd = 0; qd < zkh_quad_count(nw); qd++) __atomic_store_n(cmd + 4 * qd, seq, __ATOMIC_RELEASE);
     };
     auto quit = [&]() {
-        send(ZKH_QUIT, nullptr);
+        send(ZKH_QUIT, nullptr, 32);
         (void)hipStreamSynchronize(c->stream);
     };
     {
@@ -3797,21 +3884,72 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
         if (!em) cE = fr_mul(cE, fr_eq2(ul, w));
         return true;
     };
-    for (uint32_t lr = 0; lr < R; lr++) {
-        if ((rc = wait_msg(lr + 1, ZKH_HP_MSG))) return rc;
-        Fr sums[4] = {kZero, kZero, kZero, kZero};
-        for (uint32_t b = 0; b < nb; b++)
-            for (int t = 0; t < 4; t++) sums[t] = fr_add(sums[t], slot_fr(b, t));
-        Fr w;
-        if (!host_round(r0 + lr, sums, true, w)) {
-            quit();
-            return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r0 + lr);
+    const bool tracing = trace_on();
+    std::vector<double> tr_h;  // per message: sums seen, command sent
+    uint32_t seq = 1;
+    for (uint32_t lr = 0; lr < R; seq++) {
+        const uint32_t r1 = r0 + lr;
+        if (!P.two || R - lr < 2) {  // one round
+            if ((rc = wait_msg(seq, ZKH_HP_MSG))) return rc;
+            if (tracing) tr_h.push_back(now_us());
+            Fr sums[4] = {kZero, kZero, kZero, kZero};
+            for (uint32_t b = 0; b < nb; b++)
+                for (int t = 0; t < 4; t++) sums[t] = fr_add(sums[t], slot_fr(b, t));
+            Fr w;
+            if (!host_round(r1, sums, true, w)) {
+                quit();
+                return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r1);
+            }
+            uint32_t xm[8];
+            fr_store(fr_to_mont(w), xm);
+            send(seq, xm, 8);
+            if (tracing) tr_h.push_back(now_us());
+            lr++;
+            continue;
         }
-        uint32_t xm[8];
-        fr_store(fr_to_mont(w), xm);
-        send(lr + 1, xm);
+        // two rounds from the nine point sums G[3 a + b] (a: the first variable y1, b: the
+        // second y2; 0, 1, inf): round r1's sums at t, over the pairs (c + y2 q, c + y2 q +
+        // 2q) of its table, are G(t, 0) + rho G(t, 1), rho = u/(1 - u) of y2 relative to the
+        // cell weight (eq mode; 1 with E); round r1 + 1's are G(w1, t)
+        if ((rc = wait_msg(seq, ZKH_HP_MSG2))) return rc;
+        if (tracing) tr_h.push_back(now_us());
+        Fr G[9];
+        for (int p = 0; p < 9; p++) G[p] = kZero;
+        for (uint32_t b = 0; b < nb; b++)
+            for (int p = 0; p < 9; p++) G[p] = fr_add(G[p], slot_fr(b, p));
+        Fr rho = kOne;
+        if (!em) {
+            const uint32_t K2 = k - r1 - 2;  // eq coordinate of y2
+            rho = fr_mul((*u)[K2], eq.inv1mu[K2]);
+        }
+        // E mode: the device sums carry one 2^-256 (E S, U = 1), so they go in as exact values
+        auto val = [&](const Fr& x) { return em ? fix1(x) : x; };
+        Fr sums[4], w1, w2;
+        for (int t = 0; t < 4; t++) {
+            const Fr ft = fr_u64(t);
+            sums[t] = val(fr_add(quad_at(G[0], G[3], G[6], ft), fr_mul(rho, quad_at(G[1], G[4], G[7], ft))));
+        }
+        if (!host_round(r1, sums, !em, w1)) {
+            quit();
+            return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r1);
+        }
+        Fr H[3];
+        for (int b = 0; b < 3; b++) H[b] = quad_at(G[b], G[3 + b], G[6 + b], w1);
+        for (int t = 0; t < 4; t++) sums[t] = val(quad_at(H[0], H[1], H[2], fr_u64(t)));
+        if (!host_round(r1 + 1, sums, !em, w2)) {
+            quit();
+            return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r1 + 1);
+        }
+        // double fold weights of T[c + (2 y1 + y2) q]
+        const Fr a1 = fr_sub(kOne, w1), a2 = fr_sub(kOne, w2);
+        const Fr L[4] = {fr_mul(a1, a2), fr_mul(a1, w2), fr_mul(w1, a2), fr_mul(w1, w2)};
+        uint32_t xm[32];
+        for (int j = 0; j < 4; j++) fr_store(fr_to_mont(L[j]), xm + 8 * j);
+        send(seq, xm, 32);
+        if (tracing) tr_h.push_back(now_us());
+        lr += 2;
     }
-    if ((rc = wait_msg(R + 1, em ? 24 : 16))) return rc;
+    if ((rc = wait_msg(seq, em ? 24 : 16))) return rc;
     std::vector<Fr> ta(nb), tb(nb), te(em ? nb : 0);
     for (uint32_t b = 0; b < nb; b++) {
         ta[b] = slot_fr(b, 0);
@@ -3852,9 +3990,11 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
     s_fin = ta[0];
     u_fin = tb[0];
     e_fin = em ? te[0] : cE;
-    if (trace_on())
+    if (tracing) {
         fprintf(stderr, "[zkh] hp persistent loop: n=%u, %u blocks, %u device + %u host rounds in %.1f us\n", sz, nb, R,
                 lgnb, now_us() - t_launch);
+        trace_persist(c, "hp", slots, seq, tr_h);
+    }
     return 0;
 }
 // claim_label (eq form only): the claim is not given but is sum eq(i, u) S[i] U[i], taken
@@ -3968,8 +4108,8 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         const int fold = r > 0;
         if (persists(r)) {  // the rest in one launch
             if (s32 || u32) return fail(c, ZKH_EDEV, "internal: unfolded int32 table at the persistent loop");
-            if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, vm, claim, cE, ev_out,
-                                        ws_out, e_fin, s_fin, u_fin)))
+            if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, u_ones, vm, claim, cE,
+                                        ev_out, ws_out, e_fin, s_fin, u_fin)))
                 return rc;
             persisted = true;
             break;
