@@ -144,3 +144,36 @@ def test_absorb_trace_matches_reference_format(tmp_path):
         if chal:
             C.tr_challenge_fr(st)
     assert log.read_text().splitlines() == want
+
+
+R_MOD = 0x73EDA753299D7D483339D80809A1D80553BDA402FFFE5BFEFFFFFFFF00000001
+
+
+def _limbs(x):
+    return (ctypes.c_uint32 * 8)(*[(x >> (32 * i)) & 0xFFFFFFFF for i in range(8)])
+
+
+def _int(l):
+    return sum(int(l[i]) << (32 * i) for i in range(8))
+
+
+def test_host_scalar_ops_match_big_integers(zkh):
+    """zkh_fr_scalar (the host field arithmetic of the round logic): add, sub, mul and the
+    binary-Euclid inverse against Python integers mod r, with the inverse pinned by
+    Fermat's little theorem (x^(r-2)) and x * x^-1 = 1, and inverse(0) = 0."""
+    lib = zkh.lib()
+    f = lib.zkh_fr_scalar
+    f.restype = ctypes.c_int
+    rng = np.random.default_rng(5)
+    vals = [0, 1, 2, 3, R_MOD - 1, R_MOD - 2, (R_MOD + 1) // 2, 1 << 200, (1 << 255) % R_MOD]
+    vals += [int.from_bytes(rng.bytes(32), "little") % R_MOD for _ in range(300)]
+    out = (ctypes.c_uint32 * 8)()
+    for i, a in enumerate(vals):
+        b = vals[(7 * i + 3) % len(vals)]
+        for op, want in ((0, (a + b) % R_MOD), (1, (a - b) % R_MOD), (2, a * b % R_MOD),
+                         (3, pow(a, R_MOD - 2, R_MOD))):
+            assert f(_limbs(a), _limbs(b), op, out) == 0
+            assert _int(out) == want, (op, hex(a))
+        if a:
+            assert _int(out) * a % R_MOD == 1
+    assert f(_limbs(R_MOD), _limbs(1), 0, out) != 0  # non-canonical input is refused

@@ -1063,18 +1063,45 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
 // (P_j = P_{j-1} x_j / 2^256), so the backward walk yields plain inverses directly.  The
 // same identities combine totals: for Q = M(a, b), 1/a = M(b, 1/Q).  Block b covers
 // INV_CHK*NT entries; thread t owns entries base + j*NT + t.  Pass 1 stores P_j in A, and
-// a block-wide inclusive prefix/suffix scan of the thread totals gives each thread the
-// M-product of all OTHER threads' totals; the block total goes to blockprod.  Between the
+// a product tree over the thread totals (others_tree) gives each thread the M-product of
+// all OTHER threads' totals; the block total goes to blockprod.  Between the
 // passes, k_inv_blocks turns the block totals into "all other blocks" products and
 // publishes the grand product G, whose plain inverse the host computes once.  Pass 2 walks
 // each thread's entries backwards.  Zero entries (x + beta = 0) take 2^256, M's identity,
 // in the products and produce 0, the reference's Fermat convention; pass 1 sets *zflag when
 // it meets one (the inverse then has a zero entry).
 #define INV_CHK 16
+// The M-product of all OTHER leaves, for each of NL leaves (NL a power of 2, at most the
+// block size; thread t < NL gives leaf t): a product tree up, tr[k] = M(tr[2k], tr[2k + 1])
+// with the leaves at tr[NL + t] and the block total at tr[1], then the products outside
+// each subtree down, out[1] = 2^256 (the empty product), out[c] = M(out[c / 2], tr[c ^ 1]),
+// so out[NL + t] is the product of every leaf but t.  An M-product of a set does not depend
+// on its bracketing, so this equals the prefix-times-suffix scan, with 3 NL products
+// instead of 2 NL log2(NL) over 2 log2(NL) levels.  Every thread of the block calls it.
+template <uint32_t NL>
+ZDEV fr_t others_tree(fr_t* tr, fr_t* out, const fr_t& v) {
+    const uint32_t t = threadIdx.x;
+    if (t < NL) tr[NL + t] = v;
+    __syncthreads();
+    for (uint32_t w = NL / 2; w >= 1; w >>= 1) {  // nodes [w, 2w)
+        if (t < w) tr[w + t] = mont_mul(tr[2 * (w + t)], tr[2 * (w + t) + 1]);
+        __syncthreads();
+    }
+    if (t == 0) out[1] = one_m();
+    __syncthreads();
+    for (uint32_t w = 1; w < NL; w <<= 1) {  // the children [2w, 4w) of nodes [w, 2w)
+        if (t < 2 * w) {
+            const uint32_t c = 2 * w + t;
+            out[c] = mont_mul(out[c >> 1], tr[c ^ 1]);
+        }
+        __syncthreads();
+    }
+    return t < NL ? out[NL + t] : one_m();
+}
 __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
                                                   uint32_t* others, uint32_t* blockprod, uint32_t* zflag) {
-    __shared__ fr_t pre[NT], suf[NT];
+    __shared__ fr_t tr[2 * NT], out[2 * NT];
     const uint32_t t = threadIdx.x;
     const uint32_t base = blockIdx.x * NT * INV_CHK;
     fr_t run = one_m();
@@ -1090,22 +1117,8 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
         }
     }
     if (__ballot(zero) && (t & 63) == 0) atomicOr(zflag, 1u);  // one atomic per wave that met a zero
-    pre[t] = run;
-    suf[t] = run;
-    __syncthreads();
-    for (uint32_t off = 1; off < NT; off <<= 1) {
-        fr_t p = pre[t], q = suf[t];
-        fr_t pp = t >= off ? pre[t - off] : one_m();
-        fr_t qq = t + off < NT ? suf[t + off] : one_m();
-        __syncthreads();
-        pre[t] = mont_mul(p, pp);
-        suf[t] = mont_mul(q, qq);
-        __syncthreads();
-    }
-    fr_t ex_pre = t > 0 ? pre[t - 1] : one_m();
-    fr_t ex_suf = t + 1 < NT ? suf[t + 1] : one_m();
-    st_aos(others, blockIdx.x * NT + t, mont_mul(ex_pre, ex_suf));
-    if (t == NT - 1) st_aos(blockprod, blockIdx.x, pre[NT - 1]);
+    st_aos(others, blockIdx.x * NT + t, others_tree<NT>(tr, out, run));
+    if (t == 0) st_aos(blockprod, blockIdx.x, tr[1]);
 }
 // One block over the nb block products (Montgomery form): others[b] = product of all the
 // other blocks' products, and the grand product P published (pub.host_out[0], then the
@@ -1113,7 +1126,7 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
 #define NTI 256
 __global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__ bp, uint32_t nb,
                                                     uint32_t* others, Publish pub, const uint32_t* zflag) {
-    __shared__ fr_t pre[NTI], suf[NTI];
+    __shared__ fr_t tr[2 * NTI], out[2 * NTI];
     const uint32_t t = threadIdx.x;
     const uint32_t per = (nb + NTI - 1) / NTI;
     const uint32_t b0 = t * per, b1 = min(nb, b0 + per);
@@ -1122,27 +1135,13 @@ __global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__
         st_aos(others, b, loc);
         loc = mont_mul(loc, ld_aos(bp, b));
     }
-    pre[t] = loc;
-    suf[t] = loc;
-    __syncthreads();
-    for (uint32_t off = 1; off < NTI; off <<= 1) {
-        const fr_t p = pre[t], q = suf[t];
-        const fr_t pp = t >= off ? pre[t - off] : one_m();
-        const fr_t qq = t + off < NTI ? suf[t + off] : one_m();
-        __syncthreads();
-        pre[t] = mont_mul(p, pp);
-        suf[t] = mont_mul(q, qq);
-        __syncthreads();
-    }
-    const fr_t ex_pre = t > 0 ? pre[t - 1] : one_m();
-    const fr_t ex_suf = t + 1 < NTI ? suf[t + 1] : one_m();
-    fr_t rs = mont_mul(ex_pre, ex_suf);  // the other threads' products
+    fr_t rs = others_tree<NTI>(tr, out, loc);  // the other threads' products
     for (int b = (int)b1 - 1; b >= (int)b0; b--) {  // times the local suffix
         st_aos(others, b, mont_mul(ld_aos(others, b), rs));
         rs = mont_mul(rs, ld_aos(bp, b));
     }
-    if (t == NTI - 1) {
-        st_aos(pub.host_out, 0, pre[NTI - 1]);
+    if (t == 0) {
+        st_aos(pub.host_out, 0, tr[1]);
         pub.host_out[8] = *zflag;  // pass 1 met a zero entry
         __threadfence_system();
         __hip_atomic_store(pub.host_flag, pub.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
