@@ -993,8 +993,9 @@ void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
 template <bool Comb, bool SeqS, typename LG, typename LT, typename LM>
 __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tlen, LM mapped, uint32_t N, fr_t rm,
                                   fr_t r,
-                                  const uint4* __restrict__ blo, const uint4* __restrict__ bhi, uint4* clo,
-                                  uint4* chi, uint4* alo, uint4* ahi, uint32_t* flags) {
+                                  const uint4* __restrict__ blo, const uint4* __restrict__ bhi,
+                                  const uint32_t* __restrict__ baos, uint4* clo, uint4* chi, uint4* alo, uint4* ahi,
+                                  uint32_t* flags) {
     uint32_t f = 0;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         const fr_t g = G(i);
@@ -1014,8 +1015,14 @@ __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tle
             for (int k = 0; k < 8; k++) same = same && t.v[k] == g.v[k];
         }
         if (same) {
-            alo[i] = blo[j];
-            ahi[i] = bhi[j];
+            if (baos) {  // one 32-byte line
+                const uint4* q = reinterpret_cast<const uint4*>(baos + 8 * (size_t)j);
+                alo[i] = q[0];
+                ahi[i] = q[1];
+            } else {
+                alo[i] = blo[j];
+                ahi[i] = bhi[j];
+            }
         } else {
             f |= 2u;
         }
@@ -1026,7 +1033,7 @@ __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tle
 }
 void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
                             Src mapped, int seq_s, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host,
-                            DevPlanes Binv, DevPlanes comb, DevPlanes A, uint32_t* flags) {
+                            DevPlanes Binv, const uint32_t* binv_aos, DevPlanes comb, DevPlanes A, uint32_t* flags) {
     const fr_t low = to_fr(low_host), r = to_fr(r_host), rm = to_fr(r_m_host);
     const uint32_t g = grid_for(n, NT, 8192);
     with_loader(G, [&](auto lg) {
@@ -1034,12 +1041,12 @@ void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* lo
             with_loader(mapped, [&](auto lm) {
                 if (seq_s)
                     k_lu_tuple_gather<true, true><<<g, NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
-                                                                    PL_HI(Binv), PL_LO(comb), PL_HI(comb), PL_LO(A),
-                                                                    PL_HI(A), flags);
+                                                                    PL_HI(Binv), binv_aos, PL_LO(comb), PL_HI(comb),
+                                                                    PL_LO(A), PL_HI(A), flags);
                 else
                     k_lu_tuple_gather<true, false><<<g, NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
-                                                                     PL_HI(Binv), PL_LO(comb), PL_HI(comb), PL_LO(A),
-                                                                     PL_HI(A), flags);
+                                                                     PL_HI(Binv), binv_aos, PL_LO(comb), PL_HI(comb),
+                                                                     PL_LO(A), PL_HI(A), flags);
             });
         });
     });
@@ -1051,7 +1058,7 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
         with_loader(T, [&](auto lt) {
             k_lu_tuple_gather<false, false><<<grid_for(n, NT, 8192), NT, 0, s>>>(
                 ls, n, low, lt, tlen, LdI32{nullptr}, N, fr_t{}, fr_t{}, PL_LO(Binv), PL_HI(Binv), nullptr, nullptr,
-                PL_LO(A), PL_HI(A), flags);
+                nullptr, PL_LO(A), PL_HI(A), flags);
         });
     });
 }
@@ -1156,7 +1163,8 @@ void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, ui
 __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
                                                   const uint32_t* __restrict__ others,
-                                                  const uint32_t* __restrict__ others_blk, fr_t inv_total) {
+                                                  const uint32_t* __restrict__ others_blk, fr_t inv_total,
+                                                  uint32_t* aos) {
     const uint32_t t = threadIdx.x;
     const uint32_t base = blockIdx.x * NT * INV_CHK;
     const fr_t binv = mont_mul(inv_total, ld_aos(others_blk, blockIdx.x));
@@ -1170,6 +1178,7 @@ __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4*
         const fr_t inv = mont_mul(prev, y);
         y = mont_mul(z ? one_m() : x, y);
         st_fr(alo, ahi, idx, z ? fr_zero() : inv);
+        if (aos) st_aos(aos, idx, z ? fr_zero() : inv);
     }
 }
 uint32_t inv_blocks(uint32_t n) { return (n + NT * INV_CHK - 1) / (NT * INV_CHK); }
@@ -1180,9 +1189,9 @@ void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
 }
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
-                      const uint32_t* inv_total_host) {
+                      const uint32_t* inv_total_host, uint32_t* aos) {
     k_inv_pass2<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
-                                             PL_HI(A), others, others_blk, to_fr(inv_total_host));
+                                             PL_HI(A), others, others_blk, to_fr(inv_total_host), aos);
 }
 
 // ------------------------------------------------------------------------------------

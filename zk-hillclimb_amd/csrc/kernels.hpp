@@ -171,10 +171,11 @@ void launch_lu_map_to_i32(hipStream_t s, Src S, uint32_t n, const uint32_t* low_
 // tuple lookup, j = (G[i] - low).limb0: comb[i] = G[i] + r mapped[j]; A[i] = Binv[j] where
 // T[j] == G[i]; *flags |= 1 (j >= N) / 2 (T[j] != G[i]); r plain and in Montgomery form;
 // tlen > 0: T is the range table low + min(j, tlen - 1) (not read); seq_s: `mapped` is
-// S = mapped[(G - low).limb0] (n entries), read at i
+// S = mapped[(G - low).limb0] (n entries), read at i; binv_aos (optional): Binv as AoS
+// (32 contiguous bytes per entry: one cache line per random read instead of one per plane)
 void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
                             Src mapped, int seq_s, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host,
-                            DevPlanes Binv, DevPlanes comb, DevPlanes A, uint32_t* flags);
+                            DevPlanes Binv, const uint32_t* binv_aos, DevPlanes comb, DevPlanes A, uint32_t* flags);
 // the same for a plain range lookup: A[i] = Binv[j] (j = (S[i] - low).limb0) where T[j] == S[i]
 void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
                             uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags);
@@ -191,9 +192,10 @@ void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* be
                       DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag);
 void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, uint32_t* others_blk,
                        Publish pub, const uint32_t* zflag);
+// aos (optional): the inverses also as AoS (n entries)
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
-                      const uint32_t* inv_total_host);
+                      const uint32_t* inv_total_host, uint32_t* aos = nullptr);
 // Round kernels take the previous round's challenge (Montgomery form) either from the host
 // at launch (v_m_host) or, when vmp is given, from device words vmp[0..8) written by a relay
 // (launch_relay) that runs between the previous round and this one; vmp[8] != 0 makes the

@@ -2575,7 +2575,7 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
 // A = 1/(S + beta) into planes A (n entries)
 // any_zero (when given): whether some S[i] + beta was zero (its inverse entry is 0)
 static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, DevPlanes A,
-                         bool* any_zero = nullptr) {
+                         bool* any_zero = nullptr, uint32_t* aos = nullptr) {
     int rc = 0;
     uint32_t nb = inv_blocks(n);
     uint32_t* others = (uint32_t*)scratch_slot(c, SL_TMP4, (size_t)nb * 256 * 32, &rc);
@@ -2600,8 +2600,8 @@ static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, De
     if (any_zero) *any_zero = __atomic_load_n(c->pub_host + 8, __ATOMIC_ACQUIRE) != 0;
     uint32_t inv_g[8];
     fr_store(fr_inv(G), inv_g);
-    ProfScope ps(c, "inv_pass2", (double)n * 96 + (double)nb * 256 * 32);
-    launch_inv_pass2(c->stream, S, n, bl, A, others, others_blk, inv_g);
+    ProfScope ps(c, "inv_pass2", (double)n * (aos ? 128 : 96) + (double)nb * 256 * 32);
+    launch_inv_pass2(c->stream, S, n, bl, A, others, others_blk, inv_g, aos);
     return 0;
 }
 extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t beta[8], zkh_tensor** A_out) {
@@ -2718,7 +2718,12 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
     // T_comb = T + r mapped (zkob_glu.cu:156) and its inverse (zkob_glu.cu:168-170)
     launch_axpy(c->stream, st, r, rm, sm, N, Tcomb->planes());
     bool tzero = false, czero = false;
-    if ((rc = batch_inverse(c, Tcomb->planes(), N, fr_load(beta), Binv->planes(), &tzero))) return drop(rc);
+    // the table inverse also as AoS for the gather's random reads (a table larger than the
+    // caches: one line per read instead of one per plane)
+    uint32_t* binv_aos = D ? (uint32_t*)scratch_slot(c, SL_TMP6, (size_t)N * 32, &rc) : nullptr;
+    if (rc) return drop(rc);
+    if ((rc = batch_inverse(c, Tcomb->planes(), N, fr_load(beta), Binv->planes(), &tzero, binv_aos)))
+        return drop(rc);
     uint32_t* flags = (uint32_t*)scratch_slot(c, SL_PARTIAL, 256, &rc);
     if (rc) return drop(rc);
     HIPCHK(c, hipMemsetAsync(flags, 0, 4, c->stream));
@@ -2731,7 +2736,7 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
         // a range table at this low: T[j] == G[i] iff G[i] - low is j < len, read from G alone
         const uint32_t tlen = range_shortcut_len(T, low);
         launch_lu_tuple_gather(c->stream, sg, D, lowl, st, tlen, S ? ss : sm, S != nullptr, N, r, rm, Binv->planes(),
-                               comb->planes(), A->planes(), flags);
+                               binv_aos, comb->planes(), A->planes(), flags);
     }
     if ((rc = settle(c, flags, &hf))) return drop(rc);
     if (hf & 1u) return drop(fail(c, ZKH_EARG, "lookup witness outside the table"));
