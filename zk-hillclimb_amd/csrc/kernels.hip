@@ -1204,6 +1204,12 @@ struct EqDev {
 };
 // device weight of index i (see EqW)
 ZDEV fr_t eq_w(const EqDev& eq, uint32_t i) { return mont_mul_ol(ld_aos(eq.elo, i & 1023), ld_aos(eq.ehi, i >> 10)); }
+// A thread whose pairs i = i0 + k s have a stride s that is a multiple of 1024 keeps one Elo
+// factor, Elo[i0 & 1023], for all of them: its weighted products can take Ehi[i >> 10] alone
+// (one product per pair less) and its weighted sums the Elo factor once at the end
+// (elo_scale).  Worth it from two pairs per thread on.
+ZDEV bool elo_factored(uint32_t h, uint32_t stride) { return (stride & 1023) == 0 && h >= 2 * stride; }
+ZDEV fr_t pair_w(const EqDev& eq, uint32_t i, bool ef) { return ef ? ld_aos(eq.ehi, i >> 10) : eq_w(eq, i); }
 
 #define SB() __builtin_amdgcn_sched_barrier(0)
 // the product x y as a field element (x 1): a Montgomery product lifted by 2^512
@@ -1229,6 +1235,12 @@ struct LdsAcc {
     ZDEV void get(fr_t* out) const {
 #pragma unroll
         for (int k = 0; k < K; k++) out[k] = ld_fr(lo + k * NT, hi + k * NT, threadIdx.x);
+    }
+    // slots [0, nk) times the thread's Elo factor (see elo_factored)
+    ZDEV void elo_scale(const EqDev& eq, uint32_t i0, int nk) {
+        const fr_t e = ld_aos(eq.elo, i0 & 1023);
+        for (int k = 0; k < nk; k++)
+            st_fr(lo + k * NT, hi + k * NT, threadIdx.x, mont_mul_ol(ld_fr(lo + k * NT, hi + k * NT, threadIdx.x), e));
     }
 };
 // Tree over the block's LDS accumulators: level s adds entry t + s into entry t (t < s) of
@@ -1415,6 +1427,7 @@ ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t&
     if constexpr (derive) {
         LdsAcc<3> acc{accl, acch};
         acc.zero();
+        const bool ef = elo_factored(h, g * NT);
         for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
             fr_t wa0, wda;
             {
@@ -1423,7 +1436,7 @@ ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t&
                 SB();
                 acc.add(2, a0);
                 SB();
-                const fr_t w = eq_w(eq, i);
+                const fr_t w = pair_w(eq, i, ef);
                 SB();
                 wa0 = mont_mul_ol(w, a0);
                 SB();
@@ -1438,6 +1451,7 @@ ZDEV void lu_phase2_as(const TabDev& A, const TabDev& S, uint32_t n, const fr_t&
             acc.add(1, mont_mul_ol(wda, fr_sub(s1, s0)));
             SB();
         }
+        if (ef) acc.elo_scale(eq, lb * NT + threadIdx.x, 2);
         reduce_publish_lds<3>(acc, pub, 0, 0, g, lb);
         return;
     }
@@ -1485,6 +1499,7 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
     if constexpr (derive) {
         LdsAcc<4> acc{accl, acch};
         acc.zero();
+        const bool ef = elo_factored(h, g * NT);
         for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
             fr_t b0, b1;
             load_pair(B, i, h, n, 1, vm, b0, b1);
@@ -1500,7 +1515,7 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
             SB();
             fr_t wb0, wdb;
             {
-                const fr_t w = eq_w(eq, i);
+                const fr_t w = pair_w(eq, i, ef);
                 SB();
                 wb0 = mont_mul_ol(w, b0);
                 SB();
@@ -1515,6 +1530,7 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
             acc.add(1, mont_mul_ol(wdb, fr_sub(t1, t0)));
             SB();
         }
+        if (ef) acc.elo_scale(eq, lb * NT + threadIdx.x, 2);
         reduce_publish_lds<4>(acc, pub, 1, ga, g, lb);
         return;
     }
@@ -2032,6 +2048,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
     __shared__ uint4 accl[K * NT], acch[K * NT];
     LdsAcc<K> acc{accl, acch};
     acc.zero();
+    const bool ef = fold && elo_factored(h, gridDim.x * NT);
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t s0, s1, u0, u1, w;
         if (fold) {
@@ -2041,7 +2058,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             st_fr(S.dlo, S.dhi, i + h, s1);
             SB();
             u0 = tab_fold_at(U, i, n, vm);
-            w = eq_w(eq, i);
+            w = pair_w(eq, i, ef);
             st_fr(U.dlo, U.dhi, i, u0);
             SB();
             u1 = tab_fold_at(U, i + h, n, vm);
@@ -2100,6 +2117,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             SB();
         }
     }
+    if (ef) acc.elo_scale(eq, blockIdx.x * NT + threadIdx.x, K);
     reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
