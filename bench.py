@@ -55,10 +55,12 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 LATENCY_BOUND = {"zkip_rounds"}
-# HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs
-# (profiles/eqdot_hbm_traffic_tinyllama.txt): the counters of a 256 MiB device copy read
-# 0.500x (FETCH) and 1.000x (WRITE) of its bytes, so FETCH is scaled by 2.
-TRAFFIC = {"eqdot": 315.4e6}
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs: the
+# counters of a 256 MiB device copy read 0.500x (FETCH) and 1.000x (WRITE) of its bytes, so
+# FETCH is scaled by 2.  eqdot: profiles/eqdot_hbm_traffic_tinyllama.txt (one launch per
+# matmul step); lu_phase2: profiles/swiglu_counters_tinyllama.txt (the 9 launches of the class
+# in one SwiGLU segment, 2450.0 MB, averaged per launch like bytes_per_launch).
+TRAFFIC = {"eqdot": 315.4e6, "lu_phase2": 272.2e6}
 
 
 def load_pkg():
@@ -906,6 +908,7 @@ def main():
         layer_roofline = {"bound": "hbm", "kernel": gdom, "achieved": round(gby / (gms / 1000.0) / 1e9, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gby / (gms / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+                          "traffic": TRAFFIC.get(gdom),
                           "bytes_per_launch": gby / max(gla, 1), "avg_launch_us": gms * 1000.0 / max(gla, 1),
                           "launches_per_segment": gla,
                           "scope": "dominant kernel class of the SwiGLU segment (the layer's largest), "
