@@ -1352,22 +1352,22 @@ ZDEV void lu_as_first_nz(const TabDev& A, const TabDev& S, uint32_t n, const EqD
     const uint32_t h = n >> 1;
     LdsAcc<3> acc{accl, acch};
     acc.zero();
+    const bool ef = elo_factored(h, g * NT);
     for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
         // every load of the iteration first: one wait for memory per pair
         const fr_t a0 = ld_fr(A.slo, A.shi, i), a1 = ld_fr(A.slo, A.shi, i + h);
         const fr_t s0 = ld_fr(S.slo, S.shi, i), s1 = ld_fr(S.slo, S.shi, i + h);
-        const fr_t elo = ld_aos(eq.elo, i & 1023), ehi = ld_aos(eq.ehi, i >> 10);
+        const fr_t w = pair_w(eq, i, ef);
         SB();
         acc.add(1, a0);
         acc.add(2, a1);
         const fr_t ds = fr_sub(s1, s0);
-        const fr_t w = mont_mul_ol(elo, ehi);
-        SB();
         const fr_t wda = mont_mul_ol(w, fr_sub(a1, a0));
         SB();
         acc.add(0, mont_mul_ol(wda, ds));
         SB();
     }
+    if (ef) acc.elo_scale(eq, lb * NT + threadIdx.x, 1);
     reduce_publish_lds<3>(acc, pub, 0, 0, g, lb);
 }
 ZDEV void lu_btm_first_nz(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const EqDev& eq, uint32_t lb,
@@ -1375,11 +1375,11 @@ ZDEV void lu_btm_first_nz(const TabDev& B, const TabDev& T, const TabDev& m, uin
     const uint32_t h = n >> 1;
     LdsAcc<4> acc{accl, acch};
     acc.zero();
+    const bool ef = elo_factored(h, g * NT);
     for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
         // every load of the iteration first: one wait for memory per pair
         const fr_t b0 = ld_fr(B.slo, B.shi, i), b1 = ld_fr(B.slo, B.shi, i + h);
         const fr_t t0 = ld_fr(T.slo, T.shi, i), t1 = ld_fr(T.slo, T.shi, i + h);
-        const fr_t elo = ld_aos(eq.elo, i & 1023), ehi = ld_aos(eq.ehi, i >> 10);
         const fr_t dt = fr_sub(t1, t0);
         {  // multiplicities are small integers: exact (x 1) by the 32-bit multiply
             const fr_t m0 = tab_ld(m, i), m1 = tab_ld(m, i + h);
@@ -1398,13 +1398,14 @@ ZDEV void lu_btm_first_nz(const TabDev& B, const TabDev& T, const TabDev& m, uin
             }
         }
         SB();
-        const fr_t w = mont_mul_ol(elo, ehi);
+        const fr_t w = pair_w(eq, i, ef);
         SB();
         const fr_t wdb = mont_mul_ol(w, fr_sub(b1, b0));
         SB();
         acc.add(0, mont_mul_ol(wdb, dt));
         SB();
     }
+    if (ef) acc.elo_scale(eq, lb * NT + threadIdx.x, 1);
     reduce_publish_lds<4>(acc, pub, 1, ga, g, lb);
 }
 // phase 2 (tlookup.cu:161-279 eval/sum/dotprod + reduce kernels, fused), one launch whose
@@ -1618,7 +1619,7 @@ __global__ __launch_bounds__(NT) void k_lu_phase1_first_nz(TabDev A, TabDev S, u
     lu_as_first_nz(A, S, n, eq, blockIdx.x, gridDim.x, pub, accl, acch);
 }
 // the first round of phase 2 when A and B have no zero entry: 32 KiB, 5 blocks per CU
-__global__ __launch_bounds__(NT) void k_lu_phase2_first_nz(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m,
+__global__ __launch_bounds__(NT, 5) void k_lu_phase2_first_nz(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m,
                                                            uint32_t n, EqDev eq, Publish pub, uint32_t ga,
                                                            uint32_t gb) {
     __shared__ uint4 accl[4 * NT], acch[4 * NT];
@@ -2048,7 +2049,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
     __shared__ uint4 accl[K * NT], acch[K * NT];
     LdsAcc<K> acc{accl, acch};
     acc.zero();
-    const bool ef = fold && elo_factored(h, gridDim.x * NT);
+    const bool ef = elo_factored(h, gridDim.x * NT);
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t s0, s1, u0, u1, w;
         if (fold) {
@@ -2087,7 +2088,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
                 // small_int's range (-2^30, 2^30): differences and their product stay exact
                 auto in30 = [](int32_t v) { return v > -(1 << 30) && v < (1 << 30); };
                 if (in30(a0) && in30(a1) && in30(b0) && in30(b1)) {
-                    w = eq_w(eq, i);
+                    w = pair_w(eq, i, ef);
                     acc.add(0, fr_mul_i64(w, (int64_t)a0 * b0));
                     acc.add(1, fr_mul_i64(w, (int64_t)a1 * b1));
                     acc.add(2, fr_mul_i64(w, (int64_t)(a1 - a0) * (b1 - b0)));
@@ -2099,7 +2100,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
             s1 = tab_ld(S, i + h);
             u0 = tab_ld(U, i);
             u1 = tab_ld(U, i + h);
-            w = eq_w(eq, i);
+            w = pair_w(eq, i, ef);
             SB();
             if (small_int(s0, a0) && small_int(s1, a1) && small_int(u0, b0) && small_int(u1, b1)) {
                 // the weight (e 2^256) times the exact 64-bit products: sums e s u 2^256
