@@ -90,7 +90,7 @@ int zkh_me(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* u, uint32_t k, uin
 /* zkh_me without device allocation.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (tight serving loops, harnesses that forbid hipMalloc,
  * a process between the captures of a HIP graph that must not grow the device heap).  Its
- * device scratch (eq tables, block partials, counters: 557,312 bytes) is one static array
+ * device scratch (eq tables, block partials, job layout: 557,312 bytes) is one static array
  * per device, held until the process ends and resolved at zkh_ctx_create; the call
  * allocates nothing.  It is synchronous: it runs on the context's stream and waits for its
  * result there (a host spin with hipStreamQuery), so the call itself cannot be recorded into

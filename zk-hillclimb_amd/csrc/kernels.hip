@@ -98,40 +98,43 @@ ZDEV void block_reduce_store(fr_t* acc, uint32_t* partial) {
     block_reduce_store_at<K>(acc, partial, blockIdx.x);
 }
 
-// Block partials -> job sums in pinned host memory -> completion flag (see Publish).
-// Every thread of the block must call it.  first/nblk: the job's block range.
+// A job's layout word triple (see Publish), written by the job's first block
+ZDEV void publish_layout(const Publish& P, uint32_t job, uint32_t first, uint32_t nblk, uint32_t K) {
+    P.layout[3 * job] = first;
+    P.layout[3 * job + 1] = nblk;
+    P.layout[3 * job + 2] = K;
+}
+// Block partials of a publishing kernel (see Publish); every thread of the block calls it.
+// first/nblk: the job's block range.
 template <int K>
 ZDEV void reduce_publish(fr_t* acc, const Publish& P, uint32_t job, uint32_t first, uint32_t nblk,
                          uint32_t local) {
-    __shared__ int is_last;
     block_reduce_store_at<K>(acc, P.part, first + local);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        is_last = atomicAdd(&P.counter[job], 1u) == nblk - 1;
+    if (local == 0 && threadIdx.x == 0) publish_layout(P, job, first, nblk, K);
+}
+// The publish kernel: wave w adds the partials of the job sums w, w + 16, ... (job j's
+// sum k at host_out[j K_j + k]), then thread 0 raises the host flag.
+#define NTPUB 1024
+__global__ __launch_bounds__(NTPUB) void k_publish(Publish P) {
+    const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint32_t tot = 0;
+    for (uint32_t j = 0; j < P.njobs; j++) tot += P.layout[3 * j + 2];
+    for (uint32_t q = wv; q < tot; q += NTPUB / 64) {
+        uint32_t j = 0, k = q;
+        while (k >= P.layout[3 * j + 2]) k -= P.layout[3 * j + 2], j++;
+        const uint32_t first = P.layout[3 * j], nblk = P.layout[3 * j + 1], K = P.layout[3 * j + 2];
+        fr_t t = fr_zero();
+        for (uint32_t b = lane; b < nblk; b += 64) t = fr_add(t, ld_aos(P.part, (first + b) * K + k));
+        t = fr_wave_sum(t);
+        if (lane == 0) st_aos(P.host_out, j * K + k, t);
     }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    fr_t s[K];
-#pragma unroll
-    for (int k = 0; k < K; k++) {  // one sum at a time (register budget, see above)
-        __builtin_amdgcn_sched_barrier(0);
-        s[k] = fr_zero();
-        for (uint32_t b = threadIdx.x; b < nblk; b += NT) s[k] = fr_add(s[k], ld_aos(P.part, (first + b) * K + k));
-    }
-    block_reduce_store_at<K>(s, P.host_out, job);
     __syncthreads();
     if (threadIdx.x == 0) {
         __threadfence_system();
-        P.counter[job] = 0;
-        if (atomicAdd(&P.counter[P.njobs], 1u) == P.njobs - 1) {
-            P.counter[P.njobs] = 0;
-            __threadfence_system();
-            __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
+        __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
+void launch_publish(hipStream_t s, const Publish& P) { k_publish<<<1, NTPUB, 0, s>>>(P); }
 
 // ------------------------------------------------------------------------------------
 // conversions and layout
@@ -310,16 +313,19 @@ __global__ __launch_bounds__(NT) void k_prod_round(const uint4* alo, const uint4
 uint32_t launch_prod_round(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t h, Publish pub) {
     uint32_t g = grid_for(h, NT * 4, 1024);
     k_prod_round<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), h, pub);
+    launch_publish(s, pub);
     return g;
 }
 uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub) {
     uint32_t g = grid_for(n, NT * 4, 1024);
     k_dot_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), n, pub);
+    launch_publish(s, pub);
     return g;
 }
 uint32_t launch_sum_planes(hipStream_t s, DevPlanes a, uint32_t n, Publish pub) {
     uint32_t g = grid_for(n, NT * 8, 1024);
     k_sum_planes<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), n, pub);
+    launch_publish(s, pub);
     return g;
 }
 
@@ -481,6 +487,7 @@ uint32_t launch_stk_round(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t N, u
                           const uint32_t* E, Publish pub) {
     const uint32_t g = grid_for(Nh * D, NT, 1024);
     k_stk_round<<<g, NT, 0, s>>>(PL_LO(a), PL_HI(a), PL_LO(b), PL_HI(b), N, D, Nh, E, pub);
+    launch_publish(s, pub);
     return g;
 }
 void launch_stk_fold(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t N, uint32_t D, uint32_t Nh,
@@ -1260,47 +1267,14 @@ ZDEV void lds_tree(const LdsAcc<K>& acc) {
     }
     __syncthreads();
 }
-// reduce_publish over LDS accumulators: the block's sums by an LDS tree; a job of one block
-// writes them to the host directly, otherwise the last block of the job adds the partials
-// (thread t takes blocks t, t + NT, ...) with the same tree.  Same completion protocol.
-// The last-block flag travels through entry 1 of plane 0, dead after the tree, so that the
-// block's LDS is exactly its accumulators (K = 4 at 256 threads: 32 KiB, 5 blocks per CU).
+// reduce_publish over LDS accumulators: the block's sums by an LDS tree (entry 0 of each
+// plane), then the partials and layout as reduce_publish.
 template <int K>
 ZDEV void reduce_publish_lds(const LdsAcc<K>& acc, const Publish& P, uint32_t job, uint32_t first, uint32_t nblk,
                              uint32_t local) {
-    static_assert(NT >= 2, "the flag needs a second entry");
     lds_tree<K>(acc);
-    if (nblk > 1) {
-        if (threadIdx.x < K) st_aos(P.part, (first + local) * K + threadIdx.x, ld_fr(acc.lo + threadIdx.x * NT, acc.hi + threadIdx.x * NT, 0));
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __threadfence();
-            acc.lo[1].x = atomicAdd(&P.counter[job], 1u) == nblk - 1;
-        }
-        __syncthreads();
-        const bool is_last = acc.lo[1].x != 0;
-        __syncthreads();  // every thread has the flag before the entries are reused
-        if (!is_last) return;
-        __threadfence();
-#pragma unroll
-        for (int k = 0; k < K; k++) {
-            fr_t t = fr_zero();
-            for (uint32_t b = threadIdx.x; b < nblk; b += NT) t = fr_add(t, ld_aos(P.part, (first + b) * K + k));
-            st_fr(acc.lo + k * NT, acc.hi + k * NT, threadIdx.x, t);
-        }
-        lds_tree<K>(acc);
-    }
-    if (threadIdx.x < K) st_aos(P.host_out, job * K + threadIdx.x, ld_fr(acc.lo + threadIdx.x * NT, acc.hi + threadIdx.x * NT, 0));
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence_system();
-        P.counter[job] = 0;
-        if (atomicAdd(&P.counter[P.njobs], 1u) == P.njobs - 1) {
-            P.counter[P.njobs] = 0;
-            __threadfence_system();
-            __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
-    }
+    if (threadIdx.x < K) st_aos(P.part, (first + local) * K + threadIdx.x, ld_fr(acc.lo + threadIdx.x * NT, acc.hi + threadIdx.x * NT, 0));
+    if (local == 0 && threadIdx.x == 0) publish_layout(P, job, first, nblk, K);
 }
 // the challenge of a relayed launch: false when the relay says the proof was abandoned
 ZDEV bool relayed_vm(const uint32_t* vmp, fr_t& vm) {
@@ -1370,6 +1344,9 @@ ZDEV void lu_as_first_nz(const TabDev& A, const TabDev& S, uint32_t n, const EqD
     if (ef) acc.elo_scale(eq, lb * NT + threadIdx.x, 1);
     reduce_publish_lds<3>(acc, pub, 0, 0, g, lb);
 }
+// M32: m is an int32 table (m.s32), its entries taken as integers directly; otherwise field
+// planes, whose small-integer entries take the same 32-bit multiply
+template <bool M32>
 ZDEV void lu_btm_first_nz(const TabDev& B, const TabDev& T, const TabDev& m, uint32_t n, const EqDev& eq, uint32_t lb,
                           uint32_t g, uint32_t ga, const Publish& pub, uint4* accl, uint4* acch) {
     const uint32_t h = n >> 1;
@@ -1381,8 +1358,14 @@ ZDEV void lu_btm_first_nz(const TabDev& B, const TabDev& T, const TabDev& m, uin
         const fr_t b0 = ld_fr(B.slo, B.shi, i), b1 = ld_fr(B.slo, B.shi, i + h);
         const fr_t t0 = ld_fr(T.slo, T.shi, i), t1 = ld_fr(T.slo, T.shi, i + h);
         const fr_t dt = fr_sub(t1, t0);
-        {  // multiplicities are small integers: exact (x 1) by the 32-bit multiply
-            const fr_t m0 = tab_ld(m, i), m1 = tab_ld(m, i + h);
+        if constexpr (M32) {  // multiplicities are small integers: exact (x 1) by the 32-bit multiply
+            const int64_t i0 = m.s32[i], i1 = m.s32[i + h];
+            SB();
+            acc.add(1, fr_mul_i64s(b0, i0));
+            acc.add(2, fr_mul_i64s(b1, i1));
+            acc.add(3, fr_mul_i64(fr_sub(b1, b0), i1 - i0));
+        } else {
+            const fr_t m0 = ld_fr(m.slo, m.shi, i), m1 = ld_fr(m.slo, m.shi, i + h);
             SB();
             int64_t i0, i1;
             if (fr_int32ish(m0, i0) && fr_int32ish(m1, i1)) {
@@ -1619,12 +1602,13 @@ __global__ __launch_bounds__(NT) void k_lu_phase1_first_nz(TabDev A, TabDev S, u
     lu_as_first_nz(A, S, n, eq, blockIdx.x, gridDim.x, pub, accl, acch);
 }
 // the first round of phase 2 when A and B have no zero entry: 32 KiB, 5 blocks per CU
+template <bool M32>
 __global__ __launch_bounds__(NT, 5) void k_lu_phase2_first_nz(TabDev A, TabDev S, TabDev B, TabDev T, TabDev m,
                                                            uint32_t n, EqDev eq, Publish pub, uint32_t ga,
                                                            uint32_t gb) {
     __shared__ uint4 accl[4 * NT], acch[4 * NT];
     if (blockIdx.x < ga) lu_as_first_nz(A, S, n, eq, blockIdx.x, ga, pub, accl, acch);
-    else lu_btm_first_nz(B, T, m, n, eq, blockIdx.x - ga, gb, ga, pub, accl, acch);
+    else lu_btm_first_nz<M32>(B, T, m, n, eq, blockIdx.x - ga, gb, ga, pub, accl, acch);
 }
 uint32_t launch_lu_first_nz(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint32_t n, int phase2, EqW eq,
                             Publish partial, const int32_t* m32) {
@@ -1632,12 +1616,15 @@ uint32_t launch_lu_first_nz(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, ui
     if (!phase2) {
         const uint32_t g = grid_for(n >> 1, NT, 1536);
         k_lu_phase1_first_nz<<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, e, partial);
+        launch_publish(s, partial);
         return g;
     }
     const uint32_t ga = grid_for(n >> 1, NT, 1280 * 2 / 5), gb = grid_for(n >> 1, NT, 1280 * 3 / 5);
     TabDev md = tab_dev(m);
     md.s32 = m32;
-    k_lu_phase2_first_nz<<<ga + gb, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), md, n, e, partial, ga, gb);
+    if (m32) k_lu_phase2_first_nz<true><<<ga + gb, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), md, n, e, partial, ga, gb);
+    else k_lu_phase2_first_nz<false><<<ga + gb, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), md, n, e, partial, ga, gb);
+    launch_publish(s, partial);
     return ga + gb;
 }
 uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
@@ -1650,6 +1637,7 @@ uint32_t launch_lu_phase1(hipStream_t s, Tab A, Tab S, uint32_t n, int fold,
     if (fold && derive) k_lu_phase1<1, 1><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, vmp, beta, e, partial, inv);
     else if (fold) k_lu_phase1<1, 0><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, vmp, beta, e, partial, inv);
     else k_lu_phase1<0, 0><<<g, NT, 0, s>>>(tab_dev(A), tab_dev(S), n, vm, vmp, beta, e, partial, inv);
+    launch_publish(s, partial);
     return g;
 }
 // ------------------------------------------------------------------------------------
@@ -1675,34 +1663,17 @@ struct Rows {
     ZDEV void st(uint32_t r, uint32_t p, const fr_t& x) const { st_fr(lo + r * P, hi + r * P, p, x); }
 };
 // The block's sums (wave w < nsum holds sum w of the block in lane 0, after fr_wave_sum)
-// go to the partials of their jobs; the last block adds every block's partials and
-// publishes all jobs at once.  Sum w belongs to job jw(w) as its entry kw(w) of K(jw)
-// (K = {k0, k1}, k1 = 0 for one job); job j's block b partial is part[(j g + b) K_j + k],
-// as reduce_publish_lds lays out two jobs of g blocks each.
-ZDEV void wide_publish(const fr_t& bsum, uint32_t nsum, uint32_t k0, const Publish& P, uint32_t* s_last) {
+// go to the partials of their jobs (see Publish).  Sum w belongs to job jw(w) as its entry
+// kw(w) of K(jw) (K = {k0, k1}, k1 = 0 for one job); job j's block b partial is
+// part[(j g + b) K_j + k], as reduce_publish_lds lays out two jobs of g blocks each.
+ZDEV void wide_publish(const fr_t& bsum, uint32_t nsum, uint32_t k0, const Publish& P) {
     const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63, g = gridDim.x, b = blockIdx.x;
     const uint32_t k1 = nsum - k0;
-    auto slot = [&](uint32_t w, uint32_t blk) { return w < k0 ? blk * k0 + w : (g + blk) * k1 + (w - k0); };
-    if (wv < nsum && lane == 0) st_aos(P.part, slot(wv, b), bsum);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        *s_last = atomicAdd(&P.counter[0], 1u) == g - 1;
-    }
-    __syncthreads();
-    if (!*s_last) return;
-    __threadfence();
-    if (wv < nsum) {
-        fr_t t = fr_zero();
-        for (uint32_t q = lane; q < g; q += 64) t = fr_add(t, ld_aos(P.part, slot(wv, q)));
-        t = fr_wave_sum(t);
-        if (lane == 0) st_aos(P.host_out, wv < k0 ? wv : k1 + (wv - k0), t);
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence_system();
-        P.counter[0] = 0;
-        __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (wv < nsum && lane == 0)
+        st_aos(P.part, wv < k0 ? b * k0 + wv : (g + b) * k1 + (wv - k0), bsum);
+    if (b == 0 && threadIdx.x == 0) {
+        publish_layout(P, 0, 0, g, k0);
+        if (k1) publish_layout(P, 1, g, g, k1);
     }
 }
 // sum of row r over the block's np entries, by wave (lane-strided, then the wave's tree)
@@ -1725,7 +1696,6 @@ __global__ __launch_bounds__(NTW) void k_lu_phase2_wide(TabDev A, TabDev S, TabD
     if (!relayed_vm(vmp, vm)) return;
     constexpr uint32_t P = LUW_P;
     __shared__ uint4 rlo[21 * P], rhi[21 * P];
-    __shared__ uint32_t s_last;
     const Rows<P> R{rlo, rhi};
     const uint32_t h = n >> 1, np = h < P ? h : P, base = blockIdx.x * P;
     for (uint32_t q = threadIdx.x; q < 11 * np; q += NTW) {  // level 1
@@ -1772,7 +1742,7 @@ __global__ __launch_bounds__(NTW) void k_lu_phase2_wide(TabDev A, TabDev S, TabD
         const uint32_t row = wv == 0 ? 17 : wv == 1 ? 18 : wv == 2 ? 0 : wv == 3 ? 19 : wv == 4 ? 20 : wv == 5 ? 15 : 16;
         bs = wide_row_sum<P>(R, row, np);
     }
-    wide_publish(bs, 7, 3, pub, &s_last);
+    wide_publish(bs, 7, 3, pub);
 }
 #ifndef HPW_P
 #define HPW_P 128
@@ -1784,7 +1754,6 @@ __global__ __launch_bounds__(NTW) void k_hp_eq_round_wide(TabDev S, TabDev U, ui
     if (!relayed_vm(vmp, vm)) return;
     constexpr uint32_t P = HPW_P;
     __shared__ uint4 rlo[9 * P], rhi[9 * P];
-    __shared__ uint32_t s_last;
     const Rows<P> R{rlo, rhi};
     const uint32_t h = n >> 1, np = h < P ? h : P, base = blockIdx.x * P;
     for (uint32_t q = threadIdx.x; q < 5 * np; q += NTW) {
@@ -1815,7 +1784,7 @@ __global__ __launch_bounds__(NTW) void k_hp_eq_round_wide(TabDev S, TabDev U, ui
     const uint32_t wv = threadIdx.x >> 6;
     fr_t bs = fr_zero();
     if (wv < 2) bs = wide_row_sum<P>(R, 7 + wv, np);
-    wide_publish(bs, 2, 2, pub, &s_last);
+    wide_publish(bs, 2, 2, pub);
 }
 // Hadamard with U = 1, folding, derived sums (k_hp_round_ones<1>): rows 0..3 the folded e0
 // e1 s0 s1, 4 e0 s0, 5 de ds; sums rows 4, 5
@@ -1824,7 +1793,6 @@ __global__ __launch_bounds__(NTW) void k_hp_ones_wide(TabDev E, TabDev S, uint32
     if (!relayed_vm(vmp, vm)) return;
     constexpr uint32_t P = HPW_P;
     __shared__ uint4 rlo[6 * P], rhi[6 * P];
-    __shared__ uint32_t s_last;
     const Rows<P> R{rlo, rhi};
     const uint32_t h = n >> 1, np = h < P ? h : P, base = blockIdx.x * P;
     for (uint32_t q = threadIdx.x; q < 4 * np; q += NTW) {
@@ -1846,7 +1814,7 @@ __global__ __launch_bounds__(NTW) void k_hp_ones_wide(TabDev E, TabDev S, uint32
     const uint32_t wv = threadIdx.x >> 6;
     fr_t bs = fr_zero();
     if (wv < 2) bs = wide_row_sum<P>(R, 4 + wv, np);
-    wide_publish(bs, 2, 2, pub, &s_last);
+    wide_publish(bs, 2, 2, pub);
 }
 // the wide kernels take rounds of at most 2^ZKH_WIDE_LG pairs
 #ifndef ZKH_WIDE_LG
@@ -1884,6 +1852,7 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
     if (fold_as && fold_btm && derive && wide_round(n)) {
         const uint32_t gw = ((n >> 1) + LUW_P - 1) / LUW_P;
         k_lu_phase2_wide<<<gw, NTW, 0, s>>>(a, sd, b, t, md, n, vm, vmp, beta, e, partial);
+        launch_publish(s, partial);
         return gw;
     }
     const uint32_t g = ga + gb;
@@ -1897,6 +1866,7 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
     } else if (fold_btm) LU2(0, 1, 0);
     else LU2(0, 0, 0);
 #undef LU2
+    launch_publish(s, partial);
     return g;
 }
 
@@ -1950,6 +1920,7 @@ uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n, int fol
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     if (fold && derive) k_hp_round<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, vmp, partial);
     else k_hp_round<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), tab_dev(U), n, fold, vm, vmp, partial);
+    launch_publish(s, partial);
     return g;
 }
 // U = 1 everywhere (the RoPE obligations' Hadamard): E_t S_t U_t = E_t S_t, a quadratic in t
@@ -2006,10 +1977,12 @@ uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold,
     if (fold && derive && wide_round(n)) {
         const uint32_t gw = ((n >> 1) + HPW_P - 1) / HPW_P;
         k_hp_ones_wide<<<gw, NTW, 0, s>>>(tab_dev(E), tab_dev(S), n, vm, vmp, partial);
+        launch_publish(s, partial);
         return gw;
     }
     if (fold && derive) k_hp_round_ones<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, 0);
     else k_hp_round_ones<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, s_int);
+    launch_publish(s, partial);
     return g;
 }
 // x as an integer in (-2^30, 2^30) when it is one (a field element or its negative)
@@ -2133,10 +2106,12 @@ uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
     if (fold && derive && wide_round(n)) {
         const uint32_t gw = ((n >> 1) + HPW_P - 1) / HPW_P;
         k_hp_eq_round_wide<<<gw, NTW, 0, s>>>(sd, ud, n, vm, vmp, e, partial);
+        launch_publish(s, partial);
         return gw;
     }
     if (fold && derive) k_hp_eq_round<1><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
     else k_hp_eq_round<0><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
+    launch_publish(s, partial);
     return g;
 }
 // sum_i eq(i, u[0..K)) S[i] (U[i]) over i < n, by chunks of 1024 indices sharing their
@@ -2184,6 +2159,7 @@ uint32_t launch_eq_sum_int(hipStream_t s, int kind, const void* S, uint32_t n, E
     EqDev e{eq.elo, eq.ehi, eq.K};
     if (kind == 1) k_eq_sum_int<<<g, NT, 0, s>>>((const int32_t*)S, n, e, partial);
     else k_eq_sum_int<<<g, NT, 0, s>>>((const int64_t*)S, n, e, partial);
+    launch_publish(s, partial);
     return g;
 }
 uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t n, EqW eq,
@@ -2192,6 +2168,7 @@ uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t 
     EqDev e{eq.elo, eq.ehi, eq.K};
     k_eq_sum<<<g, NT, 0, s>>>(PL_LO(S), PL_HI(S), U ? PL_LO(*U) : nullptr, U ? PL_HI(*U) : nullptr,
                               U ? 1 : 0, n, e, partial);
+    launch_publish(s, partial);
     return g;
 }
 
@@ -2670,6 +2647,7 @@ __global__ __launch_bounds__(NT) void k_zkip_round_multi(ZkipBatch bt, Publish p
 }
 void launch_zkip_round_multi(hipStream_t s, const ZkipBatch& b, uint32_t nblocks, Publish pub) {
     k_zkip_round_multi<<<nblocks, NT, 0, s>>>(b, pub);
+    launch_publish(s, pub);
 }
 // final binds of several 2-entry tables (t[0] += v*(t[1]-t[0]) when fold is set) and the
 // terminal values a[0], b[0] written to partial[0..1] (AoS)

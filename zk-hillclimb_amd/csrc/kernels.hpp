@@ -18,17 +18,22 @@ struct DevPlanes {
     uint32_t* hi() const { return base + 4 * (size_t)cap; }
 };
 
-// Round completion without a host synchronisation: every block writes its K partial
-// sums to `part` (device); the last block of a job (device-scope counter) reduces them and
-// writes the job's K sums to host_out (coherent pinned host memory); the last job to finish
-// stores `seq` into *host_flag (system-scope release), which the host spins on.
+// Round completion without a host synchronisation: every block of a publishing kernel
+// writes its K partial sums to `part` (device) and the first block of each job its layout
+// (first block, blocks, K) to `layout`; a one-block kernel queued right behind it
+// (launch_publish) adds each job's partials, writes the job's K sums to host_out (coherent
+// pinned host memory) and stores `seq` into *host_flag (system-scope release), which the
+// host spins on.  The kernel boundary orders the partials before their reads, so the
+// round kernel's blocks take no fence and no atomic.
 struct Publish {
     uint32_t* part;       // device, [total blocks][K] AoS
-    uint32_t* counter;    // device, njobs + 1 words, zero between launches
+    uint32_t* layout;     // device, 3 words per job
     uint32_t* host_out;   // pinned, [njobs][K] AoS
     uint32_t* host_flag;  // pinned
     uint32_t seq, njobs;
 };
+// the sums of a publishing kernel's jobs to the host (queue right behind that kernel)
+void launch_publish(hipStream_t s, const Publish& P);
 
 // A table in a fused fold+evaluate round: read from src; folded entries go to dst (which
 // may be src itself).  The first fold of a caller-owned table targets a scratch copy.
@@ -249,7 +254,8 @@ uint32_t launch_eq_sum(hipStream_t s, DevPlanes S, const DevPlanes* U, uint32_t 
                        Publish pub);
 
 // setup of the allocation-free MLE evaluation: copies `words` factor words (passed by value)
-// to fac_dst and zeroes ncnt completion counters, all inside caller-provided device memory
+// to fac_dst and zeroes ncnt words at cnt (its publish layout), all inside caller-provided
+// device memory
 #define ZKH_STATIC_MAX_VARS 24
 struct StaticFacArg {
     uint32_t w[ZKH_STATIC_MAX_VARS * 16];  // (1 - u_t, u_t) per variable, Montgomery form

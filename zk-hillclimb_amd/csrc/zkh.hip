@@ -237,11 +237,11 @@ struct zkh_ctx {
         size_t bytes = 0;
     };
     std::vector<Slot> slots;
-    // round completion (Publish): coherent pinned job sums + flag, device partials/counters
+    // round completion (Publish): coherent pinned job sums + flag, device partials/job layouts
     uint32_t* pub_host = nullptr;  // [ZKH_MAX_BATCH][11] Fr sums, then the flag word
     uint32_t* pub_part = nullptr;  // device partial sums (pub_part_cap Fr)
     size_t pub_part_cap = (size_t)4096 * 11;
-    uint32_t* pub_cnt = nullptr;   // device [ZKH_MAX_BATCH + 1]
+    uint32_t* pub_lay = nullptr;   // device [ZKH_MAX_BATCH][3] job layouts (see Publish)
     uint32_t pub_seq = 0;
     // relayed round launches: coherent pinned command (three quads; word 16: a relay's
     // timeout flag) and the device words the relay fills (challenge, abandon flag)
@@ -443,8 +443,8 @@ static void* scratch_slot(zkh_ctx* c, int slot, size_t bytes, int* rc) {
     return s.p;
 }
 // Device scratch of the allocation-free entry point zkh_me_static: its eq factor table, the
-// two eq tables (up to ZKH_STATIC_MAX_VARS variables), the block partials and completion
-// counters of its one reduction.  Every device holds its own copy, at its own address, for
+// two eq tables (up to ZKH_STATIC_MAX_VARS variables), the block partials and job layout of
+// its one reduction.  Every device holds its own copy, at its own address, for
 // the life of the process; host code uses only the address that hipGetSymbolAddress gives
 // for the current device (kept per device at context creation), never the array's name.
 // Calls that overlap on one device share the copy and race.
@@ -452,8 +452,8 @@ static constexpr size_t kStFac = 0;                                  // <= 24 x 
 static constexpr size_t kStElo = 4096;                               // 1024 Fr
 static constexpr size_t kStEhi = kStElo + 1024 * 32;                 // 2^(24-10) Fr
 static constexpr size_t kStPart = kStEhi + ((size_t)32 << (ZKH_STATIC_MAX_VARS - 10));  // 1024 Fr
-static constexpr size_t kStCnt = kStPart + 1024 * 32;               // 2 words (+ padding)
-static constexpr size_t kStBytes = kStCnt + 256;                     // 557,312 bytes
+static constexpr size_t kStLay = kStPart + 1024 * 32;               // 3 words (+ padding)
+static constexpr size_t kStBytes = kStLay + 256;                     // 557,312 bytes
 static __device__ __align__(256) uint8_t scratch[kStBytes];
 #define ZKH_MAX_DEVICES 64
 static uint8_t* g_static_scratch[ZKH_MAX_DEVICES];
@@ -529,7 +529,7 @@ static uint32_t* pub_flag(zkh_ctx* c) { return c->pub_host + ZKH_MAX_BATCH * 11 
 static Publish make_pub(zkh_ctx* c, uint32_t njobs) {
     Publish p;
     p.part = c->pub_part;
-    p.counter = c->pub_cnt;
+    p.layout = c->pub_lay;
     p.host_out = c->pub_host;
     p.host_flag = pub_flag(c);
     p.seq = ++c->pub_seq;
@@ -770,8 +770,8 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
     c->slots.resize(SL_COUNT);
     if (hipHostMalloc((void**)&c->pub_host, (ZKH_MAX_BATCH * 11 * 8 + 64) * 4, hipHostMallocCoherent) != hipSuccess ||
         hipMalloc((void**)&c->pub_part, (size_t)4096 * 11 * 32) != hipSuccess ||
-        hipMalloc((void**)&c->pub_cnt, (ZKH_MAX_BATCH + 1) * 4) != hipSuccess ||
-        hipMemset(c->pub_cnt, 0, (ZKH_MAX_BATCH + 1) * 4) != hipSuccess ||
+        hipMalloc((void**)&c->pub_lay, ZKH_MAX_BATCH * 3 * 4) != hipSuccess ||
+        hipMemset(c->pub_lay, 0, ZKH_MAX_BATCH * 3 * 4) != hipSuccess ||
         hipHostMalloc((void**)&c->relay_host, 64 * 4, hipHostMallocCoherent) != hipSuccess ||
         hipMalloc((void**)&c->relay_vm, 16 * 4) != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
@@ -805,7 +805,7 @@ extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
     if (c->pub_host) (void)hipHostFree(c->pub_host);
     if (c->ps_host) (void)hipHostFree(c->ps_host);
     if (c->pub_part) (void)hipFree(c->pub_part);
-    if (c->pub_cnt) (void)hipFree(c->pub_cnt);
+    if (c->pub_lay) (void)hipFree(c->pub_lay);
     if (c->relay_host) (void)hipHostFree(c->relay_host);
     if (c->relay_vm) (void)hipFree(c->relay_vm);
     for (auto& p : c->pending) {
@@ -1274,13 +1274,13 @@ extern "C" int zkh_me_static(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u,
     uint32_t* fac_d = (uint32_t*)(base + kStFac);
     uint32_t* elo = (uint32_t*)(base + kStElo);
     uint32_t* ehi = (uint32_t*)(base + kStEhi);
-    uint32_t* cnt = (uint32_t*)(base + kStCnt);
-    launch_static_setup(c->stream, fac, kmax * 16, fac_d, cnt, 2);
+    uint32_t* lay = (uint32_t*)(base + kStLay);
+    launch_static_setup(c->stream, fac, kmax * 16, fac_d, lay, 3);
     launch_eq_mont(c->stream, fac_d, 10, 1024, elo);
     launch_eq_mont(c->stream, fac_d + 2 * 10 * 8, khi, 1u << khi, ehi);
     Publish pb = make_pub(c, 1);
     pb.part = (uint32_t*)(base + kStPart);  // launch_eq_sum uses at most 1024 blocks
-    pb.counter = cnt;
+    pb.layout = lay;
     launch_eq_sum(c->stream, t->planes(), nullptr, t->n, EqW{elo, ehi, k}, pb);
     int rc;
     if ((rc = wait_pub(c, pb.seq))) return rc;
