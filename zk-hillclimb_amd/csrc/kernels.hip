@@ -112,23 +112,52 @@ ZDEV void reduce_publish(fr_t* acc, const Publish& P, uint32_t job, uint32_t fir
     block_reduce_store_at<K>(acc, P.part, first + local);
     if (local == 0 && threadIdx.x == 0) publish_layout(P, job, first, nblk, K);
 }
-// The publish kernel: wave w adds the partials of the job sums w, w + 16, ... (job j's
-// sum k at host_out[j K_j + k]), then thread 0 raises the host flag.
+// The publish kernel: W = 16 / (job sums) waves (at least 1) per sum, each adding every
+// W-th run of 64 block partials with four loads in flight per lane, then the W wave sums of
+// each sum in LDS (job j's sum k to host_out[j K_j + k]); thread 0 raises the host flag.
 #define NTPUB 1024
+ZDEV void pub_locate(const Publish& P, uint32_t q, uint32_t& j, uint32_t& k) {
+    j = 0;
+    k = q;
+    while (k >= P.layout[3 * j + 2]) k -= P.layout[3 * j + 2], j++;
+}
 __global__ __launch_bounds__(NTPUB) void k_publish(Publish P) {
+    constexpr uint32_t NW = NTPUB / 64;
+    __shared__ fr_t red[NW];
     const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     uint32_t tot = 0;
     for (uint32_t j = 0; j < P.njobs; j++) tot += P.layout[3 * j + 2];
-    for (uint32_t q = wv; q < tot; q += NTPUB / 64) {
-        uint32_t j = 0, k = q;
-        while (k >= P.layout[3 * j + 2]) k -= P.layout[3 * j + 2], j++;
-        const uint32_t first = P.layout[3 * j], nblk = P.layout[3 * j + 1], K = P.layout[3 * j + 2];
+    const uint32_t W = tot >= NW || tot == 0 ? 1 : NW / tot, per = NW / W;  // waves per sum, sums per pass
+    for (uint32_t q0 = 0; q0 < tot; q0 += per) {
+        const uint32_t q = q0 + wv / W, share = wv % W;
         fr_t t = fr_zero();
-        for (uint32_t b = lane; b < nblk; b += 64) t = fr_add(t, ld_aos(P.part, (first + b) * K + k));
+        if (wv < per * W && q < tot) {
+            uint32_t j, k;
+            pub_locate(P, q, j, k);
+            const uint32_t first = P.layout[3 * j], nblk = P.layout[3 * j + 1], K = P.layout[3 * j + 2];
+            const uint32_t step = 64 * W;
+            for (uint32_t b = share * 64 + lane; b < nblk; b += 4 * step) {
+                fr_t x[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t bb = b + u * step;
+                    x[u] = bb < nblk ? ld_aos(P.part, (first + bb) * K + k) : fr_zero();
+                }
+                t = fr_add(t, fr_add(fr_add(x[0], x[1]), fr_add(x[2], x[3])));
+            }
+        }
         t = fr_wave_sum(t);
-        if (lane == 0) st_aos(P.host_out, j * K + k, t);
+        if (lane == 0) red[wv] = t;
+        __syncthreads();
+        if (threadIdx.x < per && q0 + threadIdx.x < tot) {
+            fr_t sum = red[threadIdx.x * W];
+            for (uint32_t w = 1; w < W; w++) sum = fr_add(sum, red[threadIdx.x * W + w]);
+            uint32_t j, k;
+            pub_locate(P, q0 + threadIdx.x, j, k);
+            st_aos(P.host_out, j * P.layout[3 * j + 2] + k, sum);
+        }
+        __syncthreads();
     }
-    __syncthreads();
     if (threadIdx.x == 0) {
         __threadfence_system();
         __hip_atomic_store(P.host_flag, P.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -1225,6 +1254,17 @@ ZDEV fr_t exact_mul(const fr_t& x, const fr_t& y) { return mont_mul_ol(mont_mul_
 #ifndef LU2_GRID
 #define LU2_GRID 1536
 #endif
+// blocks of the derived (folding) logUp phase-2 round, the first phase-2 round with no zero
+// inverse, and the folding eq-form Hadamard round
+#ifndef ZKH_LU2D_GRID
+#define ZKH_LU2D_GRID 1280
+#endif
+#ifndef ZKH_NZ_GRID
+#define ZKH_NZ_GRID 1280
+#endif
+#ifndef ZKH_HPE_GRID
+#define ZKH_HPE_GRID 1280
+#endif
 // Per-thread field accumulators kept in LDS (limb-quad planes, 16-byte lanes): registers
 // then hold only the current stage's operands, which lifts the round kernels' occupancy.
 template <int K>
@@ -1619,7 +1659,7 @@ uint32_t launch_lu_first_nz(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, ui
         launch_publish(s, partial);
         return g;
     }
-    const uint32_t ga = grid_for(n >> 1, NT, 1280 * 2 / 5), gb = grid_for(n >> 1, NT, 1280 * 3 / 5);
+    const uint32_t ga = grid_for(n >> 1, NT, ZKH_NZ_GRID * 2 / 5), gb = grid_for(n >> 1, NT, ZKH_NZ_GRID * 3 / 5);
     TabDev md = tab_dev(m);
     md.s32 = m32;
     if (m32) k_lu_phase2_first_nz<true><<<ga + gb, NT, 0, s>>>(tab_dev(A), tab_dev(S), tab_dev(B), tab_dev(T), md, n, e, partial, ga, gb);
@@ -1841,7 +1881,7 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
                           int fold_btm, const uint32_t* v_m_host, const uint32_t* vmp, const uint32_t* beta_host,
                           EqW eq, Publish partial, int inv_as, int inv_btm, int derive, const int32_t* m32) {
     // the derived variant holds 5 blocks per CU (32 KiB of accumulators): one resident wave
-    const uint32_t G = derive && fold_as && fold_btm ? 1280 : LU2_GRID;
+    const uint32_t G = derive && fold_as && fold_btm ? ZKH_LU2D_GRID : LU2_GRID;
     const uint32_t ga = grid_for(n >> 1, NT, G * 2 / 5), gb = grid_for(n >> 1, NT, G * 3 / 5);
     const fr_t vm = (fold_as || fold_btm) && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
@@ -2013,8 +2053,10 @@ ZDEV bool small_int(const fr_t& x, int32_t& out) {
 // as exact field products weighted to the same factor).
 // derive (folding rounds): sum w s1 u1 is left out (the host takes it from the previous
 // round's claim, q(0)(1 - u) + q(1) u)
+// the folding form holds 5 waves per SIMD (16 KiB of accumulators, <= 96 VGPRs), the first
+// round 4 (its 64-bit products take more registers)
 template <int derive>
-__global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
+__global__ __attribute__((amdgpu_flat_work_group_size(1, NT), amdgpu_waves_per_eu(derive ? 5 : 4))) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
                                                     const uint32_t* vmp, EqDev eq, Publish pub) {
     if (!relayed_vm(vmp, vm)) return;
     const uint32_t h = n >> 1;
@@ -2097,7 +2139,7 @@ __global__ __launch_bounds__(NT) void k_hp_eq_round(TabDev S, TabDev U, uint32_t
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial, int derive,
                             const int32_t* s32, const int32_t* u32) {
-    const uint32_t g = grid_for(n >> 1, NT, fold && derive ? 1280 : 1024);
+    const uint32_t g = grid_for(n >> 1, NT, fold && derive ? ZKH_HPE_GRID : 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
     EqDev e{eq.elo, eq.ehi, eq.K};
     TabDev sd = tab_dev(S), ud = tab_dev(U);
