@@ -2859,6 +2859,25 @@ static void trace_persist(zkh_ctx* c, const char* what, const uint32_t* slot0, u
     }
     fprintf(stderr, "\n");
 }
+// eq(i, u[0..K)) for i < h (h a power of two, log2 h <= K): the factor (1 - u_j) of every bit
+// j >= log2 h that i leaves 0, times the table of the low bits built one bit at a time
+// (K - log2 h + 2h - 2 products instead of h K)
+static void eq_low_weights(const std::vector<Fr>& u, uint32_t K, uint32_t h, std::vector<Fr>& w) {
+    uint32_t lg = 0;
+    while ((1u << lg) < h) lg++;
+    Fr base = kOne;
+    for (uint32_t j = lg; j < K; j++) base = fr_mul(base, fr_sub(kOne, u[j]));
+    w.assign(h, kZero);
+    w[0] = base;
+    for (uint32_t j = 0; j < lg; j++) {
+        const uint32_t half = 1u << j;
+        const Fr one_m = fr_sub(kOne, u[j]);
+        for (uint32_t i = 0; i < half; i++) {
+            w[i + half] = fr_mul(w[i], u[j]);
+            w[i] = fr_mul(w[i], one_m);
+        }
+    }
+}
 static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0, uint32_t n, const DevPlanes src[5],
                              bool fold_as, bool fold_btm, const uint32_t vm[8], const uint32_t beta_l[8],
                              uint32_t* ev_out, uint32_t* ws_out, Fr fin[5]) {
@@ -3020,9 +3039,10 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
         Fr sm[11];
         for (int q = 0; q < 11; q++) sm[q] = kZero;
         const std::vector<Fr>& A = t[0], &S = t[1], &B = t[2], &T = t[3], &M = t[4];
+        std::vector<Fr> wl;
+        eq_low_weights(*L.u, K, h, wl);
         for (uint32_t i = 0; i < h; i++) {
-            Fr w = kOne;
-            for (uint32_t j = 0; j < K; j++) w = fr_mul(w, ((i >> j) & 1) ? (*L.u)[j] : fr_sub(kOne, (*L.u)[j]));
+            const Fr w = wl[i];
             const Fr wa0 = fr_mul(w, A[i]), wda = fr_mul(w, fr_sub(A[i + h], A[i]));
             const Fr wb0 = fr_mul(w, B[i]), wdb = fr_mul(w, fr_sub(B[i + h], B[i]));
             const Fr add[11] = {fr_mul(wa0, fr_add(S[i], beta)), fr_mul(fr_add(wa0, wda), fr_add(S[i + h], beta)),
@@ -3966,13 +3986,15 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
     for (uint32_t r = r0 + R, m = nb; m > 1; r++, m >>= 1) {
         const uint32_t h = m >> 1, K = k - r - 1;
         Fr sums[4] = {kZero, kZero, kZero, kZero};
+        std::vector<Fr> wl;
+        if (!em) eq_low_weights(*u, K, h, wl);
         for (uint32_t i = 0; i < h; i++) {
             Fr w = kOne, de = kZero;
             if (em) {
                 w = te[i];
                 de = fr_sub(te[i + h], te[i]);
             } else {
-                for (uint32_t j = 0; j < K; j++) w = fr_mul(w, ((i >> j) & 1) ? (*u)[j] : fr_sub(kOne, (*u)[j]));
+                w = wl[i];
             }
             const Fr ds = fr_sub(ta[i + h], ta[i]), du = fr_sub(tb[i + h], tb[i]);
             Fr st = ta[i], ut = tb[i];
