@@ -593,6 +593,23 @@ ZDEV fr_t tab_fold_at(const TabDev& t, uint32_t j, uint32_t n, const fr_t& vm) {
     const fr_t x = fr_from_i64(t.s32[j]), y = fr_from_i64(t.s32[j + n]);
     return fr_add(x, mont_mul_ol(vm, fr_sub(y, x)));
 }
+// The same with the challenge also plain (vp = v, wave-uniform): an int32 table folds as
+// x + v (y - x) by the 32-bit multiply (|y - x| < 2^32), about 70 instructions instead of a
+// Montgomery product's 332
+ZDEV fr_t tab_fold_at(const TabDev& t, uint32_t j, uint32_t n, const fr_t& vm, const fr_t& vp) {
+    if (!t.s32) return fold_at(t.slo, t.shi, j, n, vm);
+    const int32_t x = t.s32[j], y = t.s32[j + n];
+    return fr_add(fr_from_i64(x), fr_mul_i64s(vp, (int64_t)y - x));
+}
+// the plain challenge of a relayed or passed vm (Montgomery form), in scalar registers
+ZDEV fr_t plain_uniform(const fr_t& vm) {
+    fr_t one = fr_zero();
+    one.v[0] = 1;
+    fr_t v = mont_mul_ol(vm, one);
+#pragma unroll
+    for (int k = 0; k < 8; k++) v.v[k] = __builtin_amdgcn_readfirstlane(v.v[k]);
+    return v;
+}
 static inline TabDev tab_dev(const Tab& t) {
     return TabDev{reinterpret_cast<const uint4*>(t.src.lo()), reinterpret_cast<const uint4*>(t.src.hi()),
                   reinterpret_cast<uint4*>(t.dst.lo()), reinterpret_cast<uint4*>(t.dst.hi()), nullptr};
@@ -606,6 +623,20 @@ ZDEV void load_pair(const TabDev& t, uint32_t i, uint32_t h, uint32_t n, int fol
         st_fr(t.dlo, t.dhi, i, x0);
         __builtin_amdgcn_sched_barrier(0);  // one fold's temporaries at a time
         x1 = tab_fold_at(t, i + h, n, vm);
+        st_fr(t.dlo, t.dhi, i + h, x1);
+    } else {
+        x0 = tab_ld(t, i);
+        x1 = tab_ld(t, i + h);
+    }
+}
+// the same with the plain challenge for an int32 table's fold (see tab_fold_at)
+ZDEV void load_pair(const TabDev& t, uint32_t i, uint32_t h, uint32_t n, int fold, const fr_t& vm, const fr_t& vp,
+                    fr_t& x0, fr_t& x1) {
+    if (fold) {
+        x0 = tab_fold_at(t, i, n, vm, vp);
+        st_fr(t.dlo, t.dhi, i, x0);
+        __builtin_amdgcn_sched_barrier(0);
+        x1 = tab_fold_at(t, i + h, n, vm, vp);
         st_fr(t.dlo, t.dhi, i + h, x1);
     } else {
         x0 = tab_ld(t, i);
@@ -1524,13 +1555,14 @@ ZDEV void lu_phase2_btm(const TabDev& B, const TabDev& T, const TabDev& m, uint3
         LdsAcc<4> acc{accl, acch};
         acc.zero();
         const bool ef = elo_factored(h, g * NT);
+        const fr_t vp = m.s32 ? plain_uniform(vm) : fr_zero();  // m's first fold
         for (uint32_t i = lb * NT + threadIdx.x; i < h; i += g * NT) {
             fr_t b0, b1;
             load_pair(B, i, h, n, 1, vm, b0, b1);
             SB();
             {
                 fr_t m0, m1;
-                load_pair(m, i, h, n, 1, vm, m0, m1);
+                load_pair(m, i, h, n, 1, vm, vp, m0, m1);
                 SB();
                 acc.add(2, mont_mul_ol(m0, b0));
                 SB();
@@ -2065,19 +2097,20 @@ __global__ __attribute__((amdgpu_flat_work_group_size(1, NT), amdgpu_waves_per_e
     LdsAcc<K> acc{accl, acch};
     acc.zero();
     const bool ef = elo_factored(h, gridDim.x * NT);
+    const fr_t vp = fold && (S.s32 || U.s32) ? plain_uniform(vm) : fr_zero();  // int32 tables' first fold
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t s0, s1, u0, u1, w;
         if (fold) {
-            s0 = tab_fold_at(S, i, n, vm);
-            s1 = tab_fold_at(S, i + h, n, vm);
+            s0 = tab_fold_at(S, i, n, vm, vp);
+            s1 = tab_fold_at(S, i + h, n, vm, vp);
             st_fr(S.dlo, S.dhi, i, s0);
             st_fr(S.dlo, S.dhi, i + h, s1);
             SB();
-            u0 = tab_fold_at(U, i, n, vm);
+            u0 = tab_fold_at(U, i, n, vm, vp);
             w = pair_w(eq, i, ef);
             st_fr(U.dlo, U.dhi, i, u0);
             SB();
-            u1 = tab_fold_at(U, i + h, n, vm);
+            u1 = tab_fold_at(U, i + h, n, vm, vp);
             st_fr(U.dlo, U.dhi, i + h, u1);
             SB();
             const fr_t ws = mont_mul_ol(w, s0);
