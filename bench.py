@@ -247,9 +247,9 @@ class RopeJob:
         outs = []
         for lab, W, S in (("c1", self.W1, self.T), ("c2", self.W2, self.Tx)):
             E = c.hadamard(Eu, W)
-            claim = c.sum(c.hadamard(E, S))
-            zkh.absorb(st, lab, claim.tobytes())
-            hp = c.hp_prove(st, claim, E, S, self.ONE)
+            # the claim sum(E S U) and its absorb inside the call, taken from the first round's
+            # sums (same transcript bytes as the product, its sum and the absorb before hp_prove)
+            hp = c.hp_prove_claim(st, lab, E, S, self.ONE)
             zkh.absorb(st, "S_f2", hp["term"][0].tobytes())
             zkh.absorb(st, "U_f2", hp["term"][1].tobytes())
             outs.append(hp["ev"].tobytes() + hp["term"].tobytes())

@@ -287,6 +287,15 @@ int zkh_hp_prove(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
 int zkh_hp_prove_eq(zkh_ctx* ctx, uint8_t transcript[32], const uint32_t claim[8],
                     const uint32_t* u, uint32_t k, const zkh_tensor* S, const zkh_tensor* U,
                     uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out);
+/* No single counterpart in the reference: zkob_rope.cu:230-238 (and :268-275) in one call --
+ * the claim c = (E * S * U).sum(), its absorb under `label`, then fs_hadamard over E, S, U.
+ * The claim comes from the first round's sums (q(0) + q(1) = c), so the products E * S * U
+ * are never formed; claim_out receives it.  Transcript, ev_out, term_out and ws_out are
+ * byte-identical to zkh_sum(zkh_hadamard(zkh_hadamard(S, U), E)) + zkh_transcript_absorb(
+ * label, c) + zkh_hp_prove.  With ZKH_XCHECK=1 the claim is also recomputed by that sum. */
+int zkh_hp_prove_claim(zkh_ctx* ctx, uint8_t transcript[32], const char* label, const zkh_tensor* E,
+                       const zkh_tensor* S, const zkh_tensor* U, uint32_t claim_out[8], uint32_t* ev_out,
+                       uint32_t* term_out, uint32_t* ws_out);
 /* No single counterpart in the reference: zkob_glu.cu:231-247's claim_H = H(u) of H = S * U
  * (multi_dim_me), its absorb under `label`, then fs_hadamard, in one call.  The claim
  * sum eq(i, u) S[i] U[i] comes from the first round's own sums (q(0) + q(1) of the round

@@ -1053,6 +1053,57 @@ def test_hp_prove_eq_small_ints(zkh, ctx, k, bits):
     assert bytes(st_g) == bytes(st_o)
 
 
+@pytest.mark.parametrize("k,form,no_persist", [(0, "ones", False), (5, "ones", False), (13, "gen", False),
+                                               (14, "ones", False), (14, "gen", False), (15, "ones_i32", False),
+                                               (14, "ones", True), (17, "ones_i32", False)])
+def test_hp_prove_claim(zkh, ctx, k, form, no_persist, monkeypatch):
+    """c = (E * S * U).sum(), its absorb, then fs_hadamard in one call (zkob_rope.cu:230-238):
+    the claim from the first round's sums (k >= 14, or every k with no persistent loop) or the
+    products' sum ahead of the persistent loop (k <= 13).  U all ones as an int32 tensor (the
+    RoPE form, S as field elements or int32 at the ends of its range) or a general U.  Claim,
+    proof and transcript equal the separate steps' (hadamard, sum, absorb, hp_prove) and, up
+    to 2^15, the oracle's."""
+    n = 1 << k
+    rng = np.random.default_rng(900 + k + 7 * len(form))
+    if no_persist:
+        monkeypatch.setenv("ZKH_NO_PERSIST", "1")
+    E = rand_fr_full(rng, n)
+    if form == "ones_i32":
+        Sv = rng.integers(-2**31, 2**31, size=n)
+        Sv[:4] = [-2**31, 2**31 - 1, 0, -1][:n]
+        S_f = C.ints_to_fr(Sv)
+        S_t = ctx.from_i32(Sv.astype(np.int32))
+    else:
+        S_f = rand_fr_full(rng, n)
+        S_t = ctx.from_fr(S_f)
+    if form == "gen":
+        U_f = rand_fr_full(rng, n)
+        U_t = ctx.from_fr(U_f)
+    else:
+        U_f = C.ints_to_fr(np.ones(n, np.int64))
+        U_t = ctx.from_i32(np.ones(n, np.int32))
+    E_t = ctx.from_fr(E)
+    st1, st_o = seed_transcript(zkh, "hpc:%d:%s" % (k, form))
+    st2 = st1.copy()
+    got = ctx.hp_prove_claim(st1, "c1", E_t, S_t, U_t)
+    claim = ctx.sum(ctx.hadamard(E_t, ctx.hadamard(S_t, U_t)))
+    zkh.absorb(st2, "c1", claim.tobytes())
+    want = ctx.hp_prove(st2, claim, E_t, S_t, U_t)
+    assert fr_eq(got["claim"], claim)
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st1) == bytes(st2)
+    if k <= 15:
+        Ei, Si, Ui = C.fr_to_ints(E), C.fr_to_ints(S_f), C.fr_to_ints(U_f)
+        oc = C.ints_to_fr([sum(a * b % P.R * c for a, b, c in zip(Ei, Si, Ui)) % P.R])[0]
+        assert fr_eq(got["claim"], oc)
+        C.tr_absorb(st_o, "c1", oc.tobytes())
+        rc, hp = C.hp_prove(st_o, oc, E, S_f, U_f)
+        assert rc == 0
+        assert fr_eq(got["ev"], hp["ev"]) and fr_eq(got["term"], hp["term"])
+        assert bytes(st1) == bytes(st_o)
+
+
 @pytest.mark.parametrize("k,kind,no_persist", [(0, "i32", False), (0, "i32", True), (6, "i32", False),
                                                (13, "i32", False), (14, "i32", False), (14, "fr", False),
                                                (18, "i32", False)])

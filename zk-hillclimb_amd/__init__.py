@@ -90,6 +90,7 @@ def lib():
         L.zkh_hp_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_hp_prove_eq.argtypes = [vp, vp, vp, vp, u32, vp, vp, vp, vp, vp]
         L.zkh_hp_prove_eq_claim.argtypes = [vp, vp, ctypes.c_char_p, vp, u32, vp, vp, vp, vp, vp, vp]
+        L.zkh_hp_prove_claim.argtypes = [vp, vp, ctypes.c_char_p, vp, vp, vp, vp, vp, vp, vp]
         L.zkh_mm_prove_batch.argtypes = [vp, vp, u32]
         L.zkh_prof_enable.argtypes = [vp, ctypes.c_int]
         L.zkh_prof_get.argtypes = [vp, ctypes.c_char_p, vp, vp, vp]
@@ -510,6 +511,18 @@ class Context:
         self._chk(lib().zkh_hp_prove_eq(self.h, _p(st), _p(claim), _p(u), k, S.h, U.h, _p(ev),
                                         _p(term), _p(ws)))
         return dict(ev=ev[:4 * k], term=term, ws=ws[:k])
+
+    def hp_prove_claim(self, st, label, E, S, U):
+        """claim = sum E[i] S[i] U[i] absorbed under label, then hp_prove, in one call (the claim
+        from the first round's sums; zkob_rope.cu:230-238)."""
+        k = ceil_log2(S.n)
+        claim = np.zeros(8, np.uint32)
+        ev = np.zeros((4 * k + 1, 8), np.uint32)
+        term = np.zeros((3, 8), np.uint32)
+        ws = np.zeros((k + 1, 8), np.uint32)
+        self._chk(lib().zkh_hp_prove_claim(self.h, _p(st), label.encode(), E.h, S.h, U.h, _p(claim), _p(ev),
+                                           _p(term), _p(ws)))
+        return dict(claim=claim, ev=ev[:4 * k], term=term, ws=ws[:k])
 
     def hp_prove_eq_claim(self, st, label, u, S, U):
         """claim = sum eq(u, i) S[i] U[i] absorbed under label, then hp_prove_eq, in one call

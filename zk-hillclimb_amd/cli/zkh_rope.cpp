@@ -118,7 +118,7 @@ int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& 
             for (uint32_t e = 0; e < C; e++) yo[(size_t)t * C + e] = Yg[(size_t)t * Cp + e];
         write_all(a[10], yo.data(), yo.size() * 8);
     }
-    Tensor tT, tTx, tW1, tW2, tY, tU, Eu, E1, E2, P1, P2;
+    Tensor tT, tTx, tW1, tW2, tY, tU, Eu, E1, E2;
     Points g, cT, cY;
     chk(zkh_tensor_from_i32(g_ctx, Tg.data(), D, &tT.t), "T");
     chk(zkh_tensor_from_i32(g_ctx, Txg.data(), D, &tTx.t), "Tx");
@@ -151,14 +151,12 @@ int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& 
     write_all(obdir + "/ev.bin", ev, 32);
     chk(zkh_eq_table(g_ctx, u.data(), logD, &Eu.t), "eq(u)");
 
-    // hadamard 1: E = eq(u).W1, S = T, U = 1
+    // hadamard 1: E = eq(u).W1, S = T, U = 1; c1 = sum E S U absorbed, then the sumcheck
+    // (zkob_rope.cu:230-238), the claim taken from the first round's sums
     uint32_t c1[8], c2[8];
     chk(zkh_hadamard(g_ctx, Eu.t, tW1.t, &E1.t), "E1");
-    chk(zkh_hadamard(g_ctx, E1.t, tT.t, &P1.t), "E1 T");
-    chk(zkh_sum(g_ctx, P1.t, c1), "c1");
-    absorb(st, "c1", c1, 32);
     std::vector<uint32_t> hev((size_t)4 * logD * 8 + 8), hterm(24), hws((size_t)logD * 8 + 8);
-    int rc = zkh_hp_prove(g_ctx, st, c1, E1.t, tT.t, tU.t, hev.data(), hterm.data(), hws.data());
+    int rc = zkh_hp_prove_claim(g_ctx, st, "c1", E1.t, tT.t, tU.t, c1, hev.data(), hterm.data(), hws.data());
     if (rc == 2) throw Err(1, "hadamard 1 round inconsistency");
     chk(rc, "hadamard 1");
     absorb(st, "S_f2", hterm.data(), 32);
@@ -190,10 +188,7 @@ int do_prove(const std::vector<std::string>& a, const std::vector<std::string>& 
 
     // hadamard 2: E = eq(u).W2, S = column-flipped T, U = 1
     chk(zkh_hadamard(g_ctx, Eu.t, tW2.t, &E2.t), "E2");
-    chk(zkh_hadamard(g_ctx, E2.t, tTx.t, &P2.t), "E2 Tx");
-    chk(zkh_sum(g_ctx, P2.t, c2), "c2");
-    absorb(st, "c2", c2, 32);
-    rc = zkh_hp_prove(g_ctx, st, c2, E2.t, tTx.t, tU.t, hev.data(), hterm.data(), hws.data());
+    rc = zkh_hp_prove_claim(g_ctx, st, "c2", E2.t, tTx.t, tU.t, c2, hev.data(), hterm.data(), hws.data());
     if (rc == 2) throw Err(1, "hadamard 2 round inconsistency");
     chk(rc, "hadamard 2");
     absorb(st, "S_f2", hterm.data(), 32);

@@ -4024,10 +4024,22 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
     }
     return 0;
 }
-// claim_label (eq form only): the claim is not given but is sum eq(i, u) S[i] U[i], taken
-// from the first round's sums (q(0) + q(1) of the round's polynomial in t, which the check
-// below compares with the claim) and absorbed under that label before the first round's
-// evaluations; claim_out receives it
+// sum_i E[i] S[i] U[i] by the elementwise products and a sum (zkob_rope.cu:232)
+static int explicit_claim(zkh_ctx* c, const zkh_tensor* E, const zkh_tensor* S, const zkh_tensor* U, Fr* out) {
+    zkh_tensor *su = nullptr, *esu = nullptr;
+    uint32_t o[8];
+    int rc = zkh_hadamard(c, S, U, &su);
+    if (!rc) rc = zkh_hadamard(c, E, su, &esu);
+    if (!rc) rc = zkh_sum(c, esu, o);
+    if (su) zkh_tensor_free(su);
+    if (esu) zkh_tensor_free(esu);
+    if (!rc) *out = fr_load(o);
+    return rc;
+}
+// claim_label: the claim is not given but is sum E[i] S[i] U[i] (E = eq(i, u) in the eq
+// form), taken from the first round's sums (q(0) + q(1) of the round's polynomial in t, which
+// the check below compares with the claim) and absorbed under that label before the first
+// round's evaluations; claim_out receives it
 static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], const zkh_tensor* E,
                      const std::vector<Fr>* ueq, const zkh_tensor* S, const zkh_tensor* U,
                      uint32_t* ev_out, uint32_t* term_out, uint32_t* ws_out, const char* claim_label = nullptr,
@@ -4036,7 +4048,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     if (!n || (n & (n - 1)) || U->n != n || (E && E->n != n))
         return fail(c, ZKH_EARG, "hadamard tables must share a power-of-two size");
     if (ueq && ((uint64_t)1 << ueq->size()) != n) return fail(c, ZKH_EARG, "eq size mismatch");
-    if (claim_label && (!ueq || !claim_out)) return fail(c, ZKH_EARG, "a derived claim needs the eq form");
+    if (claim_label && !claim_out) return fail(c, ZKH_EARG, "null argument");
     if (!claim_label && !fr_is_canonical(claim_l)) return fail(c, ZKH_EARG, "non-canonical claim");
     HIPCHK(c, hipSetDevice(c->device));
     const uint32_t k = ceil_log2(n);
@@ -4078,7 +4090,8 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     const bool derive_claim = claim_label && k > 0 && !persists(0);
     if (claim_label && !derive_claim) {  // all rounds in the persistent loop: the sum first
         // (a table this small is never read as int32, so Sc and Uc hold its planes)
-        if ((rc = eq_weighted_sum(c, Sc, &Uc, n, *ueq, &claim))) return rc;
+        if ((rc = ueq ? eq_weighted_sum(c, Sc, &Uc, n, *ueq, &claim) : explicit_claim(c, E, S, U, &claim)))
+            return rc;
         tr_absorb_fr(tr, claim_label, claim);
     }
     if (claim_label) fr_store(claim, claim_out);
@@ -4302,13 +4315,17 @@ static int hp_checked(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[8], const
     Fr e = kOne;  // eq(u, pt) = prod_i eq2(u_i, pt_i)
     for (uint32_t i = 0; i < k; i++) e = fr_mul(e, fr_eq2((*ueq)[i], fr_load(&pt[8 * (size_t)i])));
     if (!fr_eq(e, fr_load(term + 16))) return fail(c, ZKH_EROUND, "hadamard E terminal != eq(u, point) (convention bug)");
-    if (claim_label) {  // the claim taken from the first round against sum eq(u, i) S[i] U[i]
-        DevPlanes Sp, Up;
+    if (claim_label) {  // the claim taken from the first round against sum E[i] S[i] U[i]
         Fr direct;
-        if ((rc = as_planes(c, S, SL_TMP1, &Sp)) || (rc = as_planes(c, U, SL_TMP2, &Up)) ||
-            (rc = eq_weighted_sum(c, Sp, &Up, S->n, *ueq, &direct)))
+        if (ueq) {
+            DevPlanes Sp, Up;
+            if ((rc = as_planes(c, S, SL_TMP1, &Sp)) || (rc = as_planes(c, U, SL_TMP2, &Up)) ||
+                (rc = eq_weighted_sum(c, Sp, &Up, S->n, *ueq, &direct)))
+                return rc;
+        } else if ((rc = explicit_claim(c, E, S, U, &direct))) {
             return rc;
-        if (!fr_eq(direct, fr_load(claim_out))) return fail(c, ZKH_EROUND, "hadamard claim != sum eq S U");
+        }
+        if (!fr_eq(direct, fr_load(claim_out))) return fail(c, ZKH_EROUND, "hadamard claim != sum E S U");
     }
     return ZKH_OK;
 }
@@ -4325,6 +4342,12 @@ extern "C" int zkh_hp_prove_eq(zkh_ctx* c, uint8_t tr[32], const uint32_t claim[
     if (!all_canonical(u, k)) return fail(c, ZKH_EARG, "non-canonical challenge");
     std::vector<Fr> uv = load_frs(u, k);
     return hp_checked(c, tr, claim, nullptr, &uv, S, U, ev_out, term_out, ws_out);
+}
+extern "C" int zkh_hp_prove_claim(zkh_ctx* c, uint8_t tr[32], const char* label, const zkh_tensor* E,
+                                  const zkh_tensor* S, const zkh_tensor* U, uint32_t claim_out[8], uint32_t* ev_out,
+                                  uint32_t* term_out, uint32_t* ws_out) {
+    if (!c || !tr || !label || !claim_out || !E || !S || !U) return fail(c, ZKH_EARG, "null argument");
+    return hp_checked(c, tr, nullptr, E, nullptr, S, U, ev_out, term_out, ws_out, label, claim_out);
 }
 extern "C" int zkh_hp_prove_eq_claim(zkh_ctx* c, uint8_t tr[32], const char* label, const uint32_t* u, uint32_t k,
                                      const zkh_tensor* S, const zkh_tensor* U, uint32_t claim_out[8],
