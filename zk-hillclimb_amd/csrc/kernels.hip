@@ -303,8 +303,47 @@ __global__ void k_eq_mont(const uint32_t* __restrict__ fac, uint32_t K, uint32_t
     for (uint32_t b = blockIdx.x * blockDim.x + threadIdx.x; b < n; b += gridDim.x * blockDim.x)
         st_aos(out, b, eq_prod(fac, K, b));
 }
+// The same by four lanes an entry: lane q of an entry's quad multiplies the factors t = q,
+// q + 4, ... (a chain of K/4 products), then two shuffle levels combine the quad -- the
+// latency of about K/4 + 2 products instead of K, for the small tables a proof builds first
+// (Elo, Ehi).  Two tables per launch: blocks [0, g0) build table 0, the rest table 1.
+ZDEV fr_t eq_prod_quad(const uint32_t* __restrict__ fac, uint32_t K, uint32_t b, uint32_t q) {
+    fr_t e = q < K ? ld_aos(fac, 2 * q + ((b >> q) & 1)) : one_m();
+    for (uint32_t t = q + 4; t < K; t += 4) e = mont_mul(e, ld_aos(fac, 2 * t + ((b >> t) & 1)));
+    e = mont_mul(e, fr_shfl_xor(e, 1));
+    return mont_mul(e, fr_shfl_xor(e, 2));
+}
+struct EqTab {
+    const uint32_t* fac;
+    uint32_t K, n;
+    uint32_t* out;
+};
+__global__ __launch_bounds__(NT) void k_eq_mont_quad(EqTab t0, EqTab t1, uint32_t g0) {
+    const bool second = blockIdx.x >= g0;
+    const EqTab& T = second ? t1 : t0;
+    const uint32_t i = (blockIdx.x - (second ? g0 : 0)) * NT + threadIdx.x;
+    const uint32_t b = i >> 2, q = i & 3;
+    const fr_t e = eq_prod_quad(T.fac, T.K, b < T.n ? b : 0, q);  // every lane of a quad takes part
+    if (q == 0 && b < T.n) st_aos(T.out, b, e);
+}
+#define EQ_QUAD_MAX (1u << 14)  // larger tables: one entry per thread (product throughput)
 void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, uint32_t* out) {
+    if (n <= EQ_QUAD_MAX) {
+        const uint32_t g0 = (4 * n + NT - 1) / NT;
+        k_eq_mont_quad<<<g0, NT, 0, s>>>(EqTab{fac, K, n, out}, EqTab{fac, K, 0, out}, g0);
+        return;
+    }
     k_eq_mont<<<grid_for(n, NT, 4096), NT, 0, s>>>(fac, K, n, out);
+}
+void launch_eq_mont2(hipStream_t s, const uint32_t* fac0, uint32_t K0, uint32_t n0, uint32_t* out0,
+                     const uint32_t* fac1, uint32_t K1, uint32_t n1, uint32_t* out1) {
+    if (n0 > EQ_QUAD_MAX || n1 > EQ_QUAD_MAX) {
+        launch_eq_mont(s, fac0, K0, n0, out0);
+        launch_eq_mont(s, fac1, K1, n1, out1);
+        return;
+    }
+    const uint32_t g0 = (4 * n0 + NT - 1) / NT, g1 = (4 * n1 + NT - 1) / NT;
+    k_eq_mont_quad<<<g0 + g1, NT, 0, s>>>(EqTab{fac0, K0, n0, out0}, EqTab{fac1, K1, n1, out1}, g0);
 }
 
 // ------------------------------------------------------------------------------------

@@ -69,6 +69,9 @@ void launch_transpose_i32(hipStream_t s, const int32_t* in, uint32_t rows, uint3
 // ---- eq tables ----
 // out[b] = prod_t fac[2t + bit_t(b)] (Montgomery form) for b < n, AoS; K = #factors
 void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, uint32_t* out);
+// two eq tables in one launch (the small Elo, Ehi a proof builds first)
+void launch_eq_mont2(hipStream_t s, const uint32_t* fac0, uint32_t K0, uint32_t n0, uint32_t* out0,
+                     const uint32_t* fac1, uint32_t K1, uint32_t n1, uint32_t* out1);
 
 // ---- dot products / sums (block partials, AoS, summed on the host) ----
 // partial[b] = sum montmul(a_i, b_i) over the block's range (carries 2^-256)

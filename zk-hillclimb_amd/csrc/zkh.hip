@@ -713,8 +713,7 @@ static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_
     st.ehi_d = (uint32_t*)scratch_slot(c, SL_EHI, ((size_t)32 << khi), &rc);
     if (rc) return rc;
     if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
-    launch_eq_mont(c->stream, fac_d, 10, 1024, st.elo_d);
-    launch_eq_mont(c->stream, fac_d + 2 * 10 * 8, khi, 1u << khi, st.ehi_d);
+    launch_eq_mont2(c->stream, fac_d, 10, 1024, st.elo_d, fac_d + 2 * 10 * 8, khi, 1u << khi, st.ehi_d);
     // prefix[K] = prod_{t<K} (1 - u_t); corr[K] = prefix[K] / prefix[kmax]
     std::vector<Fr> prefix(kmax + 1);
     prefix[0] = kOne;
@@ -1276,8 +1275,7 @@ extern "C" int zkh_me_static(zkh_ctx* c, const zkh_tensor* t, const uint32_t* u,
     uint32_t* ehi = (uint32_t*)(base + kStEhi);
     uint32_t* lay = (uint32_t*)(base + kStLay);
     launch_static_setup(c->stream, fac, kmax * 16, fac_d, lay, 3);
-    launch_eq_mont(c->stream, fac_d, 10, 1024, elo);
-    launch_eq_mont(c->stream, fac_d + 2 * 10 * 8, khi, 1u << khi, ehi);
+    launch_eq_mont2(c->stream, fac_d, 10, 1024, elo, fac_d + 2 * 10 * 8, khi, 1u << khi, ehi);
     Publish pb = make_pub(c, 1);
     pb.part = (uint32_t*)(base + kStPart);  // launch_eq_sum uses at most 1024 blocks
     pb.layout = lay;
