@@ -2049,11 +2049,12 @@ __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32
     __shared__ uint4 accl[K * NT], acch[K * NT];
     LdsAcc<K> acc{accl, acch};
     acc.zero();
+    const fr_t vp = fold && S.s32 ? plain_uniform(vm) : fr_zero();  // an int32 S's first fold
     for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
         fr_t e0, e1, s0, s1;
         load_pair(E, i, h, n, fold, vm, e0, e1);
         SB();
-        load_pair(S, i, h, n, fold, vm, s0, s1);
+        load_pair(S, i, h, n, fold, vm, vp, s0, s1);
         SB();
         if constexpr (!derive) {
             int64_t a0, a1;
@@ -2082,17 +2083,19 @@ __global__ __launch_bounds__(NT) void k_hp_round_ones(TabDev E, TabDev S, uint32
     reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
-                              const uint32_t* vmp, Publish partial, int derive, int s_int) {
+                              const uint32_t* vmp, Publish partial, int derive, int s_int, const int32_t* s32) {
     uint32_t g = grid_for(n >> 1, NT, 1024);
     fr_t vm = fold && !vmp ? to_fr(v_m_host) : fr_t{};
-    if (fold && derive && wide_round(n)) {
+    TabDev sd = tab_dev(S);
+    sd.s32 = s32;
+    if (fold && derive && wide_round(n) && !s32) {
         const uint32_t gw = ((n >> 1) + HPW_P - 1) / HPW_P;
-        k_hp_ones_wide<<<gw, NTW, 0, s>>>(tab_dev(E), tab_dev(S), n, vm, vmp, partial);
+        k_hp_ones_wide<<<gw, NTW, 0, s>>>(tab_dev(E), sd, n, vm, vmp, partial);
         launch_publish(s, partial);
         return gw;
     }
-    if (fold && derive) k_hp_round_ones<1><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, 0);
-    else k_hp_round_ones<0><<<g, NT, 0, s>>>(tab_dev(E), tab_dev(S), n, fold, vm, vmp, partial, s_int);
+    if (fold && derive) k_hp_round_ones<1><<<g, NT, 0, s>>>(tab_dev(E), sd, n, fold, vm, vmp, partial, 0);
+    else k_hp_round_ones<0><<<g, NT, 0, s>>>(tab_dev(E), sd, n, fold, vm, vmp, partial, s_int);
     launch_publish(s, partial);
     return g;
 }

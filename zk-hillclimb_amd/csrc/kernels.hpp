@@ -242,9 +242,10 @@ uint32_t launch_lu_phase2(hipStream_t s, Tab A, Tab S, Tab B, Tab T, Tab m, uint
 uint32_t launch_hp_round(hipStream_t s, Tab E, Tab S, Tab U, uint32_t n,
                          int fold, const uint32_t* v_m_host, const uint32_t* vmp, Publish pub, int derive);
 // generic with U = 1 everywhere: sums e0*s0, e1*s1, de*ds (x 2^-256); U is not touched;
-// derive: e0*s0, de*ds; s_int (first round, S of int32 values): the sums exact (x 1)
+// derive: e0*s0, de*ds; s_int (first round, S of int32 values): the sums exact (x 1);
+// s32: S read as int32 entries (not yet folded) instead of its source planes
 uint32_t launch_hp_round_ones(hipStream_t s, Tab E, Tab S, uint32_t n, int fold, const uint32_t* v_m_host,
-                              const uint32_t* vmp, Publish pub, int derive, int s_int);
+                              const uint32_t* vmp, Publish pub, int derive, int s_int, const int32_t* s32);
 // eq-specialised: sums w*s0*u0, w*s1*u1, w*ds*du with w = eq(i,u_) (x 2^-256 when folding,
 // x 2^256 in the first round); derive: w*s0*u0, w*ds*du
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,

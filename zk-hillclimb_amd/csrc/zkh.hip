@@ -4055,12 +4055,25 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     // the round kernels up to their first fold when the first two rounds are round kernels,
     // not the persistent loop; otherwise as planes
     const bool big = (n >> 1) > ZKH_HP_PERSIST_MAX;
-    const bool s_i32 = ueq && big && S->kind == ZKH_KIND_I32 && !S->weights;
+    // U all ones (an I32 tensor measured so at ingest: the RoPE obligations' U = 1) with an
+    // explicit E: the per-round kernels skip U, whose folds stay all ones in its source
+    const bool u_ones = !ueq && U->kind == ZKH_KIND_I32 && U->ones;
+    // with U all ones and an int32 S, the first round's sums are exact (x 1): 32-bit multiplies
+    const bool s_int = u_ones && S->kind == ZKH_KIND_I32;
+    const bool s_i32 = (ueq || u_ones) && big && S->kind == ZKH_KIND_I32 && !S->weights;
     const bool u_i32 = ueq && big && U->kind == ZKH_KIND_I32 && !U->weights;
     DevPlanes Ec{}, Sc{}, Uc{};
     if (E && (rc = as_planes(c, E, SL_TMP0, &Ec))) return rc;
-    if ((!s_i32 && (rc = as_planes(c, S, SL_TMP1, &Sc))) || (!u_i32 && (rc = as_planes(c, U, SL_TMP2, &Uc))))
+    if (!s_i32 && (rc = as_planes(c, S, SL_TMP1, &Sc))) return rc;
+    if (u_ones) {
+        // only the persistent loop and the last fold read U (as ones, whatever its folds):
+        // entries below 2 ZKH_HP_PERSIST_MAX suffice
+        Uc = scratch_planes(c, SL_TMP2, n, &rc);
+        if (rc) return rc;
+        launch_i32_to_planes(c->stream, (const int32_t*)U->d, std::min<uint32_t>(n, 2 * ZKH_HP_PERSIST_MAX), Uc);
+    } else if (!u_i32 && (rc = as_planes(c, U, SL_TMP2, &Uc))) {
         return rc;
+    }
     const int32_t* s32 = s_i32 ? (const int32_t*)S->d : nullptr;  // the sources while unfolded
     const int32_t* u32 = u_i32 ? (const int32_t*)U->d : nullptr;
     DevPlanes Ew{}, Sw, Uw;
@@ -4093,11 +4106,6 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         tr_absorb_fr(tr, claim_label, claim);
     }
     if (claim_label) fr_store(claim, claim_out);
-    // U all ones (an I32 tensor measured so at ingest: the RoPE obligations' U = 1) with an
-    // explicit E: the per-round kernels skip U, whose folds stay all ones in its source
-    const bool u_ones = !ueq && U->kind == ZKH_KIND_I32 && U->ones;
-    // with U all ones and an int32 S, the first round's sums are exact (x 1): 32-bit multiplies
-    const bool s_int = u_ones && S->kind == ZKH_KIND_I32;
     // A folding round leaves its sum at 1 to the host: claim - p(0) for an explicit E; with
     // the eq form, from the inner claim I = sum eq S U over the remaining variables (the
     // running claim without the eq factor cE) as (I - (1 - u) q(0)) / u, unless u is 0.
@@ -4117,7 +4125,8 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         Launched l{make_pub(c, 1), fold && !xcheck_on() && (!ueq || !fr_eq((*ueq)[k - r - 1], kZero))};
         if (u_ones) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 2 * 32);
-            launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, l.pb, l.dv, s_int);
+            launch_hp_round_ones(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, sz, fold, vm, vmp, l.pb, l.dv, s_int,
+                                 s32);
         } else if (!ueq) {
             ProfScope ps(c, "hp_round", (fold ? 3.0 * sz : (double)sz) * 3 * 32);
             launch_hp_round(c->stream, Tab{e_src, Ew}, Tab{s_src, Sw}, Tab{u_src, Uw}, sz, fold, vm, vmp, l.pb, l.dv);
