@@ -708,12 +708,12 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one 256 MiB device-to-device copy (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--segment", choices=["glu", "rope", "commit", "batchopen", "c3", "c5glu", "mmfr", "frmul"],
+    ap.add_argument("--segment", choices=["glu", "rope", "ropek", "commit", "batchopen", "c3", "c5glu", "mmfr", "frmul"],
                     default=None, help="only run one segment repeatedly (for profiling), then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the path would shard); run with --gpus 1", file=sys.stderr)
+              "; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
 
@@ -757,6 +757,8 @@ def main():
         elif args.segment == "c3":
             c3 = synth.CONFIGS["C3"]
             job = LookupJob(zkh, synth.rng_for(3), c3["D"], c3["N"], c3["low"])
+        elif args.segment == "ropek":
+            job = RopeJob(zkh, synth, rng, "k", L["B"], L["kv"])
         else:
             job = RopeJob(zkh, synth, rng, "q", L["B"], L["d"])
         ref = job.run()
