@@ -159,14 +159,18 @@ def _int(l):
 
 def test_host_scalar_ops_match_big_integers(zkh):
     """zkh_fr_scalar (the host field arithmetic of the round logic): add, sub, mul and the
-    binary-Euclid inverse against Python integers mod r, with the inverse pinned by
-    Fermat's little theorem (x^(r-2)) and x * x^-1 = 1, and inverse(0) = 0."""
+    inverse (the optimized binary GCD: 31-step updates from 64-bit approximations) against
+    Python integers mod r, with the inverse pinned by Fermat's little theorem (x^(r-2)) and
+    x * x^-1 = 1, and inverse(0) = 0; powers of two and their negatives, whose GCD runs are
+    the longest and most lopsided, are among the inputs."""
     lib = zkh.lib()
     f = lib.zkh_fr_scalar
     f.restype = ctypes.c_int
     rng = np.random.default_rng(5)
     vals = [0, 1, 2, 3, R_MOD - 1, R_MOD - 2, (R_MOD + 1) // 2, 1 << 200, (1 << 255) % R_MOD]
     vals += [int.from_bytes(rng.bytes(32), "little") % R_MOD for _ in range(300)]
+    vals += [1 << k for k in range(0, 255, 5)] + [R_MOD - (1 << k) for k in range(0, 254, 9)]
+    vals += [int.from_bytes(rng.bytes(8), "little") for _ in range(40)]
     out = (ctypes.c_uint32 * 8)()
     for i, a in enumerate(vals):
         b = vals[(7 * i + 3) % len(vals)]

@@ -129,7 +129,7 @@ inline Fr fr_half(const Fr& x) {
 // Algorithm B with the cofactors kept mod r): u = x1 a, v = x2 a (mod r) hold throughout,
 // and gcd(a, r) = 1 ends the loop at u = 1 or v = 1.  Same value as fr_inv_fermat, about 1
 // shift or subtraction per bit instead of some 380 Montgomery products; inverse(0) = 0.
-inline Fr fr_inv(const Fr& a) {
+inline Fr fr_inv_bin(const Fr& a) {
     if (fr_eq(a, kZero)) return kZero;
     Fr u = a, v = kP, x1 = kOne, x2 = kZero;
     while (!fr_eq(u, kOne) && !fr_eq(v, kOne)) {
@@ -150,6 +150,141 @@ inline Fr fr_inv(const Fr& a) {
         }
     }
     return fr_eq(u, kOne) ? x1 : x2;
+}
+namespace inv_detail {
+// five-limb two's complement values (the products of a 256-bit value and a signed factor)
+inline void neg5(uint64_t r[5]) {
+    uint64_t c = 1;
+    for (int i = 0; i < 5; i++) {
+        const u128 s = (u128)(~r[i]) + c;
+        r[i] = (uint64_t)s;
+        c = (uint64_t)(s >> 64);
+    }
+}
+// r = x f for x < 2^256 and |f| < 2^63
+inline void mul_s64(const uint64_t x[4], int64_t f, uint64_t r[5]) {
+    const uint64_t af = f < 0 ? 0 - (uint64_t)f : (uint64_t)f;
+    u128 c = 0;
+    for (int i = 0; i < 4; i++) {
+        c = (u128)x[i] * af + (uint64_t)(c >> 64);
+        r[i] = (uint64_t)c;
+    }
+    r[4] = (uint64_t)(c >> 64);
+    if (f < 0) neg5(r);
+}
+inline void add5(uint64_t r[5], const uint64_t b[5]) {
+    uint64_t c = 0;
+    for (int i = 0; i < 5; i++) {
+        const u128 s = (u128)r[i] + b[i] + c;
+        r[i] = (uint64_t)s;
+        c = (uint64_t)(s >> 64);
+    }
+}
+inline void sar31(uint64_t r[5]) {  // arithmetic shift right by 31
+    for (int i = 0; i < 4; i++) r[i] = (r[i] >> 31) | (r[i + 1] << 33);
+    r[4] = (uint64_t)((int64_t)r[4] >> 31);
+}
+inline bool is_neg(const uint64_t r[5]) { return (int64_t)r[4] < 0; }
+// x f + y g for x, y < 2^256, |f|, |g| <= 2^31
+inline void lin(const uint64_t x[4], int64_t f, const uint64_t y[4], int64_t g, uint64_t r[5]) {
+    uint64_t t[5];
+    mul_s64(x, f, r);
+    mul_s64(y, g, t);
+    add5(r, t);
+}
+inline uint32_t bitlen(const uint64_t x[4]) {
+    for (int i = 3; i >= 0; i--)
+        if (x[i]) return 64 * i + 64 - (uint32_t)__builtin_clzll(x[i]);
+    return 0;
+}
+inline uint64_t bits_at(const uint64_t x[4], uint32_t s) {  // (x >> s) mod 2^64, s < 256
+    const uint32_t l = s >> 6, o = s & 63;
+    const uint64_t lo = x[l] >> o;
+    return o && l < 3 ? lo | (x[l + 1] << (64 - o)) : lo;
+}
+// (u f + v g) / 2^31 mod r for canonical u, v: one 31-bit Montgomery step, then 0 <= . < r
+inline Fr lin_div31(const Fr& u, int64_t f, const Fr& v, int64_t g) {
+    uint64_t t[5], qr[5];
+    lin(u.v, f, v.v, g, t);
+    const int64_t q = (int64_t)((t[0] * kInv) & 0x7fffffffULL);  // t + q r = 0 mod 2^31
+    mul_s64(kP.v, q, qr);
+    add5(t, qr);
+    sar31(t);  // now in (-2r, 3r)
+    uint64_t p5[5] = {kP.v[0], kP.v[1], kP.v[2], kP.v[3], 0};
+    while (is_neg(t)) add5(t, p5);
+    Fr x = {{t[0], t[1], t[2], t[3]}};
+    while (t[4] || fr_geq(x, kP)) {
+        uint64_t m5[5] = {kP.v[0], kP.v[1], kP.v[2], kP.v[3], 0};
+        neg5(m5);
+        add5(t, m5);
+        x = Fr{{t[0], t[1], t[2], t[3]}};
+    }
+    return x;
+}
+}  // namespace inv_detail
+// The inverse by Pornin's optimized binary GCD (T. Pornin, "Optimized Binary GCD for Modular
+// Inversion", IACR ePrint 2020/972, Algorithm 2 with k = 32).  Each outer step runs 31
+// binary-GCD iterations on 64-bit approximations of a and b (their low 31 bits and their top
+// 33 bits at the length of the longer one), collecting the update (f0 g0; f1 g1); then a, b
+// become (a f0 + b g0) / 2^31, (a f1 + b g1) / 2^31 (made nonnegative by flipping the row's
+// signs) and the cofactors u, v the same combinations divided by 2^31 mod r.  a = u y and
+// b = v y (mod r) hold throughout; with gcd(y, r) = 1 the loop ends at a = 0, b = 1, v = 1/y,
+// after about 17 outer steps for this 255-bit r instead of some 500 bit-by-bit iterations.
+// A run that does not end at b = 1 (it cannot for prime r and y != 0) falls back to
+// fr_inv_bin; inverse(0) = 0.
+inline Fr fr_inv(const Fr& y) {
+    using namespace inv_detail;
+    if (fr_eq(y, kZero)) return kZero;
+    uint64_t a[4], b[4];
+    memcpy(a, y.v, 32);
+    memcpy(b, kP.v, 32);
+    Fr u = kOne, v = kZero;
+    for (int it = 0; it < 64 && (a[0] | a[1] | a[2] | a[3]); it++) {
+        uint32_t n = bitlen(a) > bitlen(b) ? bitlen(a) : bitlen(b);
+        if (n < 64) n = 64;
+        uint64_t ab = (a[0] & 0x7fffffffULL) | (bits_at(a, n - 33) << 31);
+        uint64_t bb = (b[0] & 0x7fffffffULL) | (bits_at(b, n - 33) << 31);
+        int64_t f0 = 1, g0 = 0, f1 = 0, g1 = 1;
+        for (int j = 0; j < 31; j++) {  // branch-free: odd a swaps when a < b, then subtracts
+            const uint64_t odd = 0 - (ab & 1), sw = odd & (0 - (uint64_t)(ab < bb));
+            const uint64_t tx = (ab ^ bb) & sw;
+            ab ^= tx;
+            bb ^= tx;
+            const int64_t tf = (f0 ^ f1) & (int64_t)sw, tg = (g0 ^ g1) & (int64_t)sw;
+            f0 ^= tf;
+            f1 ^= tf;
+            g0 ^= tg;
+            g1 ^= tg;
+            ab = (ab - (bb & odd)) >> 1;
+            f0 -= f1 & (int64_t)odd;
+            g0 -= g1 & (int64_t)odd;
+            f1 *= 2;
+            g1 *= 2;
+        }
+        uint64_t na[5], nb[5];
+        lin(a, f0, b, g0, na);
+        lin(a, f1, b, g1, nb);
+        sar31(na);
+        sar31(nb);
+        if (is_neg(na)) {
+            neg5(na);
+            f0 = -f0;
+            g0 = -g0;
+        }
+        if (is_neg(nb)) {
+            neg5(nb);
+            f1 = -f1;
+            g1 = -g1;
+        }
+        if (na[4] || nb[4]) return fr_inv_bin(y);  // cannot happen: |a'|, |b'| <= max(a, b)
+        memcpy(a, na, 32);
+        memcpy(b, nb, 32);
+        const Fr nu = lin_div31(u, f0, v, g0), nv = lin_div31(u, f1, v, g1);
+        u = nu;
+        v = nv;
+    }
+    if (a[0] | a[1] | a[2] | a[3] || b[0] != 1 || b[1] | b[2] | b[3]) return fr_inv_bin(y);
+    return v;
 }
 inline Fr fr_from_i64(int64_t v) {
     if (v >= 0) return fr_u64((uint64_t)v);

@@ -842,7 +842,7 @@ __global__ __launch_bounds__(NT) void k_hist_tiles(HistArgs a) {
         if (idx >= a.N) bad = true;
         else atomicAdd(&cnt[idx >> ZKH_HIST_BITS], 1u);
     }
-    if (bad) atomicOr(a.bad, 1u);
+    if (bad) *a.bad = a.tag;
     __syncthreads();
     for (uint32_t b = threadIdx.x; b < a.nbuckets; b += NT) a.tile_cnt[(size_t)b * a.ntiles + blockIdx.x] = cnt[b];
 }
@@ -967,7 +967,7 @@ __global__ __launch_bounds__(NTH) void k_hist_slots(HistArgs a) {
         }
         lds_hist_add(h, bin, valid);
     }
-    if (bad) atomicOr(a.bad, 1u);
+    if (bad) *a.bad = a.tag;
     __syncthreads();
     uint4* out = reinterpret_cast<uint4*>(a.slot_hist + (size_t)slot * ZKH_HIST_BINS);
     for (uint32_t j = threadIdx.x; j < ZKH_HIST_BINS / 4; j += NTH)
@@ -1101,7 +1101,7 @@ __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tle
                                   fr_t r,
                                   const uint4* __restrict__ blo, const uint4* __restrict__ bhi,
                                   const uint32_t* __restrict__ baos, uint4* clo, uint4* chi, uint4* alo, uint4* ahi,
-                                  uint32_t* flags) {
+                                  uint32_t* flags, uint32_t tag) {
     uint32_t f = 0;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
         const fr_t g = G(i);
@@ -1133,13 +1133,18 @@ __global__ void k_lu_tuple_gather(LG G, uint32_t n, fr_t low, LT T, uint32_t tle
             f |= 2u;
         }
     }
-    // one atomic per wave that saw a flag
+    // one store per wave that saw a flag: flags[0] (a witness outside the table), flags[1]
+    // (a witness that is not the table's entry at its index) receive the call's tag
     const uint64_t any1 = __ballot(f & 1u), any2 = __ballot(f & 2u);
-    if ((any1 | any2) && (threadIdx.x & 63) == 0) atomicOr(flags, (any1 ? 1u : 0u) | (any2 ? 2u : 0u));
+    if ((threadIdx.x & 63) == 0) {
+        if (any1) flags[0] = tag;
+        if (any2) flags[1] = tag;
+    }
 }
 void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
                             Src mapped, int seq_s, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host,
-                            DevPlanes Binv, const uint32_t* binv_aos, DevPlanes comb, DevPlanes A, uint32_t* flags) {
+                            DevPlanes Binv, const uint32_t* binv_aos, DevPlanes comb, DevPlanes A, uint32_t* flags,
+                            uint32_t tag) {
     const fr_t low = to_fr(low_host), r = to_fr(r_host), rm = to_fr(r_m_host);
     const uint32_t g = grid_for(n, NT, 8192);
     with_loader(G, [&](auto lg) {
@@ -1148,23 +1153,23 @@ void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* lo
                 if (seq_s)
                     k_lu_tuple_gather<true, true><<<g, NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
                                                                     PL_HI(Binv), binv_aos, PL_LO(comb), PL_HI(comb),
-                                                                    PL_LO(A), PL_HI(A), flags);
+                                                                    PL_LO(A), PL_HI(A), flags, tag);
                 else
                     k_lu_tuple_gather<true, false><<<g, NT, 0, s>>>(lg, n, low, lt, tlen, lm, N, rm, r, PL_LO(Binv),
                                                                      PL_HI(Binv), binv_aos, PL_LO(comb), PL_HI(comb),
-                                                                     PL_LO(A), PL_HI(A), flags);
+                                                                     PL_LO(A), PL_HI(A), flags, tag);
             });
         });
     });
 }
 void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
-                            uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags) {
+                            uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags, uint32_t tag) {
     const fr_t low = to_fr(low_host);
     with_loader(S, [&](auto ls) {
         with_loader(T, [&](auto lt) {
             k_lu_tuple_gather<false, false><<<grid_for(n, NT, 8192), NT, 0, s>>>(
                 ls, n, low, lt, tlen, LdI32{nullptr}, N, fr_t{}, fr_t{}, PL_LO(Binv), PL_HI(Binv), nullptr, nullptr,
-                nullptr, PL_LO(A), PL_HI(A), flags);
+                nullptr, PL_LO(A), PL_HI(A), flags, tag);
         });
     });
 }
@@ -1181,8 +1186,8 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
 // passes, k_inv_blocks turns the block totals into "all other blocks" products and
 // publishes the grand product G, whose plain inverse the host computes once.  Pass 2 walks
 // each thread's entries backwards.  Zero entries (x + beta = 0) take 2^256, M's identity,
-// in the products and produce 0, the reference's Fermat convention; pass 1 sets *zflag when
-// it meets one (the inverse then has a zero entry).
+// in the products and produce 0, the reference's Fermat convention; pass 1 sets *zflag to
+// the call's tag when it meets one (the inverse then has a zero entry).
 #define INV_CHK 16
 // The M-product of all OTHER leaves, for each of NL leaves (NL a power of 2, at most the
 // block size; thread t < NL gives leaf t): a product tree up, tr[k] = M(tr[2k], tr[2k + 1])
@@ -1213,7 +1218,8 @@ ZDEV fr_t others_tree(fr_t* tr, fr_t* out, const fr_t& v) {
 }
 __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
-                                                  uint32_t* others, uint32_t* blockprod, uint32_t* zflag) {
+                                                  uint32_t* others, uint32_t* blockprod, uint32_t* zflag,
+                                                  uint32_t tag) {
     __shared__ fr_t tr[2 * NT], out[2 * NT];
     const uint32_t t = threadIdx.x;
     const uint32_t base = blockIdx.x * NT * INV_CHK;
@@ -1229,7 +1235,7 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
             st_fr(alo, ahi, idx, run);
         }
     }
-    if (__ballot(zero) && (t & 63) == 0) atomicOr(zflag, 1u);  // one atomic per wave that met a zero
+    if (__ballot(zero) && (t & 63) == 0) *zflag = tag;  // one store per wave that met a zero
     st_aos(others, blockIdx.x * NT + t, others_tree<NT>(tr, out, run));
     if (t == 0) st_aos(blockprod, blockIdx.x, tr[1]);
 }
@@ -1238,7 +1244,8 @@ __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4*
 // flag) for the host to invert.  Thread t owns products [t*per, (t+1)*per).
 #define NTI 256
 __global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__ bp, uint32_t nb,
-                                                    uint32_t* others, Publish pub, const uint32_t* zflag) {
+                                                    uint32_t* others, Publish pub, const uint32_t* zflag,
+                                                    uint32_t tag) {
     __shared__ fr_t tr[2 * NTI], out[2 * NTI];
     const uint32_t t = threadIdx.x;
     const uint32_t per = (nb + NTI - 1) / NTI;
@@ -1255,14 +1262,14 @@ __global__ __launch_bounds__(NTI) void k_inv_blocks(const uint32_t* __restrict__
     }
     if (t == 0) {
         st_aos(pub.host_out, 0, tr[1]);
-        pub.host_out[8] = *zflag;  // pass 1 met a zero entry
+        pub.host_out[8] = *zflag == tag ? 1u : 0u;  // pass 1 met a zero entry
         __threadfence_system();
         __hip_atomic_store(pub.host_flag, pub.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, uint32_t* others_blk,
-                       Publish pub, const uint32_t* zflag) {
-    k_inv_blocks<<<1, NTI, 0, s>>>(blockprod, nb, others_blk, pub, zflag);
+                       Publish pub, const uint32_t* zflag, uint32_t tag) {
+    k_inv_blocks<<<1, NTI, 0, s>>>(blockprod, nb, others_blk, pub, zflag, tag);
 }
 // 1/blockprod[b] = M(others_blk[b], 1/G), 1/(thread total) = M(others[t], 1/blockprod[b]);
 // then each thread walks its entries backwards
@@ -1270,9 +1277,13 @@ __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4*
                                                   fr_t beta, uint4* alo, uint4* ahi,
                                                   const uint32_t* __restrict__ others,
                                                   const uint32_t* __restrict__ others_blk, fr_t inv_total,
-                                                  uint32_t* aos) {
+                                                  const uint32_t* invp, uint32_t* aos) {
     const uint32_t t = threadIdx.x;
     const uint32_t base = blockIdx.x * NT * INV_CHK;
+    if (invp) {  // 1/G from a relay: invp[0..8), invp[8] != 0 when the host abandoned the call
+        if (invp[8]) return;
+        inv_total = ld_aos(invp, 0);
+    }
     const fr_t binv = mont_mul(inv_total, ld_aos(others_blk, blockIdx.x));
     fr_t y = mont_mul(binv, ld_aos(others, blockIdx.x * NT + t));
     for (int j = INV_CHK - 1; j >= 0; j--) {
@@ -1289,15 +1300,16 @@ __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4*
 }
 uint32_t inv_blocks(uint32_t n) { return (n + NT * INV_CHK - 1) / (NT * INV_CHK); }
 void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
-                      DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag) {
+                      DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag, uint32_t tag) {
     k_inv_pass1<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
-                                             PL_HI(A), others, blockprod, zflag);
+                                             PL_HI(A), others, blockprod, zflag, tag);
 }
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
-                      const uint32_t* inv_total_host, uint32_t* aos) {
-    k_inv_pass2<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
-                                             PL_HI(A), others, others_blk, to_fr(inv_total_host), aos);
+                      const uint32_t* inv_total_host, const uint32_t* invp, uint32_t* aos) {
+    k_inv_pass2<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A), PL_HI(A), others,
+                                             others_blk, inv_total_host ? to_fr(inv_total_host) : fr_t{}, invp,
+                                             aos);
 }
 
 // ------------------------------------------------------------------------------------
@@ -2947,12 +2959,14 @@ ZDEV void persist_publish(uint32_t* slot, const uint32_t* pub, uint32_t nw, uint
 }
 // completion flag of a stream (the host's settle): the value of *word (when given) to
 // host_word, then seq to the host flag
-__global__ void k_fence(uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t* host_word) {
-    if (word) __hip_atomic_store(host_word, *word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+__global__ void k_fence(uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t nwords, uint32_t* host_word) {
+    for (uint32_t i = 0; word && i < nwords; i++)
+        __hip_atomic_store(host_word + i, word[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
-void launch_fence(hipStream_t s, uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t* host_word) {
-    k_fence<<<1, 1, 0, s>>>(flag, seq, word, host_word);
+void launch_fence(hipStream_t s, uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t nwords,
+                  uint32_t* host_word) {
+    k_fence<<<1, 1, 0, s>>>(flag, seq, word, nwords, host_word);
 }
 // the relay between two round launches (launch_relay)
 __global__ __launch_bounds__(64) void k_relay(const uint32_t* cmd, uint32_t want, uint32_t* err,

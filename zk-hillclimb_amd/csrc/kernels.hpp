@@ -161,7 +161,8 @@ struct HistArgs {
     uint32_t* nslots;       // one word
     uint16_t* part;         // n partitioned low index bits
     uint32_t* slot_hist;    // [max_slots][ZKH_HIST_BINS]
-    uint32_t* bad;          // zeroed by the caller
+    uint32_t* bad;          // set to tag when an index is outside the table
+    uint32_t tag;
 };
 // scratch words needed by launch_hist for these sizes (tile_cnt .. slot_hist, 16-byte aligned parts)
 size_t hist_scratch_bytes(uint32_t n, uint32_t N);
@@ -177,16 +178,18 @@ void launch_lu_map_i32(hipStream_t s, const int32_t* S, uint32_t n, int32_t low,
 void launch_lu_map_to_i32(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, const int32_t* mapped,
                           uint32_t N, int32_t* out);
 // tuple lookup, j = (G[i] - low).limb0: comb[i] = G[i] + r mapped[j]; A[i] = Binv[j] where
-// T[j] == G[i]; *flags |= 1 (j >= N) / 2 (T[j] != G[i]); r plain and in Montgomery form;
+// T[j] == G[i]; flags[0] = tag (j >= N), flags[1] = tag (T[j] != G[i]); r plain and in
+// Montgomery form;
 // tlen > 0: T is the range table low + min(j, tlen - 1) (not read); seq_s: `mapped` is
 // S = mapped[(G - low).limb0] (n entries), read at i; binv_aos (optional): Binv as AoS
 // (32 contiguous bytes per entry: one cache line per random read instead of one per plane)
 void launch_lu_tuple_gather(hipStream_t s, Src G, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
                             Src mapped, int seq_s, uint32_t N, const uint32_t* r_host, const uint32_t* r_m_host,
-                            DevPlanes Binv, const uint32_t* binv_aos, DevPlanes comb, DevPlanes A, uint32_t* flags);
+                            DevPlanes Binv, const uint32_t* binv_aos, DevPlanes comb, DevPlanes A, uint32_t* flags,
+                            uint32_t tag);
 // the same for a plain range lookup: A[i] = Binv[j] (j = (S[i] - low).limb0) where T[j] == S[i]
 void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* low_host, Src T, uint32_t tlen,
-                            uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags);
+                            uint32_t N, DevPlanes Binv, DevPlanes A, uint32_t* flags, uint32_t tag);
 // A[i] = 1/(S[i]+beta) (0 -> 0), Montgomery's batched inversion with M(a, b) = a b 2^-256
 // products of the plain values: pass 1 writes the running products P_j to A, per-thread
 // "other threads" products to `others` (inv_blocks(n)*256 AoS) and block totals to
@@ -194,16 +197,19 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
 // other blocks' totals and publishes the grand product G (job 0 of pub); the host computes
 // the plain inverse 1/G once; pass 2 writes the plain inverses into A given inv_total = 1/G.
 uint32_t inv_blocks(uint32_t n);
-// zflag: a device word (zero before pass 1) that pass 1 sets when some S[i] + beta is zero;
-// k_inv_blocks publishes it as word 8 of pub.host_out, after G
+// zflag: a device word that pass 1 sets to tag when some S[i] + beta is zero (a word no
+// earlier call left at this tag); k_inv_blocks publishes (zflag == tag) as word 8 of
+// pub.host_out, after G
 void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
-                      DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag);
+                      DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag, uint32_t tag);
 void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, uint32_t* others_blk,
-                       Publish pub, const uint32_t* zflag);
-// aos (optional): the inverses also as AoS (n entries)
+                       Publish pub, const uint32_t* zflag, uint32_t tag);
+// 1/G from the host (inv_total_host) or, when invp is given, from device words invp[0..8)
+// written by a relay (invp[8] != 0: return at once); aos (optional): the inverses also as
+// AoS (n entries)
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
-                      const uint32_t* inv_total_host, uint32_t* aos = nullptr);
+                      const uint32_t* inv_total_host, const uint32_t* invp, uint32_t* aos = nullptr);
 // Round kernels take the previous round's challenge (Montgomery form) either from the host
 // at launch (v_m_host) or, when vmp is given, from device words vmp[0..8) written by a relay
 // (launch_relay) that runs between the previous round and this one; vmp[8] != 0 makes the
@@ -460,9 +466,10 @@ struct LuPersist {
 #define ZKH_LU_PSLOT 384   // words per block slot and command area of the logUp loop
 #define ZKH_LU_PSTAMP 352  // first clock-stamp word of its slots
 hipError_t launch_lu_persist(hipStream_t s, const LuPersist& p);
-// one thread: *word (when word is given) to *host_word, then seq to *flag (pinned host
-// memory, system scope): the completion flag of everything queued before it on the stream
-void launch_fence(hipStream_t s, uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t* host_word);
+// one thread: word[0..nwords) (when word is given) to host_word, then seq to *flag (pinned
+// host memory, system scope): the completion flag of everything queued before it on the stream
+void launch_fence(hipStream_t s, uint32_t* flag, uint32_t seq, const uint32_t* word, uint32_t nwords,
+                  uint32_t* host_word);
 // One wave that waits (as a persistent block waits for its command) until the three quads
 // at cmd carry seq `want`, then writes their eight data words to vmp[0..8) and 0 to vmp[8];
 // on ZKH_QUIT or past `deadline` (100 MHz ticks; then *err = 1) it writes 1 to vmp[8].

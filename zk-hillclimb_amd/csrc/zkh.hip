@@ -7,6 +7,7 @@
 // fused fold+evaluate kernel.  Only 32-byte scalars cross PCIe per round.
 #include <hip/hip_runtime.h>
 
+#include <assert.h>
 #include <pthread.h>
 #include <sched.h>
 #include <stdarg.h>
@@ -239,6 +240,9 @@ struct zkh_ctx {
     std::vector<Slot> slots;
     // round completion (Publish): coherent pinned job sums + flag, device partials/job layouts
     uint32_t* pub_host = nullptr;  // [ZKH_MAX_BATCH][11] Fr sums, then the flag word
+    // condition words that kernels set to a call's tag (zeroed once, written with tags only)
+    uint32_t* flag_d = nullptr;
+    uint32_t flag_tag = 0;
     uint32_t* pub_part = nullptr;  // device partial sums (pub_part_cap Fr)
     size_t pub_part_cap = (size_t)4096 * 11;
     uint32_t* pub_lay = nullptr;   // device [ZKH_MAX_BATCH][3] job layouts (see Publish)
@@ -564,13 +568,30 @@ static void pub_read(zkh_ctx* c, uint32_t j, int K, Fr* out) {
 // to pinned memory and the host spins on it (wakes sooner than hipStreamSynchronize); when
 // word (device) is given, its value reaches *out on the way.  Only for device-side work:
 // a copy into pageable host memory still needs hipStreamSynchronize.
-static int settle(zkh_ctx* c, const uint32_t* word = nullptr, uint32_t* out = nullptr) {
+static int settle(zkh_ctx* c, const uint32_t* word = nullptr, uint32_t* out = nullptr, uint32_t nwords = 1) {
     const uint32_t seq = ++c->pub_seq;
     uint32_t* hw = pub_flag(c) + 1;
-    launch_fence(c->stream, pub_flag(c), seq, word, hw);
+    launch_fence(c->stream, pub_flag(c), seq, word, nwords, hw);
     const int rc = wait_pub(c, seq);
-    if (!rc && out) *out = __atomic_load_n(hw, __ATOMIC_ACQUIRE);
+    for (uint32_t i = 0; !rc && out && i < nwords; i++) out[i] = __atomic_load_n(hw + i, __ATOMIC_ACQUIRE);
     return rc;
+}
+// A condition word of the device (c->flag_d + word) that kernels set to `tag` (plain stores,
+// no prior clearing): its words start at 0 and only ever receive tags, so a word left by an
+// earlier call never equals a new call's tag.  tag 0 (the global-atomics multiplicity
+// path): a word the caller zeroed, nonzero when set.
+struct DevFlag {
+    uint32_t* d;
+    uint32_t tag;
+    bool hit(uint32_t w) const { return tag ? w == tag : w != 0; }
+};
+enum { kFlagHist = 0, kFlagInvZero = 1, kFlagGather = 2 /* 2 words */ };
+static DevFlag dev_flag(zkh_ctx* c, uint32_t word) {
+    if (++c->flag_tag == 0) {  // tags wrapped: clear the words once, then start again at 1
+        (void)hipMemsetAsync(c->flag_d, 0, 64 * 4, c->stream);
+        c->flag_tag = 1;
+    }
+    return DevFlag{c->flag_d + word, c->flag_tag};
 }
 
 // ---- relayed round launches.  A round kernel can be queued before the host has the
@@ -696,11 +717,16 @@ struct EqState {
     std::vector<Fr> corr;     // corr[K] for K = 0..kmax
     std::vector<Fr> inv1mu;   // 1 / (1 - u_t) for t < kmax (empty for a degenerate point)
     uint32_t nvars = 0;
+    bool host_done = false;   // corr and inv1mu formed (eq_setup_host)
 };
 // all_rounds: the caller will weight shorter prefixes K < |u| (sumcheck rounds), which
 // needs every 1 - u_t invertible; a single full-length weighting (K = |u|) needs no
 // correction and accepts any point, e.g. a Boolean one.
-static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_rounds = true) {
+// The host part (corr, inv1mu: one inversion) can be left to eq_setup_host, so that a prover
+// queues its first round before that work (host_now = false).
+static int eq_setup_host(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_rounds = true);
+static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_rounds = true,
+                    bool host_now = true) {
     int rc = 0;
     std::vector<uint32_t> fac;
     make_fac(u, 10, fac);
@@ -714,6 +740,12 @@ static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_
     if (rc) return rc;
     if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
     launch_eq_mont2(c->stream, fac_d, 10, 1024, st.elo_d, fac_d + 2 * 10 * 8, khi, 1u << khi, st.ehi_d);
+    return host_now ? eq_setup_host(c, u, st, all_rounds) : 0;
+}
+static int eq_setup_host(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_rounds) {
+    if (st.host_done) return 0;
+    st.host_done = true;
+    const uint32_t kmax = std::max<uint32_t>(st.nvars, 10);
     // prefix[K] = prod_{t<K} (1 - u_t); corr[K] = prefix[K] / prefix[kmax]
     std::vector<Fr> prefix(kmax + 1);
     prefix[0] = kOne;
@@ -737,7 +769,10 @@ static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_
     }
     return 0;
 }
-static Fr eq_corr(const EqState& st, uint32_t K) { return st.corr[K]; }
+static Fr eq_corr(const EqState& st, uint32_t K) {
+    assert(st.host_done);
+    return st.corr[K];
+}
 
 static std::vector<Fr> load_frs(const uint32_t* p, uint32_t n) {
     std::vector<Fr> v(n);
@@ -772,7 +807,8 @@ extern "C" int zkh_ctx_create(int device, zkh_ctx** out) {
         hipMalloc((void**)&c->pub_lay, ZKH_MAX_BATCH * 3 * 4) != hipSuccess ||
         hipMemset(c->pub_lay, 0, ZKH_MAX_BATCH * 3 * 4) != hipSuccess ||
         hipHostMalloc((void**)&c->relay_host, 64 * 4, hipHostMallocCoherent) != hipSuccess ||
-        hipMalloc((void**)&c->relay_vm, 16 * 4) != hipSuccess) {
+        hipMalloc((void**)&c->relay_vm, 16 * 4) != hipSuccess || hipMalloc((void**)&c->flag_d, 64 * 4) != hipSuccess ||
+        hipMemset(c->flag_d, 0, 64 * 4) != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
         delete c;
         return ZKH_EDEV;
@@ -807,6 +843,7 @@ extern "C" int zkh_ctx_destroy(zkh_ctx* c) {
     if (c->pub_lay) (void)hipFree(c->pub_lay);
     if (c->relay_host) (void)hipHostFree(c->relay_host);
     if (c->relay_vm) (void)hipFree(c->relay_vm);
+    if (c->flag_d) (void)hipFree(c->flag_d);
     for (auto& p : c->pending) {
         c->pool.push_back(p.a);
         c->pool.push_back(p.b);
@@ -2424,7 +2461,7 @@ extern "C" int zkh_lu_range_table(zkh_ctx* c, int32_t low, uint32_t len, uint32_
     return ZKH_OK;
 }
 static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, uint32_t** counts_out,
-                     uint32_t** bad_out) {
+                     DevFlag* bad_out) {
     int rc = 0;
     uint32_t* counts = (uint32_t*)scratch_slot(c, SL_TMP5, (size_t)(N + 1) * 4, &rc);
     if (rc) return rc;
@@ -2440,7 +2477,7 @@ static int lu_counts(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, u
         launch_lu_count_planes(c->stream, p, S->n, lowl, N, counts, bad);
     }
     *counts_out = counts;
-    *bad_out = bad;
+    *bad_out = DevFlag{bad, 0};
     return 0;
 }
 // the tensor for the multiplicities of S against N entries: int32 counts (a 4-byte entry
@@ -2454,9 +2491,9 @@ static int mult_alloc(zkh_ctx* c, const zkh_tensor* S, uint32_t N, zkh_tensor** 
 }
 // multiplicities m (N entries, from mult_alloc) of the witness S against a table of N entries
 // at low: LDS histograms for N <= 2^24 (launch_hist), global atomics beyond.  Queues the work
-// only; *bad (device word) becomes nonzero when a witness lies outside the table (check_bad).
+// only; *bad_out (a device condition) is set when a witness lies outside the table (check_bad).
 static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, zkh_tensor* mt,
-                             uint32_t** bad_out) {
+                             DevFlag* bad_out) {
     int rc = 0;
     const DevPlanes m = mt->kind == ZKH_KIND_FR ? mt->planes() : DevPlanes{};
     int32_t* m32 = mt->kind == ZKH_KIND_I32 ? (int32_t*)mt->d : nullptr;
@@ -2479,12 +2516,11 @@ static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint3
     a.low = low;
     fr_store(fr_from_i64(low), a.low_fr);
     a.N = N;
-    uint32_t* bad = (uint32_t*)scratch_slot(c, SL_SMALL, 64, &rc);
-    if (rc) return rc;
+    const DevFlag bad = dev_flag(c, kFlagHist);
     void* hs = scratch_slot(c, SL_TMP5, hist_scratch_bytes(S->n, N), &rc);
     if (rc) return rc;
-    a.bad = bad;
-    HIPCHK(c, hipMemsetAsync(bad, 0, 4, c->stream));
+    a.bad = bad.d;
+    a.tag = bad.tag;
     {
         ProfScope ps(c, "lu_hist", (double)S->n * (S->kind == ZKH_KIND_I32 ? 4 : 32) + (double)N * 32);
         launch_hist(c->stream, a, hs, m, m32);
@@ -2494,11 +2530,11 @@ static int lu_multiplicities(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint3
 }
 // waits for the queued work and fails when the multiplicity pass flagged a witness outside
 // the table
-static int check_bad(zkh_ctx* c, const uint32_t* bad) {
+static int check_bad(zkh_ctx* c, const DevFlag& bad) {
     uint32_t hb = 0;
-    int rc = settle(c, bad, &hb);
+    int rc = settle(c, bad.d, &hb);
     if (rc) return rc;
-    if (hb) return fail(c, ZKH_EARG, "lookup witness outside the table");
+    if (bad.hit(hb)) return fail(c, ZKH_EARG, "lookup witness outside the table");
     return 0;
 }
 extern "C" int zkh_lu_prep(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_t N, zkh_tensor** m_out) {
@@ -2507,7 +2543,7 @@ extern "C" int zkh_lu_prep(zkh_ctx* c, const zkh_tensor* S, int32_t low, uint32_
     zkh_tensor* m;
     int rc;
     if ((rc = mult_alloc(c, S, N, &m))) return rc;
-    uint32_t* bad = nullptr;
+    DevFlag bad{};
     if ((rc = lu_multiplicities(c, S, low, N, m, &bad)) || (rc = check_bad(c, bad))) {
         zkh_tensor_free(m);
         return rc;
@@ -2526,7 +2562,7 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
     if ((rc = mult_alloc(c, S_in, N, &m))) return rc;
     // the mapping is queued behind the multiplicities (its kernels bound-check the index) and
     // one completion wait then checks the witness range
-    uint32_t* bad = nullptr;
+    DevFlag bad{};
     if ((rc = lu_multiplicities(c, S_in, low, N, m, &bad))) {
         zkh_tensor_free(m);
         return rc;
@@ -2570,6 +2606,14 @@ extern "C" int zkh_lu_mapping(zkh_ctx* c, const zkh_tensor* S_in, int32_t low, c
     *m_out = m;
     return ZKH_OK;
 }
+// waits for the queued work; *hf = 1 (a witness outside the table) | 2 (a witness that is not
+// the table's entry at its index) from the gather's two condition words
+static int gather_flags(zkh_ctx* c, const DevFlag& f, uint32_t* hf) {
+    uint32_t w[2] = {0, 0};
+    const int rc = settle(c, f.d, w, 2);
+    *hf = (f.hit(w[0]) ? 1u : 0u) | (f.hit(w[1]) ? 2u : 0u);
+    return rc;
+}
 // A = 1/(S + beta) into planes A (n entries)
 // any_zero (when given): whether some S[i] + beta was zero (its inverse entry is 0)
 static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, DevPlanes A,
@@ -2581,15 +2625,22 @@ static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, De
     uint32_t* bp = (uint32_t*)scratch_slot(c, SL_SMALL, (size_t)nb * 64 + 64, &rc);
     if (rc) return rc;
     uint32_t* others_blk = bp + 8 * (size_t)nb;
-    uint32_t* zflag = bp + 16 * (size_t)nb;  // in the slot's last 64 bytes
     uint32_t bl[8];
     fr_store(beta, bl);
-    HIPCHK(c, hipMemsetAsync(zflag, 0, 4, c->stream));
+    const DevFlag zf = dev_flag(c, kFlagInvZero);
     Publish pb = make_pub(c, 1);
     {
         ProfScope ps(c, "inv_pass1", (double)n * 64 + (double)nb * 256 * 32);
-        launch_inv_pass1(c->stream, S, n, bl, A, others, bp, zflag);
-        launch_inv_blocks(c->stream, bp, nb, others_blk, pb, zflag);
+        launch_inv_pass1(c->stream, S, n, bl, A, others, bp, zf.d, zf.tag);
+        launch_inv_blocks(c->stream, bp, nb, others_blk, pb, zf.d, zf.tag);
+    }
+    // pass 2 is queued now behind a relay that hands it 1/G, so that its launch overlaps the
+    // block pass and the host's inversion
+    RelayGuard relay{c};
+    relay.pending = relay_enqueue(c);
+    {
+        ProfScope ps(c, "inv_pass2", (double)n * (aos ? 128 : 96) + (double)nb * 256 * 32);
+        launch_inv_pass2(c->stream, S, n, bl, A, others, others_blk, nullptr, c->relay_vm, aos);
     }
     if ((rc = wait_pub(c, pb.seq))) return rc;
     // the grand product G (never zero) -> its plain inverse, once, on the host
@@ -2598,8 +2649,8 @@ static int batch_inverse(zkh_ctx* c, DevPlanes S, uint32_t n, const Fr& beta, De
     if (any_zero) *any_zero = __atomic_load_n(c->pub_host + 8, __ATOMIC_ACQUIRE) != 0;
     uint32_t inv_g[8];
     fr_store(fr_inv(G), inv_g);
-    ProfScope ps(c, "inv_pass2", (double)n * (aos ? 128 : 96) + (double)nb * 256 * 32);
-    launch_inv_pass2(c->stream, S, n, bl, A, others, others_blk, inv_g, aos);
+    relay_send(c, relay.pending, inv_g);
+    relay.pending = 0;
     return 0;
 }
 extern "C" int zkh_lu_inverse(zkh_ctx* c, const zkh_tensor* S, const uint32_t beta[8], zkh_tensor** A_out) {
@@ -2653,18 +2704,16 @@ extern "C" int zkh_lu_range_inverse(zkh_ctx* c, const zkh_tensor* S, int32_t low
     // the table's inverse (tlookup.cu:50-62 over T, as zkh_lu_prove takes it), then A read off it
     bool tzero = false, szero = false;
     if ((rc = batch_inverse(c, Tp, N, fr_load(beta), Binv->planes(), &tzero))) return drop(rc);
-    uint32_t* flags = (uint32_t*)scratch_slot(c, SL_PARTIAL, 256, &rc);
-    if (rc) return drop(rc);
-    HIPCHK(c, hipMemsetAsync(flags, 0, 4, c->stream));
+    const DevFlag flags = dev_flag(c, kFlagGather);
     uint32_t hf = 0;
     if (D) {
         ProfScope ps(c, "lu_range_gather", (double)D * (32 + 32 + 32));
         uint32_t lowl[8];
         fr_store(fr_from_i64(low), lowl);
         const uint32_t tlen = range_shortcut_len(T, low);
-        launch_lu_range_gather(c->stream, ss, D, lowl, st, tlen, N, Binv->planes(), A->planes(), flags);
+        launch_lu_range_gather(c->stream, ss, D, lowl, st, tlen, N, Binv->planes(), A->planes(), flags.d, flags.tag);
     }
-    if ((rc = settle(c, flags, &hf))) return drop(rc);
+    if ((rc = gather_flags(c, flags, &hf))) return drop(rc);
     // a witness outside the table or not the table's entry at its index: the direct batched
     // inversion of S (zkob_rescale.cu:121-123), as zkh_lu_inverse
     if (hf) {
@@ -2722,9 +2771,7 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
     if (rc) return drop(rc);
     if ((rc = batch_inverse(c, Tcomb->planes(), N, fr_load(beta), Binv->planes(), &tzero, binv_aos)))
         return drop(rc);
-    uint32_t* flags = (uint32_t*)scratch_slot(c, SL_PARTIAL, 256, &rc);
-    if (rc) return drop(rc);
-    HIPCHK(c, hipMemsetAsync(flags, 0, 4, c->stream));
+    const DevFlag flags = dev_flag(c, kFlagGather);
     uint32_t hf = 0;
     if (D) {
         ProfScope ps(c, "lu_tuple_gather", (double)D * (4 + 4 + 4 + 32 + 32 + 32));
@@ -2734,9 +2781,9 @@ extern "C" int zkh_lu_tuple_inverse(zkh_ctx* c, const zkh_tensor* G, int32_t low
         // a range table at this low: T[j] == G[i] iff G[i] - low is j < len, read from G alone
         const uint32_t tlen = range_shortcut_len(T, low);
         launch_lu_tuple_gather(c->stream, sg, D, lowl, st, tlen, S ? ss : sm, S != nullptr, N, r, rm, Binv->planes(),
-                               binv_aos, comb->planes(), A->planes(), flags);
+                               binv_aos, comb->planes(), A->planes(), flags.d, flags.tag);
     }
-    if ((rc = settle(c, flags, &hf))) return drop(rc);
+    if ((rc = gather_flags(c, flags, &hf))) return drop(rc);
     if (hf & 1u) return drop(fail(c, ZKH_EARG, "lookup witness outside the table"));
     // an entry whose G is not the table's at its index (comb is then no table entry): A by
     // the direct batched inversion of comb (zkob_glu.cu:158-160)
@@ -3137,11 +3184,13 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     Fr alpha_sq = fr_mul(alpha, alpha);
     Fr Cc = fr_sub(alpha_sq, bm);
     Fr claim = fr_add(alpha, alpha_sq);
-    Fr inv_ratio = fr_mul(fr_u64(N), fr_inv(fr_u64(D)));
+    // N / D with D / N a power of two: halve 1 log2(D / N) times
+    Fr inv_ratio = kOne;
+    for (uint32_t t = N; t < D; t <<= 1) inv_ratio = fr_half(inv_ratio);
     Fr inv2 = fr_inv2();
 
-    EqState eq;
-    if ((rc = eq_setup(c, u, eq))) return rc;
+    EqState eq;  // tables now, the host part once the first round is queued
+    if ((rc = eq_setup(c, u, eq, true, false))) return rc;
 
     // table handles: source = current data, dst = working buffer
     DevPlanes a_src = Ac, s_src = Sc, b_src = Bw, t_src = Tc, m_src = mc;
@@ -3249,6 +3298,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     for (uint32_t r = 0; r < logD; r++) {
         const uint32_t n = D >> r;
         if (persists(r)) {  // phase 2: the rest in one launch
+            if ((rc = eq_setup_host(c, u, eq))) return rc;
             LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD, &pc};
             if (m_src32) return fail(c, ZKH_EDEV, "internal: unfolded int32 m at the persistent loop");
             const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
@@ -3266,6 +3316,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             relay.pending = relay_enqueue(c);
             next = launch(r + 1, c->relay_vm);
         }
+        if ((rc = eq_setup_host(c, u, eq))) return rc;  // once, behind the first launches
         const uint32_t k = logD - r;  // remaining variables
         const uint32_t K = k - 1;     // eq variables of the pairs
         const Fr ul = u[k - 1];
@@ -4085,8 +4136,8 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     if (rc) return rc;
     Uw = U->kind == ZKH_KIND_FR || u_i32 ? scratch_planes(c, SL_TMP2, n / 2 + 1, &rc) : Uc;
     if (rc) return rc;
-    EqState eq;
-    if (ueq && (rc = eq_setup(c, *ueq, eq))) return rc;
+    EqState eq;  // tables now, the host part once the first round is queued
+    if (ueq && (rc = eq_setup(c, *ueq, eq, true, false))) return rc;
     Fr claim = claim_label ? kZero : fr_load(claim_l), cE = kOne;
     DevPlanes e_src = Ec, s_src = Sc, u_src = Uc;
     uint32_t vm[8] = {0};
@@ -4155,6 +4206,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         const int fold = r > 0;
         if (persists(r)) {  // the rest in one launch
             if (s32 || u32) return fail(c, ZKH_EDEV, "internal: unfolded int32 table at the persistent loop");
+            if (ueq && (rc = eq_setup_host(c, *ueq, eq))) return rc;
             if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, u_ones, vm, claim, cE,
                                         ev_out, ws_out, e_fin, s_fin, u_fin)))
                 return rc;
@@ -4170,6 +4222,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             relay.pending = relay_enqueue(c);
             next = launch(r + 1, c->relay_vm);
         }
+        if (ueq && (rc = eq_setup_host(c, *ueq, eq))) return rc;  // once, behind the first launches
         if (r == 0 && ueq && k > 1) {  // 1/u_j for the rounds that derive (batch inverse, host)
             inv_u.assign(k, kZero);
             std::vector<Fr> pre(k + 1, kOne);
