@@ -326,6 +326,19 @@ __global__ __launch_bounds__(NT) void k_eq_mont_quad(EqTab t0, EqTab t1, uint32_
     const fr_t e = eq_prod_quad(T.fac, T.K, b < T.n ? b : 0, q);  // every lane of a quad takes part
     if (q == 0 && b < T.n) st_aos(T.out, b, e);
 }
+// The same with the factors in the launch's arguments (no upload ahead of it): table 0 takes
+// factors [0, K0), table 1 factors [K0, K0 + K1), in plain form when plain1 is set.
+__global__ __launch_bounds__(NT) void k_eq_mont_quad_ka(FacArg f, uint32_t K0, uint32_t n0, uint32_t* out0,
+                                                        uint32_t K1, uint32_t n1, uint32_t* out1, uint32_t g0,
+                                                        uint32_t plain1) {
+    const bool second = blockIdx.x >= g0;
+    const uint32_t K = second ? K1 : K0, n = second ? n1 : n0;
+    uint32_t* out = second ? out1 : out0;
+    const uint32_t i = (blockIdx.x - (second ? g0 : 0)) * NT + threadIdx.x;
+    const uint32_t b = i >> 2, q = i & 3;
+    const fr_t e = eq_prod_quad(f.w + (second ? 16 * K0 : 0), K, b < n ? b : 0, q);
+    if (q == 0 && b < n) st_aos(out, b, second && plain1 ? mont_mul(e, plain_one()) : e);
+}
 #define EQ_QUAD_MAX (1u << 14)  // larger tables: one entry per thread (product throughput)
 void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, uint32_t* out) {
     if (n <= EQ_QUAD_MAX) {
@@ -334,6 +347,13 @@ void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, 
         return;
     }
     k_eq_mont<<<grid_for(n, NT, 4096), NT, 0, s>>>(fac, K, n, out);
+}
+bool launch_eq_mont2_ka(hipStream_t s, const FacArg& f, uint32_t K0, uint32_t n0, uint32_t* out0, uint32_t K1,
+                        uint32_t n1, uint32_t* out1, bool plain1) {
+    if (n0 > EQ_QUAD_MAX || n1 > EQ_QUAD_MAX || K0 + K1 > ZKH_FAC_ARG_VARS) return false;
+    const uint32_t g0 = (4 * n0 + NT - 1) / NT, g1 = (4 * n1 + NT - 1) / NT;
+    k_eq_mont_quad_ka<<<g0 + g1, NT, 0, s>>>(f, K0, n0, out0, K1, n1, out1, g0, plain1 ? 1u : 0u);
+    return true;
 }
 void launch_eq_mont2(hipStream_t s, const uint32_t* fac0, uint32_t K0, uint32_t n0, uint32_t* out0,
                      const uint32_t* fac1, uint32_t K1, uint32_t n1, uint32_t* out1) {

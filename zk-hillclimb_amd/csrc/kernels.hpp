@@ -73,6 +73,16 @@ void launch_eq_mont(hipStream_t s, const uint32_t* fac, uint32_t K, uint32_t n, 
 void launch_eq_mont2(hipStream_t s, const uint32_t* fac0, uint32_t K0, uint32_t n0, uint32_t* out0,
                      const uint32_t* fac1, uint32_t K1, uint32_t n1, uint32_t* out1);
 
+// the same with the factors (1 - u_t, u_t) as launch arguments: table 0 from factors [0, K0),
+// table 1 from [K0, K0 + K1) (plain form when plain1); false (nothing launched) when a table
+// exceeds the four-lanes form's size or the factors do not fit
+#define ZKH_FAC_ARG_VARS 32
+struct FacArg {
+    uint32_t w[ZKH_FAC_ARG_VARS * 16];
+};
+bool launch_eq_mont2_ka(hipStream_t s, const FacArg& f, uint32_t K0, uint32_t n0, uint32_t* out0, uint32_t K1,
+                        uint32_t n1, uint32_t* out1, bool plain1 = false);
+
 // ---- dot products / sums (block partials, AoS, summed on the host) ----
 // partial[b] = sum montmul(a_i, b_i) over the block's range (carries 2^-256)
 uint32_t launch_dot_planes(hipStream_t s, DevPlanes a, DevPlanes b, uint32_t n, Publish pub);

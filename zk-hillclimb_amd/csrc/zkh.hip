@@ -732,14 +732,23 @@ static int eq_setup(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_
     make_fac(u, 10, fac);
     st.nvars = (uint32_t)u.size();
     const uint32_t kmax = std::max<uint32_t>(st.nvars, 10), khi = kmax - 10;
-    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, fac.size() * 4, &rc);
-    if (rc) return rc;
     st.elo_d = (uint32_t*)scratch_slot(c, SL_ELO, 1024 * 32, &rc);
     if (rc) return rc;
     st.ehi_d = (uint32_t*)scratch_slot(c, SL_EHI, ((size_t)32 << khi), &rc);
     if (rc) return rc;
-    if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
-    launch_eq_mont2(c->stream, fac_d, 10, 1024, st.elo_d, fac_d + 2 * 10 * 8, khi, 1u << khi, st.ehi_d);
+    // the factors as launch arguments where they fit (no upload ahead of the tables' launch)
+    bool launched = false;
+    if (fac.size() <= sizeof(FacArg) / 4) {
+        FacArg fa;
+        memcpy(fa.w, fac.data(), fac.size() * 4);
+        launched = launch_eq_mont2_ka(c->stream, fa, 10, 1024, st.elo_d, khi, 1u << khi, st.ehi_d);
+    }
+    if (!launched) {
+        uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, fac.size() * 4, &rc);
+        if (rc) return rc;
+        if ((rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
+        launch_eq_mont2(c->stream, fac_d, 10, 1024, st.elo_d, fac_d + 2 * 10 * 8, khi, 1u << khi, st.ehi_d);
+    }
     return host_now ? eq_setup_host(c, u, st, all_rounds) : 0;
 }
 static int eq_setup_host(zkh_ctx* c, const std::vector<Fr>& u, EqState& st, bool all_rounds) {
@@ -1425,15 +1434,28 @@ extern "C" int zkh_eq_table(zkh_ctx* c, const uint32_t* u, uint32_t k, zkh_tenso
     int rc = 0;
     std::vector<uint32_t> fac;
     make_fac(load_frs(u, k), 0, fac);
-    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
-    if (rc) return rc;
-    if (k && (rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
     // E = Tlo (first min(k,10) variables, Montgomery) (x) Thi (the rest, plain)
     const uint32_t klo = k < 10 ? k : 10, khi = k - klo;
     uint32_t* tlo = (uint32_t*)scratch_slot(c, SL_EB, ((size_t)1 << klo) * 32, &rc);
     if (rc) return rc;
     uint32_t* thi = (uint32_t*)scratch_slot(c, SL_EO, ((size_t)1 << khi) * 32, &rc);
     if (rc) return rc;
+    zkh_tensor* t;
+    // the factors as launch arguments where they fit (no uploads ahead of the launches)
+    if (k && fac.size() <= sizeof(FacArg) / 4) {
+        FacArg fa;
+        memcpy(fa.w, fac.data(), fac.size() * 4);
+        if ((rc = tensor_alloc(c, ZKH_KIND_FR, 1u << k, &t))) return rc;
+        if (launch_eq_mont2_ka(c->stream, fa, klo, 1u << klo, tlo, khi, 1u << khi, thi, true)) {
+            launch_eq_outer(c->stream, tlo, thi, klo, 1u << k, t->planes());
+            *out = t;
+            return ZKH_OK;
+        }
+        zkh_tensor_free(t);
+    }
+    uint32_t* fac_d = (uint32_t*)scratch_slot(c, SL_FAC, std::max<size_t>(fac.size() * 4, 32), &rc);
+    if (rc) return rc;
+    if (k && (rc = upload(c, fac_d, fac.data(), fac.size() * 4))) return rc;
     EqTabDesc d[2] = {};
     d[0].fac = fac_d;
     d[0].out = tlo;
@@ -1449,7 +1471,6 @@ extern "C" int zkh_eq_table(zkh_ctx* c, const uint32_t* u, uint32_t k, zkh_tenso
     EqTabDesc* d_dev = (EqTabDesc*)scratch_slot(c, SL_DESC, sizeof(d), &rc);
     if (rc) return rc;
     if ((rc = upload(c, d_dev, d, sizeof(d)))) return rc;
-    zkh_tensor* t;
     if ((rc = tensor_alloc(c, ZKH_KIND_FR, 1u << k, &t))) return rc;
     launch_eq_mont_multi(c->stream, d_dev, 2, d[1].blk_begin + (d[1].n + 255) / 256);
     launch_eq_outer(c->stream, tlo, thi, klo, 1u << k, t->planes());
