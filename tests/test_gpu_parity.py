@@ -944,12 +944,15 @@ def test_hp_prove_eq_wrong_claim_stops(zkh, ctx, k):
     assert bytes(st_g) == bytes(st_o)
 
 
-def test_lu_hp_per_round_launch_path(zkh, ctx, monkeypatch):
-    """Every round of the lookup and Hadamard sumchecks as its own launch (the persistent loops
-    off): the folding rounds derive their sums at 1 down to 2-entry tables, the terminals come
-    from the folded tables, and the proofs equal the oracle's (phase 1 and 2, explicit E, eq
-    form, U all ones over an int32 S)."""
-    monkeypatch.setenv("ZKH_NO_PERSIST", "1")
+@pytest.mark.parametrize("mode", ["per_round", "one_round"])
+def test_lu_hp_per_round_launch_path(zkh, ctx, mode, monkeypatch):
+    """per_round: every round of the lookup and Hadamard sumchecks as its own launch (the
+    persistent loops off): the folding rounds derive their sums at 1 down to 2-entry tables,
+    the terminals come from the folded tables.  one_round: the persistent loops with one
+    round per message, in both of their phases (the blocks' own rounds, then the block that
+    gathers every block's entry).  The proofs equal the oracle's (phase 1 and 2, explicit E,
+    eq form, U all ones over an int32 S)."""
+    monkeypatch.setenv("ZKH_NO_PERSIST" if mode == "per_round" else "ZKH_PERSIST_ONE", "1")
     rng = np.random.default_rng(41)
     for D, N, low in [(1 << 10, 1 << 10, -512), (1 << 12, 1 << 8, -128)]:
         vals = rng.integers(low, low + N, size=D).astype(np.int32)

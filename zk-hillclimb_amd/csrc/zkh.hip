@@ -668,6 +668,30 @@ static uint32_t bits_for(uint64_t absmax) {
     return b;  // absmax < 2^b
 }
 static Fr fix1(const Fr& x) { return fr_mont_mul(x, kR2); }  // undo one 2^-256
+// The round logic's products take one Montgomery product each when one operand is prepared:
+// mulm(a, to_m(b)) = a b (plain), and mulm(x, to_mm(c)) = fix1(x) c for a device sum x that
+// carries one 2^-256.
+static inline Fr mulm(const Fr& a, const Fr& bm) { return fr_mont_mul(a, bm); }
+static inline Fr to_m(const Fr& b) { return fr_to_mont(b); }
+static inline Fr to_mm(const Fr& c) { return fr_to_mont(fr_to_mont(c)); }
+// e(1), e(2), e(3) of the cubic c0 + c1 t + c2 t^2 + c3 t^3 (Horner by additions)
+static void cubic_at123(const Fr c[4], Fr e[4]) {
+    e[0] = c[0];
+    e[1] = fr_add(fr_add(c[0], c[1]), fr_add(c[2], c[3]));
+    Fr a2 = c[3], a3 = c[3];
+    for (int i = 2; i >= 0; i--) {
+        a2 = fr_add(fr_add(a2, a2), c[i]);
+        a3 = fr_add(fr_add(fr_add(a3, a3), a3), c[i]);
+    }
+    e[2] = a2;
+    e[3] = a3;
+}
+// c(v) of the cubic by Horner, vm = to_m(v)
+static Fr cubic_at(const Fr c[4], const Fr& vm) {
+    Fr acc = c[3];
+    for (int i = 2; i >= 0; i--) acc = fr_add(mulm(acc, vm), c[i]);
+    return acc;
+}
 static Fr fix2(const Fr& x) {
     static const Fr r3 = fr_rpow(3);
     return fr_mont_mul(x, r3);
@@ -2836,12 +2860,9 @@ struct LuPieces {
     bool b = false;  // Ib, Mb hold (a phase-2 round has run)
 };
 // q(v) of a quadratic piece from q(0), q(1) and its t^2 coefficient c2
-static Fr quad_at(const Fr& q0, const Fr& q1, const Fr& c2, const Fr& v) {
-    return fr_add(q0, fr_mul(v, fr_add(fr_sub(fr_sub(q1, q0), c2), fr_mul(v, c2))));
-}
-// q(1) of an eq-weighted piece with claim I and eq coordinate ul: (I - (1 - ul) q(0)) / ul
-static Fr eq_piece_q1(const Fr& I, const Fr& q0, const Fr& ul, const Fr& inv_ul) {
-    return fr_mul(fr_sub(I, fr_mul(fr_sub(kOne, ul), q0)), inv_ul);
+// (vm = to_m(v))
+static Fr quad_at_m(const Fr& q0, const Fr& q1, const Fr& c2, const Fr& vm) {
+    return fr_add(q0, mulm(fr_add(fr_sub(fr_sub(q1, q0), c2), mulm(c2, vm)), vm));
 }
 // logUp phase-2 state carried across rounds (zkob_lookup.cuh:143-198): the running claim,
 // alpha and alpha^2 eq accumulators, N/D, the eq point u and its device tables
@@ -2851,34 +2872,60 @@ struct LuState {
     const EqState* eq;
     uint32_t logD;
     LuPieces* pc;
+    Fr inv_ratio_m;  // to_m(inv_ratio)
+    // a round's state update left for after its challenge is sent (lu_phase2_round's defer)
+    struct Pending {
+        bool on = false;
+        Fr coef[4], q[9], s3, s4, ul, v, v_m;
+    } pend;
 };
+// applies the update of the round whose challenge is v (the claim c(v), alpha and alpha^2
+// times eq(ul, v), the pieces at v)
+static void lu_apply(LuState& L) {
+    LuState::Pending& p = L.pend;
+    if (!p.on) return;
+    p.on = false;
+    L.claim = cubic_at(p.coef, p.v_m);
+    const Fr uv = mulm(p.ul, p.v_m);
+    const Fr eqv_m = to_m(fr_add(fr_sub(fr_add(uv, uv), fr_add(p.ul, p.v)), kOne));  // eq(ul, v)
+    L.alpha = mulm(L.alpha, eqv_m);
+    L.alpha_sq = mulm(L.alpha_sq, eqv_m);
+    L.pc->Ia = quad_at_m(p.q[0], p.q[1], p.q[2], p.v_m);
+    L.pc->Sa = fr_add(p.s3, mulm(fr_sub(p.s4, p.s3), p.v_m));
+    L.pc->Ib = quad_at_m(p.q[3], p.q[4], p.q[5], p.v_m);
+    L.pc->Mb = quad_at_m(p.q[6], p.q[7], p.q[8], p.v_m);
+    L.pc->b = true;
+}
 // One phase-2 round from its 11 sums (device order: w a s sums 0..2, sum a0, sum a1, w b t
 // sums 0..2, m b sums 0..2).  dev: sums from the device (products x 2^-256, eq weights with
 // the padded factors that corr(K) removes); otherwise exact host sums.  Absorbs "p0".."p3",
 // draws the challenge v, updates the state; false on a round inconsistency.
 static bool lu_phase2_round(uint8_t tr[32], LuState& L, uint32_t r, const Fr sm[11], bool dev, Fr& v,
-                            uint32_t* ev_out, uint32_t* ws_out) {
+                            uint32_t* ev_out, uint32_t* ws_out, bool defer = false) {
+    lu_apply(L);
     const uint32_t k = L.logD - r, K = k - 1;
     const Fr ul = (*L.u)[k - 1];
-    const Fr corr = dev ? eq_corr(*L.eq, K) : kOne;
-    auto pr = [&](const Fr& x) { return dev ? fr_mul(fix1(x), corr) : x; };  // w-weighted product sums
-    auto mb = [&](const Fr& x) { return dev ? fix1(x) : x; };                 // m b product sums
+    const Fr corr_mm = dev ? to_mm(eq_corr(*L.eq, K)) : kZero;
+    auto pr = [&](const Fr& x) { return dev ? mulm(x, corr_mm) : x; };  // w-weighted product sums
+    auto mb = [&](const Fr& x) { return dev ? fix1(x) : x; };          // m b product sums
+    LuState::Pending& p = L.pend;
     const Fr qa0 = pr(sm[0]), qa1 = pr(sm[1]), qa2 = pr(sm[2]);
     const Fr qb0 = pr(sm[5]), qb1 = pr(sm[6]), qb2 = pr(sm[7]);
-    const Fr coefBT = fr_mul(L.inv_ratio, L.alpha_sq);
-    const Fr Q0 = fr_add(fr_mul(L.alpha, qa0), fr_mul(coefBT, qb0));
-    const Fr Q1 = fr_add(fr_mul(L.alpha, fr_sub(fr_sub(qa1, qa0), qa2)), fr_mul(coefBT, fr_sub(fr_sub(qb1, qb0), qb2)));
-    const Fr Q2 = fr_add(fr_mul(L.alpha, qa2), fr_mul(coefBT, qb2));
+    const Fr alpha_m = to_m(L.alpha), coefBT_m = to_m(mulm(L.alpha_sq, L.inv_ratio_m));
+    const Fr Q0 = fr_add(mulm(qa0, alpha_m), mulm(qb0, coefBT_m));
+    const Fr Q1 = fr_add(mulm(fr_sub(fr_sub(qa1, qa0), qa2), alpha_m), mulm(fr_sub(fr_sub(qb1, qb0), qb2), coefBT_m));
+    const Fr Q2 = fr_add(mulm(qa2, alpha_m), mulm(qb2, coefBT_m));
     const Fr M0 = mb(sm[8]), M1 = mb(sm[9]), M2 = mb(sm[10]);
     const Fr Mc1 = fr_sub(fr_sub(M1, M0), M2);
-    const Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
-    Fr coef[4];
-    coef[0] = fr_sub(fr_add(fr_mul(e0, Q0), sm[3]), fr_mul(L.inv_ratio, M0));
-    coef[1] = fr_sub(fr_add(fr_add(fr_mul(e0, Q1), fr_mul(e1, Q0)), fr_sub(sm[4], sm[3])), fr_mul(L.inv_ratio, Mc1));
-    coef[2] = fr_sub(fr_add(fr_mul(e0, Q2), fr_mul(e1, Q1)), fr_mul(L.inv_ratio, M2));
-    coef[3] = fr_mul(e1, Q2);
-    const Fr e[4] = {coef[0], fr_poly_eval(coef, 3, kOne), fr_poly_eval(coef, 3, fr_u64(2)),
-                     fr_poly_eval(coef, 3, fr_u64(3))};
+    const Fr e0_m = to_m(fr_sub(kOne, ul)), e1_m = to_m(fr_sub(fr_add(ul, ul), kOne));
+    const Fr& ir_m = L.inv_ratio_m;
+    Fr* coef = p.coef;
+    coef[0] = fr_sub(fr_add(mulm(Q0, e0_m), sm[3]), mulm(M0, ir_m));
+    coef[1] = fr_sub(fr_add(fr_add(mulm(Q1, e0_m), mulm(Q0, e1_m)), fr_sub(sm[4], sm[3])), mulm(Mc1, ir_m));
+    coef[2] = fr_sub(fr_add(mulm(Q2, e0_m), mulm(Q1, e1_m)), mulm(M2, ir_m));
+    coef[3] = mulm(Q2, e1_m);
+    Fr e[4];
+    cubic_at123(coef, e);
     if (!fr_eq(L.claim, fr_add(e[0], e[1]))) return false;
     static const char* lab[4] = {"p0", "p1", "p2", "p3"};
     for (int t = 0; t < 4; t++) {
@@ -2887,15 +2934,15 @@ static bool lu_phase2_round(uint8_t tr[32], LuState& L, uint32_t r, const Fr sm[
     }
     v = tr_challenge(tr);
     if (ws_out) fr_store(v, ws_out + 8 * r);
-    L.claim = fr_poly_eval(coef, 3, v);
-    const Fr eqv = fr_eq2(ul, v);
-    L.alpha = fr_mul(L.alpha, eqv);
-    L.alpha_sq = fr_mul(L.alpha_sq, eqv);
-    L.pc->Ia = quad_at(qa0, qa1, qa2, v);
-    L.pc->Sa = fr_add(sm[3], fr_mul(v, fr_sub(sm[4], sm[3])));
-    L.pc->Ib = quad_at(qb0, qb1, qb2, v);
-    L.pc->Mb = quad_at(M0, M1, M2, v);
-    L.pc->b = true;
+    const Fr q[9] = {qa0, qa1, qa2, qb0, qb1, qb2, M0, M1, M2};
+    for (int i = 0; i < 9; i++) p.q[i] = q[i];
+    p.s3 = sm[3];
+    p.s4 = sm[4];
+    p.ul = ul;
+    p.v = v;
+    p.v_m = to_m(v);
+    p.on = true;
+    if (!defer) lu_apply(L);
     return true;
 }
 // Phase-2 rounds r0 .. logD-1 in one persistent launch (see LuPersist) once the tables have
@@ -3035,13 +3082,14 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
             for (uint32_t b = 0; b < nb; b++)
                 for (int t = 0; t < 11; t++) sm[t] = fr_add(sm[t], slot_fr(b, t));
             Fr v;
-            if (!lu_phase2_round(tr, L, r1, sm, true, v, ev_out, ws_out)) {
+            if (!lu_phase2_round(tr, L, r1, sm, true, v, ev_out, ws_out, true)) {
                 quit();
                 return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r1);
             }
             uint32_t xm[8];
-            fr_store(fr_to_mont(v), xm);
+            fr_store(L.pend.v_m, xm);
             send(seq, xm, 8);
+            lu_apply(L);  // the state update after the command
             if (tracing) tr_h.push_back(now_us());
             lr++;
             continue;
@@ -3058,36 +3106,38 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
         for (uint32_t b = 0; b < nb; b++)
             for (int p = 0; p < 31; p++) G[p] = fr_add(G[p], slot_fr(b, p));
         const uint32_t K2 = L.logD - r1 - 2;  // eq coordinate of y2
-        const Fr rho = fr_mul((*L.u)[K2], L.eq->inv1mu[K2]);
+        const Fr rho_m = mulm(to_m((*L.u)[K2]), to_m(L.eq->inv1mu[K2]));
         Fr sm[11], v1, v2;
         for (int a = 0; a < 3; a++) {
-            sm[a] = fr_add(G[3 * a], fr_mul(rho, G[3 * a + 1]));
-            sm[5 + a] = fr_add(G[9 + 3 * a], fr_mul(rho, G[9 + 3 * a + 1]));
+            sm[a] = fr_add(G[3 * a], mulm(G[3 * a + 1], rho_m));
+            sm[5 + a] = fr_add(G[9 + 3 * a], mulm(G[9 + 3 * a + 1], rho_m));
             sm[8 + a] = fr_add(G[18 + 3 * a], G[18 + 3 * a + 1]);
         }
         sm[3] = fr_add(G[27], G[28]);
         sm[4] = fr_add(G[29], G[30]);
-        if (!lu_phase2_round(tr, L, r1, sm, true, v1, ev_out, ws_out)) {
+        if (!lu_phase2_round(tr, L, r1, sm, true, v1, ev_out, ws_out, true)) {
             quit();
             return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r1);
         }
+        const Fr v1_m = L.pend.v_m;
         for (int b = 0; b < 3; b++) {
-            sm[b] = quad_at(G[b], G[3 + b], G[6 + b], v1);
-            sm[5 + b] = quad_at(G[9 + b], G[12 + b], G[15 + b], v1);
-            sm[8 + b] = quad_at(G[18 + b], G[21 + b], G[24 + b], v1);
+            sm[b] = quad_at_m(G[b], G[3 + b], G[6 + b], v1_m);
+            sm[5 + b] = quad_at_m(G[9 + b], G[12 + b], G[15 + b], v1_m);
+            sm[8 + b] = quad_at_m(G[18 + b], G[21 + b], G[24 + b], v1_m);
         }
-        sm[3] = fr_add(G[27], fr_mul(v1, fr_sub(G[29], G[27])));
-        sm[4] = fr_add(G[28], fr_mul(v1, fr_sub(G[30], G[28])));
-        if (!lu_phase2_round(tr, L, r1 + 1, sm, true, v2, ev_out, ws_out)) {
+        sm[3] = fr_add(G[27], mulm(fr_sub(G[29], G[27]), v1_m));
+        sm[4] = fr_add(G[28], mulm(fr_sub(G[30], G[28]), v1_m));
+        if (!lu_phase2_round(tr, L, r1 + 1, sm, true, v2, ev_out, ws_out, true)) {
             quit();
             return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r1 + 1);
         }
-        // double fold weights of T[c + (2 y1 + y2) q]
-        const Fr a1 = fr_sub(kOne, v1), a2 = fr_sub(kOne, v2);
-        const Fr Lw[4] = {fr_mul(a1, a2), fr_mul(a1, v2), fr_mul(v1, a2), fr_mul(v1, v2)};
+        // double fold weights of T[c + (2 y1 + y2) q], in Montgomery form: (1 - v)_m = 1_m - v_m
+        const Fr v2_m = L.pend.v_m, a1_m = fr_sub(fr_one_m(), v1_m), a2_m = fr_sub(fr_one_m(), v2_m);
+        const Fr Lw_m[4] = {mulm(a1_m, a2_m), mulm(a1_m, v2_m), mulm(v1_m, a2_m), mulm(v1_m, v2_m)};
         uint32_t xm[32];
-        for (int j = 0; j < 4; j++) fr_store(fr_to_mont(Lw[j]), xm + 8 * j);
+        for (int j = 0; j < 4; j++) fr_store(Lw_m[j], xm + 8 * j);
         send(seq, xm, 32);
+        lu_apply(L);  // the state update after the command
         if (tracing) tr_h.push_back(now_us());
         lr += 2;
     }
@@ -3108,22 +3158,26 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
         std::vector<Fr> wl;
         eq_low_weights(*L.u, K, h, wl);
         for (uint32_t i = 0; i < h; i++) {
-            const Fr w = wl[i];
-            const Fr wa0 = fr_mul(w, A[i]), wda = fr_mul(w, fr_sub(A[i + h], A[i]));
-            const Fr wb0 = fr_mul(w, B[i]), wdb = fr_mul(w, fr_sub(B[i + h], B[i]));
-            const Fr add[11] = {fr_mul(wa0, fr_add(S[i], beta)), fr_mul(fr_add(wa0, wda), fr_add(S[i + h], beta)),
-                                fr_mul(wda, fr_sub(S[i + h], S[i])), A[i], A[i + h],
-                                fr_mul(wb0, fr_add(T[i], beta)), fr_mul(fr_add(wb0, wdb), fr_add(T[i + h], beta)),
-                                fr_mul(wdb, fr_sub(T[i + h], T[i])), fr_mul(M[i], B[i]), fr_mul(M[i + h], B[i + h]),
-                                fr_mul(fr_sub(M[i + h], M[i]), fr_sub(B[i + h], B[i]))};
+            // w A, w dA, w B, w dB in Montgomery form (w_mm = w 2^512): each product below is one
+            const Fr w_mm = to_mm(wl[i]);
+            const Fr wa0 = mulm(A[i], w_mm), wda = mulm(fr_sub(A[i + h], A[i]), w_mm);
+            const Fr wb0 = mulm(B[i], w_mm), wdb = mulm(fr_sub(B[i + h], B[i]), w_mm);
+            const Fr b0_m = to_m(B[i]), b1_m = to_m(B[i + h]);
+            const Fr add[11] = {mulm(fr_add(S[i], beta), wa0), mulm(fr_add(S[i + h], beta), fr_add(wa0, wda)),
+                                mulm(fr_sub(S[i + h], S[i]), wda), A[i], A[i + h],
+                                mulm(fr_add(T[i], beta), wb0), mulm(fr_add(T[i + h], beta), fr_add(wb0, wdb)),
+                                mulm(fr_sub(T[i + h], T[i]), wdb), mulm(M[i], b0_m), mulm(M[i + h], b1_m),
+                                mulm(fr_sub(M[i + h], M[i]), fr_sub(b1_m, b0_m))};
             for (int q = 0; q < 11; q++) sm[q] = fr_add(sm[q], add[q]);
         }
         Fr v;
         if (!lu_phase2_round(tr, L, r, sm, false, v, ev_out, ws_out))
             return fail(c, ZKH_EROUND, "phase2 round inconsistency (witness bug) at round %u", r);
+        const Fr v_m = to_m(v);
         for (int q = 0; q < 5; q++)
-            for (uint32_t i = 0; i < h; i++) t[q][i] = fr_add(t[q][i], fr_mul(v, fr_sub(t[q][i + h], t[q][i])));
+            for (uint32_t i = 0; i < h; i++) t[q][i] = fr_add(t[q][i], mulm(fr_sub(t[q][i + h], t[q][i]), v_m));
     }
+    lu_apply(L);
     for (int i = 0; i < 5; i++) fin[i] = t[i][0];
     if (tracing) {
         fprintf(stderr, "[zkh] lu persistent loop: n=%u, %u blocks, %u device + %u host rounds in %.1f us\n", n, nb, R,
@@ -3208,7 +3262,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     // N / D with D / N a power of two: halve 1 log2(D / N) times
     Fr inv_ratio = kOne;
     for (uint32_t t = N; t < D; t <<= 1) inv_ratio = fr_half(inv_ratio);
-    Fr inv2 = fr_inv2();
+    const Fr inv_ratio_m = to_m(inv_ratio);
 
     EqState eq;  // tables now, the host part once the first round is queued
     if ((rc = eq_setup(c, u, eq, true, false))) return rc;
@@ -3217,7 +3271,6 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     DevPlanes a_src = Ac, s_src = Sc, b_src = Bw, t_src = Tc, m_src = mc;
     bool as_pending = false, btm_pending = false;  // a fold with vm is owed
     uint32_t vm[8] = {0};
-    Fr three = fr_u64(3);
     const bool tracing = trace_on();
     std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
     bool persisted = false;    // the last rounds ran in lu_persist_rounds
@@ -3320,7 +3373,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         const uint32_t n = D >> r;
         if (persists(r)) {  // phase 2: the rest in one launch
             if ((rc = eq_setup_host(c, u, eq))) return rc;
-            LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD, &pc};
+            LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD, &pc, inv_ratio_m, {}};
             if (m_src32) return fail(c, ZKH_EDEV, "internal: unfolded int32 m at the persistent loop");
             const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
             if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, beta_l, ev_out, ws_out, fin)))
@@ -3354,6 +3407,15 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
                     t = fr_mul(t, u[j]);
                 }
         }
+        // the round's multipliers prepared while the kernel runs (one product per use below)
+        const Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
+        const Fr corr_mm = to_mm(corr), e0_m = to_m(e0), e1_m = to_m(e1), alpha_m = to_m(alpha);
+        const Fr iu_m = inv_u.empty() ? kZero : to_m(inv_u[k - 1]);
+        // a weighted-product sum as the round polynomial takes it: x 2^256 corr, or (cf: the
+        // sum carries 2^256 already) x 2^-256 corr
+        auto wq = [&](const Fr& x, bool cf) { return mulm(x, cf ? corr : corr_mm); };
+        // q(1) of an eq-weighted piece with claim I: (I - (1 - ul) q(0)) / ul
+        auto q1_of = [&](const Fr& I, const Fr& q0) { return mulm(fr_sub(I, mulm(q0, e0_m)), iu_m); };
         if ((rc = wait_pub(c, cur.pb.seq))) return rc;
         if (tracing) tr_t.push_back(now_us());
         // the pieces' values at 0 and 1 and their t^2 coefficients (true sums)
@@ -3362,22 +3424,22 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             Fr s[5];
             if (cur.dv_a) {  // w a0 s0, w da ds, a0
                 pub_read(c, 0, 3, s);
-                qa[0] = fr_mul(fix1(s[0]), corr);
-                qa[2] = fr_mul(fix1(s[1]), corr);
-                qa[1] = eq_piece_q1(pc.Ia, qa[0], ul, inv_u[k - 1]);
+                qa[0] = wq(s[0], false);
+                qa[2] = wq(s[1], false);
+                qa[1] = q1_of(pc.Ia, qa[0]);
                 sa[0] = s[2];
                 sa[1] = fr_sub(pc.Sa, s[2]);
             } else if (cur.nz) {  // w da ds, a0, a1; sum eq a (s + beta) = sum eq = 1 (no zero in A)
                 pub_read(c, 0, 3, s);
                 qa[0] = qa[1] = kOne;
-                qa[2] = fr_mul(fix1(s[0]), corr);
+                qa[2] = wq(s[0], false);
                 sa[0] = s[1];
                 sa[1] = s[2];
             } else {
                 pub_read(c, 0, 5, s);
-                qa[0] = fr_mul(q_of(s[0], cur.cf_a), corr);
-                qa[1] = fr_mul(q_of(s[1], cur.cf_a), corr);
-                qa[2] = fr_mul(fix1(s[2]), corr);
+                qa[0] = wq(s[0], cur.cf_a);
+                qa[1] = wq(s[1], cur.cf_a);
+                qa[2] = wq(s[2], false);
                 sa[0] = s[3];
                 sa[1] = s[4];
             }
@@ -3386,48 +3448,47 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             Fr s[6];
             if (cur.dv_b) {  // w b0 t0, w db dt, m0 b0, dm db
                 pub_read(c, 1, 4, s);
-                qb[0] = fr_mul(fix1(s[0]), corr);
-                qb[2] = fr_mul(fix1(s[1]), corr);
-                qb[1] = eq_piece_q1(pc.Ib, qb[0], ul, inv_u[k - 1]);
+                qb[0] = wq(s[0], false);
+                qb[2] = wq(s[1], false);
+                qb[1] = q1_of(pc.Ib, qb[0]);
                 M[0] = fix1(s[2]);
                 M[2] = fix1(s[3]);
                 M[1] = fr_sub(pc.Mb, M[0]);
             } else if (cur.nz) {  // w db dt, m0 b0, m1 b1, dm db (exact); sum eq b (t + beta) = 1
                 pub_read(c, 1, 4, s);
                 qb[0] = qb[1] = kOne;
-                qb[2] = fr_mul(fix1(s[0]), corr);
+                qb[2] = wq(s[0], false);
                 for (int t = 0; t < 3; t++) M[t] = s[1 + t];
             } else {
                 pub_read(c, 1, 6, s);
-                qb[0] = fr_mul(q_of(s[0], cur.cf_b), corr);
-                qb[1] = fr_mul(q_of(s[1], cur.cf_b), corr);
-                qb[2] = fr_mul(fix1(s[2]), corr);
+                qb[0] = wq(s[0], cur.cf_b);
+                qb[1] = wq(s[1], cur.cf_b);
+                qb[2] = wq(s[2], false);
                 for (int t = 0; t < 3; t++) M[t] = cur.cf_b ? s[3 + t] : fix1(s[3 + t]);  // exact when cf_b
             }
         }
-        const Fr e0 = fr_sub(kOne, ul), e1 = fr_sub(fr_add(ul, ul), kOne);
         if (n > N) {  // phase 1
             const Fr qc1 = fr_sub(fr_sub(qa[1], qa[0]), qa[2]);
-            const Fr aq0 = fr_mul(alpha, qa[0]), aq1 = fr_mul(alpha, qc1), aq2 = fr_mul(alpha, qa[2]);
-            coef[0] = fr_add(fr_add(fr_mul(e0, aq0), sa[0]), fr_mul(Cc, inv2));
-            coef[1] = fr_add(fr_add(fr_mul(e0, aq1), fr_mul(e1, aq0)), fr_sub(sa[1], sa[0]));
-            coef[2] = fr_add(fr_mul(e0, aq2), fr_mul(e1, aq1));
-            coef[3] = fr_mul(e1, aq2);
+            const Fr aq0 = mulm(qa[0], alpha_m), aq1 = mulm(qc1, alpha_m), aq2 = mulm(qa[2], alpha_m);
+            coef[0] = fr_add(fr_add(mulm(aq0, e0_m), sa[0]), fr_half(Cc));
+            coef[1] = fr_add(fr_add(mulm(aq1, e0_m), mulm(aq0, e1_m)), fr_sub(sa[1], sa[0]));
+            coef[2] = fr_add(mulm(aq2, e0_m), mulm(aq1, e1_m));
+            coef[3] = mulm(aq2, e1_m);
         } else {  // phase 2
-            const Fr coefBT = fr_mul(inv_ratio, alpha_sq);
-            const Fr Q0 = fr_add(fr_mul(alpha, qa[0]), fr_mul(coefBT, qb[0]));
-            const Fr Q1 = fr_add(fr_mul(alpha, fr_sub(fr_sub(qa[1], qa[0]), qa[2])),
-                                 fr_mul(coefBT, fr_sub(fr_sub(qb[1], qb[0]), qb[2])));
-            const Fr Q2 = fr_add(fr_mul(alpha, qa[2]), fr_mul(coefBT, qb[2]));
+            const Fr coefBT_m = to_m(mulm(alpha_sq, inv_ratio_m));
+            const Fr Q0 = fr_add(mulm(qa[0], alpha_m), mulm(qb[0], coefBT_m));
+            const Fr Q1 = fr_add(mulm(fr_sub(fr_sub(qa[1], qa[0]), qa[2]), alpha_m),
+                                 mulm(fr_sub(fr_sub(qb[1], qb[0]), qb[2]), coefBT_m));
+            const Fr Q2 = fr_add(mulm(qa[2], alpha_m), mulm(qb[2], coefBT_m));
             const Fr Mc1 = fr_sub(fr_sub(M[1], M[0]), M[2]);
-            coef[0] = fr_sub(fr_add(fr_mul(e0, Q0), sa[0]), fr_mul(inv_ratio, M[0]));
-            coef[1] = fr_sub(fr_add(fr_add(fr_mul(e0, Q1), fr_mul(e1, Q0)), fr_sub(sa[1], sa[0])),
-                             fr_mul(inv_ratio, Mc1));
-            coef[2] = fr_sub(fr_add(fr_mul(e0, Q2), fr_mul(e1, Q1)), fr_mul(inv_ratio, M[2]));
-            coef[3] = fr_mul(e1, Q2);
+            coef[0] = fr_sub(fr_add(mulm(Q0, e0_m), sa[0]), mulm(M[0], inv_ratio_m));
+            coef[1] = fr_sub(fr_add(fr_add(mulm(Q1, e0_m), mulm(Q0, e1_m)), fr_sub(sa[1], sa[0])),
+                             mulm(Mc1, inv_ratio_m));
+            coef[2] = fr_sub(fr_add(mulm(Q2, e0_m), mulm(Q1, e1_m)), mulm(M[2], inv_ratio_m));
+            coef[3] = mulm(Q2, e1_m);
         }
-        Fr e[4] = {coef[0], fr_poly_eval(coef, 3, kOne), fr_poly_eval(coef, 3, fr_u64(2)),
-                   fr_poly_eval(coef, 3, three)};
+        Fr e[4];
+        cubic_at123(coef, e);
         if (!fr_eq(claim, fr_add(e[0], e[1])))
             return fail(c, ZKH_EROUND, "phase%d round inconsistency (witness bug) at round %u",
                         n > N ? 1 : 2, r);
@@ -3438,24 +3499,26 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         }
         Fr v = tr_challenge(tr);
         if (ws_out) fr_store(v, ws_out + 8 * r);
-        claim = fr_poly_eval(coef, 3, v);
-        Fr eqv = fr_eq2(ul, v);
-        alpha = fr_mul(alpha, eqv);
-        if (n > N) Cc = fr_mul(Cc, inv2);
-        else alpha_sq = fr_mul(alpha_sq, eqv);
-        pc.Ia = quad_at(qa[0], qa[1], qa[2], v);
-        pc.Sa = fr_add(sa[0], fr_mul(v, fr_sub(sa[1], sa[0])));
-        if (n <= N) {
-            pc.Ib = quad_at(qb[0], qb[1], qb[2], v);
-            pc.Mb = quad_at(M[0], M[1], M[2], v);
-            pc.b = true;
-        }
-        fr_store(fr_to_mont(v), vm);
-        if (relay_next) {
+        const Fr v_m = to_m(v);
+        fr_store(v_m, vm);
+        if (relay_next) {  // the queued round starts now; the state updates overlap it
             relay_send(c, relay.pending, vm);
             relay.pending = 0;
-            cur = next;
         }
+        claim = cubic_at(coef, v_m);
+        const Fr uv = mulm(ul, v_m);
+        const Fr eqv_m = to_m(fr_add(fr_sub(fr_add(uv, uv), fr_add(ul, v)), kOne));  // eq(ul, v)
+        alpha = mulm(alpha, eqv_m);
+        if (n > N) Cc = fr_half(Cc);
+        else alpha_sq = mulm(alpha_sq, eqv_m);
+        pc.Ia = quad_at_m(qa[0], qa[1], qa[2], v_m);
+        pc.Sa = fr_add(sa[0], mulm(fr_sub(sa[1], sa[0]), v_m));
+        if (n <= N) {
+            pc.Ib = quad_at_m(qb[0], qb[1], qb[2], v_m);
+            pc.Mb = quad_at_m(M[0], M[1], M[2], v_m);
+            pc.b = true;
+        }
+        if (relay_next) cur = next;
         launched = relay_next;
         if (tracing) tr_t.push_back(now_us());
     }
@@ -3853,18 +3916,15 @@ extern "C" int zkh_ipa_prove(zkh_ctx* c, uint8_t* transcript, const zkh_tensor* 
 // ---------------------------------------------------------------------------------------
 // Hadamard sumcheck (zkob_lookup.cuh:267-315)
 // ---------------------------------------------------------------------------------------
-static Fr lagrange4(const Fr e[4], const Fr& v) {
-    // coefficients through (0..3, e) by Newton differences, then Horner
-    static const Fr inv2 = fr_inv2(), inv6 = fr_inv(fr_u64(6));
-    Fr d1 = fr_sub(e[1], e[0]), d2 = fr_sub(e[2], e[1]), d3 = fr_sub(e[3], e[2]);
-    Fr dd1 = fr_sub(d2, d1), dd2 = fr_sub(d3, d2);
-    Fr ddd = fr_sub(dd2, dd1);
-    // p(v) = e0 + v d1 + v(v-1)/2 dd1 + v(v-1)(v-2)/6 ddd
-    Fr vm1 = fr_sub(v, kOne), vm2 = fr_sub(v, fr_u64(2));
-    Fr t1 = fr_mul(v, d1);
-    Fr t2 = fr_mul(fr_mul(fr_mul(v, vm1), inv2), dd1);
-    Fr t3 = fr_mul(fr_mul(fr_mul(fr_mul(v, vm1), vm2), inv6), ddd);
-    return fr_add(fr_add(fr_add(e[0], t1), t2), t3);
+// p(v) of the cubic through (t, e[t]), t = 0..3, for vm = to_m(v): Newton differences,
+// p(v) = e0 + v (d1 + (v - 1) (dd1 / 2 + (v - 2) ddd / 6))
+static Fr lagrange4_m(const Fr e[4], const Fr& vm) {
+    static const Fr inv6_m = to_m(fr_inv(fr_u64(6))), one_m = fr_one_m(), two_m = to_m(fr_u64(2));
+    const Fr d1 = fr_sub(e[1], e[0]), d2 = fr_sub(e[2], e[1]), d3 = fr_sub(e[3], e[2]);
+    const Fr dd1 = fr_sub(d2, d1), ddd = fr_sub(fr_sub(d3, d2), dd1);
+    Fr t = fr_add(fr_half(dd1), mulm(mulm(ddd, inv6_m), fr_sub(vm, two_m)));
+    t = fr_add(d1, mulm(t, fr_sub(vm, one_m)));
+    return fr_add(e[0], mulm(t, vm));
 }
 // Rounds r0 .. k-1 of a Hadamard sumcheck in one persistent launch (see HpPersist) once the
 // tables have sz <= ZKH_HP_PERSIST_MAX entries: one host round trip per round instead of a
@@ -3958,15 +4018,24 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
             }
         }
     };
-    auto host_round = [&](uint32_t r, const Fr sums[4], bool device, Fr& w) -> bool {
+    // one round from its sums at t = 0..3; w_m receives to_m(w)
+    auto host_round = [&](uint32_t r, const Fr sums[4], bool device, Fr& w, Fr& w_m) -> bool {
         const uint32_t K = k - r - 1;
         const Fr ul = em ? kZero : (*u)[k - r - 1];
         Fr e[4];
         if (em) {
             for (int t = 0; t < 4; t++) e[t] = device ? fix2(sums[t]) : sums[t];
         } else {
-            const Fr f = device ? fr_mul(cE, eq_corr(eq, K)) : cE;
-            for (int t = 0; t < 4; t++) e[t] = fr_mul(fr_mul(device ? fix1(sums[t]) : sums[t], f), fr_eq2(ul, fr_u64(t)));
+            // e[t] = sums_t (x 2^256 from the device) f eq(ul, t), f = cE corr(K), eq(ul, t) =
+            // (1 - ul) + t (2 ul - 1): the factors f (1 - ul) and f (2 ul - 1) prepared once
+            // f 2^512 for device sums (they carry 2^-256), else f 2^256
+            const Fr f_m = device ? mulm(to_mm(cE), to_m(eq_corr(eq, K))) : to_m(cE);
+            const Fr f0 = mulm(f_m, to_m(fr_sub(kOne, ul))), fd = mulm(f_m, to_m(fr_sub(fr_add(ul, ul), kOne)));
+            Fr ft = f0;
+            for (int t = 0; t < 4; t++) {
+                e[t] = mulm(sums[t], ft);
+                ft = fr_add(ft, fd);
+            }
         }
         if (!fr_eq(claim, fr_add(e[0], e[1]))) return false;
         for (int t = 0; t < 4; t++) {
@@ -3975,8 +4044,12 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
         }
         w = tr_challenge(tr);
         if (ws_out) fr_store(w, ws_out + 8 * r);
-        claim = lagrange4(e, w);
-        if (!em) cE = fr_mul(cE, fr_eq2(ul, w));
+        w_m = to_m(w);
+        claim = lagrange4_m(e, w_m);
+        if (!em) {
+            const Fr uw = mulm(ul, w_m);
+            cE = mulm(cE, to_m(fr_add(fr_sub(fr_add(uw, uw), fr_add(ul, w)), kOne)));  // cE eq(ul, w)
+        }
         return true;
     };
     const bool tracing = trace_on();
@@ -3990,13 +4063,13 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
             Fr sums[4] = {kZero, kZero, kZero, kZero};
             for (uint32_t b = 0; b < nb; b++)
                 for (int t = 0; t < 4; t++) sums[t] = fr_add(sums[t], slot_fr(b, t));
-            Fr w;
-            if (!host_round(r1, sums, true, w)) {
+            Fr w, w_m;
+            if (!host_round(r1, sums, true, w, w_m)) {
                 quit();
                 return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r1);
             }
             uint32_t xm[8];
-            fr_store(fr_to_mont(w), xm);
+            fr_store(w_m, xm);
             send(seq, xm, 8);
             if (tracing) tr_h.push_back(now_us());
             lr++;
@@ -4012,34 +4085,39 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
         for (int p = 0; p < 9; p++) G[p] = kZero;
         for (uint32_t b = 0; b < nb; b++)
             for (int p = 0; p < 9; p++) G[p] = fr_add(G[p], slot_fr(b, p));
-        Fr rho = kOne;
+        Fr rho_m = fr_one_m();
         if (!em) {
             const uint32_t K2 = k - r1 - 2;  // eq coordinate of y2
-            rho = fr_mul((*u)[K2], eq.inv1mu[K2]);
+            rho_m = mulm(to_m((*u)[K2]), to_m(eq.inv1mu[K2]));
         }
         // E mode: the device sums carry one 2^-256 (E S, U = 1), so they go in as exact values
         auto val = [&](const Fr& x) { return em ? fix1(x) : x; };
-        Fr sums[4], w1, w2;
-        for (int t = 0; t < 4; t++) {
-            const Fr ft = fr_u64(t);
-            sums[t] = val(fr_add(quad_at(G[0], G[3], G[6], ft), fr_mul(rho, quad_at(G[1], G[4], G[7], ft))));
-        }
-        if (!host_round(r1, sums, !em, w1)) {
+        // a quadratic piece (q(0), q(1), t^2 coefficient) at t = 0..3, by additions
+        auto at0123 = [](const Fr& q0, const Fr& q1, const Fr& c2, Fr out[4]) {
+            const Fr cq[4] = {q0, fr_sub(fr_sub(q1, q0), c2), c2, kZero};
+            cubic_at123(cq, out);
+        };
+        Fr sums[4], w1, w2, w1_m, w2_m, X[4], Y[4];
+        at0123(G[0], G[3], G[6], X);
+        at0123(G[1], G[4], G[7], Y);
+        for (int t = 0; t < 4; t++) sums[t] = val(fr_add(X[t], mulm(Y[t], rho_m)));
+        if (!host_round(r1, sums, !em, w1, w1_m)) {
             quit();
             return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r1);
         }
         Fr H[3];
-        for (int b = 0; b < 3; b++) H[b] = quad_at(G[b], G[3 + b], G[6 + b], w1);
-        for (int t = 0; t < 4; t++) sums[t] = val(quad_at(H[0], H[1], H[2], fr_u64(t)));
-        if (!host_round(r1 + 1, sums, !em, w2)) {
+        for (int b = 0; b < 3; b++) H[b] = quad_at_m(G[b], G[3 + b], G[6 + b], w1_m);
+        at0123(H[0], H[1], H[2], X);
+        for (int t = 0; t < 4; t++) sums[t] = val(X[t]);
+        if (!host_round(r1 + 1, sums, !em, w2, w2_m)) {
             quit();
             return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r1 + 1);
         }
-        // double fold weights of T[c + (2 y1 + y2) q]
-        const Fr a1 = fr_sub(kOne, w1), a2 = fr_sub(kOne, w2);
-        const Fr L[4] = {fr_mul(a1, a2), fr_mul(a1, w2), fr_mul(w1, a2), fr_mul(w1, w2)};
+        // double fold weights of T[c + (2 y1 + y2) q], in Montgomery form: (1 - w)_m = 1_m - w_m
+        const Fr a1_m = fr_sub(fr_one_m(), w1_m), a2_m = fr_sub(fr_one_m(), w2_m);
+        const Fr Lw_m[4] = {mulm(a1_m, a2_m), mulm(a1_m, w2_m), mulm(w1_m, a2_m), mulm(w1_m, w2_m)};
         uint32_t xm[32];
-        for (int j = 0; j < 4; j++) fr_store(fr_to_mont(L[j]), xm + 8 * j);
+        for (int j = 0; j < 4; j++) fr_store(Lw_m[j], xm + 8 * j);
         send(seq, xm, 32);
         if (tracing) tr_h.push_back(now_us());
         lr += 2;
@@ -4059,29 +4137,25 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
         std::vector<Fr> wl;
         if (!em) eq_low_weights(*u, K, h, wl);
         for (uint32_t i = 0; i < h; i++) {
-            Fr w = kOne, de = kZero;
-            if (em) {
-                w = te[i];
-                de = fr_sub(te[i + h], te[i]);
-            } else {
-                w = wl[i];
-            }
-            const Fr ds = fr_sub(ta[i + h], ta[i]), du = fr_sub(tb[i + h], tb[i]);
-            Fr st = ta[i], ut = tb[i];
+            // w_t S_t U_t with w_t and U_t in Montgomery form (both linear in t: to_m is linear)
+            Fr w_m = em ? to_m(te[i]) : to_m(wl[i]), ut_m = to_m(tb[i]);
+            const Fr dw_m = em ? to_m(fr_sub(te[i + h], te[i])) : kZero, du_m = to_m(fr_sub(tb[i + h], tb[i]));
+            const Fr ds = fr_sub(ta[i + h], ta[i]);
+            Fr st = ta[i];
             for (int t = 0; t < 4; t++) {
-                sums[t] = fr_add(sums[t], fr_mul(w, fr_mul(st, ut)));
+                sums[t] = fr_add(sums[t], mulm(mulm(st, w_m), ut_m));
                 st = fr_add(st, ds);
-                ut = fr_add(ut, du);
-                w = fr_add(w, de);
+                ut_m = fr_add(ut_m, du_m);
+                w_m = fr_add(w_m, dw_m);
             }
         }
-        Fr w;
-        if (!host_round(r, sums, false, w))
+        Fr w, w_m;
+        if (!host_round(r, sums, false, w, w_m))
             return fail(c, ZKH_EROUND, "hadamard round inconsistency (witness bug) at round %u", r);
         for (uint32_t i = 0; i < h; i++) {
-            ta[i] = fr_add(ta[i], fr_mul(w, fr_sub(ta[i + h], ta[i])));
-            tb[i] = fr_add(tb[i], fr_mul(w, fr_sub(tb[i + h], tb[i])));
-            if (em) te[i] = fr_add(te[i], fr_mul(w, fr_sub(te[i + h], te[i])));
+            ta[i] = fr_add(ta[i], mulm(fr_sub(ta[i + h], ta[i]), w_m));
+            tb[i] = fr_add(tb[i], mulm(fr_sub(tb[i + h], tb[i]), w_m));
+            if (em) te[i] = fr_add(te[i], mulm(fr_sub(te[i + h], te[i]), w_m));
         }
     }
     s_fin = ta[0];
@@ -4273,8 +4347,8 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
                 c2 = unfix(sums[2]);
                 q1 = unfix(sums[1]);
             }
-            const Fr c1 = fr_sub(fr_sub(q1, c0), c2);
-            for (int t = 0; t < 4; t++) e[t] = fr_add(c0, fr_mul(fr_u64(t), fr_add(c1, fr_mul(fr_u64(t), c2))));
+            const Fr cq[4] = {c0, fr_sub(fr_sub(q1, c0), c2), c2, kZero};
+            cubic_at123(cq, e);
         } else if (!ueq) {
             if (cur.dv) {
                 pub_read(c, 0, 3, sums);
@@ -4290,22 +4364,31 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
             const uint32_t K = k - r - 1;
             const Fr ul = (*ueq)[k - r - 1];
             const Fr corr = eq_corr(eq, K);
-            auto unfix = [&](const Fr& x) { return fr_mul(fold ? fix1(x) : fr_from_mont(x), corr); };
+            const Fr cm = fold ? to_mm(corr) : corr;  // fix1 (or from_mont) and corr in one product
+            auto unfix = [&](const Fr& x) { return mulm(x, cm); };
+            const Fr e0_m = to_m(fr_sub(kOne, ul)), e1_m = to_m(fr_sub(fr_add(ul, ul), kOne));
             if (cur.dv) {
                 pub_read(c, 0, 2, sums);
                 st_true[0] = unfix(sums[0]);
                 st_true[2] = unfix(sums[1]);
-                st_true[1] = eq_piece_q1(I, st_true[0], ul, inv_u[k - r - 1]);
+                // q(1) = (I - (1 - ul) q(0)) / ul
+                st_true[1] = mulm(fr_sub(I, mulm(st_true[0], e0_m)), to_m(inv_u[k - r - 1]));
             } else {
                 pub_read(c, 0, 3, sums);
                 st_true[0] = unfix(sums[0]);
                 st_true[1] = unfix(sums[1]);
                 st_true[2] = unfix(sums[2]);
             }
-            const Fr c0 = st_true[0], c2 = st_true[2], c1 = fr_sub(fr_sub(st_true[1], c0), c2);
+            const Fr cq[4] = {st_true[0], fr_sub(fr_sub(st_true[1], st_true[0]), st_true[2]), st_true[2], kZero};
+            Fr st[4];
+            cubic_at123(cq, st);
+            // e[t] = st_t cE eq(ul, t), eq(ul, t) = (1 - ul) + t (2 ul - 1): the factors cE (1 - ul)
+            // and cE (2 ul - 1) in Montgomery form, then one product per t
+            const Fr cE_m = to_m(cE), f0 = mulm(cE_m, e0_m), fd = mulm(cE_m, e1_m);
+            Fr ft = f0;
             for (int t = 0; t < 4; t++) {
-                const Fr st = fr_add(c0, fr_mul(fr_u64(t), fr_add(c1, fr_mul(fr_u64(t), c2))));
-                e[t] = fr_mul(fr_mul(st, cE), fr_eq2(ul, fr_u64(t)));
+                e[t] = mulm(st[t], ft);
+                ft = fr_add(ft, fd);
             }
         }
         if (r == 0 && derive_claim) {
@@ -4321,16 +4404,18 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         }
         Fr w = tr_challenge(tr);
         if (ws_out) fr_store(w, ws_out + 8 * r);
-        claim = lagrange4(e, w);
-        if (ueq) {
-            cE = fr_mul(cE, fr_eq2((*ueq)[k - r - 1], w));
-            I = quad_at(st_true[0], st_true[1], st_true[2], w);
-        }
-        fr_store(fr_to_mont(w), vm);
-        if (relay_next) {
+        const Fr w_m = to_m(w);
+        fr_store(w_m, vm);
+        if (relay_next) {  // the queued round starts now; the state updates overlap it
             relay_send(c, relay.pending, vm);
             relay.pending = 0;
             cur = next;
+        }
+        claim = lagrange4_m(e, w_m);
+        if (ueq) {
+            const Fr ul = (*ueq)[k - r - 1], uw = mulm(ul, w_m);
+            cE = mulm(cE, to_m(fr_add(fr_sub(fr_add(uw, uw), fr_add(ul, w)), kOne)));  // cE eq(ul, w)
+            I = quad_at_m(st_true[0], st_true[1], st_true[2], w_m);
         }
         launched = relay_next;
         if (tracing) tr_t.push_back(now_us());
