@@ -885,6 +885,54 @@ def test_hp_prove(zkh, ctx, k):
         assert bytes(st_g) == bytes(st_o)
 
 
+def test_persistent_loops_queued_on_fresh_context(zkh):
+    """The persistent loops are queued behind a relay while the round before them runs; on a
+    fresh context their first use allocates the pinned slot memory, which waits for the
+    stream, so the relay has to go in after that allocation.  A logUp proof whose loop starts
+    after two round kernels (D = 32 > N = 8) and a Hadamard proof whose loop starts after one
+    (2^14 entries), each on a new context, equal the oracle's."""
+    rng = np.random.default_rng(77)
+    D, N, low, ln = 32, 8, -3, 5
+    vals = rng.integers(low, low + ln, size=D).astype(np.int32)
+    S = C.ints_to_fr(vals)
+    T = C.range_table(low, ln, N)
+    rc, m = C.lu_prep(S, low, N)
+    assert rc == 0
+    beta, alpha = rand_fr_full(rng, 2)
+    u = rand_fr_full(rng, P.ceil_log2(D))
+    st_g, st_o = seed_transcript(zkh, "fresh:lu")
+    rc, want = C.lu_prove(st_o, C.lu_inverse(S, beta), S, T, m, alpha, beta, u)
+    assert rc == 0
+    c1 = zkh.Context(0)
+    try:
+        Sg = c1.from_i32(vals)
+        got = c1.lu_prove(st_g, c1.lu_inverse(Sg, beta), Sg, c1.range_table(low, ln, N), c1.from_fr(m), alpha,
+                          beta, u)
+    finally:
+        c1.close()
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+    k = 14
+    n = 1 << k
+    uh = rand_fr_full(rng, k)
+    E = C.build_eq(uh)
+    Sv, U = C.ints_to_fr(rng.integers(-2**20, 2**20, size=n)), rand_fr_full(rng, n)
+    Ei, Si, Ui = C.fr_to_ints(E), C.fr_to_ints(Sv), C.fr_to_ints(U)
+    claim = C.ints_to_fr([sum(a * b % P.R * c for a, b, c in zip(Ei, Si, Ui)) % P.R])[0]
+    st_g, st_o = seed_transcript(zkh, "fresh:hp")
+    rc, want = C.hp_prove(st_o, claim, E, Sv, U)
+    assert rc == 0
+    c2 = zkh.Context(0)
+    try:
+        got = c2.hp_prove_eq(st_g, claim, uh, c2.from_fr(Sv), c2.from_fr(U))
+    finally:
+        c2.close()
+    for key in ("ev", "term", "ws"):
+        assert fr_eq(got[key], want[key]), key
+    assert bytes(st_g) == bytes(st_o)
+
+
 @pytest.mark.parametrize("k,zeros", [(16, ()), (16, (14, 13)), (17, (15,))])
 def test_hp_prove_derived_rounds(zkh, ctx, k, zeros):
     """Tables above the persistent loop's size (explicit E and eq form): the folding rounds leave

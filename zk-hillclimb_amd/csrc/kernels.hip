@@ -3248,12 +3248,13 @@ __global__ __launch_bounds__(NTP) void k_hp_persist(HpPersist P) {
     uint4* rlo = zl + 2 * ntab * ls;  // 8 rows of hs: lo planes, then hi planes
     uint4* rhi = rlo + 8 * hs;
     const EqDev eq{P.elo, P.ehi, 0};
+    if (P.vmp && P.vmp[8]) return;  // the host abandoned the proof before the relay
     {
         const uint4* glo_[3] = {reinterpret_cast<const uint4*>(P.s_lo), reinterpret_cast<const uint4*>(P.u_lo),
                                 reinterpret_cast<const uint4*>(P.e_lo)};
         const uint4* ghi_[3] = {reinterpret_cast<const uint4*>(P.s_hi), reinterpret_cast<const uint4*>(P.u_hi),
                                 reinterpret_cast<const uint4*>(P.e_hi)};
-        const fr_t vm = to_fr(P.vm.v);
+        const fr_t vm = P.vmp ? ld_aos(P.vmp, 0) : to_fr(P.vm.v);
         const uint32_t nload = ntab * ls + (em ? 0 : hs);
         for (uint32_t t = threadIdx.x; t < nload; t += NTP) {  // tables, then (eq mode) W
             if (t < ntab * ls) {
@@ -3434,8 +3435,9 @@ __global__ __launch_bounds__(NTP) void k_lu_persist(LuPersist P) {
     uint4* rhi = rlo + 5 * hs;
     const EqDev eq{P.elo, P.ehi, 0};
     const fr_t beta = to_fr(P.beta.v);
+    if (P.vmp && P.vmp[8]) return;  // the host abandoned the proof before the relay
     {
-        const fr_t vm = to_fr(P.vm.v);
+        const fr_t vm = P.vmp ? ld_aos(P.vmp, 0) : to_fr(P.vm.v);
         for (uint32_t t = threadIdx.x; t < 5 * ls + hs; t += NTP) {  // tables, then W
             if (t < 5 * ls) {
                 const uint32_t i = t / ls, k = t - i * ls;

@@ -434,6 +434,7 @@ struct HpPersist {
     uint32_t* err;
     unsigned long long deadline;
     fr_arg vm;        // the owed fold's challenge (Montgomery form) when fold != 0
+    const uint32_t* vmp;  // or, when given, device words from a relay (vmp[8] != 0: return at once)
     uint32_t n, lgnb, fold, two;  // fold: entries g and g + n of the sources fold into g
 };
 #define ZKH_HP_MSG 32
@@ -467,6 +468,7 @@ struct LuPersist {
     uint32_t* err;
     unsigned long long deadline;
     fr_arg vm;    // the owed folds' challenge (Montgomery form)
+    const uint32_t* vmp;  // or, when given, device words from a relay (vmp[8] != 0: return at once)
     fr_arg beta;  // plain
     uint32_t n, lgnb, fold_as, fold_btm;  // fold_*: that group's sources hold 2n entries
     uint32_t two, pad_[3];

@@ -2991,9 +2991,12 @@ static void eq_low_weights(const std::vector<Fr>& u, uint32_t K, uint32_t h, std
         }
     }
 }
+// mode: 0 launch and serve; 1 launch only, behind a relay queued here (held by *rg) that
+// hands the kernel the owed challenge; 2 serve the loop mode 1 launched.  (The relay goes in
+// after the slot memory is in place: its first allocation waits for the stream.)
 static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0, uint32_t n, const DevPlanes src[5],
-                             bool fold_as, bool fold_btm, const uint32_t vm[8], const uint32_t beta_l[8],
-                             uint32_t* ev_out, uint32_t* ws_out, Fr fin[5]) {
+                             bool fold_as, bool fold_btm, const uint32_t vm[8], RelayGuard* rg,
+                             const uint32_t beta_l[8], uint32_t* ev_out, uint32_t* ws_out, Fr fin[5], int mode) {
     const uint32_t lgnb = n > ZKH_LH_PLS ? ceil_log2(n / ZKH_LH_PLS) : 0, nb = 1u << lgnb;
     const uint32_t R = ceil_log2(n) - lgnb;  // local rounds
     int rc;
@@ -3001,7 +3004,7 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
     uint32_t* ps = c->ps_host;
     uint32_t* slots = ps + ZKH_LU_PSLOT;
     uint32_t* cmd = ps + (size_t)ZKH_LU_PSLOT * (nb + 1);
-    memset(ps, 0, (size_t)ZKH_LU_PSLOT * (nb + 2) * 4);
+    if (mode != 2) memset(ps, 0, (size_t)ZKH_LU_PSLOT * (nb + 2) * 4);
     LuPersist P{};
     for (int i = 0; i < 5; i++) {
         P.lo[i] = src[i].lo();
@@ -3013,7 +3016,11 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
     P.cmd = cmd;
     P.err = ps;
     P.deadline = c->clock_khz * 1000 * 20;  // 20 s without a command
-    memcpy(P.vm.v, vm, 32);
+    if (vm) memcpy(P.vm.v, vm, 32);
+    if (mode == 1) {
+        rg->pending = relay_enqueue(c);
+        P.vmp = c->relay_vm;
+    }
     memcpy(P.beta.v, beta_l, 32);
     P.n = n;
     P.lgnb = lgnb;
@@ -3028,13 +3035,14 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
         send(ZKH_QUIT, nullptr, 32);
         (void)hipStreamSynchronize(c->stream);
     };
-    {
+    if (mode != 2) {
         ProfScope ps_(c, "lu_persist", (double)n * 5 * 32 * 2);
         hipError_t e = launch_lu_persist(c->stream, P);
         if (e != hipSuccess) {
             quit();
             return fail(c, ZKH_EDEV, "persistent logUp launch: %s", hipGetErrorString(e));
         }
+        if (mode == 1) return 0;
     }
     const double t_launch = now_us();
     auto slot_fr = [&](uint32_t b, uint32_t i) {
@@ -3147,7 +3155,9 @@ static int lu_persist_rounds(zkh_ctx* c, uint8_t tr[32], LuState& L, uint32_t r0
         t[i].resize(nb);
         for (uint32_t b = 0; b < nb; b++) t[i][b] = slot_fr(b, i);
     }
-    HIPCHK(c, hipStreamSynchronize(c->stream));  // the blocks have exited
+    // (no wait for the blocks to exit: none touches the slots after its last message, and
+    // later work on the stream is ordered behind the kernel; tracing reads the clock stamps)
+    if (tracing) HIPCHK(c, hipStreamSynchronize(c->stream));
     const Fr beta = fr_load(beta_l);
     // the last lgnb rounds over the blocks' entries (entry b is global index b)
     for (uint32_t r = r0 + R, m = nb; m > 1; r++, m >>= 1) {
@@ -3274,6 +3284,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
     const bool tracing = trace_on();
     std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
     bool persisted = false;    // the last rounds ran in lu_persist_rounds
+    bool persist_queued = false;  // ... launched behind the previous round's relay
     Fr fin[5];
     const bool no_persist = getenv("ZKH_NO_PERSIST") != nullptr;
     auto persists = [&](uint32_t r) {  // phase 2 small enough for the persistent loop
@@ -3376,19 +3387,29 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
             LuState L{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD, &pc, inv_ratio_m, {}};
             if (m_src32) return fail(c, ZKH_EDEV, "internal: unfolded int32 m at the persistent loop");
             const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
-            if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, beta_l, ev_out, ws_out, fin)))
+            if ((rc = lu_persist_rounds(c, tr, L, r, n, src, as_pending, btm_pending, vm, nullptr, beta_l, ev_out,
+                                        ws_out, fin, persist_queued ? 2 : 0)))
                 return rc;
             persisted = true;
             break;
         }
         if (tracing) tr_t.push_back(now_us());
         if (!launched) cur = launch(r, nullptr);
-        // round r + 1 goes behind a relay now, so that its launch overlaps this round
+        // round r + 1 (or the persistent loop) goes behind a relay now, so that its launch
+        // overlaps this round
         const bool relay_next = r + 1 < logD && !persists(r + 1);
+        const bool persist_next = r + 1 < logD && persists(r + 1) && !m_src32;
         Launched next{};
         if (relay_next) {
             relay.pending = relay_enqueue(c);
             next = launch(r + 1, c->relay_vm);
+        } else if (persist_next) {
+            LuState L0{claim, alpha, alpha_sq, inv_ratio, &u, &eq, logD, &pc, inv_ratio_m, {}};
+            const DevPlanes src[5] = {a_src, s_src, b_src, t_src, m_src};
+            if ((rc = lu_persist_rounds(c, tr, L0, r + 1, D >> (r + 1), src, as_pending, btm_pending, nullptr, &relay,
+                                        beta_l, nullptr, nullptr, fin, 1)))
+                return rc;
+            persist_queued = true;
         }
         if ((rc = eq_setup_host(c, u, eq))) return rc;  // once, behind the first launches
         const uint32_t k = logD - r;  // remaining variables
@@ -3501,7 +3522,7 @@ static int lu_prove_impl(zkh_ctx* c, uint8_t tr[32], const zkh_tensor* A, const 
         if (ws_out) fr_store(v, ws_out + 8 * r);
         const Fr v_m = to_m(v);
         fr_store(v_m, vm);
-        if (relay_next) {  // the queued round starts now; the state updates overlap it
+        if (relay_next || persist_next) {  // the queued launch starts now; the state updates overlap it
             relay_send(c, relay.pending, vm);
             relay.pending = 0;
         }
@@ -3933,10 +3954,11 @@ static Fr lagrange4_m(const Fr e[4], const Fr& vm) {
 // e[t] = sums_t with an explicit E table (e_src given, u null); then the claim check, the
 // absorbs "hp0".."hp3" and the challenge.
 #define ZKH_HP_PERSIST_MAX 8192u
+// mode as in lu_persist_rounds (1: launch only, behind a relay queued here and held by *rg)
 static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* u, const EqState& eq, uint32_t k,
                              uint32_t r0, uint32_t sz, int fold, DevPlanes e_src, DevPlanes s_src, DevPlanes u_src,
-                             bool u_ones, const uint32_t vm[8], Fr& claim, Fr& cE, uint32_t* ev_out, uint32_t* ws_out,
-                             Fr& e_fin, Fr& s_fin, Fr& u_fin) {
+                             bool u_ones, const uint32_t vm[8], RelayGuard* rg, Fr& claim, Fr& cE,
+                             uint32_t* ev_out, uint32_t* ws_out, Fr& e_fin, Fr& s_fin, Fr& u_fin, int mode) {
     const bool em = u == nullptr;  // explicit E table
     static const char* lab[4] = {"hp0", "hp1", "hp2", "hp3"};
     const uint32_t lgnb = sz > ZKH_LH_PLS ? ceil_log2(sz / ZKH_LH_PLS) : 0, nb = 1u << lgnb;
@@ -3946,7 +3968,7 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
     uint32_t* ps = c->ps_host;
     uint32_t* slots = ps + ZKH_PSLOT;
     uint32_t* cmd = ps + (size_t)ZKH_PSLOT * (nb + 1);
-    memset(ps, 0, (size_t)ZKH_PSLOT * (nb + 2) * 4);
+    if (mode != 2) memset(ps, 0, (size_t)ZKH_PSLOT * (nb + 2) * 4);
     HpPersist P{};
     P.s_lo = s_src.lo();
     P.s_hi = s_src.hi();
@@ -3960,7 +3982,11 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
     P.cmd = cmd;
     P.err = ps;
     P.deadline = c->clock_khz * 1000 * 20;  // 20 s without a command
-    memcpy(P.vm.v, vm, 32);
+    if (vm) memcpy(P.vm.v, vm, 32);
+    if (mode == 1) {
+        rg->pending = relay_enqueue(c);
+        P.vmp = c->relay_vm;
+    }
     P.n = sz;
     P.lgnb = lgnb;
     P.fold = fold ? 1 : 0;
@@ -3975,13 +4001,14 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
         send(ZKH_QUIT, nullptr, 32);
         (void)hipStreamSynchronize(c->stream);
     };
-    {
+    if (mode != 2) {
         ProfScope ps_(c, "hp_persist", (double)sz * (em ? 3 : 2) * 32 * (fold ? 3 : 1));
         hipError_t e = launch_hp_persist(c->stream, P);
         if (e != hipSuccess) {
             quit();
             return fail(c, ZKH_EDEV, "persistent hadamard launch: %s", hipGetErrorString(e));
         }
+        if (mode == 1) return 0;
     }
     const double t_launch = now_us();
     auto slot_fr = [&](uint32_t b, uint32_t i) {
@@ -4129,7 +4156,9 @@ static int hp_persist_rounds(zkh_ctx* c, uint8_t tr[32], const std::vector<Fr>* 
         tb[b] = slot_fr(b, 1);
         if (em) te[b] = slot_fr(b, 2);
     }
-    HIPCHK(c, hipStreamSynchronize(c->stream));  // the blocks have exited
+    // (no wait for the blocks to exit: none touches the slots after its last message, and
+    // later work on the stream is ordered behind the kernel; tracing reads the clock stamps)
+    if (tracing) HIPCHK(c, hipStreamSynchronize(c->stream));
     // the last lgnb rounds over the blocks' entries (entry b is global index b)
     for (uint32_t r = r0 + R, m = nb; m > 1; r++, m >>= 1) {
         const uint32_t h = m >> 1, K = k - r - 1;
@@ -4240,6 +4269,7 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
     const bool tracing = trace_on();
     std::vector<double> tr_t;  // per round: launch, sums seen, challenge done (host clock)
     bool persisted = false;    // the last rounds ran in hp_persist_rounds
+    bool persist_queued = false;  // ... launched behind the previous round's relay
     Fr e_fin = kZero, s_fin = kZero, u_fin = kZero;
     const bool no_persist = getenv("ZKH_NO_PERSIST") != nullptr;
     auto persists = [&](uint32_t r) { return (n >> r) <= ZKH_HP_PERSIST_MAX && !no_persist; };
@@ -4302,20 +4332,28 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         if (persists(r)) {  // the rest in one launch
             if (s32 || u32) return fail(c, ZKH_EDEV, "internal: unfolded int32 table at the persistent loop");
             if (ueq && (rc = eq_setup_host(c, *ueq, eq))) return rc;
-            if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, u_ones, vm, claim, cE,
-                                        ev_out, ws_out, e_fin, s_fin, u_fin)))
+            if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r, sz, fold, e_src, s_src, u_src, u_ones, vm, nullptr, claim,
+                                        cE, ev_out, ws_out, e_fin, s_fin, u_fin, persist_queued ? 2 : 0)))
                 return rc;
             persisted = true;
             break;
         }
         if (tracing) tr_t.push_back(now_us());
         if (!launched) cur = launch(r, nullptr);
-        // round r + 1 goes behind a relay now, so that its launch overlaps this round
+        // round r + 1 (or the persistent loop) goes behind a relay now, so that its launch
+        // overlaps this round
         const bool relay_next = r + 1 < k && !persists(r + 1);
+        const bool persist_next = r + 1 < k && persists(r + 1) && !s32 && !u32;
         Launched next{};
         if (relay_next) {
             relay.pending = relay_enqueue(c);
             next = launch(r + 1, c->relay_vm);
+        } else if (persist_next) {
+            Fr claim0 = claim, cE0 = cE, ef, sf, uf;  // (launch only: not read)
+            if ((rc = hp_persist_rounds(c, tr, ueq, eq, k, r + 1, n >> (r + 1), 1, e_src, s_src, u_src, u_ones, nullptr,
+                                        &relay, claim0, cE0, nullptr, nullptr, ef, sf, uf, 1)))
+                return rc;
+            persist_queued = true;
         }
         if (ueq && (rc = eq_setup_host(c, *ueq, eq))) return rc;  // once, behind the first launches
         if (r == 0 && ueq && k > 1) {  // 1/u_j for the rounds that derive (batch inverse, host)
@@ -4406,10 +4444,10 @@ static int hp_common(zkh_ctx* c, uint8_t tr[32], const uint32_t claim_l[8], cons
         if (ws_out) fr_store(w, ws_out + 8 * r);
         const Fr w_m = to_m(w);
         fr_store(w_m, vm);
-        if (relay_next) {  // the queued round starts now; the state updates overlap it
+        if (relay_next || persist_next) {  // the queued launch starts now; the state updates overlap it
             relay_send(c, relay.pending, vm);
             relay.pending = 0;
-            cur = next;
+            if (relay_next) cur = next;
         }
         claim = lagrange4_m(e, w_m);
         if (ueq) {
