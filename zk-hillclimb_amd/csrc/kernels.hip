@@ -1200,7 +1200,7 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
 //   1/x_j = M(P_{j-1}, Y_j)   and   Y_{j-1} = M(x_j, Y_j)
 // (P_j = P_{j-1} x_j / 2^256), so the backward walk yields plain inverses directly.  The
 // same identities combine totals: for Q = M(a, b), 1/a = M(b, 1/Q).  Block b covers
-// INV_CHK*NT entries; thread t owns entries base + j*NT + t.  Pass 1 stores P_j in A, and
+// CHK*NT entries (CHK = inv_chunk(n)); thread t owns entries base + j*NT + t.  Pass 1 stores P_j in A, and
 // a product tree over the thread totals (others_tree) gives each thread the M-product of
 // all OTHER threads' totals; the block total goes to blockprod.  Between the
 // passes, k_inv_blocks turns the block totals into "all other blocks" products and
@@ -1208,7 +1208,10 @@ void launch_lu_range_gather(hipStream_t s, Src S, uint32_t n, const uint32_t* lo
 // each thread's entries backwards.  Zero entries (x + beta = 0) take 2^256, M's identity,
 // in the products and produce 0, the reference's Fermat convention; pass 1 sets *zflag to
 // the call's tag when it meets one (the inverse then has a zero entry).
-#define INV_CHK 16
+// entries per thread: 16 for tables that fill the device several times over (the chains'
+// products then run at the device's rate), 4 below 2^20 entries, where a 16-long chain of
+// dependent products on few blocks sets the pass's time
+static inline uint32_t inv_chunk(uint32_t n) { return n >= (1u << 20) ? 16u : 4u; }
 // The M-product of all OTHER leaves, for each of NL leaves (NL a power of 2, at most the
 // block size; thread t < NL gives leaf t): a product tree up, tr[k] = M(tr[2k], tr[2k + 1])
 // with the leaves at tr[NL + t] and the block total at tr[1], then the products outside
@@ -1236,16 +1239,17 @@ ZDEV fr_t others_tree(fr_t* tr, fr_t* out, const fr_t& v) {
     }
     return t < NL ? out[NL + t] : one_m();
 }
+template <uint32_t CHK>
 __global__ __launch_bounds__(NT) void k_inv_pass1(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
                                                   uint32_t* others, uint32_t* blockprod, uint32_t* zflag,
                                                   uint32_t tag) {
     __shared__ fr_t tr[2 * NT], out[2 * NT];
     const uint32_t t = threadIdx.x;
-    const uint32_t base = blockIdx.x * NT * INV_CHK;
+    const uint32_t base = blockIdx.x * NT * CHK;
     fr_t run = one_m();
     bool zero = false;
-    for (uint32_t j = 0; j < INV_CHK; j++) {
+    for (uint32_t j = 0; j < CHK; j++) {
         uint32_t idx = base + j * NT + t;
         if (idx < n) {
             const fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
@@ -1293,20 +1297,21 @@ void launch_inv_blocks(hipStream_t s, const uint32_t* blockprod, uint32_t nb, ui
 }
 // 1/blockprod[b] = M(others_blk[b], 1/G), 1/(thread total) = M(others[t], 1/blockprod[b]);
 // then each thread walks its entries backwards
+template <uint32_t CHK>
 __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4* shi, uint32_t n,
                                                   fr_t beta, uint4* alo, uint4* ahi,
                                                   const uint32_t* __restrict__ others,
                                                   const uint32_t* __restrict__ others_blk, fr_t inv_total,
                                                   const uint32_t* invp, uint32_t* aos) {
     const uint32_t t = threadIdx.x;
-    const uint32_t base = blockIdx.x * NT * INV_CHK;
+    const uint32_t base = blockIdx.x * NT * CHK;
     if (invp) {  // 1/G from a relay: invp[0..8), invp[8] != 0 when the host abandoned the call
         if (invp[8]) return;
         inv_total = ld_aos(invp, 0);
     }
     const fr_t binv = mont_mul(inv_total, ld_aos(others_blk, blockIdx.x));
     fr_t y = mont_mul(binv, ld_aos(others, blockIdx.x * NT + t));
-    for (int j = INV_CHK - 1; j >= 0; j--) {
+    for (int j = CHK - 1; j >= 0; j--) {
         uint32_t idx = base + (uint32_t)j * NT + t;
         if (idx >= n) continue;
         const fr_t x = fr_add(ld_fr(slo, shi, idx), beta);
@@ -1318,16 +1323,21 @@ __global__ __launch_bounds__(NT) void k_inv_pass2(const uint4* slo, const uint4*
         if (aos) st_aos(aos, idx, z ? fr_zero() : inv);
     }
 }
-uint32_t inv_blocks(uint32_t n) { return (n + NT * INV_CHK - 1) / (NT * INV_CHK); }
+uint32_t inv_blocks(uint32_t n) {
+    const uint32_t c = inv_chunk(n);
+    return (n + NT * c - 1) / (NT * c);
+}
 void launch_inv_pass1(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, uint32_t* others, uint32_t* blockprod, uint32_t* zflag, uint32_t tag) {
-    k_inv_pass1<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
+    auto k = inv_chunk(n) == 16 ? k_inv_pass1<16> : k_inv_pass1<4>;
+    k<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A),
                                              PL_HI(A), others, blockprod, zflag, tag);
 }
 void launch_inv_pass2(hipStream_t s, DevPlanes S, uint32_t n, const uint32_t* beta_host,
                       DevPlanes A, const uint32_t* others, const uint32_t* others_blk,
                       const uint32_t* inv_total_host, const uint32_t* invp, uint32_t* aos) {
-    k_inv_pass2<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A), PL_HI(A), others,
+    auto k = inv_chunk(n) == 16 ? k_inv_pass2<16> : k_inv_pass2<4>;
+    k<<<inv_blocks(n), NT, 0, s>>>(PL_LO(S), PL_HI(S), n, to_fr(beta_host), PL_LO(A), PL_HI(A), others,
                                              others_blk, inv_total_host ? to_fr(inv_total_host) : fr_t{}, invp,
                                              aos);
 }
