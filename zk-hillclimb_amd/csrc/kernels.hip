@@ -2171,6 +2171,56 @@ ZDEV bool small_int(const fr_t& x, int32_t& out) {
 // round's claim, q(0)(1 - u) + q(1) u)
 // the folding form holds 5 waves per SIMD (16 KiB of accumulators, <= 96 VGPRs), the first
 // round 4 (its 64-bit products take more registers)
+// Sums of w p over a thread's pairs for weights w < 2^256 (canonical) and 63-bit p, as an
+// 11-limb integer (up to 2^33 terms): two multiply-add rows of 8 limbs per term, no reduction
+// until wide_mod, once per thread.  Reduction is linear, so the residue of the sum equals the
+// sum of the per-term fr_mul_u64 residues.
+ZDEV void wide_mac(uint32_t (&a)[11], const fr_t& w, uint64_t p) {
+    // the two 288-bit rows w p0 and w p1 (as fr_mul_u32 forms them), then two 32-bit carry
+    // chains into the accumulator: its limbs stay 32-bit values across the pair loop
+    const uint32_t p0 = (uint32_t)p, p1 = (uint32_t)(p >> 32);
+    uint32_t r[9];
+    uint64_t c = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        c = (uint64_t)w.v[i] * p0 + (c >> 32);
+        r[i] = (uint32_t)c;
+    }
+    r[8] = (uint32_t)(c >> 32);
+    unsigned k = 0;
+#pragma unroll
+    for (int i = 0; i < 9; i++) a[i] = __builtin_addc(a[i], r[i], k, &k);
+    a[9] = __builtin_addc(a[9], 0u, k, &k);
+    a[10] += k;
+    c = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        c = (uint64_t)w.v[i] * p1 + (c >> 32);
+        r[i] = (uint32_t)c;
+    }
+    r[8] = (uint32_t)(c >> 32);
+    k = 0;
+#pragma unroll
+    for (int i = 0; i < 9; i++) a[i + 1] = __builtin_addc(a[i + 1], r[i], k, &k);
+    a[10] += k;
+}
+// a mod r: the low 256 bits by fr_reduce288 (below r 2^32), limbs 8..10 times 2^256, 2^288,
+// 2^320 mod r by fr_mul_u32
+ZDEV fr_t wide_mod(const uint32_t (&a)[11]) {
+    const fr_t c256 = one_m();
+    const fr_t c288 = {{0xcaaf6b13u, 0x355094eau, 0x69a568efu, 0xf6b10cb3u, 0x40cc3869u, 0xe2c926a6u, 0xed269aadu,
+                        0x736a6d3bu}};
+    const fr_t c320 = {{0x0121c884u, 0xc98da28eu, 0xc7363c67u, 0xe6f4f4a0u, 0xe92e7df1u, 0xb2d6ebc4u, 0x9d26242au,
+                        0x19ae5794u}};
+    uint32_t t[9];
+#pragma unroll
+    for (int i = 0; i < 8; i++) t[i] = a[i];
+    t[8] = 0;
+    fr_t x = fr_reduce288(t);
+    x = fr_add(x, fr_mul_u32(c256, a[8]));
+    x = fr_add(x, fr_mul_u32(c288, a[9]));
+    return fr_add(x, fr_mul_u32(c320, a[10]));
+}
 template <int derive>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, NT), amdgpu_waves_per_eu(derive ? 5 : 4))) void k_hp_eq_round(TabDev S, TabDev U, uint32_t n, int fold, fr_t vm,
                                                     const uint32_t* vmp, EqDev eq, Publish pub) {
@@ -2253,6 +2303,50 @@ __global__ __attribute__((amdgpu_flat_work_group_size(1, NT), amdgpu_waves_per_e
     if (ef) acc.elo_scale(eq, blockIdx.x * NT + threadIdx.x, K);
     reduce_publish_lds<K>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
 }
+// The first round over int32 S and U (no fold): sum w (p_k + 2^62) for the exact products
+// p_0 = s0 u0, p_1 = s1 u1, p_2 = (s1 - s0)(u1 - u0) (|p_k| < 2^62 when every entry lies in
+// (-2^30, 2^30)) and sum w as wide integers, so that one reduction per thread gives
+// sum w p_k: two rows of 8 multiply-adds per term instead of a field x int64 multiply and a
+// field add.  A pair outside that range takes the field x int64 multiplies into the LDS
+// accumulators.  Same sums as k_hp_eq_round<0>.
+__global__ __launch_bounds__(NT, 4) void k_hp_eq_first_i32(TabDev S, TabDev U, uint32_t n, EqDev eq, Publish pub) {
+    const uint32_t h = n >> 1;
+    __shared__ uint4 accl[3 * NT], acch[3 * NT];
+    LdsAcc<3> acc{accl, acch};
+    acc.zero();
+    const bool ef = elo_factored(h, gridDim.x * NT);
+    uint32_t wp[3][11] = {}, wsum[9] = {};
+    auto in30 = [](int32_t v) { return v > -(1 << 30) && v < (1 << 30); };
+    for (uint32_t i = blockIdx.x * NT + threadIdx.x; i < h; i += gridDim.x * NT) {
+        const int32_t a0 = S.s32[i], a1 = S.s32[i + h], b0 = U.s32[i], b1 = U.s32[i + h];
+        const fr_t w = pair_w(eq, i, ef);
+        if (in30(a0) && in30(a1) && in30(b0) && in30(b1)) {
+            constexpr int64_t off = (int64_t)1 << 62;
+            wide_mac(wp[0], w, (uint64_t)((int64_t)a0 * b0 + off));
+            SB();
+            wide_mac(wp[1], w, (uint64_t)((int64_t)a1 * b1 + off));
+            SB();
+            wide_mac(wp[2], w, (uint64_t)((int64_t)(a1 - a0) * (b1 - b0) + off));
+            SB();
+            unsigned k = 0;
+#pragma unroll
+            for (int t = 0; t < 8; t++) wsum[t] = __builtin_addc(wsum[t], w.v[t], k, &k);
+            wsum[8] += k;
+        } else {  // int32 products exact in int64; the differences' product by two multiplies
+            acc.add(0, fr_mul_i64(w, (int64_t)a0 * b0));
+            acc.add(1, fr_mul_i64(w, (int64_t)a1 * b1));
+            acc.add(2, fr_mul_i64(fr_mul_i64(w, (int64_t)a1 - a0), (int64_t)b1 - b0));
+        }
+        SB();
+    }
+    // sum w p_k = sum w (p_k + 2^62) - 2^62 sum w
+    uint32_t ws11[11] = {wsum[0], wsum[1], wsum[2], wsum[3], wsum[4], wsum[5], wsum[6], wsum[7], wsum[8], 0u, 0u};
+    const fr_t off = fr_mul_u64(wide_mod(ws11), (uint64_t)1 << 62);
+#pragma unroll
+    for (int k = 0; k < 3; k++) acc.add(k, fr_sub(wide_mod(wp[k]), off));
+    if (ef) acc.elo_scale(eq, blockIdx.x * NT + threadIdx.x, 3);
+    reduce_publish_lds<3>(acc, pub, 0, 0, gridDim.x, blockIdx.x);
+}
 uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
                             const uint32_t* v_m_host, const uint32_t* vmp, EqW eq, Publish partial, int derive,
                             const int32_t* s32, const int32_t* u32) {
@@ -2269,6 +2363,7 @@ uint32_t launch_hp_eq_round(hipStream_t s, Tab S, Tab U, uint32_t n, int fold,
         return gw;
     }
     if (fold && derive) k_hp_eq_round<1><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
+    else if (!fold && s32 && u32 && !vmp) k_hp_eq_first_i32<<<g, NT, 0, s>>>(sd, ud, n, e, partial);
     else k_hp_eq_round<0><<<g, NT, 0, s>>>(sd, ud, n, fold, vm, vmp, e, partial);
     launch_publish(s, partial);
     return g;
