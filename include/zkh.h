@@ -134,7 +134,9 @@ int zkh_pad(zkh_ctx* ctx, const zkh_tensor* t, const uint32_t* shape, uint32_t n
 /* k_fr_fold (zkob_lookup.cuh:35-41): in-place MSB fold t[i] += v*(t[i+h]-t[i]), n -> n/2 */
 int zkh_fold(zkh_ctx* ctx, zkh_tensor* t, const uint32_t v[8]);
 /* elementwise: out = a + c*b (FrTensor operator+ / operator* by scalar, e.g. the SwiGLU
- * combiner comb = G + r*S, zkob_glu.cu:155-156) and out = a (.) b (Hadamard product) */
+ * combiner comb = G + r*S, zkob_glu.cu:155-156) and out = a (.) b (Hadamard product).
+ * Both return once the work is queued on the context's stream (later calls are ordered
+ * behind it; a device error surfaces at the next call that waits for the device). */
 int zkh_axpy(zkh_ctx* ctx, const zkh_tensor* a, const uint32_t c[8], const zkh_tensor* b,
              zkh_tensor** out);
 int zkh_hadamard(zkh_ctx* ctx, const zkh_tensor* a, const zkh_tensor* b, zkh_tensor** out);

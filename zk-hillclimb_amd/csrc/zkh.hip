@@ -1547,9 +1547,11 @@ extern "C" int zkh_axpy(zkh_ctx* c, const zkh_tensor* a, const uint32_t cc[8], c
     uint32_t cm[8];
     fr_store(fr_to_mont(fr_load(cc)), cm);
     if (a->n) launch_axpy(c->stream, sa, cc, cm, sb, a->n, o->planes());
-    if ((rc = settle(c))) {
+    // queued only: later work on the context's stream is ordered behind it (a device error
+    // surfaces at the next call that waits)
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) {
         zkh_tensor_free(o);
-        return rc;
+        return fail(c, ZKH_EDEV, "axpy launch: %s", hipGetErrorString(e));
     }
     *out = o;
     return ZKH_OK;
@@ -1571,9 +1573,9 @@ extern "C" int zkh_hadamard(zkh_ctx* c, const zkh_tensor* a, const zkh_tensor* b
         if ((rc = tensor_alloc(c, ZKH_KIND_FR, a->n, &o))) return rc;
         if (a->n) launch_hadamard(c->stream, sa, sb, a->n, o->planes());
     }
-    if ((rc = settle(c))) {
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) {  // queued only, as zkh_axpy
         zkh_tensor_free(o);
-        return rc;
+        return fail(c, ZKH_EDEV, "hadamard launch: %s", hipGetErrorString(e));
     }
     *out = o;
     return ZKH_OK;
