@@ -233,6 +233,50 @@ __device__ __forceinline__ g1_t g1_mul_quad(g1_t a, const uint32_t s[8], int q) 
     return acc;
 }
 
+// G1Jacobian_mul as g1_mul_quad, split over the two waves of a 128-thread block: wave 0 runs
+// the doubling chain a, 2a, 4a, ... and hands each 2^i a to wave 1 through LDS, G1P_B
+// doublings per block barrier; wave 1 adds the ones whose bit is set into acc one barrier
+// later.  The additions and doublings are those of g1_mul_quad in the same order (the same
+// Jacobian representative); the two chains run side by side instead of one after the
+// other.  Both waves call it with the same scalar for lane slot threadIdx.x & 63 and the
+// same `active` (wave 1 does not read `a`); the product is in wave 1's lanes.  Every thread
+// of the block takes the same 256 / G1P_B + 1 barriers.
+#define G1P_B 8
+typedef uint32_t g1_pipe_buf[2][G1P_B][16][36];
+__device__ __forceinline__ g1_t g1_mul_quad_pipe(g1_t a, const uint32_t s[8], int q, bool active,
+                                                 g1_pipe_buf& buf) {
+    static_assert(32 % G1P_B == 0, "a chunk's bits lie in one scalar limb");
+    const bool dbl_wave = threadIdx.x < 64;
+    const uint32_t slot = (threadIdx.x & 63) >> 2;
+    int top = -1;
+    if (active)
+        for (int l = 7; l >= 0 && top < 0; l--)
+            if (s[l]) top = 32 * l + 31 - __builtin_clz(s[l]);
+    g1_t acc = g1_zero();
+    constexpr int NC = 256 / G1P_B;
+    for (int k = 0; k <= NC; k++) {
+        if (dbl_wave) {
+            if (k < NC) {
+                for (int j = 0; j < G1P_B; j++) {
+                    const int i = k * G1P_B + j;
+                    if (i <= top) {
+                        if (q == 0) g1_store(buf[k & 1][j][slot], a);
+                        if (i < top) a = g1_dbl_quad(a, q);
+                    }
+                }
+            }
+        } else if (k > 0) {
+            const uint32_t w = limb8(s, (uint32_t)((k - 1) * G1P_B) >> 5);
+            for (int j = 0; j < G1P_B; j++) {
+                const int i = (k - 1) * G1P_B + j;
+                if (i <= top && ((w >> (i & 31)) & 1u)) acc = g1_add_quad(acc, g1_load(buf[(k - 1) & 1][j][slot]), q);
+            }
+        }
+        __syncthreads();
+    }
+    return acc;
+}
+
 // elementwise with a broadcast base (G1_jacobian_elementwise_mul_broadcast,
 // g1-tensor.cu:463-468): out[i] = base[i % nb] * s[i], one quad per element
 __global__ __launch_bounds__(64) void k_g1_mul(const uint32_t* __restrict__ base, uint32_t nb,
@@ -288,19 +332,27 @@ __global__ __launch_bounds__(256) void k_ipa_ip(const uint32_t* __restrict__ a, 
     // sums of a b 2^-256; times R^2 2^-256 gives the plain sums
     if (threadIdx.x < 2) st_aos(ip, threadIdx.x, mont_mul(red[threadIdx.x][0], r2));
 }
-__global__ __launch_bounds__(64) void k_ipa_scale(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
-                                                  const uint32_t* __restrict__ Q, const uint32_t* __restrict__ ip,
-                                                  uint32_t h, uint32_t* __restrict__ P) {
-    const uint32_t j = blockIdx.x * 16 + threadIdx.x / 4;
+// L and R terms (vrf_common.cuh:316-319): P[j] = g[h + j] a[j], P[h + j] = g[j] a[h + j],
+// P[2h], P[2h + 1] = Q <a_lo, b_hi>, Q <a_hi, b_lo>; 16 products per 128-thread block, each
+// on a quad of both waves (g1_mul_quad_pipe)
+__global__ __launch_bounds__(128) void k_ipa_scale(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
+                                                   const uint32_t* __restrict__ Q, const uint32_t* __restrict__ ip,
+                                                   uint32_t h, uint32_t* __restrict__ P) {
+    __shared__ g1_pipe_buf buf;
+    const uint32_t j = blockIdx.x * 16 + (threadIdx.x & 63) / 4;
     const int q = threadIdx.x & 3;
-    if (j >= 2 * h + 2) return;
-    const uint32_t* base = j < h ? g + 36 * (size_t)(h + j) : j < 2 * h ? g + 36 * (size_t)(j - h) : Q;
-    const uint32_t* sp = j < 2 * h ? a + 8 * (size_t)j : ip + 8 * (j - 2 * h);
-    uint32_t sc[8];
+    const bool active = j < 2 * h + 2;
+    uint32_t sc[8] = {};
+    g1_t base = g1_zero();
+    if (active) {
+        const uint32_t* bp = j < h ? g + 36 * (size_t)(h + j) : j < 2 * h ? g + 36 * (size_t)(j - h) : Q;
+        const uint32_t* sp = j < 2 * h ? a + 8 * (size_t)j : ip + 8 * (j - 2 * h);
 #pragma unroll
-    for (int k = 0; k < 8; k++) sc[k] = sp[k];
-    const g1_t r = g1_mul_quad(g1_load(base), sc, q);
-    if (q == 0) g1_store(P + 36 * (size_t)j, r);
+        for (int k = 0; k < 8; k++) sc[k] = sp[k];
+        if (threadIdx.x < 64) base = g1_load(bp);
+    }
+    const g1_t r = g1_mul_quad_pipe(base, sc, q, active, buf);
+    if (active && threadIdx.x >= 64 && q == 0) g1_store(P + 36 * (size_t)j, r);
 }
 __global__ __launch_bounds__(64) void k_ipa_tree(uint32_t* __restrict__ P, uint32_t h, uint32_t half) {
     const uint32_t i = blockIdx.x * 16 + threadIdx.x / 4;
@@ -319,20 +371,21 @@ __global__ __launch_bounds__(64) void k_ipa_lr(const uint32_t* __restrict__ P, u
 }
 // eight lanes per element: quad 0 computes x^-1 g_lo[i], quad 1 x g_hi[i] (k_g1_fold2's
 // two products, vrf_common.cuh:71-76), then quad 0 adds them in that order
-__global__ __launch_bounds__(64) void k_ipa_fold(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
-                                                 const uint32_t* __restrict__ b, uint32_t h, fr_t x, fr_t xi,
-                                                 fr_t xm, fr_t xim, uint32_t* __restrict__ g2,
-                                                 uint32_t* __restrict__ a2, uint32_t* __restrict__ b2) {
+__global__ __launch_bounds__(128) void k_ipa_fold(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
+                                                  const uint32_t* __restrict__ b, uint32_t h, fr_t x, fr_t xi,
+                                                  fr_t xm, fr_t xim, uint32_t* __restrict__ g2,
+                                                  uint32_t* __restrict__ a2, uint32_t* __restrict__ b2) {
+    __shared__ g1_pipe_buf buf;
     __shared__ uint32_t hi_pt[8][36];
-    const uint32_t e = threadIdx.x / 8, i = blockIdx.x * 8 + e;
+    const uint32_t e = (threadIdx.x & 63) / 8, i = blockIdx.x * 8 + e;
     const int q = threadIdx.x & 3, half_sel = (threadIdx.x >> 2) & 1;
-    g1_t r = g1_zero();
-    if (i < h) {
-        r = g1_mul_quad(g1_load(g + 36 * (size_t)(i + half_sel * h)), half_sel ? x.v : xi.v, q);
-        if (half_sel && q == 0) g1_store(hi_pt[e], r);
-    }
+    const bool active = i < h, add_wave = threadIdx.x >= 64;
+    g1_t base = g1_zero();
+    if (active && !add_wave) base = g1_load(g + 36 * (size_t)(i + half_sel * h));
+    g1_t r = g1_mul_quad_pipe(base, half_sel ? x.v : xi.v, q, active, buf);
+    if (add_wave && active && half_sel && q == 0) g1_store(hi_pt[e], r);
     __syncthreads();
-    if (i < h && !half_sel) {
+    if (add_wave && active && !half_sel) {
         r = g1_add_quad(r, g1_load(hi_pt[e]), q);
         if (q == 0) {
             g1_store(g2 + 36 * (size_t)i, r);
@@ -357,7 +410,7 @@ void launch_ipa_ip(hipStream_t s, const uint32_t* a, const uint32_t* b, uint32_t
 }
 void launch_ipa_scale(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* Q, const uint32_t* ip,
                       uint32_t h, uint32_t* P) {
-    hipLaunchKernelGGL(k_ipa_scale, dim3((2 * h + 2 + 15) / 16), dim3(64), 0, s, g, a, Q, ip, h, P);
+    hipLaunchKernelGGL(k_ipa_scale, dim3((2 * h + 2 + 15) / 16), dim3(128), 0, s, g, a, Q, ip, h, P);
 }
 void launch_ipa_tree(hipStream_t s, uint32_t* P, uint32_t h, uint32_t half) {
     hipLaunchKernelGGL(k_ipa_tree, dim3((2 * half + 15) / 16), dim3(64), 0, s, P, h, half);
@@ -375,7 +428,7 @@ void launch_ipa_fold(hipStream_t s, const uint32_t* g, const uint32_t* a, const 
         XM.v[k] = xm[k];
         XIM.v[k] = xim[k];
     }
-    hipLaunchKernelGGL(k_ipa_fold, dim3((h + 7) / 8), dim3(64), 0, s, g, a, b, h, X, XI, XM, XIM, g2, a2, b2);
+    hipLaunchKernelGGL(k_ipa_fold, dim3((h + 7) / 8), dim3(128), 0, s, g, a, b, h, X, XI, XM, XIM, g2, a2, b2);
 }
 void launch_planes_to_aos(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t n, uint32_t* out) {
     hipLaunchKernelGGL(k_planes_to_aos, dim3((n + 255) / 256), dim3(256), 0, s, lo, hi, n, out);
