@@ -438,18 +438,47 @@ def open_job(j, out):
     return b"".join(x["L"].tobytes() + x["R"].tobytes() + x["a_final"].tobytes() for x in r) + st.tobytes()
 
 
+def open_batched(jobs, outs):
+    """The same 21 openings through zkh_ipa_prove_batch: the openings' inputs formed on each
+    matmul's context, then three batched calls on one context (all W openings, all X, all Y:
+    each matmul's transcript runs W, X, Y in order as in open_job)."""
+    ins = []
+    for j, o in zip(jobs, outs):
+        c = j.ctx
+        ub, ui = o["u_batch"], o["u_input"]
+        bW = c.eq_table(o["u_output"])
+        ins.append((j.st.copy(), [(c.partial_me_window(j.Wp, ui, pow2(j.OUT)), bW, j.gen_out),
+                                  (c.partial_me_window(j.Xp, ub, pow2(j.IN)), c.eq_table(ui), j.gen_in),
+                                  (c.partial_me_window(j.Yp, ub, pow2(j.OUT)), bW, j.gen_out)]))
+        c.sync()
+    res = [[] for _ in jobs]
+    for k in range(3):
+        got = jobs[0].ctx.ipa_prove_batch([(st, t[k][0], t[k][1], t[k][2], j.Q) for j, (st, t) in zip(jobs, ins)])
+        for r, g in zip(res, got):
+            r.append(g)
+    return [b"".join(x["L"].tobytes() + x["R"].tobytes() + x["a_final"].tobytes() for x in r) + st.tobytes()
+            for r, (st, _) in zip(res, ins)]
+
+
 def openings(zkh, jobs, outs, pool, reps=2, cpu=True):
-    """The layer's 21 IPA openings (3 per matmul), the 7 matmuls concurrent on their own
-    contexts; every pass must reproduce the first pass's proofs."""
+    """The layer's 21 IPA openings (3 per matmul) through zkh_ipa_prove_batch; every pass must
+    reproduce, byte for byte, the proofs of one zkh_ipa_prove call per opening.  Also timed:
+    the 7 matmuls' openings concurrent on their own contexts, one call per opening."""
     ref = [open_job(j, o) for j, o in zip(jobs, outs)]
     times = []
     for _ in range(reps):
         t = time.perf_counter()
-        futs = [pool.submit(open_job, j, o) for j, o in zip(jobs, outs)]
-        assert [f.result() for f in futs] == ref, "non-deterministic openings"
+        assert open_batched(jobs, outs) == ref, "batched openings differ from the single-call ones"
         times.append(time.perf_counter() - t)
+    t = time.perf_counter()
+    futs = [pool.submit(open_job, j, o) for j, o in zip(jobs, outs)]
+    assert [f.result() for f in futs] == ref, "non-deterministic openings"
+    t_ctx = time.perf_counter() - t
     res = {"ipa_s_per_layer": round(min(times), 4), "ipas": 3 * len(jobs),
-           "scope": "ipa_W, ipa_X, ipa_Y of the 7 matmuls (vrf_common.cuh:302-336), byte-identical round points"}
+           "ipa_s_per_layer_contexts": round(t_ctx, 4),
+           "scope": "ipa_W, ipa_X, ipa_Y of the 7 matmuls (vrf_common.cuh:302-336) in three zkh_ipa_prove_batch "
+                    "calls, byte-identical to one zkh_ipa_prove per opening; _contexts: one call per opening, the 7 "
+                    "matmuls concurrent on their own contexts"}
     if cpu:
         sys.path.insert(0, ROOT)
         from oracle import coracle

@@ -348,6 +348,17 @@ int zkh_commit(zkh_ctx* ctx, const zkh_g1* gens, const zkh_tensor* t, zkh_g1** o
 int zkh_ipa_prove(zkh_ctx* ctx, uint8_t transcript[32], const zkh_tensor* a, const zkh_tensor* b,
                   const zkh_g1* g, const uint32_t Q[36], uint32_t* L_out, uint32_t* R_out,
                   uint32_t a_final[8]);
+/* nj <= 8 independent ipa_prove calls (vrf_common.cuh:302-336) in lockstep, job j exactly as
+ * zkh_ipa_prove(ctx, transcripts[j], a[j], b[j], g[j], Q[j], L_out[j], R_out[j], a_final[j]):
+ * one launch per kernel per round for every job still folding (jobs of different n drop out
+ * as they finish).  A round's length is that of one scalar-multiply chain whatever the
+ * number of products, so openings that a driver runs side by side (the matmuls of a layer)
+ * cost about one opening's time here instead of sharing the device's hardware queues.
+ * No reference counterpart as one call: the reference's drivers call ipa_prove once per
+ * opening; each job's transcript and outputs are byte-identical to that call's. */
+int zkh_ipa_prove_batch(zkh_ctx* ctx, uint32_t nj, uint8_t* const transcripts[], const zkh_tensor* const a[],
+                        const zkh_tensor* const b[], const zkh_g1* const g[], const uint32_t* const Q[],
+                        uint32_t* const L_out[], uint32_t* const R_out[], uint32_t* const a_final[]);
 
 #ifdef __cplusplus
 }

@@ -241,6 +241,35 @@ def test_ipa_prove_int_witness_and_errors(zkh, ctx):
     assert e.value.code == zkh.EARG
 
 
+def test_ipa_prove_batch_vs_oracle(zkh, ctx):
+    """zkh_ipa_prove_batch: jobs of different n (1, 2, 8, 32, 64: 0 to 6 rounds, so jobs drop
+    out of the lockstep rounds at different points) and transcripts, each job byte-identical
+    to the oracle's ipa_prove on its own transcript; 0 or 9 jobs are ZKH_EARG."""
+    rng = np.random.default_rng(330)
+    jobs, want = [], []
+    for t, n in enumerate((32, 1, 8, 64, 2)):
+        gens = gens_for(60 + t, n + 1)
+        a = C.ints_to_fr([int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(n)])
+        u = [int.from_bytes(rng.bytes(32), "little") % P.R for _ in range(max(n.bit_length() - 1, 0))]
+        b = C.ints_to_fr([P.eq_weight(k, u) if u else 1 for k in range(n)])
+        st_o = C.tr_init("ipab-%d" % t)
+        rc, L, R, af = C.ipa_prove(st_o, a, b, gens[:n], gens[n], n)
+        assert rc == 0
+        want.append((L, R, af, bytes(st_o)))
+        jobs.append((zkh.transcript("ipab-%d" % t), ctx.from_fr(a), ctx.from_fr(b), ctx.g1_from_host(gens[:n]), gens[n]))
+    got = ctx.ipa_prove_batch(jobs)
+    for (st, *_), g, (L, R, af, st_o) in zip(jobs, got, want):
+        assert np.array_equal(g["L"], L) and np.array_equal(g["R"], R)
+        assert np.array_equal(g["a_final"], af)
+        assert bytes(st) == st_o
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx.ipa_prove_batch([(zkh.transcript("x"),) + j[1:] for j in jobs[:1] * 9])
+    assert e.value.code == zkh.EARG
+    with pytest.raises(zkh.ZkhError) as e:
+        ctx._chk(zkh.lib().zkh_ipa_prove_batch(ctx.h, 0, None, None, None, None, None, None, None, None))
+    assert e.value.code == zkh.EARG
+
+
 def test_from_fr_rejects_non_canonical(zkh, ctx):
     """zkh_tensor_from_fr checks canonical form on the device: r itself, r + 1 and 2^256 - 1
     anywhere in the array are rejected; r - 1 and 0 round-trip."""

@@ -107,6 +107,7 @@ def lib():
         L.zkh_g1_mul.argtypes = [vp, vp, vp, ctypes.POINTER(vp)]
         L.zkh_g1_addmul.argtypes = [vp, vp, vp, vp, ctypes.POINTER(vp)]
         L.zkh_ipa_prove.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.zkh_ipa_prove_batch.argtypes = [vp, ctypes.c_uint32, vp, vp, vp, vp, vp, vp, vp, vp]
         _lib = L
     return _lib
 
@@ -412,6 +413,24 @@ class Context:
         Q = np.ascontiguousarray(Q, np.uint32)
         self._chk(lib().zkh_ipa_prove(self.h, _p(st), a.h, b.h, g.h, _p(Q), _p(L), _p(R), _p(af)))
         return {"L": L[:rounds], "R": R[:rounds], "a_final": af}
+
+    def ipa_prove_batch(self, jobs):
+        """zkh_ipa_prove_batch over jobs [(st, a, b, g, Q), ...]: one ipa_prove result per job, as
+        ipa_prove returns it; each st (32 uint8) is advanced in place."""
+        nj = len(jobs)
+        arr = lambda vals: (ctypes.c_void_p * nj)(*vals)
+        outs, keep = [], []
+        for st, a, b, g, Q in jobs:
+            rounds = max(g.n.bit_length() - 1, 0)
+            o = {"L": np.zeros((max(rounds, 1), 36), np.uint32), "R": np.zeros((max(rounds, 1), 36), np.uint32),
+                 "a_final": np.zeros(8, np.uint32), "rounds": rounds}
+            keep.append(np.ascontiguousarray(Q, np.uint32))
+            outs.append(o)
+        self._chk(lib().zkh_ipa_prove_batch(
+            self.h, nj, arr([_p(j[0]) for j in jobs]), arr([j[1].h for j in jobs]), arr([j[2].h for j in jobs]),
+            arr([j[3].h for j in jobs]), arr([_p(q) for q in keep]), arr([_p(o["L"]) for o in outs]),
+            arr([_p(o["R"]) for o in outs]), arr([_p(o["a_final"]) for o in outs])))
+        return [{"L": o["L"][:o["rounds"]], "R": o["R"][:o["rounds"]], "a_final": o["a_final"]} for o in outs]
 
     def commit(self, gens, t):
         """Commitment::commit: rows of n = gens.n scalars of tensor t -> one point per row."""

@@ -311,8 +311,11 @@ __global__ __launch_bounds__(64) void k_g1_addmul(const uint32_t* __restrict__ a
 //   pairwise trees over P[0, h) and P[h, 2h)                  (dev_msm's order)
 //   L = P[0] + P[2h], R = P[h] + P[2h+1]
 //   fold: a' = x a_lo + x^-1 a_hi, b' = x^-1 b_lo + x b_hi, g' = x^-1 g_lo + x g_hi
-__global__ __launch_bounds__(256) void k_ipa_ip(const uint32_t* __restrict__ a, const uint32_t* __restrict__ b,
-                                                uint32_t h, fr_t r2, uint32_t* __restrict__ ip) {
+__global__ __launch_bounds__(256) void k_ipa_ip(IpaBatchDev B, fr_t r2) {
+    const IpaJobDev& J = B.j[blockIdx.y];
+    const uint32_t h = J.h;
+    if (!h) return;  // the job has finished its rounds (whole block)
+    const uint32_t *a = J.a, *b = J.b;
     __shared__ fr_t red[2][256];
     fr_t sl = fr_zero(), sr = fr_zero();
     for (uint32_t i = threadIdx.x; i < h; i += 256) {
@@ -330,14 +333,15 @@ __global__ __launch_bounds__(256) void k_ipa_ip(const uint32_t* __restrict__ a, 
         __syncthreads();
     }
     // sums of a b 2^-256; times R^2 2^-256 gives the plain sums
-    if (threadIdx.x < 2) st_aos(ip, threadIdx.x, mont_mul(red[threadIdx.x][0], r2));
+    if (threadIdx.x < 2) st_aos(J.ip, threadIdx.x, mont_mul(red[threadIdx.x][0], r2));
 }
 // L and R terms (vrf_common.cuh:316-319): P[j] = g[h + j] a[j], P[h + j] = g[j] a[h + j],
 // P[2h], P[2h + 1] = Q <a_lo, b_hi>, Q <a_hi, b_lo>; 16 products per 128-thread block, each
-// on a quad of both waves (g1_mul_quad_pipe)
-__global__ __launch_bounds__(128) void k_ipa_scale(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
-                                                   const uint32_t* __restrict__ Q, const uint32_t* __restrict__ ip,
-                                                   uint32_t h, uint32_t* __restrict__ P) {
+// on a quad of both waves (g1_mul_quad_pipe); blockIdx.y is the job
+__global__ __launch_bounds__(128) void k_ipa_scale(IpaBatchDev B) {
+    const IpaJobDev& J = B.j[blockIdx.y];
+    const uint32_t h = J.h;
+    if (blockIdx.x * 16 >= 2 * h + 2 || !h) return;  // whole block: past the job's products
     __shared__ g1_pipe_buf buf;
     const uint32_t j = blockIdx.x * 16 + (threadIdx.x & 63) / 4;
     const int q = threadIdx.x & 3;
@@ -345,54 +349,78 @@ __global__ __launch_bounds__(128) void k_ipa_scale(const uint32_t* __restrict__ 
     uint32_t sc[8] = {};
     g1_t base = g1_zero();
     if (active) {
-        const uint32_t* bp = j < h ? g + 36 * (size_t)(h + j) : j < 2 * h ? g + 36 * (size_t)(j - h) : Q;
-        const uint32_t* sp = j < 2 * h ? a + 8 * (size_t)j : ip + 8 * (j - 2 * h);
+        const uint32_t* bp = j < h ? J.g + 36 * (size_t)(h + j) : j < 2 * h ? J.g + 36 * (size_t)(j - h) : J.Q;
+        const uint32_t* sp = j < 2 * h ? J.a + 8 * (size_t)j : J.ip + 8 * (j - 2 * h);
 #pragma unroll
         for (int k = 0; k < 8; k++) sc[k] = sp[k];
         if (threadIdx.x < 64) base = g1_load(bp);
     }
     const g1_t r = g1_mul_quad_pipe(base, sc, q, active, buf);
-    if (active && threadIdx.x >= 64 && q == 0) g1_store(P + 36 * (size_t)j, r);
+    if (active && threadIdx.x >= 64 && q == 0) g1_store(J.P + 36 * (size_t)j, r);
 }
-__global__ __launch_bounds__(64) void k_ipa_tree(uint32_t* __restrict__ P, uint32_t h, uint32_t half) {
+// one level of the pairwise trees over P[0, h) and P[h, 2h): half = h >> shift per job
+__global__ __launch_bounds__(64) void k_ipa_tree(IpaBatchDev B, uint32_t shift) {
+    const IpaJobDev& J = B.j[blockIdx.y];
+    const uint32_t h = J.h, half = h >> shift;
     const uint32_t i = blockIdx.x * 16 + threadIdx.x / 4;
     const int q = threadIdx.x & 3;
     if (i >= 2 * half) return;
     const size_t k = (size_t)(i / half) * h + i % half;
-    const g1_t r = g1_add_quad(g1_load(P + 36 * k), g1_load(P + 36 * (k + half)), q);
-    if (q == 0) g1_store(P + 36 * k, r);
+    const g1_t r = g1_add_quad(g1_load(J.P + 36 * k), g1_load(J.P + 36 * (k + half)), q);
+    if (q == 0) g1_store(J.P + 36 * k, r);
 }
-__global__ __launch_bounds__(64) void k_ipa_lr(const uint32_t* __restrict__ P, uint32_t h, uint32_t* __restrict__ LR) {
-    const uint32_t side = threadIdx.x / 4;
+__global__ __launch_bounds__(64) void k_ipa_lr(IpaBatchDev B) {
+    const IpaJobDev& J = B.j[blockIdx.y];
+    const uint32_t side = threadIdx.x / 4, h = J.h;
     const int q = threadIdx.x & 3;
-    if (side >= 2) return;
-    const g1_t r = g1_add_quad(g1_load(P + 36 * (size_t)(side * h)), g1_load(P + 36 * (size_t)(2 * h + side)), q);
-    if (q == 0) g1_store(LR + 36 * side, r);
+    if (side >= 2 || !h) return;
+    const g1_t r = g1_add_quad(g1_load(J.P + 36 * (size_t)(side * h)), g1_load(J.P + 36 * (size_t)(2 * h + side)), q);
+    if (q == 0) g1_store(J.LR + 36 * side, r);
 }
 // eight lanes per element: quad 0 computes x^-1 g_lo[i], quad 1 x g_hi[i] (k_g1_fold2's
 // two products, vrf_common.cuh:71-76), then quad 0 adds them in that order
-__global__ __launch_bounds__(128) void k_ipa_fold(const uint32_t* __restrict__ g, const uint32_t* __restrict__ a,
-                                                  const uint32_t* __restrict__ b, uint32_t h, fr_t x, fr_t xi,
-                                                  fr_t xm, fr_t xim, uint32_t* __restrict__ g2,
-                                                  uint32_t* __restrict__ a2, uint32_t* __restrict__ b2) {
+__global__ __launch_bounds__(128) void k_ipa_fold(IpaBatchDev B) {
+    const IpaJobDev& J = B.j[blockIdx.y];
+    const uint32_t h = J.h;
+    if (blockIdx.x * 8 >= h) return;  // whole block: past the job's pairs (or a finished job)
     __shared__ g1_pipe_buf buf;
     __shared__ uint32_t hi_pt[8][36];
     const uint32_t e = (threadIdx.x & 63) / 8, i = blockIdx.x * 8 + e;
     const int q = threadIdx.x & 3, half_sel = (threadIdx.x >> 2) & 1;
     const bool active = i < h, add_wave = threadIdx.x >= 64;
     g1_t base = g1_zero();
-    if (active && !add_wave) base = g1_load(g + 36 * (size_t)(i + half_sel * h));
-    g1_t r = g1_mul_quad_pipe(base, half_sel ? x.v : xi.v, q, active, buf);
+    if (active && !add_wave) base = g1_load(J.g + 36 * (size_t)(i + half_sel * h));
+    g1_t r = g1_mul_quad_pipe(base, half_sel ? J.x : J.xi, q, active, buf);
     if (add_wave && active && half_sel && q == 0) g1_store(hi_pt[e], r);
     __syncthreads();
     if (add_wave && active && !half_sel) {
         r = g1_add_quad(r, g1_load(hi_pt[e]), q);
         if (q == 0) {
-            g1_store(g2 + 36 * (size_t)i, r);
-            st_aos(a2, i, fr_add(mont_mul(xm, ld_aos(a, i)), mont_mul(xim, ld_aos(a, i + h))));
-            st_aos(b2, i, fr_add(mont_mul(xim, ld_aos(b, i)), mont_mul(xm, ld_aos(b, i + h))));
+            fr_t xm, xim;
+#pragma unroll
+            for (int k = 0; k < 8; k++) xm.v[k] = J.xm[k], xim.v[k] = J.xim[k];
+            g1_store(J.g2 + 36 * (size_t)i, r);
+            st_aos(J.a2, i, fr_add(mont_mul(xm, ld_aos(J.a, i)), mont_mul(xim, ld_aos(J.a, i + h))));
+            st_aos(J.b2, i, fr_add(mont_mul(xim, ld_aos(J.b, i)), mont_mul(xm, ld_aos(J.b, i + h))));
         }
     }
+}
+void launch_ipa_ip(hipStream_t s, const IpaBatchDev& B, uint32_t nj, const uint32_t r2[8]) {
+    fr_t R2;
+    for (int k = 0; k < 8; k++) R2.v[k] = r2[k];
+    hipLaunchKernelGGL(k_ipa_ip, dim3(1, nj), dim3(256), 0, s, B, R2);
+}
+void launch_ipa_scale(hipStream_t s, const IpaBatchDev& B, uint32_t nj, uint32_t hmax) {
+    hipLaunchKernelGGL(k_ipa_scale, dim3((2 * hmax + 2 + 15) / 16, nj), dim3(128), 0, s, B);
+}
+void launch_ipa_tree(hipStream_t s, const IpaBatchDev& B, uint32_t nj, uint32_t hmax, uint32_t shift) {
+    hipLaunchKernelGGL(k_ipa_tree, dim3((2 * (hmax >> shift) + 15) / 16, nj), dim3(64), 0, s, B, shift);
+}
+void launch_ipa_lr(hipStream_t s, const IpaBatchDev& B, uint32_t nj) {
+    hipLaunchKernelGGL(k_ipa_lr, dim3(1, nj), dim3(64), 0, s, B);
+}
+void launch_ipa_fold(hipStream_t s, const IpaBatchDev& B, uint32_t nj, uint32_t hmax) {
+    hipLaunchKernelGGL(k_ipa_fold, dim3((hmax + 7) / 8, nj), dim3(128), 0, s, B);
 }
 // planes -> 8-word entries
 __global__ __launch_bounds__(256) void k_planes_to_aos(const uint32_t* __restrict__ lo, const uint32_t* __restrict__ hi,
@@ -400,35 +428,6 @@ __global__ __launch_bounds__(256) void k_planes_to_aos(const uint32_t* __restric
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     st_aos(out, i, ld_fr((const uint4*)lo, (const uint4*)hi, i));
-}
-
-void launch_ipa_ip(hipStream_t s, const uint32_t* a, const uint32_t* b, uint32_t h, const uint32_t r2[8],
-                   uint32_t* ip) {
-    fr_t R2;
-    for (int k = 0; k < 8; k++) R2.v[k] = r2[k];
-    hipLaunchKernelGGL(k_ipa_ip, dim3(1), dim3(256), 0, s, a, b, h, R2, ip);
-}
-void launch_ipa_scale(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* Q, const uint32_t* ip,
-                      uint32_t h, uint32_t* P) {
-    hipLaunchKernelGGL(k_ipa_scale, dim3((2 * h + 2 + 15) / 16), dim3(128), 0, s, g, a, Q, ip, h, P);
-}
-void launch_ipa_tree(hipStream_t s, uint32_t* P, uint32_t h, uint32_t half) {
-    hipLaunchKernelGGL(k_ipa_tree, dim3((2 * half + 15) / 16), dim3(64), 0, s, P, h, half);
-}
-void launch_ipa_lr(hipStream_t s, const uint32_t* P, uint32_t h, uint32_t* LR) {
-    hipLaunchKernelGGL(k_ipa_lr, dim3(1), dim3(64), 0, s, P, h, LR);
-}
-void launch_ipa_fold(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* b, uint32_t h,
-                     const uint32_t x[8], const uint32_t xi[8], const uint32_t xm[8], const uint32_t xim[8],
-                     uint32_t* g2, uint32_t* a2, uint32_t* b2) {
-    fr_t X, XI, XM, XIM;
-    for (int k = 0; k < 8; k++) {
-        X.v[k] = x[k];
-        XI.v[k] = xi[k];
-        XM.v[k] = xm[k];
-        XIM.v[k] = xim[k];
-    }
-    hipLaunchKernelGGL(k_ipa_fold, dim3((h + 7) / 8), dim3(128), 0, s, g, a, b, h, X, XI, XM, XIM, g2, a2, b2);
 }
 void launch_planes_to_aos(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t n, uint32_t* out) {
     hipLaunchKernelGGL(k_planes_to_aos, dim3((n + 255) / 256), dim3(256), 0, s, lo, hi, n, out);

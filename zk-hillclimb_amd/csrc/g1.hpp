@@ -39,16 +39,25 @@ void launch_pip_bucket(hipStream_t s, const uint32_t* gens, const uint16_t* list
 void launch_pip_window(hipStream_t s, const uint32_t* buckets, const uint32_t* offs, const uint16_t* alias,
                        uint32_t m, uint32_t* partials);
 void launch_pip_combine(hipStream_t s, const uint32_t* partials, uint32_t m, uint32_t* out);
-// inner-product argument rounds (ipa_prove); a, b plain Fr 8 words per entry, g/P points
-void launch_ipa_ip(hipStream_t s, const uint32_t* a, const uint32_t* b, uint32_t h, const uint32_t r2[8],
-                   uint32_t* ip);
-void launch_ipa_scale(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* Q, const uint32_t* ip,
-                      uint32_t h, uint32_t* P);
-void launch_ipa_tree(hipStream_t s, uint32_t* P, uint32_t h, uint32_t half);
-void launch_ipa_lr(hipStream_t s, const uint32_t* P, uint32_t h, uint32_t* LR);
-void launch_ipa_fold(hipStream_t s, const uint32_t* g, const uint32_t* a, const uint32_t* b, uint32_t h,
-                     const uint32_t x[8], const uint32_t xi[8], const uint32_t xm[8], const uint32_t xim[8],
-                     uint32_t* g2, uint32_t* a2, uint32_t* b2);
+// inner-product argument rounds (ipa_prove) of up to ZKH_IPA_MAX_JOBS openings per launch
+// (blockIdx.y = job); a, b plain Fr 8 words per entry, g/P points.  A job with h = 0 has
+// finished its rounds and is skipped.  x, xi plain; xm, xim in Montgomery form.
+#define ZKH_IPA_MAX_JOBS 8
+struct IpaJobDev {
+    const uint32_t *g, *a, *b, *Q;
+    uint32_t *ip, *P, *LR, *g2, *a2, *b2;
+    uint32_t h, pad;
+    uint32_t x[8], xi[8], xm[8], xim[8];
+};
+struct IpaBatchDev {
+    IpaJobDev j[ZKH_IPA_MAX_JOBS];
+};
+void launch_ipa_ip(hipStream_t s, const IpaBatchDev& B, uint32_t nj, const uint32_t r2[8]);
+void launch_ipa_scale(hipStream_t s, const IpaBatchDev& B, uint32_t nj, uint32_t hmax);
+// one tree level: half = h >> shift per job (hmax the largest h)
+void launch_ipa_tree(hipStream_t s, const IpaBatchDev& B, uint32_t nj, uint32_t hmax, uint32_t shift);
+void launch_ipa_lr(hipStream_t s, const IpaBatchDev& B, uint32_t nj);
+void launch_ipa_fold(hipStream_t s, const IpaBatchDev& B, uint32_t nj, uint32_t hmax);
 void launch_planes_to_aos(hipStream_t s, const uint32_t* lo, const uint32_t* hi, uint32_t n, uint32_t* out);
 // out[i] = base[i % nb] * s[i] (G1Jacobian_mul, raw scalar bits)
 // a scalar passed by value to a kernel: 8 plain little-endian words

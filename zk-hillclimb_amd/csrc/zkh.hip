@@ -3869,71 +3869,132 @@ extern "C" int zkh_commit(zkh_ctx* c, const zkh_g1* gens, const zkh_tensor* t, z
 // inner-product argument (ipa_prove, vrf_common.cuh:302-336), continuing the caller's
 // transcript; the round points are byte-identical to the reference's (they are absorbed)
 // ---------------------------------------------------------------------------------------
+extern "C" int zkh_ipa_prove_batch(zkh_ctx* c, uint32_t nj, uint8_t* const* transcripts, const zkh_tensor* const* a,
+                                   const zkh_tensor* const* b, const zkh_g1* const* g, const uint32_t* const* Q,
+                                   uint32_t* const* L_out, uint32_t* const* R_out, uint32_t* const* a_final) {
+    if (!c || !transcripts || !a || !b || !g || !Q || !a_final || !L_out || !R_out) return fail(c, ZKH_EARG, "null argument");
+    if (!nj || nj > ZKH_IPA_MAX_JOBS) return fail(c, ZKH_EARG, "ipa_prove_batch: 1 to %d jobs", ZKH_IPA_MAX_JOBS);
+    size_t fr_words = 0, g_words = 0, p_words = 0;
+    uint32_t nmax = 0;
+    for (uint32_t j = 0; j < nj; j++) {
+        if (!transcripts[j] || !a[j] || !b[j] || !g[j] || !Q[j] || !a_final[j]) return fail(c, ZKH_EARG, "null argument");
+        const uint32_t n = g[j]->n;
+        if (!n || (n & (n - 1))) return fail(c, ZKH_EARG, "ipa_prove: n not a power of two");  // vrf_common.cuh:305
+        if (a[j]->n != n || b[j]->n != n) return fail(c, ZKH_EARG, "ipa_prove: a, b and g sizes differ");
+        if (n > 1 && (!L_out[j] || !R_out[j])) return fail(c, ZKH_EARG, "null argument");
+        fr_words += (size_t)n * 32;
+        g_words += (size_t)n * 72;
+        p_words += (size_t)(n + 2) * 36 + 256;
+        nmax = std::max(nmax, n);
+    }
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = 0;
+    // per job: a, b, g working copies (two of each, the fold writes the other), round
+    // products P, inner products, Q; one L, R area for all jobs (one copy to the host per round)
+    uint32_t* fr_w = (uint32_t*)scratch_slot(c, SL_TMP1, fr_words * 4, &rc);
+    uint32_t* g_w = rc ? nullptr : (uint32_t*)scratch_slot(c, SL_TMP2, g_words * 4, &rc);
+    uint32_t* p_w = rc ? nullptr : (uint32_t*)scratch_slot(c, SL_TMP3, (p_words + 72 * (size_t)nj) * 4, &rc);
+    if (rc) return rc;
+    uint32_t* LR = p_w + p_words;
+    IpaBatchDev B{};
+    uint32_t sz[ZKH_IPA_MAX_JOBS];
+    uint32_t *A0[ZKH_IPA_MAX_JOBS], *B0[ZKH_IPA_MAX_JOBS], *G0[ZKH_IPA_MAX_JOBS];
+    uint32_t *A1[ZKH_IPA_MAX_JOBS], *B1[ZKH_IPA_MAX_JOBS], *G1[ZKH_IPA_MAX_JOBS];
+    size_t of = 0, og = 0, op = 0;
+    for (uint32_t j = 0; j < nj; j++) {
+        const uint32_t n = g[j]->n;
+        IpaJobDev& J = B.j[j];
+        uint32_t* a0 = fr_w + of;
+        uint32_t* b0 = a0 + 16 * (size_t)n;
+        A1[j] = a0 + 8 * (size_t)n;
+        B1[j] = b0 + 8 * (size_t)n;
+        of += 32 * (size_t)n;
+        uint32_t* g0 = g_w + og;
+        G1[j] = g0 + 36 * (size_t)n;
+        og += 72 * (size_t)n;
+        J.P = p_w + op;
+        J.ip = J.P + 36 * (size_t)(n + 2);
+        uint32_t* Qd = J.ip + 16;
+        op += (size_t)(n + 2) * 36 + 256;
+        J.LR = LR + 72 * (size_t)j;
+        DevPlanes pa, pb;
+        if ((rc = as_planes(c, a[j], SL_TMP0, &pa))) return rc;
+        launch_planes_to_aos(c->stream, pa.lo(), pa.hi(), n, a0);
+        if ((rc = as_planes(c, b[j], SL_TMP0, &pb))) return rc;
+        launch_planes_to_aos(c->stream, pb.lo(), pb.hi(), n, b0);
+        HIPCHK(c, hipMemcpyAsync(g0, g[j]->d, (size_t)n * 144, hipMemcpyDeviceToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(Qd, Q[j], 144, hipMemcpyHostToDevice, c->stream));
+        J.a = A0[j] = a0;
+        J.b = B0[j] = b0;
+        J.g = G0[j] = g0;
+        J.Q = Qd;
+        sz[j] = n;
+    }
+    uint32_t r2[8];
+    fr_store(kR2, r2);
+    std::vector<uint32_t> lr(72 * (size_t)nj);
+    for (uint32_t round = 0; (nmax >> round) > 1; round++) {
+        uint32_t hmax = 0;
+        for (uint32_t j = 0; j < nj; j++) {
+            B.j[j].h = sz[j] > 1 ? sz[j] / 2 : 0;
+            hmax = std::max(hmax, B.j[j].h);
+        }
+        {
+            ProfScope ps(c, "ipa_msm", 0);
+            launch_ipa_ip(c->stream, B, nj, r2);
+            launch_ipa_scale(c->stream, B, nj, hmax);
+            for (uint32_t shift = 1; (hmax >> shift) >= 1; shift++) launch_ipa_tree(c->stream, B, nj, hmax, shift);
+            launch_ipa_lr(c->stream, B, nj);
+        }
+        HIPCHK(c, hipMemcpyAsync(lr.data(), LR, lr.size() * 4, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        for (uint32_t j = 0; j < nj; j++) {
+            IpaJobDev& J = B.j[j];
+            if (!J.h) continue;
+            const uint32_t* l = lr.data() + 72 * (size_t)j;
+            tr_absorb(transcripts[j], "L", 1, l, 144);
+            tr_absorb(transcripts[j], "R", 1, l + 36, 144);
+            const Fr x = tr_challenge(transcripts[j]), xi = fr_inv(x);
+            fr_store(x, J.x);
+            fr_store(xi, J.xi);
+            fr_store(fr_to_mont(x), J.xm);
+            fr_store(fr_to_mont(xi), J.xim);
+            J.g2 = G1[j];
+            J.a2 = A1[j];
+            J.b2 = B1[j];
+            memcpy(L_out[j] + 36 * (size_t)round, l, 144);
+            memcpy(R_out[j] + 36 * (size_t)round, l + 36, 144);
+        }
+        {
+            ProfScope ps(c, "ipa_fold", 0);
+            launch_ipa_fold(c->stream, B, nj, hmax);
+        }
+        for (uint32_t j = 0; j < nj; j++) {
+            IpaJobDev& J = B.j[j];
+            if (!J.h) continue;
+            std::swap(G0[j], G1[j]);  // the next round's fold writes the buffers just read
+            std::swap(A0[j], A1[j]);
+            std::swap(B0[j], B1[j]);
+            J.g = G0[j];
+            J.a = A0[j];
+            J.b = B0[j];
+            sz[j] /= 2;
+        }
+    }
+    for (uint32_t j = 0; j < nj; j++) HIPCHK(c, hipMemcpyAsync(a_final[j], B.j[j].a, 32, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipGetLastError());
+    return ZKH_OK;
+}
 extern "C" int zkh_ipa_prove(zkh_ctx* c, uint8_t* transcript, const zkh_tensor* a, const zkh_tensor* b,
                              const zkh_g1* g, const uint32_t* Q, uint32_t* L_out, uint32_t* R_out,
                              uint32_t* a_final) {
     if (!c || !transcript || !a || !b || !g || !Q || !a_final) return fail(c, ZKH_EARG, "null argument");
-    const uint32_t n = g->n;
-    if (!n || (n & (n - 1))) return fail(c, ZKH_EARG, "ipa_prove: n not a power of two");  // vrf_common.cuh:305
-    if (a->n != n || b->n != n) return fail(c, ZKH_EARG, "ipa_prove: a, b and g sizes differ");
-    if (n > 1 && (!L_out || !R_out)) return fail(c, ZKH_EARG, "null argument");
-    HIPCHK(c, hipSetDevice(c->device));
-    int rc = 0;
-    // a, b, g working copies (two of each, the fold writes the other), round products P,
-    // inner products, L and R
-    uint32_t* fr_w = (uint32_t*)scratch_slot(c, SL_TMP1, (size_t)n * 32 * 4, &rc);
-    uint32_t* g_w = rc ? nullptr : (uint32_t*)scratch_slot(c, SL_TMP2, (size_t)n * 144 * 2, &rc);
-    uint32_t* P = rc ? nullptr : (uint32_t*)scratch_slot(c, SL_TMP3, (size_t)(n + 2) * 144 + 1024, &rc);
-    if (rc) return rc;
-    uint32_t* ip = P + 36 * (size_t)(n + 2);
-    uint32_t* LR = ip + 16;
-    uint32_t* Qd = LR + 72;
-    uint32_t *a0 = fr_w, *a1 = fr_w + 8 * (size_t)n, *b0 = fr_w + 16 * (size_t)n, *b1 = fr_w + 24 * (size_t)n;
-    uint32_t *g0 = g_w, *g1 = g_w + 36 * (size_t)n;
-    DevPlanes pa, pb;
-    if ((rc = as_planes(c, a, SL_TMP0, &pa))) return rc;
-    launch_planes_to_aos(c->stream, pa.lo(), pa.hi(), n, a0);
-    if ((rc = as_planes(c, b, SL_TMP0, &pb))) return rc;
-    launch_planes_to_aos(c->stream, pb.lo(), pb.hi(), n, b0);
-    HIPCHK(c, hipMemcpyAsync(g0, g->d, (size_t)n * 144, hipMemcpyDeviceToDevice, c->stream));
-    HIPCHK(c, hipMemcpyAsync(Qd, Q, 144, hipMemcpyHostToDevice, c->stream));
-    uint32_t r2[8];
-    fr_store(kR2, r2);
-    uint32_t lr[72];
-    uint32_t round = 0;
-    for (uint32_t sz = n; sz > 1; sz /= 2, round++) {
-        const uint32_t h = sz / 2;
-        {
-            ProfScope ps(c, "ipa_msm", (double)sz * (144 + 32));
-            launch_ipa_ip(c->stream, a0, b0, h, r2, ip);
-            launch_ipa_scale(c->stream, g0, a0, Qd, ip, h, P);
-            for (uint32_t half = h / 2; half >= 1; half /= 2) launch_ipa_tree(c->stream, P, h, half);
-            launch_ipa_lr(c->stream, P, h, LR);
-        }
-        HIPCHK(c, hipMemcpyAsync(lr, LR, sizeof(lr), hipMemcpyDeviceToHost, c->stream));
-        HIPCHK(c, hipStreamSynchronize(c->stream));
-        tr_absorb(transcript, "L", 1, lr, 144);
-        tr_absorb(transcript, "R", 1, lr + 36, 144);
-        const Fr x = tr_challenge(transcript), xi = fr_inv(x);
-        uint32_t xv[8], xiv[8], xm[8], xim[8];
-        fr_store(x, xv);
-        fr_store(xi, xiv);
-        fr_store(fr_to_mont(x), xm);
-        fr_store(fr_to_mont(xi), xim);
-        {
-            ProfScope ps(c, "ipa_fold", (double)sz * (144 + 64));
-            launch_ipa_fold(c->stream, g0, a0, b0, h, xv, xiv, xm, xim, g1, a1, b1);
-        }
-        std::swap(g0, g1);
-        std::swap(a0, a1);
-        std::swap(b0, b1);
-        memcpy(L_out + 36 * (size_t)round, lr, 144);
-        memcpy(R_out + 36 * (size_t)round, lr + 36, 144);
-    }
-    HIPCHK(c, hipMemcpyAsync(a_final, a0, 32, hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    HIPCHK(c, hipGetLastError());
-    return ZKH_OK;
+    uint32_t lr_unused[1];
+    uint32_t* L = L_out ? L_out : lr_unused;
+    uint32_t* R = R_out ? R_out : lr_unused;
+    if (g->n > 1 && (!L_out || !R_out)) return fail(c, ZKH_EARG, "null argument");
+    return zkh_ipa_prove_batch(c, 1, &transcript, &a, &b, &g, &Q, &L, &R, &a_final);
 }
 
 // ---------------------------------------------------------------------------------------
